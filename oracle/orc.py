@@ -1,0 +1,256 @@
+"""ctypes binding of the CPU oracle (liborc.so, built from mrml_oracle.c).
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg -- as the checker or the timed CPU baseline,
+never as the product path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent / "liborc.so"
+
+_P = ctypes.c_void_p
+_Z = ctypes.c_size_t
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+
+class Gemma2(ctypes.Structure):
+    _fields_ = [
+        ("n_layers", ctypes.c_int32), ("dim", ctypes.c_int32), ("n_heads", ctypes.c_int32),
+        ("n_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("ffn_dim", ctypes.c_int32),
+        ("vocab", ctypes.c_int32), ("ctx", ctypes.c_int32),
+        ("rope_base", ctypes.c_float), ("eps", ctypes.c_float), ("attn_scale", ctypes.c_float),
+        ("tie_q8", ctypes.c_int32), ("softcap", ctypes.c_int32),
+        ("tok_embd", _P), ("output_norm", _P),
+        ("wq", _P), ("wk", _P), ("wv", _P), ("wo", _P),
+        ("wgate", _P), ("wup", _P), ("wdown", _P),
+        ("attn_norm", _P), ("post_attn_norm", _P), ("ffn_norm", _P), ("post_ffw_norm", _P),
+    ]
+
+
+_SIG = {
+    "orc_f16_to_f32": ([ctypes.c_uint16], _F),
+    "orc_f32_to_f16": ([_F], ctypes.c_uint16),
+    "orc_f32_to_f16_rne": ([_F], ctypes.c_uint16),
+    "orc_quantize_q8_0": ([_P, _P, _Z], None),
+    "orc_dequantize_q8_0": ([_P, _P, _Z], None),
+    "orc_dequantize_q4_0": ([_P, _P, _Z], None),
+    "orc_quantize_q4_0": ([_P, _P, _Z], None),
+    "orc_vec_dot_q4_0_q8_0": ([_P, _P, _Z, _I], _F),
+    "orc_vec_dot_q8_0_q8_0": ([_P, _P, _Z, _I], _F),
+    "orc_block_isums_q4_0_q8_0": ([_P, _P, _Z, _P], None),
+    "orc_block_isums_q8_0_q8_0": ([_P, _P, _Z, _P], None),
+    "orc_host_isa": ([], _I),
+    "orc_mat_vec_mul_q4_0_q8_0": ([_P, _P, _P, _Z, _Z, _I, _I], None),
+    "orc_mat_vec_mul_q4_0": ([_P, _P, _P, _Z, _Z, _I, _I], None),
+    "orc_mat_vec_mul_q8_0_q8_0": ([_P, _P, _P, _Z, _Z, _I, _I, _I], None),
+    "orc_dequantize_q4_k": ([_P, _P, _Z], None),
+    "orc_q4_k_scale_min": ([_P, _I, _P, _P], None),
+    "orc_vec_dot_q4_k_q8_0": ([_P, _P, _Z], _F),
+    "orc_mat_vec_mul_q4_k_q8_0": ([_P, _P, _P, _Z, _Z, _I], None),
+    "orc_argmax_f32": ([_P, _Z], ctypes.c_int64),
+    "orc_rms_norm": ([_P, _P, _F, _P, _Z], None),
+    "orc_rope_1d": ([_P, _Z, _Z, _F, _F], None),
+    "orc_rope_1d_batched": ([_P, _Z, _Z, _Z, _F, _F], None),
+    "orc_gelu_approx": ([_F], _F),
+    "orc_geglu": ([_P, _P, _P, _Z], None),
+    "orc_silu": ([_F], _F),
+    "orc_softmax": ([_P, _Z], None),
+    "orc_attention_f16": ([_P, _P, _P, _P, _Z, _Z, _Z, _Z, _F], None),
+    "orc_gemma2_step": ([ctypes.POINTER(Gemma2), ctypes.c_int64, ctypes.c_int64, _P, _P, _P, _I], ctypes.c_int64),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built (make -C oracle)")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, (args, res) in _SIG.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = res
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags.c_contiguous
+    return a.ctypes.data
+
+
+# ---- thin numpy wrappers ----------------------------------------------------
+
+def f16_to_f32(h: int) -> float:
+    return float(lib().orc_f16_to_f32(h))
+
+
+def f32_to_f16(f: float) -> int:
+    return int(lib().orc_f32_to_f16(f))
+
+
+def f32_to_f16_rne(f: float) -> int:
+    return int(lib().orc_f32_to_f16_rne(f))
+
+
+def host_isa() -> int:
+    return int(lib().orc_host_isa())
+
+
+def quantize_q8_0(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(x.size // 32 * 34, dtype=np.uint8)
+    lib().orc_quantize_q8_0(_p(x), _p(out), x.size)
+    return out
+
+
+def quantize_q4_0(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(x.size // 32 * 18, dtype=np.uint8)
+    lib().orc_quantize_q4_0(_p(x), _p(out), x.size)
+    return out
+
+
+def dequantize_q8_0(b: np.ndarray, n: int) -> np.ndarray:
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    out = np.zeros(n, dtype=np.float32)
+    lib().orc_dequantize_q8_0(_p(b), _p(out), n)
+    return out
+
+
+def dequantize_q4_0(b: np.ndarray, n: int) -> np.ndarray:
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    out = np.zeros(n, dtype=np.float32)
+    lib().orc_dequantize_q4_0(_p(b), _p(out), n)
+    return out
+
+
+def dequantize_q4_k(b: np.ndarray, n: int) -> np.ndarray:
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    out = np.zeros(n, dtype=np.float32)
+    lib().orc_dequantize_q4_k(_p(b), _p(out), n)
+    return out
+
+
+def vec_dot_q4_0_q8_0(w: np.ndarray, a: np.ndarray, n: int, isa: int = -1) -> float:
+    return float(lib().orc_vec_dot_q4_0_q8_0(_p(np.ascontiguousarray(w)), _p(np.ascontiguousarray(a)), n, isa))
+
+
+def vec_dot_q8_0_q8_0(x: np.ndarray, y: np.ndarray, n: int, isa: int = -1) -> float:
+    return float(lib().orc_vec_dot_q8_0_q8_0(_p(np.ascontiguousarray(x)), _p(np.ascontiguousarray(y)), n, isa))
+
+
+def vec_dot_q4_k_q8_0(w: np.ndarray, a: np.ndarray, n: int) -> float:
+    return float(lib().orc_vec_dot_q4_k_q8_0(_p(np.ascontiguousarray(w)), _p(np.ascontiguousarray(a)), n))
+
+
+def block_isums_q4_0_q8_0(w: np.ndarray, a: np.ndarray, n: int) -> np.ndarray:
+    out = np.zeros(n // 32, dtype=np.int32)
+    lib().orc_block_isums_q4_0_q8_0(_p(np.ascontiguousarray(w)), _p(np.ascontiguousarray(a)), n, _p(out))
+    return out
+
+
+def block_isums_q8_0_q8_0(x: np.ndarray, y: np.ndarray, n: int) -> np.ndarray:
+    out = np.zeros(n // 32, dtype=np.int32)
+    lib().orc_block_isums_q8_0_q8_0(_p(np.ascontiguousarray(x)), _p(np.ascontiguousarray(y)), n, _p(out))
+    return out
+
+
+def mat_vec_mul_q4_0_q8_0(w, x_q8, rows, cols, isa=-1, threads=1) -> np.ndarray:
+    y = np.zeros(rows, dtype=np.float32)
+    lib().orc_mat_vec_mul_q4_0_q8_0(_p(np.ascontiguousarray(w)), _p(np.ascontiguousarray(x_q8)), _p(y),
+                                    rows, cols, isa, threads)
+    return y
+
+
+def mat_vec_mul_q4_0(w, x, rows, cols, isa=-1, threads=1) -> np.ndarray:
+    y = np.zeros(rows, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    lib().orc_mat_vec_mul_q4_0(_p(np.ascontiguousarray(w)), _p(x), _p(y), rows, cols, isa, threads)
+    return y
+
+
+def mat_vec_mul_q8_0_q8_0(w, x_q8, rows, cols, softcap=False, isa=-1, threads=1) -> np.ndarray:
+    y = np.zeros(rows, dtype=np.float32)
+    lib().orc_mat_vec_mul_q8_0_q8_0(_p(np.ascontiguousarray(w)), _p(np.ascontiguousarray(x_q8)), _p(y),
+                                    rows, cols, int(softcap), isa, threads)
+    return y
+
+
+def mat_vec_mul_q4_k_q8_0(w, x_q8, rows, cols, threads=1) -> np.ndarray:
+    y = np.zeros(rows, dtype=np.float32)
+    lib().orc_mat_vec_mul_q4_k_q8_0(_p(np.ascontiguousarray(w)), _p(np.ascontiguousarray(x_q8)), _p(y),
+                                    rows, cols, threads)
+    return y
+
+
+def q4_k_scale_min(scales12: np.ndarray, j: int) -> tuple[int, int]:
+    sc, m = ctypes.c_uint8(), ctypes.c_uint8()
+    lib().orc_q4_k_scale_min(_p(np.ascontiguousarray(scales12, dtype=np.uint8)), j, ctypes.byref(sc),
+                             ctypes.byref(m))
+    return int(sc.value), int(m.value)
+
+
+def argmax_f32(x: np.ndarray) -> int:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return int(lib().orc_argmax_f32(_p(x), x.size))
+
+
+def rms_norm(x, w=None, eps=1e-6) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros_like(x)
+    wp = None if w is None else _p(np.ascontiguousarray(w, dtype=np.float32))
+    lib().orc_rms_norm(_p(x), wp, eps, _p(out), x.size)
+    return out
+
+
+def rope_1d(v, pos, head_dim, base=10000.0, scale=1.0) -> np.ndarray:
+    v = np.array(v, dtype=np.float32, copy=True)
+    lib().orc_rope_1d(_p(v), pos, head_dim, base, scale)
+    return v
+
+
+def rope_1d_batched(v, pos, n_heads, head_dim, base=10000.0, scale=1.0) -> np.ndarray:
+    v = np.array(v, dtype=np.float32, copy=True)
+    lib().orc_rope_1d_batched(_p(v), pos, n_heads, head_dim, base, scale)
+    return v
+
+
+def gelu_approx(x: float) -> float:
+    return float(lib().orc_gelu_approx(x))
+
+
+def geglu(g, u) -> np.ndarray:
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    u = np.ascontiguousarray(u, dtype=np.float32)
+    out = np.zeros_like(g)
+    lib().orc_geglu(_p(g), _p(u), _p(out), g.size)
+    return out
+
+
+def silu(x: float) -> float:
+    return float(lib().orc_silu(x))
+
+
+def softmax(x) -> np.ndarray:
+    x = np.array(x, dtype=np.float32, copy=True)
+    lib().orc_softmax(_p(x), x.size)
+    return x
+
+
+def attention_f16(q, k_cache, v_cache, n_past, n_heads, n_kv_heads, head_dim, scale) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    out = np.zeros(n_heads * head_dim, dtype=np.float32)
+    lib().orc_attention_f16(_p(q), _p(np.ascontiguousarray(k_cache, dtype=np.uint16)),
+                            _p(np.ascontiguousarray(v_cache, dtype=np.uint16)), _p(out), n_past, n_heads,
+                            n_kv_heads, head_dim, scale)
+    return out

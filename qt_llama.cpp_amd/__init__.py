@@ -1,0 +1,381 @@
+"""Host-side mirror of the reference's GPU operator surface over the C ABI.
+
+The reference (mitchellrenouf/QT_llama.cpp) drives its GPU path through
+``CudaDevice`` / ``CudaBuffer`` in ``crates/mrml-tensor/src/cuda.rs``.  This
+module gives the same surface -- ``HipDevice.new(0)``, ``HipBuffer.from_host``,
+``dev.gemv_q4_0(w, x, y, rows, cols)``, ``dev.sync()`` ... -- over
+``lib/libmrml_hip.so`` (``include/mrml_hip.h``) with ctypes and numpy, so
+callers and tests read like the reference's own ``tests/ops_test.rs``.
+
+Differences from the reference surface, all deliberate:
+
+* Errors raise :class:`HipError` instead of panicking (the reference's op
+  wrappers ``.expect()`` every launch, e.g. ``cuda.rs:2304``).
+* Quantised weights are converted once to the backend layout
+  (``HipBuffer.from_gguf``); ``gemv_q4_0_gguf`` reads raw GGUF bytes.
+* Matvec outputs follow the reference CPU semantics (Q8_0-quantised
+  activations, exact integer block dots, ordered f32 fold), not the
+  reference CUDA kernels' f32 dequantise-and-FMA.
+
+There is no CPU fallback: if the library or a gfx950 device is missing,
+construction raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "lib" / "libmrml_hip.so"
+
+Q4_0 = 2
+Q8_0 = 8
+Q4_K = 12
+
+# bytes per block and weights per block, GGUF (types.rs:32-70)
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144}
+BLOCK_WEIGHTS = {Q4_0: 32, Q8_0: 32, Q4_K: 256}
+
+_STATUS = {
+    0: "ok",
+    -1: "invalid argument",
+    -2: "allocation failed",
+    -3: "HIP runtime error",
+    -4: "unsupported",
+    -5: "no gfx950 device",
+}
+
+
+class HipError(RuntimeError):
+    """A C-ABI call returned a negative status."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{_STATUS.get(status, status)}: {message}")
+        self.status = status
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char * 64),
+        ("compute_units", ctypes.c_int32),
+        ("clock_khz", ctypes.c_int32),
+        ("runtime_version", ctypes.c_int32),
+        ("abi_version", ctypes.c_int32),
+        ("total_memory", ctypes.c_uint64),
+        ("l2_bytes", ctypes.c_uint64),
+    ]
+
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int32
+_Z = ctypes.c_size_t
+
+# name -> argtypes; every function returns int status unless listed in _RESTYPE
+_SIGNATURES = {
+    "mrml_hip_device_count": [ctypes.POINTER(ctypes.c_int32)],
+    "mrml_hip_create": [_I, ctypes.POINTER(_P)],
+    "mrml_hip_destroy": [_P],
+    "mrml_hip_last_error": [_P],
+    "mrml_hip_status_string": [ctypes.c_int],
+    "mrml_hip_sync": [_P],
+    "mrml_hip_device_info_get": [_P, ctypes.POINTER(DeviceInfo)],
+    "mrml_hip_memory_info": [_P, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)],
+    "mrml_hip_stream": [_P],
+    "mrml_hip_reserve_workspace": [_P, _Z],
+    "mrml_hip_graph_begin": [_P],
+    "mrml_hip_graph_end": [_P, ctypes.POINTER(_P)],
+    "mrml_hip_graph_launch": [_P, _P],
+    "mrml_hip_graph_destroy": [_P, _P],
+    "mrml_hip_malloc": [_P, _Z, ctypes.POINTER(_P)],
+    "mrml_hip_free": [_P, _P],
+    "mrml_hip_memcpy_h2d": [_P, _P, _P, _Z],
+    "mrml_hip_memcpy_d2h": [_P, _P, _P, _Z],
+    "mrml_hip_memcpy_h2d_async": [_P, _P, _P, _Z],
+    "mrml_hip_memcpy_d2d_async": [_P, _P, _P, _Z],
+    "mrml_hip_zero_async": [_P, _P, _Z],
+    "mrml_hip_copy_kernel": [_P, _P, _P, _Z],
+    "mrml_hip_repack_q4_0": [_P, _P, _P, _I, _I],
+    "mrml_hip_repack_q8_0": [_P, _P, _P, _I, _I],
+    "mrml_hip_repack_q4_k": [_P, _P, _P, _I, _I],
+    "mrml_hip_quantize_q8_0": [_P, _P, _P, _P, _I],
+    "mrml_hip_q8_0_pack_bytes": [_I],
+    "mrml_hip_gemv_q4_0": [_P, _P, _P, _P, _I, _I],
+    "mrml_hip_gemv_q4_0_q8": [_P, _P, _P, _P, _I, _I],
+    "mrml_hip_gemv_q4_0_gguf": [_P, _P, _P, _P, _I, _I],
+    "mrml_hip_gemv_q4_0_geglu": [_P, _P, _P, _P, _P, _I, _I],
+    "mrml_hip_gemv_q4_0_qkv": [_P, _P, _P, _P, _P, _P, _I, _I, _I],
+    "mrml_hip_gemv_q4_0_geglu_q8": [_P, _P, _P, _P, _P, _I, _I],
+    "mrml_hip_gemv_q4_0_qkv_q8": [_P, _P, _P, _P, _P, _P, _I, _I, _I],
+    "mrml_hip_gemv_q8_0": [_P, _P, _P, _P, _I, _I, _I],
+    "mrml_hip_gemv_q4_k": [_P, _P, _P, _P, _I, _I],
+    "mrml_hip_argmax_f32": [_P, _P, _I, _P],
+}
+_RESTYPE = {
+    "mrml_hip_last_error": ctypes.c_char_p,
+    "mrml_hip_status_string": ctypes.c_char_p,
+    "mrml_hip_stream": _P,
+    "mrml_hip_q8_0_pack_bytes": _Z,
+}
+
+_lib = None
+
+
+def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
+    """Load libmrml_hip.so and declare every exported C-ABI function."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise HipError(-4, f"{p} is not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(str(p))
+    for name, args in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = _RESTYPE.get(name, ctypes.c_int)
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def device_count() -> int:
+    n = ctypes.c_int32(0)
+    load_library().mrml_hip_device_count(ctypes.byref(n))
+    return int(n.value)
+
+
+def _ptr(x) -> int | None:
+    if x is None:
+        return None
+    if isinstance(x, HipBuffer):
+        return x.ptr
+    return int(x)
+
+
+class HipBuffer:
+    """A device allocation (CudaBuffer, cuda.rs:1243-1513).  Frees on close/GC."""
+
+    def __init__(self, dev: "HipDevice", nbytes: int, dtype=np.uint8, shape=None):
+        self.dev = dev
+        self.nbytes = int(nbytes)
+        self.dtype = np.dtype(dtype)
+        self.shape = shape if shape is not None else (self.nbytes // self.dtype.itemsize,)
+        p = ctypes.c_void_p()
+        dev._check(dev.lib.mrml_hip_malloc(dev.ctx, self.nbytes, ctypes.byref(p)))
+        self.ptr = int(p.value)
+
+    # CudaBuffer::alloc_on / from_host_on
+    @classmethod
+    def alloc(cls, dev: "HipDevice", count: int, dtype=np.float32) -> "HipBuffer":
+        dt = np.dtype(dtype)
+        return cls(dev, count * dt.itemsize, dt, (count,))
+
+    @classmethod
+    def from_host(cls, dev: "HipDevice", arr: np.ndarray) -> "HipBuffer":
+        arr = np.ascontiguousarray(arr)
+        b = cls(dev, arr.nbytes, arr.dtype, arr.shape)
+        b.copy_from_host(arr)
+        return b
+
+    @classmethod
+    def from_gguf(cls, dev: "HipDevice", gguf_bytes: np.ndarray, qtype: int, rows: int, cols: int) -> "HipBuffer":
+        """Upload a GGUF-layout quantised matrix and convert it to the backend layout."""
+        raw = cls.from_host(dev, np.ascontiguousarray(gguf_bytes, dtype=np.uint8).reshape(-1))
+        try:
+            out = cls(dev, raw.nbytes, np.uint8)
+            fn = {Q4_0: dev.lib.mrml_hip_repack_q4_0, Q8_0: dev.lib.mrml_hip_repack_q8_0,
+                  Q4_K: dev.lib.mrml_hip_repack_q4_k}[qtype]
+            dev._check(fn(dev.ctx, raw.ptr, out.ptr, rows, cols))
+            dev.sync()
+        finally:
+            raw.close()
+        return out
+
+    def copy_from_host(self, arr: np.ndarray) -> None:
+        arr = np.ascontiguousarray(arr)
+        if arr.nbytes != self.nbytes:
+            raise ValueError(f"size mismatch: {arr.nbytes} != {self.nbytes}")
+        self.dev._check(self.dev.lib.mrml_hip_memcpy_h2d(self.dev.ctx, self.ptr, arr.ctypes.data, arr.nbytes))
+
+    def copy_to_host(self, out: np.ndarray | None = None) -> np.ndarray:
+        if out is None:
+            out = np.empty(self.shape, dtype=self.dtype)
+        if out.nbytes != self.nbytes:
+            raise ValueError(f"size mismatch: {out.nbytes} != {self.nbytes}")
+        self.dev._check(self.dev.lib.mrml_hip_memcpy_d2h(self.dev.ctx, out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+    def numpy(self) -> np.ndarray:
+        return self.copy_to_host()
+
+    def close(self) -> None:
+        if self.ptr and self.dev.ctx:
+            self.dev.lib.mrml_hip_free(self.dev.ctx, self.ptr)
+        self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class HipDevice:
+    """One context = one device + one stream (CudaDevice, cuda.rs:1883-3112)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_library()
+        ctx = ctypes.c_void_p()
+        rc = self.lib.mrml_hip_create(device, ctypes.byref(ctx))
+        if rc != 0:
+            raise HipError(rc, f"mrml_hip_create({device})")
+        self.ctx = ctx.value
+        self.device = device
+
+    @classmethod
+    def new(cls, device: int = 0) -> "HipDevice":
+        return cls(device)
+
+    @staticmethod
+    def is_available() -> bool:
+        try:
+            return device_count() > 0
+        except Exception:
+            return False
+
+    def _check(self, rc: int) -> None:
+        if rc != 0:
+            msg = self.lib.mrml_hip_last_error(self.ctx) or b""
+            raise HipError(rc, msg.decode(errors="replace"))
+
+    def close(self) -> None:
+        if self.ctx:
+            self.lib.mrml_hip_destroy(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- lifecycle -----------------------------------------------------------
+    def sync(self) -> None:
+        self._check(self.lib.mrml_hip_sync(self.ctx))
+
+    def device_info(self) -> dict:
+        info = DeviceInfo()
+        self._check(self.lib.mrml_hip_device_info_get(self.ctx, ctypes.byref(info)))
+        return {f: (getattr(info, f).decode() if f == "name" else getattr(info, f)) for f, _ in info._fields_}
+
+    def memory_info(self) -> tuple[int, int]:
+        f, t = ctypes.c_uint64(), ctypes.c_uint64()
+        self._check(self.lib.mrml_hip_memory_info(self.ctx, ctypes.byref(f), ctypes.byref(t)))
+        return int(f.value), int(t.value)
+
+    @property
+    def stream(self) -> int:
+        return int(self.lib.mrml_hip_stream(self.ctx) or 0)
+
+    def reserve_workspace(self, nbytes: int) -> None:
+        self._check(self.lib.mrml_hip_reserve_workspace(self.ctx, nbytes))
+
+    def zero(self, buf, nbytes: int | None = None) -> None:
+        self._check(self.lib.mrml_hip_zero_async(self.ctx, _ptr(buf), buf.nbytes if nbytes is None else nbytes))
+
+    # ---- graphs (CudaDevice::capture / launch_graph, cuda.rs:1957-2003) -------
+    def capture(self, fn) -> "HipGraph":
+        """Record the ops `fn()` issues on this device into a replayable graph."""
+        self._check(self.lib.mrml_hip_graph_begin(self.ctx))
+        try:
+            fn()
+        except BaseException:
+            g = ctypes.c_void_p()
+            self.lib.mrml_hip_graph_end(self.ctx, ctypes.byref(g))
+            if g.value:
+                self.lib.mrml_hip_graph_destroy(self.ctx, g.value)
+            raise
+        g = ctypes.c_void_p()
+        self._check(self.lib.mrml_hip_graph_end(self.ctx, ctypes.byref(g)))
+        return HipGraph(self, g.value)
+
+    def copy_kernel(self, dst, src, nbytes: int) -> None:
+        self._check(self.lib.mrml_hip_copy_kernel(self.ctx, _ptr(dst), _ptr(src), nbytes))
+
+    # ---- ops (names follow CudaDevice) -----------------------------------------
+    def quantize_q8_0(self, x, q8_gguf=None, pack=None, n: int | None = None) -> None:
+        n = x.shape[0] if n is None else n
+        self._check(self.lib.mrml_hip_quantize_q8_0(self.ctx, _ptr(x), _ptr(q8_gguf), _ptr(pack), n))
+
+    def q8_0_pack_bytes(self, n: int) -> int:
+        return int(self.lib.mrml_hip_q8_0_pack_bytes(n))
+
+    def gemv_q4_0(self, w, x, y, rows: int, cols: int) -> None:
+        self._check(self.lib.mrml_hip_gemv_q4_0(self.ctx, _ptr(w), _ptr(x), _ptr(y), rows, cols))
+
+    def gemv_q4_0_q8(self, w, xpack, y, rows: int, cols: int) -> None:
+        self._check(self.lib.mrml_hip_gemv_q4_0_q8(self.ctx, _ptr(w), _ptr(xpack), _ptr(y), rows, cols))
+
+    def gemv_q4_0_gguf(self, w, x, y, rows: int, cols: int) -> None:
+        self._check(self.lib.mrml_hip_gemv_q4_0_gguf(self.ctx, _ptr(w), _ptr(x), _ptr(y), rows, cols))
+
+    def gemv_q4_0_geglu(self, w_gate, w_up, x, act, rows: int, cols: int) -> None:
+        self._check(self.lib.mrml_hip_gemv_q4_0_geglu(self.ctx, _ptr(w_gate), _ptr(w_up), _ptr(x), _ptr(act),
+                                                      rows, cols))
+
+    def gemv_q4_0_qkv(self, wq, wk, wv, x, y, q_rows: int, kv_rows: int, cols: int) -> None:
+        self._check(self.lib.mrml_hip_gemv_q4_0_qkv(self.ctx, _ptr(wq), _ptr(wk), _ptr(wv), _ptr(x), _ptr(y),
+                                                    q_rows, kv_rows, cols))
+
+    def gemv_q4_0_geglu_q8(self, w_gate, w_up, xpack, act, rows: int, cols: int) -> None:
+        self._check(self.lib.mrml_hip_gemv_q4_0_geglu_q8(self.ctx, _ptr(w_gate), _ptr(w_up), _ptr(xpack),
+                                                         _ptr(act), rows, cols))
+
+    def gemv_q4_0_qkv_q8(self, wq, wk, wv, xpack, y, q_rows: int, kv_rows: int, cols: int) -> None:
+        self._check(self.lib.mrml_hip_gemv_q4_0_qkv_q8(self.ctx, _ptr(wq), _ptr(wk), _ptr(wv), _ptr(xpack),
+                                                       _ptr(y), q_rows, kv_rows, cols))
+
+    def gemv_q8_0(self, w, x, y, rows: int, cols: int, softcap: bool = False) -> None:
+        self._check(self.lib.mrml_hip_gemv_q8_0(self.ctx, _ptr(w), _ptr(x), _ptr(y), rows, cols, int(softcap)))
+
+    def gemv_q4_k(self, w, x, y, rows: int, cols: int) -> None:
+        self._check(self.lib.mrml_hip_gemv_q4_k(self.ctx, _ptr(w), _ptr(x), _ptr(y), rows, cols))
+
+    def argmax_f32(self, x, n: int, out) -> None:
+        self._check(self.lib.mrml_hip_argmax_f32(self.ctx, _ptr(x), n, _ptr(out)))
+
+
+class HipGraph:
+    """An instantiated graph (CudaGraphExec, cuda.rs:1841-1858)."""
+
+    def __init__(self, dev: HipDevice, exec_ptr: int):
+        self.dev = dev
+        self.exec = exec_ptr
+
+    def launch(self) -> None:
+        self.dev._check(self.dev.lib.mrml_hip_graph_launch(self.dev.ctx, self.exec))
+
+    def close(self) -> None:
+        if self.exec and self.dev.ctx:
+            self.dev.lib.mrml_hip_graph_destroy(self.dev.ctx, self.exec)
+        self.exec = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+__all__ = [
+    "HipDevice", "HipBuffer", "HipGraph", "HipError", "load_library", "device_count", "exported_symbols",
+    "Q4_0", "Q8_0", "Q4_K", "BLOCK_BYTES", "BLOCK_WEIGHTS", "LIB_PATH",
+]

@@ -1,0 +1,171 @@
+// quant.hip -- Q8_0 activation quantiser, weight layout conversion, fills.
+
+#include "device.h"
+#include "internal.h"
+
+namespace mrml {
+
+// quant.rs:193-228, one 32-value block per half-wave (lane l owns value l).
+//   amax   : max |x| (starts at 0, NaN never wins) -- exact in any order
+//   scale  = amax / 127          (IEEE division)
+//   d      = f32_to_f16 by truncation
+//   id     = scale != 0 ? 1/scale : 0   (from the unrounded scale)
+//   q      = (int8) clamp(roundf(x*id), -128, 127), NaN -> 0
+// The pack additionally stores d widened to f32 and the block's quant sum.
+__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x,
+                                                            uint8_t *__restrict__ gguf,
+                                                            uint8_t *__restrict__ pack, int nb)
+{
+    const int gb = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 5);
+    const int l = threadIdx.x & 31;
+    if (gb >= nb) return;  // whole half-waves exit together
+    const float v = x[(size_t)gb * 32 + l];
+    float a = fabsf(v);
+    float m = (a > 0.0f) ? a : 0.0f;  // NaN -> 0
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) {
+        float o = __shfl_xor(m, off, 32);
+        m = (o > m) ? o : m;
+    }
+    const float scale = m / 127.0f;
+    const uint32_t dbits = f32_to_f16_trunc(scale);
+    const float id = (scale != 0.0f) ? 1.0f / scale : 0.0f;
+    float r = roundf(v * id);
+    r = (r < -128.0f) ? -128.0f : r;
+    r = (r > 127.0f) ? 127.0f : r;
+    const int q = (r != r) ? 0 : (int)r;
+    int s = q;
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) s += __shfl_xor(s, off, 32);
+    if (gguf) {
+        uint8_t *blk = gguf + (size_t)gb * 34;
+        if (l == 0) *reinterpret_cast<uint16_t *>(blk) = (uint16_t)dbits;
+        blk[2 + l] = (uint8_t)(int8_t)q;
+    }
+    if (pack) {
+        pack[(size_t)gb * 32 + l] = (uint8_t)(int8_t)q;
+        if (l == 0) {
+            reinterpret_cast<float *>(pack + (size_t)nb * 32)[gb] = f16_bits_to_f32(dbits);
+            reinterpret_cast<int32_t *>(pack + (size_t)nb * 36)[gb] = s;
+        }
+    }
+}
+
+int launch_quantize_q8_0(mrml_hip_ctx *ctx, const float *x, void *gguf, void *pack, int32_t n)
+{
+    const int nb = n / 32;
+    const int threads = 256;  // 8 blocks per workgroup
+    const int grid = (nb * 32 + threads - 1) / threads;
+    hipLaunchKernelGGL(quantize_q8_0_kernel, dim3(grid), dim3(threads), 0, ctx->stream, x,
+                       (uint8_t *)gguf, (uint8_t *)pack, nb);
+    return check_launch(ctx, "quantize_q8_0_kernel");
+}
+
+// GGUF Q4_0 -> backend layout: qs plane [rows*nb][16] then d plane [rows*nb] f16.
+// One thread per block; byte loads because GGUF blocks are only 2-aligned.
+__global__ void repack_q4_0_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, size_t nblocks)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const uint8_t *b = src + i * 18;
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        w[k] = (uint32_t)b[2 + 4 * k] | ((uint32_t)b[3 + 4 * k] << 8) | ((uint32_t)b[4 + 4 * k] << 16) |
+               ((uint32_t)b[5 + 4 * k] << 24);
+    reinterpret_cast<uint4 *>(dst)[i] = make_uint4(w[0], w[1], w[2], w[3]);
+    reinterpret_cast<uint16_t *>(dst + nblocks * 16)[i] = (uint16_t)(b[0] | (b[1] << 8));
+}
+
+// GGUF Q8_0 -> qs plane [rows*nb][32] then d plane [rows*nb] f16.
+__global__ void repack_q8_0_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, size_t nblocks)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const uint8_t *b = src + i * 34;
+    uint32_t w[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+        w[k] = (uint32_t)b[2 + 4 * k] | ((uint32_t)b[3 + 4 * k] << 8) | ((uint32_t)b[4 + 4 * k] << 16) |
+               ((uint32_t)b[5 + 4 * k] << 24);
+    uint4 *q = reinterpret_cast<uint4 *>(dst) + 2 * i;
+    q[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    q[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    reinterpret_cast<uint16_t *>(dst + nblocks * 32)[i] = (uint16_t)(b[0] | (b[1] << 8));
+}
+
+// GGUF Q4_K -> qs plane [rows*nsb][128] then header plane [rows*nsb][16]
+// = {d, dmin, scales[12]}.  GGUF super-blocks are 144 B, so 16-aligned.
+__global__ void repack_q4_k_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, size_t nsb)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nsb) return;
+    const uint4 *b = reinterpret_cast<const uint4 *>(src + i * 144);
+    uint4 *q = reinterpret_cast<uint4 *>(dst) + 8 * i;
+#pragma unroll
+    for (int k = 0; k < 8; k++) q[k] = b[1 + k];
+    reinterpret_cast<uint4 *>(dst + nsb * 128)[i] = b[0];
+}
+
+int launch_repack_q4_0(mrml_hip_ctx *ctx, const void *src, void *dst, int32_t rows, int32_t cols)
+{
+    size_t n = (size_t)rows * (size_t)(cols / 32);
+    hipLaunchKernelGGL(repack_q4_0_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream,
+                       (const uint8_t *)src, (uint8_t *)dst, n);
+    return check_launch(ctx, "repack_q4_0_kernel");
+}
+
+int launch_repack_q8_0(mrml_hip_ctx *ctx, const void *src, void *dst, int32_t rows, int32_t cols)
+{
+    size_t n = (size_t)rows * (size_t)(cols / 32);
+    hipLaunchKernelGGL(repack_q8_0_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream,
+                       (const uint8_t *)src, (uint8_t *)dst, n);
+    return check_launch(ctx, "repack_q8_0_kernel");
+}
+
+int launch_repack_q4_k(mrml_hip_ctx *ctx, const void *src, void *dst, int32_t rows, int32_t cols)
+{
+    if (((uintptr_t)src | (uintptr_t)dst) & 15u)
+        return fail(ctx, MRML_HIP_E_INVALID, "repack_q4_k: buffers must be 16-byte aligned");
+    size_t n = (size_t)rows * (size_t)(cols / 256);
+    hipLaunchKernelGGL(repack_q4_k_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream,
+                       (const uint8_t *)src, (uint8_t *)dst, n);
+    return check_launch(ctx, "repack_q4_k_kernel");
+}
+
+__global__ void zero_kernel(uint8_t *__restrict__ dst, size_t bytes)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; i < bytes; i += stride) dst[i] = 0;
+}
+
+// Plain streaming copy (16-byte loads and stores): the measured bandwidth
+// ceiling, and the known-size kernel that calibrates the HBM byte counters.
+__global__ __launch_bounds__(256) void copy16_kernel(uint4 *__restrict__ dst, const uint4 *__restrict__ src,
+                                                     size_t n16)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; i < n16; i += stride) dst[i] = src[i];
+}
+
+int launch_copy(mrml_hip_ctx *ctx, void *dst, const void *src, size_t bytes)
+{
+    const size_t n16 = bytes / 16;
+    size_t blocks = (n16 + 255) / 256;
+    if (blocks > 8192) blocks = 8192;   // 32 workgroups per CU, grid-stride beyond
+    hipLaunchKernelGGL(copy16_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, (uint4 *)dst,
+                       (const uint4 *)src, n16);
+    return check_launch(ctx, "copy16_kernel");
+}
+
+int launch_zero(mrml_hip_ctx *ctx, void *dst, size_t bytes)
+{
+    size_t blocks = (bytes + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, (uint8_t *)dst, bytes);
+    return check_launch(ctx, "zero_kernel");
+}
+
+}  // namespace mrml

@@ -1,0 +1,464 @@
+// runtime.hip -- the C ABI (include/mrml_hip.h): context, memory, argument
+// validation and dispatch to the kernel launchers.
+//
+// Replaces the CUDA driver-API host layer of the reference
+// (crates/mrml-tensor/src/cuda.rs): there, a dlopen'd libcuda, a PTX module
+// and a per-device stream; here, libamdhip64 linked directly, gfx950 code
+// objects linked into this library, and one stream per context.
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+
+#include "device.h"
+#include "internal.h"
+
+namespace mrml {
+
+int fail(mrml_hip_ctx *ctx, int code, const char *fmt, ...)
+{
+    if (ctx) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        ctx->err = buf;
+    }
+    return code;
+}
+
+int hip_fail(mrml_hip_ctx *ctx, hipError_t e, const char *what)
+{
+    return fail(ctx, MRML_HIP_E_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+int enter(mrml_hip_ctx *ctx)
+{
+    hipError_t e = hipSetDevice(ctx->device);
+    return e == hipSuccess ? 0 : hip_fail(ctx, e, "hipSetDevice");
+}
+
+int check_launch(mrml_hip_ctx *ctx, const char *kernel)
+{
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : hip_fail(ctx, e, kernel);
+}
+
+void *workspace(mrml_hip_ctx *ctx, size_t bytes)
+{
+    if (bytes <= ctx->ws_bytes) return ctx->ws;
+    size_t want = align_up(bytes, (size_t)1 << 20);
+    if (ctx->ws) {
+        // The old scratch may still be read by queued work.
+        hipError_t e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) { hip_fail(ctx, e, "hipStreamSynchronize (workspace)"); return nullptr; }
+        (void)hipFree(ctx->ws);
+        ctx->ws = nullptr;
+        ctx->ws_bytes = 0;
+    }
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, want);
+    if (e != hipSuccess) {
+        fail(ctx, MRML_HIP_E_ALLOC, "workspace hipMalloc(%zu): %s", want, hipGetErrorString(e));
+        return nullptr;
+    }
+    ctx->ws = p;
+    ctx->ws_bytes = want;
+    return p;
+}
+
+}  // namespace mrml
+
+using namespace mrml;
+
+#define CTX_GUARD(ctx)                                      \
+    do {                                                    \
+        if (!(ctx)) return MRML_HIP_E_INVALID;              \
+        int rc_ = enter(ctx);                               \
+        if (rc_) return rc_;                                \
+    } while (0)
+
+#define REQUIRE(ctx, cond, ...)                                             \
+    do {                                                                    \
+        if (!(cond)) return fail((ctx), MRML_HIP_E_INVALID, __VA_ARGS__);   \
+    } while (0)
+
+extern "C" {
+
+const char *mrml_hip_status_string(int status)
+{
+    switch (status) {
+    case MRML_HIP_OK: return "ok";
+    case MRML_HIP_E_INVALID: return "invalid argument";
+    case MRML_HIP_E_ALLOC: return "allocation failed";
+    case MRML_HIP_E_HIP: return "HIP runtime error";
+    case MRML_HIP_E_UNSUPPORTED: return "unsupported";
+    case MRML_HIP_E_NODEVICE: return "no gfx950 device";
+    default: return "unknown status";
+    }
+}
+
+int mrml_hip_device_count(int32_t *count)
+{
+    if (!count) return MRML_HIP_E_INVALID;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    *count = (e == hipSuccess) ? n : 0;
+    return MRML_HIP_OK;
+}
+
+int mrml_hip_create(int32_t device, mrml_hip_ctx **out)
+{
+    if (!out) return MRML_HIP_E_INVALID;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return MRML_HIP_E_NODEVICE;
+    mrml_hip_ctx *ctx = new (std::nothrow) mrml_hip_ctx();
+    if (!ctx) return MRML_HIP_E_ALLOC;
+    ctx->device = device;
+    if (hipSetDevice(device) != hipSuccess || hipGetDeviceProperties(&ctx->props, device) != hipSuccess) {
+        delete ctx;
+        return MRML_HIP_E_NODEVICE;
+    }
+    // The kernels are compiled for gfx950 only.
+    if (std::strncmp(ctx->props.gcnArchName, "gfx950", 6) != 0) {
+        delete ctx;
+        return MRML_HIP_E_NODEVICE;
+    }
+    // Default priority, non-blocking with respect to the null stream.
+    if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete ctx;
+        return MRML_HIP_E_HIP;
+    }
+    *out = ctx;
+    return MRML_HIP_OK;
+}
+
+int mrml_hip_destroy(mrml_hip_ctx *ctx)
+{
+    if (!ctx) return MRML_HIP_OK;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return MRML_HIP_OK;
+}
+
+const char *mrml_hip_last_error(const mrml_hip_ctx *ctx)
+{
+    return ctx ? ctx->err.c_str() : "null context";
+}
+
+int mrml_hip_sync(mrml_hip_ctx *ctx)
+{
+    CTX_GUARD(ctx);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? 0 : hip_fail(ctx, e, "hipStreamSynchronize");
+}
+
+int mrml_hip_device_info_get(mrml_hip_ctx *ctx, mrml_hip_device_info *info)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, info, "info is null");
+    std::memset(info, 0, sizeof *info);
+    std::snprintf(info->name, sizeof info->name, "%s", ctx->props.gcnArchName);
+    info->compute_units = ctx->props.multiProcessorCount;
+    info->clock_khz = ctx->props.clockRate;
+    int rv = 0;
+    (void)hipRuntimeGetVersion(&rv);
+    info->runtime_version = rv;
+    info->abi_version = MRML_HIP_ABI_VERSION;
+    info->total_memory = ctx->props.totalGlobalMem;
+    info->l2_bytes = (uint64_t)ctx->props.l2CacheSize;
+    return MRML_HIP_OK;
+}
+
+int mrml_hip_memory_info(mrml_hip_ctx *ctx, uint64_t *free_bytes, uint64_t *total_bytes)
+{
+    CTX_GUARD(ctx);
+    size_t f = 0, t = 0;
+    hipError_t e = hipMemGetInfo(&f, &t);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipMemGetInfo");
+    if (free_bytes) *free_bytes = f;
+    if (total_bytes) *total_bytes = t;
+    return MRML_HIP_OK;
+}
+
+void *mrml_hip_stream(mrml_hip_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int mrml_hip_reserve_workspace(mrml_hip_ctx *ctx, size_t bytes)
+{
+    CTX_GUARD(ctx);
+    return workspace(ctx, bytes) ? MRML_HIP_OK : MRML_HIP_E_ALLOC;
+}
+
+int mrml_hip_graph_begin(mrml_hip_ctx *ctx)
+{
+    CTX_GUARD(ctx);
+    hipError_t e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal);
+    return e == hipSuccess ? 0 : hip_fail(ctx, e, "hipStreamBeginCapture");
+}
+
+int mrml_hip_graph_end(mrml_hip_ctx *ctx, void **graph_exec_out)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, graph_exec_out, "graph_exec_out is null");
+    *graph_exec_out = nullptr;
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipGraphInstantiate");
+    *graph_exec_out = (void *)exec;
+    return MRML_HIP_OK;
+}
+
+int mrml_hip_graph_launch(mrml_hip_ctx *ctx, void *graph_exec)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, graph_exec, "graph_exec is null");
+    hipError_t e = hipGraphLaunch((hipGraphExec_t)graph_exec, ctx->stream);
+    return e == hipSuccess ? 0 : hip_fail(ctx, e, "hipGraphLaunch");
+}
+
+int mrml_hip_graph_destroy(mrml_hip_ctx *ctx, void *graph_exec)
+{
+    CTX_GUARD(ctx);
+    if (!graph_exec) return MRML_HIP_OK;
+    hipError_t e = hipGraphExecDestroy((hipGraphExec_t)graph_exec);
+    return e == hipSuccess ? 0 : hip_fail(ctx, e, "hipGraphExecDestroy");
+}
+
+int mrml_hip_malloc(mrml_hip_ctx *ctx, size_t bytes, void **d_out)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, d_out, "d_out is null");
+    *d_out = nullptr;
+    hipError_t e = hipMalloc(d_out, bytes ? bytes : 1);
+    if (e != hipSuccess) return fail(ctx, MRML_HIP_E_ALLOC, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    return MRML_HIP_OK;
+}
+
+int mrml_hip_free(mrml_hip_ctx *ctx, void *d_ptr)
+{
+    CTX_GUARD(ctx);
+    if (!d_ptr) return MRML_HIP_OK;
+    hipError_t e = hipFree(d_ptr);
+    return e == hipSuccess ? 0 : hip_fail(ctx, e, "hipFree");
+}
+
+int mrml_hip_memcpy_h2d(mrml_hip_ctx *ctx, void *d_dst, const void *h_src, size_t bytes)
+{
+    CTX_GUARD(ctx);
+    if (!bytes) return MRML_HIP_OK;
+    REQUIRE(ctx, d_dst && h_src, "null pointer");
+    hipError_t e = hipMemcpyAsync(d_dst, h_src, bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? 0 : hip_fail(ctx, e, "hipMemcpy H2D");
+}
+
+int mrml_hip_memcpy_d2h(mrml_hip_ctx *ctx, void *h_dst, const void *d_src, size_t bytes)
+{
+    CTX_GUARD(ctx);
+    if (!bytes) return MRML_HIP_OK;
+    REQUIRE(ctx, h_dst && d_src, "null pointer");
+    hipError_t e = hipMemcpyAsync(h_dst, d_src, bytes, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? 0 : hip_fail(ctx, e, "hipMemcpy D2H");
+}
+
+int mrml_hip_memcpy_h2d_async(mrml_hip_ctx *ctx, void *d_dst, const void *h_src, size_t bytes)
+{
+    CTX_GUARD(ctx);
+    if (!bytes) return MRML_HIP_OK;
+    REQUIRE(ctx, d_dst && h_src, "null pointer");
+    hipError_t e = hipMemcpyAsync(d_dst, h_src, bytes, hipMemcpyHostToDevice, ctx->stream);
+    return e == hipSuccess ? 0 : hip_fail(ctx, e, "hipMemcpyAsync H2D");
+}
+
+int mrml_hip_memcpy_d2d_async(mrml_hip_ctx *ctx, void *d_dst, const void *d_src, size_t bytes)
+{
+    CTX_GUARD(ctx);
+    if (!bytes) return MRML_HIP_OK;
+    REQUIRE(ctx, d_dst && d_src, "null pointer");
+    hipError_t e = hipMemcpyAsync(d_dst, d_src, bytes, hipMemcpyDeviceToDevice, ctx->stream);
+    return e == hipSuccess ? 0 : hip_fail(ctx, e, "hipMemcpyAsync D2D");
+}
+
+int mrml_hip_zero_async(mrml_hip_ctx *ctx, void *d_dst, size_t bytes)
+{
+    CTX_GUARD(ctx);
+    if (!bytes) return MRML_HIP_OK;
+    REQUIRE(ctx, d_dst, "null pointer");
+    return launch_zero(ctx, d_dst, bytes);
+}
+
+int mrml_hip_copy_kernel(mrml_hip_ctx *ctx, void *d_dst, const void *d_src, size_t bytes)
+{
+    CTX_GUARD(ctx);
+    if (!bytes) return MRML_HIP_OK;
+    REQUIRE(ctx, d_dst && d_src, "null pointer");
+    REQUIRE(ctx, bytes % 16 == 0 && ((uintptr_t)d_dst % 16) == 0 && ((uintptr_t)d_src % 16) == 0,
+            "copy_kernel: bytes and pointers must be 16-byte aligned");
+    return launch_copy(ctx, d_dst, d_src, bytes);
+}
+
+// ---- layout conversion ----------------------------------------------------
+
+int mrml_hip_repack_q4_0(mrml_hip_ctx *ctx, const void *src, void *dst, int32_t rows, int32_t cols)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, src && dst, "null pointer");
+    REQUIRE(ctx, rows > 0 && cols > 0 && cols % 32 == 0, "repack_q4_0: rows=%d cols=%d (cols %% 32 != 0?)", rows, cols);
+    REQUIRE(ctx, src != dst, "repack_q4_0: in-place conversion is not supported");
+    return launch_repack_q4_0(ctx, src, dst, rows, cols);
+}
+
+int mrml_hip_repack_q8_0(mrml_hip_ctx *ctx, const void *src, void *dst, int32_t rows, int32_t cols)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, src && dst, "null pointer");
+    REQUIRE(ctx, rows > 0 && cols > 0 && cols % 32 == 0, "repack_q8_0: rows=%d cols=%d", rows, cols);
+    REQUIRE(ctx, src != dst, "repack_q8_0: in-place conversion is not supported");
+    return launch_repack_q8_0(ctx, src, dst, rows, cols);
+}
+
+int mrml_hip_repack_q4_k(mrml_hip_ctx *ctx, const void *src, void *dst, int32_t rows, int32_t cols)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, src && dst, "null pointer");
+    REQUIRE(ctx, rows > 0 && cols > 0 && cols % 256 == 0, "repack_q4_k: rows=%d cols=%d (cols %% 256 != 0?)", rows, cols);
+    REQUIRE(ctx, src != dst, "repack_q4_k: in-place conversion is not supported");
+    return launch_repack_q4_k(ctx, src, dst, rows, cols);
+}
+
+// ---- quantiser ------------------------------------------------------------
+
+size_t mrml_hip_q8_0_pack_bytes(int32_t n) { return n > 0 ? act_pack_bytes(n / 32) : 0; }
+
+int mrml_hip_quantize_q8_0(mrml_hip_ctx *ctx, const float *x, void *gguf, void *pack, int32_t n)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, x, "x is null");
+    REQUIRE(ctx, gguf || pack, "quantize_q8_0: no output requested");
+    REQUIRE(ctx, n > 0 && n % 32 == 0, "quantize_q8_0: n=%d is not a positive multiple of 32", n);
+    return launch_quantize_q8_0(ctx, x, gguf, pack, n);
+}
+
+// Quantise x into the scratch pack; returns the pack or null (error recorded).
+static void *quantize_to_scratch(mrml_hip_ctx *ctx, const float *x, int32_t cols, size_t extra_bytes = 0)
+{
+    void *ws = workspace(ctx, act_pack_bytes(cols / 32) + extra_bytes);
+    if (!ws) return nullptr;
+    if (launch_quantize_q8_0(ctx, x, nullptr, ws, cols)) return nullptr;
+    return ws;
+}
+
+#define CHECK_MATVEC(ctx, w, x, y, rows, cols, mult)                                          \
+    do {                                                                                      \
+        REQUIRE(ctx, (w) && (x) && (y), "null pointer");                                      \
+        REQUIRE(ctx, (rows) > 0 && (cols) > 0 && (cols) % (mult) == 0,                        \
+                "rows=%d cols=%d: need rows > 0 and cols a positive multiple of %d",          \
+                (int)(rows), (int)(cols), (int)(mult));                                       \
+    } while (0)
+
+int mrml_hip_gemv_q4_0(mrml_hip_ctx *ctx, const void *w, const float *x, float *y, int32_t rows, int32_t cols)
+{
+    CTX_GUARD(ctx);
+    CHECK_MATVEC(ctx, w, x, y, rows, cols, 32);
+    void *xp = quantize_to_scratch(ctx, x, cols);
+    if (!xp) return ctx->err.empty() ? MRML_HIP_E_HIP : MRML_HIP_E_ALLOC;
+    return launch_gemv_q4_0(ctx, w, xp, y, rows, cols);
+}
+
+int mrml_hip_gemv_q4_0_q8(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows, int32_t cols)
+{
+    CTX_GUARD(ctx);
+    CHECK_MATVEC(ctx, w, xpack, y, rows, cols, 32);
+    return launch_gemv_q4_0(ctx, w, xpack, y, rows, cols);
+}
+
+int mrml_hip_gemv_q4_0_gguf(mrml_hip_ctx *ctx, const void *w, const float *x, float *y, int32_t rows, int32_t cols)
+{
+    CTX_GUARD(ctx);
+    CHECK_MATVEC(ctx, w, x, y, rows, cols, 32);
+    void *xp = quantize_to_scratch(ctx, x, cols);
+    if (!xp) return MRML_HIP_E_ALLOC;
+    return launch_gemv_q4_0_gguf(ctx, w, xp, y, rows, cols);
+}
+
+int mrml_hip_gemv_q4_0_geglu(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *x, float *act,
+                             int32_t rows, int32_t cols)
+{
+    CTX_GUARD(ctx);
+    CHECK_MATVEC(ctx, wg, x, act, rows, cols, 32);
+    REQUIRE(ctx, wu, "w_up is null");
+    void *xp = quantize_to_scratch(ctx, x, cols);
+    if (!xp) return MRML_HIP_E_ALLOC;
+    return launch_gemv_q4_0_geglu(ctx, wg, wu, xp, act, rows, cols);
+}
+
+int mrml_hip_gemv_q4_0_geglu_q8(mrml_hip_ctx *ctx, const void *wg, const void *wu, const void *xpack,
+                                float *act, int32_t rows, int32_t cols)
+{
+    CTX_GUARD(ctx);
+    CHECK_MATVEC(ctx, wg, xpack, act, rows, cols, 32);
+    REQUIRE(ctx, wu, "w_up is null");
+    return launch_gemv_q4_0_geglu(ctx, wg, wu, xpack, act, rows, cols);
+}
+
+int mrml_hip_gemv_q4_0_qkv_q8(mrml_hip_ctx *ctx, const void *wq, const void *wk, const void *wv,
+                              const void *xpack, float *y, int32_t q_rows, int32_t kv_rows, int32_t cols)
+{
+    CTX_GUARD(ctx);
+    CHECK_MATVEC(ctx, wq, xpack, y, q_rows, cols, 32);
+    REQUIRE(ctx, wk && wv, "null pointer");
+    REQUIRE(ctx, kv_rows > 0, "kv_rows=%d", kv_rows);
+    return launch_gemv_q4_0_qkv(ctx, wq, wk, wv, xpack, y, q_rows, kv_rows, cols);
+}
+
+int mrml_hip_gemv_q4_0_qkv(mrml_hip_ctx *ctx, const void *wq, const void *wk, const void *wv, const float *x,
+                           float *y, int32_t q_rows, int32_t kv_rows, int32_t cols)
+{
+    CTX_GUARD(ctx);
+    CHECK_MATVEC(ctx, wq, x, y, q_rows, cols, 32);
+    REQUIRE(ctx, wk && wv, "null pointer");
+    REQUIRE(ctx, kv_rows > 0, "kv_rows=%d", kv_rows);
+    void *xp = quantize_to_scratch(ctx, x, cols);
+    if (!xp) return MRML_HIP_E_ALLOC;
+    return launch_gemv_q4_0_qkv(ctx, wq, wk, wv, xp, y, q_rows, kv_rows, cols);
+}
+
+int mrml_hip_gemv_q8_0(mrml_hip_ctx *ctx, const void *w, const float *x, float *y, int32_t rows, int32_t cols,
+                       int32_t softcap)
+{
+    CTX_GUARD(ctx);
+    CHECK_MATVEC(ctx, w, x, y, rows, cols, 32);
+    void *xp = quantize_to_scratch(ctx, x, cols);
+    if (!xp) return MRML_HIP_E_ALLOC;
+    return launch_gemv_q8_0(ctx, w, xp, y, rows, cols, softcap);
+}
+
+int mrml_hip_gemv_q4_k(mrml_hip_ctx *ctx, const void *w, const float *x, float *y, int32_t rows, int32_t cols)
+{
+    CTX_GUARD(ctx);
+    CHECK_MATVEC(ctx, w, x, y, rows, cols, 256);
+    void *xp = quantize_to_scratch(ctx, x, cols);
+    if (!xp) return MRML_HIP_E_ALLOC;
+    return launch_gemv_q4_k(ctx, w, xp, y, rows, cols);
+}
+
+int mrml_hip_argmax_f32(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *out)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, x && out, "null pointer");
+    REQUIRE(ctx, n > 0, "argmax: n=%d", n);
+    return launch_argmax_f32(ctx, x, n, out);
+}
+
+}  // extern "C"

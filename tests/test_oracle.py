@@ -1,0 +1,487 @@
+"""Pins of the CPU oracle (oracle/mrml_oracle.c) -- CPU only.
+
+Each check is chosen so that a plausible slip in the oracle (a dropped term,
+a swapped nibble, rounding instead of truncating, an FMA, a wrong fold order)
+fails it.  Sources:
+  * the reference's own tests: crates/mrml-tensor/tests/quant_test.rs,
+    ops_test.rs, src/quant.rs:406-439 (SIMD == scalar);
+  * closed forms of examples/cuda_prefill_primitives.rs:23-49;
+  * IEEE facts checked against numpy's float16 (round-to-nearest-even);
+  * brute force: an independent numpy evaluation of the integer block sums
+    (int64 matmul over unpacked nibbles) and of the block-ordered float32 fold.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+# ---------------------------------------------------------------- helpers
+def unpack_q4_0(blocks: np.ndarray, nb: int):
+    """GGUF Q4_0 bytes -> (int8 values q-8 [.., nb, 32], f16 scales as f32 [.., nb])."""
+    b = blocks.reshape(-1, nb, 18)
+    d = b[..., 0:2].copy().view(np.float16)[..., 0].astype(np.float32)
+    qs = b[..., 2:]
+    vals = np.concatenate([(qs & 15).astype(np.int64) - 8, (qs >> 4).astype(np.int64) - 8], axis=-1)
+    return vals, d
+
+
+def unpack_q8_0(blocks: np.ndarray, nb: int):
+    b = blocks.reshape(-1, nb, 34)
+    d = b[..., 0:2].copy().view(np.float16)[..., 0].astype(np.float32)
+    q = b[..., 2:].view(np.int8).astype(np.int64)
+    return q, d
+
+
+def fold_f32(isums: np.ndarray, dw: np.ndarray, da: np.ndarray) -> np.ndarray:
+    """Block-ordered float32 fold: s = s + f32(isum_b) * (dw_b * da_b), every op rounded to f32."""
+    s = np.zeros(isums.shape[0], dtype=np.float32)
+    for b in range(isums.shape[1]):
+        scale = (dw[:, b] * da[b]).astype(np.float32)          # exact: 11-bit x 11-bit significands
+        t = (isums[:, b].astype(np.float32) * scale).astype(np.float32)
+        s = (s + t).astype(np.float32)
+    return s
+
+
+def roundf(v: np.ndarray) -> np.ndarray:
+    """C roundf (half away from zero), evaluated exactly in float64."""
+    v = v.astype(np.float64)
+    return np.sign(v) * np.floor(np.abs(v) + 0.5)
+
+
+# ---------------------------------------------------------------- f16
+def test_f16_known_answers(orc):
+    # truncation, not rounding (quant.rs:81-104): 100/127 is 0x3A4D under RNE
+    assert orc.f32_to_f16(np.float32(1) / np.float32(127)) == 0x2008
+    assert orc.f32_to_f16(np.float32(100) / np.float32(127)) == 0x3A4C
+    assert orc.f32_to_f16(np.float32(2.5) / np.float32(127)) == 0x250A
+    assert int(np.float16(np.float32(100) / np.float32(127)).view(np.uint16)) == 0x3A4D
+    assert orc.f32_to_f16(1.0) == 0x3C00
+    assert orc.f32_to_f16(1e-6) == 0x0000           # f16-subnormal range -> +0
+    assert orc.f32_to_f16(-1e-6) == 0x0000          # sign dropped too
+    assert orc.f32_to_f16(float("inf")) == 0x7C00
+    assert orc.f32_to_f16(float("-inf")) == 0xFC00
+    assert orc.f32_to_f16(1e6) == 0x7C00            # overflow -> Inf
+    assert orc.f32_to_f16(float("nan")) == 0x7E00
+    assert orc.f32_to_f16(-float("nan")) == 0xFE00
+
+
+def test_f16_to_f32_exhaustive(orc):
+    """All 65536 halves: exact conversion equals numpy's (IEEE) widening."""
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ref = h.view(np.float16).astype(np.float32)
+    got = np.array([orc.f16_to_f32(int(x)) for x in h], dtype=np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    assert np.all(np.isnan(got[nan]))
+    # NaN payload rule of quant.rs:70: mant << 13
+    assert np.float32(orc.f16_to_f32(0x7E01)).view(np.uint32) == (0xFF << 23) | (0x201 << 13)
+
+
+def test_f32_to_f16_truncation_vs_numpy(orc):
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(4000) * 10.0 ** rng.uniform(-4, 4, 4000)).astype(np.float32)
+    bits = x.view(np.uint32)
+    for xi, bi in zip(x, bits):
+        got = orc.f32_to_f16(float(xi))
+        rne = int(np.float16(xi).view(np.uint16))
+        h_abs = np.float16(xi)
+        if abs(xi) < 6.103515625e-05 or not np.isfinite(h_abs):
+            continue
+        if bi & 0x1FFF == 0:                      # exactly representable: both agree
+            assert got == rne
+        else:                                     # truncation never rounds up in magnitude
+            assert abs(np.uint16(got).view(np.float16)) <= abs(xi) <= abs(np.uint16(got + 1).view(np.float16))
+
+
+def test_f32_to_f16_rne_vs_numpy(orc):
+    rng = np.random.default_rng(2)
+    x = np.concatenate([
+        (rng.standard_normal(3000) * 10.0 ** rng.uniform(-9, 5, 3000)).astype(np.float32),
+        np.array([65504, 65519.99, 65520, 7e4, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26, 2.0 ** -26,
+                  -0.0, 0.0, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11], dtype=np.float32)])
+    got = np.array([orc.f32_to_f16_rne(float(v)) for v in x], dtype=np.uint16)
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, ref)
+
+
+# ---------------------------------------------------------------- Q8_0 quantiser
+def test_q8_0_roundtrip_quant_test(orc):
+    # quant_test.rs:3-22
+    x = ((np.arange(64, dtype=np.float32) - 32.0) * np.float32(0.1)).astype(np.float32)
+    back = orc.dequantize_q8_0(orc.quantize_q8_0(x), 64)
+    assert np.max(np.abs(back - x)) < 0.05
+
+
+def test_q8_0_all_ones_closed_form(orc):
+    q = orc.quantize_q8_0(np.ones(32, dtype=np.float32))
+    assert (int(q[0]) | (int(q[1]) << 8)) == 0x2008            # f16 trunc of 1/127
+    assert np.all(q[2:].view(np.int8) == 127)
+
+
+def test_q8_0_rounding_ties_away_from_zero(orc):
+    x = np.zeros(32, dtype=np.float32)
+    x[0] = 127.0                                   # amax 127 -> scale 1, id 1
+    x[1:7] = [2.5, -2.5, 0.5, -0.5, 1.5, -1.5]
+    q = orc.quantize_q8_0(x)[2:].view(np.int8)
+    assert list(q[:7]) == [127, 3, -3, 1, -1, 2, -2]
+
+
+def test_q8_0_zero_and_nan_blocks(orc):
+    q = orc.quantize_q8_0(np.zeros(32, dtype=np.float32))
+    assert q[0] == 0 and q[1] == 0 and np.all(q[2:] == 0)
+    x = np.ones(32, dtype=np.float32)
+    x[3] = np.nan                                  # NaN never becomes amax; its quant is 0
+    q = orc.quantize_q8_0(x)
+    assert (int(q[0]) | (int(q[1]) << 8)) == 0x2008
+    assert q[2 + 3] == 0 and np.all(np.delete(q[2:].view(np.int8), 3) == 127)
+
+
+def test_q8_0_quantiser_brute_force(orc):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(32 * 200) * 10.0 ** rng.uniform(-3, 3, 32 * 200)).astype(np.float32)
+    got = orc.quantize_q8_0(x).reshape(-1, 34)
+    xb = x.reshape(-1, 32)
+    amax = np.max(np.abs(xb), axis=1).astype(np.float32)
+    scale = (amax / np.float32(127.0)).astype(np.float32)
+    d_trunc = (scale.view(np.uint32) >> 13) - ((127 - 15) << 10)          # valid in this range
+    inv = np.where(scale != 0, (np.float32(1.0) / scale).astype(np.float32), np.float32(0))
+    prod = (xb * inv[:, None]).astype(np.float32)
+    q = np.clip(roundf(prod), -128, 127).astype(np.int8)
+    assert np.array_equal(got[:, 2:].view(np.int8), q)
+    assert np.array_equal(got[:, 0].astype(np.uint32) | (got[:, 1].astype(np.uint32) << 8),
+                          d_trunc.astype(np.uint32))
+
+
+# ---------------------------------------------------------------- Q4_0 x Q8_0
+def q4_block(d_bits: int, byte: int) -> np.ndarray:
+    b = np.full(18, byte, dtype=np.uint8)
+    b[0], b[1] = d_bits & 0xFF, d_bits >> 8
+    return b
+
+
+def test_q4_0_dequantize_0x88_is_zero(orc):
+    # quant_test.rs:24-40
+    assert np.all(orc.dequantize_q4_0(q4_block(0x3C00, 0x88), 32) == 0.0)
+
+
+def test_q4_0_dot_0x99_closed_form(orc):
+    # quant_test.rs:42-57 asserts ~32; the exact value is 4064 * (1 * f16(0x2008)) = 4064*129/16384
+    a = orc.quantize_q8_0(np.ones(32, dtype=np.float32))
+    for isa in (0, 1, 2, -1):
+        got = orc.vec_dot_q4_0_q8_0(q4_block(0x3C00, 0x99), a, 32, isa)
+        if math.isnan(got):
+            continue                                # ISA absent on this host
+        assert got == 31.998046875
+
+
+def test_q4_0_nibble_pairing_closed_forms(orc):
+    """examples/cuda_prefill_primitives.rs:23-49: 0x98 -> +x[16..32], 0x87 -> -x[0..16]."""
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal(32).astype(np.float32)
+    a = orc.quantize_q8_0(x)
+    qa = a[2:].view(np.int8).astype(np.int64)
+    da = np.uint16(int(a[0]) | (int(a[1]) << 8)).view(np.float16).astype(np.float32)
+    upper = orc.vec_dot_q4_0_q8_0(q4_block(0x3C00, 0x98), a, 32)
+    lower = orc.vec_dot_q4_0_q8_0(q4_block(0x3C00, 0x87), a, 32)
+    assert upper == np.float32(np.float32(qa[16:].sum()) * da)
+    assert lower == np.float32(np.float32(-qa[:16].sum()) * da)
+
+
+def test_q4_0_isa_variants_bit_equal(orc):
+    # quant.rs:406-432 (formula inputs of the reference test) and random rows
+    values = ((np.arange(256) * 37 % 101).astype(np.float32) - 50.0) / np.float32(13.0)
+    other = ((np.arange(256) * 19 % 89).astype(np.float32) - 44.0) / np.float32(11.0)
+    q4 = orc.quantize_q4_0(values)
+    q8 = orc.quantize_q8_0(other)
+    ref = orc.vec_dot_q4_0_q8_0(q4, q8, 256, 0)
+    for isa in (1, 2):
+        got = orc.vec_dot_q4_0_q8_0(q4, q8, 256, isa)
+        assert math.isnan(got) or got == ref
+
+
+def test_q4_0_matvec_brute_force_fold(orc, synth):
+    """Independent numpy: int64 block sums + float32 fold in block order == oracle, bit for bit."""
+    rng = synth.rng_for(99)
+    rows, cols = 97, 2304
+    nb = cols // 32
+    w = synth.q4_0_matrix(rng, rows, cols)
+    x = synth.normal_vector(rng, cols)
+    a = orc.quantize_q8_0(x)
+    y = orc.mat_vec_mul_q4_0_q8_0(w, a, rows, cols)
+    vals, dw = unpack_q4_0(w, nb)
+    qa, da = unpack_q8_0(a, nb)
+    isums = np.einsum("rbi,bi->rb", vals, qa[0])
+    for r in (0, 5, 96):
+        assert np.array_equal(orc.block_isums_q4_0_q8_0(w[r * nb * 18:(r + 1) * nb * 18], a, cols), isums[r])
+    ref = fold_f32(isums, dw[:, :] if dw.ndim == 2 else dw, da[0])
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+    # and the float64 dequantised dot agrees to rounding error
+    deq = (vals * dw[..., None]).reshape(rows, cols).astype(np.float64)
+    xq = (qa[0] * da[0][:, None]).reshape(cols).astype(np.float64)
+    exact = deq @ xq
+    assert np.max(np.abs(y - exact)) <= 1e-5 * np.max(np.abs(exact))
+
+
+def test_q4_0_fold_has_no_fma(orc):
+    """A fused multiply-add would change the low bits of some rows; the float32
+    two-rounding fold is what the oracle computes (checked above); here a case
+    where fma and mul+add differ is built explicitly."""
+    # t = isum * scale with isum*scale not representable; s + t rounding differs with fma
+    w = np.concatenate([q4_block(0x3C00, 0x99), q4_block(0x2E66, 0x9A)])  # d=1.0, d~0.1
+    x = np.concatenate([np.ones(32, np.float32), np.linspace(-1, 1, 32, dtype=np.float32)])
+    a = orc.quantize_q8_0(x)
+    got = orc.vec_dot_q4_0_q8_0(w, a, 64)
+    vals, dw = unpack_q4_0(w, 2)
+    qa, da = unpack_q8_0(a, 2)
+    isums = np.einsum("rbi,bi->rb", vals, qa[0])
+    assert np.float32(got) == fold_f32(isums, dw, da[0])[0]
+
+
+def test_matvec_entry_points_bit_equal(orc):
+    # ops_test.rs:116-140: mat_vec_mul_q4_0 == mat_vec_mul_q4_0_q8_0 bit for bit
+    rows, cols = 73, 64
+    w = np.zeros(rows * (cols // 32) * 18, dtype=np.uint8).reshape(-1, 18)
+    d = orc.f32_to_f16(0.125)
+    for bi in range(w.shape[0]):
+        w[bi, 0], w[bi, 1] = d & 0xFF, d >> 8
+        w[bi, 2:] = [(bi * 17 + i * 29) & 0xFF for i in range(16)]
+    w = w.reshape(-1)
+    x = np.sin(np.arange(cols, dtype=np.float32) * np.float32(0.31)).astype(np.float32)
+    expected = orc.mat_vec_mul_q4_0(w, x, rows, cols)
+    actual = orc.mat_vec_mul_q4_0_q8_0(w, orc.quantize_q8_0(x), rows, cols)
+    assert np.array_equal(expected.view(np.uint32), actual.view(np.uint32))
+    # row-parallel split (parallel.rs:73-116) does not change any bit
+    assert np.array_equal(orc.mat_vec_mul_q4_0_q8_0(w, orc.quantize_q8_0(x), rows, cols, threads=8), actual)
+
+
+# ---------------------------------------------------------------- Q8_0 x Q8_0
+def test_q8_0_dot_matches_dequantized_quant_test(orc):
+    # quant_test.rs:59-76
+    i = np.arange(96, dtype=np.float32)
+    x = (np.sin(i * np.float32(0.13)) * 3).astype(np.float32)
+    y = (np.cos(i * np.float32(0.07)) * 2).astype(np.float32)
+    qx, qy = orc.quantize_q8_0(x), orc.quantize_q8_0(y)
+    expected = float(np.sum(orc.dequantize_q8_0(qx, 96) * orc.dequantize_q8_0(qy, 96), dtype=np.float32))
+    for isa in (0, 1, 2):
+        got = orc.vec_dot_q8_0_q8_0(qx, qy, 96, isa)
+        assert math.isnan(got) or abs(got - expected) < 1e-3
+
+
+def test_q8_0_scalar_vnni_bit_equal_and_brute_force(orc, synth):
+    rng = synth.rng_for(98)
+    rows, cols = 33, 2048
+    nb = cols // 32
+    w = synth.q8_0_matrix(rng, rows, cols)
+    a = orc.quantize_q8_0(synth.normal_vector(rng, cols))
+    y0 = orc.mat_vec_mul_q8_0_q8_0(w, a, rows, cols, isa=0)
+    y2 = orc.mat_vec_mul_q8_0_q8_0(w, a, rows, cols, isa=2)
+    if not np.isnan(y2).any():
+        assert np.array_equal(y0.view(np.uint32), y2.view(np.uint32))
+    qw, dw = unpack_q8_0(w, nb)
+    qa, da = unpack_q8_0(a, nb)
+    isums = np.einsum("rbi,bi->rb", qw, qa[0])
+    assert np.array_equal(y0.view(np.uint32), fold_f32(isums, dw, da[0]).view(np.uint32))
+    # the AVX2-only order (quant.rs:534-561) differs only in rounding
+    y1 = orc.mat_vec_mul_q8_0_q8_0(w, a, rows, cols, isa=1)
+    if not np.isnan(y1).any():
+        assert np.max(np.abs(y1 - y0)) <= 1e-5 * np.max(np.abs(y0))
+
+
+def test_q8_0_softcap(orc):
+    # model.rs:2853: 30*tanh(y/30) after the dot (shape of ops_test.rs:188-237)
+    rows, cols = 73, 64
+    w = np.zeros((rows * 2, 34), dtype=np.uint8)
+    d = orc.f32_to_f16(0.02)
+    for bi in range(rows * 2):
+        w[bi, 0], w[bi, 1] = d & 0xFF, d >> 8
+        w[bi, 2:] = [(bi * 17 + i * 11) & 0xFF for i in range(32)]
+    w = w.reshape(-1)
+    x = np.sin(np.arange(cols, dtype=np.float32) * np.float32(0.031)).astype(np.float32)
+    a = orc.quantize_q8_0(x)
+    raw = orc.mat_vec_mul_q8_0_q8_0(w, a, rows, cols)
+    capped = orc.mat_vec_mul_q8_0_q8_0(w, a, rows, cols, softcap=True)
+    ref = (np.float32(30.0) * np.tanh(raw / np.float32(30.0))).astype(np.float32)
+    assert np.max(np.abs(capped - ref)) <= 2e-6 * 30
+    # the float64 f32-activation reference of the CUDA test is within the Q8_0 quantisation error
+    wf = orc.dequantize_q8_0(w, rows * cols).reshape(rows, cols).astype(np.float64)
+    f32ref = 30 * np.tanh((wf @ x.astype(np.float64)) / 30)
+    assert np.max(np.abs(capped - f32ref)) < 0.1
+
+
+# ---------------------------------------------------------------- ops
+def test_rms_norm_constant(orc):
+    # ops_test.rs:79-88
+    out = orc.rms_norm(np.full(4, 2.0, dtype=np.float32), None, 1e-6)
+    assert np.all(np.abs(out - 1.0) < 1e-4)
+
+
+def test_swiglu_known_value(orc):
+    # ops_test.rs:90-100: silu(2)*3
+    assert abs(orc.silu(2.0) * 3.0 - 5.28478) < 1e-3
+    assert orc.silu(0.0) == 0.0
+
+
+def test_rope_batched_equals_per_head(orc):
+    # ops_test.rs:142-158, bit equality
+    n_heads, hd = 8, 64
+    v = np.cos(np.arange(n_heads * hd, dtype=np.float32) * np.float32(0.071)).astype(np.float32)
+    per = np.concatenate([orc.rope_1d(v[h * hd:(h + 1) * hd], 137, hd) for h in range(n_heads)])
+    bat = orc.rope_1d_batched(v, 137, n_heads, hd)
+    assert np.array_equal(per.view(np.uint32), bat.view(np.uint32))
+
+
+def test_rope_closed_forms(orc):
+    v = np.random.default_rng(5).standard_normal(256).astype(np.float32)
+    assert np.array_equal(orc.rope_1d(v, 0, 256), v)          # pos 0: identity
+    r = orc.rope_1d(v, 17, 256)                                  # rotations preserve pair norms
+    pn = lambda a: np.hypot(a[:128].astype(np.float64), a[128:].astype(np.float64))
+    assert np.allclose(pn(r), pn(v), rtol=1e-6)
+    theta0 = 17.0                                                # i = 0: theta = pos
+    assert abs(r[0] - (v[0] * math.cos(theta0) - v[128] * math.sin(theta0))) < 1e-5
+
+
+def test_softmax_closed_forms(orc):
+    assert np.allclose(orc.softmax(np.full(7, 3.0, dtype=np.float32)), 1 / 7, rtol=1e-6)
+    s = orc.softmax(np.array([0.0, np.log(3.0)], dtype=np.float32))
+    assert np.allclose(s, [0.25, 0.75], rtol=1e-6)
+    assert orc.softmax(np.array([], dtype=np.float32)).size == 0
+
+
+def test_gelu_closed_forms(orc):
+    assert orc.gelu_approx(0.0) == 0.0
+    for x in (-3.0, -1.0, 0.5, 2.0):
+        k = 0.7978845608
+        ref = 0.5 * x * (1 + math.tanh(k * (x + 0.044715 * x ** 3)))
+        assert abs(orc.gelu_approx(x) - ref) <= 1e-6 * max(1.0, abs(ref))
+
+
+def test_argmax_ties_and_nan(orc):
+    assert orc.argmax_f32(np.array([1.0, 3.0, 3.0, 2.0], np.float32)) == 1
+    assert orc.argmax_f32(np.array([np.nan, 1.0, np.nan, 5.0, 5.0], np.float32)) == 3
+    assert orc.argmax_f32(np.array([np.nan, np.nan], np.float32)) == 0
+    assert orc.argmax_f32(np.array([-0.0, 0.0], np.float32)) == 0
+
+
+def test_attention_f16_against_float64(orc):
+    rng = np.random.default_rng(6)
+    n_heads, n_kv, hd, n_past = 8, 4, 64, 9
+    q = rng.standard_normal(n_heads * hd).astype(np.float32)
+    kf = rng.standard_normal((n_past + 1, n_kv, hd)).astype(np.float32)
+    vf = rng.standard_normal((n_past + 1, n_kv, hd)).astype(np.float32)
+    kc = kf.astype(np.float16).view(np.uint16)
+    vc = vf.astype(np.float16).view(np.uint16)
+    out = orc.attention_f16(q, kc, vc, n_past, n_heads, n_kv, hd, 0.125)
+    k64 = kc.view(np.float16).astype(np.float64)
+    v64 = vc.view(np.float16).astype(np.float64)
+    for h in range(n_heads):
+        g = h // (n_heads // n_kv)
+        sc = k64[:, g, :] @ q[h * hd:(h + 1) * hd].astype(np.float64) * 0.125
+        p = np.exp(sc - sc.max())
+        p /= p.sum()
+        ref = p @ v64[:, g, :]
+        assert np.allclose(out[h * hd:(h + 1) * hd], ref, rtol=1e-5, atol=1e-6)
+    # identical keys -> uniform weights -> mean of values
+    kc2 = np.repeat(kc[:1], n_past + 1, axis=0)
+    out2 = orc.attention_f16(q, kc2, vc, n_past, n_heads, n_kv, hd, 0.125)
+    assert np.allclose(out2[:hd], v64[:, 0, :].mean(axis=0), rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------- Q4_K (build-defined)
+def numpy_q4_k_dequant(blocks: np.ndarray, nsb: int) -> np.ndarray:
+    """Independent GGUF Q4_K dequantiser (from the published format)."""
+    b = blocks.reshape(nsb, 144)
+    d = b[:, 0:2].copy().view(np.float16)[:, 0].astype(np.float32)
+    dmin = b[:, 2:4].copy().view(np.float16)[:, 0].astype(np.float32)
+    s = b[:, 4:16].astype(np.int64)
+    sc = np.zeros((nsb, 8), np.int64)
+    mn = np.zeros((nsb, 8), np.int64)
+    sc[:, :4] = s[:, 0:4] & 63
+    mn[:, :4] = s[:, 4:8] & 63
+    sc[:, 4:] = (s[:, 8:12] & 15) | ((s[:, 0:4] >> 6) << 4)
+    mn[:, 4:] = (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)
+    qs = b[:, 16:].astype(np.int64).reshape(nsb, 4, 32)
+    out = np.zeros((nsb, 8, 32), np.float32)
+    for c in range(4):
+        for half, sub in ((0, 2 * c), (1, 2 * c + 1)):
+            q = (qs[:, c, :] >> (4 * half)) & 15
+            d1 = (d * sc[:, sub].astype(np.float32)).astype(np.float32)
+            m1 = (dmin * mn[:, sub].astype(np.float32)).astype(np.float32)
+            out[:, sub, :] = ((d1[:, None] * q.astype(np.float32)).astype(np.float32) - m1[:, None]).astype(np.float32)
+    return out.reshape(-1), sc, mn
+
+
+def test_q4_k_scale_packing_roundtrip(orc, synth):
+    rng = np.random.default_rng(7)
+    sc = rng.integers(0, 64, (50, 8), dtype=np.uint8)
+    mn = rng.integers(0, 64, (50, 8), dtype=np.uint8)
+    packed = synth.pack_q4_k_scales(sc, mn)
+    for i in range(50):
+        for j in range(8):
+            assert orc.q4_k_scale_min(packed[i], j) == (sc[i, j], mn[i, j])
+
+
+def test_q4_k_dequant_brute_force(orc, synth):
+    rng = synth.rng_for(97)
+    w = synth.q4_k_matrix(rng, 3, 512)
+    got = orc.dequantize_q4_k(w, 3 * 512)
+    ref, _, _ = numpy_q4_k_dequant(w, 6)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_q4_k_dot_brute_force(orc, synth):
+    rng = synth.rng_for(96)
+    rows, cols = 19, 2304
+    nsb = cols // 256
+    w = synth.q4_k_matrix(rng, rows, cols)
+    a = orc.quantize_q8_0(synth.normal_vector(rng, cols))
+    y = orc.mat_vec_mul_q4_k_q8_0(w, a, rows, cols)
+    _, sc, mn = numpy_q4_k_dequant(w, rows * nsb)
+    b = w.reshape(rows, nsb, 144)
+    d = b[:, :, 0:2].copy().view(np.float16)[..., 0].astype(np.float32)
+    dmin = b[:, :, 2:4].copy().view(np.float16)[..., 0].astype(np.float32)
+    qs = b[:, :, 16:].astype(np.int64).reshape(rows, nsb, 4, 32)
+    qa, da = unpack_q8_0(a, cols // 32)
+    qa, da = qa[0].reshape(nsb, 8, 32), da[0].reshape(nsb, 8)
+    sc = sc.reshape(rows, nsb, 8)
+    mn = mn.reshape(rows, nsb, 8)
+    s = np.zeros(rows, np.float32)
+    for k in range(nsb):
+        for j in range(8):
+            q = (qs[:, k, j // 2, :] >> (4 * (j % 2))) & 15
+            isum = (q * qa[k, j][None, :]).sum(axis=1)
+            bsum = qa[k, j].sum()
+            ds = ((d[:, k] * sc[:, k, j].astype(np.float32)).astype(np.float32) * da[k, j]).astype(np.float32)
+            dm = ((dmin[:, k] * mn[:, k, j].astype(np.float32)).astype(np.float32) * da[k, j]).astype(np.float32)
+            t = ((isum.astype(np.float32) * ds).astype(np.float32)
+                 - (np.float32(bsum) * dm).astype(np.float32)).astype(np.float32)
+            s = (s + t).astype(np.float32)
+    assert np.array_equal(y.view(np.uint32), s.view(np.uint32))
+    # float64 dequantised dot agrees to rounding error
+    deq, _, _ = numpy_q4_k_dequant(w, rows * nsb)
+    xq = (qa * da[..., None]).reshape(-1).astype(np.float64)
+    exact = deq.reshape(rows, cols).astype(np.float64) @ xq
+    assert np.max(np.abs(y - exact)) <= 1e-4 * np.max(np.abs(exact))
+
+
+# ---------------------------------------------------------------- committed fixtures
+def test_golden_fixture_kats(orc):
+    """tests/golden/kats.json: the reference tests' known answers, as data."""
+    kats = json.loads((GOLDEN / "kats.json").read_text())
+    for case in kats["f32_to_f16_trunc"]:
+        assert orc.f32_to_f16(np.float32(case["x"])) == case["h"], case
+    for case in kats["q4_0_dot"]:
+        w = np.array(case["w"], dtype=np.uint8)
+        a = orc.quantize_q8_0(np.array(case["x"], dtype=np.float32))
+        assert orc.vec_dot_q4_0_q8_0(w, a, len(case["x"])) == np.float32(case["y"]), case["name"]
+    for case in kats["q8_0_quantize"]:
+        q = orc.quantize_q8_0(np.array(case["x"], dtype=np.float32))
+        assert list(q) == case["bytes"], case["name"]
