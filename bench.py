@@ -166,9 +166,10 @@ def main() -> int:
     dev.reserve_workspace(1 << 20)
     dev.sync()
 
+    # one FFN step = mrml_hip_ffn_geglu_q4_0: two launches (GeGLU quantising x
+    # itself and emitting the activation pack, then the down projection)
     def ffn_step(s):
-        dev.gemv_q4_0_geglu(s["g"], s["u"], bx, act, FFN, DIM)
-        dev.gemv_q4_0(s["d"], act, y, DIM, FFN)
+        dev.ffn_geglu_q4_0(s["g"], s["u"], s["d"], bx, None, y, DIM, FFN)
 
     # one graph = one step over every rotating set
     for s in rot:
@@ -177,7 +178,8 @@ def main() -> int:
     g_step = dev.capture(lambda: [ffn_step(s) for s in rot])
     q_pack = be.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(DIM), np.uint8)
     dev.quantize_q8_0(bx, None, q_pack, DIM)
-    g_geglu = dev.capture(lambda: [dev.gemv_q4_0_geglu_q8(s["g"], s["u"], q_pack, act, FFN, DIM) for s in rot])
+    a_pack = be.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(FFN), np.uint8)
+    g_geglu = dev.capture(lambda: [dev.gemv_q4_0_geglu_pack(s["g"], s["u"], bx, None, a_pack, FFN, DIM) for s in rot])
 
     if args.profile_loop:
         for _ in range(args.profile_loop):
@@ -205,12 +207,12 @@ def main() -> int:
         return secs, nbytes / secs / 1e9
 
     out_f = be.HipBuffer.alloc(dev, FFN)
-    k_geglu, gbs_geglu = rate(lambda s: dev.gemv_q4_0_geglu_q8(s["g"], s["u"], q_pack, act, FFN, DIM),
+    # the step's first launch (f32 x in, activation pack out)
+    k_geglu, gbs_geglu = rate(lambda s: dev.gemv_q4_0_geglu_pack(s["g"], s["u"], bx, None, a_pack, FFN, DIM),
                               BYTES_GEGLU, sets)
     k_gate, gbs_gate = rate(lambda s: dev.gemv_q4_0_q8(s["g"], q_pack, out_f, FFN, DIM), BYTES_GATE, sets)
     k_up, gbs_up = rate(lambda s: dev.gemv_q4_0_q8(s["u"], q_pack, out_f, FFN, DIM), BYTES_GATE, sets)
-    a_pack = be.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(FFN), np.uint8)
-    dev.quantize_q8_0(act, None, a_pack, FFN)
+    # the step's second launch (activation pack in)
     k_down, gbs_down = rate(lambda s: dev.gemv_q4_0_q8(s["d"], a_pack, y, DIM, FFN), BYTES_DOWN, sets)
     # stream-copy ceiling on a buffer well above the MALL
     cbytes = 1 << 30

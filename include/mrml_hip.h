@@ -23,6 +23,10 @@
  *  - Dimensions are int32 like the reference's launch arguments; `cols` must be
  *    a multiple of 32 (256 for Q4_K), as the reference's kernel schemas require
  *    (crates/mrml-kernel/src/virtual_gpu.rs:2897-3125).
+ *  - Activation vectors (f32 x) and Q8_0 activation packs are read in 16-byte
+ *    units and must be 16-byte aligned (hipMalloc returns 256-byte aligned
+ *    memory; whole-block offsets keep the alignment); misaligned pointers are
+ *    rejected with MRML_HIP_E_INVALID.
  *  - Weight layouts: the *_gguf entry points read the raw GGUF bytes the
  *    reference uploads unchanged (model.rs:651-705).  The other weight
  *    arguments take the backend layout written by mrml_hip_repack_* (the same
@@ -152,6 +156,20 @@ int mrml_hip_gemv_q4_0_gguf(mrml_hip_ctx *ctx, const void *d_w_gguf, const float
  * products over one Q8_0(x).  rows = ffn width, cols = model width. */
 int mrml_hip_gemv_q4_0_geglu(mrml_hip_ctx *ctx, const void *d_w_gate, const void *d_w_up,
                              const float *d_x, float *d_act, int32_t rows, int32_t cols);
+/* One Gemma-style FFN, y = W_down * Q8_0(GeGLU(W_gate x, W_up x)) (model.rs:
+ * 2093-2108 with a dense GeGLU FFN): two launches, the first quantising x
+ * itself and writing the Q8_0 pack of the activation for the second.  d_act
+ * (nullable) also receives the f32 activation.  dim = model width (cols of
+ * gate/up, rows of down), ffn = hidden width. */
+int mrml_hip_ffn_geglu_q4_0(mrml_hip_ctx *ctx, const void *d_w_gate, const void *d_w_up,
+                            const void *d_w_down, const float *d_x, float *d_act, float *d_y,
+                            int32_t dim, int32_t ffn);
+/* The first launch of mrml_hip_ffn_geglu_q4_0 on its own: act = GeGLU of the
+ * two products over Q8_0(x), written as f32 (d_act, nullable) and as the
+ * activation pack of its rows values (d_act_pack, rows/32*40 bytes). */
+int mrml_hip_gemv_q4_0_geglu_pack(mrml_hip_ctx *ctx, const void *d_w_gate, const void *d_w_up,
+                                  const float *d_x, float *d_act, void *d_act_pack,
+                                  int32_t rows, int32_t cols);
 /* As mrml_hip_gemv_q4_0_geglu with x already quantised (activation pack):
  * the shared Q8_0 input of model.rs:2096-2103. */
 int mrml_hip_gemv_q4_0_geglu_q8(mrml_hip_ctx *ctx, const void *d_w_gate, const void *d_w_up,

@@ -109,6 +109,8 @@ _SIGNATURES = {
     "mrml_hip_gemv_q4_0_geglu": [_P, _P, _P, _P, _P, _I, _I],
     "mrml_hip_gemv_q4_0_qkv": [_P, _P, _P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemv_q4_0_geglu_q8": [_P, _P, _P, _P, _P, _I, _I],
+    "mrml_hip_ffn_geglu_q4_0": [_P, _P, _P, _P, _P, _P, _P, _I, _I],
+    "mrml_hip_gemv_q4_0_geglu_pack": [_P, _P, _P, _P, _P, _P, _I, _I],
     "mrml_hip_gemv_q4_0_qkv_q8": [_P, _P, _P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemv_q8_0": [_P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemv_q4_k": [_P, _P, _P, _P, _I, _I],
@@ -338,6 +340,14 @@ class HipDevice:
     def gemv_q4_0_geglu_q8(self, w_gate, w_up, xpack, act, rows: int, cols: int) -> None:
         self._check(self.lib.mrml_hip_gemv_q4_0_geglu_q8(self.ctx, _ptr(w_gate), _ptr(w_up), _ptr(xpack),
                                                          _ptr(act), rows, cols))
+
+    def gemv_q4_0_geglu_pack(self, w_gate, w_up, x, act, act_pack, rows: int, cols: int) -> None:
+        self._check(self.lib.mrml_hip_gemv_q4_0_geglu_pack(self.ctx, _ptr(w_gate), _ptr(w_up), _ptr(x), _ptr(act),
+                                                           _ptr(act_pack), rows, cols))
+
+    def ffn_geglu_q4_0(self, w_gate, w_up, w_down, x, act, y, dim: int, ffn: int) -> None:
+        self._check(self.lib.mrml_hip_ffn_geglu_q4_0(self.ctx, _ptr(w_gate), _ptr(w_up), _ptr(w_down), _ptr(x),
+                                                     _ptr(act), _ptr(y), dim, ffn))
 
     def gemv_q4_0_qkv_q8(self, wq, wk, wv, xpack, y, q_rows: int, kv_rows: int, cols: int) -> None:
         self._check(self.lib.mrml_hip_gemv_q4_0_qkv_q8(self.ctx, _ptr(wq), _ptr(wk), _ptr(wv), _ptr(xpack),

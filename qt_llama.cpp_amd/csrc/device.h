@@ -65,12 +65,125 @@ __device__ __forceinline__ float dpp_ror1(float v)
         float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xf, 0xf, false));
 }
 
+// Value of lane (i-1) mod 64 across the whole wave (wave_ror:1).
+__device__ __forceinline__ float dpp_wave_ror1(float v)
+{
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x13C, 0xf, 0xf, false));
+}
+
 // Ordered fold step across the 16 lanes of a DPP row: lane j receives the
 // running sum of lane j-1 and adds its own term.  Applied once per
 // "iteration" of 16 consecutive blocks, lane 15 ends up holding
 // ((...((s + t_0) + t_1) ...) + t_15), the block-order sequential sum of the
 // reference (quant.rs:339-366), with every addition rounded separately.
 __device__ __forceinline__ float fold16(float s, float t) { return dpp_ror1(s) + t; }
+
+// Reductions over each 32-lane half of the wave, result in every lane of the
+// half.  Within a 16-lane DPP row: quad_perm swaps (xor 1, xor 2) and
+// row_ror by 4 and 8; the two rows of a half are then combined with one
+// ds_swizzle (xor 16).  DPP moves stay in the VALU; only the last step uses
+// the LDS crossbar.
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int v)
+{
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ int swizzle_xor16(int v) { return __builtin_amdgcn_ds_swizzle(v, 0x401F); }
+
+__device__ __forceinline__ float max32(float m)
+{
+    auto step = [](float a, float b) { return (b > a) ? b : a; };
+    m = step(m, __builtin_bit_cast(float, dpp_mov<0xB1>(__builtin_bit_cast(int, m))));   // quad_perm 1,0,3,2
+    m = step(m, __builtin_bit_cast(float, dpp_mov<0x4E>(__builtin_bit_cast(int, m))));   // quad_perm 2,3,0,1
+    m = step(m, __builtin_bit_cast(float, dpp_mov<0x124>(__builtin_bit_cast(int, m))));  // row_ror:4
+    m = step(m, __builtin_bit_cast(float, dpp_mov<0x128>(__builtin_bit_cast(int, m))));  // row_ror:8
+    return step(m, __builtin_bit_cast(float, swizzle_xor16(__builtin_bit_cast(int, m))));
+}
+
+__device__ __forceinline__ int sum32(int s)
+{
+    s += dpp_mov<0xB1>(s);
+    s += dpp_mov<0x4E>(s);
+    s += dpp_mov<0x124>(s);
+    s += dpp_mov<0x128>(s);
+    return s + swizzle_xor16(s);
+}
+
+// One Q8_0 block (quant.rs:193-228) held by 32 consecutive lanes, lane l
+// owning value l:
+//   amax  = max |x| (starts at 0, NaN never wins -- exact in any order)
+//   scale = amax / 127          (IEEE division)
+//   d     = f32_to_f16 by truncation;  id = scale != 0 ? 1/scale : 0
+//   q     = (int8) clamp(roundf(x*id), -128, 127), NaN -> 0
+// Returns q; dbits is the f16 scale, qsum the block's quant sum (both
+// uniform across the 32 lanes).  Must be called by all 64 lanes of the wave.
+__device__ __forceinline__ int q8_0_block32(float v, uint32_t &dbits, int &qsum)
+{
+    float m = fabsf(v);
+    m = (m > 0.0f) ? m : 0.0f;  // NaN -> 0
+    m = max32(m);               // max is exact in any order
+    const float scale = m / 127.0f;
+    dbits = f32_to_f16_trunc(scale);
+    const float id = (scale != 0.0f) ? 1.0f / scale : 0.0f;
+    float r = roundf(v * id);
+    r = (r < -128.0f) ? -128.0f : r;
+    r = (r > 127.0f) ? 127.0f : r;
+    const int q = (r != r) ? 0 : (int)r;
+    qsum = sum32(q);
+    return q;
+}
+
+// Reductions over each aligned group of 8 lanes (quad_perm xor 1, xor 2, then
+// row_half_mirror, which maps each quad onto the other quad of its 8 lanes;
+// after the quad steps every lane of a quad holds the same value).
+__device__ __forceinline__ float max8(float m)
+{
+    auto step = [](float a, float b) { return (b > a) ? b : a; };
+    m = step(m, __builtin_bit_cast(float, dpp_mov<0xB1>(__builtin_bit_cast(int, m))));
+    m = step(m, __builtin_bit_cast(float, dpp_mov<0x4E>(__builtin_bit_cast(int, m))));
+    return step(m, __builtin_bit_cast(float, dpp_mov<0x141>(__builtin_bit_cast(int, m))));
+}
+
+__device__ __forceinline__ int sum8(int s)
+{
+    s += dpp_mov<0xB1>(s);
+    s += dpp_mov<0x4E>(s);
+    return s + dpp_mov<0x141>(s);
+}
+
+__device__ __forceinline__ int q8_0_value(float v, float id)
+{
+    float r = roundf(v * id);
+    r = (r < -128.0f) ? -128.0f : r;
+    r = (r > 127.0f) ? 127.0f : r;
+    return (r != r) ? 0 : (int)r;
+}
+
+// The same Q8_0 block rule with the block held by 8 consecutive lanes, lane l
+// owning values 4l..4l+3 (one float4).  Returns the lane's 4 quants packed
+// little-endian in a dword; dbits and qsum are uniform across the 8 lanes.
+// Must be called by all 64 lanes of the wave.
+__device__ __forceinline__ uint32_t q8_0_block8x4(float4 v, uint32_t &dbits, int &qsum)
+{
+    auto amag = [](float x) {
+        const float a = fabsf(x);
+        return (a > 0.0f) ? a : 0.0f;  // NaN -> 0
+    };
+    float m = amag(v.x);
+    m = fmaxf(m, amag(v.y));
+    m = fmaxf(m, amag(v.z));
+    m = fmaxf(m, amag(v.w));
+    m = max8(m);
+    const float scale = m / 127.0f;
+    dbits = f32_to_f16_trunc(scale);
+    const float id = (scale != 0.0f) ? 1.0f / scale : 0.0f;
+    const int q0 = q8_0_value(v.x, id), q1 = q8_0_value(v.y, id);
+    const int q2 = q8_0_value(v.z, id), q3 = q8_0_value(v.w, id);
+    qsum = sum8(q0 + q1 + q2 + q3);
+    return (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+           ((uint32_t)q3 << 24);
+}
 
 // ops.rs:101-104 evaluated in the same order (contraction is off):
 // (0.5*x) * (1 + tanh(k*(x + ((0.044715*x)*x)*x))).

@@ -6,18 +6,30 @@
 // in block order, each product and each sum rounded separately (this file is
 // compiled with -ffp-contract=off), so y is bit-identical to the CPU path.
 //
-// Mapping: one 64-lane wave owns 4 rows; the 16 lanes of a DPP row own one
-// matrix row and take 16 consecutive blocks per iteration (lane j -> block
-// 16*it + j).  In the backend layout a lane's block is one 16-byte load and
-// the 16 lanes of a row read 256 contiguous bytes, so every load instruction
-// is 4 fully used 256-byte segments.  All of a lane's weight loads are issued
-// before any is consumed; they return in order, so the in-order fold starts
-// on the first bytes to arrive.
-//   isum: 8 v_dot4_i32_i8 on (nibbles, int8 activations) minus 8*sum(a).
-//   fold: 16 row_ror:1 DPP adds per iteration; after step k lane k holds the
-//         running sum through block 16*it+k, lane 15 ends with the row result.
-// The activation pack (int8 quants, f32 scales, int32 sums) is staged once per
-// workgroup in LDS.
+// Three kernel shapes, chosen by measurement on MI355X:
+//
+//  * 16 lanes per row ("fold16"), for rows of <= ~128 blocks (cols 2048,
+//    2304): one 64-lane wave owns 4 rows; lane j takes blocks 16*it + j, one
+//    16-byte load each, so the 16 lanes of a row read 256 contiguous bytes.
+//    The ordered fold is a chain of 16 row_ror:1 DPP adds per iteration;
+//    after step k lane k holds the running sum through block 16*it + k and
+//    lane 15 ends with the row.  A staging wave copies the activation pack
+//    (or quantises f32 x itself) into LDS while the compute waves' weight
+//    loads are in flight.
+//
+//  * Relay ("relay"), for long rows (cols 9216): a workgroup of S waves owns 4
+//    rows and splits the row's iterations between them, so each wave issues
+//    and computes only 1/S of the row (per-wave work, not bandwidth, bounds
+//    the plain layout on long rows).  Each lane loads its own activation
+//    blocks straight from the pack.  The block terms go to LDS and the
+//    running sums are relayed wave to wave in iteration order (S-1
+//    barriers); the fold itself is plain adds in the 4 fold lanes.
+//
+//  * Runtime block count ("any"): the fold16 structure with nb a kernel
+//    argument, for every other shape.
+//
+// The GeGLU kernel can also quantise x itself and emit the Q8_0 pack of its
+// output for the next (down) projection, so an FFN is two launches.
 
 #include "device.h"
 #include "internal.h"
@@ -28,23 +40,10 @@ namespace {
 
 constexpr uint32_t kNib = 0x0F0F0F0Fu;
 
-// Activation pack staging.  Wave 0 of every workgroup only copies the pack
-// (nb*40 bytes, 16-byte aligned) into LDS; the compute waves issue nothing
-// but their own weight loads, so each of their in-order waits covers exactly
-// the weight bytes it consumes and the fold starts on the first to arrive.
-__device__ __forceinline__ void stage_pack_wave(const uint8_t *src, uint8_t *lds, int nb)
-{
-    const int n16 = (nb * 40 + 15) >> 4;
-    const uint4 *s = reinterpret_cast<const uint4 *>(src);
-    uint4 *d = reinterpret_cast<uint4 *>(lds);
-    for (int i = threadIdx.x; i < n16; i += 64) d[i] = s[i];
-}
-
 // Exact integer block dot of one Q4_0 block (16 packed bytes) with the
-// matching Q8_0 activation block (32 int8 in LDS) and its quant sum.
-__device__ __forceinline__ int32_t q4_0_isum(uint4 w, const int4 *aq, int32_t asum)
+// matching Q8_0 activation quants (a0 = a[0..15], a1 = a[16..31]) and their sum.
+__device__ __forceinline__ int32_t q4_0_isum(uint4 w, int4 a0, int4 a1, int32_t asum)
 {
-    const int4 a0 = aq[0], a1 = aq[1];
     int32_t s = sdot4(w.x & kNib, (uint32_t)a0.x, 0);
     s = sdot4(w.y & kNib, (uint32_t)a0.y, s);
     s = sdot4(w.z & kNib, (uint32_t)a0.z, s);
@@ -56,23 +55,85 @@ __device__ __forceinline__ int32_t q4_0_isum(uint4 w, const int4 *aq, int32_t as
     return s - 8 * asum;  // nibble offset: sum (q-8)*a = sum q*a - 8*sum a
 }
 
-// Per-lane register block of one matrix row: ITERS blocks of 16-byte quants
-// and, per block, the 32-bit word of the scale plane holding its f16 scale
-// (two neighbouring blocks share a word; a 4-byte load keeps each scale in
-// its own register so no load is consumed before the fold needs it).
-// Blocks past the row end load a clamped in-bounds address and are masked
-// out of the fold.
+// Copy an activation pack (nb*40 bytes, 16-byte aligned) into LDS with one
+// wave.  Every 16-byte load of a batch is issued before the first LDS store,
+// so the copy costs one L2 round trip per batch of 16 loads per lane.
+__device__ __forceinline__ void stage_pack_wave(const uint8_t *src, uint8_t *lds, int nb)
+{
+    constexpr int kBatch = 16;
+    const int n16 = (nb * 40 + 15) >> 4;
+    const uint4 *s = reinterpret_cast<const uint4 *>(src);
+    uint4 *d = reinterpret_cast<uint4 *>(lds);
+    const int lane = threadIdx.x & 63;
+    for (int i0 = 0; i0 < n16; i0 += 64 * kBatch) {
+        uint4 v[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int i = i0 + k * 64 + lane;
+            v[k] = s[i < n16 ? i : n16 - 1];
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int i = i0 + k * 64 + lane;
+            if (i < n16) d[i] = v[k];
+        }
+    }
+}
+
+// Quantise f32 x (NB blocks) into an activation pack in LDS with NQ waves
+// (this is wave qw): eight blocks per wave step, 8 lanes of 4 values each per
+// block; all of a wave's loads are issued before the first block is quantised.
+template <int NB, int NQ>
+__device__ __forceinline__ void quantize_into_lds(const float *__restrict__ x, uint8_t *pack, int qw)
+{
+    constexpr int K = (NB + 8 * NQ - 1) / (8 * NQ);
+    const int lane = threadIdx.x & 63, g = lane >> 3, l = lane & 7;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    float4 v[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        int b = 8 * (qw + NQ * k) + g;
+        b = b < NB ? b : NB - 1;
+        v[k] = x4[b * 8 + l];
+    }
+    uint32_t *pq = reinterpret_cast<uint32_t *>(pack);
+    float *pd = reinterpret_cast<float *>(pack + NB * 32);
+    int32_t *ps = reinterpret_cast<int32_t *>(pack + NB * 36);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int b = 8 * (qw + NQ * k) + g;
+        uint32_t dbits;
+        int s;
+        const uint32_t q = q8_0_block8x4(v[k], dbits, s);
+        if (b < NB) {
+            pq[b * 8 + l] = q;
+            if (l == 0) {
+                pd[b] = f16_bits_to_f32(dbits);
+                ps[b] = s;
+            }
+        }
+    }
+}
+
+// ---- 16 lanes per row: registers, loads and the DPP fold --------------------
+
+// Per-lane registers of one row: ITERS 16-byte quant blocks and, per block,
+// the 32-bit word of the scale plane that holds its f16 scale (a 4-byte load
+// keeps each scale in its own register, so no load is consumed early).
 template <int ITERS>
 struct RowRegs {
     uint4 w[ITERS];
     uint32_t d[ITERS];
 };
 
+// Issue every load of one row (lane j, blocks 16*it + j); blocks past the row
+// end load a clamped in-bounds block and are masked out of the fold.
 template <int ITERS>
-__device__ __forceinline__ void load_row(RowRegs<ITERS> &r, const uint4 *__restrict__ qs,
-                                         const uint16_t *__restrict__ dp, size_t base, int nb, int j)
+__device__ __forceinline__ void load_row(RowRegs<ITERS> &r, const uint8_t *__restrict__ w, size_t nblk,
+                                         size_t base, int nb, int j)
 {
-    const uint32_t *dw = reinterpret_cast<const uint32_t *>(dp);
+    const uint4 *qs = reinterpret_cast<const uint4 *>(w);
+    const uint32_t *dw = reinterpret_cast<const uint32_t *>(w + nblk * 16);
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
         int b = it * 16 + j;
@@ -82,141 +143,375 @@ __device__ __forceinline__ void load_row(RowRegs<ITERS> &r, const uint4 *__restr
     }
 }
 
-__device__ __forceinline__ uint32_t scale_bits(uint32_t word, size_t blk) { return (blk & 1) ? word >> 16 : word & 0xffffu; }
-
-// Ordered fold of one row held as RowRegs; result valid in lane 15 of the
-// DPP row.  Masked tail blocks contribute +0, which leaves a running sum
-// unchanged (the running sum is never -0: it starts at +0 and
-// round-to-nearest never produces -0 from a sum with a +0 operand).
+// Block term of iteration `it` (masked to +0 past the row end).  Computed
+// unconditionally, so the compiler has no conditional block to sink the
+// weight load into (which would delay its issue).
 template <int ITERS>
-__device__ __forceinline__ float fold_row(const RowRegs<ITERS> &r, const uint8_t *lds, size_t base, int nb, int j)
+__device__ __forceinline__ float row_term(const RowRegs<ITERS> &r, int it, const uint8_t *pack, size_t base, int nb,
+                                          int j)
 {
-    const int4 *aq = reinterpret_cast<const int4 *>(lds);
-    const float *ad = reinterpret_cast<const float *>(lds + nb * 32);
-    const int32_t *as = reinterpret_cast<const int32_t *>(lds + nb * 36);
+    const int b = it * 16 + j;
+    const int bc = b < nb ? b : nb - 1;
+    const int4 *aq = reinterpret_cast<const int4 *>(pack);
+    const float *ad = reinterpret_cast<const float *>(pack + nb * 32);
+    const int32_t *as = reinterpret_cast<const int32_t *>(pack + nb * 36);
+    const int32_t isum = q4_0_isum(r.w[it], aq[2 * bc], aq[2 * bc + 1], as[bc]);
+    const uint32_t word = r.d[it];
+    const uint32_t dbits = ((base + bc) & 1) ? word >> 16 : word & 0xffffu;
+    const float t = (float)isum * (f16_bits_to_f32(dbits) * ad[bc]);
+    return b < nb ? t : 0.0f;
+}
+
+// Ordered fold; the row result is valid in lane 15 of the DPP row.  Masked
+// tail terms are +0, which leaves a running sum unchanged (the sum starts at
+// +0 and round-to-nearest never turns it into -0).
+template <int ITERS>
+__device__ __forceinline__ float fold_row(const RowRegs<ITERS> &r, const uint8_t *pack, size_t base, int nb, int j)
+{
     float s = 0.0f;
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
-        // Computed unconditionally (tail lanes hold a clamped, valid block) so
-        // the compiler has no conditional block to sink the weight load into.
-        const int b = it * 16 + j;
-        const int bc = b < nb ? b : nb - 1;
-        const int32_t isum = q4_0_isum(r.w[it], aq + 2 * bc, as[bc]);
-        const float tv = (float)isum * (f16_bits_to_f32(scale_bits(r.d[it], base + bc)) * ad[bc]);
-        const float t = b < nb ? tv : 0.0f;
+        const float t = row_term<ITERS>(r, it, pack, base, nb, j);
 #pragma unroll
         for (int k = 0; k < 16; ++k) s = fold16(s, t);
     }
     return s;
 }
 
-// ---- plain matvec ----------------------------------------------------------
+// Two rows (gate and up) with interleaved chains.
+template <int ITERS>
+__device__ __forceinline__ void fold_row2(const RowRegs<ITERS> &ra, const RowRegs<ITERS> &rb, const uint8_t *pack,
+                                          size_t base, int nb, int j, float &sa, float &sb)
+{
+    sa = 0.0f;
+    sb = 0.0f;
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+        const float ta = row_term<ITERS>(ra, it, pack, base, nb, j);
+        const float tb = row_term<ITERS>(rb, it, pack, base, nb, j);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            sa = fold16(sa, ta);
+            sb = fold16(sb, tb);
+        }
+    }
+}
+
+// Row of matrix set {wq | wk | wv} for a stacked output row.
+struct QkvSel {
+    const uint8_t *w;
+    int local, mrows;
+};
+__device__ __forceinline__ QkvSel qkv_select(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, int row,
+                                             int q_rows, int kv_rows)
+{
+    if (row < q_rows) return {wq, row, q_rows};
+    if (row < q_rows + kv_rows) return {wk, row - q_rows, kv_rows};
+    return {wv, row - q_rows - kv_rows, kv_rows};
+}
+
+// ---- fold16 kernels, block count NB fixed at compile time --------------------
+// NQ leading waves prepare the activation pack in LDS: QX = false copies a
+// pack, QX = true quantises f32 x; the WAVES compute waves own 4 rows each.
+
+constexpr int kNQ = 4;  // staging waves when quantising x in the kernel
+
+template <int NB, bool QX>
+__device__ __forceinline__ void prepare_pack(const void *xin, uint8_t *lds, int wave)
+{
+    if constexpr (QX) quantize_into_lds<NB, kNQ>(reinterpret_cast<const float *>(xin), lds, wave);
+    else if (wave == 0) stage_pack_wave(reinterpret_cast<const uint8_t *>(xin), lds, NB);
+}
+
+template <bool QX>
+constexpr int stage_waves() { return QX ? kNQ : 1; }
+
+template <int NB, int WAVES, bool QX>
+__global__ __launch_bounds__(64 * (WAVES + (QX ? kNQ : 1))) void gemv_q4_0_kernel(
+    const uint8_t *__restrict__ w, const void *xin, float *__restrict__ y, int rows)
+{
+    constexpr int NS = stage_waves<QX>(), ITERS = (NB + 15) / 16;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int wave = threadIdx.x >> 6;
+    if (wave < NS) {
+        prepare_pack<NB, QX>(xin, lds, wave);
+        __syncthreads();
+        return;
+    }
+    const int lane = threadIdx.x & 63, j = lane & 15;
+    const int row_raw = (blockIdx.x * WAVES + wave - NS) * 4 + (lane >> 4);
+    const int row = row_raw < rows ? row_raw : rows - 1;  // tail rows recompute the last row
+    const size_t base = (size_t)row * NB;
+    RowRegs<ITERS> r;
+    load_row<ITERS>(r, w, (size_t)rows * NB, base, NB, j);
+    __syncthreads();
+    const float s = fold_row<ITERS>(r, lds, base, NB, j);
+    if (j == 15 && row_raw < rows) y[row_raw] = s;
+}
+
+template <int NB, int WAVES, bool QX>
+__global__ __launch_bounds__(64 * (WAVES + (QX ? kNQ : 1))) void gemv_q4_0_qkv_kernel(
+    const uint8_t *__restrict__ wq, const uint8_t *__restrict__ wk, const uint8_t *__restrict__ wv, const void *xin,
+    float *__restrict__ y, int q_rows, int kv_rows)
+{
+    constexpr int NS = stage_waves<QX>(), ITERS = (NB + 15) / 16;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int wave = threadIdx.x >> 6;
+    if (wave < NS) {
+        prepare_pack<NB, QX>(xin, lds, wave);
+        __syncthreads();
+        return;
+    }
+    const int total = q_rows + 2 * kv_rows;
+    const int lane = threadIdx.x & 63, j = lane & 15;
+    const int row_raw = (blockIdx.x * WAVES + wave - NS) * 4 + (lane >> 4);
+    const QkvSel m = qkv_select(wq, wk, wv, row_raw < total ? row_raw : total - 1, q_rows, kv_rows);
+    const size_t base = (size_t)m.local * NB;
+    RowRegs<ITERS> r;
+    load_row<ITERS>(r, m.w, (size_t)m.mrows * NB, base, NB, j);
+    __syncthreads();
+    const float s = fold_row<ITERS>(r, lds, base, NB, j);
+    if (j == 15 && row_raw < total) y[row_raw] = s;
+}
+
+// Gate+up with the GeGLU epilogue (model.rs:2093-2105, ops.rs:99-114).  With
+// EMIT, a workgroup owns 32 rows (WAVES = 8) and also writes the Q8_0 pack of
+// its 32 outputs (one activation block) for the next projection; act may
+// then be null.
+template <int NB, int WAVES, bool QX, bool EMIT>
+__global__ __launch_bounds__(64 * (WAVES + (QX ? kNQ : 1))) void gemv_q4_0_geglu_kernel(
+    const uint8_t *__restrict__ wg, const uint8_t *__restrict__ wu, const void *xin, float *__restrict__ act,
+    uint8_t *__restrict__ act_pack, int rows)
+{
+    static_assert(!EMIT || WAVES == 8, "the output pack block needs 32 rows per workgroup");
+    constexpr int NS = stage_waves<QX>(), ITERS = (NB + 15) / 16;
+    extern __shared__ __align__(16) uint8_t lds[];
+    float *act_lds = reinterpret_cast<float *>(lds + (NB * 40 + 15) / 16 * 16);
+    const int wave = threadIdx.x >> 6;
+    if (wave < NS) {
+        prepare_pack<NB, QX>(xin, lds, wave);
+        __syncthreads();
+        if constexpr (EMIT) {
+            __syncthreads();
+            if (wave == 0) {
+                const int lane = threadIdx.x & 63;
+                uint32_t dbits;
+                int s;
+                const int q = q8_0_block32(act_lds[lane & 31], dbits, s);
+                const int blk = blockIdx.x;
+                const int nbo = rows / 32;
+                if (lane < 32) {
+                    act_pack[(size_t)blk * 32 + lane] = (uint8_t)(int8_t)q;
+                    if (lane == 0) {
+                        reinterpret_cast<float *>(act_pack + (size_t)nbo * 32)[blk] = f16_bits_to_f32(dbits);
+                        reinterpret_cast<int32_t *>(act_pack + (size_t)nbo * 36)[blk] = s;
+                    }
+                }
+            }
+        }
+        return;
+    }
+    const int lane = threadIdx.x & 63, j = lane & 15;
+    const int row_raw = (blockIdx.x * WAVES + wave - NS) * 4 + (lane >> 4);
+    const int row = row_raw < rows ? row_raw : rows - 1;
+    const size_t nblk = (size_t)rows * NB, base = (size_t)row * NB;
+    RowRegs<ITERS> rg, ru;
+    load_row<ITERS>(rg, wg, nblk, base, NB, j);
+    load_row<ITERS>(ru, wu, nblk, base, NB, j);
+    __syncthreads();
+    float g, u;
+    fold_row2<ITERS>(rg, ru, lds, base, NB, j, g, u);
+    const float a = gelu_tanh(g) * u;
+    if (j == 15 && row_raw < rows) {
+        if (act) act[row_raw] = a;
+        if constexpr (EMIT) act_lds[row_raw - blockIdx.x * 32] = a;
+    }
+    if constexpr (EMIT) __syncthreads();
+}
+
+// ---- relay kernel for long rows ------------------------------------------------
+// S waves, 4 rows (16 lanes per row).  Wave s owns iterations
+// [s*IPW, s*IPW + IPW); each lane loads its weight block, scale word and
+// activation block (quants, scale, sum) straight from global memory, all
+// issued before any is used.  Terms go to T[s][m][k][lane]; then, in wave
+// order, wave s continues the running sums of wave s-1 over its own terms
+// (lane r < 4 folds row r) and hands them on through LDS.
+
+template <int NB, int S, int NMAT>
+__global__ __launch_bounds__(64 * S) void gemv_q4_0_relay_kernel(const uint8_t *__restrict__ w0,
+                                                                 const uint8_t *__restrict__ w1,
+                                                                 const uint8_t *__restrict__ xpack,
+                                                                 float *__restrict__ y, int rows)
+{
+    constexpr int ITERS = (NB + 15) / 16, IPW = (ITERS + S - 1) / S;
+    __shared__ __align__(16) float T[S][NMAT][IPW][64];
+    __shared__ float slot[NMAT][4];
+    const int lane = threadIdx.x & 63, j = lane & 15, ws = threadIdx.x >> 6;
+    const int row_raw = blockIdx.x * 4 + (lane >> 4);
+    const int row = row_raw < rows ? row_raw : rows - 1;
+    const size_t nblk = (size_t)rows * NB, base = (size_t)row * NB;
+    const int4 *aq = reinterpret_cast<const int4 *>(xpack);
+    const float *ad = reinterpret_cast<const float *>(xpack + NB * 32);
+    const int32_t *as = reinterpret_cast<const int32_t *>(xpack + NB * 36);
+
+    int4 a0[IPW], a1[IPW];
+    float da[IPW];
+    int32_t sa[IPW];
+    uint4 wr[NMAT][IPW];
+    uint32_t dr[NMAT][IPW];
+#pragma unroll
+    for (int k = 0; k < IPW; ++k) {
+        int it = ws * IPW + k;
+        it = it < ITERS ? it : ITERS - 1;
+        int b = it * 16 + j;
+        b = b < NB ? b : NB - 1;
+        a0[k] = aq[2 * b];
+        a1[k] = aq[2 * b + 1];
+        da[k] = ad[b];
+        sa[k] = as[b];
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) {
+            const uint8_t *w = m ? w1 : w0;
+            wr[m][k] = reinterpret_cast<const uint4 *>(w)[base + b];
+            dr[m][k] = reinterpret_cast<const uint32_t *>(w + nblk * 16)[(base + b) >> 1];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < IPW; ++k) {
+        const int it = ws * IPW + k;
+        const int b = it * 16 + j;
+        const int bc = b < NB ? b : NB - 1;
+        const bool live = it < ITERS && b < NB;
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) {
+            const int32_t isum = q4_0_isum(wr[m][k], a0[k], a1[k], sa[k]);
+            const uint32_t dbits = ((base + bc) & 1) ? dr[m][k] >> 16 : dr[m][k] & 0xffffu;
+            const float t = (float)isum * (f16_bits_to_f32(dbits) * da[k]);
+            T[ws][m][k][lane] = live ? t : 0.0f;
+        }
+    }
+    float acc[NMAT];
+    const int fr = lane & 3;
+#pragma unroll
+    for (int r = 0; r < S; ++r) {
+        if (ws == r) {
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m) {
+                float s = r == 0 ? 0.0f : slot[m][fr];
+#pragma unroll
+                for (int k = 0; k < IPW; ++k) {
+                    const float4 *v = reinterpret_cast<const float4 *>(&T[ws][m][k][fr * 16]);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 x = v[q];
+                        s = s + x.x;
+                        s = s + x.y;
+                        s = s + x.z;
+                        s = s + x.w;
+                    }
+                }
+                acc[m] = s;
+            }
+            if (r < S - 1 && lane < 4) {
+#pragma unroll
+                for (int m = 0; m < NMAT; ++m) slot[m][lane] = acc[m];
+            }
+        }
+        if (r < S - 1) __syncthreads();
+    }
+    if (ws == S - 1 && lane < 4) {
+        const int out = blockIdx.x * 4 + lane;
+        if (out < rows) y[out] = NMAT == 1 ? acc[0] : gelu_tanh(acc[0]) * acc[NMAT - 1];
+    }
+}
+
+// ---- runtime block count (fold16) -----------------------------------------------
 
 template <int ITERS, int WAVES>
-__global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_0_kernel(const uint8_t *__restrict__ w,
+__global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_0_any_kernel(const uint8_t *__restrict__ w,
                                                                      const uint8_t *xpack,
                                                                      float *__restrict__ y, int rows, int nb)
 {
-    extern __shared__ uint8_t lds[];
+    extern __shared__ __align__(16) uint8_t lds[];
     if (threadIdx.x < 64) {
         stage_pack_wave(xpack, lds, nb);
         __syncthreads();
         return;
     }
     const int lane = threadIdx.x & 63, j = lane & 15;
-    const int quad = blockIdx.x * WAVES + (threadIdx.x >> 6) - 1;
-    const int row_raw = quad * 4 + (lane >> 4);
-    const int row = row_raw < rows ? row_raw : rows - 1;  // tail rows recompute the last row
-    const size_t nblk = (size_t)rows * nb;
-    const uint4 *qs = reinterpret_cast<const uint4 *>(w);
-    const uint16_t *dp = reinterpret_cast<const uint16_t *>(w + nblk * 16);
-
+    const int row_raw = (blockIdx.x * WAVES + (threadIdx.x >> 6) - 1) * 4 + (lane >> 4);
+    const int row = row_raw < rows ? row_raw : rows - 1;
+    const size_t base = (size_t)row * nb;
     RowRegs<ITERS> r;
-    load_row<ITERS>(r, qs, dp, (size_t)row * nb, nb, j);
+    load_row<ITERS>(r, w, (size_t)rows * nb, base, nb, j);
     __syncthreads();
-    const float s = fold_row<ITERS>(r, lds, (size_t)row * nb, nb, j);
+    const float s = fold_row<ITERS>(r, lds, base, nb, j);
     if (j == 15 && row_raw < rows) y[row_raw] = s;
 }
 
-// ---- gate+up with GeGLU epilogue (model.rs:2093-2105, ops.rs:99-114) -------
-
 template <int ITERS, int WAVES>
-__global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_0_geglu_kernel(const uint8_t *__restrict__ wg,
+__global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_0_geglu_any_kernel(const uint8_t *__restrict__ wg,
                                                                            const uint8_t *__restrict__ wu,
                                                                            const uint8_t *xpack,
                                                                            float *__restrict__ act, int rows,
                                                                            int nb)
 {
-    extern __shared__ uint8_t lds[];
+    extern __shared__ __align__(16) uint8_t lds[];
     if (threadIdx.x < 64) {
         stage_pack_wave(xpack, lds, nb);
         __syncthreads();
         return;
     }
     const int lane = threadIdx.x & 63, j = lane & 15;
-    const int quad = blockIdx.x * WAVES + (threadIdx.x >> 6) - 1;
-    const int row_raw = quad * 4 + (lane >> 4);
+    const int row_raw = (blockIdx.x * WAVES + (threadIdx.x >> 6) - 1) * 4 + (lane >> 4);
     const int row = row_raw < rows ? row_raw : rows - 1;
-    const size_t nblk = (size_t)rows * nb;
-
+    const size_t nblk = (size_t)rows * nb, base = (size_t)row * nb;
     RowRegs<ITERS> rg, ru;
-    load_row<ITERS>(rg, reinterpret_cast<const uint4 *>(wg), reinterpret_cast<const uint16_t *>(wg + nblk * 16),
-                    (size_t)row * nb, nb, j);
-    load_row<ITERS>(ru, reinterpret_cast<const uint4 *>(wu), reinterpret_cast<const uint16_t *>(wu + nblk * 16),
-                    (size_t)row * nb, nb, j);
+    load_row<ITERS>(rg, wg, nblk, base, nb, j);
+    load_row<ITERS>(ru, wu, nblk, base, nb, j);
     __syncthreads();
-    const float g = fold_row<ITERS>(rg, lds, (size_t)row * nb, nb, j);
-    const float u = fold_row<ITERS>(ru, lds, (size_t)row * nb, nb, j);
+    float g, u;
+    fold_row2<ITERS>(rg, ru, lds, base, nb, j, g, u);
     if (j == 15 && row_raw < rows) act[row_raw] = gelu_tanh(g) * u;
 }
 
-// ---- fused Q/K/V: y = [Wq x | Wk x | Wv x] (cuda.rs:2378-2404) -------------
-
 template <int ITERS, int WAVES>
-__global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_0_qkv_kernel(const uint8_t *__restrict__ wq,
+__global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_0_qkv_any_kernel(const uint8_t *__restrict__ wq,
                                                                          const uint8_t *__restrict__ wk,
                                                                          const uint8_t *__restrict__ wv,
                                                                          const uint8_t *xpack,
                                                                          float *__restrict__ y, int q_rows,
                                                                          int kv_rows, int nb)
 {
-    extern __shared__ uint8_t lds[];
+    extern __shared__ __align__(16) uint8_t lds[];
     if (threadIdx.x < 64) {
         stage_pack_wave(xpack, lds, nb);
         __syncthreads();
         return;
     }
-    const int lane = threadIdx.x & 63, j = lane & 15;
     const int total = q_rows + 2 * kv_rows;
-    const int quad = blockIdx.x * WAVES + (threadIdx.x >> 6) - 1;
-    const int row_raw = quad * 4 + (lane >> 4);
-    const int row = row_raw < total ? row_raw : total - 1;
-    const uint8_t *w;
-    int local, mrows;
-    if (row < q_rows) { w = wq; local = row; mrows = q_rows; }
-    else if (row < q_rows + kv_rows) { w = wk; local = row - q_rows; mrows = kv_rows; }
-    else { w = wv; local = row - q_rows - kv_rows; mrows = kv_rows; }
-    const size_t nblk = (size_t)mrows * nb;
-
+    const int lane = threadIdx.x & 63, j = lane & 15;
+    const int row_raw = (blockIdx.x * WAVES + (threadIdx.x >> 6) - 1) * 4 + (lane >> 4);
+    const QkvSel m = qkv_select(wq, wk, wv, row_raw < total ? row_raw : total - 1, q_rows, kv_rows);
+    const size_t base = (size_t)m.local * nb;
     RowRegs<ITERS> r;
-    load_row<ITERS>(r, reinterpret_cast<const uint4 *>(w), reinterpret_cast<const uint16_t *>(w + nblk * 16),
-                    (size_t)local * nb, nb, j);
+    load_row<ITERS>(r, m.w, (size_t)m.mrows * nb, base, nb, j);
     __syncthreads();
-    const float s = fold_row<ITERS>(r, lds, (size_t)local * nb, nb, j);
+    const float s = fold_row<ITERS>(r, lds, base, nb, j);
     if (j == 15 && row_raw < total) y[row_raw] = s;
 }
 
 // ---- raw GGUF layout --------------------------------------------------------
 // The four rows of a wave are one contiguous span of 4*nb*18 bytes.  The
 // wave copies the span into LDS with 16-byte loads when it is 16-byte
-// aligned (nb % 8 == 0 and an aligned base), else with 2-byte loads, and
-// reads each 18-byte block back from LDS.  One wave per workgroup.
+// aligned, else with 2-byte loads, and reads each 18-byte block back from
+// LDS.  One wave per workgroup.
 template <int ITERS>
 __global__ __launch_bounds__(64) void gemv_q4_0_gguf_kernel(const uint8_t *__restrict__ w,
                                                             const uint8_t *xpack,
                                                             float *__restrict__ y, int rows, int nb)
 {
-    extern __shared__ uint8_t lds[];
+    extern __shared__ __align__(16) uint8_t lds[];
     uint8_t *act = lds;                                    // nb*40 bytes
     uint8_t *tile = lds + align_up((size_t)nb * 40, 16);   // 4 rows of raw blocks
     const int lane = threadIdx.x, j = lane & 15, rsub = lane >> 4;
@@ -244,17 +539,16 @@ __global__ __launch_bounds__(64) void gemv_q4_0_gguf_kernel(const uint8_t *__res
     float s = 0.0f;
     for (int it = 0; it < ITERS; ++it) {
         const int b = it * 16 + j;
-        float t = 0.0f;
-        if (b < nb) {
-            const uint16_t *blk = rowp + b * 9;  // 18 bytes = 9 halfwords
-            uint4 q;
-            q.x = blk[1] | ((uint32_t)blk[2] << 16);
-            q.y = blk[3] | ((uint32_t)blk[4] << 16);
-            q.z = blk[5] | ((uint32_t)blk[6] << 16);
-            q.w = blk[7] | ((uint32_t)blk[8] << 16);
-            const int32_t isum = q4_0_isum(q, aq + 2 * b, as[b]);
-            t = (float)isum * (f16_bits_to_f32(blk[0]) * ad[b]);
-        }
+        const int bc = b < nb ? b : nb - 1;
+        const uint16_t *blk = rowp + bc * 9;  // 18 bytes = 9 halfwords
+        uint4 q;
+        q.x = blk[1] | ((uint32_t)blk[2] << 16);
+        q.y = blk[3] | ((uint32_t)blk[4] << 16);
+        q.z = blk[5] | ((uint32_t)blk[6] << 16);
+        q.w = blk[7] | ((uint32_t)blk[8] << 16);
+        const int32_t isum = q4_0_isum(q, aq[2 * bc], aq[2 * bc + 1], as[bc]);
+        const float tv = (float)isum * (f16_bits_to_f32(blk[0]) * ad[bc]);
+        const float t = b < nb ? tv : 0.0f;
 #pragma unroll
         for (int k = 0; k < 16; ++k) s = fold16(s, t);
     }
@@ -263,8 +557,7 @@ __global__ __launch_bounds__(64) void gemv_q4_0_gguf_kernel(const uint8_t *__res
 
 // ---- dispatch ---------------------------------------------------------------
 
-// Waves per workgroup: enough rows per workgroup to amortise the LDS copy of
-// the activation pack, few enough that the grid still covers all 256 CUs.
+// Waves per workgroup of the runtime-nb kernels.
 inline int waves_for(int rows) { return rows >= 8192 ? 4 : (rows >= 2048 ? 2 : 1); }
 
 #define MRML_DISPATCH_ITERS(ITERS_VAL, BODY)                 \
@@ -291,6 +584,22 @@ inline int waves_for(int rows) { return rows >= 8192 ? 4 : (rows >= 2048 ? 2 : 1
     default: { constexpr int WV = 4; BODY; } break;          \
     }
 
+// Fixed-shape instances (the block counts of the Gemma-2-2B projections).
+constexpr int kFoldWaves = 4;   // fold16 compute waves per workgroup
+constexpr int kRelayS = 6;      // relay waves per 4 rows for 288-block rows
+
+inline bool fold16_shape(int nb) { return nb == 64 || nb == 72; }
+inline bool relay_shape(int nb) { return nb == 288; }
+
+#define MRML_FOLD16_NB(NB_VAL, BODY)                                                  \
+    switch (NB_VAL) {                                                                 \
+    case 64: { constexpr int NB = 64; BODY; } break;                                  \
+    case 72: { constexpr int NB = 72; BODY; } break;                                  \
+    default: break;                                                                   \
+    }
+
+size_t pack_lds(int nb) { return align_up((size_t)nb * 40, 16); }
+
 }  // namespace
 
 // The scale plane is read as 4-byte words, so the block count of each matrix
@@ -308,16 +617,47 @@ int launch_gemv_q4_0(mrml_hip_ctx *ctx, const void *w, const void *xpack, float 
 {
     const int nb = cols / 32;
     if (int rc = check_even(ctx, rows, nb)) return rc;
+    if (fold16_shape(nb)) {
+        const dim3 grid(((rows + 3) / 4 + kFoldWaves - 1) / kFoldWaves);
+        MRML_FOLD16_NB(nb, {
+            hipLaunchKernelGGL((gemv_q4_0_kernel<NB, kFoldWaves, false>), grid, dim3(64 * (kFoldWaves + 1)),
+                               pack_lds(NB), ctx->stream, (const uint8_t *)w, xpack, y, rows);
+        });
+        return check_launch(ctx, "gemv_q4_0_kernel");
+    }
+    if (relay_shape(nb)) {
+        hipLaunchKernelGGL((gemv_q4_0_relay_kernel<288, kRelayS, 1>), dim3((rows + 3) / 4), dim3(64 * kRelayS), 0,
+                           ctx->stream, (const uint8_t *)w, (const uint8_t *)w, (const uint8_t *)xpack, y, rows);
+        return check_launch(ctx, "gemv_q4_0_relay_kernel");
+    }
     const int iters = (nb + 15) / 16;
     const int waves = waves_for(rows);
-    const int quads = (rows + 3) / 4;
-    const dim3 grid((quads + waves - 1) / waves);
-    const size_t lds = act_pack_bytes(nb);
+    const dim3 grid(((rows + 3) / 4 + waves - 1) / waves);
     MRML_DISPATCH_ITERS(iters, MRML_DISPATCH_WAVES(waves, {
-        hipLaunchKernelGGL((gemv_q4_0_kernel<IT, WV>), grid, dim3(64 * (WV + 1)), lds, ctx->stream,
+        hipLaunchKernelGGL((gemv_q4_0_any_kernel<IT, WV>), grid, dim3(64 * (WV + 1)), pack_lds(nb), ctx->stream,
                            (const uint8_t *)w, (const uint8_t *)xpack, y, rows, nb);
     }));
-    return check_launch(ctx, "gemv_q4_0_kernel");
+    return check_launch(ctx, "gemv_q4_0_any_kernel");
+}
+
+// f32 input: quantised inside the kernel where a fixed instance exists, else
+// through the scratch pack.
+int launch_gemv_q4_0_x(mrml_hip_ctx *ctx, const void *w, const float *x, float *y, int32_t rows, int32_t cols)
+{
+    const int nb = cols / 32;
+    if (int rc = check_even(ctx, rows, nb)) return rc;
+    if (fold16_shape(nb)) {
+        const dim3 grid(((rows + 3) / 4 + kFoldWaves - 1) / kFoldWaves);
+        MRML_FOLD16_NB(nb, {
+            hipLaunchKernelGGL((gemv_q4_0_kernel<NB, kFoldWaves, true>), grid, dim3(64 * (kFoldWaves + kNQ)),
+                               pack_lds(NB), ctx->stream, (const uint8_t *)w, (const void *)x, y, rows);
+        });
+        return check_launch(ctx, "gemv_q4_0_kernel");
+    }
+    void *pk = workspace(ctx, act_pack_bytes(nb));
+    if (!pk) return MRML_HIP_E_ALLOC;
+    if (int rc = launch_quantize_q8_0(ctx, x, nullptr, pk, cols)) return rc;
+    return launch_gemv_q4_0(ctx, w, pk, y, rows, cols);
 }
 
 int launch_gemv_q4_0_geglu(mrml_hip_ctx *ctx, const void *wg, const void *wu, const void *xpack, float *act,
@@ -325,16 +665,65 @@ int launch_gemv_q4_0_geglu(mrml_hip_ctx *ctx, const void *wg, const void *wu, co
 {
     const int nb = cols / 32;
     if (int rc = check_even(ctx, rows, nb)) return rc;
+    if (fold16_shape(nb)) {
+        const dim3 grid(((rows + 3) / 4 + kFoldWaves - 1) / kFoldWaves);
+        MRML_FOLD16_NB(nb, {
+            hipLaunchKernelGGL((gemv_q4_0_geglu_kernel<NB, kFoldWaves, false, false>), grid,
+                               dim3(64 * (kFoldWaves + 1)), pack_lds(NB), ctx->stream, (const uint8_t *)wg,
+                               (const uint8_t *)wu, xpack, act, (uint8_t *)nullptr, rows);
+        });
+        return check_launch(ctx, "gemv_q4_0_geglu_kernel");
+    }
+    if (relay_shape(nb)) {
+        hipLaunchKernelGGL((gemv_q4_0_relay_kernel<288, kRelayS, 2>), dim3((rows + 3) / 4), dim3(64 * kRelayS), 0,
+                           ctx->stream, (const uint8_t *)wg, (const uint8_t *)wu, (const uint8_t *)xpack, act, rows);
+        return check_launch(ctx, "gemv_q4_0_relay_kernel");
+    }
     const int iters = (nb + 15) / 16;
     const int waves = waves_for(rows);
-    const int quads = (rows + 3) / 4;
-    const dim3 grid((quads + waves - 1) / waves);
-    const size_t lds = act_pack_bytes(nb);
+    const dim3 grid(((rows + 3) / 4 + waves - 1) / waves);
     MRML_DISPATCH_ITERS(iters, MRML_DISPATCH_WAVES(waves, {
-        hipLaunchKernelGGL((gemv_q4_0_geglu_kernel<IT, WV>), grid, dim3(64 * (WV + 1)), lds, ctx->stream,
-                           (const uint8_t *)wg, (const uint8_t *)wu, (const uint8_t *)xpack, act, rows, nb);
+        hipLaunchKernelGGL((gemv_q4_0_geglu_any_kernel<IT, WV>), grid, dim3(64 * (WV + 1)), pack_lds(nb),
+                           ctx->stream, (const uint8_t *)wg, (const uint8_t *)wu, (const uint8_t *)xpack, act, rows,
+                           nb);
     }));
-    return check_launch(ctx, "gemv_q4_0_geglu_kernel");
+    return check_launch(ctx, "gemv_q4_0_geglu_any_kernel");
+}
+
+// f32 input, optional f32 output, optional Q8_0 pack of the output (for the
+// next projection).  One launch when the shape has a fixed instance and
+// rows % 32 == 0; otherwise quantise / run / quantise separately.
+int launch_gemv_q4_0_geglu_x(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *x, float *act,
+                             void *act_pack, int32_t rows, int32_t cols)
+{
+    const int nb = cols / 32;
+    if (int rc = check_even(ctx, rows, nb)) return rc;
+    if (fold16_shape(nb) && (!act_pack || rows % 32 == 0)) {
+        const size_t lds = pack_lds(nb) + 32 * sizeof(float);
+        if (act_pack) {
+            MRML_FOLD16_NB(nb, {
+                hipLaunchKernelGGL((gemv_q4_0_geglu_kernel<NB, 8, true, true>), dim3(rows / 32), dim3(64 * (8 + kNQ)),
+                                   lds, ctx->stream, (const uint8_t *)wg, (const uint8_t *)wu, (const void *)x, act,
+                                   (uint8_t *)act_pack, rows);
+            });
+        } else {
+            const dim3 grid(((rows + 3) / 4 + kFoldWaves - 1) / kFoldWaves);
+            MRML_FOLD16_NB(nb, {
+                hipLaunchKernelGGL((gemv_q4_0_geglu_kernel<NB, kFoldWaves, true, false>), grid,
+                                   dim3(64 * (kFoldWaves + kNQ)), lds, ctx->stream, (const uint8_t *)wg,
+                                   (const uint8_t *)wu, (const void *)x, act, (uint8_t *)nullptr, rows);
+            });
+        }
+        return check_launch(ctx, "gemv_q4_0_geglu_kernel");
+    }
+    const size_t in_bytes = act_pack_bytes(nb);
+    uint8_t *ws = (uint8_t *)workspace(ctx, in_bytes + (size_t)rows * sizeof(float));
+    if (!ws) return MRML_HIP_E_ALLOC;
+    float *out = act ? act : reinterpret_cast<float *>(ws + in_bytes);
+    if (int rc = launch_quantize_q8_0(ctx, x, nullptr, ws, cols)) return rc;
+    if (int rc = launch_gemv_q4_0_geglu(ctx, wg, wu, ws, out, rows, cols)) return rc;
+    if (act_pack) return launch_quantize_q8_0(ctx, out, nullptr, act_pack, rows);
+    return MRML_HIP_OK;
 }
 
 int launch_gemv_q4_0_qkv(mrml_hip_ctx *ctx, const void *wq, const void *wk, const void *wv, const void *xpack,
@@ -343,18 +732,47 @@ int launch_gemv_q4_0_qkv(mrml_hip_ctx *ctx, const void *wq, const void *wk, cons
     const int nb = cols / 32;
     if (int rc = check_even(ctx, q_rows, nb)) return rc;
     if (int rc = check_even(ctx, kv_rows, nb)) return rc;
-    const int iters = (nb + 15) / 16;
     const int total = q_rows + 2 * kv_rows;
+    if (fold16_shape(nb)) {
+        const dim3 grid(((total + 3) / 4 + kFoldWaves - 1) / kFoldWaves);
+        MRML_FOLD16_NB(nb, {
+            hipLaunchKernelGGL((gemv_q4_0_qkv_kernel<NB, kFoldWaves, false>), grid, dim3(64 * (kFoldWaves + 1)),
+                               pack_lds(NB), ctx->stream, (const uint8_t *)wq, (const uint8_t *)wk,
+                               (const uint8_t *)wv, xpack, y, q_rows, kv_rows);
+        });
+        return check_launch(ctx, "gemv_q4_0_qkv_kernel");
+    }
+    const int iters = (nb + 15) / 16;
     const int waves = waves_for(total);
-    const int quads = (total + 3) / 4;
-    const dim3 grid((quads + waves - 1) / waves);
-    const size_t lds = act_pack_bytes(nb);
+    const dim3 grid(((total + 3) / 4 + waves - 1) / waves);
     MRML_DISPATCH_ITERS(iters, MRML_DISPATCH_WAVES(waves, {
-        hipLaunchKernelGGL((gemv_q4_0_qkv_kernel<IT, WV>), grid, dim3(64 * (WV + 1)), lds, ctx->stream,
+        hipLaunchKernelGGL((gemv_q4_0_qkv_any_kernel<IT, WV>), grid, dim3(64 * (WV + 1)), pack_lds(nb), ctx->stream,
                            (const uint8_t *)wq, (const uint8_t *)wk, (const uint8_t *)wv, (const uint8_t *)xpack,
                            y, q_rows, kv_rows, nb);
     }));
-    return check_launch(ctx, "gemv_q4_0_qkv_kernel");
+    return check_launch(ctx, "gemv_q4_0_qkv_any_kernel");
+}
+
+int launch_gemv_q4_0_qkv_x(mrml_hip_ctx *ctx, const void *wq, const void *wk, const void *wv, const float *x,
+                           float *y, int32_t q_rows, int32_t kv_rows, int32_t cols)
+{
+    const int nb = cols / 32;
+    if (int rc = check_even(ctx, q_rows, nb)) return rc;
+    if (int rc = check_even(ctx, kv_rows, nb)) return rc;
+    const int total = q_rows + 2 * kv_rows;
+    if (fold16_shape(nb)) {
+        const dim3 grid(((total + 3) / 4 + kFoldWaves - 1) / kFoldWaves);
+        MRML_FOLD16_NB(nb, {
+            hipLaunchKernelGGL((gemv_q4_0_qkv_kernel<NB, kFoldWaves, true>), grid, dim3(64 * (kFoldWaves + kNQ)),
+                               pack_lds(NB), ctx->stream, (const uint8_t *)wq, (const uint8_t *)wk,
+                               (const uint8_t *)wv, (const void *)x, y, q_rows, kv_rows);
+        });
+        return check_launch(ctx, "gemv_q4_0_qkv_kernel");
+    }
+    void *pk = workspace(ctx, act_pack_bytes(nb));
+    if (!pk) return MRML_HIP_E_ALLOC;
+    if (int rc = launch_quantize_q8_0(ctx, x, nullptr, pk, cols)) return rc;
+    return launch_gemv_q4_0_qkv(ctx, wq, wk, wv, pk, y, q_rows, kv_rows, cols);
 }
 
 int launch_gemv_q4_0_gguf(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows,

@@ -46,6 +46,12 @@ int launch_gemv_q4_0(mrml_hip_ctx *ctx, const void *w, const void *xpack, float 
                      int32_t rows, int32_t cols);
 int launch_gemv_q4_0_gguf(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y,
                           int32_t rows, int32_t cols);
+// f32-input forms: quantise x inside the kernel where a fixed instance exists.
+int launch_gemv_q4_0_x(mrml_hip_ctx *ctx, const void *w, const float *x, float *y, int32_t rows, int32_t cols);
+int launch_gemv_q4_0_geglu_x(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *x, float *act,
+                             void *act_pack, int32_t rows, int32_t cols);
+int launch_gemv_q4_0_qkv_x(mrml_hip_ctx *ctx, const void *wq, const void *wk, const void *wv, const float *x,
+                           float *y, int32_t q_rows, int32_t kv_rows, int32_t cols);
 int launch_gemv_q4_0_geglu(mrml_hip_ctx *ctx, const void *wg, const void *wu, const void *xpack,
                            float *act, int32_t rows, int32_t cols);
 int launch_gemv_q4_0_qkv(mrml_hip_ctx *ctx, const void *wq, const void *wk, const void *wv,

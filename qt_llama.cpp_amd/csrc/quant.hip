@@ -5,45 +5,29 @@
 
 namespace mrml {
 
-// quant.rs:193-228, one 32-value block per half-wave (lane l owns value l).
-//   amax   : max |x| (starts at 0, NaN never wins) -- exact in any order
-//   scale  = amax / 127          (IEEE division)
-//   d      = f32_to_f16 by truncation
-//   id     = scale != 0 ? 1/scale : 0   (from the unrounded scale)
-//   q      = (int8) clamp(roundf(x*id), -128, 127), NaN -> 0
-// The pack additionally stores d widened to f32 and the block's quant sum.
+// quant.rs:193-228, one 32-value block per 8 lanes (lane l owns values
+// 4l..4l+3); the arithmetic is q8_0_block8x4.  The pack additionally stores d
+// widened to f32 and the block's quant sum.  x must be 16-byte aligned.
 __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x,
                                                             uint8_t *__restrict__ gguf,
                                                             uint8_t *__restrict__ pack, int nb)
 {
-    const int gb = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 5);
-    const int l = threadIdx.x & 31;
-    if (gb >= nb) return;  // whole half-waves exit together
-    const float v = x[(size_t)gb * 32 + l];
-    float a = fabsf(v);
-    float m = (a > 0.0f) ? a : 0.0f;  // NaN -> 0
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) {
-        float o = __shfl_xor(m, off, 32);
-        m = (o > m) ? o : m;
-    }
-    const float scale = m / 127.0f;
-    const uint32_t dbits = f32_to_f16_trunc(scale);
-    const float id = (scale != 0.0f) ? 1.0f / scale : 0.0f;
-    float r = roundf(v * id);
-    r = (r < -128.0f) ? -128.0f : r;
-    r = (r > 127.0f) ? 127.0f : r;
-    const int q = (r != r) ? 0 : (int)r;
-    int s = q;
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) s += __shfl_xor(s, off, 32);
+    const int gb_raw = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 3);
+    const int l = threadIdx.x & 7;
+    const int gb = gb_raw < nb ? gb_raw : nb - 1;  // all lanes take part in the reductions
+    uint32_t dbits;
+    int s;
+    const uint32_t q = q8_0_block8x4(reinterpret_cast<const float4 *>(x)[(size_t)gb * 8 + l], dbits, s);
+    if (gb_raw >= nb) return;
     if (gguf) {
-        uint8_t *blk = gguf + (size_t)gb * 34;
+        uint8_t *blk = gguf + (size_t)gb * 34;  // 2-byte aligned
         if (l == 0) *reinterpret_cast<uint16_t *>(blk) = (uint16_t)dbits;
-        blk[2 + l] = (uint8_t)(int8_t)q;
+        uint16_t *qs = reinterpret_cast<uint16_t *>(blk + 2 + 4 * l);
+        qs[0] = (uint16_t)q;
+        qs[1] = (uint16_t)(q >> 16);
     }
     if (pack) {
-        pack[(size_t)gb * 32 + l] = (uint8_t)(int8_t)q;
+        reinterpret_cast<uint32_t *>(pack)[(size_t)gb * 8 + l] = q;
         if (l == 0) {
             reinterpret_cast<float *>(pack + (size_t)nb * 32)[gb] = f16_bits_to_f32(dbits);
             reinterpret_cast<int32_t *>(pack + (size_t)nb * 36)[gb] = s;
@@ -54,8 +38,8 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restr
 int launch_quantize_q8_0(mrml_hip_ctx *ctx, const float *x, void *gguf, void *pack, int32_t n)
 {
     const int nb = n / 32;
-    const int threads = 256;  // 8 blocks per workgroup
-    const int grid = (nb * 32 + threads - 1) / threads;
+    const int threads = 256;  // 32 blocks per workgroup
+    const int grid = (nb * 8 + threads - 1) / threads;
     hipLaunchKernelGGL(quantize_q8_0_kernel, dim3(grid), dim3(threads), 0, ctx->stream, x,
                        (uint8_t *)gguf, (uint8_t *)pack, nb);
     return check_launch(ctx, "quantize_q8_0_kernel");

@@ -347,6 +347,8 @@ int mrml_hip_quantize_q8_0(mrml_hip_ctx *ctx, const float *x, void *gguf, void *
     REQUIRE(ctx, x, "x is null");
     REQUIRE(ctx, gguf || pack, "quantize_q8_0: no output requested");
     REQUIRE(ctx, n > 0 && n % 32 == 0, "quantize_q8_0: n=%d is not a positive multiple of 32", n);
+    REQUIRE(ctx, ((uintptr_t)x & 15) == 0 && ((uintptr_t)pack & 15) == 0 && ((uintptr_t)gguf & 1) == 0,
+            "quantize_q8_0: x and pack must be 16-byte aligned, gguf 2-byte aligned");
     return launch_quantize_q8_0(ctx, x, gguf, pack, n);
 }
 
@@ -362,6 +364,7 @@ static void *quantize_to_scratch(mrml_hip_ctx *ctx, const float *x, int32_t cols
 #define CHECK_MATVEC(ctx, w, x, y, rows, cols, mult)                                          \
     do {                                                                                      \
         REQUIRE(ctx, (w) && (x) && (y), "null pointer");                                      \
+        REQUIRE(ctx, ((uintptr_t)(x) & 15) == 0, "x / pack must be 16-byte aligned");          \
         REQUIRE(ctx, (rows) > 0 && (cols) > 0 && (cols) % (mult) == 0,                        \
                 "rows=%d cols=%d: need rows > 0 and cols a positive multiple of %d",          \
                 (int)(rows), (int)(cols), (int)(mult));                                       \
@@ -371,9 +374,7 @@ int mrml_hip_gemv_q4_0(mrml_hip_ctx *ctx, const void *w, const float *x, float *
 {
     CTX_GUARD(ctx);
     CHECK_MATVEC(ctx, w, x, y, rows, cols, 32);
-    void *xp = quantize_to_scratch(ctx, x, cols);
-    if (!xp) return ctx->err.empty() ? MRML_HIP_E_HIP : MRML_HIP_E_ALLOC;
-    return launch_gemv_q4_0(ctx, w, xp, y, rows, cols);
+    return launch_gemv_q4_0_x(ctx, w, x, y, rows, cols);
 }
 
 int mrml_hip_gemv_q4_0_q8(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows, int32_t cols)
@@ -398,9 +399,30 @@ int mrml_hip_gemv_q4_0_geglu(mrml_hip_ctx *ctx, const void *wg, const void *wu, 
     CTX_GUARD(ctx);
     CHECK_MATVEC(ctx, wg, x, act, rows, cols, 32);
     REQUIRE(ctx, wu, "w_up is null");
-    void *xp = quantize_to_scratch(ctx, x, cols);
-    if (!xp) return MRML_HIP_E_ALLOC;
-    return launch_gemv_q4_0_geglu(ctx, wg, wu, xp, act, rows, cols);
+    return launch_gemv_q4_0_geglu_x(ctx, wg, wu, x, act, nullptr, rows, cols);
+}
+
+int mrml_hip_gemv_q4_0_geglu_pack(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *x, float *act,
+                                  void *act_pack, int32_t rows, int32_t cols)
+{
+    CTX_GUARD(ctx);
+    CHECK_MATVEC(ctx, wg, x, act_pack, rows, cols, 32);
+    REQUIRE(ctx, wu, "w_up is null");
+    REQUIRE(ctx, rows % 32 == 0, "rows=%d is not a multiple of 32", rows);
+    return launch_gemv_q4_0_geglu_x(ctx, wg, wu, x, act, act_pack, rows, cols);
+}
+
+int mrml_hip_ffn_geglu_q4_0(mrml_hip_ctx *ctx, const void *wg, const void *wu, const void *wd, const float *x,
+                            float *act, float *y, int32_t dim, int32_t ffn)
+{
+    CTX_GUARD(ctx);
+    CHECK_MATVEC(ctx, wg, x, y, ffn, dim, 32);
+    REQUIRE(ctx, wu && wd, "null pointer");
+    REQUIRE(ctx, ffn % 32 == 0, "ffn=%d is not a multiple of 32", ffn);
+    void *pk = workspace(ctx, act_pack_bytes(ffn / 32));
+    if (!pk) return MRML_HIP_E_ALLOC;
+    if (int rc = launch_gemv_q4_0_geglu_x(ctx, wg, wu, x, act, pk, ffn, dim)) return rc;
+    return launch_gemv_q4_0(ctx, wd, pk, y, dim, ffn);
 }
 
 int mrml_hip_gemv_q4_0_geglu_q8(mrml_hip_ctx *ctx, const void *wg, const void *wu, const void *xpack,
@@ -429,9 +451,7 @@ int mrml_hip_gemv_q4_0_qkv(mrml_hip_ctx *ctx, const void *wq, const void *wk, co
     CHECK_MATVEC(ctx, wq, x, y, q_rows, cols, 32);
     REQUIRE(ctx, wk && wv, "null pointer");
     REQUIRE(ctx, kv_rows > 0, "kv_rows=%d", kv_rows);
-    void *xp = quantize_to_scratch(ctx, x, cols);
-    if (!xp) return MRML_HIP_E_ALLOC;
-    return launch_gemv_q4_0_qkv(ctx, wq, wk, wv, xp, y, q_rows, kv_rows, cols);
+    return launch_gemv_q4_0_qkv_x(ctx, wq, wk, wv, x, y, q_rows, kv_rows, cols);
 }
 
 int mrml_hip_gemv_q8_0(mrml_hip_ctx *ctx, const void *w, const float *x, float *y, int32_t rows, int32_t cols,

@@ -163,6 +163,54 @@ def test_gemv_q4_0_geglu(backend, dev, orc, synth):
     print(f"geglu: max rel {np.max(rel):.2e}, bit-identical {np.mean(bits(a) == bits(ref)):.3f}")
 
 
+def test_ffn_geglu_fused(backend, dev, orc, synth):
+    """Two-launch FFN: GeGLU quantises x itself and emits the Q8_0 pack of its
+    output, which the down projection consumes.  The emitted pack must equal
+    the reference quantiser applied to the kernel's own f32 output, and y must
+    equal the oracle down projection of that output, bit for bit."""
+    dim, ffn = 2304, 9216
+    rng = synth.rng_for(5500)
+    wg, wu = synth.q4_0_matrix(rng, ffn, dim), synth.q4_0_matrix(rng, ffn, dim)
+    wd = synth.q4_0_matrix(rng, dim, ffn)
+    x = synth.rms_normalised(synth.normal_vector(rng, dim))
+    bg, bu = (backend.HipBuffer.from_gguf(dev, w, backend.Q4_0, ffn, dim) for w in (wg, wu))
+    bd = backend.HipBuffer.from_gguf(dev, wd, backend.Q4_0, dim, ffn)
+    xb = upload(backend, dev, x)
+    act = backend.HipBuffer.alloc(dev, ffn)
+    y = backend.HipBuffer.alloc(dev, dim)
+    dev.ffn_geglu_q4_0(bg, bu, bd, xb, act, y, dim, ffn)
+    dev.sync()
+    a = act.numpy()
+    xq = orc.quantize_q8_0(x)
+    ref_act = orc.geglu(orc.mat_vec_mul_q4_0_q8_0(wg, xq, ffn, dim, threads=THREADS),
+                        orc.mat_vec_mul_q4_0_q8_0(wu, xq, ffn, dim, threads=THREADS))
+    assert np.max(np.abs(a - ref_act) / np.maximum(np.abs(ref_act), 1e-30)) <= 1e-5
+    assert_bit_exact(y.numpy(), orc.mat_vec_mul_q4_0(wd, a, dim, ffn, threads=THREADS), "ffn down")
+    # the same FFN without the f32 activation output
+    y2 = backend.HipBuffer.alloc(dev, dim)
+    dev.ffn_geglu_q4_0(bg, bu, bd, xb, None, y2, dim, ffn)
+    dev.sync()
+    assert_bit_exact(y2.numpy(), y.numpy(), "ffn without act output")
+
+
+def test_gemv_q4_0_geglu_long_rows(backend, dev, orc, synth):
+    """GeGLU on 288-block rows runs the relay kernel with two matrices."""
+    rows, cols = 2304, 9216
+    rng = synth.rng_for(5600)
+    wg, wu = synth.q4_0_matrix(rng, rows, cols), synth.q4_0_matrix(rng, rows, cols)
+    x = synth.normal_vector(rng, cols)
+    xq = orc.quantize_q8_0(x)
+    ref = orc.geglu(orc.mat_vec_mul_q4_0_q8_0(wg, xq, rows, cols, threads=THREADS),
+                    orc.mat_vec_mul_q4_0_q8_0(wu, xq, rows, cols, threads=THREADS))
+    bg, bu = (backend.HipBuffer.from_gguf(dev, w, backend.Q4_0, rows, cols) for w in (wg, wu))
+    xb = upload(backend, dev, x)
+    act = backend.HipBuffer.alloc(dev, rows)
+    dev.gemv_q4_0_geglu(bg, bu, xb, act, rows, cols)
+    dev.sync()
+    a = act.numpy()
+    assert np.max(np.abs(a - ref) / np.maximum(np.abs(ref), 1e-30)) <= 1e-5
+
+
 def test_gemv_q4_0_qkv(backend, dev, orc, synth):
     q_rows, kv_rows, cols = 2048, 1024, 2304
     rng = synth.rng_for(6000)
