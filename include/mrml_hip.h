@@ -199,6 +199,95 @@ int mrml_hip_gemv_q4_k(mrml_hip_ctx *ctx, const void *d_w, const float *d_x, flo
  * never wins.  d_out: one int32 on the device. */
 int mrml_hip_argmax_f32(mrml_hip_ctx *ctx, const float *d_x, int32_t n, int32_t *d_out);
 
+/* ---- the rest of the token step ---------------------------------------------
+ * Floating-point ops whose reference results depend on libm and on the order
+ * of long f32 sums: parity is to a stated tolerance.  Where an op takes both
+ * `pos` and `d_pos`, a non-null d_pos (one int32 on the device) is read when
+ * the op executes, so a captured graph serves every position. */
+
+/* CudaDevice::rms_norm (cuda.rs:2102-2180; CPU ops.rs:24-79):
+ * out = (x * (1/sqrt(sum(x^2)/dim + eps))) * w.  d_w nullable (no weight).
+ * d_out (f32) and d_pack (the Q8_0 activation pack of the result, for the
+ * next matvec) are each nullable, not both.  dim % 32 == 0, dim <= 16384. */
+int mrml_hip_rms_norm(mrml_hip_ctx *ctx, const float *d_x, const float *d_w, float *d_out, void *d_pack,
+                      int32_t dim, float eps);
+/* Gemma-2 sandwich-norm residual, then the next block's pre-norm (the
+ * per-layer order of model.rs:1185-2260):
+ *   h += rms_norm(t, w_post);  xn = rms_norm(h, w_next) -> d_xn, d_pack (nullable). */
+int mrml_hip_residual_rms_norm(mrml_hip_ctx *ctx, const float *d_t, const float *d_w_post, float *d_h,
+                               const float *d_w_next, float *d_xn, void *d_pack, int32_t dim, float eps);
+/* CudaDevice::embedding_q8_0 (cuda.rs:2625-2656; CPU model.rs:1164-1182):
+ * out[i] = (q_i * d) * scale for row `token` of a backend-layout Q4_0 or Q8_0
+ * table (type MRML_HIP_Q4_0 / MRML_HIP_Q8_0).  d_token overrides token. */
+int mrml_hip_embedding(mrml_hip_ctx *ctx, const void *d_table, int32_t type, int32_t token,
+                       const int32_t *d_token, float *d_out, int32_t dim, int32_t vocab, float scale);
+/* RoPE angle table for positions 0..n_pos-1: d_table[(pos*head_dim/2 + i)*2]
+ * = cosf(theta), +1 = sinf(theta), theta = pos*freq_scale /
+ * powf(freq_base, 2i/head_dim) (ops.rs:185-208), computed on the host with
+ * the C library the reference calls, so table-driven RoPE is bit-exact.
+ * Synchronous (uploads n_pos*head_dim floats); call before graph capture. */
+int mrml_hip_rope_table(mrml_hip_ctx *ctx, float *d_table, int32_t n_pos, int32_t head_dim, float freq_base,
+                        float freq_scale);
+/* CudaDevice::qkv_postprocess (cuda.rs:2438-2476) without the Gemma-4 head
+ * norms: NeoX RoPE (ops.rs:185-208; theta = pos*freq_scale /
+ * freq_base^(2i/head_dim)) on the q and k heads of d_qkv = [q | k | v] in
+ * place, then k and v stored as f16 (round to nearest even) at cache row
+ * pos % capacity of [capacity][n_kv_heads][head_dim] caches.  cos/sin come
+ * from d_table (nullable; from mrml_hip_rope_table) for pos < n_table, else
+ * are evaluated on the device (double precision rounded to f32). */
+int mrml_hip_rope_kv_append_f16(mrml_hip_ctx *ctx, float *d_qkv, uint16_t *d_k_cache, uint16_t *d_v_cache,
+                                int32_t pos, const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads,
+                                int32_t head_dim, float freq_base, float freq_scale, int32_t capacity,
+                                const float *d_table, int32_t n_table);
+/* CudaDevice::attention_causal (cuda.rs:2658-2697; CPU model.rs:1457-1590)
+ * for one token: out[h] = softmax(scale * q[h] . K[t]) . V[t] over the last
+ * min(n_past+1, capacity) cache rows, kv head h / (n_heads / n_kv_heads),
+ * in the CPU path's operation order (sequential dots, softmax sum and
+ * weighted sum; the host C library's expf).  head_dim 256, group of at most
+ * 8, capacity at most 16000.  d_out (f32) and d_pack (Q8_0 pack of the
+ * n_heads*head_dim output) nullable, not both. */
+int mrml_hip_attn_decode_f16(mrml_hip_ctx *ctx, const float *d_q, const uint16_t *d_k_cache,
+                             const uint16_t *d_v_cache, float *d_out, void *d_pack, int32_t n_past,
+                             const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                             float scale, int32_t capacity);
+
+/* ---- Gemma-2-shape token step (model.rs forward_token, model.rs:1185-2260,
+ * and greedy selection, model.rs:2833-2907) ----------------------------------- */
+typedef struct mrml_hip_gemma2_config {
+    int32_t n_layers, dim, n_heads, n_kv_heads, head_dim, ffn_dim, vocab, ctx_len;
+    float   rope_base, eps, attn_scale;
+    int32_t tie_type; /* MRML_HIP_Q4_0 or MRML_HIP_Q8_0: tied embedding / LM-head table */
+} mrml_hip_gemma2_config;
+
+/* Device pointers of one layer: matrices in the backend Q4_0 layout, norm
+ * weights f32[dim]. */
+typedef struct mrml_hip_gemma2_layer {
+    const void  *wq, *wk, *wv, *wo, *w_gate, *w_up, *w_down;
+    const float *attn_norm, *post_attn_norm, *ffn_norm, *post_ffw_norm;
+} mrml_hip_gemma2_layer;
+
+typedef struct mrml_hip_gemma2 mrml_hip_gemma2;
+
+/* Bind weights (not copied; they must outlive the model) and allocate the
+ * step's activation buffers. */
+int mrml_hip_gemma2_create(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config *cfg, const void *d_tok_embd,
+                           const float *d_output_norm, const mrml_hip_gemma2_layer *layers,
+                           mrml_hip_gemma2 **out);
+int mrml_hip_gemma2_destroy(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model);
+/* Enqueue one token step.  d_state = {token, pos} (two int32 on the device)
+ * is read when the step executes; its last kernel records the greedy argmax
+ * (lowest index on ties) in d_argmax (nullable) and in d_hist[pos] (nullable,
+ * pos < hist_cap), then advances the state: pos += 1 and token =
+ * d_prompt[pos] while pos < prompt_len (prefill), else the argmax.  Caches
+ * are [n_layers][ctx_len][n_kv_heads][head_dim] f16.  d_logits (nullable)
+ * receives the vocab logits.  A graph captured around one call replays for
+ * every token. */
+int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, int32_t *d_state, uint16_t *d_k_cache,
+                         uint16_t *d_v_cache, float *d_logits, int32_t *d_argmax, int32_t *d_hist,
+                         int32_t hist_cap, const int32_t *d_prompt, int32_t prompt_len);
+/* The model's own residual stream h (f32[dim]) and logits (f32[vocab]). */
+int mrml_hip_gemma2_activations(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, float **d_h, float **d_logits);
+
 #ifdef __cplusplus
 }
 #endif

@@ -254,3 +254,37 @@ def attention_f16(q, k_cache, v_cache, n_past, n_heads, n_kv_heads, head_dim, sc
                             _p(np.ascontiguousarray(v_cache, dtype=np.uint16)), _p(out), n_past, n_heads,
                             n_kv_heads, head_dim, scale)
     return out
+
+
+class OracleGemma2:
+    """The decode-step oracle (orc_gemma2_step) over a model held as GGUF block
+    bytes (the dict of qt_llama.cpp_amd.synth.gemma2_model)."""
+
+    def __init__(self, model: dict, softcap: bool = False):
+        c = model["cfg"]
+        self.model = model
+        self.cfg = c
+        L = model["layers"]
+        n = c["n_layers"]
+        self._arrays = {}
+
+        def parr(key):
+            a = (ctypes.c_void_p * n)(*[_p(layer[key]) for layer in L])
+            self._arrays[key] = a
+            return ctypes.cast(a, _P)
+
+        self.s = Gemma2(c["n_layers"], c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["ffn_dim"],
+                        c["vocab"], c["ctx_len"], c["rope_base"], c["eps"], c["attn_scale"],
+                        int(model["tie_q8"]), int(softcap), _p(model["tok_embd"]), _p(model["output_norm"]),
+                        parr("wq"), parr("wk"), parr("wv"), parr("wo"), parr("w_gate"), parr("w_up"),
+                        parr("w_down"), parr("attn_norm"), parr("post_attn_norm"), parr("ffn_norm"),
+                        parr("post_ffw_norm"))
+        kvd = c["n_kv_heads"] * c["head_dim"]
+        self.k_cache = np.zeros(c["n_layers"] * c["ctx_len"] * kvd, np.uint16)
+        self.v_cache = np.zeros_like(self.k_cache)
+
+    def step(self, token: int, pos: int, threads: int = 1, logits: np.ndarray | None = None) -> int:
+        """One token at position pos; returns the greedy next token."""
+        lg = _p(logits) if logits is not None else None
+        return int(lib().orc_gemma2_step(ctypes.byref(self.s), int(token), int(pos), _p(self.k_cache),
+                                         _p(self.v_cache), lg, int(threads)))

@@ -73,6 +73,25 @@ class DeviceInfo(ctypes.Structure):
 _P = ctypes.c_void_p
 _I = ctypes.c_int32
 _Z = ctypes.c_size_t
+_F = ctypes.c_float
+
+
+class Gemma2Config(ctypes.Structure):
+    """mrml_hip_gemma2_config."""
+
+    _fields_ = [(n, ctypes.c_int32) for n in
+                ("n_layers", "dim", "n_heads", "n_kv_heads", "head_dim", "ffn_dim", "vocab", "ctx_len")] + \
+               [(n, ctypes.c_float) for n in ("rope_base", "eps", "attn_scale")] + [("tie_type", ctypes.c_int32)]
+
+
+GEMMA2_LAYER_TENSORS = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")
+GEMMA2_LAYER_NORMS = ("attn_norm", "post_attn_norm", "ffn_norm", "post_ffw_norm")
+
+
+class Gemma2Layer(ctypes.Structure):
+    """mrml_hip_gemma2_layer: device pointers of one layer."""
+
+    _fields_ = [(n, ctypes.c_void_p) for n in GEMMA2_LAYER_TENSORS + GEMMA2_LAYER_NORMS]
 
 # name -> argtypes; every function returns int status unless listed in _RESTYPE
 _SIGNATURES = {
@@ -115,6 +134,16 @@ _SIGNATURES = {
     "mrml_hip_gemv_q8_0": [_P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemv_q4_k": [_P, _P, _P, _P, _I, _I],
     "mrml_hip_argmax_f32": [_P, _P, _I, _P],
+    "mrml_hip_rms_norm": [_P, _P, _P, _P, _P, _I, _F],
+    "mrml_hip_residual_rms_norm": [_P, _P, _P, _P, _P, _P, _P, _I, _F],
+    "mrml_hip_embedding": [_P, _P, _I, _I, _P, _P, _I, _I, _F],
+    "mrml_hip_rope_table": [_P, _P, _I, _I, _F, _F],
+    "mrml_hip_rope_kv_append_f16": [_P, _P, _P, _P, _I, _P, _I, _I, _I, _F, _F, _I, _P, _I],
+    "mrml_hip_attn_decode_f16": [_P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _F, _I],
+    "mrml_hip_gemma2_create": [_P, _P, _P, _P, _P, ctypes.POINTER(_P)],
+    "mrml_hip_gemma2_destroy": [_P, _P],
+    "mrml_hip_gemma2_step": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I],
+    "mrml_hip_gemma2_activations": [_P, _P, ctypes.POINTER(_P), ctypes.POINTER(_P)],
 }
 _RESTYPE = {
     "mrml_hip_last_error": ctypes.c_char_p,
@@ -361,6 +390,119 @@ class HipDevice:
 
     def argmax_f32(self, x, n: int, out) -> None:
         self._check(self.lib.mrml_hip_argmax_f32(self.ctx, _ptr(x), n, _ptr(out)))
+
+    # ---- the rest of the token step ----------------------------------------------
+    def rms_norm(self, x, w, out, dim: int, eps: float, pack=None) -> None:
+        """CudaDevice::rms_norm (cuda.rs:2102-2180); `pack` also takes the Q8_0 pack."""
+        self._check(self.lib.mrml_hip_rms_norm(self.ctx, _ptr(x), _ptr(w), _ptr(out), _ptr(pack), dim, eps))
+
+    def residual_rms_norm(self, t, w_post, h, w_next, xn, dim: int, eps: float, pack=None) -> None:
+        self._check(self.lib.mrml_hip_residual_rms_norm(self.ctx, _ptr(t), _ptr(w_post), _ptr(h), _ptr(w_next),
+                                                        _ptr(xn), _ptr(pack), dim, eps))
+
+    def embedding(self, table, qtype: int, token: int, out, dim: int, vocab: int, scale: float,
+                  d_token=None) -> None:
+        """CudaDevice::embedding_q8_0 (cuda.rs:2625-2656) for Q4_0 or Q8_0 tables."""
+        self._check(self.lib.mrml_hip_embedding(self.ctx, _ptr(table), qtype, token, _ptr(d_token), _ptr(out),
+                                                dim, vocab, scale))
+
+    def rope_table(self, table, n_pos: int, head_dim: int, freq_base: float, freq_scale: float = 1.0) -> None:
+        """Fill a (cos, sin) table for positions < n_pos with the host C library."""
+        self._check(self.lib.mrml_hip_rope_table(self.ctx, _ptr(table), n_pos, head_dim, freq_base, freq_scale))
+
+    def rope_kv_append_f16(self, qkv, k_cache, v_cache, pos: int, n_heads: int, n_kv_heads: int, head_dim: int,
+                           freq_base: float, capacity: int, freq_scale: float = 1.0, d_pos=None, table=None,
+                           n_table: int = 0) -> None:
+        """CudaDevice::qkv_postprocess (cuda.rs:2438-2476) without head norms."""
+        self._check(self.lib.mrml_hip_rope_kv_append_f16(self.ctx, _ptr(qkv), _ptr(k_cache), _ptr(v_cache), pos,
+                                                         _ptr(d_pos), n_heads, n_kv_heads, head_dim, freq_base,
+                                                         freq_scale, capacity, _ptr(table), n_table))
+
+    def attention_causal(self, q, k_cache, v_cache, out, n_past: int, n_heads: int, n_kv_heads: int,
+                         head_dim: int, scale: float, capacity: int, pack=None, d_pos=None) -> None:
+        """CudaDevice::attention_causal (cuda.rs:2658-2697) for one token, f16 cache."""
+        self._check(self.lib.mrml_hip_attn_decode_f16(self.ctx, _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out),
+                                                      _ptr(pack), n_past, _ptr(d_pos), n_heads, n_kv_heads,
+                                                      head_dim, scale, capacity))
+
+
+class Gemma2Model:
+    """A Gemma-2-shape decoder bound to device weights (mrml_hip_gemma2_*).
+
+    ``layers`` is a list of dicts with the keys of GEMMA2_LAYER_TENSORS (backend
+    Q4_0 buffers) and GEMMA2_LAYER_NORMS (f32 buffers).  Weights are not copied;
+    keep them alive while the model is used.
+    """
+
+    def __init__(self, dev: HipDevice, cfg: Gemma2Config, tok_embd, output_norm, layers):
+        self.dev = dev
+        self.cfg = cfg
+        arr = (Gemma2Layer * cfg.n_layers)()
+        for i, L in enumerate(layers):
+            for name in GEMMA2_LAYER_TENSORS + GEMMA2_LAYER_NORMS:
+                setattr(arr[i], name, _ptr(L[name]))
+        h = ctypes.c_void_p()
+        dev._check(dev.lib.mrml_hip_gemma2_create(dev.ctx, ctypes.byref(cfg), _ptr(tok_embd), _ptr(output_norm),
+                                                  arr, ctypes.byref(h)))
+        self.handle = h.value
+
+    @classmethod
+    def from_host(cls, dev: HipDevice, model: dict) -> "Gemma2Model":
+        """Upload a model held as GGUF block bytes (the dict of synth.gemma2_model)
+        and convert every matrix to the backend layout; the model keeps the
+        device buffers alive."""
+        c = model["cfg"]
+        cfg = Gemma2Config(c["n_layers"], c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["ffn_dim"],
+                           c["vocab"], c["ctx_len"], c["rope_base"], c["eps"], c["attn_scale"],
+                           Q8_0 if model["tie_q8"] else Q4_0)
+        qd, kvd = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
+        shapes = {"wq": (qd, c["dim"]), "wk": (kvd, c["dim"]), "wv": (kvd, c["dim"]), "wo": (c["dim"], qd),
+                  "w_gate": (c["ffn_dim"], c["dim"]), "w_up": (c["ffn_dim"], c["dim"]),
+                  "w_down": (c["dim"], c["ffn_dim"])}
+        keep = []
+        layers = []
+        for L in model["layers"]:
+            d = {}
+            for name in GEMMA2_LAYER_TENSORS:
+                d[name] = HipBuffer.from_gguf(dev, L[name], Q4_0, *shapes[name])
+            for name in GEMMA2_LAYER_NORMS:
+                d[name] = HipBuffer.from_host(dev, L[name])
+            layers.append(d)
+            keep.extend(d.values())
+        table = HipBuffer.from_gguf(dev, model["tok_embd"], cfg.tie_type, c["vocab"], c["dim"])
+        out_norm = HipBuffer.from_host(dev, model["output_norm"])
+        self = cls(dev, cfg, table, out_norm, layers)
+        self.buffers = keep + [table, out_norm]
+        return self
+
+    def cache_elems(self) -> int:
+        """f16 elements of one of the two KV caches."""
+        c = self.cfg
+        return c.n_layers * c.ctx_len * c.n_kv_heads * c.head_dim
+
+    def step(self, state, k_cache, v_cache, logits=None, argmax=None, hist=None, hist_cap: int = 0,
+             prompt=None, prompt_len: int = 0) -> None:
+        """Enqueue one token step (model.rs forward_token + greedy pick); see mrml_hip_gemma2_step."""
+        self.dev._check(self.dev.lib.mrml_hip_gemma2_step(self.dev.ctx, self.handle, _ptr(state), _ptr(k_cache),
+                                                          _ptr(v_cache), _ptr(logits), _ptr(argmax), _ptr(hist),
+                                                          hist_cap, _ptr(prompt), prompt_len))
+
+    def activations(self) -> tuple[int, int]:
+        h, lg = ctypes.c_void_p(), ctypes.c_void_p()
+        self.dev._check(self.dev.lib.mrml_hip_gemma2_activations(self.dev.ctx, self.handle, ctypes.byref(h),
+                                                                 ctypes.byref(lg)))
+        return int(h.value), int(lg.value)
+
+    def close(self) -> None:
+        if self.handle and self.dev.ctx:
+            self.dev.lib.mrml_hip_gemma2_destroy(self.dev.ctx, self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class HipGraph:

@@ -1,0 +1,489 @@
+// decode.hip -- the ops that complete a batch-1 token step around the
+// matvecs: token embedding, RMSNorm (fused with Q8_0 quantisation of its
+// output and with the sandwich-norm residual add), RoPE with f16 KV append,
+// and GQA decode attention over the f16 cache.
+//
+// Every op follows the reference's operation order, so a token step is
+// bit-identical to the CPU path:
+//  * sums the reference evaluates sequentially in f32 (the RMSNorm sum of
+//    squares, ops.rs:24-79; the attention dot, softmax denominator and
+//    weighted sum of values, model.rs:1457-1590 / ops.rs:133-158) are
+//    evaluated sequentially here too: the parallel work (products, exps,
+//    loads) is spread over the workgroup, the dependent chain of adds runs
+//    in one wave;
+//  * expf and tanhf reproduce the host C library's results (libm_f32.h);
+//  * RoPE's cos/sin come from a table the host fills with its own libm
+//    (mrml_hip_rope_table); without a table the kernel evaluates powf, cosf
+//    and sinf in double and rounds once.
+// The Q8_0 packs these ops emit use the quantiser rule of quant.rs:193-228.
+//
+// Positions and tokens can be read from device memory (d_pos / d_token) so a
+// captured token step replays unchanged for every position.
+
+#include <math.h>
+
+#include "device.h"
+#include "internal.h"
+
+namespace mrml {
+
+namespace {
+
+constexpr int kMaxChunks = 4;  // float4 chunks per thread: dim <= 16 * blockDim
+constexpr int kScoreP = 64;    // cache positions per score workgroup (one per lane)
+constexpr int kAttnHD = 256;   // head_dim served by the attention kernels
+
+__device__ __forceinline__ float4 scale4(float4 a, float s) { return make_float4(a.x * s, a.y * s, a.z * s, a.w * s); }
+__device__ __forceinline__ float4 mul4(float4 a, float4 b)
+{
+    return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
+}
+__device__ __forceinline__ float4 add4(float4 a, float4 b)
+{
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+__device__ __forceinline__ float4 sq4(float4 a) { return make_float4(a.x * a.x, a.y * a.y, a.z * a.z, a.w * a.w); }
+
+// s = 0; s += v[i] for i = 0..n-1, each add rounded (v 16-byte aligned in
+// LDS).  Every lane of the calling wave runs the same chain on broadcast LDS
+// reads; a batch's reads are issued before its adds.
+__device__ float seq_sum(const float *v, int n)
+{
+    float s = 0.0f;
+    int i = 0;
+    for (; i + 32 <= n; i += 32) {
+        float4 b[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) b[k] = reinterpret_cast<const float4 *>(v + i)[k];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            s += b[k].x;
+            s += b[k].y;
+            s += b[k].z;
+            s += b[k].w;
+        }
+    }
+    for (; i < n; ++i) s += v[i];
+    return s;
+}
+
+// Sum of squares of the values held in v (chunks c = tid + k*blockDim), in
+// index order from +0: squares staged in LDS by all threads, summed by wave
+// 0, broadcast back.  `lds` holds n4*4 floats plus one.
+__device__ float block_seq_sum_sq(const float4 (&v)[kMaxChunks], int n4, float *lds)
+{
+    float4 *sq = reinterpret_cast<float4 *>(lds);
+    float *bcast = lds + n4 * 4;
+#pragma unroll
+    for (int k = 0; k < kMaxChunks; ++k) {
+        const int c = threadIdx.x + k * blockDim.x;
+        if (c < n4) sq[c] = sq4(v[k]);
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const float s = seq_sum(lds, n4 * 4);
+        if (threadIdx.x == 0) *bcast = s;
+    }
+    __syncthreads();
+    const float s = *bcast;
+    __syncthreads();  // lds is reused by the caller
+    return s;
+}
+
+// ops.rs:24-79: mean = sum/dim, scale = 1/sqrt(mean + eps) (IEEE sqrt and
+// divide: hipcc's defaults are correctly rounded).
+__device__ __forceinline__ float rms_scale(float sum_sq, int dim, float eps)
+{
+    const float mean = sum_sq / (float)dim;
+    return 1.0f / sqrtf(mean + eps);
+}
+
+// Q8_0 pack of the value chunk c (values 4c..4c+3); 8 consecutive threads
+// hold one block.  Every lane of the wave must call this.
+__device__ __forceinline__ void emit_q8(float4 v, int c, int n4, uint8_t *pack, int nb)
+{
+    uint32_t dbits;
+    int s;
+    const uint32_t q = q8_0_block8x4(v, dbits, s);
+    if (c < n4) {
+        reinterpret_cast<uint32_t *>(pack)[c] = q;
+        if ((c & 7) == 0) {
+            reinterpret_cast<float *>(pack + (size_t)nb * 32)[c >> 3] = f16_bits_to_f32(dbits);
+            reinterpret_cast<int32_t *>(pack + (size_t)nb * 36)[c >> 3] = s;
+        }
+    }
+}
+
+// out = (x * scale) * w per value (w nullable), stored to out (nullable) and
+// as a Q8_0 pack (nullable).
+__device__ __forceinline__ void norm_store(const float4 (&v)[kMaxChunks], float scale, const float *w, float *out,
+                                           uint8_t *pack, int n4)
+{
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+#pragma unroll
+    for (int k = 0; k < kMaxChunks; ++k) {
+        if (k * (int)blockDim.x >= n4) break;  // uniform
+        const int c = threadIdx.x + k * blockDim.x;
+        float4 o = scale4(v[k], scale);
+        if (w) o = mul4(o, w4[c < n4 ? c : 0]);
+        if (out && c < n4) reinterpret_cast<float4 *>(out)[c] = o;
+        if (pack) emit_q8(o, c, n4, pack, n4 >> 3);
+    }
+}
+
+// out = rms_norm(x, w) (CudaDevice::rms_norm, cuda.rs:2102-2180; CPU
+// ops.rs:24-79), optionally also as a Q8_0 pack.  One workgroup.
+__global__ __launch_bounds__(1024) void rms_norm_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                        float eps, float *__restrict__ out,
+                                                        uint8_t *__restrict__ pack, int dim)
+{
+    extern __shared__ __align__(16) float lds[];
+    const int n4 = dim >> 2;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    float4 v[kMaxChunks];
+#pragma unroll
+    for (int k = 0; k < kMaxChunks; ++k) {
+        const int c = threadIdx.x + k * blockDim.x;
+        v[k] = c < n4 ? x4[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    norm_store(v, rms_scale(block_seq_sum_sq(v, n4, lds), dim, eps), w, out, pack, n4);
+}
+
+// Sandwich-norm residual of a Gemma-2 block followed by the next block's
+// pre-norm (the per-layer order of model.rs:1185-2260):
+//   h  = h + rms_norm(t, w_post)
+//   xn = rms_norm(h, w_next)      -> xn (nullable) and its Q8_0 pack (nullable)
+__global__ __launch_bounds__(1024) void residual_rms_norm_kernel(const float *__restrict__ t,
+                                                                 const float *__restrict__ w_post,
+                                                                 float *__restrict__ h,
+                                                                 const float *__restrict__ w_next, float eps,
+                                                                 float *__restrict__ xn, uint8_t *__restrict__ pack,
+                                                                 int dim)
+{
+    extern __shared__ __align__(16) float lds[];
+    const int n4 = dim >> 2;
+    const float4 *t4 = reinterpret_cast<const float4 *>(t);
+    float4 *h4 = reinterpret_cast<float4 *>(h);
+    const float4 *wp4 = reinterpret_cast<const float4 *>(w_post);
+    float4 v[kMaxChunks];
+#pragma unroll
+    for (int k = 0; k < kMaxChunks; ++k) {
+        const int c = threadIdx.x + k * blockDim.x;
+        v[k] = c < n4 ? t4[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    const float s1 = rms_scale(block_seq_sum_sq(v, n4, lds), dim, eps);
+#pragma unroll
+    for (int k = 0; k < kMaxChunks; ++k) {
+        const int c = threadIdx.x + k * blockDim.x;
+        const int cc = c < n4 ? c : 0;
+        float4 tn = scale4(v[k], s1);
+        if (w_post) tn = mul4(tn, wp4[cc]);
+        const float4 hn = add4(h4[cc], tn);
+        if (c < n4) h4[c] = hn;
+        v[k] = c < n4 ? hn : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    if (!xn && !pack) return;
+    norm_store(v, rms_scale(block_seq_sum_sq(v, n4, lds), dim, eps), w_next, xn, pack, n4);
+}
+
+// Token embedding (CudaDevice::embedding_q8_0, cuda.rs:2625-2656; CPU
+// model.rs:1164-1182 with the sqrt(dim) scale of model.rs:1201): h = the
+// dequantised table row (backend Q4_0 or Q8_0 layout) times `scale`, each
+// value (q * d) * scale.  With w_norm or pack set it also writes
+// rms_norm(h, w_norm) as f32 (xn) and/or as a Q8_0 pack -- the first layer's
+// pre-norm.
+__global__ __launch_bounds__(1024) void embedding_kernel(const uint8_t *__restrict__ table, int type,
+                                                         const int32_t *__restrict__ d_token, int token, float scale,
+                                                         float *__restrict__ h, const float *__restrict__ w_norm,
+                                                         float eps, float *__restrict__ xn,
+                                                         uint8_t *__restrict__ pack, int dim, int vocab)
+{
+    extern __shared__ __align__(16) float lds[];
+    int tok = d_token ? *d_token : token;
+    tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
+    const int n4 = dim >> 2, nb = dim >> 5;
+    const size_t nblk = (size_t)vocab * nb, row = (size_t)tok * nb;
+    float4 v[kMaxChunks];
+#pragma unroll
+    for (int k = 0; k < kMaxChunks; ++k) {
+        const int c_raw = threadIdx.x + k * blockDim.x;
+        const int c = c_raw < n4 ? c_raw : n4 - 1;
+        const int b = c >> 3, p = (c & 7) * 4;  // block, first value index within it
+        float q[4], d;
+        if (type == MRML_HIP_Q4_0) {
+            const uint32_t word = *reinterpret_cast<const uint32_t *>(table + (row + b) * 16 + (p & 15));
+            const int shift = p < 16 ? 0 : 4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[e] = (float)((int)((word >> (8 * e + shift)) & 15u) - 8);
+            d = f16_bits_to_f32(reinterpret_cast<const uint16_t *>(table + nblk * 16)[row + b]);
+        } else {
+            const uint32_t word = *reinterpret_cast<const uint32_t *>(table + (row + b) * 32 + p);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[e] = (float)(int8_t)(word >> (8 * e));
+            d = f16_bits_to_f32(reinterpret_cast<const uint16_t *>(table + nblk * 32)[row + b]);
+        }
+        const float4 o = make_float4((q[0] * d) * scale, (q[1] * d) * scale, (q[2] * d) * scale, (q[3] * d) * scale);
+        if (c_raw < n4) reinterpret_cast<float4 *>(h)[c_raw] = o;
+        v[k] = c_raw < n4 ? o : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    if (!xn && !pack) return;
+    norm_store(v, rms_scale(block_seq_sum_sq(v, n4, lds), dim, eps), w_norm, xn, pack, n4);
+}
+
+// RoPE (NeoX half split, ops.rs:185-208) on the q and k heads of a stacked
+// [q | k | v] vector, then k and v appended to the f16 caches at the cache
+// row of `pos` (round to nearest even, as the reference CUDA path stores its
+// cache, kernels.rs:1300-1322).  Cache layout [capacity][n_kv_heads][head_dim];
+// a position past the capacity wraps (kernels.rs:1307-1313).  Rotated q (and
+// k) are written back into qkv.  cos/sin come from `table` ([n_table][half]
+// pairs) when pos < n_table.  Grid: n_heads + 2*n_kv_heads workgroups of
+// head_dim/2 threads.
+__global__ __launch_bounds__(512) void rope_kv_f16_kernel(float *__restrict__ qkv, uint16_t *__restrict__ k_cache,
+                                                          uint16_t *__restrict__ v_cache,
+                                                          const int32_t *__restrict__ d_pos, int pos_arg,
+                                                          int n_heads, int n_kv_heads, int head_dim, float base,
+                                                          float freq_scale, int capacity,
+                                                          const float *__restrict__ table, int n_table)
+{
+    const int pos = d_pos ? *d_pos : pos_arg;
+    const int half = head_dim >> 1, i = threadIdx.x, g = blockIdx.x;
+    const size_t kv_dim = (size_t)n_kv_heads * head_dim;
+    const size_t cache_row = (size_t)(capacity > 0 ? pos % capacity : pos) * kv_dim;
+    if (g < n_heads + n_kv_heads) {
+        float c, s;
+        if (table && pos >= 0 && pos < n_table) {
+            const float2 cs = reinterpret_cast<const float2 *>(table)[(size_t)pos * half + i];
+            c = cs.x;
+            s = cs.y;
+        } else {
+            // the reference's f32 theta; powf, cosf, sinf in double, rounded once
+            const float expo = (float)(2 * i) / (float)head_dim;
+            const float freq = (float)pow((double)base, (double)expo);
+            const float theta = (float)pos * freq_scale / freq;
+            c = (float)cos((double)theta);
+            s = (float)sin((double)theta);
+        }
+        float *v = qkv + (size_t)g * head_dim;
+        const float v0 = v[i], v1 = v[i + half];
+        const float r0 = v0 * c - v1 * s;
+        const float r1 = v0 * s + v1 * c;
+        v[i] = r0;
+        v[i + half] = r1;
+        if (g >= n_heads) {
+            uint16_t *dst = k_cache + cache_row + (size_t)(g - n_heads) * head_dim;
+            dst[i] = f32_to_f16_rne(r0);
+            dst[i + half] = f32_to_f16_rne(r1);
+        }
+    } else {
+        const int vh = g - n_heads - n_kv_heads;
+        const float *src = qkv + (size_t)(n_heads + n_kv_heads) * head_dim + (size_t)vh * head_dim;
+        uint16_t *dst = v_cache + cache_row + (size_t)vh * head_dim;
+        dst[i] = f32_to_f16_rne(src[i]);
+        dst[i + half] = f32_to_f16_rne(src[i + half]);
+    }
+}
+
+// ---- GQA decode attention (model.rs:1457-1590, kv_cache.rs:72-124,
+// ops.rs:133-158; GPU kernels.rs:1374-1561) --------------------------------------
+//
+// The window is the last min(n_past + 1, capacity) cache positions, oldest
+// first (cache row = position % capacity).  Query head h reads kv head
+// h / (n_heads / n_kv_heads).
+
+__device__ __forceinline__ size_t cache_row_of(int t, int capacity) { return (size_t)(capacity > 0 ? t % capacity : t); }
+
+__device__ __forceinline__ void attn_window(const int32_t *d_pos, int n_past_arg, int capacity, int &window,
+                                            int &start)
+{
+    const int n_past = d_pos ? *d_pos : n_past_arg;
+    const int count = n_past + 1;
+    window = (capacity > 0 && count > capacity) ? capacity : count;
+    start = count - window;
+}
+
+// Scores: score[h][p] = (sum_d q_h[d] * k_{start+p}[d], from -0.0 in d
+// order) * scale -- one lane per position, one chain per query head of the
+// group.  Grid (ceil(capacity/64), n_kv_heads) x 64 threads; workgroups past
+// the window exit at once.
+__global__ __launch_bounds__(64) void attn_scores_kernel(const float *__restrict__ q,
+                                                         const uint16_t *__restrict__ k_cache,
+                                                         const int32_t *__restrict__ d_pos, int n_past_arg,
+                                                         int n_heads, int n_kv_heads, float scale, int capacity,
+                                                         float *__restrict__ scores)
+{
+    constexpr int HD = kAttnHD;
+    __shared__ float q_s[8][HD];
+    int window, start;
+    attn_window(d_pos, n_past_arg, capacity, window, start);
+    const int p0 = blockIdx.x * kScoreP;
+    if (p0 >= window) return;
+    const int kvh = blockIdx.y, G = n_heads / n_kv_heads, lane = threadIdx.x;
+    for (int i = lane; i < G * HD; i += 64) q_s[i / HD][i % HD] = q[(size_t)kvh * G * HD + i];
+    __syncthreads();
+    const int p = p0 + lane;
+    const bool valid = p < window;
+    const size_t kv_dim = (size_t)n_kv_heads * HD;
+    const uint4 *krow =
+        reinterpret_cast<const uint4 *>(k_cache + cache_row_of(start + (valid ? p : 0), capacity) * kv_dim +
+                                        (size_t)kvh * HD);
+    float dot[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) dot[g] = -0.0f;
+    for (int d0 = 0; d0 < HD; d0 += 32) {
+        uint4 kw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kw[e] = krow[d0 / 8 + e];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t wd[4] = {kw[e].x, kw[e].y, kw[e].z, kw[e].w};
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float kf = f16_bits_to_f32((wd[u >> 1] >> (16 * (u & 1))) & 0xffffu);
+                const int d = d0 + e * 8 + u;
+#pragma unroll
+                for (int g = 0; g < 8; ++g)
+                    if (g < G) dot[g] += q_s[g][d] * kf;
+            }
+        }
+    }
+    if (valid)
+        for (int g = 0; g < G; ++g) scores[(size_t)(kvh * G + g) * capacity + p] = dot[g] * scale;
+}
+
+// Softmax and weighted values for query head h (one workgroup of head_dim
+// threads):  max over the window; e_p = expf(score_p - max); sum = 0 + e_0
+// + e_1 + ... in order; p_p = e_p * (1/sum); out[d] = 0 + p_0 v_0[d] + p_1
+// v_1[d] + ... in order.  Writes out (nullable) and the Q8_0 pack of the
+// n_heads*head_dim output (nullable).  LDS: capacity floats plus one.
+__global__ __launch_bounds__(256) void attn_softmax_v_kernel(const float *__restrict__ scores,
+                                                             const uint16_t *__restrict__ v_cache,
+                                                             const int32_t *__restrict__ d_pos, int n_past_arg,
+                                                             int n_heads, int n_kv_heads, int capacity, int expf_fused,
+                                                             float *__restrict__ out, uint8_t *__restrict__ pack)
+{
+    constexpr int HD = kAttnHD;
+    extern __shared__ __align__(16) float e_s[];
+    __shared__ float red[4];
+    int window, start;
+    attn_window(d_pos, n_past_arg, capacity, window, start);
+    const int h = blockIdx.x, d = threadIdx.x, G = n_heads / n_kv_heads, kvh = h / G;
+    const float *sc = scores + (size_t)h * capacity;
+
+    float mx = -INFINITY;
+    for (int p = d; p < window; p += HD) mx = fmaxf(mx, sc[p]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if ((d & 63) == 0) red[d >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int p = d; p < window; p += HD) e_s[p] = mrml_libm::expf(sc[p] - mx, expf_fused != 0);
+    __syncthreads();
+    float *bcast = e_s + capacity;
+    if (d < 64) {
+        const float sum = seq_sum(e_s, window);
+        if (d == 0) *bcast = sum;
+    }
+    __syncthreads();
+    const float sum = *bcast;
+    if (sum > 0.0f) {
+        const float inv = 1.0f / sum;
+        for (int p = d; p < window; p += HD) e_s[p] = e_s[p] * inv;
+    }
+    __syncthreads();
+
+    const size_t kv_dim = (size_t)n_kv_heads * HD;
+    const uint16_t *vcol = v_cache + (size_t)kvh * HD + d;
+    float acc = 0.0f;
+    int p = 0;
+    for (; p + 8 <= window; p += 8) {
+        uint16_t vb[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) vb[u] = vcol[cache_row_of(start + p + u, capacity) * kv_dim];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += e_s[p + u] * f16_bits_to_f32(vb[u]);
+    }
+    for (; p < window; ++p) acc += e_s[p] * f16_bits_to_f32(vcol[cache_row_of(start + p, capacity) * kv_dim]);
+
+    if (out) out[(size_t)h * HD + d] = acc;
+    if (pack) {
+        uint32_t dbits;
+        int s;
+        const int qv = q8_0_block32(acc, dbits, s);
+        const int nb = n_heads * HD / 32, blk = (h * HD + d) >> 5;
+        pack[(size_t)h * HD + d] = (uint8_t)(int8_t)qv;
+        if ((d & 31) == 0) {
+            reinterpret_cast<float *>(pack + (size_t)nb * 32)[blk] = f16_bits_to_f32(dbits);
+            reinterpret_cast<int32_t *>(pack + (size_t)nb * 36)[blk] = s;
+        }
+    }
+}
+
+inline int norm_threads(int dim)
+{
+    const int n4 = dim / 4;
+    int t = (n4 + kMaxChunks - 1) / kMaxChunks;
+    t = (t + 63) / 64 * 64;
+    return t < 64 ? 64 : t;
+}
+
+inline size_t norm_lds(int dim) { return (size_t)dim * sizeof(float) + 16; }
+
+}  // namespace
+
+bool norm_dim_ok(int dim) { return dim > 0 && dim % 32 == 0 && dim <= 16 * 1024; }
+
+int launch_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float eps, float *out, void *pack, int dim)
+{
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, x, w, eps, out,
+                       (uint8_t *)pack, dim);
+    return check_launch(ctx, "rms_norm_kernel");
+}
+
+int launch_residual_rms_norm(mrml_hip_ctx *ctx, const float *t, const float *w_post, float *h, const float *w_next,
+                             float eps, float *xn, void *pack, int dim)
+{
+    hipLaunchKernelGGL(residual_rms_norm_kernel, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, t,
+                       w_post, h, w_next, eps, xn, (uint8_t *)pack, dim);
+    return check_launch(ctx, "residual_rms_norm_kernel");
+}
+
+int launch_embedding(mrml_hip_ctx *ctx, const void *table, int type, const int32_t *d_token, int token, float scale,
+                     float *h, const float *w_norm, float eps, float *xn, void *pack, int dim, int vocab)
+{
+    hipLaunchKernelGGL(embedding_kernel, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream,
+                       (const uint8_t *)table, type, d_token, token, scale, h, w_norm, eps, xn, (uint8_t *)pack, dim,
+                       vocab);
+    return check_launch(ctx, "embedding_kernel");
+}
+
+int launch_rope_kv_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache, uint16_t *v_cache, const int32_t *d_pos,
+                       int pos, int n_heads, int n_kv_heads, int head_dim, float base, float freq_scale, int capacity,
+                       const float *table, int n_table)
+{
+    hipLaunchKernelGGL(rope_kv_f16_kernel, dim3(n_heads + 2 * n_kv_heads), dim3(head_dim / 2), 0, ctx->stream, qkv,
+                       k_cache, v_cache, d_pos, pos, n_heads, n_kv_heads, head_dim, base, freq_scale, capacity, table,
+                       n_table);
+    return check_launch(ctx, "rope_kv_f16_kernel");
+}
+
+int attn_head_dim() { return kAttnHD; }
+int attn_max_capacity() { return 16000; }  // the window's softmax weights live in LDS
+
+size_t attn_scratch_bytes(int n_heads, int capacity) { return (size_t)n_heads * capacity * sizeof(float); }
+
+int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                           float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
+                           float scale, int capacity, void *scratch)
+{
+    float *scores = reinterpret_cast<float *>(scratch);
+    const dim3 sgrid((capacity + kScoreP - 1) / kScoreP, n_kv_heads);
+    hipLaunchKernelGGL(attn_scores_kernel, sgrid, dim3(64), 0, ctx->stream, q, k_cache, d_pos, n_past, n_heads,
+                       n_kv_heads, scale, capacity, scores);
+    if (int rc = check_launch(ctx, "attn_scores_kernel")) return rc;
+    hipLaunchKernelGGL(attn_softmax_v_kernel, dim3(n_heads), dim3(kAttnHD), (size_t)capacity * sizeof(float) + 16,
+                       ctx->stream, scores, v_cache, d_pos, n_past, n_heads, n_kv_heads, capacity,
+                       (int)host_expf_fused(), out, (uint8_t *)pack);
+    return check_launch(ctx, "attn_softmax_v_kernel");
+}
+
+}  // namespace mrml

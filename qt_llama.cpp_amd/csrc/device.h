@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <cstdint>
 
+#include "libm_f32.h"
+
 namespace mrml {
 
 // Backend activation pack for n = 32*nb values (written by the quantiser):
@@ -186,11 +188,12 @@ __device__ __forceinline__ uint32_t q8_0_block8x4(float4 v, uint32_t &dbits, int
 }
 
 // ops.rs:101-104 evaluated in the same order (contraction is off):
-// (0.5*x) * (1 + tanh(k*(x + ((0.044715*x)*x)*x))).
+// (0.5*x) * (1 + tanh(k*(x + ((0.044715*x)*x)*x))), with the host C
+// library's tanhf reproduced bit for bit (libm_f32.h).
 __device__ __forceinline__ float gelu_tanh(float x)
 {
     const float k = 0.7978845608f;
-    return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
+    return 0.5f * x * (1.0f + mrml_libm::tanhf(k * (x + 0.044715f * x * x * x)));
 }
 
 }  // namespace mrml

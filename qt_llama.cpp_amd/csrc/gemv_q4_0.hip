@@ -693,6 +693,28 @@ int launch_gemv_q4_0_geglu(mrml_hip_ctx *ctx, const void *wg, const void *wu, co
 // f32 input, optional f32 output, optional Q8_0 pack of the output (for the
 // next projection).  One launch when the shape has a fixed instance and
 // rows % 32 == 0; otherwise quantise / run / quantise separately.
+int launch_gemv_q4_0_geglu_emit(mrml_hip_ctx *ctx, const void *wg, const void *wu, const void *xpack, float *act,
+                                void *act_pack, int32_t rows, int32_t cols)
+{
+    const int nb = cols / 32;
+    if (int rc = check_even(ctx, rows, nb)) return rc;
+    if (fold16_shape(nb) && rows % 32 == 0) {
+        MRML_FOLD16_NB(nb, {
+            hipLaunchKernelGGL((gemv_q4_0_geglu_kernel<NB, 8, false, true>), dim3(rows / 32), dim3(64 * 9),
+                               pack_lds(NB) + 32 * sizeof(float), ctx->stream, (const uint8_t *)wg,
+                               (const uint8_t *)wu, xpack, act, (uint8_t *)act_pack, rows);
+        });
+        return check_launch(ctx, "gemv_q4_0_geglu_kernel");
+    }
+    float *out = act;
+    if (!out) {
+        out = (float *)workspace(ctx, (size_t)rows * sizeof(float));
+        if (!out) return MRML_HIP_E_ALLOC;
+    }
+    if (int rc = launch_gemv_q4_0_geglu(ctx, wg, wu, xpack, out, rows, cols)) return rc;
+    return launch_quantize_q8_0(ctx, out, nullptr, act_pack, rows);
+}
+
 int launch_gemv_q4_0_geglu_x(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *x, float *act,
                              void *act_pack, int32_t rows, int32_t cols)
 {

@@ -84,7 +84,7 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q8_0_kernel(const uint8
             for (int k = 0; k < 16; ++k) s = fold16(s, t);
         }
     }
-    if (j == 15 && row_raw < rows) y[row_raw] = softcap ? 30.0f * tanhf(s / 30.0f) : s;
+    if (j == 15 && row_raw < rows) y[row_raw] = softcap ? 30.0f * mrml_libm::tanhf(s / 30.0f) : s;
 }
 
 // ---- Q4_K (build-defined semantics over the GGUF super-block) ---------------
@@ -245,15 +245,30 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *__rest
     if (threadIdx.x == 0) { pv[blockIdx.x] = v; pi[blockIdx.x] = i; }
 }
 
+// With `state` = {token, pos} (device), also advances a decode loop kept on
+// the device: hist[pos] = the argmax (when pos < hist_cap); pos += 1; token =
+// prompt[pos] while pos < prompt_len (prefill), else the argmax.
 __global__ __launch_bounds__(256) void argmax_final_kernel(const float *__restrict__ pv, const int *__restrict__ pi,
-                                                           int parts, int32_t *__restrict__ out)
+                                                           int parts, int32_t *__restrict__ out,
+                                                           int32_t *__restrict__ state, int32_t *__restrict__ hist,
+                                                           int hist_cap, const int32_t *__restrict__ prompt,
+                                                           int prompt_len)
 {
     float v = __builtin_nanf("");
     int i = 0x7fffffff;
     for (int k = threadIdx.x; k < parts; k += blockDim.x)
         if (better(pv[k], pi[k], v, i)) { v = pv[k]; i = pi[k]; }
     block_best(v, i);
-    if (threadIdx.x == 0) *out = i;
+    if (threadIdx.x == 0) {
+        if (out) *out = i;
+        if (state) {
+            const int cur = state[1];
+            if (hist && cur >= 0 && cur < hist_cap) hist[cur] = i;
+            const int pos = cur + 1;
+            state[0] = (prompt && pos < prompt_len) ? prompt[pos] : i;
+            state[1] = pos;
+        }
+    }
 }
 
 inline int waves_for(int rows) { return rows >= 8192 ? 4 : (rows >= 2048 ? 2 : 1); }
@@ -319,19 +334,31 @@ int launch_gemv_q4_k(mrml_hip_ctx *ctx, const void *w, const void *xpack, float 
     return check_launch(ctx, "gemv_q4_k_kernel");
 }
 
-int launch_argmax_f32(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *out)
+int argmax_parts(int32_t n)
 {
-    int parts = (n + 2047) / 2048;
-    if (parts > 1024) parts = 1024;
-    uint8_t *ws = (uint8_t *)workspace(ctx, (size_t)parts * 8);
-    if (!ws) return MRML_HIP_E_ALLOC;
-    float *pv = reinterpret_cast<float *>(ws);
-    int *pi = reinterpret_cast<int *>(ws + (size_t)parts * 4);
+    const int parts = (n + 2047) / 2048;
+    return parts > 1024 ? 1024 : parts;
+}
+
+int launch_argmax_step(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *out, void *scratch, int32_t *state,
+                       int32_t *hist, int hist_cap, const int32_t *prompt, int prompt_len)
+{
+    const int parts = argmax_parts(n);
+    float *pv = reinterpret_cast<float *>(scratch);
+    int *pi = reinterpret_cast<int *>(reinterpret_cast<uint8_t *>(scratch) + (size_t)parts * 4);
     hipLaunchKernelGGL(argmax_partial_kernel, dim3(parts), dim3(256), 0, ctx->stream, x, n, pv, pi);
     int rc = check_launch(ctx, "argmax_partial_kernel");
     if (rc) return rc;
-    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, ctx->stream, pv, pi, parts, out);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, ctx->stream, pv, pi, parts, out, state, hist,
+                       hist_cap, prompt, prompt_len);
     return check_launch(ctx, "argmax_final_kernel");
+}
+
+int launch_argmax_f32(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *out)
+{
+    void *ws = workspace(ctx, (size_t)argmax_parts(n) * 8);
+    if (!ws) return MRML_HIP_E_ALLOC;
+    return launch_argmax_step(ctx, x, n, out, ws, nullptr, nullptr, 0, nullptr, 0);
 }
 
 }  // namespace mrml

@@ -62,5 +62,53 @@ int launch_gemv_q8_0(mrml_hip_ctx *ctx, const void *w, const void *xpack, float 
 int launch_gemv_q4_k(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y,
                      int32_t rows, int32_t cols);
 int launch_argmax_f32(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *out);
+// GeGLU over an activation pack that also writes the Q8_0 pack of its rows
+// outputs (act nullable).
+int launch_gemv_q4_0_geglu_emit(mrml_hip_ctx *ctx, const void *wg, const void *wu, const void *xpack, float *act,
+                                void *act_pack, int32_t rows, int32_t cols);
+
+// Argmax whose final pass can also advance a device-side decode loop
+// (state = {token, pos}); scratch holds argmax_parts(n) * 8 bytes.
+int argmax_parts(int32_t n);
+int launch_argmax_step(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *out, void *scratch, int32_t *state,
+                       int32_t *hist, int hist_cap, const int32_t *prompt, int prompt_len);
+
+// ---- decode-step ops (decode.hip) --------------------------------------------
+bool norm_dim_ok(int dim);
+int launch_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float eps, float *out, void *pack, int dim);
+int launch_residual_rms_norm(mrml_hip_ctx *ctx, const float *t, const float *w_post, float *h, const float *w_next,
+                             float eps, float *xn, void *pack, int dim);
+int launch_embedding(mrml_hip_ctx *ctx, const void *table, int type, const int32_t *d_token, int token, float scale,
+                     float *h, const float *w_norm, float eps, float *xn, void *pack, int dim, int vocab);
+int launch_rope_kv_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache, uint16_t *v_cache, const int32_t *d_pos,
+                       int pos, int n_heads, int n_kv_heads, int head_dim, float base, float freq_scale, int capacity,
+                       const float *table, int n_table);
+int attn_head_dim();
+int attn_max_capacity();
+size_t attn_scratch_bytes(int n_heads, int capacity);
+int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                           float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
+                           float scale, int capacity, void *scratch);
+
+// Which form of the C library's expf the host runs (glibc picks its FMA build
+// on x86-64 CPUs with FMA and AVX2); the device reproduces the same one.
+bool host_expf_fused();
+// RoPE cos/sin table [n_pos][head_dim/2] of (cos, sin) pairs computed with the
+// host C library (the functions the reference calls), uploaded to d_table.
+int fill_rope_table(mrml_hip_ctx *ctx, float *d_table, int n_pos, int head_dim, float base, float freq_scale);
 
 }  // namespace mrml
+
+// Argument guards of the extern "C" entry points: a null context is
+// E_INVALID; every entry point first makes the context's device current.
+#define CTX_GUARD(ctx)                                      \
+    do {                                                    \
+        if (!(ctx)) return MRML_HIP_E_INVALID;              \
+        int rc_ = ::mrml::enter(ctx);                       \
+        if (rc_) return rc_;                                \
+    } while (0)
+
+#define REQUIRE(ctx, cond, ...)                                                     \
+    do {                                                                            \
+        if (!(cond)) return ::mrml::fail((ctx), MRML_HIP_E_INVALID, __VA_ARGS__);   \
+    } while (0)

@@ -1,0 +1,194 @@
+// libm_f32.h -- f32 tanh and exp with the exact results of the C library the
+// reference links.
+//
+// The reference's numerics go through crates/mrml-math/src/lib.rs, which
+// binds glibc's tanhf, expf, sinf, cosf, powf and sqrtf.  A token step only
+// reproduces the CPU path bit for bit if these return the same bits on the
+// GPU, and glibc 2.35 is not correctly rounded (tanhf differs from the
+// correctly rounded value on ~20% of inputs, expf on ~0.07%), so the device
+// code evaluates the same published algorithms, operation for operation:
+//
+//  * tanhf: the Sun fdlibm algorithm (s_tanhf.c / s_expm1f.c, freely
+//    distributable): tanh via expm1 of 2|x|, expm1 by reduction
+//    x = k ln2 + r and a rational approximation of r in float arithmetic.
+//  * expf: the table-driven algorithm of Szabolcs Nagy (Arm
+//    optimized-routines, used by glibc since 2.27): k = round(x N / ln2),
+//    2^(k/N) from a 32-entry table of doubles and a cubic in double.  glibc
+//    selects a build compiled with FMA on x86-64 CPUs that have FMA and AVX2,
+//    in which the reduction r = x N/ln2 - k and the three polynomial steps
+//    are fused multiply-adds; `fused` picks that form.
+//
+// sinf/cosf/powf are not here: RoPE reads a table computed once on the host
+// by the host's own libm.  sqrtf and division are IEEE operations on both.
+//
+// Every function is usable from host code (checked against glibc over the
+// float range) and device code.  Compile with contraction off: each
+// product and sum must round separately unless fused on purpose.
+#pragma once
+
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define MRML_HD __host__ __device__ __forceinline__
+#else
+#define MRML_HD static inline
+#endif
+
+namespace mrml_libm {
+
+MRML_HD uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+MRML_HD float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+MRML_HD uint64_t d2u(double d) { return __builtin_bit_cast(uint64_t, d); }
+MRML_HD double u2d(uint64_t u) { return __builtin_bit_cast(double, u); }
+
+// ---- expm1f / tanhf (fdlibm) --------------------------------------------------
+
+MRML_HD float expm1f(float x)
+{
+    const float ln2_hi = 6.9313812256e-01f;   // 0x3f317180
+    const float ln2_lo = 9.0580006145e-06f;   // 0x3717f7d1
+    const float invln2 = 1.4426950216e+00f;   // 0x3fb8aa3b
+    const float Q1 = -3.3333335072e-02f, Q2 = 1.5873016091e-03f, Q3 = -7.9365076090e-05f,
+                Q4 = 4.0082177293e-06f, Q5 = -2.0109921195e-07f;
+    uint32_t hx = f2u(x);
+    const uint32_t xsb = hx & 0x80000000u;
+    hx &= 0x7fffffffu;
+    if (hx >= 0x4195b844u) {             // |x| >= 27 ln2
+        if (hx >= 0x42b17218u) {         // |x| >= 88.72
+            if (hx > 0x7f800000u) return x + x;
+            if (hx == 0x7f800000u) return xsb == 0 ? x : -1.0f;
+            if (x > 8.8721679688e+01f) return __builtin_inff();
+        }
+        if (xsb != 0) return -1.0f;      // x < -27 ln2
+    }
+    float hi, lo, c = 0.0f;
+    int32_t k;
+    if (hx > 0x3eb17218u) {              // |x| > 0.5 ln2
+        if (hx < 0x3f851592u) {          // and |x| < 1.5 ln2
+            if (xsb == 0) { hi = x - ln2_hi; lo = ln2_lo; k = 1; }
+            else          { hi = x + ln2_hi; lo = -ln2_lo; k = -1; }
+        } else {
+            k = (int32_t)(invln2 * x + (xsb == 0 ? 0.5f : -0.5f));
+            const float t = (float)k;
+            hi = x - t * ln2_hi;         // exact
+            lo = t * ln2_lo;
+        }
+        x = hi - lo;
+        c = (hi - x) - lo;
+    } else if (hx < 0x33000000u) {       // |x| < 2^-25
+        const float t = 1.0f + x;
+        return x - (t - (1.0f + x));
+    } else {
+        k = 0;
+    }
+    const float hfx = 0.5f * x;
+    const float hxs = x * hfx;
+    const float r1 = 1.0f + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
+    float t = 3.0f - r1 * hfx;
+    float e = hxs * ((r1 - t) / (6.0f - x * t));
+    if (k == 0) return x - (x * e - hxs);
+    e = (x * (e - c) - c);
+    e -= hxs;
+    if (k == -1) return 0.5f * (x - e) - 0.5f;
+    if (k == 1) {
+        if (x < -0.25f) return -2.0f * (e - (x + 0.5f));
+        return 1.0f + 2.0f * (x - e);
+    }
+    if (k <= -2 || k > 56) {             // exp(x) - 1 directly
+        float y = 1.0f - (e - x);
+        y = u2f(f2u(y) + ((uint32_t)k << 23));
+        return y - 1.0f;
+    }
+    float y;
+    if (k < 23) {
+        t = u2f(0x3f800000u - (0x1000000u >> k));   // 1 - 2^-k
+        y = t - (e - x);
+        y = u2f(f2u(y) + ((uint32_t)k << 23));
+    } else {
+        t = u2f((uint32_t)(0x7f - k) << 23);        // 2^-k
+        y = x - (e + t);
+        y += 1.0f;
+        y = u2f(f2u(y) + ((uint32_t)k << 23));
+    }
+    return y;
+}
+
+MRML_HD float tanhf(float x)
+{
+    const uint32_t jx = f2u(x), ix = jx & 0x7fffffffu;
+    if (ix >= 0x7f800000u) return (jx >> 31) == 0 ? 1.0f / x + 1.0f : 1.0f / x - 1.0f;  // +-1, NaN
+    float z;
+    if (ix < 0x41b00000u) {              // |x| < 22
+        if (ix == 0) return x;
+        if (ix < 0x24000000u) return x * (1.0f + x);   // |x| < 2^-55
+        const float ax = u2f(ix);
+        if (ix >= 0x3f800000u) {         // |x| >= 1
+            const float t = expm1f(2.0f * ax);
+            z = 1.0f - 2.0f / (t + 2.0f);
+        } else {
+            const float t = expm1f(-2.0f * ax);
+            z = -t / (t + 2.0f);
+        }
+    } else {
+        z = 1.0f;                        // 1 - tiny rounds to 1
+    }
+    return (jx >> 31) == 0 ? z : -z;
+}
+
+// ---- expf (Arm optimized-routines algorithm) -------------------------------------
+
+// T[i] = bits(2^(i/32)) - (i << 47): the correctly rounded doubles 2^(i/32)
+// with the table index pre-subtracted from the exponent field.
+struct ExpfTable {
+    uint64_t t[32];
+};
+
+MRML_HD float expf(float x, bool fused)
+{
+    constexpr ExpfTable T = {{
+        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+    }};
+    const double N = 32.0;
+    const double invln2N = 0x1.71547652b82fep+0 * N;
+    const double shift = 0x1.8p+52;
+    const double C0 = 0x1.c6af84b912394p-5 / N / N / N, C1 = 0x1.ebfce50fac4f3p-3 / N / N,
+                 C2 = 0x1.62e42ff0c52d6p-1 / N;
+    const uint32_t abstop = (f2u(x) >> 20) & 0x7ffu;
+    if (abstop >= (f2u(88.0f) >> 20)) {
+        if (f2u(x) == f2u(-__builtin_inff())) return 0.0f;
+        if (abstop >= (f2u(__builtin_inff()) >> 20)) return x + x;
+        if (x > 0x1.62e42ep6f) return __builtin_inff();
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double xd = (double)x;
+    const double z = invln2N * xd;
+    double kd = z + shift;
+    const uint64_t ki = d2u(kd);
+    kd -= shift;
+    // The FMA build also fuses the reduction r = x N/ln2 - k.
+    const double r = fused ? __builtin_fma(invln2N, xd, -kd) : z - kd;
+    uint64_t t = T.t[ki % 32];
+    t += ki << 47;
+    const double s = u2d(t);
+    const double r2 = r * r;
+    double y;
+    if (fused) {
+        const double p = __builtin_fma(C0, r, C1);
+        y = __builtin_fma(C2, r, 1.0);
+        y = __builtin_fma(p, r2, y);
+    } else {
+        const double p = C0 * r + C1;
+        y = C2 * r + 1.0;
+        y = p * r2 + y;
+    }
+    return (float)(y * s);
+}
+
+}  // namespace mrml_libm

@@ -1,0 +1,280 @@
+// model.hip -- C ABI of the decode-step ops and the Gemma-2-shape token step.
+//
+// The reference composes a token step in model.rs (forward_token,
+// model.rs:1185-2260; greedy selection model.rs:2833-2907) from CudaDevice
+// calls.  mrml_hip_gemma2_step enqueues the same composition on the
+// context's stream, reading the token and position from device memory and
+// advancing them in its last kernel, so one captured graph of a step replays
+// for every prompt and generated token without a host round trip.
+//
+// Per layer (9 launches):
+//   qkv      = [Wq|Wk|Wv] * pack(xn)                      gemv_q4_0_qkv
+//   RoPE(q, k); k, v -> f16 cache row pos                  rope_kv_f16
+//   attn     = softmax(scale * q K^T) V  -> Q8_0 pack      attn partial + combine
+//   o        = Wo * pack(attn)                             gemv_q4_0
+//   h += rms_norm(o, post_attn); xn = rms_norm(h, ffn)    residual_rms_norm -> pack
+//   act      = gelu(Wg xn) * (Wu xn)     -> Q8_0 pack      gemv_q4_0_geglu (emit)
+//   f        = Wd * pack(act)                              gemv_q4_0 (relay)
+//   h += rms_norm(f, post_ffw); xn = rms_norm(h, next)    residual_rms_norm -> pack
+// then the tied LM head over pack(rms_norm(h, output_norm)) and argmax.
+
+#include <cmath>
+#include <new>
+#include <vector>
+
+#include "device.h"
+#include "internal.h"
+
+struct mrml_hip_gemma2 {
+    mrml_hip_gemma2_config cfg{};
+    const void *tok_embd = nullptr;
+    const float *output_norm = nullptr;
+    std::vector<mrml_hip_gemma2_layer> layers;
+    void *arena = nullptr;  // activations, packs, partials (one allocation)
+    float *h = nullptr, *qkv = nullptr, *o = nullptr, *f = nullptr, *logits = nullptr;
+    uint8_t *xpack = nullptr, *attn_pack = nullptr, *act_pack = nullptr;
+    void *attn_part = nullptr, *argmax_scratch = nullptr;
+    float *rope_table = nullptr;  // [ctx_len][head_dim/2] (cos, sin) from the host libm
+};
+
+using namespace mrml;
+
+namespace {
+
+int check_model_config(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config &c)
+{
+    REQUIRE(ctx, c.n_layers > 0 && c.dim > 0 && c.n_heads > 0 && c.n_kv_heads > 0 && c.ffn_dim > 0 &&
+                     c.vocab > 0 && c.ctx_len > 0,
+            "gemma2: every size must be positive");
+    REQUIRE(ctx, c.head_dim == attn_head_dim(), "gemma2: head_dim %d unsupported (the attention kernel serves %d)",
+            c.head_dim, attn_head_dim());
+    REQUIRE(ctx, c.n_heads % c.n_kv_heads == 0 && c.n_heads / c.n_kv_heads <= 8,
+            "gemma2: n_heads=%d must be a multiple of n_kv_heads=%d with a group of at most 8", c.n_heads,
+            c.n_kv_heads);
+    REQUIRE(ctx, norm_dim_ok(c.dim), "gemma2: dim=%d must be a multiple of 32 up to 16384", c.dim);
+    REQUIRE(ctx, c.ffn_dim % 32 == 0, "gemma2: ffn_dim=%d must be a multiple of 32", c.ffn_dim);
+    REQUIRE(ctx, c.tie_type == MRML_HIP_Q4_0 || c.tie_type == MRML_HIP_Q8_0,
+            "gemma2: tie_type must be Q4_0 or Q8_0");
+    REQUIRE(ctx, c.ctx_len <= attn_max_capacity(), "gemma2: ctx_len=%d above %d", c.ctx_len, attn_max_capacity());
+    return MRML_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+// ---- decode-step ops -------------------------------------------------------------
+
+int mrml_hip_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float *out, void *pack, int32_t dim,
+                      float eps)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, x && (out || pack), "rms_norm: x is null or no output requested");
+    REQUIRE(ctx, norm_dim_ok(dim), "rms_norm: dim=%d must be a multiple of 32 up to 16384", dim);
+    REQUIRE(ctx, ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)out & 15) == 0 &&
+                     ((uintptr_t)pack & 15) == 0,
+            "rms_norm: pointers must be 16-byte aligned");
+    return launch_rms_norm(ctx, x, w, eps, out, pack, dim);
+}
+
+int mrml_hip_residual_rms_norm(mrml_hip_ctx *ctx, const float *t, const float *w_post, float *h,
+                               const float *w_next, float *xn, void *pack, int32_t dim, float eps)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, t && h, "residual_rms_norm: t and h are required");
+    REQUIRE(ctx, norm_dim_ok(dim), "residual_rms_norm: dim=%d must be a multiple of 32 up to 16384", dim);
+    REQUIRE(ctx, (((uintptr_t)t | (uintptr_t)w_post | (uintptr_t)h | (uintptr_t)w_next | (uintptr_t)xn |
+                   (uintptr_t)pack) & 15) == 0,
+            "residual_rms_norm: pointers must be 16-byte aligned");
+    return launch_residual_rms_norm(ctx, t, w_post, h, w_next, eps, xn, pack, dim);
+}
+
+int mrml_hip_embedding(mrml_hip_ctx *ctx, const void *table, int32_t type, int32_t token, const int32_t *d_token,
+                       float *out, int32_t dim, int32_t vocab, float scale)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, table && out, "embedding: null pointer");
+    REQUIRE(ctx, type == MRML_HIP_Q4_0 || type == MRML_HIP_Q8_0, "embedding: type must be Q4_0 or Q8_0");
+    REQUIRE(ctx, norm_dim_ok(dim) && vocab > 0, "embedding: dim=%d vocab=%d", dim, vocab);
+    REQUIRE(ctx, d_token || (token >= 0 && token < vocab), "embedding: token %d outside [0, %d)", token, vocab);
+    REQUIRE(ctx, ((uintptr_t)out & 15) == 0 && ((uintptr_t)table & 15) == 0,
+            "embedding: pointers must be 16-byte aligned");
+    return launch_embedding(ctx, table, type, d_token, token, scale, out, nullptr, 0.0f, nullptr, nullptr, dim, vocab);
+}
+
+int mrml_hip_rope_table(mrml_hip_ctx *ctx, float *d_table, int32_t n_pos, int32_t head_dim, float freq_base,
+                        float freq_scale)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, d_table && n_pos > 0 && head_dim > 0 && head_dim % 2 == 0,
+            "rope_table: n_pos=%d head_dim=%d", n_pos, head_dim);
+    REQUIRE(ctx, ((uintptr_t)d_table & 7) == 0, "rope_table: table must be 8-byte aligned");
+    return fill_rope_table(ctx, d_table, n_pos, head_dim, freq_base, freq_scale);
+}
+
+int mrml_hip_rope_kv_append_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache, uint16_t *v_cache, int32_t pos,
+                                const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                float freq_base, float freq_scale, int32_t capacity, const float *d_table,
+                                int32_t n_table)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, qkv && k_cache && v_cache, "rope_kv_append_f16: null pointer");
+    REQUIRE(ctx, n_heads > 0 && n_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && head_dim <= 1024,
+            "rope_kv_append_f16: n_heads=%d n_kv_heads=%d head_dim=%d", n_heads, n_kv_heads, head_dim);
+    REQUIRE(ctx, capacity > 0 && (d_pos || pos >= 0), "rope_kv_append_f16: pos=%d capacity=%d", pos, capacity);
+    REQUIRE(ctx, ((uintptr_t)d_table & 7) == 0 && n_table >= 0, "rope_kv_append_f16: table");
+    return launch_rope_kv_f16(ctx, qkv, k_cache, v_cache, d_pos, pos, n_heads, n_kv_heads, head_dim, freq_base,
+                              freq_scale, capacity, d_table, d_table ? n_table : 0);
+}
+
+int mrml_hip_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                             float *out, void *pack, int32_t n_past, const int32_t *d_pos, int32_t n_heads,
+                             int32_t n_kv_heads, int32_t head_dim, float scale, int32_t capacity)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, q && k_cache && v_cache && (out || pack), "attn_decode_f16: null pointer or no output");
+    REQUIRE(ctx, head_dim == attn_head_dim(), "attn_decode_f16: head_dim=%d unsupported (kernel serves %d)",
+            head_dim, attn_head_dim());
+    REQUIRE(ctx, n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= 8,
+            "attn_decode_f16: n_heads=%d n_kv_heads=%d (group of at most 8)", n_heads, n_kv_heads);
+    REQUIRE(ctx, capacity > 0 && capacity <= attn_max_capacity() && (d_pos || n_past >= 0),
+            "attn_decode_f16: n_past=%d capacity=%d (at most %d)", n_past, capacity, attn_max_capacity());
+    REQUIRE(ctx, ((((uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)q | (uintptr_t)pack) & 15) == 0),
+            "attn_decode_f16: pointers must be 16-byte aligned");
+    void *part = workspace(ctx, attn_scratch_bytes(n_heads, capacity));
+    if (!part) return MRML_HIP_E_ALLOC;
+    return launch_attn_decode_f16(ctx, q, k_cache, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, scale,
+                                  capacity, part);
+}
+
+// ---- the Gemma-2-shape model --------------------------------------------------------
+
+int mrml_hip_gemma2_create(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config *cfg, const void *tok_embd,
+                           const float *output_norm, const mrml_hip_gemma2_layer *layers, mrml_hip_gemma2 **out)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, cfg && tok_embd && output_norm && layers && out, "gemma2_create: null argument");
+    *out = nullptr;
+    if (int rc = check_model_config(ctx, *cfg)) return rc;
+    const mrml_hip_gemma2_config &c = *cfg;
+    for (int l = 0; l < c.n_layers; ++l) {
+        const mrml_hip_gemma2_layer &L = layers[l];
+        REQUIRE(ctx, L.wq && L.wk && L.wv && L.wo && L.w_gate && L.w_up && L.w_down && L.attn_norm &&
+                         L.post_attn_norm && L.ffn_norm && L.post_ffw_norm,
+                "gemma2_create: layer %d has a null tensor", l);
+    }
+    mrml_hip_gemma2 *m = new (std::nothrow) mrml_hip_gemma2;
+    if (!m) return fail(ctx, MRML_HIP_E_ALLOC, "gemma2_create: out of host memory");
+    m->cfg = c;
+    m->tok_embd = tok_embd;
+    m->output_norm = output_norm;
+    m->layers.assign(layers, layers + c.n_layers);
+
+    const size_t qd = (size_t)c.n_heads * c.head_dim, kvd = (size_t)c.n_kv_heads * c.head_dim;
+    const size_t in_max = qd > (size_t)c.dim ? qd : (size_t)c.dim;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off = align_up(off + bytes, 256);
+        return at;
+    };
+    const size_t o_h = take(c.dim * 4), o_qkv = take((qd + 2 * kvd) * 4), o_o = take(c.dim * 4),
+                 o_f = take(c.dim * 4), o_logits = take((size_t)c.vocab * 4),
+                 o_xpack = take(act_pack_bytes((int)(in_max / 32))), o_apack = take(act_pack_bytes((int)(qd / 32))),
+                 o_actpack = take(act_pack_bytes(c.ffn_dim / 32)),
+                 o_part = take(attn_scratch_bytes(c.n_heads, c.ctx_len)),
+                 o_argmax = take((size_t)argmax_parts(c.vocab) * 8),
+                 o_rope = take((size_t)c.ctx_len * c.head_dim * sizeof(float));
+    hipError_t e = hipMalloc(&m->arena, off);
+    if (e != hipSuccess) {
+        delete m;
+        return fail(ctx, MRML_HIP_E_ALLOC, "gemma2_create: hipMalloc(%zu): %s", off, hipGetErrorString(e));
+    }
+    uint8_t *base = (uint8_t *)m->arena;
+    m->h = (float *)(base + o_h);
+    m->qkv = (float *)(base + o_qkv);
+    m->o = (float *)(base + o_o);
+    m->f = (float *)(base + o_f);
+    m->logits = (float *)(base + o_logits);
+    m->xpack = base + o_xpack;
+    m->attn_pack = base + o_apack;
+    m->act_pack = base + o_actpack;
+    m->attn_part = base + o_part;
+    m->argmax_scratch = base + o_argmax;
+    m->rope_table = (float *)(base + o_rope);
+    if (int rc = fill_rope_table(ctx, m->rope_table, c.ctx_len, c.head_dim, c.rope_base, 1.0f)) {
+        (void)hipFree(m->arena);
+        delete m;
+        return rc;
+    }
+    *out = m;
+    return MRML_HIP_OK;
+}
+
+int mrml_hip_gemma2_destroy(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m)
+{
+    CTX_GUARD(ctx);
+    if (!m) return MRML_HIP_OK;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(m->arena);
+    delete m;
+    return e == hipSuccess ? MRML_HIP_OK : hip_fail(ctx, e, "gemma2_destroy");
+}
+
+int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state, uint16_t *d_k_cache,
+                         uint16_t *d_v_cache, float *d_logits, int32_t *d_argmax, int32_t *d_hist, int32_t hist_cap,
+                         const int32_t *d_prompt, int32_t prompt_len)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, m && d_state && d_k_cache && d_v_cache, "gemma2_step: null argument");
+    REQUIRE(ctx, (((uintptr_t)d_k_cache | (uintptr_t)d_v_cache | (uintptr_t)d_logits) & 15) == 0,
+            "gemma2_step: caches and logits must be 16-byte aligned");
+    const mrml_hip_gemma2_config &c = m->cfg;
+    const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    const size_t layer_cache = (size_t)c.ctx_len * kvd;
+    int32_t *d_token = d_state, *d_pos = d_state + 1;
+    float *logits = d_logits ? d_logits : m->logits;
+    int rc;
+#define STEP(call)                      \
+    do {                                \
+        if ((rc = (call)) != 0) return rc; \
+    } while (0)
+    STEP(launch_embedding(ctx, m->tok_embd, c.tie_type, d_token, 0, sqrtf((float)c.dim), m->h,
+                          m->layers[0].attn_norm, c.eps, nullptr, m->xpack, c.dim, c.vocab));
+    for (int l = 0; l < c.n_layers; ++l) {
+        const mrml_hip_gemma2_layer &L = m->layers[l];
+        uint16_t *kc = d_k_cache + (size_t)l * layer_cache, *vc = d_v_cache + (size_t)l * layer_cache;
+        const float *next_norm = l + 1 < c.n_layers ? m->layers[l + 1].attn_norm : m->output_norm;
+        STEP(launch_gemv_q4_0_qkv(ctx, L.wq, L.wk, L.wv, m->xpack, m->qkv, qd, kvd, c.dim));
+        STEP(launch_rope_kv_f16(ctx, m->qkv, kc, vc, d_pos, 0, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_base,
+                                1.0f, c.ctx_len, m->rope_table, c.ctx_len));
+        STEP(launch_attn_decode_f16(ctx, m->qkv, kc, vc, nullptr, m->attn_pack, d_pos, 0, c.n_heads, c.n_kv_heads,
+                                    c.attn_scale, c.ctx_len, m->attn_part));
+        STEP(launch_gemv_q4_0(ctx, L.wo, m->attn_pack, m->o, c.dim, qd));
+        STEP(launch_residual_rms_norm(ctx, m->o, L.post_attn_norm, m->h, L.ffn_norm, c.eps, nullptr, m->xpack,
+                                      c.dim));
+        STEP(launch_gemv_q4_0_geglu_emit(ctx, L.w_gate, L.w_up, m->xpack, nullptr, m->act_pack, c.ffn_dim, c.dim));
+        STEP(launch_gemv_q4_0(ctx, L.w_down, m->act_pack, m->f, c.dim, c.ffn_dim));
+        STEP(launch_residual_rms_norm(ctx, m->f, L.post_ffw_norm, m->h, next_norm, c.eps, nullptr, m->xpack,
+                                      c.dim));
+    }
+    if (c.tie_type == MRML_HIP_Q4_0)
+        STEP(launch_gemv_q4_0(ctx, m->tok_embd, m->xpack, logits, c.vocab, c.dim));
+    else
+        STEP(launch_gemv_q8_0(ctx, m->tok_embd, m->xpack, logits, c.vocab, c.dim, 0));
+    STEP(launch_argmax_step(ctx, logits, c.vocab, d_argmax, m->argmax_scratch, d_state, d_hist, hist_cap, d_prompt,
+                            prompt_len));
+#undef STEP
+    return MRML_HIP_OK;
+}
+
+int mrml_hip_gemma2_activations(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, float **d_h, float **d_logits)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, m, "gemma2_activations: null model");
+    if (d_h) *d_h = m->h;
+    if (d_logits) *d_logits = m->logits;
+    return MRML_HIP_OK;
+}
+
+}  // extern "C"

@@ -6,10 +6,12 @@
 // and a per-device stream; here, libamdhip64 linked directly, gfx950 code
 // objects linked into this library, and one stream per context.
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <new>
+#include <vector>
 
 #include "device.h"
 #include "internal.h"
@@ -69,21 +71,37 @@ void *workspace(mrml_hip_ctx *ctx, size_t bytes)
     return p;
 }
 
+bool host_expf_fused()
+{
+    static const bool fused = __builtin_cpu_supports("fma") && __builtin_cpu_supports("avx2");
+    return fused;
+}
+
+int fill_rope_table(mrml_hip_ctx *ctx, float *d_table, int n_pos, int head_dim, float base, float freq_scale)
+{
+    // Called through pointers so the compiler keeps three separate libm calls
+    // (the reference calls powf, cosf and sinf; a merged sincosf is a
+    // different routine).
+    float (*volatile f_pow)(float, float) = powf;
+    float (*volatile f_cos)(float) = cosf;
+    float (*volatile f_sin)(float) = sinf;
+    const int half = head_dim / 2;
+    std::vector<float> inv(half), tab((size_t)n_pos * half * 2);
+    for (int i = 0; i < half; ++i) inv[i] = f_pow(base, (float)(2 * i) / (float)head_dim);
+    for (int p = 0; p < n_pos; ++p)
+        for (int i = 0; i < half; ++i) {
+            const float theta = (float)p * freq_scale / inv[i];  // ops.rs:185-208 order
+            tab[((size_t)p * half + i) * 2] = f_cos(theta);
+            tab[((size_t)p * half + i) * 2 + 1] = f_sin(theta);
+        }
+    hipError_t e = hipMemcpyAsync(d_table, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? MRML_HIP_OK : hip_fail(ctx, e, "rope table upload");
+}
+
 }  // namespace mrml
 
 using namespace mrml;
-
-#define CTX_GUARD(ctx)                                      \
-    do {                                                    \
-        if (!(ctx)) return MRML_HIP_E_INVALID;              \
-        int rc_ = enter(ctx);                               \
-        if (rc_) return rc_;                                \
-    } while (0)
-
-#define REQUIRE(ctx, cond, ...)                                             \
-    do {                                                                    \
-        if (!(cond)) return fail((ctx), MRML_HIP_E_INVALID, __VA_ARGS__);   \
-    } while (0)
 
 extern "C" {
 

@@ -27,12 +27,20 @@ def _f16_bits(values: np.ndarray) -> np.ndarray:
     return values.astype(np.float16).view(np.uint16)
 
 
-def q4_0_matrix(rng: np.random.Generator, rows: int, cols: int, sigma: float = 0.02) -> np.ndarray:
+def q4_0_matrix(rng: np.random.Generator, rows: int, cols: int, sigma: float = 0.02,
+                symmetric: bool = False) -> np.ndarray:
+    """Q4_0 blocks; nibbles uniform in 0..15, or in 1..15 (values -7..7, mean 0)
+    with `symmetric`."""
     nb = cols // 32
     blocks = np.empty((rows * nb, 18), dtype=np.uint8)
     d = _f16_bits(np.abs(rng.standard_normal(rows * nb, dtype=np.float32)) * np.float32(sigma) / np.float32(8.0))
     blocks[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
-    blocks[:, 2:] = rng.integers(0, 256, size=(rows * nb, 16), dtype=np.uint8)
+    if symmetric:
+        lo = rng.integers(1, 16, size=(rows * nb, 16), dtype=np.uint8)
+        hi = rng.integers(1, 16, size=(rows * nb, 16), dtype=np.uint8)
+        blocks[:, 2:] = lo | (hi << 4)
+    else:
+        blocks[:, 2:] = rng.integers(0, 256, size=(rows * nb, 16), dtype=np.uint8)
     return blocks.reshape(-1)
 
 
@@ -79,3 +87,52 @@ def rms_normalised(x: np.ndarray, eps: float = 1e-6) -> np.ndarray:
     x = np.asarray(x, dtype=np.float32)
     s = np.float32(np.mean(x.astype(np.float64) ** 2))
     return (x / np.sqrt(s + np.float32(eps))).astype(np.float32)
+
+
+# Gemma-2-2B architecture (the decode configuration: 26 layers, hidden 2304,
+# 8 query / 4 KV heads of 256, GeGLU FFN 9216, RoPE base 10000, tied
+# 256000-entry table, f16 KV cache of 4096 positions).
+GEMMA2_2B = dict(n_layers=26, dim=2304, n_heads=8, n_kv_heads=4, head_dim=256, ffn_dim=9216, vocab=256000,
+                 ctx_len=4096, rope_base=10000.0, eps=1e-6, attn_scale=1.0 / 16.0)
+
+GEMMA2_MATRICES = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")
+GEMMA2_NORMS = ("attn_norm", "post_attn_norm", "ffn_norm", "post_ffw_norm")
+
+
+def gemma2_shapes(cfg: dict) -> dict:
+    """(rows, cols) of each layer matrix."""
+    d, qd = cfg["dim"], cfg["n_heads"] * cfg["head_dim"]
+    kvd, f = cfg["n_kv_heads"] * cfg["head_dim"], cfg["ffn_dim"]
+    return {"wq": (qd, d), "wk": (kvd, d), "wv": (kvd, d), "wo": (d, qd),
+            "w_gate": (f, d), "w_up": (f, d), "w_down": (d, f)}
+
+
+def gemma2_model(cfg: dict, seed: int = 4, tie_q8: bool = False) -> dict:
+    """Random-init Gemma-2-architecture weights as GGUF block bytes.
+
+    Matrices are Q4_0 with d = f16(|N(0, 0.02)| / 8) and nibbles uniform in
+    1..15: weights -7..7 with mean 0.  (Nibbles uniform in 0..15 have mean
+    -0.5, which gives every projection a shared component along the sum of its
+    input; through 26 layers that common mode decides the argmax for any
+    token.)  The tied table is Q4_0 (or Q8_0); norm weights are f32
+    1 + 0.1 N(0, 1).
+    """
+    rng = rng_for(100 + seed)
+    shapes = gemma2_shapes(cfg)
+    layers = []
+    for _ in range(cfg["n_layers"]):
+        L = {name: q4_0_matrix(rng, *shapes[name], symmetric=True) for name in GEMMA2_MATRICES}
+        for name in GEMMA2_NORMS:
+            L[name] = (1.0 + 0.1 * rng.standard_normal(cfg["dim"], dtype=np.float32)).astype(np.float32)
+        layers.append(L)
+    if tie_q8:
+        table = q8_0_matrix(rng, cfg["vocab"], cfg["dim"])
+    else:
+        table = q4_0_matrix(rng, cfg["vocab"], cfg["dim"], symmetric=True)
+    out_norm = (1.0 + 0.1 * rng.standard_normal(cfg["dim"], dtype=np.float32)).astype(np.float32)
+    return {"cfg": dict(cfg), "tie_q8": tie_q8, "tok_embd": table, "output_norm": out_norm, "layers": layers}
+
+
+def prompt_tokens(n: int, vocab: int, seed: int = 5) -> np.ndarray:
+    """A seeded random token prompt."""
+    return rng_for(200 + seed).integers(0, vocab, size=n, dtype=np.int32)

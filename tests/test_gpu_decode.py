@@ -1,0 +1,323 @@
+"""GPU parity of the decode-step ops and the Gemma-2-shape token step (C ABI).
+
+Bar: bit-identical to the CPU oracle.  The ops follow the reference's
+operation order (sequential f32 sums where the reference sums sequentially)
+and reproduce the host C library's expf/tanhf; RoPE reads a cos/sin table
+the host fills with its own libm.  Every Q8_0 pack an op emits must equal the
+oracle's quantiser applied to the op's f32 output, and the whole model must
+produce bit-identical logits and identical greedy tokens.  The one tolerance
+op is RoPE without a table (device double-precision sin/cos, rounded once).
+"""
+
+from __future__ import annotations
+
+import math
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+THREADS = min(16, os.cpu_count() or 1)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def assert_bits(got, ref, what):
+    bad = np.flatnonzero(bits(got) != bits(ref))
+    assert bad.size == 0, f"{what}: {bad.size} of {np.size(ref)} differ, first {bad[:4]}: {np.ravel(got)[bad[:4]]} vs {np.ravel(ref)[bad[:4]]}"
+
+
+def pack_to_gguf(pack: np.ndarray, nb: int) -> np.ndarray:
+    """Backend activation pack -> GGUF Q8_0 bytes (d back to f16, exactly)."""
+    out = np.empty((nb, 34), np.uint8)
+    d = pack[nb * 32: nb * 36].view(np.float32).astype(np.float16)
+    out[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    out[:, 2:] = pack[:nb * 32].reshape(nb, 32)
+    return out.reshape(-1)
+
+
+def check_pack(orc, pack, values, what):
+    """The pack must be the oracle quantiser applied to `values`, bit for bit."""
+    n = values.size
+    nb = n // 32
+    ref = orc.quantize_q8_0(values)
+    assert np.array_equal(pack_to_gguf(pack, nb), ref), f"{what}: pack differs from Q8_0 of the f32 output"
+    sums = ref.reshape(nb, 34)[:, 2:].view(np.int8).astype(np.int32).sum(axis=1)
+    assert np.array_equal(pack[nb * 36: nb * 40].view(np.int32), sums), f"{what}: block sums"
+
+
+def max_rel(got, ref):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    return float(np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+# ------------------------------------------------------------ RMSNorm
+@pytest.mark.parametrize("dim", [2304, 256, 9216, 32])
+def test_rms_norm_and_pack(backend, dev, orc, synth, dim):
+    rng = synth.rng_for(3000 + dim)
+    x = (rng.standard_normal(dim) * 3.0).astype(np.float32)
+    w = (1.0 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+    xb, wb = backend.HipBuffer.from_host(dev, x), backend.HipBuffer.from_host(dev, w)
+    out = backend.HipBuffer.alloc(dev, dim)
+    pk = backend.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(dim), np.uint8)
+    dev.rms_norm(xb, wb, out, dim, 1e-6, pack=pk)
+    dev.sync()
+    got = out.numpy()
+    assert_bits(got, orc.rms_norm(x, w, 1e-6), "rms_norm")   # sequential f32 sum, as ops.rs:24-79
+    check_pack(orc, pk.numpy(), got, "rms_norm")
+    # no weight: the reference's Option<w> = None
+    dev.rms_norm(xb, None, out, dim, 1e-6)
+    dev.sync()
+    assert_bits(out.numpy(), orc.rms_norm(x, None, 1e-6), "rms_norm (no weight)")
+    # ops_test.rs:3-12: a constant vector normalises to 1
+    cb = backend.HipBuffer.from_host(dev, np.full(dim, 2.0, np.float32))
+    dev.rms_norm(cb, None, out, dim, 1e-6)
+    dev.sync()
+    assert np.all(np.abs(out.numpy() - 1.0) < 1e-4)
+
+
+def test_residual_rms_norm(backend, dev, orc, synth):
+    dim = 2304
+    rng = synth.rng_for(3100)
+    t = rng.standard_normal(dim).astype(np.float32) * np.float32(0.7)
+    h = rng.standard_normal(dim).astype(np.float32)
+    wp = (1.0 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+    wn = (1.0 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+    tb, hb = backend.HipBuffer.from_host(dev, t), backend.HipBuffer.from_host(dev, h)
+    wpb, wnb = backend.HipBuffer.from_host(dev, wp), backend.HipBuffer.from_host(dev, wn)
+    xn = backend.HipBuffer.alloc(dev, dim)
+    pk = backend.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(dim), np.uint8)
+    dev.residual_rms_norm(tb, wpb, hb, wnb, xn, dim, 1e-6, pack=pk)
+    dev.sync()
+    h_ref = (h + orc.rms_norm(t, wp, 1e-6)).astype(np.float32)
+    assert_bits(hb.numpy(), h_ref, "residual h")
+    xn_got = xn.numpy()
+    assert_bits(xn_got, orc.rms_norm(h_ref, wn, 1e-6), "residual xn")
+    check_pack(orc, pk.numpy(), xn_got, "residual_rms_norm")
+
+
+# ------------------------------------------------------------ embedding
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+def test_embedding_bit_exact(backend, dev, orc, synth, qtype):
+    vocab, dim = 1000, 2304
+    rng = synth.rng_for(3200)
+    if qtype == "q4_0":
+        table, t, deq, bpr = synth.q4_0_matrix(rng, vocab, dim), backend.Q4_0, orc.dequantize_q4_0, dim // 32 * 18
+    else:
+        table, t, deq, bpr = synth.q8_0_matrix(rng, vocab, dim), backend.Q8_0, orc.dequantize_q8_0, dim // 32 * 34
+    tb = backend.HipBuffer.from_gguf(dev, table, t, vocab, dim)
+    out = backend.HipBuffer.alloc(dev, dim)
+    scale = math.sqrt(dim)
+    for tok in (0, 1, 517, vocab - 1):
+        dev.embedding(tb, t, tok, out, dim, vocab, scale)
+        dev.sync()
+        ref = (deq(table[tok * bpr:(tok + 1) * bpr], dim) * np.float32(scale)).astype(np.float32)
+        assert np.array_equal(out.numpy().view(np.uint32), ref.view(np.uint32)), tok
+    # token read from device memory
+    dtok = backend.HipBuffer.from_host(dev, np.array([42], np.int32))
+    dev.embedding(tb, t, 0, out, dim, vocab, scale, d_token=dtok)
+    dev.sync()
+    ref = (deq(table[42 * bpr:43 * bpr], dim) * np.float32(scale)).astype(np.float32)
+    assert np.array_equal(out.numpy().view(np.uint32), ref.view(np.uint32))
+
+
+# ------------------------------------------------------------ RoPE + KV append
+@pytest.mark.parametrize("pos", [0, 1, 511, 767, 4095])
+@pytest.mark.parametrize("use_table", [True, False])
+def test_rope_kv_append(backend, dev, orc, synth, pos, use_table):
+    nh, nkv, hd, cap = 8, 4, 256, 4096
+    rng = synth.rng_for(3300 + pos)
+    qkv = rng.standard_normal((nh + 2 * nkv) * hd).astype(np.float32)
+    kvd = nkv * hd
+    kc = backend.HipBuffer.from_host(dev, np.zeros(cap * kvd, np.uint16))
+    vc = backend.HipBuffer.from_host(dev, np.zeros(cap * kvd, np.uint16))
+    qb = backend.HipBuffer.from_host(dev, qkv)
+    table = None
+    if use_table:
+        table = backend.HipBuffer.alloc(dev, cap * hd)
+        dev.rope_table(table, cap, hd, 10000.0)
+    dev.rope_kv_append_f16(qb, kc, vc, pos, nh, nkv, hd, 10000.0, cap, table=table, n_table=cap if table else 0)
+    dev.sync()
+    got = qb.numpy()
+    q_ref = orc.rope_1d_batched(qkv[:nh * hd], pos, nh, hd, 10000.0)
+    k_ref = orc.rope_1d_batched(qkv[nh * hd:(nh + nkv) * hd], pos, nkv, hd, 10000.0)
+    k_got = got[nh * hd:(nh + nkv) * hd]
+    if use_table:
+        # cos/sin from the host libm, as the reference calls them: bit-exact
+        assert_bits(got[:nh * hd], q_ref, "rope q")
+        assert_bits(k_got, k_ref, "rope k")
+    else:
+        # device sin/cos in double, rounded once: glibc's sinf/cosf differ from
+        # the correctly rounded value on ~1% of angles, by one ulp
+        assert np.max(np.abs(got[:nh * hd] - q_ref)) <= 2e-6 * np.max(np.abs(q_ref))
+        assert np.max(np.abs(k_got - k_ref)) <= 2e-6 * np.max(np.abs(k_ref))
+    kh, vh = kc.numpy().reshape(cap, kvd), vc.numpy().reshape(cap, kvd)
+    # the cache rows hold exactly the f16 (RNE) of the op's own f32 values
+    assert np.array_equal(kh[pos], k_got.astype(np.float16).view(np.uint16))
+    assert np.array_equal(vh[pos], qkv[(nh + nkv) * hd:].astype(np.float16).view(np.uint16))
+    others = np.delete(np.arange(cap), pos)
+    assert not kh[others].any() and not vh[others].any()
+
+
+# ------------------------------------------------------------ attention
+def attention_case(backend, dev, orc, synth, n_past, cap, seed):
+    nh, nkv, hd = 8, 4, 256
+    rng = synth.rng_for(3400 + seed)
+    kvd = nkv * hd
+    q = rng.standard_normal(nh * hd).astype(np.float32) * np.float32(0.5)
+    kc = rng.standard_normal(cap * kvd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(cap * kvd).astype(np.float16).view(np.uint16)
+    qb, kb, vb = (backend.HipBuffer.from_host(dev, a) for a in (q, kc, vc))
+    out = backend.HipBuffer.alloc(dev, nh * hd)
+    pk = backend.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(nh * hd), np.uint8)
+    dev.attention_causal(qb, kb, vb, out, n_past, nh, nkv, hd, 1.0 / 16.0, cap, pack=pk)
+    dev.sync()
+    # the window is the last min(n_past + 1, cap) positions, oldest first
+    count = n_past + 1
+    rows = [(t % cap) for t in range(max(0, count - cap), count)]
+    kr = kc.reshape(cap, kvd)[rows].reshape(-1)
+    vr = vc.reshape(cap, kvd)[rows].reshape(-1)
+    ref = orc.attention_f16(q, kr, vr, len(rows) - 1, nh, nkv, hd, 1.0 / 16.0)
+    got = out.numpy()
+    return got, ref, pk.numpy(), vc
+
+
+@pytest.mark.parametrize("n_past", [0, 1, 31, 32, 33, 63, 64, 511, 767, 4095])
+def test_attention_decode(backend, dev, orc, synth, n_past):
+    got, ref, pack, _ = attention_case(backend, dev, orc, synth, n_past, 4096, n_past)
+    assert_bits(got, ref, "attention")
+    check_pack(orc, pack, got, "attention")
+
+
+def test_attention_ring_window(backend, dev, orc, synth):
+    # past the capacity the cache is a ring holding the last `capacity` positions
+    got, ref, _, _ = attention_case(backend, dev, orc, synth, 100, 64, 77)
+    assert_bits(got, ref, "attention (ring)")
+
+
+def test_attention_large_scores(backend, dev, orc, synth):
+    # scores spread over tens of units: expf over a wide range of arguments
+    nh, nkv, hd, cap, n_past = 8, 4, 256, 512, 300
+    rng = synth.rng_for(3500)
+    q = (rng.standard_normal(nh * hd) * 4.0).astype(np.float32)
+    kc = rng.standard_normal(cap * nkv * hd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(cap * nkv * hd).astype(np.float16).view(np.uint16)
+    qb, kb, vb = (backend.HipBuffer.from_host(dev, a) for a in (q, kc, vc))
+    out = backend.HipBuffer.alloc(dev, nh * hd)
+    dev.attention_causal(qb, kb, vb, out, n_past, nh, nkv, hd, 1.0, cap)
+    dev.sync()
+    ref = orc.attention_f16(q, kc[:(n_past + 1) * nkv * hd], vc[:(n_past + 1) * nkv * hd], n_past, nh, nkv, hd,
+                            1.0)
+    assert_bits(out.numpy(), ref, "attention (wide scores)")
+
+
+def test_attention_single_position_is_v(backend, dev, orc, synth):
+    # one position: softmax weight exactly 1, so each head's output is its kv head's v row
+    got, _, _, vc = attention_case(backend, dev, orc, synth, 0, 4096, 5)
+    v0 = vc.reshape(4096, 4, 256)[0].view(np.float16).astype(np.float32)
+    assert np.array_equal(got, np.repeat(v0, 2, axis=0).reshape(-1))
+
+
+# ------------------------------------------------------------ the token step
+def run_gpu_decode(backend, dev, model, prompt, n_decode, use_graph=True):
+    """Prefill `prompt` token by token, then decode greedily.  Returns the
+    argmax of every step (hist[p] = argmax at position p), the logits of every
+    step and the final caches."""
+    m = backend.Gemma2Model.from_host(dev, model)
+    c = model["cfg"]
+    total = len(prompt) + n_decode
+    state = backend.HipBuffer.from_host(dev, np.array([prompt[0], 0], np.int32))
+    hist = backend.HipBuffer.from_host(dev, np.full(total, -1, np.int32))
+    pr = backend.HipBuffer.from_host(dev, np.asarray(prompt, np.int32))
+    kc = backend.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    vc = backend.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    logits = backend.HipBuffer.alloc(dev, c["vocab"])
+    step = lambda: m.step(state, kc, vc, logits=logits, hist=hist, hist_cap=total, prompt=pr,
+                          prompt_len=len(prompt))
+    graph = dev.capture(step) if use_graph else None
+    all_logits = []
+    for _ in range(total):
+        graph.launch() if graph else step()
+        dev.sync()
+        all_logits.append(logits.numpy())
+    h = hist.numpy()
+    st = state.numpy()
+    assert st[1] == total
+    out = (h, all_logits, kc.numpy(), vc.numpy())
+    if graph:
+        graph.close()
+    m.close()
+    return out
+
+
+def run_oracle_decode(orc, model, prompt, n_decode):
+    """The oracle's argmax at every position (teacher-forced through the prompt)."""
+    o = orc.OracleGemma2(model)
+    total = len(prompt) + n_decode
+    lg = np.zeros(model["cfg"]["vocab"], np.float32)
+    best, logits = [], []
+    tok = int(prompt[0])
+    for pos in range(total):
+        nxt = o.step(tok, pos, threads=THREADS, logits=lg)
+        logits.append(lg.copy())
+        best.append(nxt)
+        tok = int(prompt[pos + 1]) if pos + 1 < len(prompt) else nxt
+    return np.array(best, np.int32), logits, o
+
+
+def assert_same_tokens(hist, want):
+    diff = np.flatnonzero(hist != want)
+    assert diff.size == 0, f"first divergence at position {diff[0]}: gpu {hist[diff[:4]]} oracle {want[diff[:4]]}"
+
+
+TINY = dict(n_layers=2, dim=256, n_heads=2, n_kv_heads=1, head_dim=256, ffn_dim=512, vocab=1000, ctx_len=64,
+            rope_base=10000.0, eps=1e-6, attn_scale=1.0 / 16.0)
+
+
+@pytest.mark.parametrize("tie_q8", [False, True])
+def test_gemma2_tiny_greedy(backend, dev, orc, synth, tie_q8):
+    model = synth.gemma2_model(TINY, seed=11, tie_q8=tie_q8)
+    prompt = synth.prompt_tokens(5, TINY["vocab"], seed=3)
+    n_dec = 20
+    hist, lg_gpu, kc, vc = run_gpu_decode(backend, dev, model, prompt, n_dec)
+    want, lg_ref, o = run_oracle_decode(orc, model, prompt, n_dec)
+    assert_same_tokens(hist, want)
+    for s in range(len(lg_ref)):
+        assert_bits(lg_gpu[s], lg_ref[s], f"logits at step {s}")
+    assert np.array_equal(kc, o.k_cache) and np.array_equal(vc, o.v_cache)
+
+
+def test_gemma2_tiny_graph_equals_eager(backend, dev, synth):
+    model = synth.gemma2_model(TINY, seed=12)
+    prompt = synth.prompt_tokens(3, TINY["vocab"], seed=4)
+    a = run_gpu_decode(backend, dev, model, prompt, 6, use_graph=True)
+    b = run_gpu_decode(backend, dev, model, prompt, 6, use_graph=False)
+    assert np.array_equal(a[0], b[0])
+    for x, y in zip(a[1], b[1]):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+
+
+def test_gemma2_2b_greedy_64(backend, dev, orc, synth):
+    """Gemma-2-2B shape (26 layers, 2304, 8/4 heads of 256, FFN 9216, 256000 tied
+    Q4_0 vocabulary): the greedy argmax of every step matches the oracle --
+    64 teacher-forced steps over a random prompt (context-dependent picks),
+    then 64 free-running decode steps."""
+    cfg = dict(synth.GEMMA2_2B)
+    model = synth.gemma2_model(cfg, seed=1)
+    prompt = synth.prompt_tokens(64, cfg["vocab"], seed=1)
+    n_dec = 64
+    print(f"\n[gemma2-2b] gpu: prompt {len(prompt)}, decode {n_dec}", flush=True)
+    hist, lg_gpu, _, _ = run_gpu_decode(backend, dev, model, prompt, n_dec)
+    print("[gemma2-2b] oracle", flush=True)
+    want, lg_ref, _ = run_oracle_decode(orc, model, prompt, n_dec)
+    exact = sum(int(np.array_equal(bits(a), bits(b))) for a, b in zip(lg_gpu, lg_ref))
+    margins = [float(np.diff(np.sort(l)[-2:])[0] / np.max(np.abs(l))) for l in lg_ref]
+    print(f"[gemma2-2b] distinct argmax {len(set(want[:64].tolist()))} of 64 prefill steps, decode "
+          f"{want[64:72].tolist()}..., min top-2 margin {min(margins):.2e}, bit-identical logits {exact} of "
+          f"{len(lg_ref)} steps", flush=True)
+    assert_same_tokens(hist, want)
+    assert exact == len(lg_ref)

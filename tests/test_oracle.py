@@ -485,3 +485,65 @@ def test_golden_fixture_kats(orc):
     for case in kats["q8_0_quantize"]:
         q = orc.quantize_q8_0(np.array(case["x"], dtype=np.float32))
         assert list(q) == case["bytes"], case["name"]
+
+
+# ---------------------------------------------------------------- decode step composition
+TINY_GEMMA2 = dict(n_layers=2, dim=64, n_heads=4, n_kv_heads=2, head_dim=32, ffn_dim=128, vocab=96,
+                   ctx_len=16, rope_base=10000.0, eps=1e-6, attn_scale=1.0 / math.sqrt(32.0))
+
+
+def numpy_gemma2_step(orc, model, token, pos, kc, vc):
+    """The Gemma-2 token step composed independently from the pinned oracle ops
+    (model.rs:1164-1201 embedding, per-layer order of model.rs:1185-2260 with
+    sandwich norms and a dense GeGLU FFN, tied Q4_0 head, lowest-index argmax)."""
+    c = model["cfg"]
+    d, hd, nh, nkv = c["dim"], c["head_dim"], c["n_heads"], c["n_kv_heads"]
+    qd, kvd, f, V = nh * hd, nkv * hd, c["ffn_dim"], c["vocab"]
+    row = model["tok_embd"].reshape(V, -1)[token]
+    h = (orc.dequantize_q4_0(row, d) * np.float32(math.sqrt(d))).astype(np.float32)
+    for l, L in enumerate(model["layers"]):
+        xq = orc.quantize_q8_0(orc.rms_norm(h, L["attn_norm"], c["eps"]))
+        q = orc.mat_vec_mul_q4_0_q8_0(L["wq"], xq, qd, d)
+        k = orc.mat_vec_mul_q4_0_q8_0(L["wk"], xq, kvd, d)
+        v = orc.mat_vec_mul_q4_0_q8_0(L["wv"], xq, kvd, d)
+        q = orc.rope_1d_batched(q, pos, nh, hd, c["rope_base"])
+        k = orc.rope_1d_batched(k, pos, nkv, hd, c["rope_base"])
+        base = l * c["ctx_len"] * kvd
+        kc[base + pos * kvd: base + (pos + 1) * kvd] = k.astype(np.float16).view(np.uint16)
+        vc[base + pos * kvd: base + (pos + 1) * kvd] = v.astype(np.float16).view(np.uint16)
+        att = orc.attention_f16(q, kc[base: base + (pos + 1) * kvd], vc[base: base + (pos + 1) * kvd], pos, nh,
+                                nkv, hd, c["attn_scale"])
+        o = orc.mat_vec_mul_q4_0_q8_0(L["wo"], orc.quantize_q8_0(att), d, qd)
+        h = (h + orc.rms_norm(o, L["post_attn_norm"], c["eps"])).astype(np.float32)
+        xq = orc.quantize_q8_0(orc.rms_norm(h, L["ffn_norm"], c["eps"]))
+        act = orc.geglu(orc.mat_vec_mul_q4_0_q8_0(L["w_gate"], xq, f, d),
+                        orc.mat_vec_mul_q4_0_q8_0(L["w_up"], xq, f, d))
+        dn = orc.mat_vec_mul_q4_0_q8_0(L["w_down"], orc.quantize_q8_0(act), d, f)
+        h = (h + orc.rms_norm(dn, L["post_ffw_norm"], c["eps"])).astype(np.float32)
+    xq = orc.quantize_q8_0(orc.rms_norm(h, model["output_norm"], c["eps"]))
+    logits = orc.mat_vec_mul_q4_0_q8_0(model["tok_embd"], xq, V, d)
+    return orc.argmax_f32(logits), logits
+
+
+def test_gemma2_step_matches_independent_composition(orc, synth):
+    # numpy's float16 cast is IEEE round-to-nearest-even, the cache rule of the step
+    model = synth.gemma2_model(TINY_GEMMA2, seed=9)
+    o = orc.OracleGemma2(model)
+    kvd = TINY_GEMMA2["n_kv_heads"] * TINY_GEMMA2["head_dim"]
+    kc = np.zeros(TINY_GEMMA2["n_layers"] * TINY_GEMMA2["ctx_len"] * kvd, np.uint16)
+    vc = np.zeros_like(kc)
+    tok = 7
+    logits = np.zeros(TINY_GEMMA2["vocab"], np.float32)
+    for pos in range(6):
+        got = o.step(tok, pos, threads=1, logits=logits)
+        want, want_logits = numpy_gemma2_step(orc, model, tok, pos, kc, vc)
+        assert got == want
+        assert np.array_equal(logits.view(np.uint32), want_logits.view(np.uint32))
+        assert np.array_equal(o.k_cache, kc) and np.array_equal(o.v_cache, vc)
+        tok = got
+    # threads split the matvec rows only: the step's bits do not depend on them
+    o2 = orc.OracleGemma2(model)
+    tok2 = 7
+    for pos in range(6):
+        tok2 = o2.step(tok2, pos, threads=4)
+    assert tok2 == tok and np.array_equal(o2.k_cache, o.k_cache)
