@@ -1,8 +1,8 @@
 #!/usr/bin/env python3
 """Benchmark of the MRML decode hot path on one MI355X.
 
-Workload: batch-1 Q4_0 matvecs at Gemma-2-2B FFN
-shapes.  One step = one FFN pass over synthetic data:
+Headline workload: batch-1 Q4_0 matvecs at
+Gemma-2-2B FFN shapes.  One step = one FFN pass over synthetic data:
     quantize x (2304)  ->  fused gate+up GeGLU matvec (2 x 9216x2304)
     quantize act (9216) ->  down matvec (2304x9216)
 `value` is whole-step throughput in GB/s of algorithmic bytes (weights +
@@ -11,6 +11,11 @@ exceed the 256 MB MALL, timed with HIP events around a graph of the steps.
 The JSON line also carries the per-matrix GB/s (gate, up, down, fused
 gate+up), the dominant kernel's roofline, and the host-CPU baseline (the C
 oracle restating the reference CPU path, timed on this box's cores).
+
+The second half of the metric is in "decode": greedy decode tok/s
+of a random-init Gemma-2-2B-shape Q4_0 model (512-token prefill, 256 decode
+tokens, f16 KV cache of 4096), each token one replay of the captured step,
+beside the CPU oracle's tok/s for the same step ("decode_cpu_baseline").
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -123,6 +128,70 @@ def cpu_baseline(orc, synth, budget_s: float) -> dict:
             "ms_per_step": round(best * 1e3, 3)}
 
 
+def decode_bytes_per_token(cfg: dict, pos: int) -> int:
+    """Algorithmic HBM bytes of one token step at position `pos`: every layer's
+    Q4_0 weights, the tied Q4_0 head, the f16 K and V rows read by attention
+    (pos + 1 of them per layer) and written (one), the embedding row and the
+    norm weights."""
+    d, f, V, L = cfg["dim"], cfg["ffn_dim"], cfg["vocab"], cfg["n_layers"]
+    qd, kvd = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+    layer_w = Q4_ROW(d) * (qd + 2 * kvd + 2 * f) + Q4_ROW(qd) * d + Q4_ROW(f) * d
+    kv = 2 * (pos + 2) * kvd * 2
+    return L * (layer_w + kv + 4 * d * 4) + V * Q4_ROW(d) + Q4_ROW(d) + d * 4
+
+
+def decode_bench(be, synth, dev, ev, n_prefill: int, n_decode: int, cpu_steps: int) -> tuple[dict, dict | None]:
+    """random-init Gemma-2-2B-shape Q4_0 model, f16 KV cache
+    of 4096, prefill a seeded random prompt token by token, then greedy decode;
+    every step is one replay of a captured token-step graph."""
+    cfg = dict(synth.GEMMA2_2B)
+    model = synth.gemma2_model(cfg, seed=1)
+    m = be.Gemma2Model.from_host(dev, model)
+    prompt = synth.prompt_tokens(n_prefill, cfg["vocab"], seed=1)
+    total = n_prefill + n_decode
+    state = be.HipBuffer.from_host(dev, np.array([prompt[0], 0], np.int32))
+    hist = be.HipBuffer.from_host(dev, np.full(total, -1, np.int32))
+    pr = be.HipBuffer.from_host(dev, prompt)
+    kc = be.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    vc = be.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    graph = dev.capture(lambda: m.step(state, kc, vc, hist=hist, hist_cap=total, prompt=pr, prompt_len=n_prefill))
+    t_pre = time_graph(dev, ev, graph, n_prefill)
+    t_dec = time_graph(dev, ev, graph, n_decode)
+    dev.sync()
+    toks = hist.numpy()[n_prefill:]
+    nbytes = sum(decode_bytes_per_token(cfg, p) for p in range(n_prefill, total))
+    out = {"tok_s": round(n_decode / t_dec, 2), "ms_per_token": round(t_dec / n_decode * 1e3, 4),
+           "gb_s": round(nbytes / t_dec / 1e9, 1), "pct_of_hbm_peak": round(100 * nbytes / t_dec / 1e9 / PEAK_HBM_GBS, 2),
+           "bytes_per_token_avg": nbytes // n_decode, "prefill_tokens": n_prefill, "decode_tokens": n_decode,
+           "prefill_ms_per_token": round(t_pre / n_prefill * 1e3, 4),
+           "workload": "BASELINE configs[3]: 26 layers, 2304, 8/4 heads x 256, GeGLU 9216, tied 256000 Q4_0 "
+                       "head, f16 KV cache 4096, token step captured once and replayed",
+           "first_tokens": toks[:4].tolist()}
+    graph.close()
+    m.close()
+    cpu = None
+    if cpu_steps > 0:
+        sys.path.insert(0, str(ROOT))
+        from oracle import orc
+        threads = len(os.sched_getaffinity(0))
+        o = orc.OracleGemma2(model)
+        # a filled cache: positions < n_prefill hold random f16 rows (the
+        # attention work per step depends only on the position)
+        fill = np.random.default_rng(7).standard_normal(o.k_cache.size, dtype=np.float32).astype(np.float16)
+        o.k_cache[:] = fill.view(np.uint16)
+        o.v_cache[:] = fill.view(np.uint16)[::-1]
+        tok, t0 = int(prompt[-1]), time.perf_counter()
+        for i in range(cpu_steps):
+            tok = o.step(tok, n_prefill + i, threads=threads)
+        t_cpu = time.perf_counter() - t0
+        cbytes = sum(decode_bytes_per_token(cfg, p) for p in range(n_prefill, n_prefill + cpu_steps))
+        cpu = {"value": round(cpu_steps / t_cpu, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+               "gb_s": round(cbytes / t_cpu / 1e9, 2),
+               "sample": f"{cpu_steps} decode steps of the oracle token step (orc_gemma2_step) at positions "
+                         f"{n_prefill}..{n_prefill + cpu_steps - 1}, {threads} threads"}
+    return out, cpu
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -133,6 +202,10 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-loop", type=int, default=0,
                     help="only replay the GeGLU kernel graph this many times (for rocprofv3)")
+    ap.add_argument("--decode-prefill", type=int, default=512)
+    ap.add_argument("--decode-tokens", type=int, default=256)
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--cpu-decode-steps", type=int, default=8)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -228,6 +301,15 @@ def main() -> int:
         sys.path.insert(0, str(ROOT))
         from oracle import orc
         cpu = cpu_baseline(orc, synth, args.cpu_seconds)
+    # release the FFN bench buffers before the full model
+    del rot, first, src, dst
+    g_step.close()
+    g_geglu.close()
+    gc.close()
+    decode, decode_cpu = (None, None)
+    if not args.no_decode:
+        decode, decode_cpu = decode_bench(be, synth, dev, ev, args.decode_prefill, args.decode_tokens,
+                                          0 if args.no_cpu else args.cpu_decode_steps)
 
     line = {
         "metric": "Q4_0 matvec GB/s (Gemma-2-2B FFN: fused gate+up GeGLU + down, batch 1)",
@@ -256,6 +338,8 @@ def main() -> int:
                      "traffic": None, "bytes_per_launch": BYTES_GEGLU,
                      "avg_launch_us": round(k_geglu * 1e6, 3)},
         "cpu_baseline": cpu,
+        "decode": decode,
+        "decode_cpu_baseline": decode_cpu,
         "device": {"name": info["name"], "compute_units": info["compute_units"]},
     }
     print(json.dumps(line))

@@ -46,24 +46,35 @@ __device__ __forceinline__ float4 sq4(float4 a) { return make_float4(a.x * a.x, 
 
 // s = 0; s += v[i] for i = 0..n-1, each add rounded (v 16-byte aligned in
 // LDS).  Every lane of the calling wave runs the same chain on broadcast LDS
-// reads; a batch's reads are issued before its adds.
+// reads; the next batch's reads are in flight while the current batch is
+// added, so the chain runs at the rate of its dependent adds.
 __device__ float seq_sum(const float *v, int n)
 {
+    constexpr int B = 8;  // float4 per batch
+    const float4 *v4 = reinterpret_cast<const float4 *>(v);
     float s = 0.0f;
-    int i = 0;
-    for (; i + 32 <= n; i += 32) {
-        float4 b[8];
+    const int nb = n / (4 * B);
+    if (nb > 0) {
+        float4 cur[B];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) b[k] = reinterpret_cast<const float4 *>(v + i)[k];
+        for (int k = 0; k < B; ++k) cur[k] = v4[k];
+        for (int b = 0; b < nb; ++b) {
+            float4 nxt[B];
+            const int nb4 = (b + 1 < nb ? b + 1 : b) * B;  // the last batch re-reads itself
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            s += b[k].x;
-            s += b[k].y;
-            s += b[k].z;
-            s += b[k].w;
+            for (int k = 0; k < B; ++k) nxt[k] = v4[nb4 + k];
+#pragma unroll
+            for (int k = 0; k < B; ++k) {
+                s += cur[k].x;
+                s += cur[k].y;
+                s += cur[k].z;
+                s += cur[k].w;
+            }
+#pragma unroll
+            for (int k = 0; k < B; ++k) cur[k] = nxt[k];
         }
     }
-    for (; i < n; ++i) s += v[i];
+    for (int i = nb * 4 * B; i < n; ++i) s += v[i];
     return s;
 }
 
@@ -302,72 +313,130 @@ __device__ __forceinline__ void attn_window(const int32_t *d_pos, int n_past_arg
 }
 
 // Scores: score[h][p] = (sum_d q_h[d] * k_{start+p}[d], from -0.0 in d
-// order) * scale -- one lane per position, one chain per query head of the
-// group.  Grid (ceil(capacity/64), n_kv_heads) x 64 threads; workgroups past
-// the window exit at once.
-__global__ __launch_bounds__(64) void attn_scores_kernel(const float *__restrict__ q,
-                                                         const uint16_t *__restrict__ k_cache,
-                                                         const int32_t *__restrict__ d_pos, int n_past_arg,
-                                                         int n_heads, int n_kv_heads, float scale, int capacity,
-                                                         float *__restrict__ scores)
+// order) * scale.  Workgroup (tile of 64 positions, kv head) with one wave per
+// query head of the group: the K tile (64 rows x 512 B) is loaded with
+// coalesced 16-byte loads into LDS (rows padded to 520 B so a wave's 8-byte
+// reads of 64 different rows are conflict-free), then lane p of wave g runs
+// the chain of position p for head g (q from LDS as broadcasts).  Workgroups
+// past the window exit at once.
+constexpr int kKRow = kAttnHD * 2 + 8;  // padded K row in LDS, bytes
+
+__global__ __launch_bounds__(512) void attn_scores_kernel(const float *__restrict__ q,
+                                                          const uint16_t *__restrict__ k_cache,
+                                                          const int32_t *__restrict__ d_pos, int n_past_arg,
+                                                          int n_heads, int n_kv_heads, float scale, int capacity,
+                                                          float *__restrict__ scores)
 {
-    constexpr int HD = kAttnHD;
-    __shared__ float q_s[8][HD];
+    constexpr int HD = kAttnHD, P = kScoreP;
+    __shared__ __align__(16) float q_s[8][HD];
+    __shared__ __align__(16) uint8_t k_s[P * kKRow];
     int window, start;
     attn_window(d_pos, n_past_arg, capacity, window, start);
-    const int p0 = blockIdx.x * kScoreP;
+    const int p0 = blockIdx.x * P;
     if (p0 >= window) return;
-    const int kvh = blockIdx.y, G = n_heads / n_kv_heads, lane = threadIdx.x;
-    for (int i = lane; i < G * HD; i += 64) q_s[i / HD][i % HD] = q[(size_t)kvh * G * HD + i];
-    __syncthreads();
-    const int p = p0 + lane;
-    const bool valid = p < window;
+    const int kvh = blockIdx.y, G = n_heads / n_kv_heads, nt = G * 64, tid = threadIdx.x;
     const size_t kv_dim = (size_t)n_kv_heads * HD;
-    const uint4 *krow =
-        reinterpret_cast<const uint4 *>(k_cache + cache_row_of(start + (valid ? p : 0), capacity) * kv_dim +
-                                        (size_t)kvh * HD);
-    float dot[8];
+    // K tile: 64 rows x 32 chunks of 16 B, chunk c of row r at r*32 + c
+    constexpr int kChunks = P * (HD * 2 / 16);
+    for (int base = 0; base < kChunks; base += 16 * 64) {
+        uint4 tmp[16];
 #pragma unroll
-    for (int g = 0; g < 8; ++g) dot[g] = -0.0f;
-    for (int d0 = 0; d0 < HD; d0 += 32) {
-        uint4 kw[4];
+        for (int k = 0; k < 16; ++k) {
+            const int c = base + k * nt + tid;
+            const int r = c >> 5, off = c & 31;
+            const int pr = p0 + r < window ? p0 + r : window - 1;
+            tmp[k] = c < kChunks ? reinterpret_cast<const uint4 *>(
+                                       k_cache + cache_row_of(start + pr, capacity) * kv_dim + (size_t)kvh * HD)[off]
+                                 : make_uint4(0, 0, 0, 0);
+        }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) kw[e] = krow[d0 / 8 + e];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t wd[4] = {kw[e].x, kw[e].y, kw[e].z, kw[e].w};
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const float kf = f16_bits_to_f32((wd[u >> 1] >> (16 * (u & 1))) & 0xffffu);
-                const int d = d0 + e * 8 + u;
-#pragma unroll
-                for (int g = 0; g < 8; ++g)
-                    if (g < G) dot[g] += q_s[g][d] * kf;
+        for (int k = 0; k < 16; ++k) {
+            const int c = base + k * nt + tid;
+            if (c < kChunks) {
+                uint32_t *dst = reinterpret_cast<uint32_t *>(k_s + (c >> 5) * kKRow + (c & 31) * 16);
+                dst[0] = tmp[k].x;
+                dst[1] = tmp[k].y;
+                dst[2] = tmp[k].z;
+                dst[3] = tmp[k].w;
             }
         }
+        if (16 * nt >= kChunks) break;
     }
-    if (valid)
-        for (int g = 0; g < G; ++g) scores[(size_t)(kvh * G + g) * capacity + p] = dot[g] * scale;
+    for (int i = tid; i < G * HD; i += nt) q_s[i / HD][i % HD] = q[(size_t)kvh * G * HD + i];
+    __syncthreads();
+    const int g = tid >> 6, p = tid & 63;
+    const uint8_t *krow = k_s + p * kKRow;
+    const float4 *qg = reinterpret_cast<const float4 *>(q_s[g]);
+    float dot = -0.0f;
+#pragma unroll 8
+    for (int d4 = 0; d4 < HD / 4; ++d4) {
+        const uint2 kw = *reinterpret_cast<const uint2 *>(krow + d4 * 8);
+        const float4 qv = qg[d4];
+        dot += qv.x * f16_bits_to_f32(kw.x & 0xffffu);
+        dot += qv.y * f16_bits_to_f32(kw.x >> 16);
+        dot += qv.z * f16_bits_to_f32(kw.y & 0xffffu);
+        dot += qv.w * f16_bits_to_f32(kw.y >> 16);
+    }
+    if (p0 + p < window) scores[(size_t)(kvh * G + g) * capacity + p0 + p] = dot * scale;
 }
 
 // Softmax and weighted values for query head h (one workgroup of head_dim
 // threads):  max over the window; e_p = expf(score_p - max); sum = 0 + e_0
 // + e_1 + ... in order; p_p = e_p * (1/sum); out[d] = 0 + p_0 v_0[d] + p_1
-// v_1[d] + ... in order.  Writes out (nullable) and the Q8_0 pack of the
-// n_heads*head_dim output (nullable).  LDS: capacity floats plus one.
+// v_1[d] + ... in order.
+//
+// V streams through two LDS slots of 128 rows (64 KB each): while thread d
+// runs its chain over tile t, the loads of tile t+1 (16 x 16 B per thread)
+// are in flight in registers, long enough (~128 dependent steps) to cover
+// the memory latency.  The first tile loads during the softmax.  Writes out
+// (nullable) and the Q8_0 pack of the n_heads*head_dim output (nullable).
+// Dynamic LDS: capacity floats plus 4.
+constexpr int kVT = 128;  // V rows per tile
+
+// A native 4 x 32-bit vector: copies of HIP's uint4 struct lower to memcpy,
+// which keeps an array of them in scratch memory instead of registers.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Tile t of V (rows start + t*kVT ..), thread d: 16-byte chunk (d & 31) of
+// rows (d >> 5) + 8j, j < J; rows past the window reload the last row.
+template <int J>
+__device__ __forceinline__ void v_tile_load(u32x4 (&r)[J], const uint16_t *vbase, int t, int window, int start,
+                                            int capacity, size_t kv_dim, int d)
+{
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        int pr = t * kVT + (d >> 5) + 8 * j;
+        pr = pr < window ? pr : window - 1;
+        r[j] = reinterpret_cast<const u32x4 *>(vbase + cache_row_of(start + pr, capacity) * kv_dim)[d & 31];
+    }
+}
+
+template <int J>
+__device__ __forceinline__ void v_tile_store(const u32x4 (&r)[J], uint16_t *slot, int d)
+{
+#pragma unroll
+    for (int j = 0; j < J; ++j) reinterpret_cast<u32x4 *>(slot + ((d >> 5) + 8 * j) * kAttnHD)[d & 31] = r[j];
+}
+
 __global__ __launch_bounds__(256) void attn_softmax_v_kernel(const float *__restrict__ scores,
                                                              const uint16_t *__restrict__ v_cache,
                                                              const int32_t *__restrict__ d_pos, int n_past_arg,
                                                              int n_heads, int n_kv_heads, int capacity, int expf_fused,
                                                              float *__restrict__ out, uint8_t *__restrict__ pack)
 {
-    constexpr int HD = kAttnHD;
+    constexpr int HD = kAttnHD, J = kVT / 8;  // 16-byte chunks per thread per tile
     extern __shared__ __align__(16) float e_s[];
     __shared__ float red[4];
+    __shared__ __align__(16) uint16_t v_s[2][kVT][HD];
     int window, start;
     attn_window(d_pos, n_past_arg, capacity, window, start);
     const int h = blockIdx.x, d = threadIdx.x, G = n_heads / n_kv_heads, kvh = h / G;
     const float *sc = scores + (size_t)h * capacity;
+    const size_t kv_dim = (size_t)n_kv_heads * HD;
+    const uint16_t *vbase = v_cache + (size_t)kvh * HD;
+    const int ntiles = (window + kVT - 1) / kVT;
+    u32x4 vr[J];
+    v_tile_load<J>(vr, vbase, 0, window, start, capacity, kv_dim, d);
 
     float mx = -INFINITY;
     for (int p = d; p < window; p += HD) mx = fmaxf(mx, sc[p]);
@@ -383,6 +452,7 @@ __global__ __launch_bounds__(256) void attn_softmax_v_kernel(const float *__rest
         const float sum = seq_sum(e_s, window);
         if (d == 0) *bcast = sum;
     }
+    v_tile_store<J>(vr, &v_s[0][0][0], d);
     __syncthreads();
     const float sum = *bcast;
     if (sum > 0.0f) {
@@ -391,18 +461,31 @@ __global__ __launch_bounds__(256) void attn_softmax_v_kernel(const float *__rest
     }
     __syncthreads();
 
-    const size_t kv_dim = (size_t)n_kv_heads * HD;
-    const uint16_t *vcol = v_cache + (size_t)kvh * HD + d;
     float acc = 0.0f;
-    int p = 0;
-    for (; p + 8 <= window; p += 8) {
-        uint16_t vb[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) vb[u] = vcol[cache_row_of(start + p + u, capacity) * kv_dim];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) acc += e_s[p + u] * f16_bits_to_f32(vb[u]);
+    for (int t = 0; t < ntiles; ++t) {
+        // past the last tile this reloads the last one (unconditional code
+        // keeps the prefetch in registers); its copy lands in an unread slot
+        v_tile_load<J>(vr, vbase, t + 1 < ntiles ? t + 1 : t, window, start, capacity, kv_dim, d);
+        const uint16_t *vt = &v_s[t & 1][0][d];
+        const int np = window - t * kVT < kVT ? window - t * kVT : kVT;
+        if (np == kVT) {
+            const float4 *ep = reinterpret_cast<const float4 *>(e_s + t * kVT);
+#pragma unroll 8
+            for (int p4 = 0; p4 < kVT / 4; ++p4) {
+                const float4 e4 = ep[p4];
+                acc += e4.x * f16_bits_to_f32(vt[(4 * p4 + 0) * HD]);
+                acc += e4.y * f16_bits_to_f32(vt[(4 * p4 + 1) * HD]);
+                acc += e4.z * f16_bits_to_f32(vt[(4 * p4 + 2) * HD]);
+                acc += e4.w * f16_bits_to_f32(vt[(4 * p4 + 3) * HD]);
+            }
+        } else {
+            const float *e1 = e_s + t * kVT;
+            for (int p = 0; p < np; ++p) acc += e1[p] * f16_bits_to_f32(vt[p * HD]);
+        }
+        // slot (t+1)&1 was last read in tile t-1, before the previous barrier
+        v_tile_store<J>(vr, &v_s[(t + 1) & 1][0][0], d);
+        __syncthreads();
     }
-    for (; p < window; ++p) acc += e_s[p] * f16_bits_to_f32(vcol[cache_row_of(start + p, capacity) * kv_dim]);
 
     if (out) out[(size_t)h * HD + d] = acc;
     if (pack) {
@@ -467,7 +550,7 @@ int launch_rope_kv_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache, uint16_
 }
 
 int attn_head_dim() { return kAttnHD; }
-int attn_max_capacity() { return 16000; }  // the window's softmax weights live in LDS
+int attn_max_capacity() { return 6144; }  // the window's softmax weights share LDS with two 64 KB V tiles
 
 size_t attn_scratch_bytes(int n_heads, int capacity) { return (size_t)n_heads * capacity * sizeof(float); }
 
@@ -477,8 +560,8 @@ int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_
 {
     float *scores = reinterpret_cast<float *>(scratch);
     const dim3 sgrid((capacity + kScoreP - 1) / kScoreP, n_kv_heads);
-    hipLaunchKernelGGL(attn_scores_kernel, sgrid, dim3(64), 0, ctx->stream, q, k_cache, d_pos, n_past, n_heads,
-                       n_kv_heads, scale, capacity, scores);
+    hipLaunchKernelGGL(attn_scores_kernel, sgrid, dim3(64 * (n_heads / n_kv_heads)), 0, ctx->stream, q, k_cache,
+                       d_pos, n_past, n_heads, n_kv_heads, scale, capacity, scores);
     if (int rc = check_launch(ctx, "attn_scores_kernel")) return rc;
     hipLaunchKernelGGL(attn_softmax_v_kernel, dim3(n_heads), dim3(kAttnHD), (size_t)capacity * sizeof(float) + 16,
                        ctx->stream, scores, v_cache, d_pos, n_past, n_heads, n_kv_heads, capacity,
