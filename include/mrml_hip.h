@@ -208,7 +208,7 @@ int mrml_hip_argmax_f32(mrml_hip_ctx *ctx, const float *d_x, int32_t n, int32_t 
 /* CudaDevice::rms_norm (cuda.rs:2102-2180; CPU ops.rs:24-79):
  * out = (x * (1/sqrt(sum(x^2)/dim + eps))) * w.  d_w nullable (no weight).
  * d_out (f32) and d_pack (the Q8_0 activation pack of the result, for the
- * next matvec) are each nullable, not both.  dim % 32 == 0, dim <= 16384. */
+ * next matvec) are each nullable, not both.  dim % 32 == 0, dim <= 12288. */
 int mrml_hip_rms_norm(mrml_hip_ctx *ctx, const float *d_x, const float *d_w, float *d_out, void *d_pack,
                       int32_t dim, float eps);
 /* Gemma-2 sandwich-norm residual, then the next block's pre-norm (the

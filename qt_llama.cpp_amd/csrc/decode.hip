@@ -23,13 +23,15 @@
 #include <math.h>
 
 #include "device.h"
+#include "exact_sum.h"
 #include "internal.h"
 
 namespace mrml {
 
 namespace {
 
-constexpr int kMaxChunks = 4;  // float4 chunks per thread: dim <= 16 * blockDim
+constexpr int kMaxChunks = 4;        // float4 chunks per thread: dim <= 16 * blockDim
+constexpr int kNormMaxThreads = 768;  // keeps ~170 VGPRs per lane for the norm kernels
 constexpr int kScoreP = 64;    // cache positions per score workgroup (one per lane)
 constexpr int kAttnHD = 256;   // head_dim served by the attention kernels
 
@@ -79,26 +81,27 @@ __device__ float seq_sum(const float *v, int n)
 }
 
 // Sum of squares of the values held in v (chunks c = tid + k*blockDim), in
-// index order from +0: squares staged in LDS by all threads, summed by wave
-// 0, broadcast back.  `lds` holds n4*4 floats plus one.
-__device__ float block_seq_sum_sq(const float4 (&v)[kMaxChunks], int n4, float *lds)
+// index order from +0 (ops.rs:24-79), bit for bit: the sequential f32 sum
+// evaluated in parallel (exact_sum.h).  With one chunk per thread the terms
+// stay in registers; otherwise they are staged in LDS.  `lds` is laid out by
+// norm_lds().
+template <int CH>
+__device__ float block_seq_sum_sq(const float4 (&v)[CH], int n4, float *lds)
 {
+    if constexpr (CH == 1) {
+        auto *x = reinterpret_cast<mrml_xsum::Shared4 *>(lds);
+        return mrml_xsum::block_seq_sum_nonneg4(sq4(v[0]), n4 * 4, *x);
+    }
     float4 *sq = reinterpret_cast<float4 *>(lds);
-    float *bcast = lds + n4 * 4;
 #pragma unroll
-    for (int k = 0; k < kMaxChunks; ++k) {
+    for (int k = 0; k < CH; ++k) {
         const int c = threadIdx.x + k * blockDim.x;
         if (c < n4) sq[c] = sq4(v[k]);
     }
     __syncthreads();
-    if (threadIdx.x < 64) {
-        const float s = seq_sum(lds, n4 * 4);
-        if (threadIdx.x == 0) *bcast = s;
-    }
-    __syncthreads();
-    const float s = *bcast;
-    __syncthreads();  // lds is reused by the caller
-    return s;
+    uint8_t *flags = reinterpret_cast<uint8_t *>(lds + n4 * 4);
+    auto *x = reinterpret_cast<mrml_xsum::Shared *>(flags + ((n4 * 4 + 15) & ~15));
+    return mrml_xsum::block_seq_sum_nonneg(lds, n4 * 4, flags, *x);
 }
 
 // ops.rs:24-79: mean = sum/dim, scale = 1/sqrt(mean + eps) (IEEE sqrt and
@@ -127,12 +130,13 @@ __device__ __forceinline__ void emit_q8(float4 v, int c, int n4, uint8_t *pack, 
 
 // out = (x * scale) * w per value (w nullable), stored to out (nullable) and
 // as a Q8_0 pack (nullable).
-__device__ __forceinline__ void norm_store(const float4 (&v)[kMaxChunks], float scale, const float *w, float *out,
+template <int CH>
+__device__ __forceinline__ void norm_store(const float4 (&v)[CH], float scale, const float *w, float *out,
                                            uint8_t *pack, int n4)
 {
     const float4 *w4 = reinterpret_cast<const float4 *>(w);
 #pragma unroll
-    for (int k = 0; k < kMaxChunks; ++k) {
+    for (int k = 0; k < CH; ++k) {
         if (k * (int)blockDim.x >= n4) break;  // uniform
         const int c = threadIdx.x + k * blockDim.x;
         float4 o = scale4(v[k], scale);
@@ -144,16 +148,17 @@ __device__ __forceinline__ void norm_store(const float4 (&v)[kMaxChunks], float 
 
 // out = rms_norm(x, w) (CudaDevice::rms_norm, cuda.rs:2102-2180; CPU
 // ops.rs:24-79), optionally also as a Q8_0 pack.  One workgroup.
-__global__ __launch_bounds__(1024) void rms_norm_kernel(const float *__restrict__ x, const float *__restrict__ w,
+template <int CH>
+__global__ __launch_bounds__(kNormMaxThreads) void rms_norm_kernel(const float *__restrict__ x, const float *__restrict__ w,
                                                         float eps, float *__restrict__ out,
                                                         uint8_t *__restrict__ pack, int dim)
 {
     extern __shared__ __align__(16) float lds[];
     const int n4 = dim >> 2;
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
-    float4 v[kMaxChunks];
+    float4 v[CH];
 #pragma unroll
-    for (int k = 0; k < kMaxChunks; ++k) {
+    for (int k = 0; k < CH; ++k) {
         const int c = threadIdx.x + k * blockDim.x;
         v[k] = c < n4 ? x4[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
@@ -164,7 +169,8 @@ __global__ __launch_bounds__(1024) void rms_norm_kernel(const float *__restrict_
 // pre-norm (the per-layer order of model.rs:1185-2260):
 //   h  = h + rms_norm(t, w_post)
 //   xn = rms_norm(h, w_next)      -> xn (nullable) and its Q8_0 pack (nullable)
-__global__ __launch_bounds__(1024) void residual_rms_norm_kernel(const float *__restrict__ t,
+template <int CH>
+__global__ __launch_bounds__(kNormMaxThreads) void residual_rms_norm_kernel(const float *__restrict__ t,
                                                                  const float *__restrict__ w_post,
                                                                  float *__restrict__ h,
                                                                  const float *__restrict__ w_next, float eps,
@@ -176,22 +182,26 @@ __global__ __launch_bounds__(1024) void residual_rms_norm_kernel(const float *__
     const float4 *t4 = reinterpret_cast<const float4 *>(t);
     float4 *h4 = reinterpret_cast<float4 *>(h);
     const float4 *wp4 = reinterpret_cast<const float4 *>(w_post);
-    float4 v[kMaxChunks];
+    const float4 one4 = make_float4(1.0f, 1.0f, 1.0f, 1.0f), zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    // every operand's load is issued before the first sum
+    float4 v[CH], hv[CH], wv[CH];
 #pragma unroll
-    for (int k = 0; k < kMaxChunks; ++k) {
+    for (int k = 0; k < CH; ++k) {
         const int c = threadIdx.x + k * blockDim.x;
-        v[k] = c < n4 ? t4[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const int cc = c < n4 ? c : 0;
+        v[k] = c < n4 ? t4[cc] : zero4;
+        hv[k] = h4[cc];
+        wv[k] = w_post ? wp4[cc] : one4;
     }
     const float s1 = rms_scale(block_seq_sum_sq(v, n4, lds), dim, eps);
 #pragma unroll
-    for (int k = 0; k < kMaxChunks; ++k) {
+    for (int k = 0; k < CH; ++k) {
         const int c = threadIdx.x + k * blockDim.x;
-        const int cc = c < n4 ? c : 0;
         float4 tn = scale4(v[k], s1);
-        if (w_post) tn = mul4(tn, wp4[cc]);
-        const float4 hn = add4(h4[cc], tn);
+        if (w_post) tn = mul4(tn, wv[k]);
+        const float4 hn = add4(hv[k], tn);
         if (c < n4) h4[c] = hn;
-        v[k] = c < n4 ? hn : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[k] = c < n4 ? hn : zero4;
     }
     if (!xn && !pack) return;
     norm_store(v, rms_scale(block_seq_sum_sq(v, n4, lds), dim, eps), w_next, xn, pack, n4);
@@ -203,7 +213,8 @@ __global__ __launch_bounds__(1024) void residual_rms_norm_kernel(const float *__
 // value (q * d) * scale.  With w_norm or pack set it also writes
 // rms_norm(h, w_norm) as f32 (xn) and/or as a Q8_0 pack -- the first layer's
 // pre-norm.
-__global__ __launch_bounds__(1024) void embedding_kernel(const uint8_t *__restrict__ table, int type,
+template <int CH>
+__global__ __launch_bounds__(kNormMaxThreads) void embedding_kernel(const uint8_t *__restrict__ table, int type,
                                                          const int32_t *__restrict__ d_token, int token, float scale,
                                                          float *__restrict__ h, const float *__restrict__ w_norm,
                                                          float eps, float *__restrict__ xn,
@@ -214,9 +225,9 @@ __global__ __launch_bounds__(1024) void embedding_kernel(const uint8_t *__restri
     tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
     const int n4 = dim >> 2, nb = dim >> 5;
     const size_t nblk = (size_t)vocab * nb, row = (size_t)tok * nb;
-    float4 v[kMaxChunks];
+    float4 v[CH];
 #pragma unroll
-    for (int k = 0; k < kMaxChunks; ++k) {
+    for (int k = 0; k < CH; ++k) {
         const int c_raw = threadIdx.x + k * blockDim.x;
         const int c = c_raw < n4 ? c_raw : n4 - 1;
         const int b = c >> 3, p = (c & 7) * 4;  // block, first value index within it
@@ -501,41 +512,63 @@ __global__ __launch_bounds__(256) void attn_softmax_v_kernel(const float *__rest
     }
 }
 
+// One float4 chunk per thread where the workgroup allows (the exact sum's
+// per-thread share of terms stays small).
 inline int norm_threads(int dim)
 {
     const int n4 = dim / 4;
-    int t = (n4 + kMaxChunks - 1) / kMaxChunks;
+    int t = n4 <= kNormMaxThreads ? n4 : (n4 + kMaxChunks - 1) / kMaxChunks;
     t = (t + 63) / 64 * 64;
     return t < 64 ? 64 : t;
 }
 
-inline size_t norm_lds(int dim) { return (size_t)dim * sizeof(float) + 16; }
+// dims up to 4*kNormMaxThreads: one float4 chunk per thread, terms in registers
+inline bool norm_one_chunk(int dim) { return dim / 4 <= kNormMaxThreads; }
+
+inline size_t norm_lds(int dim)
+{
+    if (norm_one_chunk(dim)) return sizeof(mrml_xsum::Shared4);
+    return (size_t)dim * sizeof(float) + (((size_t)dim + 15) & ~(size_t)15) + sizeof(mrml_xsum::Shared);
+}
 
 }  // namespace
 
-bool norm_dim_ok(int dim) { return dim > 0 && dim % 32 == 0 && dim <= 16 * 1024; }
+bool norm_dim_ok(int dim) { return dim > 0 && dim % 32 == 0 && dim <= 4 * kMaxChunks * kNormMaxThreads; }
 
 int launch_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float eps, float *out, void *pack, int dim)
 {
-    hipLaunchKernelGGL(rms_norm_kernel, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, x, w, eps, out,
-                       (uint8_t *)pack, dim);
+    if (norm_one_chunk(dim))
+        hipLaunchKernelGGL(rms_norm_kernel<1>, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, x, w, eps,
+                           out, (uint8_t *)pack, dim);
+    else
+        hipLaunchKernelGGL(rms_norm_kernel<kMaxChunks>, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, x,
+                           w, eps, out, (uint8_t *)pack, dim);
     return check_launch(ctx, "rms_norm_kernel");
 }
 
 int launch_residual_rms_norm(mrml_hip_ctx *ctx, const float *t, const float *w_post, float *h, const float *w_next,
                              float eps, float *xn, void *pack, int dim)
 {
-    hipLaunchKernelGGL(residual_rms_norm_kernel, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, t,
-                       w_post, h, w_next, eps, xn, (uint8_t *)pack, dim);
+    if (norm_one_chunk(dim))
+        hipLaunchKernelGGL(residual_rms_norm_kernel<1>, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, t,
+                           w_post, h, w_next, eps, xn, (uint8_t *)pack, dim);
+    else
+        hipLaunchKernelGGL(residual_rms_norm_kernel<kMaxChunks>, dim3(1), dim3(norm_threads(dim)), norm_lds(dim),
+                           ctx->stream, t, w_post, h, w_next, eps, xn, (uint8_t *)pack, dim);
     return check_launch(ctx, "residual_rms_norm_kernel");
 }
 
 int launch_embedding(mrml_hip_ctx *ctx, const void *table, int type, const int32_t *d_token, int token, float scale,
                      float *h, const float *w_norm, float eps, float *xn, void *pack, int dim, int vocab)
 {
-    hipLaunchKernelGGL(embedding_kernel, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream,
-                       (const uint8_t *)table, type, d_token, token, scale, h, w_norm, eps, xn, (uint8_t *)pack, dim,
-                       vocab);
+    if (norm_one_chunk(dim))
+        hipLaunchKernelGGL(embedding_kernel<1>, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream,
+                           (const uint8_t *)table, type, d_token, token, scale, h, w_norm, eps, xn, (uint8_t *)pack, dim,
+                           vocab);
+    else
+        hipLaunchKernelGGL(embedding_kernel<kMaxChunks>, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream,
+                           (const uint8_t *)table, type, d_token, token, scale, h, w_norm, eps, xn, (uint8_t *)pack, dim,
+                           vocab);
     return check_launch(ctx, "embedding_kernel");
 }
 

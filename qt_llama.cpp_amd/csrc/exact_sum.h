@@ -1,0 +1,437 @@
+// exact_sum.h -- the sequential f32 sum of non-negative terms, evaluated in
+// parallel with the same result bit for bit.
+//
+// The reference sums squares (RMSNorm, ops.rs:24-79) and softmax terms
+// (ops.rs:133-158) in a loop: s = 0; s = RN(s + a_k), k = 0..n-1.  A single
+// GPU lane doing that costs one dependent add (plus operand traffic) per
+// term.  For a_k >= 0 the loop can be compressed exactly:
+//
+//  * While s stays in one binade [2^e, 2^(e+1)) the representable values
+//    are the multiples of u = 2^(e-23), so RN(s + a_k) = s + u * RNI(a_k/u)
+//    (round to nearest integer), where only an exact tie (a_k/u = n + 1/2)
+//    depends on s (its parity).  Steps that provably start and end in the
+//    same binade and are not ties therefore each add a fixed integer number
+//    of ulps, and a run of them adds u * (sum of those integers) -- an
+//    exactly representable amount, so one f32 add reproduces the whole run.
+//  * "Provably" uses approximate prefix sums P_k (any summation order): the
+//    sequential s_k satisfies |s_k - P_k| <= (k+1) 2^-24 s_k (each rounding
+//    errs by at most 2^-24 relative and s is non-decreasing), and a tree of
+//    depth D adds at most D 2^-24 relative error to P_k; a step is classed
+//    safe when P_{k-1} and P_k clear the binade boundaries by twice that.
+//  * Every other step (the first, crossings of a binade boundary, ties,
+//    s near 0) stays an event of its own, s = RN(s + a_k).
+//
+// So the sum becomes a short sequential f32 sum over events (each run's exact
+// addend, each unsafe term) whose result equals the original loop's.  The
+// classification is per term and order-free; only the ~tens of events are
+// added in sequence.  Functions are host+device so the host tests can run
+// the same classification against the plain loop.
+#pragma once
+
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define MRML_XS_HD __host__ __device__ __forceinline__
+#else
+#define MRML_XS_HD static inline
+#endif
+
+namespace mrml_xsum {
+
+MRML_XS_HD float pow2f(int e)  // 2^e for -126 <= e <= 127
+{
+    return __builtin_bit_cast(float, (uint32_t)(e + 127) << 23);
+}
+
+// Depth allowance of the approximate prefix sums (terms per thread plus the
+// scan levels of a workgroup of up to 1024 threads): P_k is within
+// kDepth * 2^-24 of the exact prefix sum, relatively.
+constexpr int kDepth = 64;
+
+struct Step {
+    int safe;   // 1: the step adds exactly inc * u
+    int inc;    // integer number of ulps added
+    float u;    // ulp of the binade the step stays in
+};
+
+// Classify step k (a = a_k >= 0 finite, pm ~ P_{k-1}, pk ~ P_k).  Written
+// without early returns: on the GPU the lanes of a wave evaluate it in step.
+MRML_XS_HD Step classify(float a, float pm, float pk, int k)
+{
+    const bool in_range = k > 0 && pm >= 0x1p-100f && pk < 0x1p+120f;
+    const float pmc = in_range ? pm : 1.0f;                                        // keeps e in range
+    const int e = (int)((__builtin_bit_cast(uint32_t, pmc) >> 23) & 0xffu) - 127;  // binade of P_{k-1}
+    const float rho = (float)(2 * (k + 1 + kDepth)) * 0x1p-24f;                    // twice the bound
+    const float lo = pow2f(e), hi = pow2f(e + 1), u = pow2f(e - 23);
+    const bool starts_in = pmc - pmc * rho >= lo;        // s_{k-1} surely >= 2^e
+    const bool ends_in = pk + pk * rho + u < hi;         // s_{k-1} + a_k surely < 2^(e+1) - u
+    const float q = a * pow2f(23 - e);                   // exact when safe: a < 2^(e+1)
+    const float r = __builtin_floorf(q);
+    const float f = q - r;                               // exact
+    Step st;
+    st.safe = (in_range && starts_in && ends_in && f != 0.5f) ? 1 : 0;  // a tie depends on s's parity
+    st.inc = st.safe ? (int)r + (f > 0.5f ? 1 : 0) : 0;
+    st.u = u;
+    return st;
+}
+
+#if defined(__HIPCC__)
+
+// ---- workgroup implementation ---------------------------------------------------
+
+constexpr int kMaxPerThread = 16;  // terms per thread (n <= 16 * blockDim)
+constexpr int kEventCap = 512;     // events held in LDS; more falls back to the plain loop
+
+// LDS of one call: n bytes of flags plus this struct (16-byte aligned).
+struct Shared {
+    float add[kEventCap];  // event addends, in order
+    float u[kEventCap];    // ulp of a run (0 for a single term)
+    int Rs[kEventCap];     // a run's ulp prefix before its first term
+    int Re[kEventCap];     // a run's ulp prefix after its last term
+    float wtot[16];        // per-wave totals of the approximate prefix scan
+    int wcnt[16];          // per-wave event counts
+    int winc[16];          // per-wave sums of the safe terms' ulp counts
+    float result;
+};
+
+// Inclusive scans over the 64 lanes of a wave with DPP: row_shr 1, 2, 4, 8
+// within each 16-lane row (lanes shifted in from outside the row read 0),
+// then row_bcast 15 and 31 carry row totals into the following rows.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_i32(int v)
+{
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, true);
+}
+
+__device__ __forceinline__ int wave_incl_scan_i32(int v)
+{
+    v += dpp_i32<0x111, 0xf>(v);  // row_shr:1
+    v += dpp_i32<0x112, 0xf>(v);  // row_shr:2
+    v += dpp_i32<0x114, 0xf>(v);  // row_shr:4
+    v += dpp_i32<0x118, 0xf>(v);  // row_shr:8
+    v += dpp_i32<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_i32<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f32(float v)
+{
+    return __builtin_bit_cast(float, dpp_i32<CTRL, ROW_MASK>(__builtin_bit_cast(int, v)));
+}
+
+__device__ __forceinline__ float wave_incl_scan_f32(float v)
+{
+    v += dpp_f32<0x111, 0xf>(v);
+    v += dpp_f32<0x112, 0xf>(v);
+    v += dpp_f32<0x114, 0xf>(v);
+    v += dpp_f32<0x118, 0xf>(v);
+    v += dpp_f32<0x142, 0xa>(v);
+    v += dpp_f32<0x143, 0xc>(v);
+    return v;
+}
+
+// s = 0; s = RN(s + a[k]) for k = 0..n-1 over a[] in LDS (a[k] >= 0, finite),
+// computed by the whole workgroup (blockDim a multiple of 64, at most 1024,
+// n <= kMaxPerThread * blockDim).  flags: n bytes of LDS.  Returns the
+// result in every thread; ends with a barrier, so a and x may be reused.
+__device__ float block_seq_sum_nonneg(const float *a, int n, uint8_t *flags, Shared &x)
+{
+    const int nt = blockDim.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
+    const int C = (n + nt - 1) / nt;
+    const int k0 = tid * C;
+    // approximate prefix sums: thread-local sequential, then the block scan
+    float av[kMaxPerThread], lp[kMaxPerThread];
+    float run = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxPerThread; ++i) {
+        av[i] = 0.0f;
+        if (i < C) {
+            const int k = k0 + i;
+            av[i] = k < n ? a[k] : 0.0f;
+            run += av[i];
+            lp[i] = run;
+        }
+    }
+    const float wincl = wave_incl_scan_f32(run);
+    if (lane == 63) x.wtot[wave] = wincl;
+    __syncthreads();
+    // exclusive prefix from the previous lane's inclusive one (wincl - run
+    // would lose the relative accuracy the classification relies on)
+    float base = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, wincl), 0x138,
+                                                                        0xf, 0xf, true));  // wave_shr:1
+    for (int w = 0; w < wave; ++w) base += x.wtot[w];
+    // classify each term, flag the unsafe ones
+    int inc[kMaxPerThread];  // ulps added by a safe term, -1 for an unsafe one
+    float uu[kMaxPerThread];
+    int my_inc = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxPerThread; ++i) {
+        inc[i] = -1;
+        uu[i] = 0.0f;
+        if (i < C) {
+            const int k = k0 + i;
+            if (k < n) {
+                const float pm = i ? base + lp[i - 1] : base;
+                const Step st = classify(av[i], pm, base + lp[i], k);
+                inc[i] = st.safe ? st.inc : -1;
+                uu[i] = st.u;
+                flags[k] = st.safe ? 0 : 1;
+                my_inc += st.safe ? st.inc : 0;
+            }
+        }
+    }
+    __syncthreads();
+    // events: every unsafe term, and every safe term that follows an unsafe
+    // one; with the running count of safe ulps, a run's total is its end
+    // prefix minus its start prefix
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxPerThread; ++i) {
+        const int k = k0 + i;
+        if (i < C && k < n && (flags[k] || k == 0 || flags[k - 1])) ++cnt;
+    }
+    const int cincl = wave_incl_scan_i32(cnt);
+    const int iincl = wave_incl_scan_i32(my_inc);
+    if (lane == 63) {
+        x.wcnt[wave] = cincl;
+        x.winc[wave] = iincl;
+    }
+    __syncthreads();
+    int ebase = cincl - cnt, ibase = iincl - my_inc, nev = 0;
+    for (int w = 0; w < nw; ++w) {
+        if (w < wave) {
+            ebase += x.wcnt[w];
+            ibase += x.winc[w];
+        }
+        nev += x.wcnt[w];
+    }
+    if (nev > kEventCap) {
+        // too many events for LDS (e.g. many exact ties): the plain loop
+        if (tid < 64) {
+            float s = 0.0f;
+            for (int k = 0; k < n; ++k) s += a[k];
+            if (tid == 0) x.result = s;
+        }
+        __syncthreads();
+        const float r = x.result;
+        __syncthreads();
+        return r;
+    }
+    int E = ebase - 1, pre = ibase;
+#pragma unroll
+    for (int i = 0; i < kMaxPerThread; ++i) {
+        const int k = k0 + i;
+        if (i < C && k < n) {
+            const bool start = flags[k] || k == 0 || flags[k - 1];
+            const bool last = k == n - 1 || flags[k + 1];  // the next term starts an event
+            if (start) ++E;
+            if (inc[i] < 0) {
+                x.add[E] = av[i];
+                x.u[E] = 0.0f;
+            } else {
+                if (start) {
+                    x.u[E] = uu[i];
+                    x.Rs[E] = pre;  // each run has one first and one last term
+                }
+                pre += inc[i];
+                if (last) x.Re[E] = pre;
+            }
+        }
+    }
+    __syncthreads();
+    for (int j = tid; j < nev; j += nt)
+        if (x.u[j] > 0.0f) x.add[j] = (float)(x.Re[j] - x.Rs[j]) * x.u[j];  // exact: < 2^24 ulps, u a power of 2
+    __syncthreads();
+    if (tid < 64) {
+        float s = 0.0f;
+        int j = 0;
+        for (; j + 8 <= nev; j += 8) {
+            float4 b0 = *reinterpret_cast<const float4 *>(&x.add[j]);
+            float4 b1 = *reinterpret_cast<const float4 *>(&x.add[j + 4]);
+            s += b0.x;
+            s += b0.y;
+            s += b0.z;
+            s += b0.w;
+            s += b1.x;
+            s += b1.y;
+            s += b1.z;
+            s += b1.w;
+        }
+        for (; j < nev; ++j) s += x.add[j];
+        if (tid == 0) x.result = s;
+    }
+    __syncthreads();
+    const float r = x.result;
+    __syncthreads();
+    return r;
+}
+
+// The same sum when thread t holds terms 4t..4t+3 in registers (n <= 4 *
+// blockDim; terms at or past n are ignored) -- the layout of the norm
+// kernels, where it needs no LDS copy of the terms and five barriers.
+// Neighbouring threads' unsafe flags travel by DPP within a wave and through
+// LDS across waves; each run's addend is formed during the walk.
+struct Shared4 {
+    float add[kEventCap];  // a single term's value, or the run's ulp (u)
+    int Rs[kEventCap];     // a run's ulp prefix before its first term (-1 marks a single term)
+    int Re[kEventCap];     // a run's ulp prefix after its last term
+    float wtot[16];
+    int wcnt[16], winc[16];
+    int wfirst[16], wlast[16];  // unsafe masks of each wave's first and last lanes
+    float result;
+};
+
+__device__ __forceinline__ int wave_shr1_i32(int v)  // lane l gets lane l-1 (lane 0: 0)
+{
+    return __builtin_amdgcn_update_dpp(0, v, 0x138, 0xf, 0xf, true);
+}
+__device__ __forceinline__ int wave_shl1_i32(int v)  // lane l gets lane l+1 (lane 63: 0)
+{
+    return __builtin_amdgcn_update_dpp(0, v, 0x130, 0xf, 0xf, true);
+}
+
+__device__ float block_seq_sum_nonneg4(float4 v, int n, Shared4 &x)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int k0 = 4 * tid;
+    const float a[4] = {v.x, v.y, v.z, v.w};
+    float lp[4], run = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        run += k0 + i < n ? a[i] : 0.0f;
+        lp[i] = run;
+    }
+    const float wincl = wave_incl_scan_f32(run);
+    if (lane == 63) x.wtot[wave] = wincl;
+    __syncthreads();  // 1
+    float base = __builtin_bit_cast(float, wave_shr1_i32(__builtin_bit_cast(int, wincl)));
+    {
+        float t[16];
+#pragma unroll
+        for (int w = 0; w < 16; ++w) t[w] = w < nw ? x.wtot[w] : 0.0f;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) base += w < wave ? t[w] : 0.0f;
+    }
+    int inc[4], mask = 0, my_inc = 0;
+    float uu[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int k = k0 + i;
+        const Step st = classify(a[i], i ? base + lp[i - 1] : base, base + lp[i], k);
+        const bool in = k < n;
+        inc[i] = (in && st.safe) ? st.inc : -1;
+        uu[i] = st.u;
+        mask |= (in && !st.safe) ? (1 << i) : 0;
+        my_inc += inc[i] > 0 ? inc[i] : 0;
+    }
+    if (lane == 0) x.wfirst[wave] = mask;
+    if (lane == 63) x.wlast[wave] = mask;
+    __syncthreads();  // 2
+    int prev = wave_shr1_i32(mask), next = wave_shl1_i32(mask);
+    if (lane == 0) prev = wave > 0 ? x.wlast[wave - 1] : 0;
+    if (lane == 63) next = wave + 1 < nw ? x.wfirst[wave + 1] : 0;
+    // term i starts an event when it is unsafe or follows an unsafe term
+    // (term 0 of the sum is always unsafe); it ends a run when the next term
+    // is unsafe or it is the last term
+    const int prev_bit3 = (prev >> 3) & 1, next_bit0 = next & 1;
+    int cnt = 0;
+    bool start[4], last[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int k = k0 + i;
+        const bool before = i ? ((mask >> (i - 1)) & 1) : prev_bit3;
+        const bool after = i < 3 ? ((mask >> (i + 1)) & 1) : next_bit0;
+        start[i] = k < n && (((mask >> i) & 1) || before);
+        last[i] = k < n && (after || k == n - 1);
+        cnt += start[i] ? 1 : 0;
+    }
+    const int cincl = wave_incl_scan_i32(cnt), iincl = wave_incl_scan_i32(my_inc);
+    if (lane == 63) {
+        x.wcnt[wave] = cincl;
+        x.winc[wave] = iincl;
+    }
+    __syncthreads();  // 3
+    int ebase = cincl - cnt, ibase = iincl - my_inc, nev = 0;
+    {
+        int c[16], ic[16];
+#pragma unroll
+        for (int w = 0; w < 16; ++w) {
+            c[w] = w < nw ? x.wcnt[w] : 0;
+            ic[w] = w < nw ? x.winc[w] : 0;
+        }
+#pragma unroll
+        for (int w = 0; w < 16; ++w) {
+            ebase += w < wave ? c[w] : 0;
+            ibase += w < wave ? ic[w] : 0;
+            nev += c[w];
+        }
+    }
+    if (nev > kEventCap) {
+        // too many events for LDS (e.g. many exact ties): the plain loop
+        // over the terms, staged through the event buffer in pieces
+        float s = 0.0f;
+        for (int c0 = 0; c0 < n; c0 += kEventCap) {
+            __syncthreads();
+            for (int i = 0; i < 4; ++i) {
+                const int k = k0 + i;
+                if (k >= c0 && k < c0 + kEventCap && k < n) x.add[k - c0] = a[i];
+            }
+            __syncthreads();
+            if (tid < 64) {
+                const int m = n - c0 < kEventCap ? n - c0 : kEventCap;
+                for (int j = 0; j < m; ++j) s += x.add[j];
+            }
+        }
+        if (tid == 0) x.result = s;
+        __syncthreads();
+        const float r = x.result;
+        __syncthreads();
+        return r;
+    }
+    int E = ebase - 1, pre = ibase;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (start[i]) ++E;
+        if (k0 + i < n) {
+            if (inc[i] < 0) {
+                x.add[E] = a[i];
+                x.Rs[E] = -1;
+            } else {
+                if (start[i]) {
+                    x.add[E] = uu[i];
+                    x.Rs[E] = pre;
+                }
+                pre += inc[i];
+                if (last[i]) x.Re[E] = pre;
+            }
+        }
+    }
+    __syncthreads();  // 4
+    if (tid < 64) {
+        // lane j forms event j's addend (a run adds (Re - Rs) ulps: exact,
+        // fewer than 2^24 of them and u a power of 2); the ordered sum then
+        // takes the lanes one by one, with no memory access on its chain
+        float s = 0.0f;
+        for (int j0 = 0; j0 < nev; j0 += 64) {
+            const int j = j0 + lane;
+            float val = 0.0f;
+            if (j < nev) {
+                const int rs = x.Rs[j];
+                val = rs < 0 ? x.add[j] : (float)(x.Re[j] - rs) * x.add[j];
+            }
+            const int m = nev - j0 < 64 ? nev - j0 : 64;
+            for (int l = 0; l < m; ++l)
+                s += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, val), l));
+        }
+        if (tid == 0) x.result = s;
+    }
+    __syncthreads();  // 5
+    const float r = x.result;
+    __syncthreads();
+    return r;
+}
+
+#endif  // __HIPCC__
+
+}  // namespace mrml_xsum

@@ -51,7 +51,7 @@ int check_model_config(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config &c)
     REQUIRE(ctx, c.n_heads % c.n_kv_heads == 0 && c.n_heads / c.n_kv_heads <= 8,
             "gemma2: n_heads=%d must be a multiple of n_kv_heads=%d with a group of at most 8", c.n_heads,
             c.n_kv_heads);
-    REQUIRE(ctx, norm_dim_ok(c.dim), "gemma2: dim=%d must be a multiple of 32 up to 16384", c.dim);
+    REQUIRE(ctx, norm_dim_ok(c.dim), "gemma2: dim=%d must be a multiple of 32 up to 12288", c.dim);
     REQUIRE(ctx, c.ffn_dim % 32 == 0, "gemma2: ffn_dim=%d must be a multiple of 32", c.ffn_dim);
     REQUIRE(ctx, c.tie_type == MRML_HIP_Q4_0 || c.tie_type == MRML_HIP_Q8_0,
             "gemma2: tie_type must be Q4_0 or Q8_0");
@@ -70,7 +70,7 @@ int mrml_hip_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float *
 {
     CTX_GUARD(ctx);
     REQUIRE(ctx, x && (out || pack), "rms_norm: x is null or no output requested");
-    REQUIRE(ctx, norm_dim_ok(dim), "rms_norm: dim=%d must be a multiple of 32 up to 16384", dim);
+    REQUIRE(ctx, norm_dim_ok(dim), "rms_norm: dim=%d must be a multiple of 32 up to 12288", dim);
     REQUIRE(ctx, ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)out & 15) == 0 &&
                      ((uintptr_t)pack & 15) == 0,
             "rms_norm: pointers must be 16-byte aligned");
@@ -82,7 +82,7 @@ int mrml_hip_residual_rms_norm(mrml_hip_ctx *ctx, const float *t, const float *w
 {
     CTX_GUARD(ctx);
     REQUIRE(ctx, t && h, "residual_rms_norm: t and h are required");
-    REQUIRE(ctx, norm_dim_ok(dim), "residual_rms_norm: dim=%d must be a multiple of 32 up to 16384", dim);
+    REQUIRE(ctx, norm_dim_ok(dim), "residual_rms_norm: dim=%d must be a multiple of 32 up to 12288", dim);
     REQUIRE(ctx, (((uintptr_t)t | (uintptr_t)w_post | (uintptr_t)h | (uintptr_t)w_next | (uintptr_t)xn |
                    (uintptr_t)pack) & 15) == 0,
             "residual_rms_norm: pointers must be 16-byte aligned");

@@ -80,6 +80,34 @@ def test_rms_norm_and_pack(backend, dev, orc, synth, dim):
     assert np.all(np.abs(out.numpy() - 1.0) < 1e-4)
 
 
+@pytest.mark.parametrize("case", ["ints", "ties", "wide", "zeros", "one_big", "ragged"])
+def test_rms_norm_exact_sum_edges(backend, dev, orc, synth, case):
+    """The sum of squares is the reference's sequential f32 loop, evaluated in
+    parallel (runs of same-binade terms as exact integer ulp counts); these
+    inputs stress binade crossings, exact ties, the plain-loop fallback and
+    zero sums."""
+    rng = synth.rng_for(3050)
+    dim = 2304 if case != "ragged" else 96
+    if case == "ints":
+        x = rng.integers(-40, 41, dim).astype(np.float32)
+    elif case == "ties":
+        x = (rng.integers(-64, 65, dim) * 2.0 ** -6).astype(np.float32)
+    elif case == "wide":
+        x = (rng.standard_normal(dim) * 10.0 ** rng.uniform(-12, 12, dim)).astype(np.float32)
+    elif case == "zeros":
+        x = np.zeros(dim, np.float32)
+    elif case == "one_big":
+        x = (rng.standard_normal(dim) * 1e-3).astype(np.float32)
+        x[1234] = 1e4
+    else:
+        x = rng.standard_normal(dim).astype(np.float32)
+    xb = backend.HipBuffer.from_host(dev, x)
+    out = backend.HipBuffer.alloc(dev, dim)
+    dev.rms_norm(xb, None, out, dim, 1e-6)
+    dev.sync()
+    assert_bits(out.numpy(), orc.rms_norm(x, None, 1e-6), f"rms_norm ({case})")
+
+
 def test_residual_rms_norm(backend, dev, orc, synth):
     dim = 2304
     rng = synth.rng_for(3100)

@@ -45,3 +45,25 @@ def test_tanhf_and_expf_match_host_libm(libm_check):
     assert counts["tanhf"] == 0, out
     key = "expf_fused" if host_expf_fused() else "expf_plain"
     assert counts[key] == 0, out
+
+
+@pytest.fixture(scope="module")
+def exact_sum_check(tmp_path_factory):
+    if shutil.which("g++") is None:
+        pytest.skip("g++ not available")
+    exe = tmp_path_factory.mktemp("xsum") / "exact_sum_check"
+    subprocess.run(["g++", "-O2", "-std=c++17", "-ffp-contract=off", str(NATIVE / "exact_sum_check.cpp"),
+                    "-o", str(exe)], check=True)
+    return exe
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+def test_exact_parallel_sum_matches_sequential_loop(exact_sum_check, seed):
+    """qt_llama.cpp_amd/csrc/exact_sum.h: the run/event compression of the
+    sequential f32 sum of non-negative terms (used for RMSNorm's sum of
+    squares) reproduces the plain loop bit for bit on 20000 random vectors
+    per seed: squares of normals over 16 decades, softmax terms, zeros and
+    outliers, tie-rich multiples of 2^-12, constants, subnormals, wide ranges."""
+    out = subprocess.run([str(exact_sum_check), "20000", str(seed)], capture_output=True, text=True)
+    assert out.returncode == 0, out.stdout
+    assert out.stdout.split()[1] == "0", out.stdout
