@@ -46,6 +46,7 @@ BYTES_DOWN = W_BYTES + FFN * 4 + DIM * 4
 BYTES_GEGLU = 2 * W_BYTES + DIM * 4 + FFN * 4          # 23,887,872 + 9,216 + 36,864
 BYTES_STEP = BYTES_GEGLU + BYTES_DOWN
 PEAK_HBM_GBS = 8000.0
+PEAK_INT8_TOPS = 5000.0                                # dense int8 MFMA, MI355X
 MALL_BYTES = 256 << 20
 
 
@@ -192,6 +193,63 @@ def decode_bench(be, synth, dev, ev, n_prefill: int, n_decode: int, cpu_steps: i
     return out, cpu
 
 
+def gemm_bench(be, synth, dev, ev, batch: int, cpu_tokens: int) -> dict:
+    """M prefill tokens x K, quantised to Q8_0, times the
+    Q4_0 gate/up (9216x2304) and down (2304x9216) matrices on int8 MFMA.
+    Ops = 2*M*rows*cols per matrix (the int8 multiply-adds of the block dots);
+    utilisation is against MI355X's dense int8 MFMA peak."""
+    rng = synth.rng_for(5)
+    mats = {"gate": (FFN, DIM), "up": (FFN, DIM), "down": (DIM, FFN)}
+    w = {k: be.HipBuffer.from_gguf(dev, synth.q4_0_matrix(rng, r, c), be.Q4_0, r, c) for k, (r, c) in mats.items()}
+    xs = {DIM: rng.standard_normal((batch, DIM)).astype(np.float32),
+          FFN: rng.standard_normal((batch, FFN)).astype(np.float32)}
+    packs, xb = {}, {}
+    for k, xv in xs.items():
+        xb[k] = be.HipBuffer.from_host(dev, xv.reshape(-1))
+        packs[k] = be.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(batch * k), np.uint8)
+        dev.quantize_q8_0(xb[k], None, packs[k], batch * k)
+    y = be.HipBuffer.alloc(dev, batch * FFN)
+    dev.sync()
+    per, total_ops, total_s = {}, 0, 0.0
+    for k, (r, c) in mats.items():
+        g = dev.capture(lambda: dev.gemm_q4_0_q8(w[k], packs[c], y, r, c, batch))
+        time_graph(dev, ev, g, 5)
+        n = 50
+        secs = time_graph(dev, ev, g, n) / n
+        g.close()
+        ops = 2 * batch * r * c
+        per[k] = {"us": round(secs * 1e6, 2), "tops": round(ops / secs / 1e12, 2)}
+        total_ops += ops
+        total_s += secs
+    # the f32 entry point: quantising the [M][K] activations + the product
+    gq = dev.capture(lambda: dev.quantize_q8_0(xb[DIM], None, packs[DIM], batch * DIM))
+    time_graph(dev, ev, gq, 5)
+    tq = time_graph(dev, ev, gq, 50) / 50
+    gq.close()
+    tops = total_ops / total_s / 1e12
+    out = {"tops": round(tops, 2), "unit": "TOPS (int8)", "mfma_util": round(tops / PEAK_INT8_TOPS, 4),
+           "peak_tops": PEAK_INT8_TOPS, "per_matrix": per, "batch": batch,
+           "quantize_q8_0_us": round(tq * 1e6, 2), "kernel": "gemm_q4_0_mfma_kernel",
+           "workload": f"BASELINE configs[4]: M={batch} tokens, Q4_0 gate/up 9216x2304 + down 2304x9216, "
+                       "activations pre-quantised to Q8_0, hipEvent around graph replays"}
+    if cpu_tokens > 0:
+        sys.path.insert(0, str(ROOT))
+        from oracle import orc
+        threads = len(os.sched_getaffinity(0))
+        hw = synth.q4_0_matrix(synth.rng_for(5), FFN, DIM)
+        xq = [orc.quantize_q8_0(xs[DIM][m]) for m in range(cpu_tokens)]
+        orc.mat_vec_mul_q4_0_q8_0(hw, xq[0], FFN, DIM, threads=threads)
+        t0 = time.perf_counter()
+        for m in range(cpu_tokens):
+            orc.mat_vec_mul_q4_0_q8_0(hw, xq[m], FFN, DIM, threads=threads)
+        t_cpu = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(2 * cpu_tokens * FFN * DIM / t_cpu / 1e12, 4), "unit": "TOPS",
+                               "cores": threads, "kind": "port",
+                               "sample": f"{cpu_tokens} tokens of the 9216x2304 gate product, token at a time "
+                                         f"(the reference CPU prefill), {threads} threads"}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -206,6 +264,9 @@ def main() -> int:
     ap.add_argument("--decode-tokens", type=int, default=256)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-decode-steps", type=int, default=8)
+    ap.add_argument("--gemm-batch", type=int, default=512)
+    ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--cpu-gemm-tokens", type=int, default=64)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -306,6 +367,9 @@ def main() -> int:
     g_step.close()
     g_geglu.close()
     gc.close()
+    gemm = None
+    if not args.no_gemm:
+        gemm = gemm_bench(be, synth, dev, ev, args.gemm_batch, 0 if args.no_cpu else args.cpu_gemm_tokens)
     decode, decode_cpu = (None, None)
     if not args.no_decode:
         decode, decode_cpu = decode_bench(be, synth, dev, ev, args.decode_prefill, args.decode_tokens,
@@ -340,6 +404,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "decode": decode,
         "decode_cpu_baseline": decode_cpu,
+        "gemm": gemm,
         "device": {"name": info["name"], "compute_units": info["compute_units"]},
     }
     print(json.dumps(line))

@@ -194,6 +194,21 @@ int mrml_hip_gemv_q8_0(mrml_hip_ctx *ctx, const void *d_w, const float *d_x, flo
 int mrml_hip_gemv_q4_k(mrml_hip_ctx *ctx, const void *d_w, const float *d_x, float *d_y,
                        int32_t rows, int32_t cols);
 
+/* ---- batched (prefill) products ------------------------------------------- */
+/* CudaDevice::gemm_q4_0 (cuda.rs:2308-2332; layout of kernels.rs:343-400):
+ * d_x is [batch][cols] f32, d_y is [batch][rows] f32, and
+ * d_y[m][r] = dot(W[r], Q8_0(x[m])) with the CPU semantics of
+ * ops::mat_vec_mul_q4_0 (ops.rs:162-180) for every token m, each output
+ * bit-identical to mrml_hip_gemv_q4_0 on that token.  The integer block dots
+ * run on int8 MFMA.  rows % 32 == 0, cols % 32 == 0, cols <= 16384. */
+int mrml_hip_gemm_q4_0(mrml_hip_ctx *ctx, const void *d_w, const float *d_x, float *d_y,
+                       int32_t rows, int32_t cols, int32_t batch);
+/* As mrml_hip_gemm_q4_0 with the batch already quantised: d_xpack is the
+ * activation pack of batch*cols values (mrml_hip_quantize_q8_0 over the
+ * whole [batch][cols] array), token m's block b at index m*(cols/32)+b. */
+int mrml_hip_gemm_q4_0_q8(mrml_hip_ctx *ctx, const void *d_w, const void *d_xpack, float *d_y,
+                          int32_t rows, int32_t cols, int32_t batch);
+
 /* Greedy pick over n f32 scores (model.rs:2869-2888; GPU tie rule
  * kernels.rs:1144-1145): index of the maximum, lowest index on ties, NaN
  * never wins.  d_out: one int32 on the device. */

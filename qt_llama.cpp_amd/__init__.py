@@ -133,6 +133,8 @@ _SIGNATURES = {
     "mrml_hip_gemv_q4_0_qkv_q8": [_P, _P, _P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemv_q8_0": [_P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemv_q4_k": [_P, _P, _P, _P, _I, _I],
+    "mrml_hip_gemm_q4_0": [_P, _P, _P, _P, _I, _I, _I],
+    "mrml_hip_gemm_q4_0_q8": [_P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_argmax_f32": [_P, _P, _I, _P],
     "mrml_hip_rms_norm": [_P, _P, _P, _P, _P, _I, _F],
     "mrml_hip_residual_rms_norm": [_P, _P, _P, _P, _P, _P, _P, _I, _F],
@@ -354,6 +356,12 @@ class HipDevice:
 
     def gemv_q4_0_q8(self, w, xpack, y, rows: int, cols: int) -> None:
         self._check(self.lib.mrml_hip_gemv_q4_0_q8(self.ctx, _ptr(w), _ptr(xpack), _ptr(y), rows, cols))
+
+    def gemm_q4_0(self, w, x, y, rows: int, cols: int, batch: int) -> None:
+        self._check(self.lib.mrml_hip_gemm_q4_0(self.ctx, _ptr(w), _ptr(x), _ptr(y), rows, cols, batch))
+
+    def gemm_q4_0_q8(self, w, xpack, y, rows: int, cols: int, batch: int) -> None:
+        self._check(self.lib.mrml_hip_gemm_q4_0_q8(self.ctx, _ptr(w), _ptr(xpack), _ptr(y), rows, cols, batch))
 
     def gemv_q4_0_gguf(self, w, x, y, rows: int, cols: int) -> None:
         self._check(self.lib.mrml_hip_gemv_q4_0_gguf(self.ctx, _ptr(w), _ptr(x), _ptr(y), rows, cols))

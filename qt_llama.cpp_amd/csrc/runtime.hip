@@ -491,6 +491,37 @@ int mrml_hip_gemv_q4_k(mrml_hip_ctx *ctx, const void *w, const float *x, float *
     return launch_gemv_q4_k(ctx, w, xp, y, rows, cols);
 }
 
+#define CHECK_GEMM(ctx, w, x, y, rows, cols, batch)                                                  \
+    do {                                                                                             \
+        REQUIRE(ctx, (w) && (x) && (y), "null pointer");                                             \
+        REQUIRE(ctx, ((uintptr_t)(x) & 15) == 0 && ((uintptr_t)(y) & 15) == 0,                       \
+                "x / pack and y must be 16-byte aligned");                                           \
+        REQUIRE(ctx, gemm_shape_ok(rows, cols, batch),                                               \
+                "gemm rows=%d cols=%d batch=%d: need rows %% 32 == 0, cols %% 32 == 0, "             \
+                "cols <= 16384, batch > 0",                                                          \
+                (int)(rows), (int)(cols), (int)(batch));                                             \
+        REQUIRE(ctx, (int64_t)(batch) * (cols) <= INT32_MAX && (int64_t)(batch) * (rows) <= INT32_MAX, \
+                "gemm batch=%d too large for rows=%d cols=%d", (int)(batch), (int)(rows), (int)(cols)); \
+    } while (0)
+
+int mrml_hip_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const float *x, float *y, int32_t rows, int32_t cols,
+                       int32_t batch)
+{
+    CTX_GUARD(ctx);
+    CHECK_GEMM(ctx, w, x, y, rows, cols, batch);
+    void *xp = quantize_to_scratch(ctx, x, batch * cols);
+    if (!xp) return MRML_HIP_E_ALLOC;
+    return launch_gemm_q4_0(ctx, w, xp, y, rows, cols, batch);
+}
+
+int mrml_hip_gemm_q4_0_q8(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows,
+                          int32_t cols, int32_t batch)
+{
+    CTX_GUARD(ctx);
+    CHECK_GEMM(ctx, w, xpack, y, rows, cols, batch);
+    return launch_gemm_q4_0(ctx, w, xpack, y, rows, cols, batch);
+}
+
 int mrml_hip_argmax_f32(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *out)
 {
     CTX_GUARD(ctx);

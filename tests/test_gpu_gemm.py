@@ -1,0 +1,120 @@
+"""GPU parity of the batched (prefill) Q4_0 x Q8_0 product on int8 MFMA.
+
+The reference has no CPU batched path (CPU prefill runs token at a time,
+model.rs:2694-2696), so the oracle is the CPU matvec applied per token:
+every output y[m][r] must be bit-identical to ops::mat_vec_mul_q4_0 on token
+m (ops.rs:162-180 via quant.rs:339-366).  The integer accumulators are pinned
+separately: with one block per row and unit scales each output IS the block's
+int32 dot, checked against a numpy integer product.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+THREADS = 16
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def assert_bit_exact(got, ref, what):
+    got, ref = np.asarray(got, np.float32), np.asarray(ref, np.float32)
+    bad = np.flatnonzero(bits(got) != bits(ref))
+    assert bad.size == 0, f"{what}: {bad.size} of {ref.size} differ, first {bad[:5]}: {got.flat[bad[:5]]} vs " \
+                          f"{ref.flat[bad[:5]]}"
+
+
+def run_gemm(backend, dev, w, x, rows, cols, batch, prequantised=False):
+    wb = backend.HipBuffer.from_gguf(dev, w, backend.Q4_0, rows, cols)
+    xb = backend.HipBuffer.from_host(dev, np.ascontiguousarray(x, np.float32).reshape(-1))
+    yb = backend.HipBuffer.alloc(dev, rows * batch)
+    if prequantised:
+        pk = backend.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(batch * cols), np.uint8)
+        dev.quantize_q8_0(xb, None, pk, batch * cols)
+        dev.gemm_q4_0_q8(wb, pk, yb, rows, cols, batch)
+    else:
+        dev.gemm_q4_0(wb, xb, yb, rows, cols, batch)
+    dev.sync()
+    return yb.numpy().reshape(batch, rows)
+
+
+def oracle_gemm(orc, w, x, rows, cols, tokens):
+    return np.stack([orc.mat_vec_mul_q4_0(w, x[m], rows, cols, threads=THREADS) for m in tokens])
+
+
+# C5: the Gemma-2-2B gate/up and down shapes at M = 512 prefill tokens.
+@pytest.mark.parametrize("rows,cols", [(9216, 2304), (2304, 9216)])
+def test_gemm_q4_0_prefill_512_bit_exact(backend, dev, orc, synth, rows, cols):
+    batch = 512
+    rng = synth.rng_for(5000 + rows)
+    w = synth.q4_0_matrix(rng, rows, cols)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    got = run_gemm(backend, dev, w, x, rows, cols, batch)
+    ref = oracle_gemm(orc, w, x, rows, cols, range(batch))
+    assert_bit_exact(got, ref, f"gemm {rows}x{cols} M={batch}")
+
+
+@pytest.mark.parametrize("rows,cols,batch", [
+    (32, 32, 1), (64, 64, 17), (96, 256, 33), (128, 2304, 100), (32, 96, 129), (256, 512, 255),
+    (1024, 2304, 16), (64, 16384, 40),
+])
+def test_gemm_q4_0_ragged_bit_exact(backend, dev, orc, synth, rows, cols, batch):
+    rng = synth.rng_for(5100 + rows + cols + batch)
+    w = synth.q4_0_matrix(rng, rows, cols)
+    x = (rng.standard_normal((batch, cols)) * 10.0 ** rng.uniform(-3, 3, (batch, 1))).astype(np.float32)
+    x[0, :32] = 0.0                                   # a zero block: scale 0, quants 0
+    got = run_gemm(backend, dev, w, x, rows, cols, batch)
+    ref = oracle_gemm(orc, w, x, rows, cols, range(batch))
+    assert_bit_exact(got, ref, f"gemm {rows}x{cols} M={batch}")
+
+
+def test_gemm_q4_0_integer_accumulators(backend, dev):
+    """One block per row, unit scales, activations exactly representable as
+    Q8_0 (amax 127 in every token): y[m][r] == sum_i (n_i(r)-8) * x_i(m), the
+    int32 block dot, for every nibble and quant pattern incl. -128 and 0/15."""
+    rows, cols, batch = 256, 32, 200
+    rng = np.random.default_rng(77)
+    nib = rng.integers(0, 16, (rows, 32))
+    nib[0], nib[1] = 0, 15                             # extreme rows
+    q = rng.integers(-127, 128, (batch, 32))
+    q[:, 0] = 127                                      # amax 127 -> scale 1.0, q == x exactly
+    q[1, 1:] = -127
+    w = np.zeros((rows, 18), np.uint8)
+    w[:, 1] = 0x3C                                     # f16 1.0
+    w[:, 2:] = (nib[:, :16] | (nib[:, 16:] << 4)).astype(np.uint8)
+    got = run_gemm(backend, dev, w.reshape(-1), q.astype(np.float32), rows, cols, batch)
+    isum = q.astype(np.int64) @ (nib - 8).T.astype(np.int64)
+    assert np.array_equal(got, isum.astype(np.float32)), "integer block dots differ"
+
+
+def test_gemm_q4_0_matches_gemv_and_pack_entry(backend, dev, orc, synth):
+    """The f32 entry, the pre-quantised entry and the batch-1 matvec agree bit
+    for bit on every token."""
+    rows, cols, batch = 2048, 2304, 48
+    rng = synth.rng_for(5200)
+    w = synth.q4_0_matrix(rng, rows, cols)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    a = run_gemm(backend, dev, w, x, rows, cols, batch)
+    b = run_gemm(backend, dev, w, x, rows, cols, batch, prequantised=True)
+    assert_bit_exact(a, b, "f32 entry vs pack entry")
+    wb = backend.HipBuffer.from_gguf(dev, w, backend.Q4_0, rows, cols)
+    yb = backend.HipBuffer.alloc(dev, rows)
+    for m in (0, 1, 31, 32, 47):
+        xb = backend.HipBuffer.from_host(dev, x[m])
+        dev.gemv_q4_0(wb, xb, yb, rows, cols)
+        dev.sync()
+        assert_bit_exact(a[m], yb.numpy(), f"gemm token {m} vs gemv")
+
+
+def test_gemm_q4_0_rejects_bad_shapes(backend, dev):
+    w = backend.HipBuffer.alloc(dev, 64 * 18, np.uint8)
+    x = backend.HipBuffer.alloc(dev, 64 * 4)
+    y = backend.HipBuffer.alloc(dev, 64 * 4)
+    for rows, cols, batch in [(33, 32, 2), (32, 48, 2), (32, 32, 0), (32, 32 * 513, 1)]:
+        with pytest.raises(backend.HipError):
+            dev.gemm_q4_0(w, x, y, rows, cols, batch)
