@@ -200,7 +200,9 @@ int mrml_hip_gemv_q4_k(mrml_hip_ctx *ctx, const void *d_w, const float *d_x, flo
  * d_y[m][r] = dot(W[r], Q8_0(x[m])) with the CPU semantics of
  * ops::mat_vec_mul_q4_0 (ops.rs:162-180) for every token m, each output
  * bit-identical to mrml_hip_gemv_q4_0 on that token.  The integer block dots
- * run on int8 MFMA.  rows % 32 == 0, cols % 32 == 0, cols <= 16384. */
+ * run on int8 MFMA.  rows % 32 == 0, cols % 32 == 0; W and the activations
+ * each below 2 GiB.  Uses the context workspace (batch/32 * cols/32 * 1152
+ * bytes rounded up) for the activations in MFMA order. */
 int mrml_hip_gemm_q4_0(mrml_hip_ctx *ctx, const void *d_w, const float *d_x, float *d_y,
                        int32_t rows, int32_t cols, int32_t batch);
 /* As mrml_hip_gemm_q4_0 with the batch already quantised: d_xpack is the
@@ -208,6 +210,16 @@ int mrml_hip_gemm_q4_0(mrml_hip_ctx *ctx, const void *d_w, const float *d_x, flo
  * whole [batch][cols] array), token m's block b at index m*(cols/32)+b. */
 int mrml_hip_gemm_q4_0_q8(mrml_hip_ctx *ctx, const void *d_w, const void *d_xpack, float *d_y,
                           int32_t rows, int32_t cols, int32_t batch);
+/* The batch quantised once for several products over the same activations
+ * (gate and up, or Q/K/V, share their input: model.rs:2452-2560): Q8_0 of
+ * every token (quant.rs:193-228) written as a GEMM pack, the MFMA operand
+ * order of these kernels, mrml_hip_gemm_pack_bytes(cols, batch) bytes. */
+size_t mrml_hip_gemm_pack_bytes(int32_t cols, int32_t batch);
+int mrml_hip_quantize_q8_0_gemm(mrml_hip_ctx *ctx, const float *d_x, void *d_gpack, int32_t cols,
+                                int32_t batch);
+/* As mrml_hip_gemm_q4_0 over a GEMM pack; no workspace. */
+int mrml_hip_gemm_q4_0_gpack(mrml_hip_ctx *ctx, const void *d_w, const void *d_gpack, float *d_y,
+                             int32_t rows, int32_t cols, int32_t batch);
 
 /* Greedy pick over n f32 scores (model.rs:2869-2888; GPU tie rule
  * kernels.rs:1144-1145): index of the maximum, lowest index on ties, NaN

@@ -135,6 +135,9 @@ _SIGNATURES = {
     "mrml_hip_gemv_q4_k": [_P, _P, _P, _P, _I, _I],
     "mrml_hip_gemm_q4_0": [_P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemm_q4_0_q8": [_P, _P, _P, _P, _I, _I, _I],
+    "mrml_hip_gemm_pack_bytes": [_I, _I],
+    "mrml_hip_quantize_q8_0_gemm": [_P, _P, _P, _I, _I],
+    "mrml_hip_gemm_q4_0_gpack": [_P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_argmax_f32": [_P, _P, _I, _P],
     "mrml_hip_rms_norm": [_P, _P, _P, _P, _P, _I, _F],
     "mrml_hip_residual_rms_norm": [_P, _P, _P, _P, _P, _P, _P, _I, _F],
@@ -152,6 +155,7 @@ _RESTYPE = {
     "mrml_hip_status_string": ctypes.c_char_p,
     "mrml_hip_stream": _P,
     "mrml_hip_q8_0_pack_bytes": _Z,
+    "mrml_hip_gemm_pack_bytes": _Z,
 }
 
 _lib = None
@@ -362,6 +366,15 @@ class HipDevice:
 
     def gemm_q4_0_q8(self, w, xpack, y, rows: int, cols: int, batch: int) -> None:
         self._check(self.lib.mrml_hip_gemm_q4_0_q8(self.ctx, _ptr(w), _ptr(xpack), _ptr(y), rows, cols, batch))
+
+    def gemm_pack_bytes(self, cols: int, batch: int) -> int:
+        return int(self.lib.mrml_hip_gemm_pack_bytes(cols, batch))
+
+    def quantize_q8_0_gemm(self, x, gpack, cols: int, batch: int) -> None:
+        self._check(self.lib.mrml_hip_quantize_q8_0_gemm(self.ctx, _ptr(x), _ptr(gpack), cols, batch))
+
+    def gemm_q4_0_gpack(self, w, gpack, y, rows: int, cols: int, batch: int) -> None:
+        self._check(self.lib.mrml_hip_gemm_q4_0_gpack(self.ctx, _ptr(w), _ptr(gpack), _ptr(y), rows, cols, batch))
 
     def gemv_q4_0_gguf(self, w, x, y, rows: int, cols: int) -> None:
         self._check(self.lib.mrml_hip_gemv_q4_0_gguf(self.ctx, _ptr(w), _ptr(x), _ptr(y), rows, cols))

@@ -13,18 +13,22 @@
 //   A = the row's 16 quant bytes, low nibbles (half 0) or high nibbles
 //       (half 1), turned into signed bytes q-8 in registers (see sbytes), so
 //       the MFMA result is isum itself;
-//   B = the token's 16 int8 quants of that K half (the activation pack).
+//   B = the token's 16 int8 quants of that K half.
 // Lane l receives D[8j+4(l/32)+i][l%32] in element 4j+i: 16 rows of ONE
 // token, so the token's block scale is a per-lane scalar and the rows'
-// scales come from LDS as float4s.
+// scales are float4 broadcasts from LDS.
 //
 // The ordered f32 fold runs on the VALU: 4 instructions per output per block
 // (cvt, dw*da, *, +) against one MFMA per 1024 outputs, so the kernel is
-// VALU-bound by construction.  Everything else is arranged around keeping the
-// VALU busy: the row tile's scales are staged once in LDS, operand loads run
-// kPF blocks ahead (buffer loads, which the compiler keeps where they are
-// written), and each block's MFMA is issued before the previous block is
-// folded so its latency overlaps VALU work.
+// VALU-bound once its operands arrive without stalls.  Operand feed:
+//   - B comes from a GEMM pack written in MFMA lane order (one 1 KB run of
+//     quants and one 128-byte run of scales per 32 tokens and block), read
+//     with one coalesced load each, kPF blocks ahead of use;
+//   - A is shared by the workgroup's four waves (four 32-token groups over
+//     one 32-row tile): kKC-block chunks of the 32 rows (128 contiguous bytes
+//     per row) and their f16 scales are loaded with coalesced loads into
+//     registers one chunk ahead and staged through kNBuf LDS buffers, one
+//     barrier per chunk.
 
 #include "device.h"
 #include "internal.h"
@@ -37,15 +41,62 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kGemmWaves = 4;             // 32-token tiles per workgroup, sharing one 32-row tile
-constexpr int kPF = 4;                    // operand prefetch distance, blocks
+constexpr int kGemmWaves = 4;             // 32-token groups per workgroup, sharing one 32-row tile
+constexpr int kPF = 4;                    // B prefetch distance, blocks
+constexpr int kKC = 8;                    // blocks per A chunk
+constexpr int kNBuf = 3;                  // A chunk buffers in LDS
 constexpr int kBufferFlags = 0x00020000;  // buffer resource word 3 (raw 32-bit data) on gfx9
 
-struct Operands {
-    u32x4 w;   // the row's 16 quant bytes
-    u32x4 a;   // the token's 16 quants of this K half
-    float da;  // the token's block scale
-};
+// GEMM pack of `batch` tokens x nb blocks, groups of 32 tokens (the last
+// group zero-padded):
+//   int8  q[g][b][h][t][16]  at byte 0              (h = K half, t = token in group)
+//   f32   d[g][b][t]         at byte ngroups*nb*1024
+__host__ __device__ inline int gemm_groups(int batch) { return (batch + 31) / 32; }
+
+// Writes token m's block b (8 lanes, lane l holding quants 4l..4l+3 packed in
+// q) into the GEMM pack.
+__device__ __forceinline__ void gemm_pack_put(uint8_t *gp, int ngroups, int nb, int m, int b, int l, uint32_t q,
+                                              float d)
+{
+    const int g = m >> 5, t = m & 31, h = l >> 2;
+    const size_t gb = (size_t)g * nb + b;
+    reinterpret_cast<uint32_t *>(gp + ((gb * 64 + 32 * h + t) * 16))[l & 3] = q;
+    if (l == 0) reinterpret_cast<float *>(gp + (size_t)ngroups * nb * 1024)[gb * 32 + t] = d;
+}
+
+// quant.rs:193-228 per block (q8_0_block8x4), written as a GEMM pack.  One
+// workgroup per (group, block): thread 8t+l handles token 32g+t, values
+// 4l..4l+3 of block b.  Tokens past `batch` are written as zeros.
+__global__ __launch_bounds__(256) void quantize_gemm_pack_kernel(const float *__restrict__ x, uint8_t *__restrict__ gp,
+                                                                 int nb, int batch, int ngroups)
+{
+    const int g = blockIdx.x / nb, b = blockIdx.x - g * nb;
+    const int t = threadIdx.x >> 3, l = threadIdx.x & 7, m = 32 * g + t;
+    const int ms = m < batch ? m : batch - 1;  // every lane takes part in the block reductions
+    uint32_t dbits;
+    int s;
+    const float4 v = reinterpret_cast<const float4 *>(x)[((size_t)ms * nb + b) * 8 + l];
+    const uint32_t q = q8_0_block8x4(v, dbits, s);
+    const bool real = m < batch;
+    gemm_pack_put(gp, ngroups, nb, m, b, l, real ? q : 0u, real ? f16_bits_to_f32(dbits) : 0.0f);
+}
+
+// An activation pack of batch*nb blocks (block (m,b) at m*nb+b) -> GEMM pack.
+__global__ __launch_bounds__(256) void gemm_pack_from_act_kernel(const uint8_t *__restrict__ pack,
+                                                                 uint8_t *__restrict__ gp, int nb, int batch,
+                                                                 int ngroups)
+{
+    const int g = blockIdx.x / nb, b = blockIdx.x - g * nb;
+    const int t = threadIdx.x >> 3, l = threadIdx.x & 7, m = 32 * g + t;
+    uint32_t q = 0;
+    float d = 0.0f;
+    if (m < batch) {
+        const size_t blk = (size_t)m * nb + b;
+        q = reinterpret_cast<const uint32_t *>(pack)[blk * 8 + l];
+        d = reinterpret_cast<const float *>(pack + (size_t)batch * nb * 32)[blk];
+    }
+    gemm_pack_put(gp, ngroups, nb, m, b, l, q, d);
+}
 
 // Four nibbles per dword (selected by shift 0 or 4) -> four signed bytes q-8.
 // Per byte: (q | 0x80) - 8 stays within 0x78..0x87, so no borrow crosses a
@@ -56,66 +107,61 @@ __device__ __forceinline__ int sbytes(uint32_t v, int sh)
     return (int)((n - 0x08080808u) ^ 0x80808080u);
 }
 
+// LDS writes of this wave complete, then the workgroup barrier.  As inline
+// asm with a memory clobber, no LDS access is moved across it; outstanding
+// global loads (the operand prefetch) stay in flight.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+struct BOps {
+    u32x4 a;   // the token's 16 quants of this K half
+    float da;  // the token's block scale
+};
+
 __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const uint8_t *__restrict__ w,
-                                                                         const uint8_t *__restrict__ xpack,
+                                                                         const uint8_t *__restrict__ gp,
                                                                          float *__restrict__ y, int rows, int nb,
-                                                                         int batch)
+                                                                         int batch, int ngroups)
 {
-    extern __shared__ __align__(16) float dws[];  // [nb][32]: the row tile's block scales, f32
+    __shared__ __align__(16) u32x4 sa[kNBuf][kKC][32];  // A chunks: [block][row] 16 quant bytes
+    __shared__ __align__(16) float sdw[kNBuf][kKC][32];  // their row scales, f32
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r0 = blockIdx.x * 32;
+    const int g = blockIdx.y * kGemmWaves + wave;  // >= ngroups: computes on zeros, stores nothing
+    const int tl = lane & 31, h = lane >> 5, sh = 4 * h;
     const uint32_t qs_bytes = (uint32_t)rows * nb * 16;
-
-    // The 32 rows' scales are one contiguous run of 32*nb f16 in the scale
-    // plane (64*nb bytes, 16-byte aligned): 8 per 16-byte load, up to kSL
-    // loads of a thread in flight together.
-    {
-        constexpr int kSL = 4, kStride = 64 * kGemmWaves;
-        const u32x4 *src = reinterpret_cast<const u32x4 *>(w + qs_bytes) + (size_t)r0 * nb / 8;
-        for (int i0 = 0; i0 < 4 * nb; i0 += kSL * kStride) {
-            u32x4 v[kSL];
-#pragma unroll
-            for (int k = 0; k < kSL; ++k) {
-                const int i = i0 + tid + k * kStride;
-                if (i < 4 * nb) v[k] = src[i];
-            }
-#pragma unroll
-            for (int k = 0; k < kSL; ++k) {
-                const int i = i0 + tid + k * kStride;
-                if (i >= 4 * nb) break;
-                int r = 8 * i / nb, b = 8 * i - r * nb;  // element 8i = row r, block b
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    dws[b * 32 + r] = f16_bits_to_f32((v[k][j >> 1] >> (16 * (j & 1))) & 0xffffu);
-                    if (++b == nb) b = 0, ++r;
-                }
-            }
-        }
-    }
-    __syncthreads();
-    const int t0 = (blockIdx.y * kGemmWaves + wave) * 32;
-    if (t0 >= batch) return;  // no barrier follows
-    const int tl = lane & 31, h = lane >> 5;
-    const int tok = t0 + tl < batch ? t0 + tl : batch - 1;  // tail lanes recompute the last token
-    const uint32_t ntot = (uint32_t)batch * nb;
-    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void *)w, (short)0, (int)qs_bytes,
+    // Loads past a row's last block read the next row or, past the end of a
+    // buffer, zeros (buffer range check); such blocks are never folded.
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void *)w, (short)0,
+                                                                        (int)(qs_bytes + (uint32_t)rows * nb * 2),
                                                                         kBufferFlags);
-    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void *)xpack, (short)0, (int)(ntot * 36),
-                                                                        kBufferFlags);
-    const uint32_t wo = (uint32_t)(r0 + tl) * nb * 16;
-    const uint32_t ao = (uint32_t)tok * nb * 32 + 16 * h;
-    const uint32_t so = ntot * 32 + (uint32_t)tok * nb * 4;
-    const int sh = 4 * h;
+    const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)gp, (short)0, (int)((uint32_t)ngroups * nb * 1152), kBufferFlags);
 
-    // Loads past the lane's last block read neighbouring rows / tokens or,
-    // past the end of a buffer, zeros (buffer range check); never used.
-    auto load = [&](int b, Operands &o) {
-        o.w = __builtin_amdgcn_raw_buffer_load_b128(wr, wo + 16u * b, 0, 0);
-        o.a = __builtin_amdgcn_raw_buffer_load_b128(xr, ao + 32u * b, 0, 0);
-        o.da = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, so + 4u * b, 0, 0));
+    // A chunk c: thread (row ar, block ak) loads 16 quant bytes and one f16 scale.
+    const int ar = tid >> 3, ak = tid & 7;
+    const uint32_t a_off = ((uint32_t)(r0 + ar) * nb + ak) * 16;
+    const uint32_t s_off = qs_bytes + ((uint32_t)(r0 + ar) * nb + ak) * 2;
+    u32x4 areg;
+    uint32_t sreg;
+    auto load_chunk = [&](int c) {
+        areg = __builtin_amdgcn_raw_buffer_load_b128(wr, a_off + (uint32_t)c * (kKC * 16), 0, 0);
+        sreg = __builtin_amdgcn_raw_buffer_load_b16(wr, s_off + (uint32_t)c * (kKC * 2), 0, 0);
     };
-    auto mfma = [&](const Operands &o) {
-        const v4i a = {sbytes(o.w.x, sh), sbytes(o.w.y, sh), sbytes(o.w.z, sh), sbytes(o.w.w, sh)};
+    auto store_chunk = [&](int buf) {
+        sa[buf][ak][ar] = areg;
+        sdw[buf][ak][ar] = f16_bits_to_f32(sreg);
+    };
+
+    // B: this wave's token group, lane order = MFMA order.
+    const uint32_t b_off = ((uint32_t)g * nb * 64 + lane) * 16;
+    const uint32_t d_off = (uint32_t)ngroups * nb * 1024 + ((uint32_t)g * nb * 32 + tl) * 4;
+    auto load_b = [&](int b, BOps &o) {
+        o.a = __builtin_amdgcn_raw_buffer_load_b128(gr, b_off + (uint32_t)b * 1024, 0, 0);
+        o.da = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(gr, d_off + (uint32_t)b * 128, 0, 0));
+    };
+    auto mfma = [&](int buf, int kc, const BOps &o) {
+        const u32x4 wv = sa[buf][kc][tl];
+        const v4i a = {sbytes(wv.x, sh), sbytes(wv.y, sh), sbytes(wv.z, sh), sbytes(wv.w, sh)};
         const v4i bq = {(int)o.a.x, (int)o.a.y, (int)o.a.z, (int)o.a.w};
         const v16i zero = {};
         return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, zero, 0, 0, 0);
@@ -124,10 +170,10 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
     float acc[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
-    // Block b's fold: the four float4s of row scales are read from LDS first
-    // (one wait for all four), then 16 x (cvt, dw*da, *, +) in block order.
-    auto fold = [&](const v16i &d, float da, int b) {
-        const float4 *dwb = reinterpret_cast<const float4 *>(dws + b * 32 + 4 * h);
+    // Block fold: the four float4s of row scales first (one wait), then
+    // 16 x (cvt, dw*da, *, +).
+    auto fold = [&](const v16i &d, float da, int buf, int kc) {
+        const float4 *dwb = reinterpret_cast<const float4 *>(&sdw[buf][kc][4 * h]);
         float4 dw[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) dw[j] = dwb[2 * j];  // rows 8j + 4h + 0..3
@@ -139,36 +185,52 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
         }
     };
 
-    // ring[s] holds the operands of block b with b % kPF == s.  Step b:
-    // issue block b+1's MFMA, fold block b (its MFMA result from the previous
-    // step, its token scale still in its slot), then refill block b's slot
-    // with block b+kPF.  Scheduling barriers keep that order (the scheduler
-    // would otherwise gather the loads at the end of the loop and wait for
-    // all of them at its top), so each wait covers only the loads of the
-    // block about to be used.  The main loop has no branches; it may issue
-    // the MFMA and loads of blocks >= nb, whose results are never folded.
-    Operands ring[kPF];
+    // Chunks 0 and 1 into LDS, chunk 2 in flight; B blocks 0..kPF-1 in flight.
+    load_chunk(0);
+    store_chunk(0);
+    load_chunk(1);
+    store_chunk(1);
+    lds_barrier();
+    load_chunk(2);
+    BOps ring[kPF];
 #pragma unroll
-    for (int s = 0; s < kPF; ++s) load(s, ring[s]);
-    v16i d = mfma(ring[0]);
-    auto step = [&](int b, Operands &cur, const Operands &next, bool refill) {
-        const v16i dn = mfma(next);
+    for (int s = 0; s < kPF; ++s) load_b(s, ring[s]);
+    v16i d = mfma(0, 0, ring[0]);
+
+    // Step (block b = kKC*c + kc): issue block b+1's MFMA, fold block b, refill
+    // block b's B slot with block b+kPF.  Scheduling barriers keep that order
+    // (the scheduler would otherwise gather the loads and wait for them all
+    // at once), so each wait covers only the block about to be used.  The
+    // steps may issue MFMAs and loads of blocks >= nb; those are never folded.
+    // Chunk reuse: at the end of chunk c, chunk c+2 is written into buffer
+    // (c+2)%3 = (c-1)%3, whose last readers (chunk c-1's MFMAs and folds)
+    // all come before the barrier that ended chunk c-1.
+    int c = 0, cb = 0, nbf = 1, wb = 2;  // chunk, its buffer, the next chunk's buffer, the buffer to write
+    auto step = [&](int kc, BOps &cur, const BOps &next, bool refill, int b) {
+        const v16i dn = (kc + 1 < kKC) ? mfma(cb, kc + 1, next) : mfma(nbf, 0, next);
         __builtin_amdgcn_sched_barrier(0);
-        fold(d, cur.da, b);
+        fold(d, cur.da, cb, kc);
         __builtin_amdgcn_sched_barrier(0);
-        if (refill) load(b + kPF, cur);
+        if (refill) load_b(b + kPF, cur);
         d = dn;
     };
-    int b0 = 0;
-    for (; b0 + kPF <= nb; b0 += kPF) {
+    for (; (c + 1) * kKC <= nb; ++c) {
 #pragma unroll
-        for (int s = 0; s < kPF; ++s) step(b0 + s, ring[s], ring[(s + 1) % kPF], true);
+        for (int kc = 0; kc < kKC; ++kc) step(kc, ring[kc % kPF], ring[(kc + 1) % kPF], true, c * kKC + kc);
+        store_chunk(wb);
+        lds_barrier();
+        load_chunk(c + 3);
+        cb = nbf;
+        nbf = wb;
+        wb = wb == kNBuf - 1 ? 0 : wb + 1;
     }
 #pragma unroll
-    for (int s = 0; s < kPF - 1; ++s)  // the last nb % kPF blocks
-        if (b0 + s < nb) step(b0 + s, ring[s], ring[(s + 1) % kPF], false);
-    if (t0 + tl < batch) {
-        float *yr = y + (size_t)(t0 + tl) * rows + r0 + 4 * h;
+    for (int kc = 0; kc < kKC - 1; ++kc)  // the last nb % kKC blocks
+        if (c * kKC + kc < nb) step(kc, ring[kc % kPF], ring[(kc + 1) % kPF], false, c * kKC + kc);
+
+    const int tok = g * 32 + tl;
+    if (tok < batch) {
+        float *yr = y + (size_t)tok * rows + r0 + 4 * h;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             *reinterpret_cast<float4 *>(yr + 8 * j) = make_float4(acc[4 * j], acc[4 * j + 1], acc[4 * j + 2],
@@ -180,19 +242,38 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
 
 bool gemm_shape_ok(int32_t rows, int32_t cols, int32_t batch)
 {
-    if (rows <= 0 || rows % 32 != 0 || cols <= 0 || cols % 32 != 0 || cols / 32 > 512 || batch <= 0) return false;
-    // 32-bit buffer offsets: the quant plane of W and the whole activation pack
+    if (rows <= 0 || rows % 32 != 0 || cols <= 0 || cols % 32 != 0 || batch <= 0) return false;
+    // 32-bit buffer offsets: the whole of W and of the GEMM pack
     const int64_t nb = cols / 32;
-    return (int64_t)rows * nb * 16 < INT32_MAX && (int64_t)batch * nb * 40 < INT32_MAX;
+    return (int64_t)rows * nb * 18 < INT32_MAX && ((int64_t)batch + 31) / 32 * nb * 1152 < INT32_MAX &&
+           (int64_t)batch * nb * 40 < INT32_MAX;
 }
 
-int launch_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows, int32_t cols,
+size_t gemm_pack_bytes(int32_t cols, int32_t batch) { return (size_t)gemm_groups(batch) * (cols / 32) * 1152; }
+
+int launch_gemm_pack_quantize(mrml_hip_ctx *ctx, const float *x, void *gpack, int32_t cols, int32_t batch)
+{
+    const int nb = cols / 32, ng = gemm_groups(batch);
+    hipLaunchKernelGGL(quantize_gemm_pack_kernel, dim3((unsigned)(ng * nb)), dim3(256), 0, ctx->stream, x,
+                       (uint8_t *)gpack, nb, batch, ng);
+    return check_launch(ctx, "quantize_gemm_pack_kernel");
+}
+
+int launch_gemm_pack_from_act(mrml_hip_ctx *ctx, const void *pack, void *gpack, int32_t cols, int32_t batch)
+{
+    const int nb = cols / 32, ng = gemm_groups(batch);
+    hipLaunchKernelGGL(gemm_pack_from_act_kernel, dim3((unsigned)(ng * nb)), dim3(256), 0, ctx->stream,
+                       (const uint8_t *)pack, (uint8_t *)gpack, nb, batch, ng);
+    return check_launch(ctx, "gemm_pack_from_act_kernel");
+}
+
+int launch_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const void *gpack, float *y, int32_t rows, int32_t cols,
                      int32_t batch)
 {
-    const int nb = cols / 32;
-    const dim3 grid(rows / 32, (batch + 32 * kGemmWaves - 1) / (32 * kGemmWaves));
-    hipLaunchKernelGGL(gemm_q4_0_mfma_kernel, grid, dim3(64 * kGemmWaves), (size_t)nb * 32 * sizeof(float),
-                       ctx->stream, (const uint8_t *)w, (const uint8_t *)xpack, y, rows, nb, batch);
+    const int nb = cols / 32, ng = gemm_groups(batch);
+    const dim3 grid(rows / 32, (ng + kGemmWaves - 1) / kGemmWaves);
+    hipLaunchKernelGGL(gemm_q4_0_mfma_kernel, grid, dim3(64 * kGemmWaves), 0, ctx->stream, (const uint8_t *)w,
+                       (const uint8_t *)gpack, y, rows, nb, batch, ng);
     return check_launch(ctx, "gemm_q4_0_mfma_kernel");
 }
 

@@ -67,10 +67,15 @@ int launch_argmax_f32(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *out
 int launch_gemv_q4_0_geglu_emit(mrml_hip_ctx *ctx, const void *wg, const void *wu, const void *xpack, float *act,
                                 void *act_pack, int32_t rows, int32_t cols);
 
-// Batched Q4_0 x Q8_0 products with int8 MFMA: xpack holds batch*cols values
-// (token m's block b at index m*(cols/32)+b), y is [batch][rows].
+// Batched Q4_0 x Q8_0 products with int8 MFMA.  The kernel reads its
+// activations from a GEMM pack (token groups of 32 in MFMA lane order,
+// gemm_pack_bytes), written from f32 rows [batch][cols] or converted from an
+// activation pack of batch*cols values; y is [batch][rows].
 bool gemm_shape_ok(int32_t rows, int32_t cols, int32_t batch);
-int launch_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows, int32_t cols,
+size_t gemm_pack_bytes(int32_t cols, int32_t batch);
+int launch_gemm_pack_quantize(mrml_hip_ctx *ctx, const float *x, void *gpack, int32_t cols, int32_t batch);
+int launch_gemm_pack_from_act(mrml_hip_ctx *ctx, const void *pack, void *gpack, int32_t cols, int32_t batch);
+int launch_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const void *gpack, float *y, int32_t rows, int32_t cols,
                      int32_t batch);
 
 // Argmax whose final pass can also advance a device-side decode loop

@@ -497,8 +497,8 @@ int mrml_hip_gemv_q4_k(mrml_hip_ctx *ctx, const void *w, const float *x, float *
         REQUIRE(ctx, ((uintptr_t)(x) & 15) == 0 && ((uintptr_t)(y) & 15) == 0,                       \
                 "x / pack and y must be 16-byte aligned");                                           \
         REQUIRE(ctx, gemm_shape_ok(rows, cols, batch),                                               \
-                "gemm rows=%d cols=%d batch=%d: need rows %% 32 == 0, cols %% 32 == 0, "             \
-                "cols <= 16384, batch > 0",                                                          \
+                "gemm rows=%d cols=%d batch=%d: need rows %% 32 == 0, cols %% 32 == 0, batch > 0 "  \
+                "and W / activations below 2 GiB",                                                   \
                 (int)(rows), (int)(cols), (int)(batch));                                             \
         REQUIRE(ctx, (int64_t)(batch) * (cols) <= INT32_MAX && (int64_t)(batch) * (rows) <= INT32_MAX, \
                 "gemm batch=%d too large for rows=%d cols=%d", (int)(batch), (int)(rows), (int)(cols)); \
@@ -509,9 +509,10 @@ int mrml_hip_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const float *x, float *
 {
     CTX_GUARD(ctx);
     CHECK_GEMM(ctx, w, x, y, rows, cols, batch);
-    void *xp = quantize_to_scratch(ctx, x, batch * cols);
-    if (!xp) return MRML_HIP_E_ALLOC;
-    return launch_gemm_q4_0(ctx, w, xp, y, rows, cols, batch);
+    void *gp = workspace(ctx, gemm_pack_bytes(cols, batch));
+    if (!gp) return MRML_HIP_E_ALLOC;
+    int rc = launch_gemm_pack_quantize(ctx, x, gp, cols, batch);
+    return rc ? rc : launch_gemm_q4_0(ctx, w, gp, y, rows, cols, batch);
 }
 
 int mrml_hip_gemm_q4_0_q8(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows,
@@ -519,7 +520,30 @@ int mrml_hip_gemm_q4_0_q8(mrml_hip_ctx *ctx, const void *w, const void *xpack, f
 {
     CTX_GUARD(ctx);
     CHECK_GEMM(ctx, w, xpack, y, rows, cols, batch);
-    return launch_gemm_q4_0(ctx, w, xpack, y, rows, cols, batch);
+    void *gp = workspace(ctx, gemm_pack_bytes(cols, batch));
+    if (!gp) return MRML_HIP_E_ALLOC;
+    int rc = launch_gemm_pack_from_act(ctx, xpack, gp, cols, batch);
+    return rc ? rc : launch_gemm_q4_0(ctx, w, gp, y, rows, cols, batch);
+}
+
+size_t mrml_hip_gemm_pack_bytes(int32_t cols, int32_t batch)
+{
+    return (cols > 0 && cols % 32 == 0 && batch > 0) ? gemm_pack_bytes(cols, batch) : 0;
+}
+
+int mrml_hip_quantize_q8_0_gemm(mrml_hip_ctx *ctx, const float *x, void *gpack, int32_t cols, int32_t batch)
+{
+    CTX_GUARD(ctx);
+    CHECK_GEMM(ctx, gpack, x, gpack, 32, cols, batch);
+    return launch_gemm_pack_quantize(ctx, x, gpack, cols, batch);
+}
+
+int mrml_hip_gemm_q4_0_gpack(mrml_hip_ctx *ctx, const void *w, const void *gpack, float *y, int32_t rows,
+                             int32_t cols, int32_t batch)
+{
+    CTX_GUARD(ctx);
+    CHECK_GEMM(ctx, w, gpack, y, rows, cols, batch);
+    return launch_gemm_q4_0(ctx, w, gpack, y, rows, cols, batch);
 }
 
 int mrml_hip_argmax_f32(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *out)

@@ -21,7 +21,7 @@ def declared_functions() -> list[str]:
 def test_header_declares_the_surface():
     names = declared_functions()
     for must in ("mrml_hip_create", "mrml_hip_gemv_q4_0", "mrml_hip_gemv_q4_0_geglu", "mrml_hip_gemv_q8_0",
-                 "mrml_hip_gemv_q4_k", "mrml_hip_gemm_q4_0", "mrml_hip_gemm_q4_0_q8", "mrml_hip_quantize_q8_0", "mrml_hip_argmax_f32", "mrml_hip_repack_q4_0"):
+                 "mrml_hip_gemv_q4_k", "mrml_hip_gemm_q4_0", "mrml_hip_gemm_q4_0_q8", "mrml_hip_gemm_q4_0_gpack", "mrml_hip_quantize_q8_0_gemm", "mrml_hip_quantize_q8_0", "mrml_hip_argmax_f32", "mrml_hip_repack_q4_0"):
         assert must in names
 
 

@@ -102,6 +102,18 @@ def test_gemm_q4_0_matches_gemv_and_pack_entry(backend, dev, orc, synth):
     a = run_gemm(backend, dev, w, x, rows, cols, batch)
     b = run_gemm(backend, dev, w, x, rows, cols, batch, prequantised=True)
     assert_bit_exact(a, b, "f32 entry vs pack entry")
+    # the GEMM pack, quantised once and used for two products
+    wb2 = backend.HipBuffer.from_gguf(dev, w, backend.Q4_0, rows, cols)
+    xb = backend.HipBuffer.from_host(dev, x.reshape(-1))
+    gp = backend.HipBuffer.alloc(dev, dev.gemm_pack_bytes(cols, batch), np.uint8)
+    y1 = backend.HipBuffer.alloc(dev, rows * batch)
+    y2 = backend.HipBuffer.alloc(dev, rows * batch)
+    dev.quantize_q8_0_gemm(xb, gp, cols, batch)
+    dev.gemm_q4_0_gpack(wb2, gp, y1, rows, cols, batch)
+    dev.gemm_q4_0_gpack(wb2, gp, y2, rows, cols, batch)
+    dev.sync()
+    assert_bit_exact(y1.numpy().reshape(batch, rows), a, "gpack entry vs f32 entry")
+    assert_bit_exact(y2.numpy().reshape(batch, rows), a, "gpack entry, second use")
     wb = backend.HipBuffer.from_gguf(dev, w, backend.Q4_0, rows, cols)
     yb = backend.HipBuffer.alloc(dev, rows)
     for m in (0, 1, 31, 32, 47):
@@ -115,6 +127,7 @@ def test_gemm_q4_0_rejects_bad_shapes(backend, dev):
     w = backend.HipBuffer.alloc(dev, 64 * 18, np.uint8)
     x = backend.HipBuffer.alloc(dev, 64 * 4)
     y = backend.HipBuffer.alloc(dev, 64 * 4)
-    for rows, cols, batch in [(33, 32, 2), (32, 48, 2), (32, 32, 0), (32, 32 * 513, 1)]:
+    # the last case: the activations would pass 2 GiB (32-bit buffer offsets)
+    for rows, cols, batch in [(33, 32, 2), (32, 48, 2), (32, 32, 0), (32, 2304, 1 << 22)]:
         with pytest.raises(backend.HipError):
             dev.gemm_q4_0(w, x, y, rows, cols, batch)
