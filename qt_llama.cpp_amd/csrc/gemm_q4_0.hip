@@ -11,24 +11,34 @@
 // The integer part is one v_mfma_i32_32x32x32_i8 per (32 rows, 32 tokens,
 // K block).  Lane l feeds row l%32 / token l%32 and K half l/32:
 //   A = the row's 16 quant bytes, low nibbles (half 0) or high nibbles
-//       (half 1), turned into signed bytes q-8 in registers (see sbytes), so
-//       the MFMA result is isum itself;
+//       (half 1), as signed bytes q-8 (see sbytes, applied when the weights
+//       are staged), so the MFMA result is isum itself;
 //   B = the token's 16 int8 quants of that K half.
 // Lane l receives D[8j+4(l/32)+i][l%32] in element 4j+i: 16 rows of ONE
 // token, so the token's block scale is a per-lane scalar and the rows'
 // scales are float4 broadcasts from LDS.
 //
 // The ordered f32 fold runs on the VALU: 4 instructions per output per block
-// (cvt, dw*da, *, +) against one MFMA per 1024 outputs, so the kernel is
-// VALU-bound once its operands arrive without stalls.  Operand feed:
+// against one MFMA per 1024 outputs.  Measured on gfx950: an MFMA holds its
+// SIMD's VALU issue while it executes (about 36 cycles for this one); f32
+// mul/add and integer ALU ops issue from two waves at once (about 2.4 SIMD
+// cycles each) while v_cvt_f32_i32 does not (about 4.5).  So the int->float
+// conversion is done without it: the MFMA accumulates onto C = 0x4B400000,
+// the bits of 1.5*2^23, and since |isum| <= 32*8*128 < 2^22 the sum stays in
+// the binade [2^23, 2^24) where one unit of the bit pattern is one unit of
+// value: D reinterpreted as f32 is exactly 1.5*2^23 + isum, and one exact
+// subtraction returns (float)isum.  Per output per block: sub, dw*da, *, +.
+// (The scale products form a rank-1 matrix that a v_mfma_f32_32x32x2_f32
+// could produce, but that MFMA costs more SIMD time than the 16 multiplies it
+// replaces.)  Operand feed:
 //   - B comes from a GEMM pack written in MFMA lane order (one 1 KB run of
 //     quants and one 128-byte run of scales per 32 tokens and block), read
 //     with one coalesced load each, kPF blocks ahead of use;
 //   - A is shared by the workgroup's four waves (four 32-token groups over
 //     one 32-row tile): kKC-block chunks of the 32 rows (128 contiguous bytes
 //     per row) and their f16 scales are loaded with coalesced loads into
-//     registers one chunk ahead and staged through kNBuf LDS buffers, one
-//     barrier per chunk.
+//     registers one chunk ahead, turned into signed bytes once (both K
+//     halves) and staged through kNBuf LDS buffers, one barrier per chunk.
 
 #include "device.h"
 #include "internal.h"
@@ -46,6 +56,8 @@ constexpr int kPF = 4;                    // B prefetch distance, blocks
 constexpr int kKC = 8;                    // blocks per A chunk
 constexpr int kNBuf = 3;                  // A chunk buffers in LDS
 constexpr int kBufferFlags = 0x00020000;  // buffer resource word 3 (raw 32-bit data) on gfx9
+constexpr float kMagic = 12582912.0f;      // 1.5 * 2^23
+constexpr int kMagicBits = 0x4B400000;     // its f32 bit pattern
 
 // GEMM pack of `batch` tokens x nb blocks, groups of 32 tokens (the last
 // group zero-padded):
@@ -122,7 +134,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
                                                                          float *__restrict__ y, int rows, int nb,
                                                                          int batch, int ngroups)
 {
-    __shared__ __align__(16) u32x4 sa[kNBuf][kKC][32];  // A chunks: [block][row] 16 quant bytes
+    __shared__ __align__(16) u32x4 sa[kNBuf][kKC][2][32];  // A chunks: [block][K half][row] 16 signed bytes
     __shared__ __align__(16) float sdw[kNBuf][kKC][32];  // their row scales, f32
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r0 = blockIdx.x * 32;
@@ -148,7 +160,10 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
         sreg = __builtin_amdgcn_raw_buffer_load_b16(wr, s_off + (uint32_t)c * (kKC * 2), 0, 0);
     };
     auto store_chunk = [&](int buf) {
-        sa[buf][ak][ar] = areg;
+        sa[buf][ak][0][ar] = u32x4{(uint32_t)sbytes(areg.x, 0), (uint32_t)sbytes(areg.y, 0),
+                                   (uint32_t)sbytes(areg.z, 0), (uint32_t)sbytes(areg.w, 0)};
+        sa[buf][ak][1][ar] = u32x4{(uint32_t)sbytes(areg.x, 4), (uint32_t)sbytes(areg.y, 4),
+                                   (uint32_t)sbytes(areg.z, 4), (uint32_t)sbytes(areg.w, 4)};
         sdw[buf][ak][ar] = f16_bits_to_f32(sreg);
     };
 
@@ -159,19 +174,22 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
         o.a = __builtin_amdgcn_raw_buffer_load_b128(gr, b_off + (uint32_t)b * 1024, 0, 0);
         o.da = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(gr, d_off + (uint32_t)b * 128, 0, 0));
     };
+    // C of every MFMA: the f32 bits of kMagic (see the header).
+    v16i cmagic;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) cmagic[e] = kMagicBits;
     auto mfma = [&](int buf, int kc, const BOps &o) {
-        const u32x4 wv = sa[buf][kc][tl];
-        const v4i a = {sbytes(wv.x, sh), sbytes(wv.y, sh), sbytes(wv.z, sh), sbytes(wv.w, sh)};
+        const u32x4 wv = sa[buf][kc][h][tl];
+        const v4i a = {(int)wv.x, (int)wv.y, (int)wv.z, (int)wv.w};
         const v4i bq = {(int)o.a.x, (int)o.a.y, (int)o.a.z, (int)o.a.w};
-        const v16i zero = {};
-        return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, zero, 0, 0, 0);
+        return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, cmagic, 0, 0, 0);
     };
 
     float acc[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
     // Block fold: the four float4s of row scales first (one wait), then
-    // 16 x (cvt, dw*da, *, +).
+    // 16 x (isum, dw*da, *, +).
     auto fold = [&](const v16i &d, float da, int buf, int kc) {
         const float4 *dwb = reinterpret_cast<const float4 *>(&sdw[buf][kc][4 * h]);
         float4 dw[4];
@@ -181,7 +199,13 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
         for (int j = 0; j < 4; ++j) {
             const float dwv[4] = {dw[j].x, dw[j].y, dw[j].z, dw[j].w};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[4 * j + i] = acc[4 * j + i] + (float)d[4 * j + i] * (dwv[i] * da);
+            for (int i = 0; i < 4; ++i) {
+                // (the element is copied out first: bit_cast of an ext-vector
+                // element lvalue reads element 0 in this compiler)
+                const int de = d[4 * j + i];
+                const float isum = __builtin_bit_cast(float, de) - kMagic;  // exact
+                acc[4 * j + i] = acc[4 * j + i] + isum * (dwv[i] * da);
+            }
         }
     };
 
@@ -195,28 +219,26 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
     BOps ring[kPF];
 #pragma unroll
     for (int s = 0; s < kPF; ++s) load_b(s, ring[s]);
-    v16i d = mfma(0, 0, ring[0]);
 
-    // Step (block b = kKC*c + kc): issue block b+1's MFMA, fold block b, refill
-    // block b's B slot with block b+kPF.  Scheduling barriers keep that order
-    // (the scheduler would otherwise gather the loads and wait for them all
-    // at once), so each wait covers only the block about to be used.  The
-    // steps may issue MFMAs and loads of blocks >= nb; those are never folded.
+    // Step (block b = kKC*c + kc): MFMA, fold, refill the block's B slot with
+    // block b+kPF.  The MFMA is not overlapped with the previous fold: while
+    // it executes no wave of the SIMD issues VALU work anyway.  A scheduling
+    // barrier keeps the refill after the fold (the scheduler would otherwise
+    // gather the loads and wait for them all at once), so each wait covers
+    // only the block about to be used.  Loads of blocks >= nb are never used.
     // Chunk reuse: at the end of chunk c, chunk c+2 is written into buffer
     // (c+2)%3 = (c-1)%3, whose last readers (chunk c-1's MFMAs and folds)
     // all come before the barrier that ended chunk c-1.
     int c = 0, cb = 0, nbf = 1, wb = 2;  // chunk, its buffer, the next chunk's buffer, the buffer to write
-    auto step = [&](int kc, BOps &cur, const BOps &next, bool refill, int b) {
-        const v16i dn = (kc + 1 < kKC) ? mfma(cb, kc + 1, next) : mfma(nbf, 0, next);
-        __builtin_amdgcn_sched_barrier(0);
+    auto step = [&](int kc, BOps &cur, bool refill, int b) {
+        const v16i d = mfma(cb, kc, cur);
         fold(d, cur.da, cb, kc);
         __builtin_amdgcn_sched_barrier(0);
         if (refill) load_b(b + kPF, cur);
-        d = dn;
     };
     for (; (c + 1) * kKC <= nb; ++c) {
 #pragma unroll
-        for (int kc = 0; kc < kKC; ++kc) step(kc, ring[kc % kPF], ring[(kc + 1) % kPF], true, c * kKC + kc);
+        for (int kc = 0; kc < kKC; ++kc) step(kc, ring[kc % kPF], true, c * kKC + kc);
         store_chunk(wb);
         lds_barrier();
         load_chunk(c + 3);
@@ -226,7 +248,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
     }
 #pragma unroll
     for (int kc = 0; kc < kKC - 1; ++kc)  // the last nb % kKC blocks
-        if (c * kKC + kc < nb) step(kc, ring[kc % kPF], ring[(kc + 1) % kPF], false, c * kKC + kc);
+        if (c * kKC + kc < nb) step(kc, ring[kc % kPF], false, c * kKC + kc);
 
     const int tok = g * 32 + tl;
     if (tok < batch) {
