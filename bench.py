@@ -48,6 +48,8 @@ BYTES_STEP = BYTES_GEGLU + BYTES_DOWN
 PEAK_HBM_GBS = 8000.0
 PEAK_INT8_TOPS = 5000.0                                # dense int8 MFMA, MI355X
 MALL_BYTES = 256 << 20
+# the dominant kernel of the step (the fused GeGLU that quantises x and emits the act pack)
+GEGLU_KERNEL = "gemv_q4_0_geglu_kernel<72, 8, true, true>"
 
 
 def load_backend():
@@ -129,6 +131,21 @@ def cpu_baseline(orc, synth, budget_s: float) -> dict:
             "ms_per_step": round(best * 1e3, 3)}
 
 
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
+    summary (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by what the
+    counter reads for the copy kernel of known size in the same run), or None
+    when no summary for this kernel exists."""
+    path = ROOT / "profiles" / "gemv_q4_0_geglu_traffic.json"
+    try:
+        d = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    if d.get("kernel") != kernel:
+        return None
+    return d.get("traffic_bytes")
+
+
 def decode_bytes_per_token(cfg: dict, pos: int) -> int:
     """Algorithmic HBM bytes of one token step at position `pos`: every layer's
     Q4_0 weights, the tied Q4_0 head, the f16 K and V rows read by attention
@@ -193,7 +210,30 @@ def decode_bench(be, synth, dev, ev, n_prefill: int, n_decode: int, cpu_steps: i
     return out, cpu
 
 
-def gemm_bench(be, synth, dev, ev, batch: int, cpu_tokens: int) -> dict:
+def decode_profile(be, synth, dev, n_prefill: int, n_steps: int) -> dict:
+    """Profiling aid for the C4 model: n_prefill + n_steps token steps issued
+    eagerly (no graph: the kernel trace then sees every launch); the last
+    n_steps are the decode steps at positions n_prefill.."""
+    cfg = dict(synth.GEMMA2_2B)
+    model = synth.gemma2_model(cfg, seed=1)
+    m = be.Gemma2Model.from_host(dev, model)
+    prompt = synth.prompt_tokens(n_prefill, cfg["vocab"], seed=1)
+    total = n_prefill + n_steps
+    state = be.HipBuffer.from_host(dev, np.array([prompt[0], 0], np.int32))
+    hist = be.HipBuffer.from_host(dev, np.full(total, -1, np.int32))
+    pr = be.HipBuffer.from_host(dev, prompt)
+    kc = be.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    vc = be.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    for i in range(total):
+        m.step(state, kc, vc, hist=hist, hist_cap=total, prompt=pr, prompt_len=n_prefill)
+        if i % 64 == 63:
+            dev.sync()
+    dev.sync()
+    m.close()
+    return {"profile_decode": n_steps, "prefill_tokens": n_prefill}
+
+
+def gemm_bench(be, synth, dev, ev, batch: int, cpu_tokens: int, profile: int = 0) -> dict:
     """M prefill tokens x K, quantised to Q8_0, times the
     Q4_0 gate/up (9216x2304) and down (2304x9216) matrices on int8 MFMA.
     Ops = 2*M*rows*cols per matrix (the int8 multiply-adds of the block dots);
@@ -210,21 +250,29 @@ def gemm_bench(be, synth, dev, ev, batch: int, cpu_tokens: int) -> dict:
         dev.quantize_q8_0_gemm(xb[k], packs[k], k, batch)
     y = be.HipBuffer.alloc(dev, batch * FFN)
     dev.sync()
+    if profile:
+        for _ in range(profile):
+            dev.quantize_q8_0_gemm(xb[DIM], packs[DIM], DIM, batch)
+            for k, (r, c) in mats.items():
+                dev.gemm_q4_0_gpack(w[k], packs[c], y, r, c, batch)
+        dev.sync()
+        return {"profile_gemm": profile, "launches": 4 * profile}
     per, total_ops, total_s = {}, 0, 0.0
+    per_graph = 10  # launches per graph, so host-side graph launch cost stays hidden
     for k, (r, c) in mats.items():
-        g = dev.capture(lambda: dev.gemm_q4_0_gpack(w[k], packs[c], y, r, c, batch))
-        time_graph(dev, ev, g, 5)
-        n = 50
-        secs = time_graph(dev, ev, g, n) / n
+        g = dev.capture(lambda: [dev.gemm_q4_0_gpack(w[k], packs[c], y, r, c, batch) for _ in range(per_graph)])
+        time_graph(dev, ev, g, 2)
+        n = 5
+        secs = time_graph(dev, ev, g, n) / (n * per_graph)
         g.close()
         ops = 2 * batch * r * c
         per[k] = {"us": round(secs * 1e6, 2), "tops": round(ops / secs / 1e12, 2)}
         total_ops += ops
         total_s += secs
     # quantising the [M][K] activations into the GEMM pack (once per input)
-    gq = dev.capture(lambda: dev.quantize_q8_0_gemm(xb[DIM], packs[DIM], DIM, batch))
-    time_graph(dev, ev, gq, 5)
-    tq = time_graph(dev, ev, gq, 50) / 50
+    gq = dev.capture(lambda: [dev.quantize_q8_0_gemm(xb[DIM], packs[DIM], DIM, batch) for _ in range(20)])
+    time_graph(dev, ev, gq, 2)
+    tq = time_graph(dev, ev, gq, 10) / 200
     gq.close()
     tops = total_ops / total_s / 1e12
     out = {"tops": round(tops, 2), "unit": "TOPS (int8)", "mfma_util": round(tops / PEAK_INT8_TOPS, 4),
@@ -265,6 +313,10 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-decode-steps", type=int, default=8)
     ap.add_argument("--gemm-batch", type=int, default=512)
+    ap.add_argument("--profile-gemm", type=int, default=0,
+                    help="profiling aid: N eager launches of each C5 product, then exit")
+    ap.add_argument("--profile-decode", type=int, default=0,
+                    help="profiling aid: prefill, then N eager decode steps of the C4 model, then exit")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--cpu-gemm-tokens", type=int, default=64)
     args = ap.parse_args()
@@ -278,6 +330,12 @@ def main() -> int:
     dev = be.HipDevice.new(0)
     info = dev.device_info()
     ev = HipEvents()
+    if args.profile_gemm:
+        print(json.dumps(gemm_bench(be, synth, dev, ev, args.gemm_batch, 0, profile=args.profile_gemm)))
+        return 0
+    if args.profile_decode:
+        print(json.dumps(decode_profile(be, synth, dev, args.decode_prefill, args.profile_decode)))
+        return 0
 
     # ---- synthetic config-2 data, rotated over > 2x MALL of distinct copies
     rng = synth.rng_for(2)
@@ -397,9 +455,9 @@ def main() -> int:
         "per_kernel_us": {"geglu": round(k_geglu * 1e6, 3), "gate": round(k_gate * 1e6, 3),
                           "up": round(k_up * 1e6, 3), "down": round(k_down * 1e6, 3)},
         "stream_copy_gbs": round(copy_gbs, 1),
-        "roofline": {"bound": "hbm", "kernel": "gemv_q4_0_geglu_kernel", "achieved": round(gbs_geglu, 1),
+        "roofline": {"bound": "hbm", "kernel": GEGLU_KERNEL, "achieved": round(gbs_geglu, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs_geglu / PEAK_HBM_GBS, 4),
-                     "traffic": None, "bytes_per_launch": BYTES_GEGLU,
+                     "traffic": measured_traffic(GEGLU_KERNEL), "bytes_per_launch": BYTES_GEGLU,
                      "avg_launch_us": round(k_geglu * 1e6, 3)},
         "cpu_baseline": cpu,
         "decode": decode,

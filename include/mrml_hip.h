@@ -227,8 +227,11 @@ int mrml_hip_gemm_q4_0_gpack(mrml_hip_ctx *ctx, const void *d_w, const void *d_g
 int mrml_hip_argmax_f32(mrml_hip_ctx *ctx, const float *d_x, int32_t n, int32_t *d_out);
 
 /* ---- the rest of the token step ---------------------------------------------
- * Floating-point ops whose reference results depend on libm and on the order
- * of long f32 sums: parity is to a stated tolerance.  Where an op takes both
+ * Every op keeps the CPU path's operation order: sums the reference evaluates
+ * sequentially in f32 (RMSNorm's sum of squares, the attention dots, softmax
+ * denominator and weighted sum of values) give the same bits here, and expf /
+ * tanhf / the RoPE table reproduce the host C library's results, so these
+ * outputs are bit-identical to the CPU path too.  Where an op takes both
  * `pos` and `d_pos`, a non-null d_pos (one int32 on the device) is read when
  * the op executes, so a captured graph serves every position. */
 
@@ -271,7 +274,7 @@ int mrml_hip_rope_kv_append_f16(mrml_hip_ctx *ctx, float *d_qkv, uint16_t *d_k_c
  * min(n_past+1, capacity) cache rows, kv head h / (n_heads / n_kv_heads),
  * in the CPU path's operation order (sequential dots, softmax sum and
  * weighted sum; the host C library's expf).  head_dim 256, group of at most
- * 8, capacity at most 16000.  d_out (f32) and d_pack (Q8_0 pack of the
+ * 8, capacity at most 6144.  d_out (f32) and d_pack (Q8_0 pack of the
  * n_heads*head_dim output) nullable, not both. */
 int mrml_hip_attn_decode_f16(mrml_hip_ctx *ctx, const float *d_q, const uint16_t *d_k_cache,
                              const uint16_t *d_v_cache, float *d_out, void *d_pack, int32_t n_past,

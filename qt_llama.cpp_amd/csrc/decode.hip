@@ -391,42 +391,58 @@ __global__ __launch_bounds__(512) void attn_scores_kernel(const float *__restric
     if (p0 + p < window) scores[(size_t)(kvh * G + g) * capacity + p0 + p] = dot * scale;
 }
 
-// Softmax and weighted values for query head h (one workgroup of head_dim
-// threads):  max over the window; e_p = expf(score_p - max); sum = 0 + e_0
-// + e_1 + ... in order; p_p = e_p * (1/sum); out[d] = 0 + p_0 v_0[d] + p_1
-// v_1[d] + ... in order.
+// Softmax and weighted values, query head h, dims [64*ds, 64*ds + 64) per
+// workgroup (blockIdx = (h, ds)):  max over the window; e_p = expf(score_p -
+// max); sum = 0 + e_0 + e_1 + ... in order; p_p = e_p * (1/sum); out[d] = 0 +
+// p_0 v_0[d] + p_1 v_1[d] + ... in order.  (The four workgroups of a head
+// each repeat the softmax; it is small next to the weighted sum.)
 //
-// V streams through two LDS slots of 128 rows (64 KB each): while thread d
-// runs its chain over tile t, the loads of tile t+1 (16 x 16 B per thread)
-// are in flight in registers, long enough (~128 dependent steps) to cover
-// the memory latency.  The first tile loads during the softmax.  Writes out
-// (nullable) and the Q8_0 pack of the n_heads*head_dim output (nullable).
+// The weighted sum splits into independent products and one ordered chain of
+// adds per dim.  Waves 1-3 stream V in tiles of kSVT positions (two tiles in
+// flight in registers, loaded before the softmax starts), form the products
+// p_t * v_t[d] and store them to LDS as [d][t]; wave 0 runs the 64 chains,
+// lane d adding its row four products per 16-byte LDS read, one tile behind
+// the producers (one barrier per tile, products double-buffered).  Writes
+// out (nullable) and the Q8_0 pack of the n_heads*head_dim output (nullable).
 // Dynamic LDS: capacity floats plus 4.
-constexpr int kVT = 128;  // V rows per tile
+constexpr int kSVD = 64;  // dims per workgroup
+constexpr int kSVT = 48;  // positions per tile: 48 rows x 8 chunks of 16 B = 2 chunks per producer thread
+constexpr int kSVP = kSVT + 4;  // product row stride (floats): 16-byte aligned, conflict-free float4 reads
 
 // A native 4 x 32-bit vector: copies of HIP's uint4 struct lower to memcpy,
 // which keeps an array of them in scratch memory instead of registers.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// Tile t of V (rows start + t*kVT ..), thread d: 16-byte chunk (d & 31) of
-// rows (d >> 5) + 8j, j < J; rows past the window reload the last row.
-template <int J>
-__device__ __forceinline__ void v_tile_load(u32x4 (&r)[J], const uint16_t *vbase, int t, int window, int start,
-                                            int capacity, size_t kv_dim, int d)
+// Producer thread pt (0..191) of tile t: chunks c = pt and pt + 192 (row c >>
+// 3, dims 8*(c & 7) .. +7 of the slice); rows past the window reload the last
+// row (their products are zeroed).
+__device__ __forceinline__ void sv_tile_load(u32x4 (&r)[2], const uint16_t *vslice, int t, int window, int start,
+                                             int capacity, size_t kv_dim, int pt)
 {
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-        int pr = t * kVT + (d >> 5) + 8 * j;
+    for (int k = 0; k < 2; ++k) {
+        const int c = pt + 192 * k;
+        int pr = t * kSVT + (c >> 3);
         pr = pr < window ? pr : window - 1;
-        r[j] = reinterpret_cast<const u32x4 *>(vbase + cache_row_of(start + pr, capacity) * kv_dim)[d & 31];
+        r[k] = reinterpret_cast<const u32x4 *>(vslice + cache_row_of(start + pr, capacity) * kv_dim)[c & 7];
     }
 }
 
-template <int J>
-__device__ __forceinline__ void v_tile_store(const u32x4 (&r)[J], uint16_t *slot, int d)
+__device__ __forceinline__ void sv_products(const u32x4 (&r)[2], const float *e_s, float (*prod)[kSVP], int t,
+                                            int window, int pt)
 {
 #pragma unroll
-    for (int j = 0; j < J; ++j) reinterpret_cast<u32x4 *>(slot + ((d >> 5) + 8 * j) * kAttnHD)[d & 31] = r[j];
+    for (int k = 0; k < 2; ++k) {
+        const int c = pt + 192 * k, row = c >> 3, d0 = 8 * (c & 7), pos = t * kSVT + row;
+        const bool live = pos < window;
+        const float pw = e_s[live ? pos : 0];
+        const uint32_t w[4] = {r[k].x, r[k].y, r[k].z, r[k].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float v = f16_bits_to_f32((w[i >> 1] >> (16 * (i & 1))) & 0xffffu);
+            prod[d0 + i][row] = live ? pw * v : 0.0f;
+        }
+    }
 }
 
 __global__ __launch_bounds__(256) void attn_softmax_v_kernel(const float *__restrict__ scores,
@@ -435,79 +451,91 @@ __global__ __launch_bounds__(256) void attn_softmax_v_kernel(const float *__rest
                                                              int n_heads, int n_kv_heads, int capacity, int expf_fused,
                                                              float *__restrict__ out, uint8_t *__restrict__ pack)
 {
-    constexpr int HD = kAttnHD, J = kVT / 8;  // 16-byte chunks per thread per tile
+    constexpr int HD = kAttnHD;
     extern __shared__ __align__(16) float e_s[];
     __shared__ float red[4];
-    __shared__ __align__(16) uint16_t v_s[2][kVT][HD];
+    __shared__ __align__(16) float prod[2][kSVD][kSVP];
     int window, start;
     attn_window(d_pos, n_past_arg, capacity, window, start);
-    const int h = blockIdx.x, d = threadIdx.x, G = n_heads / n_kv_heads, kvh = h / G;
+    const int h = blockIdx.x, ds = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int G = n_heads / n_kv_heads, kvh = h / G;
     const float *sc = scores + (size_t)h * capacity;
     const size_t kv_dim = (size_t)n_kv_heads * HD;
-    const uint16_t *vbase = v_cache + (size_t)kvh * HD;
-    const int ntiles = (window + kVT - 1) / kVT;
-    u32x4 vr[J];
-    v_tile_load<J>(vr, vbase, 0, window, start, capacity, kv_dim, d);
+    const uint16_t *vslice = v_cache + (size_t)kvh * HD + ds * kSVD;
+    const int ntiles = (window + kSVT - 1) / kSVT;
+    const bool producer = wave > 0;
+    const int pt = tid - 64;
+    u32x4 va[2], vb[2];  // tiles t (even) and t (odd) in flight
+    if (producer) {
+        sv_tile_load(va, vslice, 0, window, start, capacity, kv_dim, pt);
+        sv_tile_load(vb, vslice, 1 < ntiles ? 1 : 0, window, start, capacity, kv_dim, pt);
+    }
 
     float mx = -INFINITY;
-    for (int p = d; p < window; p += HD) mx = fmaxf(mx, sc[p]);
+    for (int p = tid; p < window; p += 256) mx = fmaxf(mx, sc[p]);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if ((d & 63) == 0) red[d >> 6] = mx;
+    if (lane == 0) red[wave] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int p = d; p < window; p += HD) e_s[p] = mrml_libm::expf(sc[p] - mx, expf_fused != 0);
+    for (int p = tid; p < window; p += 256) e_s[p] = mrml_libm::expf(sc[p] - mx, expf_fused != 0);
     __syncthreads();
     float *bcast = e_s + capacity;
-    if (d < 64) {
+    if (wave == 0) {
         const float sum = seq_sum(e_s, window);
-        if (d == 0) *bcast = sum;
+        if (lane == 0) *bcast = sum;
     }
-    v_tile_store<J>(vr, &v_s[0][0][0], d);
     __syncthreads();
     const float sum = *bcast;
     if (sum > 0.0f) {
         const float inv = 1.0f / sum;
-        for (int p = d; p < window; p += HD) e_s[p] = e_s[p] * inv;
+        for (int p = tid; p < window; p += 256) e_s[p] = e_s[p] * inv;
     }
     __syncthreads();
 
     float acc = 0.0f;
-    for (int t = 0; t < ntiles; ++t) {
-        // past the last tile this reloads the last one (unconditional code
-        // keeps the prefetch in registers); its copy lands in an unread slot
-        v_tile_load<J>(vr, vbase, t + 1 < ntiles ? t + 1 : t, window, start, capacity, kv_dim, d);
-        const uint16_t *vt = &v_s[t & 1][0][d];
-        const int np = window - t * kVT < kVT ? window - t * kVT : kVT;
-        if (np == kVT) {
-            const float4 *ep = reinterpret_cast<const float4 *>(e_s + t * kVT);
-#pragma unroll 8
-            for (int p4 = 0; p4 < kVT / 4; ++p4) {
-                const float4 e4 = ep[p4];
-                acc += e4.x * f16_bits_to_f32(vt[(4 * p4 + 0) * HD]);
-                acc += e4.y * f16_bits_to_f32(vt[(4 * p4 + 1) * HD]);
-                acc += e4.z * f16_bits_to_f32(vt[(4 * p4 + 2) * HD]);
-                acc += e4.w * f16_bits_to_f32(vt[(4 * p4 + 3) * HD]);
-            }
-        } else {
-            const float *e1 = e_s + t * kVT;
-            for (int p = 0; p < np; ++p) acc += e1[p] * f16_bits_to_f32(vt[p * HD]);
+    auto chain = [&](int t) {
+        const float4 *row = reinterpret_cast<const float4 *>(prod[t & 1][lane]);
+#pragma unroll
+        for (int q4 = 0; q4 < kSVT / 4; ++q4) {
+            const float4 x = row[q4];
+            acc = acc + x.x;  // zeroed tail products leave acc unchanged (it never holds -0)
+            acc = acc + x.y;
+            acc = acc + x.z;
+            acc = acc + x.w;
         }
-        // slot (t+1)&1 was last read in tile t-1, before the previous barrier
-        v_tile_store<J>(vr, &v_s[(t + 1) & 1][0][0], d);
+    };
+    // buffer (t+1)&1 was last read by wave 0 in tile t-1, before barrier t
+    for (int t = 0; t < ntiles; t += 2) {
+        if (producer) {
+            sv_products(va, e_s, prod[t & 1], t, window, pt);
+            sv_tile_load(va, vslice, t + 2 < ntiles ? t + 2 : t, window, start, capacity, kv_dim, pt);
+        }
         __syncthreads();
+        if (!producer) chain(t);
+        if (t + 1 < ntiles) {
+            if (producer) {
+                sv_products(vb, e_s, prod[(t + 1) & 1], t + 1, window, pt);
+                sv_tile_load(vb, vslice, t + 3 < ntiles ? t + 3 : t + 1, window, start, capacity, kv_dim, pt);
+            }
+            __syncthreads();
+            if (!producer) chain(t + 1);
+        }
     }
 
-    if (out) out[(size_t)h * HD + d] = acc;
-    if (pack) {
-        uint32_t dbits;
-        int s;
-        const int qv = q8_0_block32(acc, dbits, s);
-        const int nb = n_heads * HD / 32, blk = (h * HD + d) >> 5;
-        pack[(size_t)h * HD + d] = (uint8_t)(int8_t)qv;
-        if ((d & 31) == 0) {
-            reinterpret_cast<float *>(pack + (size_t)nb * 32)[blk] = f16_bits_to_f32(dbits);
-            reinterpret_cast<int32_t *>(pack + (size_t)nb * 36)[blk] = s;
+    if (wave == 0) {
+        const int o = h * HD + ds * kSVD + lane;
+        if (out) out[o] = acc;
+        if (pack) {
+            uint32_t dbits;
+            int s;
+            const int qv = q8_0_block32(acc, dbits, s);
+            const int nb = n_heads * HD / 32, blk = o >> 5;
+            pack[o] = (uint8_t)(int8_t)qv;
+            if ((lane & 31) == 0) {
+                reinterpret_cast<float *>(pack + (size_t)nb * 32)[blk] = f16_bits_to_f32(dbits);
+                reinterpret_cast<int32_t *>(pack + (size_t)nb * 36)[blk] = s;
+            }
         }
     }
 }
@@ -583,7 +611,7 @@ int launch_rope_kv_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache, uint16_
 }
 
 int attn_head_dim() { return kAttnHD; }
-int attn_max_capacity() { return 6144; }  // the window's softmax weights share LDS with two 64 KB V tiles
+int attn_max_capacity() { return 6144; }  // the window's softmax weights (24 KB) share LDS with the products
 
 size_t attn_scratch_bytes(int n_heads, int capacity) { return (size_t)n_heads * capacity * sizeof(float); }
 
@@ -596,7 +624,7 @@ int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_
     hipLaunchKernelGGL(attn_scores_kernel, sgrid, dim3(64 * (n_heads / n_kv_heads)), 0, ctx->stream, q, k_cache,
                        d_pos, n_past, n_heads, n_kv_heads, scale, capacity, scores);
     if (int rc = check_launch(ctx, "attn_scores_kernel")) return rc;
-    hipLaunchKernelGGL(attn_softmax_v_kernel, dim3(n_heads), dim3(kAttnHD), (size_t)capacity * sizeof(float) + 16,
+    hipLaunchKernelGGL(attn_softmax_v_kernel, dim3(n_heads, kAttnHD / kSVD), dim3(256), (size_t)capacity * sizeof(float) + 16,
                        ctx->stream, scores, v_cache, d_pos, n_past, n_heads, n_kv_heads, capacity,
                        (int)host_expf_fused(), out, (uint8_t *)pack);
     return check_launch(ctx, "attn_softmax_v_kernel");

@@ -188,6 +188,51 @@ def test_ffn_geglu_fused(backend, dev, orc, synth):
     assert_bit_exact(y2.numpy(), y.numpy(), "ffn without act output")
 
 
+def test_ffn_repeated_and_replayed(backend, dev, synth):
+    """The FFN entry point at the Gemma-2-2B shape, called many times in a row
+    and replayed from a captured graph with eager calls between the replays:
+    every result equals the composition of its two launches (GeGLU emitting
+    the act pack, then the down projection) bit for bit."""
+    dim, ffn = 2304, 9216
+    rng = synth.rng_for(5600)
+    wg, wu = synth.q4_0_matrix(rng, ffn, dim), synth.q4_0_matrix(rng, ffn, dim)
+    wd = synth.q4_0_matrix(rng, dim, ffn)
+    bg, bu = (backend.HipBuffer.from_gguf(dev, w, backend.Q4_0, ffn, dim) for w in (wg, wu))
+    bd = backend.HipBuffer.from_gguf(dev, wd, backend.Q4_0, dim, ffn)
+    apk = backend.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(ffn), np.uint8)
+    act_ref = backend.HipBuffer.alloc(dev, ffn)
+    y_ref = backend.HipBuffer.alloc(dev, dim)
+    act = backend.HipBuffer.alloc(dev, ffn)
+    y = backend.HipBuffer.alloc(dev, dim)
+    dev.reserve_workspace(1 << 20)
+
+    def reference(xb):
+        dev.gemv_q4_0_geglu_pack(bg, bu, xb, act_ref, apk, ffn, dim)
+        dev.gemv_q4_0_q8(bd, apk, y_ref, dim, ffn)
+        dev.sync()
+        return act_ref.numpy(), y_ref.numpy()
+
+    for i in range(12):
+        x = synth.rms_normalised(synth.normal_vector(rng, dim)) * np.float32(1 + i)
+        xb = upload(backend, dev, x)
+        dev.ffn_geglu_q4_0(bg, bu, bd, xb, act, y, dim, ffn)
+        dev.sync()
+        ra, ry = reference(xb)
+        assert_bit_exact(act.numpy(), ra, f"ffn act, call {i}")
+        assert_bit_exact(y.numpy(), ry, f"ffn y, call {i}")
+    xg = upload(backend, dev, synth.rms_normalised(synth.normal_vector(rng, dim)))
+    graph = dev.capture(lambda: dev.ffn_geglu_q4_0(bg, bu, bd, xg, act, y, dim, ffn))
+    _, ry = reference(xg)
+    for i in range(8):
+        graph.launch()
+        dev.sync()
+        assert_bit_exact(y.numpy(), ry, f"ffn graph replay {i}")
+        dev.ffn_geglu_q4_0(bg, bu, bd, xg, None, y, dim, ffn)  # an eager launch between replays
+        dev.sync()
+        assert_bit_exact(y.numpy(), ry, f"ffn eager after replay {i}")
+    graph.close()
+
+
 def test_gemv_q4_0_geglu_long_rows(backend, dev, orc, synth):
     """GeGLU on 288-block rows runs the relay kernel with two matrices."""
     rows, cols = 2304, 9216
