@@ -48,33 +48,41 @@ __device__ __forceinline__ float4 sq4(float4 a) { return make_float4(a.x * a.x, 
 
 // s = 0; s += v[i] for i = 0..n-1, each add rounded (v 16-byte aligned in
 // LDS).  Every lane of the calling wave runs the same chain on broadcast LDS
-// reads; the next batch's reads are in flight while the current batch is
-// added, so the chain runs at the rate of its dependent adds.
+// reads.  Two register batches alternate: one is added while the next one's
+// reads are in flight, with no copies between them, so the chain runs at the
+// latency of its dependent adds.
 __device__ float seq_sum(const float *v, int n)
 {
     constexpr int B = 8;  // float4 per batch
     const float4 *v4 = reinterpret_cast<const float4 *>(v);
     float s = 0.0f;
     const int nb = n / (4 * B);
-    if (nb > 0) {
-        float4 cur[B];
+    auto add_batch = [&](const float4 (&c)[B]) {
 #pragma unroll
-        for (int k = 0; k < B; ++k) cur[k] = v4[k];
-        for (int b = 0; b < nb; ++b) {
-            float4 nxt[B];
-            const int nb4 = (b + 1 < nb ? b + 1 : b) * B;  // the last batch re-reads itself
-#pragma unroll
-            for (int k = 0; k < B; ++k) nxt[k] = v4[nb4 + k];
-#pragma unroll
-            for (int k = 0; k < B; ++k) {
-                s += cur[k].x;
-                s += cur[k].y;
-                s += cur[k].z;
-                s += cur[k].w;
-            }
-#pragma unroll
-            for (int k = 0; k < B; ++k) cur[k] = nxt[k];
+        for (int k = 0; k < B; ++k) {
+            s += c[k].x;
+            s += c[k].y;
+            s += c[k].z;
+            s += c[k].w;
         }
+    };
+    if (nb > 0) {
+        float4 a[B], b[B];
+#pragma unroll
+        for (int k = 0; k < B; ++k) a[k] = v4[k];
+        int i = 0;
+        for (; i + 2 <= nb; i += 2) {
+            // the batch after the last re-reads the last one (never added)
+            const int nbx = (i + 1) * B;
+#pragma unroll
+            for (int k = 0; k < B; ++k) b[k] = v4[nbx + k];
+            add_batch(a);
+            const int nba = (i + 2 < nb ? i + 2 : i + 1) * B;
+#pragma unroll
+            for (int k = 0; k < B; ++k) a[k] = v4[nba + k];
+            add_batch(b);
+        }
+        if (i < nb) add_batch(a);
     }
     for (int i = nb * 4 * B; i < n; ++i) s += v[i];
     return s;
@@ -398,54 +406,66 @@ __global__ __launch_bounds__(512) void attn_scores_kernel(const float *__restric
 // each repeat the softmax; it is small next to the weighted sum.)
 //
 // The weighted sum splits into independent products and one ordered chain of
-// adds per dim.  Waves 1-3 stream V in tiles of kSVT positions (two tiles in
+// adds per dim.  Six producer waves stream V in tiles of kSVT positions (two tiles in
 // flight in registers, loaded before the softmax starts), form the products
-// p_t * v_t[d] and store them to LDS as [d][t]; wave 0 runs the 64 chains,
-// lane d adding its row four products per 16-byte LDS read, one tile behind
-// the producers (one barrier per tile, products double-buffered).  Writes
+// p_t * v_t[d] and store them to LDS as [t][d] (two 16-byte stores per 8
+// products, conflict-free); wave 0 runs the 64 chains, lane d adding column d
+// one tile behind the producers (one barrier per tile, products
+// double-buffered).  Writes
 // out (nullable) and the Q8_0 pack of the n_heads*head_dim output (nullable).
 // Dynamic LDS: capacity floats plus 4.
 constexpr int kSVD = 64;  // dims per workgroup
-constexpr int kSVT = 48;  // positions per tile: 48 rows x 8 chunks of 16 B = 2 chunks per producer thread
-constexpr int kSVP = kSVT + 4;  // product row stride (floats): 16-byte aligned, conflict-free float4 reads
+constexpr int kSVW = 8;   // waves: wave 0 adds; waves 1-3 and 5-7 produce; wave 4, which shares wave 0's SIMD, idles
+constexpr int kSVT = 96;  // positions per tile: 96 rows x 8 chunks of 16 B = 2 chunks per producer thread
+constexpr int kSVP = kSVD + 4;  // product row stride (floats): 16-byte aligned, conflict-free 16-byte stores
 
 // A native 4 x 32-bit vector: copies of HIP's uint4 struct lower to memcpy,
 // which keeps an array of them in scratch memory instead of registers.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// Producer thread pt (0..191) of tile t: chunks c = pt and pt + 192 (row c >>
-// 3, dims 8*(c & 7) .. +7 of the slice); rows past the window reload the last
-// row (their products are zeroed).
-__device__ __forceinline__ void sv_tile_load(u32x4 (&r)[2], const uint16_t *vslice, int t, int window, int start,
+// Producer thread pt (0..383) of tile t: chunks c = pt + 384k, k < kSVC (row
+// c >> 3, dims 8*(c & 7) .. +7 of the slice); rows past the window reload the
+// last row (their products are zeroed).  ring0 = cache row of the tile's
+// first position (the window's rows are consecutive modulo capacity).
+constexpr int kSVPT = 64 * (kSVW - 2);  // producer threads
+constexpr int kSVC = kSVT * 8 / kSVPT;
+static_assert(kSVT * 8 == kSVC * kSVPT, "whole chunks per producer");
+__device__ __forceinline__ void sv_tile_load(u32x4 (&r)[kSVC], const uint16_t *vslice, int t, int window, int ring0,
                                              int capacity, size_t kv_dim, int pt)
 {
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int c = pt + 192 * k;
-        int pr = t * kSVT + (c >> 3);
-        pr = pr < window ? pr : window - 1;
-        r[k] = reinterpret_cast<const u32x4 *>(vslice + cache_row_of(start + pr, capacity) * kv_dim)[c & 7];
+    for (int k = 0; k < kSVC; ++k) {
+        const int c = pt + kSVPT * k;
+        int rr = c >> 3;
+        rr = t * kSVT + rr < window ? rr : window - 1 - t * kSVT;
+        int row = ring0 + rr;
+        row = row >= capacity ? row - capacity : row;
+        r[k] = reinterpret_cast<const u32x4 *>(vslice + (size_t)row * kv_dim)[c & 7];
     }
 }
 
-__device__ __forceinline__ void sv_products(const u32x4 (&r)[2], const float *e_s, float (*prod)[kSVP], int t,
+__device__ __forceinline__ void sv_products(const u32x4 (&r)[kSVC], const float *e_s, float (*prod)[kSVP], int t,
                                             int window, int pt)
 {
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int c = pt + 192 * k, row = c >> 3, d0 = 8 * (c & 7), pos = t * kSVT + row;
+    for (int k = 0; k < kSVC; ++k) {
+        const int c = pt + kSVPT * k, row = c >> 3, d0 = 8 * (c & 7), pos = t * kSVT + row;
         const bool live = pos < window;
         const float pw = e_s[live ? pos : 0];
         const uint32_t w[4] = {r[k].x, r[k].y, r[k].z, r[k].w};
+        float pv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const float v = f16_bits_to_f32((w[i >> 1] >> (16 * (i & 1))) & 0xffffu);
-            prod[d0 + i][row] = live ? pw * v : 0.0f;
+            pv[i] = live ? pw * v : 0.0f;
         }
+        float4 *dst = reinterpret_cast<float4 *>(&prod[row][d0]);
+        dst[0] = make_float4(pv[0], pv[1], pv[2], pv[3]);
+        dst[1] = make_float4(pv[4], pv[5], pv[6], pv[7]);
     }
 }
 
-__global__ __launch_bounds__(256) void attn_softmax_v_kernel(const float *__restrict__ scores,
+__global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *__restrict__ scores,
                                                              const uint16_t *__restrict__ v_cache,
                                                              const int32_t *__restrict__ d_pos, int n_past_arg,
                                                              int n_heads, int n_kv_heads, int capacity, int expf_fused,
@@ -453,8 +473,8 @@ __global__ __launch_bounds__(256) void attn_softmax_v_kernel(const float *__rest
 {
     constexpr int HD = kAttnHD;
     extern __shared__ __align__(16) float e_s[];
-    __shared__ float red[4];
-    __shared__ __align__(16) float prod[2][kSVD][kSVP];
+    __shared__ float red[kSVW];
+    __shared__ __align__(16) float prod[2][kSVT][kSVP];
     int window, start;
     attn_window(d_pos, n_past_arg, capacity, window, start);
     const int h = blockIdx.x, ds = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -463,22 +483,33 @@ __global__ __launch_bounds__(256) void attn_softmax_v_kernel(const float *__rest
     const size_t kv_dim = (size_t)n_kv_heads * HD;
     const uint16_t *vslice = v_cache + (size_t)kvh * HD + ds * kSVD;
     const int ntiles = (window + kSVT - 1) / kSVT;
-    const bool producer = wave > 0;
-    const int pt = tid - 64;
-    u32x4 va[2], vb[2];  // tiles t (even) and t (odd) in flight
+    const bool producer = (wave & 3) != 0;
+    const int pt = (wave < 4 ? wave - 1 : wave - 2) * 64 + lane;
+    // cache row of tile t's first position: ring row of `start`, advanced by kSVT per tile
+    const int ring_start = (int)cache_row_of(start, capacity), step = kSVT % (capacity > 0 ? capacity : 1 << 30);
+    auto ring_next = [&](int r) { return r + step >= capacity ? r + step - capacity : r + step; };
+    // tiles t .. t+3 in flight in registers (slot t % 4); ring[k] = cache row of the slot's tile
+    u32x4 vt[4][kSVC];
+    int ring[4];
+    ring[0] = ring_start;
+#pragma unroll
+    for (int k = 1; k < 4; ++k) ring[k] = ring_next(ring[k - 1]);
     if (producer) {
-        sv_tile_load(va, vslice, 0, window, start, capacity, kv_dim, pt);
-        sv_tile_load(vb, vslice, 1 < ntiles ? 1 : 0, window, start, capacity, kv_dim, pt);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (k < ntiles) sv_tile_load(vt[k], vslice, k, window, ring[k], capacity, kv_dim, pt);
     }
 
+    // max over the window (exact in any order): DPP within each half-wave
     float mx = -INFINITY;
-    for (int p = tid; p < window; p += 256) mx = fmaxf(mx, sc[p]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    for (int p = tid; p < window; p += 64 * kSVW) mx = fmaxf(mx, sc[p]);
+    mx = max32(mx);
+    mx = fmaxf(mx, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx), 32)));
     if (lane == 0) red[wave] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int p = tid; p < window; p += 256) e_s[p] = mrml_libm::expf(sc[p] - mx, expf_fused != 0);
+#pragma unroll
+    for (int w = 0; w < kSVW; ++w) mx = fmaxf(mx, red[w]);
+    for (int p = tid; p < window; p += 64 * kSVW) e_s[p] = mrml_libm::expf(sc[p] - mx, expf_fused != 0);
     __syncthreads();
     float *bcast = e_s + capacity;
     if (wave == 0) {
@@ -489,38 +520,52 @@ __global__ __launch_bounds__(256) void attn_softmax_v_kernel(const float *__rest
     const float sum = *bcast;
     if (sum > 0.0f) {
         const float inv = 1.0f / sum;
-        for (int p = tid; p < window; p += 256) e_s[p] = e_s[p] * inv;
+        for (int p = tid; p < window; p += 64 * kSVW) e_s[p] = e_s[p] * inv;
     }
     __syncthreads();
 
     float acc = 0.0f;
+    // The column in batches of 16: the next batch's reads are in flight while
+    // the current one is added (16 dependent adds outlast an LDS read).
+    // Zeroed tail products leave acc unchanged (it never holds -0).
+    static_assert(kSVT % 32 == 0, "batches of 16, an even number of them");
     auto chain = [&](int t) {
-        const float4 *row = reinterpret_cast<const float4 *>(prod[t & 1][lane]);
+        const float(*col)[kSVP] = prod[t & 1];
+        float b0[16], b1[16];
+        auto fetch = [&](float (&b)[16], int g) {
 #pragma unroll
-        for (int q4 = 0; q4 < kSVT / 4; ++q4) {
-            const float4 x = row[q4];
-            acc = acc + x.x;  // zeroed tail products leave acc unchanged (it never holds -0)
-            acc = acc + x.y;
-            acc = acc + x.z;
-            acc = acc + x.w;
+            for (int i = 0; i < 16; ++i) b[i] = col[16 * g + i][lane];
+        };
+        auto add = [&](const float (&b)[16]) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc = acc + b[i];
+        };
+        fetch(b0, 0);
+#pragma unroll
+        for (int g = 0; g < kSVT / 16; g += 2) {
+            fetch(b1, g + 1);
+            add(b0);
+            if (g + 2 < kSVT / 16) fetch(b0, g + 2);
+            add(b1);
         }
     };
     // buffer (t+1)&1 was last read by wave 0 in tile t-1, before barrier t
-    for (int t = 0; t < ntiles; t += 2) {
+    auto tile = [&](int t, int k) {  // k = t % 4, a compile-time slot
         if (producer) {
-            sv_products(va, e_s, prod[t & 1], t, window, pt);
-            sv_tile_load(va, vslice, t + 2 < ntiles ? t + 2 : t, window, start, capacity, kv_dim, pt);
+            sv_products(vt[k], e_s, prod[t & 1], t, window, pt);
+            if (t + 4 < ntiles) {
+                ring[k] = ring_next(ring_next(ring_next(ring_next(ring[k]))));
+                sv_tile_load(vt[k], vslice, t + 4, window, ring[k], capacity, kv_dim, pt);
+            }
         }
         __syncthreads();
-        if (!producer) chain(t);
-        if (t + 1 < ntiles) {
-            if (producer) {
-                sv_products(vb, e_s, prod[(t + 1) & 1], t + 1, window, pt);
-                sv_tile_load(vb, vslice, t + 3 < ntiles ? t + 3 : t + 1, window, start, capacity, kv_dim, pt);
-            }
-            __syncthreads();
-            if (!producer) chain(t + 1);
-        }
+        if (wave == 0) chain(t);
+    };
+    for (int t = 0; t < ntiles; t += 4) {
+        tile(t, 0);
+        if (t + 1 < ntiles) tile(t + 1, 1);
+        if (t + 2 < ntiles) tile(t + 2, 2);
+        if (t + 3 < ntiles) tile(t + 3, 3);
     }
 
     if (wave == 0) {
@@ -624,7 +669,7 @@ int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_
     hipLaunchKernelGGL(attn_scores_kernel, sgrid, dim3(64 * (n_heads / n_kv_heads)), 0, ctx->stream, q, k_cache,
                        d_pos, n_past, n_heads, n_kv_heads, scale, capacity, scores);
     if (int rc = check_launch(ctx, "attn_scores_kernel")) return rc;
-    hipLaunchKernelGGL(attn_softmax_v_kernel, dim3(n_heads, kAttnHD / kSVD), dim3(256), (size_t)capacity * sizeof(float) + 16,
+    hipLaunchKernelGGL(attn_softmax_v_kernel, dim3(n_heads, kAttnHD / kSVD), dim3(64 * kSVW), (size_t)capacity * sizeof(float) + 16,
                        ctx->stream, scores, v_cache, d_pos, n_past, n_heads, n_kv_heads, capacity,
                        (int)host_expf_fused(), out, (uint8_t *)pack);
     return check_launch(ctx, "attn_softmax_v_kernel");
