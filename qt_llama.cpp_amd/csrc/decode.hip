@@ -136,19 +136,31 @@ __device__ __forceinline__ void emit_q8(float4 v, int c, int n4, uint8_t *pack, 
     }
 }
 
-// out = (x * scale) * w per value (w nullable), stored to out (nullable) and
-// as a Q8_0 pack (nullable).
+// Loads the weight chunks of this thread (w nullable: no load), issued
+// with the kernel's other loads so none waits behind the norm's sums.
 template <int CH>
-__device__ __forceinline__ void norm_store(const float4 (&v)[CH], float scale, const float *w, float *out,
-                                           uint8_t *pack, int n4)
+__device__ __forceinline__ void load_w(const float *w, float4 (&wv)[CH], int n4)
 {
     const float4 *w4 = reinterpret_cast<const float4 *>(w);
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+        const int c = threadIdx.x + k * blockDim.x;
+        wv[k] = w ? w4[c < n4 ? c : 0] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    }
+}
+
+// out = (x * scale) * w per value (has_w false: no weight), stored to out
+// (nullable) and as a Q8_0 pack (nullable).
+template <int CH>
+__device__ __forceinline__ void norm_store(const float4 (&v)[CH], float scale, const float4 (&wv)[CH], bool has_w,
+                                           float *out, uint8_t *pack, int n4)
+{
 #pragma unroll
     for (int k = 0; k < CH; ++k) {
         if (k * (int)blockDim.x >= n4) break;  // uniform
         const int c = threadIdx.x + k * blockDim.x;
         float4 o = scale4(v[k], scale);
-        if (w) o = mul4(o, w4[c < n4 ? c : 0]);
+        if (has_w) o = mul4(o, wv[k]);
         if (out && c < n4) reinterpret_cast<float4 *>(out)[c] = o;
         if (pack) emit_q8(o, c, n4, pack, n4 >> 3);
     }
@@ -164,13 +176,14 @@ __global__ __launch_bounds__(kNormMaxThreads) void rms_norm_kernel(const float *
     extern __shared__ __align__(16) float lds[];
     const int n4 = dim >> 2;
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
-    float4 v[CH];
+    float4 v[CH], wv[CH];
 #pragma unroll
     for (int k = 0; k < CH; ++k) {
         const int c = threadIdx.x + k * blockDim.x;
         v[k] = c < n4 ? x4[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    norm_store(v, rms_scale(block_seq_sum_sq(v, n4, lds), dim, eps), w, out, pack, n4);
+    load_w(w, wv, n4);
+    norm_store(v, rms_scale(block_seq_sum_sq(v, n4, lds), dim, eps), wv, w != nullptr, out, pack, n4);
 }
 
 // Sandwich-norm residual of a Gemma-2 block followed by the next block's
@@ -192,7 +205,7 @@ __global__ __launch_bounds__(kNormMaxThreads) void residual_rms_norm_kernel(cons
     const float4 *wp4 = reinterpret_cast<const float4 *>(w_post);
     const float4 one4 = make_float4(1.0f, 1.0f, 1.0f, 1.0f), zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     // every operand's load is issued before the first sum
-    float4 v[CH], hv[CH], wv[CH];
+    float4 v[CH], hv[CH], wv[CH], wn[CH];
 #pragma unroll
     for (int k = 0; k < CH; ++k) {
         const int c = threadIdx.x + k * blockDim.x;
@@ -201,6 +214,7 @@ __global__ __launch_bounds__(kNormMaxThreads) void residual_rms_norm_kernel(cons
         hv[k] = h4[cc];
         wv[k] = w_post ? wp4[cc] : one4;
     }
+    if (xn || pack) load_w(w_next, wn, n4);
     const float s1 = rms_scale(block_seq_sum_sq(v, n4, lds), dim, eps);
 #pragma unroll
     for (int k = 0; k < CH; ++k) {
@@ -212,7 +226,7 @@ __global__ __launch_bounds__(kNormMaxThreads) void residual_rms_norm_kernel(cons
         v[k] = c < n4 ? hn : zero4;
     }
     if (!xn && !pack) return;
-    norm_store(v, rms_scale(block_seq_sum_sq(v, n4, lds), dim, eps), w_next, xn, pack, n4);
+    norm_store(v, rms_scale(block_seq_sum_sq(v, n4, lds), dim, eps), wn, w_next != nullptr, xn, pack, n4);
 }
 
 // Token embedding (CudaDevice::embedding_q8_0, cuda.rs:2625-2656; CPU
@@ -229,11 +243,12 @@ __global__ __launch_bounds__(kNormMaxThreads) void embedding_kernel(const uint8_
                                                          uint8_t *__restrict__ pack, int dim, int vocab)
 {
     extern __shared__ __align__(16) float lds[];
-    int tok = d_token ? *d_token : token;
+    int tok = d_token ? *d_token : token;  // the weight loads below do not wait for it
     tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
     const int n4 = dim >> 2, nb = dim >> 5;
     const size_t nblk = (size_t)vocab * nb, row = (size_t)tok * nb;
-    float4 v[CH];
+    float4 v[CH], wv[CH];
+    if (xn || pack) load_w(w_norm, wv, n4);
 #pragma unroll
     for (int k = 0; k < CH; ++k) {
         const int c_raw = threadIdx.x + k * blockDim.x;
@@ -257,7 +272,7 @@ __global__ __launch_bounds__(kNormMaxThreads) void embedding_kernel(const uint8_
         v[k] = c_raw < n4 ? o : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     if (!xn && !pack) return;
-    norm_store(v, rms_scale(block_seq_sum_sq(v, n4, lds), dim, eps), w_norm, xn, pack, n4);
+    norm_store(v, rms_scale(block_seq_sum_sq(v, n4, lds), dim, eps), wv, w_norm != nullptr, xn, pack, n4);
 }
 
 // RoPE (NeoX half split, ops.rs:185-208) on the q and k heads of a stacked

@@ -269,18 +269,33 @@ __device__ float block_seq_sum_nonneg(const float *a, int n, uint8_t *flags, Sha
 
 // The same sum when thread t holds terms 4t..4t+3 in registers (n <= 4 *
 // blockDim; terms at or past n are ignored) -- the layout of the norm
-// kernels, where it needs no LDS copy of the terms and five barriers.
-// Neighbouring threads' unsafe flags travel by DPP within a wave and through
-// LDS across waves; each run's addend is formed during the walk.
+// kernels.  Each wave forms the events of its own 256 terms: its first term
+// always starts an event and its last always ends one (splitting a run of
+// exact steps keeps every partial sum exact), so no flag or ulp count
+// crosses a wave.  Each event is written by one term: an unsafe term writes
+// its value, a run's last term writes (Re - Rs) * u, where Rs (the wave's
+// ulp prefix before the run's first term) reaches it by a max-scan (the
+// prefix never decreases).  The prefix stays below 2^31: the safe steps in
+// one binade add fewer than 2^23 ulps, and s visits each binade once.
+// The events land in block order after the waves' counts are exchanged;
+// wave 0 then adds them with operands from broadcast LDS reads (a register
+// chain: v_readlane operands would cost several times more per add).  Four
+// barriers, all LDS-only (pending global stores are not waited for).  Ends
+// without a barrier after reading the result: x may be rewritten only after
+// the caller's next barrier.
+constexpr int kPadEvents = 16;  // zeros after the last event (the walk reads groups of 16)
+
 struct Shared4 {
-    float add[kEventCap];  // a single term's value, or the run's ulp (u)
-    int Rs[kEventCap];     // a run's ulp prefix before its first term (-1 marks a single term)
-    int Re[kEventCap];     // a run's ulp prefix after its last term
-    float wtot[16];
-    int wcnt[16], winc[16];
-    int wfirst[16], wlast[16];  // unsafe masks of each wave's first and last lanes
+    float ev[16 * 256 + kPadEvents];  // event addends in order (at most one per term)
+    float wtot[16];                   // per-wave totals of the approximate prefix scan
+    int wcnt[16];                     // per-wave event counts
     float result;
 };
+
+__device__ __forceinline__ void lds_barrier()  // s_barrier after this wave's LDS accesses
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 __device__ __forceinline__ int wave_shr1_i32(int v)  // lane l gets lane l-1 (lane 0: 0)
 {
@@ -291,145 +306,160 @@ __device__ __forceinline__ int wave_shl1_i32(int v)  // lane l gets lane l+1 (la
     return __builtin_amdgcn_update_dpp(0, v, 0x130, 0xf, 0xf, true);
 }
 
+// inclusive max-scan over the wave (the same DPP steps as the sums above)
+__device__ __forceinline__ uint32_t wave_incl_max_u32(uint32_t v)
+{
+    auto mx = [](uint32_t a, int b) { return a > (uint32_t)b ? a : (uint32_t)b; };
+    v = mx(v, dpp_i32<0x111, 0xf>((int)v));
+    v = mx(v, dpp_i32<0x112, 0xf>((int)v));
+    v = mx(v, dpp_i32<0x114, 0xf>((int)v));
+    v = mx(v, dpp_i32<0x118, 0xf>((int)v));
+    v = mx(v, dpp_i32<0x142, 0xa>((int)v));
+    v = mx(v, dpp_i32<0x143, 0xc>((int)v));
+    return v;
+}
+
+// inclusive scans within each 16-lane row (row 0 carries the per-wave values)
+__device__ __forceinline__ int row_incl_scan_i32(int v)
+{
+    v += dpp_i32<0x111, 0xf>(v);
+    v += dpp_i32<0x112, 0xf>(v);
+    v += dpp_i32<0x114, 0xf>(v);
+    v += dpp_i32<0x118, 0xf>(v);
+    return v;
+}
+__device__ __forceinline__ float row_incl_scan_f32(float v)
+{
+    v += dpp_f32<0x111, 0xf>(v);
+    v += dpp_f32<0x112, 0xf>(v);
+    v += dpp_f32<0x114, 0xf>(v);
+    v += dpp_f32<0x118, 0xf>(v);
+    return v;
+}
+
+__device__ __forceinline__ float readlane_f32(float v, int l)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
 __device__ float block_seq_sum_nonneg4(float4 v, int n, Shared4 &x)
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
     const int k0 = 4 * tid;
-    const float a[4] = {v.x, v.y, v.z, v.w};
+    float a[4] = {v.x, v.y, v.z, v.w};
     float lp[4], run = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        run += k0 + i < n ? a[i] : 0.0f;
+        a[i] = k0 + i < n ? a[i] : 0.0f;
+        run += a[i];
         lp[i] = run;
     }
+    // approximate prefix: thread-local, wave scan, earlier waves' totals
     const float wincl = wave_incl_scan_f32(run);
     if (lane == 63) x.wtot[wave] = wincl;
-    __syncthreads();  // 1
-    float base = __builtin_bit_cast(float, wave_shr1_i32(__builtin_bit_cast(int, wincl)));
-    {
-        float t[16];
-#pragma unroll
-        for (int w = 0; w < 16; ++w) t[w] = w < nw ? x.wtot[w] : 0.0f;
-#pragma unroll
-        for (int w = 0; w < 16; ++w) base += w < wave ? t[w] : 0.0f;
-    }
-    int inc[4], mask = 0, my_inc = 0;
+    lds_barrier();
+    const float wt = lane < wave ? x.wtot[lane] : 0.0f;  // lane < wave <= 15: row 0
+    const float base =
+        __builtin_bit_cast(float, wave_shr1_i32(__builtin_bit_cast(int, wincl))) + readlane_f32(row_incl_scan_f32(wt), 15);
+    // classify; unsafe: bit i set for an unsafe term, stop: unsafe or past n
+    uint32_t inc[4], my_inc = 0;
     float uu[4];
+    int unsafe = 0, stop = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int k = k0 + i;
         const Step st = classify(a[i], i ? base + lp[i - 1] : base, base + lp[i], k);
         const bool in = k < n;
-        inc[i] = (in && st.safe) ? st.inc : -1;
+        inc[i] = (in && st.safe) ? (uint32_t)st.inc : 0u;
         uu[i] = st.u;
-        mask |= (in && !st.safe) ? (1 << i) : 0;
-        my_inc += inc[i] > 0 ? inc[i] : 0;
+        unsafe |= (in && !st.safe) ? (1 << i) : 0;
+        stop |= (!in || !st.safe) ? (1 << i) : 0;
+        my_inc += inc[i];
     }
-    if (lane == 0) x.wfirst[wave] = mask;
-    if (lane == 63) x.wlast[wave] = mask;
-    __syncthreads();  // 2
-    int prev = wave_shr1_i32(mask), next = wave_shl1_i32(mask);
-    if (lane == 0) prev = wave > 0 ? x.wlast[wave - 1] : 0;
-    if (lane == 63) next = wave + 1 < nw ? x.wfirst[wave + 1] : 0;
-    // term i starts an event when it is unsafe or follows an unsafe term
-    // (term 0 of the sum is always unsafe); it ends a run when the next term
-    // is unsafe or it is the last term
-    const int prev_bit3 = (prev >> 3) & 1, next_bit0 = next & 1;
-    int cnt = 0;
-    bool start[4], last[4];
+    // event starts: an unsafe term, a term after an unsafe one, the wave's
+    // first term; run ends: a safe term before a stop, the wave's last term
+    const int pv = wave_shr1_i32(unsafe), nx = wave_shl1_i32(stop);  // every lane takes part
+    const int prev = lane == 0 ? 8 : pv, next = lane == 63 ? 1 : nx;
+    int starts = 0, ends = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int k = k0 + i;
-        const bool before = i ? ((mask >> (i - 1)) & 1) : prev_bit3;
-        const bool after = i < 3 ? ((mask >> (i + 1)) & 1) : next_bit0;
-        start[i] = k < n && (((mask >> i) & 1) || before);
-        last[i] = k < n && (after || k == n - 1);
-        cnt += start[i] ? 1 : 0;
+        const bool in = k0 + i < n, uns = (unsafe >> i) & 1;
+        const bool before = i ? (unsafe >> (i - 1)) & 1 : (prev >> 3) & 1;
+        const bool after = i < 3 ? (stop >> (i + 1)) & 1 : next & 1;
+        starts |= (in && (uns || before)) ? (1 << i) : 0;
+        ends |= (in && !uns && after) ? (1 << i) : 0;
     }
-    const int cincl = wave_incl_scan_i32(cnt), iincl = wave_incl_scan_i32(my_inc);
-    if (lane == 63) {
-        x.wcnt[wave] = cincl;
-        x.winc[wave] = iincl;
-    }
-    __syncthreads();  // 3
-    int ebase = cincl - cnt, ibase = iincl - my_inc, nev = 0;
-    {
-        int c[16], ic[16];
-#pragma unroll
-        for (int w = 0; w < 16; ++w) {
-            c[w] = w < nw ? x.wcnt[w] : 0;
-            ic[w] = w < nw ? x.winc[w] : 0;
-        }
-#pragma unroll
-        for (int w = 0; w < 16; ++w) {
-            ebase += w < wave ? c[w] : 0;
-            ibase += w < wave ? ic[w] : 0;
-            nev += c[w];
-        }
-    }
-    if (nev > kEventCap) {
-        // too many events for LDS (e.g. many exact ties): the plain loop
-        // over the terms, staged through the event buffer in pieces
-        float s = 0.0f;
-        for (int c0 = 0; c0 < n; c0 += kEventCap) {
-            __syncthreads();
-            for (int i = 0; i < 4; ++i) {
-                const int k = k0 + i;
-                if (k >= c0 && k < c0 + kEventCap && k < n) x.add[k - c0] = a[i];
-            }
-            __syncthreads();
-            if (tid < 64) {
-                const int m = n - c0 < kEventCap ? n - c0 : kEventCap;
-                for (int j = 0; j < m; ++j) s += x.add[j];
-            }
-        }
-        if (tid == 0) x.result = s;
-        __syncthreads();
-        const float r = x.result;
-        __syncthreads();
-        return r;
-    }
-    int E = ebase - 1, pre = ibase;
+    const int cnt = __builtin_popcount(starts);
+    const int cincl = wave_incl_scan_i32(cnt);
+    const uint32_t iincl = (uint32_t)wave_incl_scan_i32((int)my_inc);
+    // Rs of this thread's latest run start, max-scanned over the wave
+    uint32_t r = iincl - my_inc, mine = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        if (start[i]) ++E;
-        if (k0 + i < n) {
-            if (inc[i] < 0) {
-                x.add[E] = a[i];
-                x.Rs[E] = -1;
-            } else {
-                if (start[i]) {
-                    x.add[E] = uu[i];
-                    x.Rs[E] = pre;
-                }
-                pre += inc[i];
-                if (last[i]) x.Re[E] = pre;
-            }
-        }
+        if (((starts & ~unsafe) >> i) & 1) mine = r;
+        r += inc[i];
     }
-    __syncthreads();  // 4
-    if (tid < 64) {
-        // lane j forms event j's addend (a run adds (Re - Rs) ulps: exact,
-        // fewer than 2^24 of them and u a power of 2); the ordered sum then
-        // takes the lanes one by one, with no memory access on its chain
+    uint32_t rs = (uint32_t)wave_shr1_i32((int)wave_incl_max_u32(mine));
+    if (lane == 63) x.wcnt[wave] = cincl;
+    lds_barrier();
+    // this wave's offset in the block's list, and the list's length
+    const int cw = lane < nw ? x.wcnt[lane] : 0;  // row 0
+    const int ci = row_incl_scan_i32(cw);
+    const int nev = __builtin_amdgcn_readlane(ci, 15);
+    const int wv = __builtin_amdgcn_readfirstlane(wave);  // uniform: a lane index for readlane
+    const int goff = wv ? __builtin_amdgcn_readlane(ci, wv - 1) : 0;
+    if (wave == 0 && lane < kPadEvents) x.ev[nev + lane] = 0.0f;
+    float *ev = x.ev + goff;
+    int e = cincl - cnt;  // events started before this thread's terms
+    r = iincl - my_inc;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const bool st = (starts >> i) & 1;
+        e += st ? 1 : 0;
+        if (st && !((unsafe >> i) & 1)) rs = r;
+        const uint32_t re = r + inc[i];
+        if ((unsafe >> i) & 1) ev[e - 1] = a[i];
+        if ((ends >> i) & 1) ev[e - 1] = (float)(int)(re - rs) * uu[i];  // exact: < 2^23 ulps, u a power of 2
+        r = re;
+    }
+    lds_barrier();
+    // the ordered sum, by wave 0 alone: groups of 16 events read as four
+    // broadcast float4 loads, two groups alternating so one is added while
+    // the next one's loads are in flight (the zero pad makes the last group
+    // whole; +0 leaves s unchanged: s >= +0)
+    if (wave == 0) {
+        const float4 *e4 = reinterpret_cast<const float4 *>(x.ev);
+        const int ng = (nev + 15) >> 4;
         float s = 0.0f;
-        for (int j0 = 0; j0 < nev; j0 += 64) {
-            const int j = j0 + lane;
-            float val = 0.0f;
-            if (j < nev) {
-                const int rs = x.Rs[j];
-                val = rs < 0 ? x.add[j] : (float)(x.Re[j] - rs) * x.add[j];
+        auto add_group = [&](const float4 (&c)[4]) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                s += c[q].x;
+                s += c[q].y;
+                s += c[q].z;
+                s += c[q].w;
             }
-            const int m = nev - j0 < 64 ? nev - j0 : 64;
-            for (int l = 0; l < m; ++l)
-                s += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, val), l));
+        };
+        if (ng > 0) {
+            float4 ga[4], gb[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ga[q] = e4[q];
+            int g = 0;
+            for (; g + 2 <= ng; g += 2) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) gb[q] = e4[4 * (g + 1) + q];
+                add_group(ga);
+                const int gn = g + 2 < ng ? g + 2 : ng - 1;  // past the end: re-read, never added
+#pragma unroll
+                for (int q = 0; q < 4; ++q) ga[q] = e4[4 * gn + q];
+                add_group(gb);
+            }
+            if (g < ng) add_group(ga);
         }
-        if (tid == 0) x.result = s;
+        if (lane == 0) x.result = s;
     }
-    __syncthreads();  // 5
-    const float r = x.result;
-    __syncthreads();
-    return r;
+    lds_barrier();
+    return x.result;
 }
 
 #endif  // __HIPCC__

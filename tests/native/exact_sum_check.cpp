@@ -1,7 +1,7 @@
 // Checks qt_llama.cpp_amd/csrc/exact_sum.h: the events built from the
 // per-term classification (runs of safe terms -> one exact addend, other
 // terms kept) must sum sequentially to the bits of the plain loop
-// s = 0; s = s + a_k.  Approximate prefix sums come from a double-precision
+// s = 0; s = s + a_k, also with runs cut every 256 terms.  Approximate prefix sums come from a double-precision
 // pass rounded to f32 (within the classification's error allowance).
 //   exact_sum_check [cases] [seed]  -> prints "mismatches <m> cases <c> events_avg <e>"
 #include <cmath>
@@ -20,7 +20,9 @@ static float plain(const std::vector<float> &a)
     return s;
 }
 
-static float by_events(const std::vector<float> &a, size_t &nev)
+// split > 0: a run is also cut where k is a multiple of split (the GPU sum
+// cuts runs at every wave's first term); the parts stay exact.
+static float by_events(const std::vector<float> &a, size_t &nev, int split)
 {
     const int n = (int)a.size();
     std::vector<float> P(n);
@@ -40,7 +42,7 @@ static float by_events(const std::vector<float> &a, size_t &nev)
             in_run = false;
             continue;
         }
-        if (!in_run || st.u != u) {  // a run never changes binade; the check keeps the emulation honest
+        if (!in_run || st.u != u || (split > 0 && k % split == 0)) {  // a run never changes binade; the check keeps the emulation honest
             if (in_run && st.u != u) return -1.0f;
             ev.push_back(0.0f);
             R = 0;
@@ -82,11 +84,12 @@ int main(int argc, char **argv)
             }
             a[k] = (float)v;
         }
-        size_t nev = 0;
-        const float want = plain(a), got = by_events(a, nev);
+        size_t nev = 0, nev_split = 0;
+        const float want = plain(a), got = by_events(a, nev, 0), got_split = by_events(a, nev_split, 256);
         evsum += (long long)nev;
-        if (__builtin_bit_cast(uint32_t, want) != __builtin_bit_cast(uint32_t, got)) {
-            if (mism < 5) printf("case %d kind %d n %d: plain %a events %a\n", c, kind, n, want, got);
+        if (__builtin_bit_cast(uint32_t, want) != __builtin_bit_cast(uint32_t, got) ||
+            __builtin_bit_cast(uint32_t, want) != __builtin_bit_cast(uint32_t, got_split)) {
+            if (mism < 5) printf("case %d kind %d n %d: plain %a events %a split %a\n", c, kind, n, want, got, got_split);
             ++mism;
         }
     }

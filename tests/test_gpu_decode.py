@@ -56,7 +56,7 @@ def max_rel(got, ref):
 
 
 # ------------------------------------------------------------ RMSNorm
-@pytest.mark.parametrize("dim", [2304, 256, 9216, 32])
+@pytest.mark.parametrize("dim", [2304, 256, 9216, 32, 3072])
 def test_rms_norm_and_pack(backend, dev, orc, synth, dim):
     rng = synth.rng_for(3000 + dim)
     x = (rng.standard_normal(dim) * 3.0).astype(np.float32)
@@ -80,12 +80,13 @@ def test_rms_norm_and_pack(backend, dev, orc, synth, dim):
     assert np.all(np.abs(out.numpy() - 1.0) < 1e-4)
 
 
-@pytest.mark.parametrize("case", ["ints", "ties", "wide", "zeros", "one_big", "ragged"])
+@pytest.mark.parametrize("case", ["ints", "ties", "wide", "zeros", "one_big", "ragged", "all_events"])
 def test_rms_norm_exact_sum_edges(backend, dev, orc, synth, case):
     """The sum of squares is the reference's sequential f32 loop, evaluated in
     parallel (runs of same-binade terms as exact integer ulp counts); these
-    inputs stress binade crossings, exact ties, the plain-loop fallback and
-    zero sums."""
+    inputs stress binade crossings, exact ties, zero sums and a sum whose
+    every term is an event of its own (1, then 2^-24 repeated: s stays 1 and
+    each 2^-24 is an exact tie, rounded to even)."""
     rng = synth.rng_for(3050)
     dim = 2304 if case != "ragged" else 96
     if case == "ints":
@@ -96,6 +97,9 @@ def test_rms_norm_exact_sum_edges(backend, dev, orc, synth, case):
         x = (rng.standard_normal(dim) * 10.0 ** rng.uniform(-12, 12, dim)).astype(np.float32)
     elif case == "zeros":
         x = np.zeros(dim, np.float32)
+    elif case == "all_events":
+        x = np.full(dim, 2.0 ** -12, np.float32)
+        x[0] = 1.0
     elif case == "one_big":
         x = (rng.standard_normal(dim) * 1e-3).astype(np.float32)
         x[1234] = 1e4
