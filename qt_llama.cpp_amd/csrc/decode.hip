@@ -25,6 +25,7 @@
 #include "device.h"
 #include "exact_sum.h"
 #include "internal.h"
+#include "norm_block.h"
 
 namespace mrml {
 
@@ -34,17 +35,6 @@ constexpr int kMaxChunks = 4;        // float4 chunks per thread: dim <= 16 * bl
 constexpr int kNormMaxThreads = 768;  // keeps ~170 VGPRs per lane for the norm kernels
 constexpr int kScoreP = 64;    // cache positions per score workgroup (one per lane)
 constexpr int kAttnHD = 256;   // head_dim served by the attention kernels
-
-__device__ __forceinline__ float4 scale4(float4 a, float s) { return make_float4(a.x * s, a.y * s, a.z * s, a.w * s); }
-__device__ __forceinline__ float4 mul4(float4 a, float4 b)
-{
-    return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
-}
-__device__ __forceinline__ float4 add4(float4 a, float4 b)
-{
-    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
-}
-__device__ __forceinline__ float4 sq4(float4 a) { return make_float4(a.x * a.x, a.y * a.y, a.z * a.z, a.w * a.w); }
 
 // s = 0; s += v[i] for i = 0..n-1, each add rounded (v 16-byte aligned in
 // LDS).  Every lane of the calling wave runs the same chain on broadcast LDS
@@ -88,84 +78,6 @@ __device__ float seq_sum(const float *v, int n)
     return s;
 }
 
-// Sum of squares of the values held in v (chunks c = tid + k*blockDim), in
-// index order from +0 (ops.rs:24-79), bit for bit: the sequential f32 sum
-// evaluated in parallel (exact_sum.h).  With one chunk per thread the terms
-// stay in registers; otherwise they are staged in LDS.  `lds` is laid out by
-// norm_lds().
-template <int CH>
-__device__ float block_seq_sum_sq(const float4 (&v)[CH], int n4, float *lds)
-{
-    if constexpr (CH == 1) {
-        auto *x = reinterpret_cast<mrml_xsum::Shared4 *>(lds);
-        return mrml_xsum::block_seq_sum_nonneg4(sq4(v[0]), n4 * 4, *x);
-    }
-    float4 *sq = reinterpret_cast<float4 *>(lds);
-#pragma unroll
-    for (int k = 0; k < CH; ++k) {
-        const int c = threadIdx.x + k * blockDim.x;
-        if (c < n4) sq[c] = sq4(v[k]);
-    }
-    __syncthreads();
-    uint8_t *flags = reinterpret_cast<uint8_t *>(lds + n4 * 4);
-    auto *x = reinterpret_cast<mrml_xsum::Shared *>(flags + ((n4 * 4 + 15) & ~15));
-    return mrml_xsum::block_seq_sum_nonneg(lds, n4 * 4, flags, *x);
-}
-
-// ops.rs:24-79: mean = sum/dim, scale = 1/sqrt(mean + eps) (IEEE sqrt and
-// divide: hipcc's defaults are correctly rounded).
-__device__ __forceinline__ float rms_scale(float sum_sq, int dim, float eps)
-{
-    const float mean = sum_sq / (float)dim;
-    return 1.0f / sqrtf(mean + eps);
-}
-
-// Q8_0 pack of the value chunk c (values 4c..4c+3); 8 consecutive threads
-// hold one block.  Every lane of the wave must call this.
-__device__ __forceinline__ void emit_q8(float4 v, int c, int n4, uint8_t *pack, int nb)
-{
-    uint32_t dbits;
-    int s;
-    const uint32_t q = q8_0_block8x4(v, dbits, s);
-    if (c < n4) {
-        reinterpret_cast<uint32_t *>(pack)[c] = q;
-        if ((c & 7) == 0) {
-            reinterpret_cast<float *>(pack + (size_t)nb * 32)[c >> 3] = f16_bits_to_f32(dbits);
-            reinterpret_cast<int32_t *>(pack + (size_t)nb * 36)[c >> 3] = s;
-        }
-    }
-}
-
-// Loads the weight chunks of this thread (w nullable: no load), issued
-// with the kernel's other loads so none waits behind the norm's sums.
-template <int CH>
-__device__ __forceinline__ void load_w(const float *w, float4 (&wv)[CH], int n4)
-{
-    const float4 *w4 = reinterpret_cast<const float4 *>(w);
-#pragma unroll
-    for (int k = 0; k < CH; ++k) {
-        const int c = threadIdx.x + k * blockDim.x;
-        wv[k] = w ? w4[c < n4 ? c : 0] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
-    }
-}
-
-// out = (x * scale) * w per value (has_w false: no weight), stored to out
-// (nullable) and as a Q8_0 pack (nullable).
-template <int CH>
-__device__ __forceinline__ void norm_store(const float4 (&v)[CH], float scale, const float4 (&wv)[CH], bool has_w,
-                                           float *out, uint8_t *pack, int n4)
-{
-#pragma unroll
-    for (int k = 0; k < CH; ++k) {
-        if (k * (int)blockDim.x >= n4) break;  // uniform
-        const int c = threadIdx.x + k * blockDim.x;
-        float4 o = scale4(v[k], scale);
-        if (has_w) o = mul4(o, wv[k]);
-        if (out && c < n4) reinterpret_cast<float4 *>(out)[c] = o;
-        if (pack) emit_q8(o, c, n4, pack, n4 >> 3);
-    }
-}
-
 // out = rms_norm(x, w) (CudaDevice::rms_norm, cuda.rs:2102-2180; CPU
 // ops.rs:24-79), optionally also as a Q8_0 pack.  One workgroup.
 template <int CH>
@@ -188,20 +100,28 @@ __global__ __launch_bounds__(kNormMaxThreads) void rms_norm_kernel(const float *
 
 // Sandwich-norm residual of a Gemma-2 block followed by the next block's
 // pre-norm (the per-layer order of model.rs:1185-2260):
-//   h  = h + rms_norm(t, w_post)
-//   xn = rms_norm(h, w_next)      -> xn (nullable) and its Q8_0 pack (nullable)
+//   h_out = h_in + rms_norm(t, w_post)
+//   xn    = rms_norm(h_out, w_next)   -> xn (nullable) and its Q8_0 pack (nullable)
+// One workgroup; h_out may equal h_in.
 template <int CH>
 __global__ __launch_bounds__(kNormMaxThreads) void residual_rms_norm_kernel(const float *__restrict__ t,
                                                                  const float *__restrict__ w_post,
-                                                                 float *__restrict__ h,
+                                                                 const float *h_in, float *h_out,
                                                                  const float *__restrict__ w_next, float eps,
                                                                  float *__restrict__ xn, uint8_t *__restrict__ pack,
                                                                  int dim)
 {
     extern __shared__ __align__(16) float lds[];
     const int n4 = dim >> 2;
+    if constexpr (CH == 1) {
+        const ResidualOps ops = residual_load(t, w_post, h_in, (xn || pack) ? w_next : nullptr, n4);
+        residual_norm1(ops, w_post != nullptr, w_next != nullptr, eps, h_out, xn, pack, dim,
+                       *reinterpret_cast<mrml_xsum::Shared4 *>(lds));
+        return;
+    }
     const float4 *t4 = reinterpret_cast<const float4 *>(t);
-    float4 *h4 = reinterpret_cast<float4 *>(h);
+    const float4 *hi4 = reinterpret_cast<const float4 *>(h_in);
+    float4 *ho4 = reinterpret_cast<float4 *>(h_out);
     const float4 *wp4 = reinterpret_cast<const float4 *>(w_post);
     const float4 one4 = make_float4(1.0f, 1.0f, 1.0f, 1.0f), zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     // every operand's load is issued before the first sum
@@ -211,7 +131,7 @@ __global__ __launch_bounds__(kNormMaxThreads) void residual_rms_norm_kernel(cons
         const int c = threadIdx.x + k * blockDim.x;
         const int cc = c < n4 ? c : 0;
         v[k] = c < n4 ? t4[cc] : zero4;
-        hv[k] = h4[cc];
+        hv[k] = hi4[cc];
         wv[k] = w_post ? wp4[cc] : one4;
     }
     if (xn || pack) load_w(w_next, wn, n4);
@@ -222,7 +142,7 @@ __global__ __launch_bounds__(kNormMaxThreads) void residual_rms_norm_kernel(cons
         float4 tn = scale4(v[k], s1);
         if (w_post) tn = mul4(tn, wv[k]);
         const float4 hn = add4(hv[k], tn);
-        if (c < n4) h4[c] = hn;
+        if (c < n4) ho4[c] = hn;
         v[k] = c < n4 ? hn : zero4;
     }
     if (!xn && !pack) return;
@@ -634,15 +554,15 @@ int launch_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float eps
     return check_launch(ctx, "rms_norm_kernel");
 }
 
-int launch_residual_rms_norm(mrml_hip_ctx *ctx, const float *t, const float *w_post, float *h, const float *w_next,
-                             float eps, float *xn, void *pack, int dim)
+int launch_residual_rms_norm(mrml_hip_ctx *ctx, const float *t, const float *w_post, const float *h_in, float *h_out,
+                             const float *w_next, float eps, float *xn, void *pack, int dim)
 {
     if (norm_one_chunk(dim))
         hipLaunchKernelGGL(residual_rms_norm_kernel<1>, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, t,
-                           w_post, h, w_next, eps, xn, (uint8_t *)pack, dim);
+                           w_post, h_in, h_out, w_next, eps, xn, (uint8_t *)pack, dim);
     else
         hipLaunchKernelGGL(residual_rms_norm_kernel<kMaxChunks>, dim3(1), dim3(norm_threads(dim)), norm_lds(dim),
-                           ctx->stream, t, w_post, h, w_next, eps, xn, (uint8_t *)pack, dim);
+                           ctx->stream, t, w_post, h_in, h_out, w_next, eps, xn, (uint8_t *)pack, dim);
     return check_launch(ctx, "residual_rms_norm_kernel");
 }
 

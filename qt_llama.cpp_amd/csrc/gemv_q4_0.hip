@@ -33,6 +33,7 @@
 
 #include "device.h"
 #include "internal.h"
+#include "norm_block.h"
 
 namespace mrml {
 
@@ -327,6 +328,109 @@ __global__ __launch_bounds__(64 * (WAVES + (QX ? kNQ : 1))) void gemv_q4_0_geglu
         if constexpr (EMIT) act_lds[row_raw - blockIdx.x * 32] = a;
     }
     if constexpr (EMIT) __syncthreads();
+}
+
+// ---- the Gemma-2 sandwich residual ahead of the rows ---------------------------
+// Each workgroup first forms h_out = h_in + rms_norm(t, w_post) and
+// the Q8_0 pack of rms_norm(h_out, w_norm) in its own LDS (norm_block.h;
+// the same bits in every workgroup, workgroup 0 stores h_out), then its
+// compute waves fold 4 rows each against that pack.  The compute waves issue their
+// weight loads once the norm's operands have arrived, so the norm's exact
+// sums run while the weights stream in (its barriers wait on LDS only).  h_out must not alias h_in: other workgroups still read h_in.
+// dim = NB*32 <= 4*576 (one float4 chunk per thread).
+constexpr int kResWaves = 9;
+
+template <int NB>
+__device__ __forceinline__ uint8_t *resnorm_pack_lds(uint8_t *lds) { return lds; }
+template <int NB>
+__device__ __forceinline__ mrml_xsum::Shared4 *resnorm_shared(uint8_t *lds)
+{
+    return reinterpret_cast<mrml_xsum::Shared4 *>(lds + (NB * 40 + 15) / 16 * 16 + 64 * sizeof(float));
+}
+
+// Gate+up with the GeGLU epilogue and the output's Q8_0 pack, the
+// post-attention residual fused ahead.  16 waves own 64 rows (two output
+// blocks) and all of them fold rows: 144 workgroups for 9216 rows, so every
+// workgroup is resident at once (at 9 waves a CU holds one workgroup and
+// 288 of them would take two rounds, each paying for the norm).
+constexpr int kGegluResWaves = 16;
+
+template <int NB>
+__global__ __launch_bounds__(64 * kGegluResWaves) void gemv_q4_0_geglu_resnorm_kernel(
+    const uint8_t *__restrict__ wg, const uint8_t *__restrict__ wu, const float *__restrict__ t,
+    const float *__restrict__ w_post, const float *h_in, float *h_out, const float *__restrict__ w_norm, float eps,
+    uint8_t *__restrict__ act_pack, int rows)
+{
+    static_assert(NB * 8 <= 64 * kGegluResWaves, "one float4 chunk per thread");
+    constexpr int ITERS = (NB + 15) / 16;
+    extern __shared__ __align__(16) uint8_t lds[];
+    float *act_lds = reinterpret_cast<float *>(lds + (NB * 40 + 15) / 16 * 16);
+    auto *xs = reinterpret_cast<mrml_xsum::Shared4 *>(act_lds + 64);
+    // h_in, w_post, w_norm chunks parked in LDS during the norm: the weight
+    // registers plus the norm's own leave no VGPR for them
+    float4 *park = reinterpret_cast<float4 *>(reinterpret_cast<uint8_t *>(xs) + (sizeof(mrml_xsum::Shared4) + 15) / 16 * 16);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 15, tid = threadIdx.x;
+    const ResidualOps ops = residual_load(t, w_post, h_in, w_norm, NB * 8);
+    wait_vm_loads();  // the norm then waits on no weight load
+    park[tid] = ops.h;
+    park[64 * kGegluResWaves + tid] = ops.wp;
+    park[2 * 64 * kGegluResWaves + tid] = ops.wn;
+    const int row_raw = (blockIdx.x * kGegluResWaves + wave) * 4 + (lane >> 4);
+    const int row = row_raw < rows ? row_raw : rows - 1;
+    const size_t nblk = (size_t)rows * NB, base = (size_t)row * NB;
+    RowRegs<ITERS> rg, ru;
+    load_row<ITERS>(rg, wg, nblk, base, NB, j);
+    load_row<ITERS>(ru, wu, nblk, base, NB, j);
+    residual_norm1(ops.t, [&](int k) { return park[k * 64 * kGegluResWaves + tid]; }, w_post != nullptr,
+                   w_norm != nullptr, eps, blockIdx.x == 0 ? h_out : nullptr, nullptr, lds, NB * 32, *xs);
+    mrml_xsum::lds_barrier();  // the pack is whole
+    float g, u;
+    fold_row2<ITERS>(rg, ru, lds, base, NB, j, g, u);
+    const float a = gelu_tanh(g) * u;
+    if (j == 15 && row_raw < rows) act_lds[row_raw - blockIdx.x * 64] = a;
+    mrml_xsum::lds_barrier();
+    if (wave < 2) {
+        uint32_t dbits;
+        int s;
+        const int q = q8_0_block32(act_lds[wave * 32 + (lane & 31)], dbits, s);
+        const int blk = 2 * blockIdx.x + wave, nbo = rows / 32;
+        if (lane < 32 && blk < nbo) {
+            act_pack[(size_t)blk * 32 + lane] = (uint8_t)(int8_t)q;
+            if (lane == 0) {
+                reinterpret_cast<float *>(act_pack + (size_t)nbo * 32)[blk] = f16_bits_to_f32(dbits);
+                reinterpret_cast<int32_t *>(act_pack + (size_t)nbo * 36)[blk] = s;
+            }
+        }
+    }
+}
+
+// The stacked q|k|v matvec, the post-FFN residual of the previous block and
+// this block's pre-attention norm fused ahead (32 rows per workgroup).
+template <int NB>
+__global__ __launch_bounds__(64 * kResWaves) void gemv_q4_0_qkv_resnorm_kernel(
+    const uint8_t *__restrict__ wq, const uint8_t *__restrict__ wk, const uint8_t *__restrict__ wv,
+    const float *__restrict__ t, const float *__restrict__ w_post, const float *h_in, float *h_out,
+    const float *__restrict__ w_norm, float eps, float *__restrict__ y, int q_rows, int kv_rows)
+{
+    static_assert(NB * 8 <= 64 * kResWaves, "one float4 chunk per thread");
+    constexpr int ITERS = (NB + 15) / 16;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 15;
+    const ResidualOps ops = residual_load(t, w_post, h_in, w_norm, NB * 8);
+    wait_vm_loads();  // the norm then waits on no weight load
+    const int total = q_rows + 2 * kv_rows;
+    const int row_raw = (blockIdx.x * 8 + wave - 1) * 4 + (lane >> 4);
+    const QkvSel m = qkv_select(wq, wk, wv, row_raw < 0 ? 0 : (row_raw < total ? row_raw : total - 1), q_rows, kv_rows);
+    const size_t base = (size_t)m.local * NB;
+    RowRegs<ITERS> r;
+    if (wave > 0) load_row<ITERS>(r, m.w, (size_t)m.mrows * NB, base, NB, j);
+    residual_norm1(ops, w_post != nullptr, w_norm != nullptr, eps, blockIdx.x == 0 ? h_out : nullptr, nullptr,
+                   resnorm_pack_lds<NB>(lds), NB * 32, *resnorm_shared<NB>(lds));
+    mrml_xsum::lds_barrier();  // the pack is whole
+    if (wave > 0) {
+        const float s = fold_row<ITERS>(r, lds, base, NB, j);
+        if (j == 15 && row_raw >= 0 && row_raw < total) y[row_raw] = s;
+    }
 }
 
 // ---- relay kernel for long rows ------------------------------------------------
@@ -795,6 +899,52 @@ int launch_gemv_q4_0_qkv_x(mrml_hip_ctx *ctx, const void *wq, const void *wk, co
     if (!pk) return MRML_HIP_E_ALLOC;
     if (int rc = launch_quantize_q8_0(ctx, x, nullptr, pk, cols)) return rc;
     return launch_gemv_q4_0_qkv(ctx, wq, wk, wv, pk, y, q_rows, kv_rows, cols);
+}
+
+// The Gemma-2 residual fused ahead of the gate/up GeGLU (act pack out) or of
+// the q|k|v matvec.  resnorm_shape() says whether a fused instance exists;
+// otherwise the caller runs the residual norm and the matvec separately.
+bool resnorm_shape(int cols) { return fold16_shape(cols / 32) && cols % 32 == 0; }
+
+static size_t resnorm_lds(int nb) { return pack_lds(nb) + 64 * sizeof(float) + sizeof(mrml_xsum::Shared4); }
+static size_t geglu_resnorm_lds(int nb)
+{
+    return align_up(resnorm_lds(nb), 16) + (size_t)3 * 64 * kGegluResWaves * sizeof(float4);  // parked norm operands
+}
+
+int launch_geglu_resnorm(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *t, const float *w_post,
+                         const float *h_in, float *h_out, const float *w_norm, float eps, void *act_pack, int32_t rows,
+                         int32_t cols)
+{
+    const int nb = cols / 32;
+    if (!resnorm_shape(cols) || rows % 64 != 0 || h_in == h_out)
+        return fail(ctx, MRML_HIP_E_UNSUPPORTED, "geglu_resnorm: no fused instance for %dx%d (or h_in == h_out)", rows,
+                    cols);
+    if (int rc = check_even(ctx, rows, nb)) return rc;
+    MRML_FOLD16_NB(nb, {
+        hipLaunchKernelGGL((gemv_q4_0_geglu_resnorm_kernel<NB>), dim3(rows / 64), dim3(64 * kGegluResWaves),
+                           geglu_resnorm_lds(NB), ctx->stream, (const uint8_t *)wg, (const uint8_t *)wu, t, w_post, h_in,
+                           h_out, w_norm, eps, (uint8_t *)act_pack, rows);
+    });
+    return check_launch(ctx, "gemv_q4_0_geglu_resnorm_kernel");
+}
+
+int launch_qkv_resnorm(mrml_hip_ctx *ctx, const void *wq, const void *wk, const void *wv, const float *t,
+                       const float *w_post, const float *h_in, float *h_out, const float *w_norm, float eps, float *y,
+                       int32_t q_rows, int32_t kv_rows, int32_t cols)
+{
+    const int nb = cols / 32;
+    if (!resnorm_shape(cols) || h_in == h_out)
+        return fail(ctx, MRML_HIP_E_UNSUPPORTED, "qkv_resnorm: no fused instance for cols=%d (or h_in == h_out)", cols);
+    if (int rc = check_even(ctx, q_rows, nb)) return rc;
+    if (int rc = check_even(ctx, kv_rows, nb)) return rc;
+    const int total = q_rows + 2 * kv_rows;
+    MRML_FOLD16_NB(nb, {
+        hipLaunchKernelGGL((gemv_q4_0_qkv_resnorm_kernel<NB>), dim3((total + 31) / 32), dim3(64 * kResWaves),
+                           resnorm_lds(NB), ctx->stream, (const uint8_t *)wq, (const uint8_t *)wk,
+                           (const uint8_t *)wv, t, w_post, h_in, h_out, w_norm, eps, y, q_rows, kv_rows);
+    });
+    return check_launch(ctx, "gemv_q4_0_qkv_resnorm_kernel");
 }
 
 int launch_gemv_q4_0_gguf(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows,

@@ -84,11 +84,22 @@ int argmax_parts(int32_t n);
 int launch_argmax_step(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *out, void *scratch, int32_t *state,
                        int32_t *hist, int hist_cap, const int32_t *prompt, int prompt_len);
 
+// The Gemma-2 residual (h_out = h_in + rms_norm(t, w_post), then the next
+// norm with w_norm) fused ahead of the gate/up GeGLU or the q|k|v matvec
+// (gemv_q4_0.hip); h_out must not alias h_in.
+bool resnorm_shape(int cols);
+int launch_geglu_resnorm(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *t, const float *w_post,
+                         const float *h_in, float *h_out, const float *w_norm, float eps, void *act_pack, int32_t rows,
+                         int32_t cols);
+int launch_qkv_resnorm(mrml_hip_ctx *ctx, const void *wq, const void *wk, const void *wv, const float *t,
+                       const float *w_post, const float *h_in, float *h_out, const float *w_norm, float eps, float *y,
+                       int32_t q_rows, int32_t kv_rows, int32_t cols);
+
 // ---- decode-step ops (decode.hip) --------------------------------------------
 bool norm_dim_ok(int dim);
 int launch_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float eps, float *out, void *pack, int dim);
-int launch_residual_rms_norm(mrml_hip_ctx *ctx, const float *t, const float *w_post, float *h, const float *w_next,
-                             float eps, float *xn, void *pack, int dim);
+int launch_residual_rms_norm(mrml_hip_ctx *ctx, const float *t, const float *w_post, const float *h_in, float *h_out,
+                             const float *w_next, float eps, float *xn, void *pack, int dim);
 int launch_embedding(mrml_hip_ctx *ctx, const void *table, int type, const int32_t *d_token, int token, float scale,
                      float *h, const float *w_norm, float eps, float *xn, void *pack, int dim, int vocab);
 int launch_rope_kv_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache, uint16_t *v_cache, const int32_t *d_pos,

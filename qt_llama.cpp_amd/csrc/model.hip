@@ -32,6 +32,7 @@ struct mrml_hip_gemma2 {
     std::vector<mrml_hip_gemma2_layer> layers;
     void *arena = nullptr;  // activations, packs, partials (one allocation)
     float *h = nullptr, *qkv = nullptr, *o = nullptr, *f = nullptr, *logits = nullptr;
+    float *h2 = nullptr;  // the residual's other buffer when the residual runs inside the matvecs
     uint8_t *xpack = nullptr, *attn_pack = nullptr, *act_pack = nullptr;
     void *attn_part = nullptr, *argmax_scratch = nullptr;
     float *rope_table = nullptr;  // [ctx_len][head_dim/2] (cos, sin) from the host libm
@@ -86,7 +87,7 @@ int mrml_hip_residual_rms_norm(mrml_hip_ctx *ctx, const float *t, const float *w
     REQUIRE(ctx, (((uintptr_t)t | (uintptr_t)w_post | (uintptr_t)h | (uintptr_t)w_next | (uintptr_t)xn |
                    (uintptr_t)pack) & 15) == 0,
             "residual_rms_norm: pointers must be 16-byte aligned");
-    return launch_residual_rms_norm(ctx, t, w_post, h, w_next, eps, xn, pack, dim);
+    return launch_residual_rms_norm(ctx, t, w_post, h, h, w_next, eps, xn, pack, dim);
 }
 
 int mrml_hip_embedding(mrml_hip_ctx *ctx, const void *table, int32_t type, int32_t token, const int32_t *d_token,
@@ -178,7 +179,7 @@ int mrml_hip_gemma2_create(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config *cfg,
         off = align_up(off + bytes, 256);
         return at;
     };
-    const size_t o_h = take(c.dim * 4), o_qkv = take((qd + 2 * kvd) * 4), o_o = take(c.dim * 4),
+    const size_t o_h = take(c.dim * 4), o_h2 = take(c.dim * 4), o_qkv = take((qd + 2 * kvd) * 4), o_o = take(c.dim * 4),
                  o_f = take(c.dim * 4), o_logits = take((size_t)c.vocab * 4),
                  o_xpack = take(act_pack_bytes((int)(in_max / 32))), o_apack = take(act_pack_bytes((int)(qd / 32))),
                  o_actpack = take(act_pack_bytes(c.ffn_dim / 32)),
@@ -192,6 +193,7 @@ int mrml_hip_gemma2_create(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config *cfg,
     }
     uint8_t *base = (uint8_t *)m->arena;
     m->h = (float *)(base + o_h);
+    m->h2 = (float *)(base + o_h2);
     m->qkv = (float *)(base + o_qkv);
     m->o = (float *)(base + o_o);
     m->f = (float *)(base + o_f);
@@ -239,24 +241,45 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
     do {                                \
         if ((rc = (call)) != 0) return rc; \
     } while (0)
-    STEP(launch_embedding(ctx, m->tok_embd, c.tie_type, d_token, 0, sqrtf((float)c.dim), m->h,
+    // With the fused instances (resnorm_shape), each sandwich residual runs
+    // inside the matvec that consumes its norm: the post-attention one ahead
+    // of gate/up, the post-FFN one ahead of the next block's q|k|v.  Every
+    // workgroup there reads h while workgroup 0 writes the update, so h
+    // alternates between two buffers (A -> B -> A per block) and ends in A.
+    const bool fused = resnorm_shape(c.dim) && c.ffn_dim % 64 == 0;
+    float *hA = m->h, *hB = m->h2;
+    STEP(launch_embedding(ctx, m->tok_embd, c.tie_type, d_token, 0, sqrtf((float)c.dim), hA,
                           m->layers[0].attn_norm, c.eps, nullptr, m->xpack, c.dim, c.vocab));
     for (int l = 0; l < c.n_layers; ++l) {
         const mrml_hip_gemma2_layer &L = m->layers[l];
         uint16_t *kc = d_k_cache + (size_t)l * layer_cache, *vc = d_v_cache + (size_t)l * layer_cache;
         const float *next_norm = l + 1 < c.n_layers ? m->layers[l + 1].attn_norm : m->output_norm;
-        STEP(launch_gemv_q4_0_qkv(ctx, L.wq, L.wk, L.wv, m->xpack, m->qkv, qd, kvd, c.dim));
+        if (fused && l > 0)
+            STEP(launch_qkv_resnorm(ctx, L.wq, L.wk, L.wv, m->f, m->layers[l - 1].post_ffw_norm, hB, hA, L.attn_norm,
+                                    c.eps, m->qkv, qd, kvd, c.dim));
+        else
+            STEP(launch_gemv_q4_0_qkv(ctx, L.wq, L.wk, L.wv, m->xpack, m->qkv, qd, kvd, c.dim));
         STEP(launch_rope_kv_f16(ctx, m->qkv, kc, vc, d_pos, 0, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_base,
                                 1.0f, c.ctx_len, m->rope_table, c.ctx_len));
         STEP(launch_attn_decode_f16(ctx, m->qkv, kc, vc, nullptr, m->attn_pack, d_pos, 0, c.n_heads, c.n_kv_heads,
                                     c.attn_scale, c.ctx_len, m->attn_part));
         STEP(launch_gemv_q4_0(ctx, L.wo, m->attn_pack, m->o, c.dim, qd));
-        STEP(launch_residual_rms_norm(ctx, m->o, L.post_attn_norm, m->h, L.ffn_norm, c.eps, nullptr, m->xpack,
-                                      c.dim));
-        STEP(launch_gemv_q4_0_geglu_emit(ctx, L.w_gate, L.w_up, m->xpack, nullptr, m->act_pack, c.ffn_dim, c.dim));
+        if (fused) {
+            STEP(launch_geglu_resnorm(ctx, L.w_gate, L.w_up, m->o, L.post_attn_norm, hA, hB, L.ffn_norm, c.eps,
+                                      m->act_pack, c.ffn_dim, c.dim));
+        } else {
+            STEP(launch_residual_rms_norm(ctx, m->o, L.post_attn_norm, hA, hA, L.ffn_norm, c.eps, nullptr, m->xpack,
+                                          c.dim));
+            STEP(launch_gemv_q4_0_geglu_emit(ctx, L.w_gate, L.w_up, m->xpack, nullptr, m->act_pack, c.ffn_dim,
+                                             c.dim));
+        }
         STEP(launch_gemv_q4_0(ctx, L.w_down, m->act_pack, m->f, c.dim, c.ffn_dim));
-        STEP(launch_residual_rms_norm(ctx, m->f, L.post_ffw_norm, m->h, next_norm, c.eps, nullptr, m->xpack,
-                                      c.dim));
+        if (!fused)
+            STEP(launch_residual_rms_norm(ctx, m->f, L.post_ffw_norm, hA, hA, next_norm, c.eps, nullptr, m->xpack,
+                                          c.dim));
+        else if (l + 1 == c.n_layers)
+            STEP(launch_residual_rms_norm(ctx, m->f, L.post_ffw_norm, hB, hA, next_norm, c.eps, nullptr, m->xpack,
+                                          c.dim));
     }
     if (c.tie_type == MRML_HIP_Q4_0)
         STEP(launch_gemv_q4_0(ctx, m->tok_embd, m->xpack, logits, c.vocab, c.dim));
