@@ -346,6 +346,19 @@ __device__ float block_seq_sum_nonneg4(float4 v, int n, Shared4 &x)
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
     const int k0 = 4 * tid;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);  // uniform: branch and readlane index
+    if (256 * wv >= n) {
+        // no term in this wave: no prefix, no events; it keeps the barriers
+        if (lane == 63) {
+            x.wtot[wave] = 0.0f;
+        }
+        lds_barrier();
+        if (lane == 63) x.wcnt[wave] = 0;
+        lds_barrier();
+        lds_barrier();
+        lds_barrier();
+        return x.result;
+    }
     float a[4] = {v.x, v.y, v.z, v.w};
     float lp[4], run = 0.0f;
 #pragma unroll
@@ -406,7 +419,6 @@ __device__ float block_seq_sum_nonneg4(float4 v, int n, Shared4 &x)
     const int cw = lane < nw ? x.wcnt[lane] : 0;  // row 0
     const int ci = row_incl_scan_i32(cw);
     const int nev = __builtin_amdgcn_readlane(ci, 15);
-    const int wv = __builtin_amdgcn_readfirstlane(wave);  // uniform: a lane index for readlane
     const int goff = wv ? __builtin_amdgcn_readlane(ci, wv - 1) : 0;
     if (wave == 0 && lane < kPadEvents) x.ev[nev + lane] = 0.0f;
     float *ev = x.ev + goff;
