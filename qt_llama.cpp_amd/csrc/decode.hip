@@ -334,70 +334,76 @@ __global__ __launch_bounds__(512) void attn_scores_kernel(const float *__restric
     if (p0 + p < window) scores[(size_t)(kvh * G + g) * capacity + p0 + p] = dot * scale;
 }
 
-// Softmax and weighted values, query head h, dims [64*ds, 64*ds + 64) per
+// Softmax and weighted values, query head h, dims [32*ds, 32*ds + 32) per
 // workgroup (blockIdx = (h, ds)):  max over the window; e_p = expf(score_p -
 // max); sum = 0 + e_0 + e_1 + ... in order; p_p = e_p * (1/sum); out[d] = 0 +
-// p_0 v_0[d] + p_1 v_1[d] + ... in order.  (The four workgroups of a head
-// each repeat the softmax; it is small next to the weighted sum.)
+// p_0 v_0[d] + p_1 v_1[d] + ... in order.  (The eight workgroups of a head
+// each repeat the softmax; the weighted sum is bound by the CU's LDS
+// bandwidth, so a narrower slice per workgroup runs it faster.)
 //
 // The weighted sum splits into independent products and one ordered chain of
-// adds per dim.  Six producer waves stream V in tiles of kSVT positions (two tiles in
-// flight in registers, loaded before the softmax starts), form the products
-// p_t * v_t[d] and store them to LDS as [t][d] (two 16-byte stores per 8
-// products, conflict-free); wave 0 runs the 64 chains, lane d adding column d
-// one tile behind the producers (one barrier per tile, products
-// double-buffered).  Writes
-// out (nullable) and the Q8_0 pack of the n_heads*head_dim output (nullable).
-// Dynamic LDS: capacity floats plus 4.
-constexpr int kSVD = 64;  // dims per workgroup
+// adds per dim.  Six producer waves stream V in tiles of kSVT positions
+// (tiles in flight in registers, the first ones loaded before the softmax
+// starts), form the products p_t * v_t[d] and store them to LDS as [d][t]
+// (thread: 2 positions x 4 dims, one 8-byte store per dim); wave 0 runs the
+// 32 chains (lanes 32..63 repeat lanes 0..31), lane d adding row d four
+// positions per 16-byte read, one tile behind the producers (one barrier per
+// tile, products double-buffered).
+// Writes out (nullable) and the Q8_0 pack of the n_heads*head_dim output
+// (nullable).  Dynamic LDS: capacity floats plus 4.
+constexpr int kSVD = 32;  // dims per workgroup
 constexpr int kSVW = 8;   // waves: wave 0 adds; waves 1-3 and 5-7 produce; wave 4, which shares wave 0's SIMD, idles
-constexpr int kSVT = 96;  // positions per tile: 96 rows x 8 chunks of 16 B = 2 chunks per producer thread
-constexpr int kSVP = kSVD + 4;  // product row stride (floats): 16-byte aligned, conflict-free 16-byte stores
+constexpr int kSVT = 96;  // positions per tile: 48 position pairs x 8 dim quads = one per producer thread
+constexpr int kSVS = kSVT + 12;  // product row stride (floats), 27 16-byte segments: measured on gfx950, 16-byte
+                                 // reads of 64 rows at this stride run 1.4x faster than at 25 and 7.5x faster
+                                 // than at 24 segments (bank conflicts)
 
 // A native 4 x 32-bit vector: copies of HIP's uint4 struct lower to memcpy,
 // which keeps an array of them in scratch memory instead of registers.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// Producer thread pt (0..383) of tile t: chunks c = pt + 384k, k < kSVC (row
-// c >> 3, dims 8*(c & 7) .. +7 of the slice); rows past the window reload the
-// last row (their products are zeroed).  ring0 = cache row of the tile's
-// first position (the window's rows are consecutive modulo capacity).
+// Producer thread pt (0..383) of tile t: positions 2*(pt >> 3) .. +1 of the
+// tile, dims 4*(pt & 7) .. +3 of the slice (8 bytes of each V row); rows
+// past the window reload the last row (their products are zeroed).  ring0 =
+// cache row of the tile's first position (the window's rows are consecutive
+// modulo capacity).
 constexpr int kSVPT = 64 * (kSVW - 2);  // producer threads
-constexpr int kSVC = kSVT * 8 / kSVPT;
-static_assert(kSVT * 8 == kSVC * kSVPT, "whole chunks per producer");
-__device__ __forceinline__ void sv_tile_load(u32x4 (&r)[kSVC], const uint16_t *vslice, int t, int window, int ring0,
+constexpr int kSVR = 2;                 // positions per producer thread
+static_assert(kSVT / kSVR * (kSVD / 4) == kSVPT, "one position pair x dim quad per producer thread");
+__device__ __forceinline__ void sv_tile_load(u32x2 (&r)[kSVR], const uint16_t *vslice, int t, int window, int ring0,
                                              int capacity, size_t kv_dim, int pt)
 {
+    const int tq = pt >> 3, dq = pt & 7;
 #pragma unroll
-    for (int k = 0; k < kSVC; ++k) {
-        const int c = pt + kSVPT * k;
-        int rr = c >> 3;
+    for (int i = 0; i < kSVR; ++i) {
+        int rr = kSVR * tq + i;
         rr = t * kSVT + rr < window ? rr : window - 1 - t * kSVT;
         int row = ring0 + rr;
         row = row >= capacity ? row - capacity : row;
-        r[k] = reinterpret_cast<const u32x4 *>(vslice + (size_t)row * kv_dim)[c & 7];
+        r[i] = reinterpret_cast<const u32x2 *>(vslice + (size_t)row * kv_dim)[dq];
     }
 }
 
-__device__ __forceinline__ void sv_products(const u32x4 (&r)[kSVC], const float *e_s, float (*prod)[kSVP], int t,
+__device__ __forceinline__ void sv_products(const u32x2 (&r)[kSVR], const float *e_s, float (*prod)[kSVS], int t,
                                             int window, int pt)
 {
+    const int tq = pt >> 3, dq = pt & 7, pos0 = t * kSVT + kSVR * tq;
+    const float2 pw = reinterpret_cast<const float2 *>(e_s)[(pos0 < window ? pos0 : 0) >> 1];
+    const float w4[kSVR] = {pw.x, pw.y};
+    float pv[4][kSVR];  // [dim][position]
 #pragma unroll
-    for (int k = 0; k < kSVC; ++k) {
-        const int c = pt + kSVPT * k, row = c >> 3, d0 = 8 * (c & 7), pos = t * kSVT + row;
-        const bool live = pos < window;
-        const float pw = e_s[live ? pos : 0];
-        const uint32_t w[4] = {r[k].x, r[k].y, r[k].z, r[k].w};
-        float pv[8];
+    for (int i = 0; i < kSVR; ++i) {
+        const bool live = pos0 + i < window;
+        const uint32_t lo = r[i].x, hi = r[i].y;
+        const float v[4] = {f16_bits_to_f32(lo & 0xffffu), f16_bits_to_f32(lo >> 16), f16_bits_to_f32(hi & 0xffffu),
+                            f16_bits_to_f32(hi >> 16)};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float v = f16_bits_to_f32((w[i >> 1] >> (16 * (i & 1))) & 0xffffu);
-            pv[i] = live ? pw * v : 0.0f;
-        }
-        float4 *dst = reinterpret_cast<float4 *>(&prod[row][d0]);
-        dst[0] = make_float4(pv[0], pv[1], pv[2], pv[3]);
-        dst[1] = make_float4(pv[4], pv[5], pv[6], pv[7]);
+        for (int d = 0; d < 4; ++d) pv[d][i] = live ? w4[i] * v[d] : 0.0f;
     }
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+        *reinterpret_cast<float2 *>(&prod[4 * dq + d][kSVR * tq]) = make_float2(pv[d][0], pv[d][1]);
 }
 
 __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *__restrict__ scores,
@@ -409,7 +415,9 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
     constexpr int HD = kAttnHD;
     extern __shared__ __align__(16) float e_s[];
     __shared__ float red[kSVW];
-    __shared__ __align__(16) float prod[2][kSVT][kSVP];
+    __shared__ __align__(16) float prod[2][kSVD][kSVS];
+    __shared__ __align__(16) mrml_xsum::Shared4 sum_xs[1];
+    mrml_xsum::Shared4 *sum_x = sum_xs;
     int window, start;
     attn_window(d_pos, n_past_arg, capacity, window, start);
     const int h = blockIdx.x, ds = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -424,7 +432,7 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
     const int ring_start = (int)cache_row_of(start, capacity), step = kSVT % (capacity > 0 ? capacity : 1 << 30);
     auto ring_next = [&](int r) { return r + step >= capacity ? r + step - capacity : r + step; };
     // tiles t .. t+3 in flight in registers (slot t % 4); ring[k] = cache row of the slot's tile
-    u32x4 vt[4][kSVC];
+    u32x2 vt[4][kSVR];
     int ring[4];
     ring[0] = ring_start;
 #pragma unroll
@@ -435,24 +443,61 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
             if (k < ntiles) sv_tile_load(vt[k], vslice, k, window, ring[k], capacity, kv_dim, pt);
     }
 
-    // max over the window (exact in any order): DPP within each half-wave
+    // max over the window (exact in any order): DPP within each half-wave.
+    // Thread t takes positions 4t..4t+3 (+2048 per pass), so up to 2048
+    // positions its exps stay in registers for the sum.
+    constexpr int kSVE = 4 * 64 * kSVW;  // positions per pass
+    const float4 *sc4 = reinterpret_cast<const float4 *>(sc);
+    float4 sv = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
     float mx = -INFINITY;
-    for (int p = tid; p < window; p += 64 * kSVW) mx = fmaxf(mx, sc[p]);
+    for (int p0 = 0; p0 < window; p0 += kSVE) {
+        const int p = p0 + 4 * tid;
+        float4 v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        if (p + 3 < window) {
+            v = sc4[p >> 2];
+        } else if (p < window) {
+            v.x = sc[p];
+            if (p + 1 < window) v.y = sc[p + 1];
+            if (p + 2 < window) v.z = sc[p + 2];
+        }
+        if (p0 == 0) sv = v;
+        mx = fmaxf(mx, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
+    }
     mx = max32(mx);
     mx = fmaxf(mx, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx), 32)));
     if (lane == 0) red[wave] = mx;
     __syncthreads();
 #pragma unroll
     for (int w = 0; w < kSVW; ++w) mx = fmaxf(mx, red[w]);
-    for (int p = tid; p < window; p += 64 * kSVW) e_s[p] = mrml_libm::expf(sc[p] - mx, expf_fused != 0);
-    __syncthreads();
-    float *bcast = e_s + capacity;
-    if (wave == 0) {
-        const float sum = seq_sum(e_s, window);
-        if (lane == 0) *bcast = sum;
+    const bool fused_exp = expf_fused != 0;
+    float sum;
+    if (window <= kSVE) {
+        // exps in registers; the ordered sum over the block (exact_sum.h)
+        const int p = 4 * tid;
+        float4 e = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (p < window) e.x = mrml_libm::expf(sv.x - mx, fused_exp);
+        if (p + 1 < window) e.y = mrml_libm::expf(sv.y - mx, fused_exp);
+        if (p + 2 < window) e.z = mrml_libm::expf(sv.z - mx, fused_exp);
+        if (p + 3 < window) e.w = mrml_libm::expf(sv.w - mx, fused_exp);
+        if (p + 3 < window) {
+            reinterpret_cast<float4 *>(e_s)[tid] = e;
+        } else if (p < window) {
+            e_s[p] = e.x;
+            if (p + 1 < window) e_s[p + 1] = e.y;
+            if (p + 2 < window) e_s[p + 2] = e.z;
+        }
+        sum = mrml_xsum::block_seq_sum_nonneg4(e, window, *sum_x);
+    } else {
+        for (int p = tid; p < window; p += 64 * kSVW) e_s[p] = mrml_libm::expf(sc[p] - mx, fused_exp);
+        __syncthreads();
+        float *bcast = e_s + capacity;
+        if (wave == 0) {
+            const float s0 = seq_sum(e_s, window);
+            if (lane == 0) *bcast = s0;
+        }
+        __syncthreads();
+        sum = *bcast;
     }
-    __syncthreads();
-    const float sum = *bcast;
     if (sum > 0.0f) {
         const float inv = 1.0f / sum;
         for (int p = tid; p < window; p += 64 * kSVW) e_s[p] = e_s[p] * inv;
@@ -460,28 +505,23 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
     __syncthreads();
 
     float acc = 0.0f;
-    // The column in batches of 16: the next batch's reads are in flight while
-    // the current one is added (16 dependent adds outlast an LDS read).
-    // Zeroed tail products leave acc unchanged (it never holds -0).
-    static_assert(kSVT % 32 == 0, "batches of 16, an even number of them");
+    // Row `lane` of the tile: all 24 16-byte reads are issued before the
+    // first add (pinned by the scheduling barrier: under the producers' LDS
+    // traffic a read takes a few hundred cycles, more than a short prefetch
+    // covers), then the 96 ordered adds.  Zeroed tail products leave acc
+    // unchanged (it never holds -0).
     auto chain = [&](int t) {
-        const float(*col)[kSVP] = prod[t & 1];
-        float b0[16], b1[16];
-        auto fetch = [&](float (&b)[16], int g) {
+        const float4 *row = reinterpret_cast<const float4 *>(prod[t & 1][lane & (kSVD - 1)]);
+        float4 b[kSVT / 4];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) b[i] = col[16 * g + i][lane];
-        };
-        auto add = [&](const float (&b)[16]) {
+        for (int i = 0; i < kSVT / 4; ++i) b[i] = row[i];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) acc = acc + b[i];
-        };
-        fetch(b0, 0);
-#pragma unroll
-        for (int g = 0; g < kSVT / 16; g += 2) {
-            fetch(b1, g + 1);
-            add(b0);
-            if (g + 2 < kSVT / 16) fetch(b0, g + 2);
-            add(b1);
+        for (int i = 0; i < kSVT / 4; ++i) {
+            acc = acc + b[i].x;
+            acc = acc + b[i].y;
+            acc = acc + b[i].z;
+            acc = acc + b[i].w;
         }
     };
     // buffer (t+1)&1 was last read by wave 0 in tile t-1, before barrier t
@@ -494,7 +534,7 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
             }
         }
         __syncthreads();
-        if (wave == 0) chain(t);
+        if (wave == 0 && lane < kSVD) chain(t);
     };
     for (int t = 0; t < ntiles; t += 4) {
         tile(t, 0);
@@ -504,15 +544,15 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
     }
 
     if (wave == 0) {
-        const int o = h * HD + ds * kSVD + lane;
-        if (out) out[o] = acc;
+        const int o = h * HD + ds * kSVD + (lane & (kSVD - 1));
+        if (out && lane < kSVD) out[o] = acc;
         if (pack) {
             uint32_t dbits;
             int s;
             const int qv = q8_0_block32(acc, dbits, s);
             const int nb = n_heads * HD / 32, blk = o >> 5;
-            pack[o] = (uint8_t)(int8_t)qv;
-            if ((lane & 31) == 0) {
+            if (lane < kSVD) pack[o] = (uint8_t)(int8_t)qv;
+            if (lane == 0) {
                 reinterpret_cast<float *>(pack + (size_t)nb * 32)[blk] = f16_bits_to_f32(dbits);
                 reinterpret_cast<int32_t *>(pack + (size_t)nb * 36)[blk] = s;
             }
@@ -591,7 +631,7 @@ int launch_rope_kv_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache, uint16_
 }
 
 int attn_head_dim() { return kAttnHD; }
-int attn_max_capacity() { return 6144; }  // the window's softmax weights (24 KB) share LDS with the products
+int attn_max_capacity() { return 6144; }  // the window's softmax weights (24 KB) share LDS with the products and the sum
 
 size_t attn_scratch_bytes(int n_heads, int capacity) { return (size_t)n_heads * capacity * sizeof(float); }
 

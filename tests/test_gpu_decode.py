@@ -218,7 +218,7 @@ def attention_case(backend, dev, orc, synth, n_past, cap, seed):
     return got, ref, pk.numpy(), vc
 
 
-@pytest.mark.parametrize("n_past", [0, 1, 31, 32, 33, 63, 64, 511, 767, 4095])
+@pytest.mark.parametrize("n_past", [0, 1, 31, 32, 33, 63, 64, 511, 767, 2046, 2047, 2048, 4095])
 def test_attention_decode(backend, dev, orc, synth, n_past):
     got, ref, pack, _ = attention_case(backend, dev, orc, synth, n_past, 4096, n_past)
     assert_bits(got, ref, "attention")
