@@ -675,12 +675,30 @@ int64_t orc_gemma2_step(const orc_gemma2 *m, int64_t token, int64_t pos,
         orc_rope_1d_batched(k, (size_t)pos, (size_t)m->n_kv_heads, hd, m->rope_base, 1.0f);
         uint16_t *kc = k_cache + (size_t)l * (size_t)m->ctx * kvd;
         uint16_t *vc = v_cache + (size_t)l * (size_t)m->ctx * kvd;
+        /* the cache is a ring of ctx rows: position pos lands in row pos % ctx
+         * (kernels.rs:1307-1313) and attention reads the last min(pos+1, ctx)
+         * positions, oldest first (a sliding window of ctx, kernels.rs:1398-1404) */
+        const size_t ctx = (size_t)m->ctx, crow = (size_t)pos % ctx;
         for (size_t i = 0; i < kvd; i++) {
-            kc[(size_t)pos * kvd + i] = orc_f32_to_f16_rne(k[i]);
-            vc[(size_t)pos * kvd + i] = orc_f32_to_f16_rne(v[i]);
+            kc[crow * kvd + i] = orc_f32_to_f16_rne(k[i]);
+            vc[crow * kvd + i] = orc_f32_to_f16_rne(v[i]);
         }
-        orc_attention_f16(q, kc, vc, att, (size_t)pos, (size_t)m->n_heads, (size_t)m->n_kv_heads,
-                          hd, m->attn_scale);
+        const size_t count = (size_t)pos + 1, win = count > ctx ? ctx : count, start = count - win;
+        if (start == 0) {
+            orc_attention_f16(q, kc, vc, att, (size_t)pos, (size_t)m->n_heads, (size_t)m->n_kv_heads,
+                              hd, m->attn_scale);
+        } else {
+            uint16_t *wk = malloc(win * kvd * 2), *wv = malloc(win * kvd * 2);
+            for (size_t t = 0; t < win; t++) {
+                const size_t row = (start + t) % ctx;
+                memcpy(wk + t * kvd, kc + row * kvd, kvd * 2);
+                memcpy(wv + t * kvd, vc + row * kvd, kvd * 2);
+            }
+            orc_attention_f16(q, wk, wv, att, win - 1, (size_t)m->n_heads, (size_t)m->n_kv_heads, hd,
+                              m->attn_scale);
+            free(wk);
+            free(wv);
+        }
         orc_quantize_q8_0(att, xq, qd);
         orc_mat_vec_mul_q4_0_q8_0(m->wo[l], xq, tmp, dim, qd, isa, threads);
         orc_rms_norm(tmp, m->post_attn_norm[l], m->eps, xn, dim);

@@ -334,6 +334,155 @@ __global__ __launch_bounds__(512) void attn_scores_kernel(const float *__restric
     if (p0 + p < window) scores[(size_t)(kvh * G + g) * capacity + p0 + p] = dot * scale;
 }
 
+// Scores with an optional RoPE in front (the decode step's fused form).
+// Workgroup (tile of 64 positions, kv head), 256 threads; waves 0..G-1 run
+// the chains of the G query heads of the group.
+//  * The K tile (64 rows x 512 B) goes to LDS with one 16-byte store per
+//    chunk, rows padded to 528 B (16-byte aligned, conflict-free 16-byte
+//    reads of 64 rows).
+//  * ROPE: q comes raw from the stacked q|k|v vector and is rotated here
+//    (NeoX half split, ops.rs:185-208; cos/sin from the host table when pos <
+//    n_table).  The workgroup whose tile holds the newest position rotates
+//    that position's k, rounds it to f16 (round to nearest even, as the
+//    cache stores it, kernels.rs:1300-1322), uses it for that row and
+//    appends it and the position's v to the caches.  Without ROPE, q is the
+//    rotated query and the caches are complete.
+//  * Lane p of wave g: dot = -0.0 + q[0]*k_p[0] + ... in d order, each
+//    product rounded (an fma with addend -0.0 on the f16 k converted inline
+//    rounds exactly as the product does, signs of zero included).
+constexpr int kKRow2 = kAttnHD * 2 + 16;  // padded K row in LDS, bytes
+
+// Native 4 and 2 x 32-bit vectors: copies of HIP's uint4 struct lower to
+// memcpy, which keeps an array of them in scratch memory instead of registers.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+constexpr int kScoreT = 256;              // threads per score workgroup
+
+__device__ __forceinline__ void rope_cs(const float *table, int n_table, int pos, int i, int head_dim, float base,
+                                        float freq_scale, float &c, float &s)
+{
+    if (table && pos >= 0 && pos < n_table) {
+        const float2 cs = reinterpret_cast<const float2 *>(table)[(size_t)pos * (head_dim >> 1) + i];
+        c = cs.x;
+        s = cs.y;
+    } else {
+        // the reference's f32 theta; powf, cosf, sinf in double, rounded once
+        const float expo = (float)(2 * i) / (float)head_dim;
+        const float freq = (float)pow((double)base, (double)expo);
+        const float theta = (float)pos * freq_scale / freq;
+        c = (float)cos((double)theta);
+        s = (float)sin((double)theta);
+    }
+}
+
+template <bool ROPE>
+__global__ __launch_bounds__(kScoreT) void attn_scores2_kernel(const float *__restrict__ q_in,
+                                                               uint16_t *__restrict__ k_cache,
+                                                               uint16_t *__restrict__ v_cache,
+                                                               const int32_t *__restrict__ d_pos, int n_past_arg,
+                                                               int n_heads, int n_kv_heads, float scale, int capacity,
+                                                               const float *__restrict__ table, int n_table,
+                                                               float base, float freq_scale,
+                                                               float *__restrict__ scores)
+{
+    constexpr int HD = kAttnHD, P = kScoreP, half = HD / 2;
+    __shared__ __align__(16) float q_s[4][HD];
+    __shared__ __align__(16) uint8_t k_s[P * kKRow2];
+    int window, start;
+    attn_window(d_pos, n_past_arg, capacity, window, start);
+    const int p0 = blockIdx.x * P;
+    if (p0 >= window) return;
+    const int kvh = blockIdx.y, G = n_heads / n_kv_heads, tid = threadIdx.x;
+    const size_t kv_dim = (size_t)n_kv_heads * HD;
+    const int pos = start + window - 1;  // the newest position
+    const int rnew = window - 1 - p0;    // its row in this tile (valid when 0 <= rnew < P)
+    const bool has_new = ROPE && rnew < P;
+    // K tile: 2048 chunks of 16 B, chunk c of row r = c >> 5 at r*528 + (c & 31)*16
+    constexpr int kChunks = P * (HD * 2 / 16), kPer = kChunks / kScoreT;
+    u32x4 tmp[kPer];  // a native vector: arrays of HIP's uint4 struct end up in scratch memory
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int c = k * kScoreT + tid, r = c >> 5;
+        const int pr = p0 + r < window ? p0 + r : window - 1;
+        tmp[k] = reinterpret_cast<const u32x4 *>(k_cache + cache_row_of(start + pr, capacity) * kv_dim +
+                                                 (size_t)kvh * HD)[c & 31];
+    }
+    // rotated (or copied) q of the group's heads: thread -> pairs (g, i)
+    // with i = tid % 128 for every g, so one cos/sin per thread serves q and k
+    static_assert(kScoreT % half == 0, "one rotation pair index per thread");
+    float c = 1.0f, sn = 0.0f;
+    if (ROPE) rope_cs(table, n_table, pos, tid % half, HD, base, freq_scale, c, sn);
+    for (int gi = tid; gi < G * half; gi += kScoreT) {
+        const int g = gi / half, i = gi % half;
+        const float *qh = q_in + (size_t)(kvh * G + g) * HD;
+        const float v0 = qh[i], v1 = qh[i + half];
+        if (ROPE) {
+            q_s[g][i] = v0 * c - v1 * sn;
+            q_s[g][i + half] = v0 * sn + v1 * c;
+        } else {
+            q_s[g][i] = v0;
+            q_s[g][i + half] = v1;
+        }
+    }
+    if (has_new) {
+        const size_t crow = cache_row_of(pos, capacity) * kv_dim + (size_t)kvh * HD;
+        uint16_t *krow = reinterpret_cast<uint16_t *>(k_s + rnew * kKRow2);
+        if (tid < half) {
+            const int i = tid;
+            const float *kh = q_in + (size_t)(n_heads + kvh) * HD;
+            const float v0 = kh[i], v1 = kh[i + half];
+            const uint16_t k0 = f32_to_f16_rne(v0 * c - v1 * sn), k1 = f32_to_f16_rne(v0 * sn + v1 * c);
+            krow[i] = k0;
+            krow[i + half] = k1;
+            k_cache[crow + i] = k0;
+            k_cache[crow + i + half] = k1;
+        } else {
+            const int i = tid - half;
+            const float *vh = q_in + (size_t)(n_heads + n_kv_heads + kvh) * HD;
+            v_cache[crow + i] = f32_to_f16_rne(vh[i]);
+            v_cache[crow + i + half] = f32_to_f16_rne(vh[i + half]);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int c = k * kScoreT + tid, r = c >> 5;
+        if (!(has_new && r == rnew)) *reinterpret_cast<u32x4 *>(k_s + r * kKRow2 + (c & 31) * 16) = tmp[k];
+    }
+    __syncthreads();
+    const int g = tid >> 6, p = tid & 63;
+    if (g >= G) return;
+    const u32x4 *krow = reinterpret_cast<const u32x4 *>(k_s + p * kKRow2);
+    const float4 *qg = reinterpret_cast<const float4 *>(q_s[g]);
+    // -0.0 hidden from constant folding (an fma with a literal -0.0 addend
+    // becomes a plain multiply), so q * f16 k maps to one v_fma_mix_f32
+    float nz;
+    asm volatile("v_mov_b32 %0, 0x80000000" : "=v"(nz));
+    float dot = -0.0f;
+    for (int d0 = 0; d0 < HD / 8; d0 += 4) {
+        u32x4 kw[4];
+        float4 qa[8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            kw[u] = krow[d0 + u];
+            qa[2 * u] = qg[2 * (d0 + u)];
+            qa[2 * u + 1] = qg[2 * (d0 + u) + 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const u32x4 wv = kw[u];
+            const uint32_t w[4] = {wv.x, wv.y, wv.z, wv.w};
+            const float qv[8] = {qa[2 * u].x, qa[2 * u].y, qa[2 * u].z, qa[2 * u].w,
+                                 qa[2 * u + 1].x, qa[2 * u + 1].y, qa[2 * u + 1].z, qa[2 * u + 1].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const _Float16 kh = __builtin_bit_cast(_Float16, (uint16_t)(w[e >> 1] >> (16 * (e & 1))));
+                dot = dot + __builtin_fmaf(qv[e], (float)kh, nz);
+            }
+        }
+    }
+    if (p0 + p < window) scores[(size_t)(kvh * G + g) * capacity + p0 + p] = dot * scale;
+}
+
 // Softmax and weighted values, query head h, dims [32*ds, 32*ds + 32) per
 // workgroup (blockIdx = (h, ds)):  max over the window; e_p = expf(score_p -
 // max); sum = 0 + e_0 + e_1 + ... in order; p_p = e_p * (1/sum); out[d] = 0 +
@@ -358,10 +507,6 @@ constexpr int kSVS = kSVT + 12;  // product row stride (floats), 27 16-byte segm
                                  // reads of 64 rows at this stride run 1.4x faster than at 25 and 7.5x faster
                                  // than at 24 segments (bank conflicts)
 
-// A native 4 x 32-bit vector: copies of HIP's uint4 struct lower to memcpy,
-// which keeps an array of them in scratch memory instead of registers.
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Producer thread pt (0..383) of tile t: positions 2*(pt >> 3) .. +1 of the
 // tile, dims 4*(pt & 7) .. +3 of the slice (8 bytes of each V row); rows
@@ -635,12 +780,28 @@ int attn_max_capacity() { return 6144; }  // the window's softmax weights (24 KB
 
 size_t attn_scratch_bytes(int n_heads, int capacity) { return (size_t)n_heads * capacity * sizeof(float); }
 
+static int launch_softmax_v(mrml_hip_ctx *ctx, const float *scores, const uint16_t *v_cache, float *out, void *pack,
+                            const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads, int capacity)
+{
+    hipLaunchKernelGGL(attn_softmax_v_kernel, dim3(n_heads, kAttnHD / kSVD), dim3(64 * kSVW), (size_t)capacity * sizeof(float) + 16,
+                       ctx->stream, scores, v_cache, d_pos, n_past, n_heads, n_kv_heads, capacity,
+                       (int)host_expf_fused(), out, (uint8_t *)pack);
+    return check_launch(ctx, "attn_softmax_v_kernel");
+}
+
 int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache, const uint16_t *v_cache,
                            float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
                            float scale, int capacity, void *scratch)
 {
     float *scores = reinterpret_cast<float *>(scratch);
     const dim3 sgrid((capacity + kScoreP - 1) / kScoreP, n_kv_heads);
+    if (n_heads / n_kv_heads <= 4) {
+        hipLaunchKernelGGL(attn_scores2_kernel<false>, sgrid, dim3(kScoreT), 0, ctx->stream, q,
+                           const_cast<uint16_t *>(k_cache), (uint16_t *)nullptr, d_pos, n_past, n_heads, n_kv_heads,
+                           scale, capacity, (const float *)nullptr, 0, 0.0f, 0.0f, scores);
+        if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
+        return launch_softmax_v(ctx, scores, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, capacity);
+    }
     hipLaunchKernelGGL(attn_scores_kernel, sgrid, dim3(64 * (n_heads / n_kv_heads)), 0, ctx->stream, q, k_cache,
                        d_pos, n_past, n_heads, n_kv_heads, scale, capacity, scores);
     if (int rc = check_launch(ctx, "attn_scores_kernel")) return rc;
@@ -648,6 +809,24 @@ int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_
                        ctx->stream, scores, v_cache, d_pos, n_past, n_heads, n_kv_heads, capacity,
                        (int)host_expf_fused(), out, (uint8_t *)pack);
     return check_launch(ctx, "attn_softmax_v_kernel");
+}
+
+// The decode step's attention with RoPE and the K/V append in the scores
+// kernel: qkv is the raw stacked q|k|v vector.  Needs n_heads / n_kv_heads
+// <= 4 (attn_rope_ok).
+bool attn_rope_ok(int n_heads, int n_kv_heads) { return n_kv_heads > 0 && n_heads / n_kv_heads <= 4; }
+
+int launch_attn_decode_rope_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k_cache, uint16_t *v_cache,
+                                float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
+                                float scale, int capacity, const float *table, int n_table, float base,
+                                float freq_scale, void *scratch)
+{
+    float *scores = reinterpret_cast<float *>(scratch);
+    const dim3 sgrid((capacity + kScoreP - 1) / kScoreP, n_kv_heads);
+    hipLaunchKernelGGL(attn_scores2_kernel<true>, sgrid, dim3(kScoreT), 0, ctx->stream, qkv, k_cache, v_cache, d_pos,
+                       n_past, n_heads, n_kv_heads, scale, capacity, table, n_table, base, freq_scale, scores);
+    if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
+    return launch_softmax_v(ctx, scores, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, capacity);
 }
 
 }  // namespace mrml

@@ -54,25 +54,41 @@ struct Step {
     float u;    // ulp of the binade the step stays in
 };
 
-// Classify step k (a = a_k >= 0 finite, pm ~ P_{k-1}, pk ~ P_k).  Written
-// without early returns: on the GPU the lanes of a wave evaluate it in step.
-MRML_XS_HD Step classify(float a, float pm, float pk, int k)
+// Twice the relative error bound of the approximate prefix sums up to term
+// k: the classification's margin.  A term may be classed with the margin of
+// a later k (a larger margin only classes more steps unsafe); 1 - rho and
+// 1 + rho are exact floats for k < 2^22.
+MRML_XS_HD float margin(int k) { return (float)(2 * (k + 1 + kDepth)) * 0x1p-24f; }
+
+// Classify step k (a = a_k >= 0 finite, pm ~ P_{k-1}, pk ~ P_k; first: k == 0)
+// with omr = 1 - rho, opr = 1 + rho for a margin rho >= margin(k).  The
+// powers of two come from the exponent field of P_{k-1}: 2^e, 2^(e+1), the
+// ulp 2^(e-23) and its inverse 2^(23-e).  Written without early returns: on
+// the GPU the lanes of a wave evaluate it in step.
+MRML_XS_HD Step classify(float a, float pm, float pk, bool first, float omr, float opr)
 {
-    const bool in_range = k > 0 && pm >= 0x1p-100f && pk < 0x1p+120f;
-    const float pmc = in_range ? pm : 1.0f;                                        // keeps e in range
-    const int e = (int)((__builtin_bit_cast(uint32_t, pmc) >> 23) & 0xffu) - 127;  // binade of P_{k-1}
-    const float rho = (float)(2 * (k + 1 + kDepth)) * 0x1p-24f;                    // twice the bound
-    const float lo = pow2f(e), hi = pow2f(e + 1), u = pow2f(e - 23);
-    const bool starts_in = pmc - pmc * rho >= lo;        // s_{k-1} surely >= 2^e
-    const bool ends_in = pk + pk * rho + u < hi;         // s_{k-1} + a_k surely < 2^(e+1) - u
-    const float q = a * pow2f(23 - e);                   // exact when safe: a < 2^(e+1)
+    const bool in_range = !first && pm >= 0x1p-100f && pk < 0x1p+120f;
+    const uint32_t lob = __builtin_bit_cast(uint32_t, in_range ? pm : 1.0f) & 0x7f800000u;  // keeps e in range
+    const float lo = __builtin_bit_cast(float, lob);                  // 2^e
+    const float hi = __builtin_bit_cast(float, lob + 0x00800000u);    // 2^(e+1)
+    const float u = __builtin_bit_cast(float, lob - 0x0b800000u);     // 2^(e-23): exponent field minus 23
+    const float iu = __builtin_bit_cast(float, 0x8a800000u - lob);    // 2^(23-e): field 277 - (e+127)
+    const bool starts_in = pm * omr >= lo;       // s_{k-1} surely >= 2^e
+    const bool ends_in = pk * opr + u < hi;      // s_{k-1} + a_k surely < 2^(e+1) - u
+    const float q = a * iu;                      // exact when safe: a < 2^(e+1)
     const float r = __builtin_floorf(q);
-    const float f = q - r;                               // exact
+    const float f = q - r;                       // exact
     Step st;
     st.safe = (in_range && starts_in && ends_in && f != 0.5f) ? 1 : 0;  // a tie depends on s's parity
     st.inc = st.safe ? (int)r + (f > 0.5f ? 1 : 0) : 0;
     st.u = u;
     return st;
+}
+
+MRML_XS_HD Step classify(float a, float pm, float pk, int k)
+{
+    const float rho = margin(k);
+    return classify(a, pm, pk, k == 0, 1.0f - rho, 1.0f + rho);
 }
 
 #if defined(__HIPCC__)
@@ -342,7 +358,7 @@ __device__ __forceinline__ float readlane_f32(float v, int l)
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
 
-__device__ float block_seq_sum_nonneg4(float4 v, int n, Shared4 &x)
+__device__ __forceinline__ float block_seq_sum_nonneg4(float4 v, int n, Shared4 &x)
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
     const int k0 = 4 * tid;
@@ -378,10 +394,11 @@ __device__ float block_seq_sum_nonneg4(float4 v, int n, Shared4 &x)
     uint32_t inc[4], my_inc = 0;
     float uu[4];
     int unsafe = 0, stop = 0;
+    const float rho = margin(k0 + 3), omr = 1.0f - rho, opr = 1.0f + rho;  // the thread's last term's margin
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int k = k0 + i;
-        const Step st = classify(a[i], i ? base + lp[i - 1] : base, base + lp[i], k);
+        const Step st = classify(a[i], i ? base + lp[i - 1] : base, base + lp[i], k == 0, omr, opr);
         const bool in = k < n;
         inc[i] = (in && st.safe) ? (uint32_t)st.inc : 0u;
         uu[i] = st.u;
@@ -435,38 +452,32 @@ __device__ float block_seq_sum_nonneg4(float4 v, int n, Shared4 &x)
         r = re;
     }
     lds_barrier();
-    // the ordered sum, by wave 0 alone: groups of 16 events read as four
-    // broadcast float4 loads, two groups alternating so one is added while
-    // the next one's loads are in flight (the zero pad makes the last group
-    // whole; +0 leaves s unchanged: s >= +0)
+    // the ordered sum, by wave 0 alone: 32 events at a time, all of their
+    // broadcast 16-byte reads issued before the first add (an LDS read takes
+    // a few hundred cycles under load; the scheduling barrier keeps the reads
+    // ahead), then the adds (the zero pad makes the last group of 16 whole;
+    // +0 leaves s unchanged: s >= +0)
     if (wave == 0) {
         const float4 *e4 = reinterpret_cast<const float4 *>(x.ev);
-        const int ng = (nev + 15) >> 4;
+        const int n4 = ((nev + 15) >> 4) * 4;  // float4 reads covering the list
         float s = 0.0f;
-        auto add_group = [&](const float4 (&c)[4]) {
+        for (int q0 = 0; q0 < n4; q0 += 8) {
+            float4 b[8];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                s += c[q].x;
-                s += c[q].y;
-                s += c[q].z;
-                s += c[q].w;
+            for (int q = 0; q < 8; ++q) b[q] = e4[q0 + q < n4 ? q0 + q : n4 - 1];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                if (q0 + 4 * g < n4) {
+#pragma unroll
+                    for (int q = 4 * g; q < 4 * g + 4; ++q) {
+                        s += b[q].x;
+                        s += b[q].y;
+                        s += b[q].z;
+                        s += b[q].w;
+                    }
+                }
             }
-        };
-        if (ng > 0) {
-            float4 ga[4], gb[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) ga[q] = e4[q];
-            int g = 0;
-            for (; g + 2 <= ng; g += 2) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) gb[q] = e4[4 * (g + 1) + q];
-                add_group(ga);
-                const int gn = g + 2 < ng ? g + 2 : ng - 1;  // past the end: re-read, never added
-#pragma unroll
-                for (int q = 0; q < 4; ++q) ga[q] = e4[4 * gn + q];
-                add_group(gb);
-            }
-            if (g < ng) add_group(ga);
         }
         if (lane == 0) x.result = s;
     }

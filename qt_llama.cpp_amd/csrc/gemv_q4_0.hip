@@ -322,8 +322,11 @@ __global__ __launch_bounds__(64 * (WAVES + (QX ? kNQ : 1))) void gemv_q4_0_geglu
     __syncthreads();
     float g, u;
     fold_row2<ITERS>(rg, ru, lds, base, NB, j, g, u);
-    const float a = gelu_tanh(g) * u;
+    // only lane 15 of a row holds the row's sums: the GELU runs there alone
+    // (the other lanes' partial sums would send the wave down every branch
+    // of tanhf)
     if (j == 15 && row_raw < rows) {
+        const float a = gelu_tanh(g) * u;
         if (act) act[row_raw] = a;
         if constexpr (EMIT) act_lds[row_raw - blockIdx.x * 32] = a;
     }
@@ -386,8 +389,7 @@ __global__ __launch_bounds__(64 * kGegluResWaves) void gemv_q4_0_geglu_resnorm_k
     mrml_xsum::lds_barrier();  // the pack is whole
     float g, u;
     fold_row2<ITERS>(rg, ru, lds, base, NB, j, g, u);
-    const float a = gelu_tanh(g) * u;
-    if (j == 15 && row_raw < rows) act_lds[row_raw - blockIdx.x * 64] = a;
+    if (j == 15 && row_raw < rows) act_lds[row_raw - blockIdx.x * 64] = gelu_tanh(g) * u;  // lane 15 holds the row
     mrml_xsum::lds_barrier();
     if (wave < 2) {
         uint32_t dbits;

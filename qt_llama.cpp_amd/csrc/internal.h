@@ -111,6 +111,11 @@ size_t attn_scratch_bytes(int n_heads, int capacity);
 int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache, const uint16_t *v_cache,
                            float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
                            float scale, int capacity, void *scratch);
+bool attn_rope_ok(int n_heads, int n_kv_heads);
+int launch_attn_decode_rope_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k_cache, uint16_t *v_cache,
+                                float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
+                                float scale, int capacity, const float *table, int n_table, float base,
+                                float freq_scale, void *scratch);
 
 // Which form of the C library's expf the host runs (glibc picks its FMA build
 // on x86-64 CPUs with FMA and AVX2); the device reproduces the same one.

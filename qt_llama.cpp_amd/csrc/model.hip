@@ -259,10 +259,16 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
                                     c.eps, m->qkv, qd, kvd, c.dim));
         else
             STEP(launch_gemv_q4_0_qkv(ctx, L.wq, L.wk, L.wv, m->xpack, m->qkv, qd, kvd, c.dim));
-        STEP(launch_rope_kv_f16(ctx, m->qkv, kc, vc, d_pos, 0, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_base,
-                                1.0f, c.ctx_len, m->rope_table, c.ctx_len));
-        STEP(launch_attn_decode_f16(ctx, m->qkv, kc, vc, nullptr, m->attn_pack, d_pos, 0, c.n_heads, c.n_kv_heads,
-                                    c.attn_scale, c.ctx_len, m->attn_part));
+        if (attn_rope_ok(c.n_heads, c.n_kv_heads)) {
+            STEP(launch_attn_decode_rope_f16(ctx, m->qkv, kc, vc, nullptr, m->attn_pack, d_pos, 0, c.n_heads,
+                                             c.n_kv_heads, c.attn_scale, c.ctx_len, m->rope_table, c.ctx_len,
+                                             c.rope_base, 1.0f, m->attn_part));
+        } else {
+            STEP(launch_rope_kv_f16(ctx, m->qkv, kc, vc, d_pos, 0, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_base,
+                                    1.0f, c.ctx_len, m->rope_table, c.ctx_len));
+            STEP(launch_attn_decode_f16(ctx, m->qkv, kc, vc, nullptr, m->attn_pack, d_pos, 0, c.n_heads,
+                                        c.n_kv_heads, c.attn_scale, c.ctx_len, m->attn_part));
+        }
         STEP(launch_gemv_q4_0(ctx, L.wo, m->attn_pack, m->o, c.dim, qd));
         if (fused) {
             STEP(launch_geglu_resnorm(ctx, L.w_gate, L.w_up, m->o, L.post_attn_norm, hA, hB, L.ffn_norm, c.eps,

@@ -36,7 +36,10 @@ static float by_events(const std::vector<float> &a, size_t &nev, int split)
     long long R = 0;
     float u = 0.0f;
     for (int k = 0; k < n; ++k) {
-        const mrml_xsum::Step st = mrml_xsum::classify(a[k], k ? P[k - 1] : 0.0f, P[k], k);
+        // the margin of the last term of k's group of four, as the GPU's
+        // register path uses
+        const float rho = mrml_xsum::margin(k | 3);
+        const mrml_xsum::Step st = mrml_xsum::classify(a[k], k ? P[k - 1] : 0.0f, P[k], k == 0, 1.0f - rho, 1.0f + rho);
         if (!st.safe) {
             ev.push_back(a[k]);
             in_run = false;

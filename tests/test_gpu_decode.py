@@ -323,6 +323,24 @@ def test_gemma2_tiny_greedy(backend, dev, orc, synth, tie_q8):
     assert np.array_equal(kc, o.k_cache) and np.array_equal(vc, o.v_cache)
 
 
+def test_gemma2_tiny_ring_cache(backend, dev, orc, synth):
+    """Past the cache capacity the KV cache is a ring (kernels.rs:1307-1313)
+    and attention reads the last `capacity` positions (a sliding window,
+    kernels.rs:1398-1404): 30 steps over a 16-row cache, tokens, logits and
+    caches bit-identical to the oracle.  The decode step's RoPE, K/V append
+    and scores run in one kernel here (2 query heads per kv head)."""
+    cfg = dict(TINY, ctx_len=16)
+    model = synth.gemma2_model(cfg, seed=13)
+    prompt = synth.prompt_tokens(5, cfg["vocab"], seed=6)
+    n_dec = 25
+    hist, lg_gpu, kc, vc = run_gpu_decode(backend, dev, model, prompt, n_dec)
+    want, lg_ref, o = run_oracle_decode(orc, model, prompt, n_dec)
+    assert_same_tokens(hist, want)
+    for s_ in range(len(lg_ref)):
+        assert_bits(lg_gpu[s_], lg_ref[s_], f"logits at step {s_}")
+    assert np.array_equal(kc, o.k_cache) and np.array_equal(vc, o.v_cache)
+
+
 def test_gemma2_tiny_graph_equals_eager(backend, dev, synth):
     model = synth.gemma2_model(TINY, seed=12)
     prompt = synth.prompt_tokens(3, TINY["vocab"], seed=4)
