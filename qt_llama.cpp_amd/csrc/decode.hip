@@ -562,6 +562,7 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
     __shared__ float red[kSVW];
     __shared__ __align__(16) float prod[2][kSVD][kSVS];
     __shared__ __align__(16) mrml_xsum::Shared4 sum_xs[1];
+    __shared__ uint64_t exp_tab[32];
     mrml_xsum::Shared4 *sum_x = sum_xs;
     int window, start;
     attn_window(d_pos, n_past_arg, capacity, window, start);
@@ -588,6 +589,7 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
             if (k < ntiles) sv_tile_load(vt[k], vslice, k, window, ring[k], capacity, kv_dim, pt);
     }
 
+    if (tid < 32) exp_tab[tid] = mrml_libm::kExpfT.t[tid];  // read before the max's barrier
     // max over the window (exact in any order): DPP within each half-wave.
     // Thread t takes positions 4t..4t+3 (+2048 per pass), so up to 2048
     // positions its exps stay in registers for the sum.
@@ -620,10 +622,10 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
         // exps in registers; the ordered sum over the block (exact_sum.h)
         const int p = 4 * tid;
         float4 e = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (p < window) e.x = mrml_libm::expf(sv.x - mx, fused_exp);
-        if (p + 1 < window) e.y = mrml_libm::expf(sv.y - mx, fused_exp);
-        if (p + 2 < window) e.z = mrml_libm::expf(sv.z - mx, fused_exp);
-        if (p + 3 < window) e.w = mrml_libm::expf(sv.w - mx, fused_exp);
+        if (p < window) e.x = mrml_libm::expf_t(sv.x - mx, fused_exp, exp_tab);
+        if (p + 1 < window) e.y = mrml_libm::expf_t(sv.y - mx, fused_exp, exp_tab);
+        if (p + 2 < window) e.z = mrml_libm::expf_t(sv.z - mx, fused_exp, exp_tab);
+        if (p + 3 < window) e.w = mrml_libm::expf_t(sv.w - mx, fused_exp, exp_tab);
         if (p + 3 < window) {
             reinterpret_cast<float4 *>(e_s)[tid] = e;
         } else if (p < window) {
@@ -633,7 +635,7 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
         }
         sum = mrml_xsum::block_seq_sum_nonneg4(e, window, *sum_x);
     } else {
-        for (int p = tid; p < window; p += 64 * kSVW) e_s[p] = mrml_libm::expf(sc[p] - mx, fused_exp);
+        for (int p = tid; p < window; p += 64 * kSVW) e_s[p] = mrml_libm::expf_t(sc[p] - mx, fused_exp, exp_tab);
         __syncthreads();
         float *bcast = e_s + capacity;
         if (wave == 0) {

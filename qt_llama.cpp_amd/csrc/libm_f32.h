@@ -142,19 +142,22 @@ MRML_HD float tanhf(float x)
 struct ExpfTable {
     uint64_t t[32];
 };
+constexpr ExpfTable kExpfT = {{
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+}};
 
-MRML_HD float expf(float x, bool fused)
+// expf with the table read from `tab` (kExpfT's 32 entries; a kernel may keep
+// a copy in LDS, which a lane-indexed read reaches much sooner than the
+// read-only global copy after a long weight stream has left the caches).
+MRML_HD float expf_t(float x, bool fused, const uint64_t *tab)
 {
-    constexpr ExpfTable T = {{
-        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
-        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
-        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
-        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
-        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
-        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
-        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
-        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
-    }};
     const double N = 32.0;
     const double invln2N = 0x1.71547652b82fep+0 * N;
     const double shift = 0x1.8p+52;
@@ -174,7 +177,7 @@ MRML_HD float expf(float x, bool fused)
     kd -= shift;
     // The FMA build also fuses the reduction r = x N/ln2 - k.
     const double r = fused ? __builtin_fma(invln2N, xd, -kd) : z - kd;
-    uint64_t t = T.t[ki % 32];
+    uint64_t t = tab[ki % 32];
     t += ki << 47;
     const double s = u2d(t);
     const double r2 = r * r;
@@ -190,5 +193,7 @@ MRML_HD float expf(float x, bool fused)
     }
     return (float)(y * s);
 }
+
+MRML_HD float expf(float x, bool fused) { return expf_t(x, fused, kExpfT.t); }
 
 }  // namespace mrml_libm
