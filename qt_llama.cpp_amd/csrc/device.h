@@ -187,6 +187,54 @@ __device__ __forceinline__ uint32_t q8_0_block8x4(float4 v, uint32_t &dbits, int
            ((uint32_t)q3 << 24);
 }
 
+// ---- split-nibble activation blocks for the Q4_0 block dot ------------------
+// Word i < 4 of a Q4_0 block holds weight q[4i+k] in the low and q[16+4i+k]
+// in the high nibble of byte k.  For the Q8_0 quant words x = a[4i..4i+3]
+// and y = a[16+4i..16+4i+3] of the activation block:
+//   lo_i: nibble 2k = a[4i+k] & 15,  nibble 2k+1 = a[16+4i+k] & 15
+//   hi_i: the same nibbles of a >> 4 (4-bit two's complement)
+// so every value is a = 16*hi + lo, and with c = -8 * sum(a & 15) over the
+// block the exact block dot is
+//   sum_k (q_k - 8) * a_k = 16 * sdot8(w ^ 0x88888888, hi) + udot8(w, lo) + c
+// (w ^ 0x88888888 holds q - 8 as signed nibbles): 8 dot8 and 4 xor per block
+// on the raw weight words, no nibble unpacking.
+constexpr uint32_t kLoNib = 0x0F0F0F0Fu;
+__device__ __forceinline__ uint32_t split_lo(uint32_t x, uint32_t y) { return (x & kLoNib) | ((y & kLoNib) << 4); }
+__device__ __forceinline__ uint32_t split_hi(uint32_t x, uint32_t y) { return ((x >> 4) & kLoNib) | (y & ~kLoNib); }
+// sum over the 4 values of a quant word of (a & 15)
+__device__ __forceinline__ int lo_nib_sum(uint32_t x)
+{
+    return (int)__builtin_amdgcn_udot4(x & kLoNib, 0x01010101u, 0u, false);
+}
+
+// Lane l of an aligned 8-lane group holds quant word l of one block (q8_0_block8x4
+// layout).  Returns split word l of the block (lo_l for l < 4, hi_{l-4}
+// above: the word at the same position of the split block) and c in every
+// lane of the group.  Must be called by all 64 lanes of the wave.
+__device__ __forceinline__ uint32_t q8_split8(uint32_t q, int l, int &c)
+{
+    const uint32_t p = (uint32_t)__builtin_amdgcn_ds_swizzle((int)q, 0x101F);  // word l ^ 4 (xor mask 4)
+    c = -8 * sum8(lo_nib_sum(q));
+    return l < 4 ? split_lo(q, p) : split_hi(p, q);
+}
+
+// Exact Q4_0 block dot (sum (q-8)*a) of weight words w with a split block.
+__device__ __forceinline__ int32_t q4_0_isum_split(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, uint32_t lo0,
+                                                   uint32_t lo1, uint32_t lo2, uint32_t lo3, uint32_t hi0,
+                                                   uint32_t hi1, uint32_t hi2, uint32_t hi3, int32_t c)
+{
+    constexpr uint32_t k8 = 0x88888888u;
+    int32_t sh = __builtin_amdgcn_sdot8((int)(w0 ^ k8), (int)hi0, 0, false);
+    sh = __builtin_amdgcn_sdot8((int)(w1 ^ k8), (int)hi1, sh, false);
+    sh = __builtin_amdgcn_sdot8((int)(w2 ^ k8), (int)hi2, sh, false);
+    sh = __builtin_amdgcn_sdot8((int)(w3 ^ k8), (int)hi3, sh, false);
+    uint32_t sl = __builtin_amdgcn_udot8(w0, lo0, (uint32_t)c, false);  // wraps: c < 0, the total fits
+    sl = __builtin_amdgcn_udot8(w1, lo1, sl, false);
+    sl = __builtin_amdgcn_udot8(w2, lo2, sl, false);
+    sl = __builtin_amdgcn_udot8(w3, lo3, sl, false);
+    return (int32_t)(((uint32_t)sh << 4) + sl);
+}
+
 // ops.rs:101-104 evaluated in the same order (contraction is off):
 // (0.5*x) * (1 + tanh(k*(x + ((0.044715*x)*x)*x))), with the host C
 // library's tanhf reproduced bit for bit (libm_f32.h).

@@ -56,34 +56,52 @@ __device__ __forceinline__ int32_t q4_0_isum(uint4 w, int4 a0, int4 a1, int32_t 
     return s - 8 * asum;  // nibble offset: sum (q-8)*a = sum q*a - 8*sum a
 }
 
-// Copy an activation pack (nb*40 bytes, 16-byte aligned) into LDS with one
-// wave.  Every 16-byte load of a batch is issued before the first LDS store,
-// so the copy costs one L2 round trip per batch of 16 loads per lane.
-__device__ __forceinline__ void stage_pack_wave(const uint8_t *src, uint8_t *lds, int nb)
+// Stage an activation pack (Q8_0 planes, nb blocks, 16-byte aligned) into
+// LDS in split-nibble form (device.h) with one wave, one block per lane;
+// every load of a batch is issued before the first block is converted, so
+// the copy costs one L2 round trip per 64*kBatch blocks.
+__device__ __forceinline__ void stage_split_pack(const uint8_t *src, uint8_t *lds, int nb)
 {
-    constexpr int kBatch = 16;
-    const int n16 = (nb * 40 + 15) >> 4;
-    const uint4 *s = reinterpret_cast<const uint4 *>(src);
-    uint4 *d = reinterpret_cast<uint4 *>(lds);
+    constexpr int kBatch = 5;
     const int lane = threadIdx.x & 63;
-    for (int i0 = 0; i0 < n16; i0 += 64 * kBatch) {
-        uint4 v[kBatch];
+    const uint4 *sq = reinterpret_cast<const uint4 *>(src);
+    const float *sd = reinterpret_cast<const float *>(src + (size_t)nb * 32);
+    uint4 *dq = reinterpret_cast<uint4 *>(lds);
+    float *dd = reinterpret_cast<float *>(lds + nb * 32);
+    int32_t *dc = reinterpret_cast<int32_t *>(lds + nb * 36);
+    for (int b0 = 0; b0 < nb; b0 += 64 * kBatch) {
+        uint4 x[kBatch], y[kBatch];
+        float d[kBatch];
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
-            const int i = i0 + k * 64 + lane;
-            v[k] = s[i < n16 ? i : n16 - 1];
+            int b = b0 + k * 64 + lane;
+            b = b < nb ? b : nb - 1;
+            x[k] = sq[2 * b];
+            y[k] = sq[2 * b + 1];
+            d[k] = sd[b];
         }
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
-            const int i = i0 + k * 64 + lane;
-            if (i < n16) d[i] = v[k];
+            const int b = b0 + k * 64 + lane;
+            if (b < nb) {
+                const uint4 lo = make_uint4(split_lo(x[k].x, y[k].x), split_lo(x[k].y, y[k].y),
+                                            split_lo(x[k].z, y[k].z), split_lo(x[k].w, y[k].w));
+                const uint4 hi = make_uint4(split_hi(x[k].x, y[k].x), split_hi(x[k].y, y[k].y),
+                                            split_hi(x[k].z, y[k].z), split_hi(x[k].w, y[k].w));
+                dq[2 * b] = lo;
+                dq[2 * b + 1] = hi;
+                dd[b] = d[k];
+                dc[b] = -8 * (lo_nib_sum(x[k].x) + lo_nib_sum(x[k].y) + lo_nib_sum(x[k].z) + lo_nib_sum(x[k].w) +
+                              lo_nib_sum(y[k].x) + lo_nib_sum(y[k].y) + lo_nib_sum(y[k].z) + lo_nib_sum(y[k].w));
+            }
         }
     }
 }
 
-// Quantise f32 x (NB blocks) into an activation pack in LDS with NQ waves
-// (this is wave qw): eight blocks per wave step, 8 lanes of 4 values each per
-// block; all of a wave's loads are issued before the first block is quantised.
+// Quantise f32 x (NB blocks) into a split-nibble activation pack in LDS with
+// NQ waves (this is wave qw): eight blocks per wave step, 8 lanes of 4 values
+// each per block; all of a wave's loads are issued before the first block is
+// quantised.
 template <int NB, int NQ>
 __device__ __forceinline__ void quantize_into_lds(const float *__restrict__ x, uint8_t *pack, int qw)
 {
@@ -105,7 +123,7 @@ __device__ __forceinline__ void quantize_into_lds(const float *__restrict__ x, u
         const int b = 8 * (qw + NQ * k) + g;
         uint32_t dbits;
         int s;
-        const uint32_t q = q8_0_block8x4(v[k], dbits, s);
+        const uint32_t q = q8_split8(q8_0_block8x4(v[k], dbits, s), l, s);
         if (b < NB) {
             pq[b * 8 + l] = q;
             if (l == 0) {
@@ -144,19 +162,21 @@ __device__ __forceinline__ void load_row(RowRegs<ITERS> &r, const uint8_t *__res
     }
 }
 
-// Block term of iteration `it` (masked to +0 past the row end).  Computed
-// unconditionally, so the compiler has no conditional block to sink the
-// weight load into (which would delay its issue).
+// Block term of iteration `it` (masked to +0 past the row end) against a
+// split-nibble pack in LDS.  Computed unconditionally, so the compiler has
+// no conditional block to sink the weight load into (which would delay its
+// issue).
 template <int ITERS>
 __device__ __forceinline__ float row_term(const RowRegs<ITERS> &r, int it, const uint8_t *pack, size_t base, int nb,
                                           int j)
 {
     const int b = it * 16 + j;
     const int bc = b < nb ? b : nb - 1;
-    const int4 *aq = reinterpret_cast<const int4 *>(pack);
+    const uint4 *aq = reinterpret_cast<const uint4 *>(pack);
     const float *ad = reinterpret_cast<const float *>(pack + nb * 32);
-    const int32_t *as = reinterpret_cast<const int32_t *>(pack + nb * 36);
-    const int32_t isum = q4_0_isum(r.w[it], aq[2 * bc], aq[2 * bc + 1], as[bc]);
+    const int32_t *ac = reinterpret_cast<const int32_t *>(pack + nb * 36);
+    const uint4 w = r.w[it], lo = aq[2 * bc], hi = aq[2 * bc + 1];
+    const int32_t isum = q4_0_isum_split(w.x, w.y, w.z, w.w, lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w, ac[bc]);
     const uint32_t word = r.d[it];
     const uint32_t dbits = ((base + bc) & 1) ? word >> 16 : word & 0xffffu;
     const float t = (float)isum * (f16_bits_to_f32(dbits) * ad[bc]);
@@ -198,6 +218,79 @@ __device__ __forceinline__ void fold_row2(const RowRegs<ITERS> &ra, const RowReg
     }
 }
 
+// ---- transposed fold ----------------------------------------------------------
+// The same ordered fold (s = +0, then s = s + t[b] in block order) with one
+// lane per row instead of 16: the compute lanes store their block terms to
+// LDS, T[chain][b] at a stride of t_stride floats, and after a barrier one
+// lane per chain adds a row's terms in order -- one add instruction per
+// block for up to 64 rows, where the DPP fold spends 16 per 16 blocks per 4
+// rows.  The stride is an odd number of 16-byte segments, so the float4
+// reads of 64 chains spread over the banks.
+template <int NB>
+constexpr int t_stride()
+{
+    static_assert(NB % 4 == 0, "float4 reads of the terms");
+    return (NB / 4) % 2 ? NB : NB + 4;
+}
+
+// Store the terms of one row (this lane's blocks 16*it + j) to chain `chain`.
+template <int NB, int ITERS>
+__device__ __forceinline__ void store_terms(const RowRegs<ITERS> &r, const uint8_t *pack, size_t base, int j,
+                                            float *T, int chain)
+{
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+        const float t = row_term<ITERS>(r, it, pack, base, NB, j);
+        const int b = it * 16 + j;
+        if (b < NB) T[chain * t_stride<NB>() + b] = t;
+    }
+}
+
+// Two rows (gate and up): the term chains of both, computed interleaved.
+template <int NB, int ITERS>
+__device__ __forceinline__ void store_terms2(const RowRegs<ITERS> &ra, const RowRegs<ITERS> &rb, const uint8_t *pack,
+                                             size_t base, int j, float *T, int chain_a, int chain_b)
+{
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+        const float ta = row_term<ITERS>(ra, it, pack, base, NB, j);
+        const float tb = row_term<ITERS>(rb, it, pack, base, NB, j);
+        const int b = it * 16 + j;
+        if (b < NB) {
+            T[chain_a * t_stride<NB>() + b] = ta;
+            T[chain_b * t_stride<NB>() + b] = tb;
+        }
+    }
+}
+
+// The ordered sum of chain `chain` (all NB/4 reads issued before the adds).
+template <int NB>
+__device__ __forceinline__ float fold_chain(const float *T, int chain)
+{
+    const float4 *p = reinterpret_cast<const float4 *>(T + chain * t_stride<NB>());
+    float4 v[NB / 4];
+#pragma unroll
+    for (int k = 0; k < NB / 4; ++k) v[k] = p[k];
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NB / 4; ++k) {
+        s = s + v[k].x;
+        s = s + v[k].y;
+        s = s + v[k].z;
+        s = s + v[k].w;
+    }
+    return s;
+}
+
+// Value of lane (lane ^ M) (M = 16 or 32: across DPP rows, so through the
+// LDS crossbar; no LDS memory is touched).
+template <int M>
+__device__ __forceinline__ float lane_xor(float v)
+{
+    const int lane = threadIdx.x & 63;
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ M) << 2, __builtin_bit_cast(int, v)));
+}
+
 // Row of matrix set {wq | wk | wv} for a stacked output row.
 struct QkvSel {
     const uint8_t *w;
@@ -221,7 +314,7 @@ template <int NB, bool QX>
 __device__ __forceinline__ void prepare_pack(const void *xin, uint8_t *lds, int wave)
 {
     if constexpr (QX) quantize_into_lds<NB, kNQ>(reinterpret_cast<const float *>(xin), lds, wave);
-    else if (wave == 0) stage_pack_wave(reinterpret_cast<const uint8_t *>(xin), lds, NB);
+    else if (wave == 0) stage_split_pack(reinterpret_cast<const uint8_t *>(xin), lds, NB);
 }
 
 template <bool QX>
@@ -275,62 +368,67 @@ __global__ __launch_bounds__(64 * (WAVES + (QX ? kNQ : 1))) void gemv_q4_0_qkv_k
     if (j == 15 && row_raw < total) y[row_raw] = s;
 }
 
-// Gate+up with the GeGLU epilogue (model.rs:2093-2105, ops.rs:99-114).  With
-// EMIT, a workgroup owns 32 rows (WAVES = 8) and also writes the Q8_0 pack of
-// its 32 outputs (one activation block) for the next projection; act may
-// then be null.
+// Gate+up with the GeGLU epilogue (model.rs:2093-2105, ops.rs:99-114).  The
+// R = 4*WAVES rows of a workgroup are folded by its first compute wave, one
+// lane per chain (gate rows in lanes [0,R), up rows in [R,2R)).  With EMIT,
+// a workgroup owns 32 rows (WAVES = 8) and that wave also writes the Q8_0
+// pack of its 32 outputs (one activation block) for the next projection;
+// act may then be null.
 template <int NB, int WAVES, bool QX, bool EMIT>
 __global__ __launch_bounds__(64 * (WAVES + (QX ? kNQ : 1))) void gemv_q4_0_geglu_kernel(
     const uint8_t *__restrict__ wg, const uint8_t *__restrict__ wu, const void *xin, float *__restrict__ act,
     uint8_t *__restrict__ act_pack, int rows)
 {
     static_assert(!EMIT || WAVES == 8, "the output pack block needs 32 rows per workgroup");
-    constexpr int NS = stage_waves<QX>(), ITERS = (NB + 15) / 16;
+    static_assert(WAVES == 4 || WAVES == 8, "gate/up lanes pair across 16 or 32 lanes");
+    constexpr int NS = stage_waves<QX>(), ITERS = (NB + 15) / 16, R = 4 * WAVES;
     extern __shared__ __align__(16) uint8_t lds[];
-    float *act_lds = reinterpret_cast<float *>(lds + (NB * 40 + 15) / 16 * 16);
+    float *T = reinterpret_cast<float *>(lds + (NB * 40 + 15) / 16 * 16);
     const int wave = threadIdx.x >> 6;
     if (wave < NS) {
         prepare_pack<NB, QX>(xin, lds, wave);
-        __syncthreads();
-        if constexpr (EMIT) {
-            __syncthreads();
-            if (wave == 0) {
-                const int lane = threadIdx.x & 63;
-                uint32_t dbits;
-                int s;
-                const int q = q8_0_block32(act_lds[lane & 31], dbits, s);
-                const int blk = blockIdx.x;
-                const int nbo = rows / 32;
-                if (lane < 32) {
-                    act_pack[(size_t)blk * 32 + lane] = (uint8_t)(int8_t)q;
-                    if (lane == 0) {
-                        reinterpret_cast<float *>(act_pack + (size_t)nbo * 32)[blk] = f16_bits_to_f32(dbits);
-                        reinterpret_cast<int32_t *>(act_pack + (size_t)nbo * 36)[blk] = s;
-                    }
-                }
-            }
-        }
+        __syncthreads();  // the pack is whole
+        __syncthreads();  // every term is stored
         return;
     }
     const int lane = threadIdx.x & 63, j = lane & 15;
-    const int row_raw = (blockIdx.x * WAVES + wave - NS) * 4 + (lane >> 4);
-    const int row = row_raw < rows ? row_raw : rows - 1;
+    const int rl = (wave - NS) * 4 + (lane >> 4);
+    const int row_raw = blockIdx.x * R + rl;
+    const int row = row_raw < rows ? row_raw : rows - 1;  // tail rows recompute the last row
     const size_t nblk = (size_t)rows * NB, base = (size_t)row * NB;
     RowRegs<ITERS> rg, ru;
     load_row<ITERS>(rg, wg, nblk, base, NB, j);
     load_row<ITERS>(ru, wu, nblk, base, NB, j);
     __syncthreads();
-    float g, u;
-    fold_row2<ITERS>(rg, ru, lds, base, NB, j, g, u);
-    // only lane 15 of a row holds the row's sums: the GELU runs there alone
-    // (the other lanes' partial sums would send the wave down every branch
-    // of tanhf)
-    if (j == 15 && row_raw < rows) {
-        const float a = gelu_tanh(g) * u;
-        if (act) act[row_raw] = a;
-        if constexpr (EMIT) act_lds[row_raw - blockIdx.x * 32] = a;
+    store_terms2<NB, ITERS>(rg, ru, lds, base, j, T, rl, R + rl);
+    __syncthreads();
+    if (wave != NS) return;
+    const float s = fold_chain<NB>(T, lane < 2 * R ? lane : 0);
+    const float p = lane_xor<R>(s);
+    const bool up = (lane & R) != 0;
+    const float a = gelu_tanh(up ? p : s) * (up ? s : p);  // row (lane mod R)'s output, in both lanes of the pair
+    const int out = blockIdx.x * R + (lane & (R - 1));
+    if (act && lane < R && out < rows) act[out] = a;
+    if constexpr (EMIT) {
+        uint32_t dbits;
+        int qs;
+        const int q = q8_0_block32(a, dbits, qs);
+        const int blk = blockIdx.x, nbo = rows / 32;
+        if (lane < 32) {
+            act_pack[(size_t)blk * 32 + lane] = (uint8_t)(int8_t)q;
+            if (lane == 0) {
+                reinterpret_cast<float *>(act_pack + (size_t)nbo * 32)[blk] = f16_bits_to_f32(dbits);
+                reinterpret_cast<int32_t *>(act_pack + (size_t)nbo * 36)[blk] = qs;
+            }
+        }
     }
-    if constexpr (EMIT) __syncthreads();
+}
+
+// LDS of the GeGLU kernel: the pack, then 2R term chains.
+template <int NB>
+constexpr size_t geglu_lds(int waves)
+{
+    return (NB * 40 + 15) / 16 * 16 + (size_t)2 * 4 * waves * t_stride<NB>() * sizeof(float);
 }
 
 // ---- the Gemma-2 sandwich residual ahead of the rows ---------------------------
@@ -365,12 +463,14 @@ __global__ __launch_bounds__(64 * kGegluResWaves) void gemv_q4_0_geglu_resnorm_k
     uint8_t *__restrict__ act_pack, int rows)
 {
     static_assert(NB * 8 <= 64 * kGegluResWaves, "one float4 chunk per thread");
+    static_assert(2 * 64 * t_stride<NB>() * sizeof(float) <= 3 * 64 * kGegluResWaves * sizeof(float4),
+                  "the term chains fit in the parking area");
     constexpr int ITERS = (NB + 15) / 16;
     extern __shared__ __align__(16) uint8_t lds[];
-    float *act_lds = reinterpret_cast<float *>(lds + (NB * 40 + 15) / 16 * 16);
-    auto *xs = reinterpret_cast<mrml_xsum::Shared4 *>(act_lds + 64);
+    auto *xs = resnorm_shared<NB>(lds);
     // h_in, w_post, w_norm chunks parked in LDS during the norm: the weight
-    // registers plus the norm's own leave no VGPR for them
+    // registers plus the norm's own leave no VGPR for them.  The term chains
+    // reuse the area once the norm is done.
     float4 *park = reinterpret_cast<float4 *>(reinterpret_cast<uint8_t *>(xs) + (sizeof(mrml_xsum::Shared4) + 15) / 16 * 16);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 15, tid = threadIdx.x;
     const ResidualOps ops = residual_load(t, w_post, h_in, w_norm, NB * 8);
@@ -378,29 +478,34 @@ __global__ __launch_bounds__(64 * kGegluResWaves) void gemv_q4_0_geglu_resnorm_k
     park[tid] = ops.h;
     park[64 * kGegluResWaves + tid] = ops.wp;
     park[2 * 64 * kGegluResWaves + tid] = ops.wn;
-    const int row_raw = (blockIdx.x * kGegluResWaves + wave) * 4 + (lane >> 4);
+    const int rl = wave * 4 + (lane >> 4);
+    const int row_raw = blockIdx.x * 64 + rl;
     const int row = row_raw < rows ? row_raw : rows - 1;
     const size_t nblk = (size_t)rows * NB, base = (size_t)row * NB;
     RowRegs<ITERS> rg, ru;
     load_row<ITERS>(rg, wg, nblk, base, NB, j);
     load_row<ITERS>(ru, wu, nblk, base, NB, j);
-    residual_norm1(ops.t, [&](int k) { return park[k * 64 * kGegluResWaves + tid]; }, w_post != nullptr,
-                   w_norm != nullptr, eps, blockIdx.x == 0 ? h_out : nullptr, nullptr, lds, NB * 32, *xs);
-    mrml_xsum::lds_barrier();  // the pack is whole
-    float g, u;
-    fold_row2<ITERS>(rg, ru, lds, base, NB, j, g, u);
-    if (j == 15 && row_raw < rows) act_lds[row_raw - blockIdx.x * 64] = gelu_tanh(g) * u;  // lane 15 holds the row
-    mrml_xsum::lds_barrier();
+    residual_norm1<true>(ops.t, [&](int k) { return park[k * 64 * kGegluResWaves + tid]; }, w_post != nullptr,
+                         w_norm != nullptr, eps, blockIdx.x == 0 ? h_out : nullptr, nullptr, lds, NB * 32, *xs);
+    mrml_xsum::lds_barrier();  // the pack is whole, the parked operands are read
+    float *T = reinterpret_cast<float *>(park);
+    store_terms2<NB, ITERS>(rg, ru, lds, base, j, T, rl, 64 + rl);
+    mrml_xsum::lds_barrier();  // every term is stored
     if (wave < 2) {
+        // wave w folds rows 32w..32w+31: gate chains in lanes 0-31, up in 32-63
+        const float s = fold_chain<NB>(T, (lane >> 5) * 64 + 32 * wave + (lane & 31));
+        const float p = lane_xor<32>(s);
+        const bool up = lane >= 32;
+        const float a = gelu_tanh(up ? p : s) * (up ? s : p);
         uint32_t dbits;
-        int s;
-        const int q = q8_0_block32(act_lds[wave * 32 + (lane & 31)], dbits, s);
+        int qs;
+        const int q = q8_0_block32(a, dbits, qs);
         const int blk = 2 * blockIdx.x + wave, nbo = rows / 32;
         if (lane < 32 && blk < nbo) {
             act_pack[(size_t)blk * 32 + lane] = (uint8_t)(int8_t)q;
             if (lane == 0) {
                 reinterpret_cast<float *>(act_pack + (size_t)nbo * 32)[blk] = f16_bits_to_f32(dbits);
-                reinterpret_cast<int32_t *>(act_pack + (size_t)nbo * 36)[blk] = s;
+                reinterpret_cast<int32_t *>(act_pack + (size_t)nbo * 36)[blk] = qs;
             }
         }
     }
@@ -426,8 +531,8 @@ __global__ __launch_bounds__(64 * kResWaves) void gemv_q4_0_qkv_resnorm_kernel(
     const size_t base = (size_t)m.local * NB;
     RowRegs<ITERS> r;
     if (wave > 0) load_row<ITERS>(r, m.w, (size_t)m.mrows * NB, base, NB, j);
-    residual_norm1(ops, w_post != nullptr, w_norm != nullptr, eps, blockIdx.x == 0 ? h_out : nullptr, nullptr,
-                   resnorm_pack_lds<NB>(lds), NB * 32, *resnorm_shared<NB>(lds));
+    residual_norm1<true>(ops, w_post != nullptr, w_norm != nullptr, eps, blockIdx.x == 0 ? h_out : nullptr, nullptr,
+                         resnorm_pack_lds<NB>(lds), NB * 32, *resnorm_shared<NB>(lds));
     mrml_xsum::lds_barrier();  // the pack is whole
     if (wave > 0) {
         const float s = fold_row<ITERS>(r, lds, base, NB, j);
@@ -540,7 +645,7 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_0_any_kernel(const u
 {
     extern __shared__ __align__(16) uint8_t lds[];
     if (threadIdx.x < 64) {
-        stage_pack_wave(xpack, lds, nb);
+        stage_split_pack(xpack, lds, nb);
         __syncthreads();
         return;
     }
@@ -564,7 +669,7 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_0_geglu_any_kernel(c
 {
     extern __shared__ __align__(16) uint8_t lds[];
     if (threadIdx.x < 64) {
-        stage_pack_wave(xpack, lds, nb);
+        stage_split_pack(xpack, lds, nb);
         __syncthreads();
         return;
     }
@@ -591,7 +696,7 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_0_qkv_any_kernel(con
 {
     extern __shared__ __align__(16) uint8_t lds[];
     if (threadIdx.x < 64) {
-        stage_pack_wave(xpack, lds, nb);
+        stage_split_pack(xpack, lds, nb);
         __syncthreads();
         return;
     }
@@ -635,24 +740,22 @@ __global__ __launch_bounds__(64) void gemv_q4_0_gguf_kernel(const uint8_t *__res
         uint16_t *d = reinterpret_cast<uint16_t *>(tile);
         for (size_t i = lane; i < span_bytes / 2; i += 64) d[i] = s[i];
     }
-    stage_pack_wave(xpack, act, nb);
+    stage_split_pack(xpack, act, nb);
     __syncthreads();
     const int row = rsub < nrows ? rsub : nrows - 1;
     const uint16_t *rowp = reinterpret_cast<const uint16_t *>(tile + (size_t)row * row_bytes);
-    const int4 *aq = reinterpret_cast<const int4 *>(act);
+    const uint4 *aq = reinterpret_cast<const uint4 *>(act);
     const float *ad = reinterpret_cast<const float *>(act + nb * 32);
-    const int32_t *as = reinterpret_cast<const int32_t *>(act + nb * 36);
+    const int32_t *ac = reinterpret_cast<const int32_t *>(act + nb * 36);
     float s = 0.0f;
     for (int it = 0; it < ITERS; ++it) {
         const int b = it * 16 + j;
         const int bc = b < nb ? b : nb - 1;
         const uint16_t *blk = rowp + bc * 9;  // 18 bytes = 9 halfwords
-        uint4 q;
-        q.x = blk[1] | ((uint32_t)blk[2] << 16);
-        q.y = blk[3] | ((uint32_t)blk[4] << 16);
-        q.z = blk[5] | ((uint32_t)blk[6] << 16);
-        q.w = blk[7] | ((uint32_t)blk[8] << 16);
-        const int32_t isum = q4_0_isum(q, aq[2 * bc], aq[2 * bc + 1], as[bc]);
+        const uint4 lo = aq[2 * bc], hi = aq[2 * bc + 1];
+        const int32_t isum = q4_0_isum_split(blk[1] | ((uint32_t)blk[2] << 16), blk[3] | ((uint32_t)blk[4] << 16),
+                                             blk[5] | ((uint32_t)blk[6] << 16), blk[7] | ((uint32_t)blk[8] << 16),
+                                             lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w, ac[bc]);
         const float tv = (float)isum * (f16_bits_to_f32(blk[0]) * ad[bc]);
         const float t = b < nb ? tv : 0.0f;
 #pragma unroll
@@ -775,7 +878,7 @@ int launch_gemv_q4_0_geglu(mrml_hip_ctx *ctx, const void *wg, const void *wu, co
         const dim3 grid(((rows + 3) / 4 + kFoldWaves - 1) / kFoldWaves);
         MRML_FOLD16_NB(nb, {
             hipLaunchKernelGGL((gemv_q4_0_geglu_kernel<NB, kFoldWaves, false, false>), grid,
-                               dim3(64 * (kFoldWaves + 1)), pack_lds(NB), ctx->stream, (const uint8_t *)wg,
+                               dim3(64 * (kFoldWaves + 1)), geglu_lds<NB>(kFoldWaves), ctx->stream, (const uint8_t *)wg,
                                (const uint8_t *)wu, xpack, act, (uint8_t *)nullptr, rows);
         });
         return check_launch(ctx, "gemv_q4_0_geglu_kernel");
@@ -807,7 +910,7 @@ int launch_gemv_q4_0_geglu_emit(mrml_hip_ctx *ctx, const void *wg, const void *w
     if (fold16_shape(nb) && rows % 32 == 0) {
         MRML_FOLD16_NB(nb, {
             hipLaunchKernelGGL((gemv_q4_0_geglu_kernel<NB, 8, false, true>), dim3(rows / 32), dim3(64 * 9),
-                               pack_lds(NB) + 32 * sizeof(float), ctx->stream, (const uint8_t *)wg,
+                               geglu_lds<NB>(8), ctx->stream, (const uint8_t *)wg,
                                (const uint8_t *)wu, xpack, act, (uint8_t *)act_pack, rows);
         });
         return check_launch(ctx, "gemv_q4_0_geglu_kernel");
@@ -827,18 +930,17 @@ int launch_gemv_q4_0_geglu_x(mrml_hip_ctx *ctx, const void *wg, const void *wu, 
     const int nb = cols / 32;
     if (int rc = check_even(ctx, rows, nb)) return rc;
     if (fold16_shape(nb) && (!act_pack || rows % 32 == 0)) {
-        const size_t lds = pack_lds(nb) + 32 * sizeof(float);
         if (act_pack) {
             MRML_FOLD16_NB(nb, {
                 hipLaunchKernelGGL((gemv_q4_0_geglu_kernel<NB, 8, true, true>), dim3(rows / 32), dim3(64 * (8 + kNQ)),
-                                   lds, ctx->stream, (const uint8_t *)wg, (const uint8_t *)wu, (const void *)x, act,
+                                   geglu_lds<NB>(8), ctx->stream, (const uint8_t *)wg, (const uint8_t *)wu, (const void *)x, act,
                                    (uint8_t *)act_pack, rows);
             });
         } else {
             const dim3 grid(((rows + 3) / 4 + kFoldWaves - 1) / kFoldWaves);
             MRML_FOLD16_NB(nb, {
                 hipLaunchKernelGGL((gemv_q4_0_geglu_kernel<NB, kFoldWaves, true, false>), grid,
-                                   dim3(64 * (kFoldWaves + kNQ)), lds, ctx->stream, (const uint8_t *)wg,
+                                   dim3(64 * (kFoldWaves + kNQ)), geglu_lds<NB>(kFoldWaves), ctx->stream, (const uint8_t *)wg,
                                    (const uint8_t *)wu, (const void *)x, act, (uint8_t *)nullptr, rows);
             });
         }

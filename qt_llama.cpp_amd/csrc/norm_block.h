@@ -56,12 +56,16 @@ __device__ __forceinline__ float rms_scale(float sum_sq, int dim, float eps)
 }
 
 // Q8_0 pack of the value chunk c (values 4c..4c+3); 8 consecutive threads
-// hold one block.  Every lane of the wave must call this.
+// hold one block.  SPLIT writes the split-nibble form the Q4_0 kernels read
+// from LDS (device.h; the sum plane then holds c).  Every lane of the wave
+// must call this.
+template <bool SPLIT = false>
 __device__ __forceinline__ void emit_q8(float4 v, int c, int n4, uint8_t *pack, int nb)
 {
     uint32_t dbits;
     int s;
-    const uint32_t q = q8_0_block8x4(v, dbits, s);
+    uint32_t q = q8_0_block8x4(v, dbits, s);
+    if constexpr (SPLIT) q = q8_split8(q, c & 7, s);
     if (c < n4) {
         reinterpret_cast<uint32_t *>(pack)[c] = q;
         if ((c & 7) == 0) {
@@ -85,8 +89,8 @@ __device__ __forceinline__ void load_w(const float *w, float4 (&wv)[CH], int n4)
 }
 
 // out = (x * scale) * w per value (has_w false: no weight), stored to out
-// (nullable) and as a Q8_0 pack (nullable).
-template <int CH>
+// (nullable) and as a Q8_0 pack (nullable; SPLIT: split-nibble form).
+template <int CH, bool SPLIT = false>
 __device__ __forceinline__ void norm_store(const float4 (&v)[CH], float scale, const float4 (&wv)[CH], bool has_w,
                                            float *out, uint8_t *pack, int n4)
 {
@@ -97,7 +101,7 @@ __device__ __forceinline__ void norm_store(const float4 (&v)[CH], float scale, c
         float4 o = scale4(v[k], scale);
         if (has_w) o = mul4(o, wv[k]);
         if (out && c < n4) reinterpret_cast<float4 *>(out)[c] = o;
-        if (pack) emit_q8(o, c, n4, pack, n4 >> 3);
+        if (pack) emit_q8<SPLIT>(o, c, n4, pack, n4 >> 3);
     }
 }
 
@@ -136,8 +140,9 @@ __device__ __forceinline__ ResidualOps residual_load(const float *__restrict__ t
 // when they are needed (registers, or LDS where a kernel parks them to keep
 // registers free).  The pack may be in LDS; the caller synchronises before
 // reading it.  h_out may equal h_in (each thread reads its chunk before
-// writing it) only when no other workgroup reads h_in.
-template <class Fetch>
+// writing it) only when no other workgroup reads h_in.  SPLIT: the pack is
+// written in split-nibble form.
+template <bool SPLIT = false, class Fetch>
 __device__ __forceinline__ void residual_norm1(float4 t, Fetch fetch, bool has_wpost, bool has_wnext, float eps,
                                                float *h_out, float *xn, uint8_t *pack, int dim,
                                                mrml_xsum::Shared4 &x)
@@ -152,15 +157,16 @@ __device__ __forceinline__ void residual_norm1(float4 t, Fetch fetch, bool has_w
     if (!xn && !pack) return;
     v[0] = c < n4 ? hn : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     const float4 wv[1] = {fetch(2)};
-    norm_store<1>(v, rms_scale(block_seq_sum_sq<1>(v, n4, reinterpret_cast<float *>(&x)), dim, eps), wv, has_wnext,
-                  xn, pack, n4);
+    norm_store<1, SPLIT>(v, rms_scale(block_seq_sum_sq<1>(v, n4, reinterpret_cast<float *>(&x)), dim, eps), wv,
+                         has_wnext, xn, pack, n4);
 }
 
+template <bool SPLIT = false>
 __device__ __forceinline__ void residual_norm1(const ResidualOps &r, bool has_wpost, bool has_wnext, float eps,
                                                float *h_out, float *xn, uint8_t *pack, int dim,
                                                mrml_xsum::Shared4 &x)
 {
-    residual_norm1(r.t, [&](int k) { return k == 0 ? r.h : (k == 1 ? r.wp : r.wn); }, has_wpost, has_wnext, eps, h_out,
+    residual_norm1<SPLIT>(r.t, [&](int k) { return k == 0 ? r.h : (k == 1 ? r.wp : r.wn); }, has_wpost, has_wnext, eps, h_out,
                    xn, pack, dim, x);
 }
 
