@@ -224,26 +224,19 @@ __device__ __forceinline__ void fold_row2(const RowRegs<ITERS> &ra, const RowReg
 // LDS, T[chain][b] at a stride of t_stride floats, and after a barrier one
 // lane per chain adds a row's terms in order -- one add instruction per
 // block for up to 64 rows, where the DPP fold spends 16 per 16 blocks per 4
-// rows.  The stride is an odd number of 16-byte segments, so the float4
-// reads of 64 chains spread over the banks.
+// rows.  A chain has a slot for every lane's block of every iteration
+// (ITERS*16 >= NB; the slots past NB hold the masked +0 terms and are never
+// read), so the stores are unconditional: a store under `b < NB` lets the
+// compiler sink the whole term, weight load included, into the branch and
+// issue the last iteration's loads only after the first terms.  The stride
+// is an odd number of 16-byte segments, so the float4 reads of 64 chains
+// spread over the banks.
 template <int NB>
 constexpr int t_stride()
 {
     static_assert(NB % 4 == 0, "float4 reads of the terms");
-    return (NB / 4) % 2 ? NB : NB + 4;
-}
-
-// Store the terms of one row (this lane's blocks 16*it + j) to chain `chain`.
-template <int NB, int ITERS>
-__device__ __forceinline__ void store_terms(const RowRegs<ITERS> &r, const uint8_t *pack, size_t base, int j,
-                                            float *T, int chain)
-{
-#pragma unroll
-    for (int it = 0; it < ITERS; ++it) {
-        const float t = row_term<ITERS>(r, it, pack, base, NB, j);
-        const int b = it * 16 + j;
-        if (b < NB) T[chain * t_stride<NB>() + b] = t;
-    }
+    constexpr int n = (NB + 15) / 16 * 16;
+    return (n / 4) % 2 ? n : n + 4;
 }
 
 // Two rows (gate and up): the term chains of both, computed interleaved.
@@ -255,11 +248,8 @@ __device__ __forceinline__ void store_terms2(const RowRegs<ITERS> &ra, const Row
     for (int it = 0; it < ITERS; ++it) {
         const float ta = row_term<ITERS>(ra, it, pack, base, NB, j);
         const float tb = row_term<ITERS>(rb, it, pack, base, NB, j);
-        const int b = it * 16 + j;
-        if (b < NB) {
-            T[chain_a * t_stride<NB>() + b] = ta;
-            T[chain_b * t_stride<NB>() + b] = tb;
-        }
+        T[chain_a * t_stride<NB>() + it * 16 + j] = ta;
+        T[chain_b * t_stride<NB>() + it * 16 + j] = tb;
     }
 }
 
