@@ -485,6 +485,167 @@ __device__ __forceinline__ float block_seq_sum_nonneg4(float4 v, int n, Shared4 
     return x.result;
 }
 
+// ---- a group of waves with its own barrier ------------------------------------
+// The register form for the nw (<= 16) waves of a group inside a workgroup,
+// K terms per lane: lane l of group wave gw holds terms k = K*(64*gw + l) + i.
+// Classification, runs and the ordered walk are those above; the group's
+// barrier is an LDS counter (GroupSync), so the workgroup's other waves never
+// wait on the sum -- they can be stalled issuing loads meanwhile.
+
+// A barrier among the nw waves of a group: each wave adds 1 to an LDS counter
+// once its own LDS accesses are done and waits until the counter reaches nw
+// times its number of syncs so far.  The counter is zeroed (and the zero made
+// visible by a workgroup barrier) before the group's first sync.  The wait is
+// bounded: a group that never completes lets its waves go on with wrong data
+// rather than keep the device busy forever.
+constexpr int kSyncSpin = 1 << 20;
+
+struct GroupSync {
+    uint32_t *ctr;
+    uint32_t target;
+    uint32_t nw;
+    __device__ __forceinline__ void operator()()
+    {
+        target += nw;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        for (int i = 0; i < kSyncSpin; ++i) {
+            const uint32_t v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (__builtin_amdgcn_readfirstlane(v) >= target) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        asm volatile("" ::: "memory");
+    }
+};
+
+// LDS of a group sum: the event list (at most one event per term) and the
+// zero pad live at evl, sized by the caller: group_events(n) floats.
+constexpr int group_events(int n) { return n + kPadEvents; }
+
+struct GroupShared {
+    float wtot[16];
+    int wcnt[16];
+    float result;
+};
+
+// Sum of the terms held by the group (n terms in all), bit for bit the
+// sequential loop.  Every lane of the nw waves calls it; gw is the wave's
+// index in the group (uniform).
+template <int K>
+__device__ __forceinline__ float group_seq_sum_nonneg(const float (&av)[K], int n, int gw, GroupSync &sync,
+                                                      GroupShared &x, float *evl)
+{
+    static_assert(K >= 1 && K <= 32 && K + 12 <= kDepth, "masks in 32 bits; prefix depth within the margin");
+    const int lane = threadIdx.x & 63, nw = (int)sync.nw;
+    const int k0 = K * (64 * gw + lane);
+    if (64 * K * gw >= n) {
+        if (lane == 63) x.wtot[gw] = 0.0f;
+        sync();
+        if (lane == 63) x.wcnt[gw] = 0;
+        sync();
+        sync();
+        sync();
+        return x.result;
+    }
+    float a[K], lp[K], run = 0.0f;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        a[i] = k0 + i < n ? av[i] : 0.0f;
+        run += a[i];
+        lp[i] = run;
+    }
+    const float wincl = wave_incl_scan_f32(run);
+    if (lane == 63) x.wtot[gw] = wincl;
+    sync();
+    const float wt = lane < gw ? x.wtot[lane] : 0.0f;  // lane < gw <= 15: row 0
+    const float base =
+        __builtin_bit_cast(float, wave_shr1_i32(__builtin_bit_cast(int, wincl))) + readlane_f32(row_incl_scan_f32(wt), 15);
+    uint32_t inc[K], my_inc = 0;
+    float uu[K];
+    uint32_t unsafe = 0, stop = 0;
+    const float rho = margin(k0 + K - 1), omr = 1.0f - rho, opr = 1.0f + rho;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        const int k = k0 + i;
+        const Step st = classify(a[i], i ? base + lp[i - 1] : base, base + lp[i], k == 0, omr, opr);
+        const bool in = k < n;
+        inc[i] = (in && st.safe) ? (uint32_t)st.inc : 0u;
+        uu[i] = st.u;
+        unsafe |= (in && !st.safe) ? (1u << i) : 0u;
+        stop |= (!in || !st.safe) ? (1u << i) : 0u;
+        my_inc += inc[i];
+    }
+    const uint32_t pv = (uint32_t)wave_shr1_i32((int)unsafe), nx = (uint32_t)wave_shl1_i32((int)stop);
+    const uint32_t prev = lane == 0 ? (1u << (K - 1)) : pv, next = lane == 63 ? 1u : nx;
+    uint32_t starts = 0, ends = 0;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        const bool in = k0 + i < n, uns = (unsafe >> i) & 1u;
+        const bool before = i ? (unsafe >> (i - 1)) & 1u : (prev >> (K - 1)) & 1u;
+        const bool after = i < K - 1 ? (stop >> (i + 1)) & 1u : next & 1u;
+        starts |= (in && (uns || before)) ? (1u << i) : 0u;
+        ends |= (in && !uns && after) ? (1u << i) : 0u;
+    }
+    const int cnt = __builtin_popcount(starts);
+    const int cincl = wave_incl_scan_i32(cnt);
+    const uint32_t iincl = (uint32_t)wave_incl_scan_i32((int)my_inc);
+    uint32_t r = iincl - my_inc, mine = 0;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        if (((starts & ~unsafe) >> i) & 1u) mine = r;
+        r += inc[i];
+    }
+    uint32_t rs = (uint32_t)wave_shr1_i32((int)wave_incl_max_u32(mine));
+    if (lane == 63) x.wcnt[gw] = cincl;
+    sync();
+    const int cw = lane < nw ? x.wcnt[lane] : 0;  // row 0
+    const int ci = row_incl_scan_i32(cw);
+    const int nev = __builtin_amdgcn_readlane(ci, 15);
+    const int goff = gw ? __builtin_amdgcn_readlane(ci, gw - 1) : 0;
+    if (gw == 0 && lane < kPadEvents) evl[nev + lane] = 0.0f;
+    float *ev = evl + goff;
+    int e = cincl - cnt;
+    r = iincl - my_inc;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        const bool st = (starts >> i) & 1u;
+        e += st ? 1 : 0;
+        if (st && !((unsafe >> i) & 1u)) rs = r;
+        const uint32_t re = r + inc[i];
+        if ((unsafe >> i) & 1u) ev[e - 1] = a[i];
+        if ((ends >> i) & 1u) ev[e - 1] = (float)(int)(re - rs) * uu[i];  // exact: < 2^23 ulps, u a power of 2
+        r = re;
+    }
+    sync();
+    // the ordered walk by group wave 0, as in the workgroup form
+    if (gw == 0) {
+        const float4 *e4 = reinterpret_cast<const float4 *>(evl);
+        const int n4 = ((nev + 15) >> 4) * 4;
+        float s = 0.0f;
+        for (int q0 = 0; q0 < n4; q0 += 8) {
+            float4 b[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) b[q] = e4[q0 + q < n4 ? q0 + q : n4 - 1];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                if (q0 + 4 * g < n4) {
+#pragma unroll
+                    for (int q = 4 * g; q < 4 * g + 4; ++q) {
+                        s += b[q].x;
+                        s += b[q].y;
+                        s += b[q].z;
+                        s += b[q].w;
+                    }
+                }
+            }
+        }
+        if (lane == 0) x.result = s;
+    }
+    sync();
+    return x.result;
+}
+
 #endif  // __HIPCC__
 
 }  // namespace mrml_xsum

@@ -60,16 +60,26 @@ __device__ __forceinline__ int32_t q4_0_isum(uint4 w, int4 a0, int4 a1, int32_t 
 // LDS in split-nibble form (device.h) with one wave, one block per lane;
 // every load of a batch is issued before the first block is converted, so
 // the copy costs one L2 round trip per 64*kBatch blocks.
+// With ISSUE_BARRIER the wave joins one workgroup barrier (s_barrier, no
+// memory fence) right after issuing its loads: compute waves that wait on
+// that barrier before issuing their weight loads then queue behind the
+// pack's loads in the CU's memory pipeline instead of ahead of them (an L2
+// hit issued after a CU's worth of HBM misses waits for most of them).  The
+// pack is then one batch: nb <= kStageMax, checked by the launchers.
+constexpr int kStageBatch = 5, kStageMax = 64 * kStageBatch;
+
+template <bool ISSUE_BARRIER = false>
 __device__ __forceinline__ void stage_split_pack(const uint8_t *src, uint8_t *lds, int nb)
 {
-    constexpr int kBatch = 5;
+    constexpr int kBatch = kStageBatch;
     const int lane = threadIdx.x & 63;
     const uint4 *sq = reinterpret_cast<const uint4 *>(src);
     const float *sd = reinterpret_cast<const float *>(src + (size_t)nb * 32);
     uint4 *dq = reinterpret_cast<uint4 *>(lds);
     float *dd = reinterpret_cast<float *>(lds + nb * 32);
     int32_t *dc = reinterpret_cast<int32_t *>(lds + nb * 36);
-    for (int b0 = 0; b0 < nb; b0 += 64 * kBatch) {
+    const int nbatch = ISSUE_BARRIER ? 64 * kBatch : nb;  // one pass with the barrier (exactly one s_barrier)
+    for (int b0 = 0; b0 < nbatch; b0 += 64 * kBatch) {
         uint4 x[kBatch], y[kBatch];
         float d[kBatch];
 #pragma unroll
@@ -80,6 +90,7 @@ __device__ __forceinline__ void stage_split_pack(const uint8_t *src, uint8_t *ld
             y[k] = sq[2 * b + 1];
             d[k] = sd[b];
         }
+        if constexpr (ISSUE_BARRIER) __builtin_amdgcn_s_barrier();
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
             const int b = b0 + k * 64 + lane;
@@ -115,6 +126,7 @@ __device__ __forceinline__ void quantize_into_lds(const float *__restrict__ x, u
         b = b < NB ? b : NB - 1;
         v[k] = x4[b * 8 + l];
     }
+    __builtin_amdgcn_s_barrier();  // x's loads are issued (stage_split_pack's ISSUE_BARRIER)
     uint32_t *pq = reinterpret_cast<uint32_t *>(pack);
     float *pd = reinterpret_cast<float *>(pack + NB * 32);
     int32_t *ps = reinterpret_cast<int32_t *>(pack + NB * 36);
@@ -303,8 +315,9 @@ constexpr int kNQ = 4;  // staging waves when quantising x in the kernel
 template <int NB, bool QX>
 __device__ __forceinline__ void prepare_pack(const void *xin, uint8_t *lds, int wave)
 {
+    static_assert(NB <= kStageMax, "one staging batch");
     if constexpr (QX) quantize_into_lds<NB, kNQ>(reinterpret_cast<const float *>(xin), lds, wave);
-    else if (wave == 0) stage_split_pack(reinterpret_cast<const uint8_t *>(xin), lds, NB);
+    else stage_split_pack<true>(reinterpret_cast<const uint8_t *>(xin), lds, NB);
 }
 
 template <bool QX>
@@ -327,6 +340,7 @@ __global__ __launch_bounds__(64 * (WAVES + (QX ? kNQ : 1))) void gemv_q4_0_kerne
     const int row = row_raw < rows ? row_raw : rows - 1;  // tail rows recompute the last row
     const size_t base = (size_t)row * NB;
     RowRegs<ITERS> r;
+    __builtin_amdgcn_s_barrier();  // the pack's loads are issued
     load_row<ITERS>(r, w, (size_t)rows * NB, base, NB, j);
     __syncthreads();
     const float s = fold_row<ITERS>(r, lds, base, NB, j);
@@ -352,6 +366,7 @@ __global__ __launch_bounds__(64 * (WAVES + (QX ? kNQ : 1))) void gemv_q4_0_qkv_k
     const QkvSel m = qkv_select(wq, wk, wv, row_raw < total ? row_raw : total - 1, q_rows, kv_rows);
     const size_t base = (size_t)m.local * NB;
     RowRegs<ITERS> r;
+    __builtin_amdgcn_s_barrier();  // the pack's loads are issued
     load_row<ITERS>(r, m.w, (size_t)m.mrows * NB, base, NB, j);
     __syncthreads();
     const float s = fold_row<ITERS>(r, lds, base, NB, j);
@@ -387,6 +402,7 @@ __global__ __launch_bounds__(64 * (WAVES + (QX ? kNQ : 1))) void gemv_q4_0_geglu
     const int row = row_raw < rows ? row_raw : rows - 1;  // tail rows recompute the last row
     const size_t nblk = (size_t)rows * NB, base = (size_t)row * NB;
     RowRegs<ITERS> rg, ru;
+    __builtin_amdgcn_s_barrier();  // the pack's loads are issued
     load_row<ITERS>(rg, wg, nblk, base, NB, j);
     load_row<ITERS>(ru, wu, nblk, base, NB, j);
     __syncthreads();
@@ -440,11 +456,108 @@ __device__ __forceinline__ mrml_xsum::Shared4 *resnorm_shared(uint8_t *lds)
 }
 
 // Gate+up with the GeGLU epilogue and the output's Q8_0 pack, the
-// post-attention residual fused ahead.  16 waves own 64 rows (two output
-// blocks) and all of them fold rows: 144 workgroups for 9216 rows, so every
-// workgroup is resident at once (at 9 waves a CU holds one workgroup and
-// 288 of them would take two rounds, each paying for the norm).
+// post-attention residual fused ahead: 16 waves own 64 rows (two output
+// blocks), 144 workgroups for 9216 rows, so every workgroup is resident at
+// once.
 constexpr int kGegluResWaves = 16;
+
+// ---- the residual norm in a group of waves, the weight stream beside it --------
+// In the fused residual + GeGLU the two norms run in the first kNormWaves
+// waves only (exact_sum.h's group form, synchronised by an LDS counter)
+// while the other waves issue their weight loads at once: a wave issuing
+// loads into a full memory pipeline stalls, and with workgroup barriers
+// inside the norm every stall held the norm back.  The norm waves
+// issue their own rows' loads once the pack is written; everyone meets at one
+// workgroup barrier before the terms.  Norm lane l of wave w holds the KN
+// consecutive values k = KN*(64w + l) + i.
+constexpr int kNormWaves = 4;
+
+template <int NB>
+constexpr int norm_kn() { return (NB * 32 + 64 * kNormWaves - 1) / (64 * kNormWaves); }
+
+// LDS: pack | GroupShared | sync counter | xn (dim floats) + events (dim + pad),
+// the term chains reusing that last area once the pack is whole.
+template <int NB>
+constexpr size_t rn2_group_off() { return (NB * 40 + 15) / 16 * 16; }
+template <int NB>
+constexpr size_t rn2_area_off() { return rn2_group_off<NB>() + (sizeof(mrml_xsum::GroupShared) + 16 + 15) / 16 * 16; }
+template <int NB>
+constexpr size_t rn2_area_bytes(int chains)
+{
+    const size_t norm = (size_t)(NB * 32 + mrml_xsum::group_events(NB * 32)) * sizeof(float);
+    const size_t terms = (size_t)chains * t_stride<NB>() * sizeof(float);
+    return norm > terms ? norm : terms;
+}
+
+// The group's operands: lane values k = KN*(64w + l) + i of t, h_in, w_post,
+// w_norm.  Loaded unconditionally (a missing weight reads t and is replaced
+// by 1 in the norm) so that all of them are issued at once, before the
+// workgroup barrier that lets the other waves issue their weight loads.
+template <int NB>
+struct GroupNormOps {
+    float t[norm_kn<NB>()], h[norm_kn<NB>()], p[norm_kn<NB>()], n[norm_kn<NB>()];
+};
+
+template <int NB>
+__device__ __forceinline__ void group_norm_load(GroupNormOps<NB> &o, const float *__restrict__ t,
+                                                const float *__restrict__ w_post, const float *h_in,
+                                                const float *__restrict__ w_norm, int wave)
+{
+    constexpr int DIM = NB * 32, KN = norm_kn<NB>();
+    const int k0 = KN * (64 * wave + (threadIdx.x & 63));
+    const float *pp = w_post ? w_post : t, *pn = w_norm ? w_norm : t;
+#pragma unroll
+    for (int i = 0; i < KN; ++i) {
+        const int k = k0 + i < DIM ? k0 + i : DIM - 1;
+        o.t[i] = t[k];
+        o.h[i] = h_in[k];
+        o.p[i] = pp[k];
+        o.n[i] = pn[k];
+    }
+}
+
+// The residual norm of the group: h_out = h_in + rms_norm(t, w_post) (stored
+// when h_out is set), the split pack of rms_norm(h_out, w_norm) at pack.
+// Called by the kNormWaves group waves only.
+template <int NB>
+__device__ __forceinline__ void group_residual_norm(GroupNormOps<NB> &o, bool has_post, bool has_norm, float *h_out,
+                                                    float eps, uint8_t *pack, uint8_t *lds_group, float *area,
+                                                    int wave)
+{
+    constexpr int DIM = NB * 32, KN = norm_kn<NB>(), N4 = DIM / 4;
+    const int lane = threadIdx.x & 63, k0 = KN * (64 * wave + lane);
+    auto *gs = reinterpret_cast<mrml_xsum::GroupShared *>(lds_group);
+    mrml_xsum::GroupSync sync{reinterpret_cast<uint32_t *>(lds_group + sizeof(mrml_xsum::GroupShared)), 0u,
+                              (uint32_t)kNormWaves};
+    float sq[KN];
+#pragma unroll
+    for (int i = 0; i < KN; ++i) sq[i] = o.t[i] * o.t[i];
+    float *xn = area, *evl = area + DIM;
+    const float s1 = rms_scale(mrml_xsum::group_seq_sum_nonneg<KN>(sq, DIM, wave, sync, *gs, evl), DIM, eps);
+#pragma unroll
+    for (int i = 0; i < KN; ++i) {
+        float tn = o.t[i] * s1;
+        if (has_post) tn = tn * o.p[i];
+        o.h[i] = o.h[i] + tn;
+        if (h_out && k0 + i < DIM) h_out[k0 + i] = o.h[i];
+        sq[i] = o.h[i] * o.h[i];
+    }
+    const float s2 = rms_scale(mrml_xsum::group_seq_sum_nonneg<KN>(sq, DIM, wave, sync, *gs, evl), DIM, eps);
+#pragma unroll
+    for (int i = 0; i < KN; ++i) {
+        float v = o.h[i] * s2;
+        if (has_norm) v = v * o.n[i];
+        if (k0 + i < DIM) xn[k0 + i] = v;
+    }
+    sync();
+    // Q8_0 blocks: 8 consecutive lanes per block, chunk c = 64w + l + 256m
+    const float4 *x4 = reinterpret_cast<const float4 *>(xn);
+#pragma unroll
+    for (int m = 0; m < (N4 + 64 * kNormWaves - 1) / (64 * kNormWaves); ++m) {
+        const int c = 64 * wave + lane + 64 * kNormWaves * m;
+        emit_q8<true>(x4[c < N4 ? c : N4 - 1], c, N4, pack, NB);
+    }
+}
 
 template <int NB>
 __global__ __launch_bounds__(64 * kGegluResWaves) void gemv_q4_0_geglu_resnorm_kernel(
@@ -452,37 +565,36 @@ __global__ __launch_bounds__(64 * kGegluResWaves) void gemv_q4_0_geglu_resnorm_k
     const float *__restrict__ w_post, const float *h_in, float *h_out, const float *__restrict__ w_norm, float eps,
     uint8_t *__restrict__ act_pack, int rows)
 {
-    static_assert(NB * 8 <= 64 * kGegluResWaves, "one float4 chunk per thread");
-    static_assert(2 * 64 * t_stride<NB>() * sizeof(float) <= 3 * 64 * kGegluResWaves * sizeof(float4),
-                  "the term chains fit in the parking area");
     constexpr int ITERS = (NB + 15) / 16;
+    static_assert(2 * 64 <= 128, "chains");
     extern __shared__ __align__(16) uint8_t lds[];
-    auto *xs = resnorm_shared<NB>(lds);
-    // h_in, w_post, w_norm chunks parked in LDS during the norm: the weight
-    // registers plus the norm's own leave no VGPR for them.  The term chains
-    // reuse the area once the norm is done.
-    float4 *park = reinterpret_cast<float4 *>(reinterpret_cast<uint8_t *>(xs) + (sizeof(mrml_xsum::Shared4) + 15) / 16 * 16);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 15, tid = threadIdx.x;
-    const ResidualOps ops = residual_load(t, w_post, h_in, w_norm, NB * 8);
-    wait_vm_loads();  // the norm then waits on no weight load
-    park[tid] = ops.h;
-    park[64 * kGegluResWaves + tid] = ops.wp;
-    park[2 * 64 * kGegluResWaves + tid] = ops.wn;
+    uint8_t *lds_group = lds + rn2_group_off<NB>();
+    float *area = reinterpret_cast<float *>(lds + rn2_area_off<NB>());
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 15;
+    // the norm's operands are issued first, so they do not queue behind the
+    // weights; the barrier also publishes the zeroed sync counter
+    GroupNormOps<NB> ops;
+    if (wave < kNormWaves) group_norm_load<NB>(ops, t, w_post, h_in, w_norm, wave);
+    if (threadIdx.x == 0) *reinterpret_cast<uint32_t *>(lds_group + sizeof(mrml_xsum::GroupShared)) = 0u;
+    __syncthreads();
     const int rl = wave * 4 + (lane >> 4);
-    const int row_raw = blockIdx.x * 64 + rl;
-    const int row = row_raw < rows ? row_raw : rows - 1;
+    const int row = blockIdx.x * 64 + rl;  // rows % 64 == 0
     const size_t nblk = (size_t)rows * NB, base = (size_t)row * NB;
     RowRegs<ITERS> rg, ru;
-    load_row<ITERS>(rg, wg, nblk, base, NB, j);
-    load_row<ITERS>(ru, wu, nblk, base, NB, j);
-    residual_norm1<true>(ops.t, [&](int k) { return park[k * 64 * kGegluResWaves + tid]; }, w_post != nullptr,
-                         w_norm != nullptr, eps, blockIdx.x == 0 ? h_out : nullptr, nullptr, lds, NB * 32, *xs);
-    mrml_xsum::lds_barrier();  // the pack is whole, the parked operands are read
-    float *T = reinterpret_cast<float *>(park);
+    if (wave >= kNormWaves) {
+        load_row<ITERS>(rg, wg, nblk, base, NB, j);
+        load_row<ITERS>(ru, wu, nblk, base, NB, j);
+    } else {
+        group_residual_norm<NB>(ops, w_post != nullptr, w_norm != nullptr, blockIdx.x == 0 ? h_out : nullptr, eps, lds,
+                                lds_group, area, wave);
+        load_row<ITERS>(rg, wg, nblk, base, NB, j);
+        load_row<ITERS>(ru, wu, nblk, base, NB, j);
+    }
+    __syncthreads();  // the pack is whole; the norm's area is free
+    float *T = area;
     store_terms2<NB, ITERS>(rg, ru, lds, base, j, T, rl, 64 + rl);
-    mrml_xsum::lds_barrier();  // every term is stored
+    __syncthreads();  // every term is stored
     if (wave < 2) {
-        // wave w folds rows 32w..32w+31: gate chains in lanes 0-31, up in 32-63
         const float s = fold_chain<NB>(T, (lane >> 5) * 64 + 32 * wave + (lane & 31));
         const float p = lane_xor<32>(s);
         const bool up = lane >= 32;
@@ -500,6 +612,9 @@ __global__ __launch_bounds__(64 * kGegluResWaves) void gemv_q4_0_geglu_resnorm_k
         }
     }
 }
+
+template <int NB>
+constexpr size_t geglu_resnorm_lds() { return rn2_area_off<NB>() + rn2_area_bytes<NB>(128); }
 
 // The stacked q|k|v matvec, the post-FFN residual of the previous block and
 // this block's pre-attention norm fused ahead (32 rows per workgroup).
@@ -626,6 +741,85 @@ __global__ __launch_bounds__(64 * S) void gemv_q4_0_relay_kernel(const uint8_t *
     }
 }
 
+// ---- long rows: the row split over waves, one ordered fold at the end ----------
+// 4 rows per workgroup.  Wave 0 stages the activation pack into LDS in split
+// form; compute wave s owns iterations [s*IPW, s*IPW + IPW) of all 4 rows
+// (16 lanes per row, lane j: block 16*it + j) and loads only weights.  Terms
+// go to T[it][row][j] -- every store unconditional, the padding iterations
+// of the last wave included, so no weight load is sunk into a branch -- and
+// after one barrier lane r < 4 adds row r's terms in block order.
+template <int NB, int S>
+constexpr int long_ipw() { return (NB / 16 + S - 1) / S; }
+
+template <int NB, int S>
+constexpr size_t long_lds() { return (size_t)NB * 40 + (size_t)S * long_ipw<NB, S>() * 64 * sizeof(float); }
+
+template <int NB, int S, bool EARLY = true>
+__global__ __launch_bounds__(64 * (S + 1)) void gemv_q4_0_long_kernel(const uint8_t *__restrict__ w,
+                                                                    const uint8_t *xpack, float *__restrict__ y,
+                                                                    int rows)
+{
+    constexpr int ITERS = NB / 16, IPW = long_ipw<NB, S>();
+    static_assert(NB % 16 == 0 && NB % 2 == 0, "whole iterations; 16-byte aligned term area");
+    static_assert(!EARLY || NB <= 320, "the pack's loads are one batch");
+    extern __shared__ __align__(16) uint8_t lds[];
+    float *T = reinterpret_cast<float *>(lds + NB * 40);
+    const int wave = threadIdx.x >> 6;
+    if (wave == 0) {
+        stage_split_pack<EARLY>(xpack, lds, NB);
+        __syncthreads();  // the pack is whole
+        __syncthreads();  // every term is stored
+        return;
+    }
+    if constexpr (EARLY) __builtin_amdgcn_s_barrier();  // the pack's loads are issued
+    const int sw = wave - 1, lane = threadIdx.x & 63, j = lane & 15, rsub = lane >> 4;
+    const int row_raw = blockIdx.x * 4 + rsub;
+    const int row = row_raw < rows ? row_raw : rows - 1;  // tail rows recompute the last row
+    const size_t nblk = (size_t)rows * NB, base = (size_t)row * NB;
+    const uint4 *qs = reinterpret_cast<const uint4 *>(w);
+    const uint32_t *dw = reinterpret_cast<const uint32_t *>(w + nblk * 16);
+    uint4 wq[IPW];
+    uint32_t wd[IPW];
+#pragma unroll
+    for (int k = 0; k < IPW; ++k) {
+        int it = sw * IPW + k;
+        it = it < ITERS ? it : ITERS - 1;
+        const int b = it * 16 + j;
+        wq[k] = qs[base + b];
+        wd[k] = dw[(base + b) >> 1];
+    }
+    __syncthreads();
+    const uint4 *aq = reinterpret_cast<const uint4 *>(lds);
+    const float *ad = reinterpret_cast<const float *>(lds + NB * 32);
+    const int32_t *ac = reinterpret_cast<const int32_t *>(lds + NB * 36);
+#pragma unroll
+    for (int k = 0; k < IPW; ++k) {
+        int it = sw * IPW + k;
+        const int b = (it < ITERS ? it : ITERS - 1) * 16 + j;
+        const uint4 q = wq[k], lo = aq[2 * b], hi = aq[2 * b + 1];
+        const int32_t isum = q4_0_isum_split(q.x, q.y, q.z, q.w, lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w, ac[b]);
+        const uint32_t dbits = ((base + b) & 1) ? wd[k] >> 16 : wd[k] & 0xffffu;
+        T[((sw * IPW + k) * 4 + rsub) * 16 + j] = (float)isum * (f16_bits_to_f32(dbits) * ad[b]);
+    }
+    __syncthreads();
+    if (wave != 1 || lane >= 4) return;
+    const float4 *tv = reinterpret_cast<const float4 *>(T) + lane * 4;
+    float acc = 0.0f;
+#pragma unroll 6
+    for (int it = 0; it < ITERS; ++it) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 x = tv[it * 16 + q];
+            acc = acc + x.x;
+            acc = acc + x.y;
+            acc = acc + x.z;
+            acc = acc + x.w;
+        }
+    }
+    const int out = blockIdx.x * 4 + lane;
+    if (out < rows) y[out] = acc;
+}
+
 // ---- runtime block count (fold16) -----------------------------------------------
 
 template <int ITERS, int WAVES>
@@ -635,7 +829,7 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_0_any_kernel(const u
 {
     extern __shared__ __align__(16) uint8_t lds[];
     if (threadIdx.x < 64) {
-        stage_split_pack(xpack, lds, nb);
+        stage_split_pack<true>(xpack, lds, nb);
         __syncthreads();
         return;
     }
@@ -644,6 +838,7 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_0_any_kernel(const u
     const int row = row_raw < rows ? row_raw : rows - 1;
     const size_t base = (size_t)row * nb;
     RowRegs<ITERS> r;
+    __builtin_amdgcn_s_barrier();  // the pack's loads are issued
     load_row<ITERS>(r, w, (size_t)rows * nb, base, nb, j);
     __syncthreads();
     const float s = fold_row<ITERS>(r, lds, base, nb, j);
@@ -659,7 +854,7 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_0_geglu_any_kernel(c
 {
     extern __shared__ __align__(16) uint8_t lds[];
     if (threadIdx.x < 64) {
-        stage_split_pack(xpack, lds, nb);
+        stage_split_pack<true>(xpack, lds, nb);
         __syncthreads();
         return;
     }
@@ -668,6 +863,7 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_0_geglu_any_kernel(c
     const int row = row_raw < rows ? row_raw : rows - 1;
     const size_t nblk = (size_t)rows * nb, base = (size_t)row * nb;
     RowRegs<ITERS> rg, ru;
+    __builtin_amdgcn_s_barrier();  // the pack's loads are issued
     load_row<ITERS>(rg, wg, nblk, base, nb, j);
     load_row<ITERS>(ru, wu, nblk, base, nb, j);
     __syncthreads();
@@ -686,7 +882,7 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_0_qkv_any_kernel(con
 {
     extern __shared__ __align__(16) uint8_t lds[];
     if (threadIdx.x < 64) {
-        stage_split_pack(xpack, lds, nb);
+        stage_split_pack<true>(xpack, lds, nb);
         __syncthreads();
         return;
     }
@@ -696,6 +892,7 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_0_qkv_any_kernel(con
     const QkvSel m = qkv_select(wq, wk, wv, row_raw < total ? row_raw : total - 1, q_rows, kv_rows);
     const size_t base = (size_t)m.local * nb;
     RowRegs<ITERS> r;
+    __builtin_amdgcn_s_barrier();  // the pack's loads are issued
     load_row<ITERS>(r, m.w, (size_t)m.mrows * nb, base, nb, j);
     __syncthreads();
     const float s = fold_row<ITERS>(r, lds, base, nb, j);
@@ -785,7 +982,8 @@ inline int waves_for(int rows) { return rows >= 8192 ? 4 : (rows >= 2048 ? 2 : 1
 
 // Fixed-shape instances (the block counts of the Gemma-2-2B projections).
 constexpr int kFoldWaves = 4;   // fold16 compute waves per workgroup
-constexpr int kRelayS = 6;      // relay waves per 4 rows for 288-block rows
+constexpr int kRelayS = 6;      // relay waves per 4 rows for 288-block rows (gate/up pairs)
+constexpr int kLongS = 6;       // compute waves per 4 rows of the long-row kernel
 
 inline bool fold16_shape(int nb) { return nb == 64 || nb == 72; }
 inline bool relay_shape(int nb) { return nb == 288; }
@@ -825,9 +1023,9 @@ int launch_gemv_q4_0(mrml_hip_ctx *ctx, const void *w, const void *xpack, float 
         return check_launch(ctx, "gemv_q4_0_kernel");
     }
     if (relay_shape(nb)) {
-        hipLaunchKernelGGL((gemv_q4_0_relay_kernel<288, kRelayS, 1>), dim3((rows + 3) / 4), dim3(64 * kRelayS), 0,
-                           ctx->stream, (const uint8_t *)w, (const uint8_t *)w, (const uint8_t *)xpack, y, rows);
-        return check_launch(ctx, "gemv_q4_0_relay_kernel");
+        hipLaunchKernelGGL((gemv_q4_0_long_kernel<288, kLongS>), dim3((rows + 3) / 4), dim3(64 * (kLongS + 1)),
+                           (long_lds<288, kLongS>()), ctx->stream, (const uint8_t *)w, (const uint8_t *)xpack, y, rows);
+        return check_launch(ctx, "gemv_q4_0_long_kernel");
     }
     const int iters = (nb + 15) / 16;
     const int waves = waves_for(rows);
@@ -1001,10 +1199,7 @@ int launch_gemv_q4_0_qkv_x(mrml_hip_ctx *ctx, const void *wq, const void *wk, co
 bool resnorm_shape(int cols) { return fold16_shape(cols / 32) && cols % 32 == 0; }
 
 static size_t resnorm_lds(int nb) { return pack_lds(nb) + 64 * sizeof(float) + sizeof(mrml_xsum::Shared4); }
-static size_t geglu_resnorm_lds(int nb)
-{
-    return align_up(resnorm_lds(nb), 16) + (size_t)3 * 64 * kGegluResWaves * sizeof(float4);  // parked norm operands
-}
+
 
 int launch_geglu_resnorm(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *t, const float *w_post,
                          const float *h_in, float *h_out, const float *w_norm, float eps, void *act_pack, int32_t rows,
@@ -1017,8 +1212,8 @@ int launch_geglu_resnorm(mrml_hip_ctx *ctx, const void *wg, const void *wu, cons
     if (int rc = check_even(ctx, rows, nb)) return rc;
     MRML_FOLD16_NB(nb, {
         hipLaunchKernelGGL((gemv_q4_0_geglu_resnorm_kernel<NB>), dim3(rows / 64), dim3(64 * kGegluResWaves),
-                           geglu_resnorm_lds(NB), ctx->stream, (const uint8_t *)wg, (const uint8_t *)wu, t, w_post, h_in,
-                           h_out, w_norm, eps, (uint8_t *)act_pack, rows);
+                           geglu_resnorm_lds<NB>(), ctx->stream, (const uint8_t *)wg, (const uint8_t *)wu, t, w_post,
+                           h_in, h_out, w_norm, eps, (uint8_t *)act_pack, rows);
     });
     return check_launch(ctx, "gemv_q4_0_geglu_resnorm_kernel");
 }
