@@ -730,8 +730,69 @@ inline size_t norm_lds(int dim)
 
 bool norm_dim_ok(int dim) { return dim > 0 && dim % 32 == 0 && dim <= 4 * kMaxChunks * kNormMaxThreads; }
 
+// rms_norm by a group of 4 waves with K values per lane (exact_sum.h's group
+// form, the sum the fused residual + GeGLU runs beside its weight stream):
+// the same bits as rms_norm_kernel, for dim <= 256*K.  The pack goes through
+// LDS into the 8-lanes-per-block layout of emit_q8.
+constexpr int kGroupNormK = 9;
+
+__host__ __device__ constexpr size_t group_norm_head() { return (sizeof(mrml_xsum::GroupShared) + 16 + 15) / 16 * 16; }
+inline size_t group_norm_lds(int dim)
+{
+    return group_norm_head() + ((size_t)dim + 3) / 4 * 16 + (size_t)mrml_xsum::group_events(dim) * sizeof(float);
+}
+
+__global__ __launch_bounds__(256) void rms_norm_group_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                             float eps, float *__restrict__ out,
+                                                             uint8_t *__restrict__ pack, int dim)
+{
+    constexpr int K = kGroupNormK;
+    extern __shared__ __align__(16) uint8_t lds[];
+    auto *gs = reinterpret_cast<mrml_xsum::GroupShared *>(lds);
+    uint32_t *ctr = reinterpret_cast<uint32_t *>(lds + sizeof(mrml_xsum::GroupShared));
+    float *xn = reinterpret_cast<float *>(lds + group_norm_head());
+    float *evl = xn + (dim + 3) / 4 * 4;
+    const int wave = threadIdx.x >> 6, k0 = K * threadIdx.x;
+    const float *wp = w ? w : x;  // unconditional loads
+    float v[K], wv[K], sq[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        const int k = k0 + i < dim ? k0 + i : dim - 1;
+        v[i] = x[k];
+        wv[i] = wp[k];
+    }
+#pragma unroll
+    for (int i = 0; i < K; ++i) sq[i] = v[i] * v[i];
+    if (threadIdx.x == 0) *ctr = 0u;
+    __syncthreads();
+    mrml_xsum::GroupSync sync{ctr, 0u, 4u};
+    const float scale = rms_scale(mrml_xsum::group_seq_sum_nonneg<K>(sq, dim, wave, sync, *gs, evl), dim, eps);
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        float o = v[i] * scale;
+        if (w) o = o * wv[i];
+        if (k0 + i < dim) {
+            if (out) out[k0 + i] = o;
+            xn[k0 + i] = o;
+        }
+    }
+    if (!pack) return;
+    __syncthreads();
+    const int n4 = dim >> 2;
+    const float4 *x4 = reinterpret_cast<const float4 *>(xn);
+    for (int c0 = 0; c0 < n4; c0 += 256) {  // uniform
+        const int c = c0 + threadIdx.x;
+        emit_q8(x4[c < n4 ? c : n4 - 1], c, n4, pack, n4 >> 3);
+    }
+}
+
 int launch_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float eps, float *out, void *pack, int dim)
 {
+    if (dim <= 256 * kGroupNormK && dim % 4 == 0) {
+        hipLaunchKernelGGL(rms_norm_group_kernel, dim3(1), dim3(256), group_norm_lds(dim), ctx->stream, x, w, eps, out,
+                           (uint8_t *)pack, dim);
+        return check_launch(ctx, "rms_norm_group_kernel");
+    }
     if (norm_one_chunk(dim))
         hipLaunchKernelGGL(rms_norm_kernel<1>, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, x, w, eps,
                            out, (uint8_t *)pack, dim);

@@ -139,7 +139,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r0 = blockIdx.x * 32;
     const int g = blockIdx.y * kGemmWaves + wave;  // >= ngroups: computes on zeros, stores nothing
-    const int tl = lane & 31, h = lane >> 5, sh = 4 * h;
+    const int tl = lane & 31, h = lane >> 5;
     const uint32_t qs_bytes = (uint32_t)rows * nb * 16;
     // Loads past a row's last block read the next row or, past the end of a
     // buffer, zeros (buffer range check); such blocks are never folded.
