@@ -14,7 +14,7 @@
 //   o        = Wo * pack(attn)                             gemv_q4_0
 //   h += rms_norm(o, post_attn); xn = rms_norm(h, ffn)    residual_rms_norm -> pack
 //   act      = gelu(Wg xn) * (Wu xn)     -> Q8_0 pack      gemv_q4_0_geglu (emit)
-//   f        = Wd * pack(act)                              gemv_q4_0 (relay)
+//   f        = Wd * pack(act)                              gemv_q4_0 (long-row kernel)
 //   h += rms_norm(f, post_ffw); xn = rms_norm(h, next)    residual_rms_norm -> pack
 // then the tied LM head over pack(rms_norm(h, output_norm)) and argmax.
 
