@@ -741,38 +741,74 @@ __global__ __launch_bounds__(64 * S) void gemv_q4_0_relay_kernel(const uint8_t *
     }
 }
 
-// ---- long rows: the row split over waves, one ordered fold at the end ----------
+// ---- long rows: the row split over waves, the ordered fold pipelined ----------
 // 4 rows per workgroup.  Wave 0 stages the activation pack into LDS in split
-// form; compute wave s owns iterations [s*IPW, s*IPW + IPW) of all 4 rows
-// (16 lanes per row, lane j: block 16*it + j) and loads only weights.  Terms
-// go to T[it][row][j] -- every store unconditional, the padding iterations
-// of the last wave included, so no weight load is sunk into a branch -- and
-// after one barrier lane r < 4 adds row r's terms in block order.
+// form, then folds; compute wave s owns iterations it = s, s+S, s+2S, ... of
+// all 4 rows (16 lanes per row, lane j: block 16*it + j) and loads only
+// weights.  Its loads go out iteration-major across the waves, so the data,
+// and the terms, arrive roughly in block order.  Each wave stores the terms
+// of its round-k iteration to T[it][row][j] and then counts it in cnt[k];
+// wave 0's lanes r < 4 add row r's terms of a round, in block order, once all
+// of the round's waves have counted, so only the last round's adds remain
+// once the stream ends.  The waits are bounded (exact_sum.h's kSyncSpin
+// polls).
 template <int NB, int S>
 constexpr int long_ipw() { return (NB / 16 + S - 1) / S; }
 
 template <int NB, int S>
-constexpr size_t long_lds() { return (size_t)NB * 40 + (size_t)S * long_ipw<NB, S>() * 64 * sizeof(float); }
+constexpr size_t long_t_off() { return ((size_t)NB * 40 + 64 * sizeof(uint32_t) + 15) / 16 * 16; }
 
-template <int NB, int S, bool EARLY = true>
+template <int NB, int S>
+constexpr size_t long_lds() { return long_t_off<NB, S>() + (size_t)S * long_ipw<NB, S>() * 64 * sizeof(float); }
+
+template <int NB, int S>
 __global__ __launch_bounds__(64 * (S + 1)) void gemv_q4_0_long_kernel(const uint8_t *__restrict__ w,
                                                                     const uint8_t *xpack, float *__restrict__ y,
                                                                     int rows)
 {
     constexpr int ITERS = NB / 16, IPW = long_ipw<NB, S>();
-    static_assert(NB % 16 == 0 && NB % 2 == 0, "whole iterations; 16-byte aligned term area");
-    static_assert(!EARLY || NB <= 320, "the pack's loads are one batch");
+    static_assert(NB % 16 == 0 && NB <= kStageMax, "whole iterations; one staging batch");
+    static_assert(IPW <= 64, "one count per round");
     extern __shared__ __align__(16) uint8_t lds[];
-    float *T = reinterpret_cast<float *>(lds + NB * 40);
-    const int wave = threadIdx.x >> 6;
+    uint32_t *flag = reinterpret_cast<uint32_t *>(lds + NB * 40);  // cnt[k] of the text
+    float *T = reinterpret_cast<float *>(lds + long_t_off<NB, S>());
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (wave == 0) {
-        stage_split_pack<EARLY>(xpack, lds, NB);
+        flag[lane] = 0u;  // zero before the issue barrier inside the staging
+        stage_split_pack<true>(xpack, lds, NB);
         __syncthreads();  // the pack is whole
-        __syncthreads();  // every term is stored
+        if (lane >= 4) return;
+        const float4 *tv = reinterpret_cast<const float4 *>(T) + lane * 4;
+        float acc = 0.0f;
+#pragma unroll 1
+        for (int k = 0; k < IPW; ++k) {
+            const uint32_t want = (uint32_t)(ITERS - S * k < S ? ITERS - S * k : S);  // waves with a live iteration
+#pragma unroll 1
+            for (int i = 0; i < mrml_xsum::kSyncSpin; ++i) {
+                const uint32_t f = __hip_atomic_load(&flag[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                if (__builtin_amdgcn_readfirstlane(f) >= want) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+            asm volatile("" ::: "memory");
+            float4 v[4 * S];
+#pragma unroll
+            for (int q = 0; q < 4 * S; ++q) v[q] = tv[(S * k + (q >> 2)) * 16 + (q & 3)];
+#pragma unroll
+            for (int q = 0; q < 4 * S; ++q) {
+                if (S * k + (q >> 2) < ITERS) {  // uniform
+                    acc = acc + v[q].x;
+                    acc = acc + v[q].y;
+                    acc = acc + v[q].z;
+                    acc = acc + v[q].w;
+                }
+            }
+        }
+        const int out = blockIdx.x * 4 + lane;
+        if (out < rows) y[out] = acc;
         return;
     }
-    if constexpr (EARLY) __builtin_amdgcn_s_barrier();  // the pack's loads are issued
-    const int sw = wave - 1, lane = threadIdx.x & 63, j = lane & 15, rsub = lane >> 4;
+    __builtin_amdgcn_s_barrier();  // the pack's loads and the zeroed flags are in
+    const int sw = wave - 1, j = lane & 15, rsub = lane >> 4;
     const int row_raw = blockIdx.x * 4 + rsub;
     const int row = row_raw < rows ? row_raw : rows - 1;  // tail rows recompute the last row
     const size_t nblk = (size_t)rows * NB, base = (size_t)row * NB;
@@ -782,7 +818,7 @@ __global__ __launch_bounds__(64 * (S + 1)) void gemv_q4_0_long_kernel(const uint
     uint32_t wd[IPW];
 #pragma unroll
     for (int k = 0; k < IPW; ++k) {
-        int it = sw * IPW + k;
+        int it = sw + S * k;
         it = it < ITERS ? it : ITERS - 1;
         const int b = it * 16 + j;
         wq[k] = qs[base + b];
@@ -794,30 +830,18 @@ __global__ __launch_bounds__(64 * (S + 1)) void gemv_q4_0_long_kernel(const uint
     const int32_t *ac = reinterpret_cast<const int32_t *>(lds + NB * 36);
 #pragma unroll
     for (int k = 0; k < IPW; ++k) {
-        int it = sw * IPW + k;
+        const int it = sw + S * k;
         const int b = (it < ITERS ? it : ITERS - 1) * 16 + j;
         const uint4 q = wq[k], lo = aq[2 * b], hi = aq[2 * b + 1];
         const int32_t isum = q4_0_isum_split(q.x, q.y, q.z, q.w, lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w, ac[b]);
         const uint32_t dbits = ((base + b) & 1) ? wd[k] >> 16 : wd[k] & 0xffffu;
-        T[((sw * IPW + k) * 4 + rsub) * 16 + j] = (float)isum * (f16_bits_to_f32(dbits) * ad[b]);
+        // every store unconditional (padding iterations of the last waves
+        // included), so no weight load is sunk into a branch
+        T[((sw + S * k) * 4 + rsub) * 16 + j] = (float)isum * (f16_bits_to_f32(dbits) * ad[b]);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the terms are in LDS before the count
+        if (lane == 0 && it < ITERS)
+            __hip_atomic_fetch_add(&flag[k], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-    __syncthreads();
-    if (wave != 1 || lane >= 4) return;
-    const float4 *tv = reinterpret_cast<const float4 *>(T) + lane * 4;
-    float acc = 0.0f;
-#pragma unroll 6
-    for (int it = 0; it < ITERS; ++it) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float4 x = tv[it * 16 + q];
-            acc = acc + x.x;
-            acc = acc + x.y;
-            acc = acc + x.z;
-            acc = acc + x.w;
-        }
-    }
-    const int out = blockIdx.x * 4 + lane;
-    if (out < rows) y[out] = acc;
 }
 
 // ---- runtime block count (fold16) -----------------------------------------------
@@ -983,7 +1007,7 @@ inline int waves_for(int rows) { return rows >= 8192 ? 4 : (rows >= 2048 ? 2 : 1
 // Fixed-shape instances (the block counts of the Gemma-2-2B projections).
 constexpr int kFoldWaves = 4;   // fold16 compute waves per workgroup
 constexpr int kRelayS = 6;      // relay waves per 4 rows for 288-block rows (gate/up pairs)
-constexpr int kLongS = 6;       // compute waves per 4 rows of the long-row kernel
+constexpr int kLongS = 3;       // compute waves per 4 rows of the long-row kernel
 
 inline bool fold16_shape(int nb) { return nb == 64 || nb == 72; }
 inline bool relay_shape(int nb) { return nb == 288; }
