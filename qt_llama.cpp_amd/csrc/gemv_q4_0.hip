@@ -437,6 +437,80 @@ constexpr size_t geglu_lds(int waves)
     return (NB * 40 + 15) / 16 * 16 + (size_t)2 * 4 * waves * t_stride<NB>() * sizeof(float);
 }
 
+// Two chains of one lane (gate and up of a row), added in block order,
+// interleaved.
+template <int NB>
+__device__ __forceinline__ void fold_chain2(const float *T, int ca, int cb, float &sa, float &sb)
+{
+    const float4 *pa = reinterpret_cast<const float4 *>(T + ca * t_stride<NB>());
+    const float4 *pb = reinterpret_cast<const float4 *>(T + cb * t_stride<NB>());
+    float4 va[NB / 4], vb[NB / 4];
+#pragma unroll
+    for (int k = 0; k < NB / 4; ++k) {
+        va[k] = pa[k];
+        vb[k] = pb[k];
+    }
+    sa = 0.0f;
+    sb = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NB / 4; ++k) {
+        sa = sa + va[k].x;
+        sb = sb + vb[k].x;
+        sa = sa + va[k].y;
+        sb = sb + vb[k].y;
+        sa = sa + va[k].z;
+        sb = sb + vb[k].z;
+        sa = sa + va[k].w;
+        sb = sb + vb[k].w;
+    }
+}
+
+// Gate+up GeGLU with f32 output, rows spread evenly over the CUs: W compute
+// waves own R = 4W rows (W = 9: 36 rows, 256 workgroups for 9216 rows, one
+// per CU; 32-row workgroups would put two on 32 CUs, which then finish about
+// 2 us after the rest).  x is quantised in the kernel (kNQ staging waves);
+// lane r < R of the first compute wave adds both chains of row r.  Used
+// where act is wanted in f32 only: an FFN emits the Q8_0 pack from 32-row
+// workgroups instead, since forming the pack inside each down-projection
+// workgroup (576 of them) costs far more than the imbalance.
+template <int NB, int W>
+__global__ __launch_bounds__(64 * (W + kNQ)) void gemv_q4_0_geglu_f32_kernel(
+    const uint8_t *__restrict__ wg, const uint8_t *__restrict__ wu, const float *__restrict__ x,
+    float *__restrict__ act, int rows)
+{
+    constexpr int NS = kNQ, ITERS = (NB + 15) / 16, R = 4 * W;
+    static_assert(R <= 64, "one fold lane per row");
+    extern __shared__ __align__(16) uint8_t lds[];
+    float *T = reinterpret_cast<float *>(lds + (NB * 40 + 15) / 16 * 16);
+    const int wave = threadIdx.x >> 6;
+    if (wave < NS) {
+        quantize_into_lds<NB, kNQ>(x, lds, wave);
+        __syncthreads();  // the pack is whole
+        __syncthreads();  // every term is stored
+        return;
+    }
+    const int lane = threadIdx.x & 63, j = lane & 15;
+    const int rl = (wave - NS) * 4 + (lane >> 4);
+    const int row_raw = blockIdx.x * R + rl;
+    const int row = row_raw < rows ? row_raw : rows - 1;  // tail rows recompute the last row
+    const size_t nblk = (size_t)rows * NB, base = (size_t)row * NB;
+    RowRegs<ITERS> rg, ru;
+    __builtin_amdgcn_s_barrier();  // x's loads are issued
+    load_row<ITERS>(rg, wg, nblk, base, NB, j);
+    load_row<ITERS>(ru, wu, nblk, base, NB, j);
+    __syncthreads();
+    store_terms2<NB, ITERS>(rg, ru, lds, base, j, T, rl, R + rl);
+    __syncthreads();
+    if (wave != NS) return;
+    float g, u;
+    fold_chain2<NB>(T, lane < R ? lane : 0, lane < R ? R + lane : R, g, u);
+    const int out = blockIdx.x * R + lane;
+    if (lane < R && out < rows) act[out] = gelu_tanh(g) * u;
+}
+
+template <int NB, int W>
+constexpr size_t geglu_f32_lds() { return (NB * 40 + 15) / 16 * 16 + (size_t)2 * 4 * W * t_stride<NB>() * sizeof(float); }
+
 // ---- the Gemma-2 sandwich residual ahead of the rows ---------------------------
 // Each workgroup first forms h_out = h_in + rms_norm(t, w_post) and
 // the Q8_0 pack of rms_norm(h_out, w_norm) in its own LDS (norm_block.h;
@@ -1136,11 +1210,27 @@ int launch_gemv_q4_0_geglu_emit(mrml_hip_ctx *ctx, const void *wg, const void *w
     return launch_quantize_q8_0(ctx, out, nullptr, act_pack, rows);
 }
 
+// f32 in, f32 out on the balanced kernel (36 rows per workgroup).
+constexpr int kGegluF32W = 9;
+
+static int launch_geglu_f32(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *x, float *act,
+                            int32_t rows, int nb)
+{
+    constexpr int R = 4 * kGegluF32W;
+    MRML_FOLD16_NB(nb, {
+        hipLaunchKernelGGL((gemv_q4_0_geglu_f32_kernel<NB, kGegluF32W>), dim3((rows + R - 1) / R),
+                           dim3(64 * (kGegluF32W + kNQ)), (geglu_f32_lds<NB, kGegluF32W>()), ctx->stream,
+                           (const uint8_t *)wg, (const uint8_t *)wu, x, act, rows);
+    });
+    return check_launch(ctx, "gemv_q4_0_geglu_f32_kernel");
+}
+
 int launch_gemv_q4_0_geglu_x(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *x, float *act,
                              void *act_pack, int32_t rows, int32_t cols)
 {
     const int nb = cols / 32;
     if (int rc = check_even(ctx, rows, nb)) return rc;
+    if (fold16_shape(nb) && !act_pack) return launch_geglu_f32(ctx, wg, wu, x, act, rows, nb);
     if (fold16_shape(nb) && (!act_pack || rows % 32 == 0)) {
         if (act_pack) {
             MRML_FOLD16_NB(nb, {
