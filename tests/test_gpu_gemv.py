@@ -136,9 +136,10 @@ def test_gemv_q4_0_closed_forms(backend, dev, orc):
     assert np.all(got[0::2] == up) and np.all(got[1::2] == lo)
 
 
-def test_gemv_q4_0_geglu(backend, dev, orc, synth):
-    rows, cols = 9216, 2304
-    rng = synth.rng_for(5000)
+@pytest.mark.parametrize("rows,cols", [(9216, 2304), (100, 2048), (37, 2304)])
+def test_gemv_q4_0_geglu(backend, dev, orc, synth, rows, cols):
+    """f32 in, f32 out (36 rows per workgroup): full and ragged last workgroups."""
+    rng = synth.rng_for(5000 + rows)
     wg = synth.q4_0_matrix(rng, rows, cols)
     wu = synth.q4_0_matrix(rng, rows, cols)
     x = synth.rms_normalised(synth.normal_vector(rng, cols))
