@@ -79,6 +79,7 @@ Q4_SHAPES = [
     (2304, 2048),    # output projection
     (73, 64),        # ops_test.rs:116-140 shape
     (1, 64), (3, 256), (5, 512), (2, 96), (4, 32),            # ragged rows, tail blocks
+    (7, 9216),       # long rows, partial last 4-row workgroup
 ]
 
 
