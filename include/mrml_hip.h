@@ -51,7 +51,10 @@ enum {
     MRML_HIP_E_ALLOC = -2,       /* device or host allocation failed */
     MRML_HIP_E_HIP = -3,         /* a HIP runtime call failed (message has the HIP error) */
     MRML_HIP_E_UNSUPPORTED = -4, /* shape or format this build does not implement */
-    MRML_HIP_E_NODEVICE = -5     /* no gfx950 device at that index */
+    MRML_HIP_E_NODEVICE = -5,    /* no gfx950 device at that index */
+    MRML_HIP_E_FORMAT = -6,      /* malformed or unsupported GGUF file */
+    MRML_HIP_E_IO = -7,          /* a file could not be opened or read */
+    MRML_HIP_E_NOTFOUND = -8     /* no GGUF tensor or metadata key of that name */
 };
 
 /* GGUF tensor type ids (crates/mrml-tensor/src/types.rs:7-30, gguf.rs:121-133) */
@@ -317,6 +320,52 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, int32_t *d_s
                          int32_t hist_cap, const int32_t *d_prompt, int32_t prompt_len);
 /* The model's own residual stream h (f32[dim]) and logits (f32[vocab]). */
 int mrml_hip_gemma2_activations(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, float **d_h, float **d_logits);
+
+/* ---- GGUF container reader (host only; GgufFile, crates/mrml-tensor/src/
+ * gguf.rs:78-184) -----------------------------------------------------------
+ * Version 2 and 3 files.  Tensors and metadata keys are indexed in key-byte
+ * order, a repeated name keeping its last entry (the reference's OrderedMap,
+ * crates/mrml-runtime/src/map.rs:38-49).  Tensor bytes are read on demand,
+ * like GgufFile::read_tensor_bytes.  Errors are MRML_HIP_E_FORMAT (the
+ * reference's "Invalid GGUF magic number", "Unsupported GGUF version",
+ * "Unsupported GGUF dtype ID", "Unknown GGUF value type ID", non-UTF-8
+ * strings, truncation), MRML_HIP_E_IO and MRML_HIP_E_NOTFOUND; the message of
+ * the calling thread's last failure is mrml_gguf_last_error(). */
+typedef struct mrml_gguf mrml_gguf;
+
+typedef struct {
+    const char *name;    /* valid until mrml_gguf_close */
+    int32_t type;        /* GGUF type id: 0 F32, 1 F16, 2 Q4_0, 3 Q4_1, 8 Q8_0, 12 Q4_K, 13 Q5_K, 14 Q6_K, 16 IQ4_XS, 30 BF16 */
+    int32_t n_dims;      /* min(stored n_dims, 4) */
+    uint64_t dims[4];    /* ggml order (dims[0] = elements per row); unused dims are 1 */
+    uint64_t offset;     /* from the data section start */
+    uint64_t size_bytes; /* numel / block size * block bytes (gguf.rs:146-147) */
+} mrml_gguf_tensor_info;
+
+/* GgufFile::open (gguf.rs:80-171): parses the header, metadata and tensor
+ * directory. */
+int mrml_gguf_open(const char *path, mrml_gguf **out);
+int mrml_gguf_close(mrml_gguf *g);
+const char *mrml_gguf_last_error(void);
+/* version, data section offset (gguf.rs:153-163), tensor and key counts; each
+ * output nullable. */
+int mrml_gguf_header(const mrml_gguf *g, uint32_t *version, uint64_t *data_offset, int64_t *n_tensors,
+                     int64_t *n_meta);
+int mrml_gguf_tensor(const mrml_gguf *g, int64_t index, mrml_gguf_tensor_info *info);
+/* GgufFile::tensors.get(name) */
+int mrml_gguf_find_tensor(const mrml_gguf *g, const char *name, int64_t *index);
+/* GgufFile::read_tensor_bytes (gguf.rs:173-183) into a host buffer of at
+ * least size_bytes. */
+int mrml_gguf_read_tensor(const mrml_gguf *g, int64_t index, void *h_dst, uint64_t dst_bytes);
+/* Metadata key `index` in key order and its value type id (0..12). */
+int mrml_gguf_meta_key(const mrml_gguf *g, int64_t index, const char **key, int32_t *type);
+/* GgufValue::as_u32 / as_f32 / as_str (gguf.rs:25-53) of metadata `key`:
+ * MRML_HIP_E_INVALID when the value has no such reading. */
+int mrml_gguf_meta_u32(const mrml_gguf *g, const char *key, uint32_t *out);
+int mrml_gguf_meta_f32(const mrml_gguf *g, const char *key, float *out);
+int mrml_gguf_meta_str(const mrml_gguf *g, const char *key, const char **out, uint64_t *len);
+/* GgufValue::as_array (gguf.rs:55-60): item type and length. */
+int mrml_gguf_meta_array(const mrml_gguf *g, const char *key, int32_t *item_type, uint64_t *len);
 
 #ifdef __cplusplus
 }

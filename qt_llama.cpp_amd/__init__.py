@@ -47,6 +47,9 @@ _STATUS = {
     -3: "HIP runtime error",
     -4: "unsupported",
     -5: "no gfx950 device",
+    -6: "malformed GGUF file",
+    -7: "file I/O error",
+    -8: "not found",
 }
 
 

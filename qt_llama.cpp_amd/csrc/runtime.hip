@@ -114,6 +114,9 @@ const char *mrml_hip_status_string(int status)
     case MRML_HIP_E_HIP: return "HIP runtime error";
     case MRML_HIP_E_UNSUPPORTED: return "unsupported";
     case MRML_HIP_E_NODEVICE: return "no gfx950 device";
+    case MRML_HIP_E_FORMAT: return "malformed GGUF file";
+    case MRML_HIP_E_IO: return "file I/O error";
+    case MRML_HIP_E_NOTFOUND: return "not found";
     default: return "unknown status";
     }
 }

@@ -54,6 +54,13 @@ def synth():
 
 
 @pytest.fixture(scope="session")
+def gguf():
+    load_backend()
+    import qt_llama_cpp_amd.gguf as g
+    return g
+
+
+@pytest.fixture(scope="session")
 def dev(backend):
     """One context for the whole GPU session (GPU tests run in one process)."""
     if backend.device_count() < 1:

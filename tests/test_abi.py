@@ -15,7 +15,7 @@ ROOT = Path(__file__).resolve().parents[1]
 def declared_functions() -> list[str]:
     text = (ROOT / "include" / "mrml_hip.h").read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(mrml_hip_[a-z0-9_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(mrml_(?:hip|gguf)_[a-z0-9_]+)\s*\(", text)))
 
 
 def test_header_declares_the_surface():
@@ -30,7 +30,8 @@ def test_library_exports_every_declared_symbol(backend):
     missing = [n for n in declared_functions() if not hasattr(lib, n)]
     assert not missing, missing
     # and the Python mirror binds exactly the declared surface
-    assert sorted(backend.exported_symbols()) == declared_functions()
+    import qt_llama_cpp_amd.gguf as gguf
+    assert sorted(backend.exported_symbols() + gguf.exported_symbols()) == declared_functions()
 
 
 def test_library_is_gfx950_only():

@@ -323,6 +323,28 @@ def test_gemma2_tiny_greedy(backend, dev, orc, synth, tie_q8):
     assert np.array_equal(kc, o.k_cache) and np.array_equal(vc, o.v_cache)
 
 
+def test_gemma2_tiny_from_gguf(backend, dev, orc, synth, gguf, tmp_path):
+    """Weights written as a GGUF file and loaded back through the C-ABI reader
+    (token_embd / blk.N.* names) drive the same token step: tokens, logits and
+    caches bit-identical to the in-memory weights, and tokens equal to the
+    oracle's."""
+    model = synth.gemma2_model(TINY, seed=14)
+    path = tmp_path / "tiny_gemma2.gguf"
+    gguf.write_gemma2(path, model)
+    loaded = gguf.read_gemma2(path)
+    prompt = synth.prompt_tokens(4, TINY["vocab"], seed=6)
+    n_dec = 12
+    print(f"\n[gguf] {path.stat().st_size} bytes, {len(loaded['layers'])} layers", flush=True)
+    hist, lg, kc, vc = run_gpu_decode(backend, dev, loaded, prompt, n_dec)
+    hist0, lg0, kc0, vc0 = run_gpu_decode(backend, dev, model, prompt, n_dec)
+    assert np.array_equal(hist, hist0)
+    for s in range(len(lg)):
+        assert_bits(lg[s], lg0[s], f"logits at step {s}")
+    assert np.array_equal(kc, kc0) and np.array_equal(vc, vc0)
+    want, _, _ = run_oracle_decode(orc, model, prompt, n_dec)
+    assert_same_tokens(hist, want)
+
+
 def test_gemma2_tiny_ring_cache(backend, dev, orc, synth):
     """Past the cache capacity the KV cache is a ring (kernels.rs:1307-1313)
     and attention reads the last `capacity` positions (a sliding window,
