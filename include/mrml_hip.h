@@ -318,6 +318,18 @@ int mrml_hip_gemma2_destroy(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model);
 int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, int32_t *d_state, uint16_t *d_k_cache,
                          uint16_t *d_v_cache, float *d_logits, int32_t *d_argmax, int32_t *d_hist,
                          int32_t hist_cap, const int32_t *d_prompt, int32_t prompt_len);
+/* Prefill (prefill_cuda, model.rs:2395-2638): the token steps of positions
+ * pos0 .. pos0+n_tokens-1 for the tokens d_tokens[0..n_tokens) (device
+ * int32), in chunks of up to 128 tokens whose seven projections per layer run
+ * as batched Q4_0 products on MFMA (mrml_hip_gemm_q4_0).  Every op keeps the
+ * token step's arithmetic, so the caches end bit-identical to n_tokens calls
+ * of mrml_hip_gemma2_step; the last token's logits go to d_logits (nullable:
+ * the model's own buffer) and its greedy argmax to d_argmax (nullable).
+ * pos0 + n_tokens <= ctx_len (no ring wrap).  The first call allocates the
+ * chunk buffers (freed by mrml_hip_gemma2_destroy).  Not capturable. */
+int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, const int32_t *d_tokens, int32_t n_tokens,
+                            int32_t pos0, uint16_t *d_k_cache, uint16_t *d_v_cache, float *d_logits,
+                            int32_t *d_argmax);
 /* The model's own residual stream h (f32[dim]) and logits (f32[vocab]). */
 int mrml_hip_gemma2_activations(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, float **d_h, float **d_logits);
 

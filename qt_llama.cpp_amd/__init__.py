@@ -152,6 +152,7 @@ _SIGNATURES = {
     "mrml_hip_gemma2_destroy": [_P, _P],
     "mrml_hip_gemma2_step": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I],
     "mrml_hip_gemma2_activations": [_P, _P, ctypes.POINTER(_P), ctypes.POINTER(_P)],
+    "mrml_hip_gemma2_prefill": [_P, _P, _P, _I, _I, _P, _P, _P, _P],
 }
 _RESTYPE = {
     "mrml_hip_last_error": ctypes.c_char_p,
@@ -510,6 +511,13 @@ class Gemma2Model:
         self.dev._check(self.dev.lib.mrml_hip_gemma2_step(self.dev.ctx, self.handle, _ptr(state), _ptr(k_cache),
                                                           _ptr(v_cache), _ptr(logits), _ptr(argmax), _ptr(hist),
                                                           hist_cap, _ptr(prompt), prompt_len))
+
+    def prefill(self, tokens, n_tokens: int, pos0: int, k_cache, v_cache, logits=None, argmax=None) -> None:
+        """Enqueue the prefill of n_tokens device tokens from position pos0 (prefill_cuda,
+        model.rs:2395-2638); see mrml_hip_gemma2_prefill."""
+        self.dev._check(self.dev.lib.mrml_hip_gemma2_prefill(self.dev.ctx, self.handle, _ptr(tokens), n_tokens, pos0,
+                                                             _ptr(k_cache), _ptr(v_cache), _ptr(logits),
+                                                             _ptr(argmax)))
 
     def activations(self) -> tuple[int, int]:
         h, lg = ctypes.c_void_p(), ctypes.c_void_p()

@@ -18,6 +18,7 @@
 //   h += rms_norm(f, post_ffw); xn = rms_norm(h, next)    residual_rms_norm -> pack
 // then the tied LM head over pack(rms_norm(h, output_norm)) and argmax.
 
+#include <algorithm>
 #include <cmath>
 #include <new>
 #include <vector>
@@ -33,9 +34,18 @@ struct mrml_hip_gemma2 {
     void *arena = nullptr;  // activations, packs, partials (one allocation)
     float *h = nullptr, *qkv = nullptr, *o = nullptr, *f = nullptr, *logits = nullptr;
     float *h2 = nullptr;  // the residual's other buffer when the residual runs inside the matvecs
+    float *act = nullptr;  // f32 GeGLU output of the unfused path (never the context workspace, which
+                           // may be reallocated under a captured graph)
     uint8_t *xpack = nullptr, *attn_pack = nullptr, *act_pack = nullptr;
     void *attn_part = nullptr, *argmax_scratch = nullptr;
     float *rope_table = nullptr;  // [ctx_len][head_dim/2] (cos, sin) from the host libm
+    // prefill chunk buffers, allocated on the first prefill call: per token
+    // rows of h, xn, q, k, v, stacked q|k|v, attention output, o, gate, up,
+    // act and f, plus one GEMM pack
+    void *pf_arena = nullptr;
+    float *pf_h = nullptr, *pf_xn = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_qkv = nullptr,
+          *pf_attn = nullptr, *pf_o = nullptr, *pf_g = nullptr, *pf_u = nullptr, *pf_act = nullptr, *pf_f = nullptr;
+    void *pf_gpack = nullptr;
 };
 
 using namespace mrml;
@@ -180,7 +190,7 @@ int mrml_hip_gemma2_create(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config *cfg,
         return at;
     };
     const size_t o_h = take(c.dim * 4), o_h2 = take(c.dim * 4), o_qkv = take((qd + 2 * kvd) * 4), o_o = take(c.dim * 4),
-                 o_f = take(c.dim * 4), o_logits = take((size_t)c.vocab * 4),
+                 o_f = take(c.dim * 4), o_act = take((size_t)c.ffn_dim * 4), o_logits = take((size_t)c.vocab * 4),
                  o_xpack = take(act_pack_bytes((int)(in_max / 32))), o_apack = take(act_pack_bytes((int)(qd / 32))),
                  o_actpack = take(act_pack_bytes(c.ffn_dim / 32)),
                  o_part = take(attn_scratch_bytes(c.n_heads, c.ctx_len)),
@@ -197,6 +207,7 @@ int mrml_hip_gemma2_create(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config *cfg,
     m->qkv = (float *)(base + o_qkv);
     m->o = (float *)(base + o_o);
     m->f = (float *)(base + o_f);
+    m->act = (float *)(base + o_act);
     m->logits = (float *)(base + o_logits);
     m->xpack = base + o_xpack;
     m->attn_pack = base + o_apack;
@@ -219,6 +230,7 @@ int mrml_hip_gemma2_destroy(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m)
     if (!m) return MRML_HIP_OK;
     hipError_t e = hipStreamSynchronize(ctx->stream);
     (void)hipFree(m->arena);
+    if (m->pf_arena) (void)hipFree(m->pf_arena);
     delete m;
     return e == hipSuccess ? MRML_HIP_OK : hip_fail(ctx, e, "gemma2_destroy");
 }
@@ -276,7 +288,7 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
         } else {
             STEP(launch_residual_rms_norm(ctx, m->o, L.post_attn_norm, hA, hA, L.ffn_norm, c.eps, nullptr, m->xpack,
                                           c.dim));
-            STEP(launch_gemv_q4_0_geglu_emit(ctx, L.w_gate, L.w_up, m->xpack, nullptr, m->act_pack, c.ffn_dim,
+            STEP(launch_gemv_q4_0_geglu_emit(ctx, L.w_gate, L.w_up, m->xpack, m->act, m->act_pack, c.ffn_dim,
                                              c.dim));
         }
         STEP(launch_gemv_q4_0(ctx, L.w_down, m->act_pack, m->f, c.dim, c.ffn_dim));
@@ -293,6 +305,157 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
         STEP(launch_gemv_q8_0(ctx, m->tok_embd, m->xpack, logits, c.vocab, c.dim, 0));
     STEP(launch_argmax_step(ctx, logits, c.vocab, d_argmax, m->argmax_scratch, d_state, d_hist, hist_cap, d_prompt,
                             prompt_len));
+#undef STEP
+    return MRML_HIP_OK;
+}
+
+// ---- prefill through the batched product ---------------------------------------
+
+namespace {
+
+constexpr int kPrefillChunk = 128;  // tokens per chunk (prefill_cuda's tile, model.rs:2395-2638)
+
+// act = gelu_tanh(g) * u per element: the GeGLU epilogue of the matvec
+// kernels, so each act value has the bits the token step gives it.
+__global__ void geglu_rows_kernel(const float *__restrict__ g, const float *__restrict__ u, float *__restrict__ act,
+                                  int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) act[i] = gelu_tanh(g[i]) * u[i];
+}
+
+int prefill_buffers(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m)
+{
+    if (m->pf_arena) return MRML_HIP_OK;
+    const mrml_hip_gemma2_config &c = m->cfg;
+    const size_t M = kPrefillChunk, qd = (size_t)c.n_heads * c.head_dim, kvd = (size_t)c.n_kv_heads * c.head_dim;
+    const size_t widest = std::max<size_t>(std::max<size_t>(qd, c.dim), c.ffn_dim);
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off = align_up(off + bytes, 256);
+        return at;
+    };
+    const size_t o_h = take(M * c.dim * 4), o_xn = take(M * c.dim * 4), o_q = take(M * qd * 4),
+                 o_k = take(M * kvd * 4), o_v = take(M * kvd * 4), o_qkv = take(M * (qd + 2 * kvd) * 4),
+                 o_attn = take(M * qd * 4), o_o = take(M * c.dim * 4), o_g = take(M * c.ffn_dim * 4),
+                 o_u = take(M * c.ffn_dim * 4), o_act = take(M * c.ffn_dim * 4), o_f = take(M * c.dim * 4),
+                 o_gp = take(gemm_pack_bytes((int32_t)widest, (int32_t)M));
+    hipError_t e = hipMalloc(&m->pf_arena, off);
+    if (e != hipSuccess) {
+        m->pf_arena = nullptr;
+        return fail(ctx, MRML_HIP_E_ALLOC, "gemma2_prefill: hipMalloc(%zu): %s", off, hipGetErrorString(e));
+    }
+    uint8_t *b = (uint8_t *)m->pf_arena;
+    m->pf_h = (float *)(b + o_h), m->pf_xn = (float *)(b + o_xn), m->pf_q = (float *)(b + o_q);
+    m->pf_k = (float *)(b + o_k), m->pf_v = (float *)(b + o_v), m->pf_qkv = (float *)(b + o_qkv);
+    m->pf_attn = (float *)(b + o_attn), m->pf_o = (float *)(b + o_o), m->pf_g = (float *)(b + o_g);
+    m->pf_u = (float *)(b + o_u), m->pf_act = (float *)(b + o_act), m->pf_f = (float *)(b + o_f);
+    m->pf_gpack = b + o_gp;
+    return MRML_HIP_OK;
+}
+
+// Q8_0 of n rows of `cols` f32 values as a GEMM pack, then y = W * x for every row.
+int gemm_rows(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const void *w, const float *x, float *y, int rows, int cols, int n)
+{
+    if (int rc = launch_gemm_pack_quantize(ctx, x, m->pf_gpack, cols, n)) return rc;
+    return launch_gemm_q4_0(ctx, w, m->pf_gpack, y, rows, cols, n);
+}
+
+}  // namespace
+
+int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t *d_tokens, int32_t n_tokens,
+                            int32_t pos0, uint16_t *d_k_cache, uint16_t *d_v_cache, float *d_logits, int32_t *d_argmax)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, m && d_tokens && d_k_cache && d_v_cache, "gemma2_prefill: null argument");
+    const mrml_hip_gemma2_config &c = m->cfg;
+    REQUIRE(ctx, n_tokens > 0 && pos0 >= 0 && (int64_t)pos0 + n_tokens <= c.ctx_len,
+            "gemma2_prefill: positions %d..%lld must lie inside the cache of %d (no ring wrap)", pos0,
+            (long long)pos0 + n_tokens - 1, c.ctx_len);
+    REQUIRE(ctx, (((uintptr_t)d_k_cache | (uintptr_t)d_v_cache | (uintptr_t)d_logits) & 15) == 0,
+            "gemma2_prefill: caches and logits must be 16-byte aligned");
+    const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim, qkvd = qd + 2 * kvd;
+    if (!(gemm_shape_ok(qd, c.dim, kPrefillChunk) && gemm_shape_ok(kvd, c.dim, kPrefillChunk) &&
+          gemm_shape_ok(c.dim, qd, kPrefillChunk) && gemm_shape_ok(c.ffn_dim, c.dim, kPrefillChunk) &&
+          gemm_shape_ok(c.dim, c.ffn_dim, kPrefillChunk)))
+        return fail(ctx, MRML_HIP_E_UNSUPPORTED, "gemma2_prefill: a projection's shape does not fit the batched product");
+    if (int rc = prefill_buffers(ctx, m)) return rc;
+    const size_t layer_cache = (size_t)c.ctx_len * kvd;
+    const float emb_scale = sqrtf((float)c.dim);
+    int rc;
+#define STEP(call)                      \
+    do {                                \
+        if ((rc = (call)) != 0) return rc; \
+    } while (0)
+#define HIP_STEP(call)                                  \
+    do {                                                \
+        const hipError_t e_ = (call);                   \
+        if (e_ != hipSuccess) return hip_fail(ctx, e_, #call); \
+    } while (0)
+    for (int t0 = 0; t0 < n_tokens; t0 += kPrefillChunk) {
+        const int n = std::min(kPrefillChunk, n_tokens - t0), p0 = pos0 + t0;
+        float *h = m->pf_h, *xn = m->pf_xn;
+        for (int i = 0; i < n; ++i)
+            STEP(launch_embedding(ctx, m->tok_embd, c.tie_type, d_tokens + t0 + i, 0, emb_scale, h + (size_t)i * c.dim,
+                                  m->layers[0].attn_norm, c.eps, xn + (size_t)i * c.dim, nullptr, c.dim, c.vocab));
+        for (int l = 0; l < c.n_layers; ++l) {
+            const mrml_hip_gemma2_layer &L = m->layers[l];
+            uint16_t *kc = d_k_cache + (size_t)l * layer_cache, *vc = d_v_cache + (size_t)l * layer_cache;
+            const float *next_norm = l + 1 < c.n_layers ? m->layers[l + 1].attn_norm : m->output_norm;
+            // q, k, v of the chunk, stacked per token as the token step's q|k|v
+            STEP(launch_gemm_pack_quantize(ctx, xn, m->pf_gpack, c.dim, n));
+            STEP(launch_gemm_q4_0(ctx, L.wq, m->pf_gpack, m->pf_q, qd, c.dim, n));
+            STEP(launch_gemm_q4_0(ctx, L.wk, m->pf_gpack, m->pf_k, kvd, c.dim, n));
+            STEP(launch_gemm_q4_0(ctx, L.wv, m->pf_gpack, m->pf_v, kvd, c.dim, n));
+            const size_t row = (size_t)qkvd * 4;
+            HIP_STEP(hipMemcpy2DAsync(m->pf_qkv, row, m->pf_q, (size_t)qd * 4, (size_t)qd * 4, n,
+                                      hipMemcpyDeviceToDevice, ctx->stream));
+            HIP_STEP(hipMemcpy2DAsync(m->pf_qkv + qd, row, m->pf_k, (size_t)kvd * 4, (size_t)kvd * 4, n,
+                                      hipMemcpyDeviceToDevice, ctx->stream));
+            HIP_STEP(hipMemcpy2DAsync(m->pf_qkv + qd + kvd, row, m->pf_v, (size_t)kvd * 4, (size_t)kvd * 4, n,
+                                      hipMemcpyDeviceToDevice, ctx->stream));
+            // every token's rotated k and v enter the cache before any token
+            // attends; token i then reads positions <= p0 + i only
+            for (int i = 0; i < n; ++i)
+                STEP(launch_rope_kv_f16(ctx, m->pf_qkv + (size_t)i * qkvd, kc, vc, nullptr, p0 + i, c.n_heads,
+                                        c.n_kv_heads, c.head_dim, c.rope_base, 1.0f, c.ctx_len, m->rope_table,
+                                        c.ctx_len));
+            for (int i = 0; i < n; ++i)
+                STEP(launch_attn_decode_f16(ctx, m->pf_qkv + (size_t)i * qkvd, kc, vc, m->pf_attn + (size_t)i * qd,
+                                            nullptr, nullptr, p0 + i, c.n_heads, c.n_kv_heads, c.attn_scale,
+                                            c.ctx_len, m->attn_part));
+            STEP(gemm_rows(ctx, m, L.wo, m->pf_attn, m->pf_o, c.dim, qd, n));
+            for (int i = 0; i < n; ++i) {
+                float *hi = h + (size_t)i * c.dim;
+                STEP(launch_residual_rms_norm(ctx, m->pf_o + (size_t)i * c.dim, L.post_attn_norm, hi, hi, L.ffn_norm,
+                                              c.eps, xn + (size_t)i * c.dim, nullptr, c.dim));
+            }
+            STEP(launch_gemm_pack_quantize(ctx, xn, m->pf_gpack, c.dim, n));
+            STEP(launch_gemm_q4_0(ctx, L.w_gate, m->pf_gpack, m->pf_g, c.ffn_dim, c.dim, n));
+            STEP(launch_gemm_q4_0(ctx, L.w_up, m->pf_gpack, m->pf_u, c.ffn_dim, c.dim, n));
+            const int nact = n * c.ffn_dim;
+            hipLaunchKernelGGL(geglu_rows_kernel, dim3((nact + 255) / 256), dim3(256), 0, ctx->stream, m->pf_g,
+                               m->pf_u, m->pf_act, nact);
+            STEP(check_launch(ctx, "geglu_rows_kernel"));
+            STEP(gemm_rows(ctx, m, L.w_down, m->pf_act, m->pf_f, c.dim, c.ffn_dim, n));
+            for (int i = 0; i < n; ++i) {
+                float *hi = h + (size_t)i * c.dim;
+                STEP(launch_residual_rms_norm(ctx, m->pf_f + (size_t)i * c.dim, L.post_ffw_norm, hi, hi, next_norm,
+                                              c.eps, xn + (size_t)i * c.dim, nullptr, c.dim));
+            }
+        }
+        if (t0 + n < n_tokens) continue;
+        // the last token's logits and greedy pick (the LM head of its token step)
+        STEP(launch_quantize_q8_0(ctx, xn + (size_t)(n - 1) * c.dim, nullptr, m->xpack, c.dim));
+        float *logits = d_logits ? d_logits : m->logits;
+        if (c.tie_type == MRML_HIP_Q4_0)
+            STEP(launch_gemv_q4_0(ctx, m->tok_embd, m->xpack, logits, c.vocab, c.dim));
+        else
+            STEP(launch_gemv_q8_0(ctx, m->tok_embd, m->xpack, logits, c.vocab, c.dim, 0));
+        if (d_argmax) STEP(launch_argmax_f32(ctx, logits, c.vocab, d_argmax));
+    }
+#undef HIP_STEP
 #undef STEP
     return MRML_HIP_OK;
 }

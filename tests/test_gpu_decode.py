@@ -345,6 +345,69 @@ def test_gemma2_tiny_from_gguf(backend, dev, orc, synth, gguf, tmp_path):
     assert_same_tokens(hist, want)
 
 
+def run_gpu_prefill_decode(backend, dev, model, prompt, n_decode, splits):
+    """Prefill `prompt` through mrml_hip_gemma2_prefill (in calls of the given
+    sizes), then decode greedily with the token step."""
+    m = backend.Gemma2Model.from_host(dev, model)
+    c = model["cfg"]
+    P, total = len(prompt), len(prompt) + n_decode
+    kc = backend.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    vc = backend.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    logits = backend.HipBuffer.alloc(dev, c["vocab"])
+    am = backend.HipBuffer.from_host(dev, np.array([-1], np.int32))
+    toks = backend.HipBuffer.from_host(dev, np.asarray(prompt, np.int32))
+    pos = 0
+    for n in splits:
+        m.prefill(toks.ptr + 4 * pos, n, pos, kc, vc, logits=logits, argmax=am)
+        pos += n
+    assert pos == P
+    dev.sync()
+    first, lg_last = int(am.numpy()[0]), logits.numpy()
+    state = backend.HipBuffer.from_host(dev, np.array([first, P], np.int32))
+    hist = backend.HipBuffer.from_host(dev, np.full(total, -1, np.int32))
+    for _ in range(n_decode):
+        m.step(state, kc, vc, logits=logits, hist=hist, hist_cap=total)
+    dev.sync()
+    out = (first, lg_last, hist.numpy(), kc.numpy(), vc.numpy())
+    m.close()
+    return out
+
+
+@pytest.mark.parametrize("splits", [[150], [100, 50], [1, 149]])
+def test_gemma2_tiny_prefill_equals_steps(backend, dev, orc, synth, splits):
+    """The chunked prefill (batched MFMA products, chunks of 128 tokens)
+    leaves the caches, the last prompt position's logits and argmax, and the
+    decode that follows bit-identical to feeding the prompt one token step at
+    a time; the decoded tokens equal the oracle's."""
+    cfg = dict(TINY, ctx_len=256)
+    model = synth.gemma2_model(cfg, seed=15)
+    prompt = synth.prompt_tokens(150, cfg["vocab"], seed=8)
+    n_dec = 10
+    print(f"\n[prefill] splits {splits}, {len(prompt)} prompt tokens, {n_dec} decode", flush=True)
+    first, lg_last, hist, kc, vc = run_gpu_prefill_decode(backend, dev, model, prompt, n_dec, splits)
+    hist0, lg0, kc0, vc0 = run_gpu_decode(backend, dev, model, prompt, n_dec)
+    P = len(prompt)
+    assert first == hist0[P - 1]
+    assert_bits(lg_last, lg0[P - 1], "logits at the last prompt position")
+    assert np.array_equal(kc, kc0) and np.array_equal(vc, vc0)
+    assert np.array_equal(hist[P:], hist0[P:])
+    want, _, _ = run_oracle_decode(orc, model, prompt, n_dec)
+    assert_same_tokens(hist0, want)
+
+
+def test_gemma2_prefill_rejects_ring_wrap(backend, dev, synth):
+    model = synth.gemma2_model(TINY, seed=16)
+    m = backend.Gemma2Model.from_host(dev, model)
+    kc = backend.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    vc = backend.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    toks = backend.HipBuffer.from_host(dev, np.zeros(TINY["ctx_len"] + 1, np.int32))
+    with pytest.raises(backend.HipError):
+        m.prefill(toks, TINY["ctx_len"] + 1, 0, kc, vc)
+    with pytest.raises(backend.HipError):
+        m.prefill(toks, 8, TINY["ctx_len"] - 4, kc, vc)
+    m.close()
+
+
 def test_gemma2_tiny_ring_cache(backend, dev, orc, synth):
     """Past the cache capacity the KV cache is a ring (kernels.rs:1307-1313)
     and attention reads the last `capacity` positions (a sliding window,
