@@ -395,6 +395,27 @@ def test_gemma2_tiny_prefill_equals_steps(backend, dev, orc, synth, splits):
     assert_same_tokens(hist0, want)
 
 
+def test_gemma2_2b_shape_prefill_equals_fused_steps(backend, dev, synth):
+    """At the Gemma-2-2B layer shape (3 layers, dim 2304, 8/4 heads of 256,
+    FFN 9216) the token step runs its residual norms inside the gate/up and
+    q|k|v matvecs (wave-group exact sums), while the prefill runs them as
+    separate norm kernels between batched products.  Over 136 prompt tokens
+    (a full 128-token chunk and a ragged one) both leave the same caches, last
+    logits and decoded tokens, bit for bit."""
+    cfg = dict(synth.GEMMA2_2B, n_layers=3, vocab=2048, ctx_len=160)
+    model = synth.gemma2_model(cfg, seed=6)
+    prompt = synth.prompt_tokens(136, cfg["vocab"], seed=7)
+    n_dec = 8
+    print(f"\n[prefill 2b-shape] {len(prompt)} prompt tokens", flush=True)
+    first, lg_last, hist, kc, vc = run_gpu_prefill_decode(backend, dev, model, prompt, n_dec, [136])
+    hist0, lg0, kc0, vc0 = run_gpu_decode(backend, dev, model, prompt, n_dec)
+    P = len(prompt)
+    assert first == hist0[P - 1]
+    assert_bits(lg_last, lg0[P - 1], "logits at the last prompt position")
+    assert np.array_equal(kc, kc0) and np.array_equal(vc, vc0)
+    assert np.array_equal(hist[P:], hist0[P:])
+
+
 def test_gemma2_prefill_rejects_ring_wrap(backend, dev, synth):
     model = synth.gemma2_model(TINY, seed=16)
     m = backend.Gemma2Model.from_host(dev, model)
