@@ -112,6 +112,13 @@ __global__ __launch_bounds__(kNormMaxThreads) void residual_rms_norm_kernel(cons
                                                                  int dim)
 {
     extern __shared__ __align__(16) float lds[];
+    if (blockIdx.y) {  // row blockIdx.y of a batch (prefill; no pack)
+        const size_t r = (size_t)blockIdx.y * dim;
+        t += r;
+        h_in += r;
+        h_out += r;
+        if (xn) xn += r;
+    }
     const int n4 = dim >> 2;
     if constexpr (CH == 1) {
         const ResidualOps ops = residual_load(t, w_post, h_in, (xn || pack) ? w_next : nullptr, n4);
@@ -163,6 +170,12 @@ __global__ __launch_bounds__(kNormMaxThreads) void embedding_kernel(const uint8_
                                                          uint8_t *__restrict__ pack, int dim, int vocab)
 {
     extern __shared__ __align__(16) float lds[];
+    if (blockIdx.y) {  // row blockIdx.y of a batch (prefill; no pack)
+        const size_t r = (size_t)blockIdx.y * dim;
+        if (d_token) d_token += blockIdx.y;
+        h += r;
+        if (xn) xn += r;
+    }
     int tok = d_token ? *d_token : token;  // the weight loads below do not wait for it
     tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
     const int n4 = dim >> 2, nb = dim >> 5;
@@ -210,7 +223,9 @@ __global__ __launch_bounds__(512) void rope_kv_f16_kernel(float *__restrict__ qk
                                                           float freq_scale, int capacity,
                                                           const float *__restrict__ table, int n_table)
 {
-    const int pos = d_pos ? *d_pos : pos_arg;
+    // row blockIdx.y of a batch of stacked q|k|v rows at consecutive positions
+    const int pos = (d_pos ? *d_pos : pos_arg) + (int)blockIdx.y;
+    qkv += (size_t)blockIdx.y * (n_heads + 2 * n_kv_heads) * head_dim;
     const int half = head_dim >> 1, i = threadIdx.x, g = blockIdx.x;
     const size_t kv_dim = (size_t)n_kv_heads * head_dim;
     const size_t cache_row = (size_t)(capacity > 0 ? pos % capacity : pos) * kv_dim;
@@ -388,6 +403,11 @@ __global__ __launch_bounds__(kScoreT) void attn_scores2_kernel(const float *__re
     constexpr int HD = kAttnHD, P = kScoreP, half = HD / 2;
     __shared__ __align__(16) float q_s[4][HD];
     __shared__ __align__(16) uint8_t k_s[P * kKRow2];
+    // query row blockIdx.z of a batch (prefill): stacked q|k|v rows at
+    // consecutive positions, one score block per row
+    q_in += (size_t)blockIdx.z * (n_heads + 2 * n_kv_heads) * HD;
+    scores += (size_t)blockIdx.z * n_heads * capacity;
+    n_past_arg += (int)blockIdx.z;
     int window, start;
     attn_window(d_pos, n_past_arg, capacity, window, start);
     const int p0 = blockIdx.x * P;
@@ -564,6 +584,9 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
     __shared__ __align__(16) mrml_xsum::Shared4 sum_xs[1];
     __shared__ uint64_t exp_tab[32];
     mrml_xsum::Shared4 *sum_x = sum_xs;
+    scores += (size_t)blockIdx.z * n_heads * capacity;  // query row blockIdx.z of a batch (prefill; no pack)
+    if (out) out += (size_t)blockIdx.z * n_heads * HD;
+    n_past_arg += (int)blockIdx.z;
     int window, start;
     attn_window(d_pos, n_past_arg, capacity, window, start);
     const int h = blockIdx.x, ds = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -803,26 +826,26 @@ int launch_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float eps
 }
 
 int launch_residual_rms_norm(mrml_hip_ctx *ctx, const float *t, const float *w_post, const float *h_in, float *h_out,
-                             const float *w_next, float eps, float *xn, void *pack, int dim)
+                             const float *w_next, float eps, float *xn, void *pack, int dim, int rows)
 {
     if (norm_one_chunk(dim))
-        hipLaunchKernelGGL(residual_rms_norm_kernel<1>, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, t,
+        hipLaunchKernelGGL(residual_rms_norm_kernel<1>, dim3(1, rows), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, t,
                            w_post, h_in, h_out, w_next, eps, xn, (uint8_t *)pack, dim);
     else
-        hipLaunchKernelGGL(residual_rms_norm_kernel<kMaxChunks>, dim3(1), dim3(norm_threads(dim)), norm_lds(dim),
+        hipLaunchKernelGGL(residual_rms_norm_kernel<kMaxChunks>, dim3(1, rows), dim3(norm_threads(dim)), norm_lds(dim),
                            ctx->stream, t, w_post, h_in, h_out, w_next, eps, xn, (uint8_t *)pack, dim);
     return check_launch(ctx, "residual_rms_norm_kernel");
 }
 
 int launch_embedding(mrml_hip_ctx *ctx, const void *table, int type, const int32_t *d_token, int token, float scale,
-                     float *h, const float *w_norm, float eps, float *xn, void *pack, int dim, int vocab)
+                     float *h, const float *w_norm, float eps, float *xn, void *pack, int dim, int vocab, int rows)
 {
     if (norm_one_chunk(dim))
-        hipLaunchKernelGGL(embedding_kernel<1>, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream,
+        hipLaunchKernelGGL(embedding_kernel<1>, dim3(1, rows), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream,
                            (const uint8_t *)table, type, d_token, token, scale, h, w_norm, eps, xn, (uint8_t *)pack, dim,
                            vocab);
     else
-        hipLaunchKernelGGL(embedding_kernel<kMaxChunks>, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream,
+        hipLaunchKernelGGL(embedding_kernel<kMaxChunks>, dim3(1, rows), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream,
                            (const uint8_t *)table, type, d_token, token, scale, h, w_norm, eps, xn, (uint8_t *)pack, dim,
                            vocab);
     return check_launch(ctx, "embedding_kernel");
@@ -830,9 +853,9 @@ int launch_embedding(mrml_hip_ctx *ctx, const void *table, int type, const int32
 
 int launch_rope_kv_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache, uint16_t *v_cache, const int32_t *d_pos,
                        int pos, int n_heads, int n_kv_heads, int head_dim, float base, float freq_scale, int capacity,
-                       const float *table, int n_table)
+                       const float *table, int n_table, int rows)
 {
-    hipLaunchKernelGGL(rope_kv_f16_kernel, dim3(n_heads + 2 * n_kv_heads), dim3(head_dim / 2), 0, ctx->stream, qkv,
+    hipLaunchKernelGGL(rope_kv_f16_kernel, dim3(n_heads + 2 * n_kv_heads, rows), dim3(head_dim / 2), 0, ctx->stream, qkv,
                        k_cache, v_cache, d_pos, pos, n_heads, n_kv_heads, head_dim, base, freq_scale, capacity, table,
                        n_table);
     return check_launch(ctx, "rope_kv_f16_kernel");
@@ -871,6 +894,28 @@ int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_
     hipLaunchKernelGGL(attn_softmax_v_kernel, dim3(n_heads, kAttnHD / kSVD), dim3(64 * kSVW), (size_t)capacity * sizeof(float) + 16,
                        ctx->stream, scores, v_cache, d_pos, n_past, n_heads, n_kv_heads, capacity,
                        (int)host_expf_fused(), out, (uint8_t *)pack);
+    return check_launch(ctx, "attn_softmax_v_kernel");
+}
+
+// Attention of `rows` queries at consecutive positions n_past0, n_past0+1, ...
+// (the prefill of a chunk whose K/V rows are already in the cache): query row
+// r is the q of stacked q|k|v row r of qkv; output row r (n_heads*head_dim
+// f32) goes to out.  Each row's arithmetic is that of launch_attn_decode_f16
+// at its position.  scratch holds rows * n_heads * capacity floats.  Needs
+// n_heads / n_kv_heads <= 4 (attn_rope_ok).
+int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *qkv, const uint16_t *k_cache, const uint16_t *v_cache,
+                         float *out, int n_past0, int rows, int n_heads, int n_kv_heads, float scale, int capacity,
+                         void *scratch)
+{
+    float *scores = reinterpret_cast<float *>(scratch);
+    const dim3 sgrid((capacity + kScoreP - 1) / kScoreP, n_kv_heads, rows);
+    hipLaunchKernelGGL(attn_scores2_kernel<false>, sgrid, dim3(kScoreT), 0, ctx->stream, qkv,
+                       const_cast<uint16_t *>(k_cache), (uint16_t *)nullptr, (const int32_t *)nullptr, n_past0,
+                       n_heads, n_kv_heads, scale, capacity, (const float *)nullptr, 0, 0.0f, 0.0f, scores);
+    if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
+    hipLaunchKernelGGL(attn_softmax_v_kernel, dim3(n_heads, kAttnHD / kSVD, rows), dim3(64 * kSVW),
+                       (size_t)capacity * sizeof(float) + 16, ctx->stream, scores, v_cache, (const int32_t *)nullptr,
+                       n_past0, n_heads, n_kv_heads, capacity, (int)host_expf_fused(), out, (uint8_t *)nullptr);
     return check_launch(ctx, "attn_softmax_v_kernel");
 }
 

@@ -99,12 +99,13 @@ int launch_qkv_resnorm(mrml_hip_ctx *ctx, const void *wq, const void *wk, const 
 bool norm_dim_ok(int dim);
 int launch_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float eps, float *out, void *pack, int dim);
 int launch_residual_rms_norm(mrml_hip_ctx *ctx, const float *t, const float *w_post, const float *h_in, float *h_out,
-                             const float *w_next, float eps, float *xn, void *pack, int dim);
+                             const float *w_next, float eps, float *xn, void *pack, int dim, int rows = 1);
 int launch_embedding(mrml_hip_ctx *ctx, const void *table, int type, const int32_t *d_token, int token, float scale,
-                     float *h, const float *w_norm, float eps, float *xn, void *pack, int dim, int vocab);
+                     float *h, const float *w_norm, float eps, float *xn, void *pack, int dim, int vocab,
+                     int rows = 1);
 int launch_rope_kv_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache, uint16_t *v_cache, const int32_t *d_pos,
                        int pos, int n_heads, int n_kv_heads, int head_dim, float base, float freq_scale, int capacity,
-                       const float *table, int n_table);
+                       const float *table, int n_table, int rows = 1);
 int attn_head_dim();
 int attn_max_capacity();
 size_t attn_scratch_bytes(int n_heads, int capacity);
@@ -112,6 +113,11 @@ int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_
                            float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
                            float scale, int capacity, void *scratch);
 bool attn_rope_ok(int n_heads, int n_kv_heads);
+// `rows` batched queries at positions n_past0.. over stacked q|k|v rows
+// (prefill); scratch of rows * attn_scratch_bytes(n_heads, capacity).
+int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *qkv, const uint16_t *k_cache, const uint16_t *v_cache,
+                         float *out, int n_past0, int rows, int n_heads, int n_kv_heads, float scale, int capacity,
+                         void *scratch);
 int launch_attn_decode_rope_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k_cache, uint16_t *v_cache,
                                 float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
                                 float scale, int capacity, const float *table, int n_table, float base,

@@ -45,7 +45,7 @@ struct mrml_hip_gemma2 {
     void *pf_arena = nullptr;
     float *pf_h = nullptr, *pf_xn = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_qkv = nullptr,
           *pf_attn = nullptr, *pf_o = nullptr, *pf_g = nullptr, *pf_u = nullptr, *pf_act = nullptr, *pf_f = nullptr;
-    void *pf_gpack = nullptr;
+    void *pf_gpack = nullptr, *pf_scores = nullptr;  // GEMM pack; attention scores of every row
 };
 
 using namespace mrml;
@@ -340,7 +340,8 @@ int prefill_buffers(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m)
                  o_k = take(M * kvd * 4), o_v = take(M * kvd * 4), o_qkv = take(M * (qd + 2 * kvd) * 4),
                  o_attn = take(M * qd * 4), o_o = take(M * c.dim * 4), o_g = take(M * c.ffn_dim * 4),
                  o_u = take(M * c.ffn_dim * 4), o_act = take(M * c.ffn_dim * 4), o_f = take(M * c.dim * 4),
-                 o_gp = take(gemm_pack_bytes((int32_t)widest, (int32_t)M));
+                 o_gp = take(gemm_pack_bytes((int32_t)widest, (int32_t)M)),
+                 o_sc = take(M * attn_scratch_bytes(c.n_heads, c.ctx_len));
     hipError_t e = hipMalloc(&m->pf_arena, off);
     if (e != hipSuccess) {
         m->pf_arena = nullptr;
@@ -352,6 +353,7 @@ int prefill_buffers(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m)
     m->pf_attn = (float *)(b + o_attn), m->pf_o = (float *)(b + o_o), m->pf_g = (float *)(b + o_g);
     m->pf_u = (float *)(b + o_u), m->pf_act = (float *)(b + o_act), m->pf_f = (float *)(b + o_f);
     m->pf_gpack = b + o_gp;
+    m->pf_scores = b + o_sc;
     return MRML_HIP_OK;
 }
 
@@ -396,9 +398,8 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
     for (int t0 = 0; t0 < n_tokens; t0 += kPrefillChunk) {
         const int n = std::min(kPrefillChunk, n_tokens - t0), p0 = pos0 + t0;
         float *h = m->pf_h, *xn = m->pf_xn;
-        for (int i = 0; i < n; ++i)
-            STEP(launch_embedding(ctx, m->tok_embd, c.tie_type, d_tokens + t0 + i, 0, emb_scale, h + (size_t)i * c.dim,
-                                  m->layers[0].attn_norm, c.eps, xn + (size_t)i * c.dim, nullptr, c.dim, c.vocab));
+        STEP(launch_embedding(ctx, m->tok_embd, c.tie_type, d_tokens + t0, 0, emb_scale, h, m->layers[0].attn_norm,
+                              c.eps, xn, nullptr, c.dim, c.vocab, n));
         for (int l = 0; l < c.n_layers; ++l) {
             const mrml_hip_gemma2_layer &L = m->layers[l];
             uint16_t *kc = d_k_cache + (size_t)l * layer_cache, *vc = d_v_cache + (size_t)l * layer_cache;
@@ -417,20 +418,20 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
                                       hipMemcpyDeviceToDevice, ctx->stream));
             // every token's rotated k and v enter the cache before any token
             // attends; token i then reads positions <= p0 + i only
-            for (int i = 0; i < n; ++i)
-                STEP(launch_rope_kv_f16(ctx, m->pf_qkv + (size_t)i * qkvd, kc, vc, nullptr, p0 + i, c.n_heads,
-                                        c.n_kv_heads, c.head_dim, c.rope_base, 1.0f, c.ctx_len, m->rope_table,
-                                        c.ctx_len));
-            for (int i = 0; i < n; ++i)
-                STEP(launch_attn_decode_f16(ctx, m->pf_qkv + (size_t)i * qkvd, kc, vc, m->pf_attn + (size_t)i * qd,
-                                            nullptr, nullptr, p0 + i, c.n_heads, c.n_kv_heads, c.attn_scale,
-                                            c.ctx_len, m->attn_part));
-            STEP(gemm_rows(ctx, m, L.wo, m->pf_attn, m->pf_o, c.dim, qd, n));
-            for (int i = 0; i < n; ++i) {
-                float *hi = h + (size_t)i * c.dim;
-                STEP(launch_residual_rms_norm(ctx, m->pf_o + (size_t)i * c.dim, L.post_attn_norm, hi, hi, L.ffn_norm,
-                                              c.eps, xn + (size_t)i * c.dim, nullptr, c.dim));
+            STEP(launch_rope_kv_f16(ctx, m->pf_qkv, kc, vc, nullptr, p0, c.n_heads, c.n_kv_heads, c.head_dim,
+                                    c.rope_base, 1.0f, c.ctx_len, m->rope_table, c.ctx_len, n));
+            if (attn_rope_ok(c.n_heads, c.n_kv_heads)) {
+                STEP(launch_attn_rows_f16(ctx, m->pf_qkv, kc, vc, m->pf_attn, p0, n, c.n_heads, c.n_kv_heads,
+                                          c.attn_scale, c.ctx_len, m->pf_scores));
+            } else {
+                for (int i = 0; i < n; ++i)
+                    STEP(launch_attn_decode_f16(ctx, m->pf_qkv + (size_t)i * qkvd, kc, vc,
+                                                m->pf_attn + (size_t)i * qd, nullptr, nullptr, p0 + i, c.n_heads,
+                                                c.n_kv_heads, c.attn_scale, c.ctx_len, m->attn_part));
             }
+            STEP(gemm_rows(ctx, m, L.wo, m->pf_attn, m->pf_o, c.dim, qd, n));
+            STEP(launch_residual_rms_norm(ctx, m->pf_o, L.post_attn_norm, h, h, L.ffn_norm, c.eps, xn, nullptr, c.dim,
+                                          n));
             STEP(launch_gemm_pack_quantize(ctx, xn, m->pf_gpack, c.dim, n));
             STEP(launch_gemm_q4_0(ctx, L.w_gate, m->pf_gpack, m->pf_g, c.ffn_dim, c.dim, n));
             STEP(launch_gemm_q4_0(ctx, L.w_up, m->pf_gpack, m->pf_u, c.ffn_dim, c.dim, n));
@@ -439,11 +440,8 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
                                m->pf_u, m->pf_act, nact);
             STEP(check_launch(ctx, "geglu_rows_kernel"));
             STEP(gemm_rows(ctx, m, L.w_down, m->pf_act, m->pf_f, c.dim, c.ffn_dim, n));
-            for (int i = 0; i < n; ++i) {
-                float *hi = h + (size_t)i * c.dim;
-                STEP(launch_residual_rms_norm(ctx, m->pf_f + (size_t)i * c.dim, L.post_ffw_norm, hi, hi, next_norm,
-                                              c.eps, xn + (size_t)i * c.dim, nullptr, c.dim));
-            }
+            STEP(launch_residual_rms_norm(ctx, m->pf_f, L.post_ffw_norm, h, h, next_norm, c.eps, xn, nullptr, c.dim,
+                                          n));
         }
         if (t0 + n < n_tokens) continue;
         // the last token's logits and greedy pick (the LM head of its token step)
