@@ -233,6 +233,25 @@ def decode_bench(be, synth, dev, ev, n_prefill: int, n_decode: int, cpu_steps: i
     return out, cpu
 
 
+def prefill_profile(be, synth, dev, n_prefill: int) -> dict:
+    """Profiling aid for the chunked prefill of the C4 model: one warm-up
+    call of one token, then one prefill of n_prefill tokens from position 0."""
+    cfg = dict(synth.GEMMA2_2B)
+    model = synth.gemma2_model(cfg, seed=1)
+    m = be.Gemma2Model.from_host(dev, model)
+    prompt = synth.prompt_tokens(n_prefill, cfg["vocab"], seed=1)
+    pr = be.HipBuffer.from_host(dev, prompt)
+    kc = be.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    vc = be.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    am = be.HipBuffer.from_host(dev, np.array([-1], np.int32))
+    m.prefill(pr, 1, 0, kc, vc, argmax=am)
+    dev.sync()
+    m.prefill(pr, n_prefill, 0, kc, vc, argmax=am)
+    dev.sync()
+    m.close()
+    return {"profile_prefill": n_prefill, "first_token": int(am.numpy()[0])}
+
+
 def decode_profile(be, synth, dev, n_prefill: int, n_steps: int) -> dict:
     """Profiling aid for the C4 model: n_prefill + n_steps token steps issued
     eagerly (no graph: the kernel trace then sees every launch); the last
@@ -340,6 +359,8 @@ def main() -> int:
                     help="profiling aid: N eager launches of each C5 product, then exit")
     ap.add_argument("--profile-decode", type=int, default=0,
                     help="profiling aid: prefill, then N eager decode steps of the C4 model, then exit")
+    ap.add_argument("--profile-prefill", type=int, default=0,
+                    help="profiling aid: one chunked prefill of N tokens of the C4 model, then exit")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--cpu-gemm-tokens", type=int, default=64)
     args = ap.parse_args()
@@ -358,6 +379,9 @@ def main() -> int:
         return 0
     if args.profile_decode:
         print(json.dumps(decode_profile(be, synth, dev, args.decode_prefill, args.profile_decode)))
+        return 0
+    if args.profile_prefill:
+        print(json.dumps(prefill_profile(be, synth, dev, args.profile_prefill)))
         return 0
 
     # ---- synthetic config-2 data, rotated over > 2x MALL of distinct copies
