@@ -49,6 +49,7 @@ def test_status_strings_and_null_context(backend):
     assert lib.mrml_hip_sync(None) == -1
     assert lib.mrml_hip_gemv_q4_0(None, None, None, None, 1, 32) == -1
     assert lib.mrml_hip_q8_0_pack_bytes(2304) == 72 * 40
+    assert lib.mrml_hip_gemma2_prefill(None, None, None, 1, 0, None, None, None, None) == -1
 
 
 def test_no_device_fails_cleanly(backend):
