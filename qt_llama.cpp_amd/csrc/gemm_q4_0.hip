@@ -132,7 +132,7 @@ struct BOps {
 __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const uint8_t *__restrict__ w,
                                                                          const uint8_t *__restrict__ gp,
                                                                          float *__restrict__ y, int rows, int nb,
-                                                                         int batch, int ngroups)
+                                                                         int batch, int ngroups, int ldy)
 {
     __shared__ __align__(16) u32x4 sa[kNBuf][kKC][2][32];  // A chunks: [block][K half][row] 16 signed bytes
     __shared__ __align__(16) float sdw[kNBuf][kKC][32];  // their row scales, f32
@@ -252,7 +252,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
 
     const int tok = g * 32 + tl;
     if (tok < batch) {
-        float *yr = y + (size_t)tok * rows + r0 + 4 * h;
+        float *yr = y + (size_t)tok * ldy + r0 + 4 * h;  // row stride ldy (rows when packed)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             *reinterpret_cast<float4 *>(yr + 8 * j) = make_float4(acc[4 * j], acc[4 * j + 1], acc[4 * j + 2],
@@ -290,12 +290,16 @@ int launch_gemm_pack_from_act(mrml_hip_ctx *ctx, const void *pack, void *gpack, 
 }
 
 int launch_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const void *gpack, float *y, int32_t rows, int32_t cols,
-                     int32_t batch)
+                     int32_t batch, int32_t ldy)
 {
     const int nb = cols / 32, ng = gemm_groups(batch);
+    if (ldy == 0) ldy = rows;
+    if (ldy < rows || ldy % 4 != 0 || ((uintptr_t)y & 15) != 0)
+        return fail(ctx, MRML_HIP_E_INVALID, "gemm_q4_0: output stride %d (rows %d) must be a multiple of 4 and y 16-byte aligned",
+                    ldy, rows);
     const dim3 grid(rows / 32, (ng + kGemmWaves - 1) / kGemmWaves);
     hipLaunchKernelGGL(gemm_q4_0_mfma_kernel, grid, dim3(64 * kGemmWaves), 0, ctx->stream, (const uint8_t *)w,
-                       (const uint8_t *)gpack, y, rows, nb, batch, ng);
+                       (const uint8_t *)gpack, y, rows, nb, batch, ng, ldy);
     return check_launch(ctx, "gemm_q4_0_mfma_kernel");
 }
 

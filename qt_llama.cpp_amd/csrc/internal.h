@@ -75,8 +75,9 @@ bool gemm_shape_ok(int32_t rows, int32_t cols, int32_t batch);
 size_t gemm_pack_bytes(int32_t cols, int32_t batch);
 int launch_gemm_pack_quantize(mrml_hip_ctx *ctx, const float *x, void *gpack, int32_t cols, int32_t batch);
 int launch_gemm_pack_from_act(mrml_hip_ctx *ctx, const void *pack, void *gpack, int32_t cols, int32_t batch);
+// y row stride ldy floats (0: rows; a multiple of 4, y 16-byte aligned)
 int launch_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const void *gpack, float *y, int32_t rows, int32_t cols,
-                     int32_t batch);
+                     int32_t batch, int32_t ldy = 0);
 
 // Argmax whose final pass can also advance a device-side decode loop
 // (state = {token, pos}); scratch holds argmax_parts(n) * 8 bytes.

@@ -40,10 +40,10 @@ struct mrml_hip_gemma2 {
     void *attn_part = nullptr, *argmax_scratch = nullptr;
     float *rope_table = nullptr;  // [ctx_len][head_dim/2] (cos, sin) from the host libm
     // prefill chunk buffers, allocated on the first prefill call: per token
-    // rows of h, xn, q, k, v, stacked q|k|v, attention output, o, gate, up,
+    // rows of h, xn, stacked q|k|v, attention output, o, gate, up,
     // act and f, plus one GEMM pack
     void *pf_arena = nullptr;
-    float *pf_h = nullptr, *pf_xn = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_qkv = nullptr,
+    float *pf_h = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr,
           *pf_attn = nullptr, *pf_o = nullptr, *pf_g = nullptr, *pf_u = nullptr, *pf_act = nullptr, *pf_f = nullptr;
     void *pf_gpack = nullptr, *pf_scores = nullptr;  // GEMM pack; attention scores of every row
 };
@@ -336,8 +336,7 @@ int prefill_buffers(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m)
         off = align_up(off + bytes, 256);
         return at;
     };
-    const size_t o_h = take(M * c.dim * 4), o_xn = take(M * c.dim * 4), o_q = take(M * qd * 4),
-                 o_k = take(M * kvd * 4), o_v = take(M * kvd * 4), o_qkv = take(M * (qd + 2 * kvd) * 4),
+    const size_t o_h = take(M * c.dim * 4), o_xn = take(M * c.dim * 4), o_qkv = take(M * (qd + 2 * kvd) * 4),
                  o_attn = take(M * qd * 4), o_o = take(M * c.dim * 4), o_g = take(M * c.ffn_dim * 4),
                  o_u = take(M * c.ffn_dim * 4), o_act = take(M * c.ffn_dim * 4), o_f = take(M * c.dim * 4),
                  o_gp = take(gemm_pack_bytes((int32_t)widest, (int32_t)M)),
@@ -348,8 +347,7 @@ int prefill_buffers(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m)
         return fail(ctx, MRML_HIP_E_ALLOC, "gemma2_prefill: hipMalloc(%zu): %s", off, hipGetErrorString(e));
     }
     uint8_t *b = (uint8_t *)m->pf_arena;
-    m->pf_h = (float *)(b + o_h), m->pf_xn = (float *)(b + o_xn), m->pf_q = (float *)(b + o_q);
-    m->pf_k = (float *)(b + o_k), m->pf_v = (float *)(b + o_v), m->pf_qkv = (float *)(b + o_qkv);
+    m->pf_h = (float *)(b + o_h), m->pf_xn = (float *)(b + o_xn), m->pf_qkv = (float *)(b + o_qkv);
     m->pf_attn = (float *)(b + o_attn), m->pf_o = (float *)(b + o_o), m->pf_g = (float *)(b + o_g);
     m->pf_u = (float *)(b + o_u), m->pf_act = (float *)(b + o_act), m->pf_f = (float *)(b + o_f);
     m->pf_gpack = b + o_gp;
@@ -390,11 +388,6 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
     do {                                \
         if ((rc = (call)) != 0) return rc; \
     } while (0)
-#define HIP_STEP(call)                                  \
-    do {                                                \
-        const hipError_t e_ = (call);                   \
-        if (e_ != hipSuccess) return hip_fail(ctx, e_, #call); \
-    } while (0)
     for (int t0 = 0; t0 < n_tokens; t0 += kPrefillChunk) {
         const int n = std::min(kPrefillChunk, n_tokens - t0), p0 = pos0 + t0;
         float *h = m->pf_h, *xn = m->pf_xn;
@@ -406,16 +399,9 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
             const float *next_norm = l + 1 < c.n_layers ? m->layers[l + 1].attn_norm : m->output_norm;
             // q, k, v of the chunk, stacked per token as the token step's q|k|v
             STEP(launch_gemm_pack_quantize(ctx, xn, m->pf_gpack, c.dim, n));
-            STEP(launch_gemm_q4_0(ctx, L.wq, m->pf_gpack, m->pf_q, qd, c.dim, n));
-            STEP(launch_gemm_q4_0(ctx, L.wk, m->pf_gpack, m->pf_k, kvd, c.dim, n));
-            STEP(launch_gemm_q4_0(ctx, L.wv, m->pf_gpack, m->pf_v, kvd, c.dim, n));
-            const size_t row = (size_t)qkvd * 4;
-            HIP_STEP(hipMemcpy2DAsync(m->pf_qkv, row, m->pf_q, (size_t)qd * 4, (size_t)qd * 4, n,
-                                      hipMemcpyDeviceToDevice, ctx->stream));
-            HIP_STEP(hipMemcpy2DAsync(m->pf_qkv + qd, row, m->pf_k, (size_t)kvd * 4, (size_t)kvd * 4, n,
-                                      hipMemcpyDeviceToDevice, ctx->stream));
-            HIP_STEP(hipMemcpy2DAsync(m->pf_qkv + qd + kvd, row, m->pf_v, (size_t)kvd * 4, (size_t)kvd * 4, n,
-                                      hipMemcpyDeviceToDevice, ctx->stream));
+            STEP(launch_gemm_q4_0(ctx, L.wq, m->pf_gpack, m->pf_qkv, qd, c.dim, n, qkvd));
+            STEP(launch_gemm_q4_0(ctx, L.wk, m->pf_gpack, m->pf_qkv + qd, kvd, c.dim, n, qkvd));
+            STEP(launch_gemm_q4_0(ctx, L.wv, m->pf_gpack, m->pf_qkv + qd + kvd, kvd, c.dim, n, qkvd));
             // every token's rotated k and v enter the cache before any token
             // attends; token i then reads positions <= p0 + i only
             STEP(launch_rope_kv_f16(ctx, m->pf_qkv, kc, vc, nullptr, p0, c.n_heads, c.n_kv_heads, c.head_dim,
@@ -453,7 +439,6 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
             STEP(launch_gemv_q8_0(ctx, m->tok_embd, m->xpack, logits, c.vocab, c.dim, 0));
         if (d_argmax) STEP(launch_argmax_f32(ctx, logits, c.vocab, d_argmax));
     }
-#undef HIP_STEP
 #undef STEP
     return MRML_HIP_OK;
 }
