@@ -80,7 +80,15 @@ int         mrml_hip_create(int32_t device, mrml_hip_ctx **out);
 int         mrml_hip_destroy(mrml_hip_ctx *ctx);
 const char *mrml_hip_last_error(const mrml_hip_ctx *ctx);
 const char *mrml_hip_status_string(int status);
+/* Waits for the context's stream.  Also fails with MRML_HIP_E_HIP when a
+ * kernel's bounded wait for other waves of its workgroup gave up since the
+ * last sync on the device (its results are then wrong). */
 int         mrml_hip_sync(mrml_hip_ctx *ctx);
+/* Poll limit of those bounded waits on the context's device (every context
+ * on it): polls < 0 restores the default (2^20), 0 makes every wait give up
+ * at once.  No reference counterpart: it lets a test drive the error path of
+ * mrml_hip_sync with every kernel still exiting normally. */
+int         mrml_hip_set_wait_limit(mrml_hip_ctx *ctx, int32_t polls);
 int         mrml_hip_device_info_get(mrml_hip_ctx *ctx, mrml_hip_device_info *info);
 int         mrml_hip_memory_info(mrml_hip_ctx *ctx, uint64_t *free_bytes, uint64_t *total_bytes);
 /* The context's hipStream_t, for callers that record events on it. */

@@ -104,6 +104,7 @@ _SIGNATURES = {
     "mrml_hip_last_error": [_P],
     "mrml_hip_status_string": [ctypes.c_int],
     "mrml_hip_sync": [_P],
+    "mrml_hip_set_wait_limit": [_P, _I],
     "mrml_hip_device_info_get": [_P, ctypes.POINTER(DeviceInfo)],
     "mrml_hip_memory_info": [_P, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)],
     "mrml_hip_stream": [_P],
@@ -311,6 +312,11 @@ class HipDevice:
     # ---- lifecycle -----------------------------------------------------------
     def sync(self) -> None:
         self._check(self.lib.mrml_hip_sync(self.ctx))
+
+    def set_wait_limit(self, polls: int) -> None:
+        """Poll limit of the kernels' bounded waits on this device (< 0: the
+        default; 0: every wait gives up, and the next sync() raises)."""
+        self._check(self.lib.mrml_hip_set_wait_limit(self.ctx, polls))
 
     def device_info(self) -> dict:
         info = DeviceInfo()

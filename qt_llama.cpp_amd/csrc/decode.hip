@@ -937,4 +937,6 @@ int launch_attn_decode_rope_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k
     return launch_softmax_v(ctx, scores, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, capacity);
 }
 
+hipError_t wait_guard_decode(int polls, uint32_t *timeouts) { return mrml_xsum::wait_guard_io(polls, timeouts); }
+
 }  // namespace mrml

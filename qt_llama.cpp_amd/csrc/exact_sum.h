@@ -492,14 +492,59 @@ __device__ __forceinline__ float block_seq_sum_nonneg4(float4 v, int n, Shared4 
 // barrier is an LDS counter (GroupSync), so the workgroup's other waves never
 // wait on the sum -- they can be stalled issuing loads meanwhile.
 
-// A barrier among the nw waves of a group: each wave adds 1 to an LDS counter
-// once its own LDS accesses are done and waits until the counter reaches nw
-// times its number of syncs so far.  The counter is zeroed (and the zero made
-// visible by a workgroup barrier) before the group's first sync.  The wait is
-// bounded: a group that never completes lets its waves go on with wrong data
-// rather than keep the device busy forever.
+// ---- bounded waits on LDS counters ---------------------------------------------
+// A wave waiting for other waves of its workgroup polls an LDS counter at most
+// g_wait_polls times (default kSyncSpin), so a wait that never completes
+// cannot keep the device busy.  A wait that gives up lets the wave go on (its
+// LDS reads stay in bounds, the values are wrong) and adds one to
+// g_wait_timeouts; the host reads and clears that count when it synchronizes
+// and reports the failure (mrml_hip_sync returns MRML_HIP_E_HIP), so wrong
+// data never comes back with a success status.  Each translation unit that
+// includes this header has its own pair of words (no relocatable device
+// code); wait_guard_io() below is that unit's host access to them.
 constexpr int kSyncSpin = 1 << 20;
 
+static __device__ int g_wait_polls = kSyncSpin;
+static __device__ uint32_t g_wait_timeouts = 0u;
+
+// Waits until the wave-uniform value of *ctr reaches target; false (and one
+// timeout recorded per wave) if it gives up.
+__device__ __forceinline__ bool bounded_wait(const uint32_t *ctr, uint32_t target)
+{
+    const int polls = g_wait_polls;
+#pragma unroll 1
+    for (int i = 0; i < polls; ++i) {
+        const uint32_t v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (__builtin_amdgcn_readfirstlane(v) >= target) return true;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(&g_wait_timeouts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return false;
+}
+
+// Host side, for the current device: polls >= 0 sets this unit's poll limit
+// (0: every wait gives up at once), polls < 0 leaves it; timeouts (nullable)
+// receives the count of waits given up since the last call, which is then
+// cleared.
+static inline hipError_t wait_guard_io(int polls, uint32_t *timeouts)
+{
+    hipError_t e = hipSuccess;
+    if (polls >= 0) e = hipMemcpyToSymbol(HIP_SYMBOL(g_wait_polls), &polls, sizeof polls);
+    if (e == hipSuccess && timeouts) {
+        e = hipMemcpyFromSymbol(timeouts, HIP_SYMBOL(g_wait_timeouts), sizeof *timeouts);
+        if (e == hipSuccess && *timeouts) {
+            const uint32_t zero = 0u;
+            e = hipMemcpyToSymbol(HIP_SYMBOL(g_wait_timeouts), &zero, sizeof zero);
+        }
+    }
+    return e;
+}
+
+// A barrier among the nw waves of a group: each wave adds 1 to an LDS counter
+// once its own LDS accesses are done and waits (bounded_wait) until the
+// counter reaches nw times its number of syncs so far.  The counter is zeroed
+// (and the zero made visible by a workgroup barrier) before the group's first
+// sync.
 struct GroupSync {
     uint32_t *ctr;
     uint32_t target;
@@ -509,11 +554,7 @@ struct GroupSync {
         target += nw;
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        for (int i = 0; i < kSyncSpin; ++i) {
-            const uint32_t v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            if (__builtin_amdgcn_readfirstlane(v) >= target) break;
-            __builtin_amdgcn_s_sleep(1);
-        }
+        bounded_wait(ctr, target);
         asm volatile("" ::: "memory");
     }
 };
@@ -598,12 +639,17 @@ __device__ __forceinline__ float group_seq_sum_nonneg(const float (&av)[K], int 
     uint32_t rs = (uint32_t)wave_shr1_i32((int)wave_incl_max_u32(mine));
     if (lane == 63) x.wcnt[gw] = cincl;
     sync();
-    const int cw = lane < nw ? x.wcnt[lane] : 0;  // row 0
+    // The counts, offsets and stores are clamped to the n-term event list.
+    // The clamps change nothing while every wait completes (each term makes
+    // at most one event); after a wait that gave up (stale counts) they keep
+    // every LDS access inside the list and the walk below finite.
+    const int cw = lane < nw ? (int)min((uint32_t)x.wcnt[lane], (uint32_t)(64 * K)) : 0;  // row 0
     const int ci = row_incl_scan_i32(cw);
-    const int nev = __builtin_amdgcn_readlane(ci, 15);
-    const int goff = gw ? __builtin_amdgcn_readlane(ci, gw - 1) : 0;
+    const int nev = min(__builtin_amdgcn_readlane(ci, 15), n);
+    const int goff = gw ? min(__builtin_amdgcn_readlane(ci, gw - 1), n) : 0;
     if (gw == 0 && lane < kPadEvents) evl[nev + lane] = 0.0f;
     float *ev = evl + goff;
+    const int ecap = n - goff;  // events this wave may store
     int e = cincl - cnt;
     r = iincl - my_inc;
 #pragma unroll
@@ -612,8 +658,9 @@ __device__ __forceinline__ float group_seq_sum_nonneg(const float (&av)[K], int 
         e += st ? 1 : 0;
         if (st && !((unsafe >> i) & 1u)) rs = r;
         const uint32_t re = r + inc[i];
-        if ((unsafe >> i) & 1u) ev[e - 1] = a[i];
-        if ((ends >> i) & 1u) ev[e - 1] = (float)(int)(re - rs) * uu[i];  // exact: < 2^23 ulps, u a power of 2
+        const bool room = e <= ecap;
+        if (((unsafe >> i) & 1u) && room) ev[e - 1] = a[i];
+        if (((ends >> i) & 1u) && room) ev[e - 1] = (float)(int)(re - rs) * uu[i];  // exact: < 2^23 ulps, u a power of 2
         r = re;
     }
     sync();

@@ -246,9 +246,13 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
         nbf = wb;
         wb = wb == kNBuf - 1 ? 0 : wb + 1;
     }
+    // The last nb % kKC blocks.  Their ring slots are refilled as in a full
+    // chunk: with more than kPF of them, blocks kPF.. reuse the slots of
+    // blocks 0.. (loads of blocks >= nb are in range of the buffer or read
+    // zeros, and are never folded).
 #pragma unroll
-    for (int kc = 0; kc < kKC - 1; ++kc)  // the last nb % kKC blocks
-        if (c * kKC + kc < nb) step(kc, ring[kc % kPF], false, c * kKC + kc);
+    for (int kc = 0; kc < kKC - 1; ++kc)
+        if (c * kKC + kc < nb) step(kc, ring[kc % kPF], kc + kPF < kKC - 1, c * kKC + kc);
 
     const int tok = g * 32 + tl;
     if (tok < batch) {

@@ -824,8 +824,7 @@ __global__ __launch_bounds__(64 * S) void gemv_q4_0_relay_kernel(const uint8_t *
 // of its round-k iteration to T[it][row][j] and then counts it in cnt[k];
 // wave 0's lanes r < 4 add row r's terms of a round, in block order, once all
 // of the round's waves have counted, so only the last round's adds remain
-// once the stream ends.  The waits are bounded (exact_sum.h's kSyncSpin
-// polls).
+// once the stream ends.  The waits are bounded (exact_sum.h's bounded_wait).
 template <int NB, int S>
 constexpr int long_ipw() { return (NB / 16 + S - 1) / S; }
 
@@ -857,12 +856,7 @@ __global__ __launch_bounds__(64 * (S + 1)) void gemv_q4_0_long_kernel(const uint
 #pragma unroll 1
         for (int k = 0; k < IPW; ++k) {
             const uint32_t want = (uint32_t)(ITERS - S * k < S ? ITERS - S * k : S);  // waves with a live iteration
-#pragma unroll 1
-            for (int i = 0; i < mrml_xsum::kSyncSpin; ++i) {
-                const uint32_t f = __hip_atomic_load(&flag[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                if (__builtin_amdgcn_readfirstlane(f) >= want) break;
-                __builtin_amdgcn_s_sleep(1);
-            }
+            mrml_xsum::bounded_wait(&flag[k], want);
             asm volatile("" ::: "memory");
             float4 v[4 * S];
 #pragma unroll
@@ -1365,5 +1359,7 @@ int launch_gemv_q4_0_gguf(mrml_hip_ctx *ctx, const void *w, const void *xpack, f
     });
     return check_launch(ctx, "gemv_q4_0_gguf_kernel");
 }
+
+hipError_t wait_guard_gemv(int polls, uint32_t *timeouts) { return mrml_xsum::wait_guard_io(polls, timeouts); }
 
 }  // namespace mrml

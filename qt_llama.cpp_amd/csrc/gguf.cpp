@@ -23,6 +23,7 @@
 #include <cstdio>
 #include <cstring>
 #include <memory>
+#include <new>
 #include <string>
 #include <vector>
 
@@ -141,6 +142,20 @@ public:
         if (!valid_utf8(s)) return fail(MRML_HIP_E_FORMAT, "GGUF string is not valid UTF-8");
         return MRML_HIP_OK;
     }
+    // Smallest encoding of one value of a type id: the scalar's width, a
+    // string's u64 length, an array's u32 item type and u64 count.  An
+    // unknown id counts 1 byte (it fails when the first item is read).
+    static uint64_t min_encoded_bytes(uint32_t type)
+    {
+        switch (type) {
+        case 0: case 1: case 7: return 1;
+        case 2: case 3: return 2;
+        case 4: case 5: case 6: return 4;
+        case 8: case 10: case 11: case 12: return 8;
+        case 9: return 12;
+        default: return 1;
+        }
+    }
     int value(Value &v, uint32_t type, int depth)
     {
         v.type = (int32_t)type;
@@ -161,11 +176,17 @@ public:
             if (int rc = le(it)) return rc;
             if (int rc = le(n)) return rc;
             v.item_type = (int32_t)it;  // an unknown item type fails at the first item, as in gguf.rs:213-219
-            if (n > left()) return fail(MRML_HIP_E_FORMAT, "GGUF: array of %llu items at byte %llu runs past the end of file",
-                                        (unsigned long long)n, (unsigned long long)pos_);
-            v.items.resize(n);
-            for (uint64_t k = 0; k < n; ++k)
-                if (int rc = value(v.items[k], it, depth + 1)) return rc;
+            // Every item takes at least min_encoded_bytes(it) bytes of the
+            // file, so a count the file cannot hold is an error before any
+            // item is allocated, and the item list grows as items parse.
+            if (n > left() / min_encoded_bytes(it))
+                return fail(MRML_HIP_E_FORMAT, "GGUF: array of %llu items at byte %llu runs past the end of file",
+                            (unsigned long long)n, (unsigned long long)pos_);
+            v.items.clear();
+            for (uint64_t k = 0; k < n; ++k) {
+                v.items.emplace_back();
+                if (int rc = value(v.items.back(), it, depth + 1)) return rc;
+            }
             return 0;
         }
         case 10: { uint64_t x; if (int rc = le(x)) return rc; v.u = x; return 0; }
@@ -231,14 +252,10 @@ struct mrml_gguf {
     std::vector<std::pair<std::string, Tensor>> tensors;
 };
 
-extern "C" {
+namespace {
 
-const char *mrml_gguf_last_error(void) { return g_last_error.c_str(); }
-
-int mrml_gguf_open(const char *path, mrml_gguf **out)
+int open_file(const char *path, mrml_gguf **out)
 {
-    if (!path || !out) return fail(MRML_HIP_E_INVALID, "mrml_gguf_open: null argument");
-    *out = nullptr;
     std::unique_ptr<FILE, int (*)(FILE *)> f(fopen(path, "rb"), fclose);
     if (!f) return fail(MRML_HIP_E_IO, "GGUF: cannot open %s: %s", path, strerror(errno));
     if (fseeko(f.get(), 0, SEEK_END) != 0) return fail(MRML_HIP_E_IO, "GGUF: cannot seek %s", path);
@@ -301,6 +318,27 @@ int mrml_gguf_open(const char *path, mrml_gguf **out)
     g->data_offset = pos % align == 0 ? pos : pos + (align - pos % align);
     *out = g.release();
     return MRML_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *mrml_gguf_last_error(void) { return g_last_error.c_str(); }
+
+int mrml_gguf_open(const char *path, mrml_gguf **out)
+{
+    if (!path || !out) return fail(MRML_HIP_E_INVALID, "mrml_gguf_open: null argument");
+    *out = nullptr;
+    // The directory's strings, tables and arrays are host allocations; none
+    // of their exceptions may cross the C boundary.
+    try {
+        return open_file(path, out);
+    } catch (const std::bad_alloc &) {
+        return fail(MRML_HIP_E_ALLOC, "GGUF: out of host memory reading %s", path);
+    } catch (...) {
+        return fail(MRML_HIP_E_FORMAT, "GGUF: unexpected error reading %s", path);
+    }
 }
 
 int mrml_gguf_close(mrml_gguf *g)

@@ -124,6 +124,12 @@ int launch_attn_decode_rope_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k
                                 float scale, int capacity, const float *table, int n_table, float base,
                                 float freq_scale, void *scratch);
 
+// Bounded LDS-counter waits (exact_sum.h), one pair of device words per
+// translation unit that has them: polls >= 0 sets the poll limit, timeouts
+// (nullable) takes and clears the count of waits given up.
+hipError_t wait_guard_gemv(int polls, uint32_t *timeouts);
+hipError_t wait_guard_decode(int polls, uint32_t *timeouts);
+
 // Which form of the C library's expf the host runs (glibc picks its FMA build
 // on x86-64 CPUs with FMA and AVX2); the device reproduces the same one.
 bool host_expf_fused();

@@ -42,6 +42,18 @@ MRML_HD uint64_t d2u(double d) { return __builtin_bit_cast(uint64_t, d); }
 MRML_HD double u2d(uint64_t u) { return __builtin_bit_cast(double, u); }
 
 // ---- expm1f / tanhf (fdlibm) --------------------------------------------------
+//
+// expm1f and tanhf below follow fdlibm's s_expm1f.c and s_tanhf.c (float
+// conversion by Ian Lance Taylor, Cygnus Support), whose notice is:
+//
+// ====================================================
+// Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+//
+// Developed at SunPro, a Sun Microsystems, Inc. business.
+// Permission to use, copy, modify, and distribute this
+// software is freely granted, provided that this notice
+// is preserved.
+// ====================================================
 
 MRML_HD float expm1f(float x)
 {
@@ -136,6 +148,12 @@ MRML_HD float tanhf(float x)
 }
 
 // ---- expf (Arm optimized-routines algorithm) -------------------------------------
+//
+// expf below follows math/expf.c and its 2^(i/32) table (math/exp2f_data.c)
+// of Arm optimized-routines:
+//
+// Copyright (c) 2017-2018, Arm Limited.
+// SPDX-License-Identifier: MIT
 
 // T[i] = bits(2^(i/32)) - (i << 47): the correctly rounded doubles 2^(i/32)
 // with the table index pre-subtracted from the exponent field.

@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "device.h"
+#include "exact_sum.h"
 #include "internal.h"
 
 namespace mrml {
@@ -177,7 +178,27 @@ int mrml_hip_sync(mrml_hip_ctx *ctx)
 {
     CTX_GUARD(ctx);
     hipError_t e = hipStreamSynchronize(ctx->stream);
-    return e == hipSuccess ? 0 : hip_fail(ctx, e, "hipStreamSynchronize");
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
+    // Kernels whose bounded waits gave up went on with wrong data.
+    uint32_t t_gemv = 0, t_decode = 0;
+    if ((e = wait_guard_gemv(-1, &t_gemv)) != hipSuccess) return hip_fail(ctx, e, "wait guard (matvec)");
+    if ((e = wait_guard_decode(-1, &t_decode)) != hipSuccess) return hip_fail(ctx, e, "wait guard (decode)");
+    if (t_gemv + t_decode)
+        return fail(ctx, MRML_HIP_E_HIP,
+                    "%u bounded LDS-counter waits gave up (%u matvec, %u decode): the results since the last sync "
+                    "are wrong", t_gemv + t_decode, t_gemv, t_decode);
+    return MRML_HIP_OK;
+}
+
+int mrml_hip_set_wait_limit(mrml_hip_ctx *ctx, int32_t polls)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, polls <= (1 << 24), "set_wait_limit: polls=%d above 2^24", polls);
+    if (polls < 0) polls = mrml_xsum::kSyncSpin;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess) e = wait_guard_gemv(polls, nullptr);
+    if (e == hipSuccess) e = wait_guard_decode(polls, nullptr);
+    return e == hipSuccess ? MRML_HIP_OK : hip_fail(ctx, e, "set_wait_limit");
 }
 
 int mrml_hip_device_info_get(mrml_hip_ctx *ctx, mrml_hip_device_info *info)

@@ -146,6 +146,10 @@ def test_value_conversions(gguf, tmp_path):
     ("item", "Unknown GGUF value type ID: 77"),
     ("utf8", "not valid UTF-8"),
     ("bigstr", "runs past the end"),
+    # item counts the remaining bytes cannot hold at the items' smallest
+    # encoding fail before any item is allocated
+    ("bigarr", "array of 150 items"),
+    ("bignested", "array of 20 items"),
 ])
 def test_malformed_files_fail_cleanly(gguf, tmp_path, case, needle):
     good_t = [tensor_entry("t", [32], 0, 0)]
@@ -158,6 +162,8 @@ def test_malformed_files_fail_cleanly(gguf, tmp_path, case, needle):
         "item": gguf_bytes([kv("k", 9, struct.pack("<IQ", 77, 1) + b"\0")], good_t),
         "utf8": gguf_bytes([kv(b"\xff\xfe", 4, struct.pack("<I", 1))], good_t),
         "bigstr": gguf_bytes([struct.pack("<Q", 1 << 60) + b"k"], good_t),
+        "bigarr": gguf_bytes([kv("k", 9, struct.pack("<IQ", 10, 150))], good_t),
+        "bignested": gguf_bytes([kv("k", 9, struct.pack("<IQ", 9, 20))], good_t),
     }[case]
     with pytest.raises(gguf.GgufError) as e:
         gguf.GgufFile(write(tmp_path, data + bytes(128)))

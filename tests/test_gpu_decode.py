@@ -196,8 +196,8 @@ def test_rope_kv_append(backend, dev, orc, synth, pos, use_table):
 
 
 # ------------------------------------------------------------ attention
-def attention_case(backend, dev, orc, synth, n_past, cap, seed):
-    nh, nkv, hd = 8, 4, 256
+def attention_case(backend, dev, orc, synth, n_past, cap, seed, nh=8, nkv=4):
+    hd = 256
     rng = synth.rng_for(3400 + seed)
     kvd = nkv * hd
     q = rng.standard_normal(nh * hd).astype(np.float32) * np.float32(0.5)
@@ -223,6 +223,16 @@ def test_attention_decode(backend, dev, orc, synth, n_past):
     got, ref, pack, _ = attention_case(backend, dev, orc, synth, n_past, 4096, n_past)
     assert_bits(got, ref, "attention")
     check_pack(orc, pack, got, "attention")
+
+
+@pytest.mark.parametrize("nh,nkv", [(8, 8), (8, 1), (6, 1), (5, 1), (16, 4), (4, 2)])
+@pytest.mark.parametrize("n_past", [0, 37, 700])
+def test_attention_decode_head_groups(backend, dev, orc, synth, nh, nkv, n_past):
+    """Query heads per kv head from 1 to 8 (groups above 4 take their own
+    scores kernel), bit-exact against the oracle."""
+    got, ref, pack, _ = attention_case(backend, dev, orc, synth, n_past, 1024, 900 + 10 * nh + nkv, nh, nkv)
+    assert_bits(got, ref, f"attention {nh}/{nkv} heads")
+    check_pack(orc, pack, got, f"attention {nh}/{nkv} heads")
 
 
 def test_attention_ring_window(backend, dev, orc, synth):
@@ -393,6 +403,49 @@ def test_gemma2_tiny_prefill_equals_steps(backend, dev, orc, synth, splits):
     assert np.array_equal(hist[P:], hist0[P:])
     want, _, _ = run_oracle_decode(orc, model, prompt, n_dec)
     assert_same_tokens(hist0, want)
+
+
+def test_gemma2_ragged_k_prefill_equals_steps(backend, dev, orc, synth):
+    """A model whose width and FFN width leave 5 and 7 blocks past the
+    batched product's last 8-block K chunk (dim 416 = 13 blocks, ffn 480 = 15
+    blocks): the prefill equals the token steps bit for bit and the decoded
+    tokens equal the oracle's."""
+    cfg = dict(TINY, dim=416, ffn_dim=480, ctx_len=96)
+    model = synth.gemma2_model(cfg, seed=17)
+    prompt = synth.prompt_tokens(70, cfg["vocab"], seed=9)
+    n_dec = 6
+    first, lg_last, hist, kc, vc = run_gpu_prefill_decode(backend, dev, model, prompt, n_dec, [70])
+    hist0, lg0, kc0, vc0 = run_gpu_decode(backend, dev, model, prompt, n_dec)
+    P = len(prompt)
+    assert first == hist0[P - 1]
+    assert_bits(lg_last, lg0[P - 1], "logits at the last prompt position")
+    assert np.array_equal(kc, kc0) and np.array_equal(vc, vc0)
+    assert np.array_equal(hist[P:], hist0[P:])
+    want, _, _ = run_oracle_decode(orc, model, prompt, n_dec)
+    assert_same_tokens(hist0, want)
+
+
+@pytest.mark.parametrize("n_heads,n_kv_heads", [(8, 1), (6, 1), (4, 4)])
+def test_gemma2_head_groups_prefill_and_steps(backend, dev, orc, synth, n_heads, n_kv_heads):
+    """Query-head groups of 8, 6 and 1 through the whole model: the token
+    steps (graph replays) match the oracle bit for bit, and the chunked
+    prefill equals them."""
+    cfg = dict(TINY, n_heads=n_heads, n_kv_heads=n_kv_heads, ctx_len=48)
+    model = synth.gemma2_model(cfg, seed=18 + n_heads)
+    prompt = synth.prompt_tokens(30, cfg["vocab"], seed=10)
+    n_dec = 6
+    hist0, lg0, kc0, vc0 = run_gpu_decode(backend, dev, model, prompt, n_dec)
+    want, lg_ref, o = run_oracle_decode(orc, model, prompt, n_dec)
+    assert_same_tokens(hist0, want)
+    for s_ in range(len(lg_ref)):
+        assert_bits(lg0[s_], lg_ref[s_], f"logits at step {s_}")
+    assert np.array_equal(kc0, o.k_cache) and np.array_equal(vc0, o.v_cache)
+    first, lg_last, hist, kc, vc = run_gpu_prefill_decode(backend, dev, model, prompt, n_dec, [30])
+    P = len(prompt)
+    assert first == hist0[P - 1]
+    assert_bits(lg_last, lg0[P - 1], "logits at the last prompt position")
+    assert np.array_equal(kc, kc0) and np.array_equal(vc, vc0)
+    assert np.array_equal(hist[P:], hist0[P:])
 
 
 def test_gemma2_2b_shape_prefill_equals_fused_steps(backend, dev, synth):

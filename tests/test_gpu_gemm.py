@@ -62,6 +62,9 @@ def test_gemm_q4_0_prefill_512_bit_exact(backend, dev, orc, synth, rows, cols):
 @pytest.mark.parametrize("rows,cols,batch", [
     (32, 32, 1), (64, 64, 17), (96, 256, 33), (128, 2304, 100), (32, 96, 129), (256, 512, 255),
     (1024, 2304, 16), (64, 16384, 40),
+    # K tails of 5, 6 and 7 blocks past the last 8-block chunk (more tail
+    # blocks than B prefetch slots), with and without full chunks before them
+    (32, 160, 33), (64, 192, 40), (96, 224, 65), (32, 416, 7), (64, 480, 100), (32, 2272, 50),
 ])
 def test_gemm_q4_0_ragged_bit_exact(backend, dev, orc, synth, rows, cols, batch):
     rng = synth.rng_for(5100 + rows + cols + batch)

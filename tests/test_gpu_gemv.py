@@ -351,3 +351,39 @@ def test_invalid_shapes_are_rejected(backend, dev):
         dev.gemv_q4_k(wb, xb, yb, 1, 64)                 # Q4_K needs cols % 256 == 0
     assert e.value.status == -1
     dev.sync()                                           # context still healthy
+
+
+def test_bounded_wait_timeout_is_reported(backend, dev, orc, synth):
+    """Waits of one wave for others of its workgroup (LDS counters) are
+    bounded.  A wait that gives up must not hand back wrong data with a
+    success status: the kernel counts it on the device and the next sync
+    fails with MRML_HIP_E_HIP.  The host forces the condition (poll limit 0:
+    every wait gives up at once), so every kernel still runs to its end; with
+    the default restored the same ops are bit-exact again."""
+    rows, cols, dim = 2304, 9216, 2304   # the long-row down projection; the group-form rms_norm
+    rng = synth.rng_for(4100)
+    w = synth.q4_0_matrix(rng, rows, cols)
+    x = synth.normal_vector(rng, cols)
+    xn = (rng.standard_normal(dim) * 3.0).astype(np.float32)
+    wb = backend.HipBuffer.from_gguf(dev, w, backend.Q4_0, rows, cols)
+    xb, yb = upload(backend, dev, x), backend.HipBuffer.alloc(dev, rows)
+    nb, ob = upload(backend, dev, xn), backend.HipBuffer.alloc(dev, dim)
+    dev.sync()
+    dev.set_wait_limit(0)
+    try:
+        dev.gemv_q4_0(wb, xb, yb, rows, cols)
+        with pytest.raises(backend.HipError) as e:
+            dev.sync()
+        assert e.value.status == -3 and "gave up" in str(e.value) and "matvec" in str(e.value)
+        dev.rms_norm(nb, None, ob, dim, 1e-6)
+        with pytest.raises(backend.HipError) as e:
+            dev.sync()
+        assert e.value.status == -3 and "gave up" in str(e.value) and "decode" in str(e.value)
+    finally:
+        dev.set_wait_limit(-1)
+    dev.sync()                                           # the count was cleared by the failing sync
+    dev.gemv_q4_0(wb, xb, yb, rows, cols)
+    dev.rms_norm(nb, None, ob, dim, 1e-6)
+    dev.sync()
+    assert_bit_exact(yb.numpy(), orc.mat_vec_mul_q4_0(w, x, rows, cols, threads=THREADS), "q4_0 after the limit")
+    assert_bit_exact(ob.numpy(), orc.rms_norm(xn, None, 1e-6), "rms_norm after the limit")
