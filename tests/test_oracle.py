@@ -349,6 +349,92 @@ def test_rope_closed_forms(orc):
     assert abs(r[0] - (v[0] * math.cos(theta0) - v[128] * math.sin(theta0))) < 1e-5
 
 
+@pytest.mark.parametrize("pos", [1, 17, 511, 767])
+def test_rope_frequency_schedule(orc, pos):
+    """ops.rs:185-208: pair i of a head rotates by theta_i = pos * base^(-2i/d)
+    (NeoX halves: element i pairs with i + d/2).  Checked at every i against
+    float64 angles; the f32 angle is off by a few ulps of theta, so the bound
+    grows with theta.  A wrong exponent (i/d, 2i/(d-2)), a swapped sine, or
+    interleaved pairs fail it."""
+    hd, nh, base = 256, 3, 10000.0
+    rng = np.random.default_rng(40 + pos)
+    v = rng.standard_normal(nh * hd).astype(np.float32)
+    got = orc.rope_1d_batched(v, pos, nh, hd, base).reshape(nh, hd).astype(np.float64)
+    half = hd // 2
+    i = np.arange(half, dtype=np.float64)
+    theta = pos * base ** (-2.0 * i / hd)
+    c, s_ = np.cos(theta), np.sin(theta)
+    x = v.reshape(nh, hd).astype(np.float64)
+    ref0 = x[:, :half] * c - x[:, half:] * s_
+    ref1 = x[:, :half] * s_ + x[:, half:] * c
+    tol = (np.abs(x[:, :half]) + np.abs(x[:, half:])) * (4e-7 * (1.0 + theta)) + 1e-7
+    assert np.all(np.abs(got[:, :half] - ref0) <= tol)
+    assert np.all(np.abs(got[:, half:] - ref1) <= tol)
+    # the single-head form follows the same schedule
+    one = orc.rope_1d(v[:hd], pos, hd, base).astype(np.float64)
+    assert np.all(np.abs(one[:half] - ref0[0]) <= tol[0]) and np.all(np.abs(one[half:] - ref1[0]) <= tol[0])
+
+
+@pytest.mark.parametrize("dim", [4, 256, 2304])
+def test_rms_norm_weighted(orc, dim):
+    """ops.rs:24-49 with a weight: sum of squares accumulated in f32 in
+    order, scale = 1/sqrtf(sum/dim + eps), out = (x * scale) * w.  Bit-exact
+    against a numpy float32 loop (each op an IEEE single op), and within 2e-6
+    of the float64 x / rms(x) * w, so a dropped or misplaced w, eps outside
+    the root or a sum in another order fail it."""
+    rng = np.random.default_rng(50 + dim)
+    x = (rng.standard_normal(dim) * 3.0).astype(np.float32)
+    w = (1.0 + 0.5 * rng.standard_normal(dim)).astype(np.float32)
+    eps = np.float32(1e-6)
+    got = orc.rms_norm(x, w, 1e-6)
+    s = np.float32(0.0)
+    for xi in x:
+        s = np.float32(s + np.float32(xi * xi))
+    scale = np.float32(np.float32(1.0) / np.sqrt(np.float32(np.float32(s / np.float32(dim)) + eps)))
+    ref = ((x * scale).astype(np.float32) * w).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    x64 = x.astype(np.float64)
+    ref64 = x64 / np.sqrt(np.mean(x64 * x64) + 1e-6) * w.astype(np.float64)
+    assert np.max(np.abs(got - ref64)) <= 2e-6 * np.max(np.abs(ref64))
+    # the unweighted form is the weighted one with w = 1
+    assert np.array_equal(orc.rms_norm(x, None, 1e-6), orc.rms_norm(x, np.ones(dim, np.float32), 1e-6))
+
+
+def test_q4_0_dequantize_nibble_order(orc):
+    """quant.rs:135-163 on random blocks: the low nibble of byte j is weight
+    j, the high nibble weight j + 16, each (q - 8) * d with d the block's f16
+    scale (numpy's float16 widening).  An interleaved order (the reference's
+    own Q4_K dequantiser interleaves) or a missing offset fails it."""
+    rng = np.random.default_rng(60)
+    nb = 64
+    blocks = rng.integers(0, 256, (nb, 18), dtype=np.uint8)
+    d = (np.abs(rng.standard_normal(nb)) * 0.05).astype(np.float16)
+    blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    got = orc.dequantize_q4_0(blocks.reshape(-1), nb * 32).reshape(nb, 32)
+    qs = blocks[:, 2:].astype(np.int64)
+    q = np.concatenate([(qs & 15) - 8, (qs >> 4) - 8], axis=1).astype(np.float32)
+    ref = (q * d.astype(np.float32)[:, None]).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_geglu_argument_roles(orc):
+    """ops.rs:107-114: out = gelu_tanh(gate) * up, not gelu(up) * gate:
+    against float64 gelu on gate times up, on gate and up drawn from
+    different ranges.  Bound: 1e-6 relative (f32 rounding, glibc tanhf's
+    ulp) plus the cancellation of 1 + tanh(.) in f32 for large negative gate,
+    a few ulps of 1 times 0.5 |gate up|."""
+    rng = np.random.default_rng(70)
+    g = (rng.standard_normal(4096) * 2.0).astype(np.float32)
+    u = (rng.standard_normal(4096) * 0.1 + 0.3).astype(np.float32)
+    got = orc.geglu(g, u).astype(np.float64)
+    g64 = g.astype(np.float64)
+    gelu = 0.5 * g64 * (1.0 + np.tanh(0.7978845608 * (g64 + 0.044715 * g64 ** 3)))
+    ref = gelu * u.astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 1e-6 * np.abs(ref) + 2e-7 * np.abs(g64 * u))
+    swapped = orc.geglu(u, g).astype(np.float64)
+    assert np.max(np.abs(swapped - ref)) > 1e-2
+
+
 def test_softmax_closed_forms(orc):
     assert np.allclose(orc.softmax(np.full(7, 3.0, dtype=np.float32)), 1 / 7, rtol=1e-6)
     s = orc.softmax(np.array([0.0, np.log(3.0)], dtype=np.float32))
