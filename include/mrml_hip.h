@@ -232,6 +232,21 @@ int mrml_hip_quantize_q8_0_gemm(mrml_hip_ctx *ctx, const float *d_x, void *d_gpa
 int mrml_hip_gemm_q4_0_gpack(mrml_hip_ctx *ctx, const void *d_w, const void *d_gpack, float *d_y,
                              int32_t rows, int32_t cols, int32_t batch);
 
+/* As mrml_hip_gemm_q4_0 (same arguments, same bit-identical outputs), but
+ * it allocates nothing: no hipMalloc, no workspace growth.  No counterpart in
+ * the reference; it is for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation).
+ * The GEMM pack of the activations goes to a fixed device scratch of
+ * mrml_hip_gemm_q4_0_noalloc_max_pack_bytes() bytes (8 MiB: batch up to 3232
+ * tokens at cols 2304, 800 at cols 9216), one per GPU for the life of the
+ * process; shapes whose pack, mrml_hip_gemm_pack_bytes(cols, batch), is
+ * larger fail with MRML_HIP_E_INVALID.  Every call on a GPU shares that
+ * scratch, so calls that overlap on one GPU (several contexts or streams at
+ * once) race; calls ordered on one context are safe. */
+int mrml_hip_gemm_q4_0_noalloc(mrml_hip_ctx *ctx, const void *d_w, const float *d_x, float *d_y,
+                               int32_t rows, int32_t cols, int32_t batch);
+size_t mrml_hip_gemm_q4_0_noalloc_max_pack_bytes(void);
+
 /* Greedy pick over n f32 scores (model.rs:2869-2888; GPU tie rule
  * kernels.rs:1144-1145): index of the maximum, lowest index on ties, NaN
  * never wins.  d_out: one int32 on the device. */

@@ -139,6 +139,8 @@ _SIGNATURES = {
     "mrml_hip_gemv_q4_k": [_P, _P, _P, _P, _I, _I],
     "mrml_hip_gemm_q4_0": [_P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemm_q4_0_q8": [_P, _P, _P, _P, _I, _I, _I],
+    "mrml_hip_gemm_q4_0_noalloc": [_P, _P, _P, _P, _I, _I, _I],
+    "mrml_hip_gemm_q4_0_noalloc_max_pack_bytes": [],
     "mrml_hip_gemm_pack_bytes": [_I, _I],
     "mrml_hip_quantize_q8_0_gemm": [_P, _P, _P, _I, _I],
     "mrml_hip_gemm_q4_0_gpack": [_P, _P, _P, _P, _I, _I, _I],
@@ -161,6 +163,7 @@ _RESTYPE = {
     "mrml_hip_stream": _P,
     "mrml_hip_q8_0_pack_bytes": _Z,
     "mrml_hip_gemm_pack_bytes": _Z,
+    "mrml_hip_gemm_q4_0_noalloc_max_pack_bytes": _Z,
 }
 
 _lib = None
@@ -373,6 +376,15 @@ class HipDevice:
 
     def gemm_q4_0(self, w, x, y, rows: int, cols: int, batch: int) -> None:
         self._check(self.lib.mrml_hip_gemm_q4_0(self.ctx, _ptr(w), _ptr(x), _ptr(y), rows, cols, batch))
+
+    def gemm_q4_0_noalloc(self, w, x, y, rows: int, cols: int, batch: int) -> None:
+        """gemm_q4_0 without any allocation: the activations' GEMM pack goes to
+        the library's fixed per-GPU device scratch (calls overlapping on one
+        GPU race)."""
+        self._check(self.lib.mrml_hip_gemm_q4_0_noalloc(self.ctx, _ptr(w), _ptr(x), _ptr(y), rows, cols, batch))
+
+    def gemm_q4_0_noalloc_max_pack_bytes(self) -> int:
+        return int(self.lib.mrml_hip_gemm_q4_0_noalloc_max_pack_bytes())
 
     def gemm_q4_0_q8(self, w, xpack, y, rows: int, cols: int, batch: int) -> None:
         self._check(self.lib.mrml_hip_gemm_q4_0_q8(self.ctx, _ptr(w), _ptr(xpack), _ptr(y), rows, cols, batch))

@@ -40,6 +40,8 @@
 //     registers one chunk ahead, turned into signed bytes once (both K
 //     halves) and staged through kNBuf LDS buffers, one barrier per chunk.
 
+#include <mutex>
+
 #include "device.h"
 #include "internal.h"
 
@@ -264,7 +266,42 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
     }
 }
 
+// Device scratch of the allocation-free GEMM entry point
+// (mrml_hip_gemm_q4_0_noalloc): the GEMM pack of its activations lives in
+// this file-scope array, one copy per GPU, held until the process ends.  Host
+// code never passes the array's name to a kernel (on the host it is a
+// stand-in, not a device address): gemm_noalloc_scratch() resolves each
+// device's address once, with hipGetSymbolAddress, and launches take that.
+// Every call on a GPU shares its copy, so calls that overlap on one GPU race.
+// Each call writes the whole pack it reads (tokens past the batch as zeros),
+// so nothing has to start zeroed.
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) uint8_t gemm_noalloc_scratch_buf[kNoAllocScratchBytes];
+
 }  // namespace
+
+size_t gemm_noalloc_scratch_bytes() { return kNoAllocScratchBytes; }
+
+int gemm_noalloc_scratch(mrml_hip_ctx *ctx, void **out)
+{
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void *addr[kMaxDevices];
+    *out = nullptr;
+    if (ctx->device < 0 || ctx->device >= kMaxDevices)
+        return fail(ctx, MRML_HIP_E_UNSUPPORTED, "gemm scratch: device index %d above %d", ctx->device, kMaxDevices);
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[ctx->device]) {
+        // The context's device is current (every entry point makes it so).
+        void *p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(gemm_noalloc_scratch_buf));
+        if (e != hipSuccess) return hip_fail(ctx, e, "hipGetSymbolAddress (gemm scratch)");
+        if (!p) return fail(ctx, MRML_HIP_E_HIP, "hipGetSymbolAddress (gemm scratch) returned null");
+        addr[ctx->device] = p;
+    }
+    *out = addr[ctx->device];
+    return MRML_HIP_OK;
+}
 
 bool gemm_shape_ok(int32_t rows, int32_t cols, int32_t batch)
 {

@@ -14,6 +14,7 @@ struct mrml_hip_ctx {
     hipDeviceProp_t props{};
     void *ws = nullptr;     // scratch: activation packs and partial results
     size_t ws_bytes = 0;
+    void *noalloc_scratch = nullptr;  // the device's copy of the allocation-free GEMM's scratch
     std::string err;
 };
 
@@ -75,6 +76,10 @@ bool gemm_shape_ok(int32_t rows, int32_t cols, int32_t batch);
 size_t gemm_pack_bytes(int32_t cols, int32_t batch);
 int launch_gemm_pack_quantize(mrml_hip_ctx *ctx, const float *x, void *gpack, int32_t cols, int32_t batch);
 int launch_gemm_pack_from_act(mrml_hip_ctx *ctx, const void *pack, void *gpack, int32_t cols, int32_t batch);
+// The allocation-free GEMM's file-scope device scratch: its size, and its
+// address on the context's device (resolved once per device; 0 or a status).
+size_t gemm_noalloc_scratch_bytes();
+int gemm_noalloc_scratch(mrml_hip_ctx *ctx, void **out);
 // y row stride ldy floats (0: rows; a multiple of 4, y 16-byte aligned)
 int launch_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const void *gpack, float *y, int32_t rows, int32_t cols,
                      int32_t batch, int32_t ldy = 0);

@@ -154,6 +154,12 @@ int mrml_hip_create(int32_t device, mrml_hip_ctx **out)
         delete ctx;
         return MRML_HIP_E_HIP;
     }
+    // The device address of the allocation-free GEMM's scratch (once per device).
+    if (gemm_noalloc_scratch(ctx, &ctx->noalloc_scratch) != MRML_HIP_OK) {
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return MRML_HIP_E_HIP;
+    }
     *out = ctx;
     return MRML_HIP_OK;
 }
@@ -538,6 +544,24 @@ int mrml_hip_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const float *x, float *
     int rc = launch_gemm_pack_quantize(ctx, x, gp, cols, batch);
     return rc ? rc : launch_gemm_q4_0(ctx, w, gp, y, rows, cols, batch);
 }
+
+int mrml_hip_gemm_q4_0_noalloc(mrml_hip_ctx *ctx, const void *w, const float *x, float *y, int32_t rows,
+                               int32_t cols, int32_t batch)
+{
+    CTX_GUARD(ctx);
+    CHECK_GEMM(ctx, w, x, y, rows, cols, batch);
+    const size_t need = gemm_pack_bytes(cols, batch);
+    REQUIRE(ctx, need <= gemm_noalloc_scratch_bytes(),
+            "gemm_q4_0_noalloc: cols=%d batch=%d needs a %zu-byte GEMM pack, above the %zu-byte device scratch "
+            "(at most %zu token groups of 32 x cols/32 blocks x 1152 bytes)",
+            cols, batch, need, gemm_noalloc_scratch_bytes(), gemm_noalloc_scratch_bytes() / ((size_t)(cols / 32) * 1152));
+    void *gp = ctx->noalloc_scratch;
+    if (!gp) return fail(ctx, MRML_HIP_E_HIP, "gemm_q4_0_noalloc: the device scratch address is unknown");
+    int rc = launch_gemm_pack_quantize(ctx, x, gp, cols, batch);
+    return rc ? rc : launch_gemm_q4_0(ctx, w, gp, y, rows, cols, batch);
+}
+
+size_t mrml_hip_gemm_q4_0_noalloc_max_pack_bytes(void) { return gemm_noalloc_scratch_bytes(); }
 
 int mrml_hip_gemm_q4_0_q8(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows,
                           int32_t cols, int32_t batch)
