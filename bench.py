@@ -6,11 +6,19 @@ Gemma-2-2B FFN shapes.  One step = one FFN pass over synthetic data:
     quantize x (2304)  ->  fused gate+up GeGLU matvec (2 x 9216x2304)
     quantize act (9216) ->  down matvec (2304x9216)
 `value` is whole-step throughput in GB/s of algorithmic bytes (weights +
-vectors), with weights resident in HBM and rotated over enough copies to
-exceed the 256 MB MALL, timed with HIP events around a graph of the steps.
-The JSON line also carries the per-matrix GB/s (gate, up, down, fused
-gate+up), the dominant kernel's roofline, and the host-CPU baseline (the C
-oracle restating the reference CPU path, timed on this box's cores).
+vectors), with weights resident in HBM and rotated over a pool of 48
+matrices (573 MB, more than twice the 256 MB MALL), timed with HIP events
+around graph replays: W warm-up steps, then timed regions of exactly K steps
+each (as many regions as it takes to time at least 100 launches, at least 5);
+`value` is the median region, the minimum is reported beside it.  The JSON
+line also carries the per-matrix GB/s (gate, up, down, fused gate+up, each
+rotated over the whole pool), the dominant kernel's roofline, and the
+host-CPU baseline (the C oracle restating the reference CPU path, timed on
+this box's cores).
+
+BASELINE configs[0] (Q8_0 2048x2048) and configs[2] (Q4_K 256000x2304 and
+its greedy argmax) are in "q8_0" and "q4_k", each with GB/s, % of peak and
+its own CPU baseline.
 
 The second half of the metric is in "decode": greedy decode tok/s
 of a random-init Gemma-2-2B-shape Q4_0 model (512-token prefill, 256 decode
@@ -99,6 +107,29 @@ def time_graph(dev, ev, graph, launches: int) -> float:
     return ev.elapsed_ms(a, b) / 1e3
 
 
+def sample_launches(dev, ev, graph, per_graph: int, samples: int = 7, min_launches: int = 100) -> dict:
+    """`samples` timings, each of enough replays of `graph` (per_graph launches
+    of one kernel each) for at least min_launches launches; median and min
+    seconds per launch."""
+    reps = max(1, -(-min_launches // per_graph))
+    time_graph(dev, ev, graph, 1)
+    t = sorted(time_graph(dev, ev, graph, reps) / (reps * per_graph) for _ in range(samples))
+    return {"median_s": t[len(t) // 2], "min_s": t[0], "launches_per_sample": reps * per_graph,
+            "samples": samples}
+
+
+def kernel_source_hash(files=("gemv_q4_0.hip", "device.h", "exact_sum.h", "norm_block.h", "libm_f32.h",
+                              "internal.h")) -> str:
+    """sha256 (16 hex digits) of the sources the Q4_0 matvec kernels are built
+    from: a committed counter reading applies only to the kernels it measured."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in files:
+        h.update(f.encode())
+        h.update((PKG / "csrc" / f).read_bytes())
+    return h.hexdigest()[:16]
+
+
 def cpu_baseline(orc, synth, budget_s: float) -> dict:
     """The oracle (reference CPU algorithm, VNNI path where the host has it,
     row-parallel like parallel.rs) on one FFN step, best of N wall-clock
@@ -141,7 +172,7 @@ def measured_traffic(kernel: str):
         d = json.loads(path.read_text())
     except (OSError, ValueError):
         return None
-    if d.get("kernel") != kernel:
+    if d.get("kernel") != kernel or d.get("source_sha256_16") != kernel_source_hash():
         return None
     return d.get("traffic_bytes")
 
@@ -303,12 +334,12 @@ def gemm_bench(be, synth, dev, ev, batch: int, cpu_tokens: int, profile: int = 0
     per_graph = 10  # launches per graph, so host-side graph launch cost stays hidden
     for k, (r, c) in mats.items():
         g = dev.capture(lambda: [dev.gemm_q4_0_gpack(w[k], packs[c], y, r, c, batch) for _ in range(per_graph)])
-        time_graph(dev, ev, g, 2)
-        n = 5
-        secs = time_graph(dev, ev, g, n) / (n * per_graph)
+        st = sample_launches(dev, ev, g, per_graph)
         g.close()
+        secs = st["median_s"]
         ops = 2 * batch * r * c
-        per[k] = {"us": round(secs * 1e6, 2), "tops": round(ops / secs / 1e12, 2)}
+        per[k] = {"us": round(secs * 1e6, 2), "us_min": round(st["min_s"] * 1e6, 2), "tops": round(ops / secs / 1e12, 2),
+                  "launches_per_sample": st["launches_per_sample"]}
         total_ops += ops
         total_s += secs
     # quantising the [M][K] activations into the GEMM pack (once per input)
@@ -340,13 +371,181 @@ def gemm_bench(be, synth, dev, ev, batch: int, cpu_tokens: int, profile: int = 0
     return out
 
 
+def cpu_best_of(fn, budget_s: float) -> tuple[float, int]:
+    """Best-of-N wall clock of fn() (benches/hot_paths.rs:21-30) over about
+    budget_s seconds (at least 3 rounds)."""
+    fn()
+    best, rounds, t_end = float("inf"), 0, time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or rounds < 3:
+        t0 = time.perf_counter()
+        fn()
+        best = min(best, time.perf_counter() - t0)
+        rounds += 1
+    return best, rounds
+
+
+def q8_0_bench(be, synth, dev, ev, cpu_s: float) -> dict:
+    """Q8_0 2048x2048 batch-1 matvec, x quantised once by
+    the reference routine, weights rotated over 128 copies (570 MB, more than
+    twice the MALL).  Bytes per run as the survey states them: W + x (f32) +
+    y (f32)."""
+    rows = cols = 2048
+    nbytes_w = rows * cols // 32 * 34
+    nbytes = nbytes_w + cols * 4 + rows * 4
+    rng = synth.rng_for(1)
+    w = synth.q8_0_matrix(rng, rows, cols)
+    x = synth.normal_vector(rng, cols)
+    first = be.HipBuffer.from_gguf(dev, w, be.Q8_0, rows, cols)
+    copies = 128
+    pool = [first] + [be.HipBuffer(dev, first.nbytes) for _ in range(copies - 1)]
+    for b in pool[1:]:
+        dev.copy_kernel(b, first, first.nbytes)
+    xb = be.HipBuffer.from_host(dev, x)
+    pk = be.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(cols), np.uint8)
+    y = be.HipBuffer.alloc(dev, rows)
+    dev.quantize_q8_0(xb, None, pk, cols)
+    dev.sync()
+    g = dev.capture(lambda: [dev.gemv_q8_0_q8(b, pk, y, rows, cols) for b in pool])
+    st = sample_launches(dev, ev, g, copies)
+    g.close()
+    gbs = nbytes / st["median_s"] / 1e9
+    out = {"gb_s": round(gbs, 1), "gb_s_best": round(nbytes / st["min_s"] / 1e9, 1),
+           "pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2), "us_median": round(st["median_s"] * 1e6, 3),
+           "us_min": round(st["min_s"] * 1e6, 3), "bytes_per_launch": nbytes, "kernel": "gemv_q8_0_kernel",
+           "launches_per_sample": st["launches_per_sample"], "rotating_copies": copies,
+           "workload": "BASELINE configs[0]: Q8_0 2048x2048, batch 1, x pre-quantised (Q8_0 pack), "
+                       "hipEvent around graph replays over 128 weight copies"}
+    for b in pool[1:]:
+        b.close()
+    if cpu_s > 0:
+        sys.path.insert(0, str(ROOT))
+        from oracle import orc
+        threads = len(os.sched_getaffinity(0))
+        xq = orc.quantize_q8_0(x)
+        best, rounds = cpu_best_of(lambda: orc.mat_vec_mul_q8_0_q8_0(w, xq, rows, cols, threads=threads), cpu_s)
+        isa = {2: "avx-vnni", 1: "avx2", 0: "scalar"}[orc.host_isa()]
+        out["cpu_baseline"] = {"value": round(nbytes / best / 1e9, 2), "unit": "GB/s", "cores": threads,
+                               "kind": "port", "sample": f"{rounds} matvecs 2048x2048 (vec_dot_q8_0_q8_0 per row, "
+                                                         f"{isa} path), best-of wall clock, {threads} threads"}
+    return out
+
+
+def q4_k_bench(be, synth, dev, ev, cpu_s: float) -> dict:
+    """Q4_K 256000x2304 batch-1 matvec (331.8 MB, two
+    copies alternated so no launch finds its weights in the MALL) and the
+    greedy argmax over the 256000 logits."""
+    rows, cols = 256000, 2304
+    nbytes_w = rows * cols // 256 * 144
+    nbytes = nbytes_w + cols * 4 + rows * 4
+    rng = synth.rng_for(3)
+    w = synth.q4_k_matrix(rng, rows, cols)
+    x = synth.normal_vector(rng, cols)
+    first = be.HipBuffer.from_gguf(dev, w, be.Q4_K, rows, cols)
+    second = be.HipBuffer(dev, first.nbytes)
+    dev.copy_kernel(second, first, first.nbytes)
+    pool = [first, second]
+    xb = be.HipBuffer.from_host(dev, x)
+    pk = be.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(cols), np.uint8)
+    y = be.HipBuffer.alloc(dev, rows)
+    am = be.HipBuffer.alloc(dev, 1, np.int32)
+    dev.quantize_q8_0(xb, None, pk, cols)
+    dev.argmax_f32(y, rows, am)                       # sizes the argmax scratch before capture
+    dev.sync()
+    # Timing: 7 samples of 20 launches (the two copies alternating) issued
+    # eagerly on the library's stream -- how a standalone matvec call runs;
+    # at 52 us a launch the host stays far ahead of the device.  The same 20
+    # launches replayed from a graph are reported beside it: on this GPU a
+    # graph replay of this kernel takes about 6 us a launch longer (kernel
+    # trace durations agree with the eager figure).
+    per = 20
+
+    def eager(fn):
+        te = []
+        for _ in range(8):
+            a, b = ev.new(), ev.new()
+            dev.sync()
+            ev.record(a, dev.stream)
+            for i in range(per):
+                fn(i)
+            ev.record(b, dev.stream)
+            te.append(ev.elapsed_ms(a, b) / 1e3 / per)
+        te = sorted(te[1:])                           # the first sample warms up
+        return {"median_s": te[len(te) // 2], "min_s": te[0], "launches_per_sample": per, "samples": len(te)}
+
+    mv = lambda i: dev.gemv_q4_k_q8(pool[i % 2], pk, y, rows, cols)
+    st = eager(mv)
+    ga = dev.capture(lambda: [dev.argmax_f32(y, rows, am) for _ in range(10)])  # 7.5 us: replayed, not host-bound
+    sa = sample_launches(dev, ev, ga, 10)
+    ga.close()
+    sb = eager(lambda i: (mv(i), dev.argmax_f32(y, rows, am)))
+    g = dev.capture(lambda: [mv(i) for i in range(per)])
+    sg = sample_launches(dev, ev, g, per)
+    g.close()
+    dev.sync()
+    gbs = nbytes / st["median_s"] / 1e9
+    out = {"gb_s": round(gbs, 1), "gb_s_best": round(nbytes / st["min_s"] / 1e9, 1),
+           "pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2), "us_median": round(st["median_s"] * 1e6, 3),
+           "us_min": round(st["min_s"] * 1e6, 3), "bytes_per_launch": nbytes, "kernel": "gemv_q4_k_kernel",
+           "argmax_us": round(sa["median_s"] * 1e6, 3),
+           "matvec_plus_argmax_us": round(sb["median_s"] * 1e6, 3),
+           "matvec_plus_argmax_gb_s": round(nbytes / sb["median_s"] / 1e9, 1),
+           "graph_replay": {"us_median": round(sg["median_s"] * 1e6, 3), "us_min": round(sg["min_s"] * 1e6, 3),
+                            "gb_s": round(nbytes / sg["median_s"] / 1e9, 1)},
+           "argmax": int(am.numpy()[0]), "launches_per_sample": per, "samples": st["samples"],
+           "workload": "BASELINE configs[2]: Q4_K 256000x2304 (GGUF super-blocks), batch 1, x pre-quantised, "
+                       "then the greedy argmax; hipEvent around 20 eager launches alternating 2 weight copies "
+                       "(663 MB), median of 7 samples"}
+    second.close()
+    if cpu_s > 0:
+        sys.path.insert(0, str(ROOT))
+        from oracle import orc
+        threads = len(os.sched_getaffinity(0))
+        xq = orc.quantize_q8_0(x)
+        sub = 32000                                   # a row sample: 1/8 of the matrix
+        ws = w[:sub * (cols // 256) * 144]
+        best, rounds = cpu_best_of(lambda: orc.mat_vec_mul_q4_k_q8_0(ws, xq, sub, cols, threads=threads), cpu_s)
+        sbytes = sub * cols // 256 * 144 + cols * 4 + sub * 4
+        out["cpu_baseline"] = {"value": round(sbytes / best / 1e9, 2), "unit": "GB/s", "cores": threads,
+                               "kind": "port", "sample": f"{rounds} matvecs over the first {sub} rows (the oracle's "
+                                                         f"Q4_K dot; the reference has none), best-of wall clock, "
+                                                         f"{threads} threads"}
+    return out
+
+
+def lmhead_profile(be, synth, dev, n: int) -> dict:
+    """Profiling aid for BASELINE configs[2]: n launches each of the Q4_K
+    256000x2304 matvec and, for comparison, the Q4_0 matvec of the same shape
+    (the tied LM head of configs[3]), each alternating two weight copies."""
+    rows, cols = 256000, 2304
+    rng = synth.rng_for(3)
+    x = synth.normal_vector(rng, cols)
+    wk = be.HipBuffer.from_gguf(dev, synth.q4_k_matrix(rng, rows, cols), be.Q4_K, rows, cols)
+    w0 = be.HipBuffer.from_gguf(dev, synth.q4_0_matrix(rng, rows, cols), be.Q4_0, rows, cols)
+    wk2, w02 = be.HipBuffer(dev, wk.nbytes), be.HipBuffer(dev, w0.nbytes)
+    dev.copy_kernel(wk2, wk, wk.nbytes)
+    dev.copy_kernel(w02, w0, w0.nbytes)
+    xb = be.HipBuffer.from_host(dev, x)
+    pk = be.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(cols), np.uint8)
+    y = be.HipBuffer.alloc(dev, rows)
+    dev.quantize_q8_0(xb, None, pk, cols)
+    for i in range(n):
+        dev.gemv_q4_k_q8(wk if i % 2 == 0 else wk2, pk, y, rows, cols)
+    for i in range(n):
+        dev.gemv_q4_0_q8(w0 if i % 2 == 0 else w02, pk, y, rows, cols)
+    dev.sync()
+    return {"profile_lmhead": n, "launches": 2 * n}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sets", type=int, default=0, help="rotating weight sets (default: > 2x MALL)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds-small", type=float, default=3.0, help="CPU baseline budget of the C1 and C3 legs")
+    ap.add_argument("--no-q8", action="store_true", help="skip BASELINE configs[0] (Q8_0 2048x2048)")
+    ap.add_argument("--no-q4k", action="store_true", help="skip BASELINE configs[2] (Q4_K 256000x2304 + argmax)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-loop", type=int, default=0,
                     help="only replay the GeGLU kernel graph this many times (for rocprofv3)")
@@ -361,6 +560,8 @@ def main() -> int:
                     help="profiling aid: prefill, then N eager decode steps of the C4 model, then exit")
     ap.add_argument("--profile-prefill", type=int, default=0,
                     help="profiling aid: one chunked prefill of N tokens of the C4 model, then exit")
+    ap.add_argument("--profile-lmhead", type=int, default=0,
+                    help="profiling aid: N launches each of the Q4_K and Q4_0 256000x2304 matvecs, then exit")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--cpu-gemm-tokens", type=int, default=64)
     args = ap.parse_args()
@@ -380,16 +581,23 @@ def main() -> int:
     if args.profile_decode:
         print(json.dumps(decode_profile(be, synth, dev, args.decode_prefill, args.profile_decode)))
         return 0
+    if args.profile_lmhead:
+        print(json.dumps(lmhead_profile(be, synth, dev, args.profile_lmhead)))
+        return 0
     if args.profile_prefill:
         print(json.dumps(prefill_profile(be, synth, dev, args.profile_prefill)))
         return 0
 
-    # ---- synthetic config-2 data, rotated over > 2x MALL of distinct copies
+    # ---- synthetic config-2 data: a pool of 48 matrices (16 copies each of
+    # gate, up and down; 573 MB, more than twice the MALL).  FFN step i uses
+    # pool entries 3j, 3j+1, 3j+2 with j = i mod 16; the per-matrix rates
+    # rotate one kernel over all 48 entries (the three matrices have the same
+    # bytes, and the timing does not depend on the values).
     rng = synth.rng_for(2)
     host = {"g": synth.q4_0_matrix(rng, FFN, DIM), "u": synth.q4_0_matrix(rng, FFN, DIM),
             "d": synth.q4_0_matrix(rng, DIM, FFN)}
     x = synth.rms_normalised(synth.normal_vector(rng, DIM))
-    sets = args.sets or int(np.ceil(2 * MALL_BYTES / (3 * W_BYTES))) + 1
+    sets = args.sets or int(np.ceil(2 * MALL_BYTES / (3 * W_BYTES)))
     first = {"g": be.HipBuffer.from_gguf(dev, host["g"], be.Q4_0, FFN, DIM),
              "u": be.HipBuffer.from_gguf(dev, host["u"], be.Q4_0, FFN, DIM),
              "d": be.HipBuffer.from_gguf(dev, host["d"], be.Q4_0, DIM, FFN)}
@@ -399,6 +607,7 @@ def main() -> int:
         for k in s:
             dev.copy_kernel(s[k], first[k], first[k].nbytes)
         rot.append(s)
+    pool = [s[k] for s in rot for k in ("g", "u", "d")]
     bx = be.HipBuffer.from_host(dev, x)
     act = be.HipBuffer.alloc(dev, FFN)
     y = be.HipBuffer.alloc(dev, DIM)
@@ -410,49 +619,76 @@ def main() -> int:
     def ffn_step(s):
         dev.ffn_geglu_q4_0(s["g"], s["u"], s["d"], bx, None, y, DIM, FFN)
 
-    # one graph = one step over every rotating set
     for s in rot:
         ffn_step(s)
     dev.sync()
-    g_step = dev.capture(lambda: [ffn_step(s) for s in rot])
+    graphs = {}
+
+    def steps_graph(n):
+        """A graph of n consecutive FFN steps (n <= sets), cached."""
+        if n not in graphs:
+            graphs[n] = dev.capture(lambda: [ffn_step(rot[i]) for i in range(n)])
+        return graphs[n]
+
+    def run_steps(n):
+        for _ in range(n // sets):
+            steps_graph(sets).launch()
+        if n % sets:
+            steps_graph(n % sets).launch()
+
     q_pack = be.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(DIM), np.uint8)
     dev.quantize_q8_0(bx, None, q_pack, DIM)
     a_pack = be.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(FFN), np.uint8)
-    g_geglu = dev.capture(lambda: [dev.gemv_q4_0_geglu_pack(s["g"], s["u"], bx, None, a_pack, FFN, DIM) for s in rot])
+    g_geglu = dev.capture(lambda: [dev.gemv_q4_0_geglu_pack(pool[2 * i], pool[2 * i + 1], bx, None, a_pack, FFN, DIM)
+                                   for i in range(len(pool) // 2)])
 
     if args.profile_loop:
         for _ in range(args.profile_loop):
             g_geglu.launch()
         dev.sync()
-        print(json.dumps({"profile_loop": args.profile_loop, "launches": args.profile_loop * sets}))
+        print(json.dumps({"profile_loop": args.profile_loop, "launches": args.profile_loop * len(pool) // 2,
+                          "source_sha256_16": kernel_source_hash()}))
         return 0
 
-    # ---- warmup, then exactly K steps between events
-    reps_w = max(1, args.warmup // sets)
-    reps = max(1, args.steps // sets)
-    steps = reps * sets
-    time_graph(dev, ev, g_step, reps_w)
-    t = time_graph(dev, ev, g_step, reps)
-    ms_per_step = t / steps * 1e3
-    value = BYTES_STEP * steps / t / 1e9
+    # ---- W warm-up steps, then timed regions of exactly K steps each
+    K, W = args.steps, args.warmup
+    run_steps(W)
+    steps_graph(sets)
+    if K % sets:
+        steps_graph(K % sets)
+    regions = max(5, -(-100 // (2 * K)))
+    times = []
+    for _ in range(regions):
+        a, b = ev.new(), ev.new()
+        dev.sync()
+        ev.record(a, dev.stream)
+        run_steps(K)
+        ev.record(b, dev.stream)
+        times.append(ev.elapsed_ms(a, b) / 1e3)
+    dev.sync()
+    times.sort()
+    t_med, t_min = times[len(times) // 2], times[0]
+    ms_per_step = t_med / K * 1e3
+    value = BYTES_STEP * K / t_med / 1e9
 
-    # ---- per-kernel rates (each timed alone over the rotating sets)
-    def rate(fn, nbytes, per_graph):
-        g = dev.capture(lambda: [fn(s) for s in rot])
-        time_graph(dev, ev, g, 3)
-        launches = max(5, 400 // per_graph)
-        secs = time_graph(dev, ev, g, launches) / (launches * per_graph)
+    # ---- per-kernel rates, each kernel rotated over the whole pool
+    def rate(fn, nbytes, n):
+        g = dev.capture(lambda: [fn(i) for i in range(n)])
+        st = sample_launches(dev, ev, g, n)
         g.close()
-        return secs, nbytes / secs / 1e9
+        return st, nbytes / st["median_s"] / 1e9
 
     out_f = be.HipBuffer.alloc(dev, FFN)
-    # the step's first launch (f32 x in, activation pack out)
-    k_geglu, gbs_geglu = rate(lambda s: dev.gemv_q4_0_geglu_pack(s["g"], s["u"], bx, None, a_pack, FFN, DIM),
-                              BYTES_GEGLU, sets)
-    k_gate, gbs_gate = rate(lambda s: dev.gemv_q4_0_q8(s["g"], q_pack, out_f, FFN, DIM), BYTES_GATE, sets)
-    k_up, gbs_up = rate(lambda s: dev.gemv_q4_0_q8(s["u"], q_pack, out_f, FFN, DIM), BYTES_GATE, sets)
+    npool = len(pool)
+    # the step's first launch (f32 x in, activation pack out), over gate/up pairs of the pool
+    st_geglu, gbs_geglu = rate(lambda i: dev.gemv_q4_0_geglu_pack(pool[2 * i], pool[2 * i + 1], bx, None, a_pack,
+                                                                  FFN, DIM), BYTES_GEGLU, npool // 2)
+    st_gate, gbs_gate = rate(lambda i: dev.gemv_q4_0_q8(pool[i], q_pack, out_f, FFN, DIM), BYTES_GATE, npool)
+    st_up, gbs_up = rate(lambda i: dev.gemv_q4_0_q8(pool[(i + 1) % npool], q_pack, out_f, FFN, DIM), BYTES_GATE,
+                         npool)
     # the step's second launch (activation pack in)
-    k_down, gbs_down = rate(lambda s: dev.gemv_q4_0_q8(s["d"], a_pack, y, DIM, FFN), BYTES_DOWN, sets)
+    st_down, gbs_down = rate(lambda i: dev.gemv_q4_0_q8(pool[i], a_pack, y, DIM, FFN), BYTES_DOWN, npool)
+    k_geglu = st_geglu["median_s"]
     # stream-copy ceiling on a buffer well above the MALL
     cbytes = 1 << 30
     src, dst = be.HipBuffer(dev, cbytes), be.HipBuffer(dev, cbytes)
@@ -460,6 +696,18 @@ def main() -> int:
     time_graph(dev, ev, gc, 2)
     tc = time_graph(dev, ev, gc, 10) / 10
     copy_gbs = 2 * cbytes / tc / 1e9
+    gc.close()
+    # launch floor inside a graph, with product kernels: a 256-byte zero fill
+    # (no memory traffic to speak of) and a copy of one 11.94 MB matrix
+    zb = be.HipBuffer(dev, 256)
+    gz = dev.capture(lambda: [dev.zero(zb, 256) for _ in range(100)])
+    st_zero = sample_launches(dev, ev, gz, 100)
+    gz.close()
+    ncp = 24
+    gcp = dev.capture(lambda: [dev.copy_kernel(dst.ptr + i * W_BYTES, src.ptr + i * W_BYTES, W_BYTES)
+                               for i in range(ncp)])
+    st_copy = sample_launches(dev, ev, gcp, ncp)
+    gcp.close()
     dev.sync()
 
     cpu = None
@@ -467,11 +715,13 @@ def main() -> int:
         sys.path.insert(0, str(ROOT))
         from oracle import orc
         cpu = cpu_baseline(orc, synth, args.cpu_seconds)
-    # release the FFN bench buffers before the full model
-    del rot, first, src, dst
-    g_step.close()
+    # release the FFN bench buffers before the other legs
+    for g_ in graphs.values():
+        g_.close()
     g_geglu.close()
-    gc.close()
+    del rot, first, pool, src, dst
+    q8 = None if args.no_q8 else q8_0_bench(be, synth, dev, ev, 0 if args.no_cpu else args.cpu_seconds_small)
+    q4k = None if args.no_q4k else q4_k_bench(be, synth, dev, ev, 0 if args.no_cpu else args.cpu_seconds_small)
     gemm = None
     if not args.no_gemm:
         gemm = gemm_bench(be, synth, dev, ev, args.gemm_batch, 0 if args.no_cpu else args.cpu_gemm_tokens)
@@ -485,8 +735,8 @@ def main() -> int:
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": steps,
-        "warmup": reps_w * sets,
+        "steps": K,
+        "warmup": W,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -495,18 +745,31 @@ def main() -> int:
         "data": "synthetic (seeded GGUF Q4_0 bytes, N(0,1) RMS-normalised x)",
         "config": {"workload": "BASELINE configs[1]: Q4_0 gate/up 9216x2304 + down 2304x9216, batch 1",
                    "bytes_per_step": BYTES_STEP, "rotating_weight_sets": sets,
-                   "rotating_bytes": sets * 3 * W_BYTES, "timing": "hipEvent around graph replays"},
+                   "rotating_bytes": sets * 3 * W_BYTES,
+                   "timing": f"hipEvent around graph replays: {W} warm-up steps, then {regions} timed regions of "
+                             f"exactly {K} steps (2 launches each); value from the median region"},
+        "timed_regions": regions,
+        "ms_per_step_min": round(t_min / K * 1e3, 5),
+        "value_best": round(BYTES_STEP * K / t_min / 1e9, 2),
         "pct_of_hbm_peak": round(100 * value / PEAK_HBM_GBS, 2),
         "per_matrix_gbs": {"gate": round(gbs_gate, 1), "up": round(gbs_up, 1), "down": round(gbs_down, 1),
                            "fused_gate_up_geglu": round(gbs_geglu, 1)},
-        "per_kernel_us": {"geglu": round(k_geglu * 1e6, 3), "gate": round(k_gate * 1e6, 3),
-                          "up": round(k_up * 1e6, 3), "down": round(k_down * 1e6, 3)},
+        "per_kernel_us": {k_: {"median": round(v_["median_s"] * 1e6, 3), "min": round(v_["min_s"] * 1e6, 3),
+                               "launches_per_sample": v_["launches_per_sample"]}
+                          for k_, v_ in (("geglu", st_geglu), ("gate", st_gate), ("up", st_up), ("down", st_down))},
+        "per_matrix_rotation": f"each kernel over all {sets * 3} pool matrices ({sets * 3 * W_BYTES} B)",
         "stream_copy_gbs": round(copy_gbs, 1),
+        "launch_floor": {"zero_fill_256B_us": round(st_zero["median_s"] * 1e6, 3),
+                         "copy_11.94MB_us": round(st_copy["median_s"] * 1e6, 3),
+                         "how": "product kernels (mrml_hip_zero_async, mrml_hip_copy_kernel) replayed in a graph, "
+                                "median per launch"},
         "roofline": {"bound": "hbm", "kernel": GEGLU_KERNEL, "achieved": round(gbs_geglu, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs_geglu / PEAK_HBM_GBS, 4),
                      "traffic": measured_traffic(GEGLU_KERNEL), "bytes_per_launch": BYTES_GEGLU,
-                     "avg_launch_us": round(k_geglu * 1e6, 3)},
+                     "avg_launch_us": round(k_geglu * 1e6, 3), "source_sha256_16": kernel_source_hash()},
         "cpu_baseline": cpu,
+        "q8_0": q8,
+        "q4_k": q4k,
         "decode": decode,
         "decode_cpu_baseline": decode_cpu,
         "gemm": gemm,

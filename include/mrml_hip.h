@@ -135,8 +135,10 @@ int mrml_hip_repack_q4_0(mrml_hip_ctx *ctx, const void *d_src_gguf, void *d_dst,
 /* GGUF Q8_0 (34 B / 32) -> quant plane [rows][cols/32][32 B] + scale plane f16. */
 int mrml_hip_repack_q8_0(mrml_hip_ctx *ctx, const void *d_src_gguf, void *d_dst,
                          int32_t rows, int32_t cols);
-/* GGUF Q4_K (144 B / 256) -> quant plane [rows][cols/256][128 B] + header plane
- * [rows][cols/256][16 B] = {f16 d, f16 dmin, u8 scales[12]}. */
+/* GGUF Q4_K (144 B / 256) -> quant plane [rows][cols/32][16 B], one run per
+ * 32-weight sub-block in Q4_0 nibble order (byte i: weight i low, weight
+ * i+16 high), + header plane [rows][cols/256][16 B] = {f16 d, f16 dmin,
+ * u8 scales[12]}. */
 int mrml_hip_repack_q4_k(mrml_hip_ctx *ctx, const void *d_src_gguf, void *d_dst,
                          int32_t rows, int32_t cols);
 
@@ -198,12 +200,20 @@ int mrml_hip_gemv_q4_0_qkv_q8(mrml_hip_ctx *ctx, const void *d_wq, const void *d
  * then 30*tanh(y/30) when softcap != 0.  d_w: backend Q8_0 layout. */
 int mrml_hip_gemv_q8_0(mrml_hip_ctx *ctx, const void *d_w, const float *d_x, float *d_y,
                        int32_t rows, int32_t cols, int32_t softcap);
+/* As mrml_hip_gemv_q8_0 with x already quantised (an activation pack from
+ * mrml_hip_quantize_q8_0): the vocabulary loop quantises its input once
+ * (model.rs:2842-2853). */
+int mrml_hip_gemv_q8_0_q8(mrml_hip_ctx *ctx, const void *d_w, const void *d_xpack, float *d_y,
+                          int32_t rows, int32_t cols, int32_t softcap);
 /* Q4_K (build-defined semantics, GGUF layout; the reference has no Q4_K dot):
  * y[r] = sum over sub-blocks j of
  *        (float)isum_j*((d*sc_j)*d_a) - (float)bsum_j*((dmin*m_j)*d_a),
  * folded in order.  d_w: backend Q4_K layout. */
 int mrml_hip_gemv_q4_k(mrml_hip_ctx *ctx, const void *d_w, const float *d_x, float *d_y,
                        int32_t rows, int32_t cols);
+/* As mrml_hip_gemv_q4_k with x already quantised (activation pack). */
+int mrml_hip_gemv_q4_k_q8(mrml_hip_ctx *ctx, const void *d_w, const void *d_xpack, float *d_y,
+                          int32_t rows, int32_t cols);
 
 /* ---- batched (prefill) products ------------------------------------------- */
 /* CudaDevice::gemm_q4_0 (cuda.rs:2308-2332; layout of kernels.rs:343-400):

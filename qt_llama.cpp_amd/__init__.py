@@ -137,6 +137,8 @@ _SIGNATURES = {
     "mrml_hip_gemv_q4_0_qkv_q8": [_P, _P, _P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemv_q8_0": [_P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemv_q4_k": [_P, _P, _P, _P, _I, _I],
+    "mrml_hip_gemv_q8_0_q8": [_P, _P, _P, _P, _I, _I, _I],
+    "mrml_hip_gemv_q4_k_q8": [_P, _P, _P, _P, _I, _I],
     "mrml_hip_gemm_q4_0": [_P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemm_q4_0_q8": [_P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemm_q4_0_noalloc": [_P, _P, _P, _P, _I, _I, _I],
@@ -430,6 +432,13 @@ class HipDevice:
 
     def gemv_q4_k(self, w, x, y, rows: int, cols: int) -> None:
         self._check(self.lib.mrml_hip_gemv_q4_k(self.ctx, _ptr(w), _ptr(x), _ptr(y), rows, cols))
+
+    def gemv_q8_0_q8(self, w, xpack, y, rows: int, cols: int, softcap: bool = False) -> None:
+        self._check(self.lib.mrml_hip_gemv_q8_0_q8(self.ctx, _ptr(w), _ptr(xpack), _ptr(y), rows, cols,
+                                                   int(softcap)))
+
+    def gemv_q4_k_q8(self, w, xpack, y, rows: int, cols: int) -> None:
+        self._check(self.lib.mrml_hip_gemv_q4_k_q8(self.ctx, _ptr(w), _ptr(xpack), _ptr(y), rows, cols))
 
     def argmax_f32(self, x, n: int, out) -> None:
         self._check(self.lib.mrml_hip_argmax_f32(self.ctx, _ptr(x), n, _ptr(out)))

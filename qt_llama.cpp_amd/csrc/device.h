@@ -235,6 +235,74 @@ __device__ __forceinline__ int32_t q4_0_isum_split(uint32_t w0, uint32_t w1, uin
     return (int32_t)(((uint32_t)sh << 4) + sl);
 }
 
+// Stage an activation pack (Q8_0 planes, nb blocks, 16-byte aligned) into
+// LDS in split-nibble form (device.h) with one wave, one block per lane;
+// every load of a batch is issued before the first block is converted, so
+// the copy costs one L2 round trip per 64*kBatch blocks.
+// With ISSUE_BARRIER the wave joins one workgroup barrier (s_barrier, no
+// memory fence) right after issuing its loads: compute waves that wait on
+// that barrier before issuing their weight loads then queue behind the
+// pack's loads in the CU's memory pipeline instead of ahead of them (an L2
+// hit issued after a CU's worth of HBM misses waits for most of them).  The
+// pack is then one batch: nb <= kStageMax, checked by the launchers.
+constexpr int kStageBatch = 5, kStageMax = 64 * kStageBatch;
+
+//
+// With KQ (the Q4_K matvec, whose quants q = 0..15 carry no -8 offset) the
+// block constant is c = 128 * sum(hi) = 8 * sum(a) - 8 * sum(lo), so that
+// q4_0_isum_split returns sum q*a, and a fourth plane at nb*40 holds the
+// block sums sum(a) (the min term's bsum): nb*44 bytes in all.
+template <bool ISSUE_BARRIER = false, bool KQ = false>
+__device__ __forceinline__ void stage_split_pack(const uint8_t *src, uint8_t *lds, int nb)
+{
+    constexpr int kBatch = kStageBatch;
+    const int lane = threadIdx.x & 63;
+    const uint4 *sq = reinterpret_cast<const uint4 *>(src);
+    const float *sd = reinterpret_cast<const float *>(src + (size_t)nb * 32);
+    uint4 *dq = reinterpret_cast<uint4 *>(lds);
+    float *dd = reinterpret_cast<float *>(lds + nb * 32);
+    int32_t *dc = reinterpret_cast<int32_t *>(lds + nb * 36);
+    const int32_t *ss = reinterpret_cast<const int32_t *>(src + (size_t)nb * 36);
+    int32_t *dsum = reinterpret_cast<int32_t *>(lds + nb * 40);
+    const int nbatch = ISSUE_BARRIER ? 64 * kBatch : nb;  // one pass with the barrier (exactly one s_barrier)
+    for (int b0 = 0; b0 < nbatch; b0 += 64 * kBatch) {
+        uint4 x[kBatch], y[kBatch];
+        float d[kBatch];
+        int32_t bs[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            int b = b0 + k * 64 + lane;
+            b = b < nb ? b : nb - 1;
+            x[k] = sq[2 * b];
+            y[k] = sq[2 * b + 1];
+            d[k] = sd[b];
+            if constexpr (KQ) bs[k] = ss[b];
+        }
+        if constexpr (ISSUE_BARRIER) __builtin_amdgcn_s_barrier();
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int b = b0 + k * 64 + lane;
+            if (b < nb) {
+                const uint4 lo = make_uint4(split_lo(x[k].x, y[k].x), split_lo(x[k].y, y[k].y),
+                                            split_lo(x[k].z, y[k].z), split_lo(x[k].w, y[k].w));
+                const uint4 hi = make_uint4(split_hi(x[k].x, y[k].x), split_hi(x[k].y, y[k].y),
+                                            split_hi(x[k].z, y[k].z), split_hi(x[k].w, y[k].w));
+                dq[2 * b] = lo;
+                dq[2 * b + 1] = hi;
+                dd[b] = d[k];
+                const int c = -8 * (lo_nib_sum(x[k].x) + lo_nib_sum(x[k].y) + lo_nib_sum(x[k].z) + lo_nib_sum(x[k].w) +
+                                    lo_nib_sum(y[k].x) + lo_nib_sum(y[k].y) + lo_nib_sum(y[k].z) + lo_nib_sum(y[k].w));
+                if constexpr (KQ) {
+                    dc[b] = c + 8 * bs[k];
+                    dsum[b] = bs[k];
+                } else {
+                    dc[b] = c;
+                }
+            }
+        }
+    }
+}
+
 // ops.rs:101-104 evaluated in the same order (contraction is off):
 // (0.5*x) * (1 + tanh(k*(x + ((0.044715*x)*x)*x))), with the host C
 // library's tanhf reproduced bit for bit (libm_f32.h).

@@ -10,7 +10,6 @@ namespace mrml {
 
 namespace {
 
-constexpr uint32_t kNib = 0x0F0F0F0Fu;
 
 // Wave 0 of each workgroup copies the activation pack into LDS; the compute
 // waves issue only their weight loads (see gemv_q4_0.hip).
@@ -88,27 +87,27 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q8_0_kernel(const uint8
 }
 
 // ---- Q4_K (build-defined semantics over the GGUF super-block) ---------------
-// Backend layout: quant plane [rows*nsb][128 B], header plane [rows*nsb][16 B]
-// = {f16 d, f16 dmin, u8 scales[12]}.  A lane owns one 32-byte quarter c of a
-// super-block: the low nibbles are sub-block 2c, the high nibbles 2c+1.
-// Since 16 lanes cover 4 super-blocks, c = j & 3 is fixed per lane.
+// Backend layout (repack_q4_k_kernel): quant plane [rows*nsb*8][16 B], one
+// 16-byte run per 32-weight sub-block in Q4_0 nibble order, then the header
+// plane [rows*nsb][16 B] = {f16 d, f16 dmin, 96-bit field of the 6-bit
+// scales (bits 6j..) and mins (bits 48+6j..)}.  The rows then stream like
+// Q4_0 rows of 8*nsb blocks: lane j of a 16-lane row owns sub-blocks
+// 16*it + j (sub-block j & 7 of its super-block in every iteration), and the
+// ordered DPP fold adds their terms in sub-block order (super-blocks, then
+// sub-blocks, the oracle's order).  Term of a sub-block:
+//   t = (float)isum * ((d * sc) * da) - (float)bsum * ((dmin * m) * da),
+//   isum = sum q*a (q = 0..15), bsum = sum a (the activation block's sum),
+// the integer dot on the split-nibble pack (stage_split_pack's KQ form: 8
+// dot8 and 4 xor per sub-block).  The 8 lanes of a super-block share its
+// header: each lane loads one 4-byte word of it (lane j: word j & 3, so
+// every quad of lanes holds the whole header) and gets the other three by
+// DPP quad broadcasts, which keeps the header in one register per iteration
+// instead of four (occupancy).
 
-__device__ __forceinline__ uint32_t hdr_byte(const uint4 &h, int i)
+template <int K>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v)
 {
-    const uint32_t word = (i < 4) ? h.x : (i < 8) ? h.y : (i < 12) ? h.z : h.w;
-    return (word >> ((i & 3) * 8)) & 0xffu;
-}
-
-// GGUF get_scale_min_k4 for sub-block jj (0..7); scales start at header byte 4.
-__device__ __forceinline__ void q4k_scale_min(const uint4 &h, int jj, uint32_t &sc, uint32_t &m)
-{
-    if (jj < 4) {
-        sc = hdr_byte(h, 4 + jj) & 63u;
-        m = hdr_byte(h, 8 + jj) & 63u;
-    } else {
-        sc = (hdr_byte(h, 8 + jj) & 0x0fu) | ((hdr_byte(h, jj) >> 6) << 4);
-        m = (hdr_byte(h, 8 + jj) >> 4) | ((hdr_byte(h, 4 + jj) >> 6) << 4);
-    }
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, K | (K << 2) | (K << 4) | (K << 6), 0xf, 0xf, false);
 }
 
 template <int ITERS, int WAVES>
@@ -116,90 +115,60 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_k_kernel(const uint8
                                                                      const uint8_t *xpack,
                                                                      float *__restrict__ y, int rows, int nsb)
 {
-    extern __shared__ uint8_t lds[];
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int nb = nsb * 8;  // sub-blocks per row = activation blocks
     if (threadIdx.x < 64) {
-        stage_pack_wave(xpack, lds, nsb * 8);
+        stage_split_pack<true, true>(xpack, lds, nb);
         __syncthreads();
         return;
     }
-    const int lane = threadIdx.x & 63, j = lane & 15, c = j & 3;
+    const int lane = threadIdx.x & 63, j = lane & 15;
     const int quad = blockIdx.x * WAVES + (threadIdx.x >> 6) - 1;
     const int row_raw = quad * 4 + (lane >> 4);
-    const int row = row_raw < rows ? row_raw : rows - 1;
-    const size_t nsbt = (size_t)rows * nsb;
+    const int row = row_raw < rows ? row_raw : rows - 1;  // tail rows recompute the last row
     const uint4 *qs = reinterpret_cast<const uint4 *>(w);
-    const uint4 *hp = reinterpret_cast<const uint4 *>(w + nsbt * 128);
-    const size_t base = (size_t)row * nsb;
-    const int nchunks = nsb * 4;
-    const int nb = nsb * 8;
+    const uint32_t *hp = reinterpret_cast<const uint32_t *>(w + (size_t)rows * nb * 16);
+    const size_t base = (size_t)row * nb, hbase = (size_t)row * nsb;
+    const int sh_sc = 6 * (j & 7), sh_m = 16 + 6 * (j & 7);
 
-    uint4 w0[ITERS], w1[ITERS], h[ITERS];
+    // every load of the row first; past the row end a clamped in-bounds
+    // sub-block, masked out of the fold
+    uint4 q[ITERS];
+    uint32_t hw[ITERS];
+    __builtin_amdgcn_s_barrier();  // the pack's loads are issued
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
-        int g = it * 16 + j;
-        g = g < nchunks ? g : nchunks - 4 + c;  // tail lanes: an in-bounds chunk, masked below
-        const size_t sbi = base + (size_t)(g >> 2);
-        w0[it] = qs[sbi * 8 + 2 * c];
-        w1[it] = qs[sbi * 8 + 2 * c + 1];
-        h[it] = hp[sbi];
+        int b = it * 16 + j;
+        b = b < nb ? b : nb - 1;
+        q[it] = qs[base + b];
+        hw[it] = hp[(hbase + (b >> 3)) * 4 + (j & 3)];
     }
     __syncthreads();
-    const int4 *aq = reinterpret_cast<const int4 *>(lds);
+    const uint4 *aq = reinterpret_cast<const uint4 *>(lds);
     const float *ad = reinterpret_cast<const float *>(lds + nb * 32);
-    const int32_t *as = reinterpret_cast<const int32_t *>(lds + nb * 36);
+    const int32_t *ac = reinterpret_cast<const int32_t *>(lds + nb * 36);
+    const int32_t *as = reinterpret_cast<const int32_t *>(lds + nb * 40);
     float s = 0.0f;
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
-        const int gt = it * 16 + j;
-        const int g = gt < nchunks ? gt : nchunks - 4 + c;
-        float te, to;
-        {
-            const int be = (g >> 2) * 8 + 2 * c;  // activation block of sub-block 2c
-            const int4 e0 = aq[2 * be], e1 = aq[2 * be + 1];
-            const int4 o0 = aq[2 * be + 2], o1 = aq[2 * be + 3];
-            const uint4 q0 = w0[it], q1 = w1[it];
-            int32_t ie = sdot4(q0.x & kNib, (uint32_t)e0.x, 0);
-            ie = sdot4(q0.y & kNib, (uint32_t)e0.y, ie);
-            ie = sdot4(q0.z & kNib, (uint32_t)e0.z, ie);
-            ie = sdot4(q0.w & kNib, (uint32_t)e0.w, ie);
-            ie = sdot4(q1.x & kNib, (uint32_t)e1.x, ie);
-            ie = sdot4(q1.y & kNib, (uint32_t)e1.y, ie);
-            ie = sdot4(q1.z & kNib, (uint32_t)e1.z, ie);
-            ie = sdot4(q1.w & kNib, (uint32_t)e1.w, ie);
-            int32_t io = sdot4((q0.x >> 4) & kNib, (uint32_t)o0.x, 0);
-            io = sdot4((q0.y >> 4) & kNib, (uint32_t)o0.y, io);
-            io = sdot4((q0.z >> 4) & kNib, (uint32_t)o0.z, io);
-            io = sdot4((q0.w >> 4) & kNib, (uint32_t)o0.w, io);
-            io = sdot4((q1.x >> 4) & kNib, (uint32_t)o1.x, io);
-            io = sdot4((q1.y >> 4) & kNib, (uint32_t)o1.y, io);
-            io = sdot4((q1.z >> 4) & kNib, (uint32_t)o1.z, io);
-            io = sdot4((q1.w >> 4) & kNib, (uint32_t)o1.w, io);
-            const float d = f16_bits_to_f32(h[it].x & 0xffffu);
-            const float dmin = f16_bits_to_f32(h[it].x >> 16);
-            uint32_t sc, m;
-            q4k_scale_min(h[it], 2 * c, sc, m);
-            {
-                const float da = ad[be];
-                const float ds = (d * (float)sc) * da;
-                const float dm = (dmin * (float)m) * da;
-                te = (float)ie * ds - (float)as[be] * dm;
-            }
-            q4k_scale_min(h[it], 2 * c + 1, sc, m);
-            {
-                const float da = ad[be + 1];
-                const float ds = (d * (float)sc) * da;
-                const float dm = (dmin * (float)m) * da;
-                to = (float)io * ds - (float)as[be + 1] * dm;
-            }
-        }
-        te = gt < nchunks ? te : 0.0f;
-        to = gt < nchunks ? to : 0.0f;
-        // Lane k's pair (t_{2c}, t_{2c+1}) joins the running sum at step k.
+        const int bt = it * 16 + j;
+        const int b = bt < nb ? bt : nb - 1;
+        const uint4 wq = q[it], lo = aq[2 * b], hi = aq[2 * b + 1];
+        const int32_t isum = q4_0_isum_split(wq.x, wq.y, wq.z, wq.w, lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w,
+                                             ac[b]);
+        const uint32_t h0 = quad_bcast<0>(hw[it]), h1 = quad_bcast<1>(hw[it]), h2 = quad_bcast<2>(hw[it]),
+                       h3 = quad_bcast<3>(hw[it]);
+        const uint64_t f_sc = (uint64_t)h1 | ((uint64_t)h2 << 32), f_m = (uint64_t)h2 | ((uint64_t)h3 << 32);
+        const uint32_t sc = (uint32_t)(f_sc >> sh_sc) & 63u, m = (uint32_t)(f_m >> sh_m) & 63u;
+        const float d = f16_bits_to_f32(h0 & 0xffffu);
+        const float dmin = f16_bits_to_f32(h0 >> 16);
+        const float da = ad[b];
+        const float ds = (d * (float)sc) * da;
+        const float dm = (dmin * (float)m) * da;
+        const float tv = (float)isum * ds - (float)as[b] * dm;
+        const float t = bt < nb ? tv : 0.0f;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            s = dpp_ror1(s) + te;
-            s = s + to;
-        }
+        for (int k = 0; k < 16; ++k) s = fold16(s, t);
     }
     if (j == 15 && row_raw < rows) y[row_raw] = s;
 }
@@ -313,11 +282,13 @@ int launch_gemv_q8_0(mrml_hip_ctx *ctx, const void *w, const void *xpack, float 
 
 int launch_gemv_q4_k(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows, int32_t cols)
 {
-    const int nsb = cols / 256;
-    const int iters = (nsb * 4 + 15) / 16;
+    const int nsb = cols / 256, nb = nsb * 8;
+    const int iters = (nb + 15) / 16;
+    if (nb > kStageMax)
+        return fail(ctx, MRML_HIP_E_UNSUPPORTED, "q4_k matvec: cols=%d above %d", cols, kStageMax * 32);
     const int waves = waves_for(rows);
     const dim3 grid(((rows + 3) / 4 + waves - 1) / waves);
-    const size_t lds = act_pack_bytes(nsb * 8);
+    const size_t lds = (size_t)nb * 44;  // split-nibble pack with block sums (stage_split_pack, KQ)
 #define QK_CASE(N)                                                                                           \
     case N:                                                                                                  \
         MRML_DISPATCH_WAVES(waves, {                                                                         \
@@ -326,7 +297,8 @@ int launch_gemv_q4_k(mrml_hip_ctx *ctx, const void *w, const void *xpack, float 
         });                                                                                                  \
         break;
     switch (iters) {
-        QK_CASE(1) QK_CASE(2) QK_CASE(3) QK_CASE(4) QK_CASE(5) QK_CASE(6) QK_CASE(8) QK_CASE(9)
+        QK_CASE(1) QK_CASE(2) QK_CASE(3) QK_CASE(4) QK_CASE(5) QK_CASE(6) QK_CASE(8) QK_CASE(9) QK_CASE(12)
+        QK_CASE(16) QK_CASE(18) QK_CASE(20)
     default:
         return fail(ctx, MRML_HIP_E_UNSUPPORTED, "q4_k matvec: cols=%d has no kernel instance", cols);
     }

@@ -78,8 +78,18 @@ __global__ void repack_q8_0_kernel(const uint8_t *__restrict__ src, uint8_t *__r
     reinterpret_cast<uint16_t *>(dst + nblocks * 32)[i] = (uint16_t)(b[0] | (b[1] << 8));
 }
 
-// GGUF Q4_K -> qs plane [rows*nsb][128] then header plane [rows*nsb][16]
-// = {d, dmin, scales[12]}.  GGUF super-blocks are 144 B, so 16-aligned.
+// GGUF Q4_K (144-byte super-blocks: f16 d, f16 dmin, u8 scales[12], u8
+// qs[128]) -> a quant plane [rows*nsb*8][16 B], one 16-byte run per 32-weight
+// sub-block in Q4_0 nibble order (byte i: weight i in the low nibble, weight
+// i+16 in the high nibble), then a header plane [rows*nsb][16 B]:
+//   word 0      f16 d | f16 dmin << 16 (as in GGUF)
+//   words 1..3  a 96-bit field, sub-block j's 6-bit scale at bits 6j..6j+5
+//               and its 6-bit min at bits 48+6j..48+6j+5
+// (the same 96 bits as GGUF's scales[12], unpacked by get_scale_min_k4 and
+// laid out so that a sub-block's pair is two shifts of one 64-bit word).  In
+// GGUF, qs[32c..32c+31] hold sub-block 2c in their low nibbles and sub-block
+// 2c+1 in their high nibbles, weight l of the sub-block in byte 32c+l.  One
+// thread per super-block.
 __global__ void repack_q4_k_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, size_t nsb)
 {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -87,8 +97,39 @@ __global__ void repack_q4_k_kernel(const uint8_t *__restrict__ src, uint8_t *__r
     const uint4 *b = reinterpret_cast<const uint4 *>(src + i * 144);
     uint4 *q = reinterpret_cast<uint4 *>(dst) + 8 * i;
 #pragma unroll
-    for (int k = 0; k < 8; k++) q[k] = b[1 + k];
-    reinterpret_cast<uint4 *>(dst + nsb * 128)[i] = b[0];
+    for (int c = 0; c < 4; ++c) {
+        // weights 0..15 of the chunk in lo16, 16..31 in hi16 (both nibbles)
+        const uint4 lo16 = b[1 + 2 * c], hi16 = b[2 + 2 * c];
+        const uint32_t lw[4] = {lo16.x, lo16.y, lo16.z, lo16.w}, hw[4] = {hi16.x, hi16.y, hi16.z, hi16.w};
+        uint32_t ev[4], od[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            ev[k] = (lw[k] & 0x0F0F0F0Fu) | ((hw[k] & 0x0F0F0F0Fu) << 4);  // sub-block 2c
+            od[k] = ((lw[k] >> 4) & 0x0F0F0F0Fu) | (hw[k] & 0xF0F0F0F0u);  // sub-block 2c+1
+        }
+        q[2 * c] = make_uint4(ev[0], ev[1], ev[2], ev[3]);
+        q[2 * c + 1] = make_uint4(od[0], od[1], od[2], od[3]);
+    }
+    const uint4 h = b[0];
+    const uint8_t *sc12 = src + i * 144 + 4;
+    uint64_t sc = 0, mn = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {  // get_scale_min_k4
+        uint32_t s6, m6;
+        if (j < 4) {
+            s6 = sc12[j] & 63u;
+            m6 = sc12[j + 4] & 63u;
+        } else {
+            s6 = (sc12[j + 4] & 0x0fu) | ((uint32_t)(sc12[j - 4] >> 6) << 4);
+            m6 = (uint32_t)(sc12[j + 4] >> 4) | ((uint32_t)(sc12[j] >> 6) << 4);
+        }
+        sc |= (uint64_t)s6 << (6 * j);
+        mn |= (uint64_t)m6 << (6 * j);
+    }
+    // 96-bit field: scales at bits 0..47, mins at 48..95
+    const uint32_t w1 = (uint32_t)sc, w2 = (uint32_t)(sc >> 32) | (uint32_t)(mn << 16),
+                   w3 = (uint32_t)(mn >> 16);
+    reinterpret_cast<uint4 *>(dst + nsb * 128)[i] = make_uint4(h.x, w1, w2, w3);
 }
 
 int launch_repack_q4_0(mrml_hip_ctx *ctx, const void *src, void *dst, int32_t rows, int32_t cols)

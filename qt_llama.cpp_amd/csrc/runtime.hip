@@ -512,6 +512,21 @@ int mrml_hip_gemv_q8_0(mrml_hip_ctx *ctx, const void *w, const float *x, float *
     return launch_gemv_q8_0(ctx, w, xp, y, rows, cols, softcap);
 }
 
+int mrml_hip_gemv_q8_0_q8(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows, int32_t cols,
+                          int32_t softcap)
+{
+    CTX_GUARD(ctx);
+    CHECK_MATVEC(ctx, w, xpack, y, rows, cols, 32);
+    return launch_gemv_q8_0(ctx, w, xpack, y, rows, cols, softcap);
+}
+
+int mrml_hip_gemv_q4_k_q8(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows, int32_t cols)
+{
+    CTX_GUARD(ctx);
+    CHECK_MATVEC(ctx, w, xpack, y, rows, cols, 256);
+    return launch_gemv_q4_k(ctx, w, xpack, y, rows, cols);
+}
+
 int mrml_hip_gemv_q4_k(mrml_hip_ctx *ctx, const void *w, const float *x, float *y, int32_t rows, int32_t cols)
 {
     CTX_GUARD(ctx);

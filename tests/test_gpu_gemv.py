@@ -281,6 +281,13 @@ def test_gemv_q8_0_bit_exact(backend, dev, orc, synth, rows, cols):
     dev.gemv_q8_0(wb, xb, yb, rows, cols)
     dev.sync()
     assert_bit_exact(yb.numpy(), ref, f"q8_0 {rows}x{cols}")
+    # the pre-quantised entry on the same activations
+    pk = backend.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(cols), np.uint8)
+    dev.quantize_q8_0(xb, None, pk, cols)
+    dev.zero(yb)
+    dev.gemv_q8_0_q8(wb, pk, yb, rows, cols)
+    dev.sync()
+    assert_bit_exact(yb.numpy(), ref, f"q8_0 from pack {rows}x{cols}")
 
 
 def test_gemv_q8_0_softcap(backend, dev, orc, synth):
@@ -299,7 +306,7 @@ def test_gemv_q8_0_softcap(backend, dev, orc, synth):
 
 
 # ------------------------------------------------------------ Q4_K + argmax
-@pytest.mark.parametrize("rows,cols", [(256000, 2304), (37, 256), (5, 2304)])
+@pytest.mark.parametrize("rows,cols", [(256000, 2304), (37, 256), (5, 2304), (4100, 2304), (2053, 768)])
 def test_gemv_q4_k_bit_exact_and_argmax(backend, dev, orc, synth, rows, cols):
     rng = synth.rng_for(8000 + rows)
     w = synth.q4_k_matrix(rng, rows, cols)
@@ -314,6 +321,12 @@ def test_gemv_q4_k_bit_exact_and_argmax(backend, dev, orc, synth, rows, cols):
     dev.sync()
     assert_bit_exact(yb.numpy(), ref, f"q4_k {rows}x{cols}")
     assert int(ib.numpy()[0]) == orc.argmax_f32(ref)
+    pk = backend.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(cols), np.uint8)
+    dev.quantize_q8_0(xb, None, pk, cols)
+    dev.zero(yb)
+    dev.gemv_q4_k_q8(wb, pk, yb, rows, cols)
+    dev.sync()
+    assert_bit_exact(yb.numpy(), ref, f"q4_k from pack {rows}x{cols}")
 
 
 def test_argmax_tie_and_nan_rules(backend, dev, orc):
