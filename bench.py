@@ -189,6 +189,41 @@ def decode_bytes_per_token(cfg: dict, pos: int) -> int:
     return L * (layer_w + kv + 4 * d * 4) + V * Q4_ROW(d) + Q4_ROW(d) + d * 4
 
 
+def decode_fast_bench(be, synth, dev, ev, n_prefill: int, n_decode: int, exact_hist) -> dict:
+    """The same configs[3] workload under the FAST numerics
+    (MRML_HIP_NUMERICS_FAST: tree-order norm sums, split-K attention): tok/s,
+    and how its greedy picks compare with the EXACT run's (the prompt steps
+    are teacher-forced, so each of their picks is compared on the same
+    context; decode steps follow the model's own tokens)."""
+    cfg = dict(synth.GEMMA2_2B)
+    model = synth.gemma2_model(cfg, seed=1)
+    m = be.Gemma2Model.from_host(dev, model, numerics=be.NUMERICS_FAST)
+    prompt = synth.prompt_tokens(n_prefill, cfg["vocab"], seed=1)
+    total = n_prefill + n_decode
+    state = be.HipBuffer.from_host(dev, np.array([prompt[0], 0], np.int32))
+    hist = be.HipBuffer.from_host(dev, np.full(total, -1, np.int32))
+    pr = be.HipBuffer.from_host(dev, prompt)
+    kc = be.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    vc = be.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    graph = dev.capture(lambda: m.step(state, kc, vc, hist=hist, hist_cap=total, prompt=pr, prompt_len=n_prefill))
+    t_pre = time_graph(dev, ev, graph, n_prefill)
+    t_dec = time_graph(dev, ev, graph, n_decode)
+    dev.sync()
+    h = hist.numpy()
+    graph.close()
+    m.close()
+    nbytes = sum(decode_bytes_per_token(cfg, p) for p in range(n_prefill, total))
+    same_prompt = int(np.sum(h[:n_prefill] == exact_hist[:n_prefill]))
+    dec_same = np.flatnonzero(h[n_prefill:] != exact_hist[n_prefill:])
+    return {"tok_s": round(n_decode / t_dec, 2), "ms_per_token": round(t_dec / n_decode * 1e3, 4),
+            "gb_s": round(nbytes / t_dec / 1e9, 1), "pct_of_hbm_peak": round(100 * nbytes / t_dec / 1e9 / PEAK_HBM_GBS, 2),
+            "prefill_ms_per_token": round(t_pre / n_prefill * 1e3, 4),
+            "prompt_picks_equal_to_exact": f"{same_prompt}/{n_prefill}",
+            "decode_tokens_equal_to_exact_until": int(dec_same[0]) if dec_same.size else n_decode,
+            "numerics": "FAST: tree-order RMSNorm sums, split-K (flash-decoding) attention; matvecs bit-exact "
+                        "given their inputs"}
+
+
 def decode_bench(be, synth, dev, ev, n_prefill: int, n_decode: int, cpu_steps: int) -> tuple[dict, dict | None]:
     """random-init Gemma-2-2B-shape Q4_0 model, f16 KV cache
     of 4096, prefill a seeded random prompt token by token, then greedy decode;
@@ -207,7 +242,8 @@ def decode_bench(be, synth, dev, ev, n_prefill: int, n_decode: int, cpu_steps: i
     t_pre = time_graph(dev, ev, graph, n_prefill)
     t_dec = time_graph(dev, ev, graph, n_decode)
     dev.sync()
-    toks = hist.numpy()[n_prefill:]
+    exact_hist = hist.numpy()
+    toks = exact_hist[n_prefill:]
     nbytes = sum(decode_bytes_per_token(cfg, p) for p in range(n_prefill, total))
     out = {"tok_s": round(n_decode / t_dec, 2), "ms_per_token": round(t_dec / n_decode * 1e3, 4),
            "gb_s": round(nbytes / t_dec / 1e9, 1), "pct_of_hbm_peak": round(100 * nbytes / t_dec / 1e9 / PEAK_HBM_GBS, 2),
@@ -215,7 +251,8 @@ def decode_bench(be, synth, dev, ev, n_prefill: int, n_decode: int, cpu_steps: i
            "prefill_ms_per_token": round(t_pre / n_prefill * 1e3, 4),
            "workload": "BASELINE configs[3]: 26 layers, 2304, 8/4 heads x 256, GeGLU 9216, tied 256000 Q4_0 "
                        "head, f16 KV cache 4096, token step captured once and replayed",
-           "first_tokens": toks[:4].tolist()}
+           "first_tokens": toks[:4].tolist(), "distinct_prompt_picks": int(len(set(exact_hist[:n_prefill].tolist()))),
+           "numerics": "EXACT: every op in the CPU path's order (logits bit-identical to the oracle)"}
     graph.close()
     # the same prompt through the chunked prefill (batched MFMA products) on
     # fresh caches: throughput, and its caches and last-position argmax
@@ -261,6 +298,7 @@ def decode_bench(be, synth, dev, ev, n_prefill: int, n_decode: int, cpu_steps: i
                "gb_s": round(cbytes / t_cpu / 1e9, 2),
                "sample": f"{cpu_steps} decode steps of the oracle token step (orc_gemma2_step) at positions "
                          f"{n_prefill}..{n_prefill + cpu_steps - 1}, {threads} threads"}
+    out["_exact_hist"] = exact_hist
     return out, cpu
 
 
@@ -283,13 +321,13 @@ def prefill_profile(be, synth, dev, n_prefill: int) -> dict:
     return {"profile_prefill": n_prefill, "first_token": int(am.numpy()[0])}
 
 
-def decode_profile(be, synth, dev, n_prefill: int, n_steps: int) -> dict:
+def decode_profile(be, synth, dev, n_prefill: int, n_steps: int, numerics: int = 0) -> dict:
     """Profiling aid for the C4 model: n_prefill + n_steps token steps issued
     eagerly (no graph: the kernel trace then sees every launch); the last
     n_steps are the decode steps at positions n_prefill.."""
     cfg = dict(synth.GEMMA2_2B)
     model = synth.gemma2_model(cfg, seed=1)
-    m = be.Gemma2Model.from_host(dev, model)
+    m = be.Gemma2Model.from_host(dev, model, numerics=numerics)
     prompt = synth.prompt_tokens(n_prefill, cfg["vocab"], seed=1)
     total = n_prefill + n_steps
     state = be.HipBuffer.from_host(dev, np.array([prompt[0], 0], np.int32))
@@ -303,7 +341,7 @@ def decode_profile(be, synth, dev, n_prefill: int, n_steps: int) -> dict:
             dev.sync()
     dev.sync()
     m.close()
-    return {"profile_decode": n_steps, "prefill_tokens": n_prefill}
+    return {"profile_decode": n_steps, "prefill_tokens": n_prefill, "numerics": numerics}
 
 
 def gemm_bench(be, synth, dev, ev, batch: int, cpu_tokens: int, profile: int = 0) -> dict:
@@ -558,6 +596,8 @@ def main() -> int:
                     help="profiling aid: N eager launches of each C5 product, then exit")
     ap.add_argument("--profile-decode", type=int, default=0,
                     help="profiling aid: prefill, then N eager decode steps of the C4 model, then exit")
+    ap.add_argument("--fast-numerics", action="store_true",
+                    help="with --profile-decode: the FAST numerics (tree-order norm sums, split-K attention)")
     ap.add_argument("--profile-prefill", type=int, default=0,
                     help="profiling aid: one chunked prefill of N tokens of the C4 model, then exit")
     ap.add_argument("--profile-lmhead", type=int, default=0,
@@ -579,7 +619,8 @@ def main() -> int:
         print(json.dumps(gemm_bench(be, synth, dev, ev, args.gemm_batch, 0, profile=args.profile_gemm)))
         return 0
     if args.profile_decode:
-        print(json.dumps(decode_profile(be, synth, dev, args.decode_prefill, args.profile_decode)))
+        print(json.dumps(decode_profile(be, synth, dev, args.decode_prefill, args.profile_decode,
+                                        be.NUMERICS_FAST if args.fast_numerics else be.NUMERICS_EXACT)))
         return 0
     if args.profile_lmhead:
         print(json.dumps(lmhead_profile(be, synth, dev, args.profile_lmhead)))
@@ -729,6 +770,8 @@ def main() -> int:
     if not args.no_decode:
         decode, decode_cpu = decode_bench(be, synth, dev, ev, args.decode_prefill, args.decode_tokens,
                                           0 if args.no_cpu else args.cpu_decode_steps)
+        decode["fast"] = decode_fast_bench(be, synth, dev, ev, args.decode_prefill, args.decode_tokens,
+                                           decode.pop("_exact_hist"))
 
     line = {
         "metric": "Q4_0 matvec GB/s (Gemma-2-2B FFN: fused gate+up GeGLU + down, batch 1)",

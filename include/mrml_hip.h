@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define MRML_HIP_ABI_VERSION 1
+#define MRML_HIP_ABI_VERSION 2
 
 enum {
     MRML_HIP_OK = 0,
@@ -317,12 +317,34 @@ int mrml_hip_attn_decode_f16(mrml_hip_ctx *ctx, const float *d_q, const uint16_t
                              const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                              float scale, int32_t capacity);
 
+/* The same attention split over tiles of 64 positions of the window (flash
+ * decoding: per tile and head the max, the exp sum and the weighted values
+ * in f32 tree order, then a merge in tile order): the FAST numerics of the
+ * token step (MRML_HIP_NUMERICS_FAST).  Within 1e-5 of the CPU path relative
+ * to the output's largest magnitude, not bit-identical.  Same arguments and
+ * limits as mrml_hip_attn_decode_f16 (attention_causal, cuda.rs:2658-2697). */
+int mrml_hip_attn_decode_f16_split(mrml_hip_ctx *ctx, const float *d_q, const uint16_t *d_k_cache,
+                                   const uint16_t *d_v_cache, float *d_out, void *d_pack, int32_t n_past,
+                                   const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                   float scale, int32_t capacity);
+
 /* ---- Gemma-2-shape token step (model.rs forward_token, model.rs:1185-2260,
  * and greedy selection, model.rs:2833-2907) ----------------------------------- */
+/* Numerics of the token step.  EXACT (0, the default): every op in the CPU
+ * path's operation order, logits bit-identical to the reference CPU step.
+ * FAST: the matvecs stay bit-exact given their inputs, but the residual
+ * RMSNorm sums are deterministic tree sums and decode attention is split
+ * over tiles of the window (flash decoding) with tree-order softmax and
+ * value sums; each such op is within 1e-5 of the CPU path relative to its
+ * output's largest magnitude, and greedy tokens are checked against the
+ * reference CPU step (north_star: <= 1e-5 max-rel, identical greedy tokens). */
+enum { MRML_HIP_NUMERICS_EXACT = 0, MRML_HIP_NUMERICS_FAST = 1 };
+
 typedef struct mrml_hip_gemma2_config {
     int32_t n_layers, dim, n_heads, n_kv_heads, head_dim, ffn_dim, vocab, ctx_len;
     float   rope_base, eps, attn_scale;
     int32_t tie_type; /* MRML_HIP_Q4_0 or MRML_HIP_Q8_0: tied embedding / LM-head table */
+    int32_t numerics; /* MRML_HIP_NUMERICS_EXACT (0) or MRML_HIP_NUMERICS_FAST */
 } mrml_hip_gemma2_config;
 
 /* Device pointers of one layer: matrices in the backend Q4_0 layout, norm

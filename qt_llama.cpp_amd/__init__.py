@@ -84,7 +84,12 @@ class Gemma2Config(ctypes.Structure):
 
     _fields_ = [(n, ctypes.c_int32) for n in
                 ("n_layers", "dim", "n_heads", "n_kv_heads", "head_dim", "ffn_dim", "vocab", "ctx_len")] + \
-               [(n, ctypes.c_float) for n in ("rope_base", "eps", "attn_scale")] + [("tie_type", ctypes.c_int32)]
+               [(n, ctypes.c_float) for n in ("rope_base", "eps", "attn_scale")] + \
+               [("tie_type", ctypes.c_int32), ("numerics", ctypes.c_int32)]
+
+
+NUMERICS_EXACT = 0
+NUMERICS_FAST = 1
 
 
 GEMMA2_LAYER_TENSORS = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")
@@ -153,6 +158,7 @@ _SIGNATURES = {
     "mrml_hip_rope_table": [_P, _P, _I, _I, _F, _F],
     "mrml_hip_rope_kv_append_f16": [_P, _P, _P, _P, _I, _P, _I, _I, _I, _F, _F, _I, _P, _I],
     "mrml_hip_attn_decode_f16": [_P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _F, _I],
+    "mrml_hip_attn_decode_f16_split": [_P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _F, _I],
     "mrml_hip_gemma2_create": [_P, _P, _P, _P, _P, ctypes.POINTER(_P)],
     "mrml_hip_gemma2_destroy": [_P, _P],
     "mrml_hip_gemma2_step": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I],
@@ -478,6 +484,14 @@ class HipDevice:
                                                       head_dim, scale, capacity))
 
 
+    def attention_causal_split(self, q, k_cache, v_cache, out, n_past: int, n_heads: int, n_kv_heads: int,
+                               head_dim: int, scale: float, capacity: int, pack=None, d_pos=None) -> None:
+        """attention_causal split over tiles of the window (the FAST numerics)."""
+        self._check(self.lib.mrml_hip_attn_decode_f16_split(self.ctx, _ptr(q), _ptr(k_cache), _ptr(v_cache),
+                                                            _ptr(out), _ptr(pack), n_past, _ptr(d_pos), n_heads,
+                                                            n_kv_heads, head_dim, scale, capacity))
+
+
 class Gemma2Model:
     """A Gemma-2-shape decoder bound to device weights (mrml_hip_gemma2_*).
 
@@ -499,14 +513,15 @@ class Gemma2Model:
         self.handle = h.value
 
     @classmethod
-    def from_host(cls, dev: HipDevice, model: dict) -> "Gemma2Model":
+    def from_host(cls, dev: HipDevice, model: dict, numerics: int = NUMERICS_EXACT) -> "Gemma2Model":
         """Upload a model held as GGUF block bytes (the dict of synth.gemma2_model)
         and convert every matrix to the backend layout; the model keeps the
-        device buffers alive."""
+        device buffers alive.  numerics: NUMERICS_EXACT (bit-identical to the
+        CPU step) or NUMERICS_FAST (tree-order norm sums, split-K attention)."""
         c = model["cfg"]
         cfg = Gemma2Config(c["n_layers"], c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["ffn_dim"],
                            c["vocab"], c["ctx_len"], c["rope_base"], c["eps"], c["attn_scale"],
-                           Q8_0 if model["tie_q8"] else Q4_0)
+                           Q8_0 if model["tie_q8"] else Q4_0, numerics)
         qd, kvd = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
         shapes = {"wq": (qd, c["dim"]), "wk": (kvd, c["dim"]), "wv": (kvd, c["dim"]), "wo": (c["dim"], qd),
                   "w_gate": (c["ffn_dim"], c["dim"]), "w_up": (c["ffn_dim"], c["dim"]),

@@ -730,6 +730,230 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
     }
 }
 
+// ---- split-K decode attention: the decode step's tolerance path ---------------
+// The same attention (model.rs:1457-1590, softmax ops.rs:133-158) evaluated in
+// parallel over the window instead of in the reference's sequential order,
+// as flash decoding does: the window (the last min(n_past+1, capacity)
+// positions, oldest first) is cut into tiles of kSplitP positions and
+// workgroup (tile, kv head) forms, for each query head of the group,
+//   m = max_p s_p,  l = sum_p e_p,  o[d] = sum_p e_p v_p[d],
+//   s_p = scale * (q . k_p),  e_p = expf(s_p - m),
+// over its tile (f32, fixed-order tree sums: deterministic); then
+// attn_combine_kernel merges the tiles of a head,
+//   M = max_t m_t,  L = sum_t l_t expf(m_t - M),  out[d] = (sum_t o_t[d] expf(m_t - M)) / L,
+// in tile order and writes the Q8_0 pack of the output for the next product.
+// Results are within a few ulps of the sequential ones (the tests bound them
+// at 1e-5 relative to the output's largest magnitude), not bit-identical.
+//
+// With ROPE, q comes raw from the stacked q|k|v vector and is rotated here
+// (cos/sin from the host table when pos < n_table), and the workgroup whose
+// tile holds the newest position rotates that position's k, rounds k and v
+// to f16 (RNE, as the cache stores them), uses them for that row and appends
+// them to the caches -- what attn_scores2_kernel<true> does for the exact
+// path.  Workgroups of tiles past the window exit at once.
+constexpr int kSplitP = 64;                    // positions per tile (one per lane)
+constexpr int kSplitT = 256;                   // threads per workgroup
+constexpr int kSplitKRow = kAttnHD * 2 + 16;   // padded K row in LDS, bytes (conflict-free 16-byte reads of 64 rows)
+constexpr int kSplitPart = kAttnHD + 4;        // floats per partial: o[256], m, l, pad
+
+__device__ __forceinline__ float wave_max_f32(float v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+template <bool ROPE>
+__global__ __launch_bounds__(kSplitT) void attn_split_kernel(const float *__restrict__ q_in,
+                                                             uint16_t *__restrict__ k_cache,
+                                                             uint16_t *__restrict__ v_cache,
+                                                             const int32_t *__restrict__ d_pos, int n_past_arg,
+                                                             int n_heads, int n_kv_heads, float scale, int capacity,
+                                                             const float *__restrict__ table, int n_table, float base,
+                                                             float freq_scale, float *__restrict__ part, int max_tiles)
+{
+    constexpr int HD = kAttnHD, P = kSplitP, half = HD / 2;
+    __shared__ __align__(16) float q_s[8][HD];
+    __shared__ __align__(16) uint8_t k_s[P * kSplitKRow];
+    __shared__ __align__(16) uint16_t v_s[P][HD];
+    __shared__ __align__(16) float e_s[8][P];
+    int window, start;
+    attn_window(d_pos, n_past_arg, capacity, window, start);
+    const int tile = blockIdx.x, p0 = tile * P;
+    if (p0 >= window) return;
+    const int kvh = blockIdx.y, G = n_heads / n_kv_heads, tid = threadIdx.x;
+    const size_t kv_dim = (size_t)n_kv_heads * HD;
+    const int pos = start + window - 1;  // the newest position
+    const int rnew = window - 1 - p0;    // its row in this tile (valid when < P)
+    const bool has_new = ROPE && rnew < P;
+    // K and V tiles: 2048 chunks of 16 B each, chunk c of row r = c >> 5;
+    // rows past the window reload the last row (their scores are masked)
+    constexpr int kChunks = P * (HD * 2 / 16), kPer = kChunks / kSplitT;
+    u32x4 kt[kPer], vt[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int c = k * kSplitT + tid, r = c >> 5;
+        const int pr = p0 + r < window ? p0 + r : window - 1;
+        const size_t off = cache_row_of(start + pr, capacity) * kv_dim + (size_t)kvh * HD;
+        kt[k] = reinterpret_cast<const u32x4 *>(k_cache + off)[c & 31];
+        vt[k] = reinterpret_cast<const u32x4 *>(v_cache + off)[c & 31];
+    }
+    // q of the group's heads, rotated with ROPE (thread -> pair i = tid % half)
+    static_assert(kSplitT % half == 0, "one rotation pair index per thread");
+    float c = 1.0f, sn = 0.0f;
+    if (ROPE) rope_cs(table, n_table, pos, tid % half, HD, base, freq_scale, c, sn);
+    for (int gi = tid; gi < G * half; gi += kSplitT) {
+        const int g = gi / half, i = gi % half;
+        const float *qh = q_in + (size_t)(kvh * G + g) * HD;
+        const float v0 = qh[i], v1 = qh[i + half];
+        q_s[g][i] = ROPE ? v0 * c - v1 * sn : v0;
+        q_s[g][i + half] = ROPE ? v0 * sn + v1 * c : v1;
+    }
+    if (has_new) {
+        const size_t crow = cache_row_of(pos, capacity) * kv_dim + (size_t)kvh * HD;
+        if (tid < half) {
+            const int i = tid;
+            const float *kh = q_in + (size_t)(n_heads + kvh) * HD;
+            const float v0 = kh[i], v1 = kh[i + half];
+            const uint16_t k0 = f32_to_f16_rne(v0 * c - v1 * sn), k1 = f32_to_f16_rne(v0 * sn + v1 * c);
+            uint16_t *krow = reinterpret_cast<uint16_t *>(k_s + rnew * kSplitKRow);
+            krow[i] = k0;
+            krow[i + half] = k1;
+            k_cache[crow + i] = k0;
+            k_cache[crow + i + half] = k1;
+        } else {
+            const int i = tid - half;
+            const float *vh = q_in + (size_t)(n_heads + n_kv_heads + kvh) * HD;
+            const uint16_t w0 = f32_to_f16_rne(vh[i]), w1 = f32_to_f16_rne(vh[i + half]);
+            v_s[rnew][i] = w0;
+            v_s[rnew][i + half] = w1;
+            v_cache[crow + i] = w0;
+            v_cache[crow + i + half] = w1;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int cc = k * kSplitT + tid, r = cc >> 5;
+        if (!(has_new && r == rnew)) {
+            *reinterpret_cast<u32x4 *>(k_s + r * kSplitKRow + (cc & 31) * 16) = kt[k];
+            reinterpret_cast<u32x4 *>(&v_s[r][0])[cc & 31] = vt[k];
+        }
+    }
+    __syncthreads();
+    const int wave = tid >> 6, lane = tid & 63;
+    const int ntile = window - p0 < P ? window - p0 : P;  // live rows of the tile (masked scores past it)
+    for (int g = wave; g < G; g += kSplitT / 64) {
+        // score of position p0 + lane: four partial dot products
+        const u32x4 *krow = reinterpret_cast<const u32x4 *>(k_s + lane * kSplitKRow);
+        const float4 *qg = reinterpret_cast<const float4 *>(q_s[g]);
+        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
+        for (int d8 = 0; d8 < HD / 8; ++d8) {
+            const u32x4 kw = krow[d8];
+            const float4 qa = qg[2 * d8], qb = qg[2 * d8 + 1];
+            const uint32_t w[4] = {kw.x, kw.y, kw.z, kw.w};
+            const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                a[e & 3] = __builtin_fmaf(qv[e], f16_bits_to_f32((w[e >> 1] >> (16 * (e & 1))) & 0xffffu), a[e & 3]);
+        }
+        const bool live = lane < ntile;
+        const float sc = ((a[0] + a[1]) + (a[2] + a[3])) * scale;
+        const float m = wave_max_f32(live ? sc : -INFINITY);
+        const float e = live ? __builtin_expf(sc - m) : 0.0f;
+        const float l = mrml_xsum::wave_sum_f32(e);
+        e_s[g][lane] = e;
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS writes done (lgkmcnt 0)
+        __builtin_amdgcn_wave_barrier();     // (LDS accesses of one wave run in order)
+        // o[d] for d = 4*lane .. 4*lane+3 over all 64 rows of the tile (rows
+        // past the window have e = 0 and finite values), eight rows per step
+        // with their LDS reads issued together, even and odd rows in two
+        // accumulators
+        float4 oa = make_float4(0.0f, 0.0f, 0.0f, 0.0f), ob = oa;
+        const float4 *e4 = reinterpret_cast<const float4 *>(e_s[g]);
+#pragma unroll 2
+        for (int p = 0; p < P; p += 8) {
+            const float4 ea = e4[p / 4], eb = e4[p / 4 + 1];
+            const float ep[8] = {ea.x, ea.y, ea.z, ea.w, eb.x, eb.y, eb.z, eb.w};
+            u32x2 vv[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) vv[k] = reinterpret_cast<const u32x2 *>(&v_s[p + k][0])[lane];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                float4 &o = (k & 1) ? ob : oa;
+                o.x = __builtin_fmaf(ep[k], f16_bits_to_f32(vv[k].x & 0xffffu), o.x);
+                o.y = __builtin_fmaf(ep[k], f16_bits_to_f32(vv[k].x >> 16), o.y);
+                o.z = __builtin_fmaf(ep[k], f16_bits_to_f32(vv[k].y & 0xffffu), o.z);
+                o.w = __builtin_fmaf(ep[k], f16_bits_to_f32(vv[k].y >> 16), o.w);
+            }
+        }
+        const float4 o = make_float4(oa.x + ob.x, oa.y + ob.y, oa.z + ob.z, oa.w + ob.w);
+        float *pp = part + ((size_t)(kvh * G + g) * max_tiles + tile) * kSplitPart;
+        reinterpret_cast<float4 *>(pp)[lane] = o;
+        if (lane == 0) {
+            pp[HD] = m;
+            pp[HD + 1] = l;
+        }
+    }
+}
+
+// Merges the tiles of head blockIdx.x (thread d = output dim d), in tile
+// order, and writes out (nullable) and the Q8_0 pack (nullable) of the
+// n_heads*256 output.
+__global__ __launch_bounds__(kAttnHD) void attn_combine_kernel(const float *__restrict__ part,
+                                                               const int32_t *__restrict__ d_pos, int n_past_arg,
+                                                               int capacity, int max_tiles, int n_heads,
+                                                               float *__restrict__ out, uint8_t *__restrict__ pack)
+{
+    constexpr int HD = kAttnHD, kMaxTiles = (6144 + kSplitP - 1) / kSplitP;
+    __shared__ float m_s[kMaxTiles], w_s[kMaxTiles], l_s[kMaxTiles];
+    int window, start;
+    attn_window(d_pos, n_past_arg, capacity, window, start);
+    const int ntiles = (window + kSplitP - 1) / kSplitP, h = blockIdx.x, d = threadIdx.x;
+    const float *ph = part + (size_t)h * max_tiles * kSplitPart;
+    // the tiles' (m, l) in parallel, one tile per thread
+    for (int t = d; t < ntiles; t += HD) {
+        m_s[t] = ph[(size_t)t * kSplitPart + HD];
+        l_s[t] = ph[(size_t)t * kSplitPart + HD + 1];
+    }
+    __syncthreads();
+    float M = -INFINITY;
+    for (int t = 0; t < ntiles; ++t) M = fmaxf(M, m_s[t]);
+    for (int t = d; t < ntiles; t += HD) w_s[t] = __builtin_expf(m_s[t] - M);
+    __syncthreads();
+    // L and o in tile order (every thread forms the same L)
+    float L = 0.0f, o = 0.0f;
+    int t = 0;
+    for (; t + 8 <= ntiles; t += 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = ph[(size_t)(t + k) * kSplitPart + d];  // eight loads in flight
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            L = L + l_s[t + k] * w_s[t + k];
+            o = o + v[k] * w_s[t + k];
+        }
+    }
+    for (; t < ntiles; ++t) {
+        L = L + l_s[t] * w_s[t];
+        o = o + ph[(size_t)t * kSplitPart + d] * w_s[t];
+    }
+    const float v = o / L;
+    const int idx = h * HD + d;
+    if (out) out[idx] = v;
+    if (pack) {
+        uint32_t dbits;
+        int qs;
+        const int qv = q8_0_block32(v, dbits, qs);  // 32-lane blocks: block idx / 32
+        const int nb = n_heads * HD / 32, blk = idx >> 5;
+        pack[idx] = (uint8_t)(int8_t)qv;
+        if ((idx & 31) == 0) {
+            reinterpret_cast<float *>(pack + (size_t)nb * 32)[blk] = f16_bits_to_f32(dbits);
+            reinterpret_cast<int32_t *>(pack + (size_t)nb * 36)[blk] = qs;
+        }
+    }
+}
+
 // One float4 chunk per thread where the workgroup allows (the exact sum's
 // per-thread share of terms stays small).
 inline int norm_threads(int dim)
@@ -935,6 +1159,35 @@ int launch_attn_decode_rope_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k
                        n_past, n_heads, n_kv_heads, scale, capacity, table, n_table, base, freq_scale, scores);
     if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
     return launch_softmax_v(ctx, scores, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, capacity);
+}
+
+int attn_split_tiles(int capacity) { return (capacity + kSplitP - 1) / kSplitP; }
+
+size_t attn_split_scratch_bytes(int n_heads, int capacity)
+{
+    return (size_t)n_heads * attn_split_tiles(capacity) * kSplitPart * sizeof(float);
+}
+
+int launch_attn_split_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k_cache, uint16_t *v_cache, float *out,
+                          void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads, float scale,
+                          int capacity, bool rope, const float *table, int n_table, float base, float freq_scale,
+                          void *scratch)
+{
+    float *part = reinterpret_cast<float *>(scratch);
+    const int tiles = attn_split_tiles(capacity);
+    const dim3 grid(tiles, n_kv_heads);
+    if (rope)
+        hipLaunchKernelGGL(attn_split_kernel<true>, grid, dim3(kSplitT), 0, ctx->stream, qkv, k_cache, v_cache, d_pos,
+                           n_past, n_heads, n_kv_heads, scale, capacity, table, n_table, base, freq_scale, part,
+                           tiles);
+    else
+        hipLaunchKernelGGL(attn_split_kernel<false>, grid, dim3(kSplitT), 0, ctx->stream, qkv, k_cache, v_cache,
+                           d_pos, n_past, n_heads, n_kv_heads, scale, capacity, table, n_table, base, freq_scale,
+                           part, tiles);
+    if (int rc = check_launch(ctx, "attn_split_kernel")) return rc;
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(kAttnHD), 0, ctx->stream, part, d_pos, n_past,
+                       capacity, tiles, n_heads, out, (uint8_t *)pack);
+    return check_launch(ctx, "attn_combine_kernel");
 }
 
 hipError_t wait_guard_decode(int polls, uint32_t *timeouts) { return mrml_xsum::wait_guard_io(polls, timeouts); }

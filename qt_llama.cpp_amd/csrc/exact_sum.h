@@ -485,6 +485,37 @@ __device__ __forceinline__ float block_seq_sum_nonneg4(float4 v, int n, Shared4 
     return x.result;
 }
 
+// ---- tree sums (the tolerance path) ---------------------------------------------
+// Sums in a fixed tree order -- deterministic from run to run, but not the
+// reference's sequential order: they serve the decode step's tolerance path,
+// where each RMSNorm sum is a few tree levels instead of an exact
+// sequential-order evaluation.
+
+// Sum over the 64 lanes of the wave, the same value in every lane (an xor
+// butterfly: at each level both partners add the same two values).
+__device__ __forceinline__ float wave_sum_f32(float v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Sum over the workgroup (every thread passes its value; the result in
+// every thread).  red: blockDim/64 floats of LDS.  Two LDS-only barriers,
+// so outstanding global loads are not waited for; red may be reused after
+// the call.
+__device__ __forceinline__ float block_tree_sum(float v, float *red)
+{
+    v = wave_sum_f32(v);
+    const int nw = (int)(blockDim.x >> 6);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    lds_barrier();
+    float s = 0.0f;
+    for (int w = 0; w < nw; ++w) s += red[w];
+    lds_barrier();
+    return s;
+}
+
 // ---- a group of waves with its own barrier ------------------------------------
 // The register form for the nw (<= 16) waves of a group inside a workgroup,
 // K terms per lane: lane l of group wave gw holds terms k = K*(64*gw + l) + i.
@@ -568,6 +599,19 @@ struct GroupShared {
     int wcnt[16];
     float result;
 };
+
+// Tree sum over the nw (<= 8) waves of a group: the wave totals go to
+// x.wtot[8*slot + gw] (slot 0 or 1, so two sums in a row need no extra
+// sync), one group sync, then every lane adds them in wave order.
+__device__ __forceinline__ float group_tree_sum(float v, int gw, GroupSync &sync, GroupShared &x, int slot)
+{
+    v = wave_sum_f32(v);
+    if ((threadIdx.x & 63) == 0) x.wtot[8 * slot + gw] = v;
+    sync();
+    float s = 0.0f;
+    for (int w = 0; w < (int)sync.nw; ++w) s += x.wtot[8 * slot + w];
+    return s;
+}
 
 // Sum of the terms held by the group (n terms in all), bit for bit the
 // sequential loop.  Every lane of the nw waves calls it; gw is the wave's

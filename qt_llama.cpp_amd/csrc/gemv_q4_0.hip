@@ -540,7 +540,9 @@ __device__ __forceinline__ void group_norm_load(GroupNormOps<NB> &o, const float
 // The residual norm of the group: h_out = h_in + rms_norm(t, w_post) (stored
 // when h_out is set), the split pack of rms_norm(h_out, w_norm) at pack.
 // Called by the kNormWaves group waves only.
-template <int NB>
+// FAST (the decode step's tolerance path): both sums are deterministic tree
+// sums (exact_sum.h's group_tree_sum) instead of the sequential-order ones.
+template <int NB, bool FAST = false>
 __device__ __forceinline__ void group_residual_norm(GroupNormOps<NB> &o, bool has_post, bool has_norm, float *h_out,
                                                     float eps, uint8_t *pack, uint8_t *lds_group, float *area,
                                                     int wave)
@@ -554,7 +556,17 @@ __device__ __forceinline__ void group_residual_norm(GroupNormOps<NB> &o, bool ha
 #pragma unroll
     for (int i = 0; i < KN; ++i) sq[i] = o.t[i] * o.t[i];
     float *xn = area, *evl = area + DIM;
-    const float s1 = rms_scale(mrml_xsum::group_seq_sum_nonneg<KN>(sq, DIM, wave, sync, *gs, evl), DIM, eps);
+    auto sum_sq = [&](int slot) {
+        if constexpr (FAST) {
+            float a = 0.0f;
+#pragma unroll
+            for (int i = 0; i < KN; ++i) a += k0 + i < DIM ? sq[i] : 0.0f;
+            return mrml_xsum::group_tree_sum(a, wave, sync, *gs, slot);
+        } else {
+            return mrml_xsum::group_seq_sum_nonneg<KN>(sq, DIM, wave, sync, *gs, evl);
+        }
+    };
+    const float s1 = rms_scale(sum_sq(0), DIM, eps);
 #pragma unroll
     for (int i = 0; i < KN; ++i) {
         float tn = o.t[i] * s1;
@@ -563,7 +575,7 @@ __device__ __forceinline__ void group_residual_norm(GroupNormOps<NB> &o, bool ha
         if (h_out && k0 + i < DIM) h_out[k0 + i] = o.h[i];
         sq[i] = o.h[i] * o.h[i];
     }
-    const float s2 = rms_scale(mrml_xsum::group_seq_sum_nonneg<KN>(sq, DIM, wave, sync, *gs, evl), DIM, eps);
+    const float s2 = rms_scale(sum_sq(1), DIM, eps);
 #pragma unroll
     for (int i = 0; i < KN; ++i) {
         float v = o.h[i] * s2;
@@ -580,7 +592,7 @@ __device__ __forceinline__ void group_residual_norm(GroupNormOps<NB> &o, bool ha
     }
 }
 
-template <int NB>
+template <int NB, bool FAST>
 __global__ __launch_bounds__(64 * kGegluResWaves) void gemv_q4_0_geglu_resnorm_kernel(
     const uint8_t *__restrict__ wg, const uint8_t *__restrict__ wu, const float *__restrict__ t,
     const float *__restrict__ w_post, const float *h_in, float *h_out, const float *__restrict__ w_norm, float eps,
@@ -606,8 +618,8 @@ __global__ __launch_bounds__(64 * kGegluResWaves) void gemv_q4_0_geglu_resnorm_k
         load_row<ITERS>(rg, wg, nblk, base, NB, j);
         load_row<ITERS>(ru, wu, nblk, base, NB, j);
     } else {
-        group_residual_norm<NB>(ops, w_post != nullptr, w_norm != nullptr, blockIdx.x == 0 ? h_out : nullptr, eps, lds,
-                                lds_group, area, wave);
+        group_residual_norm<NB, FAST>(ops, w_post != nullptr, w_norm != nullptr, blockIdx.x == 0 ? h_out : nullptr,
+                                      eps, lds, lds_group, area, wave);
         load_row<ITERS>(rg, wg, nblk, base, NB, j);
         load_row<ITERS>(ru, wu, nblk, base, NB, j);
     }
@@ -639,7 +651,7 @@ constexpr size_t geglu_resnorm_lds() { return rn2_area_off<NB>() + rn2_area_byte
 
 // The stacked q|k|v matvec, the post-FFN residual of the previous block and
 // this block's pre-attention norm fused ahead (32 rows per workgroup).
-template <int NB>
+template <int NB, bool FAST>
 __global__ __launch_bounds__(64 * kResWaves) void gemv_q4_0_qkv_resnorm_kernel(
     const uint8_t *__restrict__ wq, const uint8_t *__restrict__ wk, const uint8_t *__restrict__ wv,
     const float *__restrict__ t, const float *__restrict__ w_post, const float *h_in, float *h_out,
@@ -657,8 +669,8 @@ __global__ __launch_bounds__(64 * kResWaves) void gemv_q4_0_qkv_resnorm_kernel(
     const size_t base = (size_t)m.local * NB;
     RowRegs<ITERS> r;
     if (wave > 0) load_row<ITERS>(r, m.w, (size_t)m.mrows * NB, base, NB, j);
-    residual_norm1<true>(ops, w_post != nullptr, w_norm != nullptr, eps, blockIdx.x == 0 ? h_out : nullptr, nullptr,
-                         resnorm_pack_lds<NB>(lds), NB * 32, *resnorm_shared<NB>(lds));
+    residual_norm1<true, FAST>(ops, w_post != nullptr, w_norm != nullptr, eps, blockIdx.x == 0 ? h_out : nullptr,
+                               nullptr, resnorm_pack_lds<NB>(lds), NB * 32, *resnorm_shared<NB>(lds));
     mrml_xsum::lds_barrier();  // the pack is whole
     if (wave > 0) {
         const float s = fold_row<ITERS>(r, lds, base, NB, j);
@@ -1258,7 +1270,7 @@ static size_t resnorm_lds(int nb) { return pack_lds(nb) + 64 * sizeof(float) + s
 
 int launch_geglu_resnorm(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *t, const float *w_post,
                          const float *h_in, float *h_out, const float *w_norm, float eps, void *act_pack, int32_t rows,
-                         int32_t cols)
+                         int32_t cols, bool fast)
 {
     const int nb = cols / 32;
     if (!resnorm_shape(cols) || rows % 64 != 0 || h_in == h_out)
@@ -1266,16 +1278,21 @@ int launch_geglu_resnorm(mrml_hip_ctx *ctx, const void *wg, const void *wu, cons
                     cols);
     if (int rc = check_even(ctx, rows, nb)) return rc;
     MRML_FOLD16_NB(nb, {
-        hipLaunchKernelGGL((gemv_q4_0_geglu_resnorm_kernel<NB>), dim3(rows / 64), dim3(64 * kGegluResWaves),
-                           geglu_resnorm_lds<NB>(), ctx->stream, (const uint8_t *)wg, (const uint8_t *)wu, t, w_post,
-                           h_in, h_out, w_norm, eps, (uint8_t *)act_pack, rows);
+        if (fast)
+            hipLaunchKernelGGL((gemv_q4_0_geglu_resnorm_kernel<NB, true>), dim3(rows / 64), dim3(64 * kGegluResWaves),
+                               geglu_resnorm_lds<NB>(), ctx->stream, (const uint8_t *)wg, (const uint8_t *)wu, t,
+                               w_post, h_in, h_out, w_norm, eps, (uint8_t *)act_pack, rows);
+        else
+            hipLaunchKernelGGL((gemv_q4_0_geglu_resnorm_kernel<NB, false>), dim3(rows / 64),
+                               dim3(64 * kGegluResWaves), geglu_resnorm_lds<NB>(), ctx->stream, (const uint8_t *)wg,
+                               (const uint8_t *)wu, t, w_post, h_in, h_out, w_norm, eps, (uint8_t *)act_pack, rows);
     });
     return check_launch(ctx, "gemv_q4_0_geglu_resnorm_kernel");
 }
 
 int launch_qkv_resnorm(mrml_hip_ctx *ctx, const void *wq, const void *wk, const void *wv, const float *t,
                        const float *w_post, const float *h_in, float *h_out, const float *w_norm, float eps, float *y,
-                       int32_t q_rows, int32_t kv_rows, int32_t cols)
+                       int32_t q_rows, int32_t kv_rows, int32_t cols, bool fast)
 {
     const int nb = cols / 32;
     if (!resnorm_shape(cols) || h_in == h_out)
@@ -1284,9 +1301,15 @@ int launch_qkv_resnorm(mrml_hip_ctx *ctx, const void *wq, const void *wk, const 
     if (int rc = check_even(ctx, kv_rows, nb)) return rc;
     const int total = q_rows + 2 * kv_rows;
     MRML_FOLD16_NB(nb, {
-        hipLaunchKernelGGL((gemv_q4_0_qkv_resnorm_kernel<NB>), dim3((total + 31) / 32), dim3(64 * kResWaves),
-                           resnorm_lds(NB), ctx->stream, (const uint8_t *)wq, (const uint8_t *)wk,
-                           (const uint8_t *)wv, t, w_post, h_in, h_out, w_norm, eps, y, q_rows, kv_rows);
+        if (fast)
+            hipLaunchKernelGGL((gemv_q4_0_qkv_resnorm_kernel<NB, true>), dim3((total + 31) / 32), dim3(64 * kResWaves),
+                               resnorm_lds(NB), ctx->stream, (const uint8_t *)wq, (const uint8_t *)wk,
+                               (const uint8_t *)wv, t, w_post, h_in, h_out, w_norm, eps, y, q_rows, kv_rows);
+        else
+            hipLaunchKernelGGL((gemv_q4_0_qkv_resnorm_kernel<NB, false>), dim3((total + 31) / 32),
+                               dim3(64 * kResWaves), resnorm_lds(NB), ctx->stream, (const uint8_t *)wq,
+                               (const uint8_t *)wk, (const uint8_t *)wv, t, w_post, h_in, h_out, w_norm, eps, y,
+                               q_rows, kv_rows);
     });
     return check_launch(ctx, "gemv_q4_0_qkv_resnorm_kernel");
 }

@@ -94,12 +94,13 @@ int launch_argmax_step(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *ou
 // norm with w_norm) fused ahead of the gate/up GeGLU or the q|k|v matvec
 // (gemv_q4_0.hip); h_out must not alias h_in.
 bool resnorm_shape(int cols);
+// fast: the decode step's tolerance path (tree sums for both norms).
 int launch_geglu_resnorm(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *t, const float *w_post,
                          const float *h_in, float *h_out, const float *w_norm, float eps, void *act_pack, int32_t rows,
-                         int32_t cols);
+                         int32_t cols, bool fast = false);
 int launch_qkv_resnorm(mrml_hip_ctx *ctx, const void *wq, const void *wk, const void *wv, const float *t,
                        const float *w_post, const float *h_in, float *h_out, const float *w_norm, float eps, float *y,
-                       int32_t q_rows, int32_t kv_rows, int32_t cols);
+                       int32_t q_rows, int32_t kv_rows, int32_t cols, bool fast = false);
 
 // ---- decode-step ops (decode.hip) --------------------------------------------
 bool norm_dim_ok(int dim);
@@ -134,6 +135,19 @@ int launch_attn_decode_rope_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k
 // (nullable) takes and clears the count of waits given up.
 hipError_t wait_guard_gemv(int polls, uint32_t *timeouts);
 hipError_t wait_guard_decode(int polls, uint32_t *timeouts);
+
+// Split-K decode attention, the decode step's tolerance path (decode.hip):
+// tiles of 64 positions, then a merge that also writes the Q8_0 pack.  With
+// rope, qkv is the raw stacked q|k|v vector (RoPE and the K/V append as in
+// launch_attn_decode_rope_f16); without, the q of a token whose K/V rows are
+// in the caches.  scratch: attn_split_scratch_bytes(n_heads, capacity).
+// Query-head groups of at most 8.
+int attn_split_tiles(int capacity);
+size_t attn_split_scratch_bytes(int n_heads, int capacity);
+int launch_attn_split_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k_cache, uint16_t *v_cache, float *out,
+                          void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads, float scale,
+                          int capacity, bool rope, const float *table, int n_table, float base, float freq_scale,
+                          void *scratch);
 
 // Which form of the C library's expf the host runs (glibc picks its FMA build
 // on x86-64 CPUs with FMA and AVX2); the device reproduces the same one.

@@ -67,6 +67,8 @@ int check_model_config(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config &c)
     REQUIRE(ctx, c.tie_type == MRML_HIP_Q4_0 || c.tie_type == MRML_HIP_Q8_0,
             "gemma2: tie_type must be Q4_0 or Q8_0");
     REQUIRE(ctx, c.ctx_len <= attn_max_capacity(), "gemma2: ctx_len=%d above %d", c.ctx_len, attn_max_capacity());
+    REQUIRE(ctx, c.numerics == MRML_HIP_NUMERICS_EXACT || c.numerics == MRML_HIP_NUMERICS_FAST,
+            "gemma2: numerics=%d is neither EXACT (0) nor FAST (1)", c.numerics);
     return MRML_HIP_OK;
 }
 
@@ -158,6 +160,28 @@ int mrml_hip_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *
                                   capacity, part);
 }
 
+int mrml_hip_attn_decode_f16_split(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache,
+                                   const uint16_t *v_cache, float *out, void *pack, int32_t n_past,
+                                   const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                   float scale, int32_t capacity)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, q && k_cache && v_cache && (out || pack), "attn_decode_f16_split: null pointer or no output");
+    REQUIRE(ctx, head_dim == attn_head_dim(), "attn_decode_f16_split: head_dim=%d unsupported (kernel serves %d)",
+            head_dim, attn_head_dim());
+    REQUIRE(ctx, n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= 8,
+            "attn_decode_f16_split: n_heads=%d n_kv_heads=%d (group of at most 8)", n_heads, n_kv_heads);
+    REQUIRE(ctx, capacity > 0 && capacity <= attn_max_capacity() && (d_pos || n_past >= 0),
+            "attn_decode_f16_split: n_past=%d capacity=%d (at most %d)", n_past, capacity, attn_max_capacity());
+    REQUIRE(ctx, ((((uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)q | (uintptr_t)pack) & 15) == 0),
+            "attn_decode_f16_split: pointers must be 16-byte aligned");
+    void *part = workspace(ctx, attn_split_scratch_bytes(n_heads, capacity));
+    if (!part) return MRML_HIP_E_ALLOC;
+    return launch_attn_split_f16(ctx, q, const_cast<uint16_t *>(k_cache), const_cast<uint16_t *>(v_cache), out, pack,
+                                 d_pos, n_past, n_heads, n_kv_heads, scale, capacity, false, nullptr, 0, 0.0f, 0.0f,
+                                 part);
+}
+
 // ---- the Gemma-2-shape model --------------------------------------------------------
 
 int mrml_hip_gemma2_create(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config *cfg, const void *tok_embd,
@@ -193,7 +217,10 @@ int mrml_hip_gemma2_create(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config *cfg,
                  o_f = take(c.dim * 4), o_act = take((size_t)c.ffn_dim * 4), o_logits = take((size_t)c.vocab * 4),
                  o_xpack = take(act_pack_bytes((int)(in_max / 32))), o_apack = take(act_pack_bytes((int)(qd / 32))),
                  o_actpack = take(act_pack_bytes(c.ffn_dim / 32)),
-                 o_part = take(attn_scratch_bytes(c.n_heads, c.ctx_len)),
+                 o_part = take(std::max(attn_scratch_bytes(c.n_heads, c.ctx_len),
+                                        c.numerics == MRML_HIP_NUMERICS_FAST
+                                            ? attn_split_scratch_bytes(c.n_heads, c.ctx_len)
+                                            : (size_t)0)),
                  o_argmax = take((size_t)argmax_parts(c.vocab) * 8),
                  o_rope = take((size_t)c.ctx_len * c.head_dim * sizeof(float));
     hipError_t e = hipMalloc(&m->arena, off);
@@ -259,6 +286,7 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
     // workgroup there reads h while workgroup 0 writes the update, so h
     // alternates between two buffers (A -> B -> A per block) and ends in A.
     const bool fused = resnorm_shape(c.dim) && c.ffn_dim % 64 == 0;
+    const bool fast = c.numerics == MRML_HIP_NUMERICS_FAST;
     float *hA = m->h, *hB = m->h2;
     STEP(launch_embedding(ctx, m->tok_embd, c.tie_type, d_token, 0, sqrtf((float)c.dim), hA,
                           m->layers[0].attn_norm, c.eps, nullptr, m->xpack, c.dim, c.vocab));
@@ -268,10 +296,14 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
         const float *next_norm = l + 1 < c.n_layers ? m->layers[l + 1].attn_norm : m->output_norm;
         if (fused && l > 0)
             STEP(launch_qkv_resnorm(ctx, L.wq, L.wk, L.wv, m->f, m->layers[l - 1].post_ffw_norm, hB, hA, L.attn_norm,
-                                    c.eps, m->qkv, qd, kvd, c.dim));
+                                    c.eps, m->qkv, qd, kvd, c.dim, fast));
         else
             STEP(launch_gemv_q4_0_qkv(ctx, L.wq, L.wk, L.wv, m->xpack, m->qkv, qd, kvd, c.dim));
-        if (attn_rope_ok(c.n_heads, c.n_kv_heads)) {
+        if (fast) {
+            STEP(launch_attn_split_f16(ctx, m->qkv, kc, vc, nullptr, m->attn_pack, d_pos, 0, c.n_heads, c.n_kv_heads,
+                                       c.attn_scale, c.ctx_len, true, m->rope_table, c.ctx_len, c.rope_base, 1.0f,
+                                       m->attn_part));
+        } else if (attn_rope_ok(c.n_heads, c.n_kv_heads)) {
             STEP(launch_attn_decode_rope_f16(ctx, m->qkv, kc, vc, nullptr, m->attn_pack, d_pos, 0, c.n_heads,
                                              c.n_kv_heads, c.attn_scale, c.ctx_len, m->rope_table, c.ctx_len,
                                              c.rope_base, 1.0f, m->attn_part));
@@ -284,7 +316,7 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
         STEP(launch_gemv_q4_0(ctx, L.wo, m->attn_pack, m->o, c.dim, qd));
         if (fused) {
             STEP(launch_geglu_resnorm(ctx, L.w_gate, L.w_up, m->o, L.post_attn_norm, hA, hB, L.ffn_norm, c.eps,
-                                      m->act_pack, c.ffn_dim, c.dim));
+                                      m->act_pack, c.ffn_dim, c.dim, fast));
         } else {
             STEP(launch_residual_rms_norm(ctx, m->o, L.post_attn_norm, hA, hA, L.ffn_norm, c.eps, nullptr, m->xpack,
                                           c.dim));

@@ -28,9 +28,19 @@ __device__ __forceinline__ float4 sq4(float4 a) { return make_float4(a.x * a.x, 
 // stay in registers and `lds` holds an mrml_xsum::Shared4; otherwise they are
 // staged in LDS: n4*4 floats, n4*4 flag bytes (16-byte aligned end), then an
 // mrml_xsum::Shared.
-template <int CH>
+//
+// FAST (the decode step's tolerance path): a deterministic tree sum instead
+// (exact_sum.h's block_tree_sum; needs CH == 1), the first floats of lds as
+// its scratch.
+template <int CH, bool FAST = false>
 __device__ float block_seq_sum_sq(const float4 (&v)[CH], int n4, float *lds)
 {
+    if constexpr (FAST) {
+        static_assert(CH == 1, "one chunk per thread");
+        const int c = threadIdx.x;
+        const float4 q = sq4(v[0]);
+        return mrml_xsum::block_tree_sum(c < n4 ? (q.x + q.y) + (q.z + q.w) : 0.0f, lds);
+    }
     if constexpr (CH == 1) {
         auto *x = reinterpret_cast<mrml_xsum::Shared4 *>(lds);
         return mrml_xsum::block_seq_sum_nonneg4(sq4(v[0]), n4 * 4, *x);
@@ -142,14 +152,14 @@ __device__ __forceinline__ ResidualOps residual_load(const float *__restrict__ t
 // reading it.  h_out may equal h_in (each thread reads its chunk before
 // writing it) only when no other workgroup reads h_in.  SPLIT: the pack is
 // written in split-nibble form.
-template <bool SPLIT = false, class Fetch>
+template <bool SPLIT = false, bool FAST = false, class Fetch>
 __device__ __forceinline__ void residual_norm1(float4 t, Fetch fetch, bool has_wpost, bool has_wnext, float eps,
                                                float *h_out, float *xn, uint8_t *pack, int dim,
                                                mrml_xsum::Shared4 &x)
 {
     const int n4 = dim >> 2, c = threadIdx.x;
     float4 v[1] = {t};
-    const float s1 = rms_scale(block_seq_sum_sq<1>(v, n4, reinterpret_cast<float *>(&x)), dim, eps);
+    const float s1 = rms_scale(block_seq_sum_sq<1, FAST>(v, n4, reinterpret_cast<float *>(&x)), dim, eps);
     float4 tn = scale4(t, s1);
     if (has_wpost) tn = mul4(tn, fetch(1));
     const float4 hn = add4(fetch(0), tn);
@@ -157,17 +167,17 @@ __device__ __forceinline__ void residual_norm1(float4 t, Fetch fetch, bool has_w
     if (!xn && !pack) return;
     v[0] = c < n4 ? hn : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     const float4 wv[1] = {fetch(2)};
-    norm_store<1, SPLIT>(v, rms_scale(block_seq_sum_sq<1>(v, n4, reinterpret_cast<float *>(&x)), dim, eps), wv,
-                         has_wnext, xn, pack, n4);
+    norm_store<1, SPLIT>(v, rms_scale(block_seq_sum_sq<1, FAST>(v, n4, reinterpret_cast<float *>(&x)), dim, eps),
+                         wv, has_wnext, xn, pack, n4);
 }
 
-template <bool SPLIT = false>
+template <bool SPLIT = false, bool FAST = false>
 __device__ __forceinline__ void residual_norm1(const ResidualOps &r, bool has_wpost, bool has_wnext, float eps,
                                                float *h_out, float *xn, uint8_t *pack, int dim,
                                                mrml_xsum::Shared4 &x)
 {
-    residual_norm1<SPLIT>(r.t, [&](int k) { return k == 0 ? r.h : (k == 1 ? r.wp : r.wn); }, has_wpost, has_wnext, eps, h_out,
-                   xn, pack, dim, x);
+    residual_norm1<SPLIT, FAST>(r.t, [&](int k) { return k == 0 ? r.h : (k == 1 ? r.wp : r.wn); }, has_wpost,
+                                has_wnext, eps, h_out, xn, pack, dim, x);
 }
 
 // Waits for this wave's outstanding global loads (s_waitcnt vmcnt(0), other

@@ -264,12 +264,62 @@ def test_attention_single_position_is_v(backend, dev, orc, synth):
     assert np.array_equal(got, np.repeat(v0, 2, axis=0).reshape(-1))
 
 
+# ------------------------------------------------------------ split-K attention (FAST numerics)
+def attention_split_case(backend, dev, orc, synth, n_past, cap, seed, nh=8, nkv=4, qscale=0.5):
+    hd = 256
+    rng = synth.rng_for(3600 + seed)
+    kvd = nkv * hd
+    q = rng.standard_normal(nh * hd).astype(np.float32) * np.float32(qscale)
+    kc = rng.standard_normal(cap * kvd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(cap * kvd).astype(np.float16).view(np.uint16)
+    qb, kb, vb = (backend.HipBuffer.from_host(dev, a) for a in (q, kc, vc))
+    out = backend.HipBuffer.alloc(dev, nh * hd)
+    pk = backend.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(nh * hd), np.uint8)
+    dev.attention_causal_split(qb, kb, vb, out, n_past, nh, nkv, hd, 1.0 / 16.0, cap, pack=pk)
+    dev.sync()
+    count = n_past + 1
+    rows = [(t % cap) for t in range(max(0, count - cap), count)]
+    kr = kc.reshape(cap, kvd)[rows].reshape(-1)
+    vr = vc.reshape(cap, kvd)[rows].reshape(-1)
+    ref = orc.attention_f16(q, kr, vr, len(rows) - 1, nh, nkv, hd, 1.0 / 16.0)
+    return out.numpy(), ref, pk.numpy()
+
+
+SPLIT_TOL = 1e-5   # north_star: <= 1e-5 max-rel against the CPU path
+
+
+@pytest.mark.parametrize("n_past", [0, 1, 62, 63, 64, 65, 511, 767, 2047, 4095])
+def test_attention_split_within_tolerance(backend, dev, orc, synth, n_past):
+    """Split-K (flash-decoding) attention against the oracle's sequential
+    attention: max |got - ref| <= 1e-5 * max |ref| per call (the FAST
+    numerics bar), and its Q8_0 pack is exactly the quantiser of its own f32
+    output."""
+    got, ref, pack = attention_split_case(backend, dev, orc, synth, n_past, 4096, n_past)
+    err = max_rel(got, ref)
+    print(f"\n[split attn] n_past {n_past}: max-rel {err:.2e}", flush=True)
+    assert err <= SPLIT_TOL
+    check_pack(orc, pack, got, "split attention")
+
+
+@pytest.mark.parametrize("nh,nkv", [(8, 8), (8, 1), (6, 1), (16, 4), (4, 2)])
+def test_attention_split_head_groups_and_ring(backend, dev, orc, synth, nh, nkv):
+    for n_past, cap in [(300, 4096), (100, 64), (1000, 96)]:   # the last two wrap the ring
+        got, ref, _ = attention_split_case(backend, dev, orc, synth, n_past, cap, 50 + nh + nkv + n_past, nh, nkv)
+        assert max_rel(got, ref) <= SPLIT_TOL, (nh, nkv, n_past, cap)
+
+
+def test_attention_split_wide_scores(backend, dev, orc, synth):
+    # scores spread over tens of units: the tile maxima differ widely
+    got, ref, _ = attention_split_case(backend, dev, orc, synth, 700, 1024, 9, qscale=4.0)
+    assert max_rel(got, ref) <= SPLIT_TOL
+
+
 # ------------------------------------------------------------ the token step
-def run_gpu_decode(backend, dev, model, prompt, n_decode, use_graph=True):
+def run_gpu_decode(backend, dev, model, prompt, n_decode, use_graph=True, numerics=0):
     """Prefill `prompt` token by token, then decode greedily.  Returns the
     argmax of every step (hist[p] = argmax at position p), the logits of every
     step and the final caches."""
-    m = backend.Gemma2Model.from_host(dev, model)
+    m = backend.Gemma2Model.from_host(dev, model, numerics=numerics)
     c = model["cfg"]
     total = len(prompt) + n_decode
     state = backend.HipBuffer.from_host(dev, np.array([prompt[0], 0], np.int32))
@@ -534,6 +584,105 @@ def test_gemma2_2b_layers_fused_residual(backend, dev, orc, synth):
         assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
 
 
+@pytest.mark.parametrize("tie_q8", [False, True])
+def test_gemma2_tiny_fast_numerics(backend, dev, orc, synth, tie_q8):
+    """FAST numerics (tree-order norm sums, split-K attention) on the tiny
+    model: the greedy tokens equal the oracle's, the graph replay equals the
+    eager step bit for bit (the fast path is deterministic), and the logits
+    stay close to the oracle's (each op is within 1e-5; a quantised
+    activation may move by one quantum, so the logits are bounded looser)."""
+    model = synth.gemma2_model(TINY, seed=11, tie_q8=tie_q8)
+    prompt = synth.prompt_tokens(5, TINY["vocab"], seed=3)
+    n_dec = 20
+    hist, lg_gpu, _, _ = run_gpu_decode(backend, dev, model, prompt, n_dec, numerics=1)
+    want, lg_ref, _ = run_oracle_decode(orc, model, prompt, n_dec)
+    assert_same_tokens(hist, want)
+    worst = max(max_rel(a, b) for a, b in zip(lg_gpu, lg_ref))
+    print(f"\n[fast tiny] worst logit max-rel {worst:.2e}", flush=True)
+    assert worst <= 2e-2
+    eager = run_gpu_decode(backend, dev, model, prompt, n_dec, use_graph=False, numerics=1)
+    assert np.array_equal(eager[0], hist)
+    for x, y in zip(eager[1], lg_gpu):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+
+
+def test_gemma2_2b_fast_numerics_picks(backend, dev, orc, synth):
+    """FAST numerics at the Gemma-2-2B shape (26 layers, 256000 tied Q4_0
+    vocabulary), 128 teacher-forced steps against the oracle.  FAST is not
+    bit-identical: a norm or attention output a few ulps off can move one
+    Q8_0 quant of the next product's input, and on this random-init model such
+    a move grows over 26 layers to a few percent of the largest logit while
+    the smallest top-2 gap of the oracle's logits is about 0.2 %.  So the bar
+    here is: the great majority of picks equal the oracle's, and every pick
+    that differs is a near-tie in the oracle's own logits (its logit within 5 %
+    of the largest magnitude of the best one).  Identical greedy tokens are
+    the EXACT numerics' guarantee (test_gemma2_2b_greedy_64)."""
+    cfg = dict(synth.GEMMA2_2B)
+    model = synth.gemma2_model(cfg, seed=1)
+    prompt = synth.prompt_tokens(128, cfg["vocab"], seed=1)
+    hist, lg_gpu, _, _ = run_gpu_decode(backend, dev, model, prompt, 0, numerics=1)
+    want, lg_ref, _ = run_oracle_decode(orc, model, prompt, 0)
+    worst = max(max_rel(a, b) for a, b in zip(lg_gpu, lg_ref))
+    same = int(np.sum(hist == want))
+    print(f"\n[fast 2b] picks equal to the oracle's {same}/{len(want)}, worst logit max-rel {worst:.2e}", flush=True)
+    assert same >= 0.85 * len(want)
+    for s_, (g, l) in enumerate(zip(hist, lg_ref)):
+        assert l[g] >= l.max() - 0.05 * np.max(np.abs(l)), f"step {s_}: pick {g} is not a near-tie of {np.argmax(l)}"
+
+
+def test_gemma2_2b_oracle_at_bench_positions(backend, dev, orc, synth):
+    """The 2B-shape step where the bench runs it: caches holding 512 seeded
+    f16 rows per layer (the same rows in the oracle's caches), then 16
+    teacher-forced steps at positions 512..527 -- logits and tokens
+    bit-identical to the oracle's (EXACT numerics); under FAST numerics every
+    pick equals the oracle's or is a near-tie of it."""
+    cfg = dict(synth.GEMMA2_2B)
+    model = synth.gemma2_model(cfg, seed=1)
+    P0, n = 512, 16
+    kvd = cfg["n_kv_heads"] * cfg["head_dim"]
+    rng = np.random.default_rng(7)
+    fill = np.zeros(cfg["n_layers"] * cfg["ctx_len"] * kvd, np.uint16).reshape(cfg["n_layers"], cfg["ctx_len"], kvd)
+    fill[:, :P0] = rng.standard_normal((cfg["n_layers"], P0, kvd), dtype=np.float32).astype(np.float16).view(np.uint16)
+    kfill = fill.reshape(-1)
+    vfill = np.ascontiguousarray(fill[:, :, ::-1]).reshape(-1)
+    toks = synth.prompt_tokens(P0 + n, cfg["vocab"], seed=2)
+    o = orc.OracleGemma2(model)
+    o.k_cache[:] = kfill
+    o.v_cache[:] = vfill
+    lg = np.zeros(cfg["vocab"], np.float32)
+    want, lg_ref = [], []
+    for i in range(n):
+        want.append(o.step(int(toks[P0 + i]), P0 + i, threads=THREADS, logits=lg))
+        lg_ref.append(lg.copy())
+    for numerics in (0, 1):
+        m = backend.Gemma2Model.from_host(dev, model, numerics=numerics)
+        kc = backend.HipBuffer.from_host(dev, kfill)
+        vc = backend.HipBuffer.from_host(dev, vfill)
+        state = backend.HipBuffer.from_host(dev, np.array([toks[P0], P0], np.int32))
+        hist = backend.HipBuffer.from_host(dev, np.full(P0 + n, -1, np.int32))
+        pr = backend.HipBuffer.from_host(dev, np.asarray(toks, np.int32))
+        logits = backend.HipBuffer.alloc(dev, cfg["vocab"])
+        got = []
+        for _ in range(n):
+            m.step(state, kc, vc, logits=logits, hist=hist, hist_cap=P0 + n, prompt=pr, prompt_len=P0 + n)
+            dev.sync()
+            got.append(logits.numpy())
+        h = hist.numpy()[P0:]
+        m.close()
+        if numerics == 0:
+            assert np.array_equal(h, np.array(want, np.int32)), (h, want)
+            for i in range(n):
+                assert_bits(got[i], lg_ref[i], f"logits at position {P0 + i}")
+        else:
+            # FAST: picks equal the oracle's or are near-ties of it (see
+            # test_gemma2_2b_fast_numerics_picks)
+            same = int(np.sum(h == np.array(want, np.int32)))
+            print(f"\n[fast 2b @512] picks equal {same}/{n}, worst logit max-rel "
+                  f"{max(max_rel(a, b) for a, b in zip(got, lg_ref)):.2e}", flush=True)
+            for i, (g, l) in enumerate(zip(h, lg_ref)):
+                assert l[g] >= l.max() - 0.05 * np.max(np.abs(l)), f"position {P0 + i}: pick {g} vs {np.argmax(l)}"
+
+
 def test_gemma2_2b_greedy_64(backend, dev, orc, synth):
     """Gemma-2-2B shape (26 layers, 2304, 8/4 heads of 256, FFN 9216, 256000 tied
     Q4_0 vocabulary): the greedy argmax of every step matches the oracle --
@@ -554,3 +703,5 @@ def test_gemma2_2b_greedy_64(backend, dev, orc, synth):
           f"{len(lg_ref)} steps", flush=True)
     assert_same_tokens(hist, want)
     assert exact == len(lg_ref)
+    # the teacher-forced picks depend on the context (not one repeated token)
+    assert len(set(want[:64].tolist())) >= 4
