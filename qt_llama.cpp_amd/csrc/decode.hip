@@ -751,7 +751,7 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
 // to f16 (RNE, as the cache stores them), uses them for that row and appends
 // them to the caches -- what attn_scores2_kernel<true> does for the exact
 // path.  Workgroups of tiles past the window exit at once.
-constexpr int kSplitP = 64;                    // positions per tile (one per lane)
+constexpr int kSplitP = 32;                    // positions per tile (two lanes each: dims 0..127, 128..255)
 constexpr int kSplitT = 256;                   // threads per workgroup
 constexpr int kSplitKRow = kAttnHD * 2 + 16;   // padded K row in LDS, bytes (conflict-free 16-byte reads of 64 rows)
 constexpr int kSplitPart = kAttnHD + 4;        // floats per partial: o[256], m, l, pad
@@ -777,6 +777,7 @@ __global__ __launch_bounds__(kSplitT) void attn_split_kernel(const float *__rest
     __shared__ __align__(16) uint8_t k_s[P * kSplitKRow];
     __shared__ __align__(16) uint16_t v_s[P][HD];
     __shared__ __align__(16) float e_s[8][P];
+    static_assert(P == 32, "two lanes per position");
     int window, start;
     attn_window(d_pos, n_past_arg, capacity, window, start);
     const int tile = blockIdx.x, p0 = tile * P;
@@ -786,7 +787,7 @@ __global__ __launch_bounds__(kSplitT) void attn_split_kernel(const float *__rest
     const int pos = start + window - 1;  // the newest position
     const int rnew = window - 1 - p0;    // its row in this tile (valid when < P)
     const bool has_new = ROPE && rnew < P;
-    // K and V tiles: 2048 chunks of 16 B each, chunk c of row r = c >> 5;
+    // K and V tiles: P*32 chunks of 16 B each, chunk c of row r = c >> 5;
     // rows past the window reload the last row (their scores are masked)
     constexpr int kChunks = P * (HD * 2 / 16), kPer = kChunks / kSplitT;
     u32x4 kt[kPer], vt[kPer];
@@ -842,13 +843,15 @@ __global__ __launch_bounds__(kSplitT) void attn_split_kernel(const float *__rest
     __syncthreads();
     const int wave = tid >> 6, lane = tid & 63;
     const int ntile = window - p0 < P ? window - p0 : P;  // live rows of the tile (masked scores past it)
+    const int pl = lane & (P - 1), dh = lane / P;  // position in the tile, half of the dims
     for (int g = wave; g < G; g += kSplitT / 64) {
-        // score of position p0 + lane: four partial dot products
-        const u32x4 *krow = reinterpret_cast<const u32x4 *>(k_s + lane * kSplitKRow);
-        const float4 *qg = reinterpret_cast<const float4 *>(q_s[g]);
+        // score of position p0 + pl: lane pl sums dims 0..127 and lane pl + 32
+        // dims 128..255, four partial dot products each
+        const u32x4 *krow = reinterpret_cast<const u32x4 *>(k_s + pl * kSplitKRow) + dh * (HD / 16);
+        const float4 *qg = reinterpret_cast<const float4 *>(q_s[g]) + dh * (HD / 8);
         float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 8
-        for (int d8 = 0; d8 < HD / 8; ++d8) {
+        for (int d8 = 0; d8 < HD / 16; ++d8) {
             const u32x4 kw = krow[d8];
             const float4 qa = qg[2 * d8], qb = qg[2 * d8 + 1];
             const uint32_t w[4] = {kw.x, kw.y, kw.z, kw.w};
@@ -857,15 +860,16 @@ __global__ __launch_bounds__(kSplitT) void attn_split_kernel(const float *__rest
             for (int e = 0; e < 8; ++e)
                 a[e & 3] = __builtin_fmaf(qv[e], f16_bits_to_f32((w[e >> 1] >> (16 * (e & 1))) & 0xffffu), a[e & 3]);
         }
-        const bool live = lane < ntile;
-        const float sc = ((a[0] + a[1]) + (a[2] + a[3])) * scale;
+        const bool live = pl < ntile;
+        const float part_dot = (a[0] + a[1]) + (a[2] + a[3]);
+        const float sc = (part_dot + __shfl_xor(part_dot, 32, 64)) * scale;  // the same in both lanes
         const float m = wave_max_f32(live ? sc : -INFINITY);
         const float e = live ? __builtin_expf(sc - m) : 0.0f;
-        const float l = mrml_xsum::wave_sum_f32(e);
-        e_s[g][lane] = e;
+        const float l = mrml_xsum::wave_sum_f32(dh == 0 ? e : 0.0f);
+        if (dh == 0) e_s[g][pl] = e;
         __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS writes done (lgkmcnt 0)
         __builtin_amdgcn_wave_barrier();     // (LDS accesses of one wave run in order)
-        // o[d] for d = 4*lane .. 4*lane+3 over all 64 rows of the tile (rows
+        // o[d] for d = 4*lane .. 4*lane+3 over all P rows of the tile (rows
         // past the window have e = 0 and finite values), eight rows per step
         // with their LDS reads issued together, even and odd rows in two
         // accumulators
@@ -993,6 +997,7 @@ __global__ __launch_bounds__(256) void rms_norm_group_kernel(const float *__rest
                                                              float eps, float *__restrict__ out,
                                                              uint8_t *__restrict__ pack, int dim)
 {
+    const int polls = mrml_xsum::wait_polls();  // before the operand loads
     constexpr int K = kGroupNormK;
     extern __shared__ __align__(16) uint8_t lds[];
     auto *gs = reinterpret_cast<mrml_xsum::GroupShared *>(lds);
@@ -1012,7 +1017,7 @@ __global__ __launch_bounds__(256) void rms_norm_group_kernel(const float *__rest
     for (int i = 0; i < K; ++i) sq[i] = v[i] * v[i];
     if (threadIdx.x == 0) *ctr = 0u;
     __syncthreads();
-    mrml_xsum::GroupSync sync{ctr, 0u, 4u};
+    mrml_xsum::GroupSync sync{ctr, 0u, 4u, polls};
     const float scale = rms_scale(mrml_xsum::group_seq_sum_nonneg<K>(sq, dim, wave, sync, *gs, evl), dim, eps);
 #pragma unroll
     for (int i = 0; i < K; ++i) {

@@ -538,11 +538,19 @@ constexpr int kSyncSpin = 1 << 20;
 static __device__ int g_wait_polls = kSyncSpin;
 static __device__ uint32_t g_wait_timeouts = 0u;
 
-// Waits until the wave-uniform value of *ctr reaches target; false (and one
-// timeout recorded per wave) if it gives up.
-__device__ __forceinline__ bool bounded_wait(const uint32_t *ctr, uint32_t target)
+// The poll limit, read once at a kernel's start (before its weight loads are
+// queued, so the read does not wait behind them) and passed to the waits.
+__device__ __forceinline__ int wait_polls()
 {
-    const int polls = g_wait_polls;
+    const int polls = __builtin_amdgcn_readfirstlane(g_wait_polls);
+    asm volatile("" ::"s"(polls));  // the value is in hand here, not fetched at the first wait
+    return polls;
+}
+
+// Waits until the wave-uniform value of *ctr reaches target, polling at most
+// `polls` times; false (and one timeout recorded per wave) if it gives up.
+__device__ __forceinline__ bool bounded_wait(const uint32_t *ctr, uint32_t target, int polls)
+{
 #pragma unroll 1
     for (int i = 0; i < polls; ++i) {
         const uint32_t v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -580,12 +588,13 @@ struct GroupSync {
     uint32_t *ctr;
     uint32_t target;
     uint32_t nw;
+    int polls;  // wait_polls(), read at the kernel's start
     __device__ __forceinline__ void operator()()
     {
         target += nw;
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        bounded_wait(ctr, target);
+        bounded_wait(ctr, target, polls);
         asm volatile("" ::: "memory");
     }
 };

@@ -545,13 +545,13 @@ __device__ __forceinline__ void group_norm_load(GroupNormOps<NB> &o, const float
 template <int NB, bool FAST = false>
 __device__ __forceinline__ void group_residual_norm(GroupNormOps<NB> &o, bool has_post, bool has_norm, float *h_out,
                                                     float eps, uint8_t *pack, uint8_t *lds_group, float *area,
-                                                    int wave)
+                                                    int wave, int polls)
 {
     constexpr int DIM = NB * 32, KN = norm_kn<NB>(), N4 = DIM / 4;
     const int lane = threadIdx.x & 63, k0 = KN * (64 * wave + lane);
     auto *gs = reinterpret_cast<mrml_xsum::GroupShared *>(lds_group);
     mrml_xsum::GroupSync sync{reinterpret_cast<uint32_t *>(lds_group + sizeof(mrml_xsum::GroupShared)), 0u,
-                              (uint32_t)kNormWaves};
+                              (uint32_t)kNormWaves, polls};
     float sq[KN];
 #pragma unroll
     for (int i = 0; i < KN; ++i) sq[i] = o.t[i] * o.t[i];
@@ -606,6 +606,7 @@ __global__ __launch_bounds__(64 * kGegluResWaves) void gemv_q4_0_geglu_resnorm_k
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 15;
     // the norm's operands are issued first, so they do not queue behind the
     // weights; the barrier also publishes the zeroed sync counter
+    const int polls = mrml_xsum::wait_polls();
     GroupNormOps<NB> ops;
     if (wave < kNormWaves) group_norm_load<NB>(ops, t, w_post, h_in, w_norm, wave);
     if (threadIdx.x == 0) *reinterpret_cast<uint32_t *>(lds_group + sizeof(mrml_xsum::GroupShared)) = 0u;
@@ -619,7 +620,7 @@ __global__ __launch_bounds__(64 * kGegluResWaves) void gemv_q4_0_geglu_resnorm_k
         load_row<ITERS>(ru, wu, nblk, base, NB, j);
     } else {
         group_residual_norm<NB, FAST>(ops, w_post != nullptr, w_norm != nullptr, blockIdx.x == 0 ? h_out : nullptr,
-                                      eps, lds, lds_group, area, wave);
+                                      eps, lds, lds_group, area, wave, polls);
         load_row<ITERS>(rg, wg, nblk, base, NB, j);
         load_row<ITERS>(ru, wu, nblk, base, NB, j);
     }
@@ -648,6 +649,7 @@ __global__ __launch_bounds__(64 * kGegluResWaves) void gemv_q4_0_geglu_resnorm_k
 
 template <int NB>
 constexpr size_t geglu_resnorm_lds() { return rn2_area_off<NB>() + rn2_area_bytes<NB>(128); }
+
 
 // The stacked q|k|v matvec, the post-FFN residual of the previous block and
 // this block's pre-attention norm fused ahead (32 rows per workgroup).
@@ -806,6 +808,7 @@ __global__ __launch_bounds__(64 * (S + 1)) void gemv_q4_0_long_kernel(const uint
     float *T = reinterpret_cast<float *>(lds + long_t_off<NB, S>());
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (wave == 0) {
+        const int polls = mrml_xsum::wait_polls();  // before the pack's loads
         flag[lane] = 0u;  // zero before the issue barrier inside the staging
         stage_split_pack<true>(xpack, lds, NB);
         __syncthreads();  // the pack is whole
@@ -815,7 +818,7 @@ __global__ __launch_bounds__(64 * (S + 1)) void gemv_q4_0_long_kernel(const uint
 #pragma unroll 1
         for (int k = 0; k < IPW; ++k) {
             const uint32_t want = (uint32_t)(ITERS - S * k < S ? ITERS - S * k : S);  // waves with a live iteration
-            mrml_xsum::bounded_wait(&flag[k], want);
+            mrml_xsum::bounded_wait(&flag[k], want, polls);
             asm volatile("" ::: "memory");
             float4 v[4 * S];
 #pragma unroll
