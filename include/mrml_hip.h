@@ -242,6 +242,23 @@ int mrml_hip_quantize_q8_0_gemm(mrml_hip_ctx *ctx, const float *d_x, void *d_gpa
 int mrml_hip_gemm_q4_0_gpack(mrml_hip_ctx *ctx, const void *d_w, const void *d_gpack, float *d_y,
                              int32_t rows, int32_t cols, int32_t batch);
 
+/* CudaDevice::gemm_q4_0_qkv (cuda.rs:2406-2436; layout of kernels.rs:402-469):
+ * d_x [batch][cols] f32, d_y [batch][q_rows + 2*kv_rows] f32 = the stacked
+ * q | k | v of every token, each output bit-identical to mrml_hip_gemv_q4_0
+ * on that token (the CPU path of model.rs:1388-1402).  One Q8_0 GEMM pack of
+ * the batch (workspace) feeds the three products.  q_rows, kv_rows, cols
+ * multiples of 32. */
+int mrml_hip_gemm_q4_0_qkv(mrml_hip_ctx *ctx, const void *d_wq, const void *d_wk, const void *d_wv,
+                           const float *d_x, float *d_y, int32_t q_rows, int32_t kv_rows, int32_t cols,
+                           int32_t batch);
+/* CudaDevice::gemm_q4_0_geglu (cuda.rs:2699-2725; layout of kernels.rs:597-
+ * 673): d_act [batch][rows] = gelu_tanh(g) * u with g, u the two products
+ * over Q8_0(x) of every token -- per token bit-identical to
+ * mrml_hip_gemv_q4_0_geglu (CPU semantics model.rs:2093-2105, the host
+ * libm's tanhf).  Workspace: the GEMM pack and 2*batch*rows floats. */
+int mrml_hip_gemm_q4_0_geglu(mrml_hip_ctx *ctx, const void *d_w_gate, const void *d_w_up, const float *d_x,
+                             float *d_act, int32_t rows, int32_t cols, int32_t batch);
+
 /* As mrml_hip_gemm_q4_0 (same arguments, same bit-identical outputs), but
  * it allocates nothing: no hipMalloc, no workspace growth.  No counterpart in
  * the reference; it is for callers that cannot allocate (code under HIP
@@ -277,6 +294,11 @@ int mrml_hip_argmax_f32(mrml_hip_ctx *ctx, const float *d_x, int32_t n, int32_t 
  * next matvec) are each nullable, not both.  dim % 32 == 0, dim <= 12288. */
 int mrml_hip_rms_norm(mrml_hip_ctx *ctx, const float *d_x, const float *d_w, float *d_out, void *d_pack,
                       int32_t dim, float eps);
+/* CudaDevice::rms_norm_batch (cuda.rs:2102-2180): rms_norm of each of
+ * `batch` consecutive vectors of dim values, d_x and d_out [batch][dim], d_w
+ * nullable; each row bit-identical to mrml_hip_rms_norm. */
+int mrml_hip_rms_norm_batch(mrml_hip_ctx *ctx, const float *d_x, const float *d_w, float *d_out, int32_t dim,
+                            int32_t batch, float eps);
 /* Gemma-2 sandwich-norm residual, then the next block's pre-norm (the
  * per-layer order of model.rs:1185-2260):
  *   h += rms_norm(t, w_post);  xn = rms_norm(h, w_next) -> d_xn, d_pack (nullable). */

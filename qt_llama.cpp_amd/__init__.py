@@ -147,6 +147,9 @@ _SIGNATURES = {
     "mrml_hip_gemm_q4_0": [_P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemm_q4_0_q8": [_P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemm_q4_0_noalloc": [_P, _P, _P, _P, _I, _I, _I],
+    "mrml_hip_gemm_q4_0_qkv": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I],
+    "mrml_hip_gemm_q4_0_geglu": [_P, _P, _P, _P, _P, _I, _I, _I],
+    "mrml_hip_rms_norm_batch": [_P, _P, _P, _P, _I, _I, _F],
     "mrml_hip_gemm_q4_0_noalloc_max_pack_bytes": [],
     "mrml_hip_gemm_pack_bytes": [_I, _I],
     "mrml_hip_quantize_q8_0_gemm": [_P, _P, _P, _I, _I],
@@ -384,6 +387,17 @@ class HipDevice:
 
     def gemm_q4_0(self, w, x, y, rows: int, cols: int, batch: int) -> None:
         self._check(self.lib.mrml_hip_gemm_q4_0(self.ctx, _ptr(w), _ptr(x), _ptr(y), rows, cols, batch))
+
+    def gemm_q4_0_qkv(self, wq, wk, wv, x, y, q_rows: int, kv_rows: int, cols: int, batch: int) -> None:
+        self._check(self.lib.mrml_hip_gemm_q4_0_qkv(self.ctx, _ptr(wq), _ptr(wk), _ptr(wv), _ptr(x), _ptr(y),
+                                                    q_rows, kv_rows, cols, batch))
+
+    def gemm_q4_0_geglu(self, w_gate, w_up, x, act, rows: int, cols: int, batch: int) -> None:
+        self._check(self.lib.mrml_hip_gemm_q4_0_geglu(self.ctx, _ptr(w_gate), _ptr(w_up), _ptr(x), _ptr(act),
+                                                      rows, cols, batch))
+
+    def rms_norm_batch(self, x, w, out, dim: int, batch: int, eps: float) -> None:
+        self._check(self.lib.mrml_hip_rms_norm_batch(self.ctx, _ptr(x), _ptr(w), _ptr(out), dim, batch, eps))
 
     def gemm_q4_0_noalloc(self, w, x, y, rows: int, cols: int, batch: int) -> None:
         """gemm_q4_0 without any allocation: the activations' GEMM pack goes to

@@ -87,6 +87,8 @@ __global__ __launch_bounds__(kNormMaxThreads) void rms_norm_kernel(const float *
 {
     extern __shared__ __align__(16) float lds[];
     const int n4 = dim >> 2;
+    x += (size_t)blockIdx.y * dim;  // row blockIdx.y of a batch (no pack then)
+    if (out) out += (size_t)blockIdx.y * dim;
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
     float4 v[CH], wv[CH];
 #pragma unroll
@@ -999,6 +1001,8 @@ __global__ __launch_bounds__(256) void rms_norm_group_kernel(const float *__rest
 {
     const int polls = mrml_xsum::wait_polls();  // before the operand loads
     constexpr int K = kGroupNormK;
+    x += (size_t)blockIdx.y * dim;  // row blockIdx.y of a batch (no pack then)
+    if (out) out += (size_t)blockIdx.y * dim;
     extern __shared__ __align__(16) uint8_t lds[];
     auto *gs = reinterpret_cast<mrml_xsum::GroupShared *>(lds);
     uint32_t *ctr = reinterpret_cast<uint32_t *>(lds + sizeof(mrml_xsum::GroupShared));
@@ -1038,18 +1042,22 @@ __global__ __launch_bounds__(256) void rms_norm_group_kernel(const float *__rest
     }
 }
 
-int launch_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float eps, float *out, void *pack, int dim)
+int launch_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float eps, float *out, void *pack, int dim,
+                    int rows)
 {
+    if (rows > 1 && pack)
+        return fail(ctx, MRML_HIP_E_INVALID, "rms_norm: a batch of rows writes no Q8_0 pack");
+    const dim3 grid(1, rows);
     if (dim <= 256 * kGroupNormK && dim % 4 == 0) {
-        hipLaunchKernelGGL(rms_norm_group_kernel, dim3(1), dim3(256), group_norm_lds(dim), ctx->stream, x, w, eps, out,
+        hipLaunchKernelGGL(rms_norm_group_kernel, grid, dim3(256), group_norm_lds(dim), ctx->stream, x, w, eps, out,
                            (uint8_t *)pack, dim);
         return check_launch(ctx, "rms_norm_group_kernel");
     }
     if (norm_one_chunk(dim))
-        hipLaunchKernelGGL(rms_norm_kernel<1>, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, x, w, eps,
+        hipLaunchKernelGGL(rms_norm_kernel<1>, grid, dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, x, w, eps,
                            out, (uint8_t *)pack, dim);
     else
-        hipLaunchKernelGGL(rms_norm_kernel<kMaxChunks>, dim3(1), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, x,
+        hipLaunchKernelGGL(rms_norm_kernel<kMaxChunks>, grid, dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, x,
                            w, eps, out, (uint8_t *)pack, dim);
     return check_launch(ctx, "rms_norm_kernel");
 }

@@ -105,19 +105,23 @@ struct RowRegs {
 };
 
 // Issue every load of one row (lane j, blocks 16*it + j); blocks past the row
-// end load a clamped in-bounds block and are masked out of the fold.
-template <int ITERS>
+// end load a clamped in-bounds block and are masked out of the fold.  ODD:
+// the matrix has an odd number of blocks, so the 4-byte word holding the
+// last scale would reach 2 bytes past the scale plane; every scale is then
+// read with a 2-byte load instead (the word's low half).
+template <int ITERS, bool ODD = false>
 __device__ __forceinline__ void load_row(RowRegs<ITERS> &r, const uint8_t *__restrict__ w, size_t nblk,
                                          size_t base, int nb, int j)
 {
     const uint4 *qs = reinterpret_cast<const uint4 *>(w);
     const uint32_t *dw = reinterpret_cast<const uint32_t *>(w + nblk * 16);
+    const uint16_t *dh = reinterpret_cast<const uint16_t *>(w + nblk * 16);
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
         int b = it * 16 + j;
         b = b < nb ? b : nb - 1;
         r.w[it] = qs[base + b];
-        r.d[it] = dw[(base + b) >> 1];
+        r.d[it] = ODD ? (uint32_t)dh[base + b] : dw[(base + b) >> 1];
     }
 }
 
@@ -125,7 +129,7 @@ __device__ __forceinline__ void load_row(RowRegs<ITERS> &r, const uint8_t *__res
 // split-nibble pack in LDS.  Computed unconditionally, so the compiler has
 // no conditional block to sink the weight load into (which would delay its
 // issue).
-template <int ITERS>
+template <int ITERS, bool ODD = false>
 __device__ __forceinline__ float row_term(const RowRegs<ITERS> &r, int it, const uint8_t *pack, size_t base, int nb,
                                           int j)
 {
@@ -137,7 +141,7 @@ __device__ __forceinline__ float row_term(const RowRegs<ITERS> &r, int it, const
     const uint4 w = r.w[it], lo = aq[2 * bc], hi = aq[2 * bc + 1];
     const int32_t isum = q4_0_isum_split(w.x, w.y, w.z, w.w, lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w, ac[bc]);
     const uint32_t word = r.d[it];
-    const uint32_t dbits = ((base + bc) & 1) ? word >> 16 : word & 0xffffu;
+    const uint32_t dbits = (!ODD && ((base + bc) & 1)) ? word >> 16 : word & 0xffffu;
     const float t = (float)isum * (f16_bits_to_f32(dbits) * ad[bc]);
     return b < nb ? t : 0.0f;
 }
@@ -145,13 +149,13 @@ __device__ __forceinline__ float row_term(const RowRegs<ITERS> &r, int it, const
 // Ordered fold; the row result is valid in lane 15 of the DPP row.  Masked
 // tail terms are +0, which leaves a running sum unchanged (the sum starts at
 // +0 and round-to-nearest never turns it into -0).
-template <int ITERS>
+template <int ITERS, bool ODD = false>
 __device__ __forceinline__ float fold_row(const RowRegs<ITERS> &r, const uint8_t *pack, size_t base, int nb, int j)
 {
     float s = 0.0f;
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
-        const float t = row_term<ITERS>(r, it, pack, base, nb, j);
+        const float t = row_term<ITERS, ODD>(r, it, pack, base, nb, j);
 #pragma unroll
         for (int k = 0; k < 16; ++k) s = fold16(s, t);
     }
@@ -876,7 +880,7 @@ __global__ __launch_bounds__(64 * (S + 1)) void gemv_q4_0_long_kernel(const uint
 
 // ---- runtime block count (fold16) -----------------------------------------------
 
-template <int ITERS, int WAVES>
+template <int ITERS, int WAVES, bool ODD = false>
 __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_0_any_kernel(const uint8_t *__restrict__ w,
                                                                      const uint8_t *xpack,
                                                                      float *__restrict__ y, int rows, int nb)
@@ -893,9 +897,9 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_0_any_kernel(const u
     const size_t base = (size_t)row * nb;
     RowRegs<ITERS> r;
     __builtin_amdgcn_s_barrier();  // the pack's loads are issued
-    load_row<ITERS>(r, w, (size_t)rows * nb, base, nb, j);
+    load_row<ITERS, ODD>(r, w, (size_t)rows * nb, base, nb, j);
     __syncthreads();
-    const float s = fold_row<ITERS>(r, lds, base, nb, j);
+    const float s = fold_row<ITERS, ODD>(r, lds, base, nb, j);
     if (j == 15 && row_raw < rows) y[row_raw] = s;
 }
 
@@ -1010,8 +1014,18 @@ __global__ __launch_bounds__(64) void gemv_q4_0_gguf_kernel(const uint8_t *__res
 // Waves per workgroup of the runtime-nb kernels.
 inline int waves_for(int rows) { return rows >= 8192 ? 4 : (rows >= 2048 ? 2 : 1); }
 
+// The smallest compiled iteration count >= iters (iterations past a row's
+// last block are masked, so a larger instance gives the same result).
+static int iters_round(int iters)
+{
+    static const int kInst[] = {1, 2, 3, 4, 5, 6, 8, 9, 12, 16, 18, 20};
+    for (int v : kInst)
+        if (v >= iters) return v;
+    return 0;
+}
+
 #define MRML_DISPATCH_ITERS(ITERS_VAL, BODY)                 \
-    switch (ITERS_VAL) {                                     \
+    switch (iters_round(ITERS_VAL)) {                        \
     case 1: { constexpr int IT = 1; BODY; } break;           \
     case 2: { constexpr int IT = 2; BODY; } break;           \
     case 3: { constexpr int IT = 3; BODY; } break;           \
@@ -1023,6 +1037,7 @@ inline int waves_for(int rows) { return rows >= 8192 ? 4 : (rows >= 2048 ? 2 : 1
     case 12: { constexpr int IT = 12; BODY; } break;         \
     case 16: { constexpr int IT = 16; BODY; } break;         \
     case 18: { constexpr int IT = 18; BODY; } break;         \
+    case 20: { constexpr int IT = 20; BODY; } break;         \
     default: return fail(ctx, MRML_HIP_E_UNSUPPORTED,        \
                          "q4_0 matvec: cols=%d (%d blocks) has no kernel instance", nb * 32, nb); \
     }
@@ -1055,19 +1070,66 @@ size_t pack_lds(int nb) { return align_up((size_t)nb * 40, 16); }
 
 // The scale plane is read as 4-byte words, so the block count of each matrix
 // (rows * cols/32) must be even: cols % 64 == 0 or an even row count.
+// A matrix with an odd number of blocks (rows * cols/32) keeps its last
+// scale in the first half of a 4-byte word that would reach past the scale
+// plane.  The fixed-shape kernels read scales as words, so such a matrix
+// goes through the runtime-block-count kernel with 2-byte scale loads
+// (ODD), and the fused entry points split into plain matvecs.
+static bool odd_blocks(int32_t rows, int nb) { return (((int64_t)rows * nb) & 1) != 0; }
+
 static int check_even(mrml_hip_ctx *ctx, int32_t rows, int nb)
 {
-    if (((int64_t)rows * nb) & 1)
+    if (odd_blocks(rows, nb))
         return fail(ctx, MRML_HIP_E_UNSUPPORTED,
-                    "q4_0 matvec: rows*cols/32 = %lld is odd (needs cols %% 64 == 0 or even rows)",
+                    "q4_0 fused matvec: rows*cols/32 = %lld is odd (the unfused entry points serve it)",
                     (long long)rows * nb);
     return 0;
+}
+
+// act[i] = gelu_tanh(g[i]) * u[i]: the GeGLU epilogue of the matvec kernels
+// (model.rs:2093-2105, ops.rs:99-114), elementwise.
+__global__ void geglu_rows_kernel(const float *__restrict__ g, const float *__restrict__ u, float *__restrict__ act,
+                                  int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) act[i] = gelu_tanh(g[i]) * u[i];
+}
+
+int launch_geglu_rows(mrml_hip_ctx *ctx, const float *g, const float *u, float *act, int n)
+{
+    hipLaunchKernelGGL(geglu_rows_kernel, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, g, u, act, n);
+    return check_launch(ctx, "geglu_rows_kernel");
+}
+
+static int launch_gemv_q4_0_odd(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows, int nb)
+{
+    const int iters = (nb + 15) / 16;
+    if (nb > kStageMax)
+        return fail(ctx, MRML_HIP_E_UNSUPPORTED, "q4_0 matvec: cols=%d with an odd block count above %d", nb * 32,
+                    kStageMax * 32);
+    const int waves = waves_for(rows);
+    const dim3 grid(((rows + 3) / 4 + waves - 1) / waves);
+    MRML_DISPATCH_ITERS(iters, MRML_DISPATCH_WAVES(waves, {
+        hipLaunchKernelGGL((gemv_q4_0_any_kernel<IT, WV, true>), grid, dim3(64 * (WV + 1)), pack_lds(nb),
+                           ctx->stream, (const uint8_t *)w, (const uint8_t *)xpack, y, rows, nb);
+    }));
+    return check_launch(ctx, "gemv_q4_0_any_kernel");
+}
+
+// GeGLU of an odd-block shape: the two products into gu (2*rows floats),
+// then the elementwise epilogue into act.
+static int geglu_odd(mrml_hip_ctx *ctx, const void *wg, const void *wu, const void *xpack, float *act, float *gu,
+                     int32_t rows, int nb)
+{
+    if (int rc = launch_gemv_q4_0_odd(ctx, wg, xpack, gu, rows, nb)) return rc;
+    if (int rc = launch_gemv_q4_0_odd(ctx, wu, xpack, gu + rows, rows, nb)) return rc;
+    return launch_geglu_rows(ctx, gu, gu + rows, act, rows);
 }
 
 int launch_gemv_q4_0(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows, int32_t cols)
 {
     const int nb = cols / 32;
-    if (int rc = check_even(ctx, rows, nb)) return rc;
+    if (odd_blocks(rows, nb)) return launch_gemv_q4_0_odd(ctx, w, xpack, y, rows, nb);
     if (fold16_shape(nb)) {
         const dim3 grid(((rows + 3) / 4 + kFoldWaves - 1) / kFoldWaves);
         MRML_FOLD16_NB(nb, {
@@ -1096,8 +1158,7 @@ int launch_gemv_q4_0(mrml_hip_ctx *ctx, const void *w, const void *xpack, float 
 int launch_gemv_q4_0_x(mrml_hip_ctx *ctx, const void *w, const float *x, float *y, int32_t rows, int32_t cols)
 {
     const int nb = cols / 32;
-    if (int rc = check_even(ctx, rows, nb)) return rc;
-    if (fold16_shape(nb)) {
+    if (fold16_shape(nb) && !odd_blocks(rows, nb)) {
         const dim3 grid(((rows + 3) / 4 + kFoldWaves - 1) / kFoldWaves);
         MRML_FOLD16_NB(nb, {
             hipLaunchKernelGGL((gemv_q4_0_kernel<NB, kFoldWaves, true>), grid, dim3(64 * (kFoldWaves + kNQ)),
@@ -1115,7 +1176,11 @@ int launch_gemv_q4_0_geglu(mrml_hip_ctx *ctx, const void *wg, const void *wu, co
                            int32_t rows, int32_t cols)
 {
     const int nb = cols / 32;
-    if (int rc = check_even(ctx, rows, nb)) return rc;
+    if (odd_blocks(rows, nb)) {  // xpack is never the workspace here (launch_gemv_q4_0_geglu_x handles its own)
+        float *gu = (float *)workspace(ctx, (size_t)2 * rows * sizeof(float));
+        if (!gu) return MRML_HIP_E_ALLOC;
+        return geglu_odd(ctx, wg, wu, xpack, act, gu, rows, nb);
+    }
     if (fold16_shape(nb)) {
         const dim3 grid(((rows + 3) / 4 + kFoldWaves - 1) / kFoldWaves);
         MRML_FOLD16_NB(nb, {
@@ -1148,7 +1213,13 @@ int launch_gemv_q4_0_geglu_emit(mrml_hip_ctx *ctx, const void *wg, const void *w
                                 void *act_pack, int32_t rows, int32_t cols)
 {
     const int nb = cols / 32;
-    if (int rc = check_even(ctx, rows, nb)) return rc;
+    if (odd_blocks(rows, nb)) {
+        float *gu = (float *)workspace(ctx, (size_t)3 * rows * sizeof(float));
+        if (!gu) return MRML_HIP_E_ALLOC;
+        float *out = act ? act : gu + 2 * (size_t)rows;
+        if (int rc = geglu_odd(ctx, wg, wu, xpack, out, gu, rows, nb)) return rc;
+        return launch_quantize_q8_0(ctx, out, nullptr, act_pack, rows);
+    }
     if (fold16_shape(nb) && rows % 32 == 0) {
         MRML_FOLD16_NB(nb, {
             hipLaunchKernelGGL((gemv_q4_0_geglu_kernel<NB, 8, false, true>), dim3(rows / 32), dim3(64 * 9),
@@ -1185,7 +1256,17 @@ int launch_gemv_q4_0_geglu_x(mrml_hip_ctx *ctx, const void *wg, const void *wu, 
                              void *act_pack, int32_t rows, int32_t cols)
 {
     const int nb = cols / 32;
-    if (int rc = check_even(ctx, rows, nb)) return rc;
+    if (odd_blocks(rows, nb)) {
+        // one workspace: x's pack, then g, u and (without act) the output
+        const size_t in_bytes = align_up(act_pack_bytes(nb), 16);
+        uint8_t *ws = (uint8_t *)workspace(ctx, in_bytes + (size_t)3 * rows * sizeof(float));
+        if (!ws) return MRML_HIP_E_ALLOC;
+        float *gu = reinterpret_cast<float *>(ws + in_bytes), *out = act ? act : gu + 2 * (size_t)rows;
+        if (int rc = launch_quantize_q8_0(ctx, x, nullptr, ws, cols)) return rc;
+        if (int rc = geglu_odd(ctx, wg, wu, ws, out, gu, rows, nb)) return rc;
+        if (act_pack) return launch_quantize_q8_0(ctx, out, nullptr, act_pack, rows);
+        return MRML_HIP_OK;
+    }
     if (fold16_shape(nb) && !act_pack) return launch_geglu_f32(ctx, wg, wu, x, act, rows, nb);
     if (fold16_shape(nb) && (!act_pack || rows % 32 == 0)) {
         if (act_pack) {
@@ -1218,8 +1299,11 @@ int launch_gemv_q4_0_qkv(mrml_hip_ctx *ctx, const void *wq, const void *wk, cons
                          float *y, int32_t q_rows, int32_t kv_rows, int32_t cols)
 {
     const int nb = cols / 32;
-    if (int rc = check_even(ctx, q_rows, nb)) return rc;
-    if (int rc = check_even(ctx, kv_rows, nb)) return rc;
+    if (odd_blocks(q_rows, nb) || odd_blocks(kv_rows, nb)) {  // three plain products into the stacked rows
+        if (int rc = launch_gemv_q4_0(ctx, wq, xpack, y, q_rows, cols)) return rc;
+        if (int rc = launch_gemv_q4_0(ctx, wk, xpack, y + q_rows, kv_rows, cols)) return rc;
+        return launch_gemv_q4_0(ctx, wv, xpack, y + q_rows + kv_rows, kv_rows, cols);
+    }
     const int total = q_rows + 2 * kv_rows;
     if (fold16_shape(nb)) {
         const dim3 grid(((total + 3) / 4 + kFoldWaves - 1) / kFoldWaves);
@@ -1245,10 +1329,8 @@ int launch_gemv_q4_0_qkv_x(mrml_hip_ctx *ctx, const void *wq, const void *wk, co
                            float *y, int32_t q_rows, int32_t kv_rows, int32_t cols)
 {
     const int nb = cols / 32;
-    if (int rc = check_even(ctx, q_rows, nb)) return rc;
-    if (int rc = check_even(ctx, kv_rows, nb)) return rc;
     const int total = q_rows + 2 * kv_rows;
-    if (fold16_shape(nb)) {
+    if (fold16_shape(nb) && !odd_blocks(q_rows, nb) && !odd_blocks(kv_rows, nb)) {
         const dim3 grid(((total + 3) / 4 + kFoldWaves - 1) / kFoldWaves);
         MRML_FOLD16_NB(nb, {
             hipLaunchKernelGGL((gemv_q4_0_qkv_kernel<NB, kFoldWaves, true>), grid, dim3(64 * (kFoldWaves + kNQ)),

@@ -24,7 +24,10 @@ __device__ __forceinline__ void stage_pack_wave(const uint8_t *src, uint8_t *lds
 // ---- Q8_0 (quant.rs:563-577 semantics; model.rs:2842-2853 softcap) ---------
 // Backend layout: quant plane [rows*nb][32 B], scale plane [rows*nb] f16.
 
-template <int ITERS, int WAVES>
+// ODD: the matrix has an odd number of blocks, so the 4-byte word of the last
+// scale would reach past the scale plane; scales are then read with 2-byte
+// loads.
+template <int ITERS, int WAVES, bool ODD>
 __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q8_0_kernel(const uint8_t *__restrict__ w,
                                                                      const uint8_t *xpack,
                                                                      float *__restrict__ y, int rows, int nb,
@@ -56,7 +59,7 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q8_0_kernel(const uint8
         b = b < nb ? b : nb - 1;
         w0[it] = qs[2 * (base + b)];
         w1[it] = qs[2 * (base + b) + 1];
-        d[it] = dw[(base + b) >> 1];
+        d[it] = ODD ? (uint32_t)dp[base + b] : dw[(base + b) >> 1];
     }
     __syncthreads();
     const int4 *aq = reinterpret_cast<const int4 *>(lds);
@@ -77,7 +80,7 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q8_0_kernel(const uint8
             isum = sdot4(w1[it].z, (uint32_t)a1.z, isum);
             isum = sdot4(w1[it].w, (uint32_t)a1.w, isum);
             const size_t blk = base + b;
-            const float tv = (float)isum * (f16_bits_to_f32((blk & 1) ? d[it] >> 16 : d[it] & 0xffffu) * ad[b]);
+            const float tv = (float)isum * (f16_bits_to_f32((!ODD && (blk & 1)) ? d[it] >> 16 : d[it] & 0xffffu) * ad[b]);
             const float t = bt < nb ? tv : 0.0f;
 #pragma unroll
             for (int k = 0; k < 16; ++k) s = fold16(s, t);
@@ -242,6 +245,16 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float *__restri
 
 inline int waves_for(int rows) { return rows >= 8192 ? 4 : (rows >= 2048 ? 2 : 1); }
 
+// The smallest compiled iteration count >= iters (iterations past a row's
+// last block are masked, so a larger instance gives the same result), or 0.
+inline int iters_instance(int iters)
+{
+    static const int kInst[] = {1, 2, 3, 4, 5, 6, 8, 9, 12, 16, 18, 20};
+    for (int v : kInst)
+        if (v >= iters) return v;
+    return 0;
+}
+
 #define MRML_DISPATCH_WAVES(WAVES_VAL, BODY)                 \
     switch (WAVES_VAL) {                                     \
     case 1: { constexpr int WV = 1; BODY; } break;           \
@@ -255,10 +268,7 @@ int launch_gemv_q8_0(mrml_hip_ctx *ctx, const void *w, const void *xpack, float 
                      int32_t softcap)
 {
     const int nb = cols / 32;
-    if (((int64_t)rows * nb) & 1)
-        return fail(ctx, MRML_HIP_E_UNSUPPORTED,
-                    "q8_0 matvec: rows*cols/32 = %lld is odd (needs cols %% 64 == 0 or even rows)",
-                    (long long)rows * nb);
+    const bool odd = (((int64_t)rows * nb) & 1) != 0;
     const int iters = (nb + 15) / 16;
     const int waves = waves_for(rows);
     const dim3 grid(((rows + 3) / 4 + waves - 1) / waves);
@@ -266,13 +276,17 @@ int launch_gemv_q8_0(mrml_hip_ctx *ctx, const void *w, const void *xpack, float 
 #define Q8_CASE(N)                                                                                           \
     case N:                                                                                                  \
         MRML_DISPATCH_WAVES(waves, {                                                                         \
-            hipLaunchKernelGGL((gemv_q8_0_kernel<N, WV>), grid, dim3(64 * (WV + 1)), lds, ctx->stream,             \
-                               (const uint8_t *)w, (const uint8_t *)xpack, y, rows, nb, softcap);           \
+            if (odd)                                                                                         \
+                hipLaunchKernelGGL((gemv_q8_0_kernel<N, WV, true>), grid, dim3(64 * (WV + 1)), lds, ctx->stream,   \
+                                   (const uint8_t *)w, (const uint8_t *)xpack, y, rows, nb, softcap);       \
+            else                                                                                             \
+                hipLaunchKernelGGL((gemv_q8_0_kernel<N, WV, false>), grid, dim3(64 * (WV + 1)), lds, ctx->stream,  \
+                                   (const uint8_t *)w, (const uint8_t *)xpack, y, rows, nb, softcap);       \
         });                                                                                                  \
         break;
-    switch (iters) {
+    switch (iters_instance(iters)) {
         Q8_CASE(1) Q8_CASE(2) Q8_CASE(3) Q8_CASE(4) Q8_CASE(5) Q8_CASE(6) Q8_CASE(8) Q8_CASE(9)
-        Q8_CASE(12) Q8_CASE(16) Q8_CASE(18)
+        Q8_CASE(12) Q8_CASE(16) Q8_CASE(18) Q8_CASE(20)
     default:
         return fail(ctx, MRML_HIP_E_UNSUPPORTED, "q8_0 matvec: cols=%d has no kernel instance", cols);
     }
@@ -296,7 +310,7 @@ int launch_gemv_q4_k(mrml_hip_ctx *ctx, const void *w, const void *xpack, float 
                                (const uint8_t *)w, (const uint8_t *)xpack, y, rows, nsb);                   \
         });                                                                                                  \
         break;
-    switch (iters) {
+    switch (iters_instance(iters)) {
         QK_CASE(1) QK_CASE(2) QK_CASE(3) QK_CASE(4) QK_CASE(5) QK_CASE(6) QK_CASE(8) QK_CASE(9) QK_CASE(12)
         QK_CASE(16) QK_CASE(18) QK_CASE(20)
     default:

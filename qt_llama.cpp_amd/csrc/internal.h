@@ -63,6 +63,8 @@ int launch_gemv_q8_0(mrml_hip_ctx *ctx, const void *w, const void *xpack, float 
 int launch_gemv_q4_k(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y,
                      int32_t rows, int32_t cols);
 int launch_argmax_f32(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *out);
+// act[i] = gelu_tanh(g[i]) * u[i] for i < n (the matvec kernels' GeGLU epilogue).
+int launch_geglu_rows(mrml_hip_ctx *ctx, const float *g, const float *u, float *act, int n);
 // GeGLU over an activation pack that also writes the Q8_0 pack of its rows
 // outputs (act nullable).
 int launch_gemv_q4_0_geglu_emit(mrml_hip_ctx *ctx, const void *wg, const void *wu, const void *xpack, float *act,
@@ -104,7 +106,9 @@ int launch_qkv_resnorm(mrml_hip_ctx *ctx, const void *wq, const void *wk, const 
 
 // ---- decode-step ops (decode.hip) --------------------------------------------
 bool norm_dim_ok(int dim);
-int launch_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float eps, float *out, void *pack, int dim);
+// rows > 1: rows consecutive vectors of dim values (out only, no pack)
+int launch_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float eps, float *out, void *pack, int dim,
+                    int rows = 1);
 int launch_residual_rms_norm(mrml_hip_ctx *ctx, const float *t, const float *w_post, const float *h_in, float *h_out,
                              const float *w_next, float eps, float *xn, void *pack, int dim, int rows = 1);
 int launch_embedding(mrml_hip_ctx *ctx, const void *table, int type, const int32_t *d_token, int token, float scale,

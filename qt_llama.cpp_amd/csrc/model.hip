@@ -90,6 +90,18 @@ int mrml_hip_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float *
     return launch_rms_norm(ctx, x, w, eps, out, pack, dim);
 }
 
+int mrml_hip_rms_norm_batch(mrml_hip_ctx *ctx, const float *x, const float *w, float *out, int32_t dim, int32_t batch,
+                            float eps)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, x && out, "rms_norm_batch: null pointer");
+    REQUIRE(ctx, norm_dim_ok(dim), "rms_norm_batch: dim=%d must be a multiple of 32 up to 12288", dim);
+    REQUIRE(ctx, batch > 0 && batch <= 65535, "rms_norm_batch: batch=%d (1..65535)", batch);
+    REQUIRE(ctx, ((((uintptr_t)x | (uintptr_t)w | (uintptr_t)out) & 15) == 0),
+            "rms_norm_batch: pointers must be 16-byte aligned");
+    return launch_rms_norm(ctx, x, w, eps, out, nullptr, dim, batch);
+}
+
 int mrml_hip_residual_rms_norm(mrml_hip_ctx *ctx, const float *t, const float *w_post, float *h,
                                const float *w_next, float *xn, void *pack, int32_t dim, float eps)
 {
@@ -347,15 +359,6 @@ namespace {
 
 constexpr int kPrefillChunk = 128;  // tokens per chunk (prefill_cuda's tile, model.rs:2395-2638)
 
-// act = gelu_tanh(g) * u per element: the GeGLU epilogue of the matvec
-// kernels, so each act value has the bits the token step gives it.
-__global__ void geglu_rows_kernel(const float *__restrict__ g, const float *__restrict__ u, float *__restrict__ act,
-                                  int n)
-{
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) act[i] = gelu_tanh(g[i]) * u[i];
-}
-
 int prefill_buffers(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m)
 {
     if (m->pf_arena) return MRML_HIP_OK;
@@ -453,10 +456,9 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
             STEP(launch_gemm_pack_quantize(ctx, xn, m->pf_gpack, c.dim, n));
             STEP(launch_gemm_q4_0(ctx, L.w_gate, m->pf_gpack, m->pf_g, c.ffn_dim, c.dim, n));
             STEP(launch_gemm_q4_0(ctx, L.w_up, m->pf_gpack, m->pf_u, c.ffn_dim, c.dim, n));
-            const int nact = n * c.ffn_dim;
-            hipLaunchKernelGGL(geglu_rows_kernel, dim3((nact + 255) / 256), dim3(256), 0, ctx->stream, m->pf_g,
-                               m->pf_u, m->pf_act, nact);
-            STEP(check_launch(ctx, "geglu_rows_kernel"));
+            // act = gelu_tanh(g) * u per element: the GeGLU epilogue of the
+            // matvec kernels, so each act value has the token step's bits
+            STEP(launch_geglu_rows(ctx, m->pf_g, m->pf_u, m->pf_act, n * c.ffn_dim));
             STEP(gemm_rows(ctx, m, L.w_down, m->pf_act, m->pf_f, c.dim, c.ffn_dim, n));
             STEP(launch_residual_rms_norm(ctx, m->pf_f, L.post_ffw_norm, h, h, next_norm, c.eps, xn, nullptr, c.dim,
                                           n));

@@ -589,6 +589,43 @@ int mrml_hip_gemm_q4_0_q8(mrml_hip_ctx *ctx, const void *w, const void *xpack, f
     return rc ? rc : launch_gemm_q4_0(ctx, w, gp, y, rows, cols, batch);
 }
 
+int mrml_hip_gemm_q4_0_qkv(mrml_hip_ctx *ctx, const void *wq, const void *wk, const void *wv, const float *x,
+                           float *y, int32_t q_rows, int32_t kv_rows, int32_t cols, int32_t batch)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, wk && wv, "gemm_q4_0_qkv: null pointer");
+    CHECK_GEMM(ctx, wq, x, y, q_rows, cols, batch);
+    REQUIRE(ctx, gemm_shape_ok(kv_rows, cols, batch), "gemm_q4_0_qkv: kv_rows=%d must be a positive multiple of 32",
+            kv_rows);
+    const int32_t total = q_rows + 2 * kv_rows;
+    REQUIRE(ctx, (int64_t)batch * total <= INT32_MAX, "gemm_q4_0_qkv: batch=%d too large", batch);
+    void *gp = workspace(ctx, gemm_pack_bytes(cols, batch));
+    if (!gp) return MRML_HIP_E_ALLOC;
+    // one GEMM pack for the three products; each writes its column range of
+    // the stacked [batch][q | k | v] rows (row stride q_rows + 2*kv_rows)
+    if (int rc = launch_gemm_pack_quantize(ctx, x, gp, cols, batch)) return rc;
+    if (int rc = launch_gemm_q4_0(ctx, wq, gp, y, q_rows, cols, batch, total)) return rc;
+    if (int rc = launch_gemm_q4_0(ctx, wk, gp, y + q_rows, kv_rows, cols, batch, total)) return rc;
+    return launch_gemm_q4_0(ctx, wv, gp, y + q_rows + kv_rows, kv_rows, cols, batch, total);
+}
+
+int mrml_hip_gemm_q4_0_geglu(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *x, float *act,
+                             int32_t rows, int32_t cols, int32_t batch)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, wu, "gemm_q4_0_geglu: null pointer");
+    CHECK_GEMM(ctx, wg, x, act, rows, cols, batch);
+    // workspace: the GEMM pack, then the gate and up products [batch][rows]
+    const size_t pk = align_up(gemm_pack_bytes(cols, batch), 256), n = (size_t)batch * rows;
+    uint8_t *ws = (uint8_t *)workspace(ctx, pk + 2 * n * sizeof(float));
+    if (!ws) return MRML_HIP_E_ALLOC;
+    float *g = reinterpret_cast<float *>(ws + pk), *u = g + n;
+    if (int rc = launch_gemm_pack_quantize(ctx, x, ws, cols, batch)) return rc;
+    if (int rc = launch_gemm_q4_0(ctx, wg, ws, g, rows, cols, batch)) return rc;
+    if (int rc = launch_gemm_q4_0(ctx, wu, ws, u, rows, cols, batch)) return rc;
+    return launch_geglu_rows(ctx, g, u, act, (int)n);
+}
+
 size_t mrml_hip_gemm_pack_bytes(int32_t cols, int32_t batch)
 {
     return (cols > 0 && cols % 32 == 0 && batch > 0) ? gemm_pack_bytes(cols, batch) : 0;

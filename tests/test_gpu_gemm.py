@@ -134,3 +134,47 @@ def test_gemm_q4_0_rejects_bad_shapes(backend, dev):
     for rows, cols, batch in [(33, 32, 2), (32, 48, 2), (32, 32, 0), (32, 2304, 1 << 22)]:
         with pytest.raises(backend.HipError):
             dev.gemm_q4_0(w, x, y, rows, cols, batch)
+
+
+# ------------------------------------------------------------ fused batched entry points
+@pytest.mark.parametrize("batch", [128, 512])
+def test_gemm_q4_0_qkv_stacked_rows(backend, dev, orc, synth, batch):
+    """CudaDevice::gemm_q4_0_qkv (cuda.rs:2406-2436): y[m] = [Wq x_m | Wk x_m |
+    Wv x_m], every output bit-identical to the CPU matvec of its token."""
+    q_rows, kv_rows, cols = 2048, 1024, 2304
+    rng = synth.rng_for(5300 + batch)
+    ws = {k: synth.q4_0_matrix(rng, r, cols) for k, r in (("q", q_rows), ("k", kv_rows), ("v", kv_rows))}
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    bufs = [backend.HipBuffer.from_gguf(dev, ws[k], backend.Q4_0, r, cols)
+            for k, r in (("q", q_rows), ("k", kv_rows), ("v", kv_rows))]
+    xb = backend.HipBuffer.from_host(dev, x.reshape(-1))
+    total = q_rows + 2 * kv_rows
+    yb = backend.HipBuffer.alloc(dev, batch * total)
+    dev.gemm_q4_0_qkv(*bufs, xb, yb, q_rows, kv_rows, cols, batch)
+    dev.sync()
+    got = yb.numpy().reshape(batch, total)
+    for name, lo, r in (("q", 0, q_rows), ("k", q_rows, kv_rows), ("v", q_rows + kv_rows, kv_rows)):
+        ref = oracle_gemm(orc, ws[name], x, r, cols, range(batch))
+        assert_bit_exact(got[:, lo:lo + r], ref, f"gemm qkv {name} M={batch}")
+
+
+@pytest.mark.parametrize("batch", [128, 512])
+def test_gemm_q4_0_geglu_per_token(backend, dev, orc, synth, batch):
+    """CudaDevice::gemm_q4_0_geglu (cuda.rs:2699-2725): act[m] = gelu(Wg x_m) *
+    (Wu x_m) with the CPU semantics (model.rs:2093-2105), bit-identical to
+    the oracle per token."""
+    rows, cols = 9216, 2304
+    rng = synth.rng_for(5400 + batch)
+    wg, wu = synth.q4_0_matrix(rng, rows, cols), synth.q4_0_matrix(rng, rows, cols)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    bg = backend.HipBuffer.from_gguf(dev, wg, backend.Q4_0, rows, cols)
+    bu = backend.HipBuffer.from_gguf(dev, wu, backend.Q4_0, rows, cols)
+    xb = backend.HipBuffer.from_host(dev, x.reshape(-1))
+    ab = backend.HipBuffer.alloc(dev, batch * rows)
+    dev.gemm_q4_0_geglu(bg, bu, xb, ab, rows, cols, batch)
+    dev.sync()
+    got = ab.numpy().reshape(batch, rows)
+    g = oracle_gemm(orc, wg, x, rows, cols, range(batch))
+    u = oracle_gemm(orc, wu, x, rows, cols, range(batch))
+    ref = np.stack([orc.geglu(g[m], u[m]) for m in range(batch)])
+    assert_bit_exact(got, ref, f"gemm geglu M={batch}")

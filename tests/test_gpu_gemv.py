@@ -358,9 +358,6 @@ def test_invalid_shapes_are_rejected(backend, dev):
         dev.gemv_q4_0(wb, xb, yb, 0, 64)
     assert e.value.status == -1
     with pytest.raises(backend.HipError) as e:
-        dev.gemv_q4_0(wb, xb, yb, 1, 32)                 # odd block count: unsupported layout
-    assert e.value.status == -4
-    with pytest.raises(backend.HipError) as e:
         dev.gemv_q4_k(wb, xb, yb, 1, 64)                 # Q4_K needs cols % 256 == 0
     assert e.value.status == -1
     dev.sync()                                           # context still healthy
@@ -400,3 +397,49 @@ def test_bounded_wait_timeout_is_reported(backend, dev, orc, synth):
     dev.sync()
     assert_bit_exact(yb.numpy(), orc.mat_vec_mul_q4_0(w, x, rows, cols, threads=THREADS), "q4_0 after the limit")
     assert_bit_exact(ob.numpy(), orc.rms_norm(xn, None, 1e-6), "rms_norm after the limit")
+
+
+# ------------------------------------------------------------ odd block counts
+@pytest.mark.parametrize("rows,cols", [(1, 32), (3, 96), (5, 224), (7, 2336), (9, 32 * 73), (37, 9248)])
+def test_odd_block_counts(backend, dev, orc, synth, rows, cols):
+    """Matrices whose rows*cols/32 is odd (the reference accepts any cols % 32
+    == 0, virtual_gpu.rs:2897-3125): plain, pre-quantised, GeGLU and stacked
+    q|k|v products and the Q8_0 matvec, bit-exact against the oracle."""
+    rng = synth.rng_for(4200 + rows + cols)
+    w = synth.q4_0_matrix(rng, rows, cols)
+    w2 = synth.q4_0_matrix(rng, rows, cols)
+    x = synth.normal_vector(rng, cols)
+    xq = orc.quantize_q8_0(x)
+    ref = orc.mat_vec_mul_q4_0_q8_0(w, xq, rows, cols, threads=THREADS)
+    ref2 = orc.mat_vec_mul_q4_0_q8_0(w2, xq, rows, cols, threads=THREADS)
+    wb = backend.HipBuffer.from_gguf(dev, w, backend.Q4_0, rows, cols)
+    wb2 = backend.HipBuffer.from_gguf(dev, w2, backend.Q4_0, rows, cols)
+    xb = upload(backend, dev, x)
+    pk = backend.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(cols), np.uint8)
+    dev.quantize_q8_0(xb, None, pk, cols)
+    yb = backend.HipBuffer.alloc(dev, rows)
+    dev.gemv_q4_0(wb, xb, yb, rows, cols)
+    dev.sync()
+    assert_bit_exact(yb.numpy(), ref, f"odd q4_0 {rows}x{cols}")
+    dev.zero(yb)
+    dev.gemv_q4_0_q8(wb, pk, yb, rows, cols)
+    dev.sync()
+    assert_bit_exact(yb.numpy(), ref, f"odd q4_0 from pack {rows}x{cols}")
+    act = backend.HipBuffer.alloc(dev, rows)
+    dev.gemv_q4_0_geglu(wb, wb2, xb, act, rows, cols)
+    dev.sync()
+    assert_bit_exact(act.numpy(), orc.geglu(ref, ref2), f"odd geglu {rows}x{cols}")
+    dev.zero(act)
+    dev.gemv_q4_0_geglu_q8(wb, wb2, pk, act, rows, cols)
+    dev.sync()
+    assert_bit_exact(act.numpy(), orc.geglu(ref, ref2), f"odd geglu from pack {rows}x{cols}")
+    qkv = backend.HipBuffer.alloc(dev, 3 * rows)
+    dev.gemv_q4_0_qkv(wb, wb2, wb, xb, qkv, rows, rows, cols)
+    dev.sync()
+    assert_bit_exact(qkv.numpy(), np.concatenate([ref, ref2, ref]), f"odd qkv {rows}x{cols}")
+    w8 = synth.q8_0_matrix(rng, rows, cols)
+    w8b = backend.HipBuffer.from_gguf(dev, w8, backend.Q8_0, rows, cols)
+    dev.gemv_q8_0(w8b, xb, yb, rows, cols)
+    dev.sync()
+    assert_bit_exact(yb.numpy(), orc.mat_vec_mul_q8_0_q8_0(w8, xq, rows, cols, isa=0, threads=THREADS),
+                     f"odd q8_0 {rows}x{cols}")
