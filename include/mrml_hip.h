@@ -279,6 +279,44 @@ size_t mrml_hip_gemm_q4_0_noalloc_max_pack_bytes(void);
  * never wins.  d_out: one int32 on the device. */
 int mrml_hip_argmax_f32(mrml_hip_ctx *ctx, const float *d_x, int32_t n, int32_t *d_out);
 
+/* Vocabulary scoring of step_generation.  Candidates: ids with
+ * d_valid[id] != 0 (d_valid nullable: all), minus 1, 2, 105 and 106 while
+ * generated_count < 4 (model.rs:2845-2850).  Scores:
+ *   MRML_HIP_SCORE_CPU (the CPU path, model.rs:2851-2856): d_logits are raw
+ *     dot products; score = 30*tanh(logit/30) (the host libm's tanhf, bit
+ *     for bit), minus 3.5 once when id is among the recent ids;
+ *   MRML_HIP_SCORE_DEVICE (the device path, kernels.rs:1110-1123): d_logits
+ *     come softcapped from the Q8 GEMV; score = logit minus 1.8 per
+ *     occurrence of id among the recent ids.
+ * NaN scores are no candidates.  Ranking: score descending, equal scores by
+ * ascending id (kernels.rs:1144-1145; the host sorts of the reference leave
+ * that order open).  d_recent: n_recent (0..32) ids on the device. */
+enum { MRML_HIP_SCORE_CPU = 0, MRML_HIP_SCORE_DEVICE = 1 };
+
+/* CudaDevice::vocab_topk (cuda.rs:3052-3111; kernels.rs:1085-1228): device
+ * scoring; partition p covers ids [vocab*p/partitions,
+ * vocab*(p+1)/partitions) and gets its k best (score, id) at
+ * d_scores/d_ids[p*k ..], (-inf, -1) past its candidates.  k 1..64; any
+ * partition size (the reference's generic kernel) up to 2048*16384/k ids. */
+int mrml_hip_vocab_topk(mrml_hip_ctx *ctx, const float *d_logits, const uint8_t *d_valid, const int32_t *d_recent,
+                        float *d_scores, int32_t *d_ids, int32_t vocab, int32_t n_recent, int32_t generated_count,
+                        int32_t k, int32_t partitions);
+
+/* The whole next-token pick of step_generation (model.rs:2842-2907) on the
+ * device: the k best candidates over the vocabulary, then temperature <= 0:
+ * the best; else p_i = expf((s_i - s_0) / max(temperature, 0.1)) summed in
+ * rank order and the first i with rng <= (acc += p_i / sum), rng =
+ * (f32)((pos * 6364136223846793005 + 1) >> 33) / (f32)UINT32_MAX with pos the
+ * reference's state.pos (the position after the token whose logits these
+ * are); no candidate: token 506.  d_token (one int32), d_scores / d_ids (k
+ * entries, -inf / -1 past the candidates) are nullable.  k 1..64 (the
+ * reference draws from 40), vocab up to 2048*16384/k.  Bit-identical to the
+ * reference CPU path's choice given its scores. */
+int mrml_hip_vocab_select(mrml_hip_ctx *ctx, const float *d_logits, int32_t vocab, const uint8_t *d_valid,
+                          const int32_t *d_recent, int32_t n_recent, int32_t generated_count, int32_t scoring,
+                          float temperature, uint64_t pos, int32_t k, int32_t *d_token, float *d_scores,
+                          int32_t *d_ids);
+
 /* ---- the rest of the token step ---------------------------------------------
  * Every op keeps the CPU path's operation order: sums the reference evaluates
  * sequentially in f32 (RMSNorm's sum of squares, the attention dots, softmax
@@ -385,10 +423,11 @@ int mrml_hip_gemma2_create(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config *cfg,
                            mrml_hip_gemma2 **out);
 int mrml_hip_gemma2_destroy(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model);
 /* Enqueue one token step.  d_state = {token, pos} (two int32 on the device)
- * is read when the step executes; its last kernel records the greedy argmax
- * (lowest index on ties) in d_argmax (nullable) and in d_hist[pos] (nullable,
- * pos < hist_cap), then advances the state: pos += 1 and token =
- * d_prompt[pos] while pos < prompt_len (prefill), else the argmax.  Caches
+ * is read when the step executes; its last kernel records the pick (the
+ * greedy argmax with lowest index on ties, or the sampler's choice, see
+ * mrml_hip_gemma2_set_sampler) in d_argmax (nullable) and in d_hist[pos]
+ * (nullable, pos < hist_cap), then advances the state: pos += 1 and token =
+ * d_prompt[pos] while pos < prompt_len (prefill), else the pick.  Caches
  * are [n_layers][ctx_len][n_kv_heads][head_dim] f16.  d_logits (nullable)
  * receives the vocab logits.  A graph captured around one call replays for
  * every token. */
@@ -407,6 +446,22 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, int32_t *d_s
 int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, const int32_t *d_tokens, int32_t n_tokens,
                             int32_t pos0, uint16_t *d_k_cache, uint16_t *d_v_cache, float *d_logits,
                             int32_t *d_argmax);
+/* The pick of mrml_hip_gemma2_step and _prefill (step_generation,
+ * model.rs:2713-2907): with a sampler, the CPU path's scoring
+ * (MRML_HIP_SCORE_CPU of mrml_hip_vocab_select: masks, 30*tanh softcap,
+ * -3.5 for the tokens of the last 32 positions) and its draw at the
+ * sampler's temperature over the top_k best (greedy when temperature <= 0),
+ * the generated count being pos - (prompt_len - 1) in a step and 0 after a
+ * prefill; without one (NULL, the default), the plain argmax.  The model
+ * keeps the tokens of the last 32 positions it processed (steps and
+ * prefills both record them).  Applies to calls enqueued, or graphs
+ * captured, after this call. */
+typedef struct mrml_hip_sampler {
+    const uint8_t *d_valid; /* nullable: every id valid; else vocab bytes on the device */
+    float          temperature;
+    int32_t        top_k;   /* 1..64 (the reference: 40) */
+} mrml_hip_sampler;
+int mrml_hip_gemma2_set_sampler(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, const mrml_hip_sampler *sampler);
 /* The model's own residual stream h (f32[dim]) and logits (f32[vocab]). */
 int mrml_hip_gemma2_activations(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, float **d_h, float **d_logits);
 

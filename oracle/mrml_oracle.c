@@ -538,6 +538,69 @@ int64_t orc_argmax_f32(const float *x, size_t n)
     return (int64_t)best;
 }
 
+/* model.rs:2842-2907 (CPU path of step_generation) */
+typedef struct { float s; int32_t id; } orc_cand;
+
+static int orc_cand_before(const orc_cand *a, const orc_cand *b)
+{
+    return a->s > b->s || (a->s == b->s && a->id < b->id);
+}
+
+int32_t orc_vocab_select(const float *logits, size_t vocab, const uint8_t *valid, const int32_t *recent,
+                         size_t n_recent, size_t generated_count, int scoring, float temperature, uint64_t pos,
+                         size_t k, float *out_scores, int32_t *out_ids, size_t *n_out)
+{
+    /* the k best candidates, kept sorted (insertion: k is small) */
+    orc_cand *best = malloc((k ? k : 1) * sizeof *best);
+    size_t nb = 0;
+    for (size_t id = 0; id < vocab; id++) {
+        if (valid && !valid[id]) continue;
+        if (generated_count < 4 && (id == 1 || id == 2 || id == 105 || id == 106)) continue;
+        float s = logits[id];
+        if (scoring == 0) { /* CPU path: softcap, 3.5 once (model.rs:2852-2856) */
+            s = 30.0f * tanhf(s / 30.0f);
+            for (size_t r = 0; r < n_recent; r++)
+                if (recent[r] == (int32_t)id) { s -= 3.5f; break; }
+        } else { /* device path: 1.8 per occurrence (kernels.rs:1114-1121) */
+            for (size_t r = 0; r < n_recent; r++)
+                if (recent[r] == (int32_t)id) s -= 1.8f;
+        }
+        if (isnan(s)) continue;
+        orc_cand c = {s, (int32_t)id};
+        if (nb == k && (k == 0 || !orc_cand_before(&c, &best[k - 1]))) continue;
+        size_t at = nb < k ? nb++ : k - 1;
+        while (at > 0 && orc_cand_before(&c, &best[at - 1])) { best[at] = best[at - 1]; at--; }
+        best[at] = c;
+    }
+    for (size_t i = 0; i < nb; i++) {
+        if (out_scores) out_scores[i] = best[i].s;
+        if (out_ids) out_ids[i] = best[i].id;
+    }
+    if (n_out) *n_out = nb;
+    int32_t token = nb ? best[0].id : 506;
+    if (nb && temperature > 0.0f) {
+        const float max_logit = best[0].s;
+        const float temp = temperature > 0.1f ? temperature : 0.1f;
+        float *probs = malloc(nb * sizeof *probs);
+        float sum_exp = 0.0f;
+        for (size_t i = 0; i < nb; i++) {
+            probs[i] = expf((best[i].s - max_logit) / temp);
+            sum_exp += probs[i];
+        }
+        if (sum_exp > 0.0f) {
+            const float rng = (float)((pos * 6364136223846793005ull + 1ull) >> 33) / (float)UINT32_MAX;
+            float acc = 0.0f;
+            for (size_t i = 0; i < nb; i++) {
+                acc += probs[i] / sum_exp;
+                if (rng <= acc) { token = best[i].id; break; }
+            }
+        }
+        free(probs);
+    }
+    free(best);
+    return token;
+}
+
 /* ops.rs:24-49 */
 void orc_rms_norm(const float *x, const float *w, float eps, float *out, size_t dim)
 {

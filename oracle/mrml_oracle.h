@@ -95,6 +95,29 @@ void orc_mat_vec_mul_q4_k_q8_0(const uint8_t *w, const uint8_t *x_q8, float *y,
 /* Index of the maximum; NaN never wins; ties go to the lowest index. */
 int64_t orc_argmax_f32(const float *x, size_t n);
 
+/* Vocabulary scoring and the next-token pick of step_generation
+ * (model.rs:2842-2907):
+ *   candidates: tokens with valid[id] != 0 (valid nullable: all), minus ids
+ *     1, 2, 105, 106 while generated_count < 4;
+ *   scoring 0 (CPU path, model.rs:2852-2856): logits are raw dot products;
+ *     score = 30 * tanhf(logit / 30), then -3.5 when id is one of the
+ *     n_recent ids of recent (once, however often it occurs);
+ *   scoring 1 (device path, kernels.rs:1110-1123 after the softcapping Q8
+ *     GEMV): score = logit, -1.8 for each occurrence of id in recent;
+ *   NaN scores are not candidates;
+ *   the k best by score, descending; equal scores by ascending id (the
+ *     reference's unstable sorts leave that order open; this is the GPU
+ *     kernels' rule, kernels.rs:1144-1145);
+ *   temperature <= 0: the first; else p_i = expf((s_i - s_0) / max(t, 0.1))
+ *     summed in order, rng = (f32)((pos * 6364136223846793005 + 1) >> 33) /
+ *     (f32)UINT32_MAX, and the first i with rng <= (acc += p_i / sum);
+ *   no candidate: token 506 (the reference's fallback).
+ * Writes the n_out = min(k, #candidates) best (score, id) to out_scores /
+ * out_ids (each nullable) and returns the token. */
+int32_t orc_vocab_select(const float *logits, size_t vocab, const uint8_t *valid, const int32_t *recent,
+                         size_t n_recent, size_t generated_count, int scoring, float temperature, uint64_t pos,
+                         size_t k, float *out_scores, int32_t *out_ids, size_t *n_out);
+
 /* ---- elementwise / normalisation (ops.rs) ------------------------------ */
 void  orc_rms_norm(const float *x, const float *w, float eps, float *out, size_t dim); /* ops.rs:24-49 */
 void  orc_rope_1d(float *v, size_t pos, size_t head_dim, float base, float scale);   /* ops.rs:82-97 */

@@ -55,6 +55,8 @@ _SIG = {
     "orc_vec_dot_q4_k_q8_0": ([_P, _P, _Z], _F),
     "orc_mat_vec_mul_q4_k_q8_0": ([_P, _P, _P, _Z, _Z, _I], None),
     "orc_argmax_f32": ([_P, _Z], ctypes.c_int64),
+    "orc_vocab_select": ([_P, _Z, _P, _P, _Z, _Z, _I, _F, ctypes.c_uint64, _Z, _P, _P, ctypes.POINTER(_Z)],
+                         ctypes.c_int32),
     "orc_rms_norm": ([_P, _P, _F, _P, _Z], None),
     "orc_rope_1d": ([_P, _Z, _Z, _F, _F], None),
     "orc_rope_1d_batched": ([_P, _Z, _Z, _Z, _F, _F], None),
@@ -198,6 +200,22 @@ def q4_k_scale_min(scales12: np.ndarray, j: int) -> tuple[int, int]:
     lib().orc_q4_k_scale_min(_p(np.ascontiguousarray(scales12, dtype=np.uint8)), j, ctypes.byref(sc),
                              ctypes.byref(m))
     return int(sc.value), int(m.value)
+
+
+def vocab_select(logits, valid=None, recent=(), generated_count=0, scoring=0, temperature=0.0, pos=0, k=40):
+    """model.rs:2842-2907: (token, top-k scores, top-k ids) of step_generation's
+    next-token pick over `logits` (orc_vocab_select); scoring 0 is the CPU
+    path (softcap, -3.5 once), 1 the device path (-1.8 per occurrence)."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    va = None if valid is None else np.ascontiguousarray(valid, dtype=np.uint8)
+    rc = np.ascontiguousarray(np.asarray(recent, dtype=np.int32).reshape(-1))
+    sc = np.zeros(max(k, 1), np.float32)
+    ids = np.zeros(max(k, 1), np.int32)
+    n = ctypes.c_size_t(0)
+    tok = lib().orc_vocab_select(_p(lg), lg.size, None if va is None else _p(va), _p(rc) if rc.size else None,
+                                 rc.size, generated_count, int(scoring), temperature, pos, k, _p(sc), _p(ids),
+                                 ctypes.byref(n))
+    return int(tok), sc[:n.value].copy(), ids[:n.value].copy()
 
 
 def argmax_f32(x: np.ndarray) -> int:

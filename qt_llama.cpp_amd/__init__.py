@@ -101,6 +101,15 @@ class Gemma2Layer(ctypes.Structure):
 
     _fields_ = [(n, ctypes.c_void_p) for n in GEMMA2_LAYER_TENSORS + GEMMA2_LAYER_NORMS]
 
+SCORE_CPU, SCORE_DEVICE = 0, 1
+
+
+class Sampler(ctypes.Structure):
+    """mrml_hip_sampler: the pick of the token step (model.rs:2842-2907)."""
+
+    _fields_ = [("d_valid", ctypes.c_void_p), ("temperature", ctypes.c_float), ("top_k", ctypes.c_int32)]
+
+
 # name -> argtypes; every function returns int status unless listed in _RESTYPE
 _SIGNATURES = {
     "mrml_hip_device_count": [ctypes.POINTER(ctypes.c_int32)],
@@ -155,6 +164,9 @@ _SIGNATURES = {
     "mrml_hip_quantize_q8_0_gemm": [_P, _P, _P, _I, _I],
     "mrml_hip_gemm_q4_0_gpack": [_P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_argmax_f32": [_P, _P, _I, _P],
+    "mrml_hip_vocab_topk": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I],
+    "mrml_hip_vocab_select": [_P, _P, _I, _P, _P, _I, _I, _I, _F, ctypes.c_uint64, _I, _P, _P, _P],
+    "mrml_hip_gemma2_set_sampler": [_P, _P, _P],
     "mrml_hip_rms_norm": [_P, _P, _P, _P, _P, _I, _F],
     "mrml_hip_residual_rms_norm": [_P, _P, _P, _P, _P, _P, _P, _I, _F],
     "mrml_hip_embedding": [_P, _P, _I, _I, _P, _P, _I, _I, _F],
@@ -463,6 +475,21 @@ class HipDevice:
     def argmax_f32(self, x, n: int, out) -> None:
         self._check(self.lib.mrml_hip_argmax_f32(self.ctx, _ptr(x), n, _ptr(out)))
 
+    def vocab_topk(self, logits, valid, recent, scores, ids, vocab_size: int, n_recent: int, generated_count: int,
+                   k: int, partitions: int) -> None:
+        """CudaDevice::vocab_topk (cuda.rs:3052-3111): each partition's k best (score, id)."""
+        self._check(self.lib.mrml_hip_vocab_topk(self.ctx, _ptr(logits), _ptr(valid), _ptr(recent), _ptr(scores),
+                                                 _ptr(ids), vocab_size, n_recent, generated_count, k, partitions))
+
+    def vocab_select(self, logits, vocab: int, valid=None, recent=None, n_recent: int = 0, generated_count: int = 0,
+                     scoring: int = 0, temperature: float = 0.0, pos: int = 0, k: int = 40, token=None,
+                     scores=None, ids=None) -> None:
+        """step_generation's next-token pick (model.rs:2842-2907) on the device; scoring
+        SCORE_CPU (softcap, -3.5 once) or SCORE_DEVICE (-1.8 per occurrence)."""
+        self._check(self.lib.mrml_hip_vocab_select(self.ctx, _ptr(logits), vocab, _ptr(valid), _ptr(recent),
+                                                   n_recent, generated_count, scoring, temperature, pos, k,
+                                                   _ptr(token), _ptr(scores), _ptr(ids)))
+
     # ---- the rest of the token step ----------------------------------------------
     def rms_norm(self, x, w, out, dim: int, eps: float, pack=None) -> None:
         """CudaDevice::rms_norm (cuda.rs:2102-2180); `pack` also takes the Q8_0 pack."""
@@ -574,6 +601,15 @@ class Gemma2Model:
         self.dev._check(self.dev.lib.mrml_hip_gemma2_prefill(self.dev.ctx, self.handle, _ptr(tokens), n_tokens, pos0,
                                                              _ptr(k_cache), _ptr(v_cache), _ptr(logits),
                                                              _ptr(argmax)))
+
+    def set_sampler(self, temperature: float = 0.0, top_k: int = 40, valid=None) -> None:
+        """Pick with the CPU path's scoring and draw (mrml_hip_gemma2_set_sampler)."""
+        sp = Sampler(_ptr(valid), temperature, top_k)
+        self.dev._check(self.dev.lib.mrml_hip_gemma2_set_sampler(self.dev.ctx, self.handle, ctypes.byref(sp)))
+
+    def clear_sampler(self) -> None:
+        """Back to the plain argmax."""
+        self.dev._check(self.dev.lib.mrml_hip_gemma2_set_sampler(self.dev.ctx, self.handle, None))
 
     def activations(self) -> tuple[int, int]:
         h, lg = ctypes.c_void_p(), ctypes.c_void_p()

@@ -5,6 +5,7 @@
 
 #include "device.h"
 #include "internal.h"
+#include "libm_f32.h"
 
 namespace mrml {
 
@@ -224,7 +225,7 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float *__restri
                                                            int parts, int32_t *__restrict__ out,
                                                            int32_t *__restrict__ state, int32_t *__restrict__ hist,
                                                            int hist_cap, const int32_t *__restrict__ prompt,
-                                                           int prompt_len)
+                                                           int prompt_len, int2 *__restrict__ ring)
 {
     float v = __builtin_nanf("");
     int i = 0x7fffffff;
@@ -235,12 +236,286 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float *__restri
         if (out) *out = i;
         if (state) {
             const int cur = state[1];
+            if (ring && cur >= 0) ring[cur % 32] = make_int2(cur, state[0]);  // the token processed at cur
             if (hist && cur >= 0 && cur < hist_cap) hist[cur] = i;
             const int pos = cur + 1;
             state[0] = (prompt && pos < prompt_len) ? prompt[pos] : i;
             state[1] = pos;
         }
     }
+}
+
+// ---- vocabulary scoring and the next-token pick (model.rs:2842-2907) -----------
+// Candidates are ranked by a 64-bit key: the score's bits made order-
+// preserving as an unsigned number in the high word, ~id in the low word, so
+// a larger key is a larger score or, on equal scores, a lower id.  Key 0
+// marks "no candidate" (masked, NaN, or past the end).
+__device__ __forceinline__ uint64_t cand_key(float s, int id)
+{
+    const uint32_t u = __builtin_bit_cast(uint32_t, s);
+    const uint32_t o = (u >> 31) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)o << 32) | (uint32_t)~(uint32_t)id;
+}
+__device__ __forceinline__ float key_score(uint64_t k)
+{
+    const uint32_t o = (uint32_t)(k >> 32);
+    return __builtin_bit_cast(float, (o >> 31) ? (o & 0x7fffffffu) : ~o);
+}
+__device__ __forceinline__ int key_id(uint64_t k) { return (int)~(uint32_t)k; }
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, off, 64);
+        const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), off, 64);
+        const uint64_t o = ((uint64_t)hi << 32) | lo;
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// The k largest keys held by the workgroup, in descending order, to out[0..k):
+// every thread holds N keys sorted descending; each round takes the largest
+// head (wave maxima, then across waves through LDS) and its owner pops it.
+// Keys are distinct except 0, so exactly one thread owns a non-zero maximum.
+template <int N>
+__device__ __forceinline__ void block_top_keys(uint64_t (&keys)[N], int k, uint64_t *out, uint64_t *red)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (int)(blockDim.x >> 6);
+    for (int r = 0; r < k; ++r) {
+        const uint64_t m = wave_max_u64(keys[0]);
+        if (lane == 0) red[wave] = m;
+        __syncthreads();
+        uint64_t best = red[0];
+        for (int w = 1; w < nw; ++w) best = red[w] > best ? red[w] : best;
+        if (threadIdx.x == 0) out[r] = best;
+        if (best != 0 && keys[0] == best) {  // the owner pops its head
+#pragma unroll
+            for (int i = 0; i + 1 < N; ++i) keys[i] = keys[i + 1];
+            keys[N - 1] = 0;
+        }
+        __syncthreads();
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void sort_desc(uint64_t (&keys)[N])
+{
+#pragma unroll
+    for (int i = 1; i < N; ++i)
+#pragma unroll
+        for (int j = i; j > 0; --j)
+            if (keys[j] > keys[j - 1]) {
+                const uint64_t t = keys[j];
+                keys[j] = keys[j - 1];
+                keys[j - 1] = t;
+            }
+}
+
+constexpr int kVocabPerThread = 8;     // candidates per thread of a partition
+constexpr int kVocabThreads = 256;
+constexpr int kVocabPart = kVocabPerThread * kVocabThreads;  // ids per partition
+constexpr int kSelectThreads = 1024;
+constexpr int kTopKMax = 64;
+constexpr int kRecentMax = 32;
+
+// Where the scores of one vocabulary pick come from.  recent: the n_recent
+// (<= 32) ids of a caller's list, or, with ring, the tokens of positions
+// cur-31 .. cur from the ring of {position, token} entries (slot q % 32),
+// cur being state[1] (the token state[0] is taken from the state itself)
+// or host_cur.  With state, the generated count is cur - (prompt_len - 1).
+struct VocabScoring {
+    const float *logits;
+    const uint8_t *valid;
+    const int32_t *recent;
+    const int2 *ring;
+    const int32_t *state;
+    long long host_cur;
+    int vocab, n_recent, generated_count, prompt_len, scoring;
+};
+
+__device__ __forceinline__ int gather_recent(const VocabScoring &v, int32_t *dst)
+{
+    if (!v.ring) {
+        for (int r = 0; r < v.n_recent; ++r) dst[r] = v.recent[r];
+        return v.n_recent;
+    }
+    const long long cur = v.state ? (long long)v.state[1] : v.host_cur;
+    int n = 0, d = 0;
+    if (v.state) {
+        dst[n++] = v.state[0];
+        d = 1;
+    }
+    for (; d < kRecentMax; ++d) {
+        const long long q = cur - d;
+        if (q < 0) break;
+        const int2 e = v.ring[q % kRecentMax];
+        if (e.x == (int)q) dst[n++] = e.y;
+    }
+    return n;
+}
+
+// Block b scores chunk b % chunks (up to 2048 ids) of partition b / chunks,
+// whose ids are [vocab*p/parts, vocab*(p+1)/parts) as in the reference's
+// launch (kernels.rs:1100-1103), and writes its k best keys to keys_out[b*k..];
+// with out_scores (chunks == 1), also the partition's (score, id) list, past
+// the candidates (-inf, -1) (kernels.rs:1160-1167).
+__global__ __launch_bounds__(kVocabThreads) void vocab_topk_partial_kernel(VocabScoring v, int parts, int chunks,
+                                                                           int k, uint64_t *__restrict__ keys_out,
+                                                                           float *__restrict__ out_scores,
+                                                                           int32_t *__restrict__ out_ids)
+{
+    __shared__ int32_t rec[kRecentMax];
+    __shared__ int n_rec;
+    __shared__ uint64_t red[kVocabThreads / 64];
+    __shared__ uint64_t top[kTopKMax];
+    int gen = v.generated_count;
+    if (v.state) {
+        const long long cur = v.state[1];
+        const long long first = v.prompt_len > 0 ? v.prompt_len - 1 : 0;
+        gen = cur > first ? (int)(cur - first) : 0;
+    }
+    if (threadIdx.x == 0) n_rec = gather_recent(v, rec);
+    __syncthreads();
+    const int nr = n_rec;
+    const int p = (int)blockIdx.x / chunks, c = (int)blockIdx.x % chunks;
+    const int pa = (int)((long long)v.vocab * p / parts), pe = (int)((long long)v.vocab * (p + 1) / parts);
+    const int start = pa + c * kVocabPart, end = min(start + kVocabPart, pe);
+    uint64_t keys[kVocabPerThread];
+#pragma unroll
+    for (int i = 0; i < kVocabPerThread; ++i) {
+        const int id = start + i * kVocabThreads + (int)threadIdx.x;
+        uint64_t key = 0;
+        if (id < end && (!v.valid || v.valid[id]) && !(gen < 4 && (id == 1 || id == 2 || id == 105 || id == 106))) {
+            float sc = v.logits[id];
+            if (v.scoring == 0) {  // CPU path: softcap here, 3.5 once
+                sc = 30.0f * mrml_libm::tanhf(sc / 30.0f);
+                for (int r = 0; r < nr; ++r)
+                    if (rec[r] == id) {
+                        sc -= 3.5f;
+                        break;
+                    }
+            } else {  // device path: softcapped logits, 1.8 per occurrence
+                for (int r = 0; r < nr; ++r)
+                    if (rec[r] == id) sc -= 1.8f;
+            }
+            if (sc == sc) key = cand_key(sc, id);
+        }
+        keys[i] = key;
+    }
+    sort_desc(keys);
+    block_top_keys(keys, k, top, red);
+    for (int r = threadIdx.x; r < k; r += blockDim.x) {
+        const uint64_t key = top[r];
+        keys_out[(size_t)blockIdx.x * k + r] = key;
+        if (out_scores) {
+            out_scores[(size_t)p * k + r] = key ? key_score(key) : -INFINITY;
+            out_ids[(size_t)p * k + r] = key ? key_id(key) : -1;
+        }
+    }
+}
+
+// Partition blockIdx.x's k best from its chunks' keys (partitions of more
+// than 2048 ids: the reference's serial kernel, kernels.rs:1170-1228).
+__global__ __launch_bounds__(kSelectThreads) void vocab_topk_merge_kernel(const uint64_t *__restrict__ keys_in,
+                                                                         int chunks, int k,
+                                                                         float *__restrict__ out_scores,
+                                                                         int32_t *__restrict__ out_ids)
+{
+    __shared__ uint64_t top[kTopKMax];
+    __shared__ uint64_t red[kSelectThreads / 64];
+    constexpr int N = 16;
+    const int total = chunks * k;
+    const uint64_t *src = keys_in + (size_t)blockIdx.x * total;
+    uint64_t keys[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const int c = i * kSelectThreads + (int)threadIdx.x;
+        keys[i] = c < total ? src[c] : 0;
+    }
+    sort_desc(keys);
+    block_top_keys(keys, k, top, red);
+    for (int r = threadIdx.x; r < k; r += blockDim.x) {
+        const uint64_t key = top[r];
+        out_scores[(size_t)blockIdx.x * k + r] = key ? key_score(key) : -INFINITY;
+        out_ids[(size_t)blockIdx.x * k + r] = key ? key_id(key) : -1;
+    }
+}
+
+// Merges the partitions' keys into the k best (descending) and picks the
+// token: temperature <= 0 -> the first; else the softmax draw of the CPU path
+// with its LCG.  Writes out_token (nullable), out_scores / out_ids (nullable,
+// k entries, -inf / -1 past the candidates) and, with state, advances the
+// decode loop as argmax_final_kernel does and records {pos, token} in ring.
+__global__ __launch_bounds__(kSelectThreads) void vocab_select_kernel(
+    const uint64_t *__restrict__ part, int n_part, int k, float temperature, unsigned long long pos_arg,
+    int expf_fused, int32_t *__restrict__ out_token, float *__restrict__ out_scores, int32_t *__restrict__ out_ids,
+    int32_t *__restrict__ state, int2 *__restrict__ ring, int32_t *__restrict__ hist, int hist_cap,
+    const int32_t *__restrict__ prompt, int prompt_len)
+{
+    __shared__ uint64_t top[kTopKMax];
+    __shared__ uint64_t red[kSelectThreads / 64];
+    constexpr int N = 16;  // keys per thread: up to 16384 partition keys
+    const int total = n_part * k;
+    uint64_t keys[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const int c = i * kSelectThreads + (int)threadIdx.x;
+        keys[i] = c < total ? part[c] : 0;
+    }
+    sort_desc(keys);
+    block_top_keys(keys, k, top, red);
+    if (threadIdx.x != 0) return;
+    int n = 0;
+    while (n < k && top[n] != 0) ++n;
+    if (out_scores || out_ids)
+        for (int i = 0; i < k; ++i) {
+            if (out_scores) out_scores[i] = i < n ? key_score(top[i]) : -INFINITY;
+            if (out_ids) out_ids[i] = i < n ? key_id(top[i]) : -1;
+        }
+    // the CPU path's state.pos: the position after the token just processed
+    const unsigned long long pos = state ? (unsigned long long)state[1] + 1ull : pos_arg;
+    int token = n ? key_id(top[0]) : 506;
+    if (n && temperature > 0.0f) {
+        const float max_logit = key_score(top[0]);
+        const float temp = temperature > 0.1f ? temperature : 0.1f;
+        const bool fused = expf_fused != 0;
+        float probs[kTopKMax];
+        float sum_exp = 0.0f;
+        for (int i = 0; i < n; ++i) {
+            probs[i] = mrml_libm::expf((key_score(top[i]) - max_logit) / temp, fused);
+            sum_exp += probs[i];
+        }
+        if (sum_exp > 0.0f) {
+            const float rng = (float)((pos * 6364136223846793005ull + 1ull) >> 33) / (float)0xffffffffu;
+            float acc = 0.0f;
+            for (int i = 0; i < n; ++i) {
+                acc += probs[i] / sum_exp;
+                if (rng <= acc) {
+                    token = key_id(top[i]);
+                    break;
+                }
+            }
+        }
+    }
+    if (out_token) *out_token = token;
+    if (state) {
+        const int cur = state[1];
+        if (ring && cur >= 0) ring[cur % kRecentMax] = make_int2(cur, state[0]);  // the token processed at cur
+        if (hist && cur >= 0 && cur < hist_cap) hist[cur] = token;
+        const int next = cur + 1;
+        state[0] = (prompt && next < prompt_len) ? prompt[next] : token;
+        state[1] = next;
+    }
+}
+
+// The ring entries of positions pos0 .. pos0+n-1 (the last 32 of them) for
+// tokens[0..n): the recent-token history of a batched prefill.
+__global__ void recent_ring_write_kernel(int2 *__restrict__ ring, const int32_t *__restrict__ tokens, int n, int pos0)
+{
+    const int i = n - 1 - (int)threadIdx.x;
+    if (threadIdx.x < kRecentMax && i >= 0) ring[(pos0 + i) % kRecentMax] = make_int2(pos0 + i, tokens[i]);
 }
 
 inline int waves_for(int rows) { return rows >= 8192 ? 4 : (rows >= 2048 ? 2 : 1); }
@@ -320,6 +595,97 @@ int launch_gemv_q4_k(mrml_hip_ctx *ctx, const void *w, const void *xpack, float 
     return check_launch(ctx, "gemv_q4_k_kernel");
 }
 
+int vocab_parts(int32_t vocab) { return (vocab + kVocabPart - 1) / kVocabPart; }
+
+size_t vocab_select_scratch_bytes(int32_t vocab, int32_t k) { return (size_t)vocab_parts(vocab) * k * 8; }
+
+bool vocab_select_ok(int32_t vocab, int32_t k)
+{
+    return vocab > 0 && k >= 1 && k <= kTopKMax && (long long)vocab_parts(vocab) * k <= 16 * kSelectThreads;
+}
+
+int vocab_topk_chunks(int32_t vocab, int32_t parts)
+{
+    const long long most = ((long long)vocab + parts - 1) / parts;  // the largest partition's ids
+    return (int)((most + kVocabPart - 1) / kVocabPart);
+}
+
+bool vocab_topk_ok(int32_t vocab, int32_t k, int32_t parts)
+{
+    return vocab > 0 && parts >= 1 && parts <= vocab && k >= 1 && k <= kTopKMax &&
+           (long long)vocab_topk_chunks(vocab, parts) * k <= 16 * kSelectThreads;
+}
+
+size_t vocab_topk_scratch_bytes(int32_t vocab, int32_t k, int32_t parts)
+{
+    return (size_t)parts * vocab_topk_chunks(vocab, parts) * k * 8;
+}
+
+namespace {
+VocabScoring scoring_of(const float *logits, int32_t vocab, const uint8_t *valid, const int32_t *recent,
+                        int32_t n_recent, int32_t generated_count, int32_t scoring, const int32_t *state,
+                        const void *ring, long long host_cur, int prompt_len)
+{
+    VocabScoring v;
+    v.logits = logits;
+    v.valid = valid;
+    v.recent = recent;
+    v.ring = (const int2 *)ring;
+    v.state = state;
+    v.host_cur = host_cur;
+    v.vocab = vocab;
+    v.n_recent = n_recent;
+    v.generated_count = generated_count;
+    v.prompt_len = prompt_len;
+    v.scoring = scoring;
+    return v;
+}
+}  // namespace
+
+size_t recent_ring_bytes() { return kRecentMax * sizeof(int2); }
+
+int launch_recent_ring_write(mrml_hip_ctx *ctx, void *ring, const int32_t *tokens, int n, int pos0)
+{
+    hipLaunchKernelGGL(recent_ring_write_kernel, dim3(1), dim3(kRecentMax), 0, ctx->stream, (int2 *)ring, tokens, n,
+                       pos0);
+    return check_launch(ctx, "recent_ring_write_kernel");
+}
+
+int launch_vocab_topk(mrml_hip_ctx *ctx, const float *logits, const uint8_t *valid, const int32_t *recent,
+                      float *out_scores, int32_t *out_ids, int32_t vocab, int32_t n_recent, int32_t generated_count,
+                      int32_t k, int32_t parts, void *scratch)
+{
+    const int chunks = vocab_topk_chunks(vocab, parts);
+    const VocabScoring v = scoring_of(logits, vocab, valid, recent, n_recent, generated_count, 1, nullptr, nullptr, 0, 0);
+    uint64_t *keys = reinterpret_cast<uint64_t *>(scratch);
+    hipLaunchKernelGGL(vocab_topk_partial_kernel, dim3(parts * chunks), dim3(kVocabThreads), 0, ctx->stream, v, parts,
+                       chunks, k, keys, chunks == 1 ? out_scores : nullptr, chunks == 1 ? out_ids : nullptr);
+    if (int rc = check_launch(ctx, "vocab_topk_partial_kernel")) return rc;
+    if (chunks == 1) return MRML_HIP_OK;
+    hipLaunchKernelGGL(vocab_topk_merge_kernel, dim3(parts), dim3(kSelectThreads), 0, ctx->stream,
+                       (const uint64_t *)keys, chunks, k, out_scores, out_ids);
+    return check_launch(ctx, "vocab_topk_merge_kernel");
+}
+
+int launch_vocab_select(mrml_hip_ctx *ctx, const float *logits, int32_t vocab, const uint8_t *valid,
+                        const int32_t *recent, int32_t n_recent, int32_t generated_count, int32_t scoring,
+                        float temperature, uint64_t pos, int32_t k, int32_t *out_token, float *out_scores,
+                        int32_t *out_ids, void *scratch, int32_t *state, void *ring, long long host_cur, int32_t *hist,
+                        int hist_cap, const int32_t *prompt, int prompt_len)
+{
+    const int parts = vocab_parts(vocab);
+    const VocabScoring v = scoring_of(logits, vocab, valid, recent, n_recent, generated_count, scoring, state, ring,
+                                      host_cur, prompt_len);
+    uint64_t *keys = reinterpret_cast<uint64_t *>(scratch);
+    hipLaunchKernelGGL(vocab_topk_partial_kernel, dim3(parts), dim3(kVocabThreads), 0, ctx->stream, v, parts, 1, k,
+                       keys, nullptr, nullptr);
+    if (int rc = check_launch(ctx, "vocab_topk_partial_kernel")) return rc;
+    hipLaunchKernelGGL(vocab_select_kernel, dim3(1), dim3(kSelectThreads), 0, ctx->stream, (const uint64_t *)keys,
+                       parts, k, temperature, (unsigned long long)pos, (int)host_expf_fused(), out_token, out_scores,
+                       out_ids, state, (int2 *)ring, hist, hist_cap, prompt, prompt_len);
+    return check_launch(ctx, "vocab_select_kernel");
+}
+
 int argmax_parts(int32_t n)
 {
     const int parts = (n + 2047) / 2048;
@@ -327,7 +693,7 @@ int argmax_parts(int32_t n)
 }
 
 int launch_argmax_step(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *out, void *scratch, int32_t *state,
-                       int32_t *hist, int hist_cap, const int32_t *prompt, int prompt_len)
+                       int32_t *hist, int hist_cap, const int32_t *prompt, int prompt_len, void *ring)
 {
     const int parts = argmax_parts(n);
     float *pv = reinterpret_cast<float *>(scratch);
@@ -336,7 +702,7 @@ int launch_argmax_step(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *ou
     int rc = check_launch(ctx, "argmax_partial_kernel");
     if (rc) return rc;
     hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, ctx->stream, pv, pi, parts, out, state, hist,
-                       hist_cap, prompt, prompt_len);
+                       hist_cap, prompt, prompt_len, (int2 *)ring);
     return check_launch(ctx, "argmax_final_kernel");
 }
 
@@ -344,7 +710,7 @@ int launch_argmax_f32(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *out
 {
     void *ws = workspace(ctx, (size_t)argmax_parts(n) * 8);
     if (!ws) return MRML_HIP_E_ALLOC;
-    return launch_argmax_step(ctx, x, n, out, ws, nullptr, nullptr, 0, nullptr, 0);
+    return launch_argmax_step(ctx, x, n, out, ws, nullptr, nullptr, 0, nullptr, 0, nullptr);
 }
 
 }  // namespace mrml

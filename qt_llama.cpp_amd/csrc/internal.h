@@ -87,10 +87,48 @@ int launch_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const void *gpack, float 
                      int32_t batch, int32_t ldy = 0);
 
 // Argmax whose final pass can also advance a device-side decode loop
-// (state = {token, pos}); scratch holds argmax_parts(n) * 8 bytes.
+// (state = {token, pos}) and record the processed token in the recent-token
+// ring (nullable); scratch holds argmax_parts(n) * 8 bytes.
 int argmax_parts(int32_t n);
 int launch_argmax_step(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *out, void *scratch, int32_t *state,
-                       int32_t *hist, int hist_cap, const int32_t *prompt, int prompt_len);
+                       int32_t *hist, int hist_cap, const int32_t *prompt, int prompt_len, void *ring);
+
+// Vocabulary scoring (model.rs:2842-2907, kernels.rs:1085-1228): candidates
+// are the valid ids minus 1, 2, 105, 106 while fewer than 4 tokens were
+// generated; scoring 0 (CPU path) softcaps the raw logits with 30*tanh(x/30)
+// and subtracts 3.5 once from recent ids, scoring 1 (device path) takes
+// softcapped logits and subtracts 1.8 per occurrence; NaN scores drop out;
+// ranks are by score, equal scores by lowest id.
+//
+// launch_vocab_topk: CudaDevice::vocab_topk's output (scoring 1), each of
+// `parts` partitions' k best (score, id), (-inf, -1) past its candidates.
+// scratch: vocab_topk_scratch_bytes.
+//
+// launch_vocab_select: the pick itself over the whole vocabulary (partitions
+// of 2048 ids, then one merge): temperature <= 0 -> the best; else the
+// CPU path's softmax draw over the k best with its LCG at position pos.
+// out_token / out_scores / out_ids nullable (k entries, -inf / -1 past the
+// candidates).  scratch: vocab_select_scratch_bytes.  The recent ids come
+// from `recent`, or with ring from the ring of {position, token} (the last
+// 32 positions up to cur = state[1] or host_cur).  With state (decode loop)
+// the generated count is cur - (prompt_len - 1), pos is cur + 1, and the
+// merge advances the loop like launch_argmax_step.
+int vocab_parts(int32_t vocab);
+size_t vocab_select_scratch_bytes(int32_t vocab, int32_t k);
+bool vocab_select_ok(int32_t vocab, int32_t k);
+int vocab_topk_chunks(int32_t vocab, int32_t parts);
+bool vocab_topk_ok(int32_t vocab, int32_t k, int32_t parts);
+size_t vocab_topk_scratch_bytes(int32_t vocab, int32_t k, int32_t parts);
+size_t recent_ring_bytes();
+int launch_recent_ring_write(mrml_hip_ctx *ctx, void *ring, const int32_t *tokens, int n, int pos0);
+int launch_vocab_topk(mrml_hip_ctx *ctx, const float *logits, const uint8_t *valid, const int32_t *recent,
+                      float *out_scores, int32_t *out_ids, int32_t vocab, int32_t n_recent, int32_t generated_count,
+                      int32_t k, int32_t parts, void *scratch);
+int launch_vocab_select(mrml_hip_ctx *ctx, const float *logits, int32_t vocab, const uint8_t *valid,
+                        const int32_t *recent, int32_t n_recent, int32_t generated_count, int32_t scoring,
+                        float temperature, uint64_t pos, int32_t k, int32_t *out_token, float *out_scores,
+                        int32_t *out_ids, void *scratch, int32_t *state, void *ring, long long host_cur, int32_t *hist,
+                        int hist_cap, const int32_t *prompt, int prompt_len);
 
 // The Gemma-2 residual (h_out = h_in + rms_norm(t, w_post), then the next
 // norm with w_norm) fused ahead of the gate/up GeGLU or the q|k|v matvec

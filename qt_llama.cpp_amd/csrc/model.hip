@@ -16,7 +16,8 @@
 //   act      = gelu(Wg xn) * (Wu xn)     -> Q8_0 pack      gemv_q4_0_geglu (emit)
 //   f        = Wd * pack(act)                              gemv_q4_0 (long-row kernel)
 //   h += rms_norm(f, post_ffw); xn = rms_norm(h, next)    residual_rms_norm -> pack
-// then the tied LM head over pack(rms_norm(h, output_norm)) and argmax.
+// then the tied LM head over pack(rms_norm(h, output_norm)) and the pick:
+// argmax, or with a sampler the reference's scoring and draw.
 
 #include <algorithm>
 #include <cmath>
@@ -38,6 +39,9 @@ struct mrml_hip_gemma2 {
                            // may be reallocated under a captured graph)
     uint8_t *xpack = nullptr, *attn_pack = nullptr, *act_pack = nullptr;
     void *attn_part = nullptr, *argmax_scratch = nullptr;
+    void *recent_ring = nullptr;    // {position, token} of the last 32 positions processed
+    void *select_scratch = nullptr;  // partition keys of the sampler's pick
+    mrml_hip_sampler sampler{};      // top_k == 0: plain argmax
     float *rope_table = nullptr;  // [ctx_len][head_dim/2] (cos, sin) from the host libm
     // prefill chunk buffers, allocated on the first prefill call: per token
     // rows of h, xn, stacked q|k|v, attention output, o, gate, up,
@@ -51,6 +55,8 @@ struct mrml_hip_gemma2 {
 using namespace mrml;
 
 namespace {
+
+constexpr int kSamplerTopKMax = 64;
 
 int check_model_config(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config &c)
 {
@@ -69,6 +75,7 @@ int check_model_config(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config &c)
     REQUIRE(ctx, c.ctx_len <= attn_max_capacity(), "gemma2: ctx_len=%d above %d", c.ctx_len, attn_max_capacity());
     REQUIRE(ctx, c.numerics == MRML_HIP_NUMERICS_EXACT || c.numerics == MRML_HIP_NUMERICS_FAST,
             "gemma2: numerics=%d is neither EXACT (0) nor FAST (1)", c.numerics);
+    REQUIRE(ctx, vocab_select_ok(c.vocab, kSamplerTopKMax), "gemma2: vocab=%d above the sampler's limit", c.vocab);
     return MRML_HIP_OK;
 }
 
@@ -233,7 +240,8 @@ int mrml_hip_gemma2_create(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config *cfg,
                                         c.numerics == MRML_HIP_NUMERICS_FAST
                                             ? attn_split_scratch_bytes(c.n_heads, c.ctx_len)
                                             : (size_t)0)),
-                 o_argmax = take((size_t)argmax_parts(c.vocab) * 8),
+                 o_argmax = take((size_t)argmax_parts(c.vocab) * 8), o_ring = take(recent_ring_bytes()),
+                 o_select = take(vocab_select_scratch_bytes(c.vocab, kSamplerTopKMax)),
                  o_rope = take((size_t)c.ctx_len * c.head_dim * sizeof(float));
     hipError_t e = hipMalloc(&m->arena, off);
     if (e != hipSuccess) {
@@ -253,7 +261,15 @@ int mrml_hip_gemma2_create(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config *cfg,
     m->act_pack = base + o_actpack;
     m->attn_part = base + o_part;
     m->argmax_scratch = base + o_argmax;
+    m->recent_ring = base + o_ring;
+    m->select_scratch = base + o_select;
     m->rope_table = (float *)(base + o_rope);
+    e = hipMemset(m->recent_ring, 0xff, recent_ring_bytes());  // position -1: no entry
+    if (e != hipSuccess) {
+        (void)hipFree(m->arena);
+        delete m;
+        return fail(ctx, MRML_HIP_E_HIP, "gemma2_create: hipMemset: %s", hipGetErrorString(e));
+    }
     if (int rc = fill_rope_table(ctx, m->rope_table, c.ctx_len, c.head_dim, c.rope_base, 1.0f)) {
         (void)hipFree(m->arena);
         delete m;
@@ -347,8 +363,16 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
         STEP(launch_gemv_q4_0(ctx, m->tok_embd, m->xpack, logits, c.vocab, c.dim));
     else
         STEP(launch_gemv_q8_0(ctx, m->tok_embd, m->xpack, logits, c.vocab, c.dim, 0));
-    STEP(launch_argmax_step(ctx, logits, c.vocab, d_argmax, m->argmax_scratch, d_state, d_hist, hist_cap, d_prompt,
-                            prompt_len));
+    if (m->sampler.top_k > 0) {
+        const mrml_hip_sampler &sp = m->sampler;
+        STEP(launch_vocab_select(ctx, logits, c.vocab, sp.d_valid, nullptr, 0, 0, MRML_HIP_SCORE_CPU, sp.temperature,
+                                 0, sp.temperature > 0.0f ? sp.top_k : 1, d_argmax, nullptr, nullptr,
+                                 m->select_scratch, d_state, m->recent_ring, 0, d_hist, hist_cap, d_prompt,
+                                 prompt_len));
+    } else {
+        STEP(launch_argmax_step(ctx, logits, c.vocab, d_argmax, m->argmax_scratch, d_state, d_hist, hist_cap,
+                                d_prompt, prompt_len, m->recent_ring));
+    }
 #undef STEP
     return MRML_HIP_OK;
 }
@@ -471,9 +495,35 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
             STEP(launch_gemv_q4_0(ctx, m->tok_embd, m->xpack, logits, c.vocab, c.dim));
         else
             STEP(launch_gemv_q8_0(ctx, m->tok_embd, m->xpack, logits, c.vocab, c.dim, 0));
-        if (d_argmax) STEP(launch_argmax_f32(ctx, logits, c.vocab, d_argmax));
+        // the prompt's last 32 tokens enter the recent-token history
+        STEP(launch_recent_ring_write(ctx, m->recent_ring, d_tokens, n_tokens, pos0));
+        if (d_argmax && m->sampler.top_k > 0) {
+            // the pick after a prompt: no token generated yet, state.pos = pos0 + n_tokens
+            const mrml_hip_sampler &sp = m->sampler;
+            STEP(launch_vocab_select(ctx, logits, c.vocab, sp.d_valid, nullptr, 0, 0, MRML_HIP_SCORE_CPU,
+                                     sp.temperature, (uint64_t)pos0 + n_tokens, sp.temperature > 0.0f ? sp.top_k : 1,
+                                     d_argmax, nullptr, nullptr, m->select_scratch, nullptr, m->recent_ring,
+                                     (long long)pos0 + n_tokens - 1, nullptr, 0, nullptr, 0));
+        } else if (d_argmax) {
+            STEP(launch_argmax_f32(ctx, logits, c.vocab, d_argmax));
+        }
     }
 #undef STEP
+    return MRML_HIP_OK;
+}
+
+int mrml_hip_gemma2_set_sampler(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const mrml_hip_sampler *sampler)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, m, "gemma2_set_sampler: null model");
+    if (!sampler) {
+        m->sampler = mrml_hip_sampler{};
+        return MRML_HIP_OK;
+    }
+    REQUIRE(ctx, sampler->top_k >= 1 && sampler->top_k <= kSamplerTopKMax,
+            "gemma2_set_sampler: top_k=%d outside 1..%d", sampler->top_k, kSamplerTopKMax);
+    REQUIRE(ctx, sampler->temperature == sampler->temperature, "gemma2_set_sampler: temperature is NaN");
+    m->sampler = *sampler;
     return MRML_HIP_OK;
 }
 

@@ -654,4 +654,39 @@ int mrml_hip_argmax_f32(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *o
     return launch_argmax_f32(ctx, x, n, out);
 }
 
+int mrml_hip_vocab_topk(mrml_hip_ctx *ctx, const float *logits, const uint8_t *valid, const int32_t *recent,
+                        float *scores, int32_t *ids, int32_t vocab, int32_t n_recent, int32_t generated_count,
+                        int32_t k, int32_t partitions)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, logits && scores && ids && (recent || n_recent == 0), "vocab_topk: null pointer");
+    REQUIRE(ctx, n_recent >= 0 && n_recent <= 32, "vocab_topk: n_recent=%d outside 0..32", n_recent);
+    REQUIRE(ctx, vocab_topk_ok(vocab, k, partitions),
+            "vocab_topk: vocab=%d, k=%d, partitions=%d unsupported (k 1..64, 1 <= partitions <= vocab, "
+            "partition size * k within 2048 * 16384)",
+            vocab, k, partitions);
+    void *ws = workspace(ctx, vocab_topk_scratch_bytes(vocab, k, partitions));
+    if (!ws) return MRML_HIP_E_ALLOC;
+    return launch_vocab_topk(ctx, logits, valid, recent, scores, ids, vocab, n_recent, generated_count, k,
+                             partitions, ws);
+}
+
+int mrml_hip_vocab_select(mrml_hip_ctx *ctx, const float *logits, int32_t vocab, const uint8_t *valid,
+                          const int32_t *recent, int32_t n_recent, int32_t generated_count, int32_t scoring,
+                          float temperature, uint64_t pos, int32_t k, int32_t *token, float *scores, int32_t *ids)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, logits && (recent || n_recent == 0), "vocab_select: null pointer");
+    REQUIRE(ctx, n_recent >= 0 && n_recent <= 32, "vocab_select: n_recent=%d outside 0..32", n_recent);
+    REQUIRE(ctx, scoring == MRML_HIP_SCORE_CPU || scoring == MRML_HIP_SCORE_DEVICE,
+            "vocab_select: scoring=%d is neither CPU (0) nor DEVICE (1)", scoring);
+    REQUIRE(ctx, temperature == temperature, "vocab_select: temperature is NaN");
+    REQUIRE(ctx, vocab_select_ok(vocab, k), "vocab_select: vocab=%d with k=%d unsupported (k 1..64, vocab/2048*k <= 16384)",
+            vocab, k);
+    void *ws = workspace(ctx, vocab_select_scratch_bytes(vocab, k));
+    if (!ws) return MRML_HIP_E_ALLOC;
+    return launch_vocab_select(ctx, logits, vocab, valid, recent, n_recent, generated_count, scoring, temperature,
+                               pos, k, token, scores, ids, ws, nullptr, nullptr, 0, nullptr, 0, nullptr, 0);
+}
+
 }  // extern "C"

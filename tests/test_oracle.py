@@ -633,3 +633,164 @@ def test_gemma2_step_matches_independent_composition(orc, synth):
     for pos in range(6):
         tok2 = o2.step(tok2, pos, threads=4)
     assert tok2 == tok and np.array_equal(o2.k_cache, o.k_cache)
+
+
+# ---------------------------------------------------------------- vocabulary pick
+
+_LIBM = None
+
+
+def libm_f32(name: str, x: float) -> float:
+    """The host C library's f32 routine (the reference's float_tanh / float_exp bind it)."""
+    global _LIBM
+    if _LIBM is None:
+        import ctypes
+        import ctypes.util
+        _LIBM = ctypes.CDLL(ctypes.util.find_library("m"))
+        for fn in ("tanhf", "expf"):
+            getattr(_LIBM, fn).argtypes = [ctypes.c_float]
+            getattr(_LIBM, fn).restype = ctypes.c_float
+    return float(getattr(_LIBM, name)(np.float32(x)))
+
+
+def numpy_vocab_rank(logits, valid, recent, generated_count, scoring, k):
+    """Candidates and ranking restated with numpy: masks as model.rs:2845-2850,
+    scores as model.rs:2851-2856 (scoring 0) or kernels.rs:1114-1121 (1),
+    then a lexsort on (-score, id)."""
+    ids = np.arange(logits.size)
+    keep = np.ones(logits.size, bool) if valid is None else valid.astype(bool)
+    if generated_count < 4:
+        keep[[i for i in (1, 2, 105, 106) if i < logits.size]] = False
+    rec = np.asarray(recent, np.int64)
+    if scoring == 0:
+        sc = np.array([np.float32(30.0) * np.float32(libm_f32("tanhf", np.float32(v) / np.float32(30.0)))
+                       for v in logits], np.float32)
+        hit = np.isin(ids, rec)
+        sc = np.where(hit, sc - np.float32(3.5), sc).astype(np.float32)
+    else:
+        sc = logits.astype(np.float32).copy()
+        for r in rec:  # one subtraction per occurrence, in list order
+            if 0 <= r < sc.size:
+                sc[r] = np.float32(sc[r] - np.float32(1.8))
+    keep &= ~np.isnan(sc)
+    ids, sc = ids[keep], sc[keep]
+    order = np.lexsort((ids, -sc.astype(np.float64)))[:k]
+    return sc[order], ids[order].astype(np.int32)
+
+
+@pytest.mark.parametrize("scoring", [0, 1])
+def test_vocab_select_ranking_brute_force(orc, scoring):
+    rng = np.random.default_rng(40 + scoring)
+    V = 3000
+    # coarse values so equal scores occur and the id tie rule matters
+    logits = (rng.integers(-400, 400, V) * 0.125).astype(np.float32)
+    logits[[17, 911]] = np.nan
+    valid = (rng.random(V) > 0.1).astype(np.uint8)
+    recent = [5, 1234, 5, 77, 2999, 0, 1234, 1234]  # duplicates: once (CPU) vs per occurrence (device)
+    for gen in (0, 3, 4, 9):
+        for k in (1, 7, 40, 64):
+            tok, sc, ids = orc.vocab_select(logits, valid, recent, gen, scoring, 0.0, 0, k)
+            want_sc, want_ids = numpy_vocab_rank(logits, valid, recent, gen, scoring, k)
+            assert np.array_equal(ids, want_ids), (gen, k)
+            assert np.array_equal(sc.view(np.uint32), want_sc.view(np.uint32)), (gen, k)
+            assert tok == want_ids[0]
+
+
+def test_vocab_select_early_token_mask(orc):
+    logits = np.zeros(200, np.float32)
+    logits[[1, 2, 105, 106]] = 5.0
+    logits[50] = 4.0
+    for gen, want in ((0, 50), (3, 50), (4, 1), (100, 1)):
+        assert orc.vocab_select(logits, generated_count=gen)[0] == want
+    # the mask drops ids, it does not penalise them: 105 wins once 1 and 2 are invalid
+    valid = np.ones(200, np.uint8)
+    valid[[1, 2]] = 0
+    assert orc.vocab_select(logits, valid, generated_count=4)[0] == 105
+
+
+def test_vocab_select_penalty_sizes(orc):
+    # CPU path: 30*tanh(x/30) then -3.5 once; device path: -1.8 per occurrence
+    logits = np.array([10.0, 8.0, 0.0], np.float32)
+    _, sc, ids = orc.vocab_select(logits, recent=[0, 0], generated_count=9, scoring=0, k=3)
+    t10 = np.float32(30.0) * np.float32(libm_f32("tanhf", np.float32(10.0) / np.float32(30.0)))
+    t8 = np.float32(30.0) * np.float32(libm_f32("tanhf", np.float32(8.0) / np.float32(30.0)))
+    assert ids.tolist() == [1, 0, 2]  # 9.64 - 3.5 falls below 7.86
+    assert sc[0] == t8 and sc[1] == np.float32(t10 - np.float32(3.5)) and sc[2] == 0.0
+    _, sc, ids = orc.vocab_select(logits, recent=[0, 0], generated_count=9, scoring=1, k=3)
+    assert ids.tolist() == [1, 0, 2] and sc[1] == np.float32(np.float32(10.0 - np.float32(1.8)) - np.float32(1.8))
+    _, sc, ids = orc.vocab_select(logits, recent=[0], generated_count=9, scoring=1, k=3)
+    assert ids.tolist() == [0, 1, 2] and sc[0] == np.float32(10.0) - np.float32(1.8)
+
+
+def test_vocab_select_no_candidate_and_nan(orc):
+    logits = np.full(16, np.nan, np.float32)
+    tok, sc, ids = orc.vocab_select(logits, temperature=1.0, pos=3)
+    assert tok == 506 and sc.size == 0 and ids.size == 0
+    assert orc.vocab_select(np.zeros(8, np.float32), valid=np.zeros(8, np.uint8))[0] == 506
+    logits = np.array([np.nan, -np.inf, -1.0], np.float32)
+    tok, sc, ids = orc.vocab_select(logits, generated_count=9, k=5, scoring=1)
+    assert tok == 2 and ids.tolist() == [2, 1]
+
+
+def lcg_rng(pos: int) -> np.float32:
+    return np.float32(np.float32(((pos * 6364136223846793005 + 1) % (1 << 64)) >> 33) / np.float32(2**32 - 1))
+
+
+def test_vocab_select_lcg_uniform_pick(orc):
+    # n equal scores: p_i = 1 and acc_i = (i+1)/n (float32 sums), so the pick is
+    # the first i with rng <= acc_i: the inverse CDF of a uniform draw
+    n = 10
+    logits = np.full(n, 2.0, np.float32)
+    counts = np.zeros(n, int)
+    for pos in range(2000):
+        tok = orc.vocab_select(logits, generated_count=9, temperature=0.7, pos=pos, k=n)[0]
+        r, acc, want = lcg_rng(pos), np.float32(0.0), n - 1
+        for i in range(n):
+            acc = np.float32(acc + np.float32(np.float32(1.0) / np.float32(n)))
+            if r <= acc:
+                want = i
+                break
+        assert tok == want, pos
+        counts[tok] += 1
+    # a 64-bit state shifted right by 33 leaves 31 bits, so the draw covers
+    # [0, 0.5) only: the reference never samples the upper half of the CDF
+    assert counts[: n // 2].min() > 300 and counts[n // 2:].sum() == 0
+    assert max(lcg_rng(p) for p in range(2000)) < 0.5
+    assert lcg_rng(0) == 0.0 and orc.vocab_select(logits, temperature=1.0, pos=0, k=n)[0] == 0
+
+
+@pytest.mark.parametrize("temperature", [0.01, 0.5, 2.0])
+def test_vocab_select_draw_frequency(orc, temperature):
+    # one best score a and nine at b: P(best) = 1 / (1 + 9 exp((b - a) / max(t, 0.1))),
+    # drawn with rng uniform on [0, 0.5), so the best is picked with frequency
+    # min(1, 2 P(best)); a wrong sign, a missing clamp or a swapped division
+    # moves it far from that
+    a, b = 1.0, 0.8
+    logits = np.array([b] * 5 + [a] + [b] * 4, np.float32)
+    t = max(temperature, 0.1)
+    p_best = 1.0 / (1.0 + 9 * math.exp((b - a) / t))
+    f = min(1.0, 2 * p_best)
+    n = 4000
+    best = sum(orc.vocab_select(logits, generated_count=9, temperature=temperature, pos=p, k=10)[0] == 5
+               for p in range(n))
+    assert abs(best / n - f) < 4 * math.sqrt(f * (1 - f) / n) + 0.01
+    # two candidates: the best holds at least half the mass, so it is always drawn
+    two = np.array([0.8, 1.0], np.float32)
+    assert all(orc.vocab_select(two, generated_count=9, temperature=2.0, pos=p, k=2)[0] == 1 for p in range(500))
+    assert orc.vocab_select(logits, generated_count=9, temperature=0.0, pos=12345)[0] == 5
+
+
+def test_vocab_topk_reference_known_answer(orc):
+    # ops_test.rs:165-212: the device path's candidates, whatever the
+    # partitioning, hold the exact global top-40 of the penalised logits
+    N, K = 4096, 40
+    i = np.arange(N)
+    logits = (((i * 7919) % 65521).astype(np.float32) * np.float32(0.001) +
+              i.astype(np.float32) * np.float32(1e-7)).astype(np.float32)
+    valid = (i % 17 != 0).astype(np.uint8)
+    recent = [31, 777, 2049, 4001]
+    _, sc, ids = orc.vocab_select(logits, valid, recent, 10, 1, 0.0, 0, K)
+    want = [(s - np.float32(1.8) if t in recent else s, t) for t, s in enumerate(logits) if valid[t]]
+    want.sort(key=lambda e: (-float(e[0]), e[1]))
+    assert [t for _, t in want[:K]] == ids.tolist()
+    assert np.array_equal(np.array([s for s, _ in want[:K]], np.float32).view(np.uint32), sc.view(np.uint32))
