@@ -297,7 +297,7 @@ enum { MRML_HIP_SCORE_CPU = 0, MRML_HIP_SCORE_DEVICE = 1 };
  * scoring; partition p covers ids [vocab*p/partitions,
  * vocab*(p+1)/partitions) and gets its k best (score, id) at
  * d_scores/d_ids[p*k ..], (-inf, -1) past its candidates.  k 1..64; any
- * partition size (the reference's generic kernel) up to 2048*16384/k ids. */
+ * partition size (the reference's generic kernel) up to 2,097,152 ids. */
 int mrml_hip_vocab_topk(mrml_hip_ctx *ctx, const float *d_logits, const uint8_t *d_valid, const int32_t *d_recent,
                         float *d_scores, int32_t *d_ids, int32_t vocab, int32_t n_recent, int32_t generated_count,
                         int32_t k, int32_t partitions);
@@ -310,7 +310,7 @@ int mrml_hip_vocab_topk(mrml_hip_ctx *ctx, const float *d_logits, const uint8_t 
  * reference's state.pos (the position after the token whose logits these
  * are); no candidate: token 506.  d_token (one int32), d_scores / d_ids (k
  * entries, -inf / -1 past the candidates) are nullable.  k 1..64 (the
- * reference draws from 40), vocab up to 2048*16384/k.  Bit-identical to the
+ * reference draws from 40), vocab up to 2,097,152.  Bit-identical to the
  * reference CPU path's choice given its scores. */
 int mrml_hip_vocab_select(mrml_hip_ctx *ctx, const float *d_logits, int32_t vocab, const uint8_t *d_valid,
                           const int32_t *d_recent, int32_t n_recent, int32_t generated_count, int32_t scoring,

@@ -263,7 +263,7 @@ __device__ __forceinline__ float key_score(uint64_t k)
 }
 __device__ __forceinline__ int key_id(uint64_t k) { return (int)~(uint32_t)k; }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v)
+__device__ __forceinline__ uint64_t wave_max(uint64_t v)
 {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
@@ -274,29 +274,58 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v)
     }
     return v;
 }
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(v, off, 64);
+        v = o > v ? o : v;
+    }
+    return v;
+}
 
-// The k largest keys held by the workgroup, in descending order, to out[0..k):
-// every thread holds N keys sorted descending; each round takes the largest
-// head (wave maxima, then across waves through LDS) and its owner pops it.
-// Keys are distinct except 0, so exactly one thread owns a non-zero maximum.
-template <int N>
-__device__ __forceinline__ void block_top_keys(uint64_t (&keys)[N], int k, uint64_t *out, uint64_t *red)
+// The workgroup's largest v, in every thread (red: one entry per wave).
+template <typename T>
+__device__ __forceinline__ T block_max(T v, T *red)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (int)(blockDim.x >> 6);
-    for (int r = 0; r < k; ++r) {
-        const uint64_t m = wave_max_u64(keys[0]);
-        if (lane == 0) red[wave] = m;
-        __syncthreads();
-        uint64_t best = red[0];
-        for (int w = 1; w < nw; ++w) best = red[w] > best ? red[w] : best;
-        if (threadIdx.x == 0) out[r] = best;
-        if (best != 0 && keys[0] == best) {  // the owner pops its head
-#pragma unroll
-            for (int i = 0; i + 1 < N; ++i) keys[i] = keys[i + 1];
-            keys[N - 1] = 0;
-        }
-        __syncthreads();
+    v = wave_max(v);
+    __syncthreads();  // red is free
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    T m = red[0];
+    for (int w = 1; w < nw; ++w) m = red[w] > m ? red[w] : m;
+    return m;
+}
+
+// The k-th largest of vals[0..n) (LDS), counted with multiplicity: the
+// largest v with at least k values >= v; `none` when n < k.  Every thread.
+template <typename T>
+__device__ __forceinline__ T kth_largest(const T *vals, int n, int k, T none, T *red)
+{
+    T best = none;
+    for (int t = threadIdx.x; t < n; t += blockDim.x) {
+        const T v = vals[t];
+        int c = 0;
+        for (int u = 0; u < n; ++u) c += vals[u] >= v ? 1 : 0;
+        if (c >= k && v > best) best = v;
     }
+    return block_max(best, red);
+}
+
+// top[0..k) = the k largest of the n_surv distinct non-zero keys in surv
+// (LDS), descending, then zeros: each key's rank is the number of larger
+// ones.  Ends with a barrier.
+__device__ __forceinline__ void rank_survivors(const uint64_t *surv, int n_surv, int k, uint64_t *top)
+{
+    for (int s = threadIdx.x; s < n_surv; s += blockDim.x) {
+        const uint64_t x = surv[s];
+        int r = 0;
+        for (int u = 0; u < n_surv; ++u) r += surv[u] > x ? 1 : 0;
+        if (r < k) top[r] = x;
+    }
+    for (int i = n_surv + (int)threadIdx.x; i < k; i += blockDim.x) top[i] = 0;
+    __syncthreads();
 }
 
 template <int N>
@@ -316,9 +345,52 @@ __device__ __forceinline__ void sort_desc(uint64_t (&keys)[N])
 constexpr int kVocabPerThread = 8;     // candidates per thread of a partition
 constexpr int kVocabThreads = 256;
 constexpr int kVocabPart = kVocabPerThread * kVocabThreads;  // ids per partition
-constexpr int kSelectThreads = 1024;
+constexpr int kSelectThreads = 1024;   // also the most lists one merge takes
 constexpr int kTopKMax = 64;
 constexpr int kRecentMax = 32;
+// 30*tanh(x/30) from the hardware exp and reciprocal is within this of the
+// host libm's value (both are within a few 1e-6 of the true one); only
+// candidates whose interval can reach the partition's k-th best get the
+// exact evaluation.
+constexpr float kSoftcapSlack = 1e-3f;
+
+__device__ __forceinline__ float softcap_approx(float x)
+{
+    const float e = __expf(x * (2.0f / 30.0f));
+    return 30.0f * (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f));
+}
+
+// The k largest keys (k <= 64) of n_lists descending lists of k keys at
+// lists[i*k ..] (global), to top[0..k) in LDS.  k == 1: the maximum.  Else
+// L = the k-th largest list head: exactly the k lists whose head is >= L
+// (fewer when L is 0) hold the answer, so their keys >= L (at most k*k)
+// are ranked.  n_lists <= blockDim.  Ends with a barrier.
+__device__ __forceinline__ void merge_lists(const uint64_t *__restrict__ lists, int n_lists, int k, uint64_t *top,
+                                            uint64_t *heads, uint64_t *surv, int *n_surv, uint64_t *red)
+{
+    if (k == 1) {
+        uint64_t b = 0;
+        for (int t = threadIdx.x; t < n_lists; t += blockDim.x) b = lists[t] > b ? lists[t] : b;
+        b = block_max(b, red);
+        if (threadIdx.x == 0) top[0] = b;
+        __syncthreads();
+        return;
+    }
+    const int t = threadIdx.x;
+    if (t == 0) *n_surv = 0;
+    heads[t] = t < n_lists ? lists[(size_t)t * k] : 0;
+    __syncthreads();
+    uint64_t L = kth_largest(heads, n_lists, k, (uint64_t)0, red);
+    L = L ? L : 1;
+    if (t < n_lists)
+        for (int i = 0; i < k; ++i) {
+            const uint64_t key = lists[(size_t)t * k + i];
+            if (key < L) break;
+            surv[atomicAdd(n_surv, 1)] = key;
+        }
+    __syncthreads();
+    rank_survivors(surv, *n_surv, k, top);
+}
 
 // Where the scores of one vocabulary pick come from.  recent: the n_recent
 // (<= 32) ids of a caller's list, or, with ring, the tokens of positions
@@ -335,25 +407,16 @@ struct VocabScoring {
     int vocab, n_recent, generated_count, prompt_len, scoring;
 };
 
-__device__ __forceinline__ int gather_recent(const VocabScoring &v, int32_t *dst)
+// Entry l (0..31) of the recent-token list, or -1.
+__device__ __forceinline__ int recent_entry(const VocabScoring &v, int l)
 {
-    if (!v.ring) {
-        for (int r = 0; r < v.n_recent; ++r) dst[r] = v.recent[r];
-        return v.n_recent;
-    }
+    if (!v.ring) return l < v.n_recent ? v.recent[l] : -1;
     const long long cur = v.state ? (long long)v.state[1] : v.host_cur;
-    int n = 0, d = 0;
-    if (v.state) {
-        dst[n++] = v.state[0];
-        d = 1;
-    }
-    for (; d < kRecentMax; ++d) {
-        const long long q = cur - d;
-        if (q < 0) break;
-        const int2 e = v.ring[q % kRecentMax];
-        if (e.x == (int)q) dst[n++] = e.y;
-    }
-    return n;
+    if (v.state && l == 0) return v.state[0];
+    const long long q = cur - l;
+    if (q < 0) return -1;
+    const int2 e = v.ring[q % kRecentMax];
+    return e.x == (int)q ? e.y : -1;
 }
 
 // Block b scores chunk b % chunks (up to 2048 ids) of partition b / chunks,
@@ -366,9 +429,12 @@ __global__ __launch_bounds__(kVocabThreads) void vocab_topk_partial_kernel(Vocab
                                                                            float *__restrict__ out_scores,
                                                                            int32_t *__restrict__ out_ids)
 {
+    constexpr int N = kVocabPerThread;
     __shared__ int32_t rec[kRecentMax];
-    __shared__ int n_rec;
-    __shared__ uint64_t red[kVocabThreads / 64];
+    __shared__ int n_rec, n_surv;
+    __shared__ float fred[kVocabThreads / 64], fvals[kVocabThreads];
+    __shared__ uint64_t kred[kVocabThreads / 64], heads[kVocabThreads];
+    __shared__ uint64_t surv[N * kTopKMax];
     __shared__ uint64_t top[kTopKMax];
     int gen = v.generated_count;
     if (v.state) {
@@ -376,36 +442,104 @@ __global__ __launch_bounds__(kVocabThreads) void vocab_topk_partial_kernel(Vocab
         const long long first = v.prompt_len > 0 ? v.prompt_len - 1 : 0;
         gen = cur > first ? (int)(cur - first) : 0;
     }
-    if (threadIdx.x == 0) n_rec = gather_recent(v, rec);
-    __syncthreads();
-    const int nr = n_rec;
     const int p = (int)blockIdx.x / chunks, c = (int)blockIdx.x % chunks;
     const int pa = (int)((long long)v.vocab * p / parts), pe = (int)((long long)v.vocab * (p + 1) / parts);
     const int start = pa + c * kVocabPart, end = min(start + kVocabPart, pe);
-    uint64_t keys[kVocabPerThread];
+    // the logits and masks are loaded first: nothing below waits twice
+    float x[N];
+    bool cand[N];
 #pragma unroll
-    for (int i = 0; i < kVocabPerThread; ++i) {
+    for (int i = 0; i < N; ++i) {
+        const int id = start + i * kVocabThreads + (int)threadIdx.x;
+        cand[i] = id < end && !(gen < 4 && (id == 1 || id == 2 || id == 105 || id == 106));
+        x[i] = v.logits[cand[i] ? id : pa];  // pa < pe <= vocab: in bounds for an empty chunk too
+        if (v.valid) cand[i] = cand[i] && v.valid[cand[i] ? id : pa];
+    }
+    // the recent ids inside [start, end), compacted by wave 0
+    if (threadIdx.x < 64) {
+        const int id = threadIdx.x < kRecentMax ? recent_entry(v, threadIdx.x) : -1;
+        const bool in = id >= start && id < end;
+        const uint64_t m = __ballot(in);
+        if (in) rec[__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u))] = id;
+        if (threadIdx.x == 0) {
+            n_rec = __popcll(m);
+            n_surv = 0;
+        }
+    }
+    __syncthreads();
+    const int nr = n_rec;
+    // scores: exact for the device path; for the CPU path an interval
+    // [lo, hi] around 30*tanh(x/30) minus the penalty
+    float lo[N], hi[N], pen[N];
+    float mlo = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const int id = start + i * kVocabThreads + (int)threadIdx.x;
+        pen[i] = 0.0f;
+        if (v.scoring == 0) {
+            for (int r = 0; r < nr; ++r)
+                if (rec[r] == id) pen[i] = 3.5f;
+            const float a = softcap_approx(x[i]);
+            lo[i] = (a - kSoftcapSlack) - pen[i];
+            hi[i] = (a + kSoftcapSlack) - pen[i];
+        } else {
+            float sc = x[i];
+            for (int r = 0; r < nr; ++r)
+                if (rec[r] == id) sc -= 1.8f;  // per occurrence, in list order
+            lo[i] = hi[i] = sc;
+        }
+        if (!cand[i] || x[i] != x[i]) {
+            cand[i] = false;
+            lo[i] = -INFINITY;
+        }
+        mlo = lo[i] > mlo ? lo[i] : mlo;
+    }
+    // T: a lower bound of the partition's k-th best score (the k-th largest
+    // per-thread best lower end); only candidates with hi >= T can place
+    float T;
+    if (k == 1) {
+        T = block_max(mlo, fred);
+    } else {
+        fvals[threadIdx.x] = mlo;
+        __syncthreads();
+        T = kth_largest(fvals, kVocabThreads, k, -INFINITY, fred);
+    }
+    uint64_t keys[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
         const int id = start + i * kVocabThreads + (int)threadIdx.x;
         uint64_t key = 0;
-        if (id < end && (!v.valid || v.valid[id]) && !(gen < 4 && (id == 1 || id == 2 || id == 105 || id == 106))) {
-            float sc = v.logits[id];
-            if (v.scoring == 0) {  // CPU path: softcap here, 3.5 once
-                sc = 30.0f * mrml_libm::tanhf(sc / 30.0f);
-                for (int r = 0; r < nr; ++r)
-                    if (rec[r] == id) {
-                        sc -= 3.5f;
-                        break;
-                    }
-            } else {  // device path: softcapped logits, 1.8 per occurrence
-                for (int r = 0; r < nr; ++r)
-                    if (rec[r] == id) sc -= 1.8f;
+        if (cand[i] && hi[i] >= T) {
+            float sc = lo[i];
+            if (v.scoring == 0) {  // the CPU path's exact score
+                sc = 30.0f * mrml_libm::tanhf(x[i] / 30.0f);
+                if (pen[i] != 0.0f) sc -= 3.5f;
             }
             if (sc == sc) key = cand_key(sc, id);
         }
         keys[i] = key;
     }
-    sort_desc(keys);
-    block_top_keys(keys, k, top, red);
+    if (k == 1) {
+        uint64_t b = 0;
+#pragma unroll
+        for (int i = 0; i < N; ++i) b = keys[i] > b ? keys[i] : b;
+        b = block_max(b, kred);
+        if (threadIdx.x == 0) top[0] = b;
+        __syncthreads();
+    } else {
+        // exact top k: L = the k-th largest per-thread best key; the k
+        // threads at or above it hold every answer (at most 8k keys >= L)
+        sort_desc(keys);
+        heads[threadIdx.x] = keys[0];
+        __syncthreads();
+        uint64_t L = kth_largest(heads, kVocabThreads, k, (uint64_t)0, kred);
+        L = L ? L : 1;
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+            if (keys[i] >= L) surv[atomicAdd(&n_surv, 1)] = keys[i];
+        __syncthreads();
+        rank_survivors(surv, n_surv, k, top);
+    }
     for (int r = threadIdx.x; r < k; r += blockDim.x) {
         const uint64_t key = top[r];
         keys_out[(size_t)blockIdx.x * k + r] = key;
@@ -416,26 +550,16 @@ __global__ __launch_bounds__(kVocabThreads) void vocab_topk_partial_kernel(Vocab
     }
 }
 
-// Partition blockIdx.x's k best from its chunks' keys (partitions of more
+// Partition blockIdx.x's k best from its chunks' lists (partitions of more
 // than 2048 ids: the reference's serial kernel, kernels.rs:1170-1228).
 __global__ __launch_bounds__(kSelectThreads) void vocab_topk_merge_kernel(const uint64_t *__restrict__ keys_in,
                                                                          int chunks, int k,
                                                                          float *__restrict__ out_scores,
                                                                          int32_t *__restrict__ out_ids)
 {
-    __shared__ uint64_t top[kTopKMax];
-    __shared__ uint64_t red[kSelectThreads / 64];
-    constexpr int N = 16;
-    const int total = chunks * k;
-    const uint64_t *src = keys_in + (size_t)blockIdx.x * total;
-    uint64_t keys[N];
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-        const int c = i * kSelectThreads + (int)threadIdx.x;
-        keys[i] = c < total ? src[c] : 0;
-    }
-    sort_desc(keys);
-    block_top_keys(keys, k, top, red);
+    __shared__ uint64_t heads[kSelectThreads], surv[kTopKMax * kTopKMax], top[kTopKMax], red[kSelectThreads / 64];
+    __shared__ int n_surv;
+    merge_lists(keys_in + (size_t)blockIdx.x * chunks * k, chunks, k, top, heads, surv, &n_surv, red);
     for (int r = threadIdx.x; r < k; r += blockDim.x) {
         const uint64_t key = top[r];
         out_scores[(size_t)blockIdx.x * k + r] = key ? key_score(key) : -INFINITY;
@@ -445,8 +569,9 @@ __global__ __launch_bounds__(kSelectThreads) void vocab_topk_merge_kernel(const 
 
 // Merges the partitions' keys into the k best (descending) and picks the
 // token: temperature <= 0 -> the first; else the softmax draw of the CPU path
-// with its LCG.  Writes out_token (nullable), out_scores / out_ids (nullable,
-// k entries, -inf / -1 past the candidates) and, with state, advances the
+// with its LCG (the exponentials in parallel, the sums in the reference's
+// order).  Writes out_token (nullable), out_scores / out_ids (nullable, k
+// entries, -inf / -1 past the candidates) and, with state, advances the
 // decode loop as argmax_final_kernel does and records {pos, token} in ring.
 __global__ __launch_bounds__(kSelectThreads) void vocab_select_kernel(
     const uint64_t *__restrict__ part, int n_part, int k, float temperature, unsigned long long pos_arg,
@@ -454,44 +579,43 @@ __global__ __launch_bounds__(kSelectThreads) void vocab_select_kernel(
     int32_t *__restrict__ state, int2 *__restrict__ ring, int32_t *__restrict__ hist, int hist_cap,
     const int32_t *__restrict__ prompt, int prompt_len)
 {
-    __shared__ uint64_t top[kTopKMax];
-    __shared__ uint64_t red[kSelectThreads / 64];
-    constexpr int N = 16;  // keys per thread: up to 16384 partition keys
-    const int total = n_part * k;
-    uint64_t keys[N];
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-        const int c = i * kSelectThreads + (int)threadIdx.x;
-        keys[i] = c < total ? part[c] : 0;
-    }
-    sort_desc(keys);
-    block_top_keys(keys, k, top, red);
-    if (threadIdx.x != 0) return;
+    __shared__ uint64_t heads[kSelectThreads], surv[kTopKMax * kTopKMax], top[kTopKMax], red[kSelectThreads / 64];
+    __shared__ float probs[kTopKMax], quot[kTopKMax];
+    __shared__ int n_surv;
+    merge_lists(part, n_part, k, top, heads, surv, &n_surv, red);
+    const int t = threadIdx.x;
     int n = 0;
-    while (n < k && top[n] != 0) ++n;
+    for (int i = 0; i < k; ++i) n += top[i] != 0 ? 1 : 0;  // the candidates lead, zeros follow
+    // the CPU path's state.pos: the position after the token just processed
+    const unsigned long long pos = state ? (unsigned long long)state[1] + 1ull : pos_arg;
+    const bool draw = n > 0 && temperature > 0.0f;
+    if (draw) {
+        const float s0 = key_score(top[0]);
+        const float temp = temperature > 0.1f ? temperature : 0.1f;
+        if (t < n) probs[t] = mrml_libm::expf((key_score(top[t]) - s0) / temp, expf_fused != 0);
+        __syncthreads();
+        if (t < n) {
+            float sum_exp = 0.0f;
+            for (int i = 0; i < n; ++i) sum_exp += probs[i];
+            quot[t] = probs[t] / sum_exp;
+        }
+        __syncthreads();
+    }
+    if (t != 0) return;
     if (out_scores || out_ids)
         for (int i = 0; i < k; ++i) {
             if (out_scores) out_scores[i] = i < n ? key_score(top[i]) : -INFINITY;
             if (out_ids) out_ids[i] = i < n ? key_id(top[i]) : -1;
         }
-    // the CPU path's state.pos: the position after the token just processed
-    const unsigned long long pos = state ? (unsigned long long)state[1] + 1ull : pos_arg;
     int token = n ? key_id(top[0]) : 506;
-    if (n && temperature > 0.0f) {
-        const float max_logit = key_score(top[0]);
-        const float temp = temperature > 0.1f ? temperature : 0.1f;
-        const bool fused = expf_fused != 0;
-        float probs[kTopKMax];
+    if (draw) {
         float sum_exp = 0.0f;
-        for (int i = 0; i < n; ++i) {
-            probs[i] = mrml_libm::expf((key_score(top[i]) - max_logit) / temp, fused);
-            sum_exp += probs[i];
-        }
+        for (int i = 0; i < n; ++i) sum_exp += probs[i];
         if (sum_exp > 0.0f) {
             const float rng = (float)((pos * 6364136223846793005ull + 1ull) >> 33) / (float)0xffffffffu;
             float acc = 0.0f;
             for (int i = 0; i < n; ++i) {
-                acc += probs[i] / sum_exp;
+                acc += quot[i];
                 if (rng <= acc) {
                     token = key_id(top[i]);
                     break;
@@ -601,7 +725,7 @@ size_t vocab_select_scratch_bytes(int32_t vocab, int32_t k) { return (size_t)voc
 
 bool vocab_select_ok(int32_t vocab, int32_t k)
 {
-    return vocab > 0 && k >= 1 && k <= kTopKMax && (long long)vocab_parts(vocab) * k <= 16 * kSelectThreads;
+    return vocab > 0 && k >= 1 && k <= kTopKMax && vocab_parts(vocab) <= kSelectThreads;
 }
 
 int vocab_topk_chunks(int32_t vocab, int32_t parts)
@@ -613,7 +737,7 @@ int vocab_topk_chunks(int32_t vocab, int32_t parts)
 bool vocab_topk_ok(int32_t vocab, int32_t k, int32_t parts)
 {
     return vocab > 0 && parts >= 1 && parts <= vocab && k >= 1 && k <= kTopKMax &&
-           (long long)vocab_topk_chunks(vocab, parts) * k <= 16 * kSelectThreads;
+           vocab_topk_chunks(vocab, parts) <= kSelectThreads;
 }
 
 size_t vocab_topk_scratch_bytes(int32_t vocab, int32_t k, int32_t parts)

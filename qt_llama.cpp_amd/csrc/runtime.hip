@@ -663,7 +663,7 @@ int mrml_hip_vocab_topk(mrml_hip_ctx *ctx, const float *logits, const uint8_t *v
     REQUIRE(ctx, n_recent >= 0 && n_recent <= 32, "vocab_topk: n_recent=%d outside 0..32", n_recent);
     REQUIRE(ctx, vocab_topk_ok(vocab, k, partitions),
             "vocab_topk: vocab=%d, k=%d, partitions=%d unsupported (k 1..64, 1 <= partitions <= vocab, "
-            "partition size * k within 2048 * 16384)",
+            "partitions of at most 2097152 ids)",
             vocab, k, partitions);
     void *ws = workspace(ctx, vocab_topk_scratch_bytes(vocab, k, partitions));
     if (!ws) return MRML_HIP_E_ALLOC;
@@ -681,7 +681,7 @@ int mrml_hip_vocab_select(mrml_hip_ctx *ctx, const float *logits, int32_t vocab,
     REQUIRE(ctx, scoring == MRML_HIP_SCORE_CPU || scoring == MRML_HIP_SCORE_DEVICE,
             "vocab_select: scoring=%d is neither CPU (0) nor DEVICE (1)", scoring);
     REQUIRE(ctx, temperature == temperature, "vocab_select: temperature is NaN");
-    REQUIRE(ctx, vocab_select_ok(vocab, k), "vocab_select: vocab=%d with k=%d unsupported (k 1..64, vocab/2048*k <= 16384)",
+    REQUIRE(ctx, vocab_select_ok(vocab, k), "vocab_select: vocab=%d with k=%d unsupported (k 1..64, vocab <= 2097152)",
             vocab, k);
     void *ws = workspace(ctx, vocab_select_scratch_bytes(vocab, k));
     if (!ws) return MRML_HIP_E_ALLOC;
