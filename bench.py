@@ -324,10 +324,13 @@ def prefill_profile(be, synth, dev, n_prefill: int) -> dict:
     return {"profile_prefill": n_prefill, "first_token": int(am.numpy()[0])}
 
 
-def decode_profile(be, synth, dev, n_prefill: int, n_steps: int, numerics: int = 0) -> dict:
+def decode_profile(be, synth, dev, n_prefill: int, n_steps: int, numerics: int = 0, prefilled: bool = False) -> dict:
     """Profiling aid for the C4 model: n_prefill + n_steps token steps issued
     eagerly (no graph: the kernel trace then sees every launch); the last
-    n_steps are the decode steps at positions n_prefill.."""
+    n_steps are the decode steps at positions n_prefill..  With prefilled,
+    the prompt goes through one batched prefill call instead of token steps
+    (few dispatches: counter passes serialise every one).  Progress goes to
+    stderr every 64 steps."""
     cfg = dict(synth.GEMMA2_2B)
     model = synth.gemma2_model(cfg, seed=1)
     m = be.Gemma2Model.from_host(dev, model, numerics=numerics)
@@ -339,13 +342,21 @@ def decode_profile(be, synth, dev, n_prefill: int, n_steps: int, numerics: int =
     pr = be.HipBuffer.from_host(dev, prompt)
     kc = be.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
     vc = be.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
-    for i in range(total):
+    first = 0
+    if prefilled:
+        am = be.HipBuffer.from_host(dev, np.array([-1], np.int32))
+        m.prefill(pr, n_prefill, 0, kc, vc, argmax=am)
+        dev.sync()
+        state.copy_from_host(np.array([int(am.numpy()[0]), n_prefill], np.int32))
+        first = n_prefill
+    for i in range(first, total):
         m.step(state, kc, vc, hist=hist, hist_cap=total, prompt=pr, prompt_len=n_prefill)
         if i % 64 == 63:
             dev.sync()
+            print(f"[profile-decode] step {i + 1}/{total}", file=sys.stderr, flush=True)
     dev.sync()
     m.close()
-    return {"profile_decode": n_steps, "prefill_tokens": n_prefill, "numerics": numerics}
+    return {"profile_decode": n_steps, "prefill_tokens": n_prefill, "numerics": numerics, "prefilled": prefilled}
 
 
 def gemm_bench(be, synth, dev, ev, batch: int, cpu_tokens: int, profile: int = 0) -> dict:
@@ -613,6 +624,8 @@ def main() -> int:
                     help="profiling aid: N eager launches of each C5 product, then exit")
     ap.add_argument("--profile-decode", type=int, default=0,
                     help="profiling aid: prefill, then N eager decode steps of the C4 model, then exit")
+    ap.add_argument("--profile-prefilled", action="store_true",
+                    help="with --profile-decode: the prompt through one batched prefill call")
     ap.add_argument("--fast-numerics", action="store_true",
                     help="with --profile-decode: the FAST numerics (tree-order norm sums, split-K attention)")
     ap.add_argument("--profile-prefill", type=int, default=0,
@@ -637,7 +650,8 @@ def main() -> int:
         return 0
     if args.profile_decode:
         print(json.dumps(decode_profile(be, synth, dev, args.decode_prefill, args.profile_decode,
-                                        be.NUMERICS_FAST if args.fast_numerics else be.NUMERICS_EXACT)))
+                                        be.NUMERICS_FAST if args.fast_numerics else be.NUMERICS_EXACT,
+                                        args.profile_prefilled)))
         return 0
     if args.profile_lmhead:
         print(json.dumps(lmhead_profile(be, synth, dev, args.profile_lmhead)))

@@ -321,7 +321,7 @@ __device__ __forceinline__ void rank_survivors(const uint64_t *surv, int n_surv,
     for (int s = threadIdx.x; s < n_surv; s += blockDim.x) {
         const uint64_t x = surv[s];
         int r = 0;
-        for (int u = 0; u < n_surv; ++u) r += surv[u] > x ? 1 : 0;
+        for (int u = 0; u < n_surv && r < k; ++u) r += surv[u] > x ? 1 : 0;  // k or more: placed nowhere
         if (r < k) top[r] = x;
     }
     for (int i = n_surv + (int)threadIdx.x; i < k; i += blockDim.x) top[i] = 0;
@@ -360,36 +360,92 @@ __device__ __forceinline__ float softcap_approx(float x)
     return 30.0f * (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f));
 }
 
+// top[0..k) = the k largest of the n_surv distinct keys in surv (LDS), which
+// hold n_seg descending segments (segment j: seg_len[j] keys from
+// seg_off[j]; surv_seg[s] = the segment of key s): a key's rank is its
+// place in its own segment plus, for every other segment, the number of
+// larger keys there (binary search).  Ends with a barrier.
+__device__ __forceinline__ void rank_segments(const uint64_t *surv, const uint8_t *surv_seg, int n_surv,
+                                              const int *seg_off, const int *seg_len, int n_seg, int k, uint64_t *top)
+{
+    for (int s = threadIdx.x; s < n_surv; s += blockDim.x) {
+        const uint64_t x = surv[s];
+        const int own = surv_seg[s];
+        int r = s - seg_off[own];
+        for (int j = 0; j < n_seg && r < k; ++j) {  // a rank of k or more places nowhere
+            if (j == own) continue;
+            const uint64_t *sj = surv + seg_off[j];
+            const int len = seg_len[j];
+            if (sj[len - 1] > x) {  // the whole segment is larger
+                r += len;
+                continue;
+            }
+            if (sj[0] < x) continue;  // the whole segment is smaller
+            int lo = 0, hi = len;
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (sj[mid] > x) lo = mid + 1;
+                else hi = mid;
+            }
+            r += lo;
+        }
+        if (r < k) top[r] = x;
+    }
+    for (int i = n_surv + (int)threadIdx.x; i < k; i += blockDim.x) top[i] = 0;
+    __syncthreads();
+}
+
+// LDS of merge_lists.
+struct MergeShared {
+    uint64_t heads[kSelectThreads];
+    uint64_t surv[kTopKMax * kTopKMax];
+    uint8_t surv_seg[kTopKMax * kTopKMax];
+    int seg_off[kTopKMax], seg_len[kTopKMax];
+    uint64_t red[kSelectThreads / 64];
+    int n_surv, n_seg;
+};
+
 // The k largest keys (k <= 64) of n_lists descending lists of k keys at
 // lists[i*k ..] (global), to top[0..k) in LDS.  k == 1: the maximum.  Else
 // L = the k-th largest list head: exactly the k lists whose head is >= L
-// (fewer when L is 0) hold the answer, so their keys >= L (at most k*k)
-// are ranked.  n_lists <= blockDim.  Ends with a barrier.
+// (fewer when L is 0) hold the answer, so their keys >= L (at most k*k, a
+// prefix of each) are ranked -- by counting when few, else per segment.
+// n_lists <= blockDim.  Ends with a barrier.
 __device__ __forceinline__ void merge_lists(const uint64_t *__restrict__ lists, int n_lists, int k, uint64_t *top,
-                                            uint64_t *heads, uint64_t *surv, int *n_surv, uint64_t *red)
+                                            MergeShared &m)
 {
     if (k == 1) {
         uint64_t b = 0;
         for (int t = threadIdx.x; t < n_lists; t += blockDim.x) b = lists[t] > b ? lists[t] : b;
-        b = block_max(b, red);
+        b = block_max(b, m.red);
         if (threadIdx.x == 0) top[0] = b;
         __syncthreads();
         return;
     }
     const int t = threadIdx.x;
-    if (t == 0) *n_surv = 0;
-    heads[t] = t < n_lists ? lists[(size_t)t * k] : 0;
+    if (t == 0) {
+        m.n_surv = 0;
+        m.n_seg = 0;
+    }
+    m.heads[t] = t < n_lists ? lists[(size_t)t * k] : 0;
     __syncthreads();
-    uint64_t L = kth_largest(heads, n_lists, k, (uint64_t)0, red);
+    uint64_t L = kth_largest(m.heads, n_lists, k, (uint64_t)0, m.red);
     L = L ? L : 1;
-    if (t < n_lists)
-        for (int i = 0; i < k; ++i) {
-            const uint64_t key = lists[(size_t)t * k + i];
-            if (key < L) break;
-            surv[atomicAdd(n_surv, 1)] = key;
+    if (t < n_lists && m.heads[t] >= L) {
+        const uint64_t *lt = lists + (size_t)t * k;
+        int c = 1;
+        while (c < k && lt[c] >= L) ++c;
+        const int off = atomicAdd(&m.n_surv, c), sg = atomicAdd(&m.n_seg, 1);
+        m.seg_off[sg] = off;
+        m.seg_len[sg] = c;
+        for (int i = 0; i < c; ++i) {
+            m.surv[off + i] = lt[i];
+            m.surv_seg[off + i] = (uint8_t)sg;
         }
+    }
     __syncthreads();
-    rank_survivors(surv, *n_surv, k, top);
+    if (m.n_surv <= 4 * kTopKMax) rank_survivors(m.surv, m.n_surv, k, top);
+    else rank_segments(m.surv, m.surv_seg, m.n_surv, m.seg_off, m.seg_len, m.n_seg, k, top);
 }
 
 // Where the scores of one vocabulary pick come from.  recent: the n_recent
@@ -431,8 +487,11 @@ __global__ __launch_bounds__(kVocabThreads) void vocab_topk_partial_kernel(Vocab
 {
     constexpr int N = kVocabPerThread;
     __shared__ int32_t rec[kRecentMax];
-    __shared__ int n_rec, n_surv;
+    __shared__ int n_rec, n_surv, n_cand;
     __shared__ float fred[kVocabThreads / 64], fvals[kVocabThreads];
+    __shared__ float c_val[kVocabPart];
+    __shared__ uint16_t c_meta[kVocabPart];
+    __shared__ uint64_t c_key[kVocabPart];
     __shared__ uint64_t kred[kVocabThreads / 64], heads[kVocabThreads];
     __shared__ uint64_t surv[N * kTopKMax];
     __shared__ uint64_t top[kTopKMax];
@@ -464,24 +523,26 @@ __global__ __launch_bounds__(kVocabThreads) void vocab_topk_partial_kernel(Vocab
         if (threadIdx.x == 0) {
             n_rec = __popcll(m);
             n_surv = 0;
+            n_cand = 0;
         }
     }
     __syncthreads();
     const int nr = n_rec;
     // scores: exact for the device path; for the CPU path an interval
     // [lo, hi] around 30*tanh(x/30) minus the penalty
-    float lo[N], hi[N], pen[N];
+    float lo[N], hi[N];
+    bool pen[N];
     float mlo = -INFINITY;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
         const int id = start + i * kVocabThreads + (int)threadIdx.x;
-        pen[i] = 0.0f;
+        pen[i] = false;
         if (v.scoring == 0) {
             for (int r = 0; r < nr; ++r)
-                if (rec[r] == id) pen[i] = 3.5f;
+                if (rec[r] == id) pen[i] = true;
             const float a = softcap_approx(x[i]);
-            lo[i] = (a - kSoftcapSlack) - pen[i];
-            hi[i] = (a + kSoftcapSlack) - pen[i];
+            lo[i] = (a - kSoftcapSlack) - (pen[i] ? 3.5f : 0.0f);
+            hi[i] = (a + kSoftcapSlack) - (pen[i] ? 3.5f : 0.0f);
         } else {
             float sc = x[i];
             for (int r = 0; r < nr; ++r)
@@ -495,7 +556,8 @@ __global__ __launch_bounds__(kVocabThreads) void vocab_topk_partial_kernel(Vocab
         mlo = lo[i] > mlo ? lo[i] : mlo;
     }
     // T: a lower bound of the partition's k-th best score (the k-th largest
-    // per-thread best lower end); only candidates with hi >= T can place
+    // per-thread best lower end); only candidates with hi >= T can place.
+    // They are compacted (element, value, penalty) for one exact pass.
     float T;
     if (k == 1) {
         T = block_max(mlo, fred);
@@ -504,20 +566,31 @@ __global__ __launch_bounds__(kVocabThreads) void vocab_topk_partial_kernel(Vocab
         __syncthreads();
         T = kth_largest(fvals, kVocabThreads, k, -INFINITY, fred);
     }
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if (cand[i] && hi[i] >= T) {
+            const int slot = atomicAdd(&n_cand, 1);
+            c_val[slot] = v.scoring == 0 ? x[i] : lo[i];
+            c_meta[slot] = (uint16_t)((i * kVocabThreads + (int)threadIdx.x) | (pen[i] ? 0x8000 : 0));
+        }
+    __syncthreads();
+    const int nc = n_cand;
+#pragma unroll 1
+    for (int s = threadIdx.x; s < nc; s += kVocabThreads) {
+        const int e = c_meta[s] & 0x7fff, id = start + e;
+        float sc = c_val[s];
+        if (v.scoring == 0) {  // the CPU path's exact score
+            sc = 30.0f * mrml_libm::tanhf(sc / 30.0f);
+            if (c_meta[s] & 0x8000) sc -= 3.5f;
+        }
+        c_key[s] = sc == sc ? cand_key(sc, id) : 0;
+    }
+    __syncthreads();
     uint64_t keys[N];
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-        const int id = start + i * kVocabThreads + (int)threadIdx.x;
-        uint64_t key = 0;
-        if (cand[i] && hi[i] >= T) {
-            float sc = lo[i];
-            if (v.scoring == 0) {  // the CPU path's exact score
-                sc = 30.0f * mrml_libm::tanhf(x[i] / 30.0f);
-                if (pen[i] != 0.0f) sc -= 3.5f;
-            }
-            if (sc == sc) key = cand_key(sc, id);
-        }
-        keys[i] = key;
+        const int s = i * kVocabThreads + (int)threadIdx.x;
+        keys[i] = s < nc ? c_key[s] : 0;
     }
     if (k == 1) {
         uint64_t b = 0;
@@ -557,9 +630,9 @@ __global__ __launch_bounds__(kSelectThreads) void vocab_topk_merge_kernel(const 
                                                                          float *__restrict__ out_scores,
                                                                          int32_t *__restrict__ out_ids)
 {
-    __shared__ uint64_t heads[kSelectThreads], surv[kTopKMax * kTopKMax], top[kTopKMax], red[kSelectThreads / 64];
-    __shared__ int n_surv;
-    merge_lists(keys_in + (size_t)blockIdx.x * chunks * k, chunks, k, top, heads, surv, &n_surv, red);
+    __shared__ MergeShared ms;
+    __shared__ uint64_t top[kTopKMax];
+    merge_lists(keys_in + (size_t)blockIdx.x * chunks * k, chunks, k, top, ms);
     for (int r = threadIdx.x; r < k; r += blockDim.x) {
         const uint64_t key = top[r];
         out_scores[(size_t)blockIdx.x * k + r] = key ? key_score(key) : -INFINITY;
@@ -579,10 +652,10 @@ __global__ __launch_bounds__(kSelectThreads) void vocab_select_kernel(
     int32_t *__restrict__ state, int2 *__restrict__ ring, int32_t *__restrict__ hist, int hist_cap,
     const int32_t *__restrict__ prompt, int prompt_len)
 {
-    __shared__ uint64_t heads[kSelectThreads], surv[kTopKMax * kTopKMax], top[kTopKMax], red[kSelectThreads / 64];
+    __shared__ MergeShared ms;
+    __shared__ uint64_t top[kTopKMax];
     __shared__ float probs[kTopKMax], quot[kTopKMax];
-    __shared__ int n_surv;
-    merge_lists(part, n_part, k, top, heads, surv, &n_surv, red);
+    merge_lists(part, n_part, k, top, ms);
     const int t = threadIdx.x;
     int n = 0;
     for (int i = 0; i < k; ++i) n += top[i] != 0 ? 1 : 0;  // the candidates lead, zeros follow
