@@ -395,6 +395,20 @@ def gemm_bench(be, synth, dev, ev, batch: int, cpu_tokens: int, profile: int = 0
                   "launches_per_sample": st["launches_per_sample"]}
         total_ops += ops
         total_s += secs
+    # the tolerance path's one-FMA fold (mrml_hip_gemm_q4_0_relaxed) beside
+    # the exact one, both from f32 activations (quantisation included)
+    relaxed = {}
+    for k in ("gate", "down"):
+        r, c = mats[k]
+        dev.gemm_q4_0(w[k], xb[c], y, r, c, batch)  # workspace sized before capture
+        row = {}
+        for name, fn in (("exact", dev.gemm_q4_0), ("relaxed", dev.gemm_q4_0_relaxed)):
+            g = dev.capture(lambda: [fn(w[k], xb[c], y, r, c, batch) for _ in range(per_graph)])
+            st = sample_launches(dev, ev, g, per_graph)
+            g.close()
+            row[name + "_us"] = round(st["median_s"] * 1e6, 2)
+        row["speedup"] = round(row["exact_us"] / row["relaxed_us"], 3)
+        relaxed[k] = row
     # quantising the [M][K] activations into the GEMM pack (once per input)
     gq = dev.capture(lambda: [dev.quantize_q8_0_gemm(xb[DIM], packs[DIM], DIM, batch) for _ in range(20)])
     time_graph(dev, ev, gq, 2)
@@ -404,6 +418,8 @@ def gemm_bench(be, synth, dev, ev, batch: int, cpu_tokens: int, profile: int = 0
     out = {"tops": round(tops, 2), "unit": "TOPS (int8)", "mfma_util": round(tops / PEAK_INT8_TOPS, 4),
            "peak_tops": PEAK_INT8_TOPS, "per_matrix": per, "batch": batch,
            "quantize_q8_0_us": round(tq * 1e6, 2), "kernel": "gemm_q4_0_mfma_kernel",
+           "relaxed_fold": dict(relaxed, how="f32 activations in (quantisation included); the FAST numerics' prefill "
+                                             "uses the relaxed fold (within 1e-5 of the exact product)"),
            "workload": f"BASELINE configs[4]: M={batch} tokens, Q4_0 gate/up 9216x2304 + down 2304x9216, "
                        "activations pre-quantised to Q8_0 (GEMM pack), hipEvent around graph replays"}
     if cpu_tokens > 0:

@@ -226,6 +226,14 @@ int mrml_hip_gemv_q4_k_q8(mrml_hip_ctx *ctx, const void *d_w, const void *d_xpac
  * bytes rounded up) for the activations in MFMA order. */
 int mrml_hip_gemm_q4_0(mrml_hip_ctx *ctx, const void *d_w, const float *d_x, float *d_y,
                        int32_t rows, int32_t cols, int32_t batch);
+/* mrml_hip_gemm_q4_0 with the tolerance path's fold: the integer block sums
+ * stay exact, each block term joins its output's sum with one FMA (one
+ * rounding instead of two), so outputs are within 1e-5 of the exact
+ * product relative to the largest output (the GEMM's time is its f32 fold;
+ * this removes a quarter of the fold's instructions).  The prefill of a
+ * MRML_HIP_NUMERICS_FAST model uses it. */
+int mrml_hip_gemm_q4_0_relaxed(mrml_hip_ctx *ctx, const void *d_w, const float *d_x, float *d_y,
+                               int32_t rows, int32_t cols, int32_t batch);
 /* As mrml_hip_gemm_q4_0 with the batch already quantised: d_xpack is the
  * activation pack of batch*cols values (mrml_hip_quantize_q8_0 over the
  * whole [batch][cols] array), token m's block b at index m*(cols/32)+b. */

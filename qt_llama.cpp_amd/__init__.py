@@ -156,6 +156,7 @@ _SIGNATURES = {
     "mrml_hip_gemm_q4_0": [_P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemm_q4_0_q8": [_P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemm_q4_0_noalloc": [_P, _P, _P, _P, _I, _I, _I],
+    "mrml_hip_gemm_q4_0_relaxed": [_P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemm_q4_0_qkv": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I],
     "mrml_hip_gemm_q4_0_geglu": [_P, _P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_rms_norm_batch": [_P, _P, _P, _P, _I, _I, _F],
@@ -399,6 +400,10 @@ class HipDevice:
 
     def gemm_q4_0(self, w, x, y, rows: int, cols: int, batch: int) -> None:
         self._check(self.lib.mrml_hip_gemm_q4_0(self.ctx, _ptr(w), _ptr(x), _ptr(y), rows, cols, batch))
+
+    def gemm_q4_0_relaxed(self, w, x, y, rows: int, cols: int, batch: int) -> None:
+        """gemm_q4_0 with the one-FMA f32 fold (within 1e-5 of the exact product)."""
+        self._check(self.lib.mrml_hip_gemm_q4_0_relaxed(self.ctx, _ptr(w), _ptr(x), _ptr(y), rows, cols, batch))
 
     def gemm_q4_0_qkv(self, wq, wk, wv, x, y, q_rows: int, kv_rows: int, cols: int, batch: int) -> None:
         self._check(self.lib.mrml_hip_gemm_q4_0_qkv(self.ctx, _ptr(wq), _ptr(wk), _ptr(wv), _ptr(x), _ptr(y),

@@ -911,58 +911,38 @@ __global__ __launch_bounds__(kAttnHD) void attn_combine_kernel(const float *__re
                                                                int capacity, int max_tiles, int n_heads,
                                                                float *__restrict__ out, uint8_t *__restrict__ pack)
 {
-    constexpr int HD = kAttnHD, kMaxTiles = (6144 + kSplitP - 1) / kSplitP, kOnePass = 32;
+    constexpr int HD = kAttnHD, kMaxTiles = (6144 + kSplitP - 1) / kSplitP;
     __shared__ float m_s[kMaxTiles], w_s[kMaxTiles], l_s[kMaxTiles];
     int window, start;
     attn_window(d_pos, n_past_arg, capacity, window, start);
     const int ntiles = (window + kSplitP - 1) / kSplitP, h = blockIdx.x, d = threadIdx.x;
     const float *ph = part + (size_t)h * max_tiles * kSplitPart;
+    // the tiles' (m, l) in parallel, one tile per thread
+    for (int t = d; t < ntiles; t += HD) {
+        m_s[t] = ph[(size_t)t * kSplitPart + HD];
+        l_s[t] = ph[(size_t)t * kSplitPart + HD + 1];
+    }
+    __syncthreads();
+    float M = -INFINITY;
+    for (int t = 0; t < ntiles; ++t) M = fmaxf(M, m_s[t]);
+    for (int t = d; t < ntiles; t += HD) w_s[t] = __builtin_expf(m_s[t] - M);
+    __syncthreads();
+    // L and o in tile order (every thread forms the same L)
     float L = 0.0f, o = 0.0f;
-    if (ntiles <= kOnePass) {
-        // one round trip: lane k of every wave loads tile k's (m, l), every
-        // thread its o[d] of all tiles; weights move between lanes by readlane
-        const int lane = d & 63, tl = lane < ntiles ? lane : ntiles - 1;
-        const float mk = ph[(size_t)tl * kSplitPart + HD], lk = ph[(size_t)tl * kSplitPart + HD + 1];
-        float ov[kOnePass];
+    int t = 0;
+    for (; t + 8 <= ntiles; t += 8) {
+        float v[8];
 #pragma unroll
-        for (int k = 0; k < kOnePass; ++k) ov[k] = ph[(size_t)(k < ntiles ? k : ntiles - 1) * kSplitPart + d];
-        const float M = wave_max_f32(lane < ntiles ? mk : -INFINITY);
-        const float wk = __builtin_expf(mk - M);
+        for (int k = 0; k < 8; ++k) v[k] = ph[(size_t)(t + k) * kSplitPart + d];  // eight loads in flight
 #pragma unroll
-        for (int k = 0; k < kOnePass; ++k)
-            if (k < ntiles) {
-                const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k));
-                const float l = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lk), k));
-                L = L + l * w;
-                o = o + ov[k] * w;
-            }
-    } else {
-        // the tiles' (m, l) in parallel, one tile per thread
-        for (int t = d; t < ntiles; t += HD) {
-            m_s[t] = ph[(size_t)t * kSplitPart + HD];
-            l_s[t] = ph[(size_t)t * kSplitPart + HD + 1];
+        for (int k = 0; k < 8; ++k) {
+            L = L + l_s[t + k] * w_s[t + k];
+            o = o + v[k] * w_s[t + k];
         }
-        __syncthreads();
-        float M = -INFINITY;
-        for (int t = 0; t < ntiles; ++t) M = fmaxf(M, m_s[t]);
-        for (int t = d; t < ntiles; t += HD) w_s[t] = __builtin_expf(m_s[t] - M);
-        __syncthreads();
-        // L and o in tile order (every thread forms the same L)
-        int t = 0;
-        for (; t + 8 <= ntiles; t += 8) {
-            float v[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = ph[(size_t)(t + k) * kSplitPart + d];  // eight loads in flight
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                L = L + l_s[t + k] * w_s[t + k];
-                o = o + v[k] * w_s[t + k];
-            }
-        }
-        for (; t < ntiles; ++t) {
-            L = L + l_s[t] * w_s[t];
-            o = o + ph[(size_t)t * kSplitPart + d] * w_s[t];
-        }
+    }
+    for (; t < ntiles; ++t) {
+        L = L + l_s[t] * w_s[t];
+        o = o + ph[(size_t)t * kSplitPart + d] * w_s[t];
     }
     const float v = o / L;
     const int idx = h * HD + d;

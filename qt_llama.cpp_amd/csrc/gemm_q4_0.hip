@@ -19,6 +19,7 @@
 // scales are float4 broadcasts from LDS.
 //
 // The ordered f32 fold runs on the VALU: 4 instructions per output per block
+// (3 with RELAXED, the tolerance path's one-FMA fold)
 // against one MFMA per 1024 outputs.  Measured on gfx950: an MFMA holds its
 // SIMD's VALU issue while it executes (about 36 cycles for this one); f32
 // mul/add and integer ALU ops issue from two waves at once (about 2.4 SIMD
@@ -131,6 +132,10 @@ struct BOps {
     float da;  // the token's block scale
 };
 
+// RELAXED: each block term joins its output's sum with one FMA instead of
+// a product and a separate add (the integer sums stay exact; the f32 sums
+// round once per block instead of twice) -- the tolerance path's prefill.
+template <bool RELAXED>
 __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const uint8_t *__restrict__ w,
                                                                          const uint8_t *__restrict__ gp,
                                                                          float *__restrict__ y, int rows, int nb,
@@ -206,7 +211,8 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
                 // element lvalue reads element 0 in this compiler)
                 const int de = d[4 * j + i];
                 const float isum = __builtin_bit_cast(float, de) - kMagic;  // exact
-                acc[4 * j + i] = acc[4 * j + i] + isum * (dwv[i] * da);
+                if constexpr (RELAXED) acc[4 * j + i] = __builtin_fmaf(isum, dwv[i] * da, acc[4 * j + i]);
+                else acc[4 * j + i] = acc[4 * j + i] + isum * (dwv[i] * da);
             }
         }
     };
@@ -331,7 +337,7 @@ int launch_gemm_pack_from_act(mrml_hip_ctx *ctx, const void *pack, void *gpack, 
 }
 
 int launch_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const void *gpack, float *y, int32_t rows, int32_t cols,
-                     int32_t batch, int32_t ldy)
+                     int32_t batch, int32_t ldy, bool relaxed)
 {
     const int nb = cols / 32, ng = gemm_groups(batch);
     if (ldy == 0) ldy = rows;
@@ -339,8 +345,12 @@ int launch_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const void *gpack, float 
         return fail(ctx, MRML_HIP_E_INVALID, "gemm_q4_0: output stride %d (rows %d) must be a multiple of 4 and y 16-byte aligned",
                     ldy, rows);
     const dim3 grid(rows / 32, (ng + kGemmWaves - 1) / kGemmWaves);
-    hipLaunchKernelGGL(gemm_q4_0_mfma_kernel, grid, dim3(64 * kGemmWaves), 0, ctx->stream, (const uint8_t *)w,
-                       (const uint8_t *)gpack, y, rows, nb, batch, ng, ldy);
+    if (relaxed)
+        hipLaunchKernelGGL(gemm_q4_0_mfma_kernel<true>, grid, dim3(64 * kGemmWaves), 0, ctx->stream, (const uint8_t *)w,
+                           (const uint8_t *)gpack, y, rows, nb, batch, ng, ldy);
+    else
+        hipLaunchKernelGGL(gemm_q4_0_mfma_kernel<false>, grid, dim3(64 * kGemmWaves), 0, ctx->stream,
+                           (const uint8_t *)w, (const uint8_t *)gpack, y, rows, nb, batch, ng, ldy);
     return check_launch(ctx, "gemm_q4_0_mfma_kernel");
 }
 

@@ -84,7 +84,7 @@ size_t gemm_noalloc_scratch_bytes();
 int gemm_noalloc_scratch(mrml_hip_ctx *ctx, void **out);
 // y row stride ldy floats (0: rows; a multiple of 4, y 16-byte aligned)
 int launch_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const void *gpack, float *y, int32_t rows, int32_t cols,
-                     int32_t batch, int32_t ldy = 0);
+                     int32_t batch, int32_t ldy = 0, bool relaxed = false);
 
 // Argmax whose final pass can also advance a device-side decode loop
 // (state = {token, pos}) and record the processed token in the recent-token

@@ -418,7 +418,7 @@ int prefill_buffers(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m)
 int gemm_rows(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const void *w, const float *x, float *y, int rows, int cols, int n)
 {
     if (int rc = launch_gemm_pack_quantize(ctx, x, m->pf_gpack, cols, n)) return rc;
-    return launch_gemm_q4_0(ctx, w, m->pf_gpack, y, rows, cols, n);
+    return launch_gemm_q4_0(ctx, w, m->pf_gpack, y, rows, cols, n, 0, m->cfg.numerics == MRML_HIP_NUMERICS_FAST);
 }
 
 }  // namespace
@@ -442,6 +442,7 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
     if (int rc = prefill_buffers(ctx, m)) return rc;
     const size_t layer_cache = (size_t)c.ctx_len * kvd;
     const float emb_scale = sqrtf((float)c.dim);
+    const bool fast = c.numerics == MRML_HIP_NUMERICS_FAST;  // the one-FMA GEMM fold
     int rc;
 #define STEP(call)                      \
     do {                                \
@@ -458,9 +459,9 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
             const float *next_norm = l + 1 < c.n_layers ? m->layers[l + 1].attn_norm : m->output_norm;
             // q, k, v of the chunk, stacked per token as the token step's q|k|v
             STEP(launch_gemm_pack_quantize(ctx, xn, m->pf_gpack, c.dim, n));
-            STEP(launch_gemm_q4_0(ctx, L.wq, m->pf_gpack, m->pf_qkv, qd, c.dim, n, qkvd));
-            STEP(launch_gemm_q4_0(ctx, L.wk, m->pf_gpack, m->pf_qkv + qd, kvd, c.dim, n, qkvd));
-            STEP(launch_gemm_q4_0(ctx, L.wv, m->pf_gpack, m->pf_qkv + qd + kvd, kvd, c.dim, n, qkvd));
+            STEP(launch_gemm_q4_0(ctx, L.wq, m->pf_gpack, m->pf_qkv, qd, c.dim, n, qkvd, fast));
+            STEP(launch_gemm_q4_0(ctx, L.wk, m->pf_gpack, m->pf_qkv + qd, kvd, c.dim, n, qkvd, fast));
+            STEP(launch_gemm_q4_0(ctx, L.wv, m->pf_gpack, m->pf_qkv + qd + kvd, kvd, c.dim, n, qkvd, fast));
             // every token's rotated k and v enter the cache before any token
             // attends; token i then reads positions <= p0 + i only
             STEP(launch_rope_kv_f16(ctx, m->pf_qkv, kc, vc, nullptr, p0, c.n_heads, c.n_kv_heads, c.head_dim,
@@ -478,8 +479,8 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
             STEP(launch_residual_rms_norm(ctx, m->pf_o, L.post_attn_norm, h, h, L.ffn_norm, c.eps, xn, nullptr, c.dim,
                                           n));
             STEP(launch_gemm_pack_quantize(ctx, xn, m->pf_gpack, c.dim, n));
-            STEP(launch_gemm_q4_0(ctx, L.w_gate, m->pf_gpack, m->pf_g, c.ffn_dim, c.dim, n));
-            STEP(launch_gemm_q4_0(ctx, L.w_up, m->pf_gpack, m->pf_u, c.ffn_dim, c.dim, n));
+            STEP(launch_gemm_q4_0(ctx, L.w_gate, m->pf_gpack, m->pf_g, c.ffn_dim, c.dim, n, 0, fast));
+            STEP(launch_gemm_q4_0(ctx, L.w_up, m->pf_gpack, m->pf_u, c.ffn_dim, c.dim, n, 0, fast));
             // act = gelu_tanh(g) * u per element: the GeGLU epilogue of the
             // matvec kernels, so each act value has the token step's bits
             STEP(launch_geglu_rows(ctx, m->pf_g, m->pf_u, m->pf_act, n * c.ffn_dim));

@@ -560,6 +560,17 @@ int mrml_hip_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const float *x, float *
     return rc ? rc : launch_gemm_q4_0(ctx, w, gp, y, rows, cols, batch);
 }
 
+int mrml_hip_gemm_q4_0_relaxed(mrml_hip_ctx *ctx, const void *w, const float *x, float *y, int32_t rows,
+                               int32_t cols, int32_t batch)
+{
+    CTX_GUARD(ctx);
+    CHECK_GEMM(ctx, w, x, y, rows, cols, batch);
+    void *gp = workspace(ctx, gemm_pack_bytes(cols, batch));
+    if (!gp) return MRML_HIP_E_ALLOC;
+    int rc = launch_gemm_pack_quantize(ctx, x, gp, cols, batch);
+    return rc ? rc : launch_gemm_q4_0(ctx, w, gp, y, rows, cols, batch, 0, true);
+}
+
 int mrml_hip_gemm_q4_0_noalloc(mrml_hip_ctx *ctx, const void *w, const float *x, float *y, int32_t rows,
                                int32_t cols, int32_t batch)
 {

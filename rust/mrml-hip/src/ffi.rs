@@ -176,6 +176,7 @@ api! {
     gemm_q4_0_gpack: fn(Ctx, *const c_void, *const c_void, *mut f32, i32, i32, i32) -> c_int = "mrml_hip_gemm_q4_0_gpack";
     gemm_q4_0_qkv: fn(Ctx, *const c_void, *const c_void, *const c_void, *const f32, *mut f32, i32, i32, i32, i32) -> c_int = "mrml_hip_gemm_q4_0_qkv";
     gemm_q4_0_geglu: fn(Ctx, *const c_void, *const c_void, *const f32, *mut f32, i32, i32, i32) -> c_int = "mrml_hip_gemm_q4_0_geglu";
+    gemm_q4_0_relaxed: fn(Ctx, *const c_void, *const f32, *mut f32, i32, i32, i32) -> c_int = "mrml_hip_gemm_q4_0_relaxed";
     gemm_q4_0_noalloc: fn(Ctx, *const c_void, *const f32, *mut f32, i32, i32, i32) -> c_int = "mrml_hip_gemm_q4_0_noalloc";
     gemm_q4_0_noalloc_max_pack_bytes: fn() -> usize = "mrml_hip_gemm_q4_0_noalloc_max_pack_bytes";
     argmax_f32: fn(Ctx, *const f32, i32, *mut i32) -> c_int = "mrml_hip_argmax_f32";

@@ -723,3 +723,28 @@ def test_gemma2_2b_greedy_64(backend, dev, orc, synth):
     assert exact == len(lg_ref)
     # the teacher-forced picks depend on the context (not one repeated token)
     assert len(set(want[:64].tolist())) >= 4
+
+
+def test_gemma2_tiny_fast_prefill(backend, dev, orc, synth):
+    """FAST numerics in the chunked prefill (the one-FMA GEMM fold): the last
+    prompt position's logits stay within the FAST bound of the oracle's, and
+    its pick equals the oracle's or is a near-tie of it."""
+    cfg = dict(TINY, ctx_len=256)
+    model = synth.gemma2_model(cfg, seed=15)
+    prompt = synth.prompt_tokens(150, cfg["vocab"], seed=8)
+    m = backend.Gemma2Model.from_host(dev, model, numerics=1)
+    kc = backend.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    vc = backend.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    logits = backend.HipBuffer.alloc(dev, cfg["vocab"])
+    am = backend.HipBuffer.from_host(dev, np.array([-1], np.int32))
+    toks = backend.HipBuffer.from_host(dev, np.asarray(prompt, np.int32))
+    m.prefill(toks, len(prompt), 0, kc, vc, logits=logits, argmax=am)
+    dev.sync()
+    got, pick = logits.numpy(), int(am.numpy()[0])
+    m.close()
+    want, lg_ref, _ = run_oracle_decode(orc, model, prompt, 0)
+    ref = lg_ref[len(prompt) - 1]
+    err = max_rel(got, ref)
+    print(f"\n[fast prefill] logits max-rel {err:.2e}, pick {pick} vs {want[len(prompt) - 1]}", flush=True)
+    assert err <= 2e-2
+    assert ref[pick] >= ref.max() - 0.05 * np.max(np.abs(ref))

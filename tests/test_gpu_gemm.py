@@ -178,3 +178,27 @@ def test_gemm_q4_0_geglu_per_token(backend, dev, orc, synth, batch):
     u = oracle_gemm(orc, wu, x, rows, cols, range(batch))
     ref = np.stack([orc.geglu(g[m], u[m]) for m in range(batch)])
     assert_bit_exact(got, ref, f"gemm geglu M={batch}")
+
+
+# The tolerance path's fold (mrml_hip_gemm_q4_0_relaxed): integer block sums
+# exact, one FMA per block term; bound 1e-5 of the largest output.
+RELAXED_TOL = 1e-5
+
+
+@pytest.mark.parametrize("rows,cols,batch", [(9216, 2304, 128), (2304, 9216, 512), (2048, 2304, 37)])
+def test_gemm_q4_0_relaxed_within_tolerance(backend, dev, synth, rows, cols, batch):
+    rng = synth.rng_for(7000 + rows + batch)
+    w = synth.q4_0_matrix(rng, rows, cols)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    wb = backend.HipBuffer.from_gguf(dev, w, backend.Q4_0, rows, cols)
+    xb = backend.HipBuffer.from_host(dev, x.reshape(-1))
+    ye = backend.HipBuffer.alloc(dev, rows * batch)
+    yr = backend.HipBuffer.alloc(dev, rows * batch)
+    dev.gemm_q4_0(wb, xb, ye, rows, cols, batch)
+    dev.gemm_q4_0_relaxed(wb, xb, yr, rows, cols, batch)
+    dev.sync()
+    e, r = ye.numpy(), yr.numpy()
+    err = float(np.max(np.abs(r.astype(np.float64) - e))) / float(np.max(np.abs(e)))
+    print(f"\n[relaxed gemm] {rows}x{cols} M={batch}: max-rel {err:.2e}", flush=True)
+    assert err <= RELAXED_TOL
+    assert not np.array_equal(r.view(np.uint32), e.view(np.uint32))  # the fold did change (a live check)
