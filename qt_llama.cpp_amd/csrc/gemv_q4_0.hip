@@ -120,7 +120,7 @@ __device__ __forceinline__ void load_row(RowRegs<ITERS> &r, const uint8_t *__res
     for (int it = 0; it < ITERS; ++it) {
         int b = it * 16 + j;
         b = b < nb ? b : nb - 1;
-        r.w[it] = qs[base + b];
+        r.w[it] = load_stream16(qs + base + b);
         r.d[it] = ODD ? (uint32_t)dh[base + b] : dw[(base + b) >> 1];
     }
 }
@@ -727,7 +727,7 @@ __global__ __launch_bounds__(64 * S) void gemv_q4_0_relay_kernel(const uint8_t *
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) {
             const uint8_t *w = m ? w1 : w0;
-            wr[m][k] = reinterpret_cast<const uint4 *>(w)[base + b];
+            wr[m][k] = load_stream16(reinterpret_cast<const uint4 *>(w) + base + b);
             dr[m][k] = reinterpret_cast<const uint32_t *>(w + nblk * 16)[(base + b) >> 1];
         }
     }
@@ -855,7 +855,7 @@ __global__ __launch_bounds__(64 * (S + 1)) void gemv_q4_0_long_kernel(const uint
         int it = sw + S * k;
         it = it < ITERS ? it : ITERS - 1;
         const int b = it * 16 + j;
-        wq[k] = qs[base + b];
+        wq[k] = load_stream16(qs + base + b);
         wd[k] = dw[(base + b) >> 1];
     }
     __syncthreads();

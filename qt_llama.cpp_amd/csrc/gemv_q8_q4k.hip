@@ -58,8 +58,8 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q8_0_kernel(const uint8
     for (int it = 0; it < ITERS; ++it) {
         int b = it * 16 + j;
         b = b < nb ? b : nb - 1;
-        w0[it] = qs[2 * (base + b)];
-        w1[it] = qs[2 * (base + b) + 1];
+        w0[it] = load_stream16(qs + 2 * (base + b));
+        w1[it] = load_stream16(qs + 2 * (base + b) + 1);
         d[it] = ODD ? (uint32_t)dp[base + b] : dw[(base + b) >> 1];
     }
     __syncthreads();
@@ -144,7 +144,7 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_k_kernel(const uint8
     for (int it = 0; it < ITERS; ++it) {
         int b = it * 16 + j;
         b = b < nb ? b : nb - 1;
-        q[it] = qs[base + b];
+        q[it] = load_stream16(qs + base + b);
         hw[it] = hp[(hbase + (b >> 3)) * 4 + (j & 3)];
     }
     __syncthreads();
