@@ -378,14 +378,17 @@ int mrml_hip_rope_kv_append_f16(mrml_hip_ctx *ctx, float *d_qkv, uint16_t *d_k_c
  * min(n_past+1, capacity) cache rows, kv head h / (n_heads / n_kv_heads),
  * in the CPU path's operation order (sequential dots, softmax sum and
  * weighted sum; the host C library's expf).  head_dim 256, group of at most
- * 8, capacity at most 6144.  d_out (f32) and d_pack (Q8_0 pack of the
- * n_heads*head_dim output) nullable, not both. */
+ * 8, capacity at most 131072: past 6144 the window's exps are summed in
+ * LDS-staged chunks, each chunk's exact sequential sum continuing the
+ * running sum (the same bits; the reference streams such windows through
+ * its online-softmax kernel, kernels.rs:1463-1561).  d_out (f32) and d_pack
+ * (Q8_0 pack of the n_heads*head_dim output) nullable, not both. */
 int mrml_hip_attn_decode_f16(mrml_hip_ctx *ctx, const float *d_q, const uint16_t *d_k_cache,
                              const uint16_t *d_v_cache, float *d_out, void *d_pack, int32_t n_past,
                              const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                              float scale, int32_t capacity);
 
-/* The same attention split over tiles of 64 positions of the window (flash
+/* The same attention split over tiles of 32 positions of the window (flash
  * decoding: per tile and head the max, the exp sum and the weighted values
  * in f32 tree order, then a merge in tile order): the FAST numerics of the
  * token step (MRML_HIP_NUMERICS_FAST).  Within 1e-5 of the CPU path relative

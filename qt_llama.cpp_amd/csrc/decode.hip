@@ -521,7 +521,7 @@ __global__ __launch_bounds__(kScoreT) void attn_scores2_kernel(const float *__re
 // positions per 16-byte read, one tile behind the producers (one barrier per
 // tile, products double-buffered).
 // Writes out (nullable) and the Q8_0 pack of the n_heads*head_dim output
-// (nullable).  Dynamic LDS: capacity floats plus 4.
+// (nullable).  Dynamic LDS: capacity floats plus 4 (sv_lds).
 constexpr int kSVD = 32;  // dims per workgroup
 constexpr int kSVW = 8;   // waves: wave 0 adds; waves 1-3 and 5-7 produce; wave 4, which shares wave 0's SIMD, idles
 constexpr int kSVT = 96;  // positions per tile: 48 position pairs x 8 dim quads = one per producer thread
@@ -552,12 +552,36 @@ __device__ __forceinline__ void sv_tile_load(u32x2 (&r)[kSVR], const uint16_t *v
     }
 }
 
-__device__ __forceinline__ void sv_products(const u32x2 (&r)[kSVR], const float *e_s, float (*prod)[kSVS], int t,
-                                            int window, int pt)
+// Softmax weights of the producer's two positions: from the normalised
+// window in LDS, or (LONG, windows too long for LDS) formed again from the
+// global scores exactly as the LDS form forms them, expf(s - max) times
+// 1/sum when sum > 0.  Positions past the window take a clamped in-window
+// score (their products are zeroed).
+struct SvWeights {
+    const float *sc;  // the head's scores (LONG)
+    float mx, inv;
+    bool scaled, fused_exp;
+    const uint64_t *exp_tab;
+};
+
+template <bool LONG>
+__device__ __forceinline__ void sv_products(const u32x2 (&r)[kSVR], const float *e_s, const SvWeights &sw,
+                                            float (*prod)[kSVS], int t, int window, int pt)
 {
     const int tq = pt >> 3, dq = pt & 7, pos0 = t * kSVT + kSVR * tq;
-    const float2 pw = reinterpret_cast<const float2 *>(e_s)[(pos0 < window ? pos0 : 0) >> 1];
-    const float w4[kSVR] = {pw.x, pw.y};
+    float w4[kSVR];
+    if (LONG) {
+#pragma unroll
+        for (int i = 0; i < kSVR; ++i) {
+            const int p = pos0 + i < window ? pos0 + i : window - 1;
+            const float e = mrml_libm::expf_t(sw.sc[p] - sw.mx, sw.fused_exp, sw.exp_tab);
+            w4[i] = sw.scaled ? e * sw.inv : e;
+        }
+    } else {
+        const float2 pw = reinterpret_cast<const float2 *>(e_s)[(pos0 < window ? pos0 : 0) >> 1];
+        w4[0] = pw.x;
+        w4[1] = pw.y;
+    }
     float pv[4][kSVR];  // [dim][position]
 #pragma unroll
     for (int i = 0; i < kSVR; ++i) {
@@ -573,6 +597,24 @@ __device__ __forceinline__ void sv_products(const u32x2 (&r)[kSVR], const float 
         *reinterpret_cast<float2 *>(&prod[4 * dq + d][kSVR * tq]) = make_float2(pv[d][0], pv[d][1]);
 }
 
+// LONG (capacities past kSVShortCap): the window's weights do not fit in
+// LDS.  The sum then runs over chunks of kSVChunk - 1 exps staged in LDS,
+// each chunk's exact sequential sum started from the running sum (prepended
+// as the chunk's first term: s = 0 + s_prev is exact, so the chunked sums
+// equal the one sequential loop), and the producers form their weights from
+// the global scores.  Dynamic LDS: kSVChunk floats, kSVChunk flag bytes and
+// the block sum's Shared.
+constexpr int kSVShortCap = 6144;  // the LDS form keeps capacity floats of weights
+constexpr int kSVChunk = 8192;     // LONG: terms per exact block sum (16 per thread)
+static_assert(kSVChunk <= mrml_xsum::kMaxPerThread * 64 * kSVW, "one block sum per chunk");
+
+__host__ __device__ constexpr bool sv_long(int capacity) { return capacity > kSVShortCap; }
+inline size_t sv_lds(int capacity)
+{
+    return sv_long(capacity) ? (size_t)kSVChunk * 5 + sizeof(mrml_xsum::Shared) : (size_t)capacity * sizeof(float) + 16;
+}
+
+template <bool LONG>
 __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *__restrict__ scores,
                                                              const uint16_t *__restrict__ v_cache,
                                                              const int32_t *__restrict__ d_pos, int n_past_arg,
@@ -620,17 +662,19 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
     // positions its exps stay in registers for the sum.
     constexpr int kSVE = 4 * 64 * kSVW;  // positions per pass
     const float4 *sc4 = reinterpret_cast<const float4 *>(sc);
+    const bool sc_a16 = (reinterpret_cast<uintptr_t>(sc) & 15) == 0;  // a capacity not a multiple of 4: scalar loads
     float4 sv = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
     float mx = -INFINITY;
     for (int p0 = 0; p0 < window; p0 += kSVE) {
         const int p = p0 + 4 * tid;
         float4 v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-        if (p + 3 < window) {
+        if (sc_a16 && p + 3 < window) {
             v = sc4[p >> 2];
         } else if (p < window) {
             v.x = sc[p];
             if (p + 1 < window) v.y = sc[p + 1];
             if (p + 2 < window) v.z = sc[p + 2];
+            if (p + 3 < window) v.w = sc[p + 3];
         }
         if (p0 == 0) sv = v;
         mx = fmaxf(mx, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
@@ -651,7 +695,8 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
         if (p + 1 < window) e.y = mrml_libm::expf_t(sv.y - mx, fused_exp, exp_tab);
         if (p + 2 < window) e.z = mrml_libm::expf_t(sv.z - mx, fused_exp, exp_tab);
         if (p + 3 < window) e.w = mrml_libm::expf_t(sv.w - mx, fused_exp, exp_tab);
-        if (p + 3 < window) {
+        if (LONG) {
+        } else if (p + 3 < window) {
             reinterpret_cast<float4 *>(e_s)[tid] = e;
         } else if (p < window) {
             e_s[p] = e.x;
@@ -659,6 +704,18 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
             if (p + 2 < window) e_s[p + 2] = e.z;
         }
         sum = mrml_xsum::block_seq_sum_nonneg4(e, window, *sum_x);
+    } else if (LONG) {
+        uint8_t *flags = reinterpret_cast<uint8_t *>(e_s + kSVChunk);
+        mrml_xsum::Shared &xs = *reinterpret_cast<mrml_xsum::Shared *>(flags + kSVChunk);
+        float s = 0.0f;
+        for (int c0 = 0; c0 < window; c0 += kSVChunk - 1) {
+            const int n = window - c0 < kSVChunk - 1 ? window - c0 : kSVChunk - 1;
+            if (tid == 0) e_s[0] = s;
+            for (int i = tid; i < n; i += 64 * kSVW) e_s[1 + i] = mrml_libm::expf_t(sc[c0 + i] - mx, fused_exp, exp_tab);
+            __syncthreads();
+            s = mrml_xsum::block_seq_sum_nonneg(e_s, n + 1, flags, xs);  // ends with a barrier
+        }
+        sum = s;
     } else {
         for (int p = tid; p < window; p += 64 * kSVW) e_s[p] = mrml_libm::expf_t(sc[p] - mx, fused_exp, exp_tab);
         __syncthreads();
@@ -670,9 +727,9 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
         __syncthreads();
         sum = *bcast;
     }
-    if (sum > 0.0f) {
-        const float inv = 1.0f / sum;
-        for (int p = tid; p < window; p += 64 * kSVW) e_s[p] = e_s[p] * inv;
+    const SvWeights sw{sc, mx, sum > 0.0f ? 1.0f / sum : 1.0f, sum > 0.0f, fused_exp, exp_tab};
+    if (!LONG && sum > 0.0f) {
+        for (int p = tid; p < window; p += 64 * kSVW) e_s[p] = e_s[p] * sw.inv;
     }
     __syncthreads();
 
@@ -699,7 +756,7 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
     // buffer (t+1)&1 was last read by wave 0 in tile t-1, before barrier t
     auto tile = [&](int t, int k) {  // k = t % 4, a compile-time slot
         if (producer) {
-            sv_products(vt[k], e_s, prod[t & 1], t, window, pt);
+            sv_products<LONG>(vt[k], e_s, sw, prod[t & 1], t, window, pt);
             if (t + 4 < ntiles) {
                 ring[k] = ring_next(ring_next(ring_next(ring_next(ring[k]))));
                 sv_tile_load(vt[k], vslice, t + 4, window, ring[k], capacity, kv_dim, pt);
@@ -911,38 +968,68 @@ __global__ __launch_bounds__(kAttnHD) void attn_combine_kernel(const float *__re
                                                                int capacity, int max_tiles, int n_heads,
                                                                float *__restrict__ out, uint8_t *__restrict__ pack)
 {
-    constexpr int HD = kAttnHD, kMaxTiles = (6144 + kSplitP - 1) / kSplitP;
+    constexpr int HD = kAttnHD, kMaxTiles = (kSVShortCap + kSplitP - 1) / kSplitP;
     __shared__ float m_s[kMaxTiles], w_s[kMaxTiles], l_s[kMaxTiles];
+    __shared__ float red[HD / 64];
     int window, start;
     attn_window(d_pos, n_past_arg, capacity, window, start);
     const int ntiles = (window + kSplitP - 1) / kSplitP, h = blockIdx.x, d = threadIdx.x;
     const float *ph = part + (size_t)h * max_tiles * kSplitPart;
-    // the tiles' (m, l) in parallel, one tile per thread
-    for (int t = d; t < ntiles; t += HD) {
-        m_s[t] = ph[(size_t)t * kSplitPart + HD];
-        l_s[t] = ph[(size_t)t * kSplitPart + HD + 1];
-    }
-    __syncthreads();
-    float M = -INFINITY;
-    for (int t = 0; t < ntiles; ++t) M = fmaxf(M, m_s[t]);
-    for (int t = d; t < ntiles; t += HD) w_s[t] = __builtin_expf(m_s[t] - M);
-    __syncthreads();
-    // L and o in tile order (every thread forms the same L)
     float L = 0.0f, o = 0.0f;
-    int t = 0;
-    for (; t + 8 <= ntiles; t += 8) {
-        float v[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = ph[(size_t)(t + k) * kSplitPart + d];  // eight loads in flight
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            L = L + l_s[t + k] * w_s[t + k];
-            o = o + v[k] * w_s[t + k];
+    if (ntiles <= kMaxTiles) {
+        // the tiles' (m, l) in parallel, one tile per thread
+        for (int t = d; t < ntiles; t += HD) {
+            m_s[t] = ph[(size_t)t * kSplitPart + HD];
+            l_s[t] = ph[(size_t)t * kSplitPart + HD + 1];
         }
-    }
-    for (; t < ntiles; ++t) {
-        L = L + l_s[t] * w_s[t];
-        o = o + ph[(size_t)t * kSplitPart + d] * w_s[t];
+        __syncthreads();
+        float M = -INFINITY;
+        for (int t = 0; t < ntiles; ++t) M = fmaxf(M, m_s[t]);
+        for (int t = d; t < ntiles; t += HD) w_s[t] = __builtin_expf(m_s[t] - M);
+        __syncthreads();
+        // L and o in tile order (every thread forms the same L)
+        int t = 0;
+        for (; t + 8 <= ntiles; t += 8) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = ph[(size_t)(t + k) * kSplitPart + d];  // eight loads in flight
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                L = L + l_s[t + k] * w_s[t + k];
+                o = o + v[k] * w_s[t + k];
+            }
+        }
+        for (; t < ntiles; ++t) {
+            L = L + l_s[t] * w_s[t];
+            o = o + ph[(size_t)t * kSplitPart + d] * w_s[t];
+        }
+    } else {
+        // windows past the LDS arrays: the same values in the same order, each
+        // tile's (m, l) read where it lies and its weight formed per thread
+        float M = -INFINITY;
+        for (int t = d; t < ntiles; t += HD) M = fmaxf(M, ph[(size_t)t * kSplitPart + HD]);
+        M = wave_max_f32(M);
+        if ((d & 63) == 0) red[d >> 6] = M;
+        __syncthreads();
+        M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        for (int t = 0; t < ntiles; t += 8) {
+            float v[8], mt[8], lt[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const size_t at = (size_t)(t + k < ntiles ? t + k : t) * kSplitPart;
+                v[k] = ph[at + d];
+                mt[k] = ph[at + HD];
+                lt[k] = ph[at + HD + 1];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if (t + k < ntiles) {
+                    const float w = __builtin_expf(mt[k] - M);
+                    L = L + lt[k] * w;
+                    o = o + v[k] * w;
+                }
+            }
+        }
     }
     const float v = o / L;
     const int idx = h * HD + d;
@@ -1099,16 +1186,22 @@ int launch_rope_kv_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache, uint16_
 }
 
 int attn_head_dim() { return kAttnHD; }
-int attn_max_capacity() { return 6144; }  // the window's softmax weights (24 KB) share LDS with the products and the sum
+int attn_max_capacity() { return 131072; }  // 2^17 positions, the Gemma family's longest context
 
 size_t attn_scratch_bytes(int n_heads, int capacity) { return (size_t)n_heads * capacity * sizeof(float); }
 
+// Softmax and weighted values of `rows` query rows (grid z), the LDS or the
+// LONG form by capacity.
 static int launch_softmax_v(mrml_hip_ctx *ctx, const float *scores, const uint16_t *v_cache, float *out, void *pack,
-                            const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads, int capacity)
+                            const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads, int capacity, int rows = 1)
 {
-    hipLaunchKernelGGL(attn_softmax_v_kernel, dim3(n_heads, kAttnHD / kSVD), dim3(64 * kSVW), (size_t)capacity * sizeof(float) + 16,
-                       ctx->stream, scores, v_cache, d_pos, n_past, n_heads, n_kv_heads, capacity,
-                       (int)host_expf_fused(), out, (uint8_t *)pack);
+    const dim3 grid(n_heads, kAttnHD / kSVD, rows), block(64 * kSVW);
+    if (sv_long(capacity))
+        hipLaunchKernelGGL(attn_softmax_v_kernel<true>, grid, block, sv_lds(capacity), ctx->stream, scores, v_cache,
+                           d_pos, n_past, n_heads, n_kv_heads, capacity, (int)host_expf_fused(), out, (uint8_t *)pack);
+    else
+        hipLaunchKernelGGL(attn_softmax_v_kernel<false>, grid, block, sv_lds(capacity), ctx->stream, scores, v_cache,
+                           d_pos, n_past, n_heads, n_kv_heads, capacity, (int)host_expf_fused(), out, (uint8_t *)pack);
     return check_launch(ctx, "attn_softmax_v_kernel");
 }
 
@@ -1123,15 +1216,12 @@ int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_
                            const_cast<uint16_t *>(k_cache), (uint16_t *)nullptr, d_pos, n_past, n_heads, n_kv_heads,
                            scale, capacity, (const float *)nullptr, 0, 0.0f, 0.0f, scores);
         if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
-        return launch_softmax_v(ctx, scores, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, capacity);
+    } else {
+        hipLaunchKernelGGL(attn_scores_kernel, sgrid, dim3(64 * (n_heads / n_kv_heads)), 0, ctx->stream, q, k_cache,
+                           d_pos, n_past, n_heads, n_kv_heads, scale, capacity, scores);
+        if (int rc = check_launch(ctx, "attn_scores_kernel")) return rc;
     }
-    hipLaunchKernelGGL(attn_scores_kernel, sgrid, dim3(64 * (n_heads / n_kv_heads)), 0, ctx->stream, q, k_cache,
-                       d_pos, n_past, n_heads, n_kv_heads, scale, capacity, scores);
-    if (int rc = check_launch(ctx, "attn_scores_kernel")) return rc;
-    hipLaunchKernelGGL(attn_softmax_v_kernel, dim3(n_heads, kAttnHD / kSVD), dim3(64 * kSVW), (size_t)capacity * sizeof(float) + 16,
-                       ctx->stream, scores, v_cache, d_pos, n_past, n_heads, n_kv_heads, capacity,
-                       (int)host_expf_fused(), out, (uint8_t *)pack);
-    return check_launch(ctx, "attn_softmax_v_kernel");
+    return launch_softmax_v(ctx, scores, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, capacity);
 }
 
 // Attention of `rows` queries at consecutive positions n_past0, n_past0+1, ...
@@ -1145,15 +1235,14 @@ int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *qkv, const uint16_t *k_
                          void *scratch)
 {
     float *scores = reinterpret_cast<float *>(scratch);
-    const dim3 sgrid((capacity + kScoreP - 1) / kScoreP, n_kv_heads, rows);
+    // score tiles up to the last row's window (the host knows every row's position)
+    const int span = std::min(capacity, n_past0 + rows);
+    const dim3 sgrid((span + kScoreP - 1) / kScoreP, n_kv_heads, rows);
     hipLaunchKernelGGL(attn_scores2_kernel<false>, sgrid, dim3(kScoreT), 0, ctx->stream, qkv,
                        const_cast<uint16_t *>(k_cache), (uint16_t *)nullptr, (const int32_t *)nullptr, n_past0,
                        n_heads, n_kv_heads, scale, capacity, (const float *)nullptr, 0, 0.0f, 0.0f, scores);
     if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
-    hipLaunchKernelGGL(attn_softmax_v_kernel, dim3(n_heads, kAttnHD / kSVD, rows), dim3(64 * kSVW),
-                       (size_t)capacity * sizeof(float) + 16, ctx->stream, scores, v_cache, (const int32_t *)nullptr,
-                       n_past0, n_heads, n_kv_heads, capacity, (int)host_expf_fused(), out, (uint8_t *)nullptr);
-    return check_launch(ctx, "attn_softmax_v_kernel");
+    return launch_softmax_v(ctx, scores, v_cache, out, nullptr, nullptr, n_past0, n_heads, n_kv_heads, capacity, rows);
 }
 
 // The decode step's attention with RoPE and the K/V append in the scores

@@ -382,6 +382,15 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
 namespace {
 
 constexpr int kPrefillChunk = 128;  // tokens per chunk (prefill_cuda's tile, model.rs:2395-2638)
+constexpr size_t kPrefillScoreBytes = 64u << 20;  // scores of the chunk's attention rows held at once
+
+// Attention rows per launch in a prefill chunk: the whole chunk unless its
+// scores (n_heads * capacity floats a row) would pass kPrefillScoreBytes.
+inline int prefill_attn_rows(const mrml_hip_gemma2_config &c)
+{
+    const size_t per = attn_scratch_bytes(c.n_heads, c.ctx_len);
+    return (int)std::max<size_t>(1, std::min<size_t>(kPrefillChunk, kPrefillScoreBytes / per));
+}
 
 int prefill_buffers(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m)
 {
@@ -399,7 +408,7 @@ int prefill_buffers(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m)
                  o_attn = take(M * qd * 4), o_o = take(M * c.dim * 4), o_g = take(M * c.ffn_dim * 4),
                  o_u = take(M * c.ffn_dim * 4), o_act = take(M * c.ffn_dim * 4), o_f = take(M * c.dim * 4),
                  o_gp = take(gemm_pack_bytes((int32_t)widest, (int32_t)M)),
-                 o_sc = take(M * attn_scratch_bytes(c.n_heads, c.ctx_len));
+                 o_sc = take((size_t)prefill_attn_rows(c) * attn_scratch_bytes(c.n_heads, c.ctx_len));
     hipError_t e = hipMalloc(&m->pf_arena, off);
     if (e != hipSuccess) {
         m->pf_arena = nullptr;
@@ -467,8 +476,10 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
             STEP(launch_rope_kv_f16(ctx, m->pf_qkv, kc, vc, nullptr, p0, c.n_heads, c.n_kv_heads, c.head_dim,
                                     c.rope_base, 1.0f, c.ctx_len, m->rope_table, c.ctx_len, n));
             if (attn_rope_ok(c.n_heads, c.n_kv_heads)) {
-                STEP(launch_attn_rows_f16(ctx, m->pf_qkv, kc, vc, m->pf_attn, p0, n, c.n_heads, c.n_kv_heads,
-                                          c.attn_scale, c.ctx_len, m->pf_scores));
+                for (int r0 = 0, rn = prefill_attn_rows(c); r0 < n; r0 += rn)
+                    STEP(launch_attn_rows_f16(ctx, m->pf_qkv + (size_t)r0 * qkvd, kc, vc, m->pf_attn + (size_t)r0 * qd,
+                                              p0 + r0, std::min(rn, n - r0), c.n_heads, c.n_kv_heads, c.attn_scale,
+                                              c.ctx_len, m->pf_scores));
             } else {
                 for (int i = 0; i < n; ++i)
                     STEP(launch_attn_decode_f16(ctx, m->pf_qkv + (size_t)i * qkvd, kc, vc,
