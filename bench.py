@@ -221,8 +221,8 @@ def decode_fast_bench(be, synth, dev, ev, n_prefill: int, n_decode: int, exact_h
             "prefill_ms_per_token": round(t_pre / n_prefill * 1e3, 4),
             "prompt_picks_equal_to_exact": f"{same_prompt}/{n_prefill}",
             "decode_tokens_equal_to_exact_until": int(dec_same[0]) if dec_same.size else n_decode,
-            "numerics": "FAST: tree-order RMSNorm sums, split-K (flash-decoding) attention; matvecs bit-exact "
-                        "given their inputs"}
+            "numerics": "FAST: tree-order RMSNorm sums, split-K (flash-decoding) attention, tree-order row sums "
+                        "in the output and down projections; the other matvecs bit-exact given their inputs"}
 
 
 def decode_bench(be, synth, dev, ev, n_prefill: int, n_decode: int, cpu_steps: int) -> tuple[dict, dict | None]:

@@ -161,6 +161,15 @@ int mrml_hip_gemv_q4_0(mrml_hip_ctx *ctx, const void *d_w, const float *d_x, flo
  * activation pack from mrml_hip_quantize_q8_0. */
 int mrml_hip_gemv_q4_0_q8(mrml_hip_ctx *ctx, const void *d_w, const void *d_xpack, float *d_y,
                           int32_t rows, int32_t cols);
+/* mrml_hip_gemv_q4_0_q8 on the tolerance path: the same integer block dots
+ * and block terms, each row's f32 sum added in tree order (lane sums, then
+ * a wave butterfly) instead of block order, nine rows a workgroup -- the
+ * token step's output and down projections under MRML_HIP_NUMERICS_FAST.
+ * Outputs within 1e-5 of the exact product relative to the largest output.
+ * Block counts that are neither a multiple of 64 nor above 256, or above
+ * 320, run the exact kernels.  No counterpart in the reference. */
+int mrml_hip_gemv_q4_0_q8_relaxed(mrml_hip_ctx *ctx, const void *d_w, const void *d_xpack, float *d_y,
+                                  int32_t rows, int32_t cols);
 /* As mrml_hip_gemv_q4_0 on raw GGUF Q4_0 bytes (no repack needed). */
 int mrml_hip_gemv_q4_0_gguf(mrml_hip_ctx *ctx, const void *d_w_gguf, const float *d_x,
                             float *d_y, int32_t rows, int32_t cols);
@@ -403,10 +412,12 @@ int mrml_hip_attn_decode_f16_split(mrml_hip_ctx *ctx, const float *d_q, const ui
  * and greedy selection, model.rs:2833-2907) ----------------------------------- */
 /* Numerics of the token step.  EXACT (0, the default): every op in the CPU
  * path's operation order, logits bit-identical to the reference CPU step.
- * FAST: the matvecs stay bit-exact given their inputs, but the residual
- * RMSNorm sums are deterministic tree sums and decode attention is split
- * over tiles of the window (flash decoding) with tree-order softmax and
- * value sums; each such op is within 1e-5 of the CPU path relative to its
+ * FAST: the residual RMSNorm sums are deterministic tree sums, decode
+ * attention is split over tiles of the window (flash decoding) with
+ * tree-order softmax and value sums, and the output and down projections
+ * add each row in tree order (mrml_hip_gemv_q4_0_q8_relaxed); the other
+ * matvecs stay bit-exact given their inputs.  Each changed op is within
+ * 1e-5 of the CPU path relative to its
  * output's largest magnitude, and greedy tokens are checked against the
  * reference CPU step (north_star: <= 1e-5 max-rel, identical greedy tokens). */
 enum { MRML_HIP_NUMERICS_EXACT = 0, MRML_HIP_NUMERICS_FAST = 1 };

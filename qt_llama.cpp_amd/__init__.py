@@ -142,6 +142,7 @@ _SIGNATURES = {
     "mrml_hip_q8_0_pack_bytes": [_I],
     "mrml_hip_gemv_q4_0": [_P, _P, _P, _P, _I, _I],
     "mrml_hip_gemv_q4_0_q8": [_P, _P, _P, _P, _I, _I],
+"mrml_hip_gemv_q4_0_q8_relaxed": [_P, _P, _P, _P, _I, _I],
     "mrml_hip_gemv_q4_0_gguf": [_P, _P, _P, _P, _I, _I],
     "mrml_hip_gemv_q4_0_geglu": [_P, _P, _P, _P, _P, _I, _I],
     "mrml_hip_gemv_q4_0_qkv": [_P, _P, _P, _P, _P, _P, _I, _I, _I],
@@ -397,6 +398,10 @@ class HipDevice:
 
     def gemv_q4_0_q8(self, w, xpack, y, rows: int, cols: int) -> None:
         self._check(self.lib.mrml_hip_gemv_q4_0_q8(self.ctx, _ptr(w), _ptr(xpack), _ptr(y), rows, cols))
+
+    def gemv_q4_0_q8_relaxed(self, w, xpack, y, rows: int, cols: int) -> None:
+        """The tolerance path's matvec (tree-order row sums; mrml_hip_gemv_q4_0_q8_relaxed)."""
+        self._check(self.lib.mrml_hip_gemv_q4_0_q8_relaxed(self.ctx, _ptr(w), _ptr(xpack), _ptr(y), rows, cols))
 
     def gemm_q4_0(self, w, x, y, rows: int, cols: int, batch: int) -> None:
         self._check(self.lib.mrml_hip_gemm_q4_0(self.ctx, _ptr(w), _ptr(x), _ptr(y), rows, cols, batch))

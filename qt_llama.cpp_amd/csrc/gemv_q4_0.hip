@@ -878,6 +878,65 @@ __global__ __launch_bounds__(64 * (S + 1)) void gemv_q4_0_long_kernel(const uint
     }
 }
 
+// ---- relaxed rows: the tolerance path's matvec -----------------------------------
+// kRelaxR rows per workgroup, one wave per row (lane l: blocks l, l+64, ...),
+// wave 0 staging the pack.  Every integer block dot and every block term is
+// the exact kernels' own; each lane adds its terms and the wave adds the
+// lanes' sums in a butterfly, so only the order of the f32 additions differs
+// from the block-ordered fold (outputs within a few ulps of it; the tests
+// bound them at 1e-5 relative to the largest output).  Nine rows a
+// workgroup put the 2304 rows of Gemma-2's output and down projections on
+// exactly 256 workgroups, one per CU, where the exact long-row kernel needs
+// 576 small ones to hide its ordered fold.  ODD: the scale plane holds an
+// odd number of f16 scales and is read with 2-byte loads.
+constexpr int kRelaxR = 9;
+
+template <int K, bool ODD>
+__global__ __launch_bounds__(64 * (kRelaxR + 1)) void gemv_q4_0_relaxed_kernel(const uint8_t *__restrict__ w,
+                                                                               const uint8_t *xpack,
+                                                                               float *__restrict__ y, int rows, int nb)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (wave == 0) {
+        stage_split_pack<true>(xpack, lds, nb);
+        __syncthreads();
+        return;
+    }
+    const int row_raw = blockIdx.x * kRelaxR + wave - 1;
+    const int row = row_raw < rows ? row_raw : rows - 1;  // tail rows recompute the last row
+    const size_t nblk = (size_t)rows * nb, base = (size_t)row * nb;
+    const uint4 *qs = reinterpret_cast<const uint4 *>(w);
+    const uint32_t *dw = reinterpret_cast<const uint32_t *>(w + nblk * 16);
+    const uint16_t *dh = reinterpret_cast<const uint16_t *>(w + nblk * 16);
+    uint4 wq[K];
+    uint32_t wd[K];
+    __builtin_amdgcn_s_barrier();  // the pack's loads are issued
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        int b = 64 * k + lane;
+        b = b < nb ? b : nb - 1;
+        wq[k] = load_stream16(qs + base + b);
+        wd[k] = ODD ? (uint32_t)dh[base + b] : dw[(base + b) >> 1];
+    }
+    __syncthreads();
+    const uint4 *aq = reinterpret_cast<const uint4 *>(lds);
+    const float *ad = reinterpret_cast<const float *>(lds + nb * 32);
+    const int32_t *ac = reinterpret_cast<const int32_t *>(lds + nb * 36);
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int bt = 64 * k + lane, b = bt < nb ? bt : nb - 1;
+        const uint4 q = wq[k], lo = aq[2 * b], hi = aq[2 * b + 1];
+        const int32_t isum = q4_0_isum_split(q.x, q.y, q.z, q.w, lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w, ac[b]);
+        const uint32_t dbits = (!ODD && ((base + b) & 1)) ? wd[k] >> 16 : wd[k] & 0xffffu;
+        const float tv = (float)isum * (f16_bits_to_f32(dbits) * ad[b]);
+        s += bt < nb ? tv : 0.0f;
+    }
+    s = mrml_xsum::wave_sum_f32(s);
+    if (lane == 0 && row_raw < rows) y[row_raw] = s;
+}
+
 // ---- runtime block count (fold16) -----------------------------------------------
 
 template <int ITERS, int WAVES, bool ODD = false>
@@ -1126,9 +1185,44 @@ static int geglu_odd(mrml_hip_ctx *ctx, const void *wg, const void *wu, const vo
     return launch_geglu_rows(ctx, gu, gu + rows, act, rows);
 }
 
-int launch_gemv_q4_0(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows, int32_t cols)
+// The relaxed rows kernel where its 64-block groups are nearly full (block
+// counts that are multiples of 64, or above 256); other shapes keep the
+// exact kernels, which meet the tolerance trivially.
+static bool relaxed_rows_shape(int nb) { return nb <= kStageMax && (nb % 64 == 0 || nb > 256); }
+
+static int launch_gemv_q4_0_relaxed(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows,
+                                    int nb)
+{
+    const dim3 grid((rows + kRelaxR - 1) / kRelaxR), block(64 * (kRelaxR + 1));
+    const int groups = (nb + 63) / 64;
+    const bool odd = odd_blocks(rows, nb);
+#define MRML_RELAXED_K(KK)                                                                                       \
+    case KK:                                                                                                     \
+        if (odd)                                                                                                 \
+            hipLaunchKernelGGL((gemv_q4_0_relaxed_kernel<KK, true>), grid, block, pack_lds(nb), ctx->stream,     \
+                               (const uint8_t *)w, (const uint8_t *)xpack, y, rows, nb);                         \
+        else                                                                                                     \
+            hipLaunchKernelGGL((gemv_q4_0_relaxed_kernel<KK, false>), grid, block, pack_lds(nb), ctx->stream,    \
+                               (const uint8_t *)w, (const uint8_t *)xpack, y, rows, nb);                         \
+        break;
+    switch (groups) {
+        MRML_RELAXED_K(1)
+        MRML_RELAXED_K(2)
+        MRML_RELAXED_K(3)
+        MRML_RELAXED_K(4)
+        MRML_RELAXED_K(5)
+        default:
+            return fail(ctx, MRML_HIP_E_UNSUPPORTED, "relaxed q4_0 matvec: %d blocks per row", nb);
+    }
+#undef MRML_RELAXED_K
+    return check_launch(ctx, "gemv_q4_0_relaxed_kernel");
+}
+
+int launch_gemv_q4_0(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows, int32_t cols,
+                     bool relaxed)
 {
     const int nb = cols / 32;
+    if (relaxed && relaxed_rows_shape(nb)) return launch_gemv_q4_0_relaxed(ctx, w, xpack, y, rows, nb);
     if (odd_blocks(rows, nb)) return launch_gemv_q4_0_odd(ctx, w, xpack, y, rows, nb);
     if (fold16_shape(nb)) {
         const dim3 grid(((rows + 3) / 4 + kFoldWaves - 1) / kFoldWaves);

@@ -43,8 +43,10 @@ int launch_zero(mrml_hip_ctx *ctx, void *dst, size_t bytes);
 int launch_copy(mrml_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
 
 // Q4_0 x Q8_0 matvec family; `xpack` is an activation pack for `cols`.
+// relaxed: the tolerance path's balanced rows kernel where it pays (the
+// f32 sum of a row in tree order, within 1e-5 of the block-ordered one)
 int launch_gemv_q4_0(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y,
-                     int32_t rows, int32_t cols);
+                     int32_t rows, int32_t cols, bool relaxed = false);
 int launch_gemv_q4_0_gguf(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y,
                           int32_t rows, int32_t cols);
 // f32-input forms: quantise x inside the kernel where a fixed instance exists.

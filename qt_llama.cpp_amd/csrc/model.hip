@@ -341,7 +341,7 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
             STEP(launch_attn_decode_f16(ctx, m->qkv, kc, vc, nullptr, m->attn_pack, d_pos, 0, c.n_heads,
                                         c.n_kv_heads, c.attn_scale, c.ctx_len, m->attn_part));
         }
-        STEP(launch_gemv_q4_0(ctx, L.wo, m->attn_pack, m->o, c.dim, qd));
+        STEP(launch_gemv_q4_0(ctx, L.wo, m->attn_pack, m->o, c.dim, qd, fast));
         if (fused) {
             STEP(launch_geglu_resnorm(ctx, L.w_gate, L.w_up, m->o, L.post_attn_norm, hA, hB, L.ffn_norm, c.eps,
                                       m->act_pack, c.ffn_dim, c.dim, fast));
@@ -351,7 +351,7 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
             STEP(launch_gemv_q4_0_geglu_emit(ctx, L.w_gate, L.w_up, m->xpack, m->act, m->act_pack, c.ffn_dim,
                                              c.dim));
         }
-        STEP(launch_gemv_q4_0(ctx, L.w_down, m->act_pack, m->f, c.dim, c.ffn_dim));
+        STEP(launch_gemv_q4_0(ctx, L.w_down, m->act_pack, m->f, c.dim, c.ffn_dim, fast));
         if (!fused)
             STEP(launch_residual_rms_norm(ctx, m->f, L.post_ffw_norm, hA, hA, next_norm, c.eps, nullptr, m->xpack,
                                           c.dim));

@@ -432,6 +432,14 @@ int mrml_hip_gemv_q4_0_q8(mrml_hip_ctx *ctx, const void *w, const void *xpack, f
     return launch_gemv_q4_0(ctx, w, xpack, y, rows, cols);
 }
 
+int mrml_hip_gemv_q4_0_q8_relaxed(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y, int32_t rows,
+                                  int32_t cols)
+{
+    CTX_GUARD(ctx);
+    CHECK_MATVEC(ctx, w, xpack, y, rows, cols, 32);
+    return launch_gemv_q4_0(ctx, w, xpack, y, rows, cols, true);
+}
+
 int mrml_hip_gemv_q4_0_gguf(mrml_hip_ctx *ctx, const void *w, const float *x, float *y, int32_t rows, int32_t cols)
 {
     CTX_GUARD(ctx);

@@ -158,6 +158,7 @@ api! {
     q8_0_pack_bytes: fn(i32) -> usize = "mrml_hip_q8_0_pack_bytes";
     gemv_q4_0: fn(Ctx, *const c_void, *const f32, *mut f32, i32, i32) -> c_int = "mrml_hip_gemv_q4_0";
     gemv_q4_0_q8: fn(Ctx, *const c_void, *const c_void, *mut f32, i32, i32) -> c_int = "mrml_hip_gemv_q4_0_q8";
+    gemv_q4_0_q8_relaxed: fn(Ctx, *const c_void, *const c_void, *mut f32, i32, i32) -> c_int = "mrml_hip_gemv_q4_0_q8_relaxed";
     gemv_q4_0_gguf: fn(Ctx, *const c_void, *const f32, *mut f32, i32, i32) -> c_int = "mrml_hip_gemv_q4_0_gguf";
     gemv_q4_0_geglu: fn(Ctx, *const c_void, *const c_void, *const f32, *mut f32, i32, i32) -> c_int = "mrml_hip_gemv_q4_0_geglu";
     ffn_geglu_q4_0: fn(Ctx, *const c_void, *const c_void, *const c_void, *const f32, *mut f32, *mut f32, i32, i32) -> c_int = "mrml_hip_ffn_geglu_q4_0";

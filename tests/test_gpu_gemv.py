@@ -117,6 +117,39 @@ def test_gemv_q4_0_prequantised_pack(backend, dev, orc, synth):
     assert_bit_exact(yb.numpy(), ref, "q4_0 from pack")
 
 
+# (rows, cols): the token step's output (2304x2048, 64 blocks) and down
+# (2304x9216, 288 blocks) projections, ragged row counts (partial last
+# workgroup of 9 rows), an odd scale plane (7 x 257 blocks), every group
+# count 1..5, and a shape that keeps the exact kernels (72 blocks)
+RELAXED_SHAPES = [(2304, 2048), (2304, 9216), (10, 2048), (2305, 9216), (7, 8224), (9, 4096), (17, 6144),
+                  (33, 8192), (100, 10240), (9216, 2304)]
+
+
+@pytest.mark.parametrize("rows,cols", RELAXED_SHAPES)
+def test_gemv_q4_0_relaxed_within_tolerance(backend, dev, orc, synth, rows, cols):
+    """The tolerance path's matvec: every output within 1e-5 of the CPU
+    path's block-ordered product relative to the largest output (the
+    north_star's matvec bar), and exact where the shape keeps the exact
+    kernels."""
+    rng = synth.rng_for(4100 + rows + cols)
+    w = synth.q4_0_matrix(rng, rows, cols)
+    x = synth.rms_normalised(synth.normal_vector(rng, cols))
+    ref = orc.mat_vec_mul_q4_0_q8_0(w, orc.quantize_q8_0(x), rows, cols, threads=THREADS)
+    wb = backend.HipBuffer.from_gguf(dev, w, backend.Q4_0, rows, cols)
+    xb = upload(backend, dev, x)
+    pk = backend.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(cols), np.uint8)
+    yb = backend.HipBuffer.alloc(dev, rows)
+    dev.quantize_q8_0(xb, None, pk, cols)
+    dev.gemv_q4_0_q8_relaxed(wb, pk, yb, rows, cols)
+    dev.sync()
+    got = yb.numpy()
+    err = float(np.max(np.abs(got.astype(np.float64) - ref)) / np.max(np.abs(ref)))
+    print(f"\n[relaxed q4_0] {rows}x{cols}: max-rel {err:.2e}", flush=True)
+    assert err <= 1e-5
+    if cols == 2304:
+        assert_bit_exact(got, ref, "relaxed entry on an exact-kernel shape")
+
+
 def test_gemv_q4_0_closed_forms(backend, dev, orc):
     """examples/cuda_prefill_primitives.rs:23-49 patterns on the GPU: 0x98 rows
     give +sum(x[16..32]), 0x87 rows give -sum(x[0..16]) (exact activations)."""
