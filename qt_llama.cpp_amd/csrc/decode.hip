@@ -977,6 +977,13 @@ __global__ __launch_bounds__(kAttnHD) void attn_combine_kernel(const float *__re
     const float *ph = part + (size_t)h * max_tiles * kSplitPart;
     float L = 0.0f, o = 0.0f;
     if (ntiles <= kMaxTiles) {
+        // the first kPre tiles' values are loaded with the tiles' (m, l), one
+        // round trip for windows up to kPre tiles (clamped loads: no branch
+        // delays their issue)
+        constexpr int kPre = 32;
+        float pv[kPre];
+#pragma unroll
+        for (int k = 0; k < kPre; ++k) pv[k] = ph[(size_t)(k < ntiles ? k : ntiles - 1) * kSplitPart + d];
         // the tiles' (m, l) in parallel, one tile per thread
         for (int t = d; t < ntiles; t += HD) {
             m_s[t] = ph[(size_t)t * kSplitPart + HD];
@@ -988,7 +995,14 @@ __global__ __launch_bounds__(kAttnHD) void attn_combine_kernel(const float *__re
         for (int t = d; t < ntiles; t += HD) w_s[t] = __builtin_expf(m_s[t] - M);
         __syncthreads();
         // L and o in tile order (every thread forms the same L)
-        int t = 0;
+#pragma unroll
+        for (int k = 0; k < kPre; ++k) {
+            if (k < ntiles) {  // uniform
+                L = L + l_s[k] * w_s[k];
+                o = o + pv[k] * w_s[k];
+            }
+        }
+        int t = kPre;
         for (; t + 8 <= ntiles; t += 8) {
             float v[8];
 #pragma unroll
