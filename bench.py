@@ -777,6 +777,14 @@ def main() -> int:
     # the step's second launch (activation pack in)
     st_down, gbs_down = rate(lambda i: dev.gemv_q4_0_q8(pool[i], a_pack, y, DIM, FFN), BYTES_DOWN, npool)
     k_geglu = st_geglu["median_s"]
+    # the tolerance path's FFN step (not the headline): the same GeGLU launch,
+    # then the down projection with tree-order row sums
+    # (mrml_hip_gemv_q4_0_q8_relaxed, within 1e-5 of the exact product)
+    st_down_r, gbs_down_r = rate(lambda i: dev.gemv_q4_0_q8_relaxed(pool[i], a_pack, y, DIM, FFN), BYTES_DOWN, npool)
+    g_fast = dev.capture(lambda: [(dev.gemv_q4_0_geglu_pack(s_["g"], s_["u"], bx, None, a_pack, FFN, DIM),
+                                   dev.gemv_q4_0_q8_relaxed(s_["d"], a_pack, y, DIM, FFN)) for s_ in rot])
+    st_fast = sample_launches(dev, ev, g_fast, len(rot))
+    g_fast.close()
     # stream-copy ceiling on a buffer well above the MALL
     cbytes = 1 << 30
     src, dst = be.HipBuffer(dev, cbytes), be.HipBuffer(dev, cbytes)
@@ -844,6 +852,13 @@ def main() -> int:
         "pct_of_hbm_peak": round(100 * value / PEAK_HBM_GBS, 2),
         "per_matrix_gbs": {"gate": round(gbs_gate, 1), "up": round(gbs_up, 1), "down": round(gbs_down, 1),
                            "fused_gate_up_geglu": round(gbs_geglu, 1)},
+        "ffn_tolerance_path": {"gb_s": round(BYTES_STEP / st_fast["median_s"] / 1e9, 1),
+                               "us_per_step": round(st_fast["median_s"] * 1e6, 3),
+                               "down_relaxed_us": round(st_down_r["median_s"] * 1e6, 3),
+                               "down_relaxed_gb_s": round(gbs_down_r, 1),
+                               "how": "GeGLU launch as in the headline, then mrml_hip_gemv_q4_0_q8_relaxed (tree-order "
+                                      "row sums, within 1e-5 of the exact product); graph replays over the weight sets; "
+                                      "not the headline, which stays bit-exact"},
         "per_kernel_us": {k_: {"median": round(v_["median_s"] * 1e6, 3), "min": round(v_["min_s"] * 1e6, 3),
                                "launches_per_sample": v_["launches_per_sample"]}
                           for k_, v_ in (("geglu", st_geglu), ("gate", st_gate), ("up", st_up), ("down", st_down))},

@@ -80,13 +80,6 @@ __device__ __forceinline__ float dpp_ror1(float v)
         float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xf, 0xf, false));
 }
 
-// Value of lane (i-1) mod 64 across the whole wave (wave_ror:1).
-__device__ __forceinline__ float dpp_wave_ror1(float v)
-{
-    return __builtin_bit_cast(
-        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x13C, 0xf, 0xf, false));
-}
-
 // Ordered fold step across the 16 lanes of a DPP row: lane j receives the
 // running sum of lane j-1 and adds its own term.  Applied once per
 // "iteration" of 16 consecutive blocks, lane 15 ends up holding
