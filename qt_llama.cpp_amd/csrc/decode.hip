@@ -971,23 +971,27 @@ __global__ __launch_bounds__(kAttnHD) void attn_combine_kernel(const float *__re
     constexpr int HD = kAttnHD, kMaxTiles = (kSVShortCap + kSplitP - 1) / kSplitP;
     __shared__ float m_s[kMaxTiles], w_s[kMaxTiles], l_s[kMaxTiles];
     __shared__ float red[HD / 64];
+    static_assert(kMaxTiles <= HD, "one tile's (m, l) per thread");
+    const int h = blockIdx.x, d = threadIdx.x, tl = max_tiles - 1;
+    const float *ph = part + (size_t)h * max_tiles * kSplitPart;
+    // The first kPre tiles' values and tile d's (m, l) are loaded before the
+    // window is known, beside the position's load (indices clamped to the
+    // buffer's tiles; tiles past the window are never used): one round trip
+    // for windows up to kPre tiles.
+    constexpr int kPre = 32;
+    float pv[kPre];
+#pragma unroll
+    for (int k = 0; k < kPre; ++k) pv[k] = ph[(size_t)(k < tl ? k : tl) * kSplitPart + d];
+    const size_t td = (size_t)(d < tl ? d : tl) * kSplitPart;
+    const float m_d = ph[td + HD], l_d = ph[td + HD + 1];
     int window, start;
     attn_window(d_pos, n_past_arg, capacity, window, start);
-    const int ntiles = (window + kSplitP - 1) / kSplitP, h = blockIdx.x, d = threadIdx.x;
-    const float *ph = part + (size_t)h * max_tiles * kSplitPart;
+    const int ntiles = (window + kSplitP - 1) / kSplitP;
     float L = 0.0f, o = 0.0f;
     if (ntiles <= kMaxTiles) {
-        // the first kPre tiles' values are loaded with the tiles' (m, l), one
-        // round trip for windows up to kPre tiles (clamped loads: no branch
-        // delays their issue)
-        constexpr int kPre = 32;
-        float pv[kPre];
-#pragma unroll
-        for (int k = 0; k < kPre; ++k) pv[k] = ph[(size_t)(k < ntiles ? k : ntiles - 1) * kSplitPart + d];
-        // the tiles' (m, l) in parallel, one tile per thread
-        for (int t = d; t < ntiles; t += HD) {
-            m_s[t] = ph[(size_t)t * kSplitPart + HD];
-            l_s[t] = ph[(size_t)t * kSplitPart + HD + 1];
+        if (d < ntiles) {
+            m_s[d] = m_d;
+            l_s[d] = l_d;
         }
         __syncthreads();
         float M = -INFINITY;
