@@ -105,7 +105,9 @@ __global__ __launch_bounds__(kNormMaxThreads) void rms_norm_kernel(const float *
 //   h_out = h_in + rms_norm(t, w_post)
 //   xn    = rms_norm(h_out, w_next)   -> xn (nullable) and its Q8_0 pack (nullable)
 // One workgroup; h_out may equal h_in.
-template <int CH>
+// FAST (one float4 per thread only): the two sums in tree order, the
+// tolerance path's norm.
+template <int CH, bool FAST = false>
 __global__ __launch_bounds__(kNormMaxThreads) void residual_rms_norm_kernel(const float *__restrict__ t,
                                                                  const float *__restrict__ w_post,
                                                                  const float *h_in, float *h_out,
@@ -124,8 +126,8 @@ __global__ __launch_bounds__(kNormMaxThreads) void residual_rms_norm_kernel(cons
     const int n4 = dim >> 2;
     if constexpr (CH == 1) {
         const ResidualOps ops = residual_load(t, w_post, h_in, (xn || pack) ? w_next : nullptr, n4);
-        residual_norm1(ops, w_post != nullptr, w_next != nullptr, eps, h_out, xn, pack, dim,
-                       *reinterpret_cast<mrml_xsum::Shared4 *>(lds));
+        residual_norm1<false, FAST>(ops, w_post != nullptr, w_next != nullptr, eps, h_out, xn, pack, dim,
+                                    *reinterpret_cast<mrml_xsum::Shared4 *>(lds));
         return;
     }
     const float4 *t4 = reinterpret_cast<const float4 *>(t);
@@ -1168,9 +1170,12 @@ int launch_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float eps
 }
 
 int launch_residual_rms_norm(mrml_hip_ctx *ctx, const float *t, const float *w_post, const float *h_in, float *h_out,
-                             const float *w_next, float eps, float *xn, void *pack, int dim, int rows)
+                             const float *w_next, float eps, float *xn, void *pack, int dim, int rows, bool fast)
 {
-    if (norm_one_chunk(dim))
+    if (norm_one_chunk(dim) && fast)
+        hipLaunchKernelGGL((residual_rms_norm_kernel<1, true>), dim3(1, rows), dim3(norm_threads(dim)), norm_lds(dim),
+                           ctx->stream, t, w_post, h_in, h_out, w_next, eps, xn, (uint8_t *)pack, dim);
+    else if (norm_one_chunk(dim))
         hipLaunchKernelGGL(residual_rms_norm_kernel<1>, dim3(1, rows), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, t,
                            w_post, h_in, h_out, w_next, eps, xn, (uint8_t *)pack, dim);
     else

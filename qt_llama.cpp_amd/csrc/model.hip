@@ -347,17 +347,17 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
                                       m->act_pack, c.ffn_dim, c.dim, fast));
         } else {
             STEP(launch_residual_rms_norm(ctx, m->o, L.post_attn_norm, hA, hA, L.ffn_norm, c.eps, nullptr, m->xpack,
-                                          c.dim));
+                                          c.dim, 1, fast));
             STEP(launch_gemv_q4_0_geglu_emit(ctx, L.w_gate, L.w_up, m->xpack, m->act, m->act_pack, c.ffn_dim,
                                              c.dim));
         }
         STEP(launch_gemv_q4_0(ctx, L.w_down, m->act_pack, m->f, c.dim, c.ffn_dim, fast));
         if (!fused)
             STEP(launch_residual_rms_norm(ctx, m->f, L.post_ffw_norm, hA, hA, next_norm, c.eps, nullptr, m->xpack,
-                                          c.dim));
+                                          c.dim, 1, fast));
         else if (l + 1 == c.n_layers)
             STEP(launch_residual_rms_norm(ctx, m->f, L.post_ffw_norm, hB, hA, next_norm, c.eps, nullptr, m->xpack,
-                                          c.dim));
+                                          c.dim, 1, fast));
     }
     if (c.tie_type == MRML_HIP_Q4_0)
         STEP(launch_gemv_q4_0(ctx, m->tok_embd, m->xpack, logits, c.vocab, c.dim));
@@ -488,7 +488,7 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
             }
             STEP(gemm_rows(ctx, m, L.wo, m->pf_attn, m->pf_o, c.dim, qd, n));
             STEP(launch_residual_rms_norm(ctx, m->pf_o, L.post_attn_norm, h, h, L.ffn_norm, c.eps, xn, nullptr, c.dim,
-                                          n));
+                                          n, fast));
             STEP(launch_gemm_pack_quantize(ctx, xn, m->pf_gpack, c.dim, n));
             STEP(launch_gemm_q4_0(ctx, L.w_gate, m->pf_gpack, m->pf_g, c.ffn_dim, c.dim, n, 0, fast));
             STEP(launch_gemm_q4_0(ctx, L.w_up, m->pf_gpack, m->pf_u, c.ffn_dim, c.dim, n, 0, fast));
@@ -497,7 +497,7 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
             STEP(launch_geglu_rows(ctx, m->pf_g, m->pf_u, m->pf_act, n * c.ffn_dim));
             STEP(gemm_rows(ctx, m, L.w_down, m->pf_act, m->pf_f, c.dim, c.ffn_dim, n));
             STEP(launch_residual_rms_norm(ctx, m->pf_f, L.post_ffw_norm, h, h, next_norm, c.eps, xn, nullptr, c.dim,
-                                          n));
+                                          n, fast));
         }
         if (t0 + n < n_tokens) continue;
         // the last token's logits and greedy pick (the LM head of its token step)
