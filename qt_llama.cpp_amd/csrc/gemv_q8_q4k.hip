@@ -400,7 +400,7 @@ struct MergeShared {
     uint64_t heads[kSelectThreads];
     uint64_t surv[kTopKMax * kTopKMax];
     uint8_t surv_seg[kTopKMax * kTopKMax];
-    int seg_off[kTopKMax], seg_len[kTopKMax];
+    int seg_off[kTopKMax], seg_len[kTopKMax], seg_list[kTopKMax];
     uint64_t red[kSelectThreads / 64];
     int n_surv, n_seg;
 };
@@ -431,16 +431,46 @@ __device__ __forceinline__ void merge_lists(const uint64_t *__restrict__ lists, 
     __syncthreads();
     uint64_t L = kth_largest(m.heads, n_lists, k, (uint64_t)0, m.red);
     L = L ? L : 1;
+    // the lists with a head >= L (at most k: the heads are distinct keys or 0)
     if (t < n_lists && m.heads[t] >= L) {
-        const uint64_t *lt = lists + (size_t)t * k;
-        int c = 1;
-        while (c < k && lt[c] >= L) ++c;
-        const int off = atomicAdd(&m.n_surv, c), sg = atomicAdd(&m.n_seg, 1);
-        m.seg_off[sg] = off;
-        m.seg_len[sg] = c;
-        for (int i = 0; i < c; ++i) {
-            m.surv[off + i] = lt[i];
-            m.surv_seg[off + i] = (uint8_t)sg;
+        const int sg = atomicAdd(&m.n_seg, 1);
+        m.seg_list[sg] = t;
+        m.seg_len[sg] = 0;
+    }
+    __syncthreads();
+    // every key of those lists loaded at once, (segment, place) pairs over
+    // the block; a list's keys >= L are a prefix of it (descending), so its
+    // length is the largest place that passes, plus one
+    const int ns = m.n_seg, npairs = ns * k;
+    constexpr int kPairs = kTopKMax * kTopKMax / kSelectThreads;
+    static_assert(kPairs * kSelectThreads == kTopKMax * kTopKMax, "whole pairs per thread");
+    uint64_t pk[kPairs];
+#pragma unroll
+    for (int i = 0; i < kPairs; ++i) {
+        const int q = t + i * kSelectThreads;
+        pk[i] = q < npairs ? lists[(size_t)m.seg_list[q / k] * k + q % k] : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < kPairs; ++i) {
+        const int q = t + i * kSelectThreads;
+        if (q < npairs && pk[i] >= L) atomicMax(&m.seg_len[q / k], q % k + 1);
+    }
+    __syncthreads();
+    if (t == 0) {
+        int off = 0;
+        for (int sg = 0; sg < ns; ++sg) {
+            m.seg_off[sg] = off;
+            off += m.seg_len[sg];
+        }
+        m.n_surv = off;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kPairs; ++i) {
+        const int q = t + i * kSelectThreads, sg = q / k, j = q % k;
+        if (q < npairs && j < m.seg_len[sg]) {
+            m.surv[m.seg_off[sg] + j] = pk[i];
+            m.surv_seg[m.seg_off[sg] + j] = (uint8_t)sg;
         }
     }
     __syncthreads();
