@@ -408,6 +408,26 @@ int mrml_hip_attn_decode_f16_split(mrml_hip_ctx *ctx, const float *d_q, const ui
                                    const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                                    float scale, int32_t capacity);
 
+/* CudaDevice::attention_causal with the reference's own argument list
+ * (cuda.rs:2658-2697; the window rule of kernels.rs:1398-1404): q holds
+ * n_heads*head_dim floats, the caches capacity rows (row = position %
+ * capacity), n_past the query's position; sliding_window > 0 limits the
+ * window to the last sliding_window positions (<= 0: no limit beyond the
+ * capacity).  The arithmetic of mrml_hip_attn_decode_f16, bit-identical to
+ * the CPU path over the same rows.  k_format / v_format: the cache formats
+ * of KvCacheFormat::cuda_code (kv_cache.rs:16-22); only 0 (f16 rows) is
+ * served, others return MRML_HIP_E_UNSUPPORTED.  head_dim 256. */
+int mrml_hip_attention_causal(mrml_hip_ctx *ctx, const float *d_q, const uint16_t *d_k_cache,
+                              const uint16_t *d_v_cache, float *d_out, int32_t n_past, int32_t n_heads,
+                              int32_t n_kv_heads, int32_t head_dim, float scale, int32_t sliding_window,
+                              int32_t capacity, int32_t k_format, int32_t v_format);
+/* The same on the tolerance path (mrml_hip_attn_decode_f16_split's split-K
+ * arithmetic, within 1e-5 of the CPU path). */
+int mrml_hip_attention_causal_split(mrml_hip_ctx *ctx, const float *d_q, const uint16_t *d_k_cache,
+                                    const uint16_t *d_v_cache, float *d_out, int32_t n_past, int32_t n_heads,
+                                    int32_t n_kv_heads, int32_t head_dim, float scale, int32_t sliding_window,
+                                    int32_t capacity, int32_t k_format, int32_t v_format);
+
 /* ---- Gemma-2-shape token step (model.rs forward_token, model.rs:1185-2260,
  * and greedy selection, model.rs:2833-2907) ----------------------------------- */
 /* Numerics of the token step.  EXACT (0, the default): every op in the CPU

@@ -176,6 +176,8 @@ _SIGNATURES = {
     "mrml_hip_rope_kv_append_f16": [_P, _P, _P, _P, _I, _P, _I, _I, _I, _F, _F, _I, _P, _I],
     "mrml_hip_attn_decode_f16": [_P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _F, _I],
     "mrml_hip_attn_decode_f16_split": [_P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _F, _I],
+    "mrml_hip_attention_causal": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _I],
+    "mrml_hip_attention_causal_split": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _I],
     "mrml_hip_gemma2_create": [_P, _P, _P, _P, _P, ctypes.POINTER(_P)],
     "mrml_hip_gemma2_destroy": [_P, _P],
     "mrml_hip_gemma2_step": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I],
@@ -541,6 +543,16 @@ class HipDevice:
         self._check(self.lib.mrml_hip_attn_decode_f16_split(self.ctx, _ptr(q), _ptr(k_cache), _ptr(v_cache),
                                                             _ptr(out), _ptr(pack), n_past, _ptr(d_pos), n_heads,
                                                             n_kv_heads, head_dim, scale, capacity))
+
+    def attention_causal_ref(self, q, k_cache, v_cache, out, n_past: int, n_heads: int, n_kv_heads: int,
+                             head_dim: int, scale: float, sliding_window, capacity: int, k_format: int = 0,
+                             v_format: int = 0, split: bool = False) -> None:
+        """CudaDevice::attention_causal with its own arguments (cuda.rs:2658-2697): sliding_window None or an
+        int (mrml_hip_attention_causal, or its split form)."""
+        fn = self.lib.mrml_hip_attention_causal_split if split else self.lib.mrml_hip_attention_causal
+        self._check(fn(self.ctx, _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), n_past, n_heads, n_kv_heads,
+                       head_dim, scale, -1 if sliding_window is None else int(sliding_window), capacity, k_format,
+                       v_format))
 
 
 class Gemma2Model:

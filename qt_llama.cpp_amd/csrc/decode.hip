@@ -276,12 +276,14 @@ __global__ __launch_bounds__(512) void rope_kv_f16_kernel(float *__restrict__ qk
 
 __device__ __forceinline__ size_t cache_row_of(int t, int capacity) { return (size_t)(capacity > 0 ? t % capacity : t); }
 
-__device__ __forceinline__ void attn_window(const int32_t *d_pos, int n_past_arg, int capacity, int &window,
-                                            int &start)
+// The window: the last min(n_past + 1, limit) positions, limit = the cache
+// capacity or, below it, the sliding window (cuda.rs:2658-2697 sliding_window;
+// kernels.rs:1398-1404).  Cache rows stay position % capacity.
+__device__ __forceinline__ void attn_window(const int32_t *d_pos, int n_past_arg, int limit, int &window, int &start)
 {
     const int n_past = d_pos ? *d_pos : n_past_arg;
     const int count = n_past + 1;
-    window = (capacity > 0 && count > capacity) ? capacity : count;
+    window = (limit > 0 && count > limit) ? limit : count;
     start = count - window;
 }
 
@@ -297,14 +299,14 @@ constexpr int kKRow = kAttnHD * 2 + 8;  // padded K row in LDS, bytes
 __global__ __launch_bounds__(512) void attn_scores_kernel(const float *__restrict__ q,
                                                           const uint16_t *__restrict__ k_cache,
                                                           const int32_t *__restrict__ d_pos, int n_past_arg,
-                                                          int n_heads, int n_kv_heads, float scale, int capacity,
+                                                          int n_heads, int n_kv_heads, float scale, int capacity, int wlimit,
                                                           float *__restrict__ scores)
 {
     constexpr int HD = kAttnHD, P = kScoreP;
     __shared__ __align__(16) float q_s[8][HD];
     __shared__ __align__(16) uint8_t k_s[P * kKRow];
     int window, start;
-    attn_window(d_pos, n_past_arg, capacity, window, start);
+    attn_window(d_pos, n_past_arg, wlimit, window, start);
     const int p0 = blockIdx.x * P;
     if (p0 >= window) return;
     const int kvh = blockIdx.y, G = n_heads / n_kv_heads, nt = G * 64, tid = threadIdx.x;
@@ -399,7 +401,7 @@ __global__ __launch_bounds__(kScoreT) void attn_scores2_kernel(const float *__re
                                                                uint16_t *__restrict__ k_cache,
                                                                uint16_t *__restrict__ v_cache,
                                                                const int32_t *__restrict__ d_pos, int n_past_arg,
-                                                               int n_heads, int n_kv_heads, float scale, int capacity,
+                                                               int n_heads, int n_kv_heads, float scale, int capacity, int wlimit,
                                                                const float *__restrict__ table, int n_table,
                                                                float base, float freq_scale,
                                                                float *__restrict__ scores)
@@ -413,7 +415,7 @@ __global__ __launch_bounds__(kScoreT) void attn_scores2_kernel(const float *__re
     scores += (size_t)blockIdx.z * n_heads * capacity;
     n_past_arg += (int)blockIdx.z;
     int window, start;
-    attn_window(d_pos, n_past_arg, capacity, window, start);
+    attn_window(d_pos, n_past_arg, wlimit, window, start);
     const int p0 = blockIdx.x * P;
     if (p0 >= window) return;
     const int kvh = blockIdx.y, G = n_heads / n_kv_heads, tid = threadIdx.x;
@@ -620,7 +622,7 @@ template <bool LONG>
 __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *__restrict__ scores,
                                                              const uint16_t *__restrict__ v_cache,
                                                              const int32_t *__restrict__ d_pos, int n_past_arg,
-                                                             int n_heads, int n_kv_heads, int capacity, int expf_fused,
+                                                             int n_heads, int n_kv_heads, int capacity, int wlimit, int expf_fused,
                                                              float *__restrict__ out, uint8_t *__restrict__ pack)
 {
     constexpr int HD = kAttnHD;
@@ -634,7 +636,7 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
     if (out) out += (size_t)blockIdx.z * n_heads * HD;
     n_past_arg += (int)blockIdx.z;
     int window, start;
-    attn_window(d_pos, n_past_arg, capacity, window, start);
+    attn_window(d_pos, n_past_arg, wlimit, window, start);
     const int h = blockIdx.x, ds = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int G = n_heads / n_kv_heads, kvh = h / G;
     const float *sc = scores + (size_t)h * capacity;
@@ -829,7 +831,7 @@ __global__ __launch_bounds__(kSplitT) void attn_split_kernel(const float *__rest
                                                              uint16_t *__restrict__ k_cache,
                                                              uint16_t *__restrict__ v_cache,
                                                              const int32_t *__restrict__ d_pos, int n_past_arg,
-                                                             int n_heads, int n_kv_heads, float scale, int capacity,
+                                                             int n_heads, int n_kv_heads, float scale, int capacity, int wlimit,
                                                              const float *__restrict__ table, int n_table, float base,
                                                              float freq_scale, float *__restrict__ part, int max_tiles)
 {
@@ -840,7 +842,7 @@ __global__ __launch_bounds__(kSplitT) void attn_split_kernel(const float *__rest
     __shared__ __align__(16) float e_s[8][P];
     static_assert(P == 32, "two lanes per position");
     int window, start;
-    attn_window(d_pos, n_past_arg, capacity, window, start);
+    attn_window(d_pos, n_past_arg, wlimit, window, start);
     const int tile = blockIdx.x, p0 = tile * P;
     if (p0 >= window) return;
     const int kvh = blockIdx.y, G = n_heads / n_kv_heads, tid = threadIdx.x;
@@ -967,7 +969,7 @@ __global__ __launch_bounds__(kSplitT) void attn_split_kernel(const float *__rest
 // n_heads*256 output.
 __global__ __launch_bounds__(kAttnHD) void attn_combine_kernel(const float *__restrict__ part,
                                                                const int32_t *__restrict__ d_pos, int n_past_arg,
-                                                               int capacity, int max_tiles, int n_heads,
+                                                               int capacity, int wlimit, int max_tiles, int n_heads,
                                                                float *__restrict__ out, uint8_t *__restrict__ pack)
 {
     constexpr int HD = kAttnHD, kMaxTiles = (kSVShortCap + kSplitP - 1) / kSplitP;
@@ -987,7 +989,7 @@ __global__ __launch_bounds__(kAttnHD) void attn_combine_kernel(const float *__re
     const size_t td = (size_t)(d < tl ? d : tl) * kSplitPart;
     const float m_d = ph[td + HD], l_d = ph[td + HD + 1];
     int window, start;
-    attn_window(d_pos, n_past_arg, capacity, window, start);
+    attn_window(d_pos, n_past_arg, wlimit, window, start);
     const int ntiles = (window + kSplitP - 1) / kSplitP;
     float L = 0.0f, o = 0.0f;
     if (ntiles <= kMaxTiles) {
@@ -1209,6 +1211,10 @@ int launch_rope_kv_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache, uint16_
 }
 
 int attn_head_dim() { return kAttnHD; }
+int attn_window_limit(int capacity, int sliding_window)
+{
+    return sliding_window > 0 && sliding_window < capacity ? sliding_window : capacity;
+}
 int attn_max_capacity() { return 131072; }  // 2^17 positions, the Gemma family's longest context
 
 size_t attn_scratch_bytes(int n_heads, int capacity) { return (size_t)n_heads * capacity * sizeof(float); }
@@ -1216,35 +1222,39 @@ size_t attn_scratch_bytes(int n_heads, int capacity) { return (size_t)n_heads * 
 // Softmax and weighted values of `rows` query rows (grid z), the LDS or the
 // LONG form by capacity.
 static int launch_softmax_v(mrml_hip_ctx *ctx, const float *scores, const uint16_t *v_cache, float *out, void *pack,
-                            const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads, int capacity, int rows = 1)
+                            const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads, int capacity, int wlimit,
+                            int rows = 1)
 {
     const dim3 grid(n_heads, kAttnHD / kSVD, rows), block(64 * kSVW);
     if (sv_long(capacity))
         hipLaunchKernelGGL(attn_softmax_v_kernel<true>, grid, block, sv_lds(capacity), ctx->stream, scores, v_cache,
-                           d_pos, n_past, n_heads, n_kv_heads, capacity, (int)host_expf_fused(), out, (uint8_t *)pack);
+                           d_pos, n_past, n_heads, n_kv_heads, capacity, wlimit, (int)host_expf_fused(), out,
+                           (uint8_t *)pack);
     else
         hipLaunchKernelGGL(attn_softmax_v_kernel<false>, grid, block, sv_lds(capacity), ctx->stream, scores, v_cache,
-                           d_pos, n_past, n_heads, n_kv_heads, capacity, (int)host_expf_fused(), out, (uint8_t *)pack);
+                           d_pos, n_past, n_heads, n_kv_heads, capacity, wlimit, (int)host_expf_fused(), out,
+                           (uint8_t *)pack);
     return check_launch(ctx, "attn_softmax_v_kernel");
 }
 
 int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache, const uint16_t *v_cache,
                            float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
-                           float scale, int capacity, void *scratch)
+                           float scale, int capacity, void *scratch, int sliding_window)
 {
     float *scores = reinterpret_cast<float *>(scratch);
     const dim3 sgrid((capacity + kScoreP - 1) / kScoreP, n_kv_heads);
+    const int wlimit = attn_window_limit(capacity, sliding_window);
     if (n_heads / n_kv_heads <= 4) {
         hipLaunchKernelGGL(attn_scores2_kernel<false>, sgrid, dim3(kScoreT), 0, ctx->stream, q,
                            const_cast<uint16_t *>(k_cache), (uint16_t *)nullptr, d_pos, n_past, n_heads, n_kv_heads,
-                           scale, capacity, (const float *)nullptr, 0, 0.0f, 0.0f, scores);
+                           scale, capacity, wlimit, (const float *)nullptr, 0, 0.0f, 0.0f, scores);
         if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
     } else {
         hipLaunchKernelGGL(attn_scores_kernel, sgrid, dim3(64 * (n_heads / n_kv_heads)), 0, ctx->stream, q, k_cache,
-                           d_pos, n_past, n_heads, n_kv_heads, scale, capacity, scores);
+                           d_pos, n_past, n_heads, n_kv_heads, scale, capacity, wlimit, scores);
         if (int rc = check_launch(ctx, "attn_scores_kernel")) return rc;
     }
-    return launch_softmax_v(ctx, scores, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, capacity);
+    return launch_softmax_v(ctx, scores, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, capacity, wlimit);
 }
 
 // Attention of `rows` queries at consecutive positions n_past0, n_past0+1, ...
@@ -1263,9 +1273,10 @@ int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *qkv, const uint16_t *k_
     const dim3 sgrid((span + kScoreP - 1) / kScoreP, n_kv_heads, rows);
     hipLaunchKernelGGL(attn_scores2_kernel<false>, sgrid, dim3(kScoreT), 0, ctx->stream, qkv,
                        const_cast<uint16_t *>(k_cache), (uint16_t *)nullptr, (const int32_t *)nullptr, n_past0,
-                       n_heads, n_kv_heads, scale, capacity, (const float *)nullptr, 0, 0.0f, 0.0f, scores);
+                       n_heads, n_kv_heads, scale, capacity, capacity, (const float *)nullptr, 0, 0.0f, 0.0f, scores);
     if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
-    return launch_softmax_v(ctx, scores, v_cache, out, nullptr, nullptr, n_past0, n_heads, n_kv_heads, capacity, rows);
+    return launch_softmax_v(ctx, scores, v_cache, out, nullptr, nullptr, n_past0, n_heads, n_kv_heads, capacity, capacity,
+                            rows);
 }
 
 // The decode step's attention with RoPE and the K/V append in the scores
@@ -1281,9 +1292,10 @@ int launch_attn_decode_rope_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k
     float *scores = reinterpret_cast<float *>(scratch);
     const dim3 sgrid((capacity + kScoreP - 1) / kScoreP, n_kv_heads);
     hipLaunchKernelGGL(attn_scores2_kernel<true>, sgrid, dim3(kScoreT), 0, ctx->stream, qkv, k_cache, v_cache, d_pos,
-                       n_past, n_heads, n_kv_heads, scale, capacity, table, n_table, base, freq_scale, scores);
+                       n_past, n_heads, n_kv_heads, scale, capacity, capacity, table, n_table, base, freq_scale,
+                       scores);
     if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
-    return launch_softmax_v(ctx, scores, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, capacity);
+    return launch_softmax_v(ctx, scores, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, capacity, capacity);
 }
 
 int attn_split_tiles(int capacity) { return (capacity + kSplitP - 1) / kSplitP; }
@@ -1296,22 +1308,22 @@ size_t attn_split_scratch_bytes(int n_heads, int capacity)
 int launch_attn_split_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k_cache, uint16_t *v_cache, float *out,
                           void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads, float scale,
                           int capacity, bool rope, const float *table, int n_table, float base, float freq_scale,
-                          void *scratch)
+                          void *scratch, int sliding_window)
 {
     float *part = reinterpret_cast<float *>(scratch);
-    const int tiles = attn_split_tiles(capacity);
+    const int tiles = attn_split_tiles(capacity), wlimit = attn_window_limit(capacity, sliding_window);
     const dim3 grid(tiles, n_kv_heads);
     if (rope)
         hipLaunchKernelGGL(attn_split_kernel<true>, grid, dim3(kSplitT), 0, ctx->stream, qkv, k_cache, v_cache, d_pos,
-                           n_past, n_heads, n_kv_heads, scale, capacity, table, n_table, base, freq_scale, part,
-                           tiles);
+                           n_past, n_heads, n_kv_heads, scale, capacity, wlimit, table, n_table, base, freq_scale,
+                           part, tiles);
     else
         hipLaunchKernelGGL(attn_split_kernel<false>, grid, dim3(kSplitT), 0, ctx->stream, qkv, k_cache, v_cache,
-                           d_pos, n_past, n_heads, n_kv_heads, scale, capacity, table, n_table, base, freq_scale,
-                           part, tiles);
+                           d_pos, n_past, n_heads, n_kv_heads, scale, capacity, wlimit, table, n_table, base,
+                           freq_scale, part, tiles);
     if (int rc = check_launch(ctx, "attn_split_kernel")) return rc;
     hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(kAttnHD), 0, ctx->stream, part, d_pos, n_past,
-                       capacity, tiles, n_heads, out, (uint8_t *)pack);
+                       capacity, wlimit, tiles, n_heads, out, (uint8_t *)pack);
     return check_launch(ctx, "attn_combine_kernel");
 }
 

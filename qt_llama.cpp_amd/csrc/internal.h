@@ -161,10 +161,13 @@ int launch_rope_kv_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache, uint16_
                        const float *table, int n_table, int rows = 1);
 int attn_head_dim();
 int attn_max_capacity();
+// The attended window's limit: the capacity, or a sliding window below it
+// (sliding_window <= 0: none).
+int attn_window_limit(int capacity, int sliding_window);
 size_t attn_scratch_bytes(int n_heads, int capacity);
 int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache, const uint16_t *v_cache,
                            float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
-                           float scale, int capacity, void *scratch);
+                           float scale, int capacity, void *scratch, int sliding_window = -1);
 bool attn_rope_ok(int n_heads, int n_kv_heads);
 // `rows` batched queries at positions n_past0.. over stacked q|k|v rows
 // (prefill); scratch of rows * attn_scratch_bytes(n_heads, capacity).
@@ -183,7 +186,7 @@ hipError_t wait_guard_gemv(int polls, uint32_t *timeouts);
 hipError_t wait_guard_decode(int polls, uint32_t *timeouts);
 
 // Split-K decode attention, the decode step's tolerance path (decode.hip):
-// tiles of 64 positions, then a merge that also writes the Q8_0 pack.  With
+// tiles of 32 positions, then a merge that also writes the Q8_0 pack.  With
 // rope, qkv is the raw stacked q|k|v vector (RoPE and the K/V append as in
 // launch_attn_decode_rope_f16); without, the q of a token whose K/V rows are
 // in the caches.  scratch: attn_split_scratch_bytes(n_heads, capacity).
@@ -193,7 +196,7 @@ size_t attn_split_scratch_bytes(int n_heads, int capacity);
 int launch_attn_split_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k_cache, uint16_t *v_cache, float *out,
                           void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads, float scale,
                           int capacity, bool rope, const float *table, int n_table, float base, float freq_scale,
-                          void *scratch);
+                          void *scratch, int sliding_window = -1);
 
 // Which form of the C library's expf the host runs (glibc picks its FMA build
 // on x86-64 CPUs with FMA and AVX2); the device reproduces the same one.

@@ -159,24 +159,53 @@ int mrml_hip_rope_kv_append_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache
                               freq_scale, capacity, d_table, d_table ? n_table : 0);
 }
 
+// Arguments shared by the decode-attention entries.
+static int attn_args_ok(mrml_hip_ctx *ctx, const char *name, const float *q, const uint16_t *k_cache,
+                        const uint16_t *v_cache, const float *out, const void *pack, int32_t n_past,
+                        const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t capacity)
+{
+    REQUIRE(ctx, q && k_cache && v_cache && (out || pack), "%s: null pointer or no output", name);
+    REQUIRE(ctx, head_dim == attn_head_dim(), "%s: head_dim=%d unsupported (kernel serves %d)", name, head_dim,
+            attn_head_dim());
+    REQUIRE(ctx, n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= 8,
+            "%s: n_heads=%d n_kv_heads=%d (group of at most 8)", name, n_heads, n_kv_heads);
+    REQUIRE(ctx, capacity > 0 && capacity <= attn_max_capacity() && (d_pos || n_past >= 0),
+            "%s: n_past=%d capacity=%d (at most %d)", name, n_past, capacity, attn_max_capacity());
+    REQUIRE(ctx, ((((uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)q | (uintptr_t)pack) & 15) == 0),
+            "%s: pointers must be 16-byte aligned", name);
+    return MRML_HIP_OK;
+}
+
+static int attn_exact(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache, const uint16_t *v_cache, float *out,
+                      void *pack, int32_t n_past, const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads,
+                      float scale, int32_t capacity, int32_t sliding_window)
+{
+    void *part = workspace(ctx, attn_scratch_bytes(n_heads, capacity));
+    if (!part) return MRML_HIP_E_ALLOC;
+    return launch_attn_decode_f16(ctx, q, k_cache, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, scale,
+                                  capacity, part, sliding_window);
+}
+
+static int attn_split(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache, const uint16_t *v_cache, float *out,
+                      void *pack, int32_t n_past, const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads,
+                      float scale, int32_t capacity, int32_t sliding_window)
+{
+    void *part = workspace(ctx, attn_split_scratch_bytes(n_heads, capacity));
+    if (!part) return MRML_HIP_E_ALLOC;
+    return launch_attn_split_f16(ctx, q, const_cast<uint16_t *>(k_cache), const_cast<uint16_t *>(v_cache), out, pack,
+                                 d_pos, n_past, n_heads, n_kv_heads, scale, capacity, false, nullptr, 0, 0.0f, 0.0f,
+                                 part, sliding_window);
+}
+
 int mrml_hip_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache, const uint16_t *v_cache,
                              float *out, void *pack, int32_t n_past, const int32_t *d_pos, int32_t n_heads,
                              int32_t n_kv_heads, int32_t head_dim, float scale, int32_t capacity)
 {
     CTX_GUARD(ctx);
-    REQUIRE(ctx, q && k_cache && v_cache && (out || pack), "attn_decode_f16: null pointer or no output");
-    REQUIRE(ctx, head_dim == attn_head_dim(), "attn_decode_f16: head_dim=%d unsupported (kernel serves %d)",
-            head_dim, attn_head_dim());
-    REQUIRE(ctx, n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= 8,
-            "attn_decode_f16: n_heads=%d n_kv_heads=%d (group of at most 8)", n_heads, n_kv_heads);
-    REQUIRE(ctx, capacity > 0 && capacity <= attn_max_capacity() && (d_pos || n_past >= 0),
-            "attn_decode_f16: n_past=%d capacity=%d (at most %d)", n_past, capacity, attn_max_capacity());
-    REQUIRE(ctx, ((((uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)q | (uintptr_t)pack) & 15) == 0),
-            "attn_decode_f16: pointers must be 16-byte aligned");
-    void *part = workspace(ctx, attn_scratch_bytes(n_heads, capacity));
-    if (!part) return MRML_HIP_E_ALLOC;
-    return launch_attn_decode_f16(ctx, q, k_cache, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, scale,
-                                  capacity, part);
+    if (int rc = attn_args_ok(ctx, "attn_decode_f16", q, k_cache, v_cache, out, pack, n_past, d_pos, n_heads,
+                              n_kv_heads, head_dim, capacity))
+        return rc;
+    return attn_exact(ctx, q, k_cache, v_cache, out, pack, n_past, d_pos, n_heads, n_kv_heads, scale, capacity, -1);
 }
 
 int mrml_hip_attn_decode_f16_split(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache,
@@ -185,20 +214,49 @@ int mrml_hip_attn_decode_f16_split(mrml_hip_ctx *ctx, const float *q, const uint
                                    float scale, int32_t capacity)
 {
     CTX_GUARD(ctx);
-    REQUIRE(ctx, q && k_cache && v_cache && (out || pack), "attn_decode_f16_split: null pointer or no output");
-    REQUIRE(ctx, head_dim == attn_head_dim(), "attn_decode_f16_split: head_dim=%d unsupported (kernel serves %d)",
-            head_dim, attn_head_dim());
-    REQUIRE(ctx, n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= 8,
-            "attn_decode_f16_split: n_heads=%d n_kv_heads=%d (group of at most 8)", n_heads, n_kv_heads);
-    REQUIRE(ctx, capacity > 0 && capacity <= attn_max_capacity() && (d_pos || n_past >= 0),
-            "attn_decode_f16_split: n_past=%d capacity=%d (at most %d)", n_past, capacity, attn_max_capacity());
-    REQUIRE(ctx, ((((uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)q | (uintptr_t)pack) & 15) == 0),
-            "attn_decode_f16_split: pointers must be 16-byte aligned");
-    void *part = workspace(ctx, attn_split_scratch_bytes(n_heads, capacity));
-    if (!part) return MRML_HIP_E_ALLOC;
-    return launch_attn_split_f16(ctx, q, const_cast<uint16_t *>(k_cache), const_cast<uint16_t *>(v_cache), out, pack,
-                                 d_pos, n_past, n_heads, n_kv_heads, scale, capacity, false, nullptr, 0, 0.0f, 0.0f,
-                                 part);
+    if (int rc = attn_args_ok(ctx, "attn_decode_f16_split", q, k_cache, v_cache, out, pack, n_past, d_pos, n_heads,
+                              n_kv_heads, head_dim, capacity))
+        return rc;
+    return attn_split(ctx, q, k_cache, v_cache, out, pack, n_past, d_pos, n_heads, n_kv_heads, scale, capacity, -1);
+}
+
+// CudaDevice::attention_causal with its own argument list (cuda.rs:2658-2697):
+// the cache formats must be 0 (f16 rows; KvCacheFormat::cuda_code,
+// kv_cache.rs:16-22).
+static int attn_formats_ok(mrml_hip_ctx *ctx, const char *name, int32_t k_format, int32_t v_format)
+{
+    if (k_format != 0 || v_format != 0)
+        return fail(ctx, MRML_HIP_E_UNSUPPORTED, "%s: k_format=%d v_format=%d (only f16 caches, format 0)", name,
+                    k_format, v_format);
+    return MRML_HIP_OK;
+}
+
+int mrml_hip_attention_causal(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                              float *out, int32_t n_past, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                              float scale, int32_t sliding_window, int32_t capacity, int32_t k_format,
+                              int32_t v_format)
+{
+    CTX_GUARD(ctx);
+    if (int rc = attn_formats_ok(ctx, "attention_causal", k_format, v_format)) return rc;
+    if (int rc = attn_args_ok(ctx, "attention_causal", q, k_cache, v_cache, out, nullptr, n_past, nullptr, n_heads,
+                              n_kv_heads, head_dim, capacity))
+        return rc;
+    return attn_exact(ctx, q, k_cache, v_cache, out, nullptr, n_past, nullptr, n_heads, n_kv_heads, scale, capacity,
+                      sliding_window);
+}
+
+int mrml_hip_attention_causal_split(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache,
+                                    const uint16_t *v_cache, float *out, int32_t n_past, int32_t n_heads,
+                                    int32_t n_kv_heads, int32_t head_dim, float scale, int32_t sliding_window,
+                                    int32_t capacity, int32_t k_format, int32_t v_format)
+{
+    CTX_GUARD(ctx);
+    if (int rc = attn_formats_ok(ctx, "attention_causal_split", k_format, v_format)) return rc;
+    if (int rc = attn_args_ok(ctx, "attention_causal_split", q, k_cache, v_cache, out, nullptr, n_past, nullptr,
+                              n_heads, n_kv_heads, head_dim, capacity))
+        return rc;
+    return attn_split(ctx, q, k_cache, v_cache, out, nullptr, n_past, nullptr, n_heads, n_kv_heads, scale, capacity,
+                      sliding_window);
 }
 
 // ---- the Gemma-2-shape model --------------------------------------------------------

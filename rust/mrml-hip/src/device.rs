@@ -328,22 +328,21 @@ impl HipDevice {
         self.inner.expect(st, "embedding_q8_0");
     }
 
-    /// `CudaDevice::attention_causal` (cuda.rs:2658-2697) for one token over f16
-    /// caches.  The cache is a ring of `cache_capacity` positions, so the
-    /// window is the last `cache_capacity` of them: a `sliding_window` must be
-    /// that size or absent.
+    /// `CudaDevice::attention_causal` (cuda.rs:2658-2697) for one token, with
+    /// the reference's arguments: the cache is a ring of `cache_capacity`
+    /// positions, `sliding_window` limits the window below it, and the cache
+    /// formats must be 0 (f16 rows, `KvCacheFormat::cuda_code`).
     #[allow(clippy::too_many_arguments)]
     pub fn attention_causal(&self, d_q: &HipBuffer<f32>, d_k_cache: &HipBuffer<u16>, d_v_cache: &HipBuffer<u16>,
                             d_out: &mut HipBuffer<f32>, n_past: usize, n_heads: usize, n_kv_heads: usize, head_dim: usize,
-                            scale: f32, sliding_window: Option<usize>, cache_capacity: usize) {
-        if let Some(w) = sliding_window {
-            assert!(w >= cache_capacity, "attention_causal: a window of {w} below the cache capacity {cache_capacity}");
-        }
+                            scale: f32, sliding_window: Option<usize>, cache_capacity: usize, k_format: i32,
+                            v_format: i32) {
+        let sw = sliding_window.map(|w| i32_of(w, "sliding_window")).unwrap_or(-1);
         let st = unsafe {
-            (self.inner.api.attn_decode_f16)(self.inner.ctx, d_q.ptr, d_k_cache.ptr, d_v_cache.ptr, d_out.ptr,
-                                             std::ptr::null_mut(), i32_of(n_past, "n_past"), std::ptr::null(),
-                                             i32_of(n_heads, "n_heads"), i32_of(n_kv_heads, "n_kv_heads"),
-                                             i32_of(head_dim, "head_dim"), scale, i32_of(cache_capacity, "cache_capacity"))
+            (self.inner.api.attention_causal)(self.inner.ctx, d_q.ptr, d_k_cache.ptr, d_v_cache.ptr, d_out.ptr,
+                                              i32_of(n_past, "n_past"), i32_of(n_heads, "n_heads"),
+                                              i32_of(n_kv_heads, "n_kv_heads"), i32_of(head_dim, "head_dim"), scale, sw,
+                                              i32_of(cache_capacity, "cache_capacity"), k_format, v_format)
         };
         self.inner.expect(st, "attention_causal");
     }

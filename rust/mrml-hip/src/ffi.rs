@@ -191,6 +191,8 @@ api! {
     rope_kv_append_f16: fn(Ctx, *mut f32, *mut u16, *mut u16, i32, *const i32, i32, i32, i32, f32, f32, i32, *const f32, i32) -> c_int = "mrml_hip_rope_kv_append_f16";
     attn_decode_f16: fn(Ctx, *const f32, *const u16, *const u16, *mut f32, *mut c_void, i32, *const i32, i32, i32, i32, f32, i32) -> c_int = "mrml_hip_attn_decode_f16";
     attn_decode_f16_split: fn(Ctx, *const f32, *const u16, *const u16, *mut f32, *mut c_void, i32, *const i32, i32, i32, i32, f32, i32) -> c_int = "mrml_hip_attn_decode_f16_split";
+    attention_causal: fn(Ctx, *const f32, *const u16, *const u16, *mut f32, i32, i32, i32, i32, f32, i32, i32, i32, i32) -> c_int = "mrml_hip_attention_causal";
+    attention_causal_split: fn(Ctx, *const f32, *const u16, *const u16, *mut f32, i32, i32, i32, i32, f32, i32, i32, i32, i32) -> c_int = "mrml_hip_attention_causal_split";
     gemma2_create: fn(Ctx, *const MrmlHipGemma2Config, *const c_void, *const f32, *const MrmlHipGemma2Layer, *mut Model) -> c_int = "mrml_hip_gemma2_create";
     gemma2_destroy: fn(Ctx, Model) -> c_int = "mrml_hip_gemma2_destroy";
     gemma2_step: fn(Ctx, Model, *mut i32, *mut u16, *mut u16, *mut f32, *mut i32, *mut i32, i32, *const i32, i32) -> c_int = "mrml_hip_gemma2_step";

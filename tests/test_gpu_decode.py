@@ -282,6 +282,57 @@ def test_attention_single_position_is_v(backend, dev, orc, synth):
     assert np.array_equal(got, np.repeat(v0, 2, axis=0).reshape(-1))
 
 
+# ------------------------------------------------------------ sliding window (attention_causal's own arguments)
+# (n_past, sliding_window, capacity): the reference's own case -- the last 4 of
+# 8 positions (ops_test.rs:375-449; its head_dim of 64 is not served here, so
+# at 256) -- windows below and above the capacity, a window that wraps the
+# ring, a long capacity, and a single position
+SW_CASES = [(7, 4, 8), (100, 37, 128), (100, 200, 128), (300, 50, 64), (9000, 4096, 8192), (0, 5, 64)]
+
+
+@pytest.mark.parametrize("n_past,sw,cap", SW_CASES)
+def test_attention_causal_sliding_window(backend, dev, orc, synth, n_past, sw, cap):
+    """mrml_hip_attention_causal (cuda.rs:2658-2697 argument list): the last
+    min(n_past + 1, sliding_window, capacity) positions, bit-identical to the
+    CPU path over those rows; the split form within 1e-5 of it."""
+    nh, nkv, hd = 8, 4, 256
+    rng = synth.rng_for(3900 + n_past + sw)
+    kvd = nkv * hd
+    q = rng.standard_normal(nh * hd).astype(np.float32) * np.float32(0.5)
+    kc = rng.standard_normal(cap * kvd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(cap * kvd).astype(np.float16).view(np.uint16)
+    qb, kb, vb = (backend.HipBuffer.from_host(dev, a) for a in (q, kc, vc))
+    out = backend.HipBuffer.alloc(dev, nh * hd)
+    window = min(n_past + 1, sw, cap)
+    rows = [t % cap for t in range(n_past + 1 - window, n_past + 1)]
+    ref = orc.attention_f16(q, kc.reshape(cap, kvd)[rows].reshape(-1), vc.reshape(cap, kvd)[rows].reshape(-1),
+                            window - 1, nh, nkv, hd, 1.0 / 16.0)
+    dev.attention_causal_ref(qb, kb, vb, out, n_past, nh, nkv, hd, 1.0 / 16.0, sw, cap)
+    dev.sync()
+    assert_bits(out.numpy(), ref, f"attention_causal window {sw} capacity {cap}")
+    dev.attention_causal_ref(qb, kb, vb, out, n_past, nh, nkv, hd, 1.0 / 16.0, sw, cap, split=True)
+    dev.sync()
+    assert max_rel(out.numpy(), ref) <= 1e-5
+    # no window: the capacity bounds it, as mrml_hip_attn_decode_f16 does
+    dev.attention_causal_ref(qb, kb, vb, out, n_past, nh, nkv, hd, 1.0 / 16.0, None, cap)
+    dev.sync()
+    full = [t % cap for t in range(max(0, n_past + 1 - cap), n_past + 1)]
+    ref_full = orc.attention_f16(q, kc.reshape(cap, kvd)[full].reshape(-1), vc.reshape(cap, kvd)[full].reshape(-1),
+                                 len(full) - 1, nh, nkv, hd, 1.0 / 16.0)
+    assert_bits(out.numpy(), ref_full, "attention_causal without a window")
+
+
+def test_attention_causal_rejects_quantised_caches(backend, dev):
+    qb = backend.HipBuffer.alloc(dev, 8 * 256)
+    kb = backend.HipBuffer.alloc(dev, 64 * 1024, np.uint16)
+    out = backend.HipBuffer.alloc(dev, 8 * 256)
+    for kf, vf in ((1, 0), (0, 2)):
+        for split in (False, True):
+            with pytest.raises(backend.HipError) as e:
+                dev.attention_causal_ref(qb, kb, kb, out, 3, 8, 4, 256, 1.0 / 16.0, None, 64, kf, vf, split=split)
+            assert e.value.status == -4  # MRML_HIP_E_UNSUPPORTED
+
+
 # ------------------------------------------------------------ split-K attention (FAST numerics)
 def attention_split_case(backend, dev, orc, synth, n_past, cap, seed, nh=8, nkv=4, qscale=0.5):
     hd = 256
