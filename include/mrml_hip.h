@@ -382,6 +382,33 @@ int mrml_hip_rope_kv_append_f16(mrml_hip_ctx *ctx, float *d_qkv, uint16_t *d_k_c
                                 int32_t pos, const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads,
                                 int32_t head_dim, float freq_base, float freq_scale, int32_t capacity,
                                 const float *d_table, int32_t n_table);
+/* CudaDevice::qkv_postprocess_batch (cuda.rs:2478-2519, the kernel at
+ * kernels.rs:1231-1330; called by prefill_cuda, model.rs:2485-2501) without
+ * the Gemma-4 head norms: `batch` stacked [q | k | v] rows of d_qkv, row i
+ * rotated at position start_pos + i as mrml_hip_rope_kv_append_f16 rotates
+ * one row, its k and v stored as f16 at cache row (cache_start + i) %
+ * capacity.  batch <= capacity (rows of one call never share a cache row);
+ * k_format / v_format must be 0 (f16 rows).  freq_scale 1 is the
+ * reference's (the batched kernel has none). */
+int mrml_hip_rope_kv_append_f16_batch(mrml_hip_ctx *ctx, float *d_qkv, uint16_t *d_k_cache, uint16_t *d_v_cache,
+                                      int32_t start_pos, int32_t cache_start, int32_t batch, int32_t n_heads,
+                                      int32_t n_kv_heads, int32_t head_dim, float freq_base, float freq_scale,
+                                      int32_t capacity, int32_t k_format, int32_t v_format, const float *d_table,
+                                      int32_t n_table);
+/* CudaDevice::rope_256k (cuda.rs:2248-2285): rope_1d_batched (ops.rs:185-208)
+ * of n_heads contiguous heads of head_dim floats in d_vec, in place, at
+ * position pos; cos/sin from d_table (nullable) for pos < n_table, else
+ * evaluated on the device as mrml_hip_rope_kv_append_f16 does.  head_dim
+ * even, at most 1024. */
+int mrml_hip_rope(mrml_hip_ctx *ctx, float *d_vec, int32_t pos, int32_t head_dim, int32_t n_heads, float freq_base,
+                  float freq_scale, const float *d_table, int32_t n_table);
+/* CudaDevice::geglu (cuda.rs:2215-2246): d_out[i] = gelu_tanh(d_gate[i]) *
+ * d_up[i] for i < n (ops.rs:99-114), bit-identical to the CPU path. */
+int mrml_hip_geglu(mrml_hip_ctx *ctx, const float *d_gate, const float *d_up, float *d_out, int32_t n);
+/* CudaDevice::swiglu (cuda.rs:2182-2213): d_out[i] = silu(d_gate[i]) *
+ * d_up[i], silu(x) = x / (1 + expf(-x)) (ops.rs:116-130), expf the host C
+ * library's, bit-identical to the CPU path. */
+int mrml_hip_swiglu(mrml_hip_ctx *ctx, const float *d_gate, const float *d_up, float *d_out, int32_t n);
 /* CudaDevice::attention_causal (cuda.rs:2658-2697; CPU model.rs:1457-1590)
  * for one token: out[h] = softmax(scale * q[h] . K[t]) . V[t] over the last
  * min(n_past+1, capacity) cache rows, kv head h / (n_heads / n_kv_heads),
@@ -427,6 +454,18 @@ int mrml_hip_attention_causal_split(mrml_hip_ctx *ctx, const float *d_q, const u
                                     const uint16_t *d_v_cache, float *d_out, int32_t n_past, int32_t n_heads,
                                     int32_t n_kv_heads, int32_t head_dim, float scale, int32_t sliding_window,
                                     int32_t capacity, int32_t k_format, int32_t v_format);
+
+/* CudaDevice::attention_prefill (cuda.rs:2727-2770; called by prefill_cuda,
+ * model.rs:2503-2522): `batch` queries at positions cache_start + i over
+ * caches that already hold every row's K/V; query row i starts i * q_stride
+ * floats into d_q (the reference's q.len() / batch, >= n_heads*head_dim),
+ * output row i (n_heads*head_dim floats) at d_out + i*n_heads*head_dim.  Row
+ * i is bit-identical to mrml_hip_attention_causal at n_past = cache_start + i
+ * with the same sliding window, capacity and formats (0 only). */
+int mrml_hip_attention_prefill(mrml_hip_ctx *ctx, const float *d_q, int32_t q_stride, const uint16_t *d_k_cache,
+                               const uint16_t *d_v_cache, float *d_out, int32_t cache_start, int32_t batch,
+                               int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, float scale,
+                               int32_t sliding_window, int32_t capacity, int32_t k_format, int32_t v_format);
 
 /* ---- Gemma-2-shape token step (model.rs forward_token, model.rs:1185-2260,
  * and greedy selection, model.rs:2833-2907) ----------------------------------- */

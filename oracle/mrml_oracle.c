@@ -657,6 +657,12 @@ void orc_geglu(const float *gate, const float *up, float *out, size_t n)
 /* ops.rs:118-120 */
 float orc_silu(float x) { return x / (1.0f + expf(-x)); }
 
+/* ops.rs:123-130 */
+void orc_swiglu(const float *gate, const float *up, float *out, size_t n)
+{
+    for (size_t i = 0; i < n; i++) out[i] = orc_silu(gate[i]) * up[i];
+}
+
 /* ops.rs:133-158 */
 void orc_softmax(float *x, size_t n)
 {

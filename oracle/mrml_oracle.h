@@ -126,6 +126,7 @@ void  orc_rope_1d_batched(float *v, size_t pos, size_t n_heads, size_t head_dim,
 float orc_gelu_approx(float x);                                                        /* ops.rs:101-104 */
 void  orc_geglu(const float *gate, const float *up, float *out, size_t n);             /* ops.rs:107-114 */
 float orc_silu(float x);                                                               /* ops.rs:118-120 */
+void  orc_swiglu(const float *gate, const float *up, float *out, size_t n);            /* ops.rs:123-130 */
 void  orc_softmax(float *x, size_t n);                                                 /* ops.rs:133-158 */
 
 /* ---- decode attention over an f16 KV cache (build-defined composition of

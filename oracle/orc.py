@@ -63,6 +63,7 @@ _SIG = {
     "orc_gelu_approx": ([_F], _F),
     "orc_geglu": ([_P, _P, _P, _Z], None),
     "orc_silu": ([_F], _F),
+    "orc_swiglu": ([_P, _P, _P, _Z], None),
     "orc_softmax": ([_P, _Z], None),
     "orc_attention_f16": ([_P, _P, _P, _P, _Z, _Z, _Z, _Z, _F], None),
     "orc_gemma2_step": ([ctypes.POINTER(Gemma2), ctypes.c_int64, ctypes.c_int64, _P, _P, _P, _I], ctypes.c_int64),
@@ -257,6 +258,14 @@ def geglu(g, u) -> np.ndarray:
 
 def silu(x: float) -> float:
     return float(lib().orc_silu(x))
+
+
+def swiglu(g, u) -> np.ndarray:
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    u = np.ascontiguousarray(u, dtype=np.float32)
+    out = np.zeros_like(g)
+    lib().orc_swiglu(_p(g), _p(u), _p(out), g.size)
+    return out
 
 
 def softmax(x) -> np.ndarray:

@@ -176,6 +176,11 @@ _SIGNATURES = {
     "mrml_hip_rope_kv_append_f16": [_P, _P, _P, _P, _I, _P, _I, _I, _I, _F, _F, _I, _P, _I],
     "mrml_hip_attn_decode_f16": [_P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _F, _I],
     "mrml_hip_attn_decode_f16_split": [_P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _F, _I],
+    "mrml_hip_rope_kv_append_f16_batch": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _F, _I, _I, _I, _P, _I],
+    "mrml_hip_rope": [_P, _P, _I, _I, _I, _F, _F, _P, _I],
+    "mrml_hip_geglu": [_P, _P, _P, _P, _I],
+    "mrml_hip_swiglu": [_P, _P, _P, _P, _I],
+    "mrml_hip_attention_prefill": [_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _I, _I],
     "mrml_hip_attention_causal": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _I],
     "mrml_hip_attention_causal_split": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _I],
     "mrml_hip_gemma2_create": [_P, _P, _P, _P, _P, ctypes.POINTER(_P)],
@@ -528,6 +533,42 @@ class HipDevice:
         self._check(self.lib.mrml_hip_rope_kv_append_f16(self.ctx, _ptr(qkv), _ptr(k_cache), _ptr(v_cache), pos,
                                                          _ptr(d_pos), n_heads, n_kv_heads, head_dim, freq_base,
                                                          freq_scale, capacity, _ptr(table), n_table))
+
+    def qkv_postprocess_batch(self, qkv, k_cache, v_cache, start_pos: int, cache_start: int, n_heads: int,
+                              n_kv_heads: int, head_dim: int, freq_base: float, batch: int, capacity: int,
+                              k_format: int = 0, v_format: int = 0, freq_scale: float = 1.0, table=None,
+                              n_table: int = 0) -> None:
+        """CudaDevice::qkv_postprocess_batch (cuda.rs:2478-2519) without head norms, the reference's argument
+        order (mrml_hip_rope_kv_append_f16_batch)."""
+        self._check(self.lib.mrml_hip_rope_kv_append_f16_batch(
+            self.ctx, _ptr(qkv), _ptr(k_cache), _ptr(v_cache), start_pos, cache_start, batch, n_heads, n_kv_heads,
+            head_dim, freq_base, freq_scale, capacity, k_format, v_format, _ptr(table), n_table))
+
+    def rope_256k(self, vec, pos: int, head_dim: int, n_heads: int, freq_base: float, freq_scale: float = 1.0,
+                  table=None, n_table: int = 0) -> None:
+        """CudaDevice::rope_256k (cuda.rs:2248-2285): RoPE of n_heads heads of vec in place."""
+        self._check(self.lib.mrml_hip_rope(self.ctx, _ptr(vec), pos, head_dim, n_heads, freq_base, freq_scale,
+                                           _ptr(table), n_table))
+
+    def geglu(self, gate, up, out, n: int) -> None:
+        """CudaDevice::geglu (cuda.rs:2215-2246): out = gelu_tanh(gate) * up."""
+        self._check(self.lib.mrml_hip_geglu(self.ctx, _ptr(gate), _ptr(up), _ptr(out), n))
+
+    def swiglu(self, gate, up, out, n: int) -> None:
+        """CudaDevice::swiglu (cuda.rs:2182-2213): out = silu(gate) * up."""
+        self._check(self.lib.mrml_hip_swiglu(self.ctx, _ptr(gate), _ptr(up), _ptr(out), n))
+
+    def attention_prefill(self, q, k_cache, v_cache, out, cache_start: int, batch: int, n_heads: int,
+                          n_kv_heads: int, head_dim: int, scale: float, sliding_window, capacity: int,
+                          k_format: int = 0, v_format: int = 0, q_stride: int | None = None) -> None:
+        """CudaDevice::attention_prefill (cuda.rs:2727-2770): q_stride defaults to the reference's
+        q.len() / batch (q a HipBuffer of f32)."""
+        if q_stride is None:
+            q_stride = (q.nbytes // 4) // batch
+        self._check(self.lib.mrml_hip_attention_prefill(
+            self.ctx, _ptr(q), q_stride, _ptr(k_cache), _ptr(v_cache), _ptr(out), cache_start, batch, n_heads,
+            n_kv_heads, head_dim, scale, -1 if sliding_window is None else int(sliding_window), capacity, k_format,
+            v_format))
 
     def attention_causal(self, q, k_cache, v_cache, out, n_past: int, n_heads: int, n_kv_heads: int,
                          head_dim: int, scale: float, capacity: int, pack=None, d_pos=None) -> None:

@@ -225,14 +225,17 @@ __global__ __launch_bounds__(512) void rope_kv_f16_kernel(float *__restrict__ qk
                                                           const int32_t *__restrict__ d_pos, int pos_arg,
                                                           int n_heads, int n_kv_heads, int head_dim, float base,
                                                           float freq_scale, int capacity,
-                                                          const float *__restrict__ table, int n_table)
+                                                          const float *__restrict__ table, int n_table,
+                                                          int cache_shift)
 {
-    // row blockIdx.y of a batch of stacked q|k|v rows at consecutive positions
+    // row blockIdx.y of a batch of stacked q|k|v rows at consecutive
+    // positions; its K/V enter cache row (position + cache_shift) % capacity
     const int pos = (d_pos ? *d_pos : pos_arg) + (int)blockIdx.y;
     qkv += (size_t)blockIdx.y * (n_heads + 2 * n_kv_heads) * head_dim;
     const int half = head_dim >> 1, i = threadIdx.x, g = blockIdx.x;
     const size_t kv_dim = (size_t)n_kv_heads * head_dim;
-    const size_t cache_row = (size_t)(capacity > 0 ? pos % capacity : pos) * kv_dim;
+    const int cpos = pos + cache_shift;
+    const size_t cache_row = (size_t)(capacity > 0 ? cpos % capacity : cpos) * kv_dim;
     if (g < n_heads + n_kv_heads) {
         float c, s;
         if (table && pos >= 0 && pos < n_table) {
@@ -396,6 +399,33 @@ __device__ __forceinline__ void rope_cs(const float *table, int n_table, int pos
     }
 }
 
+// rope_1d_batched (ops.rs:185-208) over n_heads contiguous heads of one
+// vector in place: head blockIdx.x, pair i = threadIdx.x (head_dim / 2
+// threads), cos/sin from the host table when pos < n_table.
+__global__ __launch_bounds__(512) void rope_heads_kernel(float *__restrict__ vec, int pos, int head_dim, float base,
+                                                         float freq_scale, const float *__restrict__ table, int n_table)
+{
+    const int half = head_dim >> 1, i = threadIdx.x;
+    float c, sn;
+    rope_cs(table, n_table, pos, i, head_dim, base, freq_scale, c, sn);
+    float *v = vec + (size_t)blockIdx.x * head_dim;
+    const float v0 = v[i], v1 = v[i + half];
+    v[i] = v0 * c - v1 * sn;
+    v[i + half] = v0 * sn + v1 * c;
+}
+
+// act[i] = silu(g[i]) * u[i] with silu(x) = x / (1 + expf(-x)) (ops.rs:116-130),
+// expf the glibc-exact port, so each element rounds as the CPU path's does.
+__global__ __launch_bounds__(256) void swiglu_rows_kernel(const float *__restrict__ g, const float *__restrict__ u,
+                                                          float *__restrict__ act, int n, int expf_fused)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const float x = g[i];
+        act[i] = x / (1.0f + mrml_libm::expf(-x, expf_fused != 0)) * u[i];
+    }
+}
+
 template <bool ROPE>
 __global__ __launch_bounds__(kScoreT) void attn_scores2_kernel(const float *__restrict__ q_in,
                                                                uint16_t *__restrict__ k_cache,
@@ -404,14 +434,14 @@ __global__ __launch_bounds__(kScoreT) void attn_scores2_kernel(const float *__re
                                                                int n_heads, int n_kv_heads, float scale, int capacity, int wlimit,
                                                                const float *__restrict__ table, int n_table,
                                                                float base, float freq_scale,
-                                                               float *__restrict__ scores)
+                                                               float *__restrict__ scores, int q_stride)
 {
     constexpr int HD = kAttnHD, P = kScoreP, half = HD / 2;
     __shared__ __align__(16) float q_s[4][HD];
     __shared__ __align__(16) uint8_t k_s[P * kKRow2];
-    // query row blockIdx.z of a batch (prefill): stacked q|k|v rows at
-    // consecutive positions, one score block per row
-    q_in += (size_t)blockIdx.z * (n_heads + 2 * n_kv_heads) * HD;
+    // query row blockIdx.z of a batch (prefill): rows q_stride floats apart
+    // at consecutive positions, one score block per row
+    q_in += (size_t)blockIdx.z * q_stride;
     scores += (size_t)blockIdx.z * n_heads * capacity;
     n_past_arg += (int)blockIdx.z;
     int window, start;
@@ -1202,12 +1232,27 @@ int launch_embedding(mrml_hip_ctx *ctx, const void *table, int type, const int32
 
 int launch_rope_kv_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache, uint16_t *v_cache, const int32_t *d_pos,
                        int pos, int n_heads, int n_kv_heads, int head_dim, float base, float freq_scale, int capacity,
-                       const float *table, int n_table, int rows)
+                       const float *table, int n_table, int rows, int cache_shift)
 {
     hipLaunchKernelGGL(rope_kv_f16_kernel, dim3(n_heads + 2 * n_kv_heads, rows), dim3(head_dim / 2), 0, ctx->stream, qkv,
                        k_cache, v_cache, d_pos, pos, n_heads, n_kv_heads, head_dim, base, freq_scale, capacity, table,
-                       n_table);
+                       n_table, cache_shift);
     return check_launch(ctx, "rope_kv_f16_kernel");
+}
+
+int launch_rope(mrml_hip_ctx *ctx, float *vec, int pos, int n_heads, int head_dim, float base, float freq_scale,
+                const float *table, int n_table)
+{
+    hipLaunchKernelGGL(rope_heads_kernel, dim3(n_heads), dim3(head_dim / 2), 0, ctx->stream, vec, pos, head_dim, base,
+                       freq_scale, table, n_table);
+    return check_launch(ctx, "rope_heads_kernel");
+}
+
+int launch_swiglu_rows(mrml_hip_ctx *ctx, const float *g, const float *u, float *act, int n)
+{
+    hipLaunchKernelGGL(swiglu_rows_kernel, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, g, u, act, n,
+                       (int)host_expf_fused());
+    return check_launch(ctx, "swiglu_rows_kernel");
 }
 
 int attn_head_dim() { return kAttnHD; }
@@ -1247,7 +1292,7 @@ int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_
     if (n_heads / n_kv_heads <= 4) {
         hipLaunchKernelGGL(attn_scores2_kernel<false>, sgrid, dim3(kScoreT), 0, ctx->stream, q,
                            const_cast<uint16_t *>(k_cache), (uint16_t *)nullptr, d_pos, n_past, n_heads, n_kv_heads,
-                           scale, capacity, wlimit, (const float *)nullptr, 0, 0.0f, 0.0f, scores);
+                           scale, capacity, wlimit, (const float *)nullptr, 0, 0.0f, 0.0f, scores, 0);
         if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
     } else {
         hipLaunchKernelGGL(attn_scores_kernel, sgrid, dim3(64 * (n_heads / n_kv_heads)), 0, ctx->stream, q, k_cache,
@@ -1259,23 +1304,26 @@ int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_
 
 // Attention of `rows` queries at consecutive positions n_past0, n_past0+1, ...
 // (the prefill of a chunk whose K/V rows are already in the cache): query row
-// r is the q of stacked q|k|v row r of qkv; output row r (n_heads*head_dim
-// f32) goes to out.  Each row's arithmetic is that of launch_attn_decode_f16
-// at its position.  scratch holds rows * n_heads * capacity floats.  Needs
-// n_heads / n_kv_heads <= 4 (attn_rope_ok).
-int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *qkv, const uint16_t *k_cache, const uint16_t *v_cache,
-                         float *out, int n_past0, int rows, int n_heads, int n_kv_heads, float scale, int capacity,
-                         void *scratch)
+// r starts r * q_stride floats into q (q_stride = the stacked q|k|v width
+// when q is the projection itself); output row r (n_heads*head_dim f32) goes
+// to out.  Each row's arithmetic is that of launch_attn_decode_f16 at its
+// position with the same sliding window.  scratch holds rows * n_heads *
+// capacity floats.  Needs n_heads / n_kv_heads <= 4 (attn_rope_ok).
+int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *q, int q_stride, const uint16_t *k_cache,
+                         const uint16_t *v_cache, float *out, int n_past0, int rows, int n_heads, int n_kv_heads,
+                         float scale, int capacity, void *scratch, int sliding_window)
 {
     float *scores = reinterpret_cast<float *>(scratch);
-    // score tiles up to the last row's window (the host knows every row's position)
-    const int span = std::min(capacity, n_past0 + rows);
+    const int wlimit = attn_window_limit(capacity, sliding_window);
+    // score tiles up to the widest row window (the host knows every row's position)
+    const int span = std::min(wlimit, n_past0 + rows);
     const dim3 sgrid((span + kScoreP - 1) / kScoreP, n_kv_heads, rows);
-    hipLaunchKernelGGL(attn_scores2_kernel<false>, sgrid, dim3(kScoreT), 0, ctx->stream, qkv,
+    hipLaunchKernelGGL(attn_scores2_kernel<false>, sgrid, dim3(kScoreT), 0, ctx->stream, q,
                        const_cast<uint16_t *>(k_cache), (uint16_t *)nullptr, (const int32_t *)nullptr, n_past0,
-                       n_heads, n_kv_heads, scale, capacity, capacity, (const float *)nullptr, 0, 0.0f, 0.0f, scores);
+                       n_heads, n_kv_heads, scale, capacity, wlimit, (const float *)nullptr, 0, 0.0f, 0.0f, scores,
+                       q_stride);
     if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
-    return launch_softmax_v(ctx, scores, v_cache, out, nullptr, nullptr, n_past0, n_heads, n_kv_heads, capacity, capacity,
+    return launch_softmax_v(ctx, scores, v_cache, out, nullptr, nullptr, n_past0, n_heads, n_kv_heads, capacity, wlimit,
                             rows);
 }
 
@@ -1293,7 +1341,7 @@ int launch_attn_decode_rope_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k
     const dim3 sgrid((capacity + kScoreP - 1) / kScoreP, n_kv_heads);
     hipLaunchKernelGGL(attn_scores2_kernel<true>, sgrid, dim3(kScoreT), 0, ctx->stream, qkv, k_cache, v_cache, d_pos,
                        n_past, n_heads, n_kv_heads, scale, capacity, capacity, table, n_table, base, freq_scale,
-                       scores);
+                       scores, 0);
     if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
     return launch_softmax_v(ctx, scores, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, capacity, capacity);
 }

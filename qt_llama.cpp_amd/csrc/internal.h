@@ -67,6 +67,7 @@ int launch_gemv_q4_k(mrml_hip_ctx *ctx, const void *w, const void *xpack, float 
 int launch_argmax_f32(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *out);
 // act[i] = gelu_tanh(g[i]) * u[i] for i < n (the matvec kernels' GeGLU epilogue).
 int launch_geglu_rows(mrml_hip_ctx *ctx, const float *g, const float *u, float *act, int n);
+int launch_swiglu_rows(mrml_hip_ctx *ctx, const float *g, const float *u, float *act, int n);
 // GeGLU over an activation pack that also writes the Q8_0 pack of its rows
 // outputs (act nullable).
 int launch_gemv_q4_0_geglu_emit(mrml_hip_ctx *ctx, const void *wg, const void *wu, const void *xpack, float *act,
@@ -158,7 +159,10 @@ int launch_embedding(mrml_hip_ctx *ctx, const void *table, int type, const int32
                      int rows = 1);
 int launch_rope_kv_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache, uint16_t *v_cache, const int32_t *d_pos,
                        int pos, int n_heads, int n_kv_heads, int head_dim, float base, float freq_scale, int capacity,
-                       const float *table, int n_table, int rows = 1);
+                       const float *table, int n_table, int rows = 1, int cache_shift = 0);
+// RoPE of n_heads contiguous heads of vec in place at one position.
+int launch_rope(mrml_hip_ctx *ctx, float *vec, int pos, int n_heads, int head_dim, float base, float freq_scale,
+                const float *table, int n_table);
 int attn_head_dim();
 int attn_max_capacity();
 // The attended window's limit: the capacity, or a sliding window below it
@@ -169,11 +173,11 @@ int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_
                            float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
                            float scale, int capacity, void *scratch, int sliding_window = -1);
 bool attn_rope_ok(int n_heads, int n_kv_heads);
-// `rows` batched queries at positions n_past0.. over stacked q|k|v rows
-// (prefill); scratch of rows * attn_scratch_bytes(n_heads, capacity).
-int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *qkv, const uint16_t *k_cache, const uint16_t *v_cache,
-                         float *out, int n_past0, int rows, int n_heads, int n_kv_heads, float scale, int capacity,
-                         void *scratch);
+// `rows` batched queries at positions n_past0.., query rows q_stride floats
+// apart (prefill); scratch of rows * attn_scratch_bytes(n_heads, capacity).
+int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *q, int q_stride, const uint16_t *k_cache,
+                         const uint16_t *v_cache, float *out, int n_past0, int rows, int n_heads, int n_kv_heads,
+                         float scale, int capacity, void *scratch, int sliding_window = -1);
 int launch_attn_decode_rope_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k_cache, uint16_t *v_cache,
                                 float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
                                 float scale, int capacity, const float *table, int n_table, float base,

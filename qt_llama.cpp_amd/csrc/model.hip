@@ -27,6 +27,9 @@
 #include "device.h"
 #include "internal.h"
 
+// scores of the attention rows of one batched launch held at once
+static constexpr size_t kPrefillScoreBytes = 64u << 20;
+
 struct mrml_hip_gemma2 {
     mrml_hip_gemma2_config cfg{};
     const void *tok_embd = nullptr;
@@ -159,6 +162,72 @@ int mrml_hip_rope_kv_append_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache
                               freq_scale, capacity, d_table, d_table ? n_table : 0);
 }
 
+// CudaDevice::qkv_postprocess_batch (cuda.rs:2478-2519; kernels.rs:1231-1330)
+// without the Gemma-4 head norms, as mrml_hip_rope_kv_append_f16 is the
+// single-token form: `batch` stacked q|k|v rows at positions start_pos + i,
+// row i's K/V to cache row (cache_start + i) % capacity.
+int mrml_hip_rope_kv_append_f16_batch(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache, uint16_t *v_cache,
+                                      int32_t start_pos, int32_t cache_start, int32_t batch, int32_t n_heads,
+                                      int32_t n_kv_heads, int32_t head_dim, float freq_base, float freq_scale,
+                                      int32_t capacity, int32_t k_format, int32_t v_format, const float *d_table,
+                                      int32_t n_table)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, qkv && k_cache && v_cache, "rope_kv_append_f16_batch: null pointer");
+    REQUIRE(ctx, k_format == 0 && v_format == 0,
+            "rope_kv_append_f16_batch: k_format=%d v_format=%d (only f16 caches, format 0)", k_format, v_format);
+    REQUIRE(ctx, n_heads > 0 && n_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && head_dim <= 1024,
+            "rope_kv_append_f16_batch: n_heads=%d n_kv_heads=%d head_dim=%d", n_heads, n_kv_heads, head_dim);
+    // rows of one launch must not share a cache row
+    REQUIRE(ctx, capacity > 0 && batch > 0 && batch <= capacity && batch <= 65535,
+            "rope_kv_append_f16_batch: batch=%d capacity=%d (batch within 1..min(capacity, 65535))", batch,
+            capacity);
+    REQUIRE(ctx, start_pos >= 0 && cache_start >= 0 && start_pos <= INT32_MAX - batch &&
+                     cache_start <= INT32_MAX - batch,
+            "rope_kv_append_f16_batch: start_pos=%d cache_start=%d", start_pos, cache_start);
+    REQUIRE(ctx, ((uintptr_t)d_table & 7) == 0 && n_table >= 0, "rope_kv_append_f16_batch: table");
+    return launch_rope_kv_f16(ctx, qkv, k_cache, v_cache, nullptr, start_pos, n_heads, n_kv_heads, head_dim,
+                              freq_base, freq_scale, capacity, d_table, d_table ? n_table : 0, batch,
+                              cache_start - start_pos);
+}
+
+// CudaDevice::rope_256k (cuda.rs:2248-2285): rope_1d_batched (ops.rs:185-208)
+// of n_heads contiguous heads in place, cos/sin from an optional table.
+int mrml_hip_rope(mrml_hip_ctx *ctx, float *vec, int32_t pos, int32_t head_dim, int32_t n_heads, float freq_base,
+                  float freq_scale, const float *d_table, int32_t n_table)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, vec, "rope: null pointer");
+    REQUIRE(ctx, pos >= 0 && n_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && head_dim <= 1024,
+            "rope: pos=%d n_heads=%d head_dim=%d", pos, n_heads, head_dim);
+    REQUIRE(ctx, ((uintptr_t)d_table & 7) == 0 && n_table >= 0, "rope: table");
+    return launch_rope(ctx, vec, pos, n_heads, head_dim, freq_base, freq_scale, d_table, d_table ? n_table : 0);
+}
+
+// CudaDevice::geglu / swiglu (cuda.rs:2182-2246): out = gelu_tanh(gate) * up,
+// out = silu(gate) * up elementwise (ops.rs:107-130).
+static int glu_args_ok(mrml_hip_ctx *ctx, const char *name, const float *gate, const float *up, const float *out,
+                       int32_t n)
+{
+    REQUIRE(ctx, n >= 0 && n <= INT32_MAX - 255, "%s: n=%d", name, n);
+    REQUIRE(ctx, n == 0 || (gate && up && out), "%s: null pointer", name);
+    return MRML_HIP_OK;
+}
+
+int mrml_hip_geglu(mrml_hip_ctx *ctx, const float *gate, const float *up, float *out, int32_t n)
+{
+    CTX_GUARD(ctx);
+    if (int rc = glu_args_ok(ctx, "geglu", gate, up, out, n)) return rc;
+    return n ? launch_geglu_rows(ctx, gate, up, out, n) : MRML_HIP_OK;
+}
+
+int mrml_hip_swiglu(mrml_hip_ctx *ctx, const float *gate, const float *up, float *out, int32_t n)
+{
+    CTX_GUARD(ctx);
+    if (int rc = glu_args_ok(ctx, "swiglu", gate, up, out, n)) return rc;
+    return n ? launch_swiglu_rows(ctx, gate, up, out, n) : MRML_HIP_OK;
+}
+
 // Arguments shared by the decode-attention entries.
 static int attn_args_ok(mrml_hip_ctx *ctx, const char *name, const float *q, const uint16_t *k_cache,
                         const uint16_t *v_cache, const float *out, const void *pack, int32_t n_past,
@@ -243,6 +312,47 @@ int mrml_hip_attention_causal(mrml_hip_ctx *ctx, const float *q, const uint16_t 
         return rc;
     return attn_exact(ctx, q, k_cache, v_cache, out, nullptr, n_past, nullptr, n_heads, n_kv_heads, scale, capacity,
                       sliding_window);
+}
+
+// CudaDevice::attention_prefill (cuda.rs:2727-2770): `batch` queries at
+// positions cache_start + i, query row i q_stride floats into q (the
+// reference passes q.len() / batch), output rows of n_heads * head_dim.  Row
+// i is bit-identical to mrml_hip_attention_causal at n_past = cache_start + i
+// on the same caches (the K/V of every row already appended).
+int mrml_hip_attention_prefill(mrml_hip_ctx *ctx, const float *q, int32_t q_stride, const uint16_t *k_cache,
+                               const uint16_t *v_cache, float *out, int32_t cache_start, int32_t batch,
+                               int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, float scale,
+                               int32_t sliding_window, int32_t capacity, int32_t k_format, int32_t v_format)
+{
+    CTX_GUARD(ctx);
+    if (int rc = attn_formats_ok(ctx, "attention_prefill", k_format, v_format)) return rc;
+    if (int rc = attn_args_ok(ctx, "attention_prefill", q, k_cache, v_cache, out, nullptr, cache_start, nullptr,
+                              n_heads, n_kv_heads, head_dim, capacity))
+        return rc;
+    REQUIRE(ctx, batch > 0 && cache_start <= INT32_MAX - batch, "attention_prefill: batch=%d cache_start=%d", batch,
+            cache_start);
+    REQUIRE(ctx, q_stride >= n_heads * head_dim, "attention_prefill: q_stride=%d below n_heads * head_dim = %d",
+            q_stride, n_heads * head_dim);
+    const size_t qd = (size_t)n_heads * head_dim;
+    if (!attn_rope_ok(n_heads, n_kv_heads)) {
+        // groups of 5..8 query heads: one decode-attention launch per row
+        for (int i = 0; i < batch; ++i)
+            if (int rc = attn_exact(ctx, q + (size_t)i * q_stride, k_cache, v_cache, out + i * qd, nullptr,
+                                    cache_start + i, nullptr, n_heads, n_kv_heads, scale, capacity, sliding_window))
+                return rc;
+        return MRML_HIP_OK;
+    }
+    // rows per launch: scores of at most kPrefillScoreBytes, grid z within 65535
+    const size_t per = attn_scratch_bytes(n_heads, capacity);
+    const int rn = (int)std::max<size_t>(1, std::min<size_t>(std::min(batch, 65535), kPrefillScoreBytes / per));
+    void *part = workspace(ctx, (size_t)rn * per);
+    if (!part) return MRML_HIP_E_ALLOC;
+    for (int r0 = 0; r0 < batch; r0 += rn)
+        if (int rc = launch_attn_rows_f16(ctx, q + (size_t)r0 * q_stride, q_stride, k_cache, v_cache, out + r0 * qd,
+                                          cache_start + r0, std::min(rn, batch - r0), n_heads, n_kv_heads, scale,
+                                          capacity, part, sliding_window))
+            return rc;
+    return MRML_HIP_OK;
 }
 
 int mrml_hip_attention_causal_split(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache,
@@ -440,7 +550,6 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
 namespace {
 
 constexpr int kPrefillChunk = 128;  // tokens per chunk (prefill_cuda's tile, model.rs:2395-2638)
-constexpr size_t kPrefillScoreBytes = 64u << 20;  // scores of the chunk's attention rows held at once
 
 // Attention rows per launch in a prefill chunk: the whole chunk unless its
 // scores (n_heads * capacity floats a row) would pass kPrefillScoreBytes.
@@ -535,8 +644,8 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
                                     c.rope_base, 1.0f, c.ctx_len, m->rope_table, c.ctx_len, n));
             if (attn_rope_ok(c.n_heads, c.n_kv_heads)) {
                 for (int r0 = 0, rn = prefill_attn_rows(c); r0 < n; r0 += rn)
-                    STEP(launch_attn_rows_f16(ctx, m->pf_qkv + (size_t)r0 * qkvd, kc, vc, m->pf_attn + (size_t)r0 * qd,
-                                              p0 + r0, std::min(rn, n - r0), c.n_heads, c.n_kv_heads, c.attn_scale,
+                    STEP(launch_attn_rows_f16(ctx, m->pf_qkv + (size_t)r0 * qkvd, (int)qkvd, kc, vc,
+                                              m->pf_attn + (size_t)r0 * qd, p0 + r0, std::min(rn, n - r0), c.n_heads, c.n_kv_heads, c.attn_scale,
                                               c.ctx_len, m->pf_scores));
             } else {
                 for (int i = 0; i < n; ++i)

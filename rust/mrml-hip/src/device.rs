@@ -347,6 +347,75 @@ impl HipDevice {
         self.inner.expect(st, "attention_causal");
     }
 
+    /// `CudaDevice::attention_prefill` (cuda.rs:2727-2770): `batch` queries at
+    /// positions `cache_start + i`, query rows `d_q.len / batch` floats apart;
+    /// row i equals `attention_causal` at `n_past = cache_start + i`.
+    #[allow(clippy::too_many_arguments)]
+    pub fn attention_prefill(&self, d_q: &HipBuffer<f32>, d_k_cache: &HipBuffer<u16>, d_v_cache: &HipBuffer<u16>,
+                             d_out: &mut HipBuffer<f32>, cache_start: usize, batch: usize, n_heads: usize,
+                             n_kv_heads: usize, head_dim: usize, scale: f32, sliding_window: Option<usize>,
+                             cache_capacity: usize, k_format: i32, v_format: i32) {
+        let q_stride = d_q.len / batch;
+        assert!(q_stride >= n_heads * head_dim);
+        assert_eq!(d_out.len, batch * n_heads * head_dim);
+        let sw = sliding_window.map(|w| i32_of(w, "sliding_window")).unwrap_or(-1);
+        let st = unsafe {
+            (self.inner.api.attention_prefill)(self.inner.ctx, d_q.ptr, i32_of(q_stride, "q_stride"), d_k_cache.ptr,
+                                               d_v_cache.ptr, d_out.ptr, i32_of(cache_start, "cache_start"),
+                                               i32_of(batch, "batch"), i32_of(n_heads, "n_heads"),
+                                               i32_of(n_kv_heads, "n_kv_heads"), i32_of(head_dim, "head_dim"), scale, sw,
+                                               i32_of(cache_capacity, "cache_capacity"), k_format, v_format)
+        };
+        self.inner.expect(st, "attention_prefill");
+    }
+
+    /// `CudaDevice::qkv_postprocess_batch` (cuda.rs:2478-2519) without the
+    /// Gemma-4 head norms: RoPE of `batch` stacked q|k|v rows at `start_pos + i`
+    /// and their k/v to cache rows `(cache_start + i) % cache_capacity`.
+    #[allow(clippy::too_many_arguments)]
+    pub fn rope_kv_append_f16_batch(&self, qkv: &mut HipBuffer<f32>, k_cache: &mut HipBuffer<u16>,
+                                    v_cache: &mut HipBuffer<u16>, start_pos: usize, cache_start: usize, n_heads: usize,
+                                    n_kv_heads: usize, head_dim: usize, freq_base: f32, batch: usize,
+                                    cache_capacity: usize, k_format: i32, v_format: i32) {
+        assert_eq!(qkv.len, batch * (n_heads + 2 * n_kv_heads) * head_dim);
+        let st = unsafe {
+            (self.inner.api.rope_kv_append_f16_batch)(self.inner.ctx, qkv.ptr, k_cache.ptr, v_cache.ptr,
+                                                      i32_of(start_pos, "start_pos"), i32_of(cache_start, "cache_start"),
+                                                      i32_of(batch, "batch"), i32_of(n_heads, "n_heads"),
+                                                      i32_of(n_kv_heads, "n_kv_heads"), i32_of(head_dim, "head_dim"),
+                                                      freq_base, 1.0, i32_of(cache_capacity, "cache_capacity"),
+                                                      k_format, v_format, std::ptr::null(), 0)
+        };
+        self.inner.expect(st, "rope_kv_append_f16_batch");
+    }
+
+    /// `CudaDevice::rope_256k` (cuda.rs:2248-2285): RoPE of `n_heads` heads of
+    /// `d_vec` in place at position `pos`.
+    pub fn rope_256k(&self, d_vec: &mut HipBuffer<f32>, pos: usize, head_dim: usize, n_heads: usize, freq_base: f32,
+                     freq_scale: f32) {
+        let st = unsafe {
+            (self.inner.api.rope)(self.inner.ctx, d_vec.ptr, i32_of(pos, "pos"), i32_of(head_dim, "head_dim"),
+                                  i32_of(n_heads, "n_heads"), freq_base, freq_scale, std::ptr::null(), 0)
+        };
+        self.inner.expect(st, "rope_256k");
+    }
+
+    /// `CudaDevice::geglu` (cuda.rs:2215-2246): out = gelu_tanh(gate) * up.
+    pub fn geglu(&self, d_gate: &HipBuffer<f32>, d_up: &HipBuffer<f32>, d_out: &mut HipBuffer<f32>) {
+        assert_eq!(d_gate.len, d_up.len);
+        assert_eq!(d_gate.len, d_out.len);
+        let st = unsafe { (self.inner.api.geglu)(self.inner.ctx, d_gate.ptr, d_up.ptr, d_out.ptr, i32_of(d_gate.len, "len")) };
+        self.inner.expect(st, "geglu");
+    }
+
+    /// `CudaDevice::swiglu` (cuda.rs:2182-2213): out = silu(gate) * up.
+    pub fn swiglu(&self, d_gate: &HipBuffer<f32>, d_up: &HipBuffer<f32>, d_out: &mut HipBuffer<f32>) {
+        assert_eq!(d_gate.len, d_up.len);
+        assert_eq!(d_gate.len, d_out.len);
+        let st = unsafe { (self.inner.api.swiglu)(self.inner.ctx, d_gate.ptr, d_up.ptr, d_out.ptr, i32_of(d_gate.len, "len")) };
+        self.inner.expect(st, "swiglu");
+    }
+
     /// Greedy pick over `n` scores: lowest index on ties, NaN never wins.
     pub fn argmax_f32(&self, d_x: &HipBuffer<f32>, n: usize, d_out: &mut HipBuffer<i32>) {
         let st = unsafe { (self.inner.api.argmax_f32)(self.inner.ctx, d_x.ptr, i32_of(n, "n"), d_out.ptr) };

@@ -191,6 +191,11 @@ api! {
     rope_kv_append_f16: fn(Ctx, *mut f32, *mut u16, *mut u16, i32, *const i32, i32, i32, i32, f32, f32, i32, *const f32, i32) -> c_int = "mrml_hip_rope_kv_append_f16";
     attn_decode_f16: fn(Ctx, *const f32, *const u16, *const u16, *mut f32, *mut c_void, i32, *const i32, i32, i32, i32, f32, i32) -> c_int = "mrml_hip_attn_decode_f16";
     attn_decode_f16_split: fn(Ctx, *const f32, *const u16, *const u16, *mut f32, *mut c_void, i32, *const i32, i32, i32, i32, f32, i32) -> c_int = "mrml_hip_attn_decode_f16_split";
+    rope_kv_append_f16_batch: fn(Ctx, *mut f32, *mut u16, *mut u16, i32, i32, i32, i32, i32, i32, f32, f32, i32, i32, i32, *const f32, i32) -> c_int = "mrml_hip_rope_kv_append_f16_batch";
+    rope: fn(Ctx, *mut f32, i32, i32, i32, f32, f32, *const f32, i32) -> c_int = "mrml_hip_rope";
+    geglu: fn(Ctx, *const f32, *const f32, *mut f32, i32) -> c_int = "mrml_hip_geglu";
+    swiglu: fn(Ctx, *const f32, *const f32, *mut f32, i32) -> c_int = "mrml_hip_swiglu";
+    attention_prefill: fn(Ctx, *const f32, i32, *const u16, *const u16, *mut f32, i32, i32, i32, i32, i32, f32, i32, i32, i32, i32) -> c_int = "mrml_hip_attention_prefill";
     attention_causal: fn(Ctx, *const f32, *const u16, *const u16, *mut f32, i32, i32, i32, i32, f32, i32, i32, i32, i32) -> c_int = "mrml_hip_attention_causal";
     attention_causal_split: fn(Ctx, *const f32, *const u16, *const u16, *mut f32, i32, i32, i32, i32, f32, i32, i32, i32, i32) -> c_int = "mrml_hip_attention_causal_split";
     gemma2_create: fn(Ctx, *const MrmlHipGemma2Config, *const c_void, *const f32, *const MrmlHipGemma2Layer, *mut Model) -> c_int = "mrml_hip_gemma2_create";

@@ -330,6 +330,30 @@ def test_swiglu_known_value(orc):
     assert orc.silu(0.0) == 0.0
 
 
+def test_swiglu_reference_case(orc):
+    """ops_test.rs:14-24: swiglu([0, 2, -2], [1, 3, 4]); out[0] exactly 0."""
+    out = orc.swiglu(np.array([0.0, 2.0, -2.0], np.float32), np.array([1.0, 3.0, 4.0], np.float32))
+    assert out[0] == 0.0
+    assert abs(out[1] - 5.28478) < 1e-3
+
+
+def test_swiglu_argument_roles(orc):
+    """ops.rs:123-130: out = silu(gate) * up, not silu(up) * gate: against
+    float64 silu on gate times up.  Bound: a few f32 roundings (expf within
+    1 ulp, the add, the divide and the product), 4e-7 relative."""
+    rng = np.random.default_rng(71)
+    g = (rng.standard_normal(4096) * 4.0).astype(np.float32)
+    u = (rng.standard_normal(4096) * 0.1 + 0.3).astype(np.float32)
+    got = orc.swiglu(g, u).astype(np.float64)
+    g64 = g.astype(np.float64)
+    ref = g64 / (1.0 + np.exp(-g64)) * u.astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 4e-7 * np.abs(ref) + 1e-30)
+    # the elementwise form is silu() of each element
+    assert all(np.float32(got[i]) == np.float32(np.float32(orc.silu(float(g[i]))) * u[i]) for i in range(0, 4096, 97))
+    swapped = orc.swiglu(u, g).astype(np.float64)
+    assert np.max(np.abs(swapped - ref)) > 1e-2
+
+
 def test_rope_batched_equals_per_head(orc):
     # ops_test.rs:142-158, bit equality
     n_heads, hd = 8, 64
