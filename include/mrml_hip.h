@@ -522,8 +522,13 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, int32_t *d_s
  * token step's arithmetic, so the caches end bit-identical to n_tokens calls
  * of mrml_hip_gemma2_step; the last token's logits go to d_logits (nullable:
  * the model's own buffer) and its greedy argmax to d_argmax (nullable).
- * pos0 + n_tokens <= ctx_len (no ring wrap).  The first call allocates the
- * chunk buffers (freed by mrml_hip_gemma2_destroy).  Not capturable. */
+ * Positions may pass ctx_len: a chunk that wraps the ring appends and
+ * attends token by token (its products stay batched), as the token steps
+ * do.  RoPE angles come from the model's host-computed table for positions
+ * below ctx_len and are evaluated on the device past it (double precision,
+ * rounded once: within one ulp of the host C library).  The first call
+ * allocates the chunk buffers (freed by mrml_hip_gemma2_destroy).  Not
+ * capturable. */
 int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, const int32_t *d_tokens, int32_t n_tokens,
                             int32_t pos0, uint16_t *d_k_cache, uint16_t *d_v_cache, float *d_logits,
                             int32_t *d_argmax);

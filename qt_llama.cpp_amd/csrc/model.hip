@@ -605,9 +605,8 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
     CTX_GUARD(ctx);
     REQUIRE(ctx, m && d_tokens && d_k_cache && d_v_cache, "gemma2_prefill: null argument");
     const mrml_hip_gemma2_config &c = m->cfg;
-    REQUIRE(ctx, n_tokens > 0 && pos0 >= 0 && (int64_t)pos0 + n_tokens <= c.ctx_len,
-            "gemma2_prefill: positions %d..%lld must lie inside the cache of %d (no ring wrap)", pos0,
-            (long long)pos0 + n_tokens - 1, c.ctx_len);
+    REQUIRE(ctx, n_tokens > 0 && pos0 >= 0 && (int64_t)pos0 + n_tokens <= INT32_MAX,
+            "gemma2_prefill: n_tokens=%d pos0=%d", n_tokens, pos0);
     REQUIRE(ctx, (((uintptr_t)d_k_cache | (uintptr_t)d_v_cache | (uintptr_t)d_logits) & 15) == 0,
             "gemma2_prefill: caches and logits must be 16-byte aligned");
     const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim, qkvd = qd + 2 * kvd;
@@ -638,20 +637,38 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
             STEP(launch_gemm_q4_0(ctx, L.wq, m->pf_gpack, m->pf_qkv, qd, c.dim, n, qkvd, fast));
             STEP(launch_gemm_q4_0(ctx, L.wk, m->pf_gpack, m->pf_qkv + qd, kvd, c.dim, n, qkvd, fast));
             STEP(launch_gemm_q4_0(ctx, L.wv, m->pf_gpack, m->pf_qkv + qd + kvd, kvd, c.dim, n, qkvd, fast));
-            // every token's rotated k and v enter the cache before any token
-            // attends; token i then reads positions <= p0 + i only
-            STEP(launch_rope_kv_f16(ctx, m->pf_qkv, kc, vc, nullptr, p0, c.n_heads, c.n_kv_heads, c.head_dim,
-                                    c.rope_base, 1.0f, c.ctx_len, m->rope_table, c.ctx_len, n));
-            if (attn_rope_ok(c.n_heads, c.n_kv_heads)) {
-                for (int r0 = 0, rn = prefill_attn_rows(c); r0 < n; r0 += rn)
-                    STEP(launch_attn_rows_f16(ctx, m->pf_qkv + (size_t)r0 * qkvd, (int)qkvd, kc, vc,
-                                              m->pf_attn + (size_t)r0 * qd, p0 + r0, std::min(rn, n - r0), c.n_heads, c.n_kv_heads, c.attn_scale,
-                                              c.ctx_len, m->pf_scores));
+            if ((int64_t)p0 + n > c.ctx_len) {
+                // The chunk wraps the ring: a later token's K/V row replaces
+                // a position an earlier token still attends to, so each token
+                // appends and attends in turn, as its token step does.
+                for (int i = 0; i < n; ++i) {
+                    float *qi = m->pf_qkv + (size_t)i * qkvd;
+                    STEP(launch_rope_kv_f16(ctx, qi, kc, vc, nullptr, p0 + i, c.n_heads, c.n_kv_heads, c.head_dim,
+                                            c.rope_base, 1.0f, c.ctx_len, m->rope_table, c.ctx_len));
+                    if (attn_rope_ok(c.n_heads, c.n_kv_heads))
+                        STEP(launch_attn_rows_f16(ctx, qi, (int)qkvd, kc, vc, m->pf_attn + (size_t)i * qd, p0 + i, 1,
+                                                  c.n_heads, c.n_kv_heads, c.attn_scale, c.ctx_len, m->pf_scores));
+                    else
+                        STEP(launch_attn_decode_f16(ctx, qi, kc, vc, m->pf_attn + (size_t)i * qd, nullptr, nullptr,
+                                                    p0 + i, c.n_heads, c.n_kv_heads, c.attn_scale, c.ctx_len,
+                                                    m->attn_part));
+                }
             } else {
-                for (int i = 0; i < n; ++i)
-                    STEP(launch_attn_decode_f16(ctx, m->pf_qkv + (size_t)i * qkvd, kc, vc,
-                                                m->pf_attn + (size_t)i * qd, nullptr, nullptr, p0 + i, c.n_heads,
-                                                c.n_kv_heads, c.attn_scale, c.ctx_len, m->attn_part));
+                // every token's rotated k and v enter the cache before any token
+                // attends; token i then reads positions <= p0 + i only
+                STEP(launch_rope_kv_f16(ctx, m->pf_qkv, kc, vc, nullptr, p0, c.n_heads, c.n_kv_heads, c.head_dim,
+                                        c.rope_base, 1.0f, c.ctx_len, m->rope_table, c.ctx_len, n));
+                if (attn_rope_ok(c.n_heads, c.n_kv_heads)) {
+                    for (int r0 = 0, rn = prefill_attn_rows(c); r0 < n; r0 += rn)
+                        STEP(launch_attn_rows_f16(ctx, m->pf_qkv + (size_t)r0 * qkvd, (int)qkvd, kc, vc,
+                                                  m->pf_attn + (size_t)r0 * qd, p0 + r0, std::min(rn, n - r0),
+                                                  c.n_heads, c.n_kv_heads, c.attn_scale, c.ctx_len, m->pf_scores));
+                } else {
+                    for (int i = 0; i < n; ++i)
+                        STEP(launch_attn_decode_f16(ctx, m->pf_qkv + (size_t)i * qkvd, kc, vc,
+                                                    m->pf_attn + (size_t)i * qd, nullptr, nullptr, p0 + i, c.n_heads,
+                                                    c.n_kv_heads, c.attn_scale, c.ctx_len, m->attn_part));
+                }
             }
             STEP(gemm_rows(ctx, m, L.wo, m->pf_attn, m->pf_o, c.dim, qd, n));
             STEP(launch_residual_rms_norm(ctx, m->pf_o, L.post_attn_norm, h, h, L.ffn_norm, c.eps, xn, nullptr, c.dim,

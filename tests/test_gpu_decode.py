@@ -588,16 +588,39 @@ def test_gemma2_2b_shape_prefill_equals_fused_steps(backend, dev, synth):
     assert np.array_equal(hist[P:], hist0[P:])
 
 
-def test_gemma2_prefill_rejects_ring_wrap(backend, dev, synth):
+@pytest.mark.parametrize("ctx_len,splits", [(16, [40]), (16, [10, 30]), (48, [1, 139]), (96, [150])])
+def test_gemma2_prefill_wraps_ring(backend, dev, orc, synth, ctx_len, splits):
+    """Prompts longer than the cache: chunks that wrap the ring append and
+    attend token by token (a later token's row replaces a position an
+    earlier one still reads), the rest stay batched.  Caches, the last
+    prompt position's logits and the decode that follows are bit-identical
+    to the token steps, whose tokens equal the oracle's."""
+    cfg = dict(TINY, ctx_len=ctx_len)
+    model = synth.gemma2_model(cfg, seed=16)
+    P = sum(splits)
+    prompt = synth.prompt_tokens(P, cfg["vocab"], seed=11)
+    n_dec = 6
+    print(f"\n[prefill ring] capacity {ctx_len}, splits {splits}", flush=True)
+    first, lg_last, hist, kc, vc = run_gpu_prefill_decode(backend, dev, model, prompt, n_dec, splits)
+    hist0, lg0, kc0, vc0 = run_gpu_decode(backend, dev, model, prompt, n_dec)
+    assert first == hist0[P - 1]
+    assert_bits(lg_last, lg0[P - 1], "logits at the last prompt position")
+    assert np.array_equal(kc, kc0) and np.array_equal(vc, vc0)
+    assert np.array_equal(hist[P:], hist0[P:])
+    want, _, _ = run_oracle_decode(orc, model, prompt, n_dec)
+    assert_same_tokens(hist0, want)
+
+
+def test_gemma2_prefill_rejects_bad_positions(backend, dev, synth):
     model = synth.gemma2_model(TINY, seed=16)
     m = backend.Gemma2Model.from_host(dev, model)
     kc = backend.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
     vc = backend.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
-    toks = backend.HipBuffer.from_host(dev, np.zeros(TINY["ctx_len"] + 1, np.int32))
+    toks = backend.HipBuffer.from_host(dev, np.zeros(8, np.int32))
     with pytest.raises(backend.HipError):
-        m.prefill(toks, TINY["ctx_len"] + 1, 0, kc, vc)
+        m.prefill(toks, 8, -1, kc, vc)
     with pytest.raises(backend.HipError):
-        m.prefill(toks, 8, TINY["ctx_len"] - 4, kc, vc)
+        m.prefill(toks, 0, 0, kc, vc)
     m.close()
 
 
