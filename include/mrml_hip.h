@@ -377,7 +377,10 @@ int mrml_hip_rope_table(mrml_hip_ctx *ctx, float *d_table, int32_t n_pos, int32_
  * place, then k and v stored as f16 (round to nearest even) at cache row
  * pos % capacity of [capacity][n_kv_heads][head_dim] caches.  cos/sin come
  * from d_table (nullable; from mrml_hip_rope_table) for pos < n_table, else
- * are evaluated on the device (double precision rounded to f32). */
+ * are evaluated on the device: powf in double precision rounded once, then
+ * cosf and sinf in the host C library's algorithm (glibc's, bit for bit), so
+ * the rotation has the CPU path's bits unless the host's powf rounds a pair's
+ * frequency the other way (none at base 10000). */
 int mrml_hip_rope_kv_append_f16(mrml_hip_ctx *ctx, float *d_qkv, uint16_t *d_k_cache, uint16_t *d_v_cache,
                                 int32_t pos, const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads,
                                 int32_t head_dim, float freq_base, float freq_scale, int32_t capacity,
@@ -398,7 +401,8 @@ int mrml_hip_rope_kv_append_f16_batch(mrml_hip_ctx *ctx, float *d_qkv, uint16_t 
 /* CudaDevice::rope_256k (cuda.rs:2248-2285): rope_1d_batched (ops.rs:185-208)
  * of n_heads contiguous heads of head_dim floats in d_vec, in place, at
  * position pos; cos/sin from d_table (nullable) for pos < n_table, else
- * evaluated on the device as mrml_hip_rope_kv_append_f16 does.  head_dim
+ * evaluated on the device as mrml_hip_rope_kv_append_f16 does (any position:
+ * the large-argument reduction matches the host's too).  head_dim
  * even, at most 1024. */
 int mrml_hip_rope(mrml_hip_ctx *ctx, float *d_vec, int32_t pos, int32_t head_dim, int32_t n_heads, float freq_base,
                   float freq_scale, const float *d_table, int32_t n_table);
@@ -525,8 +529,9 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, int32_t *d_s
  * Positions may pass ctx_len: a chunk that wraps the ring appends and
  * attends token by token (its products stay batched), as the token steps
  * do.  RoPE angles come from the model's host-computed table for positions
- * below ctx_len and are evaluated on the device past it (double precision,
- * rounded once: within one ulp of the host C library).  The first call
+ * below ctx_len and past it from host-computed powf values and the host C
+ * library's cosf/sinf algorithm on the device, bit-exact at every position.
+ * The first call
  * allocates the chunk buffers (freed by mrml_hip_gemma2_destroy).  Not
  * capturable. */
 int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, const int32_t *d_tokens, int32_t n_tokens,

@@ -212,21 +212,61 @@ __global__ __launch_bounds__(kNormMaxThreads) void embedding_kernel(const uint8_
     norm_store(v, rms_scale(block_seq_sum_sq(v, n4, lds), dim, eps), wv, w_norm != nullptr, xn, pack, n4);
 }
 
+// Where a RoPE kernel takes its angles (ops.rs:185-208: theta = pos *
+// freq_scale / powf(base, 2i/d) in f32, then cosf and sinf):
+//  * table: (cosf, sinf) pairs [n_table][head_dim/2] from the host's libm,
+//    for pos < n_table;
+//  * else freqs: the powf values per pair from the host's libm, theta formed
+//    here and cosf / sinf evaluated with the host libm's algorithm
+//    (libm_f32.h), so every position gets the host's bits;
+//  * else the same with powf in double precision, rounded once.  The host's
+//    powf is not correctly rounded everywhere, so a pair's frequency may then
+//    differ from it by one ulp: 6 of 13280 pairs over ten bases and eleven
+//    head sizes, none at base 10000.
+struct RopeArgs {
+    const float *table;
+    const float *freqs;
+    int n_table;
+    float base, freq_scale;
+    int fused;  // the host libm's FMA build (host_expf_fused)
+};
+
+__host__ inline RopeArgs rope_args(const float *table, int n_table, float base, float freq_scale, const float *freqs)
+{
+    return RopeArgs{table, freqs, table ? n_table : 0, base, freq_scale, (int)host_expf_fused()};
+}
+
+__device__ __forceinline__ void rope_cs(const RopeArgs &r, int pos, int i, int head_dim, float &c, float &s)
+{
+    if (r.table && pos >= 0 && pos < r.n_table) {
+        const float2 cs = reinterpret_cast<const float2 *>(r.table)[(size_t)pos * (head_dim >> 1) + i];
+        c = cs.x;
+        s = cs.y;
+    } else if (r.freqs) {
+        const float theta = (float)pos * r.freq_scale / r.freqs[i];
+        c = mrml_libm::cosf(theta, r.fused != 0);
+        s = mrml_libm::sinf(theta, r.fused != 0);
+    } else {
+        const float expo = (float)(2 * i) / (float)head_dim;
+        const float freq = (float)pow((double)r.base, (double)expo);
+        const float theta = (float)pos * r.freq_scale / freq;
+        c = mrml_libm::cosf(theta, r.fused != 0);
+        s = mrml_libm::sinf(theta, r.fused != 0);
+    }
+}
+
 // RoPE (NeoX half split, ops.rs:185-208) on the q and k heads of a stacked
 // [q | k | v] vector, then k and v appended to the f16 caches at the cache
 // row of `pos` (round to nearest even, as the reference CUDA path stores its
 // cache, kernels.rs:1300-1322).  Cache layout [capacity][n_kv_heads][head_dim];
 // a position past the capacity wraps (kernels.rs:1307-1313).  Rotated q (and
-// k) are written back into qkv.  cos/sin come from `table` ([n_table][half]
-// pairs) when pos < n_table.  Grid: n_heads + 2*n_kv_heads workgroups of
-// head_dim/2 threads.
+// k) are written back into qkv.  Angles as RopeArgs says.  Grid: n_heads +
+// 2*n_kv_heads workgroups of head_dim/2 threads.
 __global__ __launch_bounds__(512) void rope_kv_f16_kernel(float *__restrict__ qkv, uint16_t *__restrict__ k_cache,
                                                           uint16_t *__restrict__ v_cache,
                                                           const int32_t *__restrict__ d_pos, int pos_arg,
-                                                          int n_heads, int n_kv_heads, int head_dim, float base,
-                                                          float freq_scale, int capacity,
-                                                          const float *__restrict__ table, int n_table,
-                                                          int cache_shift)
+                                                          int n_heads, int n_kv_heads, int head_dim,
+                                                          RopeArgs rope, int capacity, int cache_shift)
 {
     // row blockIdx.y of a batch of stacked q|k|v rows at consecutive
     // positions; its K/V enter cache row (position + cache_shift) % capacity
@@ -238,18 +278,7 @@ __global__ __launch_bounds__(512) void rope_kv_f16_kernel(float *__restrict__ qk
     const size_t cache_row = (size_t)(capacity > 0 ? cpos % capacity : cpos) * kv_dim;
     if (g < n_heads + n_kv_heads) {
         float c, s;
-        if (table && pos >= 0 && pos < n_table) {
-            const float2 cs = reinterpret_cast<const float2 *>(table)[(size_t)pos * half + i];
-            c = cs.x;
-            s = cs.y;
-        } else {
-            // the reference's f32 theta; powf, cosf, sinf in double, rounded once
-            const float expo = (float)(2 * i) / (float)head_dim;
-            const float freq = (float)pow((double)base, (double)expo);
-            const float theta = (float)pos * freq_scale / freq;
-            c = (float)cos((double)theta);
-            s = (float)sin((double)theta);
-        }
+        rope_cs(rope, pos, i, head_dim, c, s);
         float *v = qkv + (size_t)g * head_dim;
         const float v0 = v[i], v1 = v[i + half];
         const float r0 = v0 * c - v1 * s;
@@ -382,32 +411,15 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kScoreT = 256;              // threads per score workgroup
 
-__device__ __forceinline__ void rope_cs(const float *table, int n_table, int pos, int i, int head_dim, float base,
-                                        float freq_scale, float &c, float &s)
-{
-    if (table && pos >= 0 && pos < n_table) {
-        const float2 cs = reinterpret_cast<const float2 *>(table)[(size_t)pos * (head_dim >> 1) + i];
-        c = cs.x;
-        s = cs.y;
-    } else {
-        // the reference's f32 theta; powf, cosf, sinf in double, rounded once
-        const float expo = (float)(2 * i) / (float)head_dim;
-        const float freq = (float)pow((double)base, (double)expo);
-        const float theta = (float)pos * freq_scale / freq;
-        c = (float)cos((double)theta);
-        s = (float)sin((double)theta);
-    }
-}
 
 // rope_1d_batched (ops.rs:185-208) over n_heads contiguous heads of one
 // vector in place: head blockIdx.x, pair i = threadIdx.x (head_dim / 2
-// threads), cos/sin from the host table when pos < n_table.
-__global__ __launch_bounds__(512) void rope_heads_kernel(float *__restrict__ vec, int pos, int head_dim, float base,
-                                                         float freq_scale, const float *__restrict__ table, int n_table)
+// threads), angles as RopeArgs says.
+__global__ __launch_bounds__(512) void rope_heads_kernel(float *__restrict__ vec, int pos, int head_dim, RopeArgs rope)
 {
     const int half = head_dim >> 1, i = threadIdx.x;
     float c, sn;
-    rope_cs(table, n_table, pos, i, head_dim, base, freq_scale, c, sn);
+    rope_cs(rope, pos, i, head_dim, c, sn);
     float *v = vec + (size_t)blockIdx.x * head_dim;
     const float v0 = v[i], v1 = v[i + half];
     v[i] = v0 * c - v1 * sn;
@@ -432,9 +444,7 @@ __global__ __launch_bounds__(kScoreT) void attn_scores2_kernel(const float *__re
                                                                uint16_t *__restrict__ v_cache,
                                                                const int32_t *__restrict__ d_pos, int n_past_arg,
                                                                int n_heads, int n_kv_heads, float scale, int capacity, int wlimit,
-                                                               const float *__restrict__ table, int n_table,
-                                                               float base, float freq_scale,
-                                                               float *__restrict__ scores, int q_stride)
+                                                               RopeArgs rope, float *__restrict__ scores, int q_stride)
 {
     constexpr int HD = kAttnHD, P = kScoreP, half = HD / 2;
     __shared__ __align__(16) float q_s[4][HD];
@@ -467,7 +477,7 @@ __global__ __launch_bounds__(kScoreT) void attn_scores2_kernel(const float *__re
     // with i = tid % 128 for every g, so one cos/sin per thread serves q and k
     static_assert(kScoreT % half == 0, "one rotation pair index per thread");
     float c = 1.0f, sn = 0.0f;
-    if (ROPE) rope_cs(table, n_table, pos, tid % half, HD, base, freq_scale, c, sn);
+    if (ROPE) rope_cs(rope, pos, tid % half, HD, c, sn);
     for (int gi = tid; gi < G * half; gi += kScoreT) {
         const int g = gi / half, i = gi % half;
         const float *qh = q_in + (size_t)(kvh * G + g) * HD;
@@ -862,8 +872,7 @@ __global__ __launch_bounds__(kSplitT) void attn_split_kernel(const float *__rest
                                                              uint16_t *__restrict__ v_cache,
                                                              const int32_t *__restrict__ d_pos, int n_past_arg,
                                                              int n_heads, int n_kv_heads, float scale, int capacity, int wlimit,
-                                                             const float *__restrict__ table, int n_table, float base,
-                                                             float freq_scale, float *__restrict__ part, int max_tiles)
+                                                             RopeArgs rope, float *__restrict__ part, int max_tiles)
 {
     constexpr int HD = kAttnHD, P = kSplitP, half = HD / 2;
     __shared__ __align__(16) float q_s[8][HD];
@@ -895,7 +904,7 @@ __global__ __launch_bounds__(kSplitT) void attn_split_kernel(const float *__rest
     // q of the group's heads, rotated with ROPE (thread -> pair i = tid % half)
     static_assert(kSplitT % half == 0, "one rotation pair index per thread");
     float c = 1.0f, sn = 0.0f;
-    if (ROPE) rope_cs(table, n_table, pos, tid % half, HD, base, freq_scale, c, sn);
+    if (ROPE) rope_cs(rope, pos, tid % half, HD, c, sn);
     for (int gi = tid; gi < G * half; gi += kSplitT) {
         const int g = gi / half, i = gi % half;
         const float *qh = q_in + (size_t)(kvh * G + g) * HD;
@@ -1232,19 +1241,19 @@ int launch_embedding(mrml_hip_ctx *ctx, const void *table, int type, const int32
 
 int launch_rope_kv_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache, uint16_t *v_cache, const int32_t *d_pos,
                        int pos, int n_heads, int n_kv_heads, int head_dim, float base, float freq_scale, int capacity,
-                       const float *table, int n_table, int rows, int cache_shift)
+                       const float *table, int n_table, int rows, int cache_shift, const float *freqs)
 {
     hipLaunchKernelGGL(rope_kv_f16_kernel, dim3(n_heads + 2 * n_kv_heads, rows), dim3(head_dim / 2), 0, ctx->stream, qkv,
-                       k_cache, v_cache, d_pos, pos, n_heads, n_kv_heads, head_dim, base, freq_scale, capacity, table,
-                       n_table, cache_shift);
+                       k_cache, v_cache, d_pos, pos, n_heads, n_kv_heads, head_dim,
+                       rope_args(table, n_table, base, freq_scale, freqs), capacity, cache_shift);
     return check_launch(ctx, "rope_kv_f16_kernel");
 }
 
 int launch_rope(mrml_hip_ctx *ctx, float *vec, int pos, int n_heads, int head_dim, float base, float freq_scale,
-                const float *table, int n_table)
+                const float *table, int n_table, const float *freqs)
 {
-    hipLaunchKernelGGL(rope_heads_kernel, dim3(n_heads), dim3(head_dim / 2), 0, ctx->stream, vec, pos, head_dim, base,
-                       freq_scale, table, n_table);
+    hipLaunchKernelGGL(rope_heads_kernel, dim3(n_heads), dim3(head_dim / 2), 0, ctx->stream, vec, pos, head_dim,
+                       rope_args(table, n_table, base, freq_scale, freqs));
     return check_launch(ctx, "rope_heads_kernel");
 }
 
@@ -1292,7 +1301,7 @@ int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_
     if (n_heads / n_kv_heads <= 4) {
         hipLaunchKernelGGL(attn_scores2_kernel<false>, sgrid, dim3(kScoreT), 0, ctx->stream, q,
                            const_cast<uint16_t *>(k_cache), (uint16_t *)nullptr, d_pos, n_past, n_heads, n_kv_heads,
-                           scale, capacity, wlimit, (const float *)nullptr, 0, 0.0f, 0.0f, scores, 0);
+                           scale, capacity, wlimit, RopeArgs{}, scores, 0);
         if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
     } else {
         hipLaunchKernelGGL(attn_scores_kernel, sgrid, dim3(64 * (n_heads / n_kv_heads)), 0, ctx->stream, q, k_cache,
@@ -1320,8 +1329,7 @@ int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *q, int q_stride, const 
     const dim3 sgrid((span + kScoreP - 1) / kScoreP, n_kv_heads, rows);
     hipLaunchKernelGGL(attn_scores2_kernel<false>, sgrid, dim3(kScoreT), 0, ctx->stream, q,
                        const_cast<uint16_t *>(k_cache), (uint16_t *)nullptr, (const int32_t *)nullptr, n_past0,
-                       n_heads, n_kv_heads, scale, capacity, wlimit, (const float *)nullptr, 0, 0.0f, 0.0f, scores,
-                       q_stride);
+                       n_heads, n_kv_heads, scale, capacity, wlimit, RopeArgs{}, scores, q_stride);
     if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
     return launch_softmax_v(ctx, scores, v_cache, out, nullptr, nullptr, n_past0, n_heads, n_kv_heads, capacity, wlimit,
                             rows);
@@ -1335,13 +1343,13 @@ bool attn_rope_ok(int n_heads, int n_kv_heads) { return n_kv_heads > 0 && n_head
 int launch_attn_decode_rope_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k_cache, uint16_t *v_cache,
                                 float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
                                 float scale, int capacity, const float *table, int n_table, float base,
-                                float freq_scale, void *scratch)
+                                float freq_scale, void *scratch, const float *freqs)
 {
     float *scores = reinterpret_cast<float *>(scratch);
     const dim3 sgrid((capacity + kScoreP - 1) / kScoreP, n_kv_heads);
     hipLaunchKernelGGL(attn_scores2_kernel<true>, sgrid, dim3(kScoreT), 0, ctx->stream, qkv, k_cache, v_cache, d_pos,
-                       n_past, n_heads, n_kv_heads, scale, capacity, capacity, table, n_table, base, freq_scale,
-                       scores, 0);
+                       n_past, n_heads, n_kv_heads, scale, capacity, capacity,
+                       rope_args(table, n_table, base, freq_scale, freqs), scores, 0);
     if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
     return launch_softmax_v(ctx, scores, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, capacity, capacity);
 }
@@ -1356,19 +1364,18 @@ size_t attn_split_scratch_bytes(int n_heads, int capacity)
 int launch_attn_split_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k_cache, uint16_t *v_cache, float *out,
                           void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads, float scale,
                           int capacity, bool rope, const float *table, int n_table, float base, float freq_scale,
-                          void *scratch, int sliding_window)
+                          void *scratch, int sliding_window, const float *freqs)
 {
     float *part = reinterpret_cast<float *>(scratch);
     const int tiles = attn_split_tiles(capacity), wlimit = attn_window_limit(capacity, sliding_window);
     const dim3 grid(tiles, n_kv_heads);
+    const RopeArgs ra = rope_args(table, n_table, base, freq_scale, freqs);
     if (rope)
         hipLaunchKernelGGL(attn_split_kernel<true>, grid, dim3(kSplitT), 0, ctx->stream, qkv, k_cache, v_cache, d_pos,
-                           n_past, n_heads, n_kv_heads, scale, capacity, wlimit, table, n_table, base, freq_scale,
-                           part, tiles);
+                           n_past, n_heads, n_kv_heads, scale, capacity, wlimit, ra, part, tiles);
     else
         hipLaunchKernelGGL(attn_split_kernel<false>, grid, dim3(kSplitT), 0, ctx->stream, qkv, k_cache, v_cache,
-                           d_pos, n_past, n_heads, n_kv_heads, scale, capacity, wlimit, table, n_table, base,
-                           freq_scale, part, tiles);
+                           d_pos, n_past, n_heads, n_kv_heads, scale, capacity, wlimit, ra, part, tiles);
     if (int rc = check_launch(ctx, "attn_split_kernel")) return rc;
     hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(kAttnHD), 0, ctx->stream, part, d_pos, n_past,
                        capacity, wlimit, tiles, n_heads, out, (uint8_t *)pack);

@@ -159,10 +159,16 @@ int launch_embedding(mrml_hip_ctx *ctx, const void *table, int type, const int32
                      int rows = 1);
 int launch_rope_kv_f16(mrml_hip_ctx *ctx, float *qkv, uint16_t *k_cache, uint16_t *v_cache, const int32_t *d_pos,
                        int pos, int n_heads, int n_kv_heads, int head_dim, float base, float freq_scale, int capacity,
-                       const float *table, int n_table, int rows = 1, int cache_shift = 0);
+                       const float *table, int n_table, int rows = 1, int cache_shift = 0,
+                       const float *freqs = nullptr);
 // RoPE of n_heads contiguous heads of vec in place at one position.
 int launch_rope(mrml_hip_ctx *ctx, float *vec, int pos, int n_heads, int head_dim, float base, float freq_scale,
-                const float *table, int n_table);
+                const float *table, int n_table, const float *freqs = nullptr);
+// RoPE angles of the kernels above: (cos, sin) from `table` for positions <
+// n_table; else from `freqs` (powf(base, 2i/d) per pair, host libm) with
+// the host libm's cosf/sinf algorithm; else in double precision.  The
+// pair values of fill_rope_freqs give every position the host's bits.
+int fill_rope_freqs(mrml_hip_ctx *ctx, float *d_freqs, int head_dim, float base);
 int attn_head_dim();
 int attn_max_capacity();
 // The attended window's limit: the capacity, or a sliding window below it
@@ -181,7 +187,7 @@ int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *q, int q_stride, const 
 int launch_attn_decode_rope_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k_cache, uint16_t *v_cache,
                                 float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
                                 float scale, int capacity, const float *table, int n_table, float base,
-                                float freq_scale, void *scratch);
+                                float freq_scale, void *scratch, const float *freqs = nullptr);
 
 // Bounded LDS-counter waits (exact_sum.h), one pair of device words per
 // translation unit that has them: polls >= 0 sets the poll limit, timeouts
@@ -200,7 +206,7 @@ size_t attn_split_scratch_bytes(int n_heads, int capacity);
 int launch_attn_split_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k_cache, uint16_t *v_cache, float *out,
                           void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads, float scale,
                           int capacity, bool rope, const float *table, int n_table, float base, float freq_scale,
-                          void *scratch, int sliding_window = -1);
+                          void *scratch, int sliding_window = -1, const float *freqs = nullptr);
 
 // Which form of the C library's expf the host runs (glibc picks its FMA build
 // on x86-64 CPUs with FMA and AVX2); the device reproduces the same one.

@@ -1,5 +1,5 @@
-// libm_f32.h -- f32 tanh and exp with the exact results of the C library the
-// reference links.
+// libm_f32.h -- f32 tanh, exp, sin and cos with the exact results of the C
+// library the reference links.
 //
 // The reference's numerics go through crates/mrml-math/src/lib.rs, which
 // binds glibc's tanhf, expf, sinf, cosf, powf and sqrtf.  A token step only
@@ -18,8 +18,13 @@
 //    in which the reduction r = x N/ln2 - k and the three polynomial steps
 //    are fused multiply-adds; `fused` picks that form.
 //
-// sinf/cosf/powf are not here: RoPE reads a table computed once on the host
-// by the host's own libm.  sqrtf and division are IEEE operations on both.
+//  * sinf, cosf: Arm optimized-routines as well (glibc since 2.28): a
+//    double-precision polynomial after reduction by pi/2, Payne-Hanek for
+//    large arguments.  RoPE's angles are cosf and sinf of
+//    pos * freq_scale / powf(base, 2i/d); the powf values depend on i only
+//    and come from the host's libm.
+//
+// powf is not here.  sqrtf and division are IEEE operations on both.
 //
 // Every function is usable from host code (checked against glibc over the
 // float range) and device code.  Compile with contraction off: each
@@ -213,5 +218,120 @@ MRML_HD float expf_t(float x, bool fused, const uint64_t *tab)
 }
 
 MRML_HD float expf(float x, bool fused) { return expf_t(x, fused, kExpfT.t); }
+
+// ---- sinf / cosf (Arm optimized-routines algorithm) ------------------------------
+//
+// sinf and cosf below follow math/sinf.c, math/cosf.c, math/sincosf.h and
+// math/sincosf_data.c of Arm optimized-routines (the notice above applies):
+// |x| < pi/4: a polynomial in double; |x| < 120: x - n pi/2 with n the
+// rounded x 2/pi; larger: the Payne-Hanek reduction against 96 bits of 2/pi
+// in integer arithmetic; then the sine or cosine polynomial in double,
+// rounded once to float.  `fused` selects the FMA build that glibc picks on
+// x86-64 CPUs with FMA and AVX2 (the same choice as for expf), in which
+// each polynomial step and the fast reduction are fused multiply-adds.
+
+struct SinCosTable {
+    double sign[4];               // sign of the sine in quadrants 0..3
+    double hpi_inv, hpi;          // 2/pi * 2^24, pi/2
+    double c0, c1, c2, c3, c4;    // cosine polynomial
+    double s1, s2, s3;            // sine polynomial
+};
+// Entry 1 negates the cosine polynomial (quadrants 2 and 3).
+constexpr SinCosTable kSinCos[2] = {
+    {{1.0, -1.0, -1.0, 1.0}, 0x1.45f306dc9c883p+23, 0x1.921fb54442d18p+0, 0x1p+0, -0x1.ffffffd0c621cp-2,
+     0x1.55553e1068f19p-5, -0x1.6c087e89a359dp-10, 0x1.99343027bf8c3p-16, -0x1.555545995a603p-3,
+     0x1.1107605230bc4p-7, -0x1.994eb3774cf24p-13},
+    {{1.0, -1.0, -1.0, 1.0}, 0x1.45f306dc9c883p+23, 0x1.921fb54442d18p+0, -0x1p+0, 0x1.ffffffd0c621cp-2,
+     -0x1.55553e1068f19p-5, 0x1.6c087e89a359dp-10, -0x1.99343027bf8c3p-16, -0x1.555545995a603p-3,
+     0x1.1107605230bc4p-7, -0x1.994eb3774cf24p-13},
+};
+// Windows of the bits of 2/pi = 0.a2f9836e4e441529fc2757d1f534ddc0db62...:
+// entry k holds hex digits 2k-6 .. 2k+1 of the fraction (fewer at the start).
+struct InvPio4 {
+    uint32_t w[24];
+};
+constexpr InvPio4 kInvPio4 = {{
+    0xa2u, 0xa2f9u, 0xa2f983u, 0xa2f9836eu, 0xf9836e4eu, 0x836e4e44u, 0x6e4e4415u, 0x4e441529u,
+    0x441529fcu, 0x1529fc27u, 0x29fc2757u, 0xfc2757d1u, 0x2757d1f5u, 0x57d1f534u, 0xd1f534ddu, 0xf534ddc0u,
+    0x34ddc0dbu, 0xddc0db62u, 0xc0db6295u, 0xdb629599u, 0x6295993cu, 0x95993c43u, 0x993c4390u, 0x3c439041u,
+}};
+
+MRML_HD double madd(double a, double b, double c, bool fused) { return fused ? __builtin_fma(a, b, c) : a * b + c; }
+
+// sin (n even) or cos (n odd) of the reduced argument x, x2 = x*x.
+MRML_HD float sincos_poly(double x, double x2, const SinCosTable &p, int n, bool fused)
+{
+    if ((n & 1) == 0) {
+        const double x3 = x * x2;
+        const double s1 = madd(x2, p.s3, p.s2, fused);
+        const double x7 = x3 * x2;
+        const double s = madd(x3, p.s1, x, fused);
+        return (float)madd(x7, s1, s, fused);
+    }
+    const double x4 = x2 * x2;
+    const double c2 = madd(x2, p.c4, p.c3, fused);
+    const double c1 = madd(x2, p.c1, p.c0, fused);
+    const double x6 = x4 * x2;
+    const double c = madd(x4, p.c2, c1, fused);
+    return (float)madd(x6, c2, c, fused);
+}
+
+// x - n pi/2 for |x| < 120, n = round(x 2/pi).
+MRML_HD double reduce_fast(double x, const SinCosTable &p, int &n, bool fused)
+{
+    const double r = x * p.hpi_inv;
+    n = ((int32_t)r + 0x800000) >> 24;
+    return madd(-(double)n, p.hpi, x, fused);
+}
+
+// Payne-Hanek: x mod pi/2 (scaled by 2^-62 * 2 pi) and the quadrant, from the
+// float's bits.
+MRML_HD double reduce_large(uint32_t xi, int &np)
+{
+    const uint32_t *arr = &kInvPio4.w[(xi >> 26) & 15];
+    const int shift = (xi >> 23) & 7;
+    xi = (xi & 0xffffffu) | 0x800000u;
+    xi <<= shift;
+    uint64_t res0 = (uint64_t)(uint32_t)(xi * arr[0]);
+    const uint64_t res1 = (uint64_t)xi * arr[4];
+    const uint64_t res2 = (uint64_t)xi * arr[8];
+    res0 = (res2 >> 32) | (res0 << 32);
+    res0 += res1;
+    const uint64_t n = (res0 + (1ull << 61)) >> 62;
+    res0 -= n << 62;
+    np = (int)n;
+    return (double)(int64_t)res0 * 0x1.921fb54442d18p-62;
+}
+
+// COS = false: sinf, true: cosf.
+template <bool COS>
+MRML_HD float sincosf1(float y, bool fused)
+{
+    const uint32_t top = (f2u(y) >> 20) & 0x7ffu;
+    double x = y;
+    if (top < ((f2u(0x1.921fb6p-1f) >> 20) & 0x7ffu)) {  // |y| < pi/4 (as a float)
+        if (top < ((f2u(0x1p-12f) >> 20) & 0x7ffu)) return COS ? 1.0f : y;
+        return sincos_poly(x, x * x, kSinCos[0], COS ? 1 : 0, fused);
+    }
+    int n;
+    if (top < ((f2u(120.0f) >> 20) & 0x7ffu)) {
+        x = reduce_fast(x, kSinCos[0], n, fused);
+        const double s = kSinCos[0].sign[n & 3];
+        const SinCosTable &p = kSinCos[(n & 2) ? 1 : 0];
+        return sincos_poly(x * s, x * x, p, COS ? n ^ 1 : n, fused);
+    }
+    if (top < ((f2u(__builtin_inff()) >> 20) & 0x7ffu)) {
+        const uint32_t xi = f2u(y);
+        const int sign = (int)(xi >> 31);
+        x = reduce_large(xi, n);
+        const double s = kSinCos[0].sign[(n + sign) & 3];
+        const SinCosTable &p = kSinCos[((n + sign) & 2) ? 1 : 0];
+        return sincos_poly(x * s, x * x, p, COS ? n ^ 1 : n, fused);
+    }
+    return (y - y) / (y - y);  // inf or nan: nan
+}
+
+MRML_HD float sinf(float x, bool fused) { return sincosf1<false>(x, fused); }
+MRML_HD float cosf(float x, bool fused) { return sincosf1<true>(x, fused); }
 
 }  // namespace mrml_libm

@@ -46,6 +46,7 @@ struct mrml_hip_gemma2 {
     void *select_scratch = nullptr;  // partition keys of the sampler's pick
     mrml_hip_sampler sampler{};      // top_k == 0: plain argmax
     float *rope_table = nullptr;  // [ctx_len][head_dim/2] (cos, sin) from the host libm
+    float *rope_freqs = nullptr;  // [head_dim/2] powf(base, 2i/head_dim) from the host libm (positions >= ctx_len)
     // prefill chunk buffers, allocated on the first prefill call: per token
     // rows of h, xn, stacked q|k|v, attention output, o, gate, up,
     // act and f, plus one GEMM pack
@@ -410,7 +411,8 @@ int mrml_hip_gemma2_create(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config *cfg,
                                             : (size_t)0)),
                  o_argmax = take((size_t)argmax_parts(c.vocab) * 8), o_ring = take(recent_ring_bytes()),
                  o_select = take(vocab_select_scratch_bytes(c.vocab, kSamplerTopKMax)),
-                 o_rope = take((size_t)c.ctx_len * c.head_dim * sizeof(float));
+                 o_rope = take((size_t)c.ctx_len * c.head_dim * sizeof(float)),
+                 o_freqs = take((size_t)c.head_dim / 2 * sizeof(float));
     hipError_t e = hipMalloc(&m->arena, off);
     if (e != hipSuccess) {
         delete m;
@@ -432,13 +434,16 @@ int mrml_hip_gemma2_create(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config *cfg,
     m->recent_ring = base + o_ring;
     m->select_scratch = base + o_select;
     m->rope_table = (float *)(base + o_rope);
+    m->rope_freqs = (float *)(base + o_freqs);
     e = hipMemset(m->recent_ring, 0xff, recent_ring_bytes());  // position -1: no entry
     if (e != hipSuccess) {
         (void)hipFree(m->arena);
         delete m;
         return fail(ctx, MRML_HIP_E_HIP, "gemma2_create: hipMemset: %s", hipGetErrorString(e));
     }
-    if (int rc = fill_rope_table(ctx, m->rope_table, c.ctx_len, c.head_dim, c.rope_base, 1.0f)) {
+    int rc = fill_rope_table(ctx, m->rope_table, c.ctx_len, c.head_dim, c.rope_base, 1.0f);
+    if (!rc) rc = fill_rope_freqs(ctx, m->rope_freqs, c.head_dim, c.rope_base);
+    if (rc) {
         (void)hipFree(m->arena);
         delete m;
         return rc;
@@ -498,14 +503,14 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
         if (fast) {
             STEP(launch_attn_split_f16(ctx, m->qkv, kc, vc, nullptr, m->attn_pack, d_pos, 0, c.n_heads, c.n_kv_heads,
                                        c.attn_scale, c.ctx_len, true, m->rope_table, c.ctx_len, c.rope_base, 1.0f,
-                                       m->attn_part));
+                                       m->attn_part, -1, m->rope_freqs));
         } else if (attn_rope_ok(c.n_heads, c.n_kv_heads)) {
             STEP(launch_attn_decode_rope_f16(ctx, m->qkv, kc, vc, nullptr, m->attn_pack, d_pos, 0, c.n_heads,
                                              c.n_kv_heads, c.attn_scale, c.ctx_len, m->rope_table, c.ctx_len,
-                                             c.rope_base, 1.0f, m->attn_part));
+                                             c.rope_base, 1.0f, m->attn_part, m->rope_freqs));
         } else {
             STEP(launch_rope_kv_f16(ctx, m->qkv, kc, vc, d_pos, 0, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_base,
-                                    1.0f, c.ctx_len, m->rope_table, c.ctx_len));
+                                    1.0f, c.ctx_len, m->rope_table, c.ctx_len, 1, 0, m->rope_freqs));
             STEP(launch_attn_decode_f16(ctx, m->qkv, kc, vc, nullptr, m->attn_pack, d_pos, 0, c.n_heads,
                                         c.n_kv_heads, c.attn_scale, c.ctx_len, m->attn_part));
         }
@@ -644,7 +649,8 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
                 for (int i = 0; i < n; ++i) {
                     float *qi = m->pf_qkv + (size_t)i * qkvd;
                     STEP(launch_rope_kv_f16(ctx, qi, kc, vc, nullptr, p0 + i, c.n_heads, c.n_kv_heads, c.head_dim,
-                                            c.rope_base, 1.0f, c.ctx_len, m->rope_table, c.ctx_len));
+                                            c.rope_base, 1.0f, c.ctx_len, m->rope_table, c.ctx_len, 1, 0,
+                                            m->rope_freqs));
                     if (attn_rope_ok(c.n_heads, c.n_kv_heads))
                         STEP(launch_attn_rows_f16(ctx, qi, (int)qkvd, kc, vc, m->pf_attn + (size_t)i * qd, p0 + i, 1,
                                                   c.n_heads, c.n_kv_heads, c.attn_scale, c.ctx_len, m->pf_scores));
@@ -657,7 +663,8 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
                 // every token's rotated k and v enter the cache before any token
                 // attends; token i then reads positions <= p0 + i only
                 STEP(launch_rope_kv_f16(ctx, m->pf_qkv, kc, vc, nullptr, p0, c.n_heads, c.n_kv_heads, c.head_dim,
-                                        c.rope_base, 1.0f, c.ctx_len, m->rope_table, c.ctx_len, n));
+                                        c.rope_base, 1.0f, c.ctx_len, m->rope_table, c.ctx_len, n, 0,
+                                        m->rope_freqs));
                 if (attn_rope_ok(c.n_heads, c.n_kv_heads)) {
                     for (int r0 = 0, rn = prefill_attn_rows(c); r0 < n; r0 += rn)
                         STEP(launch_attn_rows_f16(ctx, m->pf_qkv + (size_t)r0 * qkvd, (int)qkvd, kc, vc,

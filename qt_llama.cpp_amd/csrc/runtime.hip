@@ -78,6 +78,16 @@ bool host_expf_fused()
     return fused;
 }
 
+int fill_rope_freqs(mrml_hip_ctx *ctx, float *d_freqs, int head_dim, float base)
+{
+    float (*volatile f_pow)(float, float) = powf;  // the C library's powf, not a folded constant
+    std::vector<float> f(head_dim / 2);
+    for (int i = 0; i < head_dim / 2; ++i) f[i] = f_pow(base, (float)(2 * i) / (float)head_dim);
+    hipError_t e = hipMemcpyAsync(d_freqs, f.data(), f.size() * sizeof(float), hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? MRML_HIP_OK : hip_fail(ctx, e, "rope frequencies upload");
+}
+
 int fill_rope_table(mrml_hip_ctx *ctx, float *d_table, int n_pos, int head_dim, float base, float freq_scale)
 {
     // Called through pointers so the compiler keeps three separate libm calls

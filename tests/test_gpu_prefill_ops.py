@@ -6,9 +6,8 @@ qkv_postprocess_batch without the Gemma-4 head norms
 (mrml_hip_attention_prefill, cuda.rs:2727-2770); and CudaDevice's
 elementwise ops geglu / swiglu (cuda.rs:2182-2246) and rope_256k
 (cuda.rs:2248-2285).  Bar: bit-identical to the CPU oracle (ops.rs:99-130,
-185-208; model.rs:1457-1590) wherever the angles come from the host table;
-device-evaluated angles within 2e-6 of the largest magnitude, as the
-single-token RoPE entry.
+185-208; model.rs:1457-1590), RoPE angles from the host table or evaluated
+on the device with the host libm's cosf/sinf algorithm.
 """
 
 from __future__ import annotations
@@ -93,13 +92,28 @@ def test_rope_256k(backend, dev, orc, pos, hd, nh, freq_scale):
     dev.rope_256k(vb, pos, hd, nh, 10000.0, freq_scale, table=table, n_table=cap)
     dev.sync()
     assert_bits(vb.numpy(), ref, f"rope_256k pos {pos} head_dim {hd} (table)")
+    # no table: powf in double rounded once (equal to the host's powf at base
+    # 10000 for these head sizes), cosf/sinf in the host libm's algorithm
     vb.copy_from_host(v)
     dev.rope_256k(vb, pos, hd, nh, 10000.0, freq_scale)
     dev.sync()
     got = vb.numpy()
-    assert np.max(np.abs(got - ref)) <= 2e-6 * np.max(np.abs(ref))
+    assert_bits(got, ref, f"rope_256k pos {pos} head_dim {hd} (device angles)")
     if pos == 0:
         assert_bits(got, v, "rope at position 0 is the identity")
+
+
+@pytest.mark.parametrize("pos", [131071, 262143, 1 << 24, 100000007])
+def test_rope_256k_far_positions(backend, dev, orc, pos):
+    """Positions far past any table (rope_256k's name: 256k positions and
+    more): the angles' large-argument reduction (Payne-Hanek) against the
+    host libm, bit-exact."""
+    hd, nh = 256, 8
+    v = np.random.default_rng(4350 + pos % 1000).standard_normal(nh * hd).astype(np.float32)
+    vb = backend.HipBuffer.from_host(dev, v)
+    dev.rope_256k(vb, pos, hd, nh, 10000.0)
+    dev.sync()
+    assert_bits(vb.numpy(), orc.rope_1d_batched(v, pos, nh, hd, 10000.0), f"rope_256k at position {pos}")
 
 
 def test_rope_256k_invalid(backend, dev):
@@ -142,12 +156,8 @@ def test_qkv_postprocess_batch(backend, dev, orc, start_pos, cache_start, batch,
         q_ref = orc.rope_1d_batched(row[:nh * hd], start_pos + i, nh, hd, 10000.0)
         k_ref = orc.rope_1d_batched(row[nh * hd:nh * hd + kvd], start_pos + i, nkv, hd, 10000.0)
         q_got, k_got = got[i, :nh * hd], got[i, nh * hd:nh * hd + kvd]
-        if use_table:
-            assert_bits(q_got, q_ref, f"batch row {i} q")
-            assert_bits(k_got, k_ref, f"batch row {i} k")
-        else:
-            assert np.max(np.abs(q_got - q_ref)) <= 2e-6 * np.max(np.abs(q_ref))
-            assert np.max(np.abs(k_got - k_ref)) <= 2e-6 * np.max(np.abs(k_ref))
+        assert_bits(q_got, q_ref, f"batch row {i} q")
+        assert_bits(k_got, k_ref, f"batch row {i} k")
         assert_bits(got[i, nh * hd + kvd:], row[nh * hd + kvd:], f"batch row {i} v unchanged")
         r = (cache_start + i) % cap
         assert np.array_equal(kh[r], k_got.astype(np.float16).view(np.uint16))

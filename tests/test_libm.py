@@ -1,10 +1,10 @@
-"""The device's f32 tanh/exp (qt_llama.cpp_amd/csrc/libm_f32.h) against the
-host C library the reference links (crates/mrml-math/src/lib.rs binds glibc's
-tanhf/expf).  CPU only: the header is compiled for the host by g++ and every
+"""The device's f32 tanh/exp/sin/cos (qt_llama.cpp_amd/csrc/libm_f32.h)
+against the host C library the reference links (crates/mrml-math/src/lib.rs
+binds glibc's tanhf/expf/sinf/cosf).  CPU only: the header is compiled for the host by g++ and every
 97th float bit pattern (44M values, all exponent ranges) is compared bit for
 bit.  An exhaustive pass over all 2^32 floats is `libm_check 1` (~20 s on 8
-cores); it also reports 0 mismatches for tanhf and for the expf form this
-host's glibc selects."""
+cores); it also reports 0 mismatches for tanhf and for the expf, sinf and
+cosf forms this host's glibc selects."""
 
 from __future__ import annotations
 
@@ -40,11 +40,12 @@ def libm_check(tmp_path_factory):
 def test_tanhf_and_expf_match_host_libm(libm_check):
     out = subprocess.run([str(libm_check), "97"], check=True, capture_output=True, text=True).stdout
     fields = out.split()
-    counts = {fields[i]: int(fields[i + 1]) for i in range(0, 8, 2)}
+    counts = {fields[i]: int(fields[i + 1]) for i in range(0, 16, 2)}
     assert counts["checked"] > 40_000_000
     assert counts["tanhf"] == 0, out
-    key = "expf_fused" if host_expf_fused() else "expf_plain"
-    assert counts[key] == 0, out
+    form = "fused" if host_expf_fused() else "plain"
+    for fn in ("expf", "sinf", "cosf"):
+        assert counts[f"{fn}_{form}"] == 0, out
 
 
 @pytest.fixture(scope="module")
