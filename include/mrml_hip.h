@@ -532,11 +532,17 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, int32_t *d_s
  * below ctx_len and past it from host-computed powf values and the host C
  * library's cosf/sinf algorithm on the device, bit-exact at every position.
  * The first call
- * allocates the chunk buffers (freed by mrml_hip_gemma2_destroy).  Not
- * capturable. */
+ * allocates the chunk buffers (freed by mrml_hip_gemma2_destroy) unless
+ * mrml_hip_gemma2_reserve_prefill has; every later call allocates nothing
+ * and records no memset, so it can be captured into a graph, which then
+ * replays the same positions over the same token buffer. */
 int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, const int32_t *d_tokens, int32_t n_tokens,
                             int32_t pos0, uint16_t *d_k_cache, uint16_t *d_v_cache, float *d_logits,
                             int32_t *d_argmax);
+/* Allocate the prefill's chunk buffers now (synchronous; idempotent), so
+ * that the next mrml_hip_gemma2_prefill can be captured.  No counterpart in
+ * the reference, whose prefill_cuda takes pooled buffers per call. */
+int mrml_hip_gemma2_reserve_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model);
 /* The pick of mrml_hip_gemma2_step and _prefill (step_generation,
  * model.rs:2713-2907): with a sampler, the CPU path's scoring
  * (MRML_HIP_SCORE_CPU of mrml_hip_vocab_select: masks, 30*tanh softcap,

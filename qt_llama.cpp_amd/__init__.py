@@ -188,6 +188,7 @@ _SIGNATURES = {
     "mrml_hip_gemma2_step": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I],
     "mrml_hip_gemma2_activations": [_P, _P, ctypes.POINTER(_P), ctypes.POINTER(_P)],
     "mrml_hip_gemma2_prefill": [_P, _P, _P, _I, _I, _P, _P, _P, _P],
+    "mrml_hip_gemma2_reserve_prefill": [_P, _P],
 }
 _RESTYPE = {
     "mrml_hip_last_error": ctypes.c_char_p,
@@ -664,6 +665,10 @@ class Gemma2Model:
         self.dev._check(self.dev.lib.mrml_hip_gemma2_prefill(self.dev.ctx, self.handle, _ptr(tokens), n_tokens, pos0,
                                                              _ptr(k_cache), _ptr(v_cache), _ptr(logits),
                                                              _ptr(argmax)))
+
+    def reserve_prefill(self) -> None:
+        """Allocate the prefill's chunk buffers now, so a later prefill can be captured."""
+        self.dev._check(self.dev.lib.mrml_hip_gemma2_reserve_prefill(self.dev.ctx, self.handle))
 
     def set_sampler(self, temperature: float = 0.0, top_k: int = 40, valid=None) -> None:
         """Pick with the CPU path's scoring and draw (mrml_hip_gemma2_set_sampler)."""

@@ -604,6 +604,13 @@ int gemm_rows(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const void *w, const float 
 
 }  // namespace
 
+int mrml_hip_gemma2_reserve_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, m, "gemma2_reserve_prefill: null model");
+    return prefill_buffers(ctx, m);
+}
+
 int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t *d_tokens, int32_t n_tokens,
                             int32_t pos0, uint16_t *d_k_cache, uint16_t *d_v_cache, float *d_logits, int32_t *d_argmax)
 {

@@ -203,6 +203,7 @@ api! {
     gemma2_step: fn(Ctx, Model, *mut i32, *mut u16, *mut u16, *mut f32, *mut i32, *mut i32, i32, *const i32, i32) -> c_int = "mrml_hip_gemma2_step";
     gemma2_prefill: fn(Ctx, Model, *const i32, i32, i32, *mut u16, *mut u16, *mut f32, *mut i32) -> c_int = "mrml_hip_gemma2_prefill";
     gemma2_set_sampler: fn(Ctx, Model, *const MrmlHipSampler) -> c_int = "mrml_hip_gemma2_set_sampler";
+    gemma2_reserve_prefill: fn(Ctx, Model) -> c_int = "mrml_hip_gemma2_reserve_prefill";
     gemma2_activations: fn(Ctx, Model, *mut *mut f32, *mut *mut f32) -> c_int = "mrml_hip_gemma2_activations";
     gguf_open: fn(*const c_char, *mut Gguf) -> c_int = "mrml_gguf_open";
     gguf_close: fn(Gguf) -> c_int = "mrml_gguf_close";

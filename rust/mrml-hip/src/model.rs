@@ -162,6 +162,12 @@ impl Gemma2Model {
         })
     }
 
+    /// Allocate the prefill's chunk buffers now, so that a later `prefill`
+    /// can be captured into a graph.
+    pub fn reserve_prefill(&self) -> Result<()> {
+        self.inner.check(unsafe { (self.inner.api.gemma2_reserve_prefill)(self.inner.ctx, self.handle) })
+    }
+
     /// The pick of later steps and prefills: `None` for the plain argmax.
     pub fn set_sampler(&self, sampler: Option<&Sampler<'_>>) -> Result<()> {
         let s = sampler.map(|s| ffi::MrmlHipSampler {

@@ -607,6 +607,38 @@ def test_gemma2_prefill_wraps_ring(backend, dev, orc, synth, ctx_len, splits):
     assert_same_tokens(hist0, want)
 
 
+def test_gemma2_prefill_captured(backend, dev, synth):
+    """After mrml_hip_gemma2_reserve_prefill a prefill allocates nothing, so
+    it can be captured: a graph of a 150-token prefill (two chunks) replayed
+    three times, the caches cleared and the pick reset by the program's own
+    eager copies between replays, leaves caches, logits and pick
+    bit-identical to an eager prefill every time."""
+    cfg = dict(TINY, ctx_len=256)
+    model = synth.gemma2_model(cfg, seed=15)
+    prompt = synth.prompt_tokens(150, cfg["vocab"], seed=8)
+    first, lg_last, _, kc_e, vc_e = run_gpu_prefill_decode(backend, dev, model, prompt, 0, [150])
+    m = backend.Gemma2Model.from_host(dev, model)
+    m.reserve_prefill()
+    m.reserve_prefill()  # idempotent
+    zeros = np.zeros(m.cache_elems(), np.uint16)
+    kc, vc = backend.HipBuffer.from_host(dev, zeros), backend.HipBuffer.from_host(dev, zeros)
+    logits = backend.HipBuffer.alloc(dev, cfg["vocab"])
+    am = backend.HipBuffer.from_host(dev, np.array([-1], np.int32))
+    toks = backend.HipBuffer.from_host(dev, np.asarray(prompt, np.int32))
+    g = dev.capture(lambda: m.prefill(toks, len(prompt), 0, kc, vc, logits=logits, argmax=am))
+    for r in range(3):
+        kc.copy_from_host(zeros)
+        vc.copy_from_host(zeros)
+        am.copy_from_host(np.array([-1], np.int32))
+        g.launch()
+        dev.sync()
+        assert int(am.numpy()[0]) == first, f"replay {r}"
+        assert_bits(logits.numpy(), lg_last, f"logits, replay {r}")
+        assert np.array_equal(kc.numpy(), kc_e) and np.array_equal(vc.numpy(), vc_e), f"caches, replay {r}"
+    g.close()
+    m.close()
+
+
 def test_gemma2_prefill_rejects_bad_positions(backend, dev, synth):
     model = synth.gemma2_model(TINY, seed=16)
     m = backend.Gemma2Model.from_host(dev, model)
