@@ -116,6 +116,27 @@ def test_rope_256k_far_positions(backend, dev, orc, pos):
     assert_bits(vb.numpy(), orc.rope_1d_batched(v, pos, nh, hd, 10000.0), f"rope_256k at position {pos}")
 
 
+@pytest.mark.parametrize("base", [10000.0, 500000.0, 1000000.0])
+def test_rope_256k_random_positions(backend, dev, orc, base):
+    """256 random positions below 2^24 (both reductions of the angle: the
+    fast one below 120 and Payne-Hanek above), 512 pairs each (head_dim
+    1024, so 131072 angles per base), device angles against the oracle's
+    host cosf/sinf: bit-exact.  The host's powf equals powf in double
+    rounded once at every pair of these bases and head size."""
+    hd, nh = 1024, 1
+    rng = np.random.default_rng(4360 + int(base) % 997)
+    positions = np.concatenate([rng.integers(0, 200, 64), rng.integers(0, 1 << 24, 192)])
+    v = rng.standard_normal(nh * hd).astype(np.float32)
+    vb = backend.HipBuffer.from_host(dev, v)
+    outs = []
+    for pos in positions:
+        vb.copy_from_host(v)
+        dev.rope_256k(vb, int(pos), hd, nh, base)
+        outs.append(vb.numpy())
+    for pos, got in zip(positions, outs):
+        assert_bits(got, orc.rope_1d_batched(v, int(pos), nh, hd, base), f"rope_256k base {base} position {pos}")
+
+
 def test_rope_256k_invalid(backend, dev):
     vb = backend.HipBuffer.alloc(dev, 256)
     for pos, hd, nh in ((-1, 256, 1), (0, 255, 1), (0, 2048, 1), (0, 256, 0)):
