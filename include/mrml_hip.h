@@ -413,6 +413,9 @@ int mrml_hip_geglu(mrml_hip_ctx *ctx, const float *d_gate, const float *d_up, fl
  * d_up[i], silu(x) = x / (1 + expf(-x)) (ops.rs:116-130), expf the host C
  * library's, bit-identical to the CPU path. */
 int mrml_hip_swiglu(mrml_hip_ctx *ctx, const float *d_gate, const float *d_up, float *d_out, int32_t n);
+/* CudaDevice::add (cuda.rs:2579-2593): d_out[i] = d_a[i] + d_b[i] for i < n
+ * (one IEEE f32 add each; d_out may alias an input). */
+int mrml_hip_add(mrml_hip_ctx *ctx, const float *d_a, const float *d_b, float *d_out, int32_t n);
 /* CudaDevice::attention_causal (cuda.rs:2658-2697; CPU model.rs:1457-1590)
  * for one token: out[h] = softmax(scale * q[h] . K[t]) . V[t] over the last
  * min(n_past+1, capacity) cache rows, kv head h / (n_heads / n_kv_heads),

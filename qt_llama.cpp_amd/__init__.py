@@ -180,6 +180,7 @@ _SIGNATURES = {
     "mrml_hip_rope": [_P, _P, _I, _I, _I, _F, _F, _P, _I],
     "mrml_hip_geglu": [_P, _P, _P, _P, _I],
     "mrml_hip_swiglu": [_P, _P, _P, _P, _I],
+    "mrml_hip_add": [_P, _P, _P, _P, _I],
     "mrml_hip_attention_prefill": [_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _I, _I],
     "mrml_hip_attention_causal": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _I],
     "mrml_hip_attention_causal_split": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _I],
@@ -558,6 +559,10 @@ class HipDevice:
     def swiglu(self, gate, up, out, n: int) -> None:
         """CudaDevice::swiglu (cuda.rs:2182-2213): out = silu(gate) * up."""
         self._check(self.lib.mrml_hip_swiglu(self.ctx, _ptr(gate), _ptr(up), _ptr(out), n))
+
+    def add(self, a, b, out, n: int) -> None:
+        """CudaDevice::add (cuda.rs:2579-2593): out = a + b."""
+        self._check(self.lib.mrml_hip_add(self.ctx, _ptr(a), _ptr(b), _ptr(out), n))
 
     def attention_prefill(self, q, k_cache, v_cache, out, cache_start: int, batch: int, n_heads: int,
                           n_kv_heads: int, head_dim: int, scale: float, sliding_window, capacity: int,

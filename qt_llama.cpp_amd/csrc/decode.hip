@@ -438,6 +438,14 @@ __global__ __launch_bounds__(256) void swiglu_rows_kernel(const float *__restric
     }
 }
 
+// out[i] = a[i] + b[i] (kernels.rs:732-744's rust_cuda_add_f32; one IEEE add).
+__global__ __launch_bounds__(256) void add_rows_kernel(const float *__restrict__ a, const float *__restrict__ b,
+                                                       float *__restrict__ out, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = a[i] + b[i];
+}
+
 template <bool ROPE>
 __global__ __launch_bounds__(kScoreT) void attn_scores2_kernel(const float *__restrict__ q_in,
                                                                uint16_t *__restrict__ k_cache,
@@ -1255,6 +1263,12 @@ int launch_rope(mrml_hip_ctx *ctx, float *vec, int pos, int n_heads, int head_di
     hipLaunchKernelGGL(rope_heads_kernel, dim3(n_heads), dim3(head_dim / 2), 0, ctx->stream, vec, pos, head_dim,
                        rope_args(table, n_table, base, freq_scale, freqs));
     return check_launch(ctx, "rope_heads_kernel");
+}
+
+int launch_add_rows(mrml_hip_ctx *ctx, const float *a, const float *b, float *out, int n)
+{
+    hipLaunchKernelGGL(add_rows_kernel, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, a, b, out, n);
+    return check_launch(ctx, "add_rows_kernel");
 }
 
 int launch_swiglu_rows(mrml_hip_ctx *ctx, const float *g, const float *u, float *act, int n)

@@ -68,6 +68,7 @@ int launch_argmax_f32(mrml_hip_ctx *ctx, const float *x, int32_t n, int32_t *out
 // act[i] = gelu_tanh(g[i]) * u[i] for i < n (the matvec kernels' GeGLU epilogue).
 int launch_geglu_rows(mrml_hip_ctx *ctx, const float *g, const float *u, float *act, int n);
 int launch_swiglu_rows(mrml_hip_ctx *ctx, const float *g, const float *u, float *act, int n);
+int launch_add_rows(mrml_hip_ctx *ctx, const float *a, const float *b, float *out, int n);
 // GeGLU over an activation pack that also writes the Q8_0 pack of its rows
 // outputs (act nullable).
 int launch_gemv_q4_0_geglu_emit(mrml_hip_ctx *ctx, const void *wg, const void *wu, const void *xpack, float *act,

@@ -229,6 +229,14 @@ int mrml_hip_swiglu(mrml_hip_ctx *ctx, const float *gate, const float *up, float
     return n ? launch_swiglu_rows(ctx, gate, up, out, n) : MRML_HIP_OK;
 }
 
+// CudaDevice::add (cuda.rs:2579-2593): out = a + b elementwise.
+int mrml_hip_add(mrml_hip_ctx *ctx, const float *a, const float *b, float *out, int32_t n)
+{
+    CTX_GUARD(ctx);
+    if (int rc = glu_args_ok(ctx, "add", a, b, out, n)) return rc;
+    return n ? launch_add_rows(ctx, a, b, out, n) : MRML_HIP_OK;
+}
+
 // Arguments shared by the decode-attention entries.
 static int attn_args_ok(mrml_hip_ctx *ctx, const char *name, const float *q, const uint16_t *k_cache,
                         const uint16_t *v_cache, const float *out, const void *pack, int32_t n_past,

@@ -2,6 +2,7 @@
 
 use std::ffi::{c_void, CStr};
 use std::marker::PhantomData;
+use std::sync::atomic::{AtomicUsize, Ordering};
 use std::sync::Arc;
 
 use crate::ffi::{self, Api, Ctx};
@@ -67,7 +68,83 @@ pub struct HipBuffer<T> {
     inner: Arc<Inner>,
     ptr: *mut T,
     len: usize,
+    allocation: Allocation,
     _t: PhantomData<T>,
+}
+
+/// Who frees a buffer's memory (`CudaAllocation`, cuda.rs:1251-1255): the
+/// buffer itself, or the arena it was cut from (kept alive by the buffer).
+enum Allocation {
+    Owned,
+    Arena(Arc<ArenaAllocation>),
+}
+
+struct ArenaAllocation {
+    inner: Arc<Inner>,
+    ptr: *mut c_void,
+    bytes: usize,
+}
+
+unsafe impl Send for ArenaAllocation {}
+unsafe impl Sync for ArenaAllocation {}
+
+impl Drop for ArenaAllocation {
+    fn drop(&mut self) {
+        unsafe { (self.inner.api.free)(self.inner.ctx, self.ptr) };
+    }
+}
+
+/// `CudaArena` (cuda.rs:1274-1331): one device allocation handed out in
+/// 256-byte-aligned pieces; the pieces free nothing, the allocation goes
+/// when the arena and every piece are gone.
+#[derive(Clone)]
+pub struct HipArena {
+    allocation: Arc<ArenaAllocation>,
+    next: Arc<AtomicUsize>,
+}
+
+impl HipArena {
+    pub fn new(device: &HipDevice, bytes: usize) -> Result<Self> {
+        let mut p = std::ptr::null_mut();
+        device.inner.check(unsafe { (device.inner.api.malloc)(device.inner.ctx, bytes.max(1), &mut p) })?;
+        Ok(Self {
+            allocation: Arc::new(ArenaAllocation { inner: device.inner.clone(), ptr: p, bytes }),
+            next: Arc::new(AtomicUsize::new(0)),
+        })
+    }
+
+    /// `len` elements from the arena; `MRML_HIP_E_ALLOC` when it is exhausted.
+    pub fn alloc<T>(&self, len: usize) -> Result<HipBuffer<T>> {
+        let bytes = len.checked_mul(std::mem::size_of::<T>()).ok_or_else(|| Error {
+            status: ffi::MRML_HIP_E_ALLOC,
+            message: "arena allocation size overflows".into(),
+        })?;
+        let aligned = (bytes + 255) & !255;
+        let offset = self.next.fetch_add(aligned, Ordering::Relaxed);
+        if offset + aligned > self.allocation.bytes {
+            self.next.fetch_sub(aligned, Ordering::Relaxed);
+            return Err(Error {
+                status: ffi::MRML_HIP_E_ALLOC,
+                message: format!("arena exhausted: requested {bytes} bytes, {} remain",
+                                 self.allocation.bytes.saturating_sub(offset)),
+            });
+        }
+        Ok(HipBuffer {
+            inner: self.allocation.inner.clone(),
+            ptr: unsafe { (self.allocation.ptr as *mut u8).add(offset) } as *mut T,
+            len,
+            allocation: Allocation::Arena(self.allocation.clone()),
+            _t: PhantomData,
+        })
+    }
+
+    pub fn used_bytes(&self) -> usize {
+        self.next.load(Ordering::Relaxed)
+    }
+
+    pub fn capacity_bytes(&self) -> usize {
+        self.allocation.bytes
+    }
 }
 
 unsafe impl<T: Send> Send for HipBuffer<T> {}
@@ -176,6 +253,37 @@ impl HipDevice {
             (self.inner.api.memcpy_h2d_async)(self.inner.ctx, dst.ptr as *mut c_void, src.as_ptr() as *const c_void,
                                               std::mem::size_of_val(src))
         })
+    }
+
+    /// `CudaDevice::copy_from_host_at_async` (cuda.rs:2352-2376): `src` into
+    /// elements offset.. of `dst`, ordered on the stream (model.rs:1525-1526
+    /// writes KV rows this way).
+    pub fn copy_from_host_at_async<T: Copy>(&self, dst: &mut HipBuffer<T>, offset: usize, src: &[T]) -> Result<()> {
+        assert!(offset + src.len() <= dst.len, "copy_from_host_at_async: {}+{} elements into {}", offset, src.len(),
+                dst.len);
+        self.inner.check(unsafe {
+            (self.inner.api.memcpy_h2d_async)(self.inner.ctx, dst.ptr.add(offset) as *mut c_void,
+                                              src.as_ptr() as *const c_void, std::mem::size_of_val(src))
+        })
+    }
+
+    /// `CudaDevice::add` (cuda.rs:2579-2593): out = a + b elementwise.
+    pub fn add(&self, d_a: &HipBuffer<f32>, d_b: &HipBuffer<f32>, d_out: &mut HipBuffer<f32>) {
+        assert_eq!(d_a.len, d_b.len);
+        assert_eq!(d_a.len, d_out.len);
+        let st = unsafe { (self.inner.api.add)(self.inner.ctx, d_a.ptr, d_b.ptr, d_out.ptr, i32_of(d_a.len, "len")) };
+        self.inner.expect(st, "add");
+    }
+
+    /// `CudaDevice::embedding` (cuda.rs:2595-2623): row `token` of an f32
+    /// table, a device-to-device copy on the stream.
+    pub fn embedding(&self, d_table: &HipBuffer<f32>, d_out: &mut HipBuffer<f32>, token: usize, dim: usize) {
+        assert!((token + 1) * dim <= d_table.len && dim <= d_out.len, "embedding: row {token} of {dim} outside the table");
+        let st = unsafe {
+            (self.inner.api.memcpy_d2d_async)(self.inner.ctx, d_out.ptr as *mut c_void,
+                                              d_table.ptr.add(token * dim) as *const c_void, dim * 4)
+        };
+        self.inner.expect(st, "embedding");
     }
 
     // ---- weights: GGUF blocks in, backend layouts out ----------------------------
@@ -467,7 +575,28 @@ impl<T> HipBuffer<T> {
         let bytes = len.checked_mul(std::mem::size_of::<T>()).expect("allocation size overflows");
         let mut p = std::ptr::null_mut();
         device.inner.check(unsafe { (device.inner.api.malloc)(device.inner.ctx, bytes.max(1), &mut p) })?;
-        Ok(Self { inner: device.inner.clone(), ptr: p as *mut T, len, _t: PhantomData })
+        Ok(Self { inner: device.inner.clone(), ptr: p as *mut T, len, allocation: Allocation::Owned, _t: PhantomData })
+    }
+
+    /// `CudaBuffer::alloc_pooled_on` (cuda.rs:1372-1390).  The library keeps
+    /// no free-list of its own, so this is `alloc_on`; a caller that wants
+    /// reuse without allocation cuts buffers from a `HipArena`.
+    pub fn alloc_pooled_on(device: &HipDevice, len: usize) -> Result<Self> {
+        Self::alloc_on(device, len)
+    }
+
+    /// `CudaBuffer::copy_from_host_at` (cuda.rs:1424-1441): `slice` into
+    /// elements offset.., synchronous.
+    pub fn copy_from_host_at(&mut self, offset: usize, slice: &[T]) -> Result<()>
+    where
+        T: Copy,
+    {
+        assert!(offset + slice.len() <= self.len, "copy_from_host_at: {}+{} elements into {}", offset, slice.len(),
+                self.len);
+        self.inner.check(unsafe {
+            (self.inner.api.memcpy_h2d)(self.inner.ctx, self.ptr.add(offset) as *mut c_void,
+                                        slice.as_ptr() as *const c_void, std::mem::size_of_val(slice))
+        })
     }
 
     /// `CudaBuffer::from_host_on` (cuda.rs:1400-1404).
@@ -532,6 +661,8 @@ impl<T> HipBuffer<T> {
 
 impl<T> Drop for HipBuffer<T> {
     fn drop(&mut self) {
-        unsafe { (self.inner.api.free)(self.inner.ctx, self.ptr as *mut c_void) };
+        if let Allocation::Owned = self.allocation {
+            unsafe { (self.inner.api.free)(self.inner.ctx, self.ptr as *mut c_void) };
+        }
     }
 }

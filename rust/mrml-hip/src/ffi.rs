@@ -195,6 +195,7 @@ api! {
     rope: fn(Ctx, *mut f32, i32, i32, i32, f32, f32, *const f32, i32) -> c_int = "mrml_hip_rope";
     geglu: fn(Ctx, *const f32, *const f32, *mut f32, i32) -> c_int = "mrml_hip_geglu";
     swiglu: fn(Ctx, *const f32, *const f32, *mut f32, i32) -> c_int = "mrml_hip_swiglu";
+    add: fn(Ctx, *const f32, *const f32, *mut f32, i32) -> c_int = "mrml_hip_add";
     attention_prefill: fn(Ctx, *const f32, i32, *const u16, *const u16, *mut f32, i32, i32, i32, i32, i32, f32, i32, i32, i32, i32) -> c_int = "mrml_hip_attention_prefill";
     attention_causal: fn(Ctx, *const f32, *const u16, *const u16, *mut f32, i32, i32, i32, i32, f32, i32, i32, i32, i32) -> c_int = "mrml_hip_attention_causal";
     attention_causal_split: fn(Ctx, *const f32, *const u16, *const u16, *mut f32, i32, i32, i32, i32, f32, i32, i32, i32, i32) -> c_int = "mrml_hip_attention_causal_split";

@@ -19,7 +19,7 @@ mod device;
 mod gguf;
 mod model;
 
-pub use device::{DeviceInfo, HipBuffer, HipDevice, HipGraph};
+pub use device::{DeviceInfo, HipArena, HipBuffer, HipDevice, HipGraph};
 pub use gguf::{GgufFile, GgufTensor};
 pub use model::{Gemma2Config, Gemma2Layer, Gemma2Model, Numerics, Sampler};
 

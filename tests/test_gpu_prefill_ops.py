@@ -66,6 +66,31 @@ def test_geglu_bit_exact(backend, dev, orc, n):
     assert_bits(out.numpy(), orc.geglu(g, u), f"geglu n={n}")
 
 
+@pytest.mark.parametrize("n", [1, 1000, 100003])
+def test_add_bit_exact(backend, dev, n):
+    """CudaDevice::add (cuda.rs:2579-2593): one IEEE f32 add per element, the
+    same bits as numpy's float32 add (NaN where it gives NaN), with
+    infinities, NaN, signed zeros and values whose sum rounds; in place too."""
+    rng = np.random.default_rng(4700 + n)
+    a = (rng.standard_normal(n) * 1e3).astype(np.float32)
+    b = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+    special = np.array([np.inf, -np.inf, np.nan, -0.0, 0.0, 3.4e38, 1e-45, 1.0], np.float32)
+    k = min(n, special.size)
+    a[:k] = special[:k]
+    b[:k] = special[::-1][:k]
+    ab, bb = backend.HipBuffer.from_host(dev, a), backend.HipBuffer.from_host(dev, b)
+    out = backend.HipBuffer.alloc(dev, n)
+    dev.add(ab, bb, out, n)
+    dev.add(ab, bb, ab, n)  # out aliasing an input
+    dev.sync()
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = a + b
+    nan = np.isnan(ref)  # a NaN's payload is the hardware's choice
+    for got, what in ((out.numpy(), "add"), (ab.numpy(), "add in place")):
+        assert np.array_equal(np.isnan(got), nan), what
+        assert_bits(got[~nan], ref[~nan], f"{what} n={n}")
+
+
 def test_glu_empty_and_invalid(backend, dev):
     out = backend.HipBuffer.alloc(dev, 4)
     dev.swiglu(out, out, out, 0)
