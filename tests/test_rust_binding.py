@@ -102,3 +102,44 @@ def test_struct_fields_match_header_order():
     rename = {"type": "type_id"}
     for c, r in _STRUCTS.items():
         assert [rename.get(f, f) for f in c_fields(c)] == rust_fields(r), c
+
+
+def _call_args(src: str, start: int) -> list[str]:
+    """Top-level comma-separated arguments of the call whose '(' is at start."""
+    depth, args, cur = 0, [], []
+    for ch in src[start:]:
+        if ch in "([{":
+            depth += 1
+            if depth == 1:
+                continue
+        elif ch in ")]}":
+            depth -= 1
+            if depth == 0:
+                args.append("".join(cur).strip())
+                return [a for a in args if a]
+        elif ch == "," and depth == 1:
+            args.append("".join(cur).strip())
+            cur = []
+            continue
+        cur.append(ch)
+    raise AssertionError("unbalanced call")
+
+
+def test_crate_calls_match_the_table():
+    """Every `api.<name>` the crate calls is a field of its api! table, called
+    with as many arguments as that entry point takes (the crate is not
+    compiled here, so this is its argument-count check)."""
+    s = (ROOT / "rust/mrml-hip/src/ffi.rs").read_text()
+    body = s[s.index("api! {"):]
+    arity = {name: len([a for a in args.split(",") if a.strip()])
+             for name, args in re.findall(r"(\w+): fn\((.*?)\) -> .*? = \"mrml_[a-z0-9_]+\";", body)}
+    calls = 0
+    for path in sorted((ROOT / "rust/mrml-hip/src").glob("*.rs")):
+        src = path.read_text()
+        for m in re.finditer(r"\bapi\.(\w+)\)\s*\(", src):
+            name = m.group(1)
+            assert name in arity, f"{path.name}: api.{name} is not in the api! table"
+            args = _call_args(src, m.end() - 1)
+            assert len(args) == arity[name], f"{path.name}: api.{name} called with {len(args)} arguments, takes {arity[name]}"
+            calls += 1
+    assert calls > 50
