@@ -493,6 +493,13 @@ typedef struct mrml_hip_gemma2_config {
     float   rope_base, eps, attn_scale;
     int32_t tie_type; /* MRML_HIP_Q4_0 or MRML_HIP_Q8_0: tied embedding / LM-head table */
     int32_t numerics; /* MRML_HIP_NUMERICS_EXACT (0) or MRML_HIP_NUMERICS_FAST */
+    /* Per-layer attention windows (model.rs:590, 1465-1467): with
+     * sliding_window > 0 and swa_period > 0, layer l attends the last
+     * sliding_window positions unless l % swa_period == swa_period - 1 (a
+     * global layer, the whole cache).  Gemma-2: 4096 and 2 (local layers
+     * 0, 2, ...); the reference's 5 local : 1 global pattern: period 6.
+     * 0 and 0: every layer global. */
+    int32_t sliding_window, swa_period;
 } mrml_hip_gemma2_config;
 
 /* Device pointers of one layer: matrices in the backend Q4_0 layout, norm

@@ -752,7 +752,13 @@ int64_t orc_gemma2_step(const orc_gemma2 *m, int64_t token, int64_t pos,
             kc[crow * kvd + i] = orc_f32_to_f16_rne(k[i]);
             vc[crow * kvd + i] = orc_f32_to_f16_rne(v[i]);
         }
-        const size_t count = (size_t)pos + 1, win = count > ctx ? ctx : count, start = count - win;
+        /* windowed layers (model.rs:590, 1465-1467): the last sliding_window
+         * positions, unless the layer is a period's last (global) one */
+        size_t limit = ctx;
+        if (m->sliding_window > 0 && m->swa_period > 0 && l % m->swa_period != m->swa_period - 1 &&
+            (size_t)m->sliding_window < ctx)
+            limit = (size_t)m->sliding_window;
+        const size_t count = (size_t)pos + 1, win = count > limit ? limit : count, start = count - win;
         if (start == 0) {
             orc_attention_f16(q, kc, vc, att, (size_t)pos, (size_t)m->n_heads, (size_t)m->n_kv_heads,
                               hd, m->attn_scale);

@@ -144,6 +144,8 @@ typedef struct orc_gemma2 {
     float   rope_base, eps, attn_scale;
     int32_t tie_q8;          /* 0: tied table is Q4_0, 1: Q8_0 */
     int32_t softcap;         /* apply 30*tanh(x/30) to the logits */
+    int32_t sliding_window;  /* > 0: windowed layers attend the last sliding_window positions */
+    int32_t swa_period;      /* layer l is windowed unless l % swa_period == swa_period - 1 */
     const uint8_t *tok_embd; /* vocab rows of dim, GGUF bytes */
     const float   *output_norm;
     /* per-layer arrays of n_layers pointers */

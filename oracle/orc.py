@@ -27,6 +27,7 @@ class Gemma2(ctypes.Structure):
         ("vocab", ctypes.c_int32), ("ctx", ctypes.c_int32),
         ("rope_base", ctypes.c_float), ("eps", ctypes.c_float), ("attn_scale", ctypes.c_float),
         ("tie_q8", ctypes.c_int32), ("softcap", ctypes.c_int32),
+        ("sliding_window", ctypes.c_int32), ("swa_period", ctypes.c_int32),
         ("tok_embd", _P), ("output_norm", _P),
         ("wq", _P), ("wk", _P), ("wv", _P), ("wo", _P),
         ("wgate", _P), ("wup", _P), ("wdown", _P),
@@ -302,7 +303,8 @@ class OracleGemma2:
 
         self.s = Gemma2(c["n_layers"], c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["ffn_dim"],
                         c["vocab"], c["ctx_len"], c["rope_base"], c["eps"], c["attn_scale"],
-                        int(model["tie_q8"]), int(softcap), _p(model["tok_embd"]), _p(model["output_norm"]),
+                        int(model["tie_q8"]), int(softcap), int(c.get("sliding_window", 0)),
+                        int(c.get("swa_period", 0)), _p(model["tok_embd"]), _p(model["output_norm"]),
                         parr("wq"), parr("wk"), parr("wv"), parr("wo"), parr("w_gate"), parr("w_up"),
                         parr("w_down"), parr("attn_norm"), parr("post_attn_norm"), parr("ffn_norm"),
                         parr("post_ffw_norm"))

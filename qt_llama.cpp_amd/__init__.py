@@ -85,7 +85,8 @@ class Gemma2Config(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in
                 ("n_layers", "dim", "n_heads", "n_kv_heads", "head_dim", "ffn_dim", "vocab", "ctx_len")] + \
                [(n, ctypes.c_float) for n in ("rope_base", "eps", "attn_scale")] + \
-               [("tie_type", ctypes.c_int32), ("numerics", ctypes.c_int32)]
+               [("tie_type", ctypes.c_int32), ("numerics", ctypes.c_int32), ("sliding_window", ctypes.c_int32),
+                ("swa_period", ctypes.c_int32)]
 
 
 NUMERICS_EXACT = 0
@@ -631,7 +632,8 @@ class Gemma2Model:
         c = model["cfg"]
         cfg = Gemma2Config(c["n_layers"], c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["ffn_dim"],
                            c["vocab"], c["ctx_len"], c["rope_base"], c["eps"], c["attn_scale"],
-                           Q8_0 if model["tie_q8"] else Q4_0, numerics)
+                           Q8_0 if model["tie_q8"] else Q4_0, numerics, c.get("sliding_window", 0),
+                           c.get("swa_period", 0))
         qd, kvd = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
         shapes = {"wq": (qd, c["dim"]), "wk": (kvd, c["dim"]), "wv": (kvd, c["dim"]), "wo": (c["dim"], qd),
                   "w_gate": (c["ffn_dim"], c["dim"]), "w_up": (c["ffn_dim"], c["dim"]),

@@ -1357,15 +1357,16 @@ bool attn_rope_ok(int n_heads, int n_kv_heads) { return n_kv_heads > 0 && n_head
 int launch_attn_decode_rope_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k_cache, uint16_t *v_cache,
                                 float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
                                 float scale, int capacity, const float *table, int n_table, float base,
-                                float freq_scale, void *scratch, const float *freqs)
+                                float freq_scale, void *scratch, const float *freqs, int sliding_window)
 {
     float *scores = reinterpret_cast<float *>(scratch);
     const dim3 sgrid((capacity + kScoreP - 1) / kScoreP, n_kv_heads);
+    const int wlimit = attn_window_limit(capacity, sliding_window);
     hipLaunchKernelGGL(attn_scores2_kernel<true>, sgrid, dim3(kScoreT), 0, ctx->stream, qkv, k_cache, v_cache, d_pos,
-                       n_past, n_heads, n_kv_heads, scale, capacity, capacity,
+                       n_past, n_heads, n_kv_heads, scale, capacity, wlimit,
                        rope_args(table, n_table, base, freq_scale, freqs), scores, 0);
     if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
-    return launch_softmax_v(ctx, scores, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, capacity, capacity);
+    return launch_softmax_v(ctx, scores, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, capacity, wlimit);
 }
 
 int attn_split_tiles(int capacity) { return (capacity + kSplitP - 1) / kSplitP; }

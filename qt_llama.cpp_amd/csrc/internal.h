@@ -188,7 +188,8 @@ int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *q, int q_stride, const 
 int launch_attn_decode_rope_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k_cache, uint16_t *v_cache,
                                 float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
                                 float scale, int capacity, const float *table, int n_table, float base,
-                                float freq_scale, void *scratch, const float *freqs = nullptr);
+                                float freq_scale, void *scratch, const float *freqs = nullptr,
+                                int sliding_window = -1);
 
 // Bounded LDS-counter waits (exact_sum.h), one pair of device words per
 // translation unit that has them: polls >= 0 sets the poll limit, timeouts

@@ -80,7 +80,16 @@ int check_model_config(mrml_hip_ctx *ctx, const mrml_hip_gemma2_config &c)
     REQUIRE(ctx, c.numerics == MRML_HIP_NUMERICS_EXACT || c.numerics == MRML_HIP_NUMERICS_FAST,
             "gemma2: numerics=%d is neither EXACT (0) nor FAST (1)", c.numerics);
     REQUIRE(ctx, vocab_select_ok(c.vocab, kSamplerTopKMax), "gemma2: vocab=%d above the sampler's limit", c.vocab);
+    REQUIRE(ctx, c.sliding_window >= 0 && c.swa_period >= 0, "gemma2: sliding_window=%d swa_period=%d",
+            c.sliding_window, c.swa_period);
     return MRML_HIP_OK;
+}
+
+// Layer l's attention window limit for the attention launches: the sliding
+// window on a windowed layer (model.rs:590, 1465-1467), else -1 (the cache).
+int layer_window(const mrml_hip_gemma2_config &c, int l)
+{
+    return c.sliding_window > 0 && c.swa_period > 0 && l % c.swa_period != c.swa_period - 1 ? c.sliding_window : -1;
 }
 
 }  // namespace
@@ -511,16 +520,16 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
         if (fast) {
             STEP(launch_attn_split_f16(ctx, m->qkv, kc, vc, nullptr, m->attn_pack, d_pos, 0, c.n_heads, c.n_kv_heads,
                                        c.attn_scale, c.ctx_len, true, m->rope_table, c.ctx_len, c.rope_base, 1.0f,
-                                       m->attn_part, -1, m->rope_freqs));
+                                       m->attn_part, layer_window(c, l), m->rope_freqs));
         } else if (attn_rope_ok(c.n_heads, c.n_kv_heads)) {
             STEP(launch_attn_decode_rope_f16(ctx, m->qkv, kc, vc, nullptr, m->attn_pack, d_pos, 0, c.n_heads,
                                              c.n_kv_heads, c.attn_scale, c.ctx_len, m->rope_table, c.ctx_len,
-                                             c.rope_base, 1.0f, m->attn_part, m->rope_freqs));
+                                             c.rope_base, 1.0f, m->attn_part, m->rope_freqs, layer_window(c, l)));
         } else {
             STEP(launch_rope_kv_f16(ctx, m->qkv, kc, vc, d_pos, 0, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_base,
                                     1.0f, c.ctx_len, m->rope_table, c.ctx_len, 1, 0, m->rope_freqs));
             STEP(launch_attn_decode_f16(ctx, m->qkv, kc, vc, nullptr, m->attn_pack, d_pos, 0, c.n_heads,
-                                        c.n_kv_heads, c.attn_scale, c.ctx_len, m->attn_part));
+                                        c.n_kv_heads, c.attn_scale, c.ctx_len, m->attn_part, layer_window(c, l)));
         }
         STEP(launch_gemv_q4_0(ctx, L.wo, m->attn_pack, m->o, c.dim, qd, fast));
         if (fused) {
@@ -668,11 +677,12 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
                                             m->rope_freqs));
                     if (attn_rope_ok(c.n_heads, c.n_kv_heads))
                         STEP(launch_attn_rows_f16(ctx, qi, (int)qkvd, kc, vc, m->pf_attn + (size_t)i * qd, p0 + i, 1,
-                                                  c.n_heads, c.n_kv_heads, c.attn_scale, c.ctx_len, m->pf_scores));
+                                                  c.n_heads, c.n_kv_heads, c.attn_scale, c.ctx_len, m->pf_scores,
+                                                  layer_window(c, l)));
                     else
                         STEP(launch_attn_decode_f16(ctx, qi, kc, vc, m->pf_attn + (size_t)i * qd, nullptr, nullptr,
                                                     p0 + i, c.n_heads, c.n_kv_heads, c.attn_scale, c.ctx_len,
-                                                    m->attn_part));
+                                                    m->attn_part, layer_window(c, l)));
                 }
             } else {
                 // every token's rotated k and v enter the cache before any token
@@ -684,12 +694,14 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
                     for (int r0 = 0, rn = prefill_attn_rows(c); r0 < n; r0 += rn)
                         STEP(launch_attn_rows_f16(ctx, m->pf_qkv + (size_t)r0 * qkvd, (int)qkvd, kc, vc,
                                                   m->pf_attn + (size_t)r0 * qd, p0 + r0, std::min(rn, n - r0),
-                                                  c.n_heads, c.n_kv_heads, c.attn_scale, c.ctx_len, m->pf_scores));
+                                                  c.n_heads, c.n_kv_heads, c.attn_scale, c.ctx_len, m->pf_scores,
+                                                  layer_window(c, l)));
                 } else {
                     for (int i = 0; i < n; ++i)
                         STEP(launch_attn_decode_f16(ctx, m->pf_qkv + (size_t)i * qkvd, kc, vc,
                                                     m->pf_attn + (size_t)i * qd, nullptr, nullptr, p0 + i, c.n_heads,
-                                                    c.n_kv_heads, c.attn_scale, c.ctx_len, m->attn_part));
+                                                    c.n_kv_heads, c.attn_scale, c.ctx_len, m->attn_part,
+                                                    layer_window(c, l)));
                 }
             }
             STEP(gemm_rows(ctx, m, L.wo, m->pf_attn, m->pf_o, c.dim, qd, n));

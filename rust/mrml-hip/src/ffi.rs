@@ -57,6 +57,8 @@ pub struct MrmlHipGemma2Config {
     pub attn_scale: f32,
     pub tie_type: i32,
     pub numerics: i32,
+    pub sliding_window: i32,
+    pub swa_period: i32,
 }
 
 #[repr(C)]

@@ -35,6 +35,11 @@ pub struct Gemma2Config {
     /// GGUF type of the tied embedding / LM-head table: `ffi::MRML_HIP_Q4_0` or `_Q8_0`.
     pub tie_type: i32,
     pub numerics: Numerics,
+    /// Per-layer windows (model.rs:590, 1465-1467): with both > 0, layer l
+    /// attends the last `sliding_window` positions unless
+    /// `l % swa_period == swa_period - 1`.  0 and 0: every layer global.
+    pub sliding_window: usize,
+    pub swa_period: usize,
 }
 
 /// One layer's weights: matrices uploaded with `HipDevice::upload_q4_0`,
@@ -93,6 +98,8 @@ impl Gemma2Model {
                 Numerics::Exact => ffi::MRML_HIP_NUMERICS_EXACT,
                 Numerics::Fast => ffi::MRML_HIP_NUMERICS_FAST,
             },
+            sliding_window: cfg.sliding_window as i32,
+            swa_period: cfg.swa_period as i32,
         };
         let ls: Vec<ffi::MrmlHipGemma2Layer> = layers
             .iter()

@@ -699,6 +699,45 @@ def test_gemma2_tiny_ring_long_decode(backend, dev, orc, synth, numerics):
         assert max(errs) <= 2e-2
 
 
+@pytest.mark.parametrize("numerics", [0, 1])
+@pytest.mark.parametrize("n_heads,n_kv_heads", [(2, 1), (8, 1)])
+def test_gemma2_sliding_windows(backend, dev, orc, synth, numerics, n_heads, n_kv_heads):
+    """Per-layer windows (model.rs:590, 1465-1467): four layers, window 6,
+    period 2 (layers 0 and 2 attend their last 6 positions, 1 and 3 the
+    whole cache), a 32-row cache, 44 teacher-forced positions (past the
+    window and around the ring) then 4 decode steps; groups of 2 (RoPE in
+    the scores kernel) and 8 query heads per kv head.  EXACT: logits,
+    tokens and caches bit-identical to the oracle with the same windows, and
+    the chunked prefill (a batched chunk, then one that wraps the ring) equal
+    to the token steps; FAST: logits within the FAST tiny-model bound."""
+    cfg = dict(TINY, n_layers=4, n_heads=n_heads, n_kv_heads=n_kv_heads, ctx_len=32, sliding_window=6, swa_period=2)
+    model = synth.gemma2_model(cfg, seed=41 + n_heads)
+    prompt = synth.prompt_tokens(44, cfg["vocab"], seed=13)
+    n_dec = 4
+    print(f"\n[windows] numerics {numerics}, heads {n_heads}/{n_kv_heads}", flush=True)
+    hist, lg_gpu, kc, vc = run_gpu_decode(backend, dev, model, prompt, n_dec, numerics=numerics)
+    want, lg_ref, o = run_oracle_decode(orc, model, prompt, n_dec)
+    if numerics == 0:
+        assert_same_tokens(hist, want)
+        for s_ in range(len(lg_ref)):
+            assert_bits(lg_gpu[s_], lg_ref[s_], f"logits at position {s_}")
+        assert np.array_equal(kc, o.k_cache) and np.array_equal(vc, o.v_cache)
+        first, lg_last, hist_p, kc_p, vc_p = run_gpu_prefill_decode(backend, dev, model, prompt, n_dec, [30, 14])
+        P = len(prompt)
+        assert first == hist[P - 1]
+        assert_bits(lg_last, lg_gpu[P - 1], "prefill logits at the last prompt position")
+        assert np.array_equal(kc_p, kc) and np.array_equal(vc_p, vc)
+        assert np.array_equal(hist_p[P:], hist[P:])
+    else:
+        errs = [max_rel(a, b) for a, b in zip(lg_gpu[:len(prompt)], lg_ref[:len(prompt)])]
+        print(f"[windows FAST] worst logit max-rel {max(errs):.2e}", flush=True)
+        assert max(errs) <= 2e-2
+    # the windows matter here: without them the last prompt position's logits differ
+    plain = dict(model, cfg=dict(model["cfg"], sliding_window=0, swa_period=0))
+    _, lg_plain, _ = run_oracle_decode(orc, plain, prompt[:len(prompt)], 0)
+    assert not np.array_equal(lg_plain[-1], lg_ref[len(prompt) - 1])
+
+
 def test_gemma2_tiny_graph_equals_eager(backend, dev, synth):
     model = synth.gemma2_model(TINY, seed=12)
     prompt = synth.prompt_tokens(3, TINY["vocab"], seed=4)

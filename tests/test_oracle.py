@@ -818,3 +818,39 @@ def test_vocab_topk_reference_known_answer(orc):
     want.sort(key=lambda e: (-float(e[0]), e[1]))
     assert [t for _, t in want[:K]] == ids.tolist()
     assert np.array_equal(np.array([s for s, _ in want[:K]], np.float32).view(np.uint32), sc.view(np.uint32))
+
+
+# ---------------------------------------------------------------- per-layer windows
+_WIN_CFG = dict(n_layers=1, dim=256, n_heads=2, n_kv_heads=1, head_dim=256, ffn_dim=512, vocab=300, ctx_len=64,
+                rope_base=10000.0, eps=1e-6, attn_scale=1.0 / 16.0)
+
+
+def _oracle_logits(orc, model, tokens):
+    o = orc.OracleGemma2(model)
+    lg = np.zeros(model["cfg"]["vocab"], np.float32)
+    out = []
+    for pos, t in enumerate(tokens):
+        o.step(int(t), pos, logits=lg)
+        out.append(lg.copy())
+    return out
+
+
+def test_windowed_layer_equals_a_ring_of_the_window(orc, synth):
+    """model.rs:590, 1465-1467: a windowed layer attends the last
+    sliding_window positions.  A one-layer model whose layer is windowed
+    (period 2: layer 0 is local) with window 5 must give, at every position,
+    the bits of the same model without windows over a 5-row cache (a ring
+    attends the last min(pos+1, capacity) positions, oldest first); and a
+    period of 1 makes every layer global (the bits of no window at all)."""
+    tokens = synth.prompt_tokens(20, _WIN_CFG["vocab"], seed=31)
+    base = synth.gemma2_model(dict(_WIN_CFG), seed=30)
+    win = dict(base, cfg=dict(base["cfg"], sliding_window=5, swa_period=2))
+    ring = dict(base, cfg=dict(base["cfg"], ctx_len=5))
+    glob = dict(base, cfg=dict(base["cfg"], sliding_window=5, swa_period=1))
+    a, b = _oracle_logits(orc, win, tokens), _oracle_logits(orc, ring, tokens)
+    c, d = _oracle_logits(orc, glob, tokens), _oracle_logits(orc, base, tokens)
+    for pos in range(len(tokens)):
+        assert np.array_equal(a[pos].view(np.uint32), b[pos].view(np.uint32)), pos
+        assert np.array_equal(c[pos].view(np.uint32), d[pos].view(np.uint32)), pos
+    # the window changes the result once positions fall out of it
+    assert not np.array_equal(a[-1], d[-1])
