@@ -23,6 +23,7 @@ Gemma-2 weight set round-trips bit for bit.
 from __future__ import annotations
 
 import struct
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -243,3 +244,50 @@ def test_gemma2_round_trip(gguf, synth, tmp_path):
                     "blk.1.post_attention_norm.weight", "blk.0.post_ffw_norm.weight"} <= names
             assert g.tensors["blk.0.ffn_down.weight"]["dims"][:2] == [512, 256]
             assert g.meta_str("general.architecture") == "gemma2" and g.meta_u32("gemma2.block_count") == 2
+
+
+def _fuzz_seed() -> bytes:
+    """A small file with every value type, a nested array and three tensors."""
+    kvs = [kv("a.u8", 0, struct.pack("<B", 7)), kv("b.i8", 1, struct.pack("<b", -3)),
+           kv("c.u16", 2, struct.pack("<H", 500)), kv("d.i16", 3, struct.pack("<h", -500)),
+           kv("e.u32", 4, struct.pack("<I", 70000)), kv("f.i32", 5, struct.pack("<i", -70000)),
+           kv("g.f32", 6, struct.pack("<f", 1.5)), kv("h.bool", 7, struct.pack("<B", 1)),
+           kv("i.str", 8, s("hello gguf")), kv("j.u64", 10, struct.pack("<Q", 1 << 40)),
+           kv("k.i64", 11, struct.pack("<q", -(1 << 40))), kv("l.f64", 12, struct.pack("<d", 2.25)),
+           kv("m.arr", 9, struct.pack("<IQ", 8, 3) + s("x") + s("yy") + s("zzz")),
+           kv("n.nested", 9, struct.pack("<IQ", 9, 2) + struct.pack("<IQ", 4, 2) + struct.pack("<II", 1, 2) +
+              struct.pack("<IQ", 6, 1) + struct.pack("<f", 0.5)),
+           kv("general.alignment", 4, struct.pack("<I", 32))]
+    tensors = [tensor_entry("t.f32", [8, 2], 0, 0), tensor_entry("t.q8", [32, 2], 8, 64),
+               tensor_entry("t.q4", [64], 2, 160)]
+    head = gguf_bytes(kvs, tensors)
+    pad = (-len(head)) % 32
+    return head + b"\0" * pad + bytes(range(256)) * 1
+
+
+def test_reader_mutation_fuzz_under_sanitizers(tmp_path):
+    """The reader under AddressSanitizer and UBSan (host code only): 20000
+    mutants of a file with every value type, nested arrays and three tensors
+    (random byte overwrites, extreme 64-bit lengths, small type ids and
+    counts, cuts) are opened and walked completely -- every key's readings,
+    every tensor's info, name lookup and bytes.  A memory error, leak or
+    undefined behaviour aborts the program, so a clean exit is the check."""
+    import shutil
+    import subprocess
+    if shutil.which("g++") is None:
+        pytest.skip("g++ not available")
+    root = Path(__file__).resolve().parents[1]
+    exe = tmp_path / "gguf_fuzz"
+    r = subprocess.run(["g++", "-O1", "-g", "-std=c++17", "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
+                        str(root / "tests/native/gguf_fuzz.cpp"), str(root / "qt_llama.cpp_amd/csrc/gguf.cpp"),
+                        "-I", str(root / "include"), "-o", str(exe)], capture_output=True, text=True)
+    if r.returncode != 0 and "asan" in (r.stderr or "").lower():
+        pytest.skip("AddressSanitizer runtime not available")
+    assert r.returncode == 0, r.stderr[-2000:]
+    seed = tmp_path / "seed.gguf"
+    seed.write_bytes(_fuzz_seed())
+    out = subprocess.run([str(exe), str(seed), str(tmp_path / "mutant.gguf"), "20000", "7"], capture_output=True,
+                         text=True, timeout=600, env={"ASAN_OPTIONS": "detect_leaks=1"})
+    assert out.returncode == 0, (out.stdout[-500:], out.stderr[-3000:])
+    fields = out.stdout.split()
+    assert fields[0] == "ok" and int(fields[1]) == 20000 and int(fields[2]) > 1000, out.stdout
