@@ -456,8 +456,7 @@ def cpu_best_of(fn, budget_s: float) -> tuple[float, int]:
 def q8_0_bench(be, synth, dev, ev, cpu_s: float) -> dict:
     """Q8_0 2048x2048 batch-1 matvec, x quantised once by
     the reference routine, weights rotated over 128 copies (570 MB, more than
-    twice the MALL).  Bytes per run as the survey states them: W + x (f32) +
-    y (f32)."""
+    twice the MALL).  Algorithmic bytes per run: W + x (f32) + y (f32)."""
     rows = cols = 2048
     nbytes_w = rows * cols // 32 * 34
     nbytes = nbytes_w + cols * 4 + rows * 4
