@@ -332,11 +332,16 @@ __global__ __launch_bounds__(512) void attn_scores_kernel(const float *__restric
                                                           const uint16_t *__restrict__ k_cache,
                                                           const int32_t *__restrict__ d_pos, int n_past_arg,
                                                           int n_heads, int n_kv_heads, float scale, int capacity, int wlimit,
-                                                          float *__restrict__ scores)
+                                                          float *__restrict__ scores, int q_stride)
 {
     constexpr int HD = kAttnHD, P = kScoreP;
     __shared__ __align__(16) float q_s[8][HD];
     __shared__ __align__(16) uint8_t k_s[P * kKRow];
+    // query row blockIdx.z of a batch (prefill): rows q_stride floats apart
+    // at consecutive positions
+    q += (size_t)blockIdx.z * q_stride;
+    scores += (size_t)blockIdx.z * n_heads * capacity;
+    n_past_arg += (int)blockIdx.z;
     int window, start;
     attn_window(d_pos, n_past_arg, wlimit, window, start);
     const int p0 = blockIdx.x * P;
@@ -1319,7 +1324,7 @@ int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_
         if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
     } else {
         hipLaunchKernelGGL(attn_scores_kernel, sgrid, dim3(64 * (n_heads / n_kv_heads)), 0, ctx->stream, q, k_cache,
-                           d_pos, n_past, n_heads, n_kv_heads, scale, capacity, wlimit, scores);
+                           d_pos, n_past, n_heads, n_kv_heads, scale, capacity, wlimit, scores, 0);
         if (int rc = check_launch(ctx, "attn_scores_kernel")) return rc;
     }
     return launch_softmax_v(ctx, scores, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, capacity, wlimit);
@@ -1331,7 +1336,7 @@ int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_
 // when q is the projection itself); output row r (n_heads*head_dim f32) goes
 // to out.  Each row's arithmetic is that of launch_attn_decode_f16 at its
 // position with the same sliding window.  scratch holds rows * n_heads *
-// capacity floats.  Needs n_heads / n_kv_heads <= 4 (attn_rope_ok).
+// capacity floats.  Groups of up to 8 query heads per kv head.
 int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *q, int q_stride, const uint16_t *k_cache,
                          const uint16_t *v_cache, float *out, int n_past0, int rows, int n_heads, int n_kv_heads,
                          float scale, int capacity, void *scratch, int sliding_window)
@@ -1341,10 +1346,17 @@ int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *q, int q_stride, const 
     // score tiles up to the widest row window (the host knows every row's position)
     const int span = std::min(wlimit, n_past0 + rows);
     const dim3 sgrid((span + kScoreP - 1) / kScoreP, n_kv_heads, rows);
-    hipLaunchKernelGGL(attn_scores2_kernel<false>, sgrid, dim3(kScoreT), 0, ctx->stream, q,
-                       const_cast<uint16_t *>(k_cache), (uint16_t *)nullptr, (const int32_t *)nullptr, n_past0,
-                       n_heads, n_kv_heads, scale, capacity, wlimit, RopeArgs{}, scores, q_stride);
-    if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
+    if (attn_rope_ok(n_heads, n_kv_heads)) {
+        hipLaunchKernelGGL(attn_scores2_kernel<false>, sgrid, dim3(kScoreT), 0, ctx->stream, q,
+                           const_cast<uint16_t *>(k_cache), (uint16_t *)nullptr, (const int32_t *)nullptr, n_past0,
+                           n_heads, n_kv_heads, scale, capacity, wlimit, RopeArgs{}, scores, q_stride);
+        if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
+    } else {
+        hipLaunchKernelGGL(attn_scores_kernel, sgrid, dim3(64 * (n_heads / n_kv_heads)), 0, ctx->stream, q, k_cache,
+                           (const int32_t *)nullptr, n_past0, n_heads, n_kv_heads, scale, capacity, wlimit, scores,
+                           q_stride);
+        if (int rc = check_launch(ctx, "attn_scores_kernel")) return rc;
+    }
     return launch_softmax_v(ctx, scores, v_cache, out, nullptr, nullptr, n_past0, n_heads, n_kv_heads, capacity, wlimit,
                             rows);
 }

@@ -182,6 +182,7 @@ int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_
 bool attn_rope_ok(int n_heads, int n_kv_heads);
 // `rows` batched queries at positions n_past0.., query rows q_stride floats
 // apart (prefill); scratch of rows * attn_scratch_bytes(n_heads, capacity).
+// Groups of up to 8 query heads per kv head.
 int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *q, int q_stride, const uint16_t *k_cache,
                          const uint16_t *v_cache, float *out, int n_past0, int rows, int n_heads, int n_kv_heads,
                          float scale, int capacity, void *scratch, int sliding_window = -1);

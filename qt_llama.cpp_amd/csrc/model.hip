@@ -352,14 +352,6 @@ int mrml_hip_attention_prefill(mrml_hip_ctx *ctx, const float *q, int32_t q_stri
     REQUIRE(ctx, q_stride >= n_heads * head_dim, "attention_prefill: q_stride=%d below n_heads * head_dim = %d",
             q_stride, n_heads * head_dim);
     const size_t qd = (size_t)n_heads * head_dim;
-    if (!attn_rope_ok(n_heads, n_kv_heads)) {
-        // groups of 5..8 query heads: one decode-attention launch per row
-        for (int i = 0; i < batch; ++i)
-            if (int rc = attn_exact(ctx, q + (size_t)i * q_stride, k_cache, v_cache, out + i * qd, nullptr,
-                                    cache_start + i, nullptr, n_heads, n_kv_heads, scale, capacity, sliding_window))
-                return rc;
-        return MRML_HIP_OK;
-    }
     // rows per launch: scores of at most kPrefillScoreBytes, grid z within 65535
     const size_t per = attn_scratch_bytes(n_heads, capacity);
     const int rn = (int)std::max<size_t>(1, std::min<size_t>(std::min(batch, 65535), kPrefillScoreBytes / per));
@@ -675,14 +667,9 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
                     STEP(launch_rope_kv_f16(ctx, qi, kc, vc, nullptr, p0 + i, c.n_heads, c.n_kv_heads, c.head_dim,
                                             c.rope_base, 1.0f, c.ctx_len, m->rope_table, c.ctx_len, 1, 0,
                                             m->rope_freqs));
-                    if (attn_rope_ok(c.n_heads, c.n_kv_heads))
-                        STEP(launch_attn_rows_f16(ctx, qi, (int)qkvd, kc, vc, m->pf_attn + (size_t)i * qd, p0 + i, 1,
-                                                  c.n_heads, c.n_kv_heads, c.attn_scale, c.ctx_len, m->pf_scores,
-                                                  layer_window(c, l)));
-                    else
-                        STEP(launch_attn_decode_f16(ctx, qi, kc, vc, m->pf_attn + (size_t)i * qd, nullptr, nullptr,
-                                                    p0 + i, c.n_heads, c.n_kv_heads, c.attn_scale, c.ctx_len,
-                                                    m->attn_part, layer_window(c, l)));
+                    STEP(launch_attn_rows_f16(ctx, qi, (int)qkvd, kc, vc, m->pf_attn + (size_t)i * qd, p0 + i, 1,
+                                              c.n_heads, c.n_kv_heads, c.attn_scale, c.ctx_len, m->pf_scores,
+                                              layer_window(c, l)));
                 }
             } else {
                 // every token's rotated k and v enter the cache before any token
@@ -690,19 +677,11 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
                 STEP(launch_rope_kv_f16(ctx, m->pf_qkv, kc, vc, nullptr, p0, c.n_heads, c.n_kv_heads, c.head_dim,
                                         c.rope_base, 1.0f, c.ctx_len, m->rope_table, c.ctx_len, n, 0,
                                         m->rope_freqs));
-                if (attn_rope_ok(c.n_heads, c.n_kv_heads)) {
-                    for (int r0 = 0, rn = prefill_attn_rows(c); r0 < n; r0 += rn)
-                        STEP(launch_attn_rows_f16(ctx, m->pf_qkv + (size_t)r0 * qkvd, (int)qkvd, kc, vc,
-                                                  m->pf_attn + (size_t)r0 * qd, p0 + r0, std::min(rn, n - r0),
-                                                  c.n_heads, c.n_kv_heads, c.attn_scale, c.ctx_len, m->pf_scores,
-                                                  layer_window(c, l)));
-                } else {
-                    for (int i = 0; i < n; ++i)
-                        STEP(launch_attn_decode_f16(ctx, m->pf_qkv + (size_t)i * qkvd, kc, vc,
-                                                    m->pf_attn + (size_t)i * qd, nullptr, nullptr, p0 + i, c.n_heads,
-                                                    c.n_kv_heads, c.attn_scale, c.ctx_len, m->attn_part,
-                                                    layer_window(c, l)));
-                }
+                for (int r0 = 0, rn = prefill_attn_rows(c); r0 < n; r0 += rn)
+                    STEP(launch_attn_rows_f16(ctx, m->pf_qkv + (size_t)r0 * qkvd, (int)qkvd, kc, vc,
+                                              m->pf_attn + (size_t)r0 * qd, p0 + r0, std::min(rn, n - r0),
+                                              c.n_heads, c.n_kv_heads, c.attn_scale, c.ctx_len, m->pf_scores,
+                                              layer_window(c, l)));
             }
             STEP(gemm_rows(ctx, m, L.wo, m->pf_attn, m->pf_o, c.dim, qd, n));
             STEP(launch_residual_rms_norm(ctx, m->pf_o, L.post_attn_norm, h, h, L.ffn_norm, c.eps, xn, nullptr, c.dim,
