@@ -1016,6 +1016,97 @@ __global__ __launch_bounds__(kSplitT) void attn_split_kernel(const float *__rest
     }
 }
 
+// Prefill form of attn_softmax_v_kernel: one workgroup per (query row, kv
+// head), thread d = output dim d of each of the group's G query heads.  Each
+// row's arithmetic is the decode form's -- per head the max over the window,
+// e_p = expf(s_p - max), the ordered exp sum, p_p = e_p * (1/sum), out[d] =
+// 0 + p_0 v_0[d] + p_1 v_1[d] + ... in order -- but the softmax is formed
+// once per head rather than once per 32-dim slice, and each thread runs its
+// dim's chains, one per head of the group, over V rows read straight from
+// the cache: every V load feeds G chains, and the next 32 positions' loads
+// are in flight while the current 32 are added.  The decode form spreads
+// one long row over eight workgroups to cut its latency; a prefill chunk has
+// rows enough to fill the GPU this way.  Windows up to kRowsSvMax positions
+// and groups up to kRowsSvG heads (one exact block sum per head).
+constexpr int kRowsSvMax = 2048;
+constexpr int kRowsSvG = 4;
+constexpr int kRowsSvB = 32;  // positions per load batch
+static_assert(kRowsSvMax <= mrml_xsum::kMaxPerThread * kAttnHD, "one block sum per head");
+
+__global__ __launch_bounds__(kAttnHD) void attn_softmax_v_rows_kernel(const float *__restrict__ scores,
+                                                                      const uint16_t *__restrict__ v_cache,
+                                                                      int n_past0, int n_heads, int n_kv_heads,
+                                                                      int capacity, int wlimit, int expf_fused,
+                                                                      float *__restrict__ out)
+{
+    constexpr int HD = kAttnHD, B = kRowsSvB;
+    __shared__ __align__(16) float e_s[kRowsSvG][kRowsSvMax];
+    __shared__ uint8_t flags[kRowsSvMax];
+    __shared__ mrml_xsum::Shared xs;
+    __shared__ float red[HD / 64];
+    __shared__ uint64_t exp_tab[32];
+    const int kvh = blockIdx.x, z = blockIdx.y, d = threadIdx.x, G = n_heads / n_kv_heads;
+    int window, start;
+    attn_window(nullptr, n_past0 + z, wlimit, window, start);
+    if (d < 32) exp_tab[d] = mrml_libm::kExpfT.t[d];
+    const bool fused = expf_fused != 0;
+    for (int g = 0; g < G; ++g) {
+        const float *sc = scores + ((size_t)z * n_heads + kvh * G + g) * capacity;
+        float mx = -INFINITY;  // the max is exact in any order
+        for (int p = d; p < window; p += HD) mx = fmaxf(mx, sc[p]);
+        mx = wave_max_f32(mx);
+        if ((d & 63) == 0) red[d >> 6] = mx;
+        __syncthreads();
+        mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        for (int p = d; p < window; p += HD) e_s[g][p] = mrml_libm::expf_t(sc[p] - mx, fused, exp_tab);
+        __syncthreads();  // also: every thread has read red before the next head rewrites it
+        const float sum = mrml_xsum::block_seq_sum_nonneg(e_s[g], window, flags, xs);  // ends with a barrier
+        if (sum > 0.0f) {
+            const float inv = 1.0f / sum;
+            for (int p = d; p < window; p += HD) e_s[g][p] = e_s[g][p] * inv;
+        }
+    }
+    __syncthreads();
+    const size_t kv_dim = (size_t)n_kv_heads * HD;
+    const uint16_t *vb = v_cache + (size_t)kvh * HD + d;
+    float acc[kRowsSvG];
+#pragma unroll
+    for (int g = 0; g < kRowsSvG; ++g) acc[g] = 0.0f;
+    int row = (int)cache_row_of(start, capacity);  // the window's rows are consecutive modulo capacity
+    // unconditional loads (row stays a cache row; positions past the window
+    // are skipped by add), so all B of them are issued before any is used
+    auto load = [&](float (&v)[B], int) {
+        uint16_t raw[B];
+#pragma unroll
+        for (int k = 0; k < B; ++k) {
+            raw[k] = vb[(size_t)row * kv_dim];
+            row = row + 1 == capacity ? 0 : row + 1;
+        }
+#pragma unroll
+        for (int k = 0; k < B; ++k) v[k] = f16_bits_to_f32(raw[k]);
+    };
+    auto add = [&](const float (&v)[B], int t0) {
+#pragma unroll
+        for (int k = 0; k < B; ++k) {
+            if (t0 + k < window) {
+#pragma unroll
+                for (int g = 0; g < kRowsSvG; ++g)
+                    if (g < G) acc[g] = acc[g] + e_s[g][t0 + k] * v[k];
+            }
+        }
+    };
+    float va[B], vb2[B];
+    load(va, 0);
+    for (int t0 = 0; t0 < window; t0 += 2 * B) {
+        if (t0 + B < window) load(vb2, t0 + B);  // in flight while va is added
+        add(va, t0);
+        if (t0 + B >= window) break;
+        if (t0 + 2 * B < window) load(va, t0 + 2 * B);
+        add(vb2, t0 + B);
+    }
+    for (int g = 0; g < G; ++g) out[((size_t)z * n_heads + kvh * G + g) * HD + d] = acc[g];
+}
+
 // Merges the tiles of head blockIdx.x (thread d = output dim d), in tile
 // order, and writes out (nullable) and the Q8_0 pack (nullable) of the
 // n_heads*256 output.
@@ -1356,6 +1447,11 @@ int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *q, int q_stride, const 
                            (const int32_t *)nullptr, n_past0, n_heads, n_kv_heads, scale, capacity, wlimit, scores,
                            q_stride);
         if (int rc = check_launch(ctx, "attn_scores_kernel")) return rc;
+    }
+    if (span <= kRowsSvMax && n_heads / n_kv_heads <= kRowsSvG) {
+        hipLaunchKernelGGL(attn_softmax_v_rows_kernel, dim3(n_kv_heads, rows), dim3(kAttnHD), 0, ctx->stream, scores,
+                           v_cache, n_past0, n_heads, n_kv_heads, capacity, wlimit, (int)host_expf_fused(), out);
+        return check_launch(ctx, "attn_softmax_v_rows_kernel");
     }
     return launch_softmax_v(ctx, scores, v_cache, out, nullptr, nullptr, n_past0, n_heads, n_kv_heads, capacity, wlimit,
                             rows);
