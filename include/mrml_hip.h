@@ -531,7 +531,7 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *model, int32_t *d_s
                          int32_t hist_cap, const int32_t *d_prompt, int32_t prompt_len);
 /* Prefill (prefill_cuda, model.rs:2395-2638): the token steps of positions
  * pos0 .. pos0+n_tokens-1 for the tokens d_tokens[0..n_tokens) (device
- * int32), in chunks of up to 128 tokens whose seven projections per layer run
+ * int32), in chunks of up to 512 tokens whose seven projections per layer run
  * as batched Q4_0 products on MFMA (mrml_hip_gemm_q4_0).  Every op keeps the
  * token step's arithmetic, so the caches end bit-identical to n_tokens calls
  * of mrml_hip_gemma2_step; the last token's logits go to d_logits (nullable:

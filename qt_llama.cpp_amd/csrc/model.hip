@@ -563,7 +563,12 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
 
 namespace {
 
-constexpr int kPrefillChunk = 128;  // tokens per chunk (prefill_cuda's tile, model.rs:2395-2638)
+// Tokens per chunk.  prefill_cuda's tile is 128 (model.rs:2395-2638); 512
+// here gives the batched products four times the waves and streams the
+// weights once per 512 tokens (2.1x the prefill rate at the Gemma-2-2B
+// shape).  Results do not depend on it: every op keeps the token step's
+// arithmetic.
+constexpr int kPrefillChunk = 512;
 
 // Attention rows per launch in a prefill chunk: the whole chunk unless its
 // scores (n_heads * capacity floats a row) would pass kPrefillScoreBytes.

@@ -500,7 +500,7 @@ def run_gpu_prefill_decode(backend, dev, model, prompt, n_decode, splits):
 
 @pytest.mark.parametrize("splits", [[150], [100, 50], [1, 149]])
 def test_gemma2_tiny_prefill_equals_steps(backend, dev, orc, synth, splits):
-    """The chunked prefill (batched MFMA products, chunks of 128 tokens)
+    """The chunked prefill (batched MFMA products, chunks of 512 tokens)
     leaves the caches, the last prompt position's logits and argmax, and the
     decode that follows bit-identical to feeding the prompt one token step at
     a time; the decoded tokens equal the oracle's."""
@@ -567,15 +567,15 @@ def test_gemma2_2b_shape_prefill_equals_fused_steps(backend, dev, synth):
     """At the Gemma-2-2B layer shape (3 layers, dim 2304, 8/4 heads of 256,
     FFN 9216) the token step runs its residual norms inside the gate/up and
     q|k|v matvecs (wave-group exact sums), while the prefill runs them as
-    separate norm kernels between batched products.  Over 136 prompt tokens
-    (a full 128-token chunk and a ragged one) both leave the same caches, last
+    separate norm kernels between batched products.  Over 520 prompt tokens
+    (a full 512-token chunk and a ragged one) both leave the same caches, last
     logits and decoded tokens, bit for bit."""
-    cfg = dict(synth.GEMMA2_2B, n_layers=3, vocab=2048, ctx_len=160)
+    cfg = dict(synth.GEMMA2_2B, n_layers=3, vocab=2048, ctx_len=544)
     model = synth.gemma2_model(cfg, seed=6)
-    prompt = synth.prompt_tokens(136, cfg["vocab"], seed=7)
+    prompt = synth.prompt_tokens(520, cfg["vocab"], seed=7)
     n_dec = 8
     print(f"\n[prefill 2b-shape] {len(prompt)} prompt tokens", flush=True)
-    first, lg_last, hist, kc, vc = run_gpu_prefill_decode(backend, dev, model, prompt, n_dec, [136])
+    first, lg_last, hist, kc, vc = run_gpu_prefill_decode(backend, dev, model, prompt, n_dec, [520])
     hist0, lg0, kc0, vc0 = run_gpu_decode(backend, dev, model, prompt, n_dec)
     P = len(prompt)
     assert first == hist0[P - 1]
@@ -609,14 +609,14 @@ def test_gemma2_prefill_wraps_ring(backend, dev, orc, synth, ctx_len, splits):
 
 def test_gemma2_prefill_captured(backend, dev, synth):
     """After mrml_hip_gemma2_reserve_prefill a prefill allocates nothing, so
-    it can be captured: a graph of a 150-token prefill (two chunks) replayed
+    it can be captured: a graph of a 600-token prefill (two chunks) replayed
     three times, the caches cleared and the pick reset by the program's own
     eager copies between replays, leaves caches, logits and pick
     bit-identical to an eager prefill every time."""
-    cfg = dict(TINY, ctx_len=256)
+    cfg = dict(TINY, ctx_len=1024)
     model = synth.gemma2_model(cfg, seed=15)
-    prompt = synth.prompt_tokens(150, cfg["vocab"], seed=8)
-    first, lg_last, _, kc_e, vc_e = run_gpu_prefill_decode(backend, dev, model, prompt, 0, [150])
+    prompt = synth.prompt_tokens(600, cfg["vocab"], seed=8)
+    first, lg_last, _, kc_e, vc_e = run_gpu_prefill_decode(backend, dev, model, prompt, 0, [600])
     m = backend.Gemma2Model.from_host(dev, model)
     m.reserve_prefill()
     m.reserve_prefill()  # idempotent

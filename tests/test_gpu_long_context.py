@@ -137,7 +137,7 @@ def test_attention_split_max_capacity(backend, orc, dev):
 def test_gemma2_tiny_long_context(backend, dev, orc, synth, numerics):
     """The whole model at the largest capacity: caches holding 9000 seeded
     rows (the same rows in the oracle's), then a 200-token prefill from
-    position 9000 (two chunks, attention rows in launches of 64 so the
+    position 9000 (one chunk, attention rows in launches of 64 so the
     scores stay within their bound) and 4 token steps replayed from a graph.
     EXACT: the cache rows written, the prefill's last logits and every
     step's logits are bit-identical to the oracle's token steps.  FAST: the
