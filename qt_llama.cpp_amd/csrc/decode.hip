@@ -1027,25 +1027,28 @@ __global__ __launch_bounds__(kSplitT) void attn_split_kernel(const float *__rest
 // are in flight while the current 32 are added.  The decode form spreads
 // one long row over eight workgroups to cut its latency; a prefill chunk has
 // rows enough to fill the GPU this way.  Windows up to kRowsSvMax positions
-// and groups up to kRowsSvG heads (one exact block sum per head).
-constexpr int kRowsSvMax = 2048;
+// (one exact block sum per head) and groups up to kRowsSvG heads.  Dynamic
+// LDS: the group's weights, G rows of `span` floats (the launch's widest
+// window), then span flag bytes.
+constexpr int kRowsSvMax = mrml_xsum::kMaxPerThread * kAttnHD;  // 4096
 constexpr int kRowsSvG = 4;
 constexpr int kRowsSvB = 32;  // positions per load batch
-static_assert(kRowsSvMax <= mrml_xsum::kMaxPerThread * kAttnHD, "one block sum per head");
+inline size_t rows_sv_lds(int g, int span) { return (size_t)g * span * sizeof(float) + ((span + 15) & ~15); }
 
 __global__ __launch_bounds__(kAttnHD) void attn_softmax_v_rows_kernel(const float *__restrict__ scores,
                                                                       const uint16_t *__restrict__ v_cache,
                                                                       int n_past0, int n_heads, int n_kv_heads,
                                                                       int capacity, int wlimit, int expf_fused,
-                                                                      float *__restrict__ out)
+                                                                      float *__restrict__ out, int span)
 {
     constexpr int HD = kAttnHD, B = kRowsSvB;
-    __shared__ __align__(16) float e_s[kRowsSvG][kRowsSvMax];
-    __shared__ uint8_t flags[kRowsSvMax];
+    extern __shared__ __align__(16) float e_dyn[];  // [G][span] weights, then span flag bytes
     __shared__ mrml_xsum::Shared xs;
     __shared__ float red[HD / 64];
     __shared__ uint64_t exp_tab[32];
     const int kvh = blockIdx.x, z = blockIdx.y, d = threadIdx.x, G = n_heads / n_kv_heads;
+    uint8_t *flags = reinterpret_cast<uint8_t *>(e_dyn + (size_t)G * span);
+    auto e_s = [&](int g) { return e_dyn + (size_t)g * span; };
     int window, start;
     attn_window(nullptr, n_past0 + z, wlimit, window, start);
     if (d < 32) exp_tab[d] = mrml_libm::kExpfT.t[d];
@@ -1058,12 +1061,13 @@ __global__ __launch_bounds__(kAttnHD) void attn_softmax_v_rows_kernel(const floa
         if ((d & 63) == 0) red[d >> 6] = mx;
         __syncthreads();
         mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        for (int p = d; p < window; p += HD) e_s[g][p] = mrml_libm::expf_t(sc[p] - mx, fused, exp_tab);
+        float *eg = e_s(g);
+        for (int p = d; p < window; p += HD) eg[p] = mrml_libm::expf_t(sc[p] - mx, fused, exp_tab);
         __syncthreads();  // also: every thread has read red before the next head rewrites it
-        const float sum = mrml_xsum::block_seq_sum_nonneg(e_s[g], window, flags, xs);  // ends with a barrier
+        const float sum = mrml_xsum::block_seq_sum_nonneg(eg, window, flags, xs);  // ends with a barrier
         if (sum > 0.0f) {
             const float inv = 1.0f / sum;
-            for (int p = d; p < window; p += HD) e_s[g][p] = e_s[g][p] * inv;
+            for (int p = d; p < window; p += HD) eg[p] = eg[p] * inv;
         }
     }
     __syncthreads();
@@ -1091,7 +1095,7 @@ __global__ __launch_bounds__(kAttnHD) void attn_softmax_v_rows_kernel(const floa
             if (t0 + k < window) {
 #pragma unroll
                 for (int g = 0; g < kRowsSvG; ++g)
-                    if (g < G) acc[g] = acc[g] + e_s[g][t0 + k] * v[k];
+                    if (g < G) acc[g] = acc[g] + e_dyn[(size_t)g * span + t0 + k] * v[k];
             }
         }
     };
@@ -1448,9 +1452,13 @@ int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *q, int q_stride, const 
                            q_stride);
         if (int rc = check_launch(ctx, "attn_scores_kernel")) return rc;
     }
-    if (span <= kRowsSvMax && n_heads / n_kv_heads <= kRowsSvG) {
-        hipLaunchKernelGGL(attn_softmax_v_rows_kernel, dim3(n_kv_heads, rows), dim3(kAttnHD), 0, ctx->stream, scores,
-                           v_cache, n_past0, n_heads, n_kv_heads, capacity, wlimit, (int)host_expf_fused(), out);
+    // the rows form where its dynamic LDS stays within 60 KiB (no launch
+    // here asks for more than the default 64 KiB a workgroup)
+    if (span <= kRowsSvMax && n_heads / n_kv_heads <= kRowsSvG &&
+        rows_sv_lds(n_heads / n_kv_heads, span) <= (size_t)60 << 10) {
+        hipLaunchKernelGGL(attn_softmax_v_rows_kernel, dim3(n_kv_heads, rows), dim3(kAttnHD),
+                           rows_sv_lds(n_heads / n_kv_heads, span), ctx->stream, scores, v_cache, n_past0, n_heads,
+                           n_kv_heads, capacity, wlimit, (int)host_expf_fused(), out, span);
         return check_launch(ctx, "attn_softmax_v_rows_kernel");
     }
     return launch_softmax_v(ctx, scores, v_cache, out, nullptr, nullptr, n_past0, n_heads, n_kv_heads, capacity, wlimit,

@@ -247,12 +247,14 @@ def window_rows(n_past, sw, cap):
 # (cache_start, batch, sliding_window, capacity, n_heads, n_kv_heads, stacked q):
 # prefill_cuda's first chunk over the stacked projection, a later chunk, a
 # sliding window shorter than the chunk, a ring whose window covers the
-# whole capacity, a group of 8 query heads per kv head (one launch per row),
-# the long softmax form (capacity past 6144), and a batch split over two
-# launches (40 rows of 2 MiB of scores against a 64 MiB bound)
+# whole capacity, a group of 8 query heads per kv head, the long softmax form
+# (capacity past 6144), a batch split over two launches (40 rows of 2 MiB of
+# scores against a 64 MiB bound), and windows past 2048 in the prefill
+# softmax form (groups of 2 and 4)
 PREFILL_CASES = [(0, 16, None, 16, 8, 4, True), (128, 37, None, 512, 8, 4, True), (200, 40, 24, 256, 8, 4, True),
                  (300, 9, 64, 64, 8, 4, False), (700, 64, None, 2048, 8, 8, False), (20, 7, 5, 32, 16, 2, True),
-                 (6000, 3, None, 8192, 8, 4, False), (100, 40, None, 65536, 8, 4, True)]
+                 (6000, 3, None, 8192, 8, 4, False), (100, 40, None, 65536, 8, 4, True),
+                 (3000, 20, None, 4096, 8, 4, True), (3900, 9, None, 4096, 16, 4, False)]
 
 
 @pytest.mark.parametrize("cache_start,batch,sw,cap,nh,nkv,stacked", PREFILL_CASES)
