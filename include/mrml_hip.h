@@ -96,6 +96,9 @@ void       *mrml_hip_stream(mrml_hip_ctx *ctx);
 /* Grow the internal scratch (activation packs, partial results) to at least
  * `bytes` now, so later ops never allocate (e.g. under stream capture). */
 int         mrml_hip_reserve_workspace(mrml_hip_ctx *ctx, size_t bytes);
+/* Current size of that scratch in bytes.  No reference counterpart: it lets a
+ * caller check that a sequence of ops (a captured prefill, say) grew nothing. */
+int         mrml_hip_workspace_bytes(mrml_hip_ctx *ctx, size_t *bytes);
 
 /* ---- graphs: CudaDevice::{capture, launch_graph} and CudaGraphExec
  *      (cuda.rs:1841-1858, 1957-2003).  Ops issued on the context between

@@ -124,6 +124,7 @@ _SIGNATURES = {
     "mrml_hip_memory_info": [_P, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)],
     "mrml_hip_stream": [_P],
     "mrml_hip_reserve_workspace": [_P, _Z],
+    "mrml_hip_workspace_bytes": [_P, ctypes.POINTER(ctypes.c_size_t)],
     "mrml_hip_graph_begin": [_P],
     "mrml_hip_graph_end": [_P, ctypes.POINTER(_P)],
     "mrml_hip_graph_launch": [_P, _P],
@@ -372,6 +373,11 @@ class HipDevice:
 
     def reserve_workspace(self, nbytes: int) -> None:
         self._check(self.lib.mrml_hip_reserve_workspace(self.ctx, nbytes))
+
+    def workspace_bytes(self) -> int:
+        n = ctypes.c_size_t()
+        self._check(self.lib.mrml_hip_workspace_bytes(self.ctx, ctypes.byref(n)))
+        return int(n.value)
 
     def zero(self, buf, nbytes: int | None = None) -> None:
         self._check(self.lib.mrml_hip_zero_async(self.ctx, _ptr(buf), buf.nbytes if nbytes is None else nbytes))

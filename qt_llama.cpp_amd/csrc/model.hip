@@ -719,7 +719,11 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
                                      d_argmax, nullptr, nullptr, m->select_scratch, nullptr, m->recent_ring,
                                      (long long)pos0 + n_tokens - 1, nullptr, 0, nullptr, 0));
         } else if (d_argmax) {
-            STEP(launch_argmax_f32(ctx, logits, c.vocab, d_argmax));
+            // the model's own argmax scratch, as in the token step: the
+            // context workspace could be reallocated (and a captured graph
+            // left pointing at freed memory)
+            STEP(launch_argmax_step(ctx, logits, c.vocab, d_argmax, m->argmax_scratch, nullptr, nullptr, 0, nullptr,
+                                    0, nullptr));
         }
     }
 #undef STEP

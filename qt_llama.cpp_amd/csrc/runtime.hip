@@ -253,6 +253,14 @@ int mrml_hip_reserve_workspace(mrml_hip_ctx *ctx, size_t bytes)
     return workspace(ctx, bytes) ? MRML_HIP_OK : MRML_HIP_E_ALLOC;
 }
 
+int mrml_hip_workspace_bytes(mrml_hip_ctx *ctx, size_t *bytes)
+{
+    CTX_GUARD(ctx);
+    REQUIRE(ctx, bytes, "workspace_bytes: null output");
+    *bytes = ctx->ws_bytes;
+    return MRML_HIP_OK;
+}
+
 int mrml_hip_graph_begin(mrml_hip_ctx *ctx)
 {
     CTX_GUARD(ctx);

@@ -231,6 +231,13 @@ impl HipDevice {
         self.inner.check(unsafe { (self.inner.api.reserve_workspace)(self.inner.ctx, bytes) })
     }
 
+    /// Current size of the internal scratch (no `CudaDevice` counterpart).
+    pub fn workspace_bytes(&self) -> Result<usize> {
+        let mut n = 0usize;
+        self.inner.check(unsafe { (self.inner.api.workspace_bytes)(self.inner.ctx, &mut n) })?;
+        Ok(n)
+    }
+
     /// `CudaDevice::capture` (cuda.rs:1957-1994): every launch `launches`
     /// issues on this device becomes one replayable graph.
     pub fn capture<F: FnOnce()>(&self, launches: F) -> Result<HipGraph> {

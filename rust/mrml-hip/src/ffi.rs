@@ -141,6 +141,7 @@ api! {
     memory_info: fn(Ctx, *mut u64, *mut u64) -> c_int = "mrml_hip_memory_info";
     stream: fn(Ctx) -> *mut c_void = "mrml_hip_stream";
     reserve_workspace: fn(Ctx, usize) -> c_int = "mrml_hip_reserve_workspace";
+    workspace_bytes: fn(Ctx, *mut usize) -> c_int = "mrml_hip_workspace_bytes";
     graph_begin: fn(Ctx) -> c_int = "mrml_hip_graph_begin";
     graph_end: fn(Ctx, *mut *mut c_void) -> c_int = "mrml_hip_graph_end";
     graph_launch: fn(Ctx, *mut c_void) -> c_int = "mrml_hip_graph_launch";

@@ -609,34 +609,48 @@ def test_gemma2_prefill_wraps_ring(backend, dev, orc, synth, ctx_len, splits):
 
 def test_gemma2_prefill_captured(backend, dev, synth):
     """After mrml_hip_gemma2_reserve_prefill a prefill allocates nothing, so
-    it can be captured: a graph of a 600-token prefill (two chunks) replayed
-    three times, the caches cleared and the pick reset by the program's own
-    eager copies between replays, leaves caches, logits and pick
-    bit-identical to an eager prefill every time."""
+    it can be captured: on a new context that has run no op, a graph of a
+    600-token prefill (two chunks) with the greedy pick is captured, the
+    context's workspace stays as it was, and the graph replayed three times,
+    the caches cleared and the pick reset by the program's own eager copies
+    between replays (and the workspace grown by an eager op between them),
+    leaves caches, logits and pick bit-identical to an eager prefill every
+    time."""
     cfg = dict(TINY, ctx_len=1024)
     model = synth.gemma2_model(cfg, seed=15)
     prompt = synth.prompt_tokens(600, cfg["vocab"], seed=8)
     first, lg_last, _, kc_e, vc_e = run_gpu_prefill_decode(backend, dev, model, prompt, 0, [600])
-    m = backend.Gemma2Model.from_host(dev, model)
-    m.reserve_prefill()
-    m.reserve_prefill()  # idempotent
-    zeros = np.zeros(m.cache_elems(), np.uint16)
-    kc, vc = backend.HipBuffer.from_host(dev, zeros), backend.HipBuffer.from_host(dev, zeros)
-    logits = backend.HipBuffer.alloc(dev, cfg["vocab"])
-    am = backend.HipBuffer.from_host(dev, np.array([-1], np.int32))
-    toks = backend.HipBuffer.from_host(dev, np.asarray(prompt, np.int32))
-    g = dev.capture(lambda: m.prefill(toks, len(prompt), 0, kc, vc, logits=logits, argmax=am))
-    for r in range(3):
-        kc.copy_from_host(zeros)
-        vc.copy_from_host(zeros)
-        am.copy_from_host(np.array([-1], np.int32))
-        g.launch()
-        dev.sync()
-        assert int(am.numpy()[0]) == first, f"replay {r}"
-        assert_bits(logits.numpy(), lg_last, f"logits, replay {r}")
-        assert np.array_equal(kc.numpy(), kc_e) and np.array_equal(vc.numpy(), vc_e), f"caches, replay {r}"
-    g.close()
-    m.close()
+    fresh = backend.HipDevice.new(0)
+    try:
+        m = backend.Gemma2Model.from_host(fresh, model)
+        m.reserve_prefill()
+        m.reserve_prefill()  # idempotent
+        zeros = np.zeros(m.cache_elems(), np.uint16)
+        kc, vc = backend.HipBuffer.from_host(fresh, zeros), backend.HipBuffer.from_host(fresh, zeros)
+        logits = backend.HipBuffer.alloc(fresh, cfg["vocab"])
+        am = backend.HipBuffer.from_host(fresh, np.array([-1], np.int32))
+        toks = backend.HipBuffer.from_host(fresh, np.asarray(prompt, np.int32))
+        ws0 = fresh.workspace_bytes()
+        g = fresh.capture(lambda: m.prefill(toks, len(prompt), 0, kc, vc, logits=logits, argmax=am))
+        assert fresh.workspace_bytes() == ws0, "the captured prefill grew the context workspace"
+        for r in range(3):
+            kc.copy_from_host(zeros)
+            vc.copy_from_host(zeros)
+            am.copy_from_host(np.array([-1], np.int32))
+            g.launch()
+            fresh.sync()
+            assert int(am.numpy()[0]) == first, f"replay {r}"
+            assert_bits(logits.numpy(), lg_last, f"logits, replay {r}")
+            assert np.array_equal(kc.numpy(), kc_e) and np.array_equal(vc.numpy(), vc_e), f"caches, replay {r}"
+            # an eager op that grows (and so reallocates) the workspace between
+            # replays must not touch what the graph uses
+            fresh.reserve_workspace((r + 2) << 20)
+        g.close()
+        m.close()
+        for b in (kc, vc, logits, am, toks):
+            b.close()
+    finally:
+        fresh.close()
 
 
 def test_gemma2_prefill_rejects_bad_positions(backend, dev, synth):

@@ -161,6 +161,91 @@ def test_q8_0_quantiser_brute_force(orc):
                           d_trunc.astype(np.uint32))
 
 
+# ---------------------------------------------------------------- Q4_0 quantiser
+# quant.rs:372-389: amax folds from 0.0 with f32::max (a NaN never wins),
+# scale = amax / 8, d = the truncating f16 of scale, inverse = 1 / scale
+# (0 when scale is 0), q = clamp(round(x * inverse) as i32, -8, 7) + 8 with
+# round half away from zero and a saturating cast (NaN -> 0), value j in the
+# low nibble of byte j and value j + 16 in its high nibble.
+def q4_bytes(q: np.ndarray, d_bits: int) -> np.ndarray:
+    """18-byte block from 32 unsigned nibbles (0..15) and the d bits."""
+    out = np.zeros(18, np.uint8)
+    out[0], out[1] = d_bits & 0xFF, d_bits >> 8
+    out[2:] = (q[:16] | (q[16:] << 4)).astype(np.uint8)
+    return out
+
+
+def test_q4_0_quantiser_closed_forms(orc):
+    # amax 8: scale 1, d 0x3C00, inverse 1 -- q = round(x) clamped, ties away from zero
+    x = np.zeros(32, np.float32)
+    x[:10] = [8, -8, 4, -4, 0.5, -0.5, 2.5, -2.5, 1.4999999, 7.5]
+    x[16:22] = [-7.5, 3.5, -3.5, 6.49, -1.5, 1.5]
+    want = np.full(32, 8, np.int64)
+    want[:10] = np.array([7, -8, 4, -4, 1, -1, 3, -3, 1, 7]) + 8      # 8 -> 7 (clamp), 7.5 -> 8 -> 7
+    want[16:22] = np.array([-8, 4, -4, 6, -2, 2]) + 8
+    assert np.array_equal(orc.quantize_q4_0(x), q4_bytes(want, 0x3C00))
+    # a zero block: scale 0, d 0, every nibble 8
+    assert np.array_equal(orc.quantize_q4_0(np.zeros(32, np.float32)), q4_bytes(np.full(32, 8), 0))
+    # NaN is never the amax (f32::max); its own quant is `NaN as i32` = 0 -> 8
+    x = np.zeros(32, np.float32)
+    x[:3] = [np.nan, 4.0, -2.0]
+    x[20] = np.nan
+    want = np.full(32, 8, np.int64)
+    want[1], want[2] = 8 + 8 - 1, 8 - 4                                # 4 / 0.5 = 8 -> 7; -2 / 0.5 = -4
+    assert np.array_equal(orc.quantize_q4_0(x), q4_bytes(want, 0x3800))  # d = f16(0.5)
+    # the scale's f16 truncates: amax 0.3 -> scale 0.0375 -> 0x28CC (RNE gives 0x28CD)
+    x = np.zeros(32, np.float32)
+    x[0] = np.float32(0.3)
+    got = orc.quantize_q4_0(x)
+    assert (int(got[0]) | (int(got[1]) << 8)) == 0x28CC
+    assert int(np.float16(np.float32(0.3) / np.float32(8.0)).view(np.uint16)) == 0x28CD
+    assert got[2] & 15 == 15                                            # 0.3 * (1/0.0375) = 8 -> 7 -> 15
+
+
+def test_q4_0_quantiser_saturating_cast(orc):
+    """A subnormal amax: amax / 8 is the smallest subnormal, 1 / scale
+    overflows to +inf, x * inf = +-inf saturates to i32::MAX / MIN (-> 7 /
+    -8) and 0 * inf = NaN casts to 0; the scale's f16 is +0."""
+    tiny = np.float32(2.0 ** -146)
+    x = np.zeros(32, np.float32)
+    x[0], x[1], x[17] = tiny, -tiny, tiny
+    want = np.full(32, 8, np.int64)
+    want[0], want[1], want[17] = 15, 0, 15
+    assert np.array_equal(orc.quantize_q4_0(x), q4_bytes(want, 0x0000))
+    # an amax too small for amax / 8 (scale rounds to 0): inverse 0, all 8
+    x = np.zeros(32, np.float32)
+    x[5] = np.float32(2.0 ** -149)
+    assert np.array_equal(orc.quantize_q4_0(x), q4_bytes(np.full(32, 8), 0))
+
+
+def test_q4_0_quantiser_brute_force(orc):
+    """Random blocks over a wide range, NaN included, against a vectorised
+    numpy restatement; a swapped nibble pair, /7 instead of /8, RNE f16 or
+    banker's rounding each fail it."""
+    rng = np.random.default_rng(33)
+    n = 32 * 400
+    x = (rng.standard_normal(n) * 10.0 ** rng.uniform(-3, 3, n)).astype(np.float32)
+    x[rng.integers(0, n, 40)] = np.nan
+    got = orc.quantize_q4_0(x).reshape(-1, 18)
+    xb = x.reshape(-1, 32)
+    amax = np.fmax.reduce(np.abs(xb), axis=1, initial=0.0).astype(np.float32)
+    scale = np.where(amax > 0, (amax / np.float32(8.0)).astype(np.float32), np.float32(0))
+    with np.errstate(divide="ignore"):
+        inv = np.where(scale > 0, (np.float32(1.0) / scale).astype(np.float32), np.float32(0))
+    with np.errstate(invalid="ignore"):
+        r = roundf((xb * inv[:, None]).astype(np.float32))
+    q = np.where(np.isnan(r), 0, np.clip(np.nan_to_num(r, nan=0.0), -8, 7)).astype(np.int64) + 8
+    want_qs = (q[:, :16] | (q[:, 16:] << 4)).astype(np.uint8)
+    assert np.array_equal(got[:, 2:], want_qs)
+    d_trunc = np.where(scale > 0, (scale.view(np.uint32) >> 13) - ((127 - 15) << 10), 0)  # normal f16 range here
+    assert np.array_equal(got[:, 0].astype(np.uint32) | (got[:, 1].astype(np.uint32) << 8), d_trunc.astype(np.uint32))
+    # dequantised round trip: within about one scale step (the top value
+    # clamps from 8 to 7 steps; the truncated d is within 2^-10 of scale)
+    ok = ~np.isnan(xb).any(axis=1)
+    back = orc.dequantize_q4_0(orc.quantize_q4_0(xb[ok].reshape(-1)), int(ok.sum()) * 32).reshape(-1, 32)
+    assert np.all(np.abs(back - xb[ok]) <= 1.01 * scale[ok][:, None])
+
+
 # ---------------------------------------------------------------- Q4_0 x Q8_0
 def q4_block(d_bits: int, byte: int) -> np.ndarray:
     b = np.full(18, byte, dtype=np.uint8)
