@@ -6,8 +6,8 @@ Gemma-2-2B FFN shapes.  One step = one FFN pass over synthetic data:
     quantize x (2304)  ->  fused gate+up GeGLU matvec (2 x 9216x2304)
     quantize act (9216) ->  down matvec (2304x9216)
 `value` is whole-step throughput in GB/s of algorithmic bytes (weights +
-vectors), with weights resident in HBM and rotated over a pool of 48
-matrices (573 MB, more than twice the 256 MB MALL), timed with HIP events
+vectors), with weights resident in HBM and rotated over 15 weight sets
+(45 matrices, 537 MB, more than twice the 256 MB MALL), timed with HIP events
 around graph replays: W warm-up steps, then timed regions of exactly K steps
 each (as many regions as it takes to time at least 100 launches, at least 5);
 `value` is the median region, the minimum is reported beside it.  The JSON
@@ -56,6 +56,7 @@ BYTES_STEP = BYTES_GEGLU + BYTES_DOWN
 PEAK_HBM_GBS = 8000.0
 PEAK_INT8_TOPS = 5000.0                                # dense int8 MFMA, MI355X
 MALL_BYTES = 256 << 20
+PREFILL_CHUNK = 512                                    # tokens per chunk of mrml_hip_gemma2_prefill (model.hip)
 # the dominant kernel of the step (the fused GeGLU that quantises x and emits the act pack)
 GEGLU_KERNEL = "gemv_q4_0_geglu_kernel<72, 8, true, true>"
 
@@ -277,7 +278,7 @@ def decode_bench(be, synth, dev, ev, n_prefill: int, n_decode: int, cpu_steps: i
             np.array_equal(kc.numpy().reshape(shape)[:, :n_prefill], kc_ref.reshape(shape)[:, :n_prefill]) and
             np.array_equal(vc.numpy().reshape(shape)[:, :n_prefill], vc_ref.reshape(shape)[:, :n_prefill]))
     out["prefill_batched"] = {"tok_s": round(n_prefill / t_pf, 1), "ms_per_token": round(t_pf / n_prefill * 1e3, 4),
-                              "chunk": 128, "bit_identical_to_token_steps": bool(same),
+                              "chunk": PREFILL_CHUNK, "bit_identical_to_token_steps": bool(same),
                               "how": "mrml_hip_gemma2_prefill, eager (host launch time included), "
                                      "events around one call over the whole prompt"}
     m.close()
@@ -675,11 +676,11 @@ def main() -> int:
         print(json.dumps(prefill_profile(be, synth, dev, args.profile_prefill)))
         return 0
 
-    # ---- synthetic config-2 data: a pool of 48 matrices (16 copies each of
-    # gate, up and down; 573 MB, more than twice the MALL).  FFN step i uses
-    # pool entries 3j, 3j+1, 3j+2 with j = i mod 16; the per-matrix rates
-    # rotate one kernel over all 48 entries (the three matrices have the same
-    # bytes, and the timing does not depend on the values).
+    # ---- synthetic config-2 data: `sets` copies of gate, up and down (the
+    # default 15 sets: 45 matrices, 537 MB, more than twice the MALL).  FFN
+    # step i uses pool entries 3j, 3j+1, 3j+2 with j = i mod sets; the
+    # per-matrix rates rotate one kernel over all entries (the three matrices
+    # have the same bytes, and the timing does not depend on the values).
     rng = synth.rng_for(2)
     host = {"g": synth.q4_0_matrix(rng, FFN, DIM), "u": synth.q4_0_matrix(rng, FFN, DIM),
             "d": synth.q4_0_matrix(rng, DIM, FFN)}

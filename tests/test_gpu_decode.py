@@ -885,6 +885,69 @@ def test_gemma2_2b_oracle_at_bench_positions(backend, dev, orc, synth):
                 assert l[g] >= l.max() - 0.05 * np.max(np.abs(l)), f"position {P0 + i}: pick {g} vs {np.argmax(l)}"
 
 
+def test_gemma2_2b_bench_run_matches_oracle(backend, dev, orc, synth):
+    """The C4 run the bench times, checked end to end against the oracle's
+    step_generation loop (model.rs:2713-2907): the Gemma-2-2B-shape model
+    (seed 1, 26 layers, 256000 tied Q4_0 ids, f16 KV cache of 4096), the
+    bench's 512-token prompt through mrml_hip_gemma2_prefill, then 64
+    free-running token steps at positions 512..575 replayed from one captured
+    graph, each picking with the bench's sampler (early-id mask, 30*tanh
+    softcap, -3.5 for the last 32 tokens, greedy).  The oracle starts from
+    the GPU's prefilled caches (prefill == token steps is tested on its
+    own), redoes position 511 (the prompt's last logits and pick), then runs
+    its own steps and orc.vocab_select on its own logits: logits of all 65
+    positions, every pick and the caches written at 511..575 bit-identical."""
+    cfg = dict(synth.GEMMA2_2B)
+    model = synth.gemma2_model(cfg, seed=1)
+    P, n_dec = 512, 64
+    total = P + n_dec
+    prompt = synth.prompt_tokens(P, cfg["vocab"], seed=1)
+    m = backend.Gemma2Model.from_host(dev, model)
+    m.set_sampler(temperature=0.0, top_k=40)
+    kc = backend.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    vc = backend.HipBuffer.from_host(dev, np.zeros(m.cache_elems(), np.uint16))
+    logits = backend.HipBuffer.alloc(dev, cfg["vocab"])
+    am = backend.HipBuffer.from_host(dev, np.array([-1], np.int32))
+    pr = backend.HipBuffer.from_host(dev, np.asarray(prompt, np.int32))
+    print(f"\n[bench run] gpu prefill {P}, then {n_dec} captured steps", flush=True)
+    m.prefill(pr, P, 0, kc, vc, logits=logits, argmax=am)
+    dev.sync()
+    first, lg_gpu = int(am.numpy()[0]), [logits.numpy()]
+    kc_pre, vc_pre = kc.numpy(), vc.numpy()
+    state = backend.HipBuffer.from_host(dev, np.array([first, P], np.int32))
+    hist = backend.HipBuffer.from_host(dev, np.full(total, -1, np.int32))
+    graph = dev.capture(lambda: m.step(state, kc, vc, logits=logits, hist=hist, hist_cap=total, prompt_len=P))
+    for _ in range(n_dec):
+        graph.launch()
+        dev.sync()
+        lg_gpu.append(logits.numpy())
+    got = np.concatenate([[first], hist.numpy()[P:]]).astype(np.int32)
+    kc_gpu, vc_gpu = kc.numpy(), vc.numpy()
+    graph.close()
+    m.close()
+
+    print("[bench run] oracle from the prefilled caches", flush=True)
+    o = orc.OracleGemma2(model)
+    o.k_cache[:] = kc_pre
+    o.v_cache[:] = vc_pre
+    lg = np.zeros(cfg["vocab"], np.float32)
+    history = [int(t) for t in prompt[:P - 1]]
+    want, tok = [], int(prompt[P - 1])
+    for pos in range(P - 1, total):
+        o.step(tok, pos, threads=THREADS, logits=lg)
+        history.append(tok)
+        assert_bits(lg_gpu[pos - (P - 1)], lg, f"logits at position {pos}")
+        nxt = orc.vocab_select(lg, None, history[-32:], max(0, pos - (P - 1)), 0, 0.0, pos + 1, 1)[0]
+        want.append(nxt)
+        tok = nxt
+    want = np.array(want, np.int32)
+    print(f"[bench run] picks {want[:6].tolist()}..., distinct {len(set(want.tolist()))}", flush=True)
+    assert_same_tokens(got, want)
+    assert np.array_equal(kc_gpu, o.k_cache) and np.array_equal(vc_gpu, o.v_cache)
+    moved = sum(int(np.argmax(l)) != int(w) for l, w in zip(lg_gpu, want))
+    print(f"[bench run] picks the mask or penalty moved off the plain argmax: {moved} of {len(want)}", flush=True)
+
+
 def test_gemma2_2b_greedy_64(backend, dev, orc, synth):
     """Gemma-2-2B shape (26 layers, 2304, 8/4 heads of 256, FFN 9216, 256000 tied
     Q4_0 vocabulary): the greedy argmax of every step matches the oracle --
