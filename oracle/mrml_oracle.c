@@ -709,6 +709,101 @@ void orc_attention_f16(const float *q, const uint16_t *k_cache, const uint16_t *
 }
 
 /* ------------------------------------------------------------------------ */
+/* KV cache rows in the three formats of KvCacheFormat::cuda_code
+ * (kv_cache.rs:16-31): 0 f16 (the build's cache of the F32 format, RNE as
+ * the reference GPU stores it), 1 Q8_0, 2 Q4_0.  Bytes of n values. */
+size_t orc_kv_row_bytes(size_t n, int fmt)
+{
+    return fmt == 1 ? n / 32 * 34 : (fmt == 2 ? n / 32 * 18 : n * 2);
+}
+
+/* KvCacheRow::from_f32 (kv_cache.rs:54-71): the f16 cache rounds each value
+ * to nearest even; Q8_0 and Q4_0 rows are quantize_f32_to_q8_0 /
+ * quantize_f32_to_q4_0 of the whole row (blocks of 32 along it). */
+void orc_kv_store(const float *x, uint8_t *dst, size_t n, int fmt)
+{
+    if (fmt == 1) {
+        orc_quantize_q8_0(x, dst, n);
+    } else if (fmt == 2) {
+        orc_quantize_q4_0(x, dst, n);
+    } else {
+        for (size_t i = 0; i < n; i++) wr16(dst + 2 * i, orc_f32_to_f16_rne(x[i]));
+    }
+}
+
+/* KvCacheRow::dot_head (kv_cache.rs:73-95) of one head's cached keys:
+ *   fmt 0: -0.0 + q[0]*k[0] + ... in d order (the f16 cache widened exactly);
+ *   fmt 1 / 2: vec_dot_q8_0_q8_0 / vec_dot_q4_0_q8_0 of the head's K blocks
+ *     with q8 = quantize_f32_to_q8_0(q) (model.rs:1530-1531), the scalar fold
+ *     (the AVX-VNNI path gives the same bits; quant.rs:406-439). */
+float orc_kv_dot_head(const uint8_t *row, const float *q, const uint8_t *q8, size_t head_dim, int fmt)
+{
+    if (fmt == 1) return dot_q8_0_q8_0_scalar(row, q8, head_dim);
+    if (fmt == 2) return dot_q4_0_q8_0_scalar(row, q8, head_dim);
+    float dot = -0.0f;
+    for (size_t d = 0; d < head_dim; d++) dot += q[d] * orc_f16_to_f32(rd16(row + 2 * d));
+    return dot;
+}
+
+/* KvCacheRow::add_head_scaled (kv_cache.rs:97-125):
+ *   fmt 0: out[d] += p * v[d];
+ *   fmt 1: per block b, dd = f16(d_b) * p, out[32b+i] += dd * q_i;
+ *   fmt 2: per block b, dd = f16(d_b) * p, out[32b+i] += dd * (lo_i - 8) and
+ *          out[32b+16+i] += dd * (hi_i - 8) for byte i. */
+void orc_kv_add_head_scaled(const uint8_t *row, float *out, size_t head_dim, float p, int fmt)
+{
+    if (fmt == 0) {
+        for (size_t d = 0; d < head_dim; d++) out[d] += p * orc_f16_to_f32(rd16(row + 2 * d));
+        return;
+    }
+    const size_t bb = fmt == 1 ? 34 : 18;
+    for (size_t b = 0; b < head_dim / 32; b++) {
+        const uint8_t *blk = row + b * bb;
+        const float dd = orc_f16_to_f32(rd16(blk)) * p;
+        float *o = out + 32 * b;
+        if (fmt == 1) {
+            for (int i = 0; i < 32; i++) o[i] += dd * (float)(int8_t)blk[2 + i];
+        } else {
+            for (int i = 0; i < 16; i++) {
+                o[i] += dd * (float)((int)(blk[2 + i] & 15) - 8);
+                o[i + 16] += dd * (float)((int)(blk[2 + i] >> 4) - 8);
+            }
+        }
+    }
+}
+
+/* Attention over caches in those formats, the CPU loop of model.rs:1526-1547:
+ * per query head h (kv head h / (n_heads / n_kv_heads)), score_t =
+ * dot_head(k_t) * scale (the reference model's scale is 1.0, which leaves
+ * the dot as it is), softmax (ops.rs:133-158), then out = 0 and
+ * add_head_scaled(v_t, p_t) position by position.  Caches are
+ * [pos][n_kv_heads][head_dim] in the formats' bytes; positions 0..n_past are
+ * attended.  With both formats 0 this is orc_attention_f16. */
+void orc_attention_kv(const float *q, const uint8_t *k_cache, const uint8_t *v_cache, float *out, size_t n_past,
+                      size_t n_heads, size_t n_kv_heads, size_t head_dim, float scale, int k_fmt, int v_fmt)
+{
+    const size_t count = n_past + 1, group = n_heads / n_kv_heads;
+    const size_t k_head = orc_kv_row_bytes(head_dim, k_fmt), v_head = orc_kv_row_bytes(head_dim, v_fmt);
+    const size_t k_row = k_head * n_kv_heads, v_row = v_head * n_kv_heads;
+    float *scores = (float *)malloc(count * sizeof(float));
+    uint8_t *q8 = (uint8_t *)malloc(head_dim / 32 * 34 + 34);
+    for (size_t h = 0; h < n_heads; h++) {
+        const size_t kv_h = h / group;
+        const float *qh = q + h * head_dim;
+        if (k_fmt != 0) orc_quantize_q8_0(qh, q8, head_dim);
+        for (size_t t = 0; t < count; t++)
+            scores[t] = orc_kv_dot_head(k_cache + t * k_row + kv_h * k_head, qh, q8, head_dim, k_fmt) * scale;
+        orc_softmax(scores, count);
+        float *oh = out + h * head_dim;
+        for (size_t d = 0; d < head_dim; d++) oh[d] = 0.0f;
+        for (size_t t = 0; t < count; t++)
+            orc_kv_add_head_scaled(v_cache + t * v_row + kv_h * v_head, oh, head_dim, scores[t], v_fmt);
+    }
+    free(q8);
+    free(scores);
+}
+
+/* ------------------------------------------------------------------------ */
 /* Build-defined Gemma-2-2B-shape decode step (composition of the reference
  * ops in the order of model.rs:1185-2260, with Gemma-2's dense GeGLU FFN,
  * sandwich norms, 1/sqrt(head_dim) attention scale and a tied table). */

@@ -138,6 +138,23 @@ void orc_attention_f16(const float *q, const uint16_t *k_cache, const uint16_t *
                        float *out, size_t n_past, size_t n_heads, size_t n_kv_heads,
                        size_t head_dim, float scale);
 
+/* ---- KV cache formats (kv_cache.rs:8-125; KvCacheFormat::cuda_code 0 f16,
+ * 1 Q8_0, 2 Q4_0) ---------------------------------------------------------- */
+/* Bytes of n cached values in format fmt (n % 32 == 0 for 1 and 2). */
+size_t orc_kv_row_bytes(size_t n, int fmt);
+/* KvCacheRow::from_f32: f16 (round to nearest even), quantize_f32_to_q8_0 or
+ * quantize_f32_to_q4_0 of n values. */
+void   orc_kv_store(const float *x, uint8_t *dst, size_t n, int fmt);
+/* KvCacheRow::dot_head: q . k of one head's cached keys; q8 =
+ * quantize_f32_to_q8_0(q) (read for formats 1 and 2 only). */
+float  orc_kv_dot_head(const uint8_t *row, const float *q, const uint8_t *q8, size_t head_dim, int fmt);
+/* KvCacheRow::add_head_scaled: out += p * v of one head's cached values. */
+void   orc_kv_add_head_scaled(const uint8_t *row, float *out, size_t head_dim, float p, int fmt);
+/* Attention over caches of those formats (model.rs:1526-1547): positions
+ * 0..n_past of [pos][n_kv_heads][head_dim] rows in the formats' bytes. */
+void   orc_attention_kv(const float *q, const uint8_t *k_cache, const uint8_t *v_cache, float *out, size_t n_past,
+                        size_t n_heads, size_t n_kv_heads, size_t head_dim, float scale, int k_fmt, int v_fmt);
+
 /* ---- Gemma-2-2B-shape decode step (build-defined composition) ---------- */
 typedef struct orc_gemma2 {
     int32_t n_layers, dim, n_heads, n_kv_heads, head_dim, ffn_dim, vocab, ctx;

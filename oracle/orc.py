@@ -67,6 +67,11 @@ _SIG = {
     "orc_swiglu": ([_P, _P, _P, _Z], None),
     "orc_softmax": ([_P, _Z], None),
     "orc_attention_f16": ([_P, _P, _P, _P, _Z, _Z, _Z, _Z, _F], None),
+    "orc_kv_row_bytes": ([_Z, _I], _Z),
+    "orc_kv_store": ([_P, _P, _Z, _I], None),
+    "orc_kv_dot_head": ([_P, _P, _P, _Z, _I], _F),
+    "orc_kv_add_head_scaled": ([_P, _P, _Z, _F, _I], None),
+    "orc_attention_kv": ([_P, _P, _P, _P, _Z, _Z, _Z, _Z, _F, _I, _I], None),
     "orc_gemma2_step": ([ctypes.POINTER(Gemma2), ctypes.c_int64, ctypes.c_int64, _P, _P, _P, _I], ctypes.c_int64),
 }
 
@@ -281,6 +286,46 @@ def attention_f16(q, k_cache, v_cache, n_past, n_heads, n_kv_heads, head_dim, sc
     lib().orc_attention_f16(_p(q), _p(np.ascontiguousarray(k_cache, dtype=np.uint16)),
                             _p(np.ascontiguousarray(v_cache, dtype=np.uint16)), _p(out), n_past, n_heads,
                             n_kv_heads, head_dim, scale)
+    return out
+
+
+def kv_row_bytes(n: int, fmt: int) -> int:
+    """Bytes of n cached values in KV format fmt (0 f16, 1 Q8_0, 2 Q4_0)."""
+    return int(lib().orc_kv_row_bytes(n, fmt))
+
+
+def kv_store(x, fmt: int) -> np.ndarray:
+    """KvCacheRow::from_f32 (kv_cache.rs:54-71) of x in format fmt, as bytes."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.zeros(kv_row_bytes(x.size, fmt), np.uint8)
+    lib().orc_kv_store(_p(x), _p(out), x.size, fmt)
+    return out
+
+
+def kv_dot_head(row, q, fmt: int) -> float:
+    """KvCacheRow::dot_head (kv_cache.rs:73-95) of one head's cached keys."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    row = np.ascontiguousarray(row, dtype=np.uint8)
+    q8 = quantize_q8_0(q) if fmt else np.zeros(34, np.uint8)
+    return float(lib().orc_kv_dot_head(_p(row), _p(q), _p(q8), q.size, fmt))
+
+
+def kv_add_head_scaled(row, out, p: float, fmt: int) -> np.ndarray:
+    """KvCacheRow::add_head_scaled (kv_cache.rs:97-125): out += p * v, in place."""
+    row = np.ascontiguousarray(row, dtype=np.uint8)
+    assert out.dtype == np.float32 and out.flags.c_contiguous
+    lib().orc_kv_add_head_scaled(_p(row), _p(out), out.size, p, fmt)
+    return out
+
+
+def attention_kv(q, k_cache, v_cache, n_past, n_heads, n_kv_heads, head_dim, scale, k_fmt, v_fmt) -> np.ndarray:
+    """Attention over caches of KV formats k_fmt / v_fmt (orc_attention_kv):
+    caches are the bytes of positions 0..n_past, [pos][n_kv_heads][head_dim]."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    out = np.zeros(n_heads * head_dim, dtype=np.float32)
+    kc = np.ascontiguousarray(k_cache).view(np.uint8)
+    vc = np.ascontiguousarray(v_cache).view(np.uint8)
+    lib().orc_attention_kv(_p(q), _p(kc), _p(vc), _p(out), n_past, n_heads, n_kv_heads, head_dim, scale, k_fmt, v_fmt)
     return out
 
 

@@ -591,6 +591,120 @@ def test_attention_f16_against_float64(orc):
 
 
 # ---------------------------------------------------------------- Q4_K (build-defined)
+# ---------------------------------------------------------------- quantised KV caches
+def test_kv_row_bytes_reference_sizes(orc):
+    # kv_cache.rs:164-169 (cuda_layout_sizes_match_block_formats): f16 rows, Q8_0 and Q4_0 blocks
+    assert orc.kv_row_bytes(2048, 0) == 4096
+    assert orc.kv_row_bytes(2048, 1) == 2176
+    assert orc.kv_row_bytes(2048, 2) == 1152
+
+
+def test_kv_quantised_rows_reference_case(orc):
+    """kv_cache.rs:133-161 (quantized_rows_preserve_attention_operations):
+    the second head (offset 64) of a 128-value row, dot within 0.03 (Q8) and
+    1.0 (Q4) of the exact f32 dot, and add_head_scaled(0.37) within the same."""
+    values = ((np.arange(128) * 29 % 97).astype(np.float32) - 48.0) / np.float32(23.0)
+    query = ((np.arange(64) * 11 % 53).astype(np.float32) - 26.0) / np.float32(17.0)
+    exact = np.float32(np.dot(values[64:].astype(np.float64), query.astype(np.float64)))
+    for fmt, tol in ((1, 0.03), (2, 1.0)):
+        row = orc.kv_store(values, fmt)
+        head = row[orc.kv_row_bytes(64, fmt):]
+        assert abs(orc.kv_dot_head(head, query, fmt) - exact) < tol
+        out = orc.kv_add_head_scaled(head, np.zeros(64, np.float32), 0.37, fmt)
+        assert np.max(np.abs(out - values[64:] * np.float32(0.37))) < tol
+
+
+def test_kv_store_formats(orc):
+    rng = np.random.default_rng(70)
+    x = (rng.standard_normal(256) * 3).astype(np.float32)
+    assert np.array_equal(orc.kv_store(x, 0).view(np.uint16), x.astype(np.float16).view(np.uint16))  # RNE
+    assert np.array_equal(orc.kv_store(x, 1), orc.quantize_q8_0(x))
+    assert np.array_equal(orc.kv_store(x, 2), orc.quantize_q4_0(x))
+
+
+def numpy_kv_head(row: np.ndarray, fmt: int, hd: int):
+    """(int64 quants [hd], f32 block scales [hd/32]) of one cached head."""
+    if fmt == 1:
+        q, d = unpack_q8_0(row, hd // 32)
+    else:
+        q, d = unpack_q4_0(row, hd // 32)
+    return q.reshape(-1), d.reshape(-1)
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
+def test_kv_dot_and_add_brute_force(orc, fmt):
+    """dot_head and add_head_scaled of Q8_0 / Q4_0 heads against numpy: int64
+    block sums of the quants with quantize_q8_0(q), the float32 block fold
+    s = s + isum * (d_k * d_q); out += (d * p) * q per value.  A swapped
+    nibble half, a missing -8, p * (d * q) instead of (d * p) * q, or an FMA
+    each fail it (p carries full mantissa bits)."""
+    rng = np.random.default_rng(71 + fmt)
+    for hd in (32, 64, 256, 512):
+        nb = hd // 32
+        for trial in range(20):
+            x = (rng.standard_normal(hd) * 10.0 ** rng.uniform(-2, 2)).astype(np.float32)
+            q = rng.standard_normal(hd).astype(np.float32)
+            row = orc.kv_store(x, fmt)
+            kq, kd = numpy_kv_head(row, fmt, hd)
+            q8 = orc.quantize_q8_0(q)
+            aq, ad = unpack_q8_0(q8, nb)
+            isum = (kq.reshape(nb, 32) * aq.reshape(nb, 32)).sum(axis=1)
+            s = np.float32(0.0)
+            for b in range(nb):
+                s = np.float32(s + np.float32(np.float32(isum[b]) * np.float32(kd[b] * ad.reshape(-1)[b])))
+            assert np.float32(orc.kv_dot_head(row, q, fmt)) == s
+            p = np.float32(rng.uniform(0.01, 1.0))
+            base = rng.standard_normal(hd).astype(np.float32)
+            got = orc.kv_add_head_scaled(row, base.copy(), float(p), fmt)
+            dd = np.repeat((kd * p).astype(np.float32), 32)
+            want = (base + (dd * kq.astype(np.float32)).astype(np.float32)).astype(np.float32)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (hd, trial)
+
+
+def test_attention_kv_f16_is_attention_f16(orc):
+    rng = np.random.default_rng(72)
+    nh, nkv, hd, n_past = 8, 2, 128, 17
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    kc = rng.standard_normal((n_past + 1) * nkv * hd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((n_past + 1) * nkv * hd).astype(np.float16).view(np.uint16)
+    a = orc.attention_f16(q, kc, vc, n_past, nh, nkv, hd, 0.0884)
+    b = orc.attention_kv(q, kc, vc, n_past, nh, nkv, hd, 0.0884, 0, 0)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("kf,vf", [(1, 1), (2, 2), (1, 0), (0, 2)])
+def test_attention_kv_against_float64(orc, kf, vf):
+    """Quantised caches: within float32 rounding of float64 attention over the
+    dequantised caches with the query's Q8_0 quantisation (K formats 1, 2)
+    -- a wrong kv head, nibble order, scale or format mix-up fails it; the
+    group mapping h -> h / (n_heads / n_kv_heads) is checked through head 5."""
+    rng = np.random.default_rng(73 + 3 * kf + vf)
+    nh, nkv, hd, n_past = 8, 2, 64, 12
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    kx = rng.standard_normal((n_past + 1, nkv, hd)).astype(np.float32)
+    vx = rng.standard_normal((n_past + 1, nkv, hd)).astype(np.float32)
+    kc = np.concatenate([orc.kv_store(r, kf) for r in kx.reshape(n_past + 1, -1)])
+    vc = np.concatenate([orc.kv_store(r, vf) for r in vx.reshape(n_past + 1, -1)])
+    out = orc.attention_kv(q, kc, vc, n_past, nh, nkv, hd, 1.0, kf, vf).reshape(nh, hd)
+
+    def deq(buf, fmt):
+        rows = buf.reshape(n_past + 1, -1)
+        if fmt == 0:
+            return rows.view(np.float16).astype(np.float64).reshape(n_past + 1, nkv, hd)
+        f = orc.dequantize_q8_0 if fmt == 1 else orc.dequantize_q4_0
+        return np.stack([f(r, nkv * hd) for r in rows]).astype(np.float64).reshape(n_past + 1, nkv, hd)
+
+    k64, v64 = deq(kc, kf), deq(vc, vf)
+    for h in range(nh):
+        qh = q[h * hd:(h + 1) * hd]
+        q64 = orc.dequantize_q8_0(orc.quantize_q8_0(qh), hd).astype(np.float64) if kf else qh.astype(np.float64)
+        sc = k64[:, h // (nh // nkv)] @ q64
+        w = np.exp(sc - sc.max())
+        w /= w.sum()
+        ref = w @ v64[:, h // (nh // nkv)]
+        assert np.max(np.abs(out[h] - ref)) <= 2e-5 * max(1.0, np.max(np.abs(ref))), h
+
+
 def numpy_q4_k_dequant(blocks: np.ndarray, nsb: int) -> np.ndarray:
     """Independent GGUF Q4_K dequantiser (from the published format)."""
     b = blocks.reshape(nsb, 144)
