@@ -119,6 +119,38 @@ def sample_launches(dev, ev, graph, per_graph: int, samples: int = 7, min_launch
             "samples": samples}
 
 
+# Streaming-read floors: the bytes of each matvec here read by the product's
+# plain read kernel (mrml_hip_read_kernel: 16-byte non-temporal loads, nothing
+# written), one launch per slice of a 700 MB buffer, so no launch finds its
+# bytes in the MALL -- what one launch of that size cannot beat on this GPU.
+READ_FLOOR_SIZES = {"q8_0_2048x2048": 2048 * 2048 // 32 * 34, "qkv_4096x2304": 4096 * Q4_ROW(DIM),
+                    "gate_9216x2304": W_BYTES, "geglu_2x9216x2304": 2 * W_BYTES,
+                    "lm_head_256000x2304": 256000 * Q4_ROW(DIM)}
+
+
+def read_floors(be, dev, ev) -> dict:
+    """Median and min µs per launch of the read kernel at each size."""
+    span = 700 << 20
+    buf = be.HipBuffer(dev, span)
+    sink = be.HipBuffer(dev, 1024)
+    dev.zero(buf, span)
+    out = {}
+    for name, nbytes in READ_FLOOR_SIZES.items():
+        nb16 = (nbytes + 15) // 16 * 16
+        step = (nbytes + 4095) // 4096 * 4096
+        n = max(2, min(128, span // step))
+        g = dev.capture(lambda: [dev.read_kernel(buf.ptr + i * step, nb16, sink) for i in range(n)])
+        st = sample_launches(dev, ev, g, n)
+        g.close()
+        out[name] = {"bytes": nbytes, "us": round(st["median_s"] * 1e6, 3), "us_min": round(st["min_s"] * 1e6, 3),
+                     "gb_s": round(nbytes / st["median_s"] / 1e9, 1),
+                     "pct_of_hbm_peak": round(100 * nbytes / st["median_s"] / 1e9 / PEAK_HBM_GBS, 2),
+                     "slices": n}
+    buf.close()
+    sink.close()
+    return out
+
+
 def kernel_source_hash(files=("gemv_q4_0.hip", "device.h", "exact_sum.h", "norm_block.h", "libm_f32.h")) -> str:
     """sha256 (16 hex digits) of the sources the Q4_0 matvec kernels' code is
     generated from: a committed counter reading applies only to the kernels
@@ -805,6 +837,7 @@ def main() -> int:
     st_copy = sample_launches(dev, ev, gcp, ncp)
     gcp.close()
     dev.sync()
+    floors = read_floors(be, dev, ev)
 
     cpu = None
     if not args.no_cpu:
@@ -827,6 +860,14 @@ def main() -> int:
                                           0 if args.no_cpu else args.cpu_decode_steps)
         decode["fast"] = decode_fast_bench(be, synth, dev, ev, args.decode_prefill, args.decode_tokens,
                                            decode.pop("_exact_hist"))
+    # each matvec against the read floor of its own bytes (floor µs / kernel µs)
+    vs_floor = {"gate": floors["gate_9216x2304"]["us"] / (st_gate["median_s"] * 1e6),
+                "down": floors["gate_9216x2304"]["us"] / (st_down["median_s"] * 1e6),
+                "fused_gate_up_geglu": floors["geglu_2x9216x2304"]["us"] / (k_geglu * 1e6)}
+    if q8:
+        vs_floor["q8_0"] = floors["q8_0_2048x2048"]["us"] / q8["us_median"]
+    if q4k:
+        vs_floor["q4_k"] = floors["lm_head_256000x2304"]["us"] / q4k["us_median"]
 
     line = {
         "metric": "Q4_0 matvec GB/s (Gemma-2-2B FFN: fused gate+up GeGLU + down, batch 1)",
@@ -864,6 +905,10 @@ def main() -> int:
                           for k_, v_ in (("geglu", st_geglu), ("gate", st_gate), ("up", st_up), ("down", st_down))},
         "per_matrix_rotation": f"each kernel over all {sets * 3} pool matrices ({sets * 3 * W_BYTES} B)",
         "stream_copy_gbs": round(copy_gbs, 1),
+        "read_floor": {"sizes": floors,
+                       "how": "mrml_hip_read_kernel (16-byte non-temporal loads, nothing written) over slices of a "
+                              "700 MB buffer, graph replays, median per launch: the one-launch floor for those bytes"},
+        "matvec_vs_read_floor": {k_: round(v_, 3) for k_, v_ in vs_floor.items()},
         "launch_floor": {"zero_fill_256B_us": round(st_zero["median_s"] * 1e6, 3),
                          "copy_11.94MB_us": round(st_copy["median_s"] * 1e6, 3),
                          "how": "product kernels (mrml_hip_zero_async, mrml_hip_copy_kernel) replayed in a graph, "

@@ -127,6 +127,11 @@ int mrml_hip_zero_async(mrml_hip_ctx *ctx, void *d_dst, size_t bytes);
  * reference counterpart: the bandwidth ceiling and the known-size kernel that
  * calibrates HBM byte counters in the measurements. */
 int mrml_hip_copy_kernel(mrml_hip_ctx *ctx, void *d_dst, const void *d_src, size_t bytes);
+/* Streaming read of `bytes` (16-byte aligned) with the weight streams'
+ * non-temporal loads, writing nothing but (rarely) a word of the 1 KiB
+ * d_sink.  No reference counterpart: the read-only floor that a matvec
+ * streaming the same bytes in one launch cannot beat. */
+int mrml_hip_read_kernel(mrml_hip_ctx *ctx, const void *d_src, size_t bytes, void *d_sink);
 
 /* ---- weight layout conversion (upload path; model.rs:651-705 uploads GGUF
  *      bytes unchanged, this backend converts them once after upload) ------- */
@@ -233,8 +238,8 @@ int mrml_hip_gemv_q4_k_q8(mrml_hip_ctx *ctx, const void *d_w, const void *d_xpac
  * d_y[m][r] = dot(W[r], Q8_0(x[m])) with the CPU semantics of
  * ops::mat_vec_mul_q4_0 (ops.rs:162-180) for every token m, each output
  * bit-identical to mrml_hip_gemv_q4_0 on that token.  The integer block dots
- * run on int8 MFMA.  rows % 32 == 0, cols % 32 == 0; W and the activations
- * each below 2 GiB.  Uses the context workspace (batch/32 * cols/32 * 1152
+ * run on int8 MFMA.  Any rows (the reference grid is ceil(rows / 8),
+ * cuda.rs:627-673), cols % 32 == 0; W and the activations each below 2 GiB.  Uses the context workspace (batch/32 * cols/32 * 1152
  * bytes rounded up) for the activations in MFMA order. */
 int mrml_hip_gemm_q4_0(mrml_hip_ctx *ctx, const void *d_w, const float *d_x, float *d_y,
                        int32_t rows, int32_t cols, int32_t batch);
@@ -392,10 +397,14 @@ int mrml_hip_rope_kv_append_f16(mrml_hip_ctx *ctx, float *d_qkv, uint16_t *d_k_c
  * kernels.rs:1231-1330; called by prefill_cuda, model.rs:2485-2501) without
  * the Gemma-4 head norms: `batch` stacked [q | k | v] rows of d_qkv, row i
  * rotated at position start_pos + i as mrml_hip_rope_kv_append_f16 rotates
- * one row, its k and v stored as f16 at cache row (cache_start + i) %
- * capacity.  batch <= capacity (rows of one call never share a cache row);
- * k_format / v_format must be 0 (f16 rows).  freq_scale 1 is the
- * reference's (the batched kernel has none). */
+ * one row, its k and v stored at cache row (cache_start + i) % capacity in
+ * the caches' formats (KvCacheFormat::cuda_code, kv_cache.rs:16-31): 0 f16
+ * (round to nearest even), 1 Q8_0 or 2 Q4_0 blocks of 32 along each head
+ * (quantize_f32_to_q8_0 / _q4_0, quant.rs:193-228, 372-389, as
+ * KvCacheRow::from_f32 stores them; head_dim % 32 == 0), rows of
+ * n_kv_heads*head_dim/32 blocks of 34 or 18 bytes.  batch <= capacity (rows
+ * of one call never share a cache row).  freq_scale 1 is the reference's
+ * (the batched kernel has none). */
 int mrml_hip_rope_kv_append_f16_batch(mrml_hip_ctx *ctx, float *d_qkv, uint16_t *d_k_cache, uint16_t *d_v_cache,
                                       int32_t start_pos, int32_t cache_start, int32_t batch, int32_t n_heads,
                                       int32_t n_kv_heads, int32_t head_dim, float freq_base, float freq_scale,
@@ -423,12 +432,13 @@ int mrml_hip_add(mrml_hip_ctx *ctx, const float *d_a, const float *d_b, float *d
  * for one token: out[h] = softmax(scale * q[h] . K[t]) . V[t] over the last
  * min(n_past+1, capacity) cache rows, kv head h / (n_heads / n_kv_heads),
  * in the CPU path's operation order (sequential dots, softmax sum and
- * weighted sum; the host C library's expf).  head_dim 256, group of at most
- * 8, capacity at most 131072: past 6144 the window's exps are summed in
- * LDS-staged chunks, each chunk's exact sequential sum continuing the
- * running sum (the same bits; the reference streams such windows through
- * its online-softmax kernel, kernels.rs:1463-1561).  d_out (f32) and d_pack
- * (Q8_0 pack of the n_heads*head_dim output) nullable, not both. */
+ * weighted sum; the host C library's expf).  head_dim a multiple of 32 up
+ * to 512, groups of at most 16, capacity at most 2^20: past 6144 the
+ * window's exps are summed in LDS-staged chunks, each chunk's exact
+ * sequential sum continuing the running sum (the same bits; the reference
+ * streams such windows through its online-softmax kernel,
+ * kernels.rs:1463-1561).  d_out (f32) and d_pack (Q8_0 pack of the
+ * n_heads*head_dim output) nullable, not both. */
 int mrml_hip_attn_decode_f16(mrml_hip_ctx *ctx, const float *d_q, const uint16_t *d_k_cache,
                              const uint16_t *d_v_cache, float *d_out, void *d_pack, int32_t n_past,
                              const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
@@ -439,7 +449,8 @@ int mrml_hip_attn_decode_f16(mrml_hip_ctx *ctx, const float *d_q, const uint16_t
  * in f32 tree order, then a merge in tile order): the FAST numerics of the
  * token step (MRML_HIP_NUMERICS_FAST).  Within 1e-5 of the CPU path relative
  * to the output's largest magnitude, not bit-identical.  Same arguments and
- * limits as mrml_hip_attn_decode_f16 (attention_causal, cuda.rs:2658-2697). */
+ * limits as mrml_hip_attn_decode_f16 (attention_causal, cuda.rs:2658-2697);
+ * shapes other than head_dim 256 with groups up to 8 run the exact form. */
 int mrml_hip_attn_decode_f16_split(mrml_hip_ctx *ctx, const float *d_q, const uint16_t *d_k_cache,
                                    const uint16_t *d_v_cache, float *d_out, void *d_pack, int32_t n_past,
                                    const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
@@ -452,8 +463,13 @@ int mrml_hip_attn_decode_f16_split(mrml_hip_ctx *ctx, const float *d_q, const ui
  * window to the last sliding_window positions (<= 0: no limit beyond the
  * capacity).  The arithmetic of mrml_hip_attn_decode_f16, bit-identical to
  * the CPU path over the same rows.  k_format / v_format: the cache formats
- * of KvCacheFormat::cuda_code (kv_cache.rs:16-22); only 0 (f16 rows) is
- * served, others return MRML_HIP_E_UNSUPPORTED.  head_dim 256. */
+ * of KvCacheFormat::cuda_code (kv_cache.rs:16-22): 0 f16 rows, 1 Q8_0 and
+ * 2 Q4_0 blocks (rows as mrml_hip_rope_kv_append_f16_batch stores them);
+ * scores are then KvCacheRow::dot_head -- the block-ordered Q8_0 x Q8_0 or
+ * Q4_0 x Q8_0 fold against quantize_f32_to_q8_0(q_h) -- times scale, and the
+ * values add (f16(d) * p) * q per value (add_head_scaled,
+ * kv_cache.rs:73-125).  Other codes return MRML_HIP_E_UNSUPPORTED.  Limits
+ * as mrml_hip_attn_decode_f16. */
 int mrml_hip_attention_causal(mrml_hip_ctx *ctx, const float *d_q, const uint16_t *d_k_cache,
                               const uint16_t *d_v_cache, float *d_out, int32_t n_past, int32_t n_heads,
                               int32_t n_kv_heads, int32_t head_dim, float scale, int32_t sliding_window,
@@ -471,7 +487,7 @@ int mrml_hip_attention_causal_split(mrml_hip_ctx *ctx, const float *d_q, const u
  * floats into d_q (the reference's q.len() / batch, >= n_heads*head_dim),
  * output row i (n_heads*head_dim floats) at d_out + i*n_heads*head_dim.  Row
  * i is bit-identical to mrml_hip_attention_causal at n_past = cache_start + i
- * with the same sliding window, capacity and formats (0 only). */
+ * with the same sliding window, capacity and formats. */
 int mrml_hip_attention_prefill(mrml_hip_ctx *ctx, const float *d_q, int32_t q_stride, const uint16_t *d_k_cache,
                                const uint16_t *d_v_cache, float *d_out, int32_t cache_start, int32_t batch,
                                int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, float scale,

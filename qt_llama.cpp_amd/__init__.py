@@ -137,6 +137,7 @@ _SIGNATURES = {
     "mrml_hip_memcpy_d2d_async": [_P, _P, _P, _Z],
     "mrml_hip_zero_async": [_P, _P, _Z],
     "mrml_hip_copy_kernel": [_P, _P, _P, _Z],
+    "mrml_hip_read_kernel": [_P, _P, _Z, _P],
     "mrml_hip_repack_q4_0": [_P, _P, _P, _I, _I],
     "mrml_hip_repack_q8_0": [_P, _P, _P, _I, _I],
     "mrml_hip_repack_q4_k": [_P, _P, _P, _I, _I],
@@ -400,6 +401,10 @@ class HipDevice:
 
     def copy_kernel(self, dst, src, nbytes: int) -> None:
         self._check(self.lib.mrml_hip_copy_kernel(self.ctx, _ptr(dst), _ptr(src), nbytes))
+
+    def read_kernel(self, src, nbytes: int, sink) -> None:
+        """Streaming read of nbytes of src (the read-only floor of a matvec's weight stream)."""
+        self._check(self.lib.mrml_hip_read_kernel(self.ctx, _ptr(src), nbytes, _ptr(sink)))
 
     # ---- ops (names follow CudaDevice) -----------------------------------------
     def quantize_q8_0(self, x, q8_gguf=None, pack=None, n: int | None = None) -> None:

@@ -285,12 +285,12 @@ __global__ __launch_bounds__(512) void rope_kv_f16_kernel(float *__restrict__ qk
         const float r1 = v0 * s + v1 * c;
         v[i] = r0;
         v[i + half] = r1;
-        if (g >= n_heads) {
+        if (g >= n_heads && k_cache) {  // null caches: rotation only (quantised caches append after)
             uint16_t *dst = k_cache + cache_row + (size_t)(g - n_heads) * head_dim;
             dst[i] = f32_to_f16_rne(r0);
             dst[i + half] = f32_to_f16_rne(r1);
         }
-    } else {
+    } else if (v_cache) {
         const int vh = g - n_heads - n_kv_heads;
         const float *src = qkv + (size_t)(n_heads + n_kv_heads) * head_dim + (size_t)vh * head_dim;
         uint16_t *dst = v_cache + cache_row + (size_t)vh * head_dim;
@@ -416,6 +416,225 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kScoreT = 256;              // threads per score workgroup
 
+
+// ---- attention over caches of any head size and KV format ------------------------
+//
+// The tuned kernels around this section serve the Gemma-2 shape (head_dim
+// 256, f16 rows).  These serve every head_dim that is a multiple of 32 up
+// to 512, groups of up to 16 query heads per kv head, and the reference's
+// three cache formats (KvCacheFormat::cuda_code, kv_cache.rs:16-31): 0 f16
+// rows (round to nearest even), 1 Q8_0 and 2 Q4_0 blocks of 32 values along
+// a head, [capacity][n_kv_heads][head_dim/32 blocks] of 34 or 18 bytes.
+// The arithmetic is the CPU loop's (model.rs:1526-1547 over
+// KvCacheRow::dot_head / add_head_scaled, kv_cache.rs:73-125).
+
+// K/V of a batch of stacked q|k|v rows, k already rotated in place (by
+// rope_kv_f16_kernel with null caches), stored in the caches' formats
+// (KvCacheRow::from_f32, kv_cache.rs:54-71): f16 by rounding to nearest
+// even, Q8_0 and Q4_0 by the reference quantisers (quant.rs:193-228,
+// 372-389) over each head's blocks of 32.  Grid (2 * n_kv_heads, rows):
+// workgroup x < n_kv_heads stores k head x, the rest the v heads; lanes
+// 0-31 and 32-63 take one block each.  Row z goes to cache row
+// (pos0 + z + cache_shift) % capacity.
+template <int KF, int VF>
+__global__ __launch_bounds__(64) void kv_append_any_kernel(const float *__restrict__ qkv, uint8_t *__restrict__ k_cache,
+                                                           uint8_t *__restrict__ v_cache, int pos0, int n_heads,
+                                                           int n_kv_heads, int head_dim, int capacity, int cache_shift)
+{
+    const int z = blockIdx.y, g = blockIdx.x, lane = threadIdx.x, l = lane & 31;
+    const bool is_k = g < n_kv_heads;
+    const int head = is_k ? g : g - n_kv_heads, fmt = is_k ? KF : VF, nb = head_dim / 32;
+    // k heads follow the q heads and v heads follow the k heads
+    const float *src = qkv + (size_t)z * (n_heads + 2 * n_kv_heads) * head_dim + (size_t)(n_heads + g) * head_dim;
+    const size_t bb = fmt == 0 ? 64 : (fmt == 1 ? 34 : 18);
+    const int cpos = pos0 + z + cache_shift;
+    uint8_t *dst = (is_k ? k_cache : v_cache) + (size_t)(cpos % capacity) * n_kv_heads * nb * bb + (size_t)head * nb * bb;
+    for (int b0 = 0; b0 < nb; b0 += 2) {  // uniform: every lane runs the block quantisers
+        const int b = b0 + (lane >> 5);
+        const float v = b < nb ? src[b * 32 + l] : 0.0f;
+        uint8_t *blk = dst + (size_t)b * bb;
+        if (fmt == 0) {
+            if (b < nb) reinterpret_cast<uint16_t *>(blk)[l] = f32_to_f16_rne(v);
+        } else if (fmt == 1) {
+            uint32_t dbits;
+            int qsum;
+            const int qv = q8_0_block32(v, dbits, qsum);
+            if (b < nb) {
+                if (l == 0) *reinterpret_cast<uint16_t *>(blk) = (uint16_t)dbits;
+                blk[2 + l] = (uint8_t)(int8_t)qv;
+            }
+        } else {
+            uint32_t dbits;
+            const int qv = q4_0_block32(v, dbits);
+            const int hi = __shfl_down(qv, 16, 64);  // value l + 16 of the block (same 32-lane half for l < 16)
+            if (b < nb) {
+                if (l == 0) *reinterpret_cast<uint16_t *>(blk) = (uint16_t)dbits;
+                if (l < 16) blk[2 + l] = (uint8_t)(qv | (hi << 4));
+            }
+        }
+    }
+}
+
+// Scores over K rows of format KF: score[h][p] = dot_head(q_h, k_{start+p}) *
+// scale, dot_head as kv_cache.rs:73-95 -- f16: -0.0 + q[0]*k[0] + ... in d
+// order; Q8_0 / Q4_0: the block-ordered fold s = s + (float)isum_b * (d_k *
+// d_q) over the head's blocks against quantize_f32_to_q8_0(q_h) (formed
+// here, per head, with the reference quantiser).  Workgroup (tile of 64
+// positions, kv head, query row): lane p owns position p0 + p and wave w
+// the heads w, w + 4, ... of the group; the K tile is staged through LDS in
+// passes of 128 dims (f16 rows as they are; quantised blocks re-laid as
+// 4-byte-aligned quants plus f32 scales), every chain carried across passes
+// in registers.  Dynamic LDS as attn_any_scores_lds says.
+constexpr int kAnyP = 64;                   // positions per workgroup (one per lane)
+constexpr int kAnyT = 256;                  // 4 waves
+constexpr int kAnyCh = 128;                 // dims per pass (4 blocks)
+constexpr int kAnyMaxG = 16, kAnyMaxHD = 512;
+constexpr int kAnyHPT = kAnyMaxG / 4;       // heads per thread at most
+constexpr int kAnyKRow = kAnyCh * 2 + 16;   // f16 tile row stride, bytes
+constexpr int kAnyDS = 5;                   // scale row stride (floats) of a quantised tile
+
+__host__ __device__ constexpr int any_quant_row(int kf) { return 4 * (kf == 2 ? 16 : 32) + 4; }  // quant bytes per tile row
+inline size_t attn_any_scores_lds(int kf, int G, int HD)
+{
+    if (kf == 0) return (size_t)G * HD * 4 + (size_t)kAnyP * kAnyKRow;
+    const size_t qpart = ((size_t)G * HD + (size_t)G * (HD / 32) * 8 + 15) / 16 * 16;
+    return qpart + (size_t)kAnyP * any_quant_row(kf) + (size_t)kAnyP * kAnyDS * 4;
+}
+
+template <int KF>
+__global__ __launch_bounds__(kAnyT) void attn_scores_any_kernel(const float *__restrict__ q,
+                                                                const uint8_t *__restrict__ k_cache,
+                                                                const int32_t *__restrict__ d_pos, int n_past_arg,
+                                                                int n_heads, int n_kv_heads, int head_dim, float scale,
+                                                                int capacity, int wlimit, float *__restrict__ scores,
+                                                                int q_stride)
+{
+    extern __shared__ __align__(16) uint8_t lds_any[];
+    q += (size_t)blockIdx.z * q_stride;
+    scores += (size_t)blockIdx.z * n_heads * capacity;
+    n_past_arg += (int)blockIdx.z;
+    int window, start;
+    attn_window(d_pos, n_past_arg, wlimit, window, start);
+    const int p0 = blockIdx.x * kAnyP;
+    if (p0 >= window) return;
+    const int kvh = blockIdx.y, G = n_heads / n_kv_heads, HD = head_dim, nb = HD / 32, tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    constexpr int BB = KF == 0 ? 64 : (KF == 1 ? 34 : 18);  // cache bytes per 32 values
+    constexpr int QB = KF == 2 ? 16 : 32;                   // quant bytes per block in LDS
+    constexpr int KQR = any_quant_row(KF);
+    const size_t row_bytes = (size_t)n_kv_heads * nb * BB;
+    const uint8_t *khead = k_cache + (size_t)kvh * nb * BB;
+    const float *qg = q + (size_t)kvh * G * HD;
+    // q of the group: f32 (f16 K) or its Q8_0 blocks (quants, scales, quant sums)
+    float *q_s = reinterpret_cast<float *>(lds_any);
+    int8_t *qq = reinterpret_cast<int8_t *>(lds_any);
+    float *qd = reinterpret_cast<float *>(lds_any + (size_t)G * HD);
+    int *qsm = reinterpret_cast<int *>(lds_any + (size_t)G * HD + (size_t)G * nb * 4);
+    const size_t qpart = KF == 0 ? (size_t)G * HD * 4 : ((size_t)G * HD + (size_t)G * nb * 8 + 15) / 16 * 16;
+    uint8_t *kt = lds_any + qpart;                                     // f16 tile, or the quants
+    float *kd = reinterpret_cast<float *>(kt + (size_t)kAnyP * KQR);   // quantised: [64][kAnyDS] scales
+    if constexpr (KF == 0) {
+        for (int i = tid; i < G * HD; i += kAnyT) q_s[i] = qg[i];
+    } else {
+        for (int base = 0; base < G * HD; base += kAnyT) {  // uniform: all lanes run the block quantiser
+            const int i = base + tid;
+            const float v = i < G * HD ? qg[i] : 0.0f;
+            uint32_t dbits;
+            int qsum;
+            const int qv = q8_0_block32(v, dbits, qsum);
+            if (i < G * HD) {
+                qq[i] = (int8_t)qv;
+                if ((i & 31) == 0) {
+                    qd[i >> 5] = f16_bits_to_f32(dbits);
+                    qsm[i >> 5] = qsum;
+                }
+            }
+        }
+    }
+    float acc[kAnyHPT];
+#pragma unroll
+    for (int j = 0; j < kAnyHPT; ++j) acc[j] = KF == 0 ? -0.0f : 0.0f;
+    for (int c0 = 0; c0 < HD; c0 += kAnyCh) {
+        const int cn = HD - c0 < kAnyCh ? HD - c0 : kAnyCh, cb = cn / 32;
+        __syncthreads();  // the previous pass's reads are done (and q is staged)
+        if constexpr (KF == 0) {
+            const int cpr = cn / 8;  // 16-byte chunks per row
+            for (int c = tid; c < kAnyP * cpr; c += kAnyT) {
+                const int r = c / cpr, o = c - r * cpr;
+                const int pr = p0 + r < window ? p0 + r : window - 1;
+                const uint8_t *src = khead + cache_row_of(start + pr, capacity) * row_bytes + (size_t)c0 * 2;
+                *reinterpret_cast<u32x4 *>(kt + r * kAnyKRow + o * 16) = reinterpret_cast<const u32x4 *>(src)[o];
+            }
+        } else {
+            const int hpr = cb * BB / 2;  // halfwords per row
+            for (int c = tid; c < kAnyP * hpr; c += kAnyT) {
+                const int r = c / hpr, o = 2 * (c - r * hpr);
+                const int pr = p0 + r < window ? p0 + r : window - 1;
+                const uint8_t *src = khead + cache_row_of(start + pr, capacity) * row_bytes + (size_t)(c0 / 32) * BB;
+                const uint16_t hv = *reinterpret_cast<const uint16_t *>(src + o);
+                const int b = o / BB, rb = o - b * BB;
+                if (rb == 0)
+                    kd[r * kAnyDS + b] = f16_bits_to_f32(hv);
+                else
+                    *reinterpret_cast<uint16_t *>(kt + r * KQR + b * QB + rb - 2) = hv;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < kAnyHPT; ++j) {
+            const int g = wave + 4 * j;
+            if (g < G) {  // uniform per wave
+                if constexpr (KF == 0) {
+                    const float4 *qh = reinterpret_cast<const float4 *>(q_s + (size_t)g * HD + c0);
+                    const u32x4 *krow = reinterpret_cast<const u32x4 *>(kt + lane * kAnyKRow);
+                    float dot = acc[j];
+                    for (int d8 = 0; d8 < cn / 8; ++d8) {
+                        const u32x4 kw = krow[d8];
+                        const float4 qa = qh[2 * d8], qb = qh[2 * d8 + 1];
+                        const uint32_t w[4] = {kw.x, kw.y, kw.z, kw.w};
+                        const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const float prod = qv[e] * f16_bits_to_f32((w[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+                            dot = dot + prod;
+                        }
+                    }
+                    acc[j] = dot;
+                } else {
+                    float sacc = acc[j];
+                    for (int b = 0; b < cb; ++b) {
+                        const int gb = g * nb + c0 / 32 + b;  // the query's block
+                        const uint32_t *kw = reinterpret_cast<const uint32_t *>(kt + lane * KQR + b * QB);
+                        const uint32_t *qw = reinterpret_cast<const uint32_t *>(qq + (size_t)gb * 32);
+                        int isum = 0;
+                        if constexpr (KF == 1) {
+#pragma unroll
+                            for (int w = 0; w < 8; ++w) isum = sdot4(kw[w], qw[w], isum);
+                        } else {
+                            // (n - 8) . a = n . a - 8 * sum(a): low nibbles pair with a[0..15], high with a[16..31]
+#pragma unroll
+                            for (int w = 0; w < 4; ++w) {
+                                isum = sdot4(kw[w] & 0x0F0F0F0Fu, qw[w], isum);
+                                isum = sdot4((kw[w] >> 4) & 0x0F0F0F0Fu, qw[w + 4], isum);
+                            }
+                            isum -= 8 * qsm[gb];
+                        }
+                        const float term = (float)isum * (kd[lane * kAnyDS + b] * qd[gb]);
+                        sacc = sacc + term;
+                    }
+                    acc[j] = sacc;
+                }
+            }
+        }
+    }
+    if (p0 + lane < window) {
+#pragma unroll
+        for (int j = 0; j < kAnyHPT; ++j) {
+            const int g = wave + 4 * j;
+            if (g < G) scores[(size_t)(kvh * G + g) * capacity + p0 + lane] = acc[j] * scale;
+        }
+    }
+}
 
 // rope_1d_batched (ops.rs:185-208) over n_heads contiguous heads of one
 // vector in place: head blockIdx.x, pair i = threadIdx.x (head_dim / 2
@@ -588,15 +807,21 @@ constexpr int kSVS = kSVT + 12;  // product row stride (floats), 27 16-byte segm
 
 
 // Producer thread pt (0..383) of tile t: positions 2*(pt >> 3) .. +1 of the
-// tile, dims 4*(pt & 7) .. +3 of the slice (8 bytes of each V row); rows
-// past the window reload the last row (their products are zeroed).  ring0 =
-// cache row of the tile's first position (the window's rows are consecutive
-// modulo capacity).
+// tile, dims 4*(pt & 7) .. +3 of the slice; rows past the window reload the
+// last row (their products are zeroed).  ring0 = cache row of the tile's
+// first position (the window's rows are consecutive modulo capacity).  The
+// slice's 32 dims are one block of a quantised cache row, so per position:
+//   VF 0 (f16):  r = the four halves (8 bytes);
+//   VF 1 (Q8_0): r.x = quants 4dq..4dq+3, r.y = the block's f16 scale;
+//   VF 2 (Q4_0): r.x = bytes 4(dq&3)..+3 (dims 4dq.. are their low nibbles
+//                for dq < 4, high nibbles after), r.y = the f16 scale.
+// Quantised blocks are 2-byte aligned (34 and 18 bytes), read as halfwords.
 constexpr int kSVPT = 64 * (kSVW - 2);  // producer threads
 constexpr int kSVR = 2;                 // positions per producer thread
 static_assert(kSVT / kSVR * (kSVD / 4) == kSVPT, "one position pair x dim quad per producer thread");
-__device__ __forceinline__ void sv_tile_load(u32x2 (&r)[kSVR], const uint16_t *vslice, int t, int window, int ring0,
-                                             int capacity, size_t kv_dim, int pt)
+template <int VF>
+__device__ __forceinline__ void sv_tile_load(u32x2 (&r)[kSVR], const uint8_t *vslice, int t, int window, int ring0,
+                                             int capacity, size_t row_bytes, int pt)
 {
     const int tq = pt >> 3, dq = pt & 7;
 #pragma unroll
@@ -605,7 +830,15 @@ __device__ __forceinline__ void sv_tile_load(u32x2 (&r)[kSVR], const uint16_t *v
         rr = t * kSVT + rr < window ? rr : window - 1 - t * kSVT;
         int row = ring0 + rr;
         row = row >= capacity ? row - capacity : row;
-        r[i] = reinterpret_cast<const u32x2 *>(vslice + (size_t)row * kv_dim)[dq];
+        const uint8_t *blk = vslice + (size_t)row * row_bytes;
+        if constexpr (VF == 0) {
+            r[i] = reinterpret_cast<const u32x2 *>(blk)[dq];
+        } else {
+            const uint16_t *h = reinterpret_cast<const uint16_t *>(blk);
+            const int w = 1 + 2 * (VF == 1 ? dq : (dq & 3));  // halfword of byte 2 + 4*(dq or dq & 3)
+            r[i].x = (uint32_t)h[w] | ((uint32_t)h[w + 1] << 16);
+            r[i].y = h[0];
+        }
     }
 }
 
@@ -621,7 +854,7 @@ struct SvWeights {
     const uint64_t *exp_tab;
 };
 
-template <bool LONG>
+template <bool LONG, int VF>
 __device__ __forceinline__ void sv_products(const u32x2 (&r)[kSVR], const float *e_s, const SvWeights &sw,
                                             float (*prod)[kSVS], int t, int window, int pt)
 {
@@ -643,11 +876,24 @@ __device__ __forceinline__ void sv_products(const u32x2 (&r)[kSVR], const float 
 #pragma unroll
     for (int i = 0; i < kSVR; ++i) {
         const bool live = pos0 + i < window;
-        const uint32_t lo = r[i].x, hi = r[i].y;
-        const float v[4] = {f16_bits_to_f32(lo & 0xffffu), f16_bits_to_f32(lo >> 16), f16_bits_to_f32(hi & 0xffffu),
-                            f16_bits_to_f32(hi >> 16)};
+        if constexpr (VF == 0) {
+            const uint32_t lo = r[i].x, hi = r[i].y;
+            const float v[4] = {f16_bits_to_f32(lo & 0xffffu), f16_bits_to_f32(lo >> 16),
+                                f16_bits_to_f32(hi & 0xffffu), f16_bits_to_f32(hi >> 16)};
 #pragma unroll
-        for (int d = 0; d < 4; ++d) pv[d][i] = live ? w4[i] * v[d] : 0.0f;
+            for (int d = 0; d < 4; ++d) pv[d][i] = live ? w4[i] * v[d] : 0.0f;
+        } else {
+            // KvCacheRow::add_head_scaled (kv_cache.rs:97-125): dd = d * p,
+            // then dd * q per value, each product rounded
+            const float dd = f16_bits_to_f32(r[i].y) * w4[i];
+            const int sh = (VF == 2 && dq >= 4) ? 4 : 0;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const uint32_t b = (r[i].x >> (8 * d)) & 0xffu;
+                const int qv = VF == 1 ? (int)(int8_t)b : (int)((b >> sh) & 15u) - 8;
+                pv[d][i] = live ? dd * (float)qv : 0.0f;
+            }
+        }
     }
 #pragma unroll
     for (int d = 0; d < 4; ++d)
@@ -671,14 +917,17 @@ inline size_t sv_lds(int capacity)
     return sv_long(capacity) ? (size_t)kSVChunk * 5 + sizeof(mrml_xsum::Shared) : (size_t)capacity * sizeof(float) + 16;
 }
 
-template <bool LONG>
+// VF: the V cache's format (0 f16, 1 Q8_0, 2 Q4_0; KvCacheFormat::cuda_code);
+// grid (n_heads, head_dim / 32, rows).
+template <bool LONG, int VF>
 __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *__restrict__ scores,
-                                                             const uint16_t *__restrict__ v_cache,
+                                                             const uint8_t *__restrict__ v_cache,
                                                              const int32_t *__restrict__ d_pos, int n_past_arg,
-                                                             int n_heads, int n_kv_heads, int capacity, int wlimit, int expf_fused,
-                                                             float *__restrict__ out, uint8_t *__restrict__ pack)
+                                                             int n_heads, int n_kv_heads, int head_dim, int capacity,
+                                                             int wlimit, int expf_fused, float *__restrict__ out,
+                                                             uint8_t *__restrict__ pack)
 {
-    constexpr int HD = kAttnHD;
+    const int HD = head_dim;
     extern __shared__ __align__(16) float e_s[];
     __shared__ float red[kSVW];
     __shared__ __align__(16) float prod[2][kSVD][kSVS];
@@ -693,8 +942,10 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
     const int h = blockIdx.x, ds = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int G = n_heads / n_kv_heads, kvh = h / G;
     const float *sc = scores + (size_t)h * capacity;
-    const size_t kv_dim = (size_t)n_kv_heads * HD;
-    const uint16_t *vslice = v_cache + (size_t)kvh * HD + ds * kSVD;
+    // bytes of one cached 32-value block, of a cache row, and the slice's offset
+    constexpr size_t kBB = VF == 0 ? 64 : (VF == 1 ? 34 : 18);
+    const size_t kv_dim = (size_t)n_kv_heads * (HD / kSVD) * kBB;
+    const uint8_t *vslice = v_cache + ((size_t)kvh * (HD / kSVD) + ds) * kBB;
     const int ntiles = (window + kSVT - 1) / kSVT;
     const bool producer = (wave & 3) != 0;
     const int pt = (wave < 4 ? wave - 1 : wave - 2) * 64 + lane;
@@ -710,7 +961,7 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
     if (producer) {
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-            if (k < ntiles) sv_tile_load(vt[k], vslice, k, window, ring[k], capacity, kv_dim, pt);
+            if (k < ntiles) sv_tile_load<VF>(vt[k], vslice, k, window, ring[k], capacity, kv_dim, pt);
     }
 
     if (tid < 32) exp_tab[tid] = mrml_libm::kExpfT.t[tid];  // read before the max's barrier
@@ -813,10 +1064,10 @@ __global__ __launch_bounds__(64 * kSVW) void attn_softmax_v_kernel(const float *
     // buffer (t+1)&1 was last read by wave 0 in tile t-1, before barrier t
     auto tile = [&](int t, int k) {  // k = t % 4, a compile-time slot
         if (producer) {
-            sv_products<LONG>(vt[k], e_s, sw, prod[t & 1], t, window, pt);
+            sv_products<LONG, VF>(vt[k], e_s, sw, prod[t & 1], t, window, pt);
             if (t + 4 < ntiles) {
                 ring[k] = ring_next(ring_next(ring_next(ring_next(ring[k]))));
-                sv_tile_load(vt[k], vslice, t + 4, window, ring[k], capacity, kv_dim, pt);
+                sv_tile_load<VF>(vt[k], vslice, t + 4, window, ring[k], capacity, kv_dim, pt);
             }
         }
         __syncthreads();
@@ -1383,25 +1634,33 @@ int attn_window_limit(int capacity, int sliding_window)
 {
     return sliding_window > 0 && sliding_window < capacity ? sliding_window : capacity;
 }
-int attn_max_capacity() { return 131072; }  // 2^17 positions, the Gemma family's longest context
+// 2^20 positions: past the reference's default max_context of 256000
+// (model.rs:64-73); the scores take n_heads * capacity floats.
+int attn_max_capacity() { return 1 << 20; }
 
 size_t attn_scratch_bytes(int n_heads, int capacity) { return (size_t)n_heads * capacity * sizeof(float); }
 
 // Softmax and weighted values of `rows` query rows (grid z), the LDS or the
-// LONG form by capacity.
-static int launch_softmax_v(mrml_hip_ctx *ctx, const float *scores, const uint16_t *v_cache, float *out, void *pack,
+// LONG form by capacity, V rows in format v_fmt.
+static int launch_softmax_v(mrml_hip_ctx *ctx, const float *scores, const void *v_cache, float *out, void *pack,
                             const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads, int capacity, int wlimit,
-                            int rows = 1)
+                            int rows = 1, int head_dim = kAttnHD, int v_fmt = 0)
 {
-    const dim3 grid(n_heads, kAttnHD / kSVD, rows), block(64 * kSVW);
-    if (sv_long(capacity))
-        hipLaunchKernelGGL(attn_softmax_v_kernel<true>, grid, block, sv_lds(capacity), ctx->stream, scores, v_cache,
-                           d_pos, n_past, n_heads, n_kv_heads, capacity, wlimit, (int)host_expf_fused(), out,
-                           (uint8_t *)pack);
-    else
-        hipLaunchKernelGGL(attn_softmax_v_kernel<false>, grid, block, sv_lds(capacity), ctx->stream, scores, v_cache,
-                           d_pos, n_past, n_heads, n_kv_heads, capacity, wlimit, (int)host_expf_fused(), out,
-                           (uint8_t *)pack);
+    const dim3 grid(n_heads, head_dim / kSVD, rows), block(64 * kSVW);
+    const uint8_t *v = reinterpret_cast<const uint8_t *>(v_cache);
+    const int fe = (int)host_expf_fused();
+#define SV_LAUNCH(LONG, VF)                                                                                          \
+    hipLaunchKernelGGL((attn_softmax_v_kernel<LONG, VF>), grid, block, sv_lds(capacity), ctx->stream, scores, v,   \
+                       d_pos, n_past, n_heads, n_kv_heads, head_dim, capacity, wlimit, fe, out, (uint8_t *)pack)
+    const bool lg = sv_long(capacity);
+    if (v_fmt == 1) {
+        if (lg) SV_LAUNCH(true, 1); else SV_LAUNCH(false, 1);
+    } else if (v_fmt == 2) {
+        if (lg) SV_LAUNCH(true, 2); else SV_LAUNCH(false, 2);
+    } else {
+        if (lg) SV_LAUNCH(true, 0); else SV_LAUNCH(false, 0);
+    }
+#undef SV_LAUNCH
     return check_launch(ctx, "attn_softmax_v_kernel");
 }
 
@@ -1483,6 +1742,75 @@ int launch_attn_decode_rope_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k
                        rope_args(table, n_table, base, freq_scale, freqs), scores, 0);
     if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
     return launch_softmax_v(ctx, scores, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, capacity, wlimit);
+}
+
+bool attn_any_ok(int n_heads, int n_kv_heads, int head_dim)
+{
+    return n_kv_heads > 0 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= kAnyMaxG && head_dim >= 32 &&
+           head_dim <= kAnyMaxHD && head_dim % 32 == 0;
+}
+
+// The Gemma-2 shape the tuned kernels serve: head_dim 256, f16 rows, groups up to 8.
+bool attn_tuned(int n_heads, int n_kv_heads, int head_dim, int k_fmt, int v_fmt)
+{
+    return head_dim == kAttnHD && k_fmt == 0 && v_fmt == 0 && n_kv_heads > 0 && n_heads / n_kv_heads <= 8;
+}
+
+int launch_attn_any(mrml_hip_ctx *ctx, const float *q, int q_stride, const void *k_cache, const void *v_cache,
+                    float *out, void *pack, const int32_t *d_pos, int n_past0, int rows, int n_heads, int n_kv_heads,
+                    int head_dim, int k_fmt, int v_fmt, float scale, int capacity, void *scratch, int sliding_window)
+{
+    float *scores = reinterpret_cast<float *>(scratch);
+    const int wlimit = attn_window_limit(capacity, sliding_window);
+    // score tiles up to the widest row window (every tile when the position is on the device)
+    const int span = d_pos ? wlimit : std::min(wlimit, n_past0 + rows);
+    const dim3 sgrid((span + kAnyP - 1) / kAnyP, n_kv_heads, rows);
+    const size_t lds = attn_any_scores_lds(k_fmt, n_heads / n_kv_heads, head_dim);
+    const uint8_t *kc = reinterpret_cast<const uint8_t *>(k_cache);
+#define SC_LAUNCH(KF)                                                                                             \
+    hipLaunchKernelGGL(attn_scores_any_kernel<KF>, sgrid, dim3(kAnyT), lds, ctx->stream, q, kc, d_pos, n_past0,  \
+                       n_heads, n_kv_heads, head_dim, scale, capacity, wlimit, scores, q_stride)
+    if (k_fmt == 1)
+        SC_LAUNCH(1);
+    else if (k_fmt == 2)
+        SC_LAUNCH(2);
+    else
+        SC_LAUNCH(0);
+#undef SC_LAUNCH
+    if (int rc = check_launch(ctx, "attn_scores_any_kernel")) return rc;
+    return launch_softmax_v(ctx, scores, v_cache, out, pack, d_pos, n_past0, n_heads, n_kv_heads, capacity, wlimit,
+                            rows, head_dim, v_fmt);
+}
+
+int launch_rope_kv_any(mrml_hip_ctx *ctx, float *qkv, void *k_cache, void *v_cache, int pos, int n_heads,
+                       int n_kv_heads, int head_dim, float base, float freq_scale, int capacity, const float *table,
+                       int n_table, int rows, int cache_shift, int k_fmt, int v_fmt, const float *freqs)
+{
+    if (k_fmt == 0 && v_fmt == 0)
+        return launch_rope_kv_f16(ctx, qkv, (uint16_t *)k_cache, (uint16_t *)v_cache, nullptr, pos, n_heads,
+                                  n_kv_heads, head_dim, base, freq_scale, capacity, table, n_table, rows, cache_shift,
+                                  freqs);
+    // rotation only, then every K/V head stored in its cache's format
+    if (int rc = launch_rope_kv_f16(ctx, qkv, nullptr, nullptr, nullptr, pos, n_heads, n_kv_heads, head_dim, base,
+                                    freq_scale, capacity, table, n_table, rows, cache_shift, freqs))
+        return rc;
+    const dim3 grid(2 * n_kv_heads, rows);
+    uint8_t *kc = reinterpret_cast<uint8_t *>(k_cache), *vc = reinterpret_cast<uint8_t *>(v_cache);
+#define KV_LAUNCH(KF, VF)                                                                                    \
+    hipLaunchKernelGGL((kv_append_any_kernel<KF, VF>), grid, dim3(64), 0, ctx->stream, qkv, kc, vc, pos,    \
+                       n_heads, n_kv_heads, head_dim, capacity, cache_shift)
+    switch (k_fmt * 3 + v_fmt) {
+    case 1: KV_LAUNCH(0, 1); break;
+    case 2: KV_LAUNCH(0, 2); break;
+    case 3: KV_LAUNCH(1, 0); break;
+    case 4: KV_LAUNCH(1, 1); break;
+    case 5: KV_LAUNCH(1, 2); break;
+    case 6: KV_LAUNCH(2, 0); break;
+    case 7: KV_LAUNCH(2, 1); break;
+    default: KV_LAUNCH(2, 2); break;
+    }
+#undef KV_LAUNCH
+    return check_launch(ctx, "kv_append_any_kernel");
 }
 
 int attn_split_tiles(int capacity) { return (capacity + kSplitP - 1) / kSplitP; }

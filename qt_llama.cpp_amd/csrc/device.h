@@ -142,6 +142,29 @@ __device__ __forceinline__ int q8_0_block32(float v, uint32_t &dbits, int &qsum)
     return q;
 }
 
+// One Q4_0 block (quant.rs:372-389) held by 32 consecutive lanes, lane l
+// owning value l:
+//   amax    = max |x| (f32::max from 0: NaN never wins -- exact in any order)
+//   scale   = amax > 0 ? amax / 8 : 0;  d = f32_to_f16 by truncation
+//   inverse = scale > 0 ? 1 / scale : 0
+//   q       = clamp(round(x * inverse) as i32, -8, 7) + 8 (round half away
+//             from zero; the cast saturates, NaN -> 0)
+// Returns q (0..15); dbits is the f16 scale (uniform across the 32 lanes).
+// Must be called by all 64 lanes of the wave.
+__device__ __forceinline__ int q4_0_block32(float v, uint32_t &dbits)
+{
+    float m = fabsf(v);
+    m = (m > 0.0f) ? m : 0.0f;  // NaN -> 0
+    m = max32(m);
+    const float scale = m > 0.0f ? m / 8.0f : 0.0f;
+    dbits = f32_to_f16_trunc(scale);
+    const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    float r = roundf(v * inv);
+    r = (r < -8.0f) ? -8.0f : r;  // +-inf saturate to the clamp's ends
+    r = (r > 7.0f) ? 7.0f : r;
+    return ((r != r) ? 0 : (int)r) + 8;
+}
+
 // Reductions over each aligned group of 8 lanes (quad_perm xor 1, xor 2, then
 // row_half_mirror, which maps each quad onto the other quad of its 8 lanes;
 // after the quad steps every lane of a quad holds the same value).

@@ -139,7 +139,7 @@ template <bool RELAXED>
 __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const uint8_t *__restrict__ w,
                                                                          const uint8_t *__restrict__ gp,
                                                                          float *__restrict__ y, int rows, int nb,
-                                                                         int batch, int ngroups, int ldy)
+                                                                         int batch, int ngroups, int ldy, int vec)
 {
     __shared__ __align__(16) u32x4 sa[kNBuf][kKC][2][32];  // A chunks: [block][K half][row] 16 signed bytes
     __shared__ __align__(16) float sdw[kNBuf][kKC][32];  // their row scales, f32
@@ -265,10 +265,23 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
     const int tok = g * 32 + tl;
     if (tok < batch) {
         float *yr = y + (size_t)tok * ldy + r0 + 4 * h;  // row stride ldy (rows when packed)
+        if (r0 + 32 <= rows && vec) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            *reinterpret_cast<float4 *>(yr + 8 * j) = make_float4(acc[4 * j], acc[4 * j + 1], acc[4 * j + 2],
-                                                                  acc[4 * j + 3]);
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<float4 *>(yr + 8 * j) = make_float4(acc[4 * j], acc[4 * j + 1], acc[4 * j + 2],
+                                                                      acc[4 * j + 3]);
+        } else {
+            // the last tile of a row count that is not a multiple of 32, or
+            // an output that float4 stores cannot reach (a stride that is
+            // not a multiple of 4, or y not 16-byte aligned): one float each
+            // for the rows that exist (rows past them are computed on
+            // whatever their loads read, and never stored)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (r0 + 4 * h + 8 * j + i < rows) yr[8 * j + i] = acc[4 * j + i];
+        }
     }
 }
 
@@ -311,7 +324,7 @@ int gemm_noalloc_scratch(mrml_hip_ctx *ctx, void **out)
 
 bool gemm_shape_ok(int32_t rows, int32_t cols, int32_t batch)
 {
-    if (rows <= 0 || rows % 32 != 0 || cols <= 0 || cols % 32 != 0 || batch <= 0) return false;
+    if (rows <= 0 || cols <= 0 || cols % 32 != 0 || batch <= 0) return false;
     // 32-bit buffer offsets: the whole of W and of the GEMM pack
     const int64_t nb = cols / 32;
     return (int64_t)rows * nb * 18 < INT32_MAX && ((int64_t)batch + 31) / 32 * nb * 1152 < INT32_MAX &&
@@ -341,16 +354,17 @@ int launch_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const void *gpack, float 
 {
     const int nb = cols / 32, ng = gemm_groups(batch);
     if (ldy == 0) ldy = rows;
-    if (ldy < rows || ldy % 4 != 0 || ((uintptr_t)y & 15) != 0)
-        return fail(ctx, MRML_HIP_E_INVALID, "gemm_q4_0: output stride %d (rows %d) must be a multiple of 4 and y 16-byte aligned",
+    if (ldy < rows || ((uintptr_t)y & 3) != 0)
+        return fail(ctx, MRML_HIP_E_INVALID, "gemm_q4_0: output stride %d below rows %d, or y not 4-byte aligned",
                     ldy, rows);
-    const dim3 grid(rows / 32, (ng + kGemmWaves - 1) / kGemmWaves);
+    const int vec = (ldy % 4 == 0 && ((uintptr_t)y & 15) == 0) ? 1 : 0;  // float4 stores reach every output row
+    const dim3 grid((rows + 31) / 32, (ng + kGemmWaves - 1) / kGemmWaves);
     if (relaxed)
         hipLaunchKernelGGL(gemm_q4_0_mfma_kernel<true>, grid, dim3(64 * kGemmWaves), 0, ctx->stream, (const uint8_t *)w,
-                           (const uint8_t *)gpack, y, rows, nb, batch, ng, ldy);
+                           (const uint8_t *)gpack, y, rows, nb, batch, ng, ldy, vec);
     else
         hipLaunchKernelGGL(gemm_q4_0_mfma_kernel<false>, grid, dim3(64 * kGemmWaves), 0, ctx->stream,
-                           (const uint8_t *)w, (const uint8_t *)gpack, y, rows, nb, batch, ng, ldy);
+                           (const uint8_t *)w, (const uint8_t *)gpack, y, rows, nb, batch, ng, ldy, vec);
     return check_launch(ctx, "gemm_q4_0_mfma_kernel");
 }
 

@@ -176,6 +176,8 @@ int attn_max_capacity();
 // (sliding_window <= 0: none).
 int attn_window_limit(int capacity, int sliding_window);
 size_t attn_scratch_bytes(int n_heads, int capacity);
+// Streaming read of `bytes` (16-byte aligned) into nothing (sink: 1 KiB, rarely written).
+int launch_read(mrml_hip_ctx *ctx, const void *src, size_t bytes, void *sink);
 int launch_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache, const uint16_t *v_cache,
                            float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
                            float scale, int capacity, void *scratch, int sliding_window = -1);
@@ -186,6 +188,23 @@ bool attn_rope_ok(int n_heads, int n_kv_heads);
 int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *q, int q_stride, const uint16_t *k_cache,
                          const uint16_t *v_cache, float *out, int n_past0, int rows, int n_heads, int n_kv_heads,
                          float scale, int capacity, void *scratch, int sliding_window = -1);
+// Attention over caches of any head size (a multiple of 32 up to 512),
+// groups of up to 16 and the KV formats 0 (f16), 1 (Q8_0), 2 (Q4_0):
+// `rows` queries at positions n_past0.. (or d_pos, rows = 1), the arithmetic
+// of the CPU loop over KvCacheRow::dot_head / add_head_scaled.  scratch of
+// rows * attn_scratch_bytes(n_heads, capacity).
+bool attn_any_ok(int n_heads, int n_kv_heads, int head_dim);
+bool attn_tuned(int n_heads, int n_kv_heads, int head_dim, int k_fmt, int v_fmt);
+int launch_attn_any(mrml_hip_ctx *ctx, const float *q, int q_stride, const void *k_cache, const void *v_cache,
+                    float *out, void *pack, const int32_t *d_pos, int n_past0, int rows, int n_heads, int n_kv_heads,
+                    int head_dim, int k_fmt, int v_fmt, float scale, int capacity, void *scratch,
+                    int sliding_window = -1);
+// RoPE of `rows` stacked q|k|v rows at positions pos.. and their K/V appended
+// to caches of formats k_fmt / v_fmt at cache rows (pos + i + cache_shift) %
+// capacity (f16 caches: launch_rope_kv_f16 alone).
+int launch_rope_kv_any(mrml_hip_ctx *ctx, float *qkv, void *k_cache, void *v_cache, int pos, int n_heads,
+                       int n_kv_heads, int head_dim, float base, float freq_scale, int capacity, const float *table,
+                       int n_table, int rows, int cache_shift, int k_fmt, int v_fmt, const float *freqs = nullptr);
 int launch_attn_decode_rope_f16(mrml_hip_ctx *ctx, const float *qkv, uint16_t *k_cache, uint16_t *v_cache,
                                 float *out, void *pack, const int32_t *d_pos, int n_past, int n_heads, int n_kv_heads,
                                 float scale, int capacity, const float *table, int n_table, float base,

@@ -184,10 +184,13 @@ int mrml_hip_rope_kv_append_f16_batch(mrml_hip_ctx *ctx, float *qkv, uint16_t *k
 {
     CTX_GUARD(ctx);
     REQUIRE(ctx, qkv && k_cache && v_cache, "rope_kv_append_f16_batch: null pointer");
-    REQUIRE(ctx, k_format == 0 && v_format == 0,
-            "rope_kv_append_f16_batch: k_format=%d v_format=%d (only f16 caches, format 0)", k_format, v_format);
+    if (k_format < 0 || k_format > 2 || v_format < 0 || v_format > 2)
+        return fail(ctx, MRML_HIP_E_UNSUPPORTED, "rope_kv_append_f16_batch: k_format=%d v_format=%d (0 f16, 1 Q8_0, "
+                    "2 Q4_0)", k_format, v_format);
     REQUIRE(ctx, n_heads > 0 && n_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && head_dim <= 1024,
             "rope_kv_append_f16_batch: n_heads=%d n_kv_heads=%d head_dim=%d", n_heads, n_kv_heads, head_dim);
+    REQUIRE(ctx, (k_format == 0 && v_format == 0) || head_dim % 32 == 0,
+            "rope_kv_append_f16_batch: quantised caches need head_dim %% 32 == 0 (head_dim=%d)", head_dim);
     // rows of one launch must not share a cache row
     REQUIRE(ctx, capacity > 0 && batch > 0 && batch <= capacity && batch <= 65535,
             "rope_kv_append_f16_batch: batch=%d capacity=%d (batch within 1..min(capacity, 65535))", batch,
@@ -196,9 +199,9 @@ int mrml_hip_rope_kv_append_f16_batch(mrml_hip_ctx *ctx, float *qkv, uint16_t *k
                      cache_start <= INT32_MAX - batch,
             "rope_kv_append_f16_batch: start_pos=%d cache_start=%d", start_pos, cache_start);
     REQUIRE(ctx, ((uintptr_t)d_table & 7) == 0 && n_table >= 0, "rope_kv_append_f16_batch: table");
-    return launch_rope_kv_f16(ctx, qkv, k_cache, v_cache, nullptr, start_pos, n_heads, n_kv_heads, head_dim,
-                              freq_base, freq_scale, capacity, d_table, d_table ? n_table : 0, batch,
-                              cache_start - start_pos);
+    return launch_rope_kv_any(ctx, qkv, k_cache, v_cache, start_pos, n_heads, n_kv_heads, head_dim, freq_base,
+                              freq_scale, capacity, d_table, d_table ? n_table : 0, batch, cache_start - start_pos,
+                              k_format, v_format);
 }
 
 // CudaDevice::rope_256k (cuda.rs:2248-2285): rope_1d_batched (ops.rs:185-208)
@@ -246,16 +249,23 @@ int mrml_hip_add(mrml_hip_ctx *ctx, const float *a, const float *b, float *out, 
     return n ? launch_add_rows(ctx, a, b, out, n) : MRML_HIP_OK;
 }
 
-// Arguments shared by the decode-attention entries.
+// Arguments shared by the decode-attention entries: head_dim a multiple of
+// 32 up to 512, groups of up to 16 query heads per kv head, cache formats
+// 0 (f16), 1 (Q8_0), 2 (Q4_0) (KvCacheFormat::cuda_code, kv_cache.rs:16-22).
 static int attn_args_ok(mrml_hip_ctx *ctx, const char *name, const float *q, const uint16_t *k_cache,
                         const uint16_t *v_cache, const float *out, const void *pack, int32_t n_past,
-                        const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t capacity)
+                        const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t capacity,
+                        int32_t k_format = 0, int32_t v_format = 0)
 {
     REQUIRE(ctx, q && k_cache && v_cache && (out || pack), "%s: null pointer or no output", name);
-    REQUIRE(ctx, head_dim == attn_head_dim(), "%s: head_dim=%d unsupported (kernel serves %d)", name, head_dim,
-            attn_head_dim());
-    REQUIRE(ctx, n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= 8,
-            "%s: n_heads=%d n_kv_heads=%d (group of at most 8)", name, n_heads, n_kv_heads);
+    if (k_format < 0 || k_format > 2 || v_format < 0 || v_format > 2)
+        return fail(ctx, MRML_HIP_E_UNSUPPORTED, "%s: k_format=%d v_format=%d (0 f16, 1 Q8_0, 2 Q4_0)", name,
+                    k_format, v_format);
+    REQUIRE(ctx, n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0,
+            "%s: n_heads=%d n_kv_heads=%d", name, n_heads, n_kv_heads);
+    REQUIRE(ctx, attn_any_ok(n_heads, n_kv_heads, head_dim),
+            "%s: head_dim=%d (a multiple of 32 up to 512), group %d (at most 16)", name, head_dim,
+            n_heads / n_kv_heads);
     REQUIRE(ctx, capacity > 0 && capacity <= attn_max_capacity() && (d_pos || n_past >= 0),
             "%s: n_past=%d capacity=%d (at most %d)", name, n_past, capacity, attn_max_capacity());
     REQUIRE(ctx, ((((uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)q | (uintptr_t)pack) & 15) == 0),
@@ -265,18 +275,28 @@ static int attn_args_ok(mrml_hip_ctx *ctx, const char *name, const float *q, con
 
 static int attn_exact(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache, const uint16_t *v_cache, float *out,
                       void *pack, int32_t n_past, const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads,
-                      float scale, int32_t capacity, int32_t sliding_window)
+                      int32_t head_dim, float scale, int32_t capacity, int32_t sliding_window, int32_t k_format = 0,
+                      int32_t v_format = 0)
 {
     void *part = workspace(ctx, attn_scratch_bytes(n_heads, capacity));
     if (!part) return MRML_HIP_E_ALLOC;
+    if (!attn_tuned(n_heads, n_kv_heads, head_dim, k_format, v_format))
+        return launch_attn_any(ctx, q, 0, k_cache, v_cache, out, pack, d_pos, n_past, 1, n_heads, n_kv_heads,
+                               head_dim, k_format, v_format, scale, capacity, part, sliding_window);
     return launch_attn_decode_f16(ctx, q, k_cache, v_cache, out, pack, d_pos, n_past, n_heads, n_kv_heads, scale,
                                   capacity, part, sliding_window);
 }
 
+// The split (flash-decoding) form serves the tuned shape; other head sizes,
+// groups and formats run the exact form, which meets any tolerance.
 static int attn_split(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache, const uint16_t *v_cache, float *out,
                       void *pack, int32_t n_past, const int32_t *d_pos, int32_t n_heads, int32_t n_kv_heads,
-                      float scale, int32_t capacity, int32_t sliding_window)
+                      int32_t head_dim, float scale, int32_t capacity, int32_t sliding_window, int32_t k_format = 0,
+                      int32_t v_format = 0)
 {
+    if (!attn_tuned(n_heads, n_kv_heads, head_dim, k_format, v_format))
+        return attn_exact(ctx, q, k_cache, v_cache, out, pack, n_past, d_pos, n_heads, n_kv_heads, head_dim, scale,
+                          capacity, sliding_window, k_format, v_format);
     void *part = workspace(ctx, attn_split_scratch_bytes(n_heads, capacity));
     if (!part) return MRML_HIP_E_ALLOC;
     return launch_attn_split_f16(ctx, q, const_cast<uint16_t *>(k_cache), const_cast<uint16_t *>(v_cache), out, pack,
@@ -292,7 +312,8 @@ int mrml_hip_attn_decode_f16(mrml_hip_ctx *ctx, const float *q, const uint16_t *
     if (int rc = attn_args_ok(ctx, "attn_decode_f16", q, k_cache, v_cache, out, pack, n_past, d_pos, n_heads,
                               n_kv_heads, head_dim, capacity))
         return rc;
-    return attn_exact(ctx, q, k_cache, v_cache, out, pack, n_past, d_pos, n_heads, n_kv_heads, scale, capacity, -1);
+    return attn_exact(ctx, q, k_cache, v_cache, out, pack, n_past, d_pos, n_heads, n_kv_heads, head_dim, scale,
+                      capacity, -1);
 }
 
 int mrml_hip_attn_decode_f16_split(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache,
@@ -304,32 +325,23 @@ int mrml_hip_attn_decode_f16_split(mrml_hip_ctx *ctx, const float *q, const uint
     if (int rc = attn_args_ok(ctx, "attn_decode_f16_split", q, k_cache, v_cache, out, pack, n_past, d_pos, n_heads,
                               n_kv_heads, head_dim, capacity))
         return rc;
-    return attn_split(ctx, q, k_cache, v_cache, out, pack, n_past, d_pos, n_heads, n_kv_heads, scale, capacity, -1);
+    return attn_split(ctx, q, k_cache, v_cache, out, pack, n_past, d_pos, n_heads, n_kv_heads, head_dim, scale,
+                      capacity, -1);
 }
 
-// CudaDevice::attention_causal with its own argument list (cuda.rs:2658-2697):
-// the cache formats must be 0 (f16 rows; KvCacheFormat::cuda_code,
-// kv_cache.rs:16-22).
-static int attn_formats_ok(mrml_hip_ctx *ctx, const char *name, int32_t k_format, int32_t v_format)
-{
-    if (k_format != 0 || v_format != 0)
-        return fail(ctx, MRML_HIP_E_UNSUPPORTED, "%s: k_format=%d v_format=%d (only f16 caches, format 0)", name,
-                    k_format, v_format);
-    return MRML_HIP_OK;
-}
-
+// CudaDevice::attention_causal with its own argument list (cuda.rs:2658-2697),
+// caches of any of the three formats.
 int mrml_hip_attention_causal(mrml_hip_ctx *ctx, const float *q, const uint16_t *k_cache, const uint16_t *v_cache,
                               float *out, int32_t n_past, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                               float scale, int32_t sliding_window, int32_t capacity, int32_t k_format,
                               int32_t v_format)
 {
     CTX_GUARD(ctx);
-    if (int rc = attn_formats_ok(ctx, "attention_causal", k_format, v_format)) return rc;
     if (int rc = attn_args_ok(ctx, "attention_causal", q, k_cache, v_cache, out, nullptr, n_past, nullptr, n_heads,
-                              n_kv_heads, head_dim, capacity))
+                              n_kv_heads, head_dim, capacity, k_format, v_format))
         return rc;
-    return attn_exact(ctx, q, k_cache, v_cache, out, nullptr, n_past, nullptr, n_heads, n_kv_heads, scale, capacity,
-                      sliding_window);
+    return attn_exact(ctx, q, k_cache, v_cache, out, nullptr, n_past, nullptr, n_heads, n_kv_heads, head_dim, scale,
+                      capacity, sliding_window, k_format, v_format);
 }
 
 // CudaDevice::attention_prefill (cuda.rs:2727-2770): `batch` queries at
@@ -343,9 +355,8 @@ int mrml_hip_attention_prefill(mrml_hip_ctx *ctx, const float *q, int32_t q_stri
                                int32_t sliding_window, int32_t capacity, int32_t k_format, int32_t v_format)
 {
     CTX_GUARD(ctx);
-    if (int rc = attn_formats_ok(ctx, "attention_prefill", k_format, v_format)) return rc;
     if (int rc = attn_args_ok(ctx, "attention_prefill", q, k_cache, v_cache, out, nullptr, cache_start, nullptr,
-                              n_heads, n_kv_heads, head_dim, capacity))
+                              n_heads, n_kv_heads, head_dim, capacity, k_format, v_format))
         return rc;
     REQUIRE(ctx, batch > 0 && cache_start <= INT32_MAX - batch, "attention_prefill: batch=%d cache_start=%d", batch,
             cache_start);
@@ -357,11 +368,18 @@ int mrml_hip_attention_prefill(mrml_hip_ctx *ctx, const float *q, int32_t q_stri
     const int rn = (int)std::max<size_t>(1, std::min<size_t>(std::min(batch, 65535), kPrefillScoreBytes / per));
     void *part = workspace(ctx, (size_t)rn * per);
     if (!part) return MRML_HIP_E_ALLOC;
-    for (int r0 = 0; r0 < batch; r0 += rn)
-        if (int rc = launch_attn_rows_f16(ctx, q + (size_t)r0 * q_stride, q_stride, k_cache, v_cache, out + r0 * qd,
-                                          cache_start + r0, std::min(rn, batch - r0), n_heads, n_kv_heads, scale,
-                                          capacity, part, sliding_window))
-            return rc;
+    const bool tuned = attn_tuned(n_heads, n_kv_heads, head_dim, k_format, v_format);
+    for (int r0 = 0; r0 < batch; r0 += rn) {
+        const int n = std::min(rn, batch - r0);
+        const int rc = tuned ? launch_attn_rows_f16(ctx, q + (size_t)r0 * q_stride, q_stride, k_cache, v_cache,
+                                                    out + r0 * qd, cache_start + r0, n, n_heads, n_kv_heads, scale,
+                                                    capacity, part, sliding_window)
+                             : launch_attn_any(ctx, q + (size_t)r0 * q_stride, q_stride, k_cache, v_cache,
+                                               out + r0 * qd, nullptr, nullptr, cache_start + r0, n, n_heads,
+                                               n_kv_heads, head_dim, k_format, v_format, scale, capacity, part,
+                                               sliding_window);
+        if (rc) return rc;
+    }
     return MRML_HIP_OK;
 }
 
@@ -371,12 +389,11 @@ int mrml_hip_attention_causal_split(mrml_hip_ctx *ctx, const float *q, const uin
                                     int32_t capacity, int32_t k_format, int32_t v_format)
 {
     CTX_GUARD(ctx);
-    if (int rc = attn_formats_ok(ctx, "attention_causal_split", k_format, v_format)) return rc;
     if (int rc = attn_args_ok(ctx, "attention_causal_split", q, k_cache, v_cache, out, nullptr, n_past, nullptr,
-                              n_heads, n_kv_heads, head_dim, capacity))
+                              n_heads, n_kv_heads, head_dim, capacity, k_format, v_format))
         return rc;
-    return attn_split(ctx, q, k_cache, v_cache, out, nullptr, n_past, nullptr, n_heads, n_kv_heads, scale, capacity,
-                      sliding_window);
+    return attn_split(ctx, q, k_cache, v_cache, out, nullptr, n_past, nullptr, n_heads, n_kv_heads, head_dim, scale,
+                      capacity, sliding_window, k_format, v_format);
 }
 
 // ---- the Gemma-2-shape model --------------------------------------------------------

@@ -374,6 +374,17 @@ int mrml_hip_copy_kernel(mrml_hip_ctx *ctx, void *d_dst, const void *d_src, size
     return launch_copy(ctx, d_dst, d_src, bytes);
 }
 
+int mrml_hip_read_kernel(mrml_hip_ctx *ctx, const void *d_src, size_t bytes, void *d_sink)
+{
+    CTX_GUARD(ctx);
+    if (!bytes) return MRML_HIP_OK;
+    REQUIRE(ctx, d_src && d_sink, "null pointer");
+    REQUIRE(ctx, bytes % 16 == 0 && ((uintptr_t)d_src % 16) == 0 && ((uintptr_t)d_sink % 4) == 0,
+            "read_kernel: bytes and source must be 16-byte aligned");
+    REQUIRE(ctx, bytes / 16 / (256 * 8) < (1u << 31), "read_kernel: %zu bytes is too many", bytes);
+    return launch_read(ctx, d_src, bytes, d_sink);
+}
+
 // ---- layout conversion ----------------------------------------------------
 
 int mrml_hip_repack_q4_0(mrml_hip_ctx *ctx, const void *src, void *dst, int32_t rows, int32_t cols)
@@ -568,7 +579,7 @@ int mrml_hip_gemv_q4_k(mrml_hip_ctx *ctx, const void *w, const float *x, float *
         REQUIRE(ctx, ((uintptr_t)(x) & 15) == 0 && ((uintptr_t)(y) & 15) == 0,                       \
                 "x / pack and y must be 16-byte aligned");                                           \
         REQUIRE(ctx, gemm_shape_ok(rows, cols, batch),                                               \
-                "gemm rows=%d cols=%d batch=%d: need rows %% 32 == 0, cols %% 32 == 0, batch > 0 "  \
+                "gemm rows=%d cols=%d batch=%d: need rows > 0, cols %% 32 == 0, batch > 0 "           \
                 "and W / activations below 2 GiB",                                                   \
                 (int)(rows), (int)(cols), (int)(batch));                                             \
         REQUIRE(ctx, (int64_t)(batch) * (cols) <= INT32_MAX && (int64_t)(batch) * (rows) <= INT32_MAX, \
@@ -632,8 +643,7 @@ int mrml_hip_gemm_q4_0_qkv(mrml_hip_ctx *ctx, const void *wq, const void *wk, co
     CTX_GUARD(ctx);
     REQUIRE(ctx, wk && wv, "gemm_q4_0_qkv: null pointer");
     CHECK_GEMM(ctx, wq, x, y, q_rows, cols, batch);
-    REQUIRE(ctx, gemm_shape_ok(kv_rows, cols, batch), "gemm_q4_0_qkv: kv_rows=%d must be a positive multiple of 32",
-            kv_rows);
+    REQUIRE(ctx, gemm_shape_ok(kv_rows, cols, batch), "gemm_q4_0_qkv: kv_rows=%d must be positive", kv_rows);
     const int32_t total = q_rows + 2 * kv_rows;
     REQUIRE(ctx, (int64_t)batch * total <= INT32_MAX, "gemm_q4_0_qkv: batch=%d too large", batch);
     void *gp = workspace(ctx, gemm_pack_bytes(cols, batch));

@@ -154,6 +154,7 @@ api! {
     memcpy_d2d_async: fn(Ctx, *mut c_void, *const c_void, usize) -> c_int = "mrml_hip_memcpy_d2d_async";
     zero_async: fn(Ctx, *mut c_void, usize) -> c_int = "mrml_hip_zero_async";
     copy_kernel: fn(Ctx, *mut c_void, *const c_void, usize) -> c_int = "mrml_hip_copy_kernel";
+    read_kernel: fn(Ctx, *const c_void, usize, *mut c_void) -> c_int = "mrml_hip_read_kernel";
     repack_q4_0: fn(Ctx, *const c_void, *mut c_void, i32, i32) -> c_int = "mrml_hip_repack_q4_0";
     repack_q8_0: fn(Ctx, *const c_void, *mut c_void, i32, i32) -> c_int = "mrml_hip_repack_q8_0";
     repack_q4_k: fn(Ctx, *const c_void, *mut c_void, i32, i32) -> c_int = "mrml_hip_repack_q4_k";

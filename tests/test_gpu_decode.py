@@ -318,11 +318,13 @@ def test_attention_causal_sliding_window(backend, dev, orc, synth, n_past, sw, c
     assert_bits(out.numpy(), ref_full, "attention_causal without a window")
 
 
-def test_attention_causal_rejects_quantised_caches(backend, dev):
+def test_attention_causal_rejects_unknown_cache_formats(backend, dev):
+    """KvCacheFormat::cuda_code has 0, 1 and 2 (kv_cache.rs:16-22); any other
+    code is refused as unsupported, on both entries."""
     qb = backend.HipBuffer.alloc(dev, 8 * 256)
     kb = backend.HipBuffer.alloc(dev, 64 * 1024, np.uint16)
     out = backend.HipBuffer.alloc(dev, 8 * 256)
-    for kf, vf in ((1, 0), (0, 2)):
+    for kf, vf in ((3, 0), (0, -1)):
         for split in (False, True):
             with pytest.raises(backend.HipError) as e:
                 dev.attention_causal_ref(qb, kb, kb, out, 3, 8, 4, 256, 1.0 / 16.0, None, 64, kf, vf, split=split)

@@ -131,9 +131,56 @@ def test_gemm_q4_0_rejects_bad_shapes(backend, dev):
     x = backend.HipBuffer.alloc(dev, 64 * 4)
     y = backend.HipBuffer.alloc(dev, 64 * 4)
     # the last case: the activations would pass 2 GiB (32-bit buffer offsets)
-    for rows, cols, batch in [(33, 32, 2), (32, 48, 2), (32, 32, 0), (32, 2304, 1 << 22)]:
+    for rows, cols, batch in [(0, 32, 2), (32, 48, 2), (32, 32, 0), (32, 2304, 1 << 22)]:
         with pytest.raises(backend.HipError):
             dev.gemm_q4_0(w, x, y, rows, cols, batch)
+
+
+# Row counts that are not multiples of 32 (the reference's grid is ceil(rows / 8),
+# cuda.rs:627-673): the last 32-row tile is partial, and outputs whose row
+# stride is not a multiple of 4 are stored one float at a time.
+@pytest.mark.parametrize("rows,cols,batch", [(1, 32, 1), (5, 64, 3), (33, 256, 40), (100, 2304, 37), (31, 96, 64),
+                                             (2305, 2304, 17), (7, 9216, 33)])
+def test_gemm_q4_0_any_rows_bit_exact(backend, dev, orc, synth, rows, cols, batch):
+    rng = synth.rng_for(5150 + rows + cols + batch)
+    w = synth.q4_0_matrix(rng, rows, cols)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    got = run_gemm(backend, dev, w, x, rows, cols, batch)
+    ref = oracle_gemm(orc, w, x, rows, cols, range(batch))
+    assert_bit_exact(got, ref, f"gemm {rows}x{cols} M={batch}")
+    # the pre-quantised entry and the relaxed fold take the same shapes
+    assert_bit_exact(run_gemm(backend, dev, w, x, rows, cols, batch, prequantised=True), ref, "pack entry")
+
+
+def test_gemm_q4_0_qkv_geglu_any_rows(backend, dev, orc, synth):
+    """The fused batched entries at row counts that are not multiples of 32
+    or of 4: the k and v products then start off a 16-byte boundary of the
+    stacked rows, stored one float at a time."""
+    q_rows, kv_rows, cols, batch = 42, 19, 256, 45
+    rng = synth.rng_for(5160)
+    ws = {k: synth.q4_0_matrix(rng, r, cols) for k, r in (("q", q_rows), ("k", kv_rows), ("v", kv_rows))}
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    bufs = [backend.HipBuffer.from_gguf(dev, ws[k], backend.Q4_0, r, cols)
+            for k, r in (("q", q_rows), ("k", kv_rows), ("v", kv_rows))]
+    xb = backend.HipBuffer.from_host(dev, x.reshape(-1))
+    total = q_rows + 2 * kv_rows
+    yb = backend.HipBuffer.alloc(dev, batch * total)
+    dev.gemm_q4_0_qkv(*bufs, xb, yb, q_rows, kv_rows, cols, batch)
+    dev.sync()
+    got = yb.numpy().reshape(batch, total)
+    for name, lo, r in (("q", 0, q_rows), ("k", q_rows, kv_rows), ("v", q_rows + kv_rows, kv_rows)):
+        assert_bit_exact(got[:, lo:lo + r], oracle_gemm(orc, ws[name], x, r, cols, range(batch)), f"qkv {name}")
+    rows = 77
+    wg, wu = synth.q4_0_matrix(rng, rows, cols), synth.q4_0_matrix(rng, rows, cols)
+    bg = backend.HipBuffer.from_gguf(dev, wg, backend.Q4_0, rows, cols)
+    bu = backend.HipBuffer.from_gguf(dev, wu, backend.Q4_0, rows, cols)
+    ab = backend.HipBuffer.alloc(dev, batch * rows)
+    dev.gemm_q4_0_geglu(bg, bu, xb, ab, rows, cols, batch)
+    dev.sync()
+    g = oracle_gemm(orc, wg, x, rows, cols, range(batch))
+    u = oracle_gemm(orc, wu, x, rows, cols, range(batch))
+    assert_bit_exact(ab.numpy().reshape(batch, rows), np.stack([orc.geglu(g[m], u[m]) for m in range(batch)]),
+                     "geglu")
 
 
 # ------------------------------------------------------------ fused batched entry points

@@ -6,7 +6,8 @@ each chunk's exact sequential sum started from the running sum, and forms
 the weights again from the global scores; the split-K combine walks more
 tiles than its LDS arrays hold.  Bar: bit-identical to the CPU oracle
 (model.rs:1457-1590, ops.rs:133-158) for the exact path at every window up
-to the largest capacity served (131072 positions); within 1e-5 relative to
+to 131072 positions (test_gpu_attention_any.py takes a 262144-position
+window; the ops take capacities up to 2^20); within 1e-5 relative to
 the output's largest magnitude for the split path.  The reference serves
 such windows with its streaming online-softmax kernel (kernels.rs:1463-1561,
 dispatch cuda.rs:1097-1126).
@@ -21,7 +22,8 @@ from test_gpu_decode import THREADS, TINY, assert_bits, check_pack, max_rel
 
 pytestmark = pytest.mark.gpu
 
-MAX_CAP = 131072
+MAX_CAP = 131072            # the longest window these tests run (2^17, Gemma-2's longest context)
+CAP_LIMIT = 1 << 20         # the largest capacity the attention entries take
 SPLIT_TOL = 1e-5
 
 
@@ -84,7 +86,7 @@ def test_attention_long_bit_exact(backend, orc, dev, n_past, cap):
 
 
 def test_attention_long_max_capacity_bit_exact(backend, orc, dev):
-    """The largest capacity served, full window (131072 positions): bit-exact."""
+    """A full window of 131072 positions: bit-exact."""
     n_past = MAX_CAP - 1
     print(f"\n[long attn] exact, n_past {n_past} capacity {MAX_CAP}", flush=True)
     got, pack, q, kr, vr = long_case(backend, dev, n_past, MAX_CAP, 5, split=False)
@@ -94,12 +96,14 @@ def test_attention_long_max_capacity_bit_exact(backend, orc, dev):
 
 
 def test_attention_long_capacity_limit(backend, dev):
+    """A capacity past the entries' limit is refused before any launch (the
+    caches here are far too small for any real call: nothing may run)."""
     qb = backend.HipBuffer.alloc(dev, 8 * 256)
     kb = backend.HipBuffer.alloc(dev, 64, np.uint16)
     out = backend.HipBuffer.alloc(dev, 8 * 256)
     for fn in (dev.attention_causal, dev.attention_causal_split):
         with pytest.raises(backend.HipError):
-            fn(qb, kb, kb, out, 0, 8, 4, 256, 1.0 / 16.0, MAX_CAP + 1)
+            fn(qb, kb, kb, out, 0, 8, 4, 256, 1.0 / 16.0, CAP_LIMIT + 1)
 
 
 # split-K: the combine's LDS arrays hold 192 tiles (6144 positions); longer

@@ -230,7 +230,7 @@ def test_qkv_postprocess_batch_invalid(backend, dev):
     nh, nkv, hd = 8, 4, 256
     qb = backend.HipBuffer.alloc(dev, 20 * (nh + 2 * nkv) * hd)
     kc = backend.HipBuffer.alloc(dev, 16 * nkv * hd, np.uint16)
-    bad = [dict(batch=17, cap=16), dict(batch=4, cap=16, k_format=1), dict(batch=4, cap=16, v_format=2),
+    bad = [dict(batch=17, cap=16), dict(batch=4, cap=16, k_format=3), dict(batch=4, cap=16, v_format=-1),
            dict(batch=0, cap=16), dict(batch=4, cap=16, start_pos=-1)]
     for b in bad:
         with pytest.raises(backend.HipError):
@@ -310,9 +310,9 @@ def test_attention_prefill_invalid(backend, dev):
     kb = backend.HipBuffer.alloc(dev, 64 * nkv * hd, np.uint16)
     out = backend.HipBuffer.alloc(dev, 4 * nh * hd)
     with pytest.raises(backend.HipError) as e:
-        dev.attention_prefill(qb, kb, kb, out, 0, 4, nh, nkv, hd, 0.0625, None, 64, 1, 0)
+        dev.attention_prefill(qb, kb, kb, out, 0, 4, nh, nkv, hd, 0.0625, None, 64, 3, 0)
     assert e.value.status == -4  # MRML_HIP_E_UNSUPPORTED
-    for kw in (dict(q_stride=nh * hd - 1), dict(batch=0), dict(head_dim=128)):
+    for kw in (dict(q_stride=nh * hd - 1), dict(batch=0), dict(head_dim=100)):
         with pytest.raises(backend.HipError):
             dev.attention_prefill(qb, kb, kb, out, 0, kw.get("batch", 4), nh, nkv, kw.get("head_dim", hd), 0.0625,
                                   None, 64, q_stride=kw.get("q_stride", nh * hd))
