@@ -58,7 +58,7 @@ PEAK_INT8_TOPS = 5000.0                                # dense int8 MFMA, MI355X
 MALL_BYTES = 256 << 20
 PREFILL_CHUNK = 512                                    # tokens per chunk of mrml_hip_gemma2_prefill (model.hip)
 # the dominant kernel of the step (the fused GeGLU that quantises x and emits the act pack)
-GEGLU_KERNEL = "gemv_q4_0_geglu_kernel<72, 8, true, true>"
+GEGLU_KERNEL = "gemv_q4_0_geglu_split_kernel<72, 9>"
 
 
 def load_backend():
@@ -734,8 +734,10 @@ def main() -> int:
     dev.reserve_workspace(1 << 20)
     dev.sync()
 
-    # one FFN step = mrml_hip_ffn_geglu_q4_0: two launches (GeGLU quantising x
-    # itself and emitting the activation pack, then the down projection)
+    # one FFN step = mrml_hip_ffn_geglu_q4_0: two launches (the GeGLU
+    # quantising x itself, 256 workgroups of 36 rows, writing the f32 output
+    # and the pack blocks it holds whole; then the down projection, which
+    # quantises the 32 tail blocks itself)
     def ffn_step(s):
         dev.ffn_geglu_q4_0(s["g"], s["u"], s["d"], bx, None, y, DIM, FFN)
 
@@ -759,7 +761,7 @@ def main() -> int:
     q_pack = be.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(DIM), np.uint8)
     dev.quantize_q8_0(bx, None, q_pack, DIM)
     a_pack = be.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(FFN), np.uint8)
-    g_geglu = dev.capture(lambda: [dev.gemv_q4_0_geglu_pack(pool[2 * i], pool[2 * i + 1], bx, None, a_pack, FFN, DIM)
+    g_geglu = dev.capture(lambda: [dev.ffn_split_geglu(pool[2 * i], pool[2 * i + 1], bx, act, a_pack, DIM, FFN)
                                    for i in range(len(pool) // 2)])
 
     if args.profile_loop:
@@ -801,13 +803,22 @@ def main() -> int:
     out_f = be.HipBuffer.alloc(dev, FFN)
     npool = len(pool)
     # the step's first launch (f32 x in, activation pack out), over gate/up pairs of the pool
-    st_geglu, gbs_geglu = rate(lambda i: dev.gemv_q4_0_geglu_pack(pool[2 * i], pool[2 * i + 1], bx, None, a_pack,
-                                                                  FFN, DIM), BYTES_GEGLU, npool // 2)
+    st_geglu, gbs_geglu = rate(lambda i: dev.ffn_split_geglu(pool[2 * i], pool[2 * i + 1], bx, act, a_pack, DIM,
+                                                             FFN), BYTES_GEGLU, npool // 2)
+    st_geglu_e, gbs_geglu_e = rate(lambda i: dev.gemv_q4_0_geglu_pack(pool[2 * i], pool[2 * i + 1], bx, None, a_pack,
+                                                                      FFN, DIM), BYTES_GEGLU, npool // 2)
     st_gate, gbs_gate = rate(lambda i: dev.gemv_q4_0_q8(pool[i], q_pack, out_f, FFN, DIM), BYTES_GATE, npool)
     st_up, gbs_up = rate(lambda i: dev.gemv_q4_0_q8(pool[(i + 1) % npool], q_pack, out_f, FFN, DIM), BYTES_GATE,
                          npool)
-    # the step's second launch (activation pack in)
-    st_down, gbs_down = rate(lambda i: dev.gemv_q4_0_q8(pool[i], a_pack, y, DIM, FFN), BYTES_DOWN, npool)
+    # the step's second launch (the pack's whole blocks and the f32 activations in)
+    st_down, gbs_down = rate(lambda i: dev.ffn_split_down(pool[i], a_pack, act, y, DIM, FFN), BYTES_DOWN, npool)
+    st_down_e, gbs_down_e = rate(lambda i: dev.gemv_q4_0_q8(pool[i], a_pack, y, DIM, FFN), BYTES_DOWN, npool)
+    # the previous two-launch form of the step: the GeGLU emitting the
+    # activation pack (32-row workgroups), the down projection reading it
+    g_emit = dev.capture(lambda: [(dev.gemv_q4_0_geglu_pack(s_["g"], s_["u"], bx, None, a_pack, FFN, DIM),
+                                   dev.gemv_q4_0_q8(s_["d"], a_pack, y, DIM, FFN)) for s_ in rot])
+    st_emit = sample_launches(dev, ev, g_emit, sets)
+    g_emit.close()
     k_geglu = st_geglu["median_s"]
     # the tolerance path's FFN step (not the headline): the same GeGLU launch,
     # then the down projection with tree-order row sums
@@ -863,7 +874,8 @@ def main() -> int:
     # each matvec against the read floor of its own bytes (floor µs / kernel µs)
     vs_floor = {"gate": floors["gate_9216x2304"]["us"] / (st_gate["median_s"] * 1e6),
                 "down": floors["gate_9216x2304"]["us"] / (st_down["median_s"] * 1e6),
-                "fused_gate_up_geglu": floors["geglu_2x9216x2304"]["us"] / (k_geglu * 1e6)}
+                "fused_gate_up_geglu": floors["geglu_2x9216x2304"]["us"] / (k_geglu * 1e6),
+                "ffn_step": (floors["geglu_2x9216x2304"]["us"] + floors["gate_9216x2304"]["us"]) / ms_per_step / 1e3}
     if q8:
         vs_floor["q8_0"] = floors["q8_0_2048x2048"]["us"] / q8["us_median"]
     if q4k:
@@ -902,7 +914,12 @@ def main() -> int:
                                       "not the headline, which stays bit-exact"},
         "per_kernel_us": {k_: {"median": round(v_["median_s"] * 1e6, 3), "min": round(v_["min_s"] * 1e6, 3),
                                "launches_per_sample": v_["launches_per_sample"]}
-                          for k_, v_ in (("geglu", st_geglu), ("gate", st_gate), ("up", st_up), ("down", st_down))},
+                          for k_, v_ in (("geglu", st_geglu), ("gate", st_gate), ("up", st_up), ("down", st_down),
+                                         ("geglu_emit_pack", st_geglu_e), ("down_from_pack", st_down_e))},
+        "ffn_emit_pack_form": {"gb_s": round(BYTES_STEP / st_emit["median_s"] / 1e9, 1),
+                               "us_per_step": round(st_emit["median_s"] * 1e6, 3),
+                               "how": "the GeGLU emitting the Q8_0 activation pack (288 workgroups of 32 rows), then "
+                                      "the down projection reading it; graph replays over the weight sets"},
         "per_matrix_rotation": f"each kernel over all {sets * 3} pool matrices ({sets * 3 * W_BYTES} B)",
         "stream_copy_gbs": round(copy_gbs, 1),
         "read_floor": {"sizes": floors,

@@ -189,11 +189,25 @@ int mrml_hip_gemv_q4_0_geglu(mrml_hip_ctx *ctx, const void *d_w_gate, const void
 /* One Gemma-style FFN, y = W_down * Q8_0(GeGLU(W_gate x, W_up x)) (model.rs:
  * 2093-2108 with a dense GeGLU FFN): two launches, the first quantising x
  * itself and writing the Q8_0 pack of the activation for the second.  d_act
- * (nullable) also receives the f32 activation.  dim = model width (cols of
- * gate/up, rows of down), ffn = hidden width. */
+ * (nullable, 16-byte aligned) also receives the f32 activation.  dim = model
+ * width (cols of gate/up, rows of down), ffn = hidden width.  At the
+ * Gemma-2-2B shape (dim 2304, ffn 9216) the launches are the split form of
+ * mrml_hip_ffn_split_geglu / _down; the result is the same bits either way. */
 int mrml_hip_ffn_geglu_q4_0(mrml_hip_ctx *ctx, const void *d_w_gate, const void *d_w_up,
                             const void *d_w_down, const float *d_x, float *d_act, float *d_y,
                             int32_t dim, int32_t ffn);
+/* The split form's two launches on their own (no reference counterpart: the
+ * FFN entry point above, for callers that interleave other work).  The
+ * GeGLU runs one 36-row workgroup per CU: 32 rows of one activation block and
+ * 4 of the tail, and writes the f32 activation (d_act, required) and the
+ * Q8_0 pack entries of the blocks it holds whole (d_act_pack, ffn/32*40
+ * bytes); the down projection takes both, quantising the tail blocks from
+ * d_act itself.  Only the shapes of the split form (dim/32 in {64, 72}, ffn
+ * = 9216 = 256 x 36) are served; others return MRML_HIP_E_INVALID. */
+int mrml_hip_ffn_split_geglu(mrml_hip_ctx *ctx, const void *d_w_gate, const void *d_w_up, const float *d_x,
+                             float *d_act, void *d_act_pack, int32_t dim, int32_t ffn);
+int mrml_hip_ffn_split_down(mrml_hip_ctx *ctx, const void *d_w_down, const void *d_act_pack, const float *d_act,
+                            float *d_y, int32_t dim, int32_t ffn);
 /* The first launch of mrml_hip_ffn_geglu_q4_0 on its own: act = GeGLU of the
  * two products over Q8_0(x), written as f32 (d_act, nullable) and as the
  * activation pack of its rows values (d_act_pack, rows/32*40 bytes). */

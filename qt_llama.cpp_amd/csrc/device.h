@@ -281,9 +281,12 @@ constexpr int kStageBatch = 5, kStageMax = 64 * kStageBatch;
 // block constant is c = 128 * sum(hi) = 8 * sum(a) - 8 * sum(lo), so that
 // q4_0_isum_split returns sum q*a, and a fourth plane at nb*40 holds the
 // block sums sum(a) (the min term's bsum): nb*44 bytes in all.
+// nstage >= 0 stages only blocks [0, nstage) (the rest of the LDS pack is
+// written by someone else); the layout stays that of nb blocks.
 template <bool ISSUE_BARRIER = false, bool KQ = false>
-__device__ __forceinline__ void stage_split_pack(const uint8_t *src, uint8_t *lds, int nb)
+__device__ __forceinline__ void stage_split_pack(const uint8_t *src, uint8_t *lds, int nb, int nstage = -1)
 {
+    const int lim = nstage >= 0 && nstage < nb ? nstage : nb;
     constexpr int kBatch = kStageBatch;
     const int lane = threadIdx.x & 63;
     const uint4 *sq = reinterpret_cast<const uint4 *>(src);
@@ -311,7 +314,7 @@ __device__ __forceinline__ void stage_split_pack(const uint8_t *src, uint8_t *ld
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
             const int b = b0 + k * 64 + lane;
-            if (b < nb) {
+            if (b < lim) {
                 const uint4 lo = make_uint4(split_lo(x[k].x, y[k].x), split_lo(x[k].y, y[k].y),
                                             split_lo(x[k].z, y[k].z), split_lo(x[k].w, y[k].w));
                 const uint4 hi = make_uint4(split_hi(x[k].x, y[k].x), split_hi(x[k].y, y[k].y),

@@ -462,6 +462,65 @@ __global__ __launch_bounds__(64 * (W + kNQ)) void gemv_q4_0_geglu_f32_kernel(
 template <int NB, int W>
 constexpr size_t geglu_f32_lds() { return (NB * 40 + 15) / 16 * 16 + (size_t)2 * 4 * W * t_stride<NB>() * sizeof(float); }
 
+// The balanced GeGLU that still emits most of the Q8_0 activation pack: R =
+// 4W = 32 + E rows per workgroup, G workgroups, rows = G*R with G*E a
+// multiple of 32.  Workgroup w owns the whole 32-row block w (rows 32w..) and
+// E rows of the tail, 32G + E*w .. + E-1, so each workgroup has the same
+// bytes (one per CU at the Gemma-2-2B FFN: 256 x 36 rows) and the block's
+// pack entry (quant.rs:193-228 over its 32 outputs) is formed inside it.  The
+// G*E/32 tail blocks straddle workgroups; their pack entries are left
+// unwritten, and the consumer quantises them from the f32 outputs (act,
+// always written).  x is quantised by kNQ staging waves and the fold runs
+// after all terms are stored (a fold pipelined with the stream through
+// per-iteration counters, and x quantised by the compute waves themselves,
+// each measured slower: 8.5 and 8.7 against 7.9 us).
+template <int NB, int W>
+__global__ __launch_bounds__(64 * (W + kNQ)) void gemv_q4_0_geglu_split_kernel(
+    const uint8_t *__restrict__ wg, const uint8_t *__restrict__ wu, const float *__restrict__ x,
+    float *__restrict__ act, uint8_t *__restrict__ act_pack, int rows)
+{
+    constexpr int NS = kNQ, ITERS = (NB + 15) / 16, R = 4 * W, E = R - 32;
+    static_assert(R <= 64 && E > 0, "one fold lane per row, a tail share per workgroup");
+    extern __shared__ __align__(16) uint8_t lds[];
+    float *T = reinterpret_cast<float *>(lds + (NB * 40 + 15) / 16 * 16);
+    const int wave = threadIdx.x >> 6;
+    if (wave < NS) {
+        quantize_into_lds<NB, kNQ>(x, lds, wave);
+        __syncthreads();  // the pack is whole
+        __syncthreads();  // every term is stored
+        return;
+    }
+    const int G = gridDim.x;
+    auto row_of = [&](int rl) { return rl < 32 ? 32 * (int)blockIdx.x + rl : 32 * G + E * (int)blockIdx.x + rl - 32; };
+    const int lane = threadIdx.x & 63, j = lane & 15;
+    const int rl = (wave - NS) * 4 + (lane >> 4);
+    const int row = row_of(rl);
+    const size_t nblk = (size_t)rows * NB, base = (size_t)row * NB;
+    RowRegs<ITERS> rg, ru;
+    __builtin_amdgcn_s_barrier();  // x's loads are issued
+    load_row<ITERS>(rg, wg, nblk, base, NB, j);
+    load_row<ITERS>(ru, wu, nblk, base, NB, j);
+    __syncthreads();
+    store_terms2<NB, ITERS>(rg, ru, lds, base, j, T, rl, R + rl);
+    __syncthreads();
+    if (wave != NS) return;
+    float g, u;
+    fold_chain2<NB>(T, lane < R ? lane : 0, lane < R ? R + lane : R, g, u);
+    const float a = gelu_tanh(g) * u;
+    if (lane < R) act[row_of(lane)] = a;
+    uint32_t dbits;
+    int qs;
+    const int q = q8_0_block32(a, dbits, qs);  // lanes 0..31: block blockIdx.x
+    const int blk = blockIdx.x, nbo = rows / 32;
+    if (lane < 32) {
+        act_pack[(size_t)blk * 32 + lane] = (uint8_t)(int8_t)q;
+        if (lane == 0) {
+            reinterpret_cast<float *>(act_pack + (size_t)nbo * 32)[blk] = f16_bits_to_f32(dbits);
+            reinterpret_cast<int32_t *>(act_pack + (size_t)nbo * 36)[blk] = qs;
+        }
+    }
+}
+
 // ---- the Gemma-2 sandwich residual ahead of the rows ---------------------------
 // Each workgroup first forms h_out = h_in + rms_norm(t, w_post) and
 // the Q8_0 pack of rms_norm(h_out, w_norm) in its own LDS (norm_block.h;
@@ -886,6 +945,130 @@ __global__ __launch_bounds__(64 * (S + 1)) void gemv_q4_0_long_kernel(const uint
     }
 }
 
+// The long-row kernel over a pack whose blocks [nmain, NB) are missing (the
+// split GeGLU's tail blocks): wave 0 stages blocks [0, nmain) from the pack
+// and then folds, as in gemv_q4_0_long_kernel; the tail blocks are quantised
+// from the f32 activations x (quant.rs:193-228) by wave 1 and the S compute
+// waves, one step of 8 blocks each (a quantiser step is a long dependent
+// chain, so one wave doing all of them sat on the critical path: +1.25 us).
+// Every wave issues its x loads before the workgroup's issue barrier and the
+// compute waves their weight loads right after it, so the quantisation runs
+// while the weights stream in.  Requires NB - nmain <= 8 * (S + 1).
+template <int NB, int S>
+__device__ __forceinline__ void mix_tail_load(const float *__restrict__ x, float4 &v, int nmain, int step)
+{
+    const int lane = threadIdx.x & 63, g = lane >> 3, l = lane & 7;
+    int b = nmain + 8 * step + g;
+    b = b < NB ? b : NB - 1;
+    v = reinterpret_cast<const float4 *>(x)[b * 8 + l];
+}
+
+template <int NB, int S>
+__device__ __forceinline__ void mix_tail_quantize(const float4 &v, uint8_t *lds, int nmain, int step)
+{
+    const int lane = threadIdx.x & 63, g = lane >> 3, l = lane & 7;
+    const int b = nmain + 8 * step + g;
+    uint32_t dbits;
+    int sum;
+    const uint32_t q = q8_split8(q8_0_block8x4(v, dbits, sum), l, sum);  // every lane takes part
+    if (b < NB) {
+        reinterpret_cast<uint32_t *>(lds)[b * 8 + l] = q;
+        if (l == 0) {
+            reinterpret_cast<float *>(lds + NB * 32)[b] = f16_bits_to_f32(dbits);
+            reinterpret_cast<int32_t *>(lds + NB * 36)[b] = sum;
+        }
+    }
+}
+
+template <int NB, int S>
+__global__ __launch_bounds__(64 * (S + 2)) void gemv_q4_0_long_mix_kernel(const uint8_t *__restrict__ w,
+                                                                        const uint8_t *xpack,
+                                                                        const float *__restrict__ x,
+                                                                        float *__restrict__ y, int rows, int nmain)
+{
+    constexpr int ITERS = NB / 16, IPW = long_ipw<NB, S>();
+    static_assert(NB % 16 == 0 && NB <= kStageMax, "whole iterations; one staging batch");
+    static_assert(IPW <= 64, "one count per round");
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint32_t *flag = reinterpret_cast<uint32_t *>(lds + NB * 40);
+    float *T = reinterpret_cast<float *>(lds + long_t_off<NB, S>());
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (wave == 1) {
+        float4 v;
+        mix_tail_load<NB, S>(x, v, nmain, 0);
+        __builtin_amdgcn_s_barrier();  // the loads are issued
+        mix_tail_quantize<NB, S>(v, lds, nmain, 0);
+        __syncthreads();  // the pack is whole
+        return;
+    }
+    if (wave == 0) {
+        const int polls = mrml_xsum::wait_polls();
+        flag[lane] = 0u;  // zero before the issue barrier inside the staging
+        stage_split_pack<true>(xpack, lds, NB, nmain);
+        __syncthreads();  // the pack is whole
+        if (lane >= 4) return;
+        const float4 *tv = reinterpret_cast<const float4 *>(T) + lane * 4;
+        float acc = 0.0f;
+#pragma unroll 1
+        for (int k = 0; k < IPW; ++k) {
+            const uint32_t want = (uint32_t)(ITERS - S * k < S ? ITERS - S * k : S);
+            mrml_xsum::bounded_wait(&flag[k], want, polls);
+            asm volatile("" ::: "memory");
+            float4 v[4 * S];
+#pragma unroll
+            for (int q = 0; q < 4 * S; ++q) v[q] = tv[(S * k + (q >> 2)) * 16 + (q & 3)];
+#pragma unroll
+            for (int q = 0; q < 4 * S; ++q) {
+                if (S * k + (q >> 2) < ITERS) {  // uniform
+                    acc = acc + v[q].x;
+                    acc = acc + v[q].y;
+                    acc = acc + v[q].z;
+                    acc = acc + v[q].w;
+                }
+            }
+        }
+        const int out = blockIdx.x * 4 + lane;
+        if (out < rows) y[out] = acc;
+        return;
+    }
+    const int sw = wave - 2, j = lane & 15, rsub = lane >> 4;
+    float4 xv;
+    mix_tail_load<NB, S>(x, xv, nmain, sw + 1);  // before the weights: an L2 hit behind HBM misses waits
+    __builtin_amdgcn_s_barrier();  // the pack's loads and the zeroed flags are in
+    const int row_raw = blockIdx.x * 4 + rsub;
+    const int row = row_raw < rows ? row_raw : rows - 1;  // tail rows recompute the last row
+    const size_t nblk = (size_t)rows * NB, base = (size_t)row * NB;
+    const uint4 *qs = reinterpret_cast<const uint4 *>(w);
+    const uint32_t *dw = reinterpret_cast<const uint32_t *>(w + nblk * 16);
+    uint4 wq[IPW];
+    uint32_t wd[IPW];
+#pragma unroll
+    for (int k = 0; k < IPW; ++k) {
+        int it = sw + S * k;
+        it = it < ITERS ? it : ITERS - 1;
+        const int b = it * 16 + j;
+        wq[k] = load_stream16(qs + base + b);
+        wd[k] = dw[(base + b) >> 1];
+    }
+    mix_tail_quantize<NB, S>(xv, lds, nmain, sw + 1);
+    __syncthreads();
+    const uint4 *aq = reinterpret_cast<const uint4 *>(lds);
+    const float *ad = reinterpret_cast<const float *>(lds + NB * 32);
+    const int32_t *ac = reinterpret_cast<const int32_t *>(lds + NB * 36);
+#pragma unroll
+    for (int k = 0; k < IPW; ++k) {
+        const int it = sw + S * k;
+        const int b = (it < ITERS ? it : ITERS - 1) * 16 + j;
+        const uint4 q = wq[k], lo = aq[2 * b], hi = aq[2 * b + 1];
+        const int32_t isum = q4_0_isum_split(q.x, q.y, q.z, q.w, lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w, ac[b]);
+        const uint32_t dbits = ((base + b) & 1) ? wd[k] >> 16 : wd[k] & 0xffffu;
+        T[((sw + S * k) * 4 + rsub) * 16 + j] = (float)isum * (f16_bits_to_f32(dbits) * ad[b]);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the terms are in LDS before the count
+        if (lane == 0 && it < ITERS)
+            __hip_atomic_fetch_add(&flag[k], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+}
+
 // ---- relaxed rows: the tolerance path's matvec -----------------------------------
 // kRelaxR rows per workgroup, one wave per row (lane l: blocks l, l+64, ...),
 // wave 0 staging the pack.  Every integer block dot and every block term is
@@ -1124,6 +1307,22 @@ constexpr int kLongS = 3;       // compute waves per 4 rows of the long-row kern
 inline bool fold16_shape(int nb) { return nb == 64 || nb == 72; }
 inline bool relay_shape(int nb) { return nb == 288; }
 
+}  // namespace
+
+// The FFN's two launches in the balanced split form (gemv_q4_0_geglu_split_kernel
+// + gemv_q4_0_long_mix_kernel): the Gemma-2-2B FFN shape, 9216 = 256 x 36 rows.
+constexpr int kSplitW = 9;  // 36 rows a workgroup: 32 of one block, 4 of the tail
+bool ffn_split_ok(int dim, int ffn)
+{
+    const int R = 4 * kSplitW, E = R - 32;
+    if (!(relay_shape(ffn / 32) && fold16_shape(dim / 32) && ffn % R == 0)) return false;
+    const int G = ffn / R;
+    return (G * E) % 32 == 0 && G * E / 32 <= 8 * (kLongS + 1) && (((int64_t)dim * (ffn / 32)) & 1) == 0 &&
+           (((int64_t)ffn * (dim / 32)) & 1) == 0;
+}
+
+namespace {
+
 #define MRML_FOLD16_NB(NB_VAL, BODY)                                                  \
     switch (NB_VAL) {                                                                 \
     case 64: { constexpr int NB = 64; BODY; } break;                                  \
@@ -1257,6 +1456,39 @@ int launch_gemv_q4_0(mrml_hip_ctx *ctx, const void *w, const void *xpack, float 
 
 // f32 input: quantised inside the kernel where a fixed instance exists, else
 // through the scratch pack.
+// The split form's two launches.  GeGLU: x (cols f32) -> act (rows f32) and
+// the pack of its whole blocks (act_pack_bytes(rows / 32) bytes; the tail
+// blocks [split_main_blocks(rows), rows / 32) left out).  Down: the pack's
+// whole blocks plus the tail blocks quantised from act -> y (rows f32).
+int split_main_blocks(int ffn) { return ffn / (4 * kSplitW); }
+
+int launch_geglu_split(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *x, float *act, void *pack,
+                       int32_t rows, int32_t cols)
+{
+    MRML_FOLD16_NB(cols / 32, {
+        hipLaunchKernelGGL((gemv_q4_0_geglu_split_kernel<NB, kSplitW>), dim3(split_main_blocks(rows)),
+                           dim3(64 * (kSplitW + kNQ)), (geglu_f32_lds<NB, kSplitW>()), ctx->stream,
+                           (const uint8_t *)wg, (const uint8_t *)wu, x, act, (uint8_t *)pack, rows);
+    });
+    return check_launch(ctx, "gemv_q4_0_geglu_split_kernel");
+}
+
+int launch_down_mix(mrml_hip_ctx *ctx, const void *wd, const void *pack, const float *act, float *y, int32_t rows,
+                    int32_t cols)
+{
+    hipLaunchKernelGGL((gemv_q4_0_long_mix_kernel<288, kLongS>), dim3((rows + 3) / 4), dim3(64 * (kLongS + 2)),
+                       (long_lds<288, kLongS>()), ctx->stream, (const uint8_t *)wd, (const uint8_t *)pack, act, y, rows,
+                       split_main_blocks(cols));
+    return check_launch(ctx, "gemv_q4_0_long_mix_kernel");
+}
+
+int launch_ffn_split(mrml_hip_ctx *ctx, const void *wg, const void *wu, const void *wd, const float *x, float *act,
+                     void *pack, float *y, int32_t dim, int32_t ffn)
+{
+    if (int rc = launch_geglu_split(ctx, wg, wu, x, act, pack, ffn, dim)) return rc;
+    return launch_down_mix(ctx, wd, pack, act, y, dim, ffn);
+}
+
 int launch_gemv_q4_0_x(mrml_hip_ctx *ctx, const void *w, const float *x, float *y, int32_t rows, int32_t cols)
 {
     const int nb = cols / 32;

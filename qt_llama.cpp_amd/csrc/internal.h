@@ -50,6 +50,14 @@ int launch_gemv_q4_0(mrml_hip_ctx *ctx, const void *w, const void *xpack, float 
 int launch_gemv_q4_0_gguf(mrml_hip_ctx *ctx, const void *w, const void *xpack, float *y,
                           int32_t rows, int32_t cols);
 // f32-input forms: quantise x inside the kernel where a fixed instance exists.
+bool ffn_split_ok(int dim, int ffn);
+int launch_ffn_split(mrml_hip_ctx *ctx, const void *wg, const void *wu, const void *wd, const float *x, float *act,
+                     void *pack, float *y, int32_t dim, int32_t ffn);
+int split_main_blocks(int ffn);
+int launch_geglu_split(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *x, float *act, void *pack,
+                       int32_t rows, int32_t cols);
+int launch_down_mix(mrml_hip_ctx *ctx, const void *wd, const void *pack, const float *act, float *y, int32_t rows,
+                    int32_t cols);
 int launch_gemv_q4_0_x(mrml_hip_ctx *ctx, const void *w, const float *x, float *y, int32_t rows, int32_t cols);
 int launch_gemv_q4_0_geglu_x(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *x, float *act,
                              void *act_pack, int32_t rows, int32_t cols);

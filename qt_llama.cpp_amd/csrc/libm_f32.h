@@ -60,6 +60,14 @@ MRML_HD double u2d(uint64_t u) { return __builtin_bit_cast(double, u); }
 // is preserved.
 // ====================================================
 
+// Both are written without data-dependent branches: every lane evaluates
+// the argument reduction and the candidate results of fdlibm's cases, each
+// with exactly the operations of its case, and selects the one its own
+// argument picks.  A wave of GeGLU activations spans most of the cases, and
+// as branches each taken case ran for the whole wave (about 1 us of the
+// GeGLU kernel's tail).  k = 0 and k = +-1 reduce to fdlibm's generic
+// formula exactly (t*ln2_hi and t*ln2_lo are exact for t = 0, +-1, and
+// x - (-y) is x + y), so one reduction serves every case.
 MRML_HD float expm1f(float x)
 {
     const float ln2_hi = 6.9313812256e-01f;   // 0x3f317180
@@ -70,86 +78,63 @@ MRML_HD float expm1f(float x)
     uint32_t hx = f2u(x);
     const uint32_t xsb = hx & 0x80000000u;
     hx &= 0x7fffffffu;
-    if (hx >= 0x4195b844u) {             // |x| >= 27 ln2
-        if (hx >= 0x42b17218u) {         // |x| >= 88.72
-            if (hx > 0x7f800000u) return x + x;
-            if (hx == 0x7f800000u) return xsb == 0 ? x : -1.0f;
-            if (x > 8.8721679688e+01f) return __builtin_inff();
-        }
-        if (xsb != 0) return -1.0f;      // x < -27 ln2
-    }
-    float hi, lo, c = 0.0f;
-    int32_t k;
-    if (hx > 0x3eb17218u) {              // |x| > 0.5 ln2
-        if (hx < 0x3f851592u) {          // and |x| < 1.5 ln2
-            if (xsb == 0) { hi = x - ln2_hi; lo = ln2_lo; k = 1; }
-            else          { hi = x + ln2_hi; lo = -ln2_lo; k = -1; }
-        } else {
-            k = (int32_t)(invln2 * x + (xsb == 0 ? 0.5f : -0.5f));
-            const float t = (float)k;
-            hi = x - t * ln2_hi;         // exact
-            lo = t * ln2_lo;
-        }
-        x = hi - lo;
-        c = (hi - x) - lo;
-    } else if (hx < 0x33000000u) {       // |x| < 2^-25
-        const float t = 1.0f + x;
-        return x - (t - (1.0f + x));
-    } else {
-        k = 0;
-    }
-    const float hfx = 0.5f * x;
-    const float hxs = x * hfx;
+    const bool neg = xsb != 0;
+    const bool red = hx > 0x3eb17218u;     // |x| > 0.5 ln2: reduce by k ln2
+    const bool near1 = hx < 0x3f851592u;   // and |x| < 1.5 ln2: k = +-1
+    // the generic k; the clamp only keeps the conversion defined for the
+    // arguments whose result a special case replaces (|x| < 88.8 gives |k| < 129)
+    float kf = invln2 * x + (neg ? -0.5f : 0.5f);
+    kf = kf > -200.0f ? (kf < 200.0f ? kf : 200.0f) : -200.0f;
+    const int32_t k = red ? (near1 ? (neg ? -1 : 1) : (int32_t)kf) : 0;
+    const float tk = (float)k;
+    const float hi = x - tk * ln2_hi;  // exact
+    const float lo = tk * ln2_lo;
+    const float xr = hi - lo;
+    const float c = red ? (hi - xr) - lo : 0.0f;
+    const float hfx = 0.5f * xr;
+    const float hxs = xr * hfx;
     const float r1 = 1.0f + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
-    float t = 3.0f - r1 * hfx;
-    float e = hxs * ((r1 - t) / (6.0f - x * t));
-    if (k == 0) return x - (x * e - hxs);
-    e = (x * (e - c) - c);
-    e -= hxs;
-    if (k == -1) return 0.5f * (x - e) - 0.5f;
-    if (k == 1) {
-        if (x < -0.25f) return -2.0f * (e - (x + 0.5f));
-        return 1.0f + 2.0f * (x - e);
-    }
-    if (k <= -2 || k > 56) {             // exp(x) - 1 directly
-        float y = 1.0f - (e - x);
-        y = u2f(f2u(y) + ((uint32_t)k << 23));
-        return y - 1.0f;
-    }
-    float y;
-    if (k < 23) {
-        t = u2f(0x3f800000u - (0x1000000u >> k));   // 1 - 2^-k
-        y = t - (e - x);
-        y = u2f(f2u(y) + ((uint32_t)k << 23));
-    } else {
-        t = u2f((uint32_t)(0x7f - k) << 23);        // 2^-k
-        y = x - (e + t);
-        y += 1.0f;
-        y = u2f(f2u(y) + ((uint32_t)k << 23));
-    }
-    return y;
+    const float t = 3.0f - r1 * hfx;
+    const float e = hxs * ((r1 - t) / (6.0f - xr * t));
+    const float r_k0 = xr - (xr * e - hxs);
+    float e2 = (xr * (e - c) - c);
+    e2 -= hxs;
+    const float r_km1 = 0.5f * (xr - e2) - 0.5f;
+    const float r_k1 = xr < -0.25f ? -2.0f * (e2 - (xr + 0.5f)) : 1.0f + 2.0f * (xr - e2);
+    const uint32_t ksh = (uint32_t)k << 23;
+    const float r_far = u2f(f2u(1.0f - (e2 - xr)) + ksh) - 1.0f;  // k <= -2 or k > 56: exp(x) - 1 directly
+    const int32_t kl = k < 0 ? 0 : (k > 31 ? 31 : k);            // shift counts in range for every lane
+    const float r_lo = u2f(f2u(u2f(0x3f800000u - (0x1000000u >> kl)) - (e2 - xr)) + ksh);  // 2 <= k < 23
+    const int32_t kh = k < 0 ? 0 : (k > 0x7e ? 0x7e : k);
+    float y = xr - (e2 + u2f((uint32_t)(0x7f - kh) << 23));      // 23 <= k <= 56
+    y += 1.0f;
+    const float r_hi = u2f(f2u(y) + ksh);
+    float r = k == 0 ? r_k0
+                     : (k == -1 ? r_km1 : (k == 1 ? r_k1 : ((k <= -2 || k > 56) ? r_far : (k < 23 ? r_lo : r_hi))));
+    const float tt = 1.0f + x;
+    if (!red && hx < 0x33000000u) r = x - (tt - (1.0f + x));  // |x| < 2^-25
+    if (hx >= 0x4195b844u && neg) r = -1.0f;                  // x < -27 ln2
+    if (hx >= 0x42b17218u && !neg && x > 8.8721679688e+01f) r = __builtin_inff();
+    if (hx == 0x7f800000u) r = neg ? -1.0f : x;
+    if (hx > 0x7f800000u) r = x + x;
+    return r;
 }
 
 MRML_HD float tanhf(float x)
 {
     const uint32_t jx = f2u(x), ix = jx & 0x7fffffffu;
-    if (ix >= 0x7f800000u) return (jx >> 31) == 0 ? 1.0f / x + 1.0f : 1.0f / x - 1.0f;  // +-1, NaN
-    float z;
-    if (ix < 0x41b00000u) {              // |x| < 22
-        if (ix == 0) return x;
-        if (ix < 0x24000000u) return x * (1.0f + x);   // |x| < 2^-55
-        const float ax = u2f(ix);
-        if (ix >= 0x3f800000u) {         // |x| >= 1
-            const float t = expm1f(2.0f * ax);
-            z = 1.0f - 2.0f / (t + 2.0f);
-        } else {
-            const float t = expm1f(-2.0f * ax);
-            z = -t / (t + 2.0f);
-        }
-    } else {
-        z = 1.0f;                        // 1 - tiny rounds to 1
-    }
-    return (jx >> 31) == 0 ? z : -z;
+    const float ax = u2f(ix);
+    const bool ge1 = ix >= 0x3f800000u;  // |x| >= 1: 1 - 2/(expm1(2|x|) + 2); else -t/(t + 2), t = expm1(-2|x|)
+    const float t = expm1f(ge1 ? 2.0f * ax : -2.0f * ax);
+    const float q = (ge1 ? 2.0f : -t) / (t + 2.0f);
+    float z = ge1 ? 1.0f - q : q;
+    if (ix >= 0x41b00000u) z = 1.0f;     // |x| >= 22: 1 - tiny rounds to 1
+    float r = (jx >> 31) == 0 ? z : -z;
+    if (ix < 0x24000000u) r = x * (1.0f + x);  // |x| < 2^-55
+    if (ix == 0) r = x;
+    if (ix == 0x7f800000u) r = (jx >> 31) == 0 ? 1.0f : -1.0f;  // 1/x +- 1
+    if (ix > 0x7f800000u) r = x + x;                            // NaN
+    return r;
 }
 
 // ---- expf (Arm optimized-routines algorithm) -------------------------------------

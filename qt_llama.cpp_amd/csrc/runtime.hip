@@ -504,10 +504,43 @@ int mrml_hip_ffn_geglu_q4_0(mrml_hip_ctx *ctx, const void *wg, const void *wu, c
     CHECK_MATVEC(ctx, wg, x, y, ffn, dim, 32);
     REQUIRE(ctx, wu && wd, "null pointer");
     REQUIRE(ctx, ffn % 32 == 0, "ffn=%d is not a multiple of 32", ffn);
+    if (ffn_split_ok(dim, ffn)) {
+        // the balanced GeGLU (one workgroup per CU) forming the pack blocks it
+        // owns whole, then the down projection quantising the rest from the
+        // f32 outputs: the same Q8_0 bits as one quantiser over all of them
+        const size_t pk = align_up(act_pack_bytes(ffn / 32), 256);
+        uint8_t *ws = (uint8_t *)workspace(ctx, pk + (act ? 0 : (size_t)ffn * sizeof(float)));
+        if (!ws) return MRML_HIP_E_ALLOC;
+        float *a = act ? act : reinterpret_cast<float *>(ws + pk);
+        REQUIRE(ctx, ((uintptr_t)a & 15) == 0, "ffn_geglu_q4_0: act must be 16-byte aligned");
+        return launch_ffn_split(ctx, wg, wu, wd, x, a, ws, y, dim, ffn);
+    }
     void *pk = workspace(ctx, act_pack_bytes(ffn / 32));
     if (!pk) return MRML_HIP_E_ALLOC;
     if (int rc = launch_gemv_q4_0_geglu_x(ctx, wg, wu, x, act, pk, ffn, dim)) return rc;
     return launch_gemv_q4_0(ctx, wd, pk, y, dim, ffn);
+}
+
+int mrml_hip_ffn_split_geglu(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *x, float *act,
+                             void *act_pack, int32_t dim, int32_t ffn)
+{
+    CTX_GUARD(ctx);
+    CHECK_MATVEC(ctx, wg, x, act, ffn, dim, 32);
+    REQUIRE(ctx, wu && act_pack, "null pointer");
+    REQUIRE(ctx, ffn_split_ok(dim, ffn), "ffn_split_geglu: dim=%d ffn=%d is not a shape of the split form", dim, ffn);
+    REQUIRE(ctx, ((uintptr_t)act_pack & 15) == 0, "ffn_split_geglu: act_pack must be 16-byte aligned");
+    return launch_geglu_split(ctx, wg, wu, x, act, act_pack, ffn, dim);
+}
+
+int mrml_hip_ffn_split_down(mrml_hip_ctx *ctx, const void *wd, const void *act_pack, const float *act, float *y,
+                            int32_t dim, int32_t ffn)
+{
+    CTX_GUARD(ctx);
+    CHECK_MATVEC(ctx, wd, act, y, dim, ffn, 32);
+    REQUIRE(ctx, act_pack, "null pointer");
+    REQUIRE(ctx, ffn_split_ok(dim, ffn), "ffn_split_down: dim=%d ffn=%d is not a shape of the split form", dim, ffn);
+    REQUIRE(ctx, ((uintptr_t)act_pack & 15) == 0, "ffn_split_down: act_pack must be 16-byte aligned");
+    return launch_down_mix(ctx, wd, act_pack, act, y, dim, ffn);
 }
 
 int mrml_hip_gemv_q4_0_geglu_q8(mrml_hip_ctx *ctx, const void *wg, const void *wu, const void *xpack,

@@ -223,6 +223,48 @@ def test_ffn_geglu_fused(backend, dev, orc, synth):
     assert_bit_exact(y2.numpy(), y.numpy(), "ffn without act output")
 
 
+def test_ffn_split_launches(backend, dev, orc, synth):
+    """The split FFN's two launches on their own (the FFN entry point's form
+    at the Gemma-2-2B shape): the GeGLU over 256 workgroups of 36 rows writes
+    the oracle's f32 activation and, for the 256 blocks of 32 rows it holds
+    whole, the oracle quantiser's pack entries (quants, f16 scale, quant sum);
+    the down projection, quantising the 32 tail blocks from the f32
+    activation itself, equals the oracle down projection of that activation.
+    A pack whose tail blocks hold garbage leaves the result unchanged."""
+    dim, ffn = 2304, 9216
+    rng = synth.rng_for(5550)
+    wg, wu = synth.q4_0_matrix(rng, ffn, dim), synth.q4_0_matrix(rng, ffn, dim)
+    wd = synth.q4_0_matrix(rng, dim, ffn)
+    x = synth.rms_normalised(synth.normal_vector(rng, dim))
+    bg, bu = (backend.HipBuffer.from_gguf(dev, w, backend.Q4_0, ffn, dim) for w in (wg, wu))
+    bd = backend.HipBuffer.from_gguf(dev, wd, backend.Q4_0, dim, ffn)
+    xb = upload(backend, dev, x)
+    act = backend.HipBuffer.alloc(dev, ffn)
+    nbo = ffn // 32
+    pack = backend.HipBuffer.from_host(dev, np.full(nbo * 40, 0x7F, np.uint8))  # garbage in every tail block
+    y = backend.HipBuffer.alloc(dev, dim)
+    dev.ffn_split_geglu(bg, bu, xb, act, pack, dim, ffn)
+    dev.ffn_split_down(bd, pack, act, y, dim, ffn)
+    dev.sync()
+    a = act.numpy()
+    xq = orc.quantize_q8_0(x)
+    ref_act = orc.geglu(orc.mat_vec_mul_q4_0_q8_0(wg, xq, ffn, dim, threads=THREADS),
+                        orc.mat_vec_mul_q4_0_q8_0(wu, xq, ffn, dim, threads=THREADS))
+    assert_bit_exact(a, ref_act, "split ffn act")
+    pk = pack.numpy()
+    ref = orc.quantize_q8_0(a).reshape(nbo, 34)
+    main = 256
+    got_q = pk[:nbo * 32].reshape(nbo, 32)[:main]
+    got_d = pk[nbo * 32:nbo * 36].view(np.float32)[:main].astype(np.float16).view(np.uint8).reshape(main, 2)
+    assert np.array_equal(got_q, ref[:main, 2:]) and np.array_equal(got_d, ref[:main, :2]), "the whole blocks' pack"
+    sums = ref[:main, 2:].view(np.int8).astype(np.int32).sum(axis=1)
+    assert np.array_equal(pk[nbo * 36:nbo * 40].view(np.int32)[:main], sums), "block sums"
+    assert np.all(pk[main * 32:nbo * 32] == 0x7F), "tail blocks left to the consumer"
+    assert_bit_exact(y.numpy(), orc.mat_vec_mul_q4_0(wd, a, dim, ffn, threads=THREADS), "split ffn down")
+    with pytest.raises(backend.HipError):
+        dev.ffn_split_geglu(bg, bu, xb, act, pack, dim, 9216 - 288)  # not the split form's shape
+
+
 def test_ffn_repeated_and_replayed(backend, dev, synth):
     """The FFN entry point at the Gemma-2-2B shape, called many times in a row
     and replayed from a captured graph with eager calls between the replays:
