@@ -216,6 +216,49 @@ __device__ __forceinline__ void store_terms2(const RowRegs<ITERS> &ra, const Row
     }
 }
 
+// store_terms2 with every pack read of the lane (its blocks j, 16 + j, ...:
+// two 16-byte quant words, the scale and the constant of each) issued at
+// once, before the first term: the LDS latency is paid once instead of once
+// per iteration (the weights' loads set the pace after that).
+template <int NB, int ITERS>
+__device__ __forceinline__ void store_terms2_pre(const RowRegs<ITERS> &ra, const RowRegs<ITERS> &rb,
+                                                 const uint8_t *pack, size_t base, int j, float *T, int chain_a,
+                                                 int chain_b)
+{
+    const uint4 *aq = reinterpret_cast<const uint4 *>(pack);
+    const float *ad = reinterpret_cast<const float *>(pack + NB * 32);
+    const int32_t *ac = reinterpret_cast<const int32_t *>(pack + NB * 36);
+    uint4 lo[ITERS], hi[ITERS];
+    float d[ITERS];
+    int32_t c[ITERS];
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+        const int b = it * 16 + j, bc = b < NB ? b : NB - 1;
+        lo[it] = aq[2 * bc];
+        hi[it] = aq[2 * bc + 1];
+        d[it] = ad[bc];
+        c[it] = ac[bc];
+    }
+    asm volatile("" ::: "memory");  // every pack read above is issued before the terms' stores
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+        const int b = it * 16 + j, bc = b < NB ? b : NB - 1;
+        float t[2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            const RowRegs<ITERS> &r = m ? rb : ra;
+            const uint4 w = r.w[it];
+            const int32_t isum = q4_0_isum_split(w.x, w.y, w.z, w.w, lo[it].x, lo[it].y, lo[it].z, lo[it].w,
+                                                 hi[it].x, hi[it].y, hi[it].z, hi[it].w, c[it]);
+            const uint32_t dbits = ((base + bc) & 1) ? r.d[it] >> 16 : r.d[it] & 0xffffu;
+            const float tv = (float)isum * (f16_bits_to_f32(dbits) * d[it]);
+            t[m] = b < NB ? tv : 0.0f;
+        }
+        T[chain_a * t_stride<NB>() + it * 16 + j] = t[0];
+        T[chain_b * t_stride<NB>() + it * 16 + j] = t[1];
+    }
+}
+
 // The ordered sum of chain `chain` (all NB/4 reads issued before the adds).
 template <int NB>
 __device__ __forceinline__ float fold_chain(const float *T, int chain)
@@ -488,6 +531,7 @@ __global__ __launch_bounds__(64 * (W + kNQ)) void gemv_q4_0_geglu_split_kernel(
         quantize_into_lds<NB, kNQ>(x, lds, wave);
         __syncthreads();  // the pack is whole
         __syncthreads();  // every term is stored
+        __syncthreads();  // the up sums are shared
         return;
     }
     const int G = gridDim.x;
@@ -501,12 +545,19 @@ __global__ __launch_bounds__(64 * (W + kNQ)) void gemv_q4_0_geglu_split_kernel(
     load_row<ITERS>(rg, wg, nblk, base, NB, j);
     load_row<ITERS>(ru, wu, nblk, base, NB, j);
     __syncthreads();
-    store_terms2<NB, ITERS>(rg, ru, lds, base, j, T, rl, R + rl);
+    store_terms2_pre<NB, ITERS>(rg, ru, lds, base, j, T, rl, R + rl);
     __syncthreads();
-    if (wave != NS) return;
-    float g, u;
-    fold_chain2<NB>(T, lane < R ? lane : 0, lane < R ? R + lane : R, g, u);
-    const float a = gelu_tanh(g) * u;
+    // the gate chains and GELU in one wave, the up chains in the next (two
+    // dependent chains of 72 adds in one wave ran one after the other)
+    float *ushare = reinterpret_cast<float *>(lds);  // the pack is no longer read
+    if (wave != NS) {
+        if (wave == NS + 1) ushare[lane] = fold_chain<NB>(T, lane < R ? R + lane : R);
+        __syncthreads();  // the up sums are shared (every wave takes part)
+        return;
+    }
+    const float gg = gelu_tanh(fold_chain<NB>(T, lane < R ? lane : 0));
+    __syncthreads();
+    const float a = gg * ushare[lane];
     if (lane < R) act[row_of(lane)] = a;
     uint32_t dbits;
     int qs;
