@@ -293,19 +293,22 @@ __device__ float block_seq_sum_nonneg(const float *a, int n, uint8_t *flags, Sha
 // ulp prefix before the run's first term) reaches it by a max-scan (the
 // prefix never decreases).  The prefix stays below 2^31: the safe steps in
 // one binade add fewer than 2^23 ulps, and s visits each binade once.
-// The events land in block order after the waves' counts are exchanged;
-// wave 0 then adds them with operands from broadcast LDS reads (a register
-// chain: v_readlane operands would cost several times more per add).  Four
-// barriers, all LDS-only (pending global stores are not waited for).  Ends
-// without a barrier after reading the result: x may be rewritten only after
-// the caller's next barrier.
-constexpr int kPadEvents = 16;  // zeros after the last event (the walk reads groups of 16)
+// The events land in block order after the waves' counts are exchanged
+// (each lane's event stores unconditional: a lane with no event writes the
+// trash word); every wave then adds them itself, the same adds in the same
+// order, with operands from broadcast LDS reads (a register chain: v_readlane
+// operands would cost several times more per add), so no barrier broadcasts
+// the result.  Three barriers, all LDS-only (pending global stores are not
+// waited for).  A following call may reuse x at once (its writes to the list
+// come after its second barrier); other LDS the caller reuses needs the
+// caller's own barrier.
+constexpr int kPadEvents = 32;  // zeros after the last event (the walk reads groups of 32)
 
 struct Shared4 {
     float ev[16 * 256 + kPadEvents];  // event addends in order (at most one per term)
     float wtot[16];                   // per-wave totals of the approximate prefix scan
     int wcnt[16];                     // per-wave event counts
-    float result;
+    float trash;                      // target of the event stores of lanes that have no event
 };
 
 __device__ __forceinline__ void lds_barrier()  // s_barrier after this wave's LDS accesses
@@ -362,19 +365,8 @@ __device__ __forceinline__ float block_seq_sum_nonneg4(float4 v, int n, Shared4 
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
     const int k0 = 4 * tid;
-    const int wv = __builtin_amdgcn_readfirstlane(wave);  // uniform: branch and readlane index
-    if (256 * wv >= n) {
-        // no term in this wave: no prefix, no events; it keeps the barriers
-        if (lane == 63) {
-            x.wtot[wave] = 0.0f;
-        }
-        lds_barrier();
-        if (lane == 63) x.wcnt[wave] = 0;
-        lds_barrier();
-        lds_barrier();
-        lds_barrier();
-        return x.result;
-    }
+    const int wv = __builtin_amdgcn_readfirstlane(wave);  // uniform: the readlane index
+    // (a wave past n has no terms and no events; it runs the same steps)
     float a[4] = {v.x, v.y, v.z, v.w};
     float lp[4], run = 0.0f;
 #pragma unroll
@@ -437,52 +429,51 @@ __device__ __forceinline__ float block_seq_sum_nonneg4(float4 v, int n, Shared4 
     const int ci = row_incl_scan_i32(cw);
     const int nev = __builtin_amdgcn_readlane(ci, 15);
     const int goff = wv ? __builtin_amdgcn_readlane(ci, wv - 1) : 0;
-    if (wave == 0 && lane < kPadEvents) x.ev[nev + lane] = 0.0f;
+    float *const trash = &x.trash;
+    {
+        float *pz = (wave == 0 && lane < kPadEvents) ? x.ev + nev + lane : trash;
+        *pz = 0.0f;
+    }
     float *ev = x.ev + goff;
     int e = cincl - cnt;  // events started before this thread's terms
     r = iincl - my_inc;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const bool st = (starts >> i) & 1;
+        const bool st = (starts >> i) & 1, uns = (unsafe >> i) & 1, en = (ends >> i) & 1;
         e += st ? 1 : 0;
-        if (st && !((unsafe >> i) & 1)) rs = r;
+        rs = (st && !uns) ? r : rs;
         const uint32_t re = r + inc[i];
-        if ((unsafe >> i) & 1) ev[e - 1] = a[i];
-        if ((ends >> i) & 1) ev[e - 1] = (float)(int)(re - rs) * uu[i];  // exact: < 2^23 ulps, u a power of 2
+        // an unsafe term adds itself; a run's last term its run's exact total
+        // (< 2^23 ulps, u a power of 2)
+        const float val = uns ? a[i] : (float)(int)(re - rs) * uu[i];
+        float *dst = (uns || en) ? ev + (e - 1) : trash;
+        *dst = val;
         r = re;
     }
     lds_barrier();
-    // the ordered sum, by wave 0 alone: 32 events at a time, all of their
-    // broadcast 16-byte reads issued before the first add (an LDS read takes
-    // a few hundred cycles under load; the scheduling barrier keeps the reads
-    // ahead), then the adds (the zero pad makes the last group of 16 whole;
-    // +0 leaves s unchanged: s >= +0)
-    if (wave == 0) {
-        const float4 *e4 = reinterpret_cast<const float4 *>(x.ev);
-        const int n4 = ((nev + 15) >> 4) * 4;  // float4 reads covering the list
-        float s = 0.0f;
-        for (int q0 = 0; q0 < n4; q0 += 8) {
-            float4 b[8];
+    // the ordered sum, 32 events per batch: every 16-byte read of a batch
+    // issued before its first add (an LDS read takes a few hundred cycles
+    // under load; the scheduling barrier keeps the reads ahead), the zero pad
+    // completing the last batch (+0 leaves s unchanged: s >= +0)
+    const float4 *e4 = reinterpret_cast<const float4 *>(x.ev);
+    const int n4 = (nev + 3) >> 2;
+    float s = 0.0f;
+    int q0 = 0;
+    do {
+        float4 b[kPadEvents / 4];
 #pragma unroll
-            for (int q = 0; q < 8; ++q) b[q] = e4[q0 + q < n4 ? q0 + q : n4 - 1];
-            __builtin_amdgcn_sched_barrier(0);
+        for (int q = 0; q < kPadEvents / 4; ++q) b[q] = e4[q0 + q];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int g = 0; g < 2; ++g) {
-                if (q0 + 4 * g < n4) {
-#pragma unroll
-                    for (int q = 4 * g; q < 4 * g + 4; ++q) {
-                        s += b[q].x;
-                        s += b[q].y;
-                        s += b[q].z;
-                        s += b[q].w;
-                    }
-                }
-            }
+        for (int q = 0; q < kPadEvents / 4; ++q) {
+            s += b[q].x;
+            s += b[q].y;
+            s += b[q].z;
+            s += b[q].w;
         }
-        if (lane == 0) x.result = s;
-    }
-    lds_barrier();
-    return x.result;
+        q0 += kPadEvents / 4;
+    } while (q0 < n4);
+    return s;
 }
 
 // ---- tree sums (the tolerance path) ---------------------------------------------
@@ -600,13 +591,16 @@ struct GroupSync {
 };
 
 // LDS of a group sum: the event list (at most one event per term) and the
-// zero pad live at evl, sized by the caller: group_events(n) floats.
-constexpr int group_events(int n) { return n + kPadEvents; }
+// zero pad the walk reads past it, at evl, sized by the caller:
+// group_events(n) floats.
+constexpr int kGroupWalk = 32;  // events per walk batch (eight 16-byte reads)
+constexpr int group_events(int n) { return n + kGroupWalk; }
 
 struct GroupShared {
     float wtot[16];
     int wcnt[16];
     float result;
+    float trash;  // target of the event stores of lanes that have no event
 };
 
 // Tree sum over the nw (<= 8) waves of a group: the wave totals go to
@@ -624,7 +618,14 @@ __device__ __forceinline__ float group_tree_sum(float v, int gw, GroupSync &sync
 
 // Sum of the terms held by the group (n terms in all), bit for bit the
 // sequential loop.  Every lane of the nw waves calls it; gw is the wave's
-// index in the group (uniform).
+// index in the group (uniform).  The workgroup form's steps with three group
+// syncs: the wave totals, the event counts, the event list.  Each lane's
+// event stores are unconditional (a lane with no event writes the trash
+// word), and every wave walks the list itself, the same adds in the same
+// order, so no fourth sync broadcasts the result.  The caller may start the
+// next sum at once: its first LDS writes (the wave totals, then the counts
+// and events after its syncs) land only after every wave has passed this
+// sum's last sync.
 template <int K>
 __device__ __forceinline__ float group_seq_sum_nonneg(const float (&av)[K], int n, int gw, GroupSync &sync,
                                                       GroupShared &x, float *evl)
@@ -632,15 +633,6 @@ __device__ __forceinline__ float group_seq_sum_nonneg(const float (&av)[K], int 
     static_assert(K >= 1 && K <= 32 && K + 12 <= kDepth, "masks in 32 bits; prefix depth within the margin");
     const int lane = threadIdx.x & 63, nw = (int)sync.nw;
     const int k0 = K * (64 * gw + lane);
-    if (64 * K * gw >= n) {
-        if (lane == 63) x.wtot[gw] = 0.0f;
-        sync();
-        if (lane == 63) x.wcnt[gw] = 0;
-        sync();
-        sync();
-        sync();
-        return x.result;
-    }
     float a[K], lp[K], run = 0.0f;
 #pragma unroll
     for (int i = 0; i < K; ++i) {
@@ -700,50 +692,51 @@ __device__ __forceinline__ float group_seq_sum_nonneg(const float (&av)[K], int 
     const int ci = row_incl_scan_i32(cw);
     const int nev = min(__builtin_amdgcn_readlane(ci, 15), n);
     const int goff = gw ? min(__builtin_amdgcn_readlane(ci, gw - 1), n) : 0;
-    if (gw == 0 && lane < kPadEvents) evl[nev + lane] = 0.0f;
+    float *const trash = &x.trash;
+    {
+        float *pz = (gw == 0 && lane < kGroupWalk) ? evl + nev + lane : trash;
+        *pz = 0.0f;
+    }
     float *ev = evl + goff;
     const int ecap = n - goff;  // events this wave may store
     int e = cincl - cnt;
     r = iincl - my_inc;
 #pragma unroll
     for (int i = 0; i < K; ++i) {
-        const bool st = (starts >> i) & 1u;
+        const bool st = (starts >> i) & 1u, uns = (unsafe >> i) & 1u, en = (ends >> i) & 1u;
         e += st ? 1 : 0;
-        if (st && !((unsafe >> i) & 1u)) rs = r;
+        rs = (st && !uns) ? r : rs;
         const uint32_t re = r + inc[i];
-        const bool room = e <= ecap;
-        if (((unsafe >> i) & 1u) && room) ev[e - 1] = a[i];
-        if (((ends >> i) & 1u) && room) ev[e - 1] = (float)(int)(re - rs) * uu[i];  // exact: < 2^23 ulps, u a power of 2
+        // an unsafe term adds itself; a run's last term its run's exact total
+        // (< 2^23 ulps, u a power of 2)
+        const float val = uns ? a[i] : (float)(int)(re - rs) * uu[i];
+        float *dst = ((uns || en) && e <= ecap) ? ev + (e - 1) : trash;
+        *dst = val;
         r = re;
     }
     sync();
-    // the ordered walk by group wave 0, as in the workgroup form
-    if (gw == 0) {
-        const float4 *e4 = reinterpret_cast<const float4 *>(evl);
-        const int n4 = ((nev + 15) >> 4) * 4;
-        float s = 0.0f;
-        for (int q0 = 0; q0 < n4; q0 += 8) {
-            float4 b[8];
+    // the ordered walk, kGroupWalk events per batch: every 16-byte read of a
+    // batch issued before its first add (the zero pad completes the last
+    // batch; +0 leaves s unchanged: s >= +0)
+    const float4 *e4 = reinterpret_cast<const float4 *>(evl);
+    const int n4 = (nev + 3) >> 2;
+    float s = 0.0f;
+    int q0 = 0;
+    do {
+        float4 b[kGroupWalk / 4];
 #pragma unroll
-            for (int q = 0; q < 8; ++q) b[q] = e4[q0 + q < n4 ? q0 + q : n4 - 1];
-            __builtin_amdgcn_sched_barrier(0);
+        for (int q = 0; q < kGroupWalk / 4; ++q) b[q] = e4[q0 + q];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int g = 0; g < 2; ++g) {
-                if (q0 + 4 * g < n4) {
-#pragma unroll
-                    for (int q = 4 * g; q < 4 * g + 4; ++q) {
-                        s += b[q].x;
-                        s += b[q].y;
-                        s += b[q].z;
-                        s += b[q].w;
-                    }
-                }
-            }
+        for (int q = 0; q < kGroupWalk / 4; ++q) {
+            s += b[q].x;
+            s += b[q].y;
+            s += b[q].z;
+            s += b[q].w;
         }
-        if (lane == 0) x.result = s;
-    }
-    sync();
-    return x.result;
+        q0 += kGroupWalk / 4;
+    } while (q0 < n4);
+    return s;
 }
 
 #endif  // __HIPCC__

@@ -517,23 +517,18 @@ constexpr size_t geglu_f32_lds() { return (NB * 40 + 15) / 16 * 16 + (size_t)2 *
 // after all terms are stored (a fold pipelined with the stream through
 // per-iteration counters, and x quantised by the compute waves themselves,
 // each measured slower: 8.5 and 8.7 against 7.9 us).
-template <int NB, int W>
-__global__ __launch_bounds__(64 * (W + kNQ)) void gemv_q4_0_geglu_split_kernel(
-    const uint8_t *__restrict__ wg, const uint8_t *__restrict__ wu, const float *__restrict__ x,
-    float *__restrict__ act, uint8_t *__restrict__ act_pack, int rows)
+// The compute waves of the split GeGLU (waves NS.. of the workgroup): issue
+// the rows' weight loads after the staging waves' barrier, fold against the
+// pack the staging waves write to lds, and emit act and the pack block
+// blockIdx.x.  The staging waves take the same four barriers (one s_barrier
+// after their loads are issued, then three __syncthreads) and leave.
+template <int NB, int W, int NS>
+__device__ __forceinline__ void geglu_split_compute(const uint8_t *__restrict__ wg, const uint8_t *__restrict__ wu,
+                                                    float *__restrict__ act, uint8_t *__restrict__ act_pack, int rows,
+                                                    uint8_t *lds, float *T, int wave)
 {
-    constexpr int NS = kNQ, ITERS = (NB + 15) / 16, R = 4 * W, E = R - 32;
+    constexpr int ITERS = (NB + 15) / 16, R = 4 * W, E = R - 32;
     static_assert(R <= 64 && E > 0, "one fold lane per row, a tail share per workgroup");
-    extern __shared__ __align__(16) uint8_t lds[];
-    float *T = reinterpret_cast<float *>(lds + (NB * 40 + 15) / 16 * 16);
-    const int wave = threadIdx.x >> 6;
-    if (wave < NS) {
-        quantize_into_lds<NB, kNQ>(x, lds, wave);
-        __syncthreads();  // the pack is whole
-        __syncthreads();  // every term is stored
-        __syncthreads();  // the up sums are shared
-        return;
-    }
     const int G = gridDim.x;
     auto row_of = [&](int rl) { return rl < 32 ? 32 * (int)blockIdx.x + rl : 32 * G + E * (int)blockIdx.x + rl - 32; };
     const int lane = threadIdx.x & 63, j = lane & 15;
@@ -541,7 +536,7 @@ __global__ __launch_bounds__(64 * (W + kNQ)) void gemv_q4_0_geglu_split_kernel(
     const int row = row_of(rl);
     const size_t nblk = (size_t)rows * NB, base = (size_t)row * NB;
     RowRegs<ITERS> rg, ru;
-    __builtin_amdgcn_s_barrier();  // x's loads are issued
+    __builtin_amdgcn_s_barrier();  // the staging waves' loads are issued
     load_row<ITERS>(rg, wg, nblk, base, NB, j);
     load_row<ITERS>(ru, wu, nblk, base, NB, j);
     __syncthreads();
@@ -570,6 +565,24 @@ __global__ __launch_bounds__(64 * (W + kNQ)) void gemv_q4_0_geglu_split_kernel(
             reinterpret_cast<int32_t *>(act_pack + (size_t)nbo * 36)[blk] = qs;
         }
     }
+}
+
+template <int NB, int W>
+__global__ __launch_bounds__(64 * (W + kNQ)) void gemv_q4_0_geglu_split_kernel(
+    const uint8_t *__restrict__ wg, const uint8_t *__restrict__ wu, const float *__restrict__ x,
+    float *__restrict__ act, uint8_t *__restrict__ act_pack, int rows)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    float *T = reinterpret_cast<float *>(lds + (NB * 40 + 15) / 16 * 16);
+    const int wave = threadIdx.x >> 6;
+    if (wave < kNQ) {
+        quantize_into_lds<NB, kNQ>(x, lds, wave);  // takes the first barrier
+        __syncthreads();  // the pack is whole
+        __syncthreads();  // every term is stored
+        __syncthreads();  // the up sums are shared
+        return;
+    }
+    geglu_split_compute<NB, W, kNQ>(wg, wu, act, act_pack, rows, lds, T, wave);
 }
 
 // ---- the Gemma-2 sandwich residual ahead of the rows ---------------------------
@@ -768,6 +781,43 @@ __global__ __launch_bounds__(64 * kGegluResWaves) void gemv_q4_0_geglu_resnorm_k
 
 template <int NB>
 constexpr size_t geglu_resnorm_lds() { return rn2_area_off<NB>() + rn2_area_bytes<NB>(128); }
+
+// The split GeGLU with the post-attention residual ahead (the decode step's
+// FFN): its kNQ staging waves form h_out = h_in + rms_norm(t, w_post) and
+// the split pack of rms_norm(h_out, w_norm) (group_residual_norm, the same
+// bits in every workgroup, workgroup 0 stores h_out) while the compute
+// waves' weight loads stream; the rows, the fold and the emitted pack blocks
+// are gemv_q4_0_geglu_split_kernel's.  LDS: the rn2 layout, its last area
+// holding the norm's values and events, then the terms.
+static_assert(kNQ == kNormWaves, "the staging waves are the norm group");
+template <int NB, int W, bool FAST>
+__global__ __launch_bounds__(64 * (W + kNQ)) void gemv_q4_0_geglu_resnorm_split_kernel(
+    const uint8_t *__restrict__ wg, const uint8_t *__restrict__ wu, const float *__restrict__ t,
+    const float *__restrict__ w_post, const float *h_in, float *h_out, const float *__restrict__ w_norm, float eps,
+    float *__restrict__ act, uint8_t *__restrict__ act_pack, int rows)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint8_t *lds_group = lds + rn2_group_off<NB>();
+    float *area = reinterpret_cast<float *>(lds + rn2_area_off<NB>());
+    const int wave = threadIdx.x >> 6;
+    if (wave < kNQ) {
+        const int polls = mrml_xsum::wait_polls();
+        GroupNormOps<NB> ops;
+        group_norm_load<NB>(ops, t, w_post, h_in, w_norm, wave);
+        if (threadIdx.x == 0) *reinterpret_cast<uint32_t *>(lds_group + sizeof(mrml_xsum::GroupShared)) = 0u;
+        mrml_xsum::lds_barrier();  // the operands' loads are issued, the sync counter is zero
+        group_residual_norm<NB, FAST>(ops, w_post != nullptr, w_norm != nullptr, blockIdx.x == 0 ? h_out : nullptr,
+                                      eps, lds, lds_group, area, wave, polls);
+        __syncthreads();  // the pack is whole
+        __syncthreads();  // every term is stored
+        __syncthreads();  // the up sums are shared
+        return;
+    }
+    geglu_split_compute<NB, W, kNQ>(wg, wu, act, act_pack, rows, lds, area, wave);
+}
+
+template <int NB, int W>
+constexpr size_t geglu_resnorm_split_lds() { return rn2_area_off<NB>() + rn2_area_bytes<NB>(8 * W); }
 
 
 // The stacked q|k|v matvec, the post-FFN residual of the previous block and
@@ -1522,6 +1572,28 @@ int launch_geglu_split(mrml_hip_ctx *ctx, const void *wg, const void *wu, const 
                            (const uint8_t *)wg, (const uint8_t *)wu, x, act, (uint8_t *)pack, rows);
     });
     return check_launch(ctx, "gemv_q4_0_geglu_split_kernel");
+}
+
+int launch_geglu_resnorm_split(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *t,
+                               const float *w_post, const float *h_in, float *h_out, const float *w_norm, float eps,
+                               float *act, void *pack, int32_t rows, int32_t cols, bool fast)
+{
+    if (!ffn_split_ok(cols, rows) || h_in == h_out)
+        return fail(ctx, MRML_HIP_E_UNSUPPORTED, "geglu_resnorm_split: no instance for %dx%d (or h_in == h_out)", rows,
+                    cols);
+    MRML_FOLD16_NB(cols / 32, {
+        if (fast)
+            hipLaunchKernelGGL((gemv_q4_0_geglu_resnorm_split_kernel<NB, kSplitW, true>), dim3(split_main_blocks(rows)),
+                               dim3(64 * (kSplitW + kNQ)), (geglu_resnorm_split_lds<NB, kSplitW>()), ctx->stream,
+                               (const uint8_t *)wg, (const uint8_t *)wu, t, w_post, h_in, h_out, w_norm, eps, act,
+                               (uint8_t *)pack, rows);
+        else
+            hipLaunchKernelGGL((gemv_q4_0_geglu_resnorm_split_kernel<NB, kSplitW, false>),
+                               dim3(split_main_blocks(rows)), dim3(64 * (kSplitW + kNQ)),
+                               (geglu_resnorm_split_lds<NB, kSplitW>()), ctx->stream, (const uint8_t *)wg,
+                               (const uint8_t *)wu, t, w_post, h_in, h_out, w_norm, eps, act, (uint8_t *)pack, rows);
+    });
+    return check_launch(ctx, "gemv_q4_0_geglu_resnorm_split_kernel");
 }
 
 int launch_down_mix(mrml_hip_ctx *ctx, const void *wd, const void *pack, const float *act, float *y, int32_t rows,

@@ -56,6 +56,12 @@ int launch_ffn_split(mrml_hip_ctx *ctx, const void *wg, const void *wu, const vo
 int split_main_blocks(int ffn);
 int launch_geglu_split(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *x, float *act, void *pack,
                        int32_t rows, int32_t cols);
+// The split GeGLU with the post-attention sandwich residual fused ahead
+// (h_out = h_in + rms_norm(t, w_post), then rms_norm(h_out, w_norm) as its
+// input): act and the pack blocks launch_geglu_split writes.
+int launch_geglu_resnorm_split(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *t,
+                               const float *w_post, const float *h_in, float *h_out, const float *w_norm, float eps,
+                               float *act, void *pack, int32_t rows, int32_t cols, bool fast);
 int launch_down_mix(mrml_hip_ctx *ctx, const void *wd, const void *pack, const float *act, float *y, int32_t rows,
                     int32_t cols);
 int launch_gemv_q4_0_x(mrml_hip_ctx *ctx, const void *w, const float *x, float *y, int32_t rows, int32_t cols);

@@ -514,6 +514,7 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
     // alternates between two buffers (A -> B -> A per block) and ends in A.
     const bool fused = resnorm_shape(c.dim) && c.ffn_dim % 64 == 0;
     const bool fast = c.numerics == MRML_HIP_NUMERICS_FAST;
+    const bool split_ffn = ffn_split_ok(c.dim, c.ffn_dim);
     float *hA = m->h, *hB = m->h2;
     STEP(launch_embedding(ctx, m->tok_embd, c.tie_type, d_token, 0, sqrtf((float)c.dim), hA,
                           m->layers[0].attn_norm, c.eps, nullptr, m->xpack, c.dim, c.vocab));
@@ -541,7 +542,12 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
                                         c.n_kv_heads, c.attn_scale, c.ctx_len, m->attn_part, layer_window(c, l)));
         }
         STEP(launch_gemv_q4_0(ctx, L.wo, m->attn_pack, m->o, c.dim, qd, fast));
-        if (fused) {
+        if (fused && split_ffn) {
+            // the balanced split form: the GeGLU writes act and the pack blocks
+            // it holds whole, the down projection quantises the rest from act
+            STEP(launch_geglu_resnorm_split(ctx, L.w_gate, L.w_up, m->o, L.post_attn_norm, hA, hB, L.ffn_norm, c.eps,
+                                            m->act, m->act_pack, c.ffn_dim, c.dim, fast));
+        } else if (fused) {
             STEP(launch_geglu_resnorm(ctx, L.w_gate, L.w_up, m->o, L.post_attn_norm, hA, hB, L.ffn_norm, c.eps,
                                       m->act_pack, c.ffn_dim, c.dim, fast));
         } else {
@@ -550,7 +556,10 @@ int mrml_hip_gemma2_step(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, int32_t *d_state
             STEP(launch_gemv_q4_0_geglu_emit(ctx, L.w_gate, L.w_up, m->xpack, m->act, m->act_pack, c.ffn_dim,
                                              c.dim));
         }
-        STEP(launch_gemv_q4_0(ctx, L.w_down, m->act_pack, m->f, c.dim, c.ffn_dim, fast));
+        if (fused && split_ffn)
+            STEP(launch_down_mix(ctx, L.w_down, m->act_pack, m->act, m->f, c.dim, c.ffn_dim));
+        else
+            STEP(launch_gemv_q4_0(ctx, L.w_down, m->act_pack, m->f, c.dim, c.ffn_dim, fast));
         if (!fused)
             STEP(launch_residual_rms_norm(ctx, m->f, L.post_ffw_norm, hA, hA, next_norm, c.eps, nullptr, m->xpack,
                                           c.dim, 1, fast));
