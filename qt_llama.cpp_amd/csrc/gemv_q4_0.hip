@@ -518,14 +518,19 @@ constexpr size_t geglu_f32_lds() { return (NB * 40 + 15) / 16 * 16 + (size_t)2 *
 // per-iteration counters, and x quantised by the compute waves themselves,
 // each measured slower: 8.5 and 8.7 against 7.9 us).
 // The compute waves of the split GeGLU (waves NS.. of the workgroup): issue
-// the rows' weight loads after the staging waves' barrier, fold against the
-// pack the staging waves write to lds, and emit act and the pack block
-// blockIdx.x.  The staging waves take the same four barriers (one s_barrier
-// after their loads are issued, then three __syncthreads) and leave.
-template <int NB, int W, int NS>
+// the rows' weight loads after the staging waves' barrier, run hook (the
+// compute waves' share of staging the pack, with the barriers it takes),
+// fold against the pack in lds, and emit act and the pack block blockIdx.x.
+// The staging waves take the same barriers (one s_barrier after their loads
+// are issued, hook's, then three __syncthreads) and leave.
+struct NoHook {
+    __device__ __forceinline__ void operator()() const {}
+};
+
+template <int NB, int W, int NS, class Hook = NoHook>
 __device__ __forceinline__ void geglu_split_compute(const uint8_t *__restrict__ wg, const uint8_t *__restrict__ wu,
                                                     float *__restrict__ act, uint8_t *__restrict__ act_pack, int rows,
-                                                    uint8_t *lds, float *T, int wave)
+                                                    uint8_t *lds, float *T, int wave, Hook hook = Hook())
 {
     constexpr int ITERS = (NB + 15) / 16, R = 4 * W, E = R - 32;
     static_assert(R <= 64 && E > 0, "one fold lane per row, a tail share per workgroup");
@@ -539,6 +544,7 @@ __device__ __forceinline__ void geglu_split_compute(const uint8_t *__restrict__ 
     __builtin_amdgcn_s_barrier();  // the staging waves' loads are issued
     load_row<ITERS>(rg, wg, nblk, base, NB, j);
     load_row<ITERS>(ru, wu, nblk, base, NB, j);
+    hook();  // work of the waves that also take part in staging the pack
     __syncthreads();
     store_terms2_pre<NB, ITERS>(rg, ru, lds, base, j, T, rl, R + rl);
     __syncthreads();
@@ -625,8 +631,8 @@ constexpr int kGegluResWaves = 16;
 // consecutive values k = KN*(64w + l) + i.
 constexpr int kNormWaves = 4;
 
-template <int NB>
-constexpr int norm_kn() { return (NB * 32 + 64 * kNormWaves - 1) / (64 * kNormWaves); }
+template <int NB, int NW = kNormWaves>
+constexpr int norm_kn() { return (NB * 32 + 64 * NW - 1) / (64 * NW); }
 
 // LDS: pack | GroupShared | sync counter | xn (dim floats) + events (dim + pad),
 // the term chains reusing that last area once the pack is whole.
@@ -646,17 +652,17 @@ constexpr size_t rn2_area_bytes(int chains)
 // w_norm.  Loaded unconditionally (a missing weight reads t and is replaced
 // by 1 in the norm) so that all of them are issued at once, before the
 // workgroup barrier that lets the other waves issue their weight loads.
-template <int NB>
+template <int NB, int NW = kNormWaves>
 struct GroupNormOps {
-    float t[norm_kn<NB>()], h[norm_kn<NB>()], p[norm_kn<NB>()], n[norm_kn<NB>()];
+    float t[norm_kn<NB, NW>()], h[norm_kn<NB, NW>()], p[norm_kn<NB, NW>()], n[norm_kn<NB, NW>()];
 };
 
-template <int NB>
-__device__ __forceinline__ void group_norm_load(GroupNormOps<NB> &o, const float *__restrict__ t,
+template <int NB, int NW = kNormWaves>
+__device__ __forceinline__ void group_norm_load(GroupNormOps<NB, NW> &o, const float *__restrict__ t,
                                                 const float *__restrict__ w_post, const float *h_in,
                                                 const float *__restrict__ w_norm, int wave)
 {
-    constexpr int DIM = NB * 32, KN = norm_kn<NB>();
+    constexpr int DIM = NB * 32, KN = norm_kn<NB, NW>();
     const int k0 = KN * (64 * wave + (threadIdx.x & 63));
     const float *pp = w_post ? w_post : t, *pn = w_norm ? w_norm : t;
 #pragma unroll
@@ -670,20 +676,23 @@ __device__ __forceinline__ void group_norm_load(GroupNormOps<NB> &o, const float
 }
 
 // The residual norm of the group: h_out = h_in + rms_norm(t, w_post) (stored
-// when h_out is set), the split pack of rms_norm(h_out, w_norm) at pack.
-// Called by the kNormWaves group waves only.
+// when h_out is set), rms_norm(h_out, w_norm) to area[0, dim) and (EMIT) its
+// split pack at pack.  Called by the NW group waves only (group wave index
+// `wave`).  Without EMIT the caller publishes area with a workgroup barrier
+// and emits the pack itself.
 // FAST (the decode step's tolerance path): both sums are deterministic tree
 // sums (exact_sum.h's group_tree_sum) instead of the sequential-order ones.
-template <int NB, bool FAST = false>
-__device__ __forceinline__ void group_residual_norm(GroupNormOps<NB> &o, bool has_post, bool has_norm, float *h_out,
-                                                    float eps, uint8_t *pack, uint8_t *lds_group, float *area,
-                                                    int wave, int polls)
+template <int NB, bool FAST = false, int NW = kNormWaves, bool EMIT = true>
+__device__ __forceinline__ void group_residual_norm(GroupNormOps<NB, NW> &o, bool has_post, bool has_norm,
+                                                    float *h_out, float eps, uint8_t *pack, uint8_t *lds_group,
+                                                    float *area, int wave, int polls)
 {
-    constexpr int DIM = NB * 32, KN = norm_kn<NB>(), N4 = DIM / 4;
+    static_assert(NW <= 8, "group tree sums hold 8 wave totals per slot");
+    constexpr int DIM = NB * 32, KN = norm_kn<NB, NW>(), N4 = DIM / 4;
     const int lane = threadIdx.x & 63, k0 = KN * (64 * wave + lane);
     auto *gs = reinterpret_cast<mrml_xsum::GroupShared *>(lds_group);
     mrml_xsum::GroupSync sync{reinterpret_cast<uint32_t *>(lds_group + sizeof(mrml_xsum::GroupShared)), 0u,
-                              (uint32_t)kNormWaves, polls};
+                              (uint32_t)NW, polls};
     float sq[KN];
 #pragma unroll
     for (int i = 0; i < KN; ++i) sq[i] = o.t[i] * o.t[i];
@@ -714,13 +723,15 @@ __device__ __forceinline__ void group_residual_norm(GroupNormOps<NB> &o, bool ha
         if (has_norm) v = v * o.n[i];
         if (k0 + i < DIM) xn[k0 + i] = v;
     }
-    sync();
-    // Q8_0 blocks: 8 consecutive lanes per block, chunk c = 64w + l + 256m
-    const float4 *x4 = reinterpret_cast<const float4 *>(xn);
+    if constexpr (EMIT) {
+        sync();
+        // Q8_0 blocks: 8 consecutive lanes per block, chunk c = 64w + l + 64*NW*m
+        const float4 *x4 = reinterpret_cast<const float4 *>(xn);
 #pragma unroll
-    for (int m = 0; m < (N4 + 64 * kNormWaves - 1) / (64 * kNormWaves); ++m) {
-        const int c = 64 * wave + lane + 64 * kNormWaves * m;
-        emit_q8<true>(x4[c < N4 ? c : N4 - 1], c, N4, pack, NB);
+        for (int m = 0; m < (N4 + 64 * NW - 1) / (64 * NW); ++m) {
+            const int c = 64 * wave + lane + 64 * NW * m;
+            emit_q8<true>(x4[c < N4 ? c : N4 - 1], c, N4, pack, NB);
+        }
     }
 }
 
@@ -783,37 +794,56 @@ template <int NB>
 constexpr size_t geglu_resnorm_lds() { return rn2_area_off<NB>() + rn2_area_bytes<NB>(128); }
 
 // The split GeGLU with the post-attention residual ahead (the decode step's
-// FFN): its kNQ staging waves form h_out = h_in + rms_norm(t, w_post) and
-// the split pack of rms_norm(h_out, w_norm) (group_residual_norm, the same
-// bits in every workgroup, workgroup 0 stores h_out) while the compute
-// waves' weight loads stream; the rows, the fold and the emitted pack blocks
-// are gemv_q4_0_geglu_split_kernel's.  LDS: the rn2 layout, its last area
-// holding the norm's values and events, then the terms.
-static_assert(kNQ == kNormWaves, "the staging waves are the norm group");
+// FFN): h_out = h_in + rms_norm(t, w_post) and the split pack of
+// rms_norm(h_out, w_norm) (group_residual_norm: the same bits in every
+// workgroup, workgroup 0 stores h_out) form while the weights stream; the
+// rows, the fold and the emitted pack blocks are gemv_q4_0_geglu_split_kernel's.
+// The norm's two sums run in the kResSplitNW = kNQ staging waves (a group of
+// 8 with four compute waves measured slower: a compute wave first issues its
+// weight loads into the full memory pipeline, and the group's syncs wait for
+// it); every wave of the first NB*8/64 then quantises one 4-value chunk of
+// the normalised vector (three chunks per lane in the group alone took
+// 1.8 us, one chunk in nine waves 0.5 us).
+// LDS: the rn2 layout, its last area holding the normalised vector and the
+// events, then the terms.
+constexpr int kResSplitNW = kNQ;
+static_assert(kNQ == kNormWaves, "the staging waves lead the group");
 template <int NB, int W, bool FAST>
 __global__ __launch_bounds__(64 * (W + kNQ)) void gemv_q4_0_geglu_resnorm_split_kernel(
     const uint8_t *__restrict__ wg, const uint8_t *__restrict__ wu, const float *__restrict__ t,
     const float *__restrict__ w_post, const float *h_in, float *h_out, const float *__restrict__ w_norm, float eps,
     float *__restrict__ act, uint8_t *__restrict__ act_pack, int rows)
 {
+    constexpr int NW = kResSplitNW, N4 = NB * 8;
+    static_assert(NW <= kNQ + W && N4 % 64 == 0 && N4 <= 64 * (W + kNQ), "group waves; whole waves of chunks");
     extern __shared__ __align__(16) uint8_t lds[];
     uint8_t *lds_group = lds + rn2_group_off<NB>();
     float *area = reinterpret_cast<float *>(lds + rn2_area_off<NB>());
     const int wave = threadIdx.x >> 6;
+    const bool in_group = wave < NW;
+    const int polls = mrml_xsum::wait_polls();
+    GroupNormOps<NB, NW> ops;
+    if (in_group) group_norm_load<NB, NW>(ops, t, w_post, h_in, w_norm, wave);
+    if (threadIdx.x == 0) *reinterpret_cast<uint32_t *>(lds_group + sizeof(mrml_xsum::GroupShared)) = 0u;
+    // the norm's operand loads are issued and the sync counter is zero
+    // before any weight load (the compute part's first barrier is this one)
+    auto norm_and_emit = [&]() {
+        if (in_group)
+            group_residual_norm<NB, FAST, NW, false>(ops, w_post != nullptr, w_norm != nullptr,
+                                                     blockIdx.x == 0 ? h_out : nullptr, eps, lds, lds_group, area,
+                                                     wave, polls);
+        __syncthreads();  // the normalised vector is in area
+        if (wave < N4 / 64) emit_q8<true>(reinterpret_cast<const float4 *>(area)[threadIdx.x], threadIdx.x, N4, lds, NB);
+    };
     if (wave < kNQ) {
-        const int polls = mrml_xsum::wait_polls();
-        GroupNormOps<NB> ops;
-        group_norm_load<NB>(ops, t, w_post, h_in, w_norm, wave);
-        if (threadIdx.x == 0) *reinterpret_cast<uint32_t *>(lds_group + sizeof(mrml_xsum::GroupShared)) = 0u;
-        mrml_xsum::lds_barrier();  // the operands' loads are issued, the sync counter is zero
-        group_residual_norm<NB, FAST>(ops, w_post != nullptr, w_norm != nullptr, blockIdx.x == 0 ? h_out : nullptr,
-                                      eps, lds, lds_group, area, wave, polls);
+        mrml_xsum::lds_barrier();
+        norm_and_emit();
         __syncthreads();  // the pack is whole
         __syncthreads();  // every term is stored
         __syncthreads();  // the up sums are shared
         return;
     }
-    geglu_split_compute<NB, W, kNQ>(wg, wu, act, act_pack, rows, lds, area, wave);
+    geglu_split_compute<NB, W, kNQ>(wg, wu, act, act_pack, rows, lds, area, wave, norm_and_emit);
 }
 
 template <int NB, int W>
