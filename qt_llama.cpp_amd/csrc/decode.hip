@@ -755,22 +755,32 @@ __global__ __launch_bounds__(kScoreT) void attn_scores2_kernel(const float *__re
     // becomes a plain multiply), so q * f16 k maps to one v_fma_mix_f32
     float nz;
     asm volatile("v_mov_b32 %0, 0x80000000" : "=v"(nz));
+    // 32 dims per step; the next step's K and q reads are issued before
+    // this step's 32 dependent adds (double-buffered registers), so the
+    // chain does not stop for an LDS round trip at every step
     float dot = -0.0f;
-    for (int d0 = 0; d0 < HD / 8; d0 += 4) {
-        u32x4 kw[4];
-        float4 qa[8];
+    constexpr int kSteps = HD / 32;
+    u32x4 kw[2][4];
+    float4 qa[2][8];
+    auto fetch = [&](int st, int b) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            kw[u] = krow[d0 + u];
-            qa[2 * u] = qg[2 * (d0 + u)];
-            qa[2 * u + 1] = qg[2 * (d0 + u) + 1];
+            kw[b][u] = krow[4 * st + u];
+            qa[b][2 * u] = qg[2 * (4 * st + u)];
+            qa[b][2 * u + 1] = qg[2 * (4 * st + u) + 1];
         }
+    };
+    fetch(0, 0);
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) {
+        const int b = st & 1;
+        if (st + 1 < kSteps) fetch(st + 1, b ^ 1);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const u32x4 wv = kw[u];
+            const u32x4 wv = kw[b][u];
             const uint32_t w[4] = {wv.x, wv.y, wv.z, wv.w};
-            const float qv[8] = {qa[2 * u].x, qa[2 * u].y, qa[2 * u].z, qa[2 * u].w,
-                                 qa[2 * u + 1].x, qa[2 * u + 1].y, qa[2 * u + 1].z, qa[2 * u + 1].w};
+            const float qv[8] = {qa[b][2 * u].x, qa[b][2 * u].y, qa[b][2 * u].z, qa[b][2 * u].w,
+                                 qa[b][2 * u + 1].x, qa[b][2 * u + 1].y, qa[b][2 * u + 1].z, qa[b][2 * u + 1].w};
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const _Float16 kh = __builtin_bit_cast(_Float16, (uint16_t)(w[e >> 1] >> (16 * (e & 1))));
