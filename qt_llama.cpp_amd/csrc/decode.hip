@@ -1721,8 +1721,9 @@ int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *q, int q_stride, const 
                            q_stride);
         if (int rc = check_launch(ctx, "attn_scores_kernel")) return rc;
     }
-    // the rows form where its dynamic LDS stays within 60 KiB (no launch
-    // here asks for more than the default 64 KiB a workgroup)
+    // the rows form where its dynamic LDS stays within 60 KiB; with the
+    // kernel's static LDS (mrml_xsum::Shared, red, exp_tab: about 8.6 KB)
+    // a launch takes up to about 69 KB, within gfx950's 160 KiB a workgroup
     if (span <= kRowsSvMax && n_heads / n_kv_heads <= kRowsSvG &&
         rows_sv_lds(n_heads / n_kv_heads, span) <= (size_t)60 << 10) {
         hipLaunchKernelGGL(attn_softmax_v_rows_kernel, dim3(n_kv_heads, rows), dim3(kAttnHD),

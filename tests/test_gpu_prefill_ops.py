@@ -254,7 +254,41 @@ def window_rows(n_past, sw, cap):
 PREFILL_CASES = [(0, 16, None, 16, 8, 4, True), (128, 37, None, 512, 8, 4, True), (200, 40, 24, 256, 8, 4, True),
                  (300, 9, 64, 64, 8, 4, False), (700, 64, None, 2048, 8, 8, False), (20, 7, 5, 32, 16, 2, True),
                  (6000, 3, None, 8192, 8, 4, False), (100, 40, None, 65536, 8, 4, True),
-                 (3000, 20, None, 4096, 8, 4, True), (3900, 9, None, 4096, 16, 4, False)]
+                 (3000, 20, None, 4096, 8, 4, True), (3900, 9, None, 4096, 16, 4, False),
+                 # the rows form at groups of 4 and 3 (spans ~2000-4000)
+                 (1990, 10, None, 4096, 16, 4, False), (3290, 10, None, 4096, 16, 4, True),
+                 (2490, 12, None, 4096, 12, 4, False), (3990, 6, None, 4096, 12, 4, True)]
+
+
+def prefill_span(cache_start, batch, sw, cap):
+    """The widest row window of a launch (launch_attn_rows_f16's span)."""
+    wlimit = sw if sw is not None and 0 < sw < cap else cap
+    return min(wlimit, cache_start + batch)
+
+
+def rows_form(nh, nkv, span):
+    """Whether attention_prefill runs attn_softmax_v_rows_kernel (the form
+    whose workgroup serves a kv head's whole group) rather than the
+    per-head attn_softmax_v_kernel: windows up to 4096, groups up to 4, and
+    the group's weights plus span flag bytes within 60 KiB of dynamic LDS
+    (launch_attn_rows_f16 in decode.hip)."""
+    g = nh // nkv
+    return span <= 4096 and g <= 4 and g * span * 4 + ((span + 15) & ~15) <= 60 << 10
+
+
+def test_prefill_cases_cover_both_forms():
+    """The case list reaches the rows form at every group size it serves
+    (1, 2, 3, 4) and the per-head form too, so no group size is covered
+    only by a silent fallback."""
+    forms = {}
+    for start, batch, sw, cap, nh, nkv, _ in PREFILL_CASES:
+        forms.setdefault((nh // nkv, rows_form(nh, nkv, prefill_span(start, batch, sw, cap))), []).append(start)
+    for g in (1, 2, 3, 4):
+        assert (g, True) in forms, f"no attention_prefill case takes the rows form at group {g}"
+    assert any(not rows for _, rows in forms), "no case takes the per-head form"
+    # the two group-of-4 and group-of-3 cases above are rows-form cases
+    for start, batch, sw, cap, nh, nkv, _ in PREFILL_CASES[-4:]:
+        assert rows_form(nh, nkv, prefill_span(start, batch, sw, cap))
 
 
 @pytest.mark.parametrize("cache_start,batch,sw,cap,nh,nkv,stacked", PREFILL_CASES)
@@ -268,8 +302,9 @@ def test_attention_prefill_bit_exact(backend, dev, orc, cache_start, batch, sw, 
     vc = rng.standard_normal(cap * kvd).astype(np.float16).view(np.uint16)
     qb, kb, vb = (backend.HipBuffer.from_host(dev, a) for a in (q, kc, vc))
     out = backend.HipBuffer.alloc(dev, batch * qd)
-    print(f"\n[attention_prefill] start {cache_start} batch {batch} window {sw} capacity {cap} heads {nh}/{nkv}",
-          flush=True)
+    form = "rows" if rows_form(nh, nkv, prefill_span(cache_start, batch, sw, cap)) else "per-head"
+    print(f"\n[attention_prefill] start {cache_start} batch {batch} window {sw} capacity {cap} heads {nh}/{nkv} "
+          f"({form} form)", flush=True)
     dev.attention_prefill(qb, kb, vb, out, cache_start, batch, nh, nkv, hd, 1.0 / 16.0, sw, cap)
     dev.sync()
     got = out.numpy().reshape(batch, qd)
