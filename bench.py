@@ -357,13 +357,15 @@ def prefill_profile(be, synth, dev, n_prefill: int) -> dict:
     return {"profile_prefill": n_prefill, "first_token": int(am.numpy()[0])}
 
 
-def decode_profile(be, synth, dev, n_prefill: int, n_steps: int, numerics: int = 0, prefilled: bool = False) -> dict:
+def decode_profile(be, synth, dev, n_prefill: int, n_steps: int, numerics: int = 0, prefilled: bool = False,
+                   graph: bool = False) -> dict:
     """Profiling aid for the C4 model: n_prefill + n_steps token steps issued
-    eagerly (no graph: the kernel trace then sees every launch); the last
-    n_steps are the decode steps at positions n_prefill..  With prefilled,
-    the prompt goes through one batched prefill call instead of token steps
-    (few dispatches: counter passes serialise every one).  Progress goes to
-    stderr every 64 steps."""
+    eagerly (the kernel trace then sees every launch as the host issues it)
+    or, with graph, as replays of the captured step (the bench's way); the
+    last n_steps are the decode steps at positions n_prefill..  With
+    prefilled, the prompt goes through one batched prefill call instead of
+    token steps (few dispatches: counter passes serialise every one).
+    Progress goes to stderr every 64 steps."""
     cfg = dict(synth.GEMMA2_2B)
     model = synth.gemma2_model(cfg, seed=1)
     m = be.Gemma2Model.from_host(dev, model, numerics=numerics)
@@ -382,14 +384,22 @@ def decode_profile(be, synth, dev, n_prefill: int, n_steps: int, numerics: int =
         dev.sync()
         state.copy_from_host(np.array([int(am.numpy()[0]), n_prefill], np.int32))
         first = n_prefill
+    g = dev.capture(lambda: m.step(state, kc, vc, hist=hist, hist_cap=total, prompt=pr,
+                                   prompt_len=n_prefill)) if graph else None
     for i in range(first, total):
-        m.step(state, kc, vc, hist=hist, hist_cap=total, prompt=pr, prompt_len=n_prefill)
+        if g is not None:
+            g.launch()
+        else:
+            m.step(state, kc, vc, hist=hist, hist_cap=total, prompt=pr, prompt_len=n_prefill)
         if i % 64 == 63:
             dev.sync()
             print(f"[profile-decode] step {i + 1}/{total}", file=sys.stderr, flush=True)
     dev.sync()
+    if g is not None:
+        g.close()
     m.close()
-    return {"profile_decode": n_steps, "prefill_tokens": n_prefill, "numerics": numerics, "prefilled": prefilled}
+    return {"profile_decode": n_steps, "prefill_tokens": n_prefill, "numerics": numerics, "prefilled": prefilled,
+            "graph": graph}
 
 
 def gemm_bench(be, synth, dev, ev, batch: int, cpu_tokens: int, profile: int = 0) -> dict:
@@ -448,7 +458,10 @@ def gemm_bench(be, synth, dev, ev, batch: int, cpu_tokens: int, profile: int = 0
     tq = time_graph(dev, ev, gq, 10) / 200
     gq.close()
     tops = total_ops / total_s / 1e12
-    out = {"tops": round(tops, 2), "unit": "TOPS (int8)", "mfma_util": round(tops / PEAK_INT8_TOPS, 4),
+    # achieved int8 TOPS over the dense peak; the matrix cores' busy fraction
+    # from SQ_VALU_MFMA_BUSY_CYCLES is in the committed PMC summary
+    out = {"tops": round(tops, 2), "unit": "TOPS (int8)", "tops_over_peak": round(tops / PEAK_INT8_TOPS, 4),
+           "mfma_busy": "profiles/gemm_q4_0_mfma_pmc.md (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs))",
            "peak_tops": PEAK_INT8_TOPS, "per_matrix": per, "batch": batch,
            "quantize_q8_0_us": round(tq * 1e6, 2), "kernel": "gemm_q4_0_mfma_kernel",
            "relaxed_fold": dict(relaxed, how="f32 activations in (quantisation included); the FAST numerics' prefill "
@@ -662,7 +675,7 @@ def main() -> int:
     ap.add_argument("--no-q4k", action="store_true", help="skip BASELINE configs[2] (Q4_K 256000x2304 + argmax)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-loop", type=int, default=0,
-                    help="only replay the GeGLU kernel graph this many times (for rocprofv3)")
+                    help="only replay the FFN step graph over the weight sets this many times (for rocprofv3)")
     ap.add_argument("--decode-prefill", type=int, default=512)
     ap.add_argument("--decode-tokens", type=int, default=256)
     ap.add_argument("--no-decode", action="store_true")
@@ -674,6 +687,8 @@ def main() -> int:
                     help="profiling aid: prefill, then N eager decode steps of the C4 model, then exit")
     ap.add_argument("--profile-prefilled", action="store_true",
                     help="with --profile-decode: the prompt through one batched prefill call")
+    ap.add_argument("--profile-graph", action="store_true",
+                    help="with --profile-decode: every step a replay of the captured step graph")
     ap.add_argument("--fast-numerics", action="store_true",
                     help="with --profile-decode: the FAST numerics (tree-order norm sums, split-K attention)")
     ap.add_argument("--profile-prefill", type=int, default=0,
@@ -699,7 +714,7 @@ def main() -> int:
     if args.profile_decode:
         print(json.dumps(decode_profile(be, synth, dev, args.decode_prefill, args.profile_decode,
                                         be.NUMERICS_FAST if args.fast_numerics else be.NUMERICS_EXACT,
-                                        args.profile_prefilled)))
+                                        args.profile_prefilled, args.profile_graph)))
         return 0
     if args.profile_lmhead:
         print(json.dumps(lmhead_profile(be, synth, dev, args.profile_lmhead)))
@@ -761,14 +776,13 @@ def main() -> int:
     q_pack = be.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(DIM), np.uint8)
     dev.quantize_q8_0(bx, None, q_pack, DIM)
     a_pack = be.HipBuffer.alloc(dev, dev.q8_0_pack_bytes(FFN), np.uint8)
-    g_geglu = dev.capture(lambda: [dev.ffn_split_geglu(pool[2 * i], pool[2 * i + 1], bx, act, a_pack, DIM, FFN)
-                                   for i in range(len(pool) // 2)])
 
     if args.profile_loop:
+        # the FFN step (GeGLU then down) over every weight set, N times
         for _ in range(args.profile_loop):
-            g_geglu.launch()
+            steps_graph(sets).launch()
         dev.sync()
-        print(json.dumps({"profile_loop": args.profile_loop, "launches": args.profile_loop * len(pool) // 2,
+        print(json.dumps({"profile_loop": args.profile_loop, "steps": args.profile_loop * sets,
                           "source_sha256_16": kernel_source_hash()}))
         return 0
 
@@ -858,7 +872,6 @@ def main() -> int:
     # release the FFN bench buffers before the other legs
     for g_ in graphs.values():
         g_.close()
-    g_geglu.close()
     del rot, first, pool, src, dst
     q8 = None if args.no_q8 else q8_0_bench(be, synth, dev, ev, 0 if args.no_cpu else args.cpu_seconds_small)
     q4k = None if args.no_q4k else q4_k_bench(be, synth, dev, ev, 0 if args.no_cpu else args.cpu_seconds_small)
