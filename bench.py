@@ -357,15 +357,14 @@ def prefill_profile(be, synth, dev, n_prefill: int) -> dict:
     return {"profile_prefill": n_prefill, "first_token": int(am.numpy()[0])}
 
 
-def decode_profile(be, synth, dev, n_prefill: int, n_steps: int, numerics: int = 0, prefilled: bool = False,
-                   graph: bool = False) -> dict:
+def decode_profile(be, synth, dev, n_prefill: int, n_steps: int, numerics: int = 0, prefilled: bool = False) -> dict:
     """Profiling aid for the C4 model: n_prefill + n_steps token steps issued
-    eagerly (the kernel trace then sees every launch as the host issues it)
-    or, with graph, as replays of the captured step (the bench's way); the
-    last n_steps are the decode steps at positions n_prefill..  With
-    prefilled, the prompt goes through one batched prefill call instead of
-    token steps (few dispatches: counter passes serialise every one).
-    Progress goes to stderr every 64 steps."""
+    eagerly (no graph: the kernel trace then sees every launch; rocprofv3's
+    kernel trace of many graph replays crashed in the runtime's graph-launch
+    path on this image); the last n_steps are the decode steps at positions
+    n_prefill..  With prefilled, the prompt goes through one batched prefill
+    call instead of token steps (few dispatches: counter passes serialise
+    every one).  Progress goes to stderr every 64 steps."""
     cfg = dict(synth.GEMMA2_2B)
     model = synth.gemma2_model(cfg, seed=1)
     m = be.Gemma2Model.from_host(dev, model, numerics=numerics)
@@ -384,22 +383,14 @@ def decode_profile(be, synth, dev, n_prefill: int, n_steps: int, numerics: int =
         dev.sync()
         state.copy_from_host(np.array([int(am.numpy()[0]), n_prefill], np.int32))
         first = n_prefill
-    g = dev.capture(lambda: m.step(state, kc, vc, hist=hist, hist_cap=total, prompt=pr,
-                                   prompt_len=n_prefill)) if graph else None
     for i in range(first, total):
-        if g is not None:
-            g.launch()
-        else:
-            m.step(state, kc, vc, hist=hist, hist_cap=total, prompt=pr, prompt_len=n_prefill)
+        m.step(state, kc, vc, hist=hist, hist_cap=total, prompt=pr, prompt_len=n_prefill)
         if i % 64 == 63:
             dev.sync()
             print(f"[profile-decode] step {i + 1}/{total}", file=sys.stderr, flush=True)
     dev.sync()
-    if g is not None:
-        g.close()
     m.close()
-    return {"profile_decode": n_steps, "prefill_tokens": n_prefill, "numerics": numerics, "prefilled": prefilled,
-            "graph": graph}
+    return {"profile_decode": n_steps, "prefill_tokens": n_prefill, "numerics": numerics, "prefilled": prefilled}
 
 
 def gemm_bench(be, synth, dev, ev, batch: int, cpu_tokens: int, profile: int = 0) -> dict:
@@ -687,8 +678,6 @@ def main() -> int:
                     help="profiling aid: prefill, then N eager decode steps of the C4 model, then exit")
     ap.add_argument("--profile-prefilled", action="store_true",
                     help="with --profile-decode: the prompt through one batched prefill call")
-    ap.add_argument("--profile-graph", action="store_true",
-                    help="with --profile-decode: every step a replay of the captured step graph")
     ap.add_argument("--fast-numerics", action="store_true",
                     help="with --profile-decode: the FAST numerics (tree-order norm sums, split-K attention)")
     ap.add_argument("--profile-prefill", type=int, default=0,
@@ -714,7 +703,7 @@ def main() -> int:
     if args.profile_decode:
         print(json.dumps(decode_profile(be, synth, dev, args.decode_prefill, args.profile_decode,
                                         be.NUMERICS_FAST if args.fast_numerics else be.NUMERICS_EXACT,
-                                        args.profile_prefilled, args.profile_graph)))
+                                        args.profile_prefilled)))
         return 0
     if args.profile_lmhead:
         print(json.dumps(lmhead_profile(be, synth, dev, args.profile_lmhead)))
