@@ -1111,19 +1111,36 @@ __device__ __forceinline__ void mix_tail_quantize(const float4 &v, uint8_t *lds,
     }
 }
 
-template <int NB, int S>
-__global__ __launch_bounds__(64 * (S + 2)) void gemv_q4_0_long_mix_kernel(const uint8_t *__restrict__ w,
-                                                                        const uint8_t *xpack,
-                                                                        const float *__restrict__ x,
-                                                                        float *__restrict__ y, int rows, int nmain)
+// Q row quads a workgroup (4Q row slots, the first rpw of them real rows
+// blockIdx.x*rpw ..; the other slots repeat the last real row, their loads
+// L2 hits, their sums never stored): Q = 1, rpw = 4 is the plain layout;
+// Q = 3, rpw = 9 puts the 2304 rows of the Gemma-2 down projection on
+// exactly 256 workgroups, one per CU (576 workgroups of 4 rows left 64 CUs
+// a third workgroup: rows 2048 take 5.04 us, 2304 take 5.84).  Quad q's S
+// compute waves write its terms to their own slice of T; the round counters
+// count every quad's waves; fold lane s folds slot s.
+template <int NB, int S, int Q>
+constexpr size_t long_mix_lds() { return long_t_off<NB, S>() + (size_t)Q * S * long_ipw<NB, S>() * 64 * sizeof(float); }
+
+template <int NB, int S, int Q>
+__global__ __launch_bounds__(64 * (Q * S + 2)) void gemv_q4_0_long_mix_kernel(const uint8_t *__restrict__ w,
+                                                                            const uint8_t *xpack,
+                                                                            const float *__restrict__ x,
+                                                                            float *__restrict__ y, int rows,
+                                                                            int nmain, int rpw)
 {
-    constexpr int ITERS = NB / 16, IPW = long_ipw<NB, S>();
+    constexpr int ITERS = NB / 16, IPW = long_ipw<NB, S>(), QT = S * IPW * 64;  // floats of T per quad
     static_assert(NB % 16 == 0 && NB <= kStageMax, "whole iterations; one staging batch");
-    static_assert(IPW <= 64, "one count per round");
+    static_assert(IPW <= 64 && 4 * Q <= 64, "one count per round; one fold lane per slot");
     extern __shared__ __align__(16) uint8_t lds[];
     uint32_t *flag = reinterpret_cast<uint32_t *>(lds + NB * 40);
     float *T = reinterpret_cast<float *>(lds + long_t_off<NB, S>());
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int row0 = (int)blockIdx.x * rpw;
+    auto row_of = [&](int slot) {  // slots past rpw repeat the last real row; rows past the matrix its last
+        const int r = row0 + (slot < rpw ? slot : rpw - 1);
+        return r < rows ? r : rows - 1;
+    };
     if (wave == 1) {
         float4 v;
         mix_tail_load<NB, S>(x, v, nmain, 0);
@@ -1137,12 +1154,12 @@ __global__ __launch_bounds__(64 * (S + 2)) void gemv_q4_0_long_mix_kernel(const 
         flag[lane] = 0u;  // zero before the issue barrier inside the staging
         stage_split_pack<true>(xpack, lds, NB, nmain);
         __syncthreads();  // the pack is whole
-        if (lane >= 4) return;
-        const float4 *tv = reinterpret_cast<const float4 *>(T) + lane * 4;
+        if (lane >= 4 * Q) return;
+        const float4 *tv = reinterpret_cast<const float4 *>(T + (lane >> 2) * QT) + (lane & 3) * 4;
         float acc = 0.0f;
 #pragma unroll 1
         for (int k = 0; k < IPW; ++k) {
-            const uint32_t want = (uint32_t)(ITERS - S * k < S ? ITERS - S * k : S);
+            const uint32_t want = (uint32_t)Q * (ITERS - S * k < S ? ITERS - S * k : S);  // waves with a live iteration
             mrml_xsum::bounded_wait(&flag[k], want, polls);
             asm volatile("" ::: "memory");
             float4 v[4 * S];
@@ -1158,16 +1175,15 @@ __global__ __launch_bounds__(64 * (S + 2)) void gemv_q4_0_long_mix_kernel(const 
                 }
             }
         }
-        const int out = blockIdx.x * 4 + lane;
-        if (out < rows) y[out] = acc;
+        const int out = row0 + lane;
+        if (lane < rpw && out < rows) y[out] = acc;
         return;
     }
-    const int sw = wave - 2, j = lane & 15, rsub = lane >> 4;
+    const int cw = wave - 2, qd = cw / S, sw = cw - qd * S, j = lane & 15, rsub = lane >> 4;
     float4 xv;
-    mix_tail_load<NB, S>(x, xv, nmain, sw + 1);  // before the weights: an L2 hit behind HBM misses waits
+    if (qd == 0) mix_tail_load<NB, S>(x, xv, nmain, sw + 1);  // before the weights: an L2 hit behind HBM misses waits
     __builtin_amdgcn_s_barrier();  // the pack's loads and the zeroed flags are in
-    const int row_raw = blockIdx.x * 4 + rsub;
-    const int row = row_raw < rows ? row_raw : rows - 1;  // tail rows recompute the last row
+    const int row = row_of(4 * qd + rsub);
     const size_t nblk = (size_t)rows * NB, base = (size_t)row * NB;
     const uint4 *qs = reinterpret_cast<const uint4 *>(w);
     const uint32_t *dw = reinterpret_cast<const uint32_t *>(w + nblk * 16);
@@ -1181,11 +1197,12 @@ __global__ __launch_bounds__(64 * (S + 2)) void gemv_q4_0_long_mix_kernel(const 
         wq[k] = load_stream16(qs + base + b);
         wd[k] = dw[(base + b) >> 1];
     }
-    mix_tail_quantize<NB, S>(xv, lds, nmain, sw + 1);
+    if (qd == 0) mix_tail_quantize<NB, S>(xv, lds, nmain, sw + 1);
     __syncthreads();
     const uint4 *aq = reinterpret_cast<const uint4 *>(lds);
     const float *ad = reinterpret_cast<const float *>(lds + NB * 32);
     const int32_t *ac = reinterpret_cast<const int32_t *>(lds + NB * 36);
+    float *Tq = T + qd * QT;
 #pragma unroll
     for (int k = 0; k < IPW; ++k) {
         const int it = sw + S * k;
@@ -1193,7 +1210,7 @@ __global__ __launch_bounds__(64 * (S + 2)) void gemv_q4_0_long_mix_kernel(const 
         const uint4 q = wq[k], lo = aq[2 * b], hi = aq[2 * b + 1];
         const int32_t isum = q4_0_isum_split(q.x, q.y, q.z, q.w, lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w, ac[b]);
         const uint32_t dbits = ((base + b) & 1) ? wd[k] >> 16 : wd[k] & 0xffffu;
-        T[((sw + S * k) * 4 + rsub) * 16 + j] = (float)isum * (f16_bits_to_f32(dbits) * ad[b]);
+        Tq[((sw + S * k) * 4 + rsub) * 16 + j] = (float)isum * (f16_bits_to_f32(dbits) * ad[b]);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the terms are in LDS before the count
         if (lane == 0 && it < ITERS)
             __hip_atomic_fetch_add(&flag[k], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -1434,6 +1451,7 @@ static int iters_round(int iters)
 constexpr int kFoldWaves = 4;   // fold16 compute waves per workgroup
 constexpr int kRelayS = 6;      // relay waves per 4 rows for 288-block rows (gate/up pairs)
 constexpr int kLongS = 3;       // compute waves per 4 rows of the long-row kernel
+constexpr int kCUs = 256;       // MI355X compute units: workgroup counts that divide among them evenly
 
 inline bool fold16_shape(int nb) { return nb == 64 || nb == 72; }
 inline bool relay_shape(int nb) { return nb == 288; }
@@ -1629,9 +1647,16 @@ int launch_geglu_resnorm_split(mrml_hip_ctx *ctx, const void *wg, const void *wu
 int launch_down_mix(mrml_hip_ctx *ctx, const void *wd, const void *pack, const float *act, float *y, int32_t rows,
                     int32_t cols)
 {
-    hipLaunchKernelGGL((gemv_q4_0_long_mix_kernel<288, kLongS>), dim3((rows + 3) / 4), dim3(64 * (kLongS + 2)),
-                       (long_lds<288, kLongS>()), ctx->stream, (const uint8_t *)wd, (const uint8_t *)pack, act, y, rows,
-                       split_main_blocks(cols));
+    if (rows % (9 * kCUs) == 0) {
+        // nine rows a workgroup (three quads): a whole number of workgroups per CU
+        hipLaunchKernelGGL((gemv_q4_0_long_mix_kernel<288, kLongS, 3>), dim3(rows / 9), dim3(64 * (3 * kLongS + 2)),
+                           (long_mix_lds<288, kLongS, 3>()), ctx->stream, (const uint8_t *)wd, (const uint8_t *)pack,
+                           act, y, rows, split_main_blocks(cols), 9);
+    } else {
+        hipLaunchKernelGGL((gemv_q4_0_long_mix_kernel<288, kLongS, 1>), dim3((rows + 3) / 4), dim3(64 * (kLongS + 2)),
+                           (long_mix_lds<288, kLongS, 1>()), ctx->stream, (const uint8_t *)wd, (const uint8_t *)pack,
+                           act, y, rows, split_main_blocks(cols), 4);
+    }
     return check_launch(ctx, "gemv_q4_0_long_mix_kernel");
 }
 

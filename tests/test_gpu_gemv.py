@@ -223,16 +223,18 @@ def test_ffn_geglu_fused(backend, dev, orc, synth):
     assert_bit_exact(y2.numpy(), y.numpy(), "ffn without act output")
 
 
-def test_ffn_split_launches(backend, dev, orc, synth):
+@pytest.mark.parametrize("dim", [2304, 2048])
+def test_ffn_split_launches(backend, dev, orc, synth, dim):
     """The split FFN's two launches on their own (the FFN entry point's form
-    at the Gemma-2-2B shape): the GeGLU over 256 workgroups of 36 rows writes
+    at the Gemma-2-2B shape, whose 2304 down rows run nine to a workgroup, and
+    at width 2048, four to a workgroup): the GeGLU over 256 workgroups of 36 rows writes
     the oracle's f32 activation and, for the 256 blocks of 32 rows it holds
     whole, the oracle quantiser's pack entries (quants, f16 scale, quant sum);
     the down projection, quantising the 32 tail blocks from the f32
     activation itself, equals the oracle down projection of that activation.
     A pack whose tail blocks hold garbage leaves the result unchanged."""
-    dim, ffn = 2304, 9216
-    rng = synth.rng_for(5550)
+    ffn = 9216
+    rng = synth.rng_for(5550 + dim)
     wg, wu = synth.q4_0_matrix(rng, ffn, dim), synth.q4_0_matrix(rng, ffn, dim)
     wd = synth.q4_0_matrix(rng, dim, ffn)
     x = synth.rms_normalised(synth.normal_vector(rng, dim))
