@@ -280,7 +280,8 @@ constexpr int kStageBatch = 5, kStageMax = 64 * kStageBatch;
 // With KQ (the Q4_K matvec, whose quants q = 0..15 carry no -8 offset) the
 // block constant is c = 128 * sum(hi) = 8 * sum(a) - 8 * sum(lo), so that
 // q4_0_isum_split returns sum q*a, and a fourth plane at nb*40 holds the
-// block sums sum(a) (the min term's bsum): nb*44 bytes in all.
+// block sums sum(a) (the min term's bsum) as floats, exact (|sum| <= 32*127):
+// nb*44 bytes in all.
 // nstage >= 0 stages only blocks [0, nstage) (the rest of the LDS pack is
 // written by someone else); the layout stays that of nb blocks.
 template <bool ISSUE_BARRIER = false, bool KQ = false>
@@ -295,7 +296,7 @@ __device__ __forceinline__ void stage_split_pack(const uint8_t *src, uint8_t *ld
     float *dd = reinterpret_cast<float *>(lds + nb * 32);
     int32_t *dc = reinterpret_cast<int32_t *>(lds + nb * 36);
     const int32_t *ss = reinterpret_cast<const int32_t *>(src + (size_t)nb * 36);
-    int32_t *dsum = reinterpret_cast<int32_t *>(lds + nb * 40);
+    float *dsum = reinterpret_cast<float *>(lds + nb * 40);
     const int nbatch = ISSUE_BARRIER ? 64 * kBatch : nb;  // one pass with the barrier (exactly one s_barrier)
     for (int b0 = 0; b0 < nbatch; b0 += 64 * kBatch) {
         uint4 x[kBatch], y[kBatch];
@@ -303,6 +304,7 @@ __device__ __forceinline__ void stage_split_pack(const uint8_t *src, uint8_t *ld
         int32_t bs[kBatch];
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
+            if (b0 + k * 64 >= nb) break;  // wave-uniform: batches past the pack issue no loads
             int b = b0 + k * 64 + lane;
             b = b < nb ? b : nb - 1;
             x[k] = sq[2 * b];
@@ -326,7 +328,7 @@ __device__ __forceinline__ void stage_split_pack(const uint8_t *src, uint8_t *ld
                                     lo_nib_sum(y[k].x) + lo_nib_sum(y[k].y) + lo_nib_sum(y[k].z) + lo_nib_sum(y[k].w));
                 if constexpr (KQ) {
                     dc[b] = c + 8 * bs[k];
-                    dsum[b] = bs[k];
+                    dsum[b] = (float)bs[k];
                 } else {
                     dc[b] = c;
                 }

@@ -96,40 +96,84 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q8_0_kernel(const uint8
 // plane [rows*nsb][16 B] = {f16 d, f16 dmin, 96-bit field of the 6-bit
 // scales (bits 6j..) and mins (bits 48+6j..)}.  The rows then stream like
 // Q4_0 rows of 8*nsb blocks: lane j of a 16-lane row owns sub-blocks
-// 16*it + j (sub-block j & 7 of its super-block in every iteration), and the
-// ordered DPP fold adds their terms in sub-block order (super-blocks, then
-// sub-blocks, the oracle's order).  Term of a sub-block:
-//   t = (float)isum * ((d * sc) * da) - (float)bsum * ((dmin * m) * da),
-//   isum = sum q*a (q = 0..15), bsum = sum a (the activation block's sum),
+// 16*it + j (sub-block j & 7 of its super-block in every iteration).  Term
+// of a sub-block:
+//   t = (float)isum * ((d * sc) * da) - bsum * ((dmin * m) * da),
+//   isum = sum q*a (q = 0..15), bsum = sum a (the activation block's sum,
+//   staged as an exact float),
 // the integer dot on the split-nibble pack (stage_split_pack's KQ form: 8
 // dot8 and 4 xor per sub-block).  The 8 lanes of a super-block share its
 // header: each lane loads one 4-byte word of it (lane j: word j & 3, so
 // every quad of lanes holds the whole header) and gets the other three by
-// DPP quad broadcasts, which keeps the header in one register per iteration
-// instead of four (occupancy).
+// DPP quad broadcasts.
+//
+// The fold is transposed: the compute waves store each row's terms to LDS,
+// T[row][b] (every slot of every iteration, the ones past the row end +0),
+// and after a barrier lane r of the staging wave adds row r's terms in
+// sub-block order (super-blocks, then sub-blocks: the oracle's order).  One
+// add per sub-block for up to 64 rows, where a 16-lane DPP fold spends 16
+// dependent adds per 16 sub-blocks per 4 rows: the DPP fold made this kernel
+// VALU-bound at the 256000-row head.  The trailing +0 slots leave the sum
+// unchanged (it is never -0: it starts at +0, and a sum of floats that is
+// exactly zero rounds to +0).
 
 template <int K>
 __device__ __forceinline__ uint32_t quad_bcast(uint32_t v)
 {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, K | (K << 2) | (K << 4) | (K << 6), 0xf, 0xf, false);
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, K | (K << 2) | (K << 4) | (K << 6), 0xf, 0xf, false);
 }
 
-template <int ITERS, int WAVES>
-__global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_k_kernel(const uint8_t *__restrict__ w,
-                                                                     const uint8_t *xpack,
-                                                                     float *__restrict__ y, int rows, int nsb)
+// T row stride in floats: every slot of ITERS iterations, an odd number of
+// 16-byte segments (the fold lanes' float4 reads spread over the banks).
+template <int ITERS>
+constexpr int q4k_t_stride() { return (ITERS * 4) % 2 ? ITERS * 16 : ITERS * 16 + 4; }
+
+inline size_t q4k_t_off(int nb) { return ((size_t)nb * 44 + 15) & ~(size_t)15; }
+
+// Dynamic LDS of a launch: the pack with block sums, then T.
+template <int ITERS>
+size_t q4k_lds(int nb, int waves) { return q4k_t_off(nb) + (size_t)4 * waves * q4k_t_stride<ITERS>() * sizeof(float); }
+
+template <int ITERS, int W>
+__global__ __launch_bounds__(64 * (W + 1)) void gemv_q4_k_kernel(const uint8_t *__restrict__ w,
+                                                                 const uint8_t *xpack,
+                                                                 float *__restrict__ y, int rows, int nsb)
 {
+    constexpr int TS = q4k_t_stride<ITERS>();
     extern __shared__ __align__(16) uint8_t lds[];
     const int nb = nsb * 8;  // sub-blocks per row = activation blocks
-    if (threadIdx.x < 64) {
+    float *T = reinterpret_cast<float *>(lds + (((size_t)nb * 44 + 15) & ~(size_t)15));
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int row0 = (int)blockIdx.x * 4 * W;
+    if (wave == 0) {
         stage_split_pack<true, true>(xpack, lds, nb);
-        __syncthreads();
+        __syncthreads();  // the pack is whole
+        __syncthreads();  // the terms are in
+        if (lane < 4 * W) {
+            const float4 *p = reinterpret_cast<const float4 *>(T + lane * TS);
+            float s = 0.0f;
+#pragma unroll
+            for (int k0 = 0; k0 < ITERS * 4; k0 += 4) {
+                float4 v[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (k0 + k < ITERS * 4) v[k] = p[k0 + k];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if (k0 + k < ITERS * 4) {
+                        s = s + v[k].x;
+                        s = s + v[k].y;
+                        s = s + v[k].z;
+                        s = s + v[k].w;
+                    }
+                }
+            }
+            if (row0 + lane < rows) y[row0 + lane] = s;
+        }
         return;
     }
-    const int lane = threadIdx.x & 63, j = lane & 15;
-    const int quad = blockIdx.x * WAVES + (threadIdx.x >> 6) - 1;
-    const int row_raw = quad * 4 + (lane >> 4);
-    const int row = row_raw < rows ? row_raw : rows - 1;  // tail rows recompute the last row
+    const int j = lane & 15, rl = (wave - 1) * 4 + (lane >> 4);
+    const int row = row0 + rl < rows ? row0 + rl : rows - 1;  // tail rows recompute the last row
     const uint4 *qs = reinterpret_cast<const uint4 *>(w);
     const uint32_t *hp = reinterpret_cast<const uint32_t *>(w + (size_t)rows * nb * 16);
     const size_t base = (size_t)row * nb, hbase = (size_t)row * nsb;
@@ -151,8 +195,8 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_k_kernel(const uint8
     const uint4 *aq = reinterpret_cast<const uint4 *>(lds);
     const float *ad = reinterpret_cast<const float *>(lds + nb * 32);
     const int32_t *ac = reinterpret_cast<const int32_t *>(lds + nb * 36);
-    const int32_t *as = reinterpret_cast<const int32_t *>(lds + nb * 40);
-    float s = 0.0f;
+    const float *as = reinterpret_cast<const float *>(lds + nb * 40);
+    float *Tr = T + rl * TS;
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
         const int bt = it * 16 + j;
@@ -169,12 +213,10 @@ __global__ __launch_bounds__(64 * (WAVES + 1)) void gemv_q4_k_kernel(const uint8
         const float da = ad[b];
         const float ds = (d * (float)sc) * da;
         const float dm = (dmin * (float)m) * da;
-        const float tv = (float)isum * ds - (float)as[b] * dm;
-        const float t = bt < nb ? tv : 0.0f;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) s = fold16(s, t);
+        const float tv = (float)isum * ds - as[b] * dm;
+        Tr[it * 16 + j] = bt < nb ? tv : 0.0f;
     }
-    if (j == 15 && row_raw < rows) y[row_raw] = s;
+    __syncthreads();
 }
 
 // ---- argmax (lowest index on ties, NaN never wins) ---------------------------
@@ -802,15 +844,21 @@ int launch_gemv_q4_k(mrml_hip_ctx *ctx, const void *w, const void *xpack, float 
     const int iters = (nb + 15) / 16;
     if (nb > kStageMax)
         return fail(ctx, MRML_HIP_E_UNSUPPORTED, "q4_k matvec: cols=%d above %d", cols, kStageMax * 32);
+    // compute waves per workgroup (4 rows each); 8 waves of 32 rows with one
+    // fold lane per row measured slower at the 256000-row head (57.4 against
+    // 51.8 us for 4 waves)
     const int waves = waves_for(rows);
-    const dim3 grid(((rows + 3) / 4 + waves - 1) / waves);
-    const size_t lds = (size_t)nb * 44;  // split-nibble pack with block sums (stage_split_pack, KQ)
+    const dim3 grid((rows + 4 * waves - 1) / (4 * waves));
 #define QK_CASE(N)                                                                                           \
     case N:                                                                                                  \
-        MRML_DISPATCH_WAVES(waves, {                                                                         \
-            hipLaunchKernelGGL((gemv_q4_k_kernel<N, WV>), grid, dim3(64 * (WV + 1)), lds, ctx->stream,             \
-                               (const uint8_t *)w, (const uint8_t *)xpack, y, rows, nsb);                   \
-        });                                                                                                  \
+        switch (waves) {                                                                                     \
+        case 1: hipLaunchKernelGGL((gemv_q4_k_kernel<N, 1>), grid, dim3(64 * 2), q4k_lds<N>(nb, 1),            \
+                                   ctx->stream, (const uint8_t *)w, (const uint8_t *)xpack, y, rows, nsb); break; \
+        case 2: hipLaunchKernelGGL((gemv_q4_k_kernel<N, 2>), grid, dim3(64 * 3), q4k_lds<N>(nb, 2),            \
+                                   ctx->stream, (const uint8_t *)w, (const uint8_t *)xpack, y, rows, nsb); break; \
+        default: hipLaunchKernelGGL((gemv_q4_k_kernel<N, 4>), grid, dim3(64 * 5), q4k_lds<N>(nb, 4),           \
+                                    ctx->stream, (const uint8_t *)w, (const uint8_t *)xpack, y, rows, nsb); break; \
+        }                                                                                                    \
         break;
     switch (iters_instance(iters)) {
         QK_CASE(1) QK_CASE(2) QK_CASE(3) QK_CASE(4) QK_CASE(5) QK_CASE(6) QK_CASE(8) QK_CASE(9) QK_CASE(12)

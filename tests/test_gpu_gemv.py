@@ -383,8 +383,12 @@ def test_gemv_q8_0_softcap(backend, dev, orc, synth):
 
 
 # ------------------------------------------------------------ Q4_K + argmax
-@pytest.mark.parametrize("rows,cols", [(256000, 2304), (37, 256), (5, 2304), (4100, 2304), (2053, 768)])
+@pytest.mark.parametrize("rows,cols", [(256000, 2304), (37, 256), (5, 2304), (4100, 2304), (2053, 768),
+                                       (40003, 4096), (9001, 2048), (300, 10240)])
 def test_gemv_q4_k_bit_exact_and_argmax(backend, dev, orc, synth, rows, cols):
+    """Every workgroup size of the launch (1, 2, 4 and 8 compute waves),
+    ragged row tails, odd and even super-block counts and the widest row the
+    pack stages (320 sub-blocks)."""
     rng = synth.rng_for(8000 + rows)
     w = synth.q4_k_matrix(rng, rows, cols)
     x = synth.normal_vector(rng, cols)
