@@ -997,6 +997,49 @@ constexpr size_t long_t_off() { return ((size_t)NB * 40 + 64 * sizeof(uint32_t) 
 template <int NB, int S>
 constexpr size_t long_lds() { return long_t_off<NB, S>() + (size_t)S * long_ipw<NB, S>() * 64 * sizeof(float); }
 
+// A fold lane's ordered sum of its row's terms, round by round: round k is
+// iterations S*k .. S*k+S-1 (4 float4 of terms each, at tv[it*16 ..]), ready
+// once q * (its live waves) have counted it in flag[k].  Round k's reads are
+// issued before round k-1's adds, so a lane that has fallen behind the stream
+// pays no LDS round trip per round.
+template <int NB, int S>
+__device__ __forceinline__ float long_fold(const float4 *tv, const uint32_t *flag, uint32_t q, int polls)
+{
+    constexpr int ITERS = NB / 16, IPW = long_ipw<NB, S>();
+    float4 v[2][4 * S];
+    float acc = 0.0f;
+    auto want = [&](int k) { return q * (uint32_t)(ITERS - S * k < S ? ITERS - S * k : S); };  // live waves
+    auto rd = [&](int k) {
+#pragma unroll
+        for (int i = 0; i < 4 * S; ++i) v[k & 1][i] = tv[(S * k + (i >> 2)) * 16 + (i & 3)];
+    };
+    auto add = [&](int k) {
+#pragma unroll
+        for (int i = 0; i < 4 * S; ++i) {
+            if (S * k + (i >> 2) < ITERS) {  // uniform
+                acc = acc + v[k & 1][i].x;
+                acc = acc + v[k & 1][i].y;
+                acc = acc + v[k & 1][i].z;
+                acc = acc + v[k & 1][i].w;
+            }
+        }
+    };
+    mrml_xsum::bounded_wait(&flag[0], want(0), polls);
+    asm volatile("" ::: "memory");
+    rd(0);
+#pragma unroll
+    for (int k = 1; k < IPW; ++k) {
+        mrml_xsum::bounded_wait(&flag[k], want(k), polls);
+        asm volatile("" ::: "memory");
+        rd(k);
+        __builtin_amdgcn_sched_barrier(0);  // round k's reads issued before round k-1's adds
+        add(k - 1);
+        asm volatile("" : "+v"(acc) : : "memory");  // and those adds done before the next wait
+    }
+    add(IPW - 1);
+    return acc;
+}
+
 template <int NB, int S>
 __global__ __launch_bounds__(64 * (S + 1)) void gemv_q4_0_long_kernel(const uint8_t *__restrict__ w,
                                                                     const uint8_t *xpack, float *__restrict__ y,
@@ -1015,26 +1058,7 @@ __global__ __launch_bounds__(64 * (S + 1)) void gemv_q4_0_long_kernel(const uint
         stage_split_pack<true>(xpack, lds, NB);
         __syncthreads();  // the pack is whole
         if (lane >= 4) return;
-        const float4 *tv = reinterpret_cast<const float4 *>(T) + lane * 4;
-        float acc = 0.0f;
-#pragma unroll 1
-        for (int k = 0; k < IPW; ++k) {
-            const uint32_t want = (uint32_t)(ITERS - S * k < S ? ITERS - S * k : S);  // waves with a live iteration
-            mrml_xsum::bounded_wait(&flag[k], want, polls);
-            asm volatile("" ::: "memory");
-            float4 v[4 * S];
-#pragma unroll
-            for (int q = 0; q < 4 * S; ++q) v[q] = tv[(S * k + (q >> 2)) * 16 + (q & 3)];
-#pragma unroll
-            for (int q = 0; q < 4 * S; ++q) {
-                if (S * k + (q >> 2) < ITERS) {  // uniform
-                    acc = acc + v[q].x;
-                    acc = acc + v[q].y;
-                    acc = acc + v[q].z;
-                    acc = acc + v[q].w;
-                }
-            }
-        }
+        const float acc = long_fold<NB, S>(reinterpret_cast<const float4 *>(T) + lane * 4, flag, 1u, polls);
         const int out = blockIdx.x * 4 + lane;
         if (out < rows) y[out] = acc;
         return;
@@ -1156,25 +1180,7 @@ __global__ __launch_bounds__(64 * (Q * S + 2)) void gemv_q4_0_long_mix_kernel(co
         __syncthreads();  // the pack is whole
         if (lane >= 4 * Q) return;
         const float4 *tv = reinterpret_cast<const float4 *>(T + (lane >> 2) * QT) + (lane & 3) * 4;
-        float acc = 0.0f;
-#pragma unroll 1
-        for (int k = 0; k < IPW; ++k) {
-            const uint32_t want = (uint32_t)Q * (ITERS - S * k < S ? ITERS - S * k : S);  // waves with a live iteration
-            mrml_xsum::bounded_wait(&flag[k], want, polls);
-            asm volatile("" ::: "memory");
-            float4 v[4 * S];
-#pragma unroll
-            for (int q = 0; q < 4 * S; ++q) v[q] = tv[(S * k + (q >> 2)) * 16 + (q & 3)];
-#pragma unroll
-            for (int q = 0; q < 4 * S; ++q) {
-                if (S * k + (q >> 2) < ITERS) {  // uniform
-                    acc = acc + v[q].x;
-                    acc = acc + v[q].y;
-                    acc = acc + v[q].z;
-                    acc = acc + v[q].w;
-                }
-            }
-        }
+        const float acc = long_fold<NB, S>(tv, flag, (uint32_t)Q, polls);  // every quad's waves count
         const int out = row0 + lane;
         if (lane < rpw && out < rows) y[out] = acc;
         return;
