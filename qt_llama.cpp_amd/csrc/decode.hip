@@ -689,12 +689,33 @@ __global__ __launch_bounds__(kScoreT) void attn_scores2_kernel(const float *__re
     int window, start;
     attn_window(d_pos, n_past_arg, wlimit, window, start);
     const int p0 = blockIdx.x * P;
-    if (p0 >= window) return;
     const int kvh = blockIdx.y, G = n_heads / n_kv_heads, tid = threadIdx.x;
     const size_t kv_dim = (size_t)n_kv_heads * HD;
     const int pos = start + window - 1;  // the newest position
     const int rnew = window - 1 - p0;    // its row in this tile (valid when 0 <= rnew < P)
     const bool has_new = ROPE && rnew < P;
+    // The newest position's rotated k and its v go to the caches from the
+    // first workgroup past the window when the grid has one (it would exit
+    // at once otherwise); the tile holding that position then only forms the
+    // rotated row in LDS.  Stores in the tile's workgroup held its chain back
+    // (its scores landed up to 1.5 us after the other tiles').
+    const int ntile = (window + P - 1) / P;
+    const bool spare = ntile < (int)gridDim.x;
+    if (p0 >= window) {
+        if (ROPE && (int)blockIdx.x == ntile && tid < half) {
+            float c, sn;
+            rope_cs(rope, pos, tid, HD, c, sn);
+            const size_t crow = cache_row_of(pos, capacity) * kv_dim + (size_t)kvh * HD;
+            const float *kh = q_in + (size_t)(n_heads + kvh) * HD;
+            const float *vh = q_in + (size_t)(n_heads + n_kv_heads + kvh) * HD;
+            const float k0 = kh[tid], k1 = kh[tid + half], v0 = vh[tid], v1 = vh[tid + half];
+            k_cache[crow + tid] = f32_to_f16_rne(k0 * c - k1 * sn);
+            k_cache[crow + tid + half] = f32_to_f16_rne(k0 * sn + k1 * c);
+            v_cache[crow + tid] = f32_to_f16_rne(v0);
+            v_cache[crow + tid + half] = f32_to_f16_rne(v1);
+        }
+        return;
+    }
     // K tile: 2048 chunks of 16 B, chunk c of row r = c >> 5 at r*528 + (c & 31)*16
     constexpr int kChunks = P * (HD * 2 / 16), kPer = kChunks / kScoreT;
     u32x4 tmp[kPer];  // a native vector: arrays of HIP's uint4 struct end up in scratch memory
@@ -732,9 +753,11 @@ __global__ __launch_bounds__(kScoreT) void attn_scores2_kernel(const float *__re
             const uint16_t k0 = f32_to_f16_rne(v0 * c - v1 * sn), k1 = f32_to_f16_rne(v0 * sn + v1 * c);
             krow[i] = k0;
             krow[i + half] = k1;
-            k_cache[crow + i] = k0;
-            k_cache[crow + i + half] = k1;
-        } else {
+            if (!spare) {
+                k_cache[crow + i] = k0;
+                k_cache[crow + i + half] = k1;
+            }
+        } else if (!spare) {
             const int i = tid - half;
             const float *vh = q_in + (size_t)(n_heads + n_kv_heads + kvh) * HD;
             v_cache[crow + i] = f32_to_f16_rne(vh[i]);
