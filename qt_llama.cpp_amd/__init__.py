@@ -151,7 +151,7 @@ _SIGNATURES = {
     "mrml_hip_gemv_q4_0_qkv": [_P, _P, _P, _P, _P, _P, _I, _I, _I],
     "mrml_hip_gemv_q4_0_geglu_q8": [_P, _P, _P, _P, _P, _I, _I],
     "mrml_hip_ffn_geglu_q4_0": [_P, _P, _P, _P, _P, _P, _P, _I, _I],
-    "mrml_hip_ffn_split_geglu": [_P, _P, _P, _P, _P, _P, _I, _I],
+    "mrml_hip_ffn_split_geglu": [_P, _P, _P, _P, _P, _P, _P, _I, _I],
     "mrml_hip_ffn_split_down": [_P, _P, _P, _P, _P, _I, _I],
     "mrml_hip_gemv_q4_0_geglu_pack": [_P, _P, _P, _P, _P, _P, _I, _I],
     "mrml_hip_gemv_q4_0_qkv_q8": [_P, _P, _P, _P, _P, _P, _I, _I, _I],
@@ -484,10 +484,11 @@ class HipDevice:
         self._check(self.lib.mrml_hip_gemv_q4_0_geglu_pack(self.ctx, _ptr(w_gate), _ptr(w_up), _ptr(x), _ptr(act),
                                                            _ptr(act_pack), rows, cols))
 
-    def ffn_split_geglu(self, w_gate, w_up, x, act, act_pack, dim: int, ffn: int) -> None:
-        """The split FFN's GeGLU launch: f32 act and the pack's whole blocks (mrml_hip_ffn_split_geglu)."""
+    def ffn_split_geglu(self, w_gate, w_up, x, act, act_pack, dim: int, ffn: int, w_down_next=None) -> None:
+        """The split FFN's GeGLU launch: f32 act and the pack's whole blocks (mrml_hip_ffn_split_geglu);
+        w_down_next (optional): the down projection launched next, read ahead into the caches."""
         self._check(self.lib.mrml_hip_ffn_split_geglu(self.ctx, _ptr(w_gate), _ptr(w_up), _ptr(x), _ptr(act),
-                                                      _ptr(act_pack), dim, ffn))
+                                                      _ptr(act_pack), _ptr(w_down_next), dim, ffn))
 
     def ffn_split_down(self, w_down, act_pack, act, y, dim: int, ffn: int) -> None:
         """The split FFN's down launch (mrml_hip_ffn_split_down)."""

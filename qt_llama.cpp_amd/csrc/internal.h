@@ -54,8 +54,11 @@ bool ffn_split_ok(int dim, int ffn);
 int launch_ffn_split(mrml_hip_ctx *ctx, const void *wg, const void *wu, const void *wd, const float *x, float *act,
                      void *pack, float *y, int32_t dim, int32_t ffn);
 int split_main_blocks(int ffn);
+// wd (nullable): the down projection that follows, whose rows the GeGLU's
+// staging waves read ahead into the caches (when it runs nine rows a
+// workgroup); results do not depend on it.
 int launch_geglu_split(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *x, float *act, void *pack,
-                       int32_t rows, int32_t cols);
+                       int32_t rows, int32_t cols, const void *wd = nullptr);
 // The split GeGLU with the post-attention sandwich residual fused ahead
 // (h_out = h_in + rms_norm(t, w_post), then rms_norm(h_out, w_norm) as its
 // input): act and the pack blocks launch_geglu_split writes.

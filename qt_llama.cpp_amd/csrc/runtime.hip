@@ -522,14 +522,14 @@ int mrml_hip_ffn_geglu_q4_0(mrml_hip_ctx *ctx, const void *wg, const void *wu, c
 }
 
 int mrml_hip_ffn_split_geglu(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *x, float *act,
-                             void *act_pack, int32_t dim, int32_t ffn)
+                             void *act_pack, const void *wd_next, int32_t dim, int32_t ffn)
 {
     CTX_GUARD(ctx);
     CHECK_MATVEC(ctx, wg, x, act, ffn, dim, 32);
     REQUIRE(ctx, wu && act_pack, "null pointer");
     REQUIRE(ctx, ffn_split_ok(dim, ffn), "ffn_split_geglu: dim=%d ffn=%d is not a shape of the split form", dim, ffn);
     REQUIRE(ctx, ((uintptr_t)act_pack & 15) == 0, "ffn_split_geglu: act_pack must be 16-byte aligned");
-    return launch_geglu_split(ctx, wg, wu, x, act, act_pack, ffn, dim);
+    return launch_geglu_split(ctx, wg, wu, x, act, act_pack, ffn, dim, wd_next);
 }
 
 int mrml_hip_ffn_split_down(mrml_hip_ctx *ctx, const void *wd, const void *act_pack, const float *act, float *y,

@@ -166,7 +166,7 @@ api! {
     gemv_q4_0_gguf: fn(Ctx, *const c_void, *const f32, *mut f32, i32, i32) -> c_int = "mrml_hip_gemv_q4_0_gguf";
     gemv_q4_0_geglu: fn(Ctx, *const c_void, *const c_void, *const f32, *mut f32, i32, i32) -> c_int = "mrml_hip_gemv_q4_0_geglu";
     ffn_geglu_q4_0: fn(Ctx, *const c_void, *const c_void, *const c_void, *const f32, *mut f32, *mut f32, i32, i32) -> c_int = "mrml_hip_ffn_geglu_q4_0";
-    ffn_split_geglu: fn(Ctx, *const c_void, *const c_void, *const f32, *mut f32, *mut c_void, i32, i32) -> c_int = "mrml_hip_ffn_split_geglu";
+    ffn_split_geglu: fn(Ctx, *const c_void, *const c_void, *const f32, *mut f32, *mut c_void, *const c_void, i32, i32) -> c_int = "mrml_hip_ffn_split_geglu";
     ffn_split_down: fn(Ctx, *const c_void, *const c_void, *const f32, *mut f32, i32, i32) -> c_int = "mrml_hip_ffn_split_down";
     gemv_q4_0_geglu_pack: fn(Ctx, *const c_void, *const c_void, *const f32, *mut f32, *mut c_void, i32, i32) -> c_int = "mrml_hip_gemv_q4_0_geglu_pack";
     gemv_q4_0_geglu_q8: fn(Ctx, *const c_void, *const c_void, *const c_void, *mut f32, i32, i32) -> c_int = "mrml_hip_gemv_q4_0_geglu_q8";

@@ -249,6 +249,17 @@ def test_ffn_split_launches(backend, dev, orc, synth, dim):
     dev.ffn_split_down(bd, pack, act, y, dim, ffn)
     dev.sync()
     a = act.numpy()
+    # the GeGLU reading the down projection ahead (nine-row down form at 2304;
+    # no read-ahead at 2048) changes no bit of either launch
+    act2 = backend.HipBuffer.alloc(dev, ffn)
+    pack2 = backend.HipBuffer.from_host(dev, np.full(nbo * 40, 0x7F, np.uint8))
+    y2 = backend.HipBuffer.alloc(dev, dim)
+    dev.ffn_split_geglu(bg, bu, xb, act2, pack2, dim, ffn, w_down_next=bd)
+    dev.ffn_split_down(bd, pack2, act2, y2, dim, ffn)
+    dev.sync()
+    assert np.array_equal(act2.numpy().view(np.uint32), a.view(np.uint32)), "act with the read-ahead"
+    assert np.array_equal(pack2.numpy(), pack.numpy()), "pack with the read-ahead"
+    assert np.array_equal(y2.numpy().view(np.uint32), y.numpy().view(np.uint32)), "down after the read-ahead"
     xq = orc.quantize_q8_0(x)
     ref_act = orc.geglu(orc.mat_vec_mul_q4_0_q8_0(wg, xq, ffn, dim, threads=THREADS),
                         orc.mat_vec_mul_q4_0_q8_0(wu, xq, ffn, dim, threads=THREADS))
