@@ -204,10 +204,12 @@ int mrml_hip_ffn_geglu_q4_0(mrml_hip_ctx *ctx, const void *d_w_gate, const void 
  * bytes); the down projection takes both, quantising the tail blocks from
  * d_act itself.  Only the shapes of the split form (dim/32 in {64, 72}, ffn
  * = 9216 = 256 x 36) are served; others return MRML_HIP_E_INVALID.
- * d_w_down_next (nullable): the down projection the caller launches next; when
- * it runs nine rows a workgroup (dim a multiple of 2304) the GeGLU reads its
- * rows ahead into the caches while its own weights finish streaming (the
- * results do not depend on it; mrml_hip_ffn_geglu_q4_0 passes its d_w_down). */
+ * d_w_down_next (nullable): the down projection the caller launches next (a
+ * dim x ffn Q4_0 matrix in the backend layout: dim*ffn/32*18 bytes, read
+ * only); when it runs nine rows a workgroup (dim a multiple of 2304) the GeGLU
+ * reads its rows ahead into the caches while its own weights finish streaming
+ * (the results do not depend on it; mrml_hip_ffn_geglu_q4_0 passes its
+ * d_w_down). */
 int mrml_hip_ffn_split_geglu(mrml_hip_ctx *ctx, const void *d_w_gate, const void *d_w_up, const float *d_x,
                              float *d_act, void *d_act_pack, const void *d_w_down_next, int32_t dim, int32_t ffn);
 int mrml_hip_ffn_split_down(mrml_hip_ctx *ctx, const void *d_w_down, const void *d_act_pack, const float *d_act,
