@@ -185,8 +185,8 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
     v16i cmagic;
 #pragma unroll
     for (int e = 0; e < 16; ++e) cmagic[e] = kMagicBits;
-    auto mfma = [&](int buf, int kc, const BOps &o) {
-        const u32x4 wv = sa[buf][kc][h][tl];
+    auto read_a = [&](int buf, int kc) { return sa[buf][kc][h][tl]; };
+    auto mfma = [&](const u32x4 wv, const BOps &o) {
         const v4i a = {(int)wv.x, (int)wv.y, (int)wv.z, (int)wv.w};
         const v4i bq = {(int)o.a.x, (int)o.a.y, (int)o.a.z, (int)o.a.w};
         return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, cmagic, 0, 0, 0);
@@ -195,13 +195,14 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
     float acc[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
-    // Block fold: the four float4s of row scales first (one wait), then
-    // 16 x (isum, dw*da, *, +).
-    auto fold = [&](const v16i &d, float da, int buf, int kc) {
+    // The lane's 16 row scales of a block: four float4s, rows 8j + 4h + 0..3.
+    auto read_dw = [&](int buf, int kc, float4 (&dw)[4]) {
         const float4 *dwb = reinterpret_cast<const float4 *>(&sdw[buf][kc][4 * h]);
-        float4 dw[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dw[j] = dwb[2 * j];  // rows 8j + 4h + 0..3
+        for (int j = 0; j < 4; ++j) dw[j] = dwb[2 * j];
+    };
+    // Block fold: 16 x (isum, dw*da, *, +).
+    auto fold = [&](const v16i &d, float da, const float4 (&dw)[4]) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float dwv[4] = {dw[j].x, dw[j].y, dw[j].z, dw[j].w};
@@ -228,25 +229,47 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
 #pragma unroll
     for (int s = 0; s < kPF; ++s) load_b(s, ring[s]);
 
-    // Step (block b = kKC*c + kc): MFMA, fold, refill the block's B slot with
-    // block b+kPF.  The MFMA is not overlapped with the previous fold: while
-    // it executes no wave of the SIMD issues VALU work anyway.  A scheduling
-    // barrier keeps the refill after the fold (the scheduler would otherwise
-    // gather the loads and wait for them all at once), so each wait covers
-    // only the block about to be used.  Loads of blocks >= nb are never used.
+    // Step (block b = kKC*c + kc), software-pipelined so that no LDS read or
+    // MFMA result is waited for right after it is issued:
+    //   - the MFMA of block b+1, on the A operand read at step b-1;
+    //   - the LDS reads of block b+2's A operand and block b+1's row scales
+    //     (from the next chunk's buffer, already whole, near a chunk's end);
+    //   - the fold of block b (result and row scales from step b-1);
+    //   - block b+kPF into block b's B slot.
+    // A wave alone on its SIMD (down: 1152 tiles for 1024 SIMDs) otherwise
+    // waits out each latency every block: down 75.3 -> 71.1 us, gate and up
+    // about 1.5 us each.  Past the last block these MFMAs and reads work on
+    // in-range leftovers and are never folded.  A scheduling barrier keeps the
+    // refill after the fold (the scheduler would otherwise gather the loads
+    // and wait for them all at once), so each wait covers only the block about
+    // to be used.  Loads of blocks >= nb are never used.
     // Chunk reuse: at the end of chunk c, chunk c+2 is written into buffer
-    // (c+2)%3 = (c-1)%3, whose last readers (chunk c-1's MFMAs and folds)
-    // all come before the barrier that ended chunk c-1.
+    // (c+2)%3 = (c-1)%3, whose readers (chunk c-1's reads and MFMAs, the
+    // first of them issued during chunk c-2, and its folds) all come before
+    // the barrier that ended chunk c-1.
     int c = 0, cb = 0, nbf = 1, wb = 2;  // chunk, its buffer, the next chunk's buffer, the buffer to write
-    auto step = [&](int kc, BOps &cur, bool refill, int b) {
-        const v16i d = mfma(cb, kc, cur);
-        fold(d, cur.da, cb, kc);
+    v16i dq = mfma(read_a(cb, 0), ring[0]);
+    u32x4 an = read_a(cb, 1);  // block 1 (kKC > 1)
+    float4 dwc[4];
+    read_dw(cb, 0, dwc);
+    auto step = [&](int kc, int nbuf, int nkc, int nbuf2, int nkc2, bool refill, int b) {
+        const v16i dn = mfma(an, ring[(kc + 1) % kPF]);
+        an = read_a(nbuf2, nkc2);
+        float4 dwn[4];
+        read_dw(nbuf, nkc, dwn);
+        fold(dq, ring[kc % kPF].da, dwc);
         __builtin_amdgcn_sched_barrier(0);
-        if (refill) load_b(b + kPF, cur);
+        if (refill) load_b(b + kPF, ring[kc % kPF]);
+        dq = dn;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dwc[j] = dwn[j];
     };
+    static_assert(kKC > 2, "blocks b+1 and b+2 are each in this chunk or the next");
     for (; (c + 1) * kKC <= nb; ++c) {
 #pragma unroll
-        for (int kc = 0; kc < kKC; ++kc) step(kc, ring[kc % kPF], true, c * kKC + kc);
+        for (int kc = 0; kc < kKC; ++kc)
+            step(kc, kc + 1 < kKC ? cb : nbf, (kc + 1) % kKC, kc + 2 < kKC ? cb : nbf, (kc + 2) % kKC, true,
+                 c * kKC + kc);
         store_chunk(wb);
         lds_barrier();
         load_chunk(c + 3);
@@ -260,7 +283,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
     // zeros, and are never folded).
 #pragma unroll
     for (int kc = 0; kc < kKC - 1; ++kc)
-        if (c * kKC + kc < nb) step(kc, ring[kc % kPF], kc + kPF < kKC - 1, c * kKC + kc);
+        if (c * kKC + kc < nb) step(kc, cb, kc + 1, cb, (kc + 2) % kKC, kc + kPF < kKC - 1, c * kKC + kc);
 
     const int tok = g * 32 + tl;
     if (tok < batch) {
