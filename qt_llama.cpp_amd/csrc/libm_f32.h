@@ -68,24 +68,36 @@ MRML_HD double u2d(uint64_t u) { return __builtin_bit_cast(double, u); }
 // GeGLU kernel's tail).  k = 0 and k = +-1 reduce to fdlibm's generic
 // formula exactly (t*ln2_hi and t*ln2_lo are exact for t = 0, +-1, and
 // x - (-y) is x + y), so one reduction serves every case.
-MRML_HD float expm1f(float x)
+// fdlibm's expm1f cases below its overflow threshold, selected by k.
+// TANH: only the arguments tanhf passes (2|y| for |y| >= 1, where k >= 3,
+// and -2|y| for |y| < 1, where -3 <= k <= 0): the k = 1 case is left out,
+// and the caller replaces the results of the arguments that fdlibm's
+// special cases would catch (tiny, huge and non-finite y).
+template <bool TANH>
+MRML_HD float expm1f_cases(float x, uint32_t hx, bool neg)
 {
     const float ln2_hi = 6.9313812256e-01f;   // 0x3f317180
     const float ln2_lo = 9.0580006145e-06f;   // 0x3717f7d1
     const float invln2 = 1.4426950216e+00f;   // 0x3fb8aa3b
     const float Q1 = -3.3333335072e-02f, Q2 = 1.5873016091e-03f, Q3 = -7.9365076090e-05f,
                 Q4 = 4.0082177293e-06f, Q5 = -2.0109921195e-07f;
-    uint32_t hx = f2u(x);
-    const uint32_t xsb = hx & 0x80000000u;
-    hx &= 0x7fffffffu;
-    const bool neg = xsb != 0;
     const bool red = hx > 0x3eb17218u;     // |x| > 0.5 ln2: reduce by k ln2
     const bool near1 = hx < 0x3f851592u;   // and |x| < 1.5 ln2: k = +-1
     // the generic k; the clamp only keeps the conversion defined for the
     // arguments whose result a special case replaces (|x| < 88.8 gives |k| < 129)
     float kf = invln2 * x + (neg ? -0.5f : 0.5f);
     kf = kf > -200.0f ? (kf < 200.0f ? kf : 200.0f) : -200.0f;
-    const int32_t k = red ? (near1 ? (neg ? -1 : 1) : (int32_t)kf) : 0;
+    // (the empty asm statements here and in tanhf make the compiler form
+    // each candidate in every lane, so the selects stay selects: it would
+    // otherwise put the conversion and the special cases behind branches)
+    int32_t kg = (int32_t)kf;
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("" : "+v"(kg));
+#endif
+    int32_t k = red ? (near1 ? (neg ? -1 : 1) : kg) : 0;
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("" : "+v"(k));
+#endif
     const float tk = (float)k;
     const float hi = x - tk * ln2_hi;  // exact
     const float lo = tk * ln2_lo;
@@ -100,7 +112,7 @@ MRML_HD float expm1f(float x)
     float e2 = (xr * (e - c) - c);
     e2 -= hxs;
     const float r_km1 = 0.5f * (xr - e2) - 0.5f;
-    const float r_k1 = xr < -0.25f ? -2.0f * (e2 - (xr + 0.5f)) : 1.0f + 2.0f * (xr - e2);
+    const float r_k1 = TANH ? 0.0f : (xr < -0.25f ? -2.0f * (e2 - (xr + 0.5f)) : 1.0f + 2.0f * (xr - e2));
     const uint32_t ksh = (uint32_t)k << 23;
     const float r_far = u2f(f2u(1.0f - (e2 - xr)) + ksh) - 1.0f;  // k <= -2 or k > 56: exp(x) - 1 directly
     const int32_t kl = k < 0 ? 0 : (k > 31 ? 31 : k);            // shift counts in range for every lane
@@ -109,8 +121,16 @@ MRML_HD float expm1f(float x)
     float y = xr - (e2 + u2f((uint32_t)(0x7f - kh) << 23));      // 23 <= k <= 56
     y += 1.0f;
     const float r_hi = u2f(f2u(y) + ksh);
-    float r = k == 0 ? r_k0
-                     : (k == -1 ? r_km1 : (k == 1 ? r_k1 : ((k <= -2 || k > 56) ? r_far : (k < 23 ? r_lo : r_hi))));
+    const float r_mid = (k <= -2 || k > 56) ? r_far : (k < 23 ? r_lo : r_hi);
+    return k == 0 ? r_k0 : (k == -1 ? r_km1 : ((!TANH && k == 1) ? r_k1 : r_mid));
+}
+
+MRML_HD float expm1f(float x)
+{
+    const uint32_t hx = f2u(x) & 0x7fffffffu;
+    const bool neg = (f2u(x) >> 31) != 0;
+    const bool red = hx > 0x3eb17218u;
+    float r = expm1f_cases<false>(x, hx, neg);
     const float tt = 1.0f + x;
     if (!red && hx < 0x33000000u) r = x - (tt - (1.0f + x));  // |x| < 2^-25
     if (hx >= 0x4195b844u && neg) r = -1.0f;                  // x < -27 ln2
@@ -125,16 +145,22 @@ MRML_HD float tanhf(float x)
     const uint32_t jx = f2u(x), ix = jx & 0x7fffffffu;
     const float ax = u2f(ix);
     const bool ge1 = ix >= 0x3f800000u;  // |x| >= 1: 1 - 2/(expm1(2|x|) + 2); else -t/(t + 2), t = expm1(-2|x|)
-    const float t = expm1f(ge1 ? 2.0f * ax : -2.0f * ax);
-    const float q = (ge1 ? 2.0f : -t) / (t + 2.0f);
-    float z = ge1 ? 1.0f - q : q;
-    if (ix >= 0x41b00000u) z = 1.0f;     // |x| >= 22: 1 - tiny rounds to 1
-    float r = (jx >> 31) == 0 ? z : -z;
-    if (ix < 0x24000000u) r = x * (1.0f + x);  // |x| < 2^-55
-    if (ix == 0) r = x;
-    if (ix == 0x7f800000u) r = (jx >> 31) == 0 ? 1.0f : -1.0f;  // 1/x +- 1
-    if (ix > 0x7f800000u) r = x + x;                            // NaN
-    return r;
+    const float a2 = ge1 ? 2.0f * ax : -2.0f * ax;
+    const float t = expm1f_cases<true>(a2, f2u(a2) & 0x7fffffffu, !ge1);
+    float q = (ge1 ? 2.0f : -t) / (t + 2.0f);
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("" : "+v"(q));  // formed in every lane: the selects below stay selects, not branches
+#endif
+    const float z = ix >= 0x41b00000u ? 1.0f : (ge1 ? 1.0f - q : q);  // |x| >= 22: 1 - tiny rounds to 1
+    const bool sgn = (jx >> 31) != 0;
+    // fdlibm's special cases, as selects: |x| < 2^-55 (x * (1 + x), which is
+    // x itself for zeros too), +-inf (+-1), NaN (x + x)
+    float xx = x + x;
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("" : "+v"(xx));
+#endif
+    const float r = ix < 0x24000000u ? x * (1.0f + x) : (sgn ? -z : z);
+    return ix >= 0x7f800000u ? (ix == 0x7f800000u ? (sgn ? -1.0f : 1.0f) : xx) : r;
 }
 
 // ---- expf (Arm optimized-routines algorithm) -------------------------------------
