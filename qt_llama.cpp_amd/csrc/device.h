@@ -35,15 +35,17 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h)
 // the f16 normal range -> +0, overflow -> +-Inf, NaN -> sign|0x7e00.
 __device__ __forceinline__ uint32_t f32_to_f16_trunc(float f)
 {
-    uint32_t bits = __builtin_bit_cast(uint32_t, f);
-    uint32_t sign = (bits >> 31) & 1u;
-    int32_t exp = (int32_t)((bits >> 23) & 0xffu);
-    uint32_t mant = bits & 0x7fffffu;
-    if (exp == 255) return (sign << 15) | (mant == 0 ? 0x7c00u : 0x7e00u);
-    int32_t e16 = exp - 127 + 15;
-    if (e16 >= 31) return (sign << 15) | 0x7c00u;
-    if (e16 <= 0) return 0u;
-    return (sign << 15) | ((uint32_t)e16 << 10) | (mant >> 13);
+    // every case formed, then selected (as branches they cost exec-mask
+    // switches on the quantisers' critical path)
+    const uint32_t bits = __builtin_bit_cast(uint32_t, f);
+    const uint32_t sgn = (bits >> 16) & 0x8000u;
+    const int32_t exp = (int32_t)((bits >> 23) & 0xffu);
+    const uint32_t mant = bits & 0x7fffffu;
+    const int32_t e16 = exp - 127 + 15;
+    uint32_t special = sgn | (exp == 255 && mant != 0 ? 0x7e00u : 0x7c00u);  // NaN, or Inf / overflow
+    uint32_t normal = sgn | ((uint32_t)e16 << 10) | (mant >> 13);
+    asm volatile("" : "+v"(special), "+v"(normal));  // formed in every lane: the selects stay selects
+    return (exp == 255 || e16 >= 31) ? special : (e16 <= 0 ? 0u : normal);
 }
 
 // f32 -> f16, IEEE round-to-nearest-even (hardware conversion).
@@ -89,15 +91,23 @@ __device__ __forceinline__ float fold16(float s, float t) { return dpp_ror1(s) +
 
 // Reductions over each 32-lane half of the wave, result in every lane of the
 // half.  Within a 16-lane DPP row: quad_perm swaps (xor 1, xor 2) and
-// row_ror by 4 and 8; the two rows of a half are then combined with one
-// ds_swizzle (xor 16).  DPP moves stay in the VALU; only the last step uses
-// the LDS crossbar.
+// row_ror by 4 and 8; the two rows of a half are then combined through
+// v_permlane16_swap (gfx950), all in the VALU.
 template <int CTRL>
 __device__ __forceinline__ int dpp_mov(int v)
 {
     return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
 }
-__device__ __forceinline__ int swizzle_xor16(int v) { return __builtin_amdgcn_ds_swizzle(v, 0x401F); }
+// Lane l's value and lane l ^ 16's (the other row of its 32-lane half), in
+// either order: v_permlane16_swap on two copies of v exchanges the odd rows
+// of the first with the even rows of the second, leaving row 0 of each half
+// in one result and row 1 in the other.
+__device__ __forceinline__ void row_pair(int v, int &a, int &b)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+    a = (int)r[0];
+    b = (int)r[1];
+}
 
 __device__ __forceinline__ float max32(float m)
 {
@@ -106,7 +116,25 @@ __device__ __forceinline__ float max32(float m)
     m = step(m, __builtin_bit_cast(float, dpp_mov<0x4E>(__builtin_bit_cast(int, m))));   // quad_perm 2,3,0,1
     m = step(m, __builtin_bit_cast(float, dpp_mov<0x124>(__builtin_bit_cast(int, m))));  // row_ror:4
     m = step(m, __builtin_bit_cast(float, dpp_mov<0x128>(__builtin_bit_cast(int, m))));  // row_ror:8
-    return step(m, __builtin_bit_cast(float, swizzle_xor16(__builtin_bit_cast(int, m))));
+    int a, b;
+    row_pair(__builtin_bit_cast(int, m), a, b);
+    return step(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+
+// max32 of values that are all >= +0 (never NaN): their bit patterns order
+// as the values do, so an unsigned maximum, which takes its DPP operand
+// directly, gives the same bits.
+__device__ __forceinline__ float max32_nonneg(float m)
+{
+    auto step = [](uint32_t a, int b) { return a > (uint32_t)b ? a : (uint32_t)b; };
+    uint32_t u = __builtin_bit_cast(uint32_t, m);
+    u = step(u, dpp_mov<0xB1>((int)u));
+    u = step(u, dpp_mov<0x4E>((int)u));
+    u = step(u, dpp_mov<0x124>((int)u));
+    u = step(u, dpp_mov<0x128>((int)u));
+    int a, b;
+    row_pair((int)u, a, b);
+    return __builtin_bit_cast(float, step((uint32_t)a, b));
 }
 
 __device__ __forceinline__ int sum32(int s)
@@ -115,7 +143,9 @@ __device__ __forceinline__ int sum32(int s)
     s += dpp_mov<0x4E>(s);
     s += dpp_mov<0x124>(s);
     s += dpp_mov<0x128>(s);
-    return s + swizzle_xor16(s);
+    int a, b;
+    row_pair(s, a, b);
+    return a + b;
 }
 
 // One Q8_0 block (quant.rs:193-228) held by 32 consecutive lanes, lane l
@@ -130,7 +160,7 @@ __device__ __forceinline__ int q8_0_block32(float v, uint32_t &dbits, int &qsum)
 {
     float m = fabsf(v);
     m = (m > 0.0f) ? m : 0.0f;  // NaN -> 0
-    m = max32(m);               // max is exact in any order
+    m = max32_nonneg(m);        // max is exact in any order
     const float scale = m / 127.0f;
     dbits = f32_to_f16_trunc(scale);
     const float id = (scale != 0.0f) ? 1.0f / scale : 0.0f;
@@ -155,7 +185,7 @@ __device__ __forceinline__ int q4_0_block32(float v, uint32_t &dbits)
 {
     float m = fabsf(v);
     m = (m > 0.0f) ? m : 0.0f;  // NaN -> 0
-    m = max32(m);
+    m = max32_nonneg(m);
     const float scale = m > 0.0f ? m / 8.0f : 0.0f;
     dbits = f32_to_f16_trunc(scale);
     const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
