@@ -9,7 +9,9 @@
 // is bit-identical to the batch-1 CPU path for that token.
 //
 // The integer part is one v_mfma_i32_32x32x32_i8 per (32 rows, 32 tokens,
-// K block).  Lane l feeds row l%32 / token l%32 and K half l/32:
+// K block) -- or, for the last row tiles of a product whose tiles number just
+// over one per SIMD, two v_mfma_i32_16x16x32_i8 per (32 rows, 16 tokens, K
+// block) (gemm_tile below).  Lane l feeds row l%32 / token l%32 and K half l/32:
 //   A = the row's 16 quant bytes, low nibbles (half 0) or high nibbles
 //       (half 1), as signed bytes q-8 (see sbytes, applied when the weights
 //       are staged), so the MFMA result is isum itself;
@@ -61,6 +63,7 @@ constexpr int kNBuf = 3;                  // A chunk buffers in LDS
 constexpr int kBufferFlags = 0x00020000;  // buffer resource word 3 (raw 32-bit data) on gfx9
 constexpr float kMagic = 12582912.0f;      // 1.5 * 2^23
 constexpr int kMagicBits = 0x4B400000;     // its f32 bit pattern
+constexpr int kSIMDs = 1024;               // MI355X: 256 CUs x 4 SIMDs
 
 // GEMM pack of `batch` tokens x nb blocks, groups of 32 tokens (the last
 // group zero-padded):
@@ -135,18 +138,34 @@ struct BOps {
 // RELAXED: each block term joins its output's sum with one FMA instead of
 // a product and a separate add (the integer sums stay exact; the f32 sums
 // round once per block instead of twice) -- the tolerance path's prefill.
-template <bool RELAXED>
-__global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const uint8_t *__restrict__ w,
-                                                                         const uint8_t *__restrict__ gp,
-                                                                         float *__restrict__ y, int rows, int nb,
-                                                                         int batch, int ngroups, int ldy, int vec)
+//
+// Tile of one wave over all of K:
+//   FULL: 32 rows x 32 tokens, one v_mfma_i32_32x32x32_i8 a block (lane l:
+//         row / token l%32, K half l/32; 16 outputs a lane, rows
+//         8j + 4(l/32) + i of token l%32);
+//   HALF: 32 rows x 16 tokens (half of a token group), two
+//         v_mfma_i32_16x16x32_i8 a block, rows 0..15 and 16..31 (lane l:
+//         row / token l%16, K bytes 8(l/16)..+8; 8 outputs a lane, rows
+//         16j + 4(l/16) + i of token l%16).
+// A HALF wave folds half the outputs of a FULL one for the same operand
+// reads, so it serves only to spread a product whose FULL tiles number just
+// over one per SIMD (the launch below).
+template <bool RELAXED, bool HALF>
+__device__ __forceinline__ void gemm_tile(const uint8_t *__restrict__ w, const uint8_t *__restrict__ gp,
+                                          float *__restrict__ y, int rows, int nb, int batch, int ngroups, int ldy,
+                                          int vec, int rt, int gsel, u32x4 (&sa)[kNBuf][kKC][2][32],
+                                          float (&sdw)[kNBuf][kKC][32])
 {
-    __shared__ __align__(16) u32x4 sa[kNBuf][kKC][2][32];  // A chunks: [block][K half][row] 16 signed bytes
-    __shared__ __align__(16) float sdw[kNBuf][kKC][32];  // their row scales, f32
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r0 = blockIdx.x * 32;
-    const int g = blockIdx.y * kGemmWaves + wave;  // >= ngroups: computes on zeros, stores nothing
-    const int tl = lane & 31, h = lane >> 5;
+    constexpr int NACC = HALF ? 8 : 16;  // outputs a lane
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int r0 = rt * 32;
+    // FULL: token group gsel; HALF: half gsel & 1 of token group gsel >> 1.
+    // A group >= ngroups computes on zeros and stores nothing.
+    const int g = HALF ? gsel >> 1 : gsel;
+    const int tl = HALF ? 16 * (gsel & 1) + (lane & 15) : lane & 31;  // the lane's token in its group
+    const int q = lane >> 4, h = lane >> 5;                            // HALF: K quarter; FULL: K half
+    const int rbase = HALF ? 4 * q : 4 * h;                           // first row of the lane's outputs
+    constexpr int rstep = HALF ? 16 : 8;                              // rows between its output quads
     const uint32_t qs_bytes = (uint32_t)rows * nb * 16;
     // Loads past a row's last block read the next row or, past the end of a
     // buffer, zeros (buffer range check); such blocks are never folded.
@@ -174,37 +193,71 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
         sdw[buf][ak][ar] = f16_bits_to_f32(sreg);
     };
 
-    // B: this wave's token group, lane order = MFMA order.
-    const uint32_t b_off = ((uint32_t)g * nb * 64 + lane) * 16;
+    // B: the lane's quants of its token (FULL: 16 bytes, its K half; HALF:
+    // 8 bytes, its K quarter) and the token's block scale.
+    const uint32_t b_off = HALF ? ((uint32_t)g * nb * 64 + 32 * (q >> 1) + tl) * 16 + 8 * (q & 1)
+                                : ((uint32_t)g * nb * 64 + lane) * 16;
     const uint32_t d_off = (uint32_t)ngroups * nb * 1024 + ((uint32_t)g * nb * 32 + tl) * 4;
     auto load_b = [&](int b, BOps &o) {
-        o.a = __builtin_amdgcn_raw_buffer_load_b128(gr, b_off + (uint32_t)b * 1024, 0, 0);
+        if constexpr (HALF) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(gr, b_off + (uint32_t)b * 1024, 0, 0);
+            o.a = u32x4{v[0], v[1], 0u, 0u};
+        } else {
+            o.a = __builtin_amdgcn_raw_buffer_load_b128(gr, b_off + (uint32_t)b * 1024, 0, 0);
+        }
         o.da = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(gr, d_off + (uint32_t)b * 128, 0, 0));
     };
+    // The lane's A operand of a block (HALF: rows l%16 and 16 + l%16, 8 bytes each).
+    auto read_a = [&](int buf, int kc) {
+        if constexpr (HALF) {
+            const uint2 a0 = reinterpret_cast<const uint2 *>(&sa[buf][kc][q >> 1][lane & 15])[q & 1];
+            const uint2 a1 = reinterpret_cast<const uint2 *>(&sa[buf][kc][q >> 1][16 + (lane & 15)])[q & 1];
+            return u32x4{a0.x, a0.y, a1.x, a1.y};
+        } else {
+            return sa[buf][kc][h][tl];
+        }
+    };
     // C of every MFMA: the f32 bits of kMagic (see the header).
-    v16i cmagic;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) cmagic[e] = kMagicBits;
-    auto read_a = [&](int buf, int kc) { return sa[buf][kc][h][tl]; };
     auto mfma = [&](const u32x4 wv, const BOps &o) {
-        const v4i a = {(int)wv.x, (int)wv.y, (int)wv.z, (int)wv.w};
-        const v4i bq = {(int)o.a.x, (int)o.a.y, (int)o.a.z, (int)o.a.w};
-        return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, cmagic, 0, 0, 0);
+        v16i d;
+        if constexpr (HALF) {
+            const v4i cm = {kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+            const long bq = (long)((uint64_t)o.a.x | ((uint64_t)o.a.y << 32));
+            const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)((uint64_t)wv.x | ((uint64_t)wv.y << 32)), bq,
+                                                                 cm, 0, 0, 0);
+            const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)((uint64_t)wv.z | ((uint64_t)wv.w << 32)), bq,
+                                                                 cm, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                d[e] = d0[e];
+                d[4 + e] = d1[e];
+                d[8 + e] = 0;
+                d[12 + e] = 0;
+            }
+        } else {
+            v16i cmagic;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) cmagic[e] = kMagicBits;
+            const v4i a = {(int)wv.x, (int)wv.y, (int)wv.z, (int)wv.w};
+            const v4i bq = {(int)o.a.x, (int)o.a.y, (int)o.a.z, (int)o.a.w};
+            d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, cmagic, 0, 0, 0);
+        }
+        return d;
     };
 
-    float acc[16];
+    float acc[NACC];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
-    // The lane's 16 row scales of a block: four float4s, rows 8j + 4h + 0..3.
+    for (int e = 0; e < NACC; ++e) acc[e] = 0.0f;
+    // The lane's row scales of a block: NACC/4 float4s, rows rstep*j + rbase + 0..3.
     auto read_dw = [&](int buf, int kc, float4 (&dw)[4]) {
-        const float4 *dwb = reinterpret_cast<const float4 *>(&sdw[buf][kc][4 * h]);
+        const float4 *dwb = reinterpret_cast<const float4 *>(&sdw[buf][kc][rbase]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dw[j] = dwb[2 * j];
+        for (int j = 0; j < NACC / 4; ++j) dw[j] = dwb[(rstep / 4) * j];
     };
-    // Block fold: 16 x (isum, dw*da, *, +).
+    // Block fold: NACC x (isum, dw*da, *, +).
     auto fold = [&](const v16i &d, float da, const float4 (&dw)[4]) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NACC / 4; ++j) {
             const float dwv[4] = {dw[j].x, dw[j].y, dw[j].z, dw[j].w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -262,7 +315,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
         if (refill) load_b(b + kPF, ring[kc % kPF]);
         dq = dn;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dwc[j] = dwn[j];
+        for (int j = 0; j < NACC / 4; ++j) dwc[j] = dwn[j];
     };
     static_assert(kKC > 2, "blocks b+1 and b+2 are each in this chunk or the next");
     for (; (c + 1) * kKC <= nb; ++c) {
@@ -287,12 +340,12 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
 
     const int tok = g * 32 + tl;
     if (tok < batch) {
-        float *yr = y + (size_t)tok * ldy + r0 + 4 * h;  // row stride ldy (rows when packed)
+        float *yr = y + (size_t)tok * ldy + r0 + rbase;  // row stride ldy (rows when packed)
         if (r0 + 32 <= rows && vec) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                *reinterpret_cast<float4 *>(yr + 8 * j) = make_float4(acc[4 * j], acc[4 * j + 1], acc[4 * j + 2],
-                                                                      acc[4 * j + 3]);
+            for (int j = 0; j < NACC / 4; ++j)
+                *reinterpret_cast<float4 *>(yr + rstep * j) = make_float4(acc[4 * j], acc[4 * j + 1],
+                                                                          acc[4 * j + 2], acc[4 * j + 3]);
         } else {
             // the last tile of a row count that is not a multiple of 32, or
             // an output that float4 stores cannot reach (a stride that is
@@ -300,11 +353,36 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
             // for the rows that exist (rows past them are computed on
             // whatever their loads read, and never stored)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < NACC / 4; ++j)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    if (r0 + 4 * h + 8 * j + i < rows) yr[8 * j + i] = acc[4 * j + i];
+                    if (r0 + rbase + rstep * j + i < rows) yr[rstep * j + i] = acc[4 * j + i];
         }
+    }
+}
+
+// Row tiles [0, rt_full) in FULL waves (workgroup: one row tile, four token
+// groups), the rest in HALF waves (workgroup: one row tile, four half
+// groups); the workgroup index picks the form, so every wave of a
+// workgroup takes the same one.
+template <bool RELAXED>
+__global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const uint8_t *__restrict__ w,
+                                                                         const uint8_t *__restrict__ gp,
+                                                                         float *__restrict__ y, int rows, int nb,
+                                                                         int batch, int ngroups, int ldy, int vec,
+                                                                         int rt_full)
+{
+    __shared__ __align__(16) u32x4 sa[kNBuf][kKC][2][32];  // A chunks: [block][K half][row] 16 signed bytes
+    __shared__ __align__(16) float sdw[kNBuf][kKC][32];  // their row scales, f32
+    const int wave = threadIdx.x >> 6, wg = blockIdx.x;
+    const int nfull = rt_full * ((ngroups + kGemmWaves - 1) / kGemmWaves);
+    if (wg < nfull) {
+        gemm_tile<RELAXED, false>(w, gp, y, rows, nb, batch, ngroups, ldy, vec, wg % rt_full,
+                                  (wg / rt_full) * kGemmWaves + wave, sa, sdw);
+    } else {
+        const int rt_half = (rows + 31) / 32 - rt_full, hw = wg - nfull;
+        gemm_tile<RELAXED, true>(w, gp, y, rows, nb, batch, ngroups, ldy, vec, rt_full + hw % rt_half,
+                                 (hw / rt_half) * kGemmWaves + wave, sa, sdw);
     }
 }
 
@@ -381,13 +459,24 @@ int launch_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const void *gpack, float 
         return fail(ctx, MRML_HIP_E_INVALID, "gemm_q4_0: output stride %d below rows %d, or y not 4-byte aligned",
                     ldy, rows);
     const int vec = (ldy % 4 == 0 && ((uintptr_t)y & 15) == 0) ? 1 : 0;  // float4 stores reach every output row
-    const dim3 grid((rows + 31) / 32, (ng + kGemmWaves - 1) / kGemmWaves);
+    // FULL waves, one per (row tile, token group).  When they number just
+    // over one per SIMD (down at M = 512: 1152 for 1024), the SIMDs holding
+    // two of them set the launch's time; then only as many row tiles as
+    // give every SIMD one FULL wave stay FULL and the rest run as HALF waves
+    // (two per token group), which add a little over half a wave's work to
+    // some SIMDs instead of a whole one.
+    const int rt = (rows + 31) / 32, gq = (ng + kGemmWaves - 1) / kGemmWaves;
+    const int full_waves = rt * gq * kGemmWaves;
+    int rt_full = rt;
+    if (full_waves > kSIMDs && 2 * full_waves <= 3 * kSIMDs) rt_full = kSIMDs / (gq * kGemmWaves);
+    const int hq = (2 * ng + kGemmWaves - 1) / kGemmWaves;  // workgroups of HALF waves per row tile
+    const dim3 grid((unsigned)(rt_full * gq + (rt - rt_full) * hq));
     if (relaxed)
         hipLaunchKernelGGL(gemm_q4_0_mfma_kernel<true>, grid, dim3(64 * kGemmWaves), 0, ctx->stream, (const uint8_t *)w,
-                           (const uint8_t *)gpack, y, rows, nb, batch, ng, ldy, vec);
+                           (const uint8_t *)gpack, y, rows, nb, batch, ng, ldy, vec, rt_full);
     else
         hipLaunchKernelGGL(gemm_q4_0_mfma_kernel<false>, grid, dim3(64 * kGemmWaves), 0, ctx->stream,
-                           (const uint8_t *)w, (const uint8_t *)gpack, y, rows, nb, batch, ng, ldy, vec);
+                           (const uint8_t *)w, (const uint8_t *)gpack, y, rows, nb, batch, ng, ldy, vec, rt_full);
     return check_launch(ctx, "gemm_q4_0_mfma_kernel");
 }
 

@@ -152,6 +152,23 @@ def test_gemm_q4_0_any_rows_bit_exact(backend, dev, orc, synth, rows, cols, batc
     assert_bit_exact(run_gemm(backend, dev, w, x, rows, cols, batch, prequantised=True), ref, "pack entry")
 
 
+@pytest.mark.parametrize("rows,cols,batch", [(2300, 2304, 500), (1100, 512, 1000), (1056, 256, 1024)])
+def test_gemm_q4_0_split_tiles_bit_exact(backend, dev, orc, synth, rows, cols, batch):
+    """Products whose 32x32 tiles (one per row tile and 32-token group) number
+    just over one per SIMD (1024 on MI355X) run their last row tiles as
+    32-row x 16-token tiles on the 16x16x32 int8 MFMA: here with a partial
+    last row tile and a partial last token group among them (1152 and 1120
+    tiles), and at 1056 rows x 32 groups (1056 tiles, every tile whole)."""
+    rng = synth.rng_for(5170 + rows + cols + batch)
+    w = synth.q4_0_matrix(rng, rows, cols)
+    x = (rng.standard_normal((batch, cols)) * 10.0 ** rng.uniform(-3, 3, (batch, 1))).astype(np.float32)
+    x[batch - 1, :32] = 0.0  # a zero block in the last (HALF-tiled) token group
+    got = run_gemm(backend, dev, w, x, rows, cols, batch)
+    ref = oracle_gemm(orc, w, x, rows, cols, range(batch))
+    assert_bit_exact(got, ref, f"gemm {rows}x{cols} M={batch}")
+    assert_bit_exact(run_gemm(backend, dev, w, x, rows, cols, batch, prequantised=True), ref, "pack entry")
+
+
 def test_gemm_q4_0_qkv_geglu_any_rows(backend, dev, orc, synth):
     """The fused batched entries at row counts that are not multiples of 32
     or of 4: the k and v products then start off a 16-byte boundary of the
