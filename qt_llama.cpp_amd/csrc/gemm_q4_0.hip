@@ -37,8 +37,9 @@
 //   - B comes from a GEMM pack written in MFMA lane order (one 1 KB run of
 //     quants and one 128-byte run of scales per 32 tokens and block), read
 //     with one coalesced load each, kPF blocks ahead of use;
-//   - A is shared by the workgroup's four waves (four 32-token groups over
-//     one 32-row tile): kKC-block chunks of the 32 rows (128 contiguous bytes
+//   - A is shared by the workgroup's four waves (four 32-token groups, or
+//     four 16-token halves, over one 32-row tile): kKC-block chunks of the
+//     32 rows (128 contiguous bytes
 //     per row) and their f16 scales are loaded with coalesced loads into
 //     registers one chunk ahead, turned into signed bytes once (both K
 //     halves) and staged through kNBuf LDS buffers, one barrier per chunk.
