@@ -1311,14 +1311,20 @@ __global__ __launch_bounds__(kSplitT) void attn_split_kernel(const float *__rest
 // are in flight while the current 32 are added.  The decode form spreads
 // one long row over eight workgroups to cut its latency; a prefill chunk has
 // rows enough to fill the GPU this way.  Windows up to kRowsSvMax positions
-// (one exact block sum per head) and groups up to kRowsSvG heads.  Dynamic
-// LDS: the group's weights, G rows of `span` floats (the launch's widest
-// window), then span flag bytes.
+// (one exact block sum per head) and groups of G <= kRowsSvG heads (a
+// compile-time count, so the per-position work has no head loop or test).
+// Dynamic LDS: the group's weights, G rows of `span` floats (the launch's
+// widest window) at a stride of a multiple of 4 floats, then span flag bytes.
 constexpr int kRowsSvMax = mrml_xsum::kMaxPerThread * kAttnHD;  // 4096
 constexpr int kRowsSvG = 4;
 constexpr int kRowsSvB = 32;  // positions per load batch
-inline size_t rows_sv_lds(int g, int span) { return (size_t)g * span * sizeof(float) + ((span + 15) & ~15); }
+inline int rows_sv_stride(int span) { return (span + 3) & ~3; }
+inline size_t rows_sv_lds(int g, int span)
+{
+    return (size_t)g * rows_sv_stride(span) * sizeof(float) + ((span + 15) & ~15);
+}
 
+template <int G>
 __global__ __launch_bounds__(kAttnHD) void attn_softmax_v_rows_kernel(const float *__restrict__ scores,
                                                                       const uint16_t *__restrict__ v_cache,
                                                                       int n_past0, int n_heads, int n_kv_heads,
@@ -1330,13 +1336,14 @@ __global__ __launch_bounds__(kAttnHD) void attn_softmax_v_rows_kernel(const floa
     __shared__ mrml_xsum::Shared xs;
     __shared__ float red[HD / 64];
     __shared__ uint64_t exp_tab[32];
-    const int kvh = blockIdx.x, z = blockIdx.y, d = threadIdx.x, G = n_heads / n_kv_heads;
-    uint8_t *flags = reinterpret_cast<uint8_t *>(e_dyn + (size_t)G * span);
-    auto e_s = [&](int g) { return e_dyn + (size_t)g * span; };
+    const int kvh = blockIdx.x, z = blockIdx.y, d = threadIdx.x, stride = (span + 3) & ~3;
+    uint8_t *flags = reinterpret_cast<uint8_t *>(e_dyn + (size_t)G * stride);
+    auto e_s = [&](int g) { return e_dyn + (size_t)g * stride; };
     int window, start;
     attn_window(nullptr, n_past0 + z, wlimit, window, start);
     if (d < 32) exp_tab[d] = mrml_libm::kExpfT.t[d];
     const bool fused = expf_fused != 0;
+#pragma unroll 1
     for (int g = 0; g < G; ++g) {
         const float *sc = scores + ((size_t)z * n_heads + kvh * G + g) * capacity;
         float mx = -INFINITY;  // the max is exact in any order
@@ -1357,9 +1364,9 @@ __global__ __launch_bounds__(kAttnHD) void attn_softmax_v_rows_kernel(const floa
     __syncthreads();
     const size_t kv_dim = (size_t)n_kv_heads * HD;
     const uint16_t *vb = v_cache + (size_t)kvh * HD + d;
-    float acc[kRowsSvG];
+    float acc[G];
 #pragma unroll
-    for (int g = 0; g < kRowsSvG; ++g) acc[g] = 0.0f;
+    for (int g = 0; g < G; ++g) acc[g] = 0.0f;
     int row = (int)cache_row_of(start, capacity);  // the window's rows are consecutive modulo capacity
     // unconditional loads (row stays a cache row; positions past the window
     // are skipped by add), so all B of them are issued before any is used
@@ -1373,25 +1380,50 @@ __global__ __launch_bounds__(kAttnHD) void attn_softmax_v_rows_kernel(const floa
 #pragma unroll
         for (int k = 0; k < B; ++k) v[k] = f16_bits_to_f32(raw[k]);
     };
-    auto add = [&](const float (&v)[B], int t0) {
+    // a batch inside the window: each head's weights read four positions at
+    // a time (float4 broadcasts), no per-position test
+    auto add_full = [&](const float (&v)[B], int t0) {
+#pragma unroll
+        for (int i = 0; i < B / 4; ++i) {
+            float4 e4[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) e4[g] = reinterpret_cast<const float4 *>(e_s(g) + t0)[i];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                acc[g] = acc[g] + e4[g].x * v[4 * i];
+                acc[g] = acc[g] + e4[g].y * v[4 * i + 1];
+                acc[g] = acc[g] + e4[g].z * v[4 * i + 2];
+                acc[g] = acc[g] + e4[g].w * v[4 * i + 3];
+            }
+        }
+    };
+    // the window's last, partial batch
+    auto add_part = [&](const float (&v)[B], int t0) {
 #pragma unroll
         for (int k = 0; k < B; ++k) {
             if (t0 + k < window) {
 #pragma unroll
-                for (int g = 0; g < kRowsSvG; ++g)
-                    if (g < G) acc[g] = acc[g] + e_dyn[(size_t)g * span + t0 + k] * v[k];
+                for (int g = 0; g < G; ++g) acc[g] = acc[g] + e_s(g)[t0 + k] * v[k];
             }
         }
     };
     float va[B], vb2[B];
     load(va, 0);
-    for (int t0 = 0; t0 < window; t0 += 2 * B) {
-        if (t0 + B < window) load(vb2, t0 + B);  // in flight while va is added
-        add(va, t0);
-        if (t0 + B >= window) break;
-        if (t0 + 2 * B < window) load(va, t0 + 2 * B);
-        add(vb2, t0 + B);
+    int t0 = 0;
+    for (; t0 + 2 * B <= window; t0 += 2 * B) {
+        load(vb2, t0 + B);  // in flight while va is added
+        add_full(va, t0);
+        load(va, t0 + 2 * B);
+        add_full(vb2, t0 + B);
     }
+    if (t0 + B <= window) {
+        load(vb2, t0 + B);
+        add_full(va, t0);
+        add_part(vb2, t0 + B);
+    } else {
+        add_part(va, t0);
+    }
+#pragma unroll
     for (int g = 0; g < G; ++g) out[((size_t)z * n_heads + kvh * G + g) * HD + d] = acc[g];
 }
 
@@ -1749,9 +1781,17 @@ int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *q, int q_stride, const 
     // a launch takes up to about 69 KB, within gfx950's 160 KiB a workgroup
     if (span <= kRowsSvMax && n_heads / n_kv_heads <= kRowsSvG &&
         rows_sv_lds(n_heads / n_kv_heads, span) <= (size_t)60 << 10) {
-        hipLaunchKernelGGL(attn_softmax_v_rows_kernel, dim3(n_kv_heads, rows), dim3(kAttnHD),
-                           rows_sv_lds(n_heads / n_kv_heads, span), ctx->stream, scores, v_cache, n_past0, n_heads,
-                           n_kv_heads, capacity, wlimit, (int)host_expf_fused(), out, span);
+#define ROWS_SV(G)                                                                                              \
+    hipLaunchKernelGGL(attn_softmax_v_rows_kernel<G>, dim3(n_kv_heads, rows), dim3(kAttnHD),                     \
+                       rows_sv_lds(n_heads / n_kv_heads, span), ctx->stream, scores, v_cache, n_past0, n_heads,   \
+                       n_kv_heads, capacity, wlimit, (int)host_expf_fused(), out, span)
+        switch (n_heads / n_kv_heads) {
+        case 1: ROWS_SV(1); break;
+        case 2: ROWS_SV(2); break;
+        case 3: ROWS_SV(3); break;
+        default: ROWS_SV(4); break;
+        }
+#undef ROWS_SV
         return check_launch(ctx, "attn_softmax_v_rows_kernel");
     }
     return launch_softmax_v(ctx, scores, v_cache, out, nullptr, nullptr, n_past0, n_heads, n_kv_heads, capacity, wlimit,

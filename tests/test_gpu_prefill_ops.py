@@ -270,10 +270,11 @@ def rows_form(nh, nkv, span):
     """Whether attention_prefill runs attn_softmax_v_rows_kernel (the form
     whose workgroup serves a kv head's whole group) rather than the
     per-head attn_softmax_v_kernel: windows up to 4096, groups up to 4, and
-    the group's weights plus span flag bytes within 60 KiB of dynamic LDS
+    the group's weights (a row of span floats per head, at a stride rounded
+    up to 4 floats) plus span flag bytes within 60 KiB of dynamic LDS
     (launch_attn_rows_f16 in decode.hip)."""
     g = nh // nkv
-    return span <= 4096 and g <= 4 and g * span * 4 + ((span + 15) & ~15) <= 60 << 10
+    return span <= 4096 and g <= 4 and g * ((span + 3) & ~3) * 4 + ((span + 15) & ~15) <= 60 << 10
 
 
 def test_prefill_cases_cover_both_forms():
