@@ -814,6 +814,101 @@ __global__ __launch_bounds__(kScoreT) void attn_scores2_kernel(const float *__re
     if (p0 + p < window) scores[(size_t)(kvh * G + g) * capacity + p0 + p] = dot * scale;
 }
 
+// Prefill form of the scores: positions tiled absolutely, so one K tile
+// serves several query rows.  Workgroup (tile of 64 positions T0.., kv head,
+// block of RB = 8 / G consecutive query rows): the tile's K rows are staged
+// in LDS once, then wave w runs row w / G, head w % G of the group, lane p
+// the chain of position T0 + p when the row's window holds it (the same
+// arithmetic as attn_scores2_kernel: q . k from -0.0 in dim order, one
+// product and one add per dim, times scale), stored at the position's index
+// in that row's window.  Row z's position is n_past0 + z; t_lo is row 0's
+// window start.
+constexpr int kSRowsW = 8;  // waves per workgroup
+template <int G>
+__global__ __launch_bounds__(64 * kSRowsW) void attn_scores_rows_kernel(const float *__restrict__ q_in, int q_stride,
+                                                                      const uint16_t *__restrict__ k_cache,
+                                                                      int n_past0, int rows, int n_heads,
+                                                                      int n_kv_heads, float scale, int capacity,
+                                                                      int wlimit, int t_lo, float *__restrict__ scores)
+{
+    constexpr int HD = kAttnHD, P = kScoreP, RB = kSRowsW / G, NT = 64 * kSRowsW;
+    __shared__ __align__(16) float q_s[RB * G][HD];
+    __shared__ __align__(16) uint8_t k_s[P * kKRow2];
+    const int T0 = t_lo + (int)blockIdx.x * P, kvh = blockIdx.y, z0 = (int)blockIdx.z * RB, tid = threadIdx.x;
+    const int zl = (z0 + RB < rows ? z0 + RB : rows) - 1;  // the block's last row
+    int win0, start0, winl, startl;
+    attn_window(nullptr, n_past0 + z0, wlimit, win0, start0);
+    attn_window(nullptr, n_past0 + zl, wlimit, winl, startl);
+    const int pos_l = n_past0 + zl;
+    if (T0 > pos_l || T0 + P - 1 < start0) return;  // no row of the block has a position in this tile
+    const size_t kv_dim = (size_t)n_kv_heads * HD;
+    // K tile: 2048 chunks of 16 B (positions past the block's newest one
+    // reload that row; their scores are not stored)
+    constexpr int kChunks = P * (HD * 2 / 16), kPer = kChunks / NT;
+    u32x4 tmp[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int c = k * NT + tid, r = c >> 5;
+        const int t = T0 + r <= pos_l ? T0 + r : pos_l;
+        tmp[k] = reinterpret_cast<const u32x4 *>(k_cache + cache_row_of(t, capacity) * kv_dim + (size_t)kvh * HD)[c & 31];
+    }
+    // q of the block's rows and the group's heads: RB*G*HD floats, float4 each
+    for (int i = tid; i < RB * G * HD / 4; i += NT) {
+        const int w = i / (HD / 4), e = i % (HD / 4), r = w / G, g = w % G;
+        const int z = z0 + r < rows ? z0 + r : rows - 1;
+        reinterpret_cast<float4 *>(q_s[w])[e] =
+            reinterpret_cast<const float4 *>(q_in + (size_t)z * q_stride + (size_t)(kvh * G + g) * HD)[e];
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int c = k * NT + tid, r = c >> 5;
+        *reinterpret_cast<u32x4 *>(k_s + r * kKRow2 + (c & 31) * 16) = tmp[k];
+    }
+    __syncthreads();
+    const int w = tid >> 6, p = tid & 63;
+    if (w >= RB * G) return;
+    const int r = w / G, g = w % G, z = z0 + r, t = T0 + p;
+    if (z >= rows) return;
+    int window, start;
+    attn_window(nullptr, n_past0 + z, wlimit, window, start);
+    const u32x4 *krow = reinterpret_cast<const u32x4 *>(k_s + p * kKRow2);
+    const float4 *qg = reinterpret_cast<const float4 *>(q_s[w]);
+    float nz;
+    asm volatile("v_mov_b32 %0, 0x80000000" : "=v"(nz));
+    float dot = -0.0f;
+    constexpr int kSteps = HD / 32;
+    u32x4 kw[2][4];
+    float4 qa[2][8];
+    auto fetch = [&](int st, int b) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            kw[b][u] = krow[4 * st + u];
+            qa[b][2 * u] = qg[2 * (4 * st + u)];
+            qa[b][2 * u + 1] = qg[2 * (4 * st + u) + 1];
+        }
+    };
+    fetch(0, 0);
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) {
+        const int b = st & 1;
+        if (st + 1 < kSteps) fetch(st + 1, b ^ 1);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const u32x4 wv = kw[b][u];
+            const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+            const float qv[8] = {qa[b][2 * u].x, qa[b][2 * u].y, qa[b][2 * u].z, qa[b][2 * u].w,
+                                 qa[b][2 * u + 1].x, qa[b][2 * u + 1].y, qa[b][2 * u + 1].z, qa[b][2 * u + 1].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const _Float16 kh = __builtin_bit_cast(_Float16, (uint16_t)(wd[e >> 1] >> (16 * (e & 1))));
+                dot = dot + __builtin_fmaf(qv[e], (float)kh, nz);
+            }
+        }
+    }
+    if (t >= start && t < start + window)
+        scores[((size_t)z * n_heads + kvh * G + g) * capacity + (t - start)] = dot * scale;
+}
+
 // Softmax and weighted values, query head h, dims [32*ds, 32*ds + 32) per
 // workgroup (blockIdx = (h, ds)):  max over the window; e_p = expf(score_p -
 // max); sum = 0 + e_0 + e_1 + ... in order; p_p = e_p * (1/sum); out[d] = 0 +
@@ -1765,11 +1860,30 @@ int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *q, int q_stride, const 
     // score tiles up to the widest row window (the host knows every row's position)
     const int span = std::min(wlimit, n_past0 + rows);
     const dim3 sgrid((span + kScoreP - 1) / kScoreP, n_kv_heads, rows);
-    if (attn_rope_ok(n_heads, n_kv_heads)) {
+    if (attn_rope_ok(n_heads, n_kv_heads) && (q_stride % 4 != 0 || ((uintptr_t)q & 15) != 0)) {
+        // q rows that float4 reads cannot reach: one workgroup per row and tile
         hipLaunchKernelGGL(attn_scores2_kernel<false>, sgrid, dim3(kScoreT), 0, ctx->stream, q,
                            const_cast<uint16_t *>(k_cache), (uint16_t *)nullptr, (const int32_t *)nullptr, n_past0,
                            n_heads, n_kv_heads, scale, capacity, wlimit, RopeArgs{}, scores, q_stride);
         if (int rc = check_launch(ctx, "attn_scores2_kernel")) return rc;
+    } else if (attn_rope_ok(n_heads, n_kv_heads)) {
+        // positions tiled absolutely from row 0's window start to the last
+        // row's position, 8 / G rows a workgroup
+        const int g = n_heads / n_kv_heads, rb = kSRowsW / g;
+        const int count0 = n_past0 + 1, t_lo = count0 > wlimit ? count0 - wlimit : 0, t_hi = n_past0 + rows - 1;
+        const dim3 rgrid((unsigned)((t_hi - t_lo + kScoreP) / kScoreP), (unsigned)n_kv_heads,
+                         (unsigned)((rows + rb - 1) / rb));
+#define SCORES_ROWS(G)                                                                                          \
+    hipLaunchKernelGGL(attn_scores_rows_kernel<G>, rgrid, dim3(64 * kSRowsW), 0, ctx->stream, q, q_stride,       \
+                       k_cache, n_past0, rows, n_heads, n_kv_heads, scale, capacity, wlimit, t_lo, scores)
+        switch (g) {
+        case 1: SCORES_ROWS(1); break;
+        case 2: SCORES_ROWS(2); break;
+        case 3: SCORES_ROWS(3); break;
+        default: SCORES_ROWS(4); break;
+        }
+#undef SCORES_ROWS
+        if (int rc = check_launch(ctx, "attn_scores_rows_kernel")) return rc;
     } else {
         hipLaunchKernelGGL(attn_scores_kernel, sgrid, dim3(64 * (n_heads / n_kv_heads)), 0, ctx->stream, q, k_cache,
                            (const int32_t *)nullptr, n_past0, n_heads, n_kv_heads, scale, capacity, wlimit, scores,

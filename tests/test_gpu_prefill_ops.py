@@ -340,6 +340,30 @@ def test_attention_prefill_matches_causal_rows(backend, dev):
         qi.close()
 
 
+@pytest.mark.parametrize("pad", [1, 4])
+def test_attention_prefill_q_stride(backend, dev, orc, pad):
+    """Query rows pad floats apart beyond n_heads*head_dim: a stride that
+    16-byte reads cannot follow (pad 1: the rows' scores take the one-row
+    workgroup form) and one they can (pad 4: the multi-row form), each row
+    bit-exact against the CPU attention."""
+    nh, nkv, hd, cap, start, batch = 8, 4, 256, 512, 100, 40
+    rng = np.random.default_rng(4700 + pad)
+    qd, kvd, stride = nh * hd, nkv * hd, nh * hd + pad
+    q = (rng.standard_normal(batch * stride) * 0.5).astype(np.float32)
+    kc = rng.standard_normal(cap * kvd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(cap * kvd).astype(np.float16).view(np.uint16)
+    qb, kb, vb = (backend.HipBuffer.from_host(dev, a) for a in (q, kc, vc))
+    out = backend.HipBuffer.alloc(dev, batch * qd)
+    dev.attention_prefill(qb, kb, vb, out, start, batch, nh, nkv, hd, 1.0 / 16.0, None, cap, q_stride=stride)
+    dev.sync()
+    got = out.numpy().reshape(batch, qd)
+    for i in range(batch):
+        rows = window_rows(start + i, None, cap)
+        ref = orc.attention_f16(q[i * stride:i * stride + qd], kc.reshape(cap, kvd)[rows].reshape(-1),
+                                vc.reshape(cap, kvd)[rows].reshape(-1), len(rows) - 1, nh, nkv, hd, 1.0 / 16.0)
+        assert_bits(got[i], ref, f"q stride {stride}: row {i}")
+
+
 def test_attention_prefill_invalid(backend, dev):
     nh, nkv, hd = 8, 4, 256
     qb = backend.HipBuffer.alloc(dev, 4 * nh * hd)
