@@ -131,6 +131,17 @@ __device__ __forceinline__ int sbytes(uint32_t v, int sh)
 // global loads (the operand prefetch) stay in flight.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Up to three weight matrices stacked by rows (q|k|v) for one launch: row
+// tile rt (32 rows) of the stack belongs to the matrix whose row range holds
+// it (every matrix but the last a multiple of 32 rows), and its outputs go
+// to the stacked output column r (y rows hold the stack).
+constexpr int kGemmMaxMats = 3;
+struct GemmMats {
+    const uint8_t *w[kGemmMaxMats];
+    int rows[kGemmMaxMats];
+    int n;
+};
+
 struct BOps {
     u32x4 a;   // the token's 16 quants of this K half
     float da;  // the token's block scale
@@ -152,7 +163,7 @@ struct BOps {
 // reads, so it serves only to spread a product whose FULL tiles number just
 // over one per SIMD (the launch below).
 template <bool RELAXED, bool HALF>
-__device__ __forceinline__ void gemm_tile(const uint8_t *__restrict__ w, const uint8_t *__restrict__ gp,
+__device__ __forceinline__ void gemm_tile(const GemmMats &mats, const uint8_t *__restrict__ gp,
                                           float *__restrict__ y, int rows, int nb, int batch, int ngroups, int ldy,
                                           int vec, int rt, int gsel, u32x4 (&sa)[kNBuf][kKC][2][32],
                                           float (&sdw)[kNBuf][kKC][32])
@@ -167,19 +178,23 @@ __device__ __forceinline__ void gemm_tile(const uint8_t *__restrict__ w, const u
     const int q = lane >> 4, h = lane >> 5;                            // HALF: K quarter; FULL: K half
     const int rbase = HALF ? 4 * q : 4 * h;                           // first row of the lane's outputs
     constexpr int rstep = HALF ? 16 : 8;                              // rows between its output quads
-    const uint32_t qs_bytes = (uint32_t)rows * nb * 16;
+    // the tile's matrix (uniform): local rows r0 - mbase of mrows
+    int m = 0, mbase = 0;
+    while (m + 1 < mats.n && r0 >= mbase + mats.rows[m]) mbase += mats.rows[m++];
+    const int mrows = mats.rows[m], r0l = r0 - mbase;
+    const uint32_t qs_bytes = (uint32_t)mrows * nb * 16;
     // Loads past a row's last block read the next row or, past the end of a
     // buffer, zeros (buffer range check); such blocks are never folded.
-    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void *)w, (short)0,
-                                                                        (int)(qs_bytes + (uint32_t)rows * nb * 2),
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void *)mats.w[m], (short)0,
+                                                                        (int)(qs_bytes + (uint32_t)mrows * nb * 2),
                                                                         kBufferFlags);
     const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
         (void *)gp, (short)0, (int)((uint32_t)ngroups * nb * 1152), kBufferFlags);
 
     // A chunk c: thread (row ar, block ak) loads 16 quant bytes and one f16 scale.
     const int ar = tid >> 3, ak = tid & 7;
-    const uint32_t a_off = ((uint32_t)(r0 + ar) * nb + ak) * 16;
-    const uint32_t s_off = qs_bytes + ((uint32_t)(r0 + ar) * nb + ak) * 2;
+    const uint32_t a_off = ((uint32_t)(r0l + ar) * nb + ak) * 16;
+    const uint32_t s_off = qs_bytes + ((uint32_t)(r0l + ar) * nb + ak) * 2;
     u32x4 areg;
     uint32_t sreg;
     auto load_chunk = [&](int c) {
@@ -367,7 +382,7 @@ __device__ __forceinline__ void gemm_tile(const uint8_t *__restrict__ w, const u
 // groups); the workgroup index picks the form, so every wave of a
 // workgroup takes the same one.
 template <bool RELAXED>
-__global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const uint8_t *__restrict__ w,
+__global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const GemmMats mats,
                                                                          const uint8_t *__restrict__ gp,
                                                                          float *__restrict__ y, int rows, int nb,
                                                                          int batch, int ngroups, int ldy, int vec,
@@ -378,11 +393,11 @@ __global__ __launch_bounds__(64 * kGemmWaves) void gemm_q4_0_mfma_kernel(const u
     const int wave = threadIdx.x >> 6, wg = blockIdx.x;
     const int nfull = rt_full * ((ngroups + kGemmWaves - 1) / kGemmWaves);
     if (wg < nfull) {
-        gemm_tile<RELAXED, false>(w, gp, y, rows, nb, batch, ngroups, ldy, vec, wg % rt_full,
+        gemm_tile<RELAXED, false>(mats, gp, y, rows, nb, batch, ngroups, ldy, vec, wg % rt_full,
                                   (wg / rt_full) * kGemmWaves + wave, sa, sdw);
     } else {
         const int rt_half = (rows + 31) / 32 - rt_full, hw = wg - nfull;
-        gemm_tile<RELAXED, true>(w, gp, y, rows, nb, batch, ngroups, ldy, vec, rt_full + hw % rt_half,
+        gemm_tile<RELAXED, true>(mats, gp, y, rows, nb, batch, ngroups, ldy, vec, rt_full + hw % rt_half,
                                  (hw / rt_half) * kGemmWaves + wave, sa, sdw);
     }
 }
@@ -451,8 +466,8 @@ int launch_gemm_pack_from_act(mrml_hip_ctx *ctx, const void *pack, void *gpack, 
     return check_launch(ctx, "gemm_pack_from_act_kernel");
 }
 
-int launch_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const void *gpack, float *y, int32_t rows, int32_t cols,
-                     int32_t batch, int32_t ldy, bool relaxed)
+static int launch_gemm_mats(mrml_hip_ctx *ctx, const GemmMats &mats, const void *gpack, float *y, int32_t rows,
+                            int32_t cols, int32_t batch, int32_t ldy, bool relaxed)
 {
     const int nb = cols / 32, ng = gemm_groups(batch);
     if (ldy == 0) ldy = rows;
@@ -473,12 +488,54 @@ int launch_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const void *gpack, float 
     const int hq = (2 * ng + kGemmWaves - 1) / kGemmWaves;  // workgroups of HALF waves per row tile
     const dim3 grid((unsigned)(rt_full * gq + (rt - rt_full) * hq));
     if (relaxed)
-        hipLaunchKernelGGL(gemm_q4_0_mfma_kernel<true>, grid, dim3(64 * kGemmWaves), 0, ctx->stream, (const uint8_t *)w,
+        hipLaunchKernelGGL(gemm_q4_0_mfma_kernel<true>, grid, dim3(64 * kGemmWaves), 0, ctx->stream, mats,
                            (const uint8_t *)gpack, y, rows, nb, batch, ng, ldy, vec, rt_full);
     else
-        hipLaunchKernelGGL(gemm_q4_0_mfma_kernel<false>, grid, dim3(64 * kGemmWaves), 0, ctx->stream,
-                           (const uint8_t *)w, (const uint8_t *)gpack, y, rows, nb, batch, ng, ldy, vec, rt_full);
+        hipLaunchKernelGGL(gemm_q4_0_mfma_kernel<false>, grid, dim3(64 * kGemmWaves), 0, ctx->stream, mats,
+                           (const uint8_t *)gpack, y, rows, nb, batch, ng, ldy, vec, rt_full);
     return check_launch(ctx, "gemm_q4_0_mfma_kernel");
+}
+
+int launch_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const void *gpack, float *y, int32_t rows, int32_t cols,
+                     int32_t batch, int32_t ldy, bool relaxed)
+{
+    GemmMats mats{};
+    mats.w[0] = (const uint8_t *)w;
+    mats.rows[0] = rows;
+    mats.n = 1;
+    return launch_gemm_mats(ctx, mats, gpack, y, rows, cols, batch, ldy, relaxed);
+}
+
+// Up to three products over one GEMM pack in one launch, their outputs
+// stacked along y's rows (matrix m's rows start after those of the earlier
+// ones): every matrix but the last a multiple of 32 rows, so no row tile
+// straddles two.  Otherwise, one launch each at its offset.
+int launch_gemm_q4_0_stacked(mrml_hip_ctx *ctx, const void *const *w, const int32_t *rows, int n, const void *gpack,
+                             float *y, int32_t cols, int32_t batch, int32_t ldy, bool relaxed)
+{
+    if (n < 1 || n > kGemmMaxMats) return fail(ctx, MRML_HIP_E_INVALID, "gemm_q4_0: %d stacked matrices", n);
+    int total = 0;
+    bool tiles = true;
+    for (int m = 0; m < n; ++m) {
+        total += rows[m];
+        tiles = tiles && (m + 1 == n || rows[m] % 32 == 0);
+    }
+    if (!tiles) {
+        int off = 0;
+        for (int m = 0; m < n; ++m) {
+            if (int rc = launch_gemm_q4_0(ctx, w[m], gpack, y + off, rows[m], cols, batch, ldy ? ldy : total, relaxed))
+                return rc;
+            off += rows[m];
+        }
+        return MRML_HIP_OK;
+    }
+    GemmMats mats{};
+    for (int m = 0; m < n; ++m) {
+        mats.w[m] = (const uint8_t *)w[m];
+        mats.rows[m] = rows[m];
+    }
+    mats.n = n;
+    return launch_gemm_mats(ctx, mats, gpack, y, total, cols, batch, ldy, relaxed);
 }
 
 }  // namespace mrml

@@ -106,6 +106,8 @@ int gemm_noalloc_scratch(mrml_hip_ctx *ctx, void **out);
 // y row stride ldy floats (0: rows; a multiple of 4, y 16-byte aligned)
 int launch_gemm_q4_0(mrml_hip_ctx *ctx, const void *w, const void *gpack, float *y, int32_t rows, int32_t cols,
                      int32_t batch, int32_t ldy = 0, bool relaxed = false);
+int launch_gemm_q4_0_stacked(mrml_hip_ctx *ctx, const void *const *w, const int32_t *rows, int n, const void *gpack,
+                             float *y, int32_t cols, int32_t batch, int32_t ldy, bool relaxed = false);
 
 // Argmax whose final pass can also advance a device-side decode loop
 // (state = {token, pos}) and record the processed token in the recent-token

@@ -686,9 +686,11 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
             const float *next_norm = l + 1 < c.n_layers ? m->layers[l + 1].attn_norm : m->output_norm;
             // q, k, v of the chunk, stacked per token as the token step's q|k|v
             STEP(launch_gemm_pack_quantize(ctx, xn, m->pf_gpack, c.dim, n));
-            STEP(launch_gemm_q4_0(ctx, L.wq, m->pf_gpack, m->pf_qkv, qd, c.dim, n, qkvd, fast));
-            STEP(launch_gemm_q4_0(ctx, L.wk, m->pf_gpack, m->pf_qkv + qd, kvd, c.dim, n, qkvd, fast));
-            STEP(launch_gemm_q4_0(ctx, L.wv, m->pf_gpack, m->pf_qkv + qd + kvd, kvd, c.dim, n, qkvd, fast));
+            {
+                const void *qkv_w[3] = {L.wq, L.wk, L.wv};
+                const int32_t qkv_rows[3] = {qd, kvd, kvd};
+                STEP(launch_gemm_q4_0_stacked(ctx, qkv_w, qkv_rows, 3, m->pf_gpack, m->pf_qkv, c.dim, n, qkvd, fast));
+            }
             if ((int64_t)p0 + n > c.ctx_len) {
                 // The chunk wraps the ring: a later token's K/V row replaces
                 // a position an earlier token still attends to, so each token

@@ -681,12 +681,13 @@ int mrml_hip_gemm_q4_0_qkv(mrml_hip_ctx *ctx, const void *wq, const void *wk, co
     REQUIRE(ctx, (int64_t)batch * total <= INT32_MAX, "gemm_q4_0_qkv: batch=%d too large", batch);
     void *gp = workspace(ctx, gemm_pack_bytes(cols, batch));
     if (!gp) return MRML_HIP_E_ALLOC;
-    // one GEMM pack for the three products; each writes its column range of
-    // the stacked [batch][q | k | v] rows (row stride q_rows + 2*kv_rows)
+    // one GEMM pack for the three products, run as one launch over the
+    // stacked rows; each writes its column range of the stacked
+    // [batch][q | k | v] rows (row stride q_rows + 2*kv_rows)
     if (int rc = launch_gemm_pack_quantize(ctx, x, gp, cols, batch)) return rc;
-    if (int rc = launch_gemm_q4_0(ctx, wq, gp, y, q_rows, cols, batch, total)) return rc;
-    if (int rc = launch_gemm_q4_0(ctx, wk, gp, y + q_rows, kv_rows, cols, batch, total)) return rc;
-    return launch_gemm_q4_0(ctx, wv, gp, y + q_rows + kv_rows, kv_rows, cols, batch, total);
+    const void *w3[3] = {wq, wk, wv};
+    const int32_t r3[3] = {q_rows, kv_rows, kv_rows};
+    return launch_gemm_q4_0_stacked(ctx, w3, r3, 3, gp, y, cols, batch, total);
 }
 
 int mrml_hip_gemm_q4_0_geglu(mrml_hip_ctx *ctx, const void *wg, const void *wu, const float *x, float *act,
