@@ -834,7 +834,10 @@ __global__ __launch_bounds__(64 * kSRowsW) void attn_scores_rows_kernel(const fl
     constexpr int HD = kAttnHD, P = kScoreP, RB = kSRowsW / G, NT = 64 * kSRowsW;
     __shared__ __align__(16) float q_s[RB * G][HD];
     __shared__ __align__(16) uint8_t k_s[P * kKRow2];
-    const int T0 = t_lo + (int)blockIdx.x * P, kvh = blockIdx.y, z0 = (int)blockIdx.z * RB, tid = threadIdx.x;
+    // row blocks in reverse order: the latest rows, with the most tiles, are
+    // dispatched first, so the launch does not end on them
+    const int T0 = t_lo + (int)blockIdx.x * P, kvh = blockIdx.y, tid = threadIdx.x;
+    const int z0 = ((int)gridDim.z - 1 - (int)blockIdx.z) * RB;
     const int zl = (z0 + RB < rows ? z0 + RB : rows) - 1;  // the block's last row
     int win0, start0, winl, startl;
     attn_window(nullptr, n_past0 + z0, wlimit, win0, start0);
@@ -1431,7 +1434,9 @@ __global__ __launch_bounds__(kAttnHD) void attn_softmax_v_rows_kernel(const floa
     __shared__ mrml_xsum::Shared xs;
     __shared__ float red[HD / 64];
     __shared__ uint64_t exp_tab[32];
-    const int kvh = blockIdx.x, z = blockIdx.y, d = threadIdx.x, stride = (span + 3) & ~3;
+    // rows in reverse order: the longest windows are dispatched first, so the
+    // launch does not end on them
+    const int kvh = blockIdx.x, z = (int)gridDim.y - 1 - (int)blockIdx.y, d = threadIdx.x, stride = (span + 3) & ~3;
     uint8_t *flags = reinterpret_cast<uint8_t *>(e_dyn + (size_t)G * stride);
     auto e_s = [&](int g) { return e_dyn + (size_t)g * stride; };
     int window, start;
