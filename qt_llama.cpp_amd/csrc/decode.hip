@@ -1422,7 +1422,9 @@ inline size_t rows_sv_lds(int g, int span)
     return (size_t)g * rows_sv_stride(span) * sizeof(float) + ((span + 15) & ~15);
 }
 
-template <int G>
+// SHORT (windows up to 4 * kAttnHD): thread d takes positions 4d..4d+3, its
+// exps stay in registers for the register form of the exact sum.
+template <int G, bool SHORT>
 __global__ __launch_bounds__(kAttnHD) void attn_softmax_v_rows_kernel(const float *__restrict__ scores,
                                                                       const uint16_t *__restrict__ v_cache,
                                                                       int n_past0, int n_heads, int n_kv_heads,
@@ -1431,7 +1433,6 @@ __global__ __launch_bounds__(kAttnHD) void attn_softmax_v_rows_kernel(const floa
 {
     constexpr int HD = kAttnHD, B = kRowsSvB;
     extern __shared__ __align__(16) float e_dyn[];  // [G][span] weights, then span flag bytes
-    __shared__ mrml_xsum::Shared xs;
     __shared__ float red[HD / 64];
     __shared__ uint64_t exp_tab[32];
     // rows in reverse order: the longest windows are dispatched first, so the
@@ -1443,6 +1444,33 @@ __global__ __launch_bounds__(kAttnHD) void attn_softmax_v_rows_kernel(const floa
     attn_window(nullptr, n_past0 + z, wlimit, window, start);
     if (d < 32) exp_tab[d] = mrml_libm::kExpfT.t[d];
     const bool fused = expf_fused != 0;
+    if constexpr (SHORT) {
+        __shared__ mrml_xsum::Shared4 xs4;
+        const int p = 4 * d;
+#pragma unroll 1
+        for (int g = 0; g < G; ++g) {
+            const float *sc = scores + ((size_t)z * n_heads + kvh * G + g) * capacity;
+            float sv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sv[i] = p + i < window ? sc[p + i] : -INFINITY;
+            float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));  // the max is exact in any order
+            mx = wave_max_f32(mx);
+            if ((d & 63) == 0) red[d >> 6] = mx;
+            __syncthreads();
+            mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+            float e[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) e[i] = p + i < window ? mrml_libm::expf_t(sv[i] - mx, fused, exp_tab) : 0.0f;
+            // (its first barrier also orders every thread's read of red
+            // before the next head rewrites it)
+            const float sum = mrml_xsum::block_seq_sum_nonneg4(make_float4(e[0], e[1], e[2], e[3]), window, xs4);
+            const float inv = sum > 0.0f ? 1.0f / sum : 1.0f;
+            float *eg = e_s(g);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (p + i < window) eg[p + i] = sum > 0.0f ? e[i] * inv : e[i];
+        }
+    } else {
 #pragma unroll 1
     for (int g = 0; g < G; ++g) {
         const float *sc = scores + ((size_t)z * n_heads + kvh * G + g) * capacity;
@@ -1455,11 +1483,13 @@ __global__ __launch_bounds__(kAttnHD) void attn_softmax_v_rows_kernel(const floa
         float *eg = e_s(g);
         for (int p = d; p < window; p += HD) eg[p] = mrml_libm::expf_t(sc[p] - mx, fused, exp_tab);
         __syncthreads();  // also: every thread has read red before the next head rewrites it
+        __shared__ mrml_xsum::Shared xs;
         const float sum = mrml_xsum::block_seq_sum_nonneg(eg, window, flags, xs);  // ends with a barrier
         if (sum > 0.0f) {
             const float inv = 1.0f / sum;
             for (int p = d; p < window; p += HD) eg[p] = eg[p] * inv;
         }
+    }
     }
     __syncthreads();
     const size_t kv_dim = (size_t)n_kv_heads * HD;
@@ -1900,15 +1930,16 @@ int launch_attn_rows_f16(mrml_hip_ctx *ctx, const float *q, int q_stride, const 
     // a launch takes up to about 69 KB, within gfx950's 160 KiB a workgroup
     if (span <= kRowsSvMax && n_heads / n_kv_heads <= kRowsSvG &&
         rows_sv_lds(n_heads / n_kv_heads, span) <= (size_t)60 << 10) {
-#define ROWS_SV(G)                                                                                              \
-    hipLaunchKernelGGL(attn_softmax_v_rows_kernel<G>, dim3(n_kv_heads, rows), dim3(kAttnHD),                     \
+#define ROWS_SV(G, S)                                                                                           \
+    hipLaunchKernelGGL((attn_softmax_v_rows_kernel<G, S>), dim3(n_kv_heads, rows), dim3(kAttnHD),                \
                        rows_sv_lds(n_heads / n_kv_heads, span), ctx->stream, scores, v_cache, n_past0, n_heads,   \
                        n_kv_heads, capacity, wlimit, (int)host_expf_fused(), out, span)
+        const bool sh = span <= 4 * kAttnHD;
         switch (n_heads / n_kv_heads) {
-        case 1: ROWS_SV(1); break;
-        case 2: ROWS_SV(2); break;
-        case 3: ROWS_SV(3); break;
-        default: ROWS_SV(4); break;
+        case 1: if (sh) ROWS_SV(1, true); else ROWS_SV(1, false); break;
+        case 2: if (sh) ROWS_SV(2, true); else ROWS_SV(2, false); break;
+        case 3: if (sh) ROWS_SV(3, true); else ROWS_SV(3, false); break;
+        default: if (sh) ROWS_SV(4, true); else ROWS_SV(4, false); break;
         }
 #undef ROWS_SV
         return check_launch(ctx, "attn_softmax_v_rows_kernel");
