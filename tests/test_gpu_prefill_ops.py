@@ -257,7 +257,11 @@ PREFILL_CASES = [(0, 16, None, 16, 8, 4, True), (128, 37, None, 512, 8, 4, True)
                  (3000, 20, None, 4096, 8, 4, True), (3900, 9, None, 4096, 16, 4, False),
                  # the rows form at groups of 4 and 3 (spans ~2000-4000)
                  (1990, 10, None, 4096, 16, 4, False), (3290, 10, None, 4096, 16, 4, True),
-                 (2490, 12, None, 4096, 12, 4, False), (3990, 6, None, 4096, 12, 4, True)]
+                 (2490, 12, None, 4096, 12, 4, False), (3990, 6, None, 4096, 12, 4, True),
+                 # windows up to 1024 (each thread's exps in registers) at groups
+                 # of 4 and 3, and both sides of that bound (spans 1024, 1025)
+                 (500, 24, None, 4096, 16, 4, False), (900, 30, None, 1024, 12, 4, True),
+                 (1000, 24, None, 4096, 8, 4, True), (1001, 24, None, 4096, 8, 4, False)]
 
 
 def prefill_span(cache_start, batch, sw, cap):
