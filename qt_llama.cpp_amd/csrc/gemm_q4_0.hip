@@ -85,16 +85,30 @@ __device__ __forceinline__ void gemm_pack_put(uint8_t *gp, int ngroups, int nb, 
 
 // quant.rs:193-228 per block (q8_0_block8x4), written as a GEMM pack.  One
 // workgroup per (group, block): thread 8t+l handles token 32g+t, values
-// 4l..4l+3 of block b.  Tokens past `batch` are written as zeros.
-__global__ __launch_bounds__(256) void quantize_gemm_pack_kernel(const float *__restrict__ x, uint8_t *__restrict__ gp,
-                                                                 int nb, int batch, int ngroups)
+// 4l..4l+3 of block b.  Tokens past `batch` are written as zeros.  GEGLU:
+// the values quantized are gelu_tanh(x) * u elementwise (the GeGLU epilogue
+// of the matvec kernels, model.rs:2093-2105), formed in registers, so the
+// down projection's pack comes straight from the gate and up products.
+template <bool GEGLU>
+__global__ __launch_bounds__(256) void quantize_gemm_pack_kernel(const float *__restrict__ x,
+                                                                 const float *__restrict__ u,
+                                                                 uint8_t *__restrict__ gp, int nb, int batch,
+                                                                 int ngroups)
 {
     const int g = blockIdx.x / nb, b = blockIdx.x - g * nb;
     const int t = threadIdx.x >> 3, l = threadIdx.x & 7, m = 32 * g + t;
     const int ms = m < batch ? m : batch - 1;  // every lane takes part in the block reductions
     uint32_t dbits;
     int s;
-    const float4 v = reinterpret_cast<const float4 *>(x)[((size_t)ms * nb + b) * 8 + l];
+    const size_t i4 = ((size_t)ms * nb + b) * 8 + l;
+    float4 v = reinterpret_cast<const float4 *>(x)[i4];
+    if constexpr (GEGLU) {
+        const float4 w = reinterpret_cast<const float4 *>(u)[i4];
+        v.x = gelu_tanh(v.x) * w.x;
+        v.y = gelu_tanh(v.y) * w.y;
+        v.z = gelu_tanh(v.z) * w.z;
+        v.w = gelu_tanh(v.w) * w.w;
+    }
     const uint32_t q = q8_0_block8x4(v, dbits, s);
     const bool real = m < batch;
     gemm_pack_put(gp, ngroups, nb, m, b, l, real ? q : 0u, real ? f16_bits_to_f32(dbits) : 0.0f);
@@ -453,9 +467,18 @@ size_t gemm_pack_bytes(int32_t cols, int32_t batch) { return (size_t)gemm_groups
 int launch_gemm_pack_quantize(mrml_hip_ctx *ctx, const float *x, void *gpack, int32_t cols, int32_t batch)
 {
     const int nb = cols / 32, ng = gemm_groups(batch);
-    hipLaunchKernelGGL(quantize_gemm_pack_kernel, dim3((unsigned)(ng * nb)), dim3(256), 0, ctx->stream, x,
-                       (uint8_t *)gpack, nb, batch, ng);
+    hipLaunchKernelGGL(quantize_gemm_pack_kernel<false>, dim3((unsigned)(ng * nb)), dim3(256), 0, ctx->stream, x,
+                       nullptr, (uint8_t *)gpack, nb, batch, ng);
     return check_launch(ctx, "quantize_gemm_pack_kernel");
+}
+
+int launch_gemm_pack_geglu(mrml_hip_ctx *ctx, const float *g, const float *u, void *gpack, int32_t cols,
+                           int32_t batch)
+{
+    const int nb = cols / 32, ng = gemm_groups(batch);
+    hipLaunchKernelGGL(quantize_gemm_pack_kernel<true>, dim3((unsigned)(ng * nb)), dim3(256), 0, ctx->stream, g, u,
+                       (uint8_t *)gpack, nb, batch, ng);
+    return check_launch(ctx, "quantize_gemm_pack_kernel<geglu>");
 }
 
 int launch_gemm_pack_from_act(mrml_hip_ctx *ctx, const void *pack, void *gpack, int32_t cols, int32_t batch)
