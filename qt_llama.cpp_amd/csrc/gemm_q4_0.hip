@@ -89,18 +89,19 @@ __device__ __forceinline__ void gemm_pack_put(uint8_t *gp, int ngroups, int nb, 
 // the values quantized are gelu_tanh(x) * u elementwise (the GeGLU epilogue
 // of the matvec kernels, model.rs:2093-2105), formed in registers, so the
 // down projection's pack comes straight from the gate and up products.
+// Token m's values start at x + m*ld4*4 (and u + m*ld4*4).
 template <bool GEGLU>
 __global__ __launch_bounds__(256) void quantize_gemm_pack_kernel(const float *__restrict__ x,
                                                                  const float *__restrict__ u,
                                                                  uint8_t *__restrict__ gp, int nb, int batch,
-                                                                 int ngroups)
+                                                                 int ngroups, int ld4)
 {
     const int g = blockIdx.x / nb, b = blockIdx.x - g * nb;
     const int t = threadIdx.x >> 3, l = threadIdx.x & 7, m = 32 * g + t;
     const int ms = m < batch ? m : batch - 1;  // every lane takes part in the block reductions
     uint32_t dbits;
     int s;
-    const size_t i4 = ((size_t)ms * nb + b) * 8 + l;
+    const size_t i4 = (size_t)ms * ld4 + b * 8 + l;
     float4 v = reinterpret_cast<const float4 *>(x)[i4];
     if constexpr (GEGLU) {
         const float4 w = reinterpret_cast<const float4 *>(u)[i4];
@@ -468,16 +469,18 @@ int launch_gemm_pack_quantize(mrml_hip_ctx *ctx, const float *x, void *gpack, in
 {
     const int nb = cols / 32, ng = gemm_groups(batch);
     hipLaunchKernelGGL(quantize_gemm_pack_kernel<false>, dim3((unsigned)(ng * nb)), dim3(256), 0, ctx->stream, x,
-                       nullptr, (uint8_t *)gpack, nb, batch, ng);
+                       nullptr, (uint8_t *)gpack, nb, batch, ng, nb * 8);
     return check_launch(ctx, "quantize_gemm_pack_kernel");
 }
 
-int launch_gemm_pack_geglu(mrml_hip_ctx *ctx, const float *g, const float *u, void *gpack, int32_t cols,
-                           int32_t batch)
+int launch_gemm_pack_geglu(mrml_hip_ctx *ctx, const float *g, const float *u, int32_t ld, void *gpack,
+                           int32_t cols, int32_t batch)
 {
     const int nb = cols / 32, ng = gemm_groups(batch);
+    if (ld % 4 != 0 || ld < cols || ((uintptr_t)g | (uintptr_t)u) % 16 != 0)
+        return fail(ctx, MRML_HIP_E_INVALID, "gemm pack (geglu): row stride %d or operands not 16-byte aligned", ld);
     hipLaunchKernelGGL(quantize_gemm_pack_kernel<true>, dim3((unsigned)(ng * nb)), dim3(256), 0, ctx->stream, g, u,
-                       (uint8_t *)gpack, nb, batch, ng);
+                       (uint8_t *)gpack, nb, batch, ng, ld / 4);
     return check_launch(ctx, "quantize_gemm_pack_kernel<geglu>");
 }
 

@@ -98,10 +98,10 @@ int launch_gemv_q4_0_geglu_emit(mrml_hip_ctx *ctx, const void *wg, const void *w
 bool gemm_shape_ok(int32_t rows, int32_t cols, int32_t batch);
 size_t gemm_pack_bytes(int32_t cols, int32_t batch);
 int launch_gemm_pack_quantize(mrml_hip_ctx *ctx, const float *x, void *gpack, int32_t cols, int32_t batch);
-// The GEMM pack of act = gelu_tanh(g) * u (batch rows of `cols` values each),
-// without act itself written.
-int launch_gemm_pack_geglu(mrml_hip_ctx *ctx, const float *g, const float *u, void *gpack, int32_t cols,
-                           int32_t batch);
+// The GEMM pack of act = gelu_tanh(g) * u (batch rows of `cols` values each,
+// token rows `ld` floats apart in g and u), without act itself written.
+int launch_gemm_pack_geglu(mrml_hip_ctx *ctx, const float *g, const float *u, int32_t ld, void *gpack,
+                           int32_t cols, int32_t batch);
 int launch_gemm_pack_from_act(mrml_hip_ctx *ctx, const void *pack, void *gpack, int32_t cols, int32_t batch);
 // The allocation-free GEMM's file-scope device scratch: its size, and its
 // address on the context's device (resolved once per device; 0 or a status).

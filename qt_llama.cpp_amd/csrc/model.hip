@@ -48,11 +48,11 @@ struct mrml_hip_gemma2 {
     float *rope_table = nullptr;  // [ctx_len][head_dim/2] (cos, sin) from the host libm
     float *rope_freqs = nullptr;  // [head_dim/2] powf(base, 2i/head_dim) from the host libm (positions >= ctx_len)
     // prefill chunk buffers, allocated on the first prefill call: per token
-    // rows of h, xn, stacked q|k|v, attention output, o, gate, up and f,
+    // rows of h, xn, stacked q|k|v, attention output, o, stacked gate|up and f,
     // plus one GEMM pack (act is quantized into it as it is formed)
     void *pf_arena = nullptr;
     float *pf_h = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr,
-          *pf_attn = nullptr, *pf_o = nullptr, *pf_g = nullptr, *pf_u = nullptr, *pf_f = nullptr;
+          *pf_attn = nullptr, *pf_o = nullptr, *pf_gu = nullptr, *pf_f = nullptr;
     void *pf_gpack = nullptr, *pf_scores = nullptr;  // GEMM pack; attention scores of every row
 };
 
@@ -617,8 +617,8 @@ int prefill_buffers(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m)
         return at;
     };
     const size_t o_h = take(M * c.dim * 4), o_xn = take(M * c.dim * 4), o_qkv = take(M * (qd + 2 * kvd) * 4),
-                 o_attn = take(M * qd * 4), o_o = take(M * c.dim * 4), o_g = take(M * c.ffn_dim * 4),
-                 o_u = take(M * c.ffn_dim * 4), o_f = take(M * c.dim * 4),
+                 o_attn = take(M * qd * 4), o_o = take(M * c.dim * 4), o_gu = take(M * 2 * c.ffn_dim * 4),
+                 o_f = take(M * c.dim * 4),
                  o_gp = take(gemm_pack_bytes((int32_t)widest, (int32_t)M)),
                  o_sc = take((size_t)prefill_attn_rows(c) * attn_scratch_bytes(c.n_heads, c.ctx_len));
     hipError_t e = hipMalloc(&m->pf_arena, off);
@@ -628,8 +628,8 @@ int prefill_buffers(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m)
     }
     uint8_t *b = (uint8_t *)m->pf_arena;
     m->pf_h = (float *)(b + o_h), m->pf_xn = (float *)(b + o_xn), m->pf_qkv = (float *)(b + o_qkv);
-    m->pf_attn = (float *)(b + o_attn), m->pf_o = (float *)(b + o_o), m->pf_g = (float *)(b + o_g);
-    m->pf_u = (float *)(b + o_u), m->pf_f = (float *)(b + o_f);
+    m->pf_attn = (float *)(b + o_attn), m->pf_o = (float *)(b + o_o), m->pf_gu = (float *)(b + o_gu);
+    m->pf_f = (float *)(b + o_f);
     m->pf_gpack = b + o_gp;
     m->pf_scores = b + o_sc;
     return MRML_HIP_OK;
@@ -720,12 +720,15 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
             STEP(launch_residual_rms_norm(ctx, m->pf_o, L.post_attn_norm, h, h, L.ffn_norm, c.eps, xn, nullptr, c.dim,
                                           n, fast));
             STEP(launch_gemm_pack_quantize(ctx, xn, m->pf_gpack, c.dim, n));
-            STEP(launch_gemm_q4_0(ctx, L.w_gate, m->pf_gpack, m->pf_g, c.ffn_dim, c.dim, n, 0, fast));
-            STEP(launch_gemm_q4_0(ctx, L.w_up, m->pf_gpack, m->pf_u, c.ffn_dim, c.dim, n, 0, fast));
+            // gate and up in one launch: token rows of g|u
+            const void *gu_w[2] = {L.w_gate, L.w_up};
+            const int32_t gu_rows[2] = {c.ffn_dim, c.ffn_dim};
+            STEP(launch_gemm_q4_0_stacked(ctx, gu_w, gu_rows, 2, m->pf_gpack, m->pf_gu, c.dim, n, 0, fast));
             // act = gelu_tanh(g) * u per element (the GeGLU epilogue of the
             // matvec kernels, so each act value has the token step's bits),
             // quantized into the down projection's pack as it is formed
-            STEP(launch_gemm_pack_geglu(ctx, m->pf_g, m->pf_u, m->pf_gpack, c.ffn_dim, n));
+            STEP(launch_gemm_pack_geglu(ctx, m->pf_gu, m->pf_gu + c.ffn_dim, 2 * c.ffn_dim, m->pf_gpack, c.ffn_dim,
+                                        n));
             STEP(launch_gemm_q4_0(ctx, L.w_down, m->pf_gpack, m->pf_f, c.dim, c.ffn_dim, n, 0, fast));
             STEP(launch_residual_rms_norm(ctx, m->pf_f, L.post_ffw_norm, h, h, next_norm, c.eps, xn, nullptr, c.dim,
                                           n, fast));
