@@ -107,15 +107,24 @@ __global__ __launch_bounds__(kNormMaxThreads) void rms_norm_kernel(const float *
 // One workgroup; h_out may equal h_in.
 // FAST (one float4 per thread only): the two sums in tree order, the
 // tolerance path's norm.
+// gpack (one float4 per thread, xn set): xn of the batch's `rows` rows also
+// written as a GEMM pack, quantized as quantize_gemm_pack_kernel does; the
+// grid covers the pack's 32-token groups and the pad rows write zeros.
 template <int CH, bool FAST = false>
 __global__ __launch_bounds__(kNormMaxThreads) void residual_rms_norm_kernel(const float *__restrict__ t,
                                                                  const float *__restrict__ w_post,
                                                                  const float *h_in, float *h_out,
                                                                  const float *__restrict__ w_next, float eps,
                                                                  float *__restrict__ xn, uint8_t *__restrict__ pack,
-                                                                 int dim)
+                                                                 int dim, uint8_t *__restrict__ gpack, int rows)
 {
     extern __shared__ __align__(16) float lds[];
+    const int n4 = dim >> 2;
+    if (CH == 1 && gpack && (int)blockIdx.y >= rows) {
+        if ((int)threadIdx.x < n4)
+            gemm_pack_put(gpack, gemm_groups(rows), n4 >> 3, blockIdx.y, threadIdx.x >> 3, threadIdx.x & 7, 0u, 0.0f);
+        return;
+    }
     if (blockIdx.y) {  // row blockIdx.y of a batch (prefill; no pack)
         const size_t r = (size_t)blockIdx.y * dim;
         t += r;
@@ -123,11 +132,19 @@ __global__ __launch_bounds__(kNormMaxThreads) void residual_rms_norm_kernel(cons
         h_out += r;
         if (xn) xn += r;
     }
-    const int n4 = dim >> 2;
     if constexpr (CH == 1) {
         const ResidualOps ops = residual_load(t, w_post, h_in, (xn || pack) ? w_next : nullptr, n4);
         residual_norm1<false, FAST>(ops, w_post != nullptr, w_next != nullptr, eps, h_out, xn, pack, dim,
                                     *reinterpret_cast<mrml_xsum::Shared4 *>(lds));
+        if (gpack) {
+            // this thread's own chunk of xn, read back after its store
+            const int c = threadIdx.x;
+            const float4 o = c < n4 ? reinterpret_cast<const float4 *>(xn)[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            uint32_t dbits;
+            int qs;
+            const uint32_t q = q8_0_block8x4(o, dbits, qs);  // every lane takes part
+            if (c < n4) gemm_pack_put(gpack, gemm_groups(rows), n4 >> 3, blockIdx.y, c >> 3, c & 7, q, f16_bits_to_f32(dbits));
+        }
         return;
     }
     const float4 *t4 = reinterpret_cast<const float4 *>(t);
@@ -1765,17 +1782,26 @@ int launch_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float eps
 }
 
 int launch_residual_rms_norm(mrml_hip_ctx *ctx, const float *t, const float *w_post, const float *h_in, float *h_out,
-                             const float *w_next, float eps, float *xn, void *pack, int dim, int rows, bool fast)
+                             const float *w_next, float eps, float *xn, void *pack, int dim, int rows, bool fast,
+                             void *gpack)
 {
+    if (gpack && !(xn && norm_one_chunk(dim) && dim % 32 == 0)) {  // the pack from xn, a launch of its own
+        if (!xn) return fail(ctx, MRML_HIP_E_INVALID, "residual_rms_norm: a GEMM pack needs xn");
+        if (int rc = launch_residual_rms_norm(ctx, t, w_post, h_in, h_out, w_next, eps, xn, pack, dim, rows, fast))
+            return rc;
+        return launch_gemm_pack_quantize(ctx, xn, gpack, dim, rows);
+    }
+    const dim3 grid(1, gpack ? gemm_groups(rows) * 32 : rows);
+    uint8_t *gp = (uint8_t *)gpack;
     if (norm_one_chunk(dim) && fast)
-        hipLaunchKernelGGL((residual_rms_norm_kernel<1, true>), dim3(1, rows), dim3(norm_threads(dim)), norm_lds(dim),
-                           ctx->stream, t, w_post, h_in, h_out, w_next, eps, xn, (uint8_t *)pack, dim);
+        hipLaunchKernelGGL((residual_rms_norm_kernel<1, true>), grid, dim3(norm_threads(dim)), norm_lds(dim),
+                           ctx->stream, t, w_post, h_in, h_out, w_next, eps, xn, (uint8_t *)pack, dim, gp, rows);
     else if (norm_one_chunk(dim))
-        hipLaunchKernelGGL(residual_rms_norm_kernel<1>, dim3(1, rows), dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, t,
-                           w_post, h_in, h_out, w_next, eps, xn, (uint8_t *)pack, dim);
+        hipLaunchKernelGGL(residual_rms_norm_kernel<1>, grid, dim3(norm_threads(dim)), norm_lds(dim), ctx->stream, t,
+                           w_post, h_in, h_out, w_next, eps, xn, (uint8_t *)pack, dim, gp, rows);
     else
-        hipLaunchKernelGGL(residual_rms_norm_kernel<kMaxChunks>, dim3(1, rows), dim3(norm_threads(dim)), norm_lds(dim),
-                           ctx->stream, t, w_post, h_in, h_out, w_next, eps, xn, (uint8_t *)pack, dim);
+        hipLaunchKernelGGL(residual_rms_norm_kernel<kMaxChunks>, grid, dim3(norm_threads(dim)), norm_lds(dim),
+                           ctx->stream, t, w_post, h_in, h_out, w_next, eps, xn, (uint8_t *)pack, dim, gp, rows);
     return check_launch(ctx, "residual_rms_norm_kernel");
 }
 

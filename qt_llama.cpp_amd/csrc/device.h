@@ -376,4 +376,21 @@ __device__ __forceinline__ float gelu_tanh(float x)
     return 0.5f * x * (1.0f + mrml_libm::tanhf(k * (x + 0.044715f * x * x * x)));
 }
 
+// GEMM pack of `batch` tokens x nb blocks, groups of 32 tokens (the last
+// group zero-padded):
+//   int8  q[g][b][h][t][16]  at byte 0              (h = K half, t = token in group)
+//   f32   d[g][b][t]         at byte ngroups*nb*1024
+__host__ __device__ inline int gemm_groups(int batch) { return (batch + 31) / 32; }
+
+// Writes token m's block b (8 lanes, lane l holding quants 4l..4l+3 packed in
+// q) into the GEMM pack.
+__device__ __forceinline__ void gemm_pack_put(uint8_t *gp, int ngroups, int nb, int m, int b, int l, uint32_t q,
+                                              float d)
+{
+    const int g = m >> 5, t = m & 31, h = l >> 2;
+    const size_t gb = (size_t)g * nb + b;
+    reinterpret_cast<uint32_t *>(gp + ((gb * 64 + 32 * h + t) * 16))[l & 3] = q;
+    if (l == 0) reinterpret_cast<float *>(gp + (size_t)ngroups * nb * 1024)[gb * 32 + t] = d;
+}
+
 }  // namespace mrml

@@ -66,23 +66,6 @@ constexpr float kMagic = 12582912.0f;      // 1.5 * 2^23
 constexpr int kMagicBits = 0x4B400000;     // its f32 bit pattern
 constexpr int kSIMDs = 1024;               // MI355X: 256 CUs x 4 SIMDs
 
-// GEMM pack of `batch` tokens x nb blocks, groups of 32 tokens (the last
-// group zero-padded):
-//   int8  q[g][b][h][t][16]  at byte 0              (h = K half, t = token in group)
-//   f32   d[g][b][t]         at byte ngroups*nb*1024
-__host__ __device__ inline int gemm_groups(int batch) { return (batch + 31) / 32; }
-
-// Writes token m's block b (8 lanes, lane l holding quants 4l..4l+3 packed in
-// q) into the GEMM pack.
-__device__ __forceinline__ void gemm_pack_put(uint8_t *gp, int ngroups, int nb, int m, int b, int l, uint32_t q,
-                                              float d)
-{
-    const int g = m >> 5, t = m & 31, h = l >> 2;
-    const size_t gb = (size_t)g * nb + b;
-    reinterpret_cast<uint32_t *>(gp + ((gb * 64 + 32 * h + t) * 16))[l & 3] = q;
-    if (l == 0) reinterpret_cast<float *>(gp + (size_t)ngroups * nb * 1024)[gb * 32 + t] = d;
-}
-
 // quant.rs:193-228 per block (q8_0_block8x4), written as a GEMM pack.  One
 // workgroup per (group, block): thread 8t+l handles token 32g+t, values
 // 4l..4l+3 of block b.  Tokens past `batch` are written as zeros.  GEGLU:

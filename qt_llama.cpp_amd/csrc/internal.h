@@ -177,7 +177,7 @@ int launch_rms_norm(mrml_hip_ctx *ctx, const float *x, const float *w, float eps
 // fast: the tolerance path's tree-order sums (dims of one float4 per thread)
 int launch_residual_rms_norm(mrml_hip_ctx *ctx, const float *t, const float *w_post, const float *h_in, float *h_out,
                              const float *w_next, float eps, float *xn, void *pack, int dim, int rows = 1,
-                             bool fast = false);
+                             bool fast = false, void *gpack = nullptr);
 int launch_embedding(mrml_hip_ctx *ctx, const void *table, int type, const int32_t *d_token, int token, float scale,
                      float *h, const float *w_norm, float eps, float *xn, void *pack, int dim, int vocab,
                      int rows = 1);

@@ -685,7 +685,8 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
             uint16_t *kc = d_k_cache + (size_t)l * layer_cache, *vc = d_v_cache + (size_t)l * layer_cache;
             const float *next_norm = l + 1 < c.n_layers ? m->layers[l + 1].attn_norm : m->output_norm;
             // q, k, v of the chunk, stacked per token as the token step's q|k|v
-            STEP(launch_gemm_pack_quantize(ctx, xn, m->pf_gpack, c.dim, n));
+            // (the pack of xn: the previous layer's norm writes it)
+            if (l == 0) STEP(launch_gemm_pack_quantize(ctx, xn, m->pf_gpack, c.dim, n));
             {
                 const void *qkv_w[3] = {L.wq, L.wk, L.wv};
                 const int32_t qkv_rows[3] = {qd, kvd, kvd};
@@ -718,8 +719,7 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
             }
             STEP(gemm_rows(ctx, m, L.wo, m->pf_attn, m->pf_o, c.dim, qd, n));
             STEP(launch_residual_rms_norm(ctx, m->pf_o, L.post_attn_norm, h, h, L.ffn_norm, c.eps, xn, nullptr, c.dim,
-                                          n, fast));
-            STEP(launch_gemm_pack_quantize(ctx, xn, m->pf_gpack, c.dim, n));
+                                          n, fast, m->pf_gpack));
             // gate and up in one launch: token rows of g|u
             const void *gu_w[2] = {L.w_gate, L.w_up};
             const int32_t gu_rows[2] = {c.ffn_dim, c.ffn_dim};
@@ -731,7 +731,7 @@ int mrml_hip_gemma2_prefill(mrml_hip_ctx *ctx, mrml_hip_gemma2 *m, const int32_t
                                         n));
             STEP(launch_gemm_q4_0(ctx, L.w_down, m->pf_gpack, m->pf_f, c.dim, c.ffn_dim, n, 0, fast));
             STEP(launch_residual_rms_norm(ctx, m->pf_f, L.post_ffw_norm, h, h, next_norm, c.eps, xn, nullptr, c.dim,
-                                          n, fast));
+                                          n, fast, l + 1 < c.n_layers ? m->pf_gpack : nullptr));
         }
         if (t0 + n < n_tokens) continue;
         // the last token's logits and greedy pick (the LM head of its token step)
